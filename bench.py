@@ -1,0 +1,205 @@
+"""Benchmark: Llama-3-8B-shaped Q4 batch-1 greedy decode at 4k context on one
+MI355X, plus the Q4 GEMV HBM roofline and the reference CPU path beside it.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--gemv-only]
+
+A step is one decode token: one pass of the hot path (embed, 32 layers of
+normq / q-k-v GEMV / RoPE + fp16 KV attention / o GEMV / normq / SwiGLU GEMV /
+down GEMV, then the head GEMV and greedy argmax) over synthetic random-init Q4
+weights of the Llama-3-8B architecture. The prompt (random ids) is read first
+so the timed tokens run with ~4k positions of KV cache. Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import shutil
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import sheep_amd as sa  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+LLAMA = dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, n_ff=14336, n_vocab=128256,
+             rope_theta=500000.0, rms_eps=1e-5, tied=False, qkv_bias=False, nbits=4, seed=1003)
+N_CTX = 4096
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def scratch_dir():
+    for d in (os.environ.get("SML_BENCH_DIR"), "/dev/shm", tempfile.gettempdir()):
+        if d and os.path.isdir(d) and shutil.disk_usage(d).free > 12e9:
+            return d
+    return tempfile.gettempdir()
+
+
+def gemv_roofline(rows, cols, iters=400, target_bytes=1.2e9, tmp=None):
+    """Q4 GEMV over rotating copies (more bytes than the 256 MB MALL) timed
+    with HIP events on the launch stream. Returns (avg_us, bytes_per_launch)."""
+    p = os.path.join(tmp, f"gemv_{rows}x{cols}.ssf")
+    if not os.path.exists(p):
+        sa.synth_matrix(p, rows, cols, nbits=4, seed=1004)
+    first = sa.Mat.from_file(p, "w")
+    ncopy = max(2, int(target_bytes // first.bytes) + 1)
+    mats = [first] + [sa.Mat.from_file(p, "w") for _ in range(ncopy - 1)]
+    x = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
+    xd = sa.DevBuf.of(x)
+    act = sa.Act(cols)
+    sa.normq(xd, act)
+    y = sa.DevBuf(rows * 4)
+    arr = (sa.c_void_p * ncopy)(*[m.h for m in mats])
+    ms = sa.c_float()
+    lib = sa.lib()
+    for _ in range(2):   # warm-up rounds
+        assert lib.sml_hip_time_matvec(arr, ncopy, act.q.ptr, act.scale.ptr, act.sums.ptr, y.ptr, ncopy,
+                                       sa.ctypes.byref(ms)) == 0
+    trials = []
+    for _ in range(5):
+        assert lib.sml_hip_time_matvec(arr, ncopy, act.q.ptr, act.scale.ptr, act.sums.ptr, y.ptr, iters,
+                                       sa.ctypes.byref(ms)) == 0
+        trials.append(ms.value * 1000.0 / iters)
+    for m in mats:
+        m.free()
+    return float(np.median(trials)), first.bytes
+
+
+def cpu_baseline(path, threads, budget_s=12.0, max_tokens=160):
+    """The reference's own CPU decode (sml_forward on its pool threads,
+    compiled from its sources into oracle/_ref) on the same model file, from
+    position 0 for as many tokens as fit the time budget."""
+    try:
+        from oracle import bind as ob
+    except Exception as e:  # noqa: BLE001
+        return {"value": None, "error": f"oracle bindings unavailable: {e}"}
+    if not ob.have_ref():
+        return {"value": None, "error": "oracle/_ref/libsmlref.so not built"}
+    m = ob.RefModel(path, 256, threads=threads)
+    tok, n = 1, 0
+    m.forward(tok, 0)            # warm-up token (position 0)
+    t0 = time.perf_counter()
+    while n < max_tokens and time.perf_counter() - t0 < budget_s:
+        tok = int(np.argmax(m.forward(tok, n + 1)))
+        n += 1
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} greedy decode tokens at positions 2..{n + 1} of the same Llama-3-8B-shaped Q4 file "
+                      f"(short context: attention negligible), sml_forward with {threads} pool threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=120)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gemv-only", action="store_true")
+    ap.add_argument("--keep", action="store_true", help="keep the generated model file")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {a.gpus} is not supported (this build has no "
+              f"multi-GPU path)", file=sys.stderr)
+        sys.exit(2)
+    sa.init(0)
+    tmp = scratch_dir()
+    work = tempfile.mkdtemp(prefix="smlbench_", dir=tmp)
+    try:
+        res = run(a, work)
+    finally:
+        if not a.keep:
+            shutil.rmtree(work, ignore_errors=True)
+    print(json.dumps(res), flush=True)
+
+
+def run(a, work):
+    t0 = time.perf_counter()
+    g_us, g_bytes = gemv_roofline(4096, 14336, tmp=work)
+    g2_us, g2_bytes = gemv_roofline(14336, 4096, tmp=work)
+    g1_us, g1_bytes = gemv_roofline(8960, 1536, tmp=work)
+    gbs = g_bytes / (g_us * 1e-6) / 1e9
+    log(f"gemv q4 4096x14336: {g_us:.2f} us, {gbs:.0f} GB/s; 14336x4096: {g2_us:.2f} us, "
+        f"{g2_bytes / g2_us / 1e3:.0f} GB/s; 8960x1536: {g1_us:.2f} us, {g1_bytes / g1_us / 1e3:.0f} GB/s "
+        f"({time.perf_counter() - t0:.1f}s)")
+    roof = {"bound": "hbm", "kernel": "sml_gemv_q4 (4096 rows x 14336 cols, Q4)",
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None, "avg_us": round(g_us, 3), "bytes_per_launch": g_bytes}
+    gemv = {"4096x14336": {"us": round(g_us, 3), "GB/s": round(gbs, 1)},
+            "14336x4096": {"us": round(g2_us, 3), "GB/s": round(g2_bytes / g2_us / 1e3, 1)},
+            "8960x1536": {"us": round(g1_us, 3), "GB/s": round(g1_bytes / g1_us / 1e3, 1)}}
+    if a.gemv_only:
+        return {"metric": "Q4 GEMV HBM GB/s", "value": round(gbs, 1), "unit": "GB/s", "roofline": roof, "gemv_q4": gemv}
+
+    path = os.path.join(work, "llama3_8b_q4.ssf")
+    t1 = time.perf_counter()
+    sa.synth_model(path, n_ctx_train=N_CTX, **LLAMA)
+    log(f"synthetic Llama-3-8B-shaped Q4 file: {os.path.getsize(path) / 1e9:.2f} GB ({time.perf_counter() - t1:.1f}s)")
+    K, W = a.steps, a.warmup
+    prompt_len = N_CTX - K - W
+    if prompt_len < 1:
+        raise SystemExit("steps + warmup must stay below the 4096-position context")
+    t1 = time.perf_counter()
+    dec = sa.Decoder(path, n_ctx=N_CTX)
+    wbytes = dec.weight_bytes()
+    log(f"loaded on the GPU in {time.perf_counter() - t1:.1f}s; {wbytes / 1e9:.4f} GB of weights per token")
+    rng = np.random.default_rng(1003)
+    ids = rng.integers(0, LLAMA["n_vocab"], prompt_len).astype(np.int32)
+    t1 = time.perf_counter()
+    lg = dec.prefill(ids, 0, LLAMA["n_vocab"])
+    log(f"prompt of {prompt_len} ids read a token at a time in {time.perf_counter() - t1:.1f}s")
+    tok = int(np.argmax(lg))
+    pos = prompt_len
+    warm = dec.generate(tok, pos, W)            # untimed warm-up steps
+    tok, pos = int(warm[-1]), pos + W
+    sa.sync()
+    t1 = time.perf_counter()
+    out = dec.generate(tok, pos, K)             # K timed steps, one graph replay per token
+    sa.sync()
+    dt = time.perf_counter() - t1
+    ev_ms = dec.last_ms()
+    dec.close()
+    tps = K / dt
+    kv_bytes = 2 * LLAMA["n_layer"] * LLAMA["n_head_kv"] * 128 * 2 * (pos + K / 2)
+    roof_tps = HBM_PEAK_GBS * 1e9 / wbytes
+    roof_tps_kv = HBM_PEAK_GBS * 1e9 / (wbytes + kv_bytes)
+    log(f"decode: {K} tokens in {dt * 1e3:.1f} ms wall ({ev_ms:.1f} ms GPU events): {tps:.1f} tok/s; "
+        f"roofline {roof_tps:.0f} tok/s weights-only, {roof_tps_kv:.0f} with KV")
+    cpu = None
+    if not a.no_cpu:
+        th = min(16, os.cpu_count() or 1)
+        t1 = time.perf_counter()
+        cpu = cpu_baseline(path, th)
+        log(f"cpu baseline: {cpu} ({time.perf_counter() - t1:.1f}s)")
+    return {
+        "metric": "Q4 GEMV HBM GB/s (% of peak); batch-1 decode tokens/s, Llama-3-8B shape",
+        "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(dt * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8xq4 (int32 dot, fp32 epilogue)", "data": "synthetic",
+        "config": {"workload": "Llama-3-8B-shaped decoder, random-init Q4 SSF weights (32 layers, hidden 4096, "
+                               "FFN 14336 SwiGLU, 32/8 heads, head_dim 128, vocab 128256, rope theta 5e5), "
+                               "fp16 KV cache, batch-1 greedy decode at positions "
+                               f"{pos}..{pos + K - 1} of a {N_CTX}-position context",
+                   "global_batch": 1, "seq_len": N_CTX, "parallelism": "single GPU"},
+        "decode": {"tokens_per_s": round(tps, 2), "gpu_event_ms": round(ev_ms, 3),
+                   "weight_bytes_per_token": wbytes, "kv_bytes_per_token_avg": int(kv_bytes),
+                   "roofline_tokens_per_s_weights_only": round(roof_tps, 1),
+                   "roofline_tokens_per_s_with_kv": round(roof_tps_kv, 1),
+                   "frac_of_weights_roofline": round(tps / roof_tps, 4),
+                   "frac_of_weights_kv_roofline": round(tps / roof_tps_kv, 4),
+                   "effective_GB/s": round((wbytes + kv_bytes) * tps / 1e9, 1),
+                   "first_tokens": [int(t) for t in out[:8]]},
+        "gemv_q4": gemv,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+
+
+if __name__ == "__main__":
+    main()

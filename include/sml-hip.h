@@ -1,0 +1,95 @@
+// Kernel-level C ABI of the MI355X (gfx950) decode path.
+//
+// Plain pointers and sizes only. Device pointers come from sml_hip_malloc (or
+// any HIP allocation in the same process). Every call returns 0 on success and
+// -1 on failure (sml_hip_last_error() says why), or NULL for constructors;
+// nothing ends the process. Each entry point names the reference CPU/GPU
+// interface it replaces; the GPU forward pass itself is in sml-gpu.h.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// ------------------------------------------------------------ device plumbing
+// replaces the driver binding of sml/sml-gpu-drv.h:13-216 (cu_open, MemAlloc,
+// MemcpyHtoD/DtoH, cu_check)
+int          sml_hip_init(int device, char * why, int nwhy);
+const char * sml_hip_last_error(void);
+void *       sml_hip_malloc(size_t n);
+int          sml_hip_free(void * p);
+int          sml_hip_h2d(void * dst, const void * src, size_t n);
+int          sml_hip_d2h(void * dst, const void * src, size_t n);
+int          sml_hip_memset(void * p, int value, size_t n);
+int          sml_hip_sync(void);
+// Test hook: make the n-th HIP call from now fail (n < 0 disables).
+void         sml_hip_fail_after(long n);
+
+// ------------------------------------------------------------ matrices
+// A quantized FLAT matrix resident in HBM (the file's planes and fields;
+// 6-bit group fields are widened to bytes with the min bias moved to 127).
+// replaces the reference's per-tensor upload up_tensor (sml/sml-gpu-fwd.c:99-160)
+typedef struct sml_hip_mat sml_hip_mat;
+sml_hip_mat * sml_hip_mat_upload(const uint8_t * const planes[4], const uint16_t * sd, const uint8_t * sq,
+                                 const uint16_t * md, const uint8_t * mq,
+                                 int rows, int cols, int nbits, int scale6, int minneg);
+// The same, for record `name` of an SSF file.
+sml_hip_mat * sml_hip_mat_from_file(const char * path, const char * name);
+void          sml_hip_mat_free(sml_hip_mat * m);
+int           sml_hip_mat_info(const sml_hip_mat * m, int * rows, int * cols, int * nbits);
+// Bytes the matrix occupies in HBM (codes + fields): what one GEMV streams.
+size_t        sml_hip_mat_bytes(const sml_hip_mat * m);
+
+// ------------------------------------------------------------ activations
+// RMSNorm (w != NULL) of x after x += resid (resid != NULL), gathered through
+// perm (NULL = identity), quantized per 32 (per256 = 0) or per 256 values.
+// replaces sml_quantize_act / sml_quantize_act_sb (sml/sml-kernel.h:136,318),
+// sml_gather (:151) and rms_norm (sml/sml-run.c:147-152), as one kernel like
+// the reference GPU's sml_g_normq2 (sml/sml-gpu-fast.cu:64-111)
+int sml_hip_normq(float * x, const float * resid, const float * w, float eps, int n,
+                  const int32_t * perm, int8_t * q, float * scale, int32_t * sums, int per256);
+
+// ------------------------------------------------------------ GEMV
+// y = W.x for the quantized activation (q, scale, sums) of x, any FLAT width.
+// replaces sml_matvec_rows_flat4 / _flat6 / _flat8 / sml_matvec_rows +
+// sml_matvec_bits1 (sml/sml-kernel.h:239,246,212,190,206) as dispatched by
+// issue_rows_act (sml/sml-run.c:612-680); y is written, not accumulated.
+int sml_hip_matvec(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums,
+                   float * y);
+// h = silu(gate.x) * (up.x), the fused gate/up of sml_g_ffns (sml/sml-gpu-fast.cu:319-354)
+int sml_hip_matvec_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q,
+                          const float * scale, const int32_t * sums, float * h);
+// Time `iters` back-to-back launches of sml_hip_matvec, rotating over `ncopy`
+// matrices of one shape (so repeats are not served from cache), with HIP
+// events on the launch stream. ms_total receives the elapsed milliseconds.
+int sml_hip_time_matvec(const sml_hip_mat * const * mats, int ncopy, const int8_t * q, const float * scale,
+                        const int32_t * sums, float * y, int iters, float * ms_total);
+
+// ------------------------------------------------------------ unpack / embed
+// Integer code of every weight of rows [row0, row0+nrows), one byte each,
+// permuted column order: the unpack truth of sml_dequant_row_* (sml/sml-kernel.c:2134-2260)
+int sml_hip_unpack(const sml_hip_mat * m, int row0, int nrows, uint8_t * out);
+// Row *tok dequantized and scattered through perm into x (sml/sml-run.c:3291-3344)
+int sml_hip_embed(const sml_hip_mat * m, const int32_t * tok, const int32_t * perm, float * x);
+
+// ------------------------------------------------------------ attention
+// RoPE q and k at position *pos (halved pairs, table rows of `half` floats),
+// write k and v as fp16 into the layer's cache at *pos, then softmax attention
+// of every query head over positions [0, *pos] into out (n_head*hd floats).
+// replaces rope_tab + f32_to_f16 + attn_head (sml/sml-run.c:339-372,3414-3434)
+// and the reference GPU's sml_g_attn2 (sml/sml-gpu-fast.cu:363-453).
+// hd must be 128; n_head/n_kv at most 8; part needs attn_part_floats().
+size_t sml_hip_attn_part_floats(int n_head, int hd, int n_ctx);
+int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,
+                      const float * cos_t, const float * sin_t, const int32_t * pos,
+                      int n_head, int n_kv, int hd, int n_ctx, float * part, float * out);
+
+// ------------------------------------------------------------ argmax
+// First-max greedy pick into *tok (sml_sample_greedy, sml/sml-run.c:3539-3544)
+int sml_hip_argmax(const float * logits, int n, int32_t * tok);
+
+#ifdef __cplusplus
+}
+#endif

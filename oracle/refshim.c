@@ -1,0 +1,77 @@
+// CPU ORACLE — test infrastructure only. A thin C wrapper compiled together
+// with the reference engine's own CPU sources (sml-kernel.c, sml-pool.c,
+// sml-model.c, sml-run.c, read where they lie) into oracle/_ref/libsmlref.so.
+// It gives ctypes flat entry points for the reference's context-based API and
+// reports the reference's struct layout so the format can be cross-checked.
+#include <stddef.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "sml-run.h"
+
+// Layout of the reference's packed structs: sizes then field offsets.
+void ref_layout(long * out) {
+    out[0] = (long) sizeof(sml_hdr);
+    out[1] = (long) sizeof(sml_rec);
+    out[2] = (long) offsetof(sml_hdr, table_off);
+    out[3] = (long) offsetof(sml_hdr, flags);
+    out[4] = (long) offsetof(sml_hdr, n_expert_used);
+    out[5] = (long) offsetof(sml_hdr, moe_flags);
+    out[6] = (long) offsetof(sml_hdr, gdn_dk);
+    out[7] = (long) offsetof(sml_rec, perm_off);
+    out[8] = (long) offsetof(sml_rec, mq_n);
+    out[9] = (long) offsetof(sml_rec, codes_off);
+    out[10] = (long) offsetof(sml_rec, nbits);
+    out[11] = (long) offsetof(sml_hdr, rope_theta);
+}
+
+typedef struct { sml_model m; sml_ctx c; int have_ctx; } ref_h;
+
+void * ref_open(const char * path, int n_ctx, int threads, int with_ctx) {
+    ref_h * h = calloc(1, sizeof *h);
+    if (!h) return NULL;
+    if (!sml_model_open(&h->m, path)) { free(h); return NULL; }
+    if (with_ctx) {
+        if (!sml_ctx_init(&h->c, &h->m, n_ctx, threads)) { sml_model_close(&h->m); free(h); return NULL; }
+        h->have_ctx = 1;
+    }
+    return h;
+}
+
+void ref_close(void * p) {
+    ref_h * h = (ref_h *) p;
+    if (!h) return;
+    if (h->have_ctx) sml_ctx_free(&h->c);
+    sml_model_close(&h->m);
+    free(h);
+}
+
+const float * ref_forward(void * p, int tok, int pos) {
+    ref_h * h = (ref_h *) p;
+    return sml_forward(&h->c, tok, pos, 0);
+}
+
+const float * ref_prefill(void * p, const int32_t * ids, int pos0, int n) {
+    ref_h * h = (ref_h *) p;
+    return sml_prefill(&h->c, ids, pos0, n, 0);
+}
+
+int ref_n_vocab(void * p) { return (int) ((ref_h *) p)->m.hdr->n_vocab; }
+
+// The model's tensor record by name: returns the record's address inside the
+// mapped file (its offsets are absolute file offsets) or NULL.
+const void * ref_find(void * p, const char * name) { return sml_find(&((ref_h *) p)->m, name); }
+const void * ref_base(void * p) { return ((ref_h *) p)->m.base; }
+
+// sml_moe_route with a header carrying only the routing fields.
+int ref_moe_route(const float * lg, int ne, int k, unsigned moe_flags, int * sel, float * w) {
+    sml_hdr hd;
+    sml_layer ly;
+    memset(&hd, 0, sizeof hd);
+    memset(&ly, 0, sizeof ly);
+    hd.n_expert_used = (uint32_t) k;
+    hd.moe_flags = moe_flags;
+    ly.n_exp = ne;
+    float sc[64], ch[64];
+    return sml_moe_route(&hd, &ly, lg, sc, ch, sel, w);
+}

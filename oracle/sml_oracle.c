@@ -1,0 +1,619 @@
+// CPU ORACLE — test infrastructure only (see sml_oracle.h). Never linked into
+// or called by the GPU library.
+#include "sml_oracle.h"
+
+#include <fcntl.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+// ------------------------------------------------------------ activations
+
+// sml/sml-kernel.c:86-106: amax over 32, s = amax/127, is = 1/s (0 when s == 0),
+// q = lrintf(x*is) clamped to +-127 (lrintf rounds half to even under the
+// default rounding mode), sums = sum of q.
+void orc_quantize_act(const float * x, int n, int8_t * q, float * scale, int32_t * sums) {
+    for (int g = 0; g < n / 32; g++) {
+        const float * xs = x + g * 32;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; i++) { const float v = fabsf(xs[i]); if (v > amax) amax = v; }
+        const float s = amax / 127.0f;
+        const float is = s > 0.0f ? 1.0f / s : 0.0f;
+        int32_t sum = 0;
+        for (int i = 0; i < 32; i++) {
+            long v = lrintf(xs[i] * is);
+            if (v > 127) v = 127;
+            if (v < -127) v = -127;
+            q[g * 32 + i] = (int8_t) v;
+            sum += (int32_t) v;
+        }
+        scale[g] = s;
+        sums[g] = sum;
+    }
+}
+
+// sml/sml-kernel.c:165-184: one amax per 256 values (the partial last superblock
+// uses what it has), the same s/is/rounding, the scale copied into every group.
+void orc_quantize_act_sb(const float * x, int n, int8_t * q, float * scale, int32_t * sums) {
+    const int ng = n / 32;
+    for (int g0 = 0; g0 < ng; g0 += 8) {
+        const int g1 = g0 + 8 < ng ? g0 + 8 : ng;
+        float amax = 0.0f;
+        for (int i = g0 * 32; i < g1 * 32; i++) { const float v = fabsf(x[i]); if (v > amax) amax = v; }
+        const float s = amax / 127.0f;
+        const float is = s > 0.0f ? 1.0f / s : 0.0f;
+        for (int g = g0; g < g1; g++) {
+            int32_t sum = 0;
+            for (int i = 0; i < 32; i++) {
+                long v = lrintf(x[g * 32 + i] * is);
+                if (v > 127) v = 127;
+                if (v < -127) v = -127;
+                q[g * 32 + i] = (int8_t) v;
+                sum += (int32_t) v;
+            }
+            scale[g] = s;
+            sums[g] = sum;
+        }
+    }
+}
+
+// ------------------------------------------------------------ fp16
+
+// sml/sml-run.c:85-109 (scalar encode, round to nearest even)
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, rawe = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (rawe == 0xffu) return (uint16_t) (sign | 0x7c00u | (man ? 0x200u : 0u));
+    const int32_t e = (int32_t) rawe - 127 + 15;
+    if (e >= 31) return (uint16_t) (sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t) sign;
+        man |= 0x800000u;
+        const uint32_t sh = (uint32_t) (14 - e);
+        uint32_t sub = man >> sh;
+        const uint32_t rem = man & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+        if (rem > half || (rem == half && (sub & 1u))) sub++;
+        return (uint16_t) (sign | sub);
+    }
+    uint32_t h = ((uint32_t) e << 10) | (man >> 13);
+    const uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t) (sign | h);
+}
+
+// sml/sml-kernel.c:14-38 (scalar decode)
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t s = (uint32_t) (h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu, bits;
+    if (e == 0) {
+        if (m == 0) bits = s;
+        else {
+            e = 127 - 15 + 1;
+            while (!(m & 0x400u)) { m <<= 1; e--; }
+            m &= 0x3ffu;
+            bits = s | (e << 23) | (m << 13);
+        }
+    } else if (e == 31) bits = s | 0x7f800000u | (m << 13);
+    else bits = s | ((e - 15 + 127) << 23) | (m << 13);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+// ------------------------------------------------------------ fields and codes
+
+// sml/sml-kernel.h:79-98: four 6-bit values in three bytes
+static int field(const uint8_t * base, int g, int six) {
+    if (!six) return base[g];
+    const uint8_t * p = base + (size_t) (g >> 2) * 3;
+    const uint32_t b0 = p[0], b1 = p[1], b2 = p[2];
+    switch (g & 3) {
+    case 0: return (int) (b0 & 63u);
+    case 1: return (int) (((b0 >> 6) | (b1 << 2)) & 63u);
+    case 2: return (int) (((b1 >> 4) | (b2 << 4)) & 63u);
+    default: return (int) ((b2 >> 2) & 63u);
+    }
+}
+
+static size_t field_row(const orc_tensor * t) {
+    const int ng = t->cols / 32;
+    return t->scale6 ? (size_t) (ng / 4) * 3 : (size_t) ng;
+}
+
+float orc_step(const orc_tensor * t, int row, int g) {
+    const int ns = (t->cols / 32 + 7) / 8;
+    return orc_f16_to_f32(t->sd[(size_t) row * ns + g / 8])
+         * (float) field(t->sq + (size_t) row * field_row(t), g, t->scale6);
+}
+
+float orc_min(const orc_tensor * t, int row, int g) {
+    if (!t->mq) return 0.0f;
+    const int ns = (t->cols / 32 + 7) / 8;
+    const float bias = t->scale6 ? (t->minneg ? 63.0f : 31.0f) : 127.0f;
+    return orc_f16_to_f32(t->md[(size_t) row * ns + g / 8])
+         * ((float) field(t->mq + (size_t) row * field_row(t), g, t->scale6) - bias);
+}
+
+// one plane's bits of every weight of a row, per plane width
+static void plane_bits(const uint8_t * plane, int pbits, int row, int cols, int * out) {
+    if (pbits == 4) {
+        // sml/sml-kernel.c:2140-2156: quad of 64 bytes = 4 groups; first 32 bytes
+        // hold groups 4q (low nibble) and 4q+1 (high), the second 32 the next two
+        const uint8_t * cp = plane + (size_t) row * (cols / 2);
+        for (int g = 0; g < cols / 32; g++) {
+            const uint8_t * blk = cp + (size_t) (g / 4) * 64 + ((g % 4) >= 2 ? 32 : 0);
+            const int hi = g & 1;
+            for (int j = 0; j < 32; j++) out[g * 32 + j] = hi ? (blk[j] >> 4) & 15 : blk[j] & 15;
+        }
+    } else if (pbits == 2) {
+        // sml/sml-kernel.c:243-250: pack of 32 bytes per 128 weights, bit-plane
+        // k of byte j is weight 128p + 32k + j
+        const uint8_t * cp = plane + (size_t) row * (cols / 4);
+        for (int col = 0; col < cols; col++) {
+            const int p = col / 128, k = (col % 128) / 32, j = col % 32;
+            out[col] = (cp[(size_t) p * 32 + j] >> (2 * k)) & 3;
+        }
+    } else {
+        // sml/sml-kernel.c:2164-2169: 4 bytes per group, bit j = weight j
+        const uint8_t * cp = plane + (size_t) row * (cols / 8);
+        for (int col = 0; col < cols; col++) {
+            const int g = col / 32, j = col % 32;
+            out[col] = (cp[(size_t) g * 4 + (j >> 3)] >> (j & 7)) & 1;
+        }
+    }
+}
+
+void orc_unpack_row(const orc_tensor * t, int row, uint8_t * codes) {
+    const int n = t->cols;
+    int * a = malloc((size_t) n * sizeof(int)), * b = malloc((size_t) n * sizeof(int));
+    for (int i = 0; i < n; i++) codes[i] = 0;
+    switch (t->nbits) {
+    case 2:
+        plane_bits(t->plane[0], 2, row, n, a);
+        for (int i = 0; i < n; i++) codes[i] = (uint8_t) a[i];
+        break;
+    case 3: // 2-bit plane + 4 * 1-bit plane (sml/sml-run.c:589-592)
+        plane_bits(t->plane[0], 2, row, n, a);
+        plane_bits(t->plane[1], 1, row, n, b);
+        for (int i = 0; i < n; i++) codes[i] = (uint8_t) (a[i] | (b[i] << 2));
+        break;
+    case 4:
+        plane_bits(t->plane[0], 4, row, n, a);
+        for (int i = 0; i < n; i++) codes[i] = (uint8_t) a[i];
+        break;
+    case 5: // nibble + 16 * 1-bit (sml/sml-run.c:593-595)
+        plane_bits(t->plane[0], 4, row, n, a);
+        plane_bits(t->plane[1], 1, row, n, b);
+        for (int i = 0; i < n; i++) codes[i] = (uint8_t) (a[i] | (b[i] << 4));
+        break;
+    case 6: // plane 0 = 2-bit high part, plane 1 = nibble (sml/sml-run.c:3319-3326)
+        plane_bits(t->plane[0], 2, row, n, a);
+        plane_bits(t->plane[1], 4, row, n, b);
+        for (int i = 0; i < n; i++) codes[i] = (uint8_t) (b[i] | (a[i] << 4));
+        break;
+    case 7: { // nibble + 16 * 2-bit + 64 * 1-bit (sml/sml-run.c:596-602)
+        int * c = malloc((size_t) n * sizeof(int));
+        plane_bits(t->plane[0], 4, row, n, a);
+        plane_bits(t->plane[1], 2, row, n, b);
+        plane_bits(t->plane[2], 1, row, n, c);
+        for (int i = 0; i < n; i++) codes[i] = (uint8_t) (a[i] | (b[i] << 4) | (c[i] << 6));
+        free(c);
+        break;
+    }
+    case 8: // low + 16 * high nibble planes (sml/sml-kernel.c:2185-2197)
+        plane_bits(t->plane[0], 4, row, n, a);
+        plane_bits(t->plane[1], 4, row, n, b);
+        for (int i = 0; i < n; i++) codes[i] = (uint8_t) (a[i] | (b[i] << 4));
+        break;
+    default:
+        break;
+    }
+    free(a); free(b);
+}
+
+void orc_dequant_row(const orc_tensor * t, int row, float * out) {
+    uint8_t * c = malloc((size_t) t->cols);
+    orc_unpack_row(t, row, c);
+    for (int g = 0; g < t->cols / 32; g++) {
+        const float st = orc_step(t, row, g), mn = orc_min(t, row, g);
+        for (int j = 0; j < 32; j++) out[g * 32 + j] = (float) c[g * 32 + j] * st + mn;
+    }
+    free(c);
+}
+
+// sml/sml-kernel.c:2027-2066 per group: sum += ws * s_g * dot; sum += mn * s_g * sum_g
+void orc_matvec(const orc_tensor * t, const int8_t * q, const float * scale, const int32_t * sums,
+                float * y, int row0, int row1) {
+    const int n = t->cols, ng = n / 32;
+    #pragma omp parallel
+    {
+        uint8_t * c = malloc((size_t) n);
+        #pragma omp for schedule(static)
+        for (int r = row0; r < row1; r++) {
+            orc_unpack_row(t, r, c);
+            float sum = 0.0f;
+            for (int g = 0; g < ng; g++) {
+                int32_t d = 0;
+                for (int j = 0; j < 32; j++) d += (int32_t) c[g * 32 + j] * (int32_t) q[g * 32 + j];
+                sum += orc_step(t, r, g) * scale[g] * (float) d;
+                if (t->mq) sum += orc_min(t, r, g) * scale[g] * (float) sums[g];
+            }
+            y[r] = sum;
+        }
+        free(c);
+    }
+}
+
+// ------------------------------------------------------------ small ops
+
+void orc_rms_norm(float * out, const float * x, const float * w, int n, float eps) {
+    double ss = 0.0;
+    for (int i = 0; i < n; i++) ss += (double) x[i] * x[i];
+    const float s = 1.0f / sqrtf((float) (ss / n) + eps);
+    for (int i = 0; i < n; i++) out[i] = x[i] * s * w[i];
+}
+
+void orc_rope_table(float theta, int half, int n_ctx, float * cos_t, float * sin_t) {
+    for (int p = 0; p < n_ctx; p++)
+        for (int i = 0; i < half; i++) {
+            const float freq = powf(theta, -(float) i / (float) half);
+            const float a = (float) p * freq;
+            cos_t[(size_t) p * half + i] = cosf(a);
+            sin_t[(size_t) p * half + i] = sinf(a);
+        }
+}
+
+void orc_rope(float * x, int n_head, int head_dim, int half, const float * cs, const float * sn) {
+    for (int h = 0; h < n_head; h++) {
+        float * v = x + (size_t) h * head_dim;
+        for (int i = 0; i < half; i++) {
+            const float x0 = v[i], x1 = v[i + half];
+            v[i] = x0 * cs[i] - x1 * sn[i];
+            v[i + half] = x0 * sn[i] + x1 * cs[i];
+        }
+    }
+}
+
+// sml/sml-run.c:242-266 scalar arm + softmax :280-287
+void orc_attn_head(const float * qh, const uint16_t * kc, const uint16_t * vc, size_t stride,
+                   int pos, int hd, float inv, float * a, float * out) {
+    for (int t = 0; t <= pos; t++) {
+        const uint16_t * kh = kc + (size_t) t * stride;
+        float s = 0.0f;
+        for (int i = 0; i < hd; i++) s += qh[i] * orc_f16_to_f32(kh[i]);
+        a[t] = s * inv;
+    }
+    float mx = a[0];
+    for (int i = 1; i <= pos; i++) if (a[i] > mx) mx = a[i];
+    float sum = 0.0f;
+    for (int i = 0; i <= pos; i++) { a[i] = expf(a[i] - mx); sum += a[i]; }
+    const float iv = 1.0f / sum;
+    for (int i = 0; i <= pos; i++) a[i] *= iv;
+    for (int i = 0; i < hd; i++) out[i] = 0.0f;
+    for (int u = 0; u <= pos; u++) {
+        const uint16_t * vh = vc + (size_t) u * stride;
+        for (int i = 0; i < hd; i++) out[i] += a[u] * orc_f16_to_f32(vh[i]);
+    }
+}
+
+void orc_silu_mul(float * g, const float * u, int n) {
+    for (int i = 0; i < n; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+}
+
+int orc_moe_route(const float * lg, int ne, int k, unsigned moe_flags, int * sel, float * w) {
+    if (k <= 0 || k > ne) k = ne;
+    for (int j = 0; j < k; j++) {
+        int best = -1;
+        for (int e = 0; e < ne; e++) {
+            int taken = 0;
+            for (int q = 0; q < j; q++) if (sel[q] == e) taken = 1;
+            if (!taken && (best < 0 || lg[e] > lg[best])) best = e;
+        }
+        sel[j] = best;
+    }
+    if (moe_flags & 1u) {
+        double sum = 0.0;
+        for (int j = 0; j < k; j++) { w[j] = expf(lg[sel[j]] - lg[sel[0]]); sum += w[j]; }
+        for (int j = 0; j < k; j++) w[j] = (float) (w[j] / sum);
+    } else {
+        float mx = lg[0];
+        for (int e = 1; e < ne; e++) if (lg[e] > mx) mx = lg[e];
+        double sum = 0.0;
+        for (int e = 0; e < ne; e++) sum += expf(lg[e] - mx);
+        for (int j = 0; j < k; j++) w[j] = (float) (expf(lg[sel[j]] - mx) / sum);
+    }
+    return k;
+}
+
+void orc_router(const float * router, const float * x, int ne, int n_embd, float * lg) {
+    for (int e = 0; e < ne; e++) {
+        double s = 0.0;
+        for (int i = 0; i < n_embd; i++) s += (double) router[(size_t) e * n_embd + i] * x[i];
+        lg[e] = (float) s;
+    }
+}
+
+int orc_argmax(const float * logits, int n) {
+    int best = 0;
+    float bv = logits[0];
+    for (int i = 1; i < n; i++) if (logits[i] > bv) { bv = logits[i]; best = i; }
+    return best;
+}
+
+// ------------------------------------------------------------ decoder
+
+// The oracle reads the file with its own parser: offsets of the packed
+// header and record structs (sml/sml-model.h:78-160), independent of the GPU
+// library's reader.
+#define H_N_LAYER 8
+#define REC_SIZE 248
+
+typedef struct {
+    char name[64];
+    uint32_t kind, rows, cols;
+    uint64_t f32_off, sd_off, sq_off, perm_off, md_off, mq_off, mq_n;
+    uint64_t plane_off[4];
+    uint32_t nbits;
+} orec;
+
+typedef struct {
+    const orec * q, * k, * v, * o, * gate, * up, * down;
+    const float * an, * fn, * qb, * kb, * vb;
+    const float * router;
+    int ne;
+    const orec ** eg, ** eu, ** ed;
+} olayer;
+
+struct orc_model {
+    const uint8_t * base;
+    size_t size;
+    uint32_t n_layer, n_embd, n_head, n_kv, n_ff, n_vocab;
+    float theta, eps;
+    uint32_t flags, n_expert_used, moe_flags;
+    int n_ctx, hd, half;
+    orec * recs;
+    int nrec;
+    olayer * L;
+    const orec * emb, * head;
+    const float * out_norm;
+    float * rc, * rs;
+    uint16_t * kc, * vc;
+    float * x, * xb, * xg, * q, * k, * v, * att, * hb, * hb2, * logits, * acc, * tmp;
+    int8_t * aq;
+    float * as;
+    int32_t * asum;
+};
+
+static uint32_t rd32(const uint8_t * p) { uint32_t v; memcpy(&v, p, 4); return v; }
+static uint64_t rd64(const uint8_t * p) { uint64_t v; memcpy(&v, p, 8); return v; }
+static float rdf(const uint8_t * p) { float v; memcpy(&v, p, 4); return v; }
+
+static const orec * findrec(const orc_model * m, const char * fmt, int a, int b) {
+    char nm[96];
+    snprintf(nm, sizeof nm, fmt, a, b);
+    for (int i = 0; i < m->nrec; i++) if (strncmp(m->recs[i].name, nm, 64) == 0) return &m->recs[i];
+    return NULL;
+}
+
+static orc_tensor view(const orc_model * m, const orec * r) {
+    orc_tensor t;
+    memset(&t, 0, sizeof t);
+    for (int i = 0; i < 4; i++) t.plane[i] = r->plane_off[i] ? m->base + r->plane_off[i] : NULL;
+    t.sd = (const uint16_t *) (m->base + r->sd_off);
+    t.sq = m->base + r->sq_off;
+    t.md = r->mq_n ? (const uint16_t *) (m->base + r->md_off) : NULL;
+    t.mq = r->mq_n ? m->base + r->mq_off : NULL;
+    t.rows = (int) r->rows; t.cols = (int) r->cols; t.nbits = (int) r->nbits;
+    t.scale6 = (m->flags & 2u) != 0;
+    t.minneg = (m->flags & 4u) != 0;
+    return t;
+}
+
+int orc_model_tensor(const orc_model * m, const char * name, orc_tensor * out, const int32_t ** perm) {
+    for (int i = 0; i < m->nrec; i++)
+        if (strncmp(m->recs[i].name, name, 64) == 0) {
+            *out = view(m, &m->recs[i]);
+            if (perm) *perm = (const int32_t *) (m->base + m->recs[i].perm_off);
+            return 1;
+        }
+    return 0;
+}
+
+orc_model * orc_model_open(const char * path, int n_ctx) {
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) return NULL;
+    struct stat st;
+    if (fstat(fd, &st) != 0) { close(fd); return NULL; }
+    void * base = mmap(NULL, (size_t) st.st_size, PROT_READ, MAP_SHARED, fd, 0);
+    close(fd);
+    if (base == MAP_FAILED) return NULL;
+    orc_model * m = calloc(1, sizeof *m);
+    const uint8_t * h = (const uint8_t *) base;
+    m->base = h; m->size = (size_t) st.st_size;
+    // header offsets (packed): magic 0, version 4, n_layer 8 .. n_ctx_train 32,
+    // rope_theta 36, rms_eps 40, group 44, n_levels 48, level_bits 52..67,
+    // n_tensors 68, table_off 76, ..., flags 152, n_expert_used 168, moe_flags 172
+    m->n_layer = rd32(h + 8); m->n_embd = rd32(h + 12); m->n_head = rd32(h + 16);
+    m->n_kv = rd32(h + 20); m->n_ff = rd32(h + 24); m->n_vocab = rd32(h + 28);
+    m->theta = rdf(h + 36); m->eps = rdf(h + 40);
+    const uint64_t nt = rd64(h + 68), toff = rd64(h + 76);
+    m->flags = rd32(h + 152);
+    m->n_expert_used = rd32(h + 168); m->moe_flags = rd32(h + 172);
+    m->nrec = (int) nt;
+    m->recs = calloc((size_t) nt, sizeof(orec));
+    for (uint64_t i = 0; i < nt; i++) {
+        const uint8_t * r = h + toff + i * REC_SIZE;
+        orec * o = &m->recs[i];
+        memcpy(o->name, r, 64);
+        o->kind = rd32(r + 64); o->rows = rd32(r + 68); o->cols = rd32(r + 72);
+        o->f32_off = rd64(r + 80);
+        o->sd_off = rd64(r + 96); o->sq_off = rd64(r + 112); o->perm_off = rd64(r + 128);
+        o->md_off = rd64(r + 144); o->mq_off = rd64(r + 160); o->mq_n = rd64(r + 168);
+        for (int j = 0; j < 4; j++) o->plane_off[j] = rd64(r + 176 + 8 * j);
+        o->nbits = rd32(r + 244);
+    }
+    m->n_ctx = n_ctx;
+    m->hd = (int) (m->n_embd / m->n_head);
+    const orec * q0 = findrec(m, "blk.%d.attn_q.weight", 0, 0);
+    if (q0 && q0->rows % m->n_head == 0) m->hd = (int) (q0->rows / m->n_head);
+    m->half = m->hd / 2;
+    m->emb = findrec(m, "token_embd.weight", 0, 0);
+    m->head = findrec(m, "output.weight", 0, 0);
+    if (!m->head) m->head = m->emb;
+    const orec * on = findrec(m, "output_norm.weight", 0, 0);
+    m->out_norm = on ? (const float *) (h + on->f32_off) : NULL;
+    m->L = calloc(m->n_layer, sizeof(olayer));
+    for (int L = 0; L < (int) m->n_layer; L++) {
+        olayer * y = &m->L[L];
+        y->q = findrec(m, "blk.%d.attn_q.weight", L, 0);
+        y->k = findrec(m, "blk.%d.attn_k.weight", L, 0);
+        y->v = findrec(m, "blk.%d.attn_v.weight", L, 0);
+        y->o = findrec(m, "blk.%d.attn_output.weight", L, 0);
+        const orec * r;
+        y->an = (r = findrec(m, "blk.%d.attn_norm.weight", L, 0)) ? (const float *) (h + r->f32_off) : NULL;
+        y->fn = (r = findrec(m, "blk.%d.ffn_norm.weight", L, 0)) ? (const float *) (h + r->f32_off) : NULL;
+        y->qb = (r = findrec(m, "blk.%d.attn_q.bias", L, 0)) ? (const float *) (h + r->f32_off) : NULL;
+        y->kb = (r = findrec(m, "blk.%d.attn_k.bias", L, 0)) ? (const float *) (h + r->f32_off) : NULL;
+        y->vb = (r = findrec(m, "blk.%d.attn_v.bias", L, 0)) ? (const float *) (h + r->f32_off) : NULL;
+        y->gate = findrec(m, "blk.%d.ffn_gate.weight", L, 0);
+        y->up = findrec(m, "blk.%d.ffn_up.weight", L, 0);
+        y->down = findrec(m, "blk.%d.ffn_down.weight", L, 0);
+        const orec * rt = findrec(m, "blk.%d.ffn_gate_inp.weight", L, 0);
+        if (rt) {
+            y->router = (const float *) (h + rt->f32_off);
+            y->ne = (int) (((uint64_t) rt->rows * rt->cols) / m->n_embd);
+            y->eg = calloc((size_t) y->ne, sizeof(orec *));
+            y->eu = calloc((size_t) y->ne, sizeof(orec *));
+            y->ed = calloc((size_t) y->ne, sizeof(orec *));
+            for (int e = 0; e < y->ne; e++) {
+                y->eg[e] = findrec(m, "blk.%d.ffn_gate.%d.weight", L, e);
+                y->eu[e] = findrec(m, "blk.%d.ffn_up.%d.weight", L, e);
+                y->ed[e] = findrec(m, "blk.%d.ffn_down.%d.weight", L, e);
+            }
+        }
+    }
+    m->rc = malloc((size_t) n_ctx * m->half * sizeof(float));
+    m->rs = malloc((size_t) n_ctx * m->half * sizeof(float));
+    orc_rope_table(m->theta, m->half, n_ctx, m->rc, m->rs);
+    const size_t kvd = (size_t) m->n_kv * m->hd;
+    m->kc = calloc((size_t) m->n_layer * n_ctx * kvd, 2);
+    m->vc = calloc((size_t) m->n_layer * n_ctx * kvd, 2);
+    size_t wide = m->n_ff > m->n_embd ? m->n_ff : m->n_embd;
+    if ((size_t) m->n_head * m->hd > wide) wide = (size_t) m->n_head * m->hd;
+    m->x = calloc(wide, 4); m->xb = calloc(wide, 4); m->xg = calloc(wide, 4);
+    m->q = calloc((size_t) m->n_head * m->hd, 4); m->k = calloc(kvd, 4); m->v = calloc(kvd, 4);
+    m->att = calloc((size_t) n_ctx, 4);
+    m->hb = calloc(wide, 4); m->hb2 = calloc(wide, 4);
+    m->acc = calloc(wide, 4); m->tmp = calloc(wide, 4);
+    m->logits = calloc(m->n_vocab, 4);
+    m->aq = calloc(wide, 1); m->as = calloc(wide / 32, 4); m->asum = calloc(wide / 32, 4);
+    return m;
+}
+
+void orc_model_close(orc_model * m) {
+    if (!m) return;
+    for (int L = 0; L < (int) m->n_layer; L++) { free(m->L[L].eg); free(m->L[L].eu); free(m->L[L].ed); }
+    free(m->L); free(m->recs); free(m->rc); free(m->rs); free(m->kc); free(m->vc);
+    free(m->x); free(m->xb); free(m->xg); free(m->q); free(m->k); free(m->v); free(m->att);
+    free(m->hb); free(m->hb2); free(m->acc); free(m->tmp); free(m->logits);
+    free(m->aq); free(m->as); free(m->asum);
+    munmap((void *) m->base, m->size);
+    free(m);
+}
+
+int orc_n_vocab(const orc_model * m) { return (int) m->n_vocab; }
+
+// ORC_DUMP=<file> appends the residual after the embedding and after every
+// layer, in the reference's SML_DUMP format (sml/sml-run.c:2696-2703)
+static void dump_x(const float * x, int n) {
+    const char * p = getenv("ORC_DUMP");
+    if (!p) return;
+    FILE * f = fopen(p, "ab");
+    if (!f) return;
+    fwrite(x, sizeof(float), (size_t) n, f);
+    fclose(f);
+}
+
+// gather through the tensor's permutation, quantize, matvec (sml/sml-run.c:711-757)
+static void mv(orc_model * m, const orec * r, const float * x, float * y) {
+    const int n = (int) r->cols;
+    const int32_t * perm = (const int32_t *) (m->base + r->perm_off);
+    for (int i = 0; i < n; i++) m->xg[i] = x[perm[i]];
+    orc_quantize_act(m->xg, n, m->aq, m->as, m->asum);
+    orc_tensor t = view(m, r);
+    orc_matvec(&t, m->aq, m->as, m->asum, y, 0, (int) r->rows);
+}
+
+const float * orc_forward(orc_model * m, int token, int pos) {
+    const int E = (int) m->n_embd, H = (int) m->n_head, KV = (int) m->n_kv, hd = m->hd;
+    const int kvd = KV * hd, rep = H / KV, F = (int) m->n_ff;
+    // embedding: dequantized row, scattered back through the permutation (sml/sml-run.c:3291-3344)
+    {
+        orc_tensor t = view(m, m->emb);
+        orc_dequant_row(&t, token, m->xb);
+        const int32_t * perm = (const int32_t *) (m->base + m->emb->perm_off);
+        for (int i = 0; i < E; i++) m->x[perm[i]] = m->xb[i];
+        dump_x(m->x, E);
+    }
+    for (int L = 0; L < (int) m->n_layer; L++) {
+        const olayer * y = &m->L[L];
+        orc_rms_norm(m->xb, m->x, y->an, E, m->eps);
+        mv(m, y->q, m->xb, m->q);
+        mv(m, y->k, m->xb, m->k);
+        mv(m, y->v, m->xb, m->v);
+        if (y->qb) for (int i = 0; i < H * hd; i++) m->q[i] += y->qb[i];
+        if (y->kb) for (int i = 0; i < kvd; i++) m->k[i] += y->kb[i];
+        if (y->vb) for (int i = 0; i < kvd; i++) m->v[i] += y->vb[i];
+        orc_rope(m->q, H, hd, m->half, m->rc + (size_t) pos * m->half, m->rs + (size_t) pos * m->half);
+        orc_rope(m->k, KV, hd, m->half, m->rc + (size_t) pos * m->half, m->rs + (size_t) pos * m->half);
+        uint16_t * kl = m->kc + (size_t) L * m->n_ctx * kvd, * vl = m->vc + (size_t) L * m->n_ctx * kvd;
+        for (int i = 0; i < kvd; i++) {
+            kl[(size_t) pos * kvd + i] = orc_f32_to_f16(m->k[i]);
+            vl[(size_t) pos * kvd + i] = orc_f32_to_f16(m->v[i]);
+        }
+        const float inv = 1.0f / sqrtf((float) hd);
+        for (int h = 0; h < H; h++) {
+            const int kh = h / rep;
+            orc_attn_head(m->q + (size_t) h * hd, kl + (size_t) kh * hd, vl + (size_t) kh * hd, (size_t) kvd,
+                          pos, hd, inv, m->att, m->xb + (size_t) h * hd);
+        }
+        mv(m, y->o, m->xb, m->hb2);
+        for (int i = 0; i < E; i++) m->x[i] += m->hb2[i];
+        orc_rms_norm(m->xb, m->x, y->fn, E, m->eps);
+        if (y->ne) {
+            // sml/sml-run.c:3071-3124: router in double, route, experts summed in choice order
+            float lg[64];
+            int sel[8];
+            float w[8];
+            orc_router(y->router, m->xb, y->ne, E, lg);
+            const int k = orc_moe_route(lg, y->ne, (int) m->n_expert_used, m->moe_flags, sel, w);
+            for (int i = 0; i < E; i++) m->acc[i] = 0.0f;
+            for (int j = 0; j < k; j++) {
+                const int e = sel[j];
+                const int fe = (int) y->eu[e]->rows;
+                mv(m, y->eg[e], m->xb, m->hb);
+                mv(m, y->eu[e], m->xb, m->hb2);
+                orc_silu_mul(m->hb, m->hb2, fe);
+                mv(m, y->ed[e], m->hb, m->tmp);
+                for (int i = 0; i < E; i++) m->acc[i] += w[j] * m->tmp[i];
+            }
+            for (int i = 0; i < E; i++) m->x[i] += m->acc[i];
+            dump_x(m->x, E);
+            continue;
+        }
+        mv(m, y->gate, m->xb, m->hb);
+        mv(m, y->up, m->xb, m->hb2);
+        orc_silu_mul(m->hb, m->hb2, F);
+        mv(m, y->down, m->hb, m->xb);
+        for (int i = 0; i < E; i++) m->x[i] += m->xb[i];
+        dump_x(m->x, E);
+    }
+    orc_rms_norm(m->xb, m->x, m->out_norm, E, m->eps);
+    mv(m, m->head, m->xb, m->logits);
+    return m->logits;
+}

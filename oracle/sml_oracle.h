@@ -1,0 +1,105 @@
+// CPU ORACLE — test infrastructure only.
+//
+// A plain-C restatement of the reference SML engine's CPU path for the
+// quantized decode hot path. Only tests/, __graft_entry__.smoke() and
+// bench.py's cpu_baseline leg may load it, and only as the checker or the
+// reported CPU baseline: the GPU library never links, calls or falls back to
+// anything here.
+//
+// Every function names the reference file:line it follows. How each one is
+// pinned (reference build, closed forms, brute force) is listed in the tests
+// that exercise it; none is left unpinned.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Activation quantization, one scale per 32 values.
+// follows sml/sml-kernel.c:86-106 (scalar arm; the AVX2 arm at :44-85 is the
+// same arithmetic bit for bit)
+void orc_quantize_act(const float * x, int n, int8_t * q, float * scale, int32_t * sums);
+// One scale per 256 values, written into every group of the superblock.
+// follows sml/sml-kernel.c:165-184
+void orc_quantize_act_sb(const float * x, int n, int8_t * q, float * scale, int32_t * sums);
+
+// A quantized FLAT tensor as stored in the file: planes in storage order and the
+// four field arrays. scale6 / minneg are the file flags (sml/sml-kernel.h:64-98).
+typedef struct {
+    const uint8_t  * plane[4];
+    const uint16_t * sd;
+    const uint8_t  * sq;
+    const uint16_t * md;      // NULL: symmetric file (no min)
+    const uint8_t  * mq;
+    int rows, cols, nbits;
+    int scale6, minneg;
+} orc_tensor;
+
+// Integer code of every weight of one row (permuted column order).
+// Plane order follows tooling/sml_quantize.py:104-106 (FLAT_PLANES) and the
+// reads follow sml/sml-kernel.c:231-263 (2-bit), :2134-2157 (nibbles),
+// :2160-2170 (1-bit), :2174-2198 (Q8), :2235-2260 (Q6), dispatched as
+// sml/sml-run.c:586-603,3300-3335.
+void orc_unpack_row(const orc_tensor * t, int row, uint8_t * codes);
+
+// Group g's step and min of one row: step = f16(sd)*sq, min = f16(md)*(mq - bias),
+// bias 127 (8-bit fields), 31 (6-bit), 63 (6-bit negative-only).
+// follows sml/sml-kernel.c:206-215,254-258,2146-2149
+float orc_step(const orc_tensor * t, int row, int g);
+float orc_min(const orc_tensor * t, int row, int g);
+
+// One row dequantized, code*step + min, in permuted order.
+// follows sml/sml-kernel.c:2134-2157 (and the per-width forms listed above)
+void orc_dequant_row(const orc_tensor * t, int row, float * out);
+
+// y[r] = sum over groups of step*s*dot + min*s*sum  for r in [row0, row1), no
+// accumulation into y (callers of the reference zero y first, sml/sml-run.c:757).
+// The per-group arithmetic follows the scalar arm sml/sml-kernel.c:2027-2066
+// (flat4) and :1934-1971 (2-bit planes), with the plane dispatch of
+// sml/sml-run.c:612-680 folded into one integer dot over the unpacked code
+// (the code is linear in its planes, so the integer dot is the same number).
+void orc_matvec(const orc_tensor * t, const int8_t * q, const float * scale, const int32_t * sums,
+                float * y, int row0, int row1);
+
+// RMSNorm with a double sum of squares. follows sml/sml-run.c:147-152
+void orc_rms_norm(float * out, const float * x, const float * w, int n, float eps);
+// cos/sin table, halved pairs. follows sml/sml-run.c:1383-1393
+void orc_rope_table(float theta, int half, int n_ctx, float * cos_t, float * sin_t);
+// follows sml/sml-run.c:339-372 (halved pairs branch)
+void orc_rope(float * x, int n_head, int head_dim, int half, const float * cos_row, const float * sin_row);
+// fp16 round-to-nearest-even encode / decode. follows sml/sml-run.c:68-77,85-109
+uint16_t orc_f32_to_f16(float f);
+float    orc_f16_to_f32(uint16_t h);
+// Decode attention of one head over positions [0, pos], keys/values fp16,
+// `stride` halves apart. follows sml/sml-run.c:180-266 (scalar arm) and
+// softmax :280-287
+void orc_attn_head(const float * qh, const uint16_t * kc, const uint16_t * vc, size_t stride,
+                   int pos, int hd, float inv, float * scratch, float * out);
+// g = g/(1+exp(-g)) * u. follows sml/sml-run.c:451-454
+void orc_silu_mul(float * g, const float * u, int n);
+// Top-k routing, ties to the lower index; moe_flags bit 0 renormalises over
+// the chosen. follows sml/sml-run.c:3010-3035
+int orc_moe_route(const float * lg, int ne, int k, unsigned moe_flags, int * sel, float * w);
+// Router logits with a double accumulator. follows sml/sml-run.c:3075-3080
+void orc_router(const float * router, const float * x, int ne, int n_embd, float * lg);
+// First-max greedy pick. follows sml/sml-run.c:3539-3544
+int orc_argmax(const float * logits, int n);
+
+// ---------------------------------------------------------------- decoder
+// A whole decode step over an SSF file (Llama / Qwen2 / Mixtral family: RMSNorm,
+// halved RoPE, GQA, SwiGLU, optional q/k/v bias, tied or untied head, top-k MoE).
+// follows sml/sml-run.c:3243-3523 for those features.
+typedef struct orc_model orc_model;
+orc_model * orc_model_open(const char * path, int n_ctx);
+void        orc_model_close(orc_model * m);
+// logits of token at position pos (positions must be fed in order from 0)
+const float * orc_forward(orc_model * m, int token, int pos);
+int orc_n_vocab(const orc_model * m);
+// Tensor view by name, for single-matrix checks.
+int orc_model_tensor(const orc_model * m, const char * name, orc_tensor * out, const int32_t ** perm);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,273 @@
+"""MI355X-native SML decode path: ctypes bindings over libsmlhip.so.
+
+The library (built from sheep_amd/csrc by __graft_entry__.build()) carries the
+C host and the gfx950 code object. Nothing here computes on the CPU in place of
+the GPU: if the library is missing, every entry point raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsmlhip.so")
+
+_lib = None
+
+c_int, c_float, c_size_t, c_char_p, c_void_p = ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_void_p
+c_long, c_uint64 = ctypes.c_long, ctypes.c_uint64
+P = ctypes.POINTER
+
+
+class SynthSpec(ctypes.Structure):
+    """ssf_synth_spec (sheep_amd/csrc/ssf.h)."""
+    _fields_ = [("n_layer", ctypes.c_uint32), ("n_embd", ctypes.c_uint32), ("n_head", ctypes.c_uint32),
+                ("n_head_kv", ctypes.c_uint32), ("n_ff", ctypes.c_uint32), ("n_vocab", ctypes.c_uint32),
+                ("n_ctx_train", ctypes.c_uint32), ("rope_theta", c_float), ("rms_eps", c_float),
+                ("nbits", c_int), ("tied", c_int), ("qkv_bias", c_int), ("random_perm", c_int),
+                ("n_expert", c_int), ("n_expert_used", c_int), ("moe_flags", ctypes.c_uint32),
+                ("step_sigma", c_float), ("router_sigma", c_float), ("seed", c_uint64)]
+
+
+# (name, restype, argtypes) of every export
+_SIGS = [
+    ("sml_gpu_open", c_int, [c_char_p, c_int, c_int, c_int, c_char_p, c_int]),
+    ("sml_gpu_prefill", P(c_float), [P(c_int), c_int, c_int]),
+    ("sml_gpu_step", P(c_float), [c_int, c_int]),
+    ("sml_gpu_layers", c_int, [P(c_int)]),
+    ("sml_gpu_prompt_mode", None, [c_int]),
+    ("sml_gpu_decode_cpu", c_int, [c_int]),
+    ("sml_gpu_set_middle", None, [c_int, c_void_p]),
+    ("sml_gpu_close", None, []),
+    ("sml_gpu_generate", c_int, [c_int, c_int, c_int, P(c_int)]),
+    ("sml_gpu_last_ms", c_float, []),
+    ("sml_gpu_weight_bytes", c_uint64, []),
+    ("sml_gpu_last_error", c_char_p, []),
+    ("sml_hip_init", c_int, [c_int, c_char_p, c_int]),
+    ("sml_hip_last_error", c_char_p, []),
+    ("sml_hip_malloc", c_void_p, [c_size_t]),
+    ("sml_hip_free", c_int, [c_void_p]),
+    ("sml_hip_h2d", c_int, [c_void_p, c_void_p, c_size_t]),
+    ("sml_hip_d2h", c_int, [c_void_p, c_void_p, c_size_t]),
+    ("sml_hip_memset", c_int, [c_void_p, c_int, c_size_t]),
+    ("sml_hip_sync", c_int, []),
+    ("sml_hip_fail_after", None, [c_long]),
+    ("sml_hip_mat_upload", c_void_p, [P(c_void_p), c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int]),
+    ("sml_hip_mat_from_file", c_void_p, [c_char_p, c_char_p]),
+    ("sml_hip_mat_free", None, [c_void_p]),
+    ("sml_hip_mat_info", c_int, [c_void_p, P(c_int), P(c_int), P(c_int)]),
+    ("sml_hip_mat_bytes", c_size_t, [c_void_p]),
+    ("sml_hip_normq", c_int, [c_void_p, c_void_p, c_void_p, c_float, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int]),
+    ("sml_hip_matvec", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("sml_hip_matvec_swiglu", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("sml_hip_time_matvec", c_int, [P(c_void_p), c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, P(c_float)]),
+    ("sml_hip_unpack", c_int, [c_void_p, c_int, c_int, c_void_p]),
+    ("sml_hip_embed", c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("sml_hip_attn_part_floats", c_size_t, [c_int, c_int, c_int]),
+    ("sml_hip_attention", c_int, [c_void_p] * 8 + [c_int] * 4 + [c_void_p, c_void_p]),
+    ("sml_hip_argmax", c_int, [c_void_p, c_int, c_void_p]),
+    ("ssf_synth_model", c_int, [c_char_p, P(SynthSpec), c_char_p, c_int]),
+    ("ssf_synth_matrix", c_int, [c_char_p, c_int, c_int, c_int, c_int, c_float, c_uint64, c_char_p, c_int]),
+    ("ssf_f32_to_f16", ctypes.c_uint16, [c_float]),
+    ("ssf_f16_to_f32", c_float, [ctypes.c_uint16]),
+]
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, res, args in _SIGS:
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def _chk(rc, what="call"):
+    if rc != 0:
+        raise HipError(f"{what}: {lib().sml_hip_last_error().decode(errors='replace')}")
+
+
+def init(device=0):
+    why = ctypes.create_string_buffer(512)
+    if not lib().sml_hip_init(device, why, 512):
+        raise HipError(f"init: {lib().sml_hip_last_error().decode(errors='replace')}")
+
+
+class DevBuf:
+    """A device allocation owned by the library's HIP runtime."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = lib().sml_hip_malloc(max(1, self.nbytes))
+        if not self.ptr:
+            raise HipError(f"malloc: {lib().sml_hip_last_error().decode(errors='replace')}")
+
+    @classmethod
+    def of(cls, arr):
+        a = np.ascontiguousarray(arr)
+        b = cls(a.nbytes)
+        b.write(a)
+        return b
+
+    def write(self, a):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        _chk(lib().sml_hip_h2d(self.ptr, a.ctypes.data, a.nbytes), "h2d")
+
+    def read(self, dtype, count=None):
+        dtype = np.dtype(dtype)
+        n = self.nbytes // dtype.itemsize if count is None else int(count)
+        out = np.empty(n, dtype=dtype)
+        _chk(lib().sml_hip_d2h(out.ctypes.data, self.ptr, out.nbytes), "d2h")
+        return out
+
+    def zero(self):
+        _chk(lib().sml_hip_memset(self.ptr, 0, self.nbytes), "memset")
+
+    def free(self):
+        if self.ptr:
+            lib().sml_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Mat:
+    """A quantized FLAT matrix resident in HBM."""
+
+    def __init__(self, handle):
+        if not handle:
+            raise HipError(f"matrix upload: {lib().sml_hip_last_error().decode(errors='replace')}")
+        self.h = handle
+        r, c, b = c_int(), c_int(), c_int()
+        lib().sml_hip_mat_info(handle, ctypes.byref(r), ctypes.byref(c), ctypes.byref(b))
+        self.rows, self.cols, self.nbits = r.value, c.value, b.value
+        self.bytes = lib().sml_hip_mat_bytes(handle)
+
+    @classmethod
+    def from_file(cls, path, name):
+        return cls(lib().sml_hip_mat_from_file(str(path).encode(), name.encode()))
+
+    def free(self):
+        if self.h:
+            lib().sml_hip_mat_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Act:
+    """A quantized activation on the device: int8 codes, per-group scale and sum."""
+
+    def __init__(self, n):
+        self.n = n
+        self.q = DevBuf(n)
+        self.scale = DevBuf(n // 32 * 4)
+        self.sums = DevBuf(n // 32 * 4)
+
+    def read(self):
+        return (self.q.read(np.int8), self.scale.read(np.float32), self.sums.read(np.int32))
+
+
+def normq(x, act, perm=None, w=None, resid=None, eps=1e-6, per256=False):
+    """Device RMSNorm (w given) + gather + int8 quantize of device vector x."""
+    _chk(lib().sml_hip_normq(x.ptr, resid.ptr if resid else None, w.ptr if w else None, eps, act.n,
+                             perm.ptr if perm else None, act.q.ptr, act.scale.ptr, act.sums.ptr,
+                             1 if per256 else 0), "normq")
+
+
+def matvec(m, act, y):
+    _chk(lib().sml_hip_matvec(m.h, act.q.ptr, act.scale.ptr, act.sums.ptr, y.ptr), "matvec")
+
+
+def matvec_swiglu(gate, up, act, h):
+    _chk(lib().sml_hip_matvec_swiglu(gate.h, up.h, act.q.ptr, act.scale.ptr, act.sums.ptr, h.ptr), "swiglu")
+
+
+def unpack(m, row0, nrows):
+    out = DevBuf(max(1, nrows * m.cols))
+    _chk(lib().sml_hip_unpack(m.h, row0, nrows, out.ptr), "unpack")
+    return out.read(np.uint8, nrows * m.cols).reshape(nrows, m.cols)
+
+
+def sync():
+    _chk(lib().sml_hip_sync(), "sync")
+
+
+def synth_model(path, n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx_train=4096,
+                rope_theta=1e6, rms_eps=1e-6, nbits=4, tied=False, qkv_bias=False, random_perm=False,
+                n_expert=0, n_expert_used=0, moe_flags=0, step_sigma=0.02, router_sigma=1.0 / 64, seed=1):
+    """Write a seeded synthetic SSF decoder (sheep_amd/csrc/ssf.c)."""
+    sp = SynthSpec(n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx_train, rope_theta, rms_eps,
+                   nbits, int(tied), int(qkv_bias), int(random_perm), n_expert, n_expert_used, moe_flags,
+                   step_sigma, router_sigma, seed)
+    why = ctypes.create_string_buffer(512)
+    if not lib().ssf_synth_model(str(path).encode(), ctypes.byref(sp), why, 512):
+        raise RuntimeError(why.value.decode())
+    return path
+
+
+def synth_matrix(path, rows, cols, nbits=4, random_perm=False, step_sigma=0.02, seed=1):
+    """Write a seeded SSF file holding one quantized matrix named 'w'."""
+    why = ctypes.create_string_buffer(512)
+    if not lib().ssf_synth_matrix(str(path).encode(), rows, cols, nbits, int(random_perm), step_sigma, seed, why, 512):
+        raise RuntimeError(why.value.decode())
+    return path
+
+
+class Decoder:
+    """The sml-gpu.h forward pass: one model per process."""
+
+    def __init__(self, path, n_ctx=4096, gpu_layers=0):
+        why = ctypes.create_string_buffer(1024)
+        if not lib().sml_gpu_open(str(path).encode(), n_ctx, 1, gpu_layers, why, 1024):
+            raise HipError(f"sml_gpu_open: {why.value.decode(errors='replace')}")
+        of = c_int()
+        self.n_layer = lib().sml_gpu_layers(ctypes.byref(of))
+        self.n_ctx = n_ctx
+
+    def step(self, tok, pos, n_vocab):
+        p = lib().sml_gpu_step(tok, pos)
+        if not p:
+            raise HipError(f"sml_gpu_step: {lib().sml_gpu_last_error().decode(errors='replace')}")
+        return np.ctypeslib.as_array(p, shape=(n_vocab,)).copy()
+
+    def prefill(self, ids, pos0, n_vocab):
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        p = lib().sml_gpu_prefill(a.ctypes.data_as(P(c_int)), pos0, len(a))
+        if not p:
+            raise HipError(f"sml_gpu_prefill: {lib().sml_gpu_last_error().decode(errors='replace')}")
+        return np.ctypeslib.as_array(p, shape=(n_vocab,)).copy()
+
+    def generate(self, tok, pos, n):
+        out = np.zeros(n, dtype=np.int32)
+        if lib().sml_gpu_generate(tok, pos, n, out.ctypes.data_as(P(c_int))) != n:
+            raise HipError(f"sml_gpu_generate: {lib().sml_gpu_last_error().decode(errors='replace')}")
+        return out
+
+    def last_ms(self):
+        return lib().sml_gpu_last_ms()
+
+    def weight_bytes(self):
+        return lib().sml_gpu_weight_bytes()
+
+    def close(self):
+        lib().sml_gpu_close()

@@ -1,0 +1,495 @@
+// The GPU forward pass behind sml-gpu.h, MI355X-native.
+//
+// One model and one fp16 KV cache per process. A decode step is a fixed
+// sequence of gfx950 kernels on one stream -- embed, then per layer
+// normq / q-k-v GEMV / RoPE + KV write + split attention / quantize /
+// o GEMV + residual / normq / fused gate-up SwiGLU GEMV / quantize /
+// down GEMV + residual, then normq / head GEMV / argmax -- captured once into
+// HIP graphs and replayed per token. The token and position the graphs read
+// live in device memory (a token history array and a position scalar), so
+// greedy decoding needs no host round trip per token. The layer math follows
+// the reference's CPU forward pass (sml/sml-run.c:3243-3523) for the
+// Llama / Qwen2 family (RMSNorm, halved RoPE, GQA, SwiGLU, optional q/k/v
+// bias, tied or untied head); other architectures are refused at open by name.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "ops.h"
+#include "sml-gpu-ext.h"
+#include "sml-gpu.h"
+
+#define MAXACT 3
+
+typedef struct {
+    sml_hip_mat * w[3];        // q, k, v
+    sml_hip_mat * o, * gate, * up, * down;
+    float * bias[3];           // device q/k/v biases, or NULL
+    float * an, * fn;          // device norm weights
+    int perm_qkv[3], perm_o, perm_gu[2], perm_down;   // index into perms, -1 = identity
+} eng_layer;
+
+static struct {
+    int open;
+    int n_layer, E, H, KV, hd, F, V, n_ctx;
+    float eps;
+    eng_layer * L;
+    sml_hip_mat * emb, * head;
+    int perm_emb, perm_head;
+    float * out_norm;
+    int nperm;
+    int32_t * perm_dev[512];
+    const int32_t * perm_host[512];
+    int perm_len[512];
+    float * x, * q, * k, * v, * att, * hb, * hb2, * logits, * part, * rc, * rs;
+    int8_t * aq[MAXACT];
+    float * as[MAXACT];
+    int32_t * asum[MAXACT];
+    uint16_t * kc, * vc;
+    int32_t * hist, * pos, * tok;
+    float * lg_host;
+    int32_t * pin;             // pinned: [0] tok, [1] pos, [2..] prompt ids
+    hipStream_t st;
+    hipGraphExec_t g_body, g_tail, g_adv;
+    int use_graph;
+    hipEvent_t e0, e1;
+    float last_ms;
+    uint64_t weight_bytes;
+    int prompt_level;
+    void * dev[4096];          // every device allocation, freed at close
+    int ndev;
+    sml_hip_mat * mats[8192];
+    int nmats;
+} G;
+
+static int (*g_mid_fn)(float *, int, int);
+static int g_mid_layers;
+
+static void * dalloc(size_t n) {
+    if (G.ndev >= (int) (sizeof G.dev / sizeof G.dev[0])) hx_failf("too many device buffers");
+    void * p = hx_malloc(n);
+    G.dev[G.ndev++] = p;
+    return p;
+}
+
+static void * dupload(const void * src, size_t n) {
+    void * p = dalloc(n);
+    HX(hipMemcpy(p, src, n, hipMemcpyHostToDevice));
+    return p;
+}
+
+static sml_hip_mat * upmat(const ssf_file * f, const ssf_record * r) {
+    if (G.nmats >= (int) (sizeof G.mats / sizeof G.mats[0])) hx_failf("too many matrices");
+    sml_hip_mat * m = mat_from_record(f, r);
+    G.mats[G.nmats++] = m;
+    return m;
+}
+
+// Index of the record's permutation among the distinct ones uploaded; -1 for
+// the identity (the gather is skipped).
+static int perm_of(const ssf_file * f, const ssf_record * r) {
+    const int n = (int) r->cols;
+    if (!r->perm_bytes) return -1;
+    const int32_t * p = (const int32_t *) ssf_at(f, r->perm_off);
+    int ident = 1;
+    for (int i = 0; i < n && ident; i++) ident = p[i] == i;
+    if (ident) return -1;
+    for (int i = 0; i < G.nperm; i++)
+        if (G.perm_len[i] == n && (G.perm_host[i] == p || memcmp(G.perm_host[i], p, (size_t) n * 4) == 0)) return i;
+    if (G.nperm >= 512) hx_failf("too many distinct permutations");
+    for (int i = 0; i < n; i++) if (p[i] < 0 || p[i] >= n) hx_failf("%.64s: permutation out of range", r->name);
+    G.perm_host[G.nperm] = p;
+    G.perm_len[G.nperm] = n;
+    G.perm_dev[G.nperm] = dupload(p, (size_t) n * 4);
+    return G.nperm++;
+}
+
+static const int32_t * pdev(int i) { return i < 0 ? NULL : G.perm_dev[i]; }
+
+static float * f32_tensor(const ssf_file * f, const char * fmt, int L, int want) {
+    const ssf_record * r = ssf_findf(f, fmt, L);
+    if (!r) return NULL;
+    if (r->kind != SSF_KIND_F32 || (uint64_t) r->rows * r->cols != (uint64_t) want)
+        hx_failf("%.64s: expected %d f32 values", r->name, want);
+    return dupload(ssf_at(f, r->f32_off), (size_t) want * 4);
+}
+
+static const ssf_record * need(const ssf_file * f, const char * fmt, int L) {
+    const ssf_record * r = ssf_findf(f, fmt, L);
+    if (!r) {
+        char nm[96];
+        snprintf(nm, sizeof nm, fmt, L);
+        hx_failf("model has no %s", nm);
+    }
+    return r;
+}
+
+// ------------------------------------------------------------ one token
+
+// normq into activation slots for up to three consumers, deduplicating by
+// permutation; slot_of[i] receives consumer i's slot
+static void prep(float * x, const float * w, const float * resid, int n, const int * perms, int ncons, int * slot_of) {
+    const int32_t * pp[MAXACT];
+    int8_t * qq[MAXACT];
+    float * ss[MAXACT];
+    int32_t * uu[MAXACT];
+    int ids[MAXACT], nout = 0;
+    for (int i = 0; i < ncons; i++) {
+        int s = -1;
+        for (int j = 0; j < nout; j++) if (ids[j] == perms[i]) s = j;
+        if (s < 0) { s = nout++; ids[s] = perms[i]; }
+        slot_of[i] = s;
+    }
+    for (int j = 0; j < nout; j++) { pp[j] = pdev(ids[j]); qq[j] = G.aq[j]; ss[j] = G.as[j]; uu[j] = G.asum[j]; }
+    op_normq(G.st, x, resid, w, G.eps, n, nout, pp, qq, ss, uu, NULL, 0);
+}
+
+static void gemv1(sml_hip_mat * m, int slot, int epi, float * y, const float * bias, const float * resid) {
+    const sml_hip_mat * ms[1] = { m };
+    float * ys[1] = { y };
+    const float * bs[1] = { bias };
+    op_gemv(G.st, ms, 1, epi, G.aq[slot], G.as[slot], G.asum[slot], ys, bs, resid);
+}
+
+static void launch_layer(int L) {
+    eng_layer * y = &G.L[L];
+    const size_t kvd = (size_t) G.KV * G.hd;
+    int slot[3];
+    prep(G.x, y->an, NULL, G.E, y->perm_qkv, 3, slot);
+    float * outs[3] = { G.q, G.k, G.v };
+    // one launch per (activation slot, width) group of q/k/v
+    int done[3] = { 0, 0, 0 };
+    for (int i = 0; i < 3; i++) {
+        if (done[i]) continue;
+        const sml_hip_mat * ms[3];
+        float * ys[3];
+        const float * bs[3];
+        int nm = 0;
+        for (int j = i; j < 3; j++)
+            if (!done[j] && slot[j] == slot[i] && y->w[j]->nbits == y->w[i]->nbits) {
+                ms[nm] = y->w[j]; ys[nm] = outs[j]; bs[nm] = y->bias[j]; nm++; done[j] = 1;
+            }
+        op_gemv(G.st, ms, nm, SML_EPI_STORE, G.aq[slot[i]], G.as[slot[i]], G.asum[slot[i]], ys, bs, NULL);
+    }
+    op_attention(G.st, G.q, G.k, G.v, G.kc + (size_t) L * G.n_ctx * kvd, G.vc + (size_t) L * G.n_ctx * kvd,
+                 G.rc, G.rs, G.pos, G.H, G.KV, G.hd, G.n_ctx, G.part, G.att);
+    prep(G.att, NULL, NULL, G.H * G.hd, &y->perm_o, 1, slot);
+    gemv1(y->o, slot[0], SML_EPI_RESIDUAL, G.x, NULL, G.x);
+    prep(G.x, y->fn, NULL, G.E, y->perm_gu, 2, slot);
+    if (slot[0] == slot[1] && y->gate->nbits == y->up->nbits) {
+        const sml_hip_mat * ms[2] = { y->gate, y->up };
+        float * ys[2] = { G.hb, G.hb };
+        op_gemv(G.st, ms, 2, SML_EPI_SWIGLU, G.aq[slot[0]], G.as[slot[0]], G.asum[slot[0]], ys, NULL, NULL);
+    } else {
+        gemv1(y->gate, slot[0], SML_EPI_STORE, G.hb, NULL, NULL);
+        gemv1(y->up, slot[1], SML_EPI_STORE, G.hb2, NULL, NULL);
+        op_silu_mul(G.st, G.hb, G.hb2, G.F);
+    }
+    prep(G.hb, NULL, NULL, G.F, &y->perm_down, 1, slot);
+    gemv1(y->down, slot[0], SML_EPI_RESIDUAL, G.x, NULL, G.x);
+}
+
+static void launch_body(void) {
+    op_embed(G.st, G.emb, G.hist, G.pos, pdev(G.perm_emb), G.x);
+    for (int L = 0; L < G.n_layer; L++) launch_layer(L);
+}
+
+static void launch_tail(void) {
+    int slot[1];
+    prep(G.x, G.out_norm, NULL, G.E, &G.perm_head, 1, slot);
+    gemv1(G.head, slot[0], SML_EPI_STORE, G.logits, NULL, NULL);
+    op_argmax(G.st, G.logits, G.V, G.tok, G.pos, G.hist, G.n_ctx + 1);
+}
+
+static void launch_adv(void) { op_advance(G.st, G.pos); }
+
+static hipGraphExec_t capture(void (*fn)(void)) {
+    hipGraph_t g;
+    hipGraphExec_t e;
+    HX(hipStreamBeginCapture(G.st, hipStreamCaptureModeThreadLocal));
+    fn();
+    HX(hipStreamEndCapture(G.st, &g));
+    HX(hipGraphInstantiate(&e, g, NULL, NULL, 0));
+    HX(hipGraphDestroy(g));
+    return e;
+}
+
+static void run_body(void) { if (G.use_graph) HX(hipGraphLaunch(G.g_body, G.st)); else launch_body(); }
+static void run_tail(void) { if (G.use_graph) HX(hipGraphLaunch(G.g_tail, G.st)); else launch_tail(); }
+static void run_adv(void) { if (G.use_graph) HX(hipGraphLaunch(G.g_adv, G.st)); else launch_adv(); }
+
+// ------------------------------------------------------------ open / close
+
+static void release(void) {
+    // best effort: failures while tearing down are ignored
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    hx.jb = &jb;
+    if (!setjmp(jb)) {
+        if (G.st) hipStreamSynchronize(G.st);
+        if (G.g_body) hipGraphExecDestroy(G.g_body);
+        if (G.g_tail) hipGraphExecDestroy(G.g_tail);
+        if (G.g_adv) hipGraphExecDestroy(G.g_adv);
+        for (int i = 0; i < G.nmats; i++) { if (G.mats[i]->mem) hipFree(G.mats[i]->mem); free(G.mats[i]); }
+        for (int i = 0; i < G.ndev; i++) hipFree(G.dev[i]);
+        if (G.lg_host) hipHostFree(G.lg_host);
+        if (G.pin) hipHostFree(G.pin);
+        if (G.e0) hipEventDestroy(G.e0);
+        if (G.e1) hipEventDestroy(G.e1);
+        if (G.st) hipStreamDestroy(G.st);
+    }
+    hx.jb = outer;
+    free(G.L);
+    memset(&G, 0, sizeof G);
+}
+
+void sml_gpu_close(void) { release(); }
+
+static int env_int(const char * name, int dflt) {
+    const char * e = getenv(name);
+    return e && *e ? atoi(e) : dflt;
+}
+
+// Refuse what this path does not compute rather than run it wrong
+// (the reference does the same by name, sml/sml-gpu-fwd.c:1813-1865).
+static const char * unsupported(const ssf_file * f) {
+    const ssf_header * h = f->hdr;
+    if (h->flags & SSF_FLAG_HADAMARD) return "Hadamard-rotated weights";
+    if (h->flags & SSF_FLAG_EXACT) return "an exact-f32 file";
+    if (h->n_levels != 1) return "LADDER codes";
+    if (h->norm_type != 0) return "LayerNorm";
+    if (h->rope_type != 0) return "interleaved RoPE";
+    if (h->arch_bits) return "a non-Llama architecture flag";
+    if (h->n_swa) return "sliding-window attention";
+    if (h->attn_scale != 0.0f || h->logit_softcap != 0.0f || h->attn_softcap != 0.0f || h->clip_qkv != 0.0f)
+        return "attention scale, soft caps or clamps";
+    if (h->emb_scale != 0.0f || h->res_scale != 0.0f || h->logit_scale != 0.0f) return "embedding/residual/logit scales";
+    if (h->n_rot) return "partial rotary";
+    if (ssf_find(f, "blk.0.ffn_gate_inp.weight")) return "mixture-of-experts layers";
+    if (ssf_find(f, "rope_freqs") || ssf_find(f, "position_embd.weight")) return "stored or learned positions";
+    const char * extra[] = { "blk.0.attn_q_norm.weight", "blk.0.attn_output.bias", "blk.0.ffn_up.bias",
+                             "blk.0.ffn_down.bias", "blk.0.attn_norm.bias", "output.bias", "token_embd_norm.weight",
+                             "blk.0.attn_post_norm.weight", "blk.0.ffn_post_norm.weight" };
+    for (size_t i = 0; i < sizeof extra / sizeof extra[0]; i++)
+        if (ssf_find(f, extra[i])) return "tensors of an architecture this path does not compute";
+    return NULL;
+}
+
+static void setup(const char * path, int want_ctx, int gpu_layers) {
+    ssf_file f;
+    char why[512];
+    if (!ssf_open(&f, path, why, sizeof why)) hx_failf("%s", why);
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) { ssf_close(&f); hx.jb = outer; longjmp(*outer, 1); }
+    hx.jb = &jb;
+    const ssf_header * h = f.hdr;
+    const char * no = unsupported(&f);
+    if (no) hx_failf("this GPU path does not compute %s", no);
+    G.n_layer = (int) h->n_layer; G.E = (int) h->n_embd; G.H = (int) h->n_head; G.KV = (int) h->n_head_kv;
+    G.F = (int) h->n_ff; G.V = (int) h->n_vocab; G.eps = h->rms_eps;
+    if (gpu_layers > 0 && gpu_layers < G.n_layer)
+        hx_failf("a GPU/CPU layer split (%d of %d layers) is not built; every layer runs on the card", gpu_layers, G.n_layer);
+    const int n_ctx = want_ctx > 0 ? want_ctx : h->n_ctx_train ? (int) h->n_ctx_train : 4096;
+    G.n_ctx = n_ctx;
+    const ssf_record * q0 = need(&f, "blk.%d.attn_q.weight", 0);
+    G.hd = (int) q0->rows / G.H;
+    if ((int) q0->rows % G.H || G.hd != 128 || G.KV <= 0 || G.H % G.KV || G.H / G.KV > 8)
+        hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", G.H, G.KV, G.hd);
+    hx_init(env_int("SML_DEVICE", 0));
+    HX(hipStreamCreateWithFlags(&G.st, hipStreamNonBlocking));
+    HX(hipEventCreate(&G.e0));
+    HX(hipEventCreate(&G.e1));
+    const int half = G.hd / 2;
+    // weights
+    const ssf_record * er = need(&f, "token_embd.weight", 0);
+    G.emb = upmat(&f, er);
+    G.perm_emb = perm_of(&f, er);
+    const ssf_record * hr = ssf_find(&f, "output.weight");
+    if (hr) { G.head = upmat(&f, hr); G.perm_head = perm_of(&f, hr); }
+    else { G.head = G.emb; G.perm_head = G.perm_emb; }
+    G.weight_bytes = G.head->bytes;
+    const ssf_record * on = need(&f, "output_norm.weight", 0);
+    G.out_norm = f32_tensor(&f, "output_norm.weight", 0, G.E);
+    (void) on;
+    G.L = calloc((size_t) G.n_layer, sizeof(eng_layer));
+    if (!G.L) hx_failf("out of host memory");
+    const char * wn[3] = { "blk.%d.attn_q.weight", "blk.%d.attn_k.weight", "blk.%d.attn_v.weight" };
+    const char * bn[3] = { "blk.%d.attn_q.bias", "blk.%d.attn_k.bias", "blk.%d.attn_v.bias" };
+    const int wrows[3] = { G.H * G.hd, G.KV * G.hd, G.KV * G.hd };
+    for (int L = 0; L < G.n_layer; L++) {
+        eng_layer * y = &G.L[L];
+        for (int i = 0; i < 3; i++) {
+            const ssf_record * r = need(&f, wn[i], L);
+            if ((int) r->rows != wrows[i] || (int) r->cols != G.E) hx_failf("%.64s has an unexpected shape", r->name);
+            y->w[i] = upmat(&f, r);
+            y->perm_qkv[i] = perm_of(&f, r);
+            y->bias[i] = f32_tensor(&f, bn[i], L, wrows[i]);
+        }
+        const ssf_record * r;
+        r = need(&f, "blk.%d.attn_output.weight", L); y->o = upmat(&f, r); y->perm_o = perm_of(&f, r);
+        r = need(&f, "blk.%d.ffn_gate.weight", L); y->gate = upmat(&f, r); y->perm_gu[0] = perm_of(&f, r);
+        r = need(&f, "blk.%d.ffn_up.weight", L); y->up = upmat(&f, r); y->perm_gu[1] = perm_of(&f, r);
+        r = need(&f, "blk.%d.ffn_down.weight", L); y->down = upmat(&f, r); y->perm_down = perm_of(&f, r);
+        if (y->o->k.rows != G.E || y->o->cols != G.H * G.hd || y->gate->k.rows != G.F || y->up->k.rows != G.F ||
+            y->down->k.rows != G.E || y->down->cols != G.F)
+            hx_failf("layer %d has unexpected projection shapes", L);
+        y->an = f32_tensor(&f, "blk.%d.attn_norm.weight", L, G.E);
+        y->fn = f32_tensor(&f, "blk.%d.ffn_norm.weight", L, G.E);
+        if (!y->an || !y->fn) hx_failf("layer %d lacks a norm", L);
+        for (int i = 0; i < 3; i++) G.weight_bytes += y->w[i]->bytes;
+        G.weight_bytes += y->o->bytes + y->gate->bytes + y->up->bytes + y->down->bytes;
+    }
+    // RoPE table on the host, exactly as the reference builds it (sml/sml-run.c:1383-1393)
+    {
+        const size_t nt = (size_t) n_ctx * half;
+        float * c = malloc(nt * 4), * s = malloc(nt * 4);
+        if (!c || !s) { free(c); free(s); hx_failf("out of host memory"); }
+        for (int p = 0; p < n_ctx; p++)
+            for (int i = 0; i < half; i++) {
+                const float freq = powf(h->rope_theta, -(float) i / (float) half);
+                const float a = (float) p * freq;
+                c[(size_t) p * half + i] = cosf(a);
+                s[(size_t) p * half + i] = sinf(a);
+            }
+        G.rc = dupload(c, nt * 4);
+        G.rs = dupload(s, nt * 4);
+        free(c); free(s);
+    }
+    // activations and cache
+    int wide = G.F > G.E ? G.F : G.E;
+    if (G.H * G.hd > wide) wide = G.H * G.hd;
+    G.x = dalloc((size_t) G.E * 4);
+    G.q = dalloc((size_t) G.H * G.hd * 4);
+    G.k = dalloc((size_t) G.KV * G.hd * 4);
+    G.v = dalloc((size_t) G.KV * G.hd * 4);
+    G.att = dalloc((size_t) G.H * G.hd * 4);
+    G.hb = dalloc((size_t) G.F * 4);
+    G.hb2 = dalloc((size_t) G.F * 4);
+    G.logits = dalloc((size_t) G.V * 4);
+    G.part = dalloc(sml_hip_attn_part_floats(G.H, G.hd, n_ctx) * 4);
+    for (int i = 0; i < MAXACT; i++) {
+        G.aq[i] = dalloc((size_t) wide);
+        G.as[i] = dalloc((size_t) wide / 32 * 4);
+        G.asum[i] = dalloc((size_t) wide / 32 * 4);
+    }
+    const size_t kvn = (size_t) G.n_layer * n_ctx * G.KV * G.hd;
+    G.kc = dalloc(kvn * 2);
+    G.vc = dalloc(kvn * 2);
+    HX(hipMemset(G.kc, 0, kvn * 2));
+    HX(hipMemset(G.vc, 0, kvn * 2));
+    G.hist = dalloc((size_t) (n_ctx + 1) * 4);
+    HX(hipMemset(G.hist, 0, (size_t) (n_ctx + 1) * 4));
+    G.pos = dalloc(64);
+    G.tok = dalloc(64);
+    HX(hipMemset(G.pos, 0, 64));
+    HX(hipHostMalloc((void **) &G.lg_host, (size_t) G.V * 4, 0));
+    HX(hipHostMalloc((void **) &G.pin, (size_t) (n_ctx + 8) * 4, 0));
+    HX(hipDeviceSynchronize());
+    G.use_graph = env_int("SML_GRAPH", 1) != 0;
+    if (G.use_graph) {
+        G.g_body = capture(launch_body);
+        G.g_tail = capture(launch_tail);
+        G.g_adv = capture(launch_adv);
+    }
+    hx.jb = outer;
+    ssf_close(&f);
+}
+
+int sml_gpu_open(const char * path, int n_ctx, int threads, int gpu_layers, char * why, int nwhy) {
+    (void) threads;
+    if (G.open) release();
+    HX_ENTRY(0);
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) {
+        hx.jb = outer;
+        if (why && nwhy > 0) snprintf(why, (size_t) nwhy, "%s", hx.err);
+        release();
+        HX_LEAVE();
+        return 0;
+    }
+    hx.jb = &jb;
+    setup(path, n_ctx, gpu_layers);
+    hx.jb = outer;
+    G.open = 1;
+    HX_LEAVE();
+    return 1;
+}
+
+// ------------------------------------------------------------ decode
+
+static void fetch_logits(void) {
+    HX(hipMemcpyAsync(G.lg_host, G.logits, (size_t) G.V * 4, hipMemcpyDeviceToHost, G.st));
+    HX(hipStreamSynchronize(G.st));
+}
+
+const float * sml_gpu_step(int tok, int pos) {
+    if (!G.open || pos < 0 || pos >= G.n_ctx || tok < 0 || tok >= G.V) return NULL;
+    HX_ENTRY(NULL);
+    G.pin[0] = tok;
+    G.pin[1] = pos;
+    HX(hipMemcpyAsync(G.hist + pos, &G.pin[0], 4, hipMemcpyHostToDevice, G.st));
+    HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
+    run_body();
+    run_tail();
+    fetch_logits();
+    HX_LEAVE();
+    return G.lg_host;
+}
+
+const float * sml_gpu_prefill(const int * ids, int pos0, int n) {
+    if (!G.open || n <= 0 || pos0 < 0 || pos0 + n > G.n_ctx) return NULL;
+    for (int i = 0; i < n; i++) if (ids[i] < 0 || ids[i] >= G.V) return NULL;
+    HX_ENTRY(NULL);
+    G.pin[1] = pos0;
+    memcpy(G.pin + 2, ids, (size_t) n * 4);
+    HX(hipMemcpyAsync(G.hist + pos0, G.pin + 2, (size_t) n * 4, hipMemcpyHostToDevice, G.st));
+    HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
+    for (int i = 0; i < n; i++) {
+        run_body();
+        if (i + 1 < n) run_adv();
+    }
+    run_tail();
+    fetch_logits();
+    HX_LEAVE();
+    return G.lg_host;
+}
+
+int sml_gpu_generate(int tok, int pos, int n, int * out) {
+    if (!G.open || n <= 0 || pos < 0 || pos + n > G.n_ctx || tok < 0 || tok >= G.V) return -1;
+    HX_ENTRY(-1);
+    G.pin[0] = tok;
+    G.pin[1] = pos;
+    HX(hipMemcpyAsync(G.hist + pos, &G.pin[0], 4, hipMemcpyHostToDevice, G.st));
+    HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
+    HX(hipEventRecord(G.e0, G.st));
+    for (int i = 0; i < n; i++) { run_body(); run_tail(); }
+    HX(hipEventRecord(G.e1, G.st));
+    HX(hipMemcpyAsync(G.pin + 2, G.hist + pos + 1, (size_t) n * 4, hipMemcpyDeviceToHost, G.st));
+    HX(hipStreamSynchronize(G.st));
+    HX(hipEventElapsedTime(&G.last_ms, G.e0, G.e1));
+    memcpy(out, G.pin + 2, (size_t) n * 4);
+    HX_LEAVE();
+    return n;
+}
+
+float sml_gpu_last_ms(void) { return G.open ? G.last_ms : -1.0f; }
+uint64_t sml_gpu_weight_bytes(void) { return G.open ? G.weight_bytes : 0; }
+const char * sml_gpu_last_error(void) { return hx.err; }
+
+int sml_gpu_layers(int * of) {
+    if (of) *of = G.open ? G.n_layer : 0;
+    return G.open ? G.n_layer : 0;
+}
+
+void sml_gpu_prompt_mode(int level) { G.prompt_level = level > 0 ? 0 : level; }
+
+int sml_gpu_decode_cpu(int on) { (void) on; return 0; }
+
+void sml_gpu_set_middle(int layers, int (*fn)(float * rows, int pos0, int n)) {
+    g_mid_layers = layers;
+    g_mid_fn = fn;
+}

@@ -1,0 +1,114 @@
+// Kernel argument blocks, shared by the gfx950 kernels (kernels.hip, C++) and
+// the C host (engine.c). Every kernel takes exactly one of these by value, so
+// the host fills the same struct it hands to hipModuleLaunchKernel.
+#pragma once
+#include <stdint.h>
+
+#define SML_MAX_MATS 3
+
+// One quantized FLAT matrix resident in HBM, in the file's own arrays:
+// planes in storage order, 8-bit group fields (6-bit files are widened at
+// upload), fp16 superblock fields.
+typedef struct {
+    const uint8_t  * plane[3];
+    const uint8_t  * sq;
+    const uint8_t  * mq;          // NULL: no per-group min
+    const uint16_t * sd;
+    const uint16_t * md;
+    const float    * bias;        // added to the output row, or NULL
+    float          * y;
+    int rows;
+    int row_begin;                // first row of this matrix in the launch's row space
+} sml_kmat;
+
+enum { SML_EPI_STORE = 0, SML_EPI_RESIDUAL = 1, SML_EPI_SWIGLU = 2 };
+
+typedef struct {
+    sml_kmat m[SML_MAX_MATS];
+    int nmat;
+    int cols;                     // input width shared by every matrix
+    int total_rows;               // row space of the launch (SWIGLU: rows of one matrix)
+    int epi;                      // SML_EPI_*
+    const int8_t  * q;            // activation, canonical layout (reference sml_act)
+    const float   * scale;
+    const int32_t * sums;
+    const float   * resid;        // SML_EPI_RESIDUAL: y = resid + W.x (resid may alias y)
+} sml_kgemv;
+
+// Gather + optional residual add + optional RMSNorm + per-group int8 quantize.
+typedef struct {
+    float         * x;            // n floats; updated in place when resid != NULL
+    const float   * resid;        // x += resid first, or NULL
+    const float   * norm_w;       // RMSNorm weight, or NULL for none
+    float           eps;
+    int             n;
+    int             nout;         // activations to produce (distinct permutations)
+    const int32_t * perm[3];      // column permutation per output, NULL = identity
+    int8_t        * q[3];
+    float         * scale[3];
+    int32_t       * sums[3];
+    float         * normed;       // optional copy of the normalised vector (pre-gather), or NULL
+    int             per256;       // 1: one scale per 256 values (reference prompt regime)
+} sml_knormq;
+
+// Integer codes of rows [row0, row0+nrows) of one matrix, one byte per weight.
+typedef struct {
+    sml_kmat m;
+    int nbits, cols, row0, nrows;
+    uint8_t * out;
+} sml_kunpack;
+
+// Embedding: dequantized row of the token held in device memory, scattered
+// back through the permutation.
+typedef struct {
+    sml_kmat m;
+    int nbits, cols;
+    const int32_t * tok;          // token ids; row = tok[*pos] when pos != NULL, else *tok
+    const int32_t * pos;
+    const int32_t * perm;         // NULL = identity
+    float * x;
+} sml_kembed;
+
+typedef struct {
+    float * q;                    // n_head * hd, rotated in place
+    const float * k, * v;         // n_kv * hd
+    uint16_t * kcache, * vcache;  // layer base, [pos][n_kv * hd] fp16
+    const float * cos_t, * sin_t; // [n_ctx][half]
+    const int32_t * pos;
+    int n_head, n_kv, hd, half;
+} sml_kropekv;
+
+typedef struct {
+    const float * q;              // rotated
+    const uint16_t * kcache, * vcache;
+    const int32_t * pos;
+    float * part;                 // [n_head][nsplit][hd + 2]
+    int n_head, n_kv, hd, chunk, nsplit;
+    float inv;
+} sml_kattn;
+
+typedef struct {
+    const float * part;
+    const int32_t * pos;
+    float * out;                  // n_head * hd
+    int n_head, hd, chunk, nsplit;
+} sml_kattn_comb;
+
+typedef struct {
+    const float * logits;
+    int n;
+    int32_t * tok;                // argmax written here
+    int32_t * pos;                // when non-NULL: hist[*pos + 1] = argmax (if inside), then *pos += 1
+    int32_t * hist;
+    int hist_n;
+} sml_kargmax;
+
+typedef struct {
+    int32_t * pos;                // *pos += 1
+} sml_kadvance;
+
+typedef struct {
+    float * g;                    // g = silu(g) * u
+    const float * u;
+    int n;
+} sml_ksilu;

@@ -1,0 +1,121 @@
+"""The sml-gpu.h forward pass on the GPU against the oracle's decoder.
+
+Logits agree to the size an int8 activation-code flip makes (the quantized
+activations turn last-bit float differences into one-code steps; see the
+reference's own per-position correlation grading, sml/sml-gpu-fwd.c:2565-2601).
+Greedy token ids must be identical; a mismatch reports the oracle's top-2
+margin against the reference's 1%-of-s.d. tie rule as the diagnostic.
+"""
+import numpy as np
+import pytest
+
+import sheep_amd as sa
+from oracle import bind as ob
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    p = tmp_path_factory.mktemp("dec") / "tiny.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000,
+                   qkv_bias=True, random_perm=True, seed=31)
+    return p
+
+
+@pytest.fixture(scope="module")
+def qwenish(tmp_path_factory):
+    """Qwen2.5-1.5B layer shapes (hidden 1536, FFN 8960, 12/2 heads, q/k/v bias,
+    tied head) with 4 layers and a 32000 vocabulary."""
+    p = tmp_path_factory.mktemp("dec") / "qwenish.ssf"
+    sa.synth_model(p, n_layer=4, n_embd=1536, n_head=12, n_head_kv=2, n_ff=8960, n_vocab=32000,
+                   rope_theta=1e6, qkv_bias=True, tied=True, random_perm=True, seed=1002)
+    return p
+
+
+def greedy_oracle(path, tok, n, n_ctx):
+    m = ob.OracleModel(path, n_ctx)
+    toks, logits = [tok], []
+    for pos in range(n):
+        lg = m.forward(toks[-1], pos)
+        logits.append(lg)
+        toks.append(int(np.argmax(lg)))
+    m.close()
+    return toks, logits
+
+
+def tie_margin(lg):
+    top = np.sort(lg)[-2:]
+    return (top[1] - top[0]) / lg.std()
+
+
+def check_tokens(gpu_toks, orc_toks, orc_logits):
+    for i, (a, b) in enumerate(zip(gpu_toks, orc_toks)):
+        if a != b:
+            m = tie_margin(orc_logits[i])
+            pytest.fail(f"step {i}: gpu {a} oracle {b}; oracle top-2 margin {m:.4f} s.d. "
+                        f"({'inside' if m <= 0.01 else 'outside'} the reference's 1% tie rule)")
+
+
+@pytest.mark.parametrize("graph", ["1", "0"])
+def test_teacher_forced_logits(tiny, graph, monkeypatch):
+    monkeypatch.setenv("SML_GRAPH", graph)
+    toks, logits = greedy_oracle(tiny, 3, 12, 64)
+    d = sa.Decoder(tiny, n_ctx=64)
+    try:
+        for pos in range(12):
+            lg = d.step(toks[pos], pos, 2000)
+            ref = logits[pos]
+            assert np.corrcoef(lg, ref)[0, 1] > 0.999, pos
+            assert np.abs(lg - ref).max() <= 3e-2 * np.abs(ref).max(), pos
+    finally:
+        d.close()
+
+
+def test_greedy_tokens_tiny(tiny):
+    n = 40
+    toks, logits = greedy_oracle(tiny, 11, n, 64)
+    d = sa.Decoder(tiny, n_ctx=64)
+    try:
+        out = d.generate(11, 0, n)
+    finally:
+        d.close()
+    check_tokens(list(out), toks[1:], logits)
+
+
+def test_generate_equals_stepping_and_prefill(tiny):
+    d = sa.Decoder(tiny, n_ctx=64)
+    try:
+        gen = d.generate(5, 0, 16)
+        # stepping the same positions with the generated tokens reproduces them
+        seq = [5] + list(gen)
+        stepped = [int(np.argmax(d.step(seq[i], i, 2000))) for i in range(16)]
+        assert stepped == list(gen)
+        # a prompt read at once continues exactly as stepping did
+        lg = d.prefill(np.array(seq[:10], np.int32), 0, 2000)
+        assert int(np.argmax(lg)) == gen[9]
+    finally:
+        d.close()
+
+
+def test_greedy_tokens_qwen_layers(qwenish):
+    n = 24
+    toks, logits = greedy_oracle(qwenish, 100, n, 128)
+    d = sa.Decoder(qwenish, n_ctx=128)
+    try:
+        out = d.generate(100, 0, n)
+    finally:
+        d.close()
+    check_tokens(list(out), toks[1:], logits)
+
+
+def test_bounds_and_reopen(tiny):
+    d = sa.Decoder(tiny, n_ctx=32)
+    try:
+        assert not sa.lib().sml_gpu_step(1, 32)
+        assert not sa.lib().sml_gpu_step(2000, 0)
+        assert sa.lib().sml_gpu_generate(1, 30, 5, (sa.ctypes.c_int * 5)()) == -1
+    finally:
+        d.close()
+    d = sa.Decoder(tiny, n_ctx=32)
+    d.close()

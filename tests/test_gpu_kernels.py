@@ -1,0 +1,232 @@
+"""GPU parity of each kernel against the oracle on the same seeded inputs.
+
+Integer work (unpacked codes, int8 activation codes/scales/sums, argmax) is
+bit-exact. Float outputs (GEMV, attention) must agree within 1e-3 relative:
+    max|gpu - oracle| <= 1e-3 * max|oracle|   and   rel-RMS <= 1e-4.
+"""
+import numpy as np
+import pytest
+
+import sheep_amd as sa
+from oracle import bind as ob
+from sheep_amd.ssf import SSF
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAX = 1e-3
+TOL_RMS = 1e-4
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    sa.init(0)
+
+
+def close(gpu, ref, what):
+    err = np.abs(gpu.astype(np.float64) - ref.astype(np.float64))
+    scale = np.abs(ref).max()
+    rms = np.sqrt((err ** 2).mean()) / max(np.sqrt((ref.astype(np.float64) ** 2).mean()), 1e-30)
+    assert err.max() <= TOL_MAX * scale, f"{what}: max err {err.max():.3g} vs scale {scale:.3g}"
+    assert rms <= TOL_RMS, f"{what}: rel-RMS {rms:.3g}"
+
+
+def dev_quantize(x, perm=None, per256=False, w=None, eps=1e-6):
+    xd = sa.DevBuf.of(np.ascontiguousarray(x, np.float32))
+    act = sa.Act(len(x))
+    pd = sa.DevBuf.of(np.ascontiguousarray(perm, np.int32)) if perm is not None else None
+    wd = sa.DevBuf.of(np.ascontiguousarray(w, np.float32)) if w is not None else None
+    sa.normq(xd, act, perm=pd, w=wd, eps=eps, per256=per256)
+    return act
+
+
+# ------------------------------------------------------------ activations
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("per256", [False, True])
+def test_quantize_bitexact(seed, per256):
+    rng = np.random.default_rng(seed)
+    n = 14336
+    x = (rng.standard_normal(n) * 10.0 ** rng.uniform(-3, 3)).astype(np.float32)
+    x[:32] = 0.0
+    x[32:64] = np.arange(32, dtype=np.float32) * 0.5
+    perm = rng.permutation(n).astype(np.int32) if seed % 2 else None
+    act = dev_quantize(x, perm=perm, per256=per256)
+    xg = x[perm] if perm is not None else x
+    want = ob.quantize_act(xg, per256=per256)
+    for got, exp, name in zip(act.read(), want, ("q", "scale", "sums")):
+        np.testing.assert_array_equal(got, exp, err_msg=name)
+
+
+def test_quantize_golden():
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "act_quant.npz"))
+    for i in range(2):
+        for per256 in (0, 1):
+            got = dev_quantize(g[f"x{i}"], per256=bool(per256)).read()
+            for a, b in zip(got, (g[f"q{i}_{per256}"], g[f"s{i}_{per256}"], g[f"u{i}_{per256}"])):
+                np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("n", [1536, 4096])
+def test_normq_bitexact(n):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+    perm = rng.permutation(n).astype(np.int32)
+    act = dev_quantize(x, perm=perm, w=w, eps=1e-6)
+    normed = np.zeros(n, np.float32)
+    ob.oracle().orc_rms_norm(normed.ctypes.data, x.ctypes.data, w.ctypes.data, n, 1e-6)
+    for a, b in zip(act.read(), ob.quantize_act(normed[perm])):
+        np.testing.assert_array_equal(a, b)
+
+
+# ------------------------------------------------------------ unpack
+
+@pytest.mark.parametrize("nb", range(2, 9))
+def test_unpack_bitexact(tmpdir_s, nb):
+    p = tmpdir_s / f"u{nb}.ssf"
+    sa.synth_matrix(p, 96, 1536, nbits=nb, random_perm=True, seed=300 + nb)
+    t = SSF(p)["w"]
+    m = sa.Mat.from_file(p, "w")
+    got = sa.unpack(m, 0, 96)
+    want = np.stack([ob.unpack(t, r) for r in range(96)])
+    np.testing.assert_array_equal(got, want)
+
+
+# ------------------------------------------------------------ GEMV
+
+def gemv_case(tmpdir_s, rows, cols, nb, perm=False, seed=1, check_ref=False):
+    p = tmpdir_s / f"g_{rows}x{cols}_q{nb}_{int(perm)}_{seed}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, rows, cols, nbits=nb, random_perm=perm, seed=seed)
+    f = SSF(p)
+    t = f["w"]
+    x = np.random.default_rng(seed).standard_normal(cols).astype(np.float32)
+    m = sa.Mat.from_file(p, "w")
+    act = dev_quantize(x, perm=t.perm)
+    y = sa.DevBuf(rows * 4)
+    sa.matvec(m, act, y)
+    got = y.read(np.float32)
+    q, s, u = ob.quantize_act(x[t.perm])
+    close(got, ob.matvec(t, q, s, u), f"{rows}x{cols} Q{nb}")
+    if check_ref and ob.have_ref():
+        close(got, ob.ref_matvec(t, q, s, u), f"{rows}x{cols} Q{nb} vs reference build")
+    return got
+
+
+@pytest.mark.parametrize("nb", range(2, 9))
+def test_gemv_small(tmpdir_s, nb):
+    gemv_case(tmpdir_s, 256, 1536, nb, perm=True, seed=10 + nb, check_ref=True)
+
+
+@pytest.mark.parametrize("perm", [False, True])
+def test_gemv_single_q4_8960x1536(tmpdir_s, perm):
+    """The single-GEMV workload: Qwen2.5-1.5B FFN-up shape, rows 8960 x cols 1536."""
+    gemv_case(tmpdir_s, 8960, 1536, 4, perm=perm, seed=1001, check_ref=True)
+
+
+@pytest.mark.parametrize("shape", [(4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("nb", [2, 3, 4, 5, 6, 8])
+def test_gemv_width_sweep(tmpdir_s, shape, nb):
+    gemv_case(tmpdir_s, shape[0], shape[1], nb, seed=1004)
+
+
+def test_gemv_rows_not_multiple_of_block(tmpdir_s):
+    gemv_case(tmpdir_s, 257, 512, 4, seed=3)
+    gemv_case(tmpdir_s, 1, 128, 4, seed=4)
+
+
+def test_gemv_repeat_is_deterministic(tmpdir_s):
+    a = gemv_case(tmpdir_s, 4096, 4096, 4, seed=5)
+    b = gemv_case(tmpdir_s, 4096, 4096, 4, seed=5)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_swiglu(tmpdir_s):
+    p = tmpdir_s / "ffn.ssf"
+    sa.synth_model(p, n_layer=1, n_embd=1536, n_head=12, n_head_kv=2, n_ff=8960, n_vocab=256, seed=77)
+    f = SSF(p)
+    g, u = f["blk.0.ffn_gate.weight"], f["blk.0.ffn_up.weight"]
+    x = np.random.default_rng(0).standard_normal(1536).astype(np.float32)
+    act = dev_quantize(x, perm=g.perm)
+    mg, mu = sa.Mat.from_file(p, g.name), sa.Mat.from_file(p, u.name)
+    h = sa.DevBuf(8960 * 4)
+    sa.matvec_swiglu(mg, mu, act, h)
+    q, s, su = ob.quantize_act(x[g.perm])
+    yg, yu = ob.matvec(g, q, s, su), ob.matvec(u, q, s, su)
+    ob.oracle().orc_silu_mul(yg.ctypes.data, yu.ctypes.data, 8960)
+    close(h.read(np.float32), yg, "swiglu")
+
+
+# ------------------------------------------------------------ embed, attention, argmax
+
+@pytest.mark.parametrize("nb", [4, 6, 8])
+def test_embed(tmpdir_s, nb):
+    p = tmpdir_s / f"emb{nb}.ssf"
+    sa.synth_matrix(p, 1000, 1536, nbits=nb, random_perm=True, seed=500 + nb)
+    t = SSF(p)["w"]
+    m = sa.Mat.from_file(p, "w")
+    for tok in (0, 537, 999):
+        td = sa.DevBuf.of(np.array([tok], np.int32))
+        pd = sa.DevBuf.of(t.perm.astype(np.int32))
+        x = sa.DevBuf(1536 * 4)
+        assert sa.lib().sml_hip_embed(m.h, td.ptr, pd.ptr, x.ptr) == 0
+        want = np.zeros(1536, np.float32)
+        want[t.perm] = ob.dequant_row(t, tok)
+        np.testing.assert_array_equal(x.read(np.float32), want)
+
+
+@pytest.mark.parametrize("heads", [(12, 2), (32, 8)])
+def test_attention(heads):
+    H, KV = heads
+    hd, n_ctx, half = 128, 512, 64
+    rng = np.random.default_rng(H)
+    cos_t = np.zeros(n_ctx * half, np.float32)
+    sin_t = np.zeros(n_ctx * half, np.float32)
+    ob.oracle().orc_rope_table(1e6, half, n_ctx, cos_t.ctypes.data, sin_t.ctypes.data)
+    kvd = KV * hd
+    kc = np.zeros((n_ctx, kvd), np.uint16)
+    vc = np.zeros((n_ctx, kvd), np.uint16)
+    dkc, dvc = sa.DevBuf.of(kc), sa.DevBuf.of(vc)
+    dcos, dsin = sa.DevBuf.of(cos_t), sa.DevBuf.of(sin_t)
+    part = sa.DevBuf(sa.lib().sml_hip_attn_part_floats(H, hd, n_ctx) * 4)
+    out = sa.DevBuf(H * hd * 4)
+    scratch = np.zeros(n_ctx, np.float32)
+    for pos in range(0, 300):
+        q = rng.standard_normal(H * hd).astype(np.float32)
+        k = rng.standard_normal(kvd).astype(np.float32)
+        v = rng.standard_normal(kvd).astype(np.float32)
+        dq, dk, dv = sa.DevBuf.of(q), sa.DevBuf.of(k), sa.DevBuf.of(v)
+        dpos = sa.DevBuf.of(np.array([pos], np.int32))
+        rc = sa.lib().sml_hip_attention(dq.ptr, dk.ptr, dv.ptr, dkc.ptr, dvc.ptr, dcos.ptr, dsin.ptr, dpos.ptr,
+                                        H, KV, hd, n_ctx, part.ptr, out.ptr)
+        assert rc == 0, sa.lib().sml_hip_last_error()
+        # oracle: rotate, store fp16, attend
+        qr, kr = q.copy(), k.copy()
+        ob.oracle().orc_rope(qr.ctypes.data, H, hd, half, cos_t[pos * half:].ctypes.data, sin_t[pos * half:].ctypes.data)
+        ob.oracle().orc_rope(kr.ctypes.data, KV, hd, half, cos_t[pos * half:].ctypes.data, sin_t[pos * half:].ctypes.data)
+        kc[pos] = kr.astype(np.float16).view(np.uint16)
+        vc[pos] = v.astype(np.float16).view(np.uint16)
+        if pos not in (0, 1, 63, 64, 65, 127, 200, 299):
+            continue
+        np.testing.assert_array_equal(dkc.read(np.uint16).reshape(n_ctx, kvd)[pos], kc[pos])
+        np.testing.assert_array_equal(dvc.read(np.uint16).reshape(n_ctx, kvd)[pos], vc[pos])
+        want = np.zeros(H * hd, np.float32)
+        inv = np.float32(1) / np.sqrt(np.float32(hd))
+        for h in range(H):
+            kh = h // (H // KV)
+            ob.oracle().orc_attn_head(qr[h * hd:].ctypes.data, kc[:, kh * hd:].ctypes.data, vc[:, kh * hd:].ctypes.data,
+                                      kvd, pos, hd, inv, scratch.ctypes.data, want[h * hd:].ctypes.data)
+        close(out.read(np.float32), want, f"attention pos {pos}")
+
+
+def test_argmax_first_max():
+    rng = np.random.default_rng(0)
+    for n, tie in [(151936, True), (128256, False), (1000, True), (5, False)]:
+        lg = rng.standard_normal(n).astype(np.float32)
+        if tie:
+            lg[n // 3] = lg[n - 1] = lg.max() + 1.0
+        d = sa.DevBuf.of(lg)
+        t = sa.DevBuf(4)
+        assert sa.lib().sml_hip_argmax(d.ptr, n, t.ptr) == 0
+        assert int(t.read(np.int32)[0]) == ob.oracle().orc_argmax(lg.ctypes.data, n)

@@ -1,0 +1,279 @@
+"""Pinning the CPU oracle (oracle/sml_oracle.c).
+
+Each restated function is checked three ways where they apply: against the
+golden vectors the reference build wrote (tests/golden/), against the
+reference's own CPU path when it is built here (oracle/_ref), and against what
+the mathematics fixes (closed forms, brute force in float64, invariants) --
+chosen so that a dropped term, a wrong index or a swapped plane fails.
+"""
+import ctypes
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import sheep_amd as sa
+from oracle import bind as ob
+from sheep_amd.ssf import SSF
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+needs_ref = pytest.mark.skipif(not ob.have_ref(), reason="reference CPU build not present")
+
+
+def f16(u16):
+    return np.asarray(u16, np.uint16).view(np.float16).astype(np.float32)
+
+
+# ------------------------------------------------------------ activations
+
+def test_quantize_act_golden():
+    g = np.load(os.path.join(GOLD, "act_quant.npz"))
+    for i in range(2):
+        for per256 in (0, 1):
+            q, s, u = ob.quantize_act(g[f"x{i}"], per256=bool(per256))
+            np.testing.assert_array_equal(q, g[f"q{i}_{per256}"])
+            np.testing.assert_array_equal(s, g[f"s{i}_{per256}"])
+            np.testing.assert_array_equal(u, g[f"u{i}_{per256}"])
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", range(6))
+def test_quantize_act_matches_reference(seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(4096) * 10.0 ** rng.uniform(-3, 3)).astype(np.float32)
+    x[rng.integers(0, 4096, 50)] = np.round(x[rng.integers(0, 4096, 50)])  # integers hit exact halves often
+    for per256 in (False, True):
+        for a, b in zip(ob.quantize_act(x, per256), ob.ref_quantize_act(x, per256)):
+            np.testing.assert_array_equal(a, b)
+
+
+def test_quantize_act_closed_form():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(2048).astype(np.float32)
+    q, s, u = ob.quantize_act(x)
+    g = x.reshape(-1, 32)
+    amax = np.abs(g).max(1)
+    np.testing.assert_array_equal(s, (amax / np.float32(127)).astype(np.float32))
+    inv = (np.float32(1) / s).astype(np.float32)
+    want = np.clip(np.rint((g * inv[:, None]).astype(np.float32)), -127, 127).astype(np.int8)
+    np.testing.assert_array_equal(q.reshape(-1, 32), want)
+    np.testing.assert_array_equal(u, want.astype(np.int32).sum(1))
+    # the group maximum always lands on +-127
+    assert (np.abs(q.reshape(-1, 32)).max(1) == 127).all()
+
+
+# ------------------------------------------------------------ codes and GEMV per width
+
+@pytest.mark.parametrize("nb", range(2, 9))
+def test_widths_golden(tmpdir_s, nb):
+    g = np.load(os.path.join(GOLD, "widths.npz"))
+    p = tmpdir_s / f"gold{nb}.ssf"
+    sa.synth_matrix(p, 16, 256, nbits=nb, random_perm=True, seed=100 + nb)
+    assert hashlib.sha256(p.read_bytes()).digest() == g[f"sha{nb}"].tobytes(), "synthetic file drifted"
+    t = SSF(p)["w"]
+    deq = np.stack([ob.dequant_row(t, r) for r in range(16)])
+    np.testing.assert_array_equal(deq, g[f"deq{nb}"])
+    q, s, u = ob.quantize_act(g[f"x{nb}"])
+    y = ob.matvec(t, q, s, u)
+    ref = g[f"y{nb}"]
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("nb", range(2, 9))
+def test_codes_closed_form(tmpdir_s, nb):
+    """dequant == code*step + min with step/min from the fields; brute-force
+    GEMV in float64 over the dequantized row agrees with the oracle GEMV."""
+    p = tmpdir_s / f"cf{nb}.ssf"
+    sa.synth_matrix(p, 12, 384, nbits=nb, random_perm=True, seed=40 + nb)
+    t = SSF(p)["w"]
+    ng = 384 // 32
+    sd = f16(t.sd).reshape(12, -1)
+    md = f16(t.md).reshape(12, -1)
+    sq = t.sq.reshape(12, ng).astype(np.float32)
+    mq = t.mq.reshape(12, ng).astype(np.float32)
+    x = np.random.default_rng(nb).standard_normal(384).astype(np.float32)
+    q, s, u = ob.quantize_act(x)
+    y = ob.matvec(t, q, s, u)
+    for r in range(12):
+        c = ob.unpack(t, r).astype(np.float32).reshape(ng, 32)
+        step = (sd[r][np.arange(ng) // 8] * sq[r]).astype(np.float32)
+        mn = (md[r][np.arange(ng) // 8] * (mq[r] - np.float32(127))).astype(np.float32)
+        want = (c * step[:, None]).astype(np.float32) + mn[:, None]
+        np.testing.assert_array_equal(ob.dequant_row(t, r).reshape(ng, 32), want.astype(np.float32))
+        xq = q.astype(np.float64) * np.repeat(s.astype(np.float64), 32)
+        brute = float(np.dot(want.reshape(-1).astype(np.float64), xq))
+        assert abs(y[r] - brute) <= 2e-6 * (np.abs(want).sum() * np.abs(xq).max() + 1e-30)
+
+
+@pytest.mark.parametrize("nb", range(2, 9))
+def test_plane_layout_independent_reading(tmpdir_s, nb):
+    """The oracle's plane reads against a numpy reading of the layout rule
+    (tooling/sml_format.py:392-448): nibble quads, 2-bit packs, 1-bit words."""
+    p = tmpdir_s / f"pl{nb}.ssf"
+    sa.synth_matrix(p, 4, 256, nbits=nb, seed=60 + nb)
+    t = SSF(p)["w"]
+    planes = t.planes()
+    from sheep_amd.ssf import FLAT_PLANES
+    widths = FLAT_PLANES[nb]
+    for r in range(4):
+        parts = []
+        for w, pl in zip(widths, planes):
+            if w == 4:
+                b = pl.reshape(4, -1)[r].reshape(-1, 2, 32)          # quads: [half][col]
+                lo, hi = b & 15, b >> 4
+                g = np.stack([lo[:, 0], hi[:, 0], lo[:, 1], hi[:, 1]], 1).reshape(-1)
+            elif w == 2:
+                b = pl.reshape(4, -1)[r].reshape(-1, 32)
+                g = np.stack([(b >> (2 * k)) & 3 for k in range(4)], 1).reshape(-1)
+            else:
+                b = pl.reshape(4, -1)[r]
+                g = np.unpackbits(b, bitorder="little")
+            parts.append(g.astype(np.int32))
+        if nb == 6:
+            code = parts[1] | (parts[0] << 4)
+        else:
+            code, sh = np.zeros(256, np.int32), 0
+            for w, g in zip(widths, parts):
+                code |= g << sh
+                sh += w
+        np.testing.assert_array_equal(ob.unpack(t, r), code.astype(np.uint8))
+
+
+@needs_ref
+@pytest.mark.parametrize("nb", range(2, 9))
+def test_widths_match_reference(tmpdir_s, nb):
+    p = tmpdir_s / f"rw{nb}.ssf"
+    sa.synth_matrix(p, 64, 1536, nbits=nb, random_perm=True, seed=200 + nb)
+    t = SSF(p)["w"]
+    for r in (0, 17, 63):
+        np.testing.assert_array_equal(ob.dequant_row(t, r), ob.ref_dequant_row(t, r))
+    x = np.random.default_rng(nb).standard_normal(1536).astype(np.float32)
+    q, s, u = ob.quantize_act(x)
+    y, yr = ob.matvec(t, q, s, u), ob.ref_matvec(t, q, s, u)
+    assert np.abs(y - yr).max() <= 1e-5 * np.abs(yr).max()
+
+
+# ------------------------------------------------------------ small ops
+
+def test_rms_norm_closed_form():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(1536).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(1536)).astype(np.float32)
+    out = np.zeros_like(x)
+    ob.oracle().orc_rms_norm(out.ctypes.data, x.ctypes.data, w.ctypes.data, 1536, 1e-6)
+    ss = float(np.sum(x.astype(np.float64) ** 2))
+    sc = np.float32(1) / np.sqrt(np.float32(ss / 1536) + np.float32(1e-6))
+    np.testing.assert_array_equal(out, (x * sc).astype(np.float32) * w)
+
+
+def test_rope_table_and_rotation():
+    half, n_ctx, theta = 64, 16, 1e6
+    c = np.zeros(n_ctx * half, np.float32)
+    s = np.zeros(n_ctx * half, np.float32)
+    ob.oracle().orc_rope_table(theta, half, n_ctx, c.ctypes.data, s.ctypes.data)
+    ang = np.arange(n_ctx)[:, None] * theta ** (-np.arange(half) / half)
+    assert np.abs(c.reshape(n_ctx, half) - np.cos(ang)).max() < 2e-6 * n_ctx
+    assert np.abs(s.reshape(n_ctx, half) - np.sin(ang)).max() < 2e-6 * n_ctx
+    x = np.random.default_rng(0).standard_normal(2 * 128).astype(np.float32)
+    y = x.copy()
+    ob.oracle().orc_rope(y.ctypes.data, 2, 128, half, c[5 * half:].ctypes.data, s[5 * half:].ctypes.data)
+    # a rotation: each (i, i+half) pair keeps its norm
+    for h in range(2):
+        a, b = x[h * 128:(h + 1) * 128], y[h * 128:(h + 1) * 128]
+        np.testing.assert_allclose(a[:half] ** 2 + a[half:] ** 2, b[:half] ** 2 + b[half:] ** 2, rtol=1e-5)
+
+
+def test_attention_head_closed_form():
+    rng = np.random.default_rng(4)
+    hd, T, stride = 128, 37, 256
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.standard_normal((T, stride)).astype(np.float16)
+    v = rng.standard_normal((T, stride)).astype(np.float16)
+    scratch = np.zeros(T, np.float32)
+    out = np.zeros(hd, np.float32)
+    inv = 1 / np.sqrt(np.float32(hd))
+    ob.oracle().orc_attn_head(q.ctypes.data, k.view(np.uint16).ctypes.data, v.view(np.uint16).ctypes.data, stride,
+                              T - 1, hd, np.float32(inv), scratch.ctypes.data, out.ctypes.data)
+    sc = (k[:, :hd].astype(np.float64) @ q.astype(np.float64)) * inv
+    p = np.exp(sc - sc.max())
+    p /= p.sum()
+    want = p @ v[:, :hd].astype(np.float64)
+    np.testing.assert_allclose(out, want, rtol=1e-4, atol=1e-5)
+
+
+def test_f16_roundtrip_matches_numpy():
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([rng.standard_normal(2000) * 10.0 ** rng.uniform(-9, 5, 2000),
+                         [0.0, -0.0, 65504.0, 65520.0, 1e-8, 6e-8, np.inf, -np.inf]]).astype(np.float32)
+    o = ob.oracle()
+    for x in xs:
+        h = o.orc_f32_to_f16(float(x))
+        assert h == int(np.float16(x).view(np.uint16)), x
+        assert o.orc_f16_to_f32(h) == np.float32(np.float16(x)) or np.isnan(x)
+
+
+def test_moe_route_golden_and_brute_force():
+    g = np.load(os.path.join(GOLD, "decoder.npz"))
+    lgs = g["route_lg"]
+    for i in range(len(lgs)):
+        sel = np.zeros(2, np.int32)
+        w = np.zeros(2, np.float32)
+        lg = np.ascontiguousarray(lgs[i])
+        ob.oracle().orc_moe_route(lg.ctypes.data, 8, 2, 1, sel.ctypes.data, w.ctypes.data)
+        np.testing.assert_array_equal(sel, g["route_sel"][i])
+        np.testing.assert_array_equal(w, g["route_w"][i])
+        # brute force: stable descending order (ties -> lower index), softmax over the chosen
+        order = sorted(range(8), key=lambda e: (-lg[e], e))[:2]
+        assert list(sel) == order
+        e = np.exp(lg[order].astype(np.float64) - lg[order[0]])
+        np.testing.assert_allclose(w, e / e.sum(), rtol=1e-6)
+
+
+# ------------------------------------------------------------ decoder
+
+def test_decoder_golden(tmpdir_s):
+    g = np.load(os.path.join(GOLD, "decoder.npz"))
+    p = tmpdir_s / "tiny.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=256, n_head=2, n_head_kv=1, n_ff=512, n_vocab=1000,
+                   qkv_bias=True, random_perm=True, seed=7)
+    assert hashlib.sha256(p.read_bytes()).digest() == g["sha"].tobytes()
+    m = ob.OracleModel(p, 32)
+    toks = g["tokens"]
+    for pos in range(6):
+        lg = m.forward(int(toks[pos]), pos)
+        ref = g["logits"][pos]
+        # int8 activation codes can flip on last-bit differences; the logits agree
+        # to the size of one flip and far closer in correlation
+        assert np.corrcoef(lg, ref)[0, 1] > 0.9999
+        assert np.abs(lg - ref).max() <= 2e-2 * np.abs(ref).max()
+        top = np.sort(ref)[-2:]
+        if top[1] - top[0] > 1e-2 * ref.std():
+            assert int(np.argmax(lg)) == int(toks[pos + 1])
+    m.close()
+
+
+@needs_ref
+def test_decoder_layers_match_reference(tmpdir_s, monkeypatch):
+    """Per-layer residuals (SML_DUMP / ORC_DUMP) of the oracle and the reference."""
+    p = tmpdir_s / "layers.ssf"
+    sa.synth_model(p, n_layer=3, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=500,
+                   qkv_bias=False, random_perm=True, seed=21)
+    d_ref, d_orc = tmpdir_s / "dump_ref", tmpdir_s / "dump_orc"
+    for d in (d_ref, d_orc):
+        if d.exists():
+            d.unlink()
+    monkeypatch.setenv("SML_DUMP", str(d_ref))
+    monkeypatch.setenv("ORC_DUMP", str(d_orc))
+    om, rm = ob.OracleModel(p, 16), ob.RefModel(p, 16, threads=1)
+    for pos, tok in enumerate([3, 99, 250, 7]):
+        om.forward(tok, pos)
+        rm.forward(tok, pos)
+    om.close()
+    rm.close()
+    A = np.fromfile(d_orc, np.float32).reshape(-1, 512)
+    B = np.fromfile(d_ref, np.float32).reshape(-1, 512)
+    assert A.shape == B.shape == (16, 512)
+    for a, b in zip(A, B):
+        assert np.abs(a - b).max() <= 1e-2 * np.abs(b).max()
+        assert np.corrcoef(a, b)[0, 1] > 0.9999
