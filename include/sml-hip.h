@@ -67,6 +67,12 @@ int sml_hip_matvec_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, cons
 int sml_hip_time_matvec(const sml_hip_mat * const * mats, int ncopy, const int8_t * q, const float * scale,
                         const int32_t * sums, float * y, int iters, float * ms_total);
 
+// Calibration: time `iters` launches of a plain streaming read of `bytes`
+// from each buffer in turn (grid workgroups of 256 threads, 128-bit loads).
+// No counterpart in the reference: it measures what one kernel can read from
+// HBM on this machine, the denominator next to the GEMV's achieved bandwidth.
+int sml_hip_time_read(const void * const * bufs, int nbuf, size_t bytes, int grid, int iters, float * ms_total);
+
 // ------------------------------------------------------------ unpack / embed
 // Integer code of every weight of rows [row0, row0+nrows), one byte each,
 // permuted column order: the unpack truth of sml_dequant_row_* (sml/sml-kernel.c:2134-2260)

@@ -6,15 +6,16 @@
 
 #define SML_MAX_MATS 3
 
-// One quantized FLAT matrix resident in HBM, in the file's own arrays:
-// planes in storage order, 8-bit group fields (6-bit files are widened at
-// upload), fp16 superblock fields.
+// One quantized FLAT matrix resident in HBM: the file's code planes in
+// storage order, and its four field arrays interleaved pairwise at upload --
+// per group (sq, mq) as two bytes, per superblock (sd, md) as two halves --
+// so a lane reads its group's fields with two loads instead of four. 6-bit
+// files are widened to bytes with the min bias moved to 127; a tensor with
+// no min stores mq = 127, md = 0.
 typedef struct {
     const uint8_t  * plane[3];
-    const uint8_t  * sq;
-    const uint8_t  * mq;          // NULL: no per-group min
-    const uint16_t * sd;
-    const uint16_t * md;
+    const uint8_t  * sqmq;        // [rows][ngroups][2]
+    const uint16_t * sdmd;        // [rows][nsuper][2]
     const float    * bias;        // added to the output row, or NULL
     float          * y;
     int rows;
@@ -112,3 +113,12 @@ typedef struct {
     const float * u;
     int n;
 } sml_ksilu;
+
+// Plain streaming read of `bytes` (multiple of 16) for bandwidth calibration:
+// every 16-byte word is read once and folded into one word per wave.
+typedef struct {
+    const uint8_t * src;
+    uint64_t bytes;
+    uint32_t * sink;              // one word per wave
+    int pattern;                  // 0: coalesced grid-stride; 1: each lane 64 contiguous bytes per step
+} sml_kread;

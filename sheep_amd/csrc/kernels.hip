@@ -2,14 +2,15 @@
 // object (--genco) and loaded by the C host with hipModuleLoadData; every
 // kernel is extern "C" and takes one argument block from kargs.h.
 //
-// Wave64 throughout. The GEMV's unit of work is a 16-byte chunk of a row's
-// nibble plane: chunk c holds columns 16*(c&1)..+15 of the group pair
-// (c&~1, c|1) (the reference's flat-4 layout, sml/sml-kernel.c:2140-2156), so
-// one lane loads one 128-bit word per plane, computes partial int8 dot
-// products for both groups with v_dot4, swaps one of them with its pair lane
-// through DPP, and ends up owning the full dot of group c. Group c's float
-// epilogue follows the reference's per-group arithmetic
-// (sml/sml-kernel.c:2054-2063): step*(s*dot) + min*(s*sum).
+// Wave64 throughout. The GEMV's unit of work is a quad: 128 consecutive
+// weights of one row = 4 whole groups of 32, which in the reference's FLAT
+// planes is 64 contiguous bytes of the nibble plane (groups 4q, 4q+1 as the
+// low/high nibbles of bytes 0-31, groups 4q+2, 4q+3 of bytes 32-63;
+// sml/sml-kernel.c:2140-2156), one 32-byte pack of a 2-bit plane and 16
+// bytes of a 1-bit plane. One lane streams a quad with 128-bit loads,
+// dots it against the int8 activation held in LDS with v_dot4, and applies
+// the reference's per-group float epilogue (sml/sml-kernel.c:2054-2063):
+// step*(s*dot) + min*(s*sum).
 #include <hip/hip_runtime.h>
 #include "kargs.h"
 
@@ -17,12 +18,10 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
-
-// lane i <-> lane i^1 (DPP quad_perm [1,0,3,2])
-__device__ __forceinline__ int pair_swap(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
 
 __device__ __forceinline__ float wave_sum(float v) {
     #pragma unroll
@@ -35,231 +34,264 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+__device__ __forceinline__ int dot4(unsigned a, int b, int c) { return __builtin_amdgcn_sdot4((int) a, b, c, false); }
 
 // 4 bits (one per column) -> 4 bytes of 0/1
-__device__ __forceinline__ uint32_t bits4_to_bytes(uint32_t nib) { return (nib * 0x00204081u) & 0x01010101u; }
+__device__ __forceinline__ unsigned bits4_to_bytes(unsigned nib) { return (nib * 0x00204081u) & 0x01010101u; }
 
-// ---------------------------------------------------------------- code chunks
+// ---------------------------------------------------------------- chunks
 //
-// Codes of chunk c of one row, as int8 lanes: ca[i] holds 4 columns of group
-// c&~1, cb[i] the same columns of group c|1 (columns 16*(c&1) + 4i .. +3).
-// Every width below 8 yields codes <= 127, so one signed dot4 per word serves.
-// Plane orders follow tooling/sml_quantize.py:104-106.
-template <int NB>
-struct Chunk {
-    v4u a, b;          // low part (or the whole code)
-    v4u ha, hb;        // Q8 only: high nibbles
+// A chunk is 16 bytes of a row's nibble plane: columns 16*(c&1)..+15 of the
+// group pair (c&~1, c|1) -- byte i's low nibble belongs to the first group,
+// its high nibble to the second (the FLAT layout, sml/sml-kernel.c:2140-2156).
+// Lane c of a row loads chunk c, so 64 lanes read 1 KB of contiguous bytes
+// per instruction; the other planes' bytes for the same weights are equally
+// contiguous across lanes (a 2-bit pack serves two lanes, a 1-bit word pair
+// serves a lane pair). Plane orders per width follow
+// tooling/sml_quantize.py:104-106: Q2 [2], Q3 [2,1], Q4 [4], Q5 [4,1],
+// Q6 [2,4] (the 2-bit plane holds bits 4-5), Q7 [4,2,1], Q8 [4,4].
+template <int NB> struct Planes {
+    static constexpr bool N4 = NB == 4 || NB == 5 || NB == 6 || NB == 7 || NB == 8;
+    static constexpr bool N2 = NB == 2 || NB == 3 || NB == 6 || NB == 7;
+    static constexpr bool N1 = NB == 3 || NB == 5 || NB == 7;
+    static constexpr int P4 = NB == 6 ? 1 : 0;
+    static constexpr int P2 = NB == 7 ? 1 : 0;
+    static constexpr int P1 = NB == 7 ? 2 : 1;
+    // bytes of each plane per row for `cols` weights
+    static __device__ __forceinline__ size_t b4(int cols) { return (size_t) cols / 2; }
+    static __device__ __forceinline__ size_t b2(int cols) { return (size_t) cols / 4; }
+    static __device__ __forceinline__ size_t b1(int cols) { return (size_t) cols / 8; }
 };
 
+template <int NB> struct ChunkW {
+    v4u n4;                       // nibble plane word (or zeros)
+    v4u h4;                       // Q8 high nibbles
+    v4u t2;                       // 2-bit pack half
+    v2u o1;                       // 1-bit words of the group pair
+};
+
+// row bases of each plane (pl[] already offset to the row)
 template <int NB>
-__device__ __forceinline__ Chunk<NB> load_chunk(const uint8_t * const * pl, size_t row, int cols, int c) {
-    Chunk<NB> k;
-    const int h = c & 1, ga = c & ~1;
-    const size_t nib_row = (size_t) cols / 2, two_row = (size_t) cols / 4, bit_row = (size_t) cols / 8;
-    // plane index of each part for this width
-    constexpr int P4 = NB == 6 ? 1 : 0;                     // nibble plane
-    constexpr int P2 = NB == 6 ? 0 : NB == 7 ? 1 : 0;       // 2-bit plane
-    constexpr int P1 = NB == 7 ? 2 : 1;                     // 1-bit plane
-    constexpr bool HAS4 = NB == 4 || NB == 5 || NB == 6 || NB == 7 || NB == 8;
-    constexpr bool HAS2 = NB == 2 || NB == 3 || NB == 6 || NB == 7;
-    constexpr bool HAS1 = NB == 3 || NB == 5 || NB == 7;
-    v4u la = {0u, 0u, 0u, 0u}, lb = {0u, 0u, 0u, 0u};
-    int sh = 0;
-    if constexpr (HAS4) {
-        const v4u w = *(const v4u *) (pl[P4] + row * nib_row + (size_t) c * 16);
-        la = w & 0x0F0F0F0Fu;
-        lb = (w >> 4u) & 0x0F0F0F0Fu;
-        sh = 4;
-    }
-    if constexpr (HAS2) {
-        // pack of 32 bytes per 128 weights; bit-plane k of byte j = group 4P+k, column j
-        const v4u e = *(const v4u *) (pl[P2] + row * two_row + (size_t) (c >> 2) * 32 + h * 16);
-        const unsigned ka = 2u * (unsigned) (ga & 3);
-        const v4u ea = (e >> ka) & 0x03030303u, eb = (e >> (ka + 2u)) & 0x03030303u;
-        if constexpr (HAS4) { la |= ea << 4u; lb |= eb << 4u; sh = 6; }
-        else { la = ea; lb = eb; sh = 2; }
-    }
-    if constexpr (HAS1) {
-        // 4 bytes per group, bit j = column j
-        const uint2 wd = *(const uint2 *) (pl[P1] + row * bit_row + (size_t) ga * 4);
-        const uint32_t wa = wd.x >> (16 * h), wb = wd.y >> (16 * h);
-        #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            la[i] |= bits4_to_bytes((wa >> (4 * i)) & 15u) << sh;
-            lb[i] |= bits4_to_bytes((wb >> (4 * i)) & 15u) << sh;
-        }
-    }
-    k.a = la; k.b = lb;
-    if constexpr (NB == 8) {
-        const v4u w = *(const v4u *) (pl[1] + row * nib_row + (size_t) c * 16);
-        k.ha = w & 0x0F0F0F0Fu;
-        k.hb = (w >> 4u) & 0x0F0F0F0Fu;
-    }
-    return k;
+__device__ __forceinline__ void load_chunk(ChunkW<NB> & w, const uint8_t * const * pl, int c) {
+    using P = Planes<NB>;
+    if constexpr (P::N4) w.n4 = __builtin_nontemporal_load((const v4u *) (pl[P::P4] + (size_t) c * 16));
+    if constexpr (NB == 8) w.h4 = __builtin_nontemporal_load((const v4u *) (pl[1] + (size_t) c * 16));
+    if constexpr (P::N2) w.t2 = __builtin_nontemporal_load((const v4u *) (pl[P::P2] + (size_t) (c >> 2) * 32 + (c & 1) * 16));
+    if constexpr (P::N1) w.o1 = __builtin_nontemporal_load((const v2u *) (pl[P::P1] + (size_t) (c >> 1) * 8));
 }
 
-// partial dots of the chunk over its 16 columns against activation words xa, xb
 template <int NB>
-__device__ __forceinline__ void chunk_dots(const Chunk<NB> & k, const v4i xa, const v4i xb, int & da, int & db) {
+__device__ __forceinline__ void zero_chunk(ChunkW<NB> & w) {
+    w.n4 = v4u{0u, 0u, 0u, 0u}; w.h4 = w.n4; w.t2 = w.n4; w.o1 = v2u{0u, 0u};
+}
+
+// partial dots of chunk c over its 16 columns: da for group c&~1 against
+// xa, db for group c|1 against xb
+template <int NB>
+__device__ __forceinline__ void chunk_dots(const ChunkW<NB> & w, int c, const v4i xa, const v4i xb, int & da, int & db) {
+    using P = Planes<NB>;
+    v4u ca = {0u, 0u, 0u, 0u}, cb = {0u, 0u, 0u, 0u};
+    int sh = 0;
+    if constexpr (P::N4) { ca = w.n4 & 0x0F0F0F0Fu; cb = (w.n4 >> 4u) & 0x0F0F0F0Fu; sh = 4; }
+    if constexpr (P::N2) {
+        const unsigned k = 2u * (unsigned) (c & 2);          // bit-plane of group c&~1 within its pack
+        const v4u ea = (w.t2 >> k) & 0x03030303u, eb = (w.t2 >> (k + 2u)) & 0x03030303u;
+        if constexpr (P::N4) { ca |= ea << 4u; cb |= eb << 4u; sh = 6; }
+        else { ca = ea; cb = eb; sh = 2; }
+    }
+    if constexpr (P::N1) {
+        const unsigned wa = w.o1.x >> (16 * (c & 1)), wb = w.o1.y >> (16 * (c & 1));
+        #pragma unroll
+        for (int i = 0; i < 4; i++) {
+            ca[i] |= bits4_to_bytes((wa >> (4 * i)) & 15u) << sh;
+            cb[i] |= bits4_to_bytes((wb >> (4 * i)) & 15u) << sh;
+        }
+    }
     int a = 0, b = 0;
     #pragma unroll
-    for (int i = 0; i < 4; i++) { a = dot4((int) k.a[i], xa[i], a); b = dot4((int) k.b[i], xb[i], b); }
+    for (int i = 0; i < 4; i++) { a = dot4(ca[i], xa[i], a); b = dot4(cb[i], xb[i], b); }
     if constexpr (NB == 8) {
         int ha = 0, hb = 0;
         #pragma unroll
-        for (int i = 0; i < 4; i++) { ha = dot4((int) k.ha[i], xa[i], ha); hb = dot4((int) k.hb[i], xb[i], hb); }
+        for (int i = 0; i < 4; i++) {
+            ha = dot4(w.h4[i] & 0x0F0F0F0Fu, xa[i], ha);
+            hb = dot4((w.h4[i] >> 4u) & 0x0F0F0F0Fu, xb[i], hb);
+        }
         a += ha << 4;
         b += hb << 4;
     }
     da = a; db = b;
 }
 
+// lane i <-> lane i^1 (DPP quad_perm [1,0,3,2])
+__device__ __forceinline__ int pair_swap(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+
 // ---------------------------------------------------------------- GEMV
 //
 // One launch covers up to three matrices that read the same activation (the
-// reference's shared-activation groups, sml/sml-run.c:924-1121). Each wave
-// takes RB consecutive rows at a time and streams them with one lane per
-// 16-byte chunk; the activation (int8 codes, per-group scale and sum) is
-// staged once per workgroup in LDS.
+// reference's shared-activation groups, sml/sml-run.c:924-1121), or gate and
+// up paired for the fused SwiGLU. A wave owns RB rows and streams them whole:
+// lane c takes chunks c, c+64, ... (NI per lane, all loaded before any is
+// used), so every load instruction is 1 KB of contiguous bytes per row and a
+// 34 MB matrix is in flight at once. The activation is staged in LDS by the
+// workgroup, its global loads issued ahead of the weights' (loads return in
+// order), as int8 codes and per-group (scale, scale*sum).
 #define GEMV_THREADS 256
-#define GEMV_U 4
 
-template <int NB, int NR>
-__device__ __forceinline__ void gemv_rows(const sml_kmat * const mats[NR], const int rows_idx[NR], int cols,
-                                          const int8_t * lq, const float * ls, const int32_t * lsum, float acc[NR]) {
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int ng = cols / 32, ns = (ng + 7) / 8;
+template <int NB, int RB, int NI>
+__device__ void gemv_body(const sml_kgemv & a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8;
+    int8_t * lq = (int8_t *) lds;
+    float2 * lsc = (float2 *) (lds + n);
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+    const bool swiglu = a.epi == SML_EPI_SWIGLU;
+    const int rows_per_wave = swiglu ? RB / 2 : RB;
+    const int row0 = (blockIdx.x * (GEMV_THREADS / WAVE) + (tid >> 6)) * rows_per_wave;
+
+    // 1. activation loads (L2-resident, issued first)
+    constexpr int SQ = 4, SG = 2;                  // staged words per thread per round
+    v4i sq_[SQ];
+    int sg_i[SG];
+    float sg_s[SG];
+    int32_t sg_u[SG];
+    const int nq16 = n / 16;
     #pragma unroll
-    for (int r = 0; r < NR; r++) acc[r] = 0.0f;
-    for (int c0 = 0; c0 < ng; c0 += WAVE * GEMV_U) {
-        Chunk<NB> ch[GEMV_U][NR];
-        uint32_t sqv[GEMV_U][NR], mqv[GEMV_U][NR];
-        uint16_t sdv[GEMV_U][NR], mdv[GEMV_U][NR];
+    for (int k = 0; k < SQ; k++) { const int i = tid + k * GEMV_THREADS; if (i < nq16) sq_[k] = ((const v4i *) a.q)[i]; }
+    #pragma unroll
+    for (int k = 0; k < SG; k++) {
+        const int i = tid + k * GEMV_THREADS;
+        sg_i[k] = i;
+        if (i < ng) { sg_s[k] = a.scale[i]; sg_u[k] = a.sums[i]; }
+    }
+
+    // 2. this wave's rows: plane row bases and field rows
+    using P = Planes<NB>;
+    const uint8_t * pl[RB][3];
+    const uint16_t * fq[RB];          // (sq, mq) pairs as one 16-bit word per group
+    const uint32_t * fd[RB];          // (sd, md) pairs as one 32-bit word per superblock
+    int orow[RB];
+    bool valid[RB];
+    #pragma unroll
+    for (int s = 0; s < RB; s++) {
+        const int grow = swiglu ? row0 + (s >> 1) : row0 + s;
+        orow[s] = grow;
+        valid[s] = grow < a.total_rows;
+        int mi = swiglu ? (s & 1) : 0;
+        if (!swiglu) {
+            #pragma unroll
+            for (int i = 1; i < SML_MAX_MATS; i++) if (i < a.nmat && grow >= a.m[i].row_begin) mi = i;
+        }
+        const sml_kmat & m = a.m[mi];
+        const size_t r = (size_t) (valid[s] ? (swiglu ? grow : grow - m.row_begin) : 0);
+        pl[s][0] = m.plane[0]; pl[s][1] = m.plane[1]; pl[s][2] = m.plane[2];
+        if constexpr (P::N4) pl[s][P::P4] = m.plane[P::P4] + r * P::b4(n);
+        if constexpr (NB == 8) pl[s][1] = m.plane[1] + r * P::b4(n);
+        if constexpr (P::N2) pl[s][P::P2] = m.plane[P::P2] + r * P::b2(n);
+        if constexpr (P::N1) pl[s][P::P1] = m.plane[P::P1] + r * P::b1(n);
+        fq[s] = (const uint16_t *) (m.sqmq + r * (size_t) ng * 2);
+        fd[s] = (const uint32_t *) (m.sdmd + r * (size_t) ns * 2);
+    }
+
+    float acc[RB];
+    #pragma unroll
+    for (int s = 0; s < RB; s++) acc[s] = 0.0f;
+    bool staged = false;
+    for (int c0 = 0; c0 < ng; c0 += WAVE * NI) {
+        // 3. every weight load of this lane for NI chunks of RB rows
+        ChunkW<NB> w[NI][RB];
+        uint32_t fqv[NI][RB], fdv[NI][RB];
         #pragma unroll
-        for (int u = 0; u < GEMV_U; u++) {
-            const int c = c0 + u * WAVE + lane;
-            if (c < ng) {
-                #pragma unroll
-                for (int r = 0; r < NR; r++) {
-                    const sml_kmat * m = mats[r];
-                    const size_t row = (size_t) rows_idx[r];
-                    ch[u][r] = load_chunk<NB>(m->plane, row, cols, c);
-                    sqv[u][r] = m->sq[row * ng + c];
-                    sdv[u][r] = m->sd[row * ns + (c >> 3)];
-                    if (m->mq) { mqv[u][r] = m->mq[row * ng + c]; mdv[u][r] = m->md[row * ns + (c >> 3)]; }
-                    else { mqv[u][r] = 127u; mdv[u][r] = 0; }
+        for (int i = 0; i < NI; i++) {
+            const int c = c0 + i * WAVE + lane;
+            #pragma unroll
+            for (int s = 0; s < RB; s++) {
+                if (c < ng && valid[s]) {
+                    load_chunk<NB>(w[i][s], pl[s], c);
+                    fqv[i][s] = fq[s][c];
+                    fdv[i][s] = fd[s][c >> 3];
+                } else {
+                    zero_chunk<NB>(w[i][s]);
+                    fqv[i][s] = 0x7F00u;            // sq 0, mq 127: contributes nothing
+                    fdv[i][s] = 0u;
                 }
             }
         }
+        if (!staged) {
+            // 4. activation into LDS (waits only for the activation loads)
+            #pragma unroll
+            for (int k = 0; k < SQ; k++) { const int idx = tid + k * GEMV_THREADS; if (idx < nq16) ((v4i *) lq)[idx] = sq_[k]; }
+            #pragma unroll
+            for (int k = 0; k < SG; k++) if (sg_i[k] < ng) lsc[sg_i[k]] = make_float2(sg_s[k], sg_s[k] * (float) sg_u[k]);
+            // widths beyond one round of staging
+            for (int idx = tid + SQ * GEMV_THREADS; idx < nq16; idx += GEMV_THREADS) ((v4i *) lq)[idx] = ((const v4i *) a.q)[idx];
+            for (int g = tid + SG * GEMV_THREADS; g < ng; g += GEMV_THREADS) lsc[g] = make_float2(a.scale[g], a.scale[g] * (float) a.sums[g]);
+            __syncthreads();
+            staged = true;
+        }
+        // 5. dots and the per-group epilogue; lane c ends up owning group c
         #pragma unroll
-        for (int u = 0; u < GEMV_U; u++) {
-            const int c = c0 + u * WAVE + lane;
-            if (c < ng) {
-                const int off = 32 * (c & ~1) + 16 * (c & 1);
-                const v4i xa = *(const v4i *) (lq + off);
-                const v4i xb = *(const v4i *) (lq + off + 32);
-                const float s = ls[c];
-                const float sm = s * (float) lsum[c];
-                #pragma unroll
-                for (int r = 0; r < NR; r++) {
-                    int da, db;
-                    chunk_dots<NB>(ch[u][r], xa, xb, da, db);
-                    const int odd = c & 1;
-                    const int keep = odd ? db : da, send = odd ? da : db;
-                    const int dot = keep + pair_swap(send);
-                    const float wsc = h2f(sdv[u][r]) * (float) sqv[u][r];
-                    const float wmn = h2f(mdv[u][r]) * ((float) mqv[u][r] - 127.0f);
-                    acc[r] += wsc * (s * (float) dot);
-                    acc[r] += wmn * sm;
-                }
+        for (int i = 0; i < NI; i++) {
+            const int c = c0 + i * WAVE + lane;
+            const int cc = c < ng ? c : ng - 1;           // keep LDS reads in range
+            const int off = 32 * (cc & ~1) + 16 * (cc & 1);
+            const v4i xa = *(const v4i *) (lq + off);
+            const v4i xb = *(const v4i *) (lq + off + 32);
+            const float2 sc = lsc[cc];
+            const int odd = c & 1;
+            #pragma unroll
+            for (int s = 0; s < RB; s++) {
+                int da, db;
+                chunk_dots<NB>(w[i][s], c, xa, xb, da, db);
+                const int keep = odd ? db : da, send = odd ? da : db;
+                const int dot = keep + pair_swap(send);
+                const uint32_t f = fqv[i][s], d2 = fdv[i][s];
+                const float wsc = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
+                const float wmn = h2f((uint16_t) (d2 >> 16)) * ((float) (f >> 8) - 127.0f);
+                acc[s] += wsc * (sc.x * (float) dot);
+                acc[s] += wmn * sc.y;
             }
         }
     }
     #pragma unroll
-    for (int r = 0; r < NR; r++) acc[r] = wave_sum(acc[r]);
-}
-
-__device__ __forceinline__ void stage_act(const sml_kgemv & a, int8_t * lq, float * ls, int32_t * lsum) {
-    const int n = a.cols, ng = n / 32;
-    for (int i = threadIdx.x; i < n / 16; i += blockDim.x) ((v4i *) lq)[i] = ((const v4i *) a.q)[i];
-    for (int i = threadIdx.x; i < ng; i += blockDim.x) { ls[i] = a.scale[i]; lsum[i] = a.sums[i]; }
-    __syncthreads();
-}
-
-template <int NB, int RB>
-__device__ void gemv_body(const sml_kgemv & a) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    int8_t * lq = (int8_t *) lds;
-    float * ls = (float *) (lds + a.cols);
-    int32_t * lsum = (int32_t *) (lds + a.cols + 4 * (a.cols / 32));
-    stage_act(a, lq, ls, lsum);
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int gw = blockIdx.x * (GEMV_THREADS / WAVE) + (threadIdx.x >> 6);
-    const int nw = gridDim.x * (GEMV_THREADS / WAVE);
-    if (a.epi == SML_EPI_SWIGLU) {
-        // gate row r and up row r together; h[r] = silu(g) * u (sml/sml-run.c:451-454)
-        const int nrb = a.total_rows / RB;
-        for (int rb = gw; rb < nrb; rb += nw) {
-            const sml_kmat * mats[2 * RB];
-            int ri[2 * RB];
-            #pragma unroll
-            for (int r = 0; r < RB; r++) {
-                mats[2 * r] = &a.m[0]; mats[2 * r + 1] = &a.m[1];
-                ri[2 * r] = ri[2 * r + 1] = rb * RB + r;
-            }
-            float acc[2 * RB];
-            gemv_rows<NB, 2 * RB>(mats, ri, a.cols, lq, ls, lsum, acc);
-            if (lane == 0) {
-                #pragma unroll
-                for (int r = 0; r < RB; r++) {
-                    const int row = rb * RB + r;
-                    float g = acc[2 * r], u = acc[2 * r + 1];
-                    if (a.m[0].bias) g += a.m[0].bias[row];
-                    if (a.m[1].bias) u += a.m[1].bias[row];
-                    a.m[0].y[row] = (g / (1.0f + expf(-g))) * u;
-                }
-            }
+    for (int s = 0; s < RB; s++) acc[s] = wave_sum(acc[s]);
+    if (lane != 0) return;
+    if (swiglu) {
+        #pragma unroll
+        for (int s = 0; s < RB; s += 2) {
+            if (!valid[s]) continue;
+            const int row = orow[s];
+            float g = acc[s], u = acc[s + 1];
+            if (a.m[0].bias) g += a.m[0].bias[row];
+            if (a.m[1].bias) u += a.m[1].bias[row];
+            a.m[0].y[row] = (g / (1.0f + expf(-g))) * u;   // sml/sml-run.c:451-454
         }
         return;
     }
-    const int nrb = a.total_rows / RB;
-    for (int rb = gw; rb < nrb; rb += nw) {
-        const int row0 = rb * RB;
+    #pragma unroll
+    for (int s = 0; s < RB; s++) {
+        if (!valid[s]) continue;
         int mi = 0;
         #pragma unroll
-        for (int i = 1; i < SML_MAX_MATS; i++) if (i < a.nmat && row0 >= a.m[i].row_begin) mi = i;
-        const sml_kmat * m = &a.m[mi];
-        const int lrow = row0 - m->row_begin;
-        const sml_kmat * mats[RB];
-        int ri[RB];
-        #pragma unroll
-        for (int r = 0; r < RB; r++) { mats[r] = m; ri[r] = lrow + r; }
-        float acc[RB];
-        gemv_rows<NB, RB>(mats, ri, a.cols, lq, ls, lsum, acc);
-        if (lane == 0) {
-            #pragma unroll
-            for (int r = 0; r < RB; r++) {
-                float v = acc[r];
-                if (m->bias) v += m->bias[lrow + r];
-                if (a.epi == SML_EPI_RESIDUAL) v = a.resid[lrow + r] + v;
-                m->y[lrow + r] = v;
-            }
-        }
+        for (int i = 1; i < SML_MAX_MATS; i++) if (i < a.nmat && orow[s] >= a.m[i].row_begin) mi = i;
+        const sml_kmat & m = a.m[mi];
+        const int lr = orow[s] - m.row_begin;
+        float v = acc[s];
+        if (m.bias) v += m.bias[lr];
+        if (a.epi == SML_EPI_RESIDUAL) v = a.resid[lr] + v;
+        m.y[lr] = v;
     }
 }
 
-#define GEMV_KERNEL(NB, RB)                                                                   \
-    extern "C" __global__ __launch_bounds__(GEMV_THREADS) void sml_gemv_q##NB##_r##RB(const sml_kgemv a) { \
-        gemv_body<NB, RB>(a);                                                                \
+#define GEMV_KERNEL(NB, RB, NI)                                                                                   \
+    extern "C" __global__ __launch_bounds__(GEMV_THREADS) void sml_gemv_q##NB##_r##RB##_i##NI(const sml_kgemv a) { \
+        gemv_body<NB, RB, NI>(a);                                                                                 \
     }
-GEMV_KERNEL(2, 1) GEMV_KERNEL(2, 2)
-GEMV_KERNEL(3, 1) GEMV_KERNEL(3, 2)
-GEMV_KERNEL(4, 1) GEMV_KERNEL(4, 2) GEMV_KERNEL(4, 4)
-GEMV_KERNEL(5, 1) GEMV_KERNEL(5, 2)
-GEMV_KERNEL(6, 1) GEMV_KERNEL(6, 2)
-GEMV_KERNEL(7, 1) GEMV_KERNEL(7, 2)
-GEMV_KERNEL(8, 1) GEMV_KERNEL(8, 2)
+#define GEMV_WIDTH(NB)                                                                     \
+    GEMV_KERNEL(NB, 1, 2) GEMV_KERNEL(NB, 1, 4) GEMV_KERNEL(NB, 1, 8)                     \
+    GEMV_KERNEL(NB, 2, 1) GEMV_KERNEL(NB, 2, 2) GEMV_KERNEL(NB, 2, 4) GEMV_KERNEL(NB, 2, 8) \
+    GEMV_KERNEL(NB, 4, 1) GEMV_KERNEL(NB, 4, 2) GEMV_KERNEL(NB, 4, 4)
+GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH(7) GEMV_WIDTH(8)
 
 // ---------------------------------------------------------------- norm + quantize
 //
@@ -320,7 +352,10 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
                 int w = 0;
                 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    int t = (int) __builtin_rintf(v[j + k] * is);
+                    // x86 cvtps2dq (the reference's AVX2 arm) yields INT_MIN for
+                    // NaN and out-of-range values; the clamp then gives -127
+                    const float r = __builtin_rintf(v[j + k] * is);
+                    int t = (r >= -2147483648.0f && r < 2147483648.0f) ? (int) r : (int) 0x80000000u;
                     t = t > 127 ? 127 : t < -127 ? -127 : t;
                     sum += t;
                     w |= (t & 0xFF) << (8 * k);
@@ -335,8 +370,8 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
 
 // ---------------------------------------------------------------- unpack / embed
 
-// The integer codes of group g of one row, from the planes (same reads as
-// load_chunk, one group at a time).
+// The integer codes of group g of one row, from the planes (the reads of
+// load_chunk / chunk_dots, one group at a time).
 __device__ void group_codes(const sml_kmat & m, int nb, int cols, size_t row, int g, uint8_t out[32]) {
     int pb[3], np = 0;
     // plane widths in storage order (tooling/sml_quantize.py:104-106)
@@ -388,8 +423,10 @@ extern "C" __global__ void sml_embed(const sml_kembed a) {
     const size_t row = (size_t) (a.pos ? a.tok[*a.pos] : *a.tok);
     uint8_t c[32];
     group_codes(a.m, a.nbits, a.cols, row, g, c);
-    const float step = h2f(a.m.sd[row * ns + g / 8]) * (float) a.m.sq[row * ng + g];
-    const float mn = a.m.mq ? h2f(a.m.md[row * ns + g / 8]) * ((float) a.m.mq[row * ng + g] - 127.0f) : 0.0f;
+    const uint8_t * f = a.m.sqmq + (row * ng + g) * 2;
+    const uint16_t * d = a.m.sdmd + (row * ns + g / 8) * 2;
+    const float step = h2f(d[0]) * (float) f[0];
+    const float mn = h2f(d[1]) * ((float) f[1] - 127.0f);
     for (int j = 0; j < 32; j++) {
         const int col = g * 32 + j;
         a.x[a.perm ? a.perm[col] : col] = (float) c[j] * step + mn;
@@ -566,4 +603,29 @@ extern "C" __global__ void sml_advance(const sml_kadvance a) {
 extern "C" __global__ void sml_silu_mul(const sml_ksilu a) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < a.n) { const float g = a.g[i]; a.g[i] = (g / (1.0f + expf(-g))) * a.u[i]; }
+}
+
+// ---------------------------------------------------------------- calibration
+// A streaming read with the GEMV's access size (128-bit loads), grid-stride:
+// what one kernel can pull from HBM on this machine, for the roofline.
+extern "C" __global__ __launch_bounds__(256) void sml_read_stream(const sml_kread a) {
+    const v4u * p = (const v4u *) a.src;
+    const uint64_t nw = a.bytes / 16;
+    v4u acc = {0u, 0u, 0u, 0u};
+    if (a.pattern == 0) {
+        for (uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x; i < nw; i += (uint64_t) gridDim.x * 256)
+            acc ^= __builtin_nontemporal_load(p + i);
+    } else {
+        // the GEMV's quad-per-lane shape: lane reads 4 consecutive 16-byte words
+        for (uint64_t i = ((uint64_t) blockIdx.x * 256 + threadIdx.x) * 4; i + 3 < nw; i += (uint64_t) gridDim.x * 1024) {
+            acc ^= __builtin_nontemporal_load(p + i);
+            acc ^= __builtin_nontemporal_load(p + i + 1);
+            acc ^= __builtin_nontemporal_load(p + i + 2);
+            acc ^= __builtin_nontemporal_load(p + i + 3);
+        }
+    }
+    unsigned v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    #pragma unroll
+    for (int o = 32; o; o >>= 1) v ^= __shfl_xor(v, o);
+    if ((threadIdx.x & 63) == 0) a.sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = v;
 }

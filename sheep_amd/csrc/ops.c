@@ -34,6 +34,18 @@ int sml_hip_sync(void) { OP_BEGIN(-1); HX(hipDeviceSynchronize()); HX_LEAVE(); r
 
 // ------------------------------------------------------------ matrices
 
+// 6-bit group field g of one row (four values in three bytes, sml/sml-kernel.h:79-86)
+static uint32_t field6(const uint8_t * row, size_t g) {
+    const uint8_t * p = row + (g >> 2) * 3;
+    const uint32_t b0 = p[0], b1 = p[1], b2 = p[2];
+    switch (g & 3) {
+    case 0: return b0 & 63u;
+    case 1: return ((b0 >> 6) | (b1 << 2)) & 63u;
+    case 2: return ((b1 >> 4) | (b2 << 4)) & 63u;
+    default: return (b2 >> 2) & 63u;
+    }
+}
+
 sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, const uint8_t * sq,
                          const uint16_t * md, const uint8_t * mq, int rows, int cols, int nbits,
                          int scale6, int minneg) {
@@ -42,59 +54,59 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
     int pb[SSF_MAX_PLANES];
     const int np = ssf_flat_planes(nbits, pb);
     const size_t R = (size_t) rows, ng = (size_t) cols / 32, ns = (size_t) SSF_NSUPER(cols);
-    size_t off[8], sz[8];
-    size_t tot = 0;
-    for (int i = 0; i < np; i++) { sz[i] = R * ssf_plane_row_bytes(pb[i], cols); }
-    sz[3] = R * ns * 2; sz[4] = R * ng; sz[5] = md ? R * ns * 2 : 0; sz[6] = mq ? R * ng : 0;
-    for (int i = np; i < 3; i++) sz[i] = 0;
-    for (int i = 0; i < 7; i++) { off[i] = tot; tot += al256(sz[i]); }
+    size_t off[5], sz[5], tot = 0;
+    for (int i = 0; i < 3; i++) sz[i] = i < np ? R * ssf_plane_row_bytes(pb[i], cols) : 0;
+    sz[3] = R * ng * 2;          // (sq, mq) per group
+    sz[4] = R * ns * 4;          // (sd, md) per superblock
+    for (int i = 0; i < 5; i++) { off[i] = tot; tot += al256(sz[i]); }
+    // the fields interleaved on the host: 8-bit (or widened 6-bit) values, min bias 127
+    uint8_t * fq = malloc(sz[3]);
+    uint16_t * fd = malloc(sz[4]);
+    if (!fq || !fd) { free(fq); free(fd); hx_failf("out of host memory"); }
+    const size_t grow = scale6 ? (ng / 4) * 3 : ng;
+    const uint32_t madd = scale6 ? (minneg ? 64u : 96u) : 0u;   // (v - 31) = (v + 96) - 127; (v - 63) = (v + 64) - 127
+    for (size_t r = 0; r < R; r++) {
+        for (size_t g = 0; g < ng; g++) {
+            const uint32_t q = scale6 ? field6(sq + r * grow, g) : sq[r * grow + g];
+            const uint32_t m = mq ? (scale6 ? field6(mq + r * grow, g) + madd : mq[r * grow + g]) : 127u;
+            fq[(r * ng + g) * 2] = (uint8_t) q;
+            fq[(r * ng + g) * 2 + 1] = (uint8_t) m;
+        }
+        for (size_t k = 0; k < ns; k++) {
+            fd[(r * ns + k) * 2] = sd[r * ns + k];
+            fd[(r * ns + k) * 2 + 1] = md ? md[r * ns + k] : 0;
+        }
+    }
     sml_hip_mat * m = calloc(1, sizeof *m);
-    if (!m) hx_failf("out of host memory");
+    if (!m) { free(fq); free(fd); hx_failf("out of host memory"); }
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) {
+        hx.jb = outer;
+        free(fq); free(fd);
+        if (m->mem) hipFree(m->mem);
+        free(m);
+        longjmp(*outer, 1);
+    }
+    hx.jb = &jb;
     m->mem = hx_malloc(tot);
     uint8_t * base = (uint8_t *) m->mem;
-    m->nbits = nbits;
-    m->cols = cols;
-    m->bytes = 0;
-    for (int i = 0; i < 7; i++) m->bytes += sz[i];
     for (int i = 0; i < np; i++) {
         HX(hipMemcpy(base + off[i], planes[i], sz[i], hipMemcpyHostToDevice));
         m->k.plane[i] = base + off[i];
     }
-    HX(hipMemcpy(base + off[3], sd, sz[3], hipMemcpyHostToDevice));
-    if (md) HX(hipMemcpy(base + off[5], md, sz[5], hipMemcpyHostToDevice));
-    if (!scale6) {
-        HX(hipMemcpy(base + off[4], sq, sz[4], hipMemcpyHostToDevice));
-        if (mq) HX(hipMemcpy(base + off[6], mq, sz[6], hipMemcpyHostToDevice));
-    } else {
-        // widen 6-bit fields (four in three bytes, sml/sml-kernel.h:79-86) to bytes; the
-        // min moves to the 8-bit bias: (v - 31) = (v + 96) - 127, negative-only (v - 63) = (v + 64) - 127
-        uint8_t * w = malloc(R * ng);
-        if (!w) hx_failf("out of host memory");
-        for (int pass = 0; pass < (mq ? 2 : 1); pass++) {
-            const uint8_t * src = pass ? mq : sq;
-            const int add = pass ? (minneg ? 64 : 96) : 0;
-            for (size_t r = 0; r < R; r++)
-                for (size_t g = 0; g < ng; g++) {
-                    const uint8_t * p = src + r * (ng / 4) * 3 + (g >> 2) * 3;
-                    const uint32_t b0 = p[0], b1 = p[1], b2 = p[2];
-                    uint32_t v;
-                    switch (g & 3) {
-                    case 0: v = b0 & 63u; break;
-                    case 1: v = ((b0 >> 6) | (b1 << 2)) & 63u; break;
-                    case 2: v = ((b1 >> 4) | (b2 << 4)) & 63u; break;
-                    default: v = (b2 >> 2) & 63u; break;
-                    }
-                    w[r * ng + g] = (uint8_t) (v + (uint32_t) add);
-                }
-            HX(hipMemcpy(base + off[pass ? 6 : 4], w, R * ng, hipMemcpyHostToDevice));
-        }
-        free(w);
-    }
-    m->k.sd = (const uint16_t *) (base + off[3]);
-    m->k.sq = base + off[4];
-    m->k.md = md ? (const uint16_t *) (base + off[5]) : NULL;
-    m->k.mq = mq ? base + off[6] : NULL;
+    HX(hipMemcpy(base + off[3], fq, sz[3], hipMemcpyHostToDevice));
+    HX(hipMemcpy(base + off[4], fd, sz[4], hipMemcpyHostToDevice));
+    hx.jb = outer;
+    free(fq);
+    free(fd);
+    m->k.sqmq = base + off[3];
+    m->k.sdmd = (const uint16_t *) (base + off[4]);
     m->k.rows = rows;
+    m->nbits = nbits;
+    m->cols = cols;
+    // the bytes a GEMV streams: the file's planes and fields at 8 bits
+    m->bytes = sz[0] + sz[1] + sz[2] + R * ng * (mq ? 2 : 1) + R * ns * (md ? 4 : 2);
     return m;
 }
 
@@ -186,13 +198,26 @@ static int env_int(const char * name, int dflt) {
     return e && *e ? atoi(e) : dflt;
 }
 
-// rows per wave step: 2 where every matrix allows it (SML_GEMV_RB overrides)
-static int pick_rb(int nbits, const int * rows, int nm) {
-    int rb = env_int("SML_GEMV_RB", 2);
-    if (rb != 1 && rb != 2 && rb != 4) rb = 2;
-    if (rb == 4 && nbits != 4) rb = 2;
-    for (int i = 0; i < nm; i++) while (rb > 1 && rows[i] % rb) rb /= 2;
-    return rb;
+// Shape of a GEMV launch: NI chunks per lane (enough that one pass covers a
+// row: ng <= 64*NI, at most 8), RB rows per wave (more rows per wave for tall
+// matrices, so ~2048+ waves carry the whole matrix at once while the loads a
+// lane holds stay within RB*NI <= 16). SML_GEMV_RB / SML_GEMV_NI override.
+static void pick_shape(int rows, int cols, int swiglu, int * rb, int * ni) {
+    const int ng = cols / 32;
+    int i = 1;
+    while (i < 8 && 64 * i < ng) i *= 2;
+    int r = 1;
+    while (r < 4 && rows / (2 * r) >= 2048 && 2 * r * i <= 16) r *= 2;
+    if (swiglu) r = r < 2 ? 2 : r;
+    if (r == 4 && i == 8) i = 4;
+    if (r == 1 && i == 1) i = 2;
+    const int fr = env_int("SML_GEMV_RB", 0), fi = env_int("SML_GEMV_NI", 0);
+    if (fr == 1 || fr == 2 || fr == 4) r = swiglu && fr == 1 ? 2 : fr;
+    if (fi == 1 || fi == 2 || fi == 4 || fi == 8) i = fi;
+    if (r == 1 && i == 1) i = 2;
+    if (r == 4 && i == 8) i = 4;
+    *rb = r;
+    *ni = i;
 }
 
 void op_gemv(hipStream_t st, const sml_hip_mat * const * mats, int nm, int epi, const int8_t * q,
@@ -202,27 +227,27 @@ void op_gemv(hipStream_t st, const sml_hip_mat * const * mats, int nm, int epi, 
     sml_kgemv a;
     memset(&a, 0, sizeof a);
     const int nb = mats[0]->nbits, cols = mats[0]->cols;
-    int rows[SML_MAX_MATS], tot = 0;
+    int tot = 0;
     for (int i = 0; i < nm; i++) {
         if (mats[i]->nbits != nb || mats[i]->cols != cols) hx_failf("gemv group mixes shapes or widths");
         a.m[i] = mats[i]->k;
         a.m[i].y = y[i];
         a.m[i].bias = bias ? bias[i] : NULL;
         a.m[i].row_begin = tot;
-        rows[i] = mats[i]->k.rows;
-        tot += rows[i];
+        tot += mats[i]->k.rows;
     }
-    if (epi == SML_EPI_SWIGLU && (nm != 2 || rows[0] != rows[1])) hx_failf("swiglu needs gate and up of one shape");
+    if (epi == SML_EPI_SWIGLU && (nm != 2 || mats[0]->k.rows != mats[1]->k.rows))
+        hx_failf("swiglu needs gate and up of one shape");
     a.nmat = nm; a.cols = cols; a.epi = epi;
     a.q = q; a.scale = scale; a.sums = sums; a.resid = resid;
-    const int rb = pick_rb(nb, rows, nm);
-    a.total_rows = epi == SML_EPI_SWIGLU ? rows[0] : tot;
-    const int nrb = a.total_rows / rb;
-    int wgs = (nrb + 3) / 4;
-    const int cap = env_int("SML_GEMV_WG_CAP", 0);
-    if (cap > 0 && wgs > cap) wgs = cap;
-    char name[32];
-    snprintf(name, sizeof name, "sml_gemv_q%d_r%d", nb, rb);
+    a.total_rows = epi == SML_EPI_SWIGLU ? mats[0]->k.rows : tot;
+    int rb, ni;
+    pick_shape(a.total_rows, cols, epi == SML_EPI_SWIGLU, &rb, &ni);
+    const int rows_per_wave = epi == SML_EPI_SWIGLU ? rb / 2 : rb;
+    const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
+    const int wgs = (waves + 3) / 4;
+    char name[40];
+    snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d", nb, rb, ni);
     hx_launch(name, (unsigned) wgs, 1, 256, (size_t) cols + 8u * (size_t) (cols / 32), st, &a);
 }
 
@@ -347,6 +372,33 @@ void op_silu_mul(hipStream_t st, float * g, const float * u, int n) {
 int sml_hip_argmax(const float * logits, int n, int32_t * tok) {
     OP_BEGIN(-1);
     op_argmax(0, logits, n, tok, NULL, NULL, 0);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_time_read(const void * const * bufs, int nbuf, size_t bytes, int grid, int iters, float * ms_total) {
+    OP_BEGIN(-1);
+    const int pattern = getenv("SML_READ_PATTERN") ? atoi(getenv("SML_READ_PATTERN")) : 0;
+    if (nbuf < 1 || bytes % 16 || grid < 1) hx_failf("read calibration arguments");
+    uint32_t * sink = hx_malloc((size_t) grid * 16);
+    hipEvent_t e0, e1;
+    HX(hipEventCreate(&e0));
+    HX(hipEventCreate(&e1));
+    sml_kread a;
+    a.bytes = bytes; a.sink = sink; a.pattern = pattern;
+    a.src = bufs[0];
+    hx_launch("sml_read_stream", (unsigned) grid, 1, 256, 0, 0, &a);
+    HX(hipEventRecord(e0, 0));
+    for (int i = 0; i < iters; i++) {
+        a.src = bufs[i % nbuf];
+        hx_launch("sml_read_stream", (unsigned) grid, 1, 256, 0, 0, &a);
+    }
+    HX(hipEventRecord(e1, 0));
+    HX(hipEventSynchronize(e1));
+    HX(hipEventElapsedTime(ms_total, e0, e1));
+    HX(hipEventDestroy(e0));
+    HX(hipEventDestroy(e1));
+    HX(hipFree(sink));
     HX_LEAVE();
     return 0;
 }
