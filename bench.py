@@ -103,6 +103,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemv-only", action="store_true")
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
+    ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: fill the 4096 context)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {a.gpus} is not supported (this build has no "
@@ -142,8 +143,8 @@ def run(a, work):
     sa.synth_model(path, n_ctx_train=N_CTX, **LLAMA)
     log(f"synthetic Llama-3-8B-shaped Q4 file: {os.path.getsize(path) / 1e9:.2f} GB ({time.perf_counter() - t1:.1f}s)")
     K, W = a.steps, a.warmup
-    prompt_len = N_CTX - K - W
-    if prompt_len < 1:
+    prompt_len = a.prompt if a.prompt > 0 else N_CTX - K - W
+    if prompt_len < 1 or prompt_len + K + W > N_CTX:
         raise SystemExit("steps + warmup must stay below the 4096-position context")
     t1 = time.perf_counter()
     dec = sa.Decoder(path, n_ctx=N_CTX)

@@ -173,9 +173,14 @@ static void launch_layer(int L) {
             }
         op_gemv(G.st, ms, nm, SML_EPI_STORE, G.aq[slot[i]], G.as[slot[i]], G.asum[slot[i]], ys, bs, NULL);
     }
+    // with an identity o-proj permutation the attention kernel quantizes its
+    // own output for the o GEMV; otherwise a gather + quantize follows it
+    const int fuse_q = y->perm_o < 0;
     op_attention(G.st, G.q, G.k, G.v, G.kc + (size_t) L * G.n_ctx * kvd, G.vc + (size_t) L * G.n_ctx * kvd,
-                 G.rc, G.rs, G.pos, G.H, G.KV, G.hd, G.n_ctx, G.part, G.att);
-    prep(G.att, NULL, NULL, G.H * G.hd, &y->perm_o, 1, slot);
+                 G.rc, G.rs, G.pos, G.H, G.KV, G.hd, G.n_ctx, G.part, G.att,
+                 fuse_q ? G.aq[0] : NULL, fuse_q ? G.as[0] : NULL, fuse_q ? G.asum[0] : NULL);
+    if (fuse_q) slot[0] = 0;
+    else prep(G.att, NULL, NULL, G.H * G.hd, &y->perm_o, 1, slot);
     gemv1(y->o, slot[0], SML_EPI_RESIDUAL, G.x, NULL, G.x);
     prep(G.x, y->fn, NULL, G.E, y->perm_gu, 2, slot);
     if (slot[0] == slot[1] && y->gate->nbits == y->up->nbits) {

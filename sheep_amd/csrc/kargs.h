@@ -37,6 +37,21 @@ typedef struct {
 } sml_kgemv;
 
 // Gather + optional residual add + optional RMSNorm + per-group int8 quantize.
+// Multi-workgroup RMSNorm + gather + quantize: every workgroup reduces the
+// whole vector's sum of squares itself (in double) and quantizes its own 8
+// groups of each output.
+typedef struct {
+    const float   * x;
+    const float   * norm_w;       // NULL: no norm
+    float           eps;
+    int             n;
+    int             nout;
+    const int32_t * perm[3];
+    int8_t        * q[3];
+    float         * scale[3];
+    int32_t       * sums[3];
+} sml_knormq2;
+
 typedef struct {
     float         * x;            // n floats; updated in place when resid != NULL
     const float   * resid;        // x += resid first, or NULL
@@ -70,30 +85,26 @@ typedef struct {
     float * x;
 } sml_kembed;
 
-typedef struct {
-    float * q;                    // n_head * hd, rotated in place
-    const float * k, * v;         // n_kv * hd
-    uint16_t * kcache, * vcache;  // layer base, [pos][n_kv * hd] fp16
-    const float * cos_t, * sin_t; // [n_ctx][half]
-    const int32_t * pos;
-    int n_head, n_kv, hd, half;
-} sml_kropekv;
 
+// Decode attention: RoPE of q and k at *pos, the fp16 KV write and the
+// split-context scores / softmax / V sums per (split, kv head) workgroup
+// (sml_attn), then the merge of the splits per head (sml_attn_merge), which
+// can also quantize the output per 32 (identity permutation) for the next GEMV.
 typedef struct {
-    const float * q;              // rotated
-    const uint16_t * kcache, * vcache;
+    const float * q;              // n_head * hd, after bias, not rotated
+    const float * k, * v;         // n_kv * hd, after bias
+    uint16_t * kcache, * vcache;  // layer base, [pos][n_kv * hd] fp16
+    const float * cos_t, * sin_t; // [n_ctx][hd/2]
     const int32_t * pos;
     float * part;                 // [n_head][nsplit][hd + 2]
-    int n_head, n_kv, hd, chunk, nsplit;
+    float * out;                  // n_head * hd
+    int8_t * q_out;               // quantized out (or NULL)
+    float * s_out;
+    int32_t * u_out;
+    int n_head, n_kv, nsplit;
     float inv;
 } sml_kattn;
 
-typedef struct {
-    const float * part;
-    const int32_t * pos;
-    float * out;                  // n_head * hd
-    int n_head, hd, chunk, nsplit;
-} sml_kattn_comb;
 
 typedef struct {
     const float * logits;

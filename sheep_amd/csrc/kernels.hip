@@ -34,6 +34,33 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Butterflies inside a 16-lane DPP row (quad_perm xor 1, xor 2, then the
+// half-row and row mirrors): every lane of the row ends with the row's result.
+// A swizzle (xor 16) extends them to 32 lanes.
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL> __device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+__device__ __forceinline__ float sum16(float v) {
+    v += dpp_f<0xB1>(v); v += dpp_f<0x4E>(v); v += dpp_f<0x141>(v); v += dpp_f<0x140>(v);
+    return v;
+}
+__device__ __forceinline__ float max16(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v)); v = fmaxf(v, dpp_f<0x4E>(v)); v = fmaxf(v, dpp_f<0x141>(v)); v = fmaxf(v, dpp_f<0x140>(v));
+    return v;
+}
+__device__ __forceinline__ int isum16(int v) {
+    v += dpp_i<0xB1>(v); v += dpp_i<0x4E>(v); v += dpp_i<0x141>(v); v += dpp_i<0x140>(v);
+    return v;
+}
+// xor 16 within 32 lanes (ds_swizzle bit mode: and 0x1F, xor 0x10)
+__device__ __forceinline__ float swz16_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ float sum32(float v) { v = sum16(v); return v + swz16_f(v); }
+__device__ __forceinline__ float max32(float v) { v = max16(v); return fmaxf(v, swz16_f(v)); }
+__device__ __forceinline__ int isum32(int v) { v = isum16(v); return v + __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+
 __device__ __forceinline__ int dot4(unsigned a, int b, int c) { return __builtin_amdgcn_sdot4((int) a, b, c, false); }
 
 // 4 bits (one per column) -> 4 bytes of 0/1
@@ -63,6 +90,12 @@ template <int NB> struct Planes {
     static __device__ __forceinline__ size_t b1(int cols) { return (size_t) cols / 8; }
 };
 
+template <bool NT, typename T>
+__device__ __forceinline__ T ld(const T * p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
 template <int NB> struct ChunkW {
     v4u n4;                       // nibble plane word (or zeros)
     v4u h4;                       // Q8 high nibbles
@@ -71,18 +104,13 @@ template <int NB> struct ChunkW {
 };
 
 // row bases of each plane (pl[] already offset to the row)
-template <int NB>
+template <int NB, bool NT>
 __device__ __forceinline__ void load_chunk(ChunkW<NB> & w, const uint8_t * const * pl, int c) {
     using P = Planes<NB>;
-    if constexpr (P::N4) w.n4 = __builtin_nontemporal_load((const v4u *) (pl[P::P4] + (size_t) c * 16));
-    if constexpr (NB == 8) w.h4 = __builtin_nontemporal_load((const v4u *) (pl[1] + (size_t) c * 16));
-    if constexpr (P::N2) w.t2 = __builtin_nontemporal_load((const v4u *) (pl[P::P2] + (size_t) (c >> 2) * 32 + (c & 1) * 16));
-    if constexpr (P::N1) w.o1 = __builtin_nontemporal_load((const v2u *) (pl[P::P1] + (size_t) (c >> 1) * 8));
-}
-
-template <int NB>
-__device__ __forceinline__ void zero_chunk(ChunkW<NB> & w) {
-    w.n4 = v4u{0u, 0u, 0u, 0u}; w.h4 = w.n4; w.t2 = w.n4; w.o1 = v2u{0u, 0u};
+    if constexpr (P::N4) w.n4 = ld<NT>((const v4u *) (pl[P::P4] + (size_t) c * 16));
+    if constexpr (NB == 8) w.h4 = ld<NT>((const v4u *) (pl[1] + (size_t) c * 16));
+    if constexpr (P::N2) w.t2 = ld<NT>((const v4u *) (pl[P::P2] + (size_t) (c >> 2) * 32 + (c & 1) * 16));
+    if constexpr (P::N1) w.o1 = ld<NT>((const v2u *) (pl[P::P1] + (size_t) (c >> 1) * 8));
 }
 
 // partial dots of chunk c over its 16 columns: da for group c&~1 against
@@ -136,10 +164,22 @@ __device__ __forceinline__ int pair_swap(int v) { return __builtin_amdgcn_mov_dp
 // 34 MB matrix is in flight at once. The activation is staged in LDS by the
 // workgroup, its global loads issued ahead of the weights' (loads return in
 // order), as int8 codes and per-group (scale, scale*sum).
-#define GEMV_THREADS 256
+// Sum over the wave with DPP: row shifts within each 16-lane row, then the
+// row broadcasts; lane 63 ends up with the total.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    int x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true)); x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true)); x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true)); x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true)); x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false)); x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false));
+    return v;
+}
 
-template <int NB, int RB, int NI>
+template <int NB, int RB, int NI, int WG, bool NT>
 __device__ void gemv_body(const sml_kgemv & a) {
+    constexpr int GEMV_THREADS = WG;
     extern __shared__ __align__(16) uint8_t lds[];
     const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8;
     int8_t * lq = (int8_t *) lds;
@@ -165,7 +205,8 @@ __device__ void gemv_body(const sml_kgemv & a) {
         if (i < ng) { sg_s[k] = a.scale[i]; sg_u[k] = a.sums[i]; }
     }
 
-    // 2. this wave's rows: plane row bases and field rows
+    // 2. this wave's rows: plane row bases and field rows. Rows past the end
+    // read row 0 and contribute nothing (their fields are zeroed below).
     using P = Planes<NB>;
     const uint8_t * pl[RB][3];
     const uint16_t * fq[RB];          // (sq, mq) pairs as one 16-bit word per group
@@ -198,23 +239,28 @@ __device__ void gemv_body(const sml_kgemv & a) {
     for (int s = 0; s < RB; s++) acc[s] = 0.0f;
     bool staged = false;
     for (int c0 = 0; c0 < ng; c0 += WAVE * NI) {
-        // 3. every weight load of this lane for NI chunks of RB rows
+        // 3. every weight load of this lane for NI chunks of RB rows, with no
+        // branches: a chunk past the row's end reads the row's last chunk and
+        // has its fields zeroed (sq 0, md 0), so it adds exactly nothing
         ChunkW<NB> w[NI][RB];
         uint32_t fqv[NI][RB], fdv[NI][RB];
         #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int c = c0 + i * WAVE + lane;
+            const int cl = c < ng ? c : ng - 1;
             #pragma unroll
             for (int s = 0; s < RB; s++) {
-                if (c < ng && valid[s]) {
-                    load_chunk<NB>(w[i][s], pl[s], c);
-                    fqv[i][s] = fq[s][c];
-                    fdv[i][s] = fd[s][c >> 3];
-                } else {
-                    zero_chunk<NB>(w[i][s]);
-                    fqv[i][s] = 0x7F00u;            // sq 0, mq 127: contributes nothing
-                    fdv[i][s] = 0u;
-                }
+                load_chunk<NB, NT>(w[i][s], pl[s], cl);
+                fqv[i][s] = fq[s][cl];
+                fdv[i][s] = fd[s][cl >> 3];
+            }
+        }
+        #pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const bool live = c0 + i * WAVE + lane < ng;
+            #pragma unroll
+            for (int s = 0; s < RB; s++) {
+                if (!(live && valid[s])) { fqv[i][s] = 0x7F00u; fdv[i][s] = 0u; }
             }
         }
         if (!staged) {
@@ -254,8 +300,8 @@ __device__ void gemv_body(const sml_kgemv & a) {
         }
     }
     #pragma unroll
-    for (int s = 0; s < RB; s++) acc[s] = wave_sum(acc[s]);
-    if (lane != 0) return;
+    for (int s = 0; s < RB; s++) acc[s] = wave_sum_dpp(acc[s]);
+    if (lane != WAVE - 1) return;
     if (swiglu) {
         #pragma unroll
         for (int s = 0; s < RB; s += 2) {
@@ -283,10 +329,18 @@ __device__ void gemv_body(const sml_kgemv & a) {
     }
 }
 
-#define GEMV_KERNEL(NB, RB, NI)                                                                                   \
-    extern "C" __global__ __launch_bounds__(GEMV_THREADS) void sml_gemv_q##NB##_r##RB##_i##NI(const sml_kgemv a) { \
-        gemv_body<NB, RB, NI>(a);                                                                                 \
+#define GEMV_KERNEL(NB, RB, NI)                                                                        \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_r##RB##_i##NI(const sml_kgemv a) { \
+        gemv_body<NB, RB, NI, 256, true>(a);                                                           \
     }
+// workgroup-size and load-kind variants of Q4, for tuning
+#define GEMV_KERNEL_V(RB, NI, WG, NT)                                                                                    \
+    extern "C" __global__ __launch_bounds__(WG) void sml_gemv_q4_r##RB##_i##NI##_w##WG##_t##NT(const sml_kgemv a) {   \
+        gemv_body<4, RB, NI, WG, NT>(a);                                                                                 \
+    }
+#define GEMV_V(RB, NI) GEMV_KERNEL_V(RB, NI, 256, 0) GEMV_KERNEL_V(RB, NI, 512, 1) GEMV_KERNEL_V(RB, NI, 512, 0) \
+                       GEMV_KERNEL_V(RB, NI, 1024, 1) GEMV_KERNEL_V(RB, NI, 1024, 0)
+GEMV_V(1, 8) GEMV_V(1, 4) GEMV_V(2, 4) GEMV_V(2, 2) GEMV_V(4, 2) GEMV_V(4, 1) GEMV_V(2, 8)
 #define GEMV_WIDTH(NB)                                                                     \
     GEMV_KERNEL(NB, 1, 2) GEMV_KERNEL(NB, 1, 4) GEMV_KERNEL(NB, 1, 8)                     \
     GEMV_KERNEL(NB, 2, 1) GEMV_KERNEL(NB, 2, 2) GEMV_KERNEL(NB, 2, 4) GEMV_KERNEL(NB, 2, 8) \
@@ -368,6 +422,43 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
     }
 }
 
+// Multi-workgroup form (the decode path's): workgroup b quantizes groups
+// 8b..8b+7 of each output; each reduces the full sum of squares first.
+extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a) {
+    __shared__ double red[4];
+    const int n = a.n, tid = threadIdx.x;
+    float sc = 1.0f;
+    if (a.norm_w) {
+        double ss = 0.0;
+        for (int i = tid * 4; i < n; i += 1024) {
+            const float4 v = *(const float4 *) (a.x + i);
+            ss += (double) v.x * v.x + (double) v.y * v.y + (double) v.z * v.z + (double) v.w * v.w;
+        }
+        #pragma unroll
+        for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        const double tot = red[0] + red[1] + red[2] + red[3];
+        sc = 1.0f / sqrtf((float) (tot / (double) n) + a.eps);
+    }
+    const int j = blockIdx.x * 256 + tid;           // element (group j/32) of every output
+    if (j >= n) return;
+    const int l32 = tid & 31, g = j >> 5;
+    for (int o = 0; o < a.nout; o++) {
+        const int src = a.perm[o] ? a.perm[o][j] : j;
+        const float v = a.norm_w ? a.x[src] * sc * a.norm_w[src] : a.x[src];
+        const float amax = max32(fabsf(v));
+        const float s = amax / 127.0f;
+        const float is = s > 0.0f ? 1.0f / s : 0.0f;
+        const float r = __builtin_rintf(v * is);
+        int t = (r >= -2147483648.0f && r < 2147483648.0f) ? (int) r : (int) 0x80000000u;
+        t = t > 127 ? 127 : t < -127 ? -127 : t;
+        const int sum = isum32(t);
+        a.q[o][j] = (int8_t) t;
+        if (l32 == 0) { a.scale[o][g] = s; a.sums[o][g] = sum; }
+    }
+}
+
 // ---------------------------------------------------------------- unpack / embed
 
 // The integer codes of group g of one row, from the planes (the reads of
@@ -435,130 +526,180 @@ extern "C" __global__ void sml_embed(const sml_kembed a) {
 
 // ---------------------------------------------------------------- attention
 //
-// RoPE (halved pairs, sml/sml-run.c:339-372) on q and k at position *pos, and
-// the fp16 round-to-nearest-even KV write (sml/sml-run.c:68-77,3414-3415).
-extern "C" __global__ void sml_rope_kv(const sml_kropekv a) {
-    const int pos = *a.pos, half = a.half, hd = a.hd, kvd = a.n_kv * hd;
-    const float * cs = a.cos_t + (size_t) pos * half, * sn = a.sin_t + (size_t) pos * half;
-    for (int i = threadIdx.x; i < a.n_head * half; i += blockDim.x) {
-        const int h = i / half, j = i % half;
-        float * v = a.q + (size_t) h * hd;
-        const float x0 = v[j], x1 = v[j + half];
-        v[j] = x0 * cs[j] - x1 * sn[j];
-        v[j + half] = x0 * sn[j] + x1 * cs[j];
-    }
-    uint16_t * kc = a.kcache + (size_t) pos * kvd, * vc = a.vcache + (size_t) pos * kvd;
-    for (int i = threadIdx.x; i < a.n_kv * half; i += blockDim.x) {
-        const int h = i / half, j = i % half;
-        const float * v = a.k + (size_t) h * hd;
-        const float x0 = v[j], x1 = v[j + half];
-        kc[h * hd + j] = f2h(x0 * cs[j] - x1 * sn[j]);
-        kc[h * hd + j + half] = f2h(x0 * sn[j] + x1 * cs[j]);
-    }
-    for (int i = threadIdx.x; i < kvd; i += blockDim.x) vc[i] = f2h(a.v[i]);
-}
-
-// Split-context decode attention (sml/sml-run.c:180-287 computes the same
-// softmax-weighted sum per head in one pass). Workgroup (split, kv head)
-// scores its chunk of positions for every query head sharing that KV head,
-// keeps an unnormalised partial (max, sum, weighted V), and sml_attn_combine
-// merges the partials. head_dim 128, chunk 64.
+// Decode attention in one launch (sml/sml-run.c:180-287 per head: scores
+// q.k/sqrt(hd), softmax with the running max subtracted, weighted sum of V).
+// Workgroup (split, kv head) covers ATTN_CHUNK positions for the rep query
+// heads sharing that KV head: 16 lanes per position read 256 contiguous bytes
+// of K (then of V), so the cache streams coalesced. The workgroup holding
+// position *pos rotates and rounds k to fp16 itself, writes k and v to the
+// cache and uses them from LDS. Each split leaves (max, sum, unnormalised V
+// sum) for sml_attn_merge.
 #define ATTN_THREADS 256
-#define ATTN_CHUNK 64
+#define ATTN_CHUNK 128
 #define ATTN_MAXREP 8
+#define HD 128
 
-extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn_part(const sml_kattn a) {
-    __shared__ float qs[ATTN_MAXREP][128];
+extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_kattn a) {
+    __shared__ float qs[ATTN_MAXREP][HD];
     __shared__ float sc[ATTN_MAXREP][ATTN_CHUNK];
-    __shared__ float ov[ATTN_MAXREP][2][128];
-    const int kh = blockIdx.y, split = blockIdx.x;
-    const int rep = a.n_head / a.n_kv, hd = 128, kvd = a.n_kv * hd;
-    const int T = *a.pos + 1, t0 = split * ATTN_CHUNK;
-    const int tid = threadIdx.x;
-    float * part0 = a.part + ((size_t) (kh * rep) * a.nsplit + split) * (hd + 2);
-    if (t0 >= T) {
-        // empty split: marks itself so the combine skips it
-        for (int j = 0; j < rep; j++)
-            if (tid == 0) part0[(size_t) j * a.nsplit * (hd + 2) + hd] = -INFINITY;
-        return;
-    }
+    __shared__ float kp[HD], vp[HD];
+    __shared__ float red[4][ATTN_MAXREP][HD];
+    __shared__ float mx_s[ATTN_MAXREP], l_s[ATTN_MAXREP];
+    const int kh = blockIdx.y, split = blockIdx.x, tid = threadIdx.x;
+    const int rep = a.n_head / a.n_kv, kvd = a.n_kv * HD, half = HD / 2;
+    const int pos = *a.pos, T = pos + 1, t0 = split * ATTN_CHUNK;
+    if (t0 >= T) return;
     const int t1 = min(T, t0 + ATTN_CHUNK);
-    for (int i = tid; i < rep * hd; i += ATTN_THREADS) qs[i / hd][i % hd] = a.q[(size_t) (kh * rep) * hd + i];
+    const float * cs = a.cos_t + (size_t) pos * half, * sn = a.sin_t + (size_t) pos * half;
+    // RoPE of this kv head's query heads (halved pairs, sml/sml-run.c:363-368)
+    for (int i = tid; i < rep * half; i += ATTN_THREADS) {
+        const int j = i / half, d = i % half;
+        const float * v = a.q + (size_t) (kh * rep + j) * HD;
+        const float x0 = v[d], x1 = v[d + half];
+        qs[j][d] = x0 * cs[d] - x1 * sn[d];
+        qs[j][d + half] = x0 * sn[d] + x1 * cs[d];
+    }
+    const bool has_pos = t0 <= pos && pos < t1;
+    if (has_pos) {
+        // k rotated, then rounded to fp16 as the cache stores it (sml/sml-run.c:3414-3415)
+        uint16_t * kc = a.kcache + (size_t) pos * kvd + (size_t) kh * HD;
+        uint16_t * vc = a.vcache + (size_t) pos * kvd + (size_t) kh * HD;
+        if (tid < half) {
+            const float * v = a.k + (size_t) kh * HD;
+            const float x0 = v[tid], x1 = v[tid + half];
+            const uint16_t h0 = f2h(x0 * cs[tid] - x1 * sn[tid]), h1 = f2h(x0 * sn[tid] + x1 * cs[tid]);
+            kc[tid] = h0; kc[tid + half] = h1;
+            kp[tid] = h2f(h0); kp[tid + half] = h2f(h1);
+        } else if (tid < half + HD) {
+            const int d = tid - half;
+            const uint16_t h = f2h(a.v[(size_t) kh * HD + d]);
+            vc[d] = h;
+            vp[d] = h2f(h);
+        }
+    }
     __syncthreads();
-    // scores: 16 lanes per position, 8 dims (16 bytes of K) per lane
+    // scores: 16 lanes per position, 16 positions per pass
     const int grp = tid >> 4, l16 = tid & 15;
-    for (int t = t0 + grp; t < t0 + ATTN_CHUNK; t += ATTN_THREADS / 16) {
+    for (int t = t0 + grp; t < t0 + ATTN_CHUNK; t += 16) {
         float kf[8];
-        const bool live = t < t1;
-        if (live) {
-            const v4i w = *(const v4i *) (a.kcache + (size_t) t * kvd + (size_t) kh * hd + l16 * 8);
+        if (t < t1 && t != pos) {
+            const v4u w = *(const v4u *) (a.kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8);
             #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                kf[2 * i] = h2f((uint16_t) (w[i] & 0xFFFF));
-                kf[2 * i + 1] = h2f((uint16_t) ((uint32_t) w[i] >> 16));
-            }
+            for (int i = 0; i < 4; i++) { kf[2 * i] = h2f((uint16_t) (w[i] & 0xFFFFu)); kf[2 * i + 1] = h2f((uint16_t) (w[i] >> 16)); }
         } else {
             #pragma unroll
-            for (int i = 0; i < 8; i++) kf[i] = 0.0f;
+            for (int i = 0; i < 8; i++) kf[i] = t == pos ? kp[l16 * 8 + i] : 0.0f;
         }
-        for (int j = 0; j < rep; j++) {
+        #pragma unroll
+        for (int j = 0; j < ATTN_MAXREP; j++) {
+            if (j >= rep) break;
             float p = 0.0f;
             #pragma unroll
             for (int i = 0; i < 8; i++) p += qs[j][l16 * 8 + i] * kf[i];
-            #pragma unroll
-            for (int o = 8; o; o >>= 1) p += __shfl_xor(p, o);
-            if (l16 == 0) sc[j][t - t0] = live ? p * a.inv : -INFINITY;
+            p = sum16(p);
+            if (l16 == 0) sc[j][t - t0] = t < t1 ? p * a.inv : -INFINITY;
         }
     }
     __syncthreads();
-    // per head: max and exp over the chunk (one wave per head, one lane per position)
+    // per head: chunk max, exponentials, sum (one wave per head, two positions per lane)
     const int wave = tid >> 6, lane = tid & 63;
-    __shared__ float mx_s[ATTN_MAXREP], l_s[ATTN_MAXREP];
     for (int j = wave; j < rep; j += ATTN_THREADS / WAVE) {
-        const float s = sc[j][lane];
-        const float m = wave_max(s);
-        const float p = s == -INFINITY ? 0.0f : expf(s - m);
-        const float l = wave_sum(p);
-        sc[j][lane] = p;
+        const float s0 = sc[j][lane], s1 = sc[j][lane + 64];
+        const float m = wave_max(fmaxf(s0, s1));
+        const float p0 = s0 == -INFINITY ? 0.0f : expf(s0 - m), p1 = s1 == -INFINITY ? 0.0f : expf(s1 - m);
+        const float l = wave_sum(p0 + p1);
+        sc[j][lane] = p0;
+        sc[j][lane + 64] = p1;
         if (lane == 0) { mx_s[j] = m; l_s[j] = l; }
     }
     __syncthreads();
-    // weighted V: thread (half, d) over positions of its parity
-    const int d = tid & 127, hf = tid >> 7;
-    float acc[ATTN_MAXREP];
+    // weighted V: 16 dim-chunks of 8 x 16 position lanes
+    const int dc = tid & 15, pl = tid >> 4;
+    float acc[ATTN_MAXREP][8];
     #pragma unroll
-    for (int j = 0; j < ATTN_MAXREP; j++) acc[j] = 0.0f;
-    for (int t = t0 + hf; t < t1; t += 2) {
-        const float v = h2f(a.vcache[(size_t) t * kvd + (size_t) kh * hd + d]);
+    for (int j = 0; j < ATTN_MAXREP; j++)
         #pragma unroll
-        for (int j = 0; j < ATTN_MAXREP; j++) if (j < rep) acc[j] += sc[j][t - t0] * v;
-    }
-    #pragma unroll
-    for (int j = 0; j < ATTN_MAXREP; j++) if (j < rep) ov[j][hf][d] = acc[j];
-    __syncthreads();
-    if (hf == 0) {
-        for (int j = 0; j < rep; j++) {
-            float * part = part0 + (size_t) j * a.nsplit * (hd + 2);
-            part[d] = ov[j][0][d] + ov[j][1][d];
-            if (d == 0) { part[hd] = mx_s[j]; part[hd + 1] = l_s[j]; }
+        for (int i = 0; i < 8; i++) acc[j][i] = 0.0f;
+    for (int t = t0 + pl; t < t1; t += 16) {
+        float vf[8];
+        if (t != pos) {
+            const v4u w = *(const v4u *) (a.vcache + (size_t) t * kvd + (size_t) kh * HD + dc * 8);
+            #pragma unroll
+            for (int i = 0; i < 4; i++) { vf[2 * i] = h2f((uint16_t) (w[i] & 0xFFFFu)); vf[2 * i + 1] = h2f((uint16_t) (w[i] >> 16)); }
+        } else {
+            #pragma unroll
+            for (int i = 0; i < 8; i++) vf[i] = vp[dc * 8 + i];
         }
+        #pragma unroll
+        for (int j = 0; j < ATTN_MAXREP; j++) {
+            if (j >= rep) break;
+            const float p = sc[j][t - t0];
+            #pragma unroll
+            for (int i = 0; i < 8; i++) acc[j][i] += p * vf[i];
+        }
+    }
+    // reduce over the 4 position lanes of a wave (lanes 16 apart), then over waves
+    #pragma unroll
+    for (int j = 0; j < ATTN_MAXREP; j++) {
+        if (j >= rep) break;
+        #pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float v = acc[j][i];
+            v += swz16_f(v);
+            v += __shfl_xor(v, 32);
+            acc[j][i] = v;
+        }
+        if (lane < 16) {
+            #pragma unroll
+            for (int i = 0; i < 8; i++) red[wave][j][dc * 8 + i] = acc[j][i];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < rep * HD; i += ATTN_THREADS) {
+        const int j = i / HD, d = i % HD;
+        float * part = a.part + ((size_t) (kh * rep + j) * a.nsplit + split) * (HD + 2);
+        part[d] = red[0][j][d] + red[1][j][d] + red[2][j][d] + red[3][j][d];
+        if (d == 0) { part[HD] = mx_s[j]; part[HD + 1] = l_s[j]; }
     }
 }
 
-extern "C" __global__ void sml_attn_combine(const sml_kattn_comb a) {
-    const int h = blockIdx.x, d = threadIdx.x, hd = a.hd;
-    const int T = *a.pos + 1, ns = (T + a.chunk - 1) / a.chunk;
-    const float * p = a.part + (size_t) h * a.nsplit * (hd + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, p[(size_t) s * (hd + 2) + hd]);
-    float l = 0.0f, o = 0.0f;
-    for (int s = 0; s < ns; s++) {
-        const float * ps = p + (size_t) s * (hd + 2);
-        const float e = expf(ps[hd] - M);
-        l += e * ps[hd + 1];
-        o += e * ps[d];
+// Merge of the splits of one query head (grid: n_head workgroups of HD
+// threads), in split order: out = sum_s e_s o_s / sum_s e_s l_s with
+// e_s = exp(m_s - max m). With q_out set, the head's 128 outputs (4 groups of
+// 32, identity permutation) are also quantized for the next GEMV
+// (sml/sml-kernel.c:86-106).
+extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn a) {
+    __shared__ float em[64], ls[64];
+    __shared__ float lsum;
+    const int h = blockIdx.x, d = threadIdx.x;
+    const int T = *a.pos + 1, nact = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    const float * p = a.part + (size_t) h * a.nsplit * (HD + 2);
+    for (int s2 = d; s2 < nact; s2 += HD) { em[s2] = p[(size_t) s2 * (HD + 2) + HD]; ls[s2] = p[(size_t) s2 * (HD + 2) + HD + 1]; }
+    __syncthreads();
+    if (d == 0) {
+        float M = -INFINITY;
+        for (int s2 = 0; s2 < nact; s2++) M = fmaxf(M, em[s2]);
+        float l = 0.0f;
+        for (int s2 = 0; s2 < nact; s2++) { const float e = expf(em[s2] - M); em[s2] = e; l += e * ls[s2]; }
+        lsum = l;
     }
-    a.out[(size_t) h * hd + d] = o / l;
+    __syncthreads();
+    float o = 0.0f;
+    #pragma unroll 8
+    for (int s2 = 0; s2 < nact; s2++) o += em[s2] * p[(size_t) s2 * (HD + 2) + d];
+    const float r = o / lsum;
+    a.out[(size_t) h * HD + d] = r;
+    if (!a.q_out) return;
+    const float amax = max32(fabsf(r));
+    const float s = amax / 127.0f;
+    const float is = s > 0.0f ? 1.0f / s : 0.0f;
+    const float rr = __builtin_rintf(r * is);
+    int t = (rr >= -2147483648.0f && rr < 2147483648.0f) ? (int) rr : (int) 0x80000000u;
+    t = t > 127 ? 127 : t < -127 ? -127 : t;
+    const int sum = isum32(t);
+    const int g = h * 4 + (d >> 5);
+    a.q_out[(size_t) h * HD + d] = (int8_t) t;
+    if ((d & 31) == 0) { a.s_out[g] = s; a.u_out[g] = sum; }
 }
 
 // ---------------------------------------------------------------- argmax
@@ -615,6 +756,14 @@ extern "C" __global__ __launch_bounds__(256) void sml_read_stream(const sml_krea
     if (a.pattern == 0) {
         for (uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x; i < nw; i += (uint64_t) gridDim.x * 256)
             acc ^= __builtin_nontemporal_load(p + i);
+    } else if (a.pattern == 2) {
+        // one shot: each thread issues its 4 coalesced words before using any
+        const uint64_t base = (uint64_t) blockIdx.x * 1024 + threadIdx.x;
+        v4u t[4];
+        #pragma unroll
+        for (int k = 0; k < 4; k++) { const uint64_t i = base + (uint64_t) k * 256; t[k] = __builtin_nontemporal_load(p + (i < nw ? i : 0)); }
+        #pragma unroll
+        for (int k = 0; k < 4; k++) acc ^= t[k];
     } else {
         // the GEMV's quad-per-lane shape: lane reads 4 consecutive 16-byte words
         for (uint64_t i = ((uint64_t) blockIdx.x * 256 + threadIdx.x) * 4; i + 3 < nw; i += (uint64_t) gridDim.x * 1024) {

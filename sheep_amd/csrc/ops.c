@@ -182,6 +182,14 @@ void op_normq(hipStream_t st, float * x, const float * resid, const float * w, f
     a.x = x; a.resid = resid; a.norm_w = w; a.eps = eps; a.n = n; a.nout = nout;
     for (int i = 0; i < nout; i++) { a.perm[i] = perm[i]; a.q[i] = q[i]; a.scale[i] = scale[i]; a.sums[i] = sums[i]; }
     a.normed = normed; a.per256 = per256;
+    if (!resid && !normed && !per256) {
+        sml_knormq2 b;
+        memset(&b, 0, sizeof b);
+        b.x = x; b.norm_w = w; b.eps = eps; b.n = n; b.nout = nout;
+        for (int i = 0; i < nout; i++) { b.perm[i] = perm[i]; b.q[i] = q[i]; b.scale[i] = scale[i]; b.sums[i] = sums[i]; }
+        hx_launch("sml_normq2", (unsigned) ((n + 255) / 256), 1, 256, 0, st, &b);
+        return;
+    }
     hx_launch("sml_normq", 1, 1, 1024, (size_t) n * 4, st, &a);
 }
 
@@ -246,7 +254,15 @@ void op_gemv(hipStream_t st, const sml_hip_mat * const * mats, int nm, int epi, 
     const int rows_per_wave = epi == SML_EPI_SWIGLU ? rb / 2 : rb;
     const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
     const int wgs = (waves + 3) / 4;
-    char name[40];
+    const int wg = env_int("SML_GEMV_WG", 256), nt = env_int("SML_GEMV_NT", 1);
+    char name[48];
+    if (nb == 4 && (wg != 256 || !nt) && (wg == 256 || wg == 512 || wg == 1024)) {
+        snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_w%d_t%d", nb, rb, ni, wg, nt ? 1 : 0);
+        const int wpg = wg / 64;
+        hx_launch(name, (unsigned) ((waves + wpg - 1) / wpg), 1, (unsigned) wg,
+                  (size_t) cols + 8u * (size_t) (cols / 32), st, &a);
+        return;
+    }
     snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d", nb, rb, ni);
     hx_launch(name, (unsigned) wgs, 1, 256, (size_t) cols + 8u * (size_t) (cols / 32), st, &a);
 }
@@ -312,41 +328,36 @@ int sml_hip_embed(const sml_hip_mat * m, const int32_t * tok, const int32_t * pe
     return 0;
 }
 
-#define ATTN_CHUNK 64
+#define ATTN_CHUNK 128
 
 size_t sml_hip_attn_part_floats(int n_head, int hd, int n_ctx) {
     const int ns = (n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
     return (size_t) n_head * ns * (size_t) (hd + 2);
 }
 
-void op_attention(hipStream_t st, float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
+void op_attention(hipStream_t st, const float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
                   const float * cos_t, const float * sin_t, const int32_t * pos, int n_head, int n_kv,
-                  int hd, int n_ctx, float * part, float * out) {
+                  int hd, int n_ctx, float * part, float * out, int8_t * q_out, float * s_out,
+                  int32_t * u_out) {
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
-    sml_kropekv r;
-    memset(&r, 0, sizeof r);
-    r.q = q; r.k = k; r.v = v; r.kcache = kc; r.vcache = vc; r.cos_t = cos_t; r.sin_t = sin_t; r.pos = pos;
-    r.n_head = n_head; r.n_kv = n_kv; r.hd = hd; r.half = hd / 2;
-    hx_launch("sml_rope_kv", 1, 1, 256, 0, st, &r);
     const int ns = (n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
     sml_kattn a;
     memset(&a, 0, sizeof a);
-    a.q = q; a.kcache = kc; a.vcache = vc; a.pos = pos; a.part = part;
-    a.n_head = n_head; a.n_kv = n_kv; a.hd = hd; a.chunk = ATTN_CHUNK; a.nsplit = ns;
+    a.q = q; a.k = k; a.v = v; a.kcache = kc; a.vcache = vc; a.cos_t = cos_t; a.sin_t = sin_t; a.pos = pos;
+    a.part = part; a.out = out; a.q_out = q_out; a.s_out = s_out; a.u_out = u_out;
+    a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
-    hx_launch("sml_attn_part", (unsigned) ns, (unsigned) n_kv, 256, 0, st, &a);
-    sml_kattn_comb c;
-    memset(&c, 0, sizeof c);
-    c.part = part; c.pos = pos; c.out = out; c.n_head = n_head; c.hd = hd; c.chunk = ATTN_CHUNK; c.nsplit = ns;
-    hx_launch("sml_attn_combine", (unsigned) n_head, 1, (unsigned) hd, 0, st, &c);
+    hx_launch("sml_attn", (unsigned) ns, (unsigned) n_kv, 256, 0, st, &a);
+    hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
 }
 
 int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,
                       const float * cos_t, const float * sin_t, const int32_t * pos,
                       int n_head, int n_kv, int hd, int n_ctx, float * part, float * out) {
     OP_BEGIN(-1);
-    op_attention(0, q, k, v, kcache, vcache, cos_t, sin_t, pos, n_head, n_kv, hd, n_ctx, part, out);
+    op_attention(0, q, k, v, kcache, vcache, cos_t, sin_t, pos, n_head, n_kv, hd, n_ctx, part, out,
+                 NULL, NULL, NULL);
     HX_LEAVE();
     return 0;
 }

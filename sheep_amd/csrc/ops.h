@@ -28,9 +28,10 @@ void op_gemv(hipStream_t st, const sml_hip_mat * const * mats, int nm, int epi, 
              const float * resid);
 void op_embed(hipStream_t st, const sml_hip_mat * m, const int32_t * tok, const int32_t * pos,
               const int32_t * perm, float * x);
-void op_attention(hipStream_t st, float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
+void op_attention(hipStream_t st, const float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
                   const float * cos_t, const float * sin_t, const int32_t * pos, int n_head, int n_kv,
-                  int hd, int n_ctx, float * part, float * out);
+                  int hd, int n_ctx, float * part, float * out, int8_t * q_out, float * s_out,
+                  int32_t * u_out);
 void op_argmax(hipStream_t st, const float * logits, int n, int32_t * tok, int32_t * pos, int32_t * hist,
                int hist_n);
 void op_advance(hipStream_t st, int32_t * pos);
