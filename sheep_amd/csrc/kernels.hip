@@ -550,6 +550,17 @@ extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_ka
     const int pos = *a.pos, T = pos + 1, t0 = split * ATTN_CHUNK;
     if (t0 >= T) return;
     const int t1 = min(T, t0 + ATTN_CHUNK);
+    // every K and V load of this lane first (one round trip for the chunk):
+    // lane (grp, l16) covers positions t0 + grp + 16i, dims 8*l16 .. +7
+    const int grp = tid >> 4, l16 = tid & 15;
+    v4u kw[ATTN_CHUNK / 16], vw[ATTN_CHUNK / 16];
+    #pragma unroll
+    for (int i = 0; i < ATTN_CHUNK / 16; i++) {
+        int t = t0 + grp + 16 * i;
+        t = t < t1 ? t : t0;                          // in range; masked below
+        kw[i] = __builtin_nontemporal_load((const v4u *) (a.kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
+        vw[i] = __builtin_nontemporal_load((const v4u *) (a.vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
+    }
     const float * cs = a.cos_t + (size_t) pos * half, * sn = a.sin_t + (size_t) pos * half;
     // RoPE of this kv head's query heads (halved pairs, sml/sml-run.c:363-368)
     for (int i = tid; i < rep * half; i += ATTN_THREADS) {
@@ -579,23 +590,23 @@ extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_ka
     }
     __syncthreads();
     // scores: 16 lanes per position, 16 positions per pass
-    const int grp = tid >> 4, l16 = tid & 15;
-    for (int t = t0 + grp; t < t0 + ATTN_CHUNK; t += 16) {
+    #pragma unroll
+    for (int i = 0; i < ATTN_CHUNK / 16; i++) {
+        const int t = t0 + grp + 16 * i;
         float kf[8];
-        if (t < t1 && t != pos) {
-            const v4u w = *(const v4u *) (a.kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8);
+        if (t != pos) {
             #pragma unroll
-            for (int i = 0; i < 4; i++) { kf[2 * i] = h2f((uint16_t) (w[i] & 0xFFFFu)); kf[2 * i + 1] = h2f((uint16_t) (w[i] >> 16)); }
+            for (int e = 0; e < 4; e++) { kf[2 * e] = h2f((uint16_t) (kw[i][e] & 0xFFFFu)); kf[2 * e + 1] = h2f((uint16_t) (kw[i][e] >> 16)); }
         } else {
             #pragma unroll
-            for (int i = 0; i < 8; i++) kf[i] = t == pos ? kp[l16 * 8 + i] : 0.0f;
+            for (int e = 0; e < 8; e++) kf[e] = kp[l16 * 8 + e];
         }
         #pragma unroll
         for (int j = 0; j < ATTN_MAXREP; j++) {
             if (j >= rep) break;
             float p = 0.0f;
             #pragma unroll
-            for (int i = 0; i < 8; i++) p += qs[j][l16 * 8 + i] * kf[i];
+            for (int e = 0; e < 8; e++) p += qs[j][l16 * 8 + e] * kf[e];
             p = sum16(p);
             if (l16 == 0) sc[j][t - t0] = t < t1 ? p * a.inv : -INFINITY;
         }
@@ -613,29 +624,30 @@ extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_ka
         if (lane == 0) { mx_s[j] = m; l_s[j] = l; }
     }
     __syncthreads();
-    // weighted V: 16 dim-chunks of 8 x 16 position lanes
-    const int dc = tid & 15, pl = tid >> 4;
+    // weighted V over the same positions (weights of masked positions are 0)
+    const int dc = l16;
     float acc[ATTN_MAXREP][8];
     #pragma unroll
     for (int j = 0; j < ATTN_MAXREP; j++)
         #pragma unroll
-        for (int i = 0; i < 8; i++) acc[j][i] = 0.0f;
-    for (int t = t0 + pl; t < t1; t += 16) {
+        for (int e = 0; e < 8; e++) acc[j][e] = 0.0f;
+    #pragma unroll
+    for (int i = 0; i < ATTN_CHUNK / 16; i++) {
+        const int t = t0 + grp + 16 * i;
         float vf[8];
         if (t != pos) {
-            const v4u w = *(const v4u *) (a.vcache + (size_t) t * kvd + (size_t) kh * HD + dc * 8);
             #pragma unroll
-            for (int i = 0; i < 4; i++) { vf[2 * i] = h2f((uint16_t) (w[i] & 0xFFFFu)); vf[2 * i + 1] = h2f((uint16_t) (w[i] >> 16)); }
+            for (int e = 0; e < 4; e++) { vf[2 * e] = h2f((uint16_t) (vw[i][e] & 0xFFFFu)); vf[2 * e + 1] = h2f((uint16_t) (vw[i][e] >> 16)); }
         } else {
             #pragma unroll
-            for (int i = 0; i < 8; i++) vf[i] = vp[dc * 8 + i];
+            for (int e = 0; e < 8; e++) vf[e] = vp[dc * 8 + e];
         }
         #pragma unroll
         for (int j = 0; j < ATTN_MAXREP; j++) {
             if (j >= rep) break;
-            const float p = sc[j][t - t0];
+            const float p = t < t1 ? sc[j][t - t0] : 0.0f;
             #pragma unroll
-            for (int i = 0; i < 8; i++) acc[j][i] += p * vf[i];
+            for (int e = 0; e < 8; e++) acc[j][e] += p * vf[e];
         }
     }
     // reduce over the 4 position lanes of a wave (lanes 16 apart), then over waves
