@@ -1,7 +1,7 @@
 """Benchmark: Llama-3-8B-shaped Q4 batch-1 greedy decode at 4k context on one
 MI355X, plus the Q4 GEMV HBM roofline and the reference CPU path beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--gemv-only]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-traffic] [--gemv-only]
 
 A step is one decode token: one pass of the hot path (embed, 32 layers of
 normq / q-k-v GEMV / RoPE + fp16 KV attention / o GEMV / normq / SwiGLU GEMV /
@@ -71,7 +71,82 @@ def gemv_roofline(rows, cols, iters=400, target_bytes=1.2e9, tmp=None):
     return float(np.median(trials)), first.bytes
 
 
-def cpu_baseline(path, threads, budget_s=12.0, max_tokens=160):
+COPY_BYTES = 256 << 20
+PROBE_LAUNCHES = 12
+
+
+def pmc_probe(path):
+    """Child of traffic(): the roofline GEMV on two copies of one matrix
+    (PROBE_LAUNCHES launches) and a plain copy of COPY_BYTES (3 launches), so
+    a counter pass sees both kernels in one process."""
+    sa.init(0)
+    a, b = sa.DevBuf(COPY_BYTES), sa.DevBuf(COPY_BYTES)
+    for _ in range(3):
+        if sa.lib().sml_hip_copy(b.ptr, a.ptr, COPY_BYTES) != 0:
+            raise SystemExit("copy failed: " + sa.lib().sml_hip_last_error().decode())
+    mats = [sa.Mat.from_file(path, "w") for _ in range(2)]
+    rows, cols = mats[0].rows, mats[0].cols
+    x = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
+    act = sa.Act(cols)
+    sa.normq(sa.DevBuf.of(x), act)
+    y = sa.DevBuf(rows * 4)
+    for i in range(PROBE_LAUNCHES):
+        sa.matvec(mats[i % 2], act, y)
+    sa.sync()
+
+
+def _counter_means(out_dir, counter):
+    """Mean counter value per dispatch, by kernel name, from a rocprofv3
+    counter-collection CSV."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(out_dir, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise RuntimeError(f"no counter_collection.csv under {out_dir}")
+    vals = {}
+    with open(files[0], newline="") as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") != counter:
+                continue
+            vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return {k: float(np.mean(v)) for k, v in vals.items()}
+
+
+def traffic(path, work):
+    """HBM bytes per launch of the roofline GEMV from two rocprofv3 --pmc
+    passes (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by
+    what the same counter reads for the copy kernel of known size. Returns
+    (bytes, detail) or (None, reason)."""
+    import subprocess
+    rp = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3" if os.path.exists("/opt/rocm/bin/rocprofv3") else None)
+    if rp is None:
+        return None, "rocprofv3 not found"
+    tmp = tempfile.mkdtemp(prefix="pmc_", dir=work)
+    env = dict(os.environ, TMPDIR=tmp)
+    got = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = os.path.join(tmp, counter)
+        cmd = ["timeout", "-s", "KILL", "90", rp, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc",
+               "--", sys.executable, os.path.abspath(__file__), "--pmc-probe", path]
+        r = subprocess.run(cmd, cwd=tmp, env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        if r.returncode != 0:
+            return None, f"rocprofv3 --pmc {counter} exited {r.returncode}: {r.stdout[-300:]}"
+        means = _counter_means(d, counter)
+        gemv = [v for k, v in means.items() if k.startswith("sml_gemv_q4")]
+        copy = [v for k, v in means.items() if k.startswith("sml_copy_stream")]
+        if len(gemv) != 1 or len(copy) != 1:
+            return None, f"{counter}: kernels seen {sorted(means)}"
+        got[counter] = (gemv[0], copy[0])
+    kib = COPY_BYTES / 1024.0
+    f_fetch = kib / got["FETCH_SIZE"][1]
+    f_write = kib / got["WRITE_SIZE"][1]
+    t = got["FETCH_SIZE"][0] * 1024 * f_fetch + got["WRITE_SIZE"][0] * 1024 * f_write
+    return t, {"fetch_kib": round(got["FETCH_SIZE"][0], 1), "write_kib": round(got["WRITE_SIZE"][0], 1),
+               "copy_fetch_kib": round(got["FETCH_SIZE"][1], 1), "copy_write_kib": round(got["WRITE_SIZE"][1], 1),
+               "copy_bytes": COPY_BYTES, "fetch_scale": round(f_fetch, 4), "write_scale": round(f_write, 4)}
+
+
+def cpu_baseline(path, threads, budget_s=12.0, max_tokens=1200):
     """The reference's own CPU decode (sml_forward on its pool threads,
     compiled from its sources into oracle/_ref) on the same model file, from
     position 0 for as many tokens as fit the time budget."""
@@ -81,7 +156,7 @@ def cpu_baseline(path, threads, budget_s=12.0, max_tokens=160):
         return {"value": None, "error": f"oracle bindings unavailable: {e}"}
     if not ob.have_ref():
         return {"value": None, "error": "oracle/_ref/libsmlref.so not built"}
-    m = ob.RefModel(path, 256, threads=threads)
+    m = ob.RefModel(path, max_tokens + 8, threads=threads)
     tok, n = 1, 0
     m.forward(tok, 0)            # warm-up token (position 0)
     t0 = time.perf_counter()
@@ -98,13 +173,18 @@ def cpu_baseline(path, threads, budget_s=12.0, max_tokens=160):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=120)
+    ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemv-only", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
+    ap.add_argument("--pmc-probe", metavar="SSF", help=argparse.SUPPRESS)
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: fill the 4096 context)")
     a = ap.parse_args()
+    if a.pmc_probe:
+        pmc_probe(a.pmc_probe)
+        return
     if a.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {a.gpus} is not supported (this build has no "
               f"multi-GPU path)", file=sys.stderr)
@@ -132,6 +212,12 @@ def run(a, work):
     roof = {"bound": "hbm", "kernel": "sml_gemv_q4 (4096 rows x 14336 cols, Q4)",
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None, "avg_us": round(g_us, 3), "bytes_per_launch": g_bytes}
+    if not a.no_traffic:
+        t1 = time.perf_counter()
+        tb, detail = traffic(os.path.join(work, "gemv_4096x14336.ssf"), work)
+        roof["traffic"] = None if tb is None else int(round(tb))
+        roof["traffic_detail"] = detail
+        log(f"pmc traffic: {tb} bytes/launch vs {g_bytes} algorithmic; {detail} ({time.perf_counter() - t1:.1f}s)")
     gemv = {"4096x14336": {"us": round(g_us, 3), "GB/s": round(gbs, 1)},
             "14336x4096": {"us": round(g2_us, 3), "GB/s": round(g2_bytes / g2_us / 1e3, 1)},
             "8960x1536": {"us": round(g1_us, 3), "GB/s": round(g1_bytes / g1_us / 1e3, 1)}}

@@ -72,6 +72,10 @@ int sml_hip_time_matvec(const sml_hip_mat * const * mats, int ncopy, const int8_
 // No counterpart in the reference: it measures what one kernel can read from
 // HBM on this machine, the denominator next to the GEMV's achieved bandwidth.
 int sml_hip_time_read(const void * const * bufs, int nbuf, size_t bytes, int grid, int iters, float * ms_total);
+// Calibration: copy `bytes` (a multiple of 16) with one plain 128-bit
+// streaming kernel and wait for it. No counterpart in the reference: its HBM
+// read and write counters give the scale for the GEMV's counter readings.
+int sml_hip_copy(void * dst, const void * src, size_t bytes);
 
 // ------------------------------------------------------------ unpack / embed
 // Integer code of every weight of rows [row0, row0+nrows), one byte each,

@@ -133,3 +133,11 @@ typedef struct {
     uint32_t * sink;              // one word per wave
     int pattern;                  // 0: coalesced grid-stride; 1: each lane 64 contiguous bytes per step
 } sml_kread;
+
+// Plain device copy of `bytes` (multiple of 16): the known-size reference
+// against which HBM byte counters are scaled.
+typedef struct {
+    const uint8_t * src;
+    uint8_t * dst;
+    uint64_t bytes;
+} sml_kcopy;

@@ -790,3 +790,12 @@ extern "C" __global__ __launch_bounds__(256) void sml_read_stream(const sml_krea
     for (int o = 32; o; o >>= 1) v ^= __shfl_xor(v, o);
     if ((threadIdx.x & 63) == 0) a.sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = v;
 }
+
+// Grid-stride 128-bit copy: reads and writes `bytes` once each.
+extern "C" __global__ __launch_bounds__(256) void sml_copy_stream(const sml_kcopy a) {
+    const v4u * s = (const v4u *) a.src;
+    v4u * d = (v4u *) a.dst;
+    const uint64_t nw = a.bytes / 16;
+    for (uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x; i < nw; i += (uint64_t) gridDim.x * 256)
+        d[i] = __builtin_nontemporal_load(s + i);
+}

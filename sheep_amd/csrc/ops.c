@@ -387,6 +387,20 @@ int sml_hip_argmax(const float * logits, int n, int32_t * tok) {
     return 0;
 }
 
+int sml_hip_copy(void * dst, const void * src, size_t bytes) {
+    OP_BEGIN(-1);
+    if (!dst || !src || bytes % 16) hx_failf("copy arguments");
+    sml_kcopy a;
+    a.src = src; a.dst = dst; a.bytes = bytes;
+    uint64_t words = bytes / 16, grid = (words + 255) / 256;
+    if (grid > 8192) grid = 8192;
+    if (grid < 1) grid = 1;
+    hx_launch("sml_copy_stream", (unsigned) grid, 1, 256, 0, 0, &a);
+    HX(hipStreamSynchronize(0));
+    HX_LEAVE();
+    return 0;
+}
+
 int sml_hip_time_read(const void * const * bufs, int nbuf, size_t bytes, int grid, int iters, float * ms_total) {
     OP_BEGIN(-1);
     const int pattern = getenv("SML_READ_PATTERN") ? atoi(getenv("SML_READ_PATTERN")) : 0;

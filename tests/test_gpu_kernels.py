@@ -230,3 +230,15 @@ def test_argmax_first_max():
         t = sa.DevBuf(4)
         assert sa.lib().sml_hip_argmax(d.ptr, n, t.ptr) == 0
         assert int(t.read(np.int32)[0]) == ob.oracle().orc_argmax(lg.ctypes.data, n)
+
+
+def test_copy_calibration_kernel():
+    """The counter-calibration copy moves exactly the bytes asked for."""
+    rng = np.random.default_rng(5)
+    for n in (16, 4096 + 48, 3 << 20):
+        src = rng.integers(0, 256, n + 64, dtype=np.uint8)
+        s, d = sa.DevBuf.of(src), sa.DevBuf.of(np.zeros(n + 64, np.uint8))
+        assert sa.lib().sml_hip_copy(d.ptr, s.ptr, n) == 0
+        out = d.read(np.uint8)
+        assert np.array_equal(out[:n], src[:n]) and not out[n:].any()
+    assert sa.lib().sml_hip_copy(d.ptr, s.ptr, 17) == -1
