@@ -213,6 +213,22 @@ def test_f16_roundtrip_matches_numpy():
         assert o.orc_f16_to_f32(h) == np.float32(np.float16(x)) or np.isnan(x)
 
 
+def test_argmax_first_max_rule():
+    """First maximum wins on ties (what np.argmax also returns); a NaN is never
+    larger, so NaN at index 0 keeps 0 and NaN elsewhere is skipped."""
+    rng = np.random.default_rng(6)
+    o = ob.oracle()
+    for n in (1, 2, 7, 1000, 151936):
+        lg = rng.standard_normal(n).astype(np.float32)
+        if n > 3:
+            lg[n // 3] = lg[n - 1] = lg.max() + 1.0
+        assert o.orc_argmax(lg.ctypes.data, n) == int(np.argmax(lg))
+    lg = np.array([np.nan, 1.0, 3.0, 3.0], np.float32)
+    assert o.orc_argmax(lg.ctypes.data, 4) == 0
+    lg = np.array([1.0, np.nan, 3.0, 2.0], np.float32)
+    assert o.orc_argmax(lg.ctypes.data, 4) == 2
+
+
 def test_moe_route_golden_and_brute_force():
     g = np.load(os.path.join(GOLD, "decoder.npz"))
     lgs = g["route_lg"]
