@@ -61,6 +61,24 @@ int sml_hip_matvec(const sml_hip_mat * m, const int8_t * q, const float * scale,
 // h = silu(gate.x) * (up.x), the fused gate/up of sml_g_ffns (sml/sml-gpu-fast.cu:319-354)
 int sml_hip_matvec_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q,
                           const float * scale, const int32_t * sums, float * h);
+// y = W.a where a is the per-32 quantization of RMSNorm(x) (w != NULL; w NULL:
+// x itself) gathered through perm (NULL = identity), computed inside the GEMV's
+// prologue by every workgroup instead of by a separate launch; cols <= 4096.
+// The activation equals sml_hip_normq's bit for bit, so y equals
+// sml_hip_normq + sml_hip_matvec. replaces sml_g_normq2 + sml_g_qdmv2
+// (sml/sml-gpu-fast.cu:64-111,267-288), on the CPU rms_norm + sml_gather +
+// sml_quantize_act + the matvec (sml/sml-run.c:147-152,612-680)
+int sml_hip_matvec_normq(const sml_hip_mat * m, const float * x, const float * w, float eps, const int32_t * perm,
+                         float * y);
+// sml_hip_matvec_swiglu with its two fusions: x != NULL computes the activation
+// in the prologue as sml_hip_matvec_normq does (cols <= 8192 when hq is given,
+// else 4096; q/scale/sums unused), otherwise q/scale/sums are read; hq != NULL
+// also writes the per-32 quantization of h in order (rows a multiple of 32)
+// into hq/hscale/hsums, equal to sml_hip_normq of h without norm.
+// replaces sml_g_ffns + sml_g_quantw2 (sml/sml-gpu-fast.cu:319-354,522-543)
+int sml_hip_matvec_swiglu_fused(const sml_hip_mat * gate, const sml_hip_mat * up, const float * x, const float * w,
+                                float eps, const int32_t * perm, const int8_t * q, const float * scale,
+                                const int32_t * sums, float * h, int8_t * hq, float * hscale, int32_t * hsums);
 // Time `iters` back-to-back launches of sml_hip_matvec, rotating over `ncopy`
 // matrices of one shape (so repeats are not served from cache), with HIP
 // events on the launch stream. ms_total receives the elapsed milliseconds.

@@ -10,7 +10,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libsmlhip.so")
+# SML_HIP_LIB points at another build of the same library (tuning experiments)
+LIB_PATH = os.environ.get("SML_HIP_LIB") or os.path.join(HERE, "libsmlhip.so")
 
 _lib = None
 
@@ -60,6 +61,9 @@ _SIGS = [
     ("sml_hip_normq", c_int, [c_void_p, c_void_p, c_void_p, c_float, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int]),
     ("sml_hip_matvec", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("sml_hip_matvec_swiglu", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("sml_hip_matvec_normq", c_int, [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p]),
+    ("sml_hip_matvec_swiglu_fused", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p,
+                                            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("sml_hip_time_matvec", c_int, [P(c_void_p), c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, P(c_float)]),
     ("sml_hip_unpack", c_int, [c_void_p, c_int, c_int, c_void_p]),
     ("sml_hip_time_read", c_int, [P(c_void_p), c_int, c_size_t, c_int, c_int, P(c_float)]),
@@ -202,6 +206,21 @@ def matvec(m, act, y):
 
 def matvec_swiglu(gate, up, act, h):
     _chk(lib().sml_hip_matvec_swiglu(gate.h, up.h, act.q.ptr, act.scale.ptr, act.sums.ptr, h.ptr), "swiglu")
+
+
+def matvec_normq(m, x, y, w=None, perm=None, eps=1e-6):
+    """y = W . quantize(gather(RMSNorm(x))), the activation computed in the GEMV's prologue."""
+    _chk(lib().sml_hip_matvec_normq(m.h, x.ptr, w.ptr if w else None, eps, perm.ptr if perm else None, y.ptr),
+         "matvec_normq")
+
+
+def matvec_swiglu_fused(gate, up, h, x=None, w=None, perm=None, eps=1e-6, act=None, hact=None):
+    """SwiGLU GEMV with the prologue fusion (x given) and/or h quantized into hact."""
+    _chk(lib().sml_hip_matvec_swiglu_fused(
+        gate.h, up.h, x.ptr if x else None, w.ptr if w else None, eps, perm.ptr if perm else None,
+        act.q.ptr if act else None, act.scale.ptr if act else None, act.sums.ptr if act else None, h.ptr,
+        hact.q.ptr if hact else None, hact.scale.ptr if hact else None, hact.sums.ptr if hact else None),
+        "swiglu_fused")
 
 
 def unpack(m, row0, nrows):

@@ -24,7 +24,9 @@
 #define MAXACT 3
 
 typedef struct {
-    sml_hip_mat * w[3];        // q, k, v
+    sml_hip_mat * qkv;         // q, k and v rows stacked (one GEMV), or NULL: w[]
+    float * bias_qkv;          // their biases stacked, or NULL
+    sml_hip_mat * w[3];        // q, k, v when they cannot be stacked
     sml_hip_mat * o, * gate, * up, * down;
     float * bias[3];           // device q/k/v biases, or NULL
     float * an, * fn;          // device norm weights
@@ -47,6 +49,10 @@ static struct {
     int8_t * aq[MAXACT];
     float * as[MAXACT];
     int32_t * asum[MAXACT];
+    int8_t * hq;               // the SwiGLU kernel's quantized h, input of down
+    float * hs;
+    int32_t * hsum;
+    int fuse;                  // fused activation prologues / h quantization (SML_FUSE, default on)
     uint16_t * kc, * vc;
     int32_t * hist, * pos, * tok;
     float * lg_host;
@@ -147,31 +153,26 @@ static void prep(float * x, const float * w, const float * resid, int n, const i
 }
 
 static void gemv1(sml_hip_mat * m, int slot, int epi, float * y, const float * bias, const float * resid) {
-    const sml_hip_mat * ms[1] = { m };
-    float * ys[1] = { y };
-    const float * bs[1] = { bias };
-    op_gemv(G.st, ms, 1, epi, G.aq[slot], G.as[slot], G.asum[slot], ys, bs, resid);
+    op_gemv(G.st, m, NULL, epi, G.aq[slot], G.as[slot], G.asum[slot], y, bias, NULL, resid, NULL);
 }
 
 static void launch_layer(int L) {
     eng_layer * y = &G.L[L];
     const size_t kvd = (size_t) G.KV * G.hd;
     int slot[3];
-    prep(G.x, y->an, NULL, G.E, y->perm_qkv, 3, slot);
-    float * outs[3] = { G.q, G.k, G.v };
-    // one launch per (activation slot, width) group of q/k/v
-    int done[3] = { 0, 0, 0 };
-    for (int i = 0; i < 3; i++) {
-        if (done[i]) continue;
-        const sml_hip_mat * ms[3];
-        float * ys[3];
-        const float * bs[3];
-        int nm = 0;
-        for (int j = i; j < 3; j++)
-            if (!done[j] && slot[j] == slot[i] && y->w[j]->nbits == y->w[i]->nbits) {
-                ms[nm] = y->w[j]; ys[nm] = outs[j]; bs[nm] = y->bias[j]; nm++; done[j] = 1;
-            }
-        op_gemv(G.st, ms, nm, SML_EPI_STORE, G.aq[slot[i]], G.as[slot[i]], G.asum[slot[i]], ys, bs, NULL);
+    // q/k/v: the stacked GEMV computes RMSNorm + quantize of x in its prologue
+    if (y->qkv && G.fuse && G.E <= gemv_fuse_max_cols(0)) {
+        gemv_fuse fu;
+        memset(&fu, 0, sizeof fu);
+        fu.x = G.x; fu.norm_w = y->an; fu.eps = G.eps; fu.perm = pdev(y->perm_qkv[0]);
+        op_gemv(G.st, y->qkv, NULL, SML_EPI_STORE, NULL, NULL, NULL, G.q, y->bias_qkv, NULL, NULL, &fu);
+    } else {
+        prep(G.x, y->an, NULL, G.E, y->perm_qkv, 3, slot);
+        if (y->qkv) gemv1(y->qkv, slot[0], SML_EPI_STORE, G.q, y->bias_qkv, NULL);
+        else {
+            float * outs[3] = { G.q, G.k, G.v };
+            for (int i = 0; i < 3; i++) gemv1(y->w[i], slot[i], SML_EPI_STORE, outs[i], y->bias[i], NULL);
+        }
     }
     // with an identity o-proj permutation the attention kernel quantizes its
     // own output for the o GEMV; otherwise a gather + quantize follows it
@@ -182,12 +183,24 @@ static void launch_layer(int L) {
     if (fuse_q) slot[0] = 0;
     else prep(G.att, NULL, NULL, G.H * G.hd, &y->perm_o, 1, slot);
     gemv1(y->o, slot[0], SML_EPI_RESIDUAL, G.x, NULL, G.x);
-    prep(G.x, y->fn, NULL, G.E, y->perm_gu, 2, slot);
-    if (slot[0] == slot[1] && y->gate->nbits == y->up->nbits) {
-        const sml_hip_mat * ms[2] = { y->gate, y->up };
-        float * ys[2] = { G.hb, G.hb };
-        op_gemv(G.st, ms, 2, SML_EPI_SWIGLU, G.aq[slot[0]], G.as[slot[0]], G.asum[slot[0]], ys, NULL, NULL);
+    // gate/up: one SwiGLU launch when they share a permutation and width; it
+    // also quantizes h for down when down reads h in order
+    const int h_fused = G.fuse && y->perm_down < 0 && G.F % 32 == 0;
+    if (y->perm_gu[0] == y->perm_gu[1] && y->gate->nbits == y->up->nbits) {
+        gemv_fuse fu;
+        memset(&fu, 0, sizeof fu);
+        const int x_fused = G.fuse && G.E <= gemv_fuse_max_cols(h_fused);
+        if (x_fused) { fu.x = G.x; fu.norm_w = y->fn; fu.eps = G.eps; fu.perm = pdev(y->perm_gu[0]); }
+        else prep(G.x, y->fn, NULL, G.E, y->perm_gu, 2, slot);
+        if (h_fused) { fu.hq = G.hq; fu.hscale = G.hs; fu.hsums = G.hsum; }
+        op_gemv(G.st, y->gate, y->up, SML_EPI_SWIGLU, x_fused ? NULL : G.aq[slot[0]], x_fused ? NULL : G.as[slot[0]],
+                x_fused ? NULL : G.asum[slot[0]], G.hb, NULL, NULL, NULL, (x_fused || h_fused) ? &fu : NULL);
+        if (h_fused) {
+            op_gemv(G.st, y->down, NULL, SML_EPI_RESIDUAL, G.hq, G.hs, G.hsum, G.x, NULL, NULL, G.x, NULL);
+            return;
+        }
     } else {
+        prep(G.x, y->fn, NULL, G.E, y->perm_gu, 2, slot);
         gemv1(y->gate, slot[0], SML_EPI_STORE, G.hb, NULL, NULL);
         gemv1(y->up, slot[1], SML_EPI_STORE, G.hb2, NULL, NULL);
         op_silu_mul(G.st, G.hb, G.hb2, G.F);
@@ -324,14 +337,36 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     const char * wn[3] = { "blk.%d.attn_q.weight", "blk.%d.attn_k.weight", "blk.%d.attn_v.weight" };
     const char * bn[3] = { "blk.%d.attn_q.bias", "blk.%d.attn_k.bias", "blk.%d.attn_v.bias" };
     const int wrows[3] = { G.H * G.hd, G.KV * G.hd, G.KV * G.hd };
+    const int qkv_rows = wrows[0] + wrows[1] + wrows[2];
     for (int L = 0; L < G.n_layer; L++) {
         eng_layer * y = &G.L[L];
+        const ssf_record * rq[3];
         for (int i = 0; i < 3; i++) {
-            const ssf_record * r = need(&f, wn[i], L);
-            if ((int) r->rows != wrows[i] || (int) r->cols != G.E) hx_failf("%.64s has an unexpected shape", r->name);
-            y->w[i] = upmat(&f, r);
-            y->perm_qkv[i] = perm_of(&f, r);
+            rq[i] = need(&f, wn[i], L);
+            if ((int) rq[i]->rows != wrows[i] || (int) rq[i]->cols != G.E) hx_failf("%.64s has an unexpected shape", rq[i]->name);
+            y->perm_qkv[i] = perm_of(&f, rq[i]);
             y->bias[i] = f32_tensor(&f, bn[i], L, wrows[i]);
+        }
+        // q, k and v read the same input: one stacked matrix and one GEMV
+        // when they share a permutation and width
+        if (y->perm_qkv[1] == y->perm_qkv[0] && y->perm_qkv[2] == y->perm_qkv[0]) {
+            if (G.nmats >= (int) (sizeof G.mats / sizeof G.mats[0])) hx_failf("too many matrices");
+            y->qkv = mat_stack(&f, rq, 3);
+            if (y->qkv) G.mats[G.nmats++] = y->qkv;
+        }
+        if (y->qkv) {
+            if (y->bias[0] || y->bias[1] || y->bias[2]) {
+                y->bias_qkv = dalloc((size_t) qkv_rows * 4);
+                float * at = y->bias_qkv;
+                for (int i = 0; i < 3; i++) {
+                    if (y->bias[i]) HX(hipMemcpy(at, y->bias[i], (size_t) wrows[i] * 4, hipMemcpyDeviceToDevice));
+                    else HX(hipMemset(at, 0, (size_t) wrows[i] * 4));
+                    at += wrows[i];
+                }
+            }
+            G.weight_bytes += y->qkv->bytes;
+        } else {
+            for (int i = 0; i < 3; i++) { y->w[i] = upmat(&f, rq[i]); G.weight_bytes += y->w[i]->bytes; }
         }
         const ssf_record * r;
         r = need(&f, "blk.%d.attn_output.weight", L); y->o = upmat(&f, r); y->perm_o = perm_of(&f, r);
@@ -344,7 +379,6 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
         y->an = f32_tensor(&f, "blk.%d.attn_norm.weight", L, G.E);
         y->fn = f32_tensor(&f, "blk.%d.ffn_norm.weight", L, G.E);
         if (!y->an || !y->fn) hx_failf("layer %d lacks a norm", L);
-        for (int i = 0; i < 3; i++) G.weight_bytes += y->w[i]->bytes;
         G.weight_bytes += y->o->bytes + y->gate->bytes + y->up->bytes + y->down->bytes;
     }
     // RoPE table on the host, exactly as the reference builds it (sml/sml-run.c:1383-1393)
@@ -367,9 +401,10 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     int wide = G.F > G.E ? G.F : G.E;
     if (G.H * G.hd > wide) wide = G.H * G.hd;
     G.x = dalloc((size_t) G.E * 4);
-    G.q = dalloc((size_t) G.H * G.hd * 4);
-    G.k = dalloc((size_t) G.KV * G.hd * 4);
-    G.v = dalloc((size_t) G.KV * G.hd * 4);
+    // q, k and v contiguous: the stacked GEMV writes all three
+    G.q = dalloc((size_t) (G.H + 2 * G.KV) * G.hd * 4);
+    G.k = G.q + (size_t) G.H * G.hd;
+    G.v = G.k + (size_t) G.KV * G.hd;
     G.att = dalloc((size_t) G.H * G.hd * 4);
     G.hb = dalloc((size_t) G.F * 4);
     G.hb2 = dalloc((size_t) G.F * 4);
@@ -380,6 +415,10 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
         G.as[i] = dalloc((size_t) wide / 32 * 4);
         G.asum[i] = dalloc((size_t) wide / 32 * 4);
     }
+    G.hq = dalloc((size_t) G.F);
+    G.hs = dalloc((size_t) G.F / 32 * 4);
+    G.hsum = dalloc((size_t) G.F / 32 * 4);
+    G.fuse = env_int("SML_FUSE", 1) != 0;
     const size_t kvn = (size_t) G.n_layer * n_ctx * G.KV * G.hd;
     G.kc = dalloc(kvn * 2);
     G.vc = dalloc(kvn * 2);

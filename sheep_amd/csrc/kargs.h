@@ -4,8 +4,6 @@
 #pragma once
 #include <stdint.h>
 
-#define SML_MAX_MATS 3
-
 // One quantized FLAT matrix resident in HBM: the file's code planes in
 // storage order, and its four field arrays interleaved pairwise at upload --
 // per group (sq, mq) as two bytes, per superblock (sd, md) as two halves --
@@ -19,21 +17,36 @@ typedef struct {
     const float    * bias;        // added to the output row, or NULL
     float          * y;
     int rows;
-    int row_begin;                // first row of this matrix in the launch's row space
+    int pad_;
 } sml_kmat;
 
 enum { SML_EPI_STORE = 0, SML_EPI_RESIDUAL = 1, SML_EPI_SWIGLU = 2 };
 
+// One GEMV launch over one matrix m[0] (SwiGLU: gate m[0] and up m[1] of one
+// shape, h written to m[0].y).
 typedef struct {
-    sml_kmat m[SML_MAX_MATS];
-    int nmat;
-    int cols;                     // input width shared by every matrix
-    int total_rows;               // row space of the launch (SWIGLU: rows of one matrix)
+    sml_kmat m[2];
+    int cols;                     // input width
+    int total_rows;               // output rows
     int epi;                      // SML_EPI_*
     const int8_t  * q;            // activation, canonical layout (reference sml_act)
     const float   * scale;
     const int32_t * sums;
     const float   * resid;        // SML_EPI_RESIDUAL: y = resid + W.x (resid may alias y)
+    // Fused activation prologue (the _n kernels): every workgroup computes the
+    // activation itself from the fp32 vector x -- RMSNorm with norm_w (NULL:
+    // none), gather through perm (NULL: identity), per-32 int8 quantization --
+    // instead of reading q/scale/sums.
+    const float   * x;
+    const float   * norm_w;
+    const int32_t * perm;
+    float           eps;
+    // SwiGLU h quantization (the _h kernels): each workgroup owns 32
+    // consecutive outputs h and also writes their per-32 quantization
+    // (identity order) for the down projection.
+    int8_t        * hq;
+    float         * hscale;
+    int32_t       * hsums;
 } sml_kgemv;
 
 // Gather + optional residual add + optional RMSNorm + per-group int8 quantize.

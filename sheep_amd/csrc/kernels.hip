@@ -177,36 +177,140 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return v;
 }
 
-template <int NB, int RB, int NI, int WG, bool NT>
+// Max / sum over aligned groups of 8 lanes (quad butterflies, then the half-row mirror)
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v)); v = fmaxf(v, dpp_f<0x4E>(v)); return fmaxf(v, dpp_f<0x141>(v));
+}
+__device__ __forceinline__ int isum8(int v) { v += dpp_i<0xB1>(v); v += dpp_i<0x4E>(v); return v + dpp_i<0x141>(v); }
+
+// One activation code: lrintf(v * is) clamped to +-127, where an out-of-range
+// or NaN product converts to INT_MIN as the reference's x86 build does
+// (sml/sml-kernel.c:86-106), so it clamps to -127.
+__device__ __forceinline__ int quant1(float v, float is) {
+    const float r = __builtin_rintf(v * is);
+    int t = (r >= -2147483648.0f && r < 2147483648.0f) ? (int) r : (int) 0x80000000u;
+    return t > 127 ? 127 : t < -127 ? -127 : t;
+}
+
+// Fused activation prologue: RMSNorm (double sum of squares, out = x*sc*w,
+// sml/sml-run.c:147-152), gather through perm, and the per-32 quantization
+// (sml/sml-kernel.c:86-106) of the whole input vector, into the workgroup's
+// LDS copy (lq: int8 codes, lsc: per group (s, s*sum)). Thread t holds the
+// float4 words t + k*WG (loaded before the weights); 8 consecutive threads
+// hold one group of 32. The arithmetic is the normq kernels', so the codes,
+// scales and sums are theirs bit for bit.
+template <int WG, int FK>
+__device__ __forceinline__ void fused_act(const sml_kgemv & a, const float4 (&fx)[FK], const float4 (&fw)[FK],
+                                          const int4 (&fp)[FK], int8_t * lq, float2 * lsc, float * nrm, double * red) {
+    const int n = a.cols, tid = threadIdx.x, n4 = n / 4;
+    float sc = 1.0f;
+    if (a.norm_w) {
+        double ss = 0.0;
+        #pragma unroll
+        for (int k = 0; k < FK; k++)
+            if (tid + k * WG < n4) {
+                const float4 v = fx[k];
+                ss += (double) v.x * v.x + (double) v.y * v.y + (double) v.z * v.z + (double) v.w * v.w;
+            }
+        #pragma unroll
+        for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        double tot = 0.0;
+        #pragma unroll
+        for (int w = 0; w < WG / 64; w++) tot += red[w];
+        sc = 1.0f / sqrtf((float) (tot / (double) n) + a.eps);
+    }
+    float v[FK][4];
+    #pragma unroll
+    for (int k = 0; k < FK; k++) {
+        v[k][0] = fx[k].x; v[k][1] = fx[k].y; v[k][2] = fx[k].z; v[k][3] = fx[k].w;
+        if (a.norm_w) {
+            v[k][0] = v[k][0] * sc * fw[k].x; v[k][1] = v[k][1] * sc * fw[k].y;
+            v[k][2] = v[k][2] * sc * fw[k].z; v[k][3] = v[k][3] * sc * fw[k].w;
+        }
+    }
+    if (a.perm) {
+        #pragma unroll
+        for (int k = 0; k < FK; k++) {
+            const int f = tid + k * WG;
+            if (f < n4) *(float4 *) (nrm + 4 * f) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+        }
+        __syncthreads();
+        #pragma unroll
+        for (int k = 0; k < FK; k++)
+            if (tid + k * WG < n4) {
+                v[k][0] = nrm[fp[k].x]; v[k][1] = nrm[fp[k].y]; v[k][2] = nrm[fp[k].z]; v[k][3] = nrm[fp[k].w];
+            }
+    }
+    #pragma unroll
+    for (int k = 0; k < FK; k++) {
+        const int f = tid + k * WG;
+        if (f >= n4) continue;                  // whole 8-lane groups drop out together (n % 32 == 0)
+        const float am = max8(fmaxf(fmaxf(fabsf(v[k][0]), fabsf(v[k][1])), fmaxf(fabsf(v[k][2]), fabsf(v[k][3]))));
+        const float s = am / 127.0f;
+        const float is = s > 0.0f ? 1.0f / s : 0.0f;
+        const int t0 = quant1(v[k][0], is), t1 = quant1(v[k][1], is), t2 = quant1(v[k][2], is), t3 = quant1(v[k][3], is);
+        const int sum = isum8(t0 + t1 + t2 + t3);
+        ((int *) lq)[f] = (t0 & 0xFF) | (t1 & 0xFF) << 8 | (t2 & 0xFF) << 16 | (int) ((unsigned) t3 << 24);
+        if ((tid & 7) == 0) lsc[f >> 3] = make_float2(s, s * (float) sum);
+    }
+}
+
+// The GEMV body. One wave owns RB output rows (SW: RB/2 gate/up row pairs);
+// lane c of the wave streams chunk c, c+64, ... of each row. The argument
+// block is only ever read at fixed offsets: a run-time index into it makes
+// the compiler copy it to scratch or read it with vector loads that wait
+// for every load already in flight (the activation prefetch included).
+//
+// Chunks past a row's end read the row's last chunk (a broadcast of bytes
+// already fetched) and contribute nothing because their activation scale is
+// taken as zero; rows past the end read row 0 and are never stored.
+template <int NB, int RB, int NI, int WG, bool NT, int AM, bool SW, bool HQ>
 __device__ void gemv_body(const sml_kgemv & a) {
-    constexpr int GEMV_THREADS = WG;
     extern __shared__ __align__(16) uint8_t lds[];
     const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8;
     int8_t * lq = (int8_t *) lds;
     float2 * lsc = (float2 *) (lds + n);
     const int tid = threadIdx.x, lane = tid & (WAVE - 1);
-    const bool swiglu = a.epi == SML_EPI_SWIGLU;
-    const int rows_per_wave = swiglu ? RB / 2 : RB;
-    const int row0 = (blockIdx.x * (GEMV_THREADS / WAVE) + (tid >> 6)) * rows_per_wave;
+    constexpr int RPW = SW ? RB / 2 : RB;          // output rows per wave
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row0 = (blockIdx.x * (WG / WAVE) + wave) * RPW;
 
     // 1. activation loads (L2-resident, issued first)
-    constexpr int SQ = 4, SG = 2;                  // staged words per thread per round
+    constexpr int SQ = AM == 0 ? 4 : 1, SG = AM == 0 ? 2 : 1;   // staged words per thread per round
     v4i sq_[SQ];
     int sg_i[SG];
     float sg_s[SG];
     int32_t sg_u[SG];
     const int nq16 = n / 16;
-    #pragma unroll
-    for (int k = 0; k < SQ; k++) { const int i = tid + k * GEMV_THREADS; if (i < nq16) sq_[k] = ((const v4i *) a.q)[i]; }
-    #pragma unroll
-    for (int k = 0; k < SG; k++) {
-        const int i = tid + k * GEMV_THREADS;
-        sg_i[k] = i;
-        if (i < ng) { sg_s[k] = a.scale[i]; sg_u[k] = a.sums[i]; }
+    // fused prologue: float4 words of x, norm_w and perm per thread
+    constexpr int FK = AM == 0 ? 1 : (WG >= 1024 ? 2 : 4);
+    float4 fx[FK], fw[FK];
+    int4 fp[FK];
+    if constexpr (AM == 0) {
+        #pragma unroll
+        for (int k = 0; k < SQ; k++) { const int i = tid + k * WG; if (i < nq16) sq_[k] = ((const v4i *) a.q)[i]; }
+        #pragma unroll
+        for (int k = 0; k < SG; k++) {
+            const int i = tid + k * WG;
+            sg_i[k] = i;
+            if (i < ng) { sg_s[k] = a.scale[i]; sg_u[k] = a.sums[i]; }
+        }
+    } else {
+        #pragma unroll
+        for (int k = 0; k < FK; k++) {
+            const int f = tid + k * WG;
+            fx[k] = make_float4(0.f, 0.f, 0.f, 0.f); fw[k] = fx[k]; fp[k] = make_int4(0, 0, 0, 0);
+            if (f < n / 4) {
+                fx[k] = ((const float4 *) a.x)[f];
+                if (a.norm_w) fw[k] = ((const float4 *) a.norm_w)[f];
+                if (a.perm) fp[k] = ((const int4 *) a.perm)[f];
+            }
+        }
     }
 
-    // 2. this wave's rows: plane row bases and field rows. Rows past the end
-    // read row 0 and contribute nothing (their fields are zeroed below).
+    // 2. this wave's rows: plane row bases and field rows
     using P = Planes<NB>;
     const uint8_t * pl[RB][3];
     const uint16_t * fq[RB];          // (sq, mq) pairs as one 16-bit word per group
@@ -215,16 +319,11 @@ __device__ void gemv_body(const sml_kgemv & a) {
     bool valid[RB];
     #pragma unroll
     for (int s = 0; s < RB; s++) {
-        const int grow = swiglu ? row0 + (s >> 1) : row0 + s;
+        const int grow = SW ? row0 + (s >> 1) : row0 + s;
         orow[s] = grow;
         valid[s] = grow < a.total_rows;
-        int mi = swiglu ? (s & 1) : 0;
-        if (!swiglu) {
-            #pragma unroll
-            for (int i = 1; i < SML_MAX_MATS; i++) if (i < a.nmat && grow >= a.m[i].row_begin) mi = i;
-        }
-        const sml_kmat & m = a.m[mi];
-        const size_t r = (size_t) (valid[s] ? (swiglu ? grow : grow - m.row_begin) : 0);
+        const sml_kmat & m = (SW && (s & 1)) ? a.m[1] : a.m[0];
+        const size_t r = (size_t) (valid[s] ? grow : 0);
         pl[s][0] = m.plane[0]; pl[s][1] = m.plane[1]; pl[s][2] = m.plane[2];
         if constexpr (P::N4) pl[s][P::P4] = m.plane[P::P4] + r * P::b4(n);
         if constexpr (NB == 8) pl[s][1] = m.plane[1] + r * P::b4(n);
@@ -239,9 +338,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
     for (int s = 0; s < RB; s++) acc[s] = 0.0f;
     bool staged = false;
     for (int c0 = 0; c0 < ng; c0 += WAVE * NI) {
-        // 3. every weight load of this lane for NI chunks of RB rows, with no
-        // branches: a chunk past the row's end reads the row's last chunk and
-        // has its fields zeroed (sq 0, md 0), so it adds exactly nothing
+        // 3. every weight load of this lane for NI chunks of RB rows, with no branches
         ChunkW<NB> w[NI][RB];
         uint32_t fqv[NI][RB], fdv[NI][RB];
         #pragma unroll
@@ -255,23 +352,22 @@ __device__ void gemv_body(const sml_kgemv & a) {
                 fdv[i][s] = fd[s][cl >> 3];
             }
         }
-        #pragma unroll
-        for (int i = 0; i < NI; i++) {
-            const bool live = c0 + i * WAVE + lane < ng;
-            #pragma unroll
-            for (int s = 0; s < RB; s++) {
-                if (!(live && valid[s])) { fqv[i][s] = 0x7F00u; fdv[i][s] = 0u; }
-            }
-        }
         if (!staged) {
-            // 4. activation into LDS (waits only for the activation loads)
-            #pragma unroll
-            for (int k = 0; k < SQ; k++) { const int idx = tid + k * GEMV_THREADS; if (idx < nq16) ((v4i *) lq)[idx] = sq_[k]; }
-            #pragma unroll
-            for (int k = 0; k < SG; k++) if (sg_i[k] < ng) lsc[sg_i[k]] = make_float2(sg_s[k], sg_s[k] * (float) sg_u[k]);
-            // widths beyond one round of staging
-            for (int idx = tid + SQ * GEMV_THREADS; idx < nq16; idx += GEMV_THREADS) ((v4i *) lq)[idx] = ((const v4i *) a.q)[idx];
-            for (int g = tid + SG * GEMV_THREADS; g < ng; g += GEMV_THREADS) lsc[g] = make_float2(a.scale[g], a.scale[g] * (float) a.sums[g]);
+            if constexpr (AM == 1) {
+                // 4'. the activation computed from x into LDS (the gather
+                // buffer starts 16-byte aligned after the codes and fields)
+                __shared__ double red[WG / 64];
+                fused_act<WG, FK>(a, fx, fw, fp, lq, lsc, (float *) (lds + ((n + 8 * ng + 15) & ~15)), red);
+            } else {
+                // 4. activation into LDS (waits only for the activation loads)
+                #pragma unroll
+                for (int k = 0; k < SQ; k++) { const int idx = tid + k * WG; if (idx < nq16) ((v4i *) lq)[idx] = sq_[k]; }
+                #pragma unroll
+                for (int k = 0; k < SG; k++) if (sg_i[k] < ng) lsc[sg_i[k]] = make_float2(sg_s[k], sg_s[k] * (float) sg_u[k]);
+                // widths beyond one round of staging
+                for (int idx = tid + SQ * WG; idx < nq16; idx += WG) ((v4i *) lq)[idx] = ((const v4i *) a.q)[idx];
+                for (int g = tid + SG * WG; g < ng; g += WG) lsc[g] = make_float2(a.scale[g], a.scale[g] * (float) a.sums[g]);
+            }
             __syncthreads();
             staged = true;
         }
@@ -279,11 +375,13 @@ __device__ void gemv_body(const sml_kgemv & a) {
         #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int c = c0 + i * WAVE + lane;
-            const int cc = c < ng ? c : ng - 1;           // keep LDS reads in range
+            const bool live = c < ng;                     // the pair (c&~1, c|1) is live or dead as a whole
+            const int cc = live ? c : ng - 1;             // keep LDS reads in range
             const int off = 32 * (cc & ~1) + 16 * (cc & 1);
             const v4i xa = *(const v4i *) (lq + off);
             const v4i xb = *(const v4i *) (lq + off + 32);
-            const float2 sc = lsc[cc];
+            float2 sc = lsc[cc];
+            if (!live) sc = make_float2(0.0f, 0.0f);
             const int odd = c & 1;
             #pragma unroll
             for (int s = 0; s < RB; s++) {
@@ -301,8 +399,42 @@ __device__ void gemv_body(const sml_kgemv & a) {
     }
     #pragma unroll
     for (int s = 0; s < RB; s++) acc[s] = wave_sum_dpp(acc[s]);
+    if constexpr (HQ) {
+        // 32 consecutive outputs per workgroup (RB/2 gate/up pairs per wave):
+        // h = silu(g)*u, then its per-32 quantization for the down projection
+        __shared__ float hb[32];
+        if (lane == WAVE - 1) {
+            #pragma unroll
+            for (int s = 0; s < RB; s += 2) {
+                const int row = orow[s];
+                float h = 0.0f;
+                if (valid[s]) {
+                    float g = acc[s], u = acc[s + 1];
+                    if (a.m[0].bias) g += a.m[0].bias[row];
+                    if (a.m[1].bias) u += a.m[1].bias[row];
+                    h = (g / (1.0f + expf(-g))) * u;             // sml/sml-run.c:451-454
+                    a.m[0].y[row] = h;
+                }
+                hb[wave * RPW + (s >> 1)] = h;
+            }
+        }
+        __syncthreads();
+        if (tid < 32) {
+            const float v = hb[tid];
+            const float s = max32(fabsf(v)) / 127.0f;
+            const float is = s > 0.0f ? 1.0f / s : 0.0f;
+            const int t = quant1(v, is);
+            const int sum = isum32(t);
+            const int row = blockIdx.x * 32 + tid;
+            if (row < a.total_rows) {
+                a.hq[row] = (int8_t) t;
+                if (tid == 0) { a.hscale[row >> 5] = s; a.hsums[row >> 5] = sum; }
+            }
+        }
+        return;
+    }
     if (lane != WAVE - 1) return;
-    if (swiglu) {
+    if constexpr (SW) {
         #pragma unroll
         for (int s = 0; s < RB; s += 2) {
             if (!valid[s]) continue;
@@ -312,39 +444,56 @@ __device__ void gemv_body(const sml_kgemv & a) {
             if (a.m[1].bias) u += a.m[1].bias[row];
             a.m[0].y[row] = (g / (1.0f + expf(-g))) * u;   // sml/sml-run.c:451-454
         }
-        return;
-    }
-    #pragma unroll
-    for (int s = 0; s < RB; s++) {
-        if (!valid[s]) continue;
-        int mi = 0;
+    } else {
         #pragma unroll
-        for (int i = 1; i < SML_MAX_MATS; i++) if (i < a.nmat && orow[s] >= a.m[i].row_begin) mi = i;
-        const sml_kmat & m = a.m[mi];
-        const int lr = orow[s] - m.row_begin;
-        float v = acc[s];
-        if (m.bias) v += m.bias[lr];
-        if (a.epi == SML_EPI_RESIDUAL) v = a.resid[lr] + v;
-        m.y[lr] = v;
+        for (int s = 0; s < RB; s++) {
+            if (!valid[s]) continue;
+            const int row = orow[s];
+            float v = acc[s];
+            if (a.m[0].bias) v += a.m[0].bias[row];
+            if (a.epi == SML_EPI_RESIDUAL) v = a.resid[row] + v;
+            a.m[0].y[row] = v;
+        }
     }
 }
 
-#define GEMV_KERNEL(NB, RB, NI)                                                                        \
-    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_r##RB##_i##NI(const sml_kgemv a) { \
-        gemv_body<NB, RB, NI, 256, true>(a);                                                           \
+// Kernel names: sml_gemv_q<bits>_r<rows per wave>_i<chunks per lane>, with
+// suffix _n for the fused activation prologue (input width up to 4096);
+// sml_gemv_q<bits>_s_r<RB>_i<NI> for SwiGLU (RB/2 gate/up pairs per wave, _sn
+// with the prologue); sml_gemv_q<bits>_h_i<NI> for SwiGLU that also
+// quantizes h (16 waves x 2 pairs = 32 outputs per workgroup; _hn with the
+// prologue, input width up to 8192).
+#define GEMV_KERNEL(NB, RB, NI)                                                                             \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_r##RB##_i##NI(const sml_kgemv a) {     \
+        gemv_body<NB, RB, NI, 256, true, 0, false, false>(a);                                               \
     }
-// workgroup-size and load-kind variants of Q4, for tuning
-#define GEMV_KERNEL_V(RB, NI, WG, NT)                                                                                    \
-    extern "C" __global__ __launch_bounds__(WG) void sml_gemv_q4_r##RB##_i##NI##_w##WG##_t##NT(const sml_kgemv a) {   \
-        gemv_body<4, RB, NI, WG, NT>(a);                                                                                 \
+#define GEMV_KERNEL_N(NB, RB, NI)                                                                           \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_r##RB##_i##NI##_n(const sml_kgemv a) { \
+        gemv_body<NB, RB, NI, 256, true, 1, false, false>(a);                                               \
     }
-#define GEMV_V(RB, NI) GEMV_KERNEL_V(RB, NI, 256, 0) GEMV_KERNEL_V(RB, NI, 512, 1) GEMV_KERNEL_V(RB, NI, 512, 0) \
-                       GEMV_KERNEL_V(RB, NI, 1024, 1) GEMV_KERNEL_V(RB, NI, 1024, 0)
-GEMV_V(1, 8) GEMV_V(1, 4) GEMV_V(2, 4) GEMV_V(2, 2) GEMV_V(4, 2) GEMV_V(4, 1) GEMV_V(2, 8)
+#define GEMV_KERNEL_S(NB, RB, NI)                                                                           \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_s_r##RB##_i##NI(const sml_kgemv a) {   \
+        gemv_body<NB, RB, NI, 256, true, 0, true, false>(a);                                                \
+    }                                                                                                       \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_sn_r##RB##_i##NI(const sml_kgemv a) {  \
+        gemv_body<NB, RB, NI, 256, true, 1, true, false>(a);                                                \
+    }
+#define GEMV_KERNEL_H(NB, NI)                                                                               \
+    extern "C" __global__ __launch_bounds__(1024) void sml_gemv_q##NB##_h_i##NI(const sml_kgemv a) {         \
+        gemv_body<NB, 4, NI, 1024, true, 0, true, true>(a);                                                 \
+    }                                                                                                       \
+    extern "C" __global__ __launch_bounds__(1024) void sml_gemv_q##NB##_hn_i##NI(const sml_kgemv a) {        \
+        gemv_body<NB, 4, NI, 1024, true, 1, true, true>(a);                                                 \
+    }
 #define GEMV_WIDTH(NB)                                                                     \
     GEMV_KERNEL(NB, 1, 2) GEMV_KERNEL(NB, 1, 4) GEMV_KERNEL(NB, 1, 8)                     \
     GEMV_KERNEL(NB, 2, 1) GEMV_KERNEL(NB, 2, 2) GEMV_KERNEL(NB, 2, 4) GEMV_KERNEL(NB, 2, 8) \
-    GEMV_KERNEL(NB, 4, 1) GEMV_KERNEL(NB, 4, 2) GEMV_KERNEL(NB, 4, 4)
+    GEMV_KERNEL(NB, 4, 1) GEMV_KERNEL(NB, 4, 2) GEMV_KERNEL(NB, 4, 4)                     \
+    GEMV_KERNEL_N(NB, 1, 1) GEMV_KERNEL_N(NB, 1, 2) GEMV_KERNEL_N(NB, 2, 1)               \
+    GEMV_KERNEL_N(NB, 2, 2) GEMV_KERNEL_N(NB, 4, 1) GEMV_KERNEL_N(NB, 4, 2)               \
+    GEMV_KERNEL_S(NB, 2, 1) GEMV_KERNEL_S(NB, 2, 2) GEMV_KERNEL_S(NB, 2, 4)               \
+    GEMV_KERNEL_S(NB, 4, 1) GEMV_KERNEL_S(NB, 4, 2) GEMV_KERNEL_S(NB, 4, 4)               \
+    GEMV_KERNEL_H(NB, 1) GEMV_KERNEL_H(NB, 2) GEMV_KERNEL_H(NB, 4)
 GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH(7) GEMV_WIDTH(8)
 
 // ---------------------------------------------------------------- norm + quantize

@@ -131,6 +131,76 @@ sml_hip_mat * mat_from_record(const ssf_file * f, const ssf_record * r) {
                       (int) r->rows, (int) r->cols, (int) r->nbits, six, neg);
 }
 
+// Total rows of records that can be stacked (same FLAT width, input width
+// and min presence), or 0.
+static size_t stack_rows(const ssf_record * const * recs, int n) {
+    size_t rows = 0;
+    for (int i = 0; i < n; i++) {
+        const ssf_record * r = recs[i];
+        if (r->kind != SSF_KIND_QUANT || r->layout != SSF_LAYOUT_FLAT || r->nbits != recs[0]->nbits ||
+            r->cols != recs[0]->cols || (r->mq_bytes != 0) != (recs[0]->mq_bytes != 0))
+            return 0;
+        rows += r->rows;
+    }
+    return rows;
+}
+
+static void free_stack(uint8_t ** pl, uint8_t * sq, uint8_t * mq, uint16_t * sd, uint16_t * md) {
+    for (int p = 0; p < 4; p++) free(pl[p]);
+    free(sq); free(mq); free(sd); free(md);
+}
+
+// Upload the stacked host copy and free it, also when the upload fails.
+static sml_hip_mat * upload_stack(uint8_t ** pl, uint8_t * sq, uint8_t * mq, uint16_t * sd, uint16_t * md,
+                                  int rows, int cols, int nb, int six, int neg) {
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) { hx.jb = outer; free_stack(pl, sq, mq, sd, md); longjmp(*outer, 1); }
+    hx.jb = &jb;
+    sml_hip_mat * m = mat_upload((const uint8_t * const *) pl, sd, sq, md, mq, rows, cols, nb, six, neg);
+    hx.jb = outer;
+    free_stack(pl, sq, mq, sd, md);
+    return m;
+}
+
+sml_hip_mat * mat_stack(const ssf_file * f, const ssf_record * const * recs, int n) {
+    const ssf_record * r0 = recs[0];
+    const int nb = (int) r0->nbits, cols = (int) r0->cols, has_min = r0->mq_bytes != 0;
+    const size_t rows = stack_rows(recs, n);
+    if (!rows) return NULL;
+    int pb[SSF_MAX_PLANES];
+    const int np = ssf_flat_planes(nb, pb);
+    const int six = (f->hdr->flags & SSF_FLAG_SCALE6) != 0, neg = (f->hdr->flags & SSF_FLAG_MINNEG) != 0;
+    const size_t ng = (size_t) cols / 32, ns = (size_t) SSF_NSUPER(cols), grow = six ? ng / 4 * 3 : ng;
+    size_t prb[SSF_MAX_PLANES];
+    uint8_t * pl[4] = { 0 };
+    uint8_t * sq = malloc(rows * grow), * mq = has_min ? malloc(rows * grow) : NULL;
+    uint16_t * sd = malloc(rows * ns * 2), * md = has_min ? malloc(rows * ns * 2) : NULL;
+    int ok = sq && sd && (!has_min || (mq && md));
+    for (int p = 0; p < np; p++) {
+        prb[p] = ssf_plane_row_bytes(pb[p], cols);
+        pl[p] = malloc(rows * prb[p]);
+        ok = ok && pl[p];
+    }
+    if (ok) {
+        size_t at = 0;
+        for (int i = 0; i < n; i++) {
+            const ssf_record * r = recs[i];
+            const size_t R = r->rows;
+            for (int p = 0; p < np; p++) memcpy(pl[p] + at * prb[p], ssf_at(f, r->plane_off[p]), R * prb[p]);
+            memcpy(sq + at * grow, ssf_at(f, r->sq_off), R * grow);
+            memcpy(sd + at * ns, ssf_at(f, r->sd_off), R * ns * 2);
+            if (has_min) {
+                memcpy(mq + at * grow, ssf_at(f, r->mq_off), R * grow);
+                memcpy(md + at * ns, ssf_at(f, r->md_off), R * ns * 2);
+            }
+            at += R;
+        }
+    }
+    if (!ok) { free_stack(pl, sq, mq, sd, md); hx_failf("out of host memory"); }
+    return upload_stack(pl, sq, mq, sd, md, (int) rows, cols, nb, six, neg);
+}
+
 sml_hip_mat * sml_hip_mat_from_file(const char * path, const char * name) {
     OP_BEGIN(NULL);
     ssf_file f;
@@ -207,69 +277,81 @@ static int env_int(const char * name, int dflt) {
 }
 
 // Shape of a GEMV launch: NI chunks per lane (enough that one pass covers a
-// row: ng <= 64*NI, at most 8), RB rows per wave (more rows per wave for tall
-// matrices, so ~2048+ waves carry the whole matrix at once while the loads a
-// lane holds stay within RB*NI <= 16). SML_GEMV_RB / SML_GEMV_NI override.
-static void pick_shape(int rows, int cols, int swiglu, int * rb, int * ni) {
+// row: ng <= 64*NI, at most 8; SwiGLU and the fused prologue at most 4 and 2),
+// RB rows per wave (more rows per wave for tall matrices, so ~2048+ waves
+// carry the whole matrix at once while the loads a lane holds stay within
+// RB*NI <= 16; SwiGLU takes 2 or 4: one or two gate/up pairs).
+// SML_GEMV_RB / SML_GEMV_NI override for tuning sweeps.
+static void pick_shape(int rows, int cols, int swiglu, int fused, int * rb, int * ni) {
     const int ng = cols / 32;
+    const int imax = fused ? 2 : swiglu ? 4 : 8;
     int i = 1;
-    while (i < 8 && 64 * i < ng) i *= 2;
+    while (i < imax && 64 * i < ng) i *= 2;
     int r = 1;
     while (r < 4 && rows / (2 * r) >= 2048 && 2 * r * i <= 16) r *= 2;
-    if (swiglu) r = r < 2 ? 2 : r;
-    if (r == 4 && i == 8) i = 4;
-    if (r == 1 && i == 1) i = 2;
     const int fr = env_int("SML_GEMV_RB", 0), fi = env_int("SML_GEMV_NI", 0);
-    if (fr == 1 || fr == 2 || fr == 4) r = swiglu && fr == 1 ? 2 : fr;
-    if (fi == 1 || fi == 2 || fi == 4 || fi == 8) i = fi;
-    if (r == 1 && i == 1) i = 2;
-    if (r == 4 && i == 8) i = 4;
+    if (fr == 1 || fr == 2 || fr == 4) r = fr;
+    if ((fi == 1 || fi == 2 || fi == 4 || fi == 8) && fi <= imax) i = fi;
+    if (swiglu && r < 2) r = 2;
+    if (!swiglu && !fused && r == 1 && i == 1) i = 2;
+    if (!swiglu && r == 4 && i == 8) i = 4;
     *rb = r;
     *ni = i;
 }
 
-void op_gemv(hipStream_t st, const sml_hip_mat * const * mats, int nm, int epi, const int8_t * q,
-             const float * scale, const int32_t * sums, float * const * y, const float * const * bias,
-             const float * resid) {
-    if (nm < 1 || nm > SML_MAX_MATS) hx_failf("gemv of %d matrices", nm);
+int gemv_fuse_max_cols(int hq) { return hq ? 8192 : 4096; }
+
+void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int epi, const int8_t * q,
+             const float * scale, const int32_t * sums, float * y, const float * bias, const float * up_bias,
+             const float * resid, const gemv_fuse * fu) {
+    const int swiglu = epi == SML_EPI_SWIGLU;
+    if (swiglu != (up != NULL)) hx_failf("SwiGLU takes gate and up; other GEMVs one matrix");
+    if (up && (up->nbits != m->nbits || up->cols != m->cols || up->k.rows != m->k.rows))
+        hx_failf("SwiGLU needs gate and up of one shape and width");
+    if (epi == SML_EPI_RESIDUAL && !resid) hx_failf("residual GEMV without a residual");
     sml_kgemv a;
     memset(&a, 0, sizeof a);
-    const int nb = mats[0]->nbits, cols = mats[0]->cols;
-    int tot = 0;
-    for (int i = 0; i < nm; i++) {
-        if (mats[i]->nbits != nb || mats[i]->cols != cols) hx_failf("gemv group mixes shapes or widths");
-        a.m[i] = mats[i]->k;
-        a.m[i].y = y[i];
-        a.m[i].bias = bias ? bias[i] : NULL;
-        a.m[i].row_begin = tot;
-        tot += mats[i]->k.rows;
-    }
-    if (epi == SML_EPI_SWIGLU && (nm != 2 || mats[0]->k.rows != mats[1]->k.rows))
-        hx_failf("swiglu needs gate and up of one shape");
-    a.nmat = nm; a.cols = cols; a.epi = epi;
+    const int nb = m->nbits, cols = m->cols;
+    a.m[0] = m->k;
+    a.m[0].y = y;
+    a.m[0].bias = bias;
+    if (up) { a.m[1] = up->k; a.m[1].y = y; a.m[1].bias = up_bias; }
+    a.cols = cols; a.epi = epi; a.total_rows = m->k.rows;
     a.q = q; a.scale = scale; a.sums = sums; a.resid = resid;
-    a.total_rows = epi == SML_EPI_SWIGLU ? mats[0]->k.rows : tot;
-    int rb, ni;
-    pick_shape(a.total_rows, cols, epi == SML_EPI_SWIGLU, &rb, &ni);
-    const int rows_per_wave = epi == SML_EPI_SWIGLU ? rb / 2 : rb;
-    const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
-    const int wgs = (waves + 3) / 4;
-    const int wg = env_int("SML_GEMV_WG", 256), nt = env_int("SML_GEMV_NT", 1);
+    const int am = fu && fu->x, hq = fu && fu->hq;
+    if (am) {
+        if (cols > gemv_fuse_max_cols(hq)) hx_failf("fused activation prologue takes at most %d columns", gemv_fuse_max_cols(hq));
+        a.x = fu->x; a.norm_w = fu->norm_w; a.perm = fu->perm; a.eps = fu->eps;
+    } else if (!q || !scale || !sums) {
+        hx_failf("gemv without an activation");
+    }
+    if (hq) {
+        if (!swiglu || a.total_rows % 32) hx_failf("h quantization needs SwiGLU rows in whole groups");
+        a.hq = fu->hq; a.hscale = fu->hscale; a.hsums = fu->hsums;
+    }
+    // LDS: int8 codes, per-group (s, s*sum), and the fused prologue's gather buffer
+    const size_t lds = ((size_t) cols + 8u * (size_t) (cols / 32) + 15u) / 16u * 16u + (am && fu->perm ? 4u * (size_t) cols : 0u);
     char name[48];
-    if (nb == 4 && (wg != 256 || !nt) && (wg == 256 || wg == 512 || wg == 1024)) {
-        snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_w%d_t%d", nb, rb, ni, wg, nt ? 1 : 0);
-        const int wpg = wg / 64;
-        hx_launch(name, (unsigned) ((waves + wpg - 1) / wpg), 1, (unsigned) wg,
-                  (size_t) cols + 8u * (size_t) (cols / 32), st, &a);
+    if (hq) {
+        const int ng = cols / 32;
+        int ni = 1;
+        while (ni < 4 && 64 * ni < ng) ni *= 2;
+        snprintf(name, sizeof name, "sml_gemv_q%d_h%s_i%d", nb, am ? "n" : "", ni);
+        hx_launch(name, (unsigned) (a.total_rows / 32), 1, 1024, lds, st, &a);
         return;
     }
-    snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d", nb, rb, ni);
-    hx_launch(name, (unsigned) wgs, 1, 256, (size_t) cols + 8u * (size_t) (cols / 32), st, &a);
+    int rb, ni;
+    pick_shape(a.total_rows, cols, swiglu, am, &rb, &ni);
+    const int rows_per_wave = swiglu ? rb / 2 : rb;
+    const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
+    if (swiglu) snprintf(name, sizeof name, "sml_gemv_q%d_s%s_r%d_i%d", nb, am ? "n" : "", rb, ni);
+    else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d%s", nb, rb, ni, am ? "_n" : "");
+    hx_launch(name, (unsigned) ((waves + 3) / 4), 1, 256, lds, st, &a);
 }
 
 int sml_hip_matvec(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, float * y) {
     OP_BEGIN(-1);
-    op_gemv(0, &m, 1, SML_EPI_STORE, q, scale, sums, &y, NULL, NULL);
+    op_gemv(0, m, NULL, SML_EPI_STORE, q, scale, sums, y, NULL, NULL, NULL, NULL);
     HX_LEAVE();
     return 0;
 }
@@ -277,9 +359,33 @@ int sml_hip_matvec(const sml_hip_mat * m, const int8_t * q, const float * scale,
 int sml_hip_matvec_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q,
                           const float * scale, const int32_t * sums, float * h) {
     OP_BEGIN(-1);
-    const sml_hip_mat * ms[2] = { gate, up };
-    float * ys[2] = { h, h };
-    op_gemv(0, ms, 2, SML_EPI_SWIGLU, q, scale, sums, ys, NULL, NULL);
+    op_gemv(0, gate, up, SML_EPI_SWIGLU, q, scale, sums, h, NULL, NULL, NULL, NULL);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_matvec_normq(const sml_hip_mat * m, const float * x, const float * w, float eps, const int32_t * perm,
+                         float * y) {
+    OP_BEGIN(-1);
+    if (!x) hx_failf("matvec_normq needs x");
+    gemv_fuse fu;
+    memset(&fu, 0, sizeof fu);
+    fu.x = x; fu.norm_w = w; fu.eps = eps; fu.perm = perm;
+    op_gemv(0, m, NULL, SML_EPI_STORE, NULL, NULL, NULL, y, NULL, NULL, NULL, &fu);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_matvec_swiglu_fused(const sml_hip_mat * gate, const sml_hip_mat * up, const float * x, const float * w,
+                                float eps, const int32_t * perm, const int8_t * q, const float * scale,
+                                const int32_t * sums, float * h, int8_t * hq, float * hscale, int32_t * hsums) {
+    OP_BEGIN(-1);
+    if (hq && (!hscale || !hsums)) hx_failf("h quantization needs hq, hscale and hsums");
+    gemv_fuse fu;
+    memset(&fu, 0, sizeof fu);
+    fu.x = x; fu.norm_w = w; fu.eps = eps; fu.perm = perm;
+    fu.hq = hq; fu.hscale = hscale; fu.hsums = hsums;
+    op_gemv(0, gate, up, SML_EPI_SWIGLU, q, scale, sums, h, NULL, NULL, NULL, &fu);
     HX_LEAVE();
     return 0;
 }
@@ -291,7 +397,7 @@ int sml_hip_time_matvec(const sml_hip_mat * const * mats, int ncopy, const int8_
     HX(hipEventCreate(&e0));
     HX(hipEventCreate(&e1));
     HX(hipEventRecord(e0, 0));
-    for (int i = 0; i < iters; i++) op_gemv(0, &mats[i % ncopy], 1, SML_EPI_STORE, q, scale, sums, &y, NULL, NULL);
+    for (int i = 0; i < iters; i++) op_gemv(0, mats[i % ncopy], NULL, SML_EPI_STORE, q, scale, sums, y, NULL, NULL, NULL, NULL);
     HX(hipEventRecord(e1, 0));
     HX(hipEventSynchronize(e1));
     HX(hipEventElapsedTime(ms_total, e0, e1));

@@ -23,9 +23,30 @@ void mat_free(sml_hip_mat * m);
 void op_normq(hipStream_t st, float * x, const float * resid, const float * w, float eps, int n,
               int nout, const int32_t * const * perm, int8_t * const * q, float * const * scale,
               int32_t * const * sums, float * normed, int per256);
-void op_gemv(hipStream_t st, const sml_hip_mat * const * mats, int nm, int epi, const int8_t * q,
-             const float * scale, const int32_t * sums, float * const * y, const float * const * bias,
-             const float * resid);
+// Optional fusions of a GEMV launch: x != NULL computes the activation in the
+// kernel's prologue (RMSNorm with norm_w if not NULL, gather through perm if
+// not NULL, per-32 quantization) instead of reading q/scale/sums; hq != NULL
+// (SwiGLU only, rows a multiple of 32) also quantizes h per 32 into
+// hq/hscale/hsums.
+typedef struct {
+    const float * x;
+    const float * norm_w;
+    const int32_t * perm;
+    float eps;
+    int8_t * hq;
+    float * hscale;
+    int32_t * hsums;
+} gemv_fuse;
+// Widest input the fused prologue takes (hq: the 1024-thread SwiGLU kernels).
+int gemv_fuse_max_cols(int hq);
+// y = W.x (+ bias, + resid for SML_EPI_RESIDUAL) for one matrix m; SwiGLU
+// (up != NULL): y = silu(gate.x + bias) * (up.x + up_bias).
+void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int epi, const int8_t * q,
+             const float * scale, const int32_t * sums, float * y, const float * bias, const float * up_bias,
+             const float * resid, const gemv_fuse * fu);
+// One matrix holding the rows of several FLAT records of one width and input
+// width, stacked in order (the q, k and v projections as one GEMV).
+sml_hip_mat * mat_stack(const ssf_file * f, const ssf_record * const * recs, int n);
 void op_embed(hipStream_t st, const sml_hip_mat * m, const int32_t * tok, const int32_t * pos,
               const int32_t * perm, float * x);
 void op_attention(hipStream_t st, const float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,

@@ -24,6 +24,16 @@ def tiny(tmp_path_factory):
 
 
 @pytest.fixture(scope="module")
+def tiny_inorder(tmp_path_factory):
+    """No permutations: the q/k/v and gate/up GEMVs compute their activations
+    in their prologues, attention quantizes o's input and SwiGLU quantizes h."""
+    p = tmp_path_factory.mktemp("dec") / "tiny_inorder.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000,
+                   qkv_bias=True, random_perm=False, seed=32)
+    return p
+
+
+@pytest.fixture(scope="module")
 def qwenish(tmp_path_factory):
     """Qwen2.5-1.5B layer shapes (hidden 1536, FFN 8960, 12/2 heads, q/k/v bias,
     tied head) with 4 layers and a 32000 vocabulary."""
@@ -81,6 +91,36 @@ def test_greedy_tokens_tiny(tiny):
     finally:
         d.close()
     check_tokens(list(out), toks[1:], logits)
+
+
+def test_greedy_tokens_inorder(tiny_inorder):
+    n = 40
+    toks, logits = greedy_oracle(tiny_inorder, 7, n, 64)
+    d = sa.Decoder(tiny_inorder, n_ctx=64)
+    try:
+        out = d.generate(7, 0, n)
+    finally:
+        d.close()
+    check_tokens(list(out), toks[1:], logits)
+
+
+@pytest.mark.parametrize("model", ["tiny", "tiny_inorder"])
+def test_fusions_do_not_change_logits(model, request, monkeypatch):
+    """With the fused prologues and h quantization switched off, each layer
+    runs the separate normq launches instead. The activations are the same
+    bits and every output row sums its chunks in the same order, so the
+    logits are identical."""
+    path = request.getfixturevalue(model)
+    outs = []
+    for fuse in ("1", "0"):
+        monkeypatch.setenv("SML_FUSE", fuse)
+        d = sa.Decoder(path, n_ctx=64)
+        try:
+            outs.append([d.step(t, i, 2000).copy() for i, t in enumerate([3, 17, 250, 9, 1999])])
+        finally:
+            d.close()
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
 
 
 def test_generate_equals_stepping_and_prefill(tiny):

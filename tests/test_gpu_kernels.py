@@ -158,6 +158,71 @@ def test_swiglu(tmpdir_s):
     close(h.read(np.float32), yg, "swiglu")
 
 
+# ------------------------------------------------------------ fused activation prologue, h quantization
+
+@pytest.mark.parametrize("nb", [4, 3, 6, 8])
+@pytest.mark.parametrize("cols,use_perm,use_norm", [(1536, True, True), (4096, False, True), (4096, True, False),
+                                                     (2048, False, False)])
+def test_matvec_normq_equals_normq_then_matvec(tmpdir_s, nb, cols, use_perm, use_norm):
+    """The prologue computes the normq kernel's activation bit for bit, so the
+    fused GEMV's output equals normq + matvec exactly; both match the oracle."""
+    p = tmpdir_s / f"fz{nb}_{cols}_{int(use_perm)}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, 1000, cols, nbits=nb, random_perm=use_perm, seed=900 + nb + cols)
+    t = SSF(p)["w"]
+    m = sa.Mat.from_file(p, "w")
+    rng = np.random.default_rng(cols + nb)
+    x = (rng.standard_normal(cols) * 3).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
+    perm = t.perm.astype(np.int32) if use_perm else None
+    act = dev_quantize(x, perm=perm, w=w if use_norm else None, eps=1e-5)
+    y0, y1 = sa.DevBuf(1000 * 4), sa.DevBuf(1000 * 4)
+    sa.matvec(m, act, y0)
+    xd, wd = sa.DevBuf.of(x), sa.DevBuf.of(w)
+    pd = sa.DevBuf.of(perm) if use_perm else None
+    sa.matvec_normq(m, xd, y1, w=wd if use_norm else None, perm=pd, eps=1e-5)
+    got = y1.read(np.float32)
+    np.testing.assert_array_equal(got, y0.read(np.float32))
+    v = x
+    if use_norm:
+        v = np.zeros(cols, np.float32)
+        ob.oracle().orc_rms_norm(v.ctypes.data, x.ctypes.data, w.ctypes.data, cols, np.float32(1e-5))
+    q, sc, su = ob.quantize_act(v[perm] if use_perm else v)
+    close(got, ob.matvec(t, q, sc, su), "matvec_normq")
+
+
+@pytest.mark.parametrize("n_embd,nb,xin,perm", [(1536, 4, True, True), (1536, 5, False, False),
+                                                (4096, 4, True, False), (4096, 8, True, True)])
+def test_swiglu_h_quantization(tmpdir_s, n_embd, nb, xin, perm):
+    """The SwiGLU kernel's h equals the plain SwiGLU's exactly, and its per-32
+    quantization of h equals the normq kernel's (no norm, in order) bit for bit."""
+    p = tmpdir_s / f"ffnh{n_embd}_{nb}_{int(perm)}.ssf"
+    n_ff = 2048 + 128       # 68 groups of h: 68 workgroups of the h kernel
+    if not p.exists():
+        sa.synth_model(p, n_layer=1, n_embd=n_embd, n_head=n_embd // 128, n_head_kv=2, n_ff=n_ff, n_vocab=256, nbits=nb,
+                       random_perm=perm, seed=78 + nb)
+    f = SSF(p)
+    g, u = f["blk.0.ffn_gate.weight"], f["blk.0.ffn_up.weight"]
+    rng = np.random.default_rng(n_embd)
+    x = (rng.standard_normal(n_embd) * 2).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(n_embd)).astype(np.float32)
+    gp = g.perm.astype(np.int32) if g.perm is not None else None
+    act = dev_quantize(x, perm=gp, w=w, eps=1e-5)
+    mg, mu = sa.Mat.from_file(p, g.name), sa.Mat.from_file(p, u.name)
+    h0, h1 = sa.DevBuf(n_ff * 4), sa.DevBuf(n_ff * 4)
+    sa.matvec_swiglu(mg, mu, act, h0)
+    hact = sa.Act(n_ff)
+    if xin:
+        sa.matvec_swiglu_fused(mg, mu, h1, x=sa.DevBuf.of(x), w=sa.DevBuf.of(w), eps=1e-5,
+                               perm=sa.DevBuf.of(gp) if gp is not None else None, hact=hact)
+    else:
+        sa.matvec_swiglu_fused(mg, mu, h1, act=act, hact=hact)
+    h = h1.read(np.float32)
+    np.testing.assert_array_equal(h, h0.read(np.float32))
+    for a, b, name in zip(hact.read(), ob.quantize_act(h), ("q", "scale", "sums")):
+        np.testing.assert_array_equal(a, b, err_msg=name)
+
+
 # ------------------------------------------------------------ embed, attention, argmax
 
 @pytest.mark.parametrize("nb", [4, 6, 8])
