@@ -71,8 +71,8 @@ int sml_hip_matvec_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, cons
 int sml_hip_matvec_normq(const sml_hip_mat * m, const float * x, const float * w, float eps, const int32_t * perm,
                          float * y);
 // sml_hip_matvec_swiglu with its two fusions: x != NULL computes the activation
-// in the prologue as sml_hip_matvec_normq does (cols <= 8192 when hq is given,
-// else 4096; q/scale/sums unused), otherwise q/scale/sums are read; hq != NULL
+// in the prologue as sml_hip_matvec_normq does (cols <= 4096; q/scale/sums
+// unused), otherwise q/scale/sums are read; hq != NULL
 // also writes the per-32 quantization of h in order (rows a multiple of 32)
 // into hq/hscale/hsums, equal to sml_hip_normq of h without norm.
 // replaces sml_g_ffns + sml_g_quantw2 (sml/sml-gpu-fast.cu:319-354,522-543)

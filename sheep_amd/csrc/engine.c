@@ -52,7 +52,7 @@ static struct {
     int8_t * hq;               // the SwiGLU kernel's quantized h, input of down
     float * hs;
     int32_t * hsum;
-    int fuse;                  // fused activation prologues / h quantization (SML_FUSE, default on)
+    int fuse;                  // SML_FUSE bits: 1 activation prologues, 2 h quantization (default 3)
     uint16_t * kc, * vc;
     int32_t * hist, * pos, * tok;
     float * lg_host;
@@ -161,7 +161,7 @@ static void launch_layer(int L) {
     const size_t kvd = (size_t) G.KV * G.hd;
     int slot[3];
     // q/k/v: the stacked GEMV computes RMSNorm + quantize of x in its prologue
-    if (y->qkv && G.fuse && G.E <= gemv_fuse_max_cols(0)) {
+    if (y->qkv && (G.fuse & 1) && G.E <= gemv_fuse_max_cols(0)) {
         gemv_fuse fu;
         memset(&fu, 0, sizeof fu);
         fu.x = G.x; fu.norm_w = y->an; fu.eps = G.eps; fu.perm = pdev(y->perm_qkv[0]);
@@ -185,11 +185,11 @@ static void launch_layer(int L) {
     gemv1(y->o, slot[0], SML_EPI_RESIDUAL, G.x, NULL, G.x);
     // gate/up: one SwiGLU launch when they share a permutation and width; it
     // also quantizes h for down when down reads h in order
-    const int h_fused = G.fuse && y->perm_down < 0 && G.F % 32 == 0;
+    const int h_fused = (G.fuse & 2) && y->perm_down < 0 && G.F % 32 == 0;
     if (y->perm_gu[0] == y->perm_gu[1] && y->gate->nbits == y->up->nbits) {
         gemv_fuse fu;
         memset(&fu, 0, sizeof fu);
-        const int x_fused = G.fuse && G.E <= gemv_fuse_max_cols(h_fused);
+        const int x_fused = (G.fuse & 1) && G.E <= gemv_fuse_max_cols(h_fused);
         if (x_fused) { fu.x = G.x; fu.norm_w = y->fn; fu.eps = G.eps; fu.perm = pdev(y->perm_gu[0]); }
         else prep(G.x, y->fn, NULL, G.E, y->perm_gu, 2, slot);
         if (h_fused) { fu.hq = G.hq; fu.hscale = G.hs; fu.hsums = G.hsum; }
@@ -418,7 +418,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     G.hq = dalloc((size_t) G.F);
     G.hs = dalloc((size_t) G.F / 32 * 4);
     G.hsum = dalloc((size_t) G.F / 32 * 4);
-    G.fuse = env_int("SML_FUSE", 1) != 0;
+    G.fuse = env_int("SML_FUSE", 3);
     const size_t kvn = (size_t) G.n_layer * n_ctx * G.KV * G.hd;
     G.kc = dalloc(kvn * 2);
     G.vc = dalloc(kvn * 2);

@@ -103,14 +103,16 @@ template <int NB> struct ChunkW {
     v2u o1;                       // 1-bit words of the group pair
 };
 
-// row bases of each plane (pl[] already offset to the row)
+// Chunk c of one row: pl[] are the planes' bases (uniform), ro[] the row's
+// byte offset in each plane. Offsets are 32-bit so the loads address as
+// uniform base + per-lane offset, which keeps one VGPR per address.
 template <int NB, bool NT>
-__device__ __forceinline__ void load_chunk(ChunkW<NB> & w, const uint8_t * const * pl, int c) {
+__device__ __forceinline__ void load_chunk(ChunkW<NB> & w, const uint8_t * const * pl, const uint32_t * ro, int c) {
     using P = Planes<NB>;
-    if constexpr (P::N4) w.n4 = ld<NT>((const v4u *) (pl[P::P4] + (size_t) c * 16));
-    if constexpr (NB == 8) w.h4 = ld<NT>((const v4u *) (pl[1] + (size_t) c * 16));
-    if constexpr (P::N2) w.t2 = ld<NT>((const v4u *) (pl[P::P2] + (size_t) (c >> 2) * 32 + (c & 1) * 16));
-    if constexpr (P::N1) w.o1 = ld<NT>((const v2u *) (pl[P::P1] + (size_t) (c >> 1) * 8));
+    if constexpr (P::N4) w.n4 = ld<NT>((const v4u *) (pl[P::P4] + (ro[P::P4] + (uint32_t) c * 16u)));
+    if constexpr (NB == 8) w.h4 = ld<NT>((const v4u *) (pl[1] + (ro[1] + (uint32_t) c * 16u)));
+    if constexpr (P::N2) w.t2 = ld<NT>((const v4u *) (pl[P::P2] + (ro[P::P2] + (uint32_t) (c >> 2) * 32u + (uint32_t) (c & 1) * 16u)));
+    if constexpr (P::N1) w.o1 = ld<NT>((const v2u *) (pl[P::P1] + (ro[P::P1] + (uint32_t) (c >> 1) * 8u)));
 }
 
 // partial dots of chunk c over its 16 columns: da for group c&~1 against
@@ -266,14 +268,34 @@ __device__ __forceinline__ void fused_act(const sml_kgemv & a, const float4 (&fx
 // Chunks past a row's end read the row's last chunk (a broadcast of bytes
 // already fetched) and contribute nothing because their activation scale is
 // taken as zero; rows past the end read row 0 and are never stored.
-template <int NB, int RB, int NI, int WG, bool NT, int AM, bool SW, bool HQ>
+// Sum over aligned segments of LPR lanes (16, 32 or 64): the row shifts give
+// an inclusive scan inside each 16-lane DPP row, the row broadcasts carry it
+// across rows. The segment's last lane ends up with its total.
+template <int LPR>
+__device__ __forceinline__ float seg_sum(float v) {
+    int x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true)); x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true)); x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true)); x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true)); x = __builtin_bit_cast(int, v);
+    if constexpr (LPR >= 32) {
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false)); x = __builtin_bit_cast(int, v);
+    }
+    if constexpr (LPR == 64) v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false));
+    return v;
+}
+
+template <int NB, int RB, int NI, int WG, bool NT, int AM, bool SW, bool HQ, int LPR = 64>
 __device__ void gemv_body(const sml_kgemv & a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8;
     int8_t * lq = (int8_t *) lds;
     float2 * lsc = (float2 *) (lds + n);
     const int tid = threadIdx.x, lane = tid & (WAVE - 1);
-    constexpr int RPW = SW ? RB / 2 : RB;          // output rows per wave
+    // LPR lanes stream one row; a wave holds SUB = 64/LPR rows per row slot
+    constexpr int SUB = WAVE / LPR;
+    const int l = lane % LPR, u = lane / LPR;
+    constexpr int RPW = (SW ? RB / 2 : RB) * SUB;  // output rows per wave
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = (blockIdx.x * (WG / WAVE) + wave) * RPW;
 
@@ -285,7 +307,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
     int32_t sg_u[SG];
     const int nq16 = n / 16;
     // fused prologue: float4 words of x, norm_w and perm per thread
-    constexpr int FK = AM == 0 ? 1 : (WG >= 1024 ? 2 : 4);
+    constexpr int FK = AM == 0 ? 1 : (WG >= 512 ? 2 : 4);
     float4 fx[FK], fw[FK];
     int4 fp[FK];
     if constexpr (AM == 0) {
@@ -310,46 +332,52 @@ __device__ void gemv_body(const sml_kgemv & a) {
         }
     }
 
-    // 2. this wave's rows: plane row bases and field rows
+    // 2. this wave's rows: uniform plane and field bases per row slot, and
+    // each lane's 32-bit row offsets (the host keeps every plane under 4 GB)
     using P = Planes<NB>;
     const uint8_t * pl[RB][3];
-    const uint16_t * fq[RB];          // (sq, mq) pairs as one 16-bit word per group
-    const uint32_t * fd[RB];          // (sd, md) pairs as one 32-bit word per superblock
+    uint32_t ro[RB][3];
+    const uint8_t * fqb[RB];          // (sq, mq) pairs as one 16-bit word per group
+    const uint8_t * fdb[RB];          // (sd, md) pairs as one 32-bit word per superblock
+    uint32_t fqo[RB], fdo[RB];
     int orow[RB];
     bool valid[RB];
     #pragma unroll
     for (int s = 0; s < RB; s++) {
-        const int grow = SW ? row0 + (s >> 1) : row0 + s;
+        const int grow = row0 + (SW ? (s >> 1) : s) * SUB + u;
         orow[s] = grow;
         valid[s] = grow < a.total_rows;
         const sml_kmat & m = (SW && (s & 1)) ? a.m[1] : a.m[0];
-        const size_t r = (size_t) (valid[s] ? grow : 0);
+        const uint32_t r = (uint32_t) (valid[s] ? grow : 0);
         pl[s][0] = m.plane[0]; pl[s][1] = m.plane[1]; pl[s][2] = m.plane[2];
-        if constexpr (P::N4) pl[s][P::P4] = m.plane[P::P4] + r * P::b4(n);
-        if constexpr (NB == 8) pl[s][1] = m.plane[1] + r * P::b4(n);
-        if constexpr (P::N2) pl[s][P::P2] = m.plane[P::P2] + r * P::b2(n);
-        if constexpr (P::N1) pl[s][P::P1] = m.plane[P::P1] + r * P::b1(n);
-        fq[s] = (const uint16_t *) (m.sqmq + r * (size_t) ng * 2);
-        fd[s] = (const uint32_t *) (m.sdmd + r * (size_t) ns * 2);
+        ro[s][0] = ro[s][1] = ro[s][2] = 0;
+        if constexpr (P::N4) ro[s][P::P4] = r * (uint32_t) P::b4(n);
+        if constexpr (NB == 8) ro[s][1] = r * (uint32_t) P::b4(n);
+        if constexpr (P::N2) ro[s][P::P2] = r * (uint32_t) P::b2(n);
+        if constexpr (P::N1) ro[s][P::P1] = r * (uint32_t) P::b1(n);
+        fqb[s] = m.sqmq;
+        fdb[s] = (const uint8_t *) m.sdmd;
+        fqo[s] = r * (uint32_t) ng * 2u;
+        fdo[s] = r * (uint32_t) ns * 4u;
     }
 
     float acc[RB];
     #pragma unroll
     for (int s = 0; s < RB; s++) acc[s] = 0.0f;
     bool staged = false;
-    for (int c0 = 0; c0 < ng; c0 += WAVE * NI) {
+    for (int c0 = 0; c0 < ng; c0 += LPR * NI) {
         // 3. every weight load of this lane for NI chunks of RB rows, with no branches
         ChunkW<NB> w[NI][RB];
         uint32_t fqv[NI][RB], fdv[NI][RB];
         #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const int c = c0 + i * WAVE + lane;
+            const int c = c0 + i * LPR + l;
             const int cl = c < ng ? c : ng - 1;
             #pragma unroll
             for (int s = 0; s < RB; s++) {
-                load_chunk<NB, NT>(w[i][s], pl[s], cl);
-                fqv[i][s] = fq[s][cl];
-                fdv[i][s] = fd[s][cl >> 3];
+                load_chunk<NB, NT>(w[i][s], pl[s], ro[s], cl);
+                fqv[i][s] = *(const uint16_t *) (fqb[s] + (fqo[s] + (uint32_t) cl * 2u));
+                fdv[i][s] = *(const uint32_t *) (fdb[s] + (fdo[s] + (uint32_t) (cl >> 3) * 4u));
             }
         }
         if (!staged) {
@@ -374,7 +402,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
         // 5. dots and the per-group epilogue; lane c ends up owning group c
         #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const int c = c0 + i * WAVE + lane;
+            const int c = c0 + i * LPR + l;
             const bool live = c < ng;                     // the pair (c&~1, c|1) is live or dead as a whole
             const int cc = live ? c : ng - 1;             // keep LDS reads in range
             const int off = 32 * (cc & ~1) + 16 * (cc & 1);
@@ -398,12 +426,12 @@ __device__ void gemv_body(const sml_kgemv & a) {
         }
     }
     #pragma unroll
-    for (int s = 0; s < RB; s++) acc[s] = wave_sum_dpp(acc[s]);
+    for (int s = 0; s < RB; s++) acc[s] = seg_sum<LPR>(acc[s]);
     if constexpr (HQ) {
         // 32 consecutive outputs per workgroup (RB/2 gate/up pairs per wave):
         // h = silu(g)*u, then its per-32 quantization for the down projection
         __shared__ float hb[32];
-        if (lane == WAVE - 1) {
+        if (l == LPR - 1) {
             #pragma unroll
             for (int s = 0; s < RB; s += 2) {
                 const int row = orow[s];
@@ -415,7 +443,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
                     h = (g / (1.0f + expf(-g))) * u;             // sml/sml-run.c:451-454
                     a.m[0].y[row] = h;
                 }
-                hb[wave * RPW + (s >> 1)] = h;
+                hb[wave * RPW + (s >> 1) * SUB + u] = h;
             }
         }
         __syncthreads();
@@ -433,7 +461,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
         }
         return;
     }
-    if (lane != WAVE - 1) return;
+    if (l != LPR - 1) return;
     if constexpr (SW) {
         #pragma unroll
         for (int s = 0; s < RB; s += 2) {
@@ -461,8 +489,8 @@ __device__ void gemv_body(const sml_kgemv & a) {
 // suffix _n for the fused activation prologue (input width up to 4096);
 // sml_gemv_q<bits>_s_r<RB>_i<NI> for SwiGLU (RB/2 gate/up pairs per wave, _sn
 // with the prologue); sml_gemv_q<bits>_h_i<NI> for SwiGLU that also
-// quantizes h (16 waves x 2 pairs = 32 outputs per workgroup; _hn with the
-// prologue, input width up to 8192).
+// quantizes h: 16 lanes per row, so 8 waves x 4 pairs = 32 outputs per
+// 512-thread workgroup (_hn with the prologue, input width up to 4096).
 #define GEMV_KERNEL(NB, RB, NI)                                                                             \
     extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_r##RB##_i##NI(const sml_kgemv a) {     \
         gemv_body<NB, RB, NI, 256, true, 0, false, false>(a);                                               \
@@ -479,11 +507,11 @@ __device__ void gemv_body(const sml_kgemv & a) {
         gemv_body<NB, RB, NI, 256, true, 1, true, false>(a);                                                \
     }
 #define GEMV_KERNEL_H(NB, NI)                                                                               \
-    extern "C" __global__ __launch_bounds__(1024) void sml_gemv_q##NB##_h_i##NI(const sml_kgemv a) {         \
-        gemv_body<NB, 4, NI, 1024, true, 0, true, true>(a);                                                 \
+    extern "C" __global__ __launch_bounds__(512) void sml_gemv_q##NB##_h_i##NI(const sml_kgemv a) {       \
+        gemv_body<NB, 2, NI, 512, true, 0, true, true, 16>(a);                                              \
     }                                                                                                       \
-    extern "C" __global__ __launch_bounds__(1024) void sml_gemv_q##NB##_hn_i##NI(const sml_kgemv a) {        \
-        gemv_body<NB, 4, NI, 1024, true, 1, true, true>(a);                                                 \
+    extern "C" __global__ __launch_bounds__(512) void sml_gemv_q##NB##_hn_i##NI(const sml_kgemv a) {      \
+        gemv_body<NB, 2, NI, 512, true, 1, true, true, 16>(a);                                              \
     }
 #define GEMV_WIDTH(NB)                                                                     \
     GEMV_KERNEL(NB, 1, 2) GEMV_KERNEL(NB, 1, 4) GEMV_KERNEL(NB, 1, 8)                     \
@@ -493,7 +521,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
     GEMV_KERNEL_N(NB, 2, 2) GEMV_KERNEL_N(NB, 4, 1) GEMV_KERNEL_N(NB, 4, 2)               \
     GEMV_KERNEL_S(NB, 2, 1) GEMV_KERNEL_S(NB, 2, 2) GEMV_KERNEL_S(NB, 2, 4)               \
     GEMV_KERNEL_S(NB, 4, 1) GEMV_KERNEL_S(NB, 4, 2) GEMV_KERNEL_S(NB, 4, 4)               \
-    GEMV_KERNEL_H(NB, 1) GEMV_KERNEL_H(NB, 2) GEMV_KERNEL_H(NB, 4)
+    GEMV_KERNEL_H(NB, 2) GEMV_KERNEL_H(NB, 4) GEMV_KERNEL_H(NB, 8)
 GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH(7) GEMV_WIDTH(8)
 
 // ---------------------------------------------------------------- norm + quantize

@@ -299,7 +299,7 @@ static void pick_shape(int rows, int cols, int swiglu, int fused, int * rb, int 
     *ni = i;
 }
 
-int gemv_fuse_max_cols(int hq) { return hq ? 8192 : 4096; }
+int gemv_fuse_max_cols(int hq) { (void) hq; return 4096; }
 
 void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int epi, const int8_t * q,
              const float * scale, const int32_t * sums, float * y, const float * bias, const float * up_bias,
@@ -316,6 +316,8 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
     a.m[0].y = y;
     a.m[0].bias = bias;
     if (up) { a.m[1] = up->k; a.m[1].y = y; a.m[1].bias = up_bias; }
+    // the kernels address each plane and field array with 32-bit offsets
+    if ((uint64_t) m->k.rows * (uint64_t) cols >= (1ull << 32)) hx_failf("matrix too large for one GEMV launch");
     a.cols = cols; a.epi = epi; a.total_rows = m->k.rows;
     a.q = q; a.scale = scale; a.sums = sums; a.resid = resid;
     const int am = fu && fu->x, hq = fu && fu->hq;
@@ -333,11 +335,13 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
     const size_t lds = ((size_t) cols + 8u * (size_t) (cols / 32) + 15u) / 16u * 16u + (am && fu->perm ? 4u * (size_t) cols : 0u);
     char name[48];
     if (hq) {
+        // 16 lanes per row: NI chunks per lane with 16*NI >= groups (a second
+        // pass beyond 8)
         const int ng = cols / 32;
-        int ni = 1;
-        while (ni < 4 && 64 * ni < ng) ni *= 2;
+        int ni = 2;
+        while (ni < 8 && 16 * ni < ng) ni *= 2;
         snprintf(name, sizeof name, "sml_gemv_q%d_h%s_i%d", nb, am ? "n" : "", ni);
-        hx_launch(name, (unsigned) (a.total_rows / 32), 1, 1024, lds, st, &a);
+        hx_launch(name, (unsigned) (a.total_rows / 32), 1, 512, lds, st, &a);
         return;
     }
     int rb, ni;

@@ -107,12 +107,13 @@ def test_greedy_tokens_inorder(tiny_inorder):
 @pytest.mark.parametrize("model", ["tiny", "tiny_inorder"])
 def test_fusions_do_not_change_logits(model, request, monkeypatch):
     """With the fused prologues and h quantization switched off, each layer
-    runs the separate normq launches instead. The activations are the same
-    bits and every output row sums its chunks in the same order, so the
-    logits are identical."""
+    runs the separate normq launches instead. The prologue's activations are
+    the same bits; the h-quantizing SwiGLU sums each row over 16 lanes instead
+    of 64, which moves h by float rounding (and can move an int8 code of h by
+    one step). The logits agree closely and pick the same token."""
     path = request.getfixturevalue(model)
     outs = []
-    for fuse in ("1", "0"):
+    for fuse in ("3", "0"):
         monkeypatch.setenv("SML_FUSE", fuse)
         d = sa.Decoder(path, n_ctx=64)
         try:
@@ -120,7 +121,8 @@ def test_fusions_do_not_change_logits(model, request, monkeypatch):
         finally:
             d.close()
     for a, b in zip(*outs):
-        np.testing.assert_array_equal(a, b)
+        assert np.corrcoef(a, b)[0, 1] > 0.9999
+        assert int(np.argmax(a)) == int(np.argmax(b))
 
 
 def test_generate_equals_stepping_and_prefill(tiny):

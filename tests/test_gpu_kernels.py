@@ -194,8 +194,9 @@ def test_matvec_normq_equals_normq_then_matvec(tmpdir_s, nb, cols, use_perm, use
 @pytest.mark.parametrize("n_embd,nb,xin,perm", [(1536, 4, True, True), (1536, 5, False, False),
                                                 (4096, 4, True, False), (4096, 8, True, True)])
 def test_swiglu_h_quantization(tmpdir_s, n_embd, nb, xin, perm):
-    """The SwiGLU kernel's h equals the plain SwiGLU's exactly, and its per-32
-    quantization of h equals the normq kernel's (no norm, in order) bit for bit."""
+    """The h-quantizing SwiGLU kernel (16 lanes per row) agrees with the plain
+    SwiGLU to float rounding of the same sums, and its per-32 quantization of
+    its own h equals the normq kernel's (no norm, in order) bit for bit."""
     p = tmpdir_s / f"ffnh{n_embd}_{nb}_{int(perm)}.ssf"
     n_ff = 2048 + 128       # 68 groups of h: 68 workgroups of the h kernel
     if not p.exists():
@@ -218,7 +219,8 @@ def test_swiglu_h_quantization(tmpdir_s, n_embd, nb, xin, perm):
     else:
         sa.matvec_swiglu_fused(mg, mu, h1, act=act, hact=hact)
     h = h1.read(np.float32)
-    np.testing.assert_array_equal(h, h0.read(np.float32))
+    h_ref = h0.read(np.float32)
+    assert np.abs(h - h_ref).max() <= 1e-6 * np.abs(h_ref).max()
     for a, b, name in zip(hact.read(), ob.quantize_act(h), ("q", "scale", "sums")):
         np.testing.assert_array_equal(a, b, err_msg=name)
 
