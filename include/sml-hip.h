@@ -95,6 +95,31 @@ int sml_hip_time_read(const void * const * bufs, int nbuf, size_t bytes, int gri
 // read and write counters give the scale for the GEMV's counter readings.
 int sml_hip_copy(void * dst, const void * src, size_t bytes);
 
+// ------------------------------------------------------------ GPTQ-style 4-bit
+// A GPTQ (AutoGPTQ / optimum) 4-bit matrix resident in HBM as its own three
+// arrays, rows = outputs, cols = inputs: qweight int32 [cols/8][rows] (8 codes
+// along the input, lowest nibble first), qzeros int32 [cols/128][rows/8] (8
+// zero codes along the output), scales fp16 [cols/128][rows]; group 128,
+// identity g_idx; zero_add 1 for the v1 files (stored zero = zero - 1), 0 for
+// v2. Weight = (code - zero) * scale, the layout tooling/sml_unpack.py:66-95
+// (dequant_gptq) converts offline; the reference engine has no GPU kernel for
+// it. rows % 8 == 0, cols % 128 == 0.
+typedef struct sml_hip_gptq sml_hip_gptq;
+sml_hip_gptq * sml_hip_gptq_upload(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                                   int rows, int cols, int group, int zero_add);
+void           sml_hip_gptq_free(sml_hip_gptq * m);
+// Bytes the matrix occupies in HBM (qweight + qzeros + scales).
+size_t         sml_hip_gptq_bytes(const sml_hip_gptq * m);
+// y = W.x with fp32 x (no activation quantization).
+int sml_hip_gptq_matvec(const sml_hip_gptq * m, const float * x, float * y);
+// Codes [nrows][cols] and zeros [nrows][cols/128] (stored zero + zero_add) of
+// rows [row0, row0+nrows): the integers dequant_gptq works on
+// (tooling/sml_unpack.py:66-76,84-89).
+int sml_hip_gptq_unpack(const sml_hip_gptq * m, int row0, int nrows, uint8_t * codes, uint8_t * zeros);
+// Time `iters` launches of sml_hip_gptq_matvec rotating over `ncopy` matrices.
+int sml_hip_gptq_time(const sml_hip_gptq * const * mats, int ncopy, const float * x, float * y, int iters,
+                      float * ms_total);
+
 // ------------------------------------------------------------ unpack / embed
 // Integer code of every weight of rows [row0, row0+nrows), one byte each,
 // permuted column order: the unpack truth of sml_dequant_row_* (sml/sml-kernel.c:2134-2260)

@@ -56,6 +56,9 @@ def oracle():
             "orc_moe_route": (c_int, [c_void_p, c_int, c_int, c_uint, c_void_p, c_void_p]),
             "orc_router": (None, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
             "orc_argmax": (c_int, [c_void_p, c_int]),
+            "orc_gptq_unpack_row": (None, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+            "orc_gptq_dequant_row": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
+            "orc_gptq_matvec": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
             "orc_model_open": (c_void_p, [c_char_p, c_int]),
             "orc_model_close": (None, [c_void_p]),
             "orc_forward": (P(c_float), [c_void_p, c_int, c_int]),
@@ -275,3 +278,25 @@ class RefModel:
         if self.h:
             ref().ref_close(self.h)
             self.h = None
+
+
+# ------------------------------------------------------------ GPTQ-style 4-bit
+
+def gptq_unpack_row(qweight, qzeros, rows, cols, row, group=128, zero_add=1):
+    c = np.zeros(cols, np.uint8)
+    z = np.zeros(cols // group, np.uint8)
+    oracle().orc_gptq_unpack_row(ptr(qweight), ptr(qzeros), rows, cols, group, zero_add, row, ptr(c), ptr(z))
+    return c, z
+
+
+def gptq_dequant_row(qweight, qzeros, scales, rows, cols, row, group=128, zero_add=1):
+    out = np.zeros(cols, np.float32)
+    oracle().orc_gptq_dequant_row(ptr(qweight), ptr(qzeros), ptr(scales), rows, cols, group, zero_add, row, ptr(out))
+    return out
+
+
+def gptq_matvec(qweight, qzeros, scales, rows, cols, x, group=128, zero_add=1):
+    y = np.zeros(rows, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    oracle().orc_gptq_matvec(ptr(qweight), ptr(qzeros), ptr(scales), rows, cols, group, zero_add, ptr(x), ptr(y))
+    return y

@@ -345,6 +345,52 @@ int orc_argmax(const float * logits, int n) {
     return best;
 }
 
+// ------------------------------------------------------------ GPTQ-style 4-bit
+
+// tooling/sml_unpack.py:66-76 (_unpack_ints): word k of column o holds codes
+// of inputs 8k..8k+7, input 8k+i in bits 4i..4i+3 (dim 0 for qweight, dim 1
+// for qzeros, where word j of a group row holds outputs 8j..8j+7).
+void orc_gptq_unpack_row(const int32_t * qweight, const int32_t * qzeros, int rows, int cols, int group,
+                         int zero_add, int row, uint8_t * codes, uint8_t * zeros) {
+    for (int k = 0; k < cols; k++) {
+        const uint32_t w = (uint32_t) qweight[(size_t) (k / 8) * rows + row];
+        codes[k] = (uint8_t) ((w >> (4 * (k % 8))) & 15u);
+    }
+    for (int g = 0; g < cols / group; g++) {
+        const uint32_t z = (uint32_t) qzeros[(size_t) g * (rows / 8) + row / 8];
+        zeros[g] = (uint8_t) (((z >> (4 * (row % 8))) & 15u) + (uint32_t) zero_add);
+    }
+}
+
+// tooling/sml_unpack.py:84-95 (dequant_gptq): (w - z[g]).float() * scales[g]
+void orc_gptq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows,
+                          int cols, int group, int zero_add, int row, float * out) {
+    uint8_t * c = malloc((size_t) cols), * z = malloc((size_t) (cols / group));
+    orc_gptq_unpack_row(qweight, qzeros, rows, cols, group, zero_add, row, c, z);
+    for (int k = 0; k < cols; k++) {
+        const int g = k / group;
+        out[k] = (float) ((int) c[k] - (int) z[g]) * orc_f16_to_f32(scales[(size_t) g * rows + row]);
+    }
+    free(c);
+    free(z);
+}
+
+void orc_gptq_matvec(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows, int cols,
+                     int group, int zero_add, const float * x, float * y) {
+    #pragma omp parallel
+    {
+        float * w = malloc((size_t) cols * 4);
+        #pragma omp for schedule(static)
+        for (int r = 0; r < rows; r++) {
+            orc_gptq_dequant_row(qweight, qzeros, scales, rows, cols, group, zero_add, r, w);
+            double acc = 0.0;
+            for (int k = 0; k < cols; k++) acc += (double) w[k] * (double) x[k];
+            y[r] = (float) acc;
+        }
+        free(w);
+    }
+}
+
 // ------------------------------------------------------------ decoder
 
 // The oracle reads the file with its own parser: offsets of the packed

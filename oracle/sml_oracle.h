@@ -87,6 +87,21 @@ void orc_router(const float * router, const float * x, int ne, int n_embd, float
 // First-max greedy pick. follows sml/sml-run.c:3539-3544
 int orc_argmax(const float * logits, int n);
 
+// GPTQ-style 4-bit (tooling/sml_unpack.py:66-95): qweight int32 [cols/8][rows]
+// (8 codes along the input, lowest nibble first), qzeros int32
+// [cols/group][rows/8] (8 zero codes along the output), scales fp16
+// [cols/group][rows]; zero = stored + zero_add (1 for the v1 files);
+// g = input // group (identity g_idx).
+// Codes (cols) and zeros (cols/group) of one output row.
+void orc_gptq_unpack_row(const int32_t * qweight, const int32_t * qzeros, int rows, int cols, int group,
+                         int zero_add, int row, uint8_t * codes, uint8_t * zeros);
+// Weights of one output row: (float) (code - zero) * (float) scale.
+void orc_gptq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows,
+                          int cols, int group, int zero_add, int row, float * out);
+// y = W.x with the dequantized weights, summed in double.
+void orc_gptq_matvec(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows, int cols,
+                     int group, int zero_add, const float * x, float * y);
+
 // ---------------------------------------------------------------- decoder
 // A whole decode step over an SSF file (Llama / Qwen2 / Mixtral family: RMSNorm,
 // halved RoPE, GQA, SwiGLU, optional q/k/v bias, tied or untied head, top-k MoE).

@@ -68,6 +68,12 @@ _SIGS = [
     ("sml_hip_unpack", c_int, [c_void_p, c_int, c_int, c_void_p]),
     ("sml_hip_time_read", c_int, [P(c_void_p), c_int, c_size_t, c_int, c_int, P(c_float)]),
     ("sml_hip_copy", c_int, [c_void_p, c_void_p, c_size_t]),
+    ("sml_hip_gptq_upload", c_void_p, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int]),
+    ("sml_hip_gptq_free", None, [c_void_p]),
+    ("sml_hip_gptq_bytes", c_size_t, [c_void_p]),
+    ("sml_hip_gptq_matvec", c_int, [c_void_p, c_void_p, c_void_p]),
+    ("sml_hip_gptq_unpack", c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    ("sml_hip_gptq_time", c_int, [P(c_void_p), c_int, c_void_p, c_void_p, c_int, P(c_float)]),
     ("sml_hip_embed", c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
     ("sml_hip_attn_part_floats", c_size_t, [c_int, c_int, c_int]),
     ("sml_hip_attention", c_int, [c_void_p] * 8 + [c_int] * 4 + [c_void_p, c_void_p]),

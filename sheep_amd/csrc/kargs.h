@@ -154,3 +154,28 @@ typedef struct {
     uint8_t * dst;
     uint64_t bytes;
 } sml_kcopy;
+
+// GPTQ-style 4-bit matrix (rows = outputs, cols = inputs, groups of 128
+// inputs, identity g_idx): qweight [cols/8][rows] int32 with 8 codes along
+// the input, lowest nibble first; qzeros [cols/128][rows/8] int32 with 8
+// zero codes along the output; scales [cols/128][rows] fp16.
+typedef struct {
+    const uint32_t * qweight;
+    const uint32_t * qzeros;
+    const uint16_t * scales;
+    const float    * x;           // fp32 input, cols
+    float          * part;        // [nslice][rows] partial sums (8 groups each)
+    float          * y;           // rows
+    int rows, cols;
+    int zero_add;                 // added to the stored zero: 1 for the v1 files, 0 for v2
+    int nslice;                   // cols / 1024 rounded up
+} sml_kgptq;
+
+typedef struct {
+    const uint32_t * qweight;
+    const uint32_t * qzeros;
+    int rows, cols, zero_add;
+    int row0, nrows;
+    uint8_t * codes;              // [nrows][cols]
+    uint8_t * zeros;              // [nrows][cols/128], stored zero + zero_add
+} sml_kgptq_unpack;

@@ -976,3 +976,110 @@ extern "C" __global__ __launch_bounds__(256) void sml_copy_stream(const sml_kcop
     for (uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x; i < nw; i += (uint64_t) gridDim.x * 256)
         d[i] = __builtin_nontemporal_load(s + i);
 }
+
+// ---------------------------------------------------------------- GPTQ-style 4-bit GEMV
+//
+// The layout of tooling/sml_unpack.py:66-95 (dequant_gptq): weight
+// (q - z) * s with q packed 8 per int32 along the input. Consecutive outputs
+// are contiguous there, so a lane loads 16 bytes = 4 outputs x 8 inputs and
+// a wave streams 256 outputs of one group of 128 inputs (16 loads per lane,
+// all issued before any use). The activation stays fp32, staged per wave
+// in LDS and read as broadcasts: per group, s * (sum q*x - z * sum x). The GPTQ_WAVES waves of a workgroup cover
+// consecutive groups, summed in LDS into one partial per output;
+// sml_gptq_reduce adds the partials in a fixed order.
+#define GPTQ_WAVES 8
+extern "C" __global__ __launch_bounds__(64 * GPTQ_WAVES) void sml_gptq_gemv(const sml_kgptq a) {
+    __shared__ float xs[GPTQ_WAVES][128];
+    __shared__ float red[GPTQ_WAVES][256];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ngr = a.cols / 128;
+    const int g = blockIdx.y * GPTQ_WAVES + w;
+    const bool gv = g < ngr;
+    const int o = blockIdx.x * 256 + lane * 4;
+    const bool ov = o < a.rows;
+    const int gc = gv ? g : 0, oc = ov ? o : 0;
+    const float * xg = a.x + (size_t) gc * 128;
+    // 1. this group's inputs (two per lane, for their sum), every weight word,
+    // then the group fields
+    const float2 xv = ((const float2 *) xg)[lane];
+    v4u q[16];
+    #pragma unroll
+    for (int kk = 0; kk < 16; kk++)
+        q[kk] = __builtin_nontemporal_load((const v4u *) (a.qweight + ((size_t) gc * 16 + kk) * a.rows + oc));
+    const v2u sc = *(const v2u *) (a.scales + (size_t) gc * a.rows + oc);
+    const uint32_t zw = a.qzeros[(size_t) gc * (a.rows / 8) + oc / 8];
+    xs[w][2 * lane] = xv.x;
+    xs[w][2 * lane + 1] = xv.y;
+    const float sx = wave_sum(xv.x + xv.y);
+    __syncthreads();
+    // 2. sum q*x per output: the low and high nibbles of each byte are
+    // inputs 2i and 2i+1 of the word's 8
+    float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+    #pragma unroll
+    for (int kk = 0; kk < 16; kk++) {
+        const float4 x0 = *(const float4 *) &xs[w][kk * 8], x1 = *(const float4 *) &xs[w][kk * 8 + 4];
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t wd = q[kk][j], lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+            float t = acc[j];
+            t = fmaf((float) (lo & 0xFFu), x0.x, t);
+            t = fmaf((float) (hi & 0xFFu), x0.y, t);
+            t = fmaf((float) ((lo >> 8) & 0xFFu), x0.z, t);
+            t = fmaf((float) ((hi >> 8) & 0xFFu), x0.w, t);
+            t = fmaf((float) ((lo >> 16) & 0xFFu), x1.x, t);
+            t = fmaf((float) ((hi >> 16) & 0xFFu), x1.y, t);
+            t = fmaf((float) (lo >> 24), x1.z, t);
+            t = fmaf((float) (hi >> 24), x1.w, t);
+            acc[j] = t;
+        }
+    }
+    // 3. the group epilogue and the workgroup's sum over its groups
+    #pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float s = h2f((uint16_t) ((j < 2 ? sc.x : sc.y) >> (16 * (j & 1))));
+        const float z = (float) (((zw >> (4 * ((oc & 7) + j))) & 15u) + (uint32_t) a.zero_add);
+        red[w][lane * 4 + j] = gv ? s * (acc[j] - z * sx) : 0.0f;
+    }
+    __syncthreads();
+    if (tid < 64 && ov) {
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float v = red[0][lane * 4 + j];
+            #pragma unroll
+            for (int k = 1; k < GPTQ_WAVES; k++) v += red[k][lane * 4 + j];
+            a.part[(size_t) blockIdx.y * a.rows + o + j] = v;
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void sml_gptq_reduce(const sml_kgptq a) {
+    const int o = blockIdx.x * 256 + threadIdx.x;
+    if (o >= a.rows) return;
+    float p[8];
+    float v = 0.0f;
+    for (int s0 = 0; s0 < a.nslice; s0 += 8) {
+        #pragma unroll
+        for (int k = 0; k < 8; k++) p[k] = s0 + k < a.nslice ? a.part[(size_t) (s0 + k) * a.rows + o] : 0.0f;
+        #pragma unroll
+        for (int k = 0; k < 8; k++) v += p[k];
+    }
+    a.y[o] = v;
+}
+
+// Integer codes and zeros of rows [row0, row0+nrows): one thread per (row, 8 inputs).
+extern "C" __global__ void sml_gptq_unpack(const sml_kgptq_unpack a) {
+    const long t = (long) blockIdx.x * blockDim.x + threadIdx.x;
+    const int nk = a.cols / 8;
+    if (t >= (long) a.nrows * nk) return;
+    const int r = (int) (t / nk), kk = (int) (t % nk), o = a.row0 + r;
+    const uint32_t wd = a.qweight[(size_t) kk * a.rows + o];
+    uint8_t * c = a.codes + (size_t) r * a.cols + (size_t) kk * 8;
+    #pragma unroll
+    for (int i = 0; i < 8; i++) c[i] = (uint8_t) ((wd >> (4 * i)) & 15u);
+    if ((kk & 15) == 0) {
+        const int g = kk / 16;
+        const uint32_t zw = a.qzeros[(size_t) g * (a.rows / 8) + o / 8];
+        a.zeros[(size_t) r * (a.cols / 128) + g] = (uint8_t) (((zw >> (4 * (o & 7))) & 15u) + (uint32_t) a.zero_add);
+    }
+}

@@ -537,3 +537,109 @@ int sml_hip_time_read(const void * const * bufs, int nbuf, size_t bytes, int gri
     HX_LEAVE();
     return 0;
 }
+
+// ------------------------------------------------------------ GPTQ-style 4-bit
+
+#define GPTQ_GROUPS_PER_WG 8     // waves (one group of 128 inputs each) per sml_gptq_gemv workgroup
+
+struct sml_hip_gptq {
+    uint32_t * qweight, * qzeros;
+    uint16_t * scales;
+    float * part;
+    int rows, cols, zero_add;
+    size_t bytes;
+};
+
+sml_hip_gptq * sml_hip_gptq_upload(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                                   int rows, int cols, int group, int zero_add) {
+    OP_BEGIN(NULL);
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 128 || group != 128 || zero_add < 0 || zero_add > 1)
+        hx_failf("GPTQ matrix %dx%d group %d: rows must be a multiple of 8, cols of 128, group 128", rows, cols, group);
+    sml_hip_gptq * m = calloc(1, sizeof *m);
+    if (!m) hx_failf("out of host memory");
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) {
+        hx.jb = outer;
+        hipFree(m->qweight); hipFree(m->qzeros); hipFree(m->scales); hipFree(m->part);
+        free(m);
+        longjmp(*outer, 1);
+    }
+    hx.jb = &jb;
+    const size_t R = (size_t) rows, ng = (size_t) cols / 128, nslice = (ng + GPTQ_GROUPS_PER_WG - 1) / GPTQ_GROUPS_PER_WG;
+    const size_t bw = (size_t) cols / 8 * R * 4, bz = ng * (R / 8) * 4, bs = ng * R * 2;
+    m->qweight = hx_malloc(bw);
+    m->qzeros = hx_malloc(bz);
+    m->scales = hx_malloc(bs);
+    m->part = hx_malloc(nslice * R * 4);
+    HX(hipMemcpy(m->qweight, qweight, bw, hipMemcpyHostToDevice));
+    HX(hipMemcpy(m->qzeros, qzeros, bz, hipMemcpyHostToDevice));
+    HX(hipMemcpy(m->scales, scales, bs, hipMemcpyHostToDevice));
+    hx.jb = outer;
+    m->rows = rows; m->cols = cols; m->zero_add = zero_add;
+    m->bytes = bw + bz + bs;
+    HX_LEAVE();
+    return m;
+}
+
+void sml_hip_gptq_free(sml_hip_gptq * m) {
+    HX_ENTRY();
+    if (m) {
+        HX(hipFree(m->qweight)); HX(hipFree(m->qzeros)); HX(hipFree(m->scales)); HX(hipFree(m->part));
+        free(m);
+    }
+    HX_LEAVE();
+}
+
+size_t sml_hip_gptq_bytes(const sml_hip_gptq * m) { return m ? m->bytes : 0; }
+
+static void op_gptq(hipStream_t st, const sml_hip_gptq * m, const float * x, float * y) {
+    sml_kgptq a;
+    memset(&a, 0, sizeof a);
+    a.qweight = m->qweight; a.qzeros = m->qzeros; a.scales = m->scales;
+    a.x = x; a.part = m->part; a.y = y;
+    a.rows = m->rows; a.cols = m->cols; a.zero_add = m->zero_add;
+    a.nslice = (m->cols / 128 + GPTQ_GROUPS_PER_WG - 1) / GPTQ_GROUPS_PER_WG;
+    hx_launch("sml_gptq_gemv", (unsigned) ((m->rows + 255) / 256), (unsigned) a.nslice, 64 * GPTQ_GROUPS_PER_WG, 0, st, &a);
+    hx_launch("sml_gptq_reduce", (unsigned) ((m->rows + 255) / 256), 1, 256, 0, st, &a);
+}
+
+int sml_hip_gptq_matvec(const sml_hip_gptq * m, const float * x, float * y) {
+    OP_BEGIN(-1);
+    if (!m || !x || !y) hx_failf("gptq_matvec arguments");
+    op_gptq(0, m, x, y);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_gptq_unpack(const sml_hip_gptq * m, int row0, int nrows, uint8_t * codes, uint8_t * zeros) {
+    OP_BEGIN(-1);
+    if (!m || row0 < 0 || nrows <= 0 || row0 + nrows > m->rows) hx_failf("gptq_unpack rows out of range");
+    sml_kgptq_unpack a;
+    memset(&a, 0, sizeof a);
+    a.qweight = m->qweight; a.qzeros = m->qzeros;
+    a.rows = m->rows; a.cols = m->cols; a.zero_add = m->zero_add;
+    a.row0 = row0; a.nrows = nrows; a.codes = codes; a.zeros = zeros;
+    const long n = (long) nrows * (m->cols / 8);
+    hx_launch("sml_gptq_unpack", (unsigned) ((n + 255) / 256), 1, 256, 0, 0, &a);
+    HX(hipStreamSynchronize(0));
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_gptq_time(const sml_hip_gptq * const * mats, int ncopy, const float * x, float * y, int iters,
+                      float * ms_total) {
+    OP_BEGIN(-1);
+    hipEvent_t e0, e1;
+    HX(hipEventCreate(&e0));
+    HX(hipEventCreate(&e1));
+    HX(hipEventRecord(e0, 0));
+    for (int i = 0; i < iters; i++) op_gptq(0, mats[i % ncopy], x, y);
+    HX(hipEventRecord(e1, 0));
+    HX(hipEventSynchronize(e1));
+    HX(hipEventElapsedTime(ms_total, e0, e1));
+    HX(hipEventDestroy(e0));
+    HX(hipEventDestroy(e1));
+    HX_LEAVE();
+    return 0;
+}

@@ -309,3 +309,31 @@ def test_copy_calibration_kernel():
         out = d.read(np.uint8)
         assert np.array_equal(out[:n], src[:n]) and not out[n:].any()
     assert sa.lib().sml_hip_copy(d.ptr, s.ptr, 17) == -1
+
+
+# ------------------------------------------------------------ GPTQ-style 4-bit
+
+@pytest.mark.parametrize("rows,cols", [(256, 1024), (1000, 1152), (4096, 14336), (14336, 4096)])
+def test_gptq_gemv(rows, cols):
+    from sheep_amd import gptq as gq
+    qw, qz, sc = gq.synth(rows, cols, seed=rows + cols)
+    m = gq.GptqMat(qw, qz, sc, rows, cols)
+    x = np.random.default_rng(cols).standard_normal(cols).astype(np.float32)
+    y = sa.DevBuf(rows * 4)
+    m.matvec(sa.DevBuf.of(x), y)
+    close(y.read(np.float32), ob.gptq_matvec(qw, qz, sc, rows, cols, x), f"gptq {rows}x{cols}")
+
+
+@pytest.mark.parametrize("rows,cols,zero_add", [(4096, 14336, 1), (1000, 1152, 0)])
+def test_gptq_unpack_bitexact(rows, cols, zero_add):
+    from sheep_amd import gptq as gq
+    qw, qz, sc = gq.synth(rows, cols, seed=7 + rows)
+    rng = np.random.default_rng(rows)
+    qz = rng.integers(0, 1 << 32, qz.shape, dtype=np.uint64).astype(np.uint32).view(np.int32)
+    m = gq.GptqMat(qw, qz, sc, rows, cols, zero_add=zero_add)
+    for r0, n in ((0, 8), (rows - 5, 5), (rows // 2, 3)):
+        c, z = m.unpack(r0, n)
+        for i in range(n):
+            wc, wz = ob.gptq_unpack_row(qw, qz, rows, cols, r0 + i, zero_add=zero_add)
+            np.testing.assert_array_equal(c[i], wc)
+            np.testing.assert_array_equal(z[i], wz)

@@ -293,3 +293,45 @@ def test_decoder_layers_match_reference(tmpdir_s, monkeypatch):
     for a, b in zip(A, B):
         assert np.abs(a - b).max() <= 1e-2 * np.abs(b).max()
         assert np.corrcoef(a, b)[0, 1] > 0.9999
+
+
+# ------------------------------------------------------------ GPTQ-style 4-bit
+
+def test_gptq_packing_bit_order():
+    """The documented AutoGPTQ layout (tooling/sml_unpack.py:66-76): input 8k+i
+    of output o in bits 4i..4i+3 of qweight[k, o]; output 8j+i's zero in bits
+    4i..4i+3 of qzeros[g, j]; v1 stores zero - 1."""
+    from sheep_amd import gptq as gq
+    codes = np.zeros((8, 128), np.uint8)
+    codes[0, :8] = np.arange(8)
+    zeros = np.arange(1, 9).reshape(8, 1)
+    qw, qz, _ = gq.pack(codes, zeros, np.ones((8, 1)), zero_add=1)
+    assert qw.view(np.uint32)[0, 0] == 0x76543210 and not qw.view(np.uint32)[1:, 0].any()
+    assert qz.view(np.uint32)[0, 0] == 0x76543210
+    c, z = ob.gptq_unpack_row(qw, qz, 8, 128, 0)
+    assert list(c[:8]) == list(range(8)) and not c[8:].any() and z[0] == 1
+
+
+@pytest.mark.parametrize("zero_add", [1, 0])
+def test_gptq_known_answer(zero_add):
+    """The known answer of mlmi/tests/test_unpack.py:74-103 restated: 64 inputs x
+    32 outputs, group 16, codes 0..15, zeros 1..15, fp16 scales in [0.1, 1.1);
+    unpacking the packed arrays gives (q - z) * s exactly (max |diff| 0.0)."""
+    from sheep_amd import gptq as gq
+    rng = np.random.default_rng(0)
+    IN, OUT, GS = 64, 32, 16
+    q = rng.integers(0, 16, (OUT, IN))
+    z = rng.integers(1, 16, (OUT, IN // GS))
+    s = (rng.random((OUT, IN // GS)) + 0.1).astype(np.float16)
+    qw, qz, sc = gq.pack(q, z, s, zero_add=zero_add)
+    W = np.zeros((OUT, IN), np.float32)
+    for o in range(OUT):
+        c, zz = ob.gptq_unpack_row(qw, qz, OUT, IN, o, group=GS, zero_add=zero_add)
+        np.testing.assert_array_equal(c, q[o])
+        np.testing.assert_array_equal(zz, z[o])
+        W[o] = ob.gptq_dequant_row(qw, qz, sc, OUT, IN, o, group=GS, zero_add=zero_add)
+    want = (q - np.repeat(z, GS, axis=1)).astype(np.float32) * np.repeat(s.astype(np.float32), GS, axis=1)
+    assert np.abs(W - want).max() == 0.0
+    x = rng.standard_normal(IN).astype(np.float32)
+    y = ob.gptq_matvec(qw, qz, sc, OUT, IN, x, group=GS, zero_add=zero_add)
+    np.testing.assert_allclose(y, (want.astype(np.float64) @ x.astype(np.float64)).astype(np.float32), rtol=1e-6, atol=1e-6)
