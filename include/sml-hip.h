@@ -95,6 +95,41 @@ int sml_hip_time_read(const void * const * bufs, int nbuf, size_t bytes, int gri
 // read and write counters give the scale for the GEMV's counter readings.
 int sml_hip_copy(void * dst, const void * src, size_t bytes);
 
+// ------------------------------------------------------------ small-M GEMM
+// y[r] = W.a[r] for nrow (1..16) activation rows a[r] (q [nrow][cols], scale
+// and sums [nrow][cols/32]) into y [nrow][rows]: each weight streams once for
+// all rows. replaces sml_matvec_batch_flat4 / batch_group for the exact
+// per-32 regime (sml/sml-kernel.c:1008-1021, sml/sml-run.c:2058-2183)
+int sml_hip_gemm(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
+                 float * y);
+// h[r] = silu(gate.a[r]) * (up.a[r]) for nrow rows, h [nrow][gate rows]
+// (the batched gate/up of moe_expert_batch, sml/sml-run.c:3166-3185)
+int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q, const float * scale,
+                        const int32_t * sums, int nrow, float * h);
+
+// ------------------------------------------------------------ MoE expert FFN
+// One MoE FFN layer resident in HBM: the f32 router (and bias) and every
+// expert's gate/up/down of record blk.<layer>.ffn_{gate,up,down}.<e>.weight,
+// for up to max_tokens (1..16) tokens per call. Routing modes: top-k with
+// softmax over the chosen (moe_flags bit 0, Mixtral/Granite) or over all
+// experts; other modes, shared experts and expert biases are refused.
+// replaces the expert weights of sml_load_layers (sml/sml-run.c:1676-1745)
+typedef struct sml_hip_moe sml_hip_moe;
+sml_hip_moe * sml_hip_moe_from_file(const char * path, int layer, int max_tokens);
+void          sml_hip_moe_free(sml_hip_moe * m);
+int           sml_hip_moe_info(const sml_hip_moe * m, int * nexp, int * k, int * n_ff, size_t * expert_bytes);
+// out[t] = sum over the chosen experts j of w[t][j] * FFN_e(x[t]) for T tokens
+// of normed input x [T][n_embd]: the router in double (sml/sml-run.c:3075-3080),
+// sml_moe_route's choice (sml/sml-run.c:2925-3037), each chosen expert's
+// weights read once for all tokens that chose it (moe_ffn_batch,
+// sml/sml-run.c:3189-3241), outputs added in choice order. sel/w ([T][k])
+// and logits ([T][nexp]) receive the routing when not NULL. Device pointers.
+int sml_hip_moe_ffn(sml_hip_moe * m, const float * x, int T, float * out, int32_t * sel, float * w, float * logits);
+// Time `iters` calls (HIP events); count_out (host, nexp) gets the tokens per
+// expert of the last call when not NULL.
+int sml_hip_moe_time(sml_hip_moe * m, const float * x, int T, float * out, int iters, float * ms_total,
+                     int32_t * count_out);
+
 // ------------------------------------------------------------ GPTQ-style 4-bit
 // A GPTQ (AutoGPTQ / optimum) 4-bit matrix resident in HBM as its own three
 // arrays, rows = outputs, cols = inputs: qweight int32 [cols/8][rows] (8 codes

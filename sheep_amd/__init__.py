@@ -68,6 +68,13 @@ _SIGS = [
     ("sml_hip_unpack", c_int, [c_void_p, c_int, c_int, c_void_p]),
     ("sml_hip_time_read", c_int, [P(c_void_p), c_int, c_size_t, c_int, c_int, P(c_float)]),
     ("sml_hip_copy", c_int, [c_void_p, c_void_p, c_size_t]),
+    ("sml_hip_gemm", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    ("sml_hip_gemm_swiglu", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    ("sml_hip_moe_from_file", c_void_p, [c_char_p, c_int, c_int]),
+    ("sml_hip_moe_free", None, [c_void_p]),
+    ("sml_hip_moe_info", c_int, [c_void_p, P(c_int), P(c_int), P(c_int), P(c_size_t)]),
+    ("sml_hip_moe_ffn", c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("sml_hip_moe_time", c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, P(c_float), c_void_p]),
     ("sml_hip_gptq_upload", c_void_p, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int]),
     ("sml_hip_gptq_free", None, [c_void_p]),
     ("sml_hip_gptq_bytes", c_size_t, [c_void_p]),
@@ -298,3 +305,46 @@ class Decoder:
 
     def close(self):
         lib().sml_gpu_close()
+
+
+class MoE:
+    """One MoE FFN layer of an SSF file resident in HBM (sml_hip_moe_*)."""
+
+    def __init__(self, path, layer=0, max_tokens=16):
+        h = lib().sml_hip_moe_from_file(str(path).encode(), layer, max_tokens)
+        if not h:
+            raise HipError(f"moe: {lib().sml_hip_last_error().decode(errors='replace')}")
+        self.h = h
+        ne, k, nf, eb = c_int(), c_int(), c_int(), c_size_t()
+        lib().sml_hip_moe_info(h, ctypes.byref(ne), ctypes.byref(k), ctypes.byref(nf), ctypes.byref(eb))
+        self.nexp, self.k, self.n_ff, self.expert_bytes = ne.value, k.value, nf.value, eb.value
+
+    def ffn(self, x, T, out, sel=None, w=None, logits=None):
+        _chk(lib().sml_hip_moe_ffn(self.h, x.ptr, T, out.ptr, sel.ptr if sel else None, w.ptr if w else None,
+                                   logits.ptr if logits else None), "moe_ffn")
+
+    def time(self, x, T, out, iters):
+        ms = c_float()
+        cnt = np.zeros(self.nexp, np.int32)
+        _chk(lib().sml_hip_moe_time(self.h, x.ptr, T, out.ptr, iters, ctypes.byref(ms), cnt.ctypes.data), "moe_time")
+        return ms.value, cnt
+
+    def free(self):
+        if self.h:
+            lib().sml_hip_moe_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def gemm(m, act_q, act_s, act_u, nrow, y):
+    """y [nrow][rows] = W . a[r] for nrow activation rows (device buffers)."""
+    _chk(lib().sml_hip_gemm(m.h, act_q.ptr, act_s.ptr, act_u.ptr, nrow, y.ptr), "gemm")
+
+
+def gemm_swiglu(gate, up, act_q, act_s, act_u, nrow, h):
+    _chk(lib().sml_hip_gemm_swiglu(gate.h, up.h, act_q.ptr, act_s.ptr, act_u.ptr, nrow, h.ptr), "gemm_swiglu")

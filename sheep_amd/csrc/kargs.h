@@ -179,3 +179,63 @@ typedef struct {
     uint8_t * codes;              // [nrows][cols]
     uint8_t * zeros;              // [nrows][cols/128], stored zero + zero_add
 } sml_kgptq_unpack;
+
+// ------------------------------------------------------------ MoE and small-M GEMM
+
+// Router, top-k routing and the per-expert token lists for T tokens (one
+// workgroup).
+typedef struct {
+    const float   * x;            // [T][n] normed inputs of the expert FFN
+    const float   * router;       // [nexp][n]
+    const float   * router_b;     // [nexp] or NULL
+    int T, n, nexp, k, mmax;
+    unsigned moe_flags;
+    float   * logits;             // [T][nexp]
+    int32_t * sel;                // [T][k] chosen experts, in choice order
+    float   * w;                  // [T][k] their weights
+    int32_t * slot;               // [T][k] position of (t, j) in its expert's list
+    int32_t * count;              // [nexp] tokens per expert
+    int32_t * list;               // [nexp][mmax] entries t*k + j, by token then choice
+} sml_kmoe_route;
+
+// Per-32 int8 quantization of activation rows into per-expert slots:
+// mode 0 gathers row list[e][r] / k of x [T][n]; mode 1 takes row (e, r) of
+// src [nexp][mmax][n]. perms: device table of nexp permutations (NULL entries
+// or a NULL table: identity).
+typedef struct {
+    const float   * src;
+    int mode;
+    const int32_t * const * perms;
+    int n, mmax, k;
+    const int32_t * count;
+    const int32_t * list;
+    int8_t * q;                   // [nexp][mmax][n]
+    float * scale;                // [nexp][mmax][n/32]
+    int32_t * sums;
+} sml_kmquant;
+
+// Small-M GEMM over groups of matrices (one per expert, or a single one):
+// for group e and its count[e] (or m_all) activation rows, y[e][r] = W_e.a[e][r]
+// (SwiGLU: silu(gate.a) * (up.a)). Each group's weights stream once for all
+// its rows.
+typedef struct {
+    const sml_kmat * mats;        // device table: group e's matrices at [e * nmat + i]
+    int nmat;                     // 1, or 2 for SwiGLU (gate, up)
+    int cols, rows;               // per matrix
+    const int32_t * count;        // [ngroups] or NULL
+    int m_all;
+    int mmax;                     // activation / output slots per group
+    const int8_t  * q;            // [ngroups][mmax][cols]
+    const float   * scale;        // [ngroups][mmax][cols/32]
+    const int32_t * sums;
+    float * y;                    // [ngroups][mmax][rows]
+} sml_kgemm;
+
+// out[t] = sum over j of w[t][j] * y[sel[t][j]][slot[t][j]], in choice order.
+typedef struct {
+    const float   * y;            // [nexp][mmax][n]
+    const int32_t * sel, * slot;
+    const float   * w;
+    int T, n, k, mmax;
+    float * out;                  // [T][n]
+} sml_kmoe_comb;

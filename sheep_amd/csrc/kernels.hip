@@ -1083,3 +1083,280 @@ extern "C" __global__ void sml_gptq_unpack(const sml_kgptq_unpack a) {
         a.zeros[(size_t) r * (a.cols / 128) + g] = (uint8_t) (((zw >> (4 * (o & 7))) & 15u) + (uint32_t) a.zero_add);
     }
 }
+
+// ---------------------------------------------------------------- MoE: route and plan
+//
+// sml_moe_route, one workgroup per token: the router logits
+// (sml/sml-run.c:3075-3080: a double sum per expert, then (float) + bias),
+// one wave per expert at a time; then the top-k choice with ties to the
+// lower index and the Mixtral / Granite weights (moe_flags bit 0: softmax
+// over the chosen; else softmax over all, sml/sml-run.c:3017-3034).
+// sml_moe_plan then lists each expert's tokens in token-then-choice order,
+// the order moe_ffn_batch gathers them in (sml/sml-run.c:3211-3219).
+#define MOE_ROUTE_THREADS 512
+extern "C" __global__ __launch_bounds__(MOE_ROUTE_THREADS) void sml_moe_route(const sml_kmoe_route a) {
+    __shared__ float lg[64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, t = blockIdx.x;
+    const float * x = a.x + (size_t) t * a.n;
+    for (int e = wv; e < a.nexp; e += MOE_ROUTE_THREADS / 64) {
+        const float * r = a.router + (size_t) e * a.n;
+        double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+        int i = lane * 4;
+        for (; i + 3 < a.n; i += 256) {
+            const float4 rv = *(const float4 *) (r + i), xv = *(const float4 *) (x + i);
+            s0 += (double) rv.x * (double) xv.x;
+            s1 += (double) rv.y * (double) xv.y;
+            s2 += (double) rv.z * (double) xv.z;
+            s3 += (double) rv.w * (double) xv.w;
+        }
+        double s = (s0 + s1) + (s2 + s3);
+        #pragma unroll
+        for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
+        if (lane == 0) {
+            const float v = (float) s + (a.router_b ? a.router_b[e] : 0.0f);
+            lg[e] = v;
+            a.logits[(size_t) t * a.nexp + e] = v;
+        }
+    }
+    __syncthreads();
+    if (tid != 0) return;
+    int32_t * sel = a.sel + t * a.k;
+    float * w = a.w + t * a.k;
+    int sl[16];
+    for (int j = 0; j < a.k; j++) {
+        int best = -1;
+        for (int e = 0; e < a.nexp; e++) {
+            bool taken = false;
+            for (int q = 0; q < j; q++) taken = taken || sl[q] == e;
+            if (!taken && (best < 0 || lg[e] > lg[best])) best = e;
+        }
+        sl[j] = best;
+        sel[j] = best;
+    }
+    if (a.moe_flags & 1u) {
+        float wj[16];
+        double sum = 0.0;
+        for (int j = 0; j < a.k; j++) { wj[j] = expf(lg[sl[j]] - lg[sl[0]]); sum += wj[j]; }
+        for (int j = 0; j < a.k; j++) w[j] = (float) (wj[j] / sum);
+    } else {
+        float mx = lg[0];
+        for (int e = 1; e < a.nexp; e++) mx = lg[e] > mx ? lg[e] : mx;
+        double sum = 0.0;
+        for (int e = 0; e < a.nexp; e++) sum += expf(lg[e] - mx);
+        for (int j = 0; j < a.k; j++) w[j] = (float) (expf(lg[sl[j]] - mx) / sum);
+    }
+}
+
+// one thread per expert scans the choices (staged in LDS) in order
+extern "C" __global__ __launch_bounds__(64) void sml_moe_plan(const sml_kmoe_route a) {
+    __shared__ int32_t sel[16 * 16];                  // T * k <= 256
+    const int nk = a.T * a.k;
+    for (int i = threadIdx.x; i < nk; i += 64) sel[i] = a.sel[i];
+    __syncthreads();
+    const int e = threadIdx.x;
+    if (e >= a.nexp) return;
+    int m = 0;
+    for (int i = 0; i < nk; i++)
+        if (sel[i] == e) {
+            a.list[e * a.mmax + m] = i;
+            a.slot[i] = m;
+            m++;
+        }
+    a.count[e] = m;
+}
+
+// Per-32 quantization of one activation row per workgroup (grid mmax x nexp),
+// the normq arithmetic (bit-exact with sml_quantize_act): a thread takes 4
+// consecutive values, 8 threads a group.
+#define MOE_QUANT_THREADS 1024
+extern "C" __global__ __launch_bounds__(MOE_QUANT_THREADS) void sml_moe_quant(const sml_kmquant a) {
+    const int r = blockIdx.x, e = blockIdx.y;
+    if (r >= a.count[e]) return;
+    const int n = a.n, ng = n / 32;
+    const float * src = a.mode == 0 ? a.src + (size_t) (a.list[e * a.mmax + r] / a.k) * n
+                                    : a.src + ((size_t) e * a.mmax + r) * n;
+    const int32_t * perm = a.perms ? a.perms[e] : nullptr;
+    const size_t slot = (size_t) e * a.mmax + r;
+    for (int f = threadIdx.x; f < n / 4; f += MOE_QUANT_THREADS) {   // whole 8-thread groups stay together
+        float v[4];
+        if (perm) {
+            const int4 p = ((const int4 *) perm)[f];
+            v[0] = src[p.x]; v[1] = src[p.y]; v[2] = src[p.z]; v[3] = src[p.w];
+        } else {
+            const float4 q = ((const float4 *) src)[f];
+            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+        }
+        const float am = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        const float s = am / 127.0f;
+        const float is = s > 0.0f ? 1.0f / s : 0.0f;
+        const int t0 = quant1(v[0], is), t1 = quant1(v[1], is), t2 = quant1(v[2], is), t3 = quant1(v[3], is);
+        const int sum = isum8(t0 + t1 + t2 + t3);
+        ((int *) (a.q + slot * n))[f] = (t0 & 0xFF) | (t1 & 0xFF) << 8 | (t2 & 0xFF) << 16 | (int) ((unsigned) t3 << 24);
+        if ((threadIdx.x & 7) == 0) { a.scale[slot * ng + f / 8] = s; a.sums[slot * ng + f / 8] = sum; }
+    }
+}
+
+// out[t] = sum_j w[t][j] * y[sel][slot] in choice order (sml/sml-run.c:3227-3234)
+extern "C" __global__ __launch_bounds__(256) void sml_moe_combine(const sml_kmoe_comb a) {
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.n) return;
+    float acc = 0.0f;
+    for (int j = 0; j < a.k; j++) {
+        const int e = a.sel[t * a.k + j], r = a.slot[t * a.k + j];
+        acc += a.w[t * a.k + j] * a.y[((size_t) e * a.mmax + r) * a.n + i];
+    }
+    a.out[(size_t) t * a.n + i] = acc;
+}
+
+// ---------------------------------------------------------------- small-M GEMM
+//
+// The GEMV's chunk-per-lane streaming with M activation rows: each weight
+// chunk is unpacked once and dotted with every row's int8 codes from LDS.
+// The input is taken in passes of 64*GEMM_NI chunks (4096 columns); each pass
+// issues its weight loads, then stages that slice of every row's codes and
+// (s, s*sum) pairs in LDS. Group e of the grid's y dimension uses matrix
+// table entry e (an expert) and its own activation slots.
+#define GEMM_NI 2
+template <int NB, int RB, int MT, bool SW>
+__device__ void gemm_body(const sml_kgemm & a) {
+    constexpr int NI = GEMM_NI, TILE = WAVE * NI;
+    extern __shared__ __align__(16) uint8_t lds[];
+    int8_t * lq = (int8_t *) lds;                       // [MT][TILE * 32]
+    float2 * lsc = (float2 *) (lds + MT * TILE * 32);   // [MT][TILE]
+    const int e = blockIdx.y;
+    const int m = a.count ? a.count[e] : a.m_all;
+    if (m <= 0) return;
+    const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1);
+    constexpr int RPW = SW ? RB / 2 : RB;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int row0 = (blockIdx.x * 4 + wave) * RPW;
+    const sml_kmat * mt = a.mats + (size_t) e * (SW ? 2 : 1);
+    const size_t abase = (size_t) e * a.mmax;
+    using P = Planes<NB>;
+    const uint8_t * pl[RB][3];
+    uint32_t ro[RB][3];
+    const uint8_t * fqb[RB];
+    const uint8_t * fdb[RB];
+    uint32_t fqo[RB], fdo[RB];
+    int orow[RB];
+    bool valid[RB];
+    #pragma unroll
+    for (int s = 0; s < RB; s++) {
+        const int grow = row0 + (SW ? (s >> 1) : s);
+        orow[s] = grow;
+        valid[s] = grow < a.rows;
+        const sml_kmat & mm = mt[(SW && (s & 1)) ? 1 : 0];
+        const uint32_t r = (uint32_t) (valid[s] ? grow : 0);
+        pl[s][0] = mm.plane[0]; pl[s][1] = mm.plane[1]; pl[s][2] = mm.plane[2];
+        ro[s][0] = ro[s][1] = ro[s][2] = 0;
+        if constexpr (P::N4) ro[s][P::P4] = r * (uint32_t) P::b4(n);
+        if constexpr (NB == 8) ro[s][1] = r * (uint32_t) P::b4(n);
+        if constexpr (P::N2) ro[s][P::P2] = r * (uint32_t) P::b2(n);
+        if constexpr (P::N1) ro[s][P::P1] = r * (uint32_t) P::b1(n);
+        fqb[s] = mm.sqmq;
+        fdb[s] = (const uint8_t *) mm.sdmd;
+        fqo[s] = r * (uint32_t) ng * 2u;
+        fdo[s] = r * (uint32_t) ns * 4u;
+    }
+    float acc[RB][MT];
+    #pragma unroll
+    for (int s = 0; s < RB; s++)
+        #pragma unroll
+        for (int t = 0; t < MT; t++) acc[s][t] = 0.0f;
+    for (int c0 = 0; c0 < ng; c0 += TILE) {
+        ChunkW<NB> w[NI][RB];
+        uint32_t fqv[NI][RB], fdv[NI][RB];
+        #pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int c = c0 + i * WAVE + lane;
+            const int cl = c < ng ? c : ng - 1;
+            #pragma unroll
+            for (int s = 0; s < RB; s++) {
+                load_chunk<NB, true>(w[i][s], pl[s], ro[s], cl);
+                fqv[i][s] = *(const uint16_t *) (fqb[s] + (fqo[s] + (uint32_t) cl * 2u));
+                fdv[i][s] = *(const uint32_t *) (fdb[s] + (fdo[s] + (uint32_t) (cl >> 3) * 4u));
+            }
+        }
+        // this pass's slice of every activation row into LDS
+        const int tg = ng - c0 < TILE ? ng - c0 : TILE;  // groups in the slice
+        __syncthreads();                                 // the previous pass's reads are done
+        for (int idx = tid; idx < m * tg * 2; idx += 256) {
+            const int t = idx / (tg * 2), wd = idx % (tg * 2);
+            ((v4i *) (lq + t * TILE * 32))[wd] = ((const v4i *) (a.q + (abase + t) * n + (size_t) c0 * 32))[wd];
+        }
+        for (int idx = tid; idx < m * tg; idx += 256) {
+            const int t = idx / tg, g = idx % tg;
+            const size_t fi = (abase + t) * ng + c0 + g;
+            const float sv = a.scale[fi];
+            lsc[t * TILE + g] = make_float2(sv, sv * (float) a.sums[fi]);
+        }
+        __syncthreads();
+        #pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int c = c0 + i * WAVE + lane;
+            const bool live = c < ng;
+            const int cl = (live ? c : ng - 1) - c0;     // index within the slice
+            const int off = 32 * (cl & ~1) + 16 * (cl & 1);
+            const int odd = c & 1;
+            float wsc[RB], wmn[RB];
+            #pragma unroll
+            for (int s = 0; s < RB; s++) {
+                const uint32_t f = fqv[i][s], d2 = fdv[i][s];
+                wsc[s] = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
+                wmn[s] = h2f((uint16_t) (d2 >> 16)) * ((float) (f >> 8) - 127.0f);
+            }
+            #pragma unroll
+            for (int t = 0; t < MT; t++) {
+                if (t < m) {
+                const v4i xa = *(const v4i *) (lq + t * TILE * 32 + off);
+                const v4i xb = *(const v4i *) (lq + t * TILE * 32 + off + 32);
+                float2 sc = lsc[t * TILE + cl];
+                if (!live) sc = make_float2(0.0f, 0.0f);
+                #pragma unroll
+                for (int s = 0; s < RB; s++) {
+                    int da, db;
+                    chunk_dots<NB>(w[i][s], c, xa, xb, da, db);
+                    const int keep = odd ? db : da, send = odd ? da : db;
+                    const int dot = keep + pair_swap(send);
+                    acc[s][t] += wsc[s] * (sc.x * (float) dot);
+                    acc[s][t] += wmn[s] * sc.y;
+                }
+                }
+            }
+        }
+    }
+    #pragma unroll
+    for (int t = 0; t < MT; t++)
+        if (t < m) {
+            #pragma unroll
+            for (int s = 0; s < RB; s++) acc[s][t] = wave_sum_dpp(acc[s][t]);
+        }
+    if (lane != WAVE - 1) return;
+    #pragma unroll
+    for (int t = 0; t < MT; t++) {
+        if (t >= m) continue;
+        float * y = a.y + (abase + t) * a.rows;
+        if constexpr (SW) {
+            #pragma unroll
+            for (int s = 0; s < RB; s += 2) {
+                if (!valid[s]) continue;
+                const float g = acc[s][t], u = acc[s + 1][t];
+                y[orow[s]] = (g / (1.0f + expf(-g))) * u;     // sml/sml-run.c:451-454
+            }
+        } else {
+            #pragma unroll
+            for (int s = 0; s < RB; s++) if (valid[s]) y[orow[s]] = acc[s][t];
+        }
+    }
+}
+
+#define GEMM_KERNEL(NB, MT)                                                                              \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemm_q##NB##_m##MT(const sml_kgemm a) {         \
+        gemm_body<NB, 2, MT, false>(a);                                                                  \
+    }                                                                                                    \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemm_q##NB##_s_m##MT(const sml_kgemm a) {       \
+        gemm_body<NB, 4, MT, true>(a);                                                                   \
+    }
+#define GEMM_WIDTH(NB) GEMM_KERNEL(NB, 1) GEMM_KERNEL(NB, 4) GEMM_KERNEL(NB, 8) GEMM_KERNEL(NB, 16)
+GEMM_WIDTH(2) GEMM_WIDTH(3) GEMM_WIDTH(4) GEMM_WIDTH(5) GEMM_WIDTH(6) GEMM_WIDTH(7) GEMM_WIDTH(8)

@@ -54,11 +54,12 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
     int pb[SSF_MAX_PLANES];
     const int np = ssf_flat_planes(nbits, pb);
     const size_t R = (size_t) rows, ng = (size_t) cols / 32, ns = (size_t) SSF_NSUPER(cols);
-    size_t off[5], sz[5], tot = 0;
+    size_t off[6], sz[6], tot = 0;
     for (int i = 0; i < 3; i++) sz[i] = i < np ? R * ssf_plane_row_bytes(pb[i], cols) : 0;
     sz[3] = R * ng * 2;          // (sq, mq) per group
     sz[4] = R * ns * 4;          // (sd, md) per superblock
-    for (int i = 0; i < 5; i++) { off[i] = tot; tot += al256(sz[i]); }
+    sz[5] = sizeof(sml_kmat);    // the descriptor, for small-M GEMM tables
+    for (int i = 0; i < 6; i++) { off[i] = tot; tot += al256(sz[i]); }
     // the fields interleaved on the host: 8-bit (or widened 6-bit) values, min bias 127
     uint8_t * fq = malloc(sz[3]);
     uint16_t * fd = malloc(sz[4]);
@@ -105,6 +106,8 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
     m->k.rows = rows;
     m->nbits = nbits;
     m->cols = cols;
+    m->kdev = (sml_kmat *) (base + off[5]);
+    HX(hipMemcpy(m->kdev, &m->k, sizeof m->k, hipMemcpyHostToDevice));
     // the bytes a GEMV streams: the file's planes and fields at 8 bits
     m->bytes = sz[0] + sz[1] + sz[2] + R * ng * (mq ? 2 : 1) + R * ns * (md ? 4 : 2);
     return m;
@@ -640,6 +643,307 @@ int sml_hip_gptq_time(const sml_hip_gptq * const * mats, int ncopy, const float 
     HX(hipEventElapsedTime(ms_total, e0, e1));
     HX(hipEventDestroy(e0));
     HX(hipEventDestroy(e1));
+    HX_LEAVE();
+    return 0;
+}
+
+// ------------------------------------------------------------ small-M GEMM
+
+int gemm_mt(int m) { return m <= 1 ? 1 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
+
+#define GEMM_TILE 128            // chunks (groups) per pass: 64 lanes x GEMM_NI
+
+void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
+             const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
+             const int32_t * sums, float * y) {
+    if (mt != 1 && mt != 4 && mt != 8 && mt != 16) hx_failf("small-M GEMM takes at most 16 rows");
+    if (!count && (m_all < 1 || m_all > mt)) hx_failf("small-M GEMM of %d rows", m_all);
+    if ((uint64_t) rows * (uint64_t) cols >= (1ull << 32)) hx_failf("matrix too large for one GEMM launch");
+    sml_kgemm a;
+    memset(&a, 0, sizeof a);
+    a.mats = tab; a.nmat = swiglu ? 2 : 1; a.cols = cols; a.rows = rows;
+    a.count = count; a.m_all = m_all; a.mmax = mmax;
+    a.q = q; a.scale = scale; a.sums = sums; a.y = y;
+    char name[40];
+    snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d", nbits, swiglu ? "_s" : "", mt);
+    const size_t lds = (size_t) mt * GEMM_TILE * (32 + 8);
+    // 4 waves x 2 rows (SwiGLU: 2 gate/up pairs) per workgroup
+    hx_launch(name, (unsigned) ((rows + 7) / 8), (unsigned) ngroups, 256, lds, st, &a);
+}
+
+int sml_hip_gemm(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
+                 float * y) {
+    OP_BEGIN(-1);
+    if (!m || nrow < 1 || nrow > 16) hx_failf("gemm of %d rows (1..16)", nrow);
+    op_gemm(0, m->kdev, 1, 0, m->nbits, m->k.rows, m->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, y);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q, const float * scale,
+                        const int32_t * sums, int nrow, float * h) {
+    OP_BEGIN(-1);
+    if (!gate || !up || nrow < 1 || nrow > 16) hx_failf("gemm of %d rows (1..16)", nrow);
+    if (up->nbits != gate->nbits || up->cols != gate->cols || up->k.rows != gate->k.rows)
+        hx_failf("SwiGLU needs gate and up of one shape and width");
+    sml_kmat tab[2] = { gate->k, up->k };
+    sml_kmat * dt = hx_malloc(sizeof tab);
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) { hx.jb = outer; hipFree(dt); longjmp(*outer, 1); }
+    hx.jb = &jb;
+    HX(hipMemcpy(dt, tab, sizeof tab, hipMemcpyHostToDevice));
+    op_gemm(0, dt, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h);
+    HX(hipStreamSynchronize(0));
+    hx.jb = outer;
+    HX(hipFree(dt));
+    HX_LEAVE();
+    return 0;
+}
+
+// ------------------------------------------------------------ MoE expert FFN
+
+struct sml_hip_moe {
+    int nexp, k, n_embd, n_ff, tmax, nbits;
+    unsigned flags;
+    float * router, * router_b;
+    sml_hip_mat ** mats;          // [nexp][3]: gate, up, down
+    sml_kmat * tab_gu, * tab_d;   // device tables
+    const int32_t ** ptab_gu, ** ptab_d;   // device tables of device permutations, or NULL (identity)
+    void * work;                  // scratch: logits, route, lists, activations, h, expert outputs
+    float * logits, * w, * h, * yd;
+    int32_t * sel, * slot, * count, * list;
+    int8_t * qx, * qh;
+    float * sx, * sh;
+    int32_t * ux, * uh;
+    void * owned[160];            // every device allocation: up to 2 permutations per expert + buffers
+    int nowned;
+    size_t expert_bytes;
+};
+
+static void * moe_own(sml_hip_moe * m, size_t n) {
+    if (m->nowned >= (int) (sizeof m->owned / sizeof m->owned[0])) hx_failf("too many MoE allocations");
+    void * p = hx_malloc(n);
+    m->owned[m->nowned++] = p;
+    return p;
+}
+
+static void moe_release(sml_hip_moe * m) {
+    if (!m) return;
+    if (m->mats) for (int i = 0; i < 3 * m->nexp; i++) if (m->mats[i]) { hipFree(m->mats[i]->mem); free(m->mats[i]); }
+    free(m->mats);
+    for (int i = 0; i < m->nowned; i++) hipFree(m->owned[i]);
+    free(m);
+}
+
+// Upload one permutation (NULL for none or the identity).
+static int32_t * moe_perm(sml_hip_moe * m, const ssf_file * f, const ssf_record * r) {
+    if (!r->perm_bytes) return NULL;
+    const int32_t * p = (const int32_t *) ssf_at(f, r->perm_off);
+    int ident = 1;
+    for (int i = 0; i < (int) r->cols && ident; i++) ident = p[i] == i;
+    if (ident) return NULL;
+    for (int i = 0; i < (int) r->cols; i++) if (p[i] < 0 || p[i] >= (int) r->cols) hx_failf("%.64s: permutation out of range", r->name);
+    int32_t * d = moe_own(m, (size_t) r->cols * 4);
+    HX(hipMemcpy(d, p, (size_t) r->cols * 4, hipMemcpyHostToDevice));
+    return d;
+}
+
+static void moe_setup(sml_hip_moe * m, const ssf_file * f, int L, int tmax) {
+    const ssf_header * h = f->hdr;
+    if (h->moe_flags & ~1u) hx_failf("routing mode 0x%x not built (top-k with softmax over all or over the chosen only)", h->moe_flags);
+    if (h->moe_scale != 0.0f || h->moe_groups > 1) hx_failf("scaled or grouped routing not built");
+    char nm[96];
+    snprintf(nm, sizeof nm, "blk.%d.ffn_gate_shexp.weight", L);
+    if (ssf_find(f, nm)) hx_failf("shared experts not built");
+    snprintf(nm, sizeof nm, "blk.%d.exp_probs_b.weight", L);
+    if (ssf_find(f, nm)) hx_failf("expert score bias not built");
+    m->n_embd = (int) h->n_embd;
+    // the router's rows are the experts (sml/sml-run.c:1676-1680)
+    const ssf_record * rt = ssf_findf(f, "blk.%d.ffn_gate_inp.weight", L);
+    if (!rt) hx_failf("layer %d has no experts (no router)", L);
+    if (rt->kind != SSF_KIND_F32 || ((uint64_t) rt->rows * rt->cols) % (uint64_t) m->n_embd)
+        hx_failf("layer %d: the router is not f32 n_expert x %d", L, m->n_embd);
+    m->nexp = (int) (((uint64_t) rt->rows * rt->cols) / (uint64_t) m->n_embd);
+    m->k = (int) h->n_expert_used;
+    if (m->k <= 0 || m->k > m->nexp) m->k = m->nexp;
+    if (m->k > 16 || m->nexp > 64 || m->nexp < 1) hx_failf("%d of %d experts: at most 16 of 64", m->k, m->nexp);
+    m->flags = h->moe_flags;
+    m->tmax = tmax;
+    m->router = moe_own(m, (size_t) m->nexp * m->n_embd * 4);
+    HX(hipMemcpy(m->router, ssf_at(f, rt->f32_off), (size_t) m->nexp * m->n_embd * 4, hipMemcpyHostToDevice));
+    const ssf_record * rb = ssf_findf(f, "blk.%d.ffn_gate_inp.bias", L);
+    if (rb) {
+        if (rb->kind != SSF_KIND_F32 || (uint64_t) rb->rows * rb->cols != (uint64_t) m->nexp) hx_failf("router bias shape");
+        m->router_b = moe_own(m, (size_t) m->nexp * 4);
+        HX(hipMemcpy(m->router_b, ssf_at(f, rb->f32_off), (size_t) m->nexp * 4, hipMemcpyHostToDevice));
+    }
+    m->mats = calloc((size_t) m->nexp * 3, sizeof *m->mats);
+    if (!m->mats) hx_failf("out of host memory");
+    sml_kmat * tgu = calloc((size_t) m->nexp * 3, sizeof *tgu);
+    const int32_t ** pgu = calloc((size_t) m->nexp * 2, sizeof *pgu);
+    if (!tgu || !pgu) { free(tgu); free(pgu); hx_failf("out of host memory"); }
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) { hx.jb = outer; free(tgu); free(pgu); longjmp(*outer, 1); }
+    hx.jb = &jb;
+    const char * kind[3] = { "gate", "up", "down" };
+    int any_gu = 0, any_d = 0;
+    for (int e = 0; e < m->nexp; e++) {
+        const ssf_record * r[3];
+        for (int i = 0; i < 3; i++) {
+            snprintf(nm, sizeof nm, "blk.%d.ffn_%s.%d.weight", L, kind[i], e);
+            r[i] = ssf_find(f, nm);
+            if (!r[i]) hx_failf("model has no %s", nm);
+            snprintf(nm, sizeof nm, "blk.%d.ffn_%s.%d.bias", L, kind[i], e);
+            if (ssf_find(f, nm)) hx_failf("expert biases not built");
+        }
+        if ((int) r[0]->cols != m->n_embd || r[1]->cols != r[0]->cols || r[1]->rows != r[0]->rows ||
+            (int) r[2]->rows != m->n_embd || r[2]->cols != r[0]->rows || r[1]->nbits != r[0]->nbits)
+            hx_failf("expert %d has unexpected shapes", e);
+        if (e == 0) { m->n_ff = (int) r[0]->rows; m->nbits = (int) r[0]->nbits; }
+        if ((int) r[0]->rows != m->n_ff || (int) r[0]->nbits != m->nbits || (int) r[2]->nbits != m->nbits)
+            hx_failf("experts of different widths or sizes not built");
+        for (int i = 0; i < 3; i++) {
+            m->mats[e * 3 + i] = mat_from_record(f, r[i]);
+            m->expert_bytes += e == 0 ? m->mats[e * 3 + i]->bytes : 0;
+        }
+        tgu[e * 2] = m->mats[e * 3]->k;
+        tgu[e * 2 + 1] = m->mats[e * 3 + 1]->k;
+        tgu[2 * m->nexp + e] = m->mats[e * 3 + 2]->k;
+        const int32_t * pg = moe_perm(m, f, r[0]), * pu = moe_perm(m, f, r[1]);
+        const int same = (!pg && !pu) || (pg && pu && r[0]->perm_off == r[1]->perm_off);
+        if (!same) hx_failf("expert %d: gate and up read different permutations", e);
+        pgu[e] = pg;
+        pgu[m->nexp + e] = moe_perm(m, f, r[2]);
+        any_gu |= pg != NULL;
+        any_d |= pgu[m->nexp + e] != NULL;
+    }
+    m->tab_gu = moe_own(m, (size_t) m->nexp * 2 * sizeof(sml_kmat));
+    m->tab_d = moe_own(m, (size_t) m->nexp * sizeof(sml_kmat));
+    HX(hipMemcpy(m->tab_gu, tgu, (size_t) m->nexp * 2 * sizeof(sml_kmat), hipMemcpyHostToDevice));
+    HX(hipMemcpy(m->tab_d, tgu + 2 * m->nexp, (size_t) m->nexp * sizeof(sml_kmat), hipMemcpyHostToDevice));
+    if (any_gu) {
+        m->ptab_gu = moe_own(m, (size_t) m->nexp * sizeof(void *));
+        HX(hipMemcpy(m->ptab_gu, pgu, (size_t) m->nexp * sizeof(void *), hipMemcpyHostToDevice));
+    }
+    if (any_d) {
+        m->ptab_d = moe_own(m, (size_t) m->nexp * sizeof(void *));
+        HX(hipMemcpy(m->ptab_d, pgu + m->nexp, (size_t) m->nexp * sizeof(void *), hipMemcpyHostToDevice));
+    }
+    hx.jb = outer;
+    free(tgu);
+    free(pgu);
+    // scratch
+    const size_t E = (size_t) m->nexp, T = (size_t) tmax, K = (size_t) m->k, ne = (size_t) m->n_embd, nf = (size_t) m->n_ff;
+    m->logits = moe_own(m, T * E * 4);
+    m->w = moe_own(m, T * K * 4);
+    m->sel = moe_own(m, T * K * 4);
+    m->slot = moe_own(m, T * K * 4);
+    m->count = moe_own(m, E * 4);
+    m->list = moe_own(m, E * T * 4);
+    m->qx = moe_own(m, E * T * ne);
+    m->sx = moe_own(m, E * T * (ne / 32) * 8);
+    m->ux = (int32_t *) (m->sx + E * T * (ne / 32));
+    m->h = moe_own(m, E * T * nf * 4);
+    m->qh = moe_own(m, E * T * nf + E * T * (nf / 32) * 8);
+    m->sh = (float *) (m->qh + E * T * nf);
+    m->uh = (int32_t *) (m->sh + E * T * (nf / 32));
+    m->yd = moe_own(m, E * T * ne * 4);
+}
+
+sml_hip_moe * sml_hip_moe_from_file(const char * path, int layer, int max_tokens) {
+    OP_BEGIN(NULL);
+    if (max_tokens < 1 || max_tokens > 16) hx_failf("max_tokens %d (1..16)", max_tokens);
+    ssf_file f;
+    char why[256];
+    if (!ssf_open(&f, path, why, sizeof why)) hx_failf("%s", why);
+    sml_hip_moe * m = calloc(1, sizeof *m);
+    if (!m) { ssf_close(&f); hx_failf("out of host memory"); }
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) { hx.jb = outer; ssf_close(&f); moe_release(m); longjmp(*outer, 1); }
+    hx.jb = &jb;
+    if (layer < 0 || layer >= (int) f.hdr->n_layer) hx_failf("layer %d of %u", layer, f.hdr->n_layer);
+    moe_setup(m, &f, layer, max_tokens);
+    hx.jb = outer;
+    ssf_close(&f);
+    HX_LEAVE();
+    return m;
+}
+
+void sml_hip_moe_free(sml_hip_moe * m) {
+    HX_ENTRY();
+    if (m) HX(hipDeviceSynchronize());
+    moe_release(m);
+    HX_LEAVE();
+}
+
+int sml_hip_moe_info(const sml_hip_moe * m, int * nexp, int * k, int * n_ff, size_t * expert_bytes) {
+    if (!m) return -1;
+    if (nexp) *nexp = m->nexp;
+    if (k) *k = m->k;
+    if (n_ff) *n_ff = m->n_ff;
+    if (expert_bytes) *expert_bytes = m->expert_bytes;
+    return 0;
+}
+
+static void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out) {
+    sml_kmoe_route r;
+    memset(&r, 0, sizeof r);
+    r.x = x; r.router = m->router; r.router_b = m->router_b;
+    r.T = T; r.n = m->n_embd; r.nexp = m->nexp; r.k = m->k; r.mmax = m->tmax; r.moe_flags = m->flags;
+    r.logits = m->logits; r.sel = m->sel; r.w = m->w; r.slot = m->slot; r.count = m->count; r.list = m->list;
+    hx_launch("sml_moe_route", (unsigned) T, 1, 512, 0, st, &r);
+    hx_launch("sml_moe_plan", 1, 1, 64, 0, st, &r);
+    sml_kmquant qa;
+    memset(&qa, 0, sizeof qa);
+    qa.src = x; qa.mode = 0; qa.perms = m->ptab_gu; qa.n = m->n_embd; qa.mmax = m->tmax; qa.k = m->k;
+    qa.count = m->count; qa.list = m->list; qa.q = m->qx; qa.scale = m->sx; qa.sums = m->ux;
+    hx_launch("sml_moe_quant", (unsigned) T, (unsigned) m->nexp, 1024, 0, st, &qa);
+    const int mt = gemm_mt(T);
+    op_gemm(st, m->tab_gu, m->nexp, 1, m->nbits, m->n_ff, m->n_embd, m->count, 0, mt, m->tmax,
+            m->qx, m->sx, m->ux, m->h);
+    sml_kmquant qb = qa;
+    qb.src = m->h; qb.mode = 1; qb.perms = m->ptab_d; qb.n = m->n_ff; qb.q = m->qh; qb.scale = m->sh; qb.sums = m->uh;
+    hx_launch("sml_moe_quant", (unsigned) T, (unsigned) m->nexp, 1024, 0, st, &qb);
+    op_gemm(st, m->tab_d, m->nexp, 0, m->nbits, m->n_embd, m->n_ff, m->count, 0, mt, m->tmax,
+            m->qh, m->sh, m->uh, m->yd);
+    sml_kmoe_comb c;
+    memset(&c, 0, sizeof c);
+    c.y = m->yd; c.sel = m->sel; c.slot = m->slot; c.w = m->w; c.T = T; c.n = m->n_embd; c.k = m->k;
+    c.mmax = m->tmax; c.out = out;
+    hx_launch("sml_moe_combine", (unsigned) ((m->n_embd + 255) / 256), (unsigned) T, 256, 0, st, &c);
+}
+
+int sml_hip_moe_ffn(sml_hip_moe * m, const float * x, int T, float * out, int32_t * sel, float * w, float * logits) {
+    OP_BEGIN(-1);
+    if (!m || !x || !out || T < 1 || T > m->tmax) hx_failf("moe_ffn of %d tokens (max %d)", T, m ? m->tmax : 0);
+    op_moe(0, m, x, T, out);
+    if (sel) HX(hipMemcpyAsync(sel, m->sel, (size_t) T * m->k * 4, hipMemcpyDeviceToDevice, 0));
+    if (w) HX(hipMemcpyAsync(w, m->w, (size_t) T * m->k * 4, hipMemcpyDeviceToDevice, 0));
+    if (logits) HX(hipMemcpyAsync(logits, m->logits, (size_t) T * m->nexp * 4, hipMemcpyDeviceToDevice, 0));
+    HX(hipStreamSynchronize(0));
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_moe_time(sml_hip_moe * m, const float * x, int T, float * out, int iters, float * ms_total,
+                     int32_t * count_out) {
+    OP_BEGIN(-1);
+    if (!m || T < 1 || T > m->tmax || iters < 1) hx_failf("moe_time arguments");
+    hipEvent_t e0, e1;
+    HX(hipEventCreate(&e0));
+    HX(hipEventCreate(&e1));
+    op_moe(0, m, x, T, out);
+    HX(hipEventRecord(e0, 0));
+    for (int i = 0; i < iters; i++) op_moe(0, m, x, T, out);
+    HX(hipEventRecord(e1, 0));
+    HX(hipEventSynchronize(e1));
+    HX(hipEventElapsedTime(ms_total, e0, e1));
+    HX(hipEventDestroy(e0));
+    HX(hipEventDestroy(e1));
+    if (count_out) HX(hipMemcpy(count_out, m->count, (size_t) m->nexp * 4, hipMemcpyDeviceToHost));
     HX_LEAVE();
     return 0;
 }

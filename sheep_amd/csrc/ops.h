@@ -8,6 +8,7 @@
 
 struct sml_hip_mat {
     sml_kmat k;          // device pointers; k.rows is the row count
+    sml_kmat * kdev;     // the same descriptor in device memory (small-M GEMM tables)
     int nbits, cols;
     void * mem;          // the single allocation holding planes and fields
     size_t bytes;        // planes + fields bytes (what one GEMV streams)
@@ -44,6 +45,13 @@ int gemv_fuse_max_cols(int hq);
 void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int epi, const int8_t * q,
              const float * scale, const int32_t * sums, float * y, const float * bias, const float * up_bias,
              const float * resid, const gemv_fuse * fu);
+// Small-M GEMM over ngroups matrix groups (device table tab: one matrix per
+// group, or gate/up pairs for SwiGLU); m_all rows (count == NULL) or count[e]
+// rows per group, at most mt (1, 4, 8 or 16).
+void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
+             const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
+             const int32_t * sums, float * y);
+int gemm_mt(int m);
 // One matrix holding the rows of several FLAT records of one width and input
 // width, stacked in order (the q, k and v projections as one GEMV).
 sml_hip_mat * mat_stack(const ssf_file * f, const ssf_record * const * recs, int n);

@@ -1,0 +1,141 @@
+"""Small-M GEMM and the MoE expert FFN on the GPU against the oracle.
+
+The small-M GEMM streams each weight once for all its rows with the GEMV's
+per-row arithmetic order, so each row's output equals the GEMV's exactly.
+MoE routing (the chosen experts) must equal the oracle's restatement of
+sml_moe_route bit for bit; logits and weights agree to float rounding of the
+same double sums; the FFN output is within 1e-3 of the oracle's per-token
+composition (quantize, gate/up, SiLU, quantize, down, weighted sum in choice
+order).
+"""
+import numpy as np
+import pytest
+
+import sheep_amd as sa
+from oracle import bind as ob
+from sheep_amd.ssf import SSF
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAX = 1e-3
+TOL_RMS = 1e-4
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    sa.init(0)
+
+
+def close(gpu, ref, what):
+    err = np.abs(gpu.astype(np.float64) - ref.astype(np.float64))
+    scale = np.abs(ref).max()
+    rms = np.sqrt((err ** 2).mean()) / max(np.sqrt((ref.astype(np.float64) ** 2).mean()), 1e-30)
+    assert err.max() <= TOL_MAX * scale, f"{what}: max err {err.max():.3g} vs scale {scale:.3g}"
+    assert rms <= TOL_RMS, f"{what}: rel-RMS {rms:.3g}"
+
+
+def quant_rows(xs):
+    q, s, u = zip(*(ob.quantize_act(np.ascontiguousarray(x, np.float32)) for x in xs))
+    return (sa.DevBuf.of(np.concatenate(q)), sa.DevBuf.of(np.concatenate(s)), sa.DevBuf.of(np.concatenate(u)))
+
+
+@pytest.mark.parametrize("nb", [4, 3, 6, 8])
+@pytest.mark.parametrize("cols", [1536, 5120])
+def test_gemm_rows_equal_gemv(tmpdir_s, nb, cols):
+    p = tmpdir_s / f"gemm{nb}_{cols}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, 1000, cols, nbits=nb, random_perm=False, seed=300 + nb)
+    t = SSF(p)["w"]
+    m = sa.Mat.from_file(p, "w")
+    rng = np.random.default_rng(nb * cols)
+    for nrow in (1, 3, 4, 7, 16):
+        xs = [rng.standard_normal(cols).astype(np.float32) * (1 + r) for r in range(nrow)]
+        q, s, u = quant_rows(xs)
+        y = sa.DevBuf(nrow * 1000 * 4)
+        sa.gemm(m, q, s, u, nrow, y)
+        got = y.read(np.float32).reshape(nrow, 1000)
+        for r in range(nrow):
+            act = sa.Act(cols)
+            act.q.write(ob.quantize_act(xs[r])[0]); act.scale.write(ob.quantize_act(xs[r])[1])
+            act.sums.write(ob.quantize_act(xs[r])[2])
+            y1 = sa.DevBuf(1000 * 4)
+            sa.matvec(m, act, y1)
+            np.testing.assert_array_equal(got[r], y1.read(np.float32), err_msg=f"row {r} of {nrow}")
+            close(got[r], ob.matvec(t, *ob.quantize_act(xs[r])), f"gemm q{nb} row {r}")
+
+
+def test_gemm_swiglu_rows(tmpdir_s):
+    p = tmpdir_s / "gemm_ffn.ssf"
+    sa.synth_model(p, n_layer=1, n_embd=1536, n_head=12, n_head_kv=2, n_ff=2048, n_vocab=256, seed=41)
+    f = SSF(p)
+    g, u = f["blk.0.ffn_gate.weight"], f["blk.0.ffn_up.weight"]
+    mg, mu = sa.Mat.from_file(p, g.name), sa.Mat.from_file(p, u.name)
+    rng = np.random.default_rng(5)
+    xs = [rng.standard_normal(1536).astype(np.float32) for _ in range(5)]
+    q, s, su = quant_rows([x[g.perm] for x in xs])
+    h = sa.DevBuf(5 * 2048 * 4)
+    sa.gemm_swiglu(mg, mu, q, s, su, 5, h)
+    got = h.read(np.float32).reshape(5, 2048)
+    for r, x in enumerate(xs):
+        qa, sa_, ua = ob.quantize_act(x[g.perm])
+        yg, yu = ob.matvec(g, qa, sa_, ua), ob.matvec(u, qa, sa_, ua)
+        ob.oracle().orc_silu_mul(yg.ctypes.data, yu.ctypes.data, 2048)
+        close(got[r], yg, f"gemm swiglu row {r}")
+
+
+def moe_model(tmpdir_s, name, n_embd, n_ff, nexp, k, perm, seed):
+    p = tmpdir_s / name
+    if not p.exists():
+        sa.synth_model(p, n_layer=1, n_embd=n_embd, n_head=n_embd // 128, n_head_kv=2, n_ff=n_ff, n_vocab=512,
+                       n_expert=nexp, n_expert_used=k, moe_flags=1, random_perm=perm, seed=seed)
+    return p
+
+
+def oracle_moe(f, x, nexp, k, n_embd, flags=1):
+    """Per token, as moe_ffn (sml/sml-run.c:3071-3124) with the oracle's kernels."""
+    router = np.ascontiguousarray(f["blk.0.ffn_gate_inp.weight"].f32)
+    lg = np.zeros(nexp, np.float32)
+    ob.oracle().orc_router(router.ctypes.data, x.ctypes.data, nexp, n_embd, lg.ctypes.data)
+    sel = np.zeros(k, np.int32)
+    w = np.zeros(k, np.float32)
+    ob.oracle().orc_moe_route(lg.ctypes.data, nexp, k, flags, sel.ctypes.data, w.ctypes.data)
+    acc = np.zeros(n_embd, np.float32)
+    for j in range(k):
+        e = int(sel[j])
+        g, u, d = (f[f"blk.0.ffn_{kind}.{e}.weight"] for kind in ("gate", "up", "down"))
+        qa = ob.quantize_act(np.ascontiguousarray(x[g.perm]))
+        yg, yu = ob.matvec(g, *qa), ob.matvec(u, *qa)
+        ob.oracle().orc_silu_mul(yg.ctypes.data, yu.ctypes.data, len(yg))
+        yd = ob.matvec(d, *ob.quantize_act(np.ascontiguousarray(yg[d.perm])))
+        acc += w[j] * yd
+    return lg, sel, w, acc
+
+
+@pytest.mark.parametrize("T,perm", [(1, False), (5, True), (16, False), (16, True)])
+def test_moe_ffn(tmpdir_s, T, perm):
+    n_embd, n_ff, nexp, k = 1024, 1536, 8, 2
+    p = moe_model(tmpdir_s, f"moe_{int(perm)}.ssf", n_embd, n_ff, nexp, k, perm, seed=1005 + int(perm))
+    f = SSF(p)
+    moe = sa.MoE(p, 0, 16)
+    assert (moe.nexp, moe.k, moe.n_ff) == (nexp, k, n_ff)
+    rng = np.random.default_rng(T * 7 + int(perm))
+    x = rng.standard_normal((T, n_embd)).astype(np.float32)
+    out, sel, w, lg = sa.DevBuf(T * n_embd * 4), sa.DevBuf(T * k * 4), sa.DevBuf(T * k * 4), sa.DevBuf(T * nexp * 4)
+    moe.ffn(sa.DevBuf.of(x), T, out, sel, w, lg)
+    got_out = out.read(np.float32).reshape(T, n_embd)
+    got_sel = sel.read(np.int32).reshape(T, k)
+    got_w = w.read(np.float32).reshape(T, k)
+    got_lg = lg.read(np.float32).reshape(T, nexp)
+    for t in range(T):
+        rl, rs, rw, ro = oracle_moe(f, x[t], nexp, k, n_embd)
+        np.testing.assert_allclose(got_lg[t], rl, rtol=1e-6, atol=1e-7)
+        np.testing.assert_array_equal(got_sel[t], rs, err_msg=f"token {t} routing")
+        np.testing.assert_allclose(got_w[t], rw, rtol=1e-6, atol=1e-7)
+        close(got_out[t], ro, f"moe token {t}")
+
+
+def test_moe_refuses_dense_layer(tmpdir_s):
+    p = tmpdir_s / "dense_for_moe.ssf"
+    sa.synth_model(p, n_layer=1, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=256, seed=3)
+    with pytest.raises(sa.HipError, match="no experts"):
+        sa.MoE(p, 0, 4)
