@@ -31,6 +31,7 @@ typedef struct {
     float * bias[3];           // device q/k/v biases, or NULL
     float * an, * fn;          // device norm weights
     int perm_qkv[3], perm_o, perm_gu[2], perm_down;   // index into perms, -1 = identity
+    sml_hip_moe * moe;         // a mixture-of-experts FFN in place of gate/up/down, or NULL
 } eng_layer;
 
 static struct {
@@ -49,6 +50,7 @@ static struct {
     int8_t * aq[MAXACT];
     float * as[MAXACT];
     int32_t * asum[MAXACT];
+    float * xn;                // RMSNorm(x) for a MoE FFN's router and experts
     int8_t * hq;               // the SwiGLU kernel's quantized h, input of down
     float * hs;
     int32_t * hsum;
@@ -68,6 +70,7 @@ static struct {
     int ndev;
     sml_hip_mat * mats[8192];
     int nmats;
+    sml_hip_moe * moe_first;   // the MoE layer whose scratch the others share
 } G;
 
 static int (*g_mid_fn)(float *, int, int);
@@ -183,6 +186,13 @@ static void launch_layer(int L) {
     if (fuse_q) slot[0] = 0;
     else prep(G.att, NULL, NULL, G.H * G.hd, &y->perm_o, 1, slot);
     gemv1(y->o, slot[0], SML_EPI_RESIDUAL, G.x, NULL, G.x);
+    if (y->moe) {
+        // ffn_norm into fp32 for the router, then the routed experts; the
+        // combine adds the residual (sml/sml-run.c:3470-3480)
+        op_normq(G.st, G.x, NULL, y->fn, G.eps, G.E, 0, NULL, NULL, NULL, NULL, G.xn, 0);
+        op_moe(G.st, y->moe, G.xn, 1, G.x, G.x);
+        return;
+    }
     // gate/up: one SwiGLU launch when they share a permutation and width; it
     // also quantizes h for down when down reads h in order
     const int h_fused = (G.fuse & 2) && y->perm_down < 0 && G.F % 32 == 0;
@@ -251,6 +261,7 @@ static void release(void) {
         if (G.g_tail) hipGraphExecDestroy(G.g_tail);
         if (G.g_adv) hipGraphExecDestroy(G.g_adv);
         for (int i = 0; i < G.nmats; i++) { if (G.mats[i]->mem) hipFree(G.mats[i]->mem); free(G.mats[i]); }
+        if (G.L) for (int L = 0; L < G.n_layer; L++) if (G.L[L].moe) { moe_free(G.L[L].moe); G.L[L].moe = NULL; }
         for (int i = 0; i < G.ndev; i++) hipFree(G.dev[i]);
         if (G.lg_host) hipHostFree(G.lg_host);
         if (G.pin) hipHostFree(G.pin);
@@ -285,7 +296,6 @@ static const char * unsupported(const ssf_file * f) {
         return "attention scale, soft caps or clamps";
     if (h->emb_scale != 0.0f || h->res_scale != 0.0f || h->logit_scale != 0.0f) return "embedding/residual/logit scales";
     if (h->n_rot) return "partial rotary";
-    if (ssf_find(f, "blk.0.ffn_gate_inp.weight")) return "mixture-of-experts layers";
     if (ssf_find(f, "rope_freqs") || ssf_find(f, "position_embd.weight")) return "stored or learned positions";
     const char * extra[] = { "blk.0.attn_q_norm.weight", "blk.0.attn_output.bias", "blk.0.ffn_up.bias",
                              "blk.0.ffn_down.bias", "blk.0.attn_norm.bias", "output.bias", "token_embd_norm.weight",
@@ -370,16 +380,25 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
         }
         const ssf_record * r;
         r = need(&f, "blk.%d.attn_output.weight", L); y->o = upmat(&f, r); y->perm_o = perm_of(&f, r);
-        r = need(&f, "blk.%d.ffn_gate.weight", L); y->gate = upmat(&f, r); y->perm_gu[0] = perm_of(&f, r);
-        r = need(&f, "blk.%d.ffn_up.weight", L); y->up = upmat(&f, r); y->perm_gu[1] = perm_of(&f, r);
-        r = need(&f, "blk.%d.ffn_down.weight", L); y->down = upmat(&f, r); y->perm_down = perm_of(&f, r);
-        if (y->o->k.rows != G.E || y->o->cols != G.H * G.hd || y->gate->k.rows != G.F || y->up->k.rows != G.F ||
-            y->down->k.rows != G.E || y->down->cols != G.F)
-            hx_failf("layer %d has unexpected projection shapes", L);
+        if (ssf_findf(&f, "blk.%d.ffn_gate_inp.weight", L)) {
+            y->moe = moe_load(&f, L, 1, G.moe_first);
+            if (!G.moe_first) G.moe_first = y->moe;
+            // bytes one step reads: the router and the k chosen experts
+            G.weight_bytes += (uint64_t) y->moe->k * y->moe->expert_bytes + (uint64_t) y->moe->nexp * G.E * 4;
+            if (y->o->k.rows != G.E || y->o->cols != G.H * G.hd) hx_failf("layer %d has unexpected projection shapes", L);
+        } else {
+            r = need(&f, "blk.%d.ffn_gate.weight", L); y->gate = upmat(&f, r); y->perm_gu[0] = perm_of(&f, r);
+            r = need(&f, "blk.%d.ffn_up.weight", L); y->up = upmat(&f, r); y->perm_gu[1] = perm_of(&f, r);
+            r = need(&f, "blk.%d.ffn_down.weight", L); y->down = upmat(&f, r); y->perm_down = perm_of(&f, r);
+            if (y->o->k.rows != G.E || y->o->cols != G.H * G.hd || y->gate->k.rows != G.F || y->up->k.rows != G.F ||
+                y->down->k.rows != G.E || y->down->cols != G.F)
+                hx_failf("layer %d has unexpected projection shapes", L);
+            G.weight_bytes += y->gate->bytes + y->up->bytes + y->down->bytes;
+        }
         y->an = f32_tensor(&f, "blk.%d.attn_norm.weight", L, G.E);
         y->fn = f32_tensor(&f, "blk.%d.ffn_norm.weight", L, G.E);
         if (!y->an || !y->fn) hx_failf("layer %d lacks a norm", L);
-        G.weight_bytes += y->o->bytes + y->gate->bytes + y->up->bytes + y->down->bytes;
+        G.weight_bytes += y->o->bytes;
     }
     // RoPE table on the host, exactly as the reference builds it (sml/sml-run.c:1383-1393)
     {
@@ -415,6 +434,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
         G.as[i] = dalloc((size_t) wide / 32 * 4);
         G.asum[i] = dalloc((size_t) wide / 32 * 4);
     }
+    G.xn = dalloc((size_t) G.E * 4);
     G.hq = dalloc((size_t) G.F);
     G.hs = dalloc((size_t) G.F / 32 * 4);
     G.hsum = dalloc((size_t) G.F / 32 * 4);

@@ -237,5 +237,6 @@ typedef struct {
     const int32_t * sel, * slot;
     const float   * w;
     int T, n, k, mmax;
+    const float * resid;          // [T][n] added first (may alias out), or NULL
     float * out;                  // [T][n]
 } sml_kmoe_comb;

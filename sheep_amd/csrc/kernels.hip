@@ -1205,7 +1205,8 @@ extern "C" __global__ __launch_bounds__(256) void sml_moe_combine(const sml_kmoe
         const int e = a.sel[t * a.k + j], r = a.slot[t * a.k + j];
         acc += a.w[t * a.k + j] * a.y[((size_t) e * a.mmax + r) * a.n + i];
     }
-    a.out[(size_t) t * a.n + i] = acc;
+    const size_t o = (size_t) t * a.n + i;
+    a.out[o] = a.resid ? a.resid[o] + acc : acc;    // the residual add after moe_ffn, sml/sml-run.c:3475-3480
 }
 
 // ---------------------------------------------------------------- small-M GEMM

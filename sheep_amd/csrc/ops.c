@@ -703,23 +703,7 @@ int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const 
 
 // ------------------------------------------------------------ MoE expert FFN
 
-struct sml_hip_moe {
-    int nexp, k, n_embd, n_ff, tmax, nbits;
-    unsigned flags;
-    float * router, * router_b;
-    sml_hip_mat ** mats;          // [nexp][3]: gate, up, down
-    sml_kmat * tab_gu, * tab_d;   // device tables
-    const int32_t ** ptab_gu, ** ptab_d;   // device tables of device permutations, or NULL (identity)
-    void * work;                  // scratch: logits, route, lists, activations, h, expert outputs
-    float * logits, * w, * h, * yd;
-    int32_t * sel, * slot, * count, * list;
-    int8_t * qx, * qh;
-    float * sx, * sh;
-    int32_t * ux, * uh;
-    void * owned[160];            // every device allocation: up to 2 permutations per expert + buffers
-    int nowned;
-    size_t expert_bytes;
-};
+
 
 static void * moe_own(sml_hip_moe * m, size_t n) {
     if (m->nowned >= (int) (sizeof m->owned / sizeof m->owned[0])) hx_failf("too many MoE allocations");
@@ -749,7 +733,7 @@ static int32_t * moe_perm(sml_hip_moe * m, const ssf_file * f, const ssf_record 
     return d;
 }
 
-static void moe_setup(sml_hip_moe * m, const ssf_file * f, int L, int tmax) {
+static void moe_setup(sml_hip_moe * m, const ssf_file * f, int L, int tmax, const sml_hip_moe * share) {
     const ssf_header * h = f->hdr;
     if (h->moe_flags & ~1u) hx_failf("routing mode 0x%x not built (top-k with softmax over all or over the chosen only)", h->moe_flags);
     if (h->moe_scale != 0.0f || h->moe_groups > 1) hx_failf("scaled or grouped routing not built");
@@ -834,7 +818,17 @@ static void moe_setup(sml_hip_moe * m, const ssf_file * f, int L, int tmax) {
     hx.jb = outer;
     free(tgu);
     free(pgu);
-    // scratch
+    // scratch: this layer's own, or another layer's of the same shape (layers run one after another)
+    if (share) {
+        if (share->nexp != m->nexp || share->k != m->k || share->n_ff != m->n_ff || share->n_embd != m->n_embd ||
+            share->tmax < tmax)
+            hx_failf("layer %d: experts of a different shape than layer 0's", L);
+        m->logits = share->logits; m->w = share->w; m->sel = share->sel; m->slot = share->slot;
+        m->count = share->count; m->list = share->list; m->qx = share->qx; m->sx = share->sx; m->ux = share->ux;
+        m->h = share->h; m->qh = share->qh; m->sh = share->sh; m->uh = share->uh; m->yd = share->yd;
+        m->tmax = share->tmax;
+        return;
+    }
     const size_t E = (size_t) m->nexp, T = (size_t) tmax, K = (size_t) m->k, ne = (size_t) m->n_embd, nf = (size_t) m->n_ff;
     m->logits = moe_own(m, T * E * 4);
     m->w = moe_own(m, T * K * 4);
@@ -865,7 +859,7 @@ sml_hip_moe * sml_hip_moe_from_file(const char * path, int layer, int max_tokens
     if (setjmp(jb)) { hx.jb = outer; ssf_close(&f); moe_release(m); longjmp(*outer, 1); }
     hx.jb = &jb;
     if (layer < 0 || layer >= (int) f.hdr->n_layer) hx_failf("layer %d of %u", layer, f.hdr->n_layer);
-    moe_setup(m, &f, layer, max_tokens);
+    moe_setup(m, &f, layer, max_tokens, NULL);
     hx.jb = outer;
     ssf_close(&f);
     HX_LEAVE();
@@ -888,7 +882,21 @@ int sml_hip_moe_info(const sml_hip_moe * m, int * nexp, int * k, int * n_ff, siz
     return 0;
 }
 
-static void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out) {
+sml_hip_moe * moe_load(const ssf_file * f, int layer, int tmax, const sml_hip_moe * share) {
+    sml_hip_moe * m = calloc(1, sizeof *m);
+    if (!m) hx_failf("out of host memory");
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) { hx.jb = outer; moe_release(m); longjmp(*outer, 1); }
+    hx.jb = &jb;
+    moe_setup(m, f, layer, tmax, share);
+    hx.jb = outer;
+    return m;
+}
+
+void moe_free(sml_hip_moe * m) { moe_release(m); }
+
+void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out, const float * resid) {
     sml_kmoe_route r;
     memset(&r, 0, sizeof r);
     r.x = x; r.router = m->router; r.router_b = m->router_b;
@@ -912,14 +920,14 @@ static void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, floa
     sml_kmoe_comb c;
     memset(&c, 0, sizeof c);
     c.y = m->yd; c.sel = m->sel; c.slot = m->slot; c.w = m->w; c.T = T; c.n = m->n_embd; c.k = m->k;
-    c.mmax = m->tmax; c.out = out;
+    c.mmax = m->tmax; c.out = out; c.resid = resid;
     hx_launch("sml_moe_combine", (unsigned) ((m->n_embd + 255) / 256), (unsigned) T, 256, 0, st, &c);
 }
 
 int sml_hip_moe_ffn(sml_hip_moe * m, const float * x, int T, float * out, int32_t * sel, float * w, float * logits) {
     OP_BEGIN(-1);
     if (!m || !x || !out || T < 1 || T > m->tmax) hx_failf("moe_ffn of %d tokens (max %d)", T, m ? m->tmax : 0);
-    op_moe(0, m, x, T, out);
+    op_moe(0, m, x, T, out, NULL);
     if (sel) HX(hipMemcpyAsync(sel, m->sel, (size_t) T * m->k * 4, hipMemcpyDeviceToDevice, 0));
     if (w) HX(hipMemcpyAsync(w, m->w, (size_t) T * m->k * 4, hipMemcpyDeviceToDevice, 0));
     if (logits) HX(hipMemcpyAsync(logits, m->logits, (size_t) T * m->nexp * 4, hipMemcpyDeviceToDevice, 0));
@@ -935,9 +943,9 @@ int sml_hip_moe_time(sml_hip_moe * m, const float * x, int T, float * out, int i
     hipEvent_t e0, e1;
     HX(hipEventCreate(&e0));
     HX(hipEventCreate(&e1));
-    op_moe(0, m, x, T, out);
+    op_moe(0, m, x, T, out, NULL);
     HX(hipEventRecord(e0, 0));
-    for (int i = 0; i < iters; i++) op_moe(0, m, x, T, out);
+    for (int i = 0; i < iters; i++) op_moe(0, m, x, T, out, NULL);
     HX(hipEventRecord(e1, 0));
     HX(hipEventSynchronize(e1));
     HX(hipEventElapsedTime(ms_total, e0, e1));

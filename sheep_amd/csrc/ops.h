@@ -65,3 +65,28 @@ void op_argmax(hipStream_t st, const float * logits, int n, int32_t * tok, int32
                int hist_n);
 void op_advance(hipStream_t st, int32_t * pos);
 void op_silu_mul(hipStream_t st, float * g, const float * u, int n);
+
+// One MoE FFN layer: router, experts and (shared between layers) scratch.
+struct sml_hip_moe {
+    int nexp, k, n_embd, n_ff, tmax, nbits;
+    unsigned flags;
+    float * router, * router_b;
+    sml_hip_mat ** mats;          // [nexp][3]: gate, up, down
+    sml_kmat * tab_gu, * tab_d;   // device tables
+    const int32_t ** ptab_gu, ** ptab_d;   // device tables of device permutations, or NULL (identity)
+    void * work;                  // scratch: logits, route, lists, activations, h, expert outputs
+    float * logits, * w, * h, * yd;
+    int32_t * sel, * slot, * count, * list;
+    int8_t * qx, * qh;
+    float * sx, * sh;
+    int32_t * ux, * uh;
+    void * owned[160];            // every device allocation: up to 2 permutations per expert + buffers
+    int nowned;
+    size_t expert_bytes;
+};
+// Experts of layer `layer` for up to tmax tokens per call; scratch shared with
+// `share` (a loaded layer of the same shape) when not NULL.
+sml_hip_moe * moe_load(const ssf_file * f, int layer, int tmax, const sml_hip_moe * share);
+void moe_free(sml_hip_moe * m);
+// out[t] = (resid[t] +) sum over the chosen experts of w * FFN_e(x[t]).
+void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out, const float * resid);

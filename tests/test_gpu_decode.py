@@ -151,6 +151,26 @@ def test_greedy_tokens_qwen_layers(qwenish):
     check_tokens(list(out), toks[1:], logits)
 
 
+@pytest.mark.parametrize("perm", [False, True])
+def test_greedy_tokens_moe(tmp_path, perm):
+    """A Mixtral-shaped decoder (8 experts, top-2, softmax over the chosen):
+    routed experts on the GPU, tokens identical to the oracle."""
+    p = tmp_path / "moe.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, n_expert=8,
+                   n_expert_used=2, moe_flags=1, random_perm=perm, seed=60 + int(perm))
+    n = 24
+    toks, logits = greedy_oracle(p, 9, n, 64)
+    d = sa.Decoder(p, n_ctx=64)
+    try:
+        for pos in range(4):
+            lg = d.step(toks[pos], pos, 2000)
+            assert np.corrcoef(lg, logits[pos])[0, 1] > 0.999, pos
+        out = d.generate(9, 0, n)
+    finally:
+        d.close()
+    check_tokens(list(out), toks[1:], logits)
+
+
 def test_bounds_and_reopen(tiny):
     d = sa.Decoder(tiny, n_ctx=32)
     try:

@@ -295,6 +295,26 @@ def test_decoder_layers_match_reference(tmpdir_s, monkeypatch):
         assert np.corrcoef(a, b)[0, 1] > 0.9999
 
 
+@needs_ref
+@pytest.mark.parametrize("perm", [False, True])
+def test_moe_decoder_matches_reference(tmpdir_s, perm):
+    """A Mixtral-shaped decoder (4 experts, top-2, softmax over the chosen):
+    the oracle's router, routing and expert FFN against the reference's
+    sml_forward, position by position."""
+    p = tmpdir_s / f"moe_dec_{int(perm)}.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=600, n_expert=4,
+                   n_expert_used=2, moe_flags=1, random_perm=perm, seed=55 + int(perm))
+    om, rm = ob.OracleModel(p, 16), ob.RefModel(p, 16, threads=1)
+    try:
+        for pos, tok in enumerate([1, 77, 300, 5, 599, 42]):
+            a, b = om.forward(tok, pos), rm.forward(tok, pos)
+            assert np.corrcoef(a, b)[0, 1] > 0.9999, pos
+            assert np.abs(a - b).max() <= 2e-2 * np.abs(b).max(), pos
+    finally:
+        om.close()
+        rm.close()
+
+
 # ------------------------------------------------------------ GPTQ-style 4-bit
 
 def test_gptq_packing_bit_order():
