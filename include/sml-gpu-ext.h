@@ -29,6 +29,25 @@ uint64_t sml_gpu_weight_bytes(void);
 // Last failure message.
 const char * sml_gpu_last_error(void);
 
+// ---------------------------------------------------------------- several sequences
+// The multi-sequence step sml-batched drives on the CPU through
+// sml_forward_multi (sml/sml-run.h:290-294, sml/sml-batched.c:82-130), in its
+// exact activation regime (SML_MULTI=exact: per-32 int8 activations, so every
+// sequence's logits equal decoding it alone, bit for bit).
+//
+// Give the open model ns (1..16) KV cache slots; slot 0 is the cache
+// sml_gpu_step / sml_gpu_prefill use. Every layer's q, k and v must share one
+// permutation and width (and gate/up likewise). Returns ns, or 0.
+int sml_gpu_slots(int ns);
+// sml_gpu_prefill into slot `slot`'s cache; logits of the last id (the
+// library's host buffer), NULL on failure.
+const float * sml_gpu_prefill_slot(int slot, const int * ids, int pos0, int n);
+// One token for each of ns sequences: sequence b feeds tok[b] at position
+// pos[b] into slot slot[b] (distinct slots). Each weight matrix is read once
+// for all of them. Logits land in logits_out[b * n_vocab] (caller's host
+// memory). Returns ns, or 0.
+int sml_gpu_step_multi(const int * tok, const int * pos, const int * slot, int ns, float * logits_out);
+
 #ifdef __cplusplus
 }
 #endif

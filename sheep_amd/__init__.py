@@ -44,6 +44,9 @@ _SIGS = [
     ("sml_gpu_last_ms", c_float, []),
     ("sml_gpu_weight_bytes", c_uint64, []),
     ("sml_gpu_last_error", c_char_p, []),
+    ("sml_gpu_slots", c_int, [c_int]),
+    ("sml_gpu_prefill_slot", P(c_float), [c_int, P(c_int), c_int, c_int]),
+    ("sml_gpu_step_multi", c_int, [P(c_int), P(c_int), P(c_int), c_int, c_void_p]),
     ("sml_hip_init", c_int, [c_int, c_char_p, c_int]),
     ("sml_hip_last_error", c_char_p, []),
     ("sml_hip_malloc", c_void_p, [c_size_t]),
@@ -283,6 +286,27 @@ class Decoder:
         if not p:
             raise HipError(f"sml_gpu_step: {lib().sml_gpu_last_error().decode(errors='replace')}")
         return np.ctypeslib.as_array(p, shape=(n_vocab,)).copy()
+
+    def slots(self, ns):
+        if lib().sml_gpu_slots(ns) != ns:
+            raise HipError(f"sml_gpu_slots: {lib().sml_gpu_last_error().decode(errors='replace')}")
+
+    def prefill_slot(self, slot, ids, pos0, n_vocab):
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        p = lib().sml_gpu_prefill_slot(slot, a.ctypes.data_as(P(c_int)), pos0, len(a))
+        if not p:
+            raise HipError(f"sml_gpu_prefill_slot: {lib().sml_gpu_last_error().decode(errors='replace')}")
+        return np.ctypeslib.as_array(p, shape=(n_vocab,)).copy()
+
+    def step_multi(self, toks, poss, slots, n_vocab):
+        t = np.ascontiguousarray(toks, np.int32)
+        p = np.ascontiguousarray(poss, np.int32)
+        s = np.ascontiguousarray(slots, np.int32)
+        out = np.zeros((len(t), n_vocab), np.float32)
+        if lib().sml_gpu_step_multi(t.ctypes.data_as(P(c_int)), p.ctypes.data_as(P(c_int)), s.ctypes.data_as(P(c_int)),
+                                    len(t), out.ctypes.data) != len(t):
+            raise HipError(f"sml_gpu_step_multi: {lib().sml_gpu_last_error().decode(errors='replace')}")
+        return out
 
     def prefill(self, ids, pos0, n_vocab):
         a = np.ascontiguousarray(ids, dtype=np.int32)

@@ -32,7 +32,10 @@ typedef struct {
     float * an, * fn;          // device norm weights
     int perm_qkv[3], perm_o, perm_gu[2], perm_down;   // index into perms, -1 = identity
     sml_hip_moe * moe;         // a mixture-of-experts FFN in place of gate/up/down, or NULL
+    sml_kmat * gu_tab;         // device (gate, up) pair for the batched SwiGLU GEMM
 } eng_layer;
+
+#define MAX_SLOTS 16
 
 static struct {
     int open;
@@ -71,6 +74,14 @@ static struct {
     sml_hip_mat * mats[8192];
     int nmats;
     sml_hip_moe * moe_first;   // the MoE layer whose scratch the others share
+    // several sequences: a KV cache per slot (slot 0's is kc/vc) and batch buffers
+    int nslot, cur_slot;
+    uint16_t * kcs[MAX_SLOTS], * vcs[MAX_SLOTS];
+    float * mx, * mqkv, * matt, * mh, * mxn, * mlog;
+    int8_t * maq;
+    float * mas;
+    int32_t * masum, * mtok, * mpos;
+    int32_t * mpin;            // pinned: tokens then positions of a batched step
 } G;
 
 static int (*g_mid_fn)(float *, int, int);
@@ -180,7 +191,8 @@ static void launch_layer(int L) {
     // with an identity o-proj permutation the attention kernel quantizes its
     // own output for the o GEMV; otherwise a gather + quantize follows it
     const int fuse_q = y->perm_o < 0;
-    op_attention(G.st, G.q, G.k, G.v, G.kc + (size_t) L * G.n_ctx * kvd, G.vc + (size_t) L * G.n_ctx * kvd,
+    uint16_t * kc = G.cur_slot ? G.kcs[G.cur_slot] : G.kc, * vc = G.cur_slot ? G.vcs[G.cur_slot] : G.vc;
+    op_attention(G.st, G.q, G.k, G.v, kc + (size_t) L * G.n_ctx * kvd, vc + (size_t) L * G.n_ctx * kvd,
                  G.rc, G.rs, G.pos, G.H, G.KV, G.hd, G.n_ctx, G.part, G.att,
                  fuse_q ? G.aq[0] : NULL, fuse_q ? G.as[0] : NULL, fuse_q ? G.asum[0] : NULL);
     if (fuse_q) slot[0] = 0;
@@ -265,6 +277,7 @@ static void release(void) {
         for (int i = 0; i < G.ndev; i++) hipFree(G.dev[i]);
         if (G.lg_host) hipHostFree(G.lg_host);
         if (G.pin) hipHostFree(G.pin);
+        if (G.mpin) hipHostFree(G.mpin);
         if (G.e0) hipEventDestroy(G.e0);
         if (G.e1) hipEventDestroy(G.e1);
         if (G.st) hipStreamDestroy(G.st);
@@ -381,7 +394,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
         const ssf_record * r;
         r = need(&f, "blk.%d.attn_output.weight", L); y->o = upmat(&f, r); y->perm_o = perm_of(&f, r);
         if (ssf_findf(&f, "blk.%d.ffn_gate_inp.weight", L)) {
-            y->moe = moe_load(&f, L, 1, G.moe_first);
+            y->moe = moe_load(&f, L, MAX_SLOTS, G.moe_first);
             if (!G.moe_first) G.moe_first = y->moe;
             // bytes one step reads: the router and the k chosen experts
             G.weight_bytes += (uint64_t) y->moe->k * y->moe->expert_bytes + (uint64_t) y->moe->nexp * G.E * 4;
@@ -556,4 +569,152 @@ int sml_gpu_decode_cpu(int on) { (void) on; return 0; }
 void sml_gpu_set_middle(int layers, int (*fn)(float * rows, int pos0, int n)) {
     g_mid_layers = layers;
     g_mid_fn = fn;
+}
+
+// ---------------------------------------------------------------- several sequences
+//
+// The GPU twin of sml_forward_multi (sml/sml-run.c:2559-2599) in its exact
+// regime (SML_MULTI=exact: per-32 activations, every sequence bit for bit as
+// decoded alone): each weight matrix streams once per step for all
+// sequences through the small-M GEMM, whose per-row arithmetic is the GEMV's;
+// attention runs per sequence over that sequence's KV cache slot.
+
+int sml_gpu_slots(int ns) {
+    if (!G.open || ns < 1 || ns > MAX_SLOTS) return 0;
+    HX_ENTRY(0);
+    for (int L = 0; L < G.n_layer; L++) {
+        eng_layer * y = &G.L[L];
+        if (!y->qkv) hx_failf("layer %d: q, k and v are not one matrix; the batched step needs them stacked", L);
+        if (!y->moe && (y->perm_gu[0] != y->perm_gu[1] || y->gate->nbits != y->up->nbits))
+            hx_failf("layer %d: gate and up differ in permutation or width", L);
+        if (!y->moe && !y->gu_tab) {
+            const sml_kmat t[2] = { y->gate->k, y->up->k };
+            y->gu_tab = dupload(t, sizeof t);
+        }
+    }
+    const size_t kvn = (size_t) G.n_layer * G.n_ctx * G.KV * G.hd;
+    for (int s = G.nslot > 1 ? G.nslot : 1; s < ns; s++) {
+        G.kcs[s] = dalloc(kvn * 2);
+        G.vcs[s] = dalloc(kvn * 2);
+        HX(hipMemset(G.kcs[s], 0, kvn * 2));
+        HX(hipMemset(G.vcs[s], 0, kvn * 2));
+    }
+    if (!G.mx) {
+        const size_t R = MAX_SLOTS;
+        size_t wide = (size_t) (G.F > G.E ? G.F : G.E);
+        if ((size_t) G.H * G.hd > wide) wide = (size_t) G.H * G.hd;
+        G.mx = dalloc(R * G.E * 4);
+        G.mxn = dalloc(R * G.E * 4);
+        G.mqkv = dalloc(R * (size_t) (G.H + 2 * G.KV) * G.hd * 4);
+        G.matt = dalloc(R * (size_t) G.H * G.hd * 4);
+        G.mh = dalloc(R * (size_t) G.F * 4);
+        G.mlog = dalloc(R * (size_t) G.V * 4);
+        G.maq = dalloc(R * wide);
+        G.mas = dalloc(R * wide / 32 * 4);
+        G.masum = dalloc(R * wide / 32 * 4);
+        G.mtok = dalloc(R * 4);
+        G.mpos = dalloc(R * 4);
+        HX(hipHostMalloc((void **) &G.mpin, 2 * R * 4, 0));
+    }
+    if (ns > G.nslot) G.nslot = ns;
+    HX(hipDeviceSynchronize());
+    HX_LEAVE();
+    return ns;
+}
+
+const float * sml_gpu_prefill_slot(int slot, const int * ids, int pos0, int n) {
+    if (slot == 0) return sml_gpu_prefill(ids, pos0, n);
+    if (!G.open || slot < 0 || slot >= G.nslot || n <= 0 || pos0 < 0 || pos0 + n > G.n_ctx) return NULL;
+    for (int i = 0; i < n; i++) if (ids[i] < 0 || ids[i] >= G.V) return NULL;
+    HX_ENTRY(NULL);
+    G.pin[1] = pos0;
+    memcpy(G.pin + 2, ids, (size_t) n * 4);
+    HX(hipMemcpyAsync(G.hist + pos0, G.pin + 2, (size_t) n * 4, hipMemcpyHostToDevice, G.st));
+    HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
+    // the captured graphs hold slot 0's cache: other slots launch directly
+    G.cur_slot = slot;
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) { G.cur_slot = 0; hx.jb = outer; longjmp(*outer, 1); }
+    hx.jb = &jb;
+    for (int i = 0; i < n; i++) {
+        launch_body();
+        if (i + 1 < n) launch_adv();
+    }
+    launch_tail();
+    hx.jb = outer;
+    G.cur_slot = 0;
+    fetch_logits();
+    HX_LEAVE();
+    return G.lg_host;
+}
+
+static void launch_multi(int ns, const int * slot) {
+    const size_t kvd = (size_t) G.KV * G.hd, qkv = (size_t) (G.H + 2 * G.KV) * G.hd, hq = (size_t) G.H * G.hd;
+    const int mt = gemm_mt(ns);
+    op_embed_rows(G.st, G.emb, G.mtok, NULL, ns, pdev(G.perm_emb), G.mx);
+    for (int L = 0; L < G.n_layer; L++) {
+        eng_layer * y = &G.L[L];
+        const int32_t * pp[1];
+        int8_t * qq[1] = { G.maq };
+        float * ss[1] = { G.mas };
+        int32_t * uu[1] = { G.masum };
+        pp[0] = pdev(y->perm_qkv[0]);
+        op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, 0);
+        op_gemm(G.st, y->qkv->kdev, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
+                G.mqkv, y->bias_qkv, NULL);
+        const int fuse_q = y->perm_o < 0;
+        for (int b = 0; b < ns; b++) {
+            const float * q = G.mqkv + (size_t) b * qkv;
+            uint16_t * kc = slot[b] ? G.kcs[slot[b]] : G.kc, * vc = slot[b] ? G.vcs[slot[b]] : G.vc;
+            op_attention(G.st, q, q + hq, q + hq + kvd, kc + (size_t) L * G.n_ctx * kvd, vc + (size_t) L * G.n_ctx * kvd,
+                         G.rc, G.rs, G.mpos + b, G.H, G.KV, G.hd, G.n_ctx, G.part, G.matt + (size_t) b * hq,
+                         fuse_q ? G.maq + (size_t) b * hq : NULL, fuse_q ? G.mas + (size_t) b * hq / 32 : NULL,
+                         fuse_q ? G.masum + (size_t) b * hq / 32 : NULL);
+        }
+        if (!fuse_q) {
+            pp[0] = pdev(y->perm_o);
+            op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, 0);
+        }
+        op_gemm(G.st, y->o->kdev, 1, 0, y->o->nbits, G.E, (int) hq, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
+                G.mx, NULL, G.mx);
+        if (y->moe) {
+            op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 0, NULL, NULL, NULL, NULL, G.mxn, 0);
+            op_moe(G.st, y->moe, G.mxn, ns, G.mx, G.mx);
+            continue;
+        }
+        pp[0] = pdev(y->perm_gu[0]);
+        op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, 0);
+        op_gemm(G.st, y->gu_tab, 1, 1, y->gate->nbits, G.F, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mh,
+                NULL, NULL);
+        pp[0] = pdev(y->perm_down);
+        op_normq_rows(G.st, G.mh, NULL, NULL, G.eps, G.F, ns, 1, pp, qq, ss, uu, NULL, 0);
+        op_gemm(G.st, y->down->kdev, 1, 0, y->down->nbits, G.E, G.F, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
+                G.mx, NULL, G.mx);
+    }
+    const int32_t * pp[1] = { pdev(G.perm_head) };
+    int8_t * qq[1] = { G.maq };
+    float * ss[1] = { G.mas };
+    int32_t * uu[1] = { G.masum };
+    op_normq_rows(G.st, G.mx, NULL, G.out_norm, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, 0);
+    op_gemm(G.st, G.head->kdev, 1, 0, G.head->nbits, G.V, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mlog,
+            NULL, NULL);
+}
+
+int sml_gpu_step_multi(const int * tok, const int * pos, const int * slot, int ns, float * logits_out) {
+    if (!G.open || ns < 1 || ns > G.nslot || !tok || !pos || !slot || !logits_out) return 0;
+    for (int b = 0; b < ns; b++) {
+        if (tok[b] < 0 || tok[b] >= G.V || pos[b] < 0 || pos[b] >= G.n_ctx || slot[b] < 0 || slot[b] >= G.nslot) return 0;
+        for (int c = 0; c < b; c++) if (slot[c] == slot[b]) return 0;
+    }
+    HX_ENTRY(0);
+    memcpy(G.mpin, tok, (size_t) ns * 4);
+    memcpy(G.mpin + MAX_SLOTS, pos, (size_t) ns * 4);
+    HX(hipMemcpyAsync(G.mtok, G.mpin, (size_t) ns * 4, hipMemcpyHostToDevice, G.st));
+    HX(hipMemcpyAsync(G.mpos, G.mpin + MAX_SLOTS, (size_t) ns * 4, hipMemcpyHostToDevice, G.st));
+    launch_multi(ns, slot);
+    HX(hipMemcpyAsync(logits_out, G.mlog, (size_t) ns * G.V * 4, hipMemcpyDeviceToHost, G.st));
+    HX(hipStreamSynchronize(G.st));
+    HX_LEAVE();
+    return ns;
 }

@@ -229,6 +229,8 @@ typedef struct {
     const float   * scale;        // [ngroups][mmax][cols/32]
     const int32_t * sums;
     float * y;                    // [ngroups][mmax][rows]
+    const float * bias;           // [rows] added to each row (plain GEMM only), or NULL
+    const float * resid;          // [ngroups][mmax][rows]: y = resid + (W.a + bias), may alias y; or NULL
 } sml_kgemm;
 
 // out[t] = sum over j of w[t][j] * y[sel[t][j]][slot[t][j]], in choice order.

@@ -537,10 +537,14 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
     extern __shared__ __align__(16) float sx[];
     __shared__ double red[NORMQ_THREADS / WAVE];
     const int n = a.n, tid = threadIdx.x;
+    // row blockIdx.y of a batch (every pointer strided by its row)
+    const size_t bo = (size_t) blockIdx.y * n, bg = (size_t) blockIdx.y * (n / 32);
+    float * x = a.x + bo;
+    const float * resid = a.resid ? a.resid + bo : nullptr;
     double ss = 0.0;
     for (int i = tid; i < n; i += NORMQ_THREADS) {
-        float v = a.x[i];
-        if (a.resid) { v = v + a.resid[i]; a.x[i] = v; }
+        float v = x[i];
+        if (resid) { v = v + resid[i]; x[i] = v; }
         sx[i] = v;
         ss += (double) v * (double) v;
     }
@@ -557,7 +561,7 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
         for (int i = tid; i < n; i += NORMQ_THREADS) sx[i] = sx[i] * sc * a.norm_w[i];
     }
     __syncthreads();
-    if (a.normed) for (int i = tid; i < n; i += NORMQ_THREADS) a.normed[i] = sx[i];
+    if (a.normed) for (int i = tid; i < n; i += NORMQ_THREADS) a.normed[bo + i] = sx[i];
     const int ng = n / 32;
     for (int o = 0; o < a.nout; o++) {
         const int32_t * perm = a.perm[o];
@@ -577,7 +581,7 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
             const float s = amax / 127.0f;
             const float is = s > 0.0f ? 1.0f / s : 0.0f;
             int sum = 0;
-            int8_t * q = a.q[o] + g * 32;
+            int8_t * q = a.q[o] + bo + g * 32;
             #pragma unroll
             for (int j = 0; j < 32; j += 4) {
                 int w = 0;
@@ -593,8 +597,8 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
                 }
                 *(int *) (q + j) = w;
             }
-            a.scale[o][g] = s;
-            a.sums[o][g] = sum;
+            a.scale[o][bg + g] = s;
+            a.sums[o][bg + g] = sum;
         }
     }
 }
@@ -604,11 +608,14 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
 extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a) {
     __shared__ double red[4];
     const int n = a.n, tid = threadIdx.x;
+    // row blockIdx.y of a batch (every pointer strided by its row)
+    const size_t bo = (size_t) blockIdx.y * n, bg = (size_t) blockIdx.y * (n / 32);
+    const float * x = a.x + bo;
     float sc = 1.0f;
     if (a.norm_w) {
         double ss = 0.0;
         for (int i = tid * 4; i < n; i += 1024) {
-            const float4 v = *(const float4 *) (a.x + i);
+            const float4 v = *(const float4 *) (x + i);
             ss += (double) v.x * v.x + (double) v.y * v.y + (double) v.z * v.z + (double) v.w * v.w;
         }
         #pragma unroll
@@ -623,7 +630,7 @@ extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a
     const int l32 = tid & 31, g = j >> 5;
     for (int o = 0; o < a.nout; o++) {
         const int src = a.perm[o] ? a.perm[o][j] : j;
-        const float v = a.norm_w ? a.x[src] * sc * a.norm_w[src] : a.x[src];
+        const float v = a.norm_w ? x[src] * sc * a.norm_w[src] : x[src];
         const float amax = max32(fabsf(v));
         const float s = amax / 127.0f;
         const float is = s > 0.0f ? 1.0f / s : 0.0f;
@@ -631,8 +638,8 @@ extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a
         int t = (r >= -2147483648.0f && r < 2147483648.0f) ? (int) r : (int) 0x80000000u;
         t = t > 127 ? 127 : t < -127 ? -127 : t;
         const int sum = isum32(t);
-        a.q[o][j] = (int8_t) t;
-        if (l32 == 0) { a.scale[o][g] = s; a.sums[o][g] = sum; }
+        a.q[o][bo + j] = (int8_t) t;
+        if (l32 == 0) { a.scale[o][bg + g] = s; a.sums[o][bg + g] = sum; }
     }
 }
 
@@ -688,7 +695,10 @@ extern "C" __global__ void sml_embed(const sml_kembed a) {
     const int ng = a.cols / 32, ns = (ng + 7) / 8;
     const int g = blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= ng) return;
-    const size_t row = (size_t) (a.pos ? a.tok[*a.pos] : *a.tok);
+    // a batch (pos NULL, grid y = rows): row b takes token tok[b] into x + b*cols
+    const int b = a.pos ? 0 : (int) blockIdx.y;
+    const size_t row = (size_t) (a.pos ? a.tok[*a.pos] : a.tok[b]);
+    float * x = a.x + (size_t) b * a.cols;
     uint8_t c[32];
     group_codes(a.m, a.nbits, a.cols, row, g, c);
     const uint8_t * f = a.m.sqmq + (row * ng + g) * 2;
@@ -697,7 +707,7 @@ extern "C" __global__ void sml_embed(const sml_kembed a) {
     const float mn = h2f(d[1]) * ((float) f[1] - 127.0f);
     for (int j = 0; j < 32; j++) {
         const int col = g * 32 + j;
-        a.x[a.perm ? a.perm[col] : col] = (float) c[j] * step + mn;
+        x[a.perm ? a.perm[col] : col] = (float) c[j] * step + mn;
     }
 }
 
@@ -1346,8 +1356,15 @@ __device__ void gemm_body(const sml_kgemm & a) {
                 y[orow[s]] = (g / (1.0f + expf(-g))) * u;     // sml/sml-run.c:451-454
             }
         } else {
+            const float * res = a.resid ? a.resid + (abase + t) * a.rows : nullptr;
             #pragma unroll
-            for (int s = 0; s < RB; s++) if (valid[s]) y[orow[s]] = acc[s][t];
+            for (int s = 0; s < RB; s++) {
+                if (!valid[s]) continue;
+                float v = acc[s][t];
+                if (a.bias) v += a.bias[orow[s]];
+                if (res) v = res[orow[s]] + v;
+                y[orow[s]] = v;
+            }
         }
     }
 }

@@ -249,6 +249,13 @@ size_t sml_hip_mat_bytes(const sml_hip_mat * m) { return m ? m->bytes : 0; }
 void op_normq(hipStream_t st, float * x, const float * resid, const float * w, float eps, int n,
               int nout, const int32_t * const * perm, int8_t * const * q, float * const * scale,
               int32_t * const * sums, float * normed, int per256) {
+    op_normq_rows(st, x, resid, w, eps, n, 1, nout, perm, q, scale, sums, normed, per256);
+}
+
+void op_normq_rows(hipStream_t st, float * x, const float * resid, const float * w, float eps, int n, int rows,
+                   int nout, const int32_t * const * perm, int8_t * const * q, float * const * scale,
+                   int32_t * const * sums, float * normed, int per256) {
+    if (rows < 1 || rows > 65535) hx_failf("normq of %d rows", rows);
     if (n <= 0 || n % 32 || n > 16384) hx_failf("normq width %d not supported", n);
     sml_knormq a;
     memset(&a, 0, sizeof a);
@@ -260,10 +267,10 @@ void op_normq(hipStream_t st, float * x, const float * resid, const float * w, f
         memset(&b, 0, sizeof b);
         b.x = x; b.norm_w = w; b.eps = eps; b.n = n; b.nout = nout;
         for (int i = 0; i < nout; i++) { b.perm[i] = perm[i]; b.q[i] = q[i]; b.scale[i] = scale[i]; b.sums[i] = sums[i]; }
-        hx_launch("sml_normq2", (unsigned) ((n + 255) / 256), 1, 256, 0, st, &b);
+        hx_launch("sml_normq2", (unsigned) ((n + 255) / 256), (unsigned) rows, 256, 0, st, &b);
         return;
     }
-    hx_launch("sml_normq", 1, 1, 1024, (size_t) n * 4, st, &a);
+    hx_launch("sml_normq", 1, (unsigned) rows, 1024, (size_t) n * 4, st, &a);
 }
 
 int sml_hip_normq(float * x, const float * resid, const float * w, float eps, int n,
@@ -428,10 +435,16 @@ int sml_hip_unpack(const sml_hip_mat * m, int row0, int nrows, uint8_t * out) {
 
 void op_embed(hipStream_t st, const sml_hip_mat * m, const int32_t * tok, const int32_t * pos,
               const int32_t * perm, float * x) {
+    op_embed_rows(st, m, tok, pos, 1, perm, x);
+}
+
+void op_embed_rows(hipStream_t st, const sml_hip_mat * m, const int32_t * tok, const int32_t * pos, int rows,
+                   const int32_t * perm, float * x) {
+    if (pos && rows != 1) hx_failf("a batch of embeddings takes its tokens directly");
     sml_kembed a;
     memset(&a, 0, sizeof a);
     a.m = m->k; a.nbits = m->nbits; a.cols = m->cols; a.tok = tok; a.pos = pos; a.perm = perm; a.x = x;
-    hx_launch("sml_embed", (unsigned) ((m->cols / 32 + 63) / 64), 1, 64, 0, st, &a);
+    hx_launch("sml_embed", (unsigned) ((m->cols / 32 + 63) / 64), (unsigned) rows, 64, 0, st, &a);
 }
 
 int sml_hip_embed(const sml_hip_mat * m, const int32_t * tok, const int32_t * perm, float * x) {
@@ -655,7 +668,8 @@ int gemm_mt(int m) { return m <= 1 ? 1 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
 
 void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
-             const int32_t * sums, float * y) {
+             const int32_t * sums, float * y, const float * bias, const float * resid) {
+    if (swiglu && (bias || resid)) hx_failf("SwiGLU GEMM takes no bias or residual");
     if (mt != 1 && mt != 4 && mt != 8 && mt != 16) hx_failf("small-M GEMM takes at most 16 rows");
     if (!count && (m_all < 1 || m_all > mt)) hx_failf("small-M GEMM of %d rows", m_all);
     if ((uint64_t) rows * (uint64_t) cols >= (1ull << 32)) hx_failf("matrix too large for one GEMM launch");
@@ -663,7 +677,7 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
     memset(&a, 0, sizeof a);
     a.mats = tab; a.nmat = swiglu ? 2 : 1; a.cols = cols; a.rows = rows;
     a.count = count; a.m_all = m_all; a.mmax = mmax;
-    a.q = q; a.scale = scale; a.sums = sums; a.y = y;
+    a.q = q; a.scale = scale; a.sums = sums; a.y = y; a.bias = bias; a.resid = resid;
     char name[40];
     snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d", nbits, swiglu ? "_s" : "", mt);
     const size_t lds = (size_t) mt * GEMM_TILE * (32 + 8);
@@ -675,7 +689,7 @@ int sml_hip_gemm(const sml_hip_mat * m, const int8_t * q, const float * scale, c
                  float * y) {
     OP_BEGIN(-1);
     if (!m || nrow < 1 || nrow > 16) hx_failf("gemm of %d rows (1..16)", nrow);
-    op_gemm(0, m->kdev, 1, 0, m->nbits, m->k.rows, m->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, y);
+    op_gemm(0, m->kdev, 1, 0, m->nbits, m->k.rows, m->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, y, NULL, NULL);
     HX_LEAVE();
     return 0;
 }
@@ -693,7 +707,7 @@ int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const 
     if (setjmp(jb)) { hx.jb = outer; hipFree(dt); longjmp(*outer, 1); }
     hx.jb = &jb;
     HX(hipMemcpy(dt, tab, sizeof tab, hipMemcpyHostToDevice));
-    op_gemm(0, dt, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h);
+    op_gemm(0, dt, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h, NULL, NULL);
     HX(hipStreamSynchronize(0));
     hx.jb = outer;
     HX(hipFree(dt));
@@ -911,12 +925,12 @@ void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out
     hx_launch("sml_moe_quant", (unsigned) T, (unsigned) m->nexp, 1024, 0, st, &qa);
     const int mt = gemm_mt(T);
     op_gemm(st, m->tab_gu, m->nexp, 1, m->nbits, m->n_ff, m->n_embd, m->count, 0, mt, m->tmax,
-            m->qx, m->sx, m->ux, m->h);
+            m->qx, m->sx, m->ux, m->h, NULL, NULL);
     sml_kmquant qb = qa;
     qb.src = m->h; qb.mode = 1; qb.perms = m->ptab_d; qb.n = m->n_ff; qb.q = m->qh; qb.scale = m->sh; qb.sums = m->uh;
     hx_launch("sml_moe_quant", (unsigned) T, (unsigned) m->nexp, 1024, 0, st, &qb);
     op_gemm(st, m->tab_d, m->nexp, 0, m->nbits, m->n_embd, m->n_ff, m->count, 0, mt, m->tmax,
-            m->qh, m->sh, m->uh, m->yd);
+            m->qh, m->sh, m->uh, m->yd, NULL, NULL);
     sml_kmoe_comb c;
     memset(&c, 0, sizeof c);
     c.y = m->yd; c.sel = m->sel; c.slot = m->slot; c.w = m->w; c.T = T; c.n = m->n_embd; c.k = m->k;

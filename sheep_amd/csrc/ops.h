@@ -50,13 +50,20 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
 // rows per group, at most mt (1, 4, 8 or 16).
 void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
-             const int32_t * sums, float * y);
+             const int32_t * sums, float * y, const float * bias, const float * resid);
 int gemm_mt(int m);
 // One matrix holding the rows of several FLAT records of one width and input
 // width, stacked in order (the q, k and v projections as one GEMV).
 sml_hip_mat * mat_stack(const ssf_file * f, const ssf_record * const * recs, int n);
 void op_embed(hipStream_t st, const sml_hip_mat * m, const int32_t * tok, const int32_t * pos,
               const int32_t * perm, float * x);
+// rows embeddings: row b of x [rows][cols] from token tok[b] (pos NULL)
+void op_embed_rows(hipStream_t st, const sml_hip_mat * m, const int32_t * tok, const int32_t * pos, int rows,
+                   const int32_t * perm, float * x);
+// op_normq over rows vectors: every pointer advances by n (scale, sums by n/32) per row
+void op_normq_rows(hipStream_t st, float * x, const float * resid, const float * w, float eps, int n, int rows,
+                   int nout, const int32_t * const * perm, int8_t * const * q, float * const * scale,
+                   int32_t * const * sums, float * normed, int per256);
 void op_attention(hipStream_t st, const float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
                   const float * cos_t, const float * sin_t, const int32_t * pos, int n_head, int n_kv,
                   int hd, int n_ctx, float * part, float * out, int8_t * q_out, float * s_out,

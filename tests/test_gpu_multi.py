@@ -1,0 +1,108 @@
+"""The multi-sequence step (sml_gpu_step_multi) on the GPU.
+
+In the exact regime every sequence's logits equal decoding it alone, bit for
+bit: the small-M GEMM gives each row the GEMV's arithmetic, and attention runs
+per sequence over its own KV slot. The single-sequence reference runs with
+the activation prologue fused but h quantized by its own launch (SML_FUSE=1),
+which is the same arithmetic the batched step uses.
+"""
+import numpy as np
+import pytest
+
+import sheep_amd as sa
+from oracle import bind as ob
+
+pytestmark = pytest.mark.gpu
+
+PROMPTS = [[5, 17, 300], [1], [42, 42, 7, 1999, 3], [250, 11]]
+
+
+def run_multi(path, n_vocab, steps):
+    d = sa.Decoder(path, n_ctx=64)
+    try:
+        d.slots(len(PROMPTS))
+        last = [d.prefill_slot(b, p, 0, n_vocab) for b, p in enumerate(PROMPTS)]
+        toks = [int(np.argmax(l)) for l in last]
+        pos = [len(p) for p in PROMPTS]
+        out = []
+        for _ in range(steps):
+            lg = d.step_multi(toks, pos, list(range(len(PROMPTS))), n_vocab)
+            out.append(lg)
+            toks = [int(np.argmax(l)) for l in lg]
+            pos = [p + 1 for p in pos]
+        return last, out
+    finally:
+        d.close()
+
+
+def run_alone(path, n_vocab, b, steps):
+    d = sa.Decoder(path, n_ctx=64)
+    try:
+        last = d.prefill(np.array(PROMPTS[b], np.int32), 0, n_vocab)
+        tok, pos, out = int(np.argmax(last)), len(PROMPTS[b]), []
+        for _ in range(steps):
+            lg = d.step(tok, pos, n_vocab)
+            out.append(lg)
+            tok, pos = int(np.argmax(lg)), pos + 1
+        return last, out
+    finally:
+        d.close()
+
+
+@pytest.mark.parametrize("kind", ["dense", "dense_perm", "moe"])
+def test_step_multi_equals_decoding_alone(tmp_path, kind, monkeypatch):
+    monkeypatch.setenv("SML_FUSE", "1")
+    p = tmp_path / f"{kind}.ssf"
+    extra = dict(n_expert=8, n_expert_used=2, moe_flags=1) if kind == "moe" else {}
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, qkv_bias=True,
+                   random_perm=kind == "dense_perm", seed=70, **extra)
+    steps = 6
+    m_last, m_out = run_multi(p, 2000, steps)
+    for b in range(len(PROMPTS)):
+        a_last, a_out = run_alone(p, 2000, b, steps)
+        np.testing.assert_array_equal(m_last[b], a_last, err_msg=f"prefill of slot {b}")
+        for i in range(steps):
+            np.testing.assert_array_equal(m_out[i][b], a_out[i], err_msg=f"sequence {b} step {i}")
+
+
+def test_step_multi_greedy_tokens_match_oracle(tmp_path):
+    p = tmp_path / "multi_orc.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, random_perm=True,
+                   seed=71)
+    steps = 10
+    _, m_out = run_multi(p, 2000, steps)
+    for b, prompt in enumerate(PROMPTS):
+        om = ob.OracleModel(p, 64)
+        try:
+            for i, t in enumerate(prompt):
+                lg = om.forward(t, i)
+            pos, tok = len(prompt), int(np.argmax(lg))
+            for i in range(steps):
+                ref = om.forward(tok, pos)
+                got = m_out[i][b]
+                assert np.corrcoef(got, ref)[0, 1] > 0.999, (b, i)
+                top = np.sort(ref)[-2:]
+                if top[1] - top[0] > 1e-2 * ref.std():
+                    assert int(np.argmax(got)) == int(np.argmax(ref)), (b, i)
+                tok, pos = int(np.argmax(got)), pos + 1
+        finally:
+            om.close()
+
+
+def test_step_multi_rejects_bad_arguments(tmp_path):
+    p = tmp_path / "multi_bad.ssf"
+    sa.synth_model(p, n_layer=1, n_embd=256, n_head=2, n_head_kv=1, n_ff=512, n_vocab=300, seed=72)
+    d = sa.Decoder(p, n_ctx=16)
+    try:
+        assert sa.lib().sml_gpu_slots(17) == 0
+        d.slots(2)
+        out = np.zeros((2, 300), np.float32)
+        I = sa.ctypes.c_int * 2
+        f = sa.lib().sml_gpu_step_multi
+        assert f(I(1, 2), I(0, 0), I(0, 0), 2, out.ctypes.data) == 0      # one slot twice
+        assert f(I(1, 2), I(0, 16), I(0, 1), 2, out.ctypes.data) == 0     # position past n_ctx
+        assert f(I(1, 300), I(0, 0), I(0, 1), 2, out.ctypes.data) == 0    # token past n_vocab
+        assert f(I(1, 2), I(0, 0), I(0, 2), 2, out.ctypes.data) == 0      # slot not allocated
+        assert f(I(1, 2), I(0, 0), I(0, 1), 2, out.ctypes.data) == 2
+    finally:
+        d.close()
