@@ -80,8 +80,10 @@ static struct {
     float * mx, * mqkv, * matt, * mh, * mxn, * mlog;
     int8_t * maq;
     float * mas;
-    int32_t * masum, * mtok, * mpos;
-    int32_t * mpin;            // pinned: tokens then positions of a batched step
+    int32_t * masum, * mtok, * mpos, * mslot;
+    int32_t * mpin;            // pinned: tokens, positions, slots of a batched step
+    uint16_t ** kc_tab, ** vc_tab;   // device tables of every slot's cache base
+    float * mpart;             // attention partials of every sequence of a batch
 } G;
 
 static int (*g_mid_fn)(float *, int, int);
@@ -614,9 +616,17 @@ int sml_gpu_slots(int ns) {
         G.masum = dalloc(R * wide / 32 * 4);
         G.mtok = dalloc(R * 4);
         G.mpos = dalloc(R * 4);
-        HX(hipHostMalloc((void **) &G.mpin, 2 * R * 4, 0));
+        G.mslot = dalloc(R * 4);
+        G.mpart = dalloc(R * sml_hip_attn_part_floats(G.H, G.hd, G.n_ctx) * 4);
+        G.kc_tab = dalloc(R * sizeof(void *));
+        G.vc_tab = dalloc(R * sizeof(void *));
+        HX(hipHostMalloc((void **) &G.mpin, 3 * R * 4, 0));
     }
     if (ns > G.nslot) G.nslot = ns;
+    G.kcs[0] = G.kc;
+    G.vcs[0] = G.vc;
+    HX(hipMemcpy(G.kc_tab, G.kcs, MAX_SLOTS * sizeof(void *), hipMemcpyHostToDevice));
+    HX(hipMemcpy(G.vc_tab, G.vcs, MAX_SLOTS * sizeof(void *), hipMemcpyHostToDevice));
     HX(hipDeviceSynchronize());
     HX_LEAVE();
     return ns;
@@ -649,7 +659,7 @@ const float * sml_gpu_prefill_slot(int slot, const int * ids, int pos0, int n) {
     return G.lg_host;
 }
 
-static void launch_multi(int ns, const int * slot) {
+static void launch_multi(int ns) {
     const size_t kvd = (size_t) G.KV * G.hd, qkv = (size_t) (G.H + 2 * G.KV) * G.hd, hq = (size_t) G.H * G.hd;
     const int mt = gemm_mt(ns);
     op_embed_rows(G.st, G.emb, G.mtok, NULL, ns, pdev(G.perm_emb), G.mx);
@@ -664,14 +674,9 @@ static void launch_multi(int ns, const int * slot) {
         op_gemm(G.st, y->qkv->kdev, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
                 G.mqkv, y->bias_qkv, NULL);
         const int fuse_q = y->perm_o < 0;
-        for (int b = 0; b < ns; b++) {
-            const float * q = G.mqkv + (size_t) b * qkv;
-            uint16_t * kc = slot[b] ? G.kcs[slot[b]] : G.kc, * vc = slot[b] ? G.vcs[slot[b]] : G.vc;
-            op_attention(G.st, q, q + hq, q + hq + kvd, kc + (size_t) L * G.n_ctx * kvd, vc + (size_t) L * G.n_ctx * kvd,
-                         G.rc, G.rs, G.mpos + b, G.H, G.KV, G.hd, G.n_ctx, G.part, G.matt + (size_t) b * hq,
-                         fuse_q ? G.maq + (size_t) b * hq : NULL, fuse_q ? G.mas + (size_t) b * hq / 32 : NULL,
-                         fuse_q ? G.masum + (size_t) b * hq / 32 : NULL);
-        }
+        op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, G.mslot, (size_t) L * G.n_ctx * kvd,
+                           G.rc, G.rs, G.mpos, ns, G.H, G.KV, G.hd, G.n_ctx, G.mpart, G.matt,
+                           fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL);
         if (!fuse_q) {
             pp[0] = pdev(y->perm_o);
             op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, 0);
@@ -710,9 +715,11 @@ int sml_gpu_step_multi(const int * tok, const int * pos, const int * slot, int n
     HX_ENTRY(0);
     memcpy(G.mpin, tok, (size_t) ns * 4);
     memcpy(G.mpin + MAX_SLOTS, pos, (size_t) ns * 4);
+    memcpy(G.mpin + 2 * MAX_SLOTS, slot, (size_t) ns * 4);
     HX(hipMemcpyAsync(G.mtok, G.mpin, (size_t) ns * 4, hipMemcpyHostToDevice, G.st));
     HX(hipMemcpyAsync(G.mpos, G.mpin + MAX_SLOTS, (size_t) ns * 4, hipMemcpyHostToDevice, G.st));
-    launch_multi(ns, slot);
+    HX(hipMemcpyAsync(G.mslot, G.mpin + 2 * MAX_SLOTS, (size_t) ns * 4, hipMemcpyHostToDevice, G.st));
+    launch_multi(ns);
     HX(hipMemcpyAsync(logits_out, G.mlog, (size_t) ns * G.V * 4, hipMemcpyDeviceToHost, G.st));
     HX(hipStreamSynchronize(G.st));
     HX_LEAVE();

@@ -61,8 +61,13 @@ hipFunction_t hx_fn(const char * name) {
 
 void hx_launch(const char * name, unsigned gx, unsigned gy, unsigned bx, size_t shmem,
                hipStream_t st, void * args) {
+    hx_launch3(name, gx, gy, 1, bx, shmem, st, args);
+}
+
+void hx_launch3(const char * name, unsigned gx, unsigned gy, unsigned gz, unsigned bx, size_t shmem,
+                hipStream_t st, void * args) {
     void * params[] = { args };
-    HX(hipModuleLaunchKernel(hx_fn(name), gx, gy, 1, bx, 1, 1, (unsigned) shmem, st, params, NULL));
+    HX(hipModuleLaunchKernel(hx_fn(name), gx, gy, gz, bx, 1, 1, (unsigned) shmem, st, params, NULL));
 }
 
 void * hx_malloc(size_t n) {

@@ -46,4 +46,7 @@ void hx_init(int device);
 hipFunction_t hx_fn(const char * name);
 void hx_launch(const char * name, unsigned gx, unsigned gy, unsigned bx, size_t shmem,
                hipStream_t st, void * args);
+// the same with a z dimension to the grid
+void hx_launch3(const char * name, unsigned gx, unsigned gy, unsigned gz, unsigned bx, size_t shmem,
+                hipStream_t st, void * args);
 void * hx_malloc(size_t n);

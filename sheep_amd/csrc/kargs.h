@@ -116,6 +116,15 @@ typedef struct {
     int32_t * u_out;
     int n_head, n_kv, nsplit;
     float inv;
+    // A batch of sequences (grid z): sequence b reads q, k, v at + b * qkv_stride
+    // and position pos[b], uses the cache of its slot (kc_slots[slot[b]] +
+    // layer_off when kc_slots is not NULL, else kcache/vcache), and writes part,
+    // out and the quantized out at + b times their per-sequence size.
+    int qkv_stride;
+    uint16_t * const * kc_slots;
+    uint16_t * const * vc_slots;
+    const int32_t * slot;
+    size_t layer_off;
 } sml_kattn;
 
 

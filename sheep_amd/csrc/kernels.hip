@@ -734,7 +734,14 @@ extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_ka
     __shared__ float mx_s[ATTN_MAXREP], l_s[ATTN_MAXREP];
     const int kh = blockIdx.y, split = blockIdx.x, tid = threadIdx.x;
     const int rep = a.n_head / a.n_kv, kvd = a.n_kv * HD, half = HD / 2;
-    const int pos = *a.pos, T = pos + 1, t0 = split * ATTN_CHUNK;
+    // sequence blockIdx.z of a batch
+    const int b = blockIdx.z;
+    const float * aq = a.q + (size_t) b * a.qkv_stride, * ak = a.k + (size_t) b * a.qkv_stride,
+                * av = a.v + (size_t) b * a.qkv_stride;
+    uint16_t * kcache = a.kc_slots ? a.kc_slots[a.slot[b]] + a.layer_off : a.kcache;
+    uint16_t * vcache = a.vc_slots ? a.vc_slots[a.slot[b]] + a.layer_off : a.vcache;
+    float * apart = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
+    const int pos = a.pos[b], T = pos + 1, t0 = split * ATTN_CHUNK;
     if (t0 >= T) return;
     const int t1 = min(T, t0 + ATTN_CHUNK);
     // every K and V load of this lane first (one round trip for the chunk):
@@ -745,14 +752,14 @@ extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_ka
     for (int i = 0; i < ATTN_CHUNK / 16; i++) {
         int t = t0 + grp + 16 * i;
         t = t < t1 ? t : t0;                          // in range; masked below
-        kw[i] = __builtin_nontemporal_load((const v4u *) (a.kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
-        vw[i] = __builtin_nontemporal_load((const v4u *) (a.vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
+        kw[i] = __builtin_nontemporal_load((const v4u *) (kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
+        vw[i] = __builtin_nontemporal_load((const v4u *) (vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
     }
     const float * cs = a.cos_t + (size_t) pos * half, * sn = a.sin_t + (size_t) pos * half;
     // RoPE of this kv head's query heads (halved pairs, sml/sml-run.c:363-368)
     for (int i = tid; i < rep * half; i += ATTN_THREADS) {
         const int j = i / half, d = i % half;
-        const float * v = a.q + (size_t) (kh * rep + j) * HD;
+        const float * v = aq + (size_t) (kh * rep + j) * HD;
         const float x0 = v[d], x1 = v[d + half];
         qs[j][d] = x0 * cs[d] - x1 * sn[d];
         qs[j][d + half] = x0 * sn[d] + x1 * cs[d];
@@ -760,17 +767,17 @@ extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_ka
     const bool has_pos = t0 <= pos && pos < t1;
     if (has_pos) {
         // k rotated, then rounded to fp16 as the cache stores it (sml/sml-run.c:3414-3415)
-        uint16_t * kc = a.kcache + (size_t) pos * kvd + (size_t) kh * HD;
-        uint16_t * vc = a.vcache + (size_t) pos * kvd + (size_t) kh * HD;
+        uint16_t * kc = kcache + (size_t) pos * kvd + (size_t) kh * HD;
+        uint16_t * vc = vcache + (size_t) pos * kvd + (size_t) kh * HD;
         if (tid < half) {
-            const float * v = a.k + (size_t) kh * HD;
+            const float * v = ak + (size_t) kh * HD;
             const float x0 = v[tid], x1 = v[tid + half];
             const uint16_t h0 = f2h(x0 * cs[tid] - x1 * sn[tid]), h1 = f2h(x0 * sn[tid] + x1 * cs[tid]);
             kc[tid] = h0; kc[tid + half] = h1;
             kp[tid] = h2f(h0); kp[tid + half] = h2f(h1);
         } else if (tid < half + HD) {
             const int d = tid - half;
-            const uint16_t h = f2h(a.v[(size_t) kh * HD + d]);
+            const uint16_t h = f2h(av[(size_t) kh * HD + d]);
             vc[d] = h;
             vp[d] = h2f(h);
         }
@@ -856,7 +863,7 @@ extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_ka
     __syncthreads();
     for (int i = tid; i < rep * HD; i += ATTN_THREADS) {
         const int j = i / HD, d = i % HD;
-        float * part = a.part + ((size_t) (kh * rep + j) * a.nsplit + split) * (HD + 2);
+        float * part = apart + ((size_t) (kh * rep + j) * a.nsplit + split) * (HD + 2);
         part[d] = red[0][j][d] + red[1][j][d] + red[2][j][d] + red[3][j][d];
         if (d == 0) { part[HD] = mx_s[j]; part[HD + 1] = l_s[j]; }
     }
@@ -870,9 +877,10 @@ extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_ka
 extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn a) {
     __shared__ float em[64], ls[64];
     __shared__ float lsum;
-    const int h = blockIdx.x, d = threadIdx.x;
-    const int T = *a.pos + 1, nact = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    const float * p = a.part + (size_t) h * a.nsplit * (HD + 2);
+    const int h = blockIdx.x, d = threadIdx.x, b = blockIdx.z;     // head, dim, sequence
+    const int T = a.pos[b] + 1, nact = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    const float * p = a.part + ((size_t) b * a.n_head + h) * a.nsplit * (HD + 2);
+    const size_t ob = (size_t) b * a.n_head * HD;
     for (int s2 = d; s2 < nact; s2 += HD) { em[s2] = p[(size_t) s2 * (HD + 2) + HD]; ls[s2] = p[(size_t) s2 * (HD + 2) + HD + 1]; }
     __syncthreads();
     if (d == 0) {
@@ -887,7 +895,7 @@ extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn 
     #pragma unroll 8
     for (int s2 = 0; s2 < nact; s2++) o += em[s2] * p[(size_t) s2 * (HD + 2) + d];
     const float r = o / lsum;
-    a.out[(size_t) h * HD + d] = r;
+    a.out[ob + (size_t) h * HD + d] = r;
     if (!a.q_out) return;
     const float amax = max32(fabsf(r));
     const float s = amax / 127.0f;
@@ -897,8 +905,8 @@ extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn 
     t = t > 127 ? 127 : t < -127 ? -127 : t;
     const int sum = isum32(t);
     const int g = h * 4 + (d >> 5);
-    a.q_out[(size_t) h * HD + d] = (int8_t) t;
-    if ((d & 31) == 0) { a.s_out[g] = s; a.u_out[g] = sum; }
+    a.q_out[ob + (size_t) h * HD + d] = (int8_t) t;
+    if ((d & 31) == 0) { a.s_out[ob / 32 + g] = s; a.u_out[ob / 32 + g] = sum; }
 }
 
 // ---------------------------------------------------------------- argmax

@@ -478,6 +478,26 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
 }
 
+void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
+                        uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
+                        const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
+                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out) {
+    if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
+        hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
+    if (nseq < 1 || nseq > 65535) hx_failf("attention batch of %d", nseq);
+    const int ns = (n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    sml_kattn a;
+    memset(&a, 0, sizeof a);
+    a.q = qkv; a.k = qkv + (size_t) n_head * hd; a.v = a.k + (size_t) n_kv * hd;
+    a.qkv_stride = qkv_stride; a.kc_slots = kc_slots; a.vc_slots = vc_slots; a.slot = slot; a.layer_off = layer_off;
+    a.cos_t = cos_t; a.sin_t = sin_t; a.pos = pos;
+    a.part = part; a.out = out; a.q_out = q_out; a.s_out = s_out; a.u_out = u_out;
+    a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
+    a.inv = 1.0f / __builtin_sqrtf((float) hd);
+    hx_launch3("sml_attn", (unsigned) ns, (unsigned) n_kv, (unsigned) nseq, 256, 0, st, &a);
+    hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
+}
+
 int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,
                       const float * cos_t, const float * sin_t, const int32_t * pos,
                       int n_head, int n_kv, int hd, int n_ctx, float * part, float * out) {

@@ -68,6 +68,14 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
                   const float * cos_t, const float * sin_t, const int32_t * pos, int n_head, int n_kv,
                   int hd, int n_ctx, float * part, float * out, int8_t * q_out, float * s_out,
                   int32_t * u_out);
+// Attention for nseq sequences in one launch: sequence b's q, k, v at
+// qkv + b * qkv_stride (q, then k, then v), its cache kc_slots[slot[b]] +
+// layer_off, its position pos[b]; part, out and the quantized out hold one
+// sequence's worth per b.
+void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
+                        uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
+                        const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
+                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out);
 void op_argmax(hipStream_t st, const float * logits, int n, int32_t * tok, int32_t * pos, int32_t * hist,
                int hist_n);
 void op_advance(hipStream_t st, int32_t * pos);
