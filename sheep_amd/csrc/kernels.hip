@@ -1386,3 +1386,167 @@ __device__ void gemm_body(const sml_kgemm & a) {
     }
 #define GEMM_WIDTH(NB) GEMM_KERNEL(NB, 1) GEMM_KERNEL(NB, 4) GEMM_KERNEL(NB, 8) GEMM_KERNEL(NB, 16)
 GEMM_WIDTH(2) GEMM_WIDTH(3) GEMM_WIDTH(4) GEMM_WIDTH(5) GEMM_WIDTH(6) GEMM_WIDTH(7) GEMM_WIDTH(8)
+
+// ---------------------------------------------------------------- small-M GEMM on MFMA (Q4)
+//
+// The same product as gemm_body for up to 16 activation rows, with the
+// per-group integer dots on v_mfma_i32_16x16x32_i8: A = 16 weight rows x 32
+// codes of one group, B = 32 activation codes x 16 activation rows. Lane l
+// holds A row l%16 / B column l%16 for codes 8*(l/16)..+7, and receives the
+// dots of weight rows 4*(l/16)..+3 for activation row l%16 -- where the
+// per-group epilogue step*s*dot + min*s*sum runs in fp32. In the Q4 plane an
+// 8-byte word at quad q, half h, offset 8*(l/16) holds those codes of groups
+// 4q+2h (low nibbles) and 4q+2h+1 (high nibbles), so one load feeds two
+// MFMAs. Activations are read from L2 (each lane's 8-byte B words), not
+// staged. A workgroup owns RB blocks of 16 rows (SwiGLU: the gate and up
+// blocks of the same rows); its 4 waves split the groups and their partial
+// sums meet in LDS, added in wave order. The float order differs from the
+// GEMV's, so rows agree with it to rounding, not bit for bit.
+#define MG_U 4            // group pairs whose loads are issued together
+template <bool SW, int RB>
+__device__ void mgemm_q4_body(const sml_kgemm & a) {
+    typedef long v1l;
+    constexpr int NM = SW ? 2 : 1, NACC = NM * RB * 4;
+    __shared__ float red[4][NACC][64];
+    const int e = blockIdx.y;
+    const int m = a.count ? a.count[e] : a.m_all;
+    if (m <= 0) return;
+    const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8, np = ng / 2;
+    const int tid = threadIdx.x, lane = tid & 63, c = lane >> 4, i16 = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb0 = blockIdx.x * (16 * RB);                       // first row of this workgroup
+    const int p0 = wave * np / 4, p1 = (wave + 1) * np / 4;      // this wave's group pairs
+    const sml_kmat * mt = a.mats + (size_t) e * (SW ? 2 : 1);
+    const size_t abase = (size_t) e * a.mmax;
+    const uint8_t * plane[NM];
+    const uint8_t * fqb[NM];
+    const uint8_t * fdb[NM];
+    #pragma unroll
+    for (int k = 0; k < NM; k++) { plane[k] = mt[k].plane[0]; fqb[k] = mt[k].sqmq; fdb[k] = (const uint8_t *) mt[k].sdmd; }
+    const uint32_t rowb = (uint32_t) n / 2;                       // nibble-plane bytes per row
+    // A rows of this lane (clamped in range; rows past the end are never stored)
+    uint32_t aoff[RB];
+    uint32_t fqo[RB][4], fdo[RB][4];                              // field offsets of the lane's 4 result rows
+    #pragma unroll
+    for (int bk = 0; bk < RB; bk++) {
+        const int ra = rb0 + bk * 16 + i16;
+        aoff[bk] = (uint32_t) (ra < a.rows ? ra : a.rows - 1) * rowb + 8u * (uint32_t) c;
+        #pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rd = rb0 + bk * 16 + 4 * c + r;
+            const uint32_t rc = (uint32_t) (rd < a.rows ? rd : a.rows - 1);
+            fqo[bk][r] = rc * (uint32_t) ng * 2u;
+            fdo[bk][r] = rc * (uint32_t) ns * 4u;
+        }
+    }
+    // B: activation row i16 (zero past m)
+    const bool tv = i16 < m;
+    const size_t ar = abase + (size_t) (tv ? i16 : 0);
+    const int8_t * qrow = a.q + ar * n + 8 * c;
+    const float * srow = a.scale + ar * ng;
+    const int32_t * urow = a.sums + ar * ng;
+    float acc[NM][RB][4];
+    #pragma unroll
+    for (int k = 0; k < NM; k++)
+        #pragma unroll
+        for (int bk = 0; bk < RB; bk++)
+            #pragma unroll
+            for (int r = 0; r < 4; r++) acc[k][bk][r] = 0.0f;
+    for (int pb = p0; pb < p1; pb += MG_U) {
+        // loads of MG_U group pairs: A words, B words, activation scales, fields
+        v2u aw[MG_U][NM][RB];
+        v1l bw[MG_U][2];
+        float sv[MG_U][2];
+        int32_t uv[MG_U][2];
+        uint32_t fq[MG_U][NM][RB][4], fd[MG_U][NM][RB][4];
+        #pragma unroll
+        for (int p = 0; p < MG_U; p++) {
+            const int pc = pb + p < p1 ? pb + p : p1 - 1;
+            const int gc = 2 * pc;
+            const uint32_t boff = (uint32_t) (gc >> 2) * 64u + (uint32_t) ((gc >> 1) & 1) * 32u;
+            #pragma unroll
+            for (int k = 0; k < NM; k++)
+                #pragma unroll
+                for (int bk = 0; bk < RB; bk++) {
+                    aw[p][k][bk] = __builtin_nontemporal_load((const v2u *) (plane[k] + (aoff[bk] + boff)));
+                    #pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        fq[p][k][bk][r] = *(const uint32_t *) (fqb[k] + (fqo[bk][r] + (uint32_t) gc * 2u));
+                        fd[p][k][bk][r] = *(const uint32_t *) (fdb[k] + (fdo[bk][r] + (uint32_t) (gc >> 3) * 4u));
+                    }
+                }
+            #pragma unroll
+            for (int h = 0; h < 2; h++) {
+                bw[p][h] = *(const v1l *) (qrow + (size_t) (gc + h) * 32);
+                sv[p][h] = srow[gc + h];
+                uv[p][h] = urow[gc + h];
+            }
+        }
+        #pragma unroll
+        for (int p = 0; p < MG_U; p++) {
+            if (pb + p < p1) {
+                #pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const v1l b = tv ? bw[p][h] : 0;
+                    const float s = tv ? sv[p][h] : 0.0f;
+                    const float ss = s * (float) uv[p][h];
+                    #pragma unroll
+                    for (int k = 0; k < NM; k++)
+                        #pragma unroll
+                        for (int bk = 0; bk < RB; bk++) {
+                            const v2u w = aw[p][k][bk];
+                            const v2u cd = h ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
+                            const v1l av = (v1l) (((unsigned long) cd.y << 32) | cd.x);
+                            v4i d = { 0, 0, 0, 0 };
+                            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, d, 0, 0, 0);
+                            #pragma unroll
+                            for (int r = 0; r < 4; r++) {
+                                const uint32_t f = fq[p][k][bk][r] >> (16 * h), d2 = fd[p][k][bk][r];
+                                const float wsc = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
+                                const float wmn = h2f((uint16_t) (d2 >> 16)) * ((float) ((f >> 8) & 0xFFu) - 127.0f);
+                                acc[k][bk][r] += wsc * (s * (float) d[r]);
+                                acc[k][bk][r] += wmn * ss;
+                            }
+                        }
+                }
+            }
+        }
+    }
+    // the 4 waves' partial sums, added in wave order
+    #pragma unroll
+    for (int k = 0; k < NM; k++)
+        #pragma unroll
+        for (int bk = 0; bk < RB; bk++)
+            #pragma unroll
+            for (int r = 0; r < 4; r++) red[wave][(k * RB + bk) * 4 + r][lane] = acc[k][bk][r];
+    __syncthreads();
+    if (wave != 0 || !tv) return;
+    float * y = a.y + (abase + i16) * a.rows;
+    const float * res = a.resid ? a.resid + (abase + i16) * a.rows : nullptr;
+    #pragma unroll
+    for (int bk = 0; bk < RB; bk++)
+        #pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = rb0 + bk * 16 + 4 * c + r;
+            if (row >= a.rows) continue;
+            float t[NM];
+            #pragma unroll
+            for (int k = 0; k < NM; k++) {
+                const int j = (k * RB + bk) * 4 + r;
+                t[k] = ((red[0][j][lane] + red[1][j][lane]) + red[2][j][lane]) + red[3][j][lane];
+            }
+            if constexpr (SW) {
+                y[row] = (t[0] / (1.0f + expf(-t[0]))) * t[1];           // sml/sml-run.c:451-454
+            } else {
+                float v = t[0];
+                if (a.bias) v += a.bias[row];
+                if (res) v = res[row] + v;
+                y[row] = v;
+            }
+        }
+}
+
+extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_r1(const sml_kgemm a) { mgemm_q4_body<false, 1>(a); }
+extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_r2(const sml_kgemm a) { mgemm_q4_body<false, 2>(a); }
+extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_s_r1(const sml_kgemm a) { mgemm_q4_body<true, 1>(a); }
+extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_s_r2(const sml_kgemm a) { mgemm_q4_body<true, 2>(a); }

@@ -699,6 +699,18 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
     a.count = count; a.m_all = m_all; a.mmax = mmax;
     a.q = q; a.scale = scale; a.sums = sums; a.y = y; a.bias = bias; a.resid = resid;
     char name[40];
+    // Q4 with more than 8 activation rows runs on MFMA (measured faster there;
+    // below, the VALU dot4 kernel wins) unless the exact regime is asked for
+    // (SML_MULTI=exact: every row bit for bit the GEMV's). Expert groups
+    // (count != NULL) hold few rows each and stay on VALU.
+    const char * mode = getenv("SML_MULTI");
+    const int exact = mode && !strcmp(mode, "exact");
+    if (nbits == 4 && !count && m_all > 8 && !exact) {
+        const int rb = !swiglu && rows >= 32768 ? 2 : 1;
+        snprintf(name, sizeof name, "sml_mgemm_q4%s_r%d", swiglu ? "_s" : "", rb);
+        hx_launch(name, (unsigned) ((rows + 16 * rb - 1) / (16 * rb)), (unsigned) ngroups, 256, 0, st, &a);
+        return;
+    }
     snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d", nbits, swiglu ? "_s" : "", mt);
     const size_t lds = (size_t) mt * GEMM_TILE * (32 + 8);
     // 4 waves x 2 rows (SwiGLU: 2 gate/up pairs) per workgroup

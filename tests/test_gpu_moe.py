@@ -41,7 +41,9 @@ def quant_rows(xs):
 
 @pytest.mark.parametrize("nb", [4, 3, 6, 8])
 @pytest.mark.parametrize("cols", [1536, 5120])
-def test_gemm_rows_equal_gemv(tmpdir_s, nb, cols):
+def test_gemm_rows_equal_gemv(tmpdir_s, nb, cols, monkeypatch):
+    """The exact regime (SML_MULTI=exact): each row bit for bit the GEMV's."""
+    monkeypatch.setenv("SML_MULTI", "exact")
     p = tmpdir_s / f"gemm{nb}_{cols}.ssf"
     if not p.exists():
         sa.synth_matrix(p, 1000, cols, nbits=nb, random_perm=False, seed=300 + nb)
@@ -62,6 +64,25 @@ def test_gemm_rows_equal_gemv(tmpdir_s, nb, cols):
             sa.matvec(m, act, y1)
             np.testing.assert_array_equal(got[r], y1.read(np.float32), err_msg=f"row {r} of {nrow}")
             close(got[r], ob.matvec(t, *ob.quantize_act(xs[r])), f"gemm q{nb} row {r}")
+
+
+@pytest.mark.parametrize("cols,rows", [(1536, 1000), (5120, 2048), (4096, 40000)])
+def test_mfma_gemm_q4(tmpdir_s, cols, rows):
+    """Q4 with more than 8 rows on MFMA: each row within 1e-3 of the oracle."""
+    p = tmpdir_s / f"mg_{cols}_{rows}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, rows, cols, nbits=4, random_perm=False, seed=400 + cols)
+    t = SSF(p)["w"]
+    m = sa.Mat.from_file(p, "w")
+    rng = np.random.default_rng(cols)
+    for nrow in (9, 16):
+        xs = [rng.standard_normal(cols).astype(np.float32) * (1 + r) for r in range(nrow)]
+        q, s, u = quant_rows(xs)
+        y = sa.DevBuf(nrow * rows * 4)
+        sa.gemm(m, q, s, u, nrow, y)
+        got = y.read(np.float32).reshape(nrow, rows)
+        for r in range(nrow):
+            close(got[r], ob.matvec(t, *ob.quantize_act(xs[r])), f"mfma gemm row {r} of {nrow}")
 
 
 def test_gemm_swiglu_rows(tmpdir_s):

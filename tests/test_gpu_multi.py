@@ -52,6 +52,7 @@ def run_alone(path, n_vocab, b, steps):
 @pytest.mark.parametrize("kind", ["dense", "dense_perm", "moe"])
 def test_step_multi_equals_decoding_alone(tmp_path, kind, monkeypatch):
     monkeypatch.setenv("SML_FUSE", "1")
+    monkeypatch.setenv("SML_MULTI", "exact")
     p = tmp_path / f"{kind}.ssf"
     extra = dict(n_expert=8, n_expert_used=2, moe_flags=1) if kind == "moe" else {}
     sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, qkv_bias=True,
@@ -63,6 +64,24 @@ def test_step_multi_equals_decoding_alone(tmp_path, kind, monkeypatch):
         np.testing.assert_array_equal(m_last[b], a_last, err_msg=f"prefill of slot {b}")
         for i in range(steps):
             np.testing.assert_array_equal(m_out[i][b], a_out[i], err_msg=f"sequence {b} step {i}")
+
+
+@pytest.mark.parametrize("kind", ["dense", "moe"])
+def test_step_multi_default_regime_close_to_alone(tmp_path, kind):
+    """The default batched regime (Q4 rows on MFMA) agrees with decoding alone
+    to float rounding: same greedy tokens, logits correlated to 0.9999."""
+    p = tmp_path / f"{kind}_mfma.ssf"
+    extra = dict(n_expert=8, n_expert_used=2, moe_flags=1) if kind == "moe" else {}
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, seed=73, **extra)
+    steps = 6
+    m_last, m_out = run_multi(p, 2000, steps)
+    for b in range(len(PROMPTS)):
+        a_last, a_out = run_alone(p, 2000, b, steps)
+        for i in range(steps):
+            assert np.corrcoef(m_out[i][b], a_out[i])[0, 1] > 0.9999, (b, i)
+            top = np.sort(a_out[i])[-2:]
+            if top[1] - top[0] > 1e-2 * a_out[i].std():
+                assert int(np.argmax(m_out[i][b])) == int(np.argmax(a_out[i])), (b, i)
 
 
 def test_step_multi_greedy_tokens_match_oracle(tmp_path):
