@@ -146,6 +146,89 @@ def traffic(path, work):
                "copy_bytes": COPY_BYTES, "fetch_scale": round(f_fetch, 4), "write_scale": round(f_write, 4)}
 
 
+def width_sweep(tmp, target_bytes=6e8, iters=200):
+    """The fused GEMV at every SSF width and the GPTQ-style 4-bit layout, at
+    4096 x 14336 and 14336 x 4096, over rotating copies (> the 256 MB MALL)."""
+    from sheep_amd import gptq as gq
+    out = {}
+    x_cache = {}
+    for rows, cols in ((4096, 14336), (14336, 4096)):
+        for nb in (2, 3, 4, 5, 6, 8):
+            p = os.path.join(tmp, f"sweep_q{nb}_{rows}x{cols}.ssf")
+            sa.synth_matrix(p, rows, cols, nbits=nb, seed=1004)
+            first = sa.Mat.from_file(p, "w")
+            mats = [first] + [sa.Mat.from_file(p, "w") for _ in range(max(1, int(target_bytes // first.bytes)))]
+            x = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
+            act = sa.Act(cols)
+            sa.normq(sa.DevBuf.of(x), act)
+            y = sa.DevBuf(rows * 4)
+            arr = (sa.c_void_p * len(mats))(*[m.h for m in mats])
+            ms = sa.c_float()
+            lib = sa.lib()
+            assert lib.sml_hip_time_matvec(arr, len(mats), act.q.ptr, act.scale.ptr, act.sums.ptr, y.ptr, len(mats),
+                                           sa.ctypes.byref(ms)) == 0
+            t = []
+            for _ in range(3):
+                assert lib.sml_hip_time_matvec(arr, len(mats), act.q.ptr, act.scale.ptr, act.sums.ptr, y.ptr, iters,
+                                               sa.ctypes.byref(ms)) == 0
+                t.append(ms.value * 1000.0 / iters)
+            us = float(np.median(t))
+            out[f"q{nb}_{rows}x{cols}"] = {"us": round(us, 3), "bytes": first.bytes,
+                                           "GB/s": round(first.bytes / us / 1e3, 1)}
+            for m in mats:
+                m.free()
+            os.remove(p)
+        qw, qz, sc = gq.synth(rows, cols, seed=1004)
+        first = gq.GptqMat(qw, qz, sc, rows, cols)
+        mats = [first] + [gq.GptqMat(qw, qz, sc, rows, cols) for _ in range(max(1, int(target_bytes // first.bytes)))]
+        xd = sa.DevBuf.of(np.random.default_rng(0).standard_normal(cols).astype(np.float32))
+        y = sa.DevBuf(rows * 4)
+        gq.time_matvec(mats, xd, y, len(mats))
+        us = float(np.median([gq.time_matvec(mats, xd, y, iters) * 1000.0 / iters for _ in range(3)]))
+        out[f"gptq4_{rows}x{cols}"] = {"us": round(us, 3), "bytes": first.bytes, "GB/s": round(first.bytes / us / 1e3, 1)}
+        for m in mats:
+            m.free()
+    return out
+
+
+def moe_layer(tmp, T=16, iters=50):
+    """A Mixtral-shaped MoE FFN layer (hidden 4096, 8 experts of 14336 SwiGLU
+    Q4, top-2 softmax over the chosen, f32 router) on T tokens of N(0,1)
+    input: time per step and the bytes of the experts the step touches."""
+    p = os.path.join(tmp, "mixtral_layer.ssf")
+    sa.synth_model(p, n_layer=1, n_embd=4096, n_head=32, n_head_kv=8, n_ff=14336, n_vocab=1024, n_expert=8,
+                   n_expert_used=2, moe_flags=1, rope_theta=1e6, seed=1005)
+    moe = sa.MoE(p, 0, 16)
+    x = sa.DevBuf.of(np.random.default_rng(1005).standard_normal((T, 4096)).astype(np.float32))
+    out = sa.DevBuf(T * 4096 * 4)
+    moe.time(x, T, out, 3)
+    ms, cnt = moe.time(x, T, out, iters)
+    us = ms * 1000.0 / iters
+    touched = int((cnt > 0).sum())
+    b = touched * moe.expert_bytes + moe.nexp * 4096 * 4
+    moe.free()
+    os.remove(p)
+    return {"tokens": T, "us_per_step": round(us, 2), "experts_touched": touched, "tokens_per_expert": cnt.tolist(),
+            "bytes_per_step": b, "GB/s": round(b / us / 1e3, 1)}
+
+
+def batched_decode(dec, n_vocab, ns=16, steps=20, pos0=1024):
+    """Aggregate tokens/s of ns sequences stepped together (sml_gpu_step_multi)
+    at positions pos0.. of their own KV slots."""
+    dec.slots(ns)
+    for b in range(ns):
+        dec.prefill_slot(b, (np.arange(8, dtype=np.int32) * 7 + b) % n_vocab, pos0 - 8, n_vocab)
+    toks = list(range(1, ns + 1))
+    dec.step_multi(toks, [pos0] * ns, list(range(ns)), n_vocab)
+    sa.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        dec.step_multi(toks, [pos0 + 1 + i] * ns, list(range(ns)), n_vocab)
+    dt = time.perf_counter() - t0
+    return {"sequences": ns, "ms_per_step": round(dt / steps * 1e3, 3), "tokens_per_s": round(ns * steps / dt, 1),
+            "positions": f"{pos0 + 1}..{pos0 + steps}"}
+
+
 def cpu_baseline(path, threads, budget_s=12.0, max_tokens=1200):
     """The reference's own CPU decode (sml_forward on its pool threads,
     compiled from its sources into oracle/_ref) on the same model file, from
@@ -178,6 +261,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemv-only", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
+    ap.add_argument("--no-extra", action="store_true", help="skip the batched, MoE and width-sweep lines")
     ap.add_argument("--pmc-probe", metavar="SSF", help=argparse.SUPPRESS)
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: fill the 4096 context)")
@@ -251,7 +335,20 @@ def run(a, work):
     sa.sync()
     dt = time.perf_counter() - t1
     ev_ms = dec.last_ms()
+    extra = {}
+    if not a.gemv_only and not a.no_extra:
+        t1 = time.perf_counter()
+        extra["batched_decode"] = batched_decode(dec, LLAMA["n_vocab"])
+        log(f"batched: {extra['batched_decode']} ({time.perf_counter() - t1:.1f}s)")
     dec.close()
+    if not a.no_extra:
+        t1 = time.perf_counter()
+        extra["moe_layer"] = moe_layer(work)
+        log(f"moe: {extra['moe_layer']} ({time.perf_counter() - t1:.1f}s)")
+        t1 = time.perf_counter()
+        extra["width_sweep"] = width_sweep(work)
+        log(f"width sweep ({time.perf_counter() - t1:.1f}s): " +
+            ", ".join(f"{k} {v['GB/s']}" for k, v in extra["width_sweep"].items()))
     tps = K / dt
     kv_bytes = 2 * LLAMA["n_layer"] * LLAMA["n_head_kv"] * 128 * 2 * (pos + K / 2)
     roof_tps = HBM_PEAK_GBS * 1e9 / wbytes
@@ -283,6 +380,7 @@ def run(a, work):
                    "effective_GB/s": round((wbytes + kv_bytes) * tps / 1e9, 1),
                    "first_tokens": [int(t) for t in out[:8]]},
         "gemv_q4": gemv,
+        **extra,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
