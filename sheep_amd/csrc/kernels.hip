@@ -715,194 +715,285 @@ extern "C" __global__ void sml_embed(const sml_kembed a) {
 //
 // Decode attention in one launch (sml/sml-run.c:180-287 per head: scores
 // q.k/sqrt(hd), softmax with the running max subtracted, weighted sum of V).
-// Workgroup (split, kv head) covers ATTN_CHUNK positions for the rep query
-// heads sharing that KV head: 16 lanes per position read 256 contiguous bytes
-// of K (then of V), so the cache streams coalesced. The workgroup holding
-// position *pos rotates and rounds k to fp16 itself, writes k and v to the
-// cache and uses them from LDS. Each split leaves (max, sum, unnormalised V
-// sum) for sml_attn_merge.
+// Workgroup (split, kv head, sequence) covers ATTN_CHUNK positions for the REP
+// query heads sharing that KV head. Lane (grp = tid/16, l16 = tid%16) owns
+// dims 8*l16..+7 of positions t0 + grp + 16i: 16 lanes read 256 contiguous
+// bytes of a position's K (then V) row, so the cache streams coalesced.
+//
+// Latency, not bandwidth, bounds the kernel below a few thousand positions,
+// so every global load is issued before the first wait: q, k and v of the
+// lane's dims (independent of the position) with the position itself, then
+// the whole K/V chunk and the RoPE table row. RoPE is applied in registers
+// (the (d, d+64) partner of lane l16 is lane l16^8 of the same DPP row), the
+// scores reduce over 16 lanes with DPP, and each wave keeps its own softmax
+// max, so the only LDS round trip is the final combine of the 4 waves. The
+// workgroup holding position *pos rounds the rotated k and v to fp16, writes
+// them to the cache and uses them in place of the row it loaded. A split past
+// the position writes an empty partial (max -inf, sum 0), so sml_attn_merge
+// needs no position.
 #define ATTN_THREADS 256
 #define ATTN_CHUNK 128
 #define ATTN_MAXREP 8
 #define HD 128
 
-extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn(const sml_kattn a) {
-    __shared__ float qs[ATTN_MAXREP][HD];
-    __shared__ float sc[ATTN_MAXREP][ATTN_CHUNK];
-    __shared__ float kp[HD], vp[HD];
-    __shared__ float red[4][ATTN_MAXREP][HD];
-    __shared__ float mx_s[ATTN_MAXREP], l_s[ATTN_MAXREP];
-    const int kh = blockIdx.y, split = blockIdx.x, tid = threadIdx.x;
-    const int rep = a.n_head / a.n_kv, kvd = a.n_kv * HD, half = HD / 2;
-    // sequence blockIdx.z of a batch
-    const int b = blockIdx.z;
-    const float * aq = a.q + (size_t) b * a.qkv_stride, * ak = a.k + (size_t) b * a.qkv_stride,
-                * av = a.v + (size_t) b * a.qkv_stride;
+__device__ __forceinline__ void unpack_h8(const v4u w, float (&f)[8]) {
+    #pragma unroll
+    for (int e = 0; e < 4; e++) { f[2 * e] = h2f((uint16_t) (w[e] & 0xFFFFu)); f[2 * e + 1] = h2f((uint16_t) (w[e] >> 16)); }
+}
+__device__ __forceinline__ void load_f8(const float * p, float (&f)[8]) {
+    const float4 a = *(const float4 *) p, b = *(const float4 *) (p + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+// Rotate the lane's 8 dims by the (d, d+64) pair rule of sml/sml-run.c:363-368:
+// lanes 0-7 of a row hold the first halves, lanes 8-15 the second, and
+// row_ror:8 brings each lane its partner.
+__device__ __forceinline__ void rope8(float (&x)[8], const float (&c)[8], const float (&s)[8], bool lo) {
+    float p[8];
+    #pragma unroll
+    for (int e = 0; e < 8; e++) p[e] = dpp_f<0x128>(x[e]);
+    #pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = lo ? x[e] * c[e] - p[e] * s[e] : p[e] * s[e] + x[e] * c[e];
+}
+// Reduce-scatter of four values over the 4 rows of a wave with the gfx950
+// row swaps (v_permlane16_swap: rows 1 and 3 of the first operand trade
+// places with rows 0 and 2 of the second; v_permlane32_swap: rows 2-3 of the
+// first with rows 0-1 of the second). On return a lane of row r holds the
+// sum (max) over the rows of its argument r. The operands of each swap are
+// always distinct values: the compiler folds a register swapped with itself
+// into the wrong result.
+__device__ __forceinline__ int fbits(float v) { return __builtin_bit_cast(int, v); }
+__device__ __forceinline__ float ibits(int v) { return __builtin_bit_cast(float, v); }
+__device__ __forceinline__ float rows_sum4(float a, float b, float c, float d) {
+    const auto p = __builtin_amdgcn_permlane16_swap(fbits(a), fbits(b), false, false);
+    const auto q = __builtin_amdgcn_permlane16_swap(fbits(c), fbits(d), false, false);
+    const float u = ibits(p[0]) + ibits(p[1]), w = ibits(q[0]) + ibits(q[1]);
+    const auto r = __builtin_amdgcn_permlane32_swap(fbits(u), fbits(w), false, false);
+    return ibits(r[0]) + ibits(r[1]);
+}
+__device__ __forceinline__ float rows_max4(float a, float b, float c, float d) {
+    const auto p = __builtin_amdgcn_permlane16_swap(fbits(a), fbits(b), false, false);
+    const auto q = __builtin_amdgcn_permlane16_swap(fbits(c), fbits(d), false, false);
+    const float u = fmaxf(ibits(p[0]), ibits(p[1])), w = fmaxf(ibits(q[0]), ibits(q[1]));
+    const auto r = __builtin_amdgcn_permlane32_swap(fbits(u), fbits(w), false, false);
+    return fmaxf(ibits(r[0]), ibits(r[1]));
+}
+__device__ __forceinline__ float rl(float v, int lane) { return ibits(__builtin_amdgcn_readlane(fbits(v), lane)); }
+
+// Wave-uniform max / sum over the wave of per-head values x[j] (each the same
+// across a row's 16 lanes), four heads per reduce-scatter.
+template <int REP>
+__device__ __forceinline__ void wave_heads(const float (&x)[REP], float (&out)[REP], bool is_max) {
+    #pragma unroll
+    for (int g = 0; g < REP; g += 4) {
+        const float pad = is_max ? -INFINITY : 0.0f;
+        const float a = x[g], b = g + 1 < REP ? x[g + 1 < REP ? g + 1 : g] : pad,
+                    c = g + 2 < REP ? x[g + 2 < REP ? g + 2 : g] : pad, d = g + 3 < REP ? x[g + 3 < REP ? g + 3 : g] : pad;
+        const float r = is_max ? rows_max4(a, b, c, d) : rows_sum4(a, b, c, d);
+        #pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (g + k < REP) out[g + k] = rl(r, 16 * k);
+    }
+}
+
+template <int REP>
+__device__ __forceinline__ void attn_body(const sml_kattn & a) {
+    __shared__ float red[4][REP][HD];
+    __shared__ float wm[4][REP], wl[4][REP];
+    const int kh = blockIdx.y, split = blockIdx.x, b = blockIdx.z, tid = threadIdx.x;
+    const int wave = tid >> 6, grp = tid >> 4, l16 = tid & 15, kvd = a.n_kv * HD;
+    const float * aq = a.q + (size_t) b * a.qkv_stride + (size_t) kh * REP * HD + l16 * 8;
+    const float * ak = a.k + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
+    const float * av = a.v + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
+    float q[REP][8], kn[8], vn[8];
+    #pragma unroll
+    for (int j = 0; j < REP; j++) load_f8(aq + j * HD, q[j]);
+    load_f8(ak, kn);
+    load_f8(av, vn);
+    const int pos = a.pos[b], T = pos + 1, t0 = split * ATTN_CHUNK;
+    float * apart = a.part + ((size_t) b * a.n_head + (size_t) kh * REP) * a.nsplit * (HD + 2);
+    if (t0 >= T) {
+        if (tid < REP) {
+            float * part = apart + ((size_t) tid * a.nsplit + split) * (HD + 2);
+            part[HD] = -INFINITY;
+            part[HD + 1] = 0.0f;
+        }
+        return;
+    }
+    const int t1 = min(T, t0 + ATTN_CHUNK);
     uint16_t * kcache = a.kc_slots ? a.kc_slots[a.slot[b]] + a.layer_off : a.kcache;
     uint16_t * vcache = a.vc_slots ? a.vc_slots[a.slot[b]] + a.layer_off : a.vcache;
-    float * apart = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
-    const int pos = a.pos[b], T = pos + 1, t0 = split * ATTN_CHUNK;
-    if (t0 >= T) return;
-    const int t1 = min(T, t0 + ATTN_CHUNK);
-    // every K and V load of this lane first (one round trip for the chunk):
-    // lane (grp, l16) covers positions t0 + grp + 16i, dims 8*l16 .. +7
-    const int grp = tid >> 4, l16 = tid & 15;
+    // all of K, then all of V: loads return in order, so the scores and the
+    // softmax run while V is still arriving
     v4u kw[ATTN_CHUNK / 16], vw[ATTN_CHUNK / 16];
     #pragma unroll
     for (int i = 0; i < ATTN_CHUNK / 16; i++) {
         int t = t0 + grp + 16 * i;
         t = t < t1 ? t : t0;                          // in range; masked below
         kw[i] = __builtin_nontemporal_load((const v4u *) (kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
+    }
+    #pragma unroll
+    for (int i = 0; i < ATTN_CHUNK / 16; i++) {
+        int t = t0 + grp + 16 * i;
+        t = t < t1 ? t : t0;
         vw[i] = __builtin_nontemporal_load((const v4u *) (vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
     }
-    const float * cs = a.cos_t + (size_t) pos * half, * sn = a.sin_t + (size_t) pos * half;
-    // RoPE of this kv head's query heads (halved pairs, sml/sml-run.c:363-368)
-    for (int i = tid; i < rep * half; i += ATTN_THREADS) {
-        const int j = i / half, d = i % half;
-        const float * v = aq + (size_t) (kh * rep + j) * HD;
-        const float x0 = v[d], x1 = v[d + half];
-        qs[j][d] = x0 * cs[d] - x1 * sn[d];
-        qs[j][d + half] = x0 * sn[d] + x1 * cs[d];
+    const int half = HD / 2;
+    float cs[8], sn[8];
+    load_f8(a.cos_t + (size_t) pos * half + (l16 & 7) * 8, cs);
+    load_f8(a.sin_t + (size_t) pos * half + (l16 & 7) * 8, sn);
+    const bool lo = l16 < 8;
+    const float sl = a.inv * 1.44269504088896341f;
+    #pragma unroll
+    for (int j = 0; j < REP; j++) rope8(q[j], cs, sn, lo);
+    // k rotated, then k and v rounded to fp16 as the cache stores them (sml/sml-run.c:3414-3415)
+    rope8(kn, cs, sn, lo);
+    v4u knew, vnew;
+    #pragma unroll
+    for (int e = 0; e < 4; e++) {
+        knew[e] = (unsigned) f2h(kn[2 * e]) | ((unsigned) f2h(kn[2 * e + 1]) << 16);
+        vnew[e] = (unsigned) f2h(vn[2 * e]) | ((unsigned) f2h(vn[2 * e + 1]) << 16);
     }
-    const bool has_pos = t0 <= pos && pos < t1;
-    if (has_pos) {
-        // k rotated, then rounded to fp16 as the cache stores it (sml/sml-run.c:3414-3415)
-        uint16_t * kc = kcache + (size_t) pos * kvd + (size_t) kh * HD;
-        uint16_t * vc = vcache + (size_t) pos * kvd + (size_t) kh * HD;
-        if (tid < half) {
-            const float * v = ak + (size_t) kh * HD;
-            const float x0 = v[tid], x1 = v[tid + half];
-            const uint16_t h0 = f2h(x0 * cs[tid] - x1 * sn[tid]), h1 = f2h(x0 * sn[tid] + x1 * cs[tid]);
-            kc[tid] = h0; kc[tid + half] = h1;
-            kp[tid] = h2f(h0); kp[tid + half] = h2f(h1);
-        } else if (tid < half + HD) {
-            const int d = tid - half;
-            const uint16_t h = f2h(av[(size_t) kh * HD + d]);
-            vc[d] = h;
-            vp[d] = h2f(h);
-        }
+    if (t0 <= pos && pos < t1 && tid < 16) {
+        *(v4u *) (kcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = knew;
+        *(v4u *) (vcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = vnew;
     }
-    __syncthreads();
-    // scores: 16 lanes per position, 16 positions per pass
+    // scores: 8 FMAs per lane, summed over the 16 lanes of the row
+    float sc[ATTN_CHUNK / 16][REP];
     #pragma unroll
     for (int i = 0; i < ATTN_CHUNK / 16; i++) {
         const int t = t0 + grp + 16 * i;
         float kf[8];
-        if (t != pos) {
-            #pragma unroll
-            for (int e = 0; e < 4; e++) { kf[2 * e] = h2f((uint16_t) (kw[i][e] & 0xFFFFu)); kf[2 * e + 1] = h2f((uint16_t) (kw[i][e] >> 16)); }
-        } else {
-            #pragma unroll
-            for (int e = 0; e < 8; e++) kf[e] = kp[l16 * 8 + e];
-        }
+        unpack_h8(t == pos ? knew : kw[i], kf);
         #pragma unroll
-        for (int j = 0; j < ATTN_MAXREP; j++) {
-            if (j >= rep) break;
+        for (int j = 0; j < REP; j++) {
             float p = 0.0f;
             #pragma unroll
-            for (int e = 0; e < 8; e++) p += qs[j][l16 * 8 + e] * kf[e];
+            for (int e = 0; e < 8; e++) p += q[j][e] * kf[e];
             p = sum16(p);
-            if (l16 == 0) sc[j][t - t0] = t < t1 ? p * a.inv : -INFINITY;
+            sc[i][j] = t < t1 ? p * sl : -INFINITY;
         }
     }
-    __syncthreads();
-    // per head: chunk max, exponentials, sum (one wave per head, two positions per lane)
-    const int wave = tid >> 6, lane = tid & 63;
-    for (int j = wave; j < rep; j += ATTN_THREADS / WAVE) {
-        const float s0 = sc[j][lane], s1 = sc[j][lane + 64];
-        const float m = wave_max(fmaxf(s0, s1));
-        const float p0 = s0 == -INFINITY ? 0.0f : expf(s0 - m), p1 = s1 == -INFINITY ? 0.0f : expf(s1 - m);
-        const float l = wave_sum(p0 + p1);
-        sc[j][lane] = p0;
-        sc[j][lane + 64] = p1;
-        if (lane == 0) { mx_s[j] = m; l_s[j] = l; }
-    }
-    __syncthreads();
-    // weighted V over the same positions (weights of masked positions are 0)
-    const int dc = l16;
-    float acc[ATTN_MAXREP][8];
+    // the wave's softmax over its 32 positions, in base 2 (scores were scaled
+    // by log2 e): every lane of a row holds the row's scores, so the row
+    // swaps cover the wave
+    float m[REP], l[REP], xs[REP];
     #pragma unroll
-    for (int j = 0; j < ATTN_MAXREP; j++)
+    for (int j = 0; j < REP; j++) {
+        float x = sc[0][j];
+        #pragma unroll
+        for (int i = 1; i < ATTN_CHUNK / 16; i++) x = fmaxf(x, sc[i][j]);
+        xs[j] = x;
+    }
+    wave_heads<REP>(xs, m, true);
+    #pragma unroll
+    for (int j = 0; j < REP; j++) {
+        const float mj = m[j] == -INFINITY ? 0.0f : m[j];   // a wave with no position left
+        float ls = 0.0f;
+        #pragma unroll
+        for (int i = 0; i < ATTN_CHUNK / 16; i++) {
+            const float p = __builtin_amdgcn_exp2f(sc[i][j] - mj);
+            sc[i][j] = p;
+            ls += p;
+        }
+        xs[j] = ls;
+    }
+    wave_heads<REP>(xs, l, false);
+    // weighted V over the same positions (masked weights are 0)
+    float acc[REP][8];
+    #pragma unroll
+    for (int j = 0; j < REP; j++)
         #pragma unroll
         for (int e = 0; e < 8; e++) acc[j][e] = 0.0f;
     #pragma unroll
     for (int i = 0; i < ATTN_CHUNK / 16; i++) {
         const int t = t0 + grp + 16 * i;
         float vf[8];
-        if (t != pos) {
-            #pragma unroll
-            for (int e = 0; e < 4; e++) { vf[2 * e] = h2f((uint16_t) (vw[i][e] & 0xFFFFu)); vf[2 * e + 1] = h2f((uint16_t) (vw[i][e] >> 16)); }
-        } else {
-            #pragma unroll
-            for (int e = 0; e < 8; e++) vf[e] = vp[dc * 8 + e];
-        }
+        unpack_h8(t == pos ? vnew : vw[i], vf);
         #pragma unroll
-        for (int j = 0; j < ATTN_MAXREP; j++) {
-            if (j >= rep) break;
-            const float p = t < t1 ? sc[j][t - t0] : 0.0f;
+        for (int j = 0; j < REP; j++)
             #pragma unroll
-            for (int e = 0; e < 8; e++) acc[j][e] += p * vf[e];
-        }
+            for (int e = 0; e < 8; e++) acc[j][e] += sc[i][j] * vf[e];
     }
-    // reduce over the 4 position lanes of a wave (lanes 16 apart), then over waves
+    // sums over the wave's 4 rows, scattered: row r keeps dims l16*8 + 4h + r
+    const int row = (tid >> 4) & 3;
     #pragma unroll
-    for (int j = 0; j < ATTN_MAXREP; j++) {
-        if (j >= rep) break;
+    for (int j = 0; j < REP; j++)
         #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float v = acc[j][i];
-            v += swz16_f(v);
-            v += __shfl_xor(v, 32);
-            acc[j][i] = v;
-        }
-        if (lane < 16) {
-            #pragma unroll
-            for (int i = 0; i < 8; i++) red[wave][j][dc * 8 + i] = acc[j][i];
-        }
+        for (int h = 0; h < 2; h++)
+            red[wave][j][l16 * 8 + 4 * h + row] =
+                rows_sum4(acc[j][4 * h], acc[j][4 * h + 1], acc[j][4 * h + 2], acc[j][4 * h + 3]);
+    if ((tid & 63) == 0) {
+        #pragma unroll
+        for (int j = 0; j < REP; j++) { wm[wave][j] = m[j]; wl[wave][j] = l[j]; }
     }
     __syncthreads();
-    for (int i = tid; i < rep * HD; i += ATTN_THREADS) {
-        const int j = i / HD, d = i % HD;
-        float * part = apart + ((size_t) (kh * rep + j) * a.nsplit + split) * (HD + 2);
-        part[d] = red[0][j][d] + red[1][j][d] + red[2][j][d] + red[3][j][d];
-        if (d == 0) { part[HD] = mx_s[j]; part[HD + 1] = l_s[j]; }
+    // combine the 4 waves: rescale each by 2^(m_w - M)
+    for (int idx = tid; idx < REP * HD; idx += ATTN_THREADS) {
+        const int j = idx / HD, d = idx % HD;
+        float M = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+        float o = 0.0f, L = 0.0f;
+        #pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float e = __builtin_amdgcn_exp2f(wm[w][j] - M);     // M is finite: wave 0 holds t0
+            o += e * red[w][j][d];
+            L += e * wl[w][j];
+        }
+        float * part = apart + ((size_t) j * a.nsplit + split) * (HD + 2);
+        part[d] = o;
+        if (d == 0) { part[HD] = M; part[HD + 1] = L; }
     }
 }
 
+#define ATTN_KERNEL(R) \
+    extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn_r##R(const sml_kattn a) { attn_body<R>(a); }
+ATTN_KERNEL(1) ATTN_KERNEL(2) ATTN_KERNEL(3) ATTN_KERNEL(4) ATTN_KERNEL(5) ATTN_KERNEL(6) ATTN_KERNEL(7) ATTN_KERNEL(8)
+
 // Merge of the splits of one query head (grid: n_head workgroups of HD
-// threads), in split order: out = sum_s e_s o_s / sum_s e_s l_s with
-// e_s = exp(m_s - max m). With q_out set, the head's 128 outputs (4 groups of
-// 32, identity permutation) are also quantized for the next GEMV
-// (sml/sml-kernel.c:86-106).
+// threads): out = sum_s e_s o_s / sum_s e_s l_s with e_s = 2^(m_s - max m)
+// (the split maxima are in base 2).
+// Every split has a partial (max -inf for splits past the position), so the
+// loads of a batch of 32 splits go out together with no position read first.
+// With q_out set, the head's 128 outputs (4 groups of 32, identity
+// permutation) are also quantized for the next GEMV (sml/sml-kernel.c:86-106).
+#define MERGE_BATCH 32
 extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn a) {
-    __shared__ float em[64], ls[64];
-    __shared__ float lsum;
     const int h = blockIdx.x, d = threadIdx.x, b = blockIdx.z;     // head, dim, sequence
-    const int T = a.pos[b] + 1, nact = (T + ATTN_CHUNK - 1) / ATTN_CHUNK;
     const float * p = a.part + ((size_t) b * a.n_head + h) * a.nsplit * (HD + 2);
     const size_t ob = (size_t) b * a.n_head * HD;
-    for (int s2 = d; s2 < nact; s2 += HD) { em[s2] = p[(size_t) s2 * (HD + 2) + HD]; ls[s2] = p[(size_t) s2 * (HD + 2) + HD + 1]; }
-    __syncthreads();
-    if (d == 0) {
-        float M = -INFINITY;
-        for (int s2 = 0; s2 < nact; s2++) M = fmaxf(M, em[s2]);
-        float l = 0.0f;
-        for (int s2 = 0; s2 < nact; s2++) { const float e = expf(em[s2] - M); em[s2] = e; l += e * ls[s2]; }
-        lsum = l;
+    float M = -INFINITY, L = 0.0f, o = 0.0f;
+    for (int s0 = 0; s0 < a.nsplit; s0 += MERGE_BATCH) {
+        const int n = min(MERGE_BATCH, a.nsplit - s0);
+        float mv[MERGE_BATCH], lv[MERGE_BATCH], ov[MERGE_BATCH];
+        #pragma unroll
+        for (int s = 0; s < MERGE_BATCH; s++) {
+            const float * ps = p + (size_t) (s0 + (s < n ? s : 0)) * (HD + 2);   // in range; masked below
+            mv[s] = ps[HD];
+            lv[s] = ps[HD + 1];
+            ov[s] = ps[d];
+        }
+        #pragma unroll
+        for (int s = 0; s < MERGE_BATCH; s++) mv[s] = s < n ? mv[s] : -INFINITY;
+        float Mb = M;
+        #pragma unroll
+        for (int s = 0; s < MERGE_BATCH; s++) Mb = fmaxf(Mb, mv[s]);
+        const float r = __builtin_amdgcn_exp2f(M - Mb);      // M = -inf: 0; Mb is finite (split 0 is active)
+        o *= r;
+        L *= r;
+        #pragma unroll
+        for (int s = 0; s < MERGE_BATCH; s++) {
+            const float e = __builtin_amdgcn_exp2f(mv[s] - Mb);
+            L += e * lv[s];
+            o += e != 0.0f ? e * ov[s] : 0.0f;
+        }
+        M = Mb;
     }
-    __syncthreads();
-    float o = 0.0f;
-    #pragma unroll 8
-    for (int s2 = 0; s2 < nact; s2++) o += em[s2] * p[(size_t) s2 * (HD + 2) + d];
-    const float r = o / lsum;
+    const float r = o / L;
     a.out[ob + (size_t) h * HD + d] = r;
     if (!a.q_out) return;
     const float amax = max32(fabsf(r));
     const float s = amax / 127.0f;
     const float is = s > 0.0f ? 1.0f / s : 0.0f;
-    const float rr = __builtin_rintf(r * is);
-    int t = (rr >= -2147483648.0f && rr < 2147483648.0f) ? (int) rr : (int) 0x80000000u;
-    t = t > 127 ? 127 : t < -127 ? -127 : t;
+    const int t = quant1(r, is);
     const int sum = isum32(t);
     const int g = h * 4 + (d >> 5);
     a.q_out[ob + (size_t) h * HD + d] = (int8_t) t;

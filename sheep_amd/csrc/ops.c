@@ -474,7 +474,9 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     a.part = part; a.out = out; a.q_out = q_out; a.s_out = s_out; a.u_out = u_out;
     a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
-    hx_launch("sml_attn", (unsigned) ns, (unsigned) n_kv, 256, 0, st, &a);
+    char name[32];
+    snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
+    hx_launch(name, (unsigned) ns, (unsigned) n_kv, 256, 0, st, &a);
     hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
 }
 
@@ -494,7 +496,9 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     a.part = part; a.out = out; a.q_out = q_out; a.s_out = s_out; a.u_out = u_out;
     a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
-    hx_launch3("sml_attn", (unsigned) ns, (unsigned) n_kv, (unsigned) nseq, 256, 0, st, &a);
+    char name[32];
+    snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
+    hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) nseq, 256, 0, st, &a);
     hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
 }
 
