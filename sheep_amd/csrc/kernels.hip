@@ -307,7 +307,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
     int32_t sg_u[SG];
     const int nq16 = n / 16;
     // fused prologue: float4 words of x, norm_w and perm per thread
-    constexpr int FK = AM == 0 ? 1 : (WG >= 512 ? 2 : 4);
+    constexpr int FK = AM == 0 ? 1 : (WG >= 1024 ? 1 : WG >= 512 ? 2 : 4);
     float4 fx[FK], fw[FK];
     int4 fp[FK];
     if constexpr (AM == 0) {
@@ -428,9 +428,11 @@ __device__ void gemv_body(const sml_kgemv & a) {
     #pragma unroll
     for (int s = 0; s < RB; s++) acc[s] = seg_sum<LPR>(acc[s]);
     if constexpr (HQ) {
-        // 32 consecutive outputs per workgroup (RB/2 gate/up pairs per wave):
-        // h = silu(g)*u, then its per-32 quantization for the down projection
-        __shared__ float hb[32];
+        // WG/16 consecutive outputs per workgroup (RB/2 gate/up pairs per
+        // wave, whole groups of 32): h = silu(g)*u, then its per-32
+        // quantization for the down projection
+        constexpr int HO = WG / 16;
+        __shared__ float hb[HO];
         if (l == LPR - 1) {
             #pragma unroll
             for (int s = 0; s < RB; s += 2) {
@@ -447,16 +449,16 @@ __device__ void gemv_body(const sml_kgemv & a) {
             }
         }
         __syncthreads();
-        if (tid < 32) {
+        if (tid < HO) {
             const float v = hb[tid];
             const float s = max32(fabsf(v)) / 127.0f;
             const float is = s > 0.0f ? 1.0f / s : 0.0f;
             const int t = quant1(v, is);
             const int sum = isum32(t);
-            const int row = blockIdx.x * 32 + tid;
+            const int row = blockIdx.x * HO + tid;
             if (row < a.total_rows) {
                 a.hq[row] = (int8_t) t;
-                if (tid == 0) { a.hscale[row >> 5] = s; a.hsums[row >> 5] = sum; }
+                if ((tid & 31) == 0) { a.hscale[row >> 5] = s; a.hsums[row >> 5] = sum; }
             }
         }
         return;
@@ -513,15 +515,28 @@ __device__ void gemv_body(const sml_kgemv & a) {
     extern "C" __global__ __launch_bounds__(512) void sml_gemv_q##NB##_hn_i##NI(const sml_kgemv a) {      \
         gemv_body<NB, 2, NI, 512, true, 1, true, true, 16>(a);                                              \
     }
+// Wider workgroups for the fused prologue, which every workgroup computes
+// in full: _n512 / _n1024 (input width up to 4096), and _hn1024_i<NI> with
+// 64 outputs of h per workgroup.
+#define GEMV_KERNEL_NW(NB, RB, NI, W)                                                                       \
+    extern "C" __global__ __launch_bounds__(W) void sml_gemv_q##NB##_r##RB##_i##NI##_n##W(const sml_kgemv a) { \
+        gemv_body<NB, RB, NI, W, true, 1, false, false>(a);                                                 \
+    }
+#define GEMV_KERNEL_HW(NB, NI, W)                                                                           \
+    extern "C" __global__ __launch_bounds__(W) void sml_gemv_q##NB##_hn##W##_i##NI(const sml_kgemv a) {     \
+        gemv_body<NB, 2, NI, W, true, 1, true, true, 16>(a);                                                \
+    }
+#define GEMV_WIDE(NB)                                                                                       \
+    GEMV_KERNEL_NW(NB, 1, 1, 512) GEMV_KERNEL_NW(NB, 2, 1, 512) GEMV_KERNEL_NW(NB, 4, 1, 512)               \
+    GEMV_KERNEL_NW(NB, 1, 1, 1024) GEMV_KERNEL_NW(NB, 2, 1, 1024) GEMV_KERNEL_HW(NB, 2, 1024)
 #define GEMV_WIDTH(NB)                                                                     \
-    GEMV_KERNEL(NB, 1, 2) GEMV_KERNEL(NB, 1, 4) GEMV_KERNEL(NB, 1, 8)                     \
-    GEMV_KERNEL(NB, 2, 1) GEMV_KERNEL(NB, 2, 2) GEMV_KERNEL(NB, 2, 4) GEMV_KERNEL(NB, 2, 8) \
+    GEMV_KERNEL(NB, 1, 2) GEMV_KERNEL(NB, 1, 4)                                            \
+    GEMV_KERNEL(NB, 2, 1) GEMV_KERNEL(NB, 2, 2) GEMV_KERNEL(NB, 2, 4)                     \
     GEMV_KERNEL(NB, 4, 1) GEMV_KERNEL(NB, 4, 2) GEMV_KERNEL(NB, 4, 4)                     \
-    GEMV_KERNEL_N(NB, 1, 1) GEMV_KERNEL_N(NB, 1, 2) GEMV_KERNEL_N(NB, 2, 1)               \
-    GEMV_KERNEL_N(NB, 2, 2) GEMV_KERNEL_N(NB, 4, 1) GEMV_KERNEL_N(NB, 4, 2)               \
+    GEMV_KERNEL_N(NB, 1, 1) GEMV_KERNEL_N(NB, 2, 1) GEMV_KERNEL_N(NB, 4, 1)               \
     GEMV_KERNEL_S(NB, 2, 1) GEMV_KERNEL_S(NB, 2, 2) GEMV_KERNEL_S(NB, 2, 4)               \
     GEMV_KERNEL_S(NB, 4, 1) GEMV_KERNEL_S(NB, 4, 2) GEMV_KERNEL_S(NB, 4, 4)               \
-    GEMV_KERNEL_H(NB, 2) GEMV_KERNEL_H(NB, 4) GEMV_KERNEL_H(NB, 8)
+    GEMV_KERNEL_H(NB, 2) GEMV_KERNEL_H(NB, 4) GEMV_WIDE(NB)
 GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH(7) GEMV_WIDTH(8)
 
 // ---------------------------------------------------------------- norm + quantize
@@ -1001,27 +1016,51 @@ extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn 
 }
 
 // ---------------------------------------------------------------- argmax
-// First maximum wins (sml/sml-run.c:3539-3544).
-extern "C" __global__ __launch_bounds__(1024) void sml_argmax(const sml_kargmax a) {
-    __shared__ float bv_s[16];
-    __shared__ int bi_s[16];
+// First maximum wins (sml/sml-run.c:3539-3544). One workgroup: every thread
+// issues all of its float4 loads (16 per round) before comparing, so the
+// 513 KB of a 128k vocabulary arrive in a few round trips.
+#define ARGMAX_THREADS 1024
+#define ARGMAX_UNROLL 16
+__device__ __forceinline__ void amax_take(float v, int i, float & bv, int & bi) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+extern "C" __global__ __launch_bounds__(ARGMAX_THREADS) void sml_argmax(const sml_kargmax a) {
+    __shared__ float bv_s[ARGMAX_THREADS / 64];
+    __shared__ int bi_s[ARGMAX_THREADS / 64];
+    const int tid = threadIdx.x;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < a.n; i += 1024) {
-        const float v = a.logits[i];
-        if (v > bv) { bv = v; bi = i; }
+    const bool al = ((uintptr_t) a.logits & 15) == 0;
+    const int n4 = al ? a.n / 4 : 0;
+    const float4 * l4 = (const float4 *) a.logits;
+    for (int base = 0; base < n4; base += ARGMAX_THREADS * ARGMAX_UNROLL) {
+        float4 v[ARGMAX_UNROLL];
+        #pragma unroll
+        for (int k = 0; k < ARGMAX_UNROLL; k++) {
+            const int f = base + k * ARGMAX_THREADS + tid;
+            v[k] = l4[f < n4 ? f : 0];
+        }
+        #pragma unroll
+        for (int k = 0; k < ARGMAX_UNROLL; k++) {
+            const int f = base + k * ARGMAX_THREADS + tid;
+            if (f < n4) {
+                // NaN never compares greater, as in the reference's loop
+                amax_take(v[k].x, 4 * f, bv, bi); amax_take(v[k].y, 4 * f + 1, bv, bi);
+                amax_take(v[k].z, 4 * f + 2, bv, bi); amax_take(v[k].w, 4 * f + 3, bv, bi);
+            }
+        }
     }
+    for (int i = 4 * n4 + tid; i < a.n; i += ARGMAX_THREADS) amax_take(a.logits[i], i, bv, bi);
     #pragma unroll
     for (int o = 32; o; o >>= 1) {
         const float ov = __shfl_xor(bv, o);
         const int oi = __shfl_xor(bi, o);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        amax_take(ov, oi, bv, bi);
     }
-    if ((threadIdx.x & 63) == 0) { bv_s[threadIdx.x >> 6] = bv; bi_s[threadIdx.x >> 6] = bi; }
+    if ((tid & 63) == 0) { bv_s[tid >> 6] = bv; bi_s[tid >> 6] = bi; }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 16; w++)
-            if (bv_s[w] > bv_s[0] || (bv_s[w] == bv_s[0] && bi_s[w] < bi_s[0])) { bv_s[0] = bv_s[w]; bi_s[0] = bi_s[w]; }
+    if (tid == 0) {
+        for (int w = 1; w < ARGMAX_THREADS / 64; w++) amax_take(bv_s[w], bi_s[w], bv_s[0], bi_s[0]);
         // a NaN first logit is never beaten in the reference's loop
         const float l0 = a.logits[0];
         const int tok = (bi_s[0] == 0x7fffffff || l0 != l0) ? 0 : bi_s[0];

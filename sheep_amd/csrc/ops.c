@@ -292,13 +292,24 @@ static int env_int(const char * name, int dflt) {
 // carry the whole matrix at once while the loads a lane holds stay within
 // RB*NI <= 16; SwiGLU takes 2 or 4: one or two gate/up pairs).
 // SML_GEMV_RB / SML_GEMV_NI override for tuning sweeps.
+// Launch shape of a GEMV: RB rows per wave, NI chunks per lane per pass.
+// Measured on MI355X, occupancy beats bytes in flight per wave: at most 4
+// chunks per lane (two passes over a 14336-wide row), and the fused-prologue
+// kernels run 512-thread workgroups with 4 rows per wave and one chunk per
+// pass, so that the fewest workgroups (each repeating the prologue) still
+// cover the chip.
 static void pick_shape(int rows, int cols, int swiglu, int fused, int * rb, int * ni) {
     const int ng = cols / 32;
-    const int imax = fused ? 2 : swiglu ? 4 : 8;
+    const int imax = fused ? 1 : 4;
     int i = 1;
     while (i < imax && 64 * i < ng) i *= 2;
     int r = 1;
-    while (r < 4 && rows / (2 * r) >= 2048 && 2 * r * i <= 16) r *= 2;
+    if (fused) {
+        r = 4;
+        while (r > 1 && rows / (8 * r) < 192) r /= 2;
+    } else {
+        while (r < 4 && rows / (2 * r) >= 2048 && 2 * r * i <= 16) r *= 2;
+    }
     const int fr = env_int("SML_GEMV_RB", 0), fi = env_int("SML_GEMV_NI", 0);
     if (fr == 1 || fr == 2 || fr == 4) r = fr;
     if ((fi == 1 || fi == 2 || fi == 4 || fi == 8) && fi <= imax) i = fi;
@@ -347,20 +358,27 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
     if (hq) {
         // 16 lanes per row: NI chunks per lane with 16*NI >= groups (a second
         // pass beyond 8)
-        const int ng = cols / 32;
         int ni = 2;
-        while (ni < 8 && 16 * ni < ng) ni *= 2;
-        snprintf(name, sizeof name, "sml_gemv_q%d_h%s_i%d", nb, am ? "n" : "", ni);
-        hx_launch(name, (unsigned) (a.total_rows / 32), 1, 512, lds, st, &a);
+        const int fi = env_int("SML_GEMV_HNI", 0);
+        if (fi == 2 || fi == 4) ni = fi;
+        const int wg = am && env_int("SML_GEMV_HWG", 512) == 1024 && ni <= 4 ? 1024 : 512;
+        if (a.total_rows % (wg / 16)) hx_failf("h quantization needs rows in whole workgroups");
+        if (wg == 1024) snprintf(name, sizeof name, "sml_gemv_q%d_hn1024_i%d", nb, ni);
+        else snprintf(name, sizeof name, "sml_gemv_q%d_h%s_i%d", nb, am ? "n" : "", ni);
+        hx_launch(name, (unsigned) (a.total_rows / (wg / 16)), 1, (unsigned) wg, lds, st, &a);
         return;
     }
     int rb, ni;
     pick_shape(a.total_rows, cols, swiglu, am, &rb, &ni);
     const int rows_per_wave = swiglu ? rb / 2 : rb;
     const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
+    int wg = 256;
     if (swiglu) snprintf(name, sizeof name, "sml_gemv_q%d_s%s_r%d_i%d", nb, am ? "n" : "", rb, ni);
-    else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d%s", nb, rb, ni, am ? "_n" : "");
-    hx_launch(name, (unsigned) ((waves + 3) / 4), 1, 256, lds, st, &a);
+    else if (am && env_int("SML_GEMV_WG", 512) != 256) {
+        wg = env_int("SML_GEMV_WG", 512) == 1024 ? 1024 : 512;
+        snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_n%d", nb, rb, ni, wg);
+    } else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d%s", nb, rb, ni, am ? "_n" : "");
+    hx_launch(name, (unsigned) ((waves + wg / 64 - 1) / (wg / 64)), 1, (unsigned) wg, lds, st, &a);
 }
 
 int sml_hip_matvec(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, float * y) {
