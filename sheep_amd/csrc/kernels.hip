@@ -825,13 +825,12 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     load_f8(ak, kn);
     load_f8(av, vn);
     const int pos = a.pos[b], T = pos + 1, t0 = split * ATTN_CHUNK;
-    float * apart = a.part + ((size_t) b * a.n_head + (size_t) kh * REP) * a.nsplit * (HD + 2);
+    // partials of sequence b: V sums [head][split][HD], then (max, sum) [head][split]
+    float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
+    float * po = blk + (size_t) kh * REP * a.nsplit * HD;
+    float2 * pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) kh * REP * a.nsplit;
     if (t0 >= T) {
-        if (tid < REP) {
-            float * part = apart + ((size_t) tid * a.nsplit + split) * (HD + 2);
-            part[HD] = -INFINITY;
-            part[HD + 1] = 0.0f;
-        }
+        if (tid < REP) pml[(size_t) tid * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
         return;
     }
     const int t1 = min(T, t0 + ATTN_CHUNK);
@@ -953,9 +952,8 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             o += e * red[w][j][d];
             L += e * wl[w][j];
         }
-        float * part = apart + ((size_t) j * a.nsplit + split) * (HD + 2);
-        part[d] = o;
-        if (d == 0) { part[HD] = M; part[HD + 1] = L; }
+        po[((size_t) j * a.nsplit + split) * HD + d] = o;
+        if (d == 0) pml[(size_t) j * a.nsplit + split] = make_float2(M, L);
     }
 }
 
@@ -965,41 +963,38 @@ ATTN_KERNEL(1) ATTN_KERNEL(2) ATTN_KERNEL(3) ATTN_KERNEL(4) ATTN_KERNEL(5) ATTN_
 
 // Merge of the splits of one query head (grid: n_head workgroups of HD
 // threads): out = sum_s e_s o_s / sum_s e_s l_s with e_s = 2^(m_s - max m)
-// (the split maxima are in base 2).
-// Every split has a partial (max -inf for splits past the position), so the
-// loads of a batch of 32 splits go out together with no position read first.
+// (the split maxima are in base 2). Every split has a partial (max -inf for
+// splits past the position), so a batch of 32 splits is loaded at once with
+// no position read first: lane s of each wave takes split s's (max, sum) and
+// its weight e_s, which the dims then read back as a scalar.
 // With q_out set, the head's 128 outputs (4 groups of 32, identity
 // permutation) are also quantized for the next GEMV (sml/sml-kernel.c:86-106).
 #define MERGE_BATCH 32
 extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn a) {
-    const int h = blockIdx.x, d = threadIdx.x, b = blockIdx.z;     // head, dim, sequence
-    const float * p = a.part + ((size_t) b * a.n_head + h) * a.nsplit * (HD + 2);
+    const int h = blockIdx.x, d = threadIdx.x, b = blockIdx.z, lane = d & 63;     // head, dim, sequence
+    const float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
+    const float * po = blk + (size_t) h * a.nsplit * HD;
+    const float2 * pml = (const float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) h * a.nsplit;
     const size_t ob = (size_t) b * a.n_head * HD;
     float M = -INFINITY, L = 0.0f, o = 0.0f;
     for (int s0 = 0; s0 < a.nsplit; s0 += MERGE_BATCH) {
         const int n = min(MERGE_BATCH, a.nsplit - s0);
-        float mv[MERGE_BATCH], lv[MERGE_BATCH], ov[MERGE_BATCH];
+        float ov[MERGE_BATCH];
+        #pragma unroll
+        for (int s = 0; s < MERGE_BATCH; s++) ov[s] = po[(size_t) (s0 + (s < n ? s : 0)) * HD + d];   // masked below
+        const float2 ml = pml[s0 + (lane < n ? lane : 0)];
+        const float mj = lane < n ? ml.x : -INFINITY;
+        const float Mb = fmaxf(M, rl(max32(mj), 0));         // finite: split 0 is active
+        const float r = __builtin_amdgcn_exp2f(M - Mb);      // M = -inf: 0
+        const float e = __builtin_amdgcn_exp2f(mj - Mb);     // 0 for splits past the position
+        L = L * r + rl(sum32(lane < n ? e * ml.y : 0.0f), 0);
+        float acc[4] = {o * r, 0.0f, 0.0f, 0.0f};
         #pragma unroll
         for (int s = 0; s < MERGE_BATCH; s++) {
-            const float * ps = p + (size_t) (s0 + (s < n ? s : 0)) * (HD + 2);   // in range; masked below
-            mv[s] = ps[HD];
-            lv[s] = ps[HD + 1];
-            ov[s] = ps[d];
+            const float es = rl(e, s);
+            acc[s & 3] += es != 0.0f ? es * ov[s] : 0.0f;     // an empty split's V sums are not read
         }
-        #pragma unroll
-        for (int s = 0; s < MERGE_BATCH; s++) mv[s] = s < n ? mv[s] : -INFINITY;
-        float Mb = M;
-        #pragma unroll
-        for (int s = 0; s < MERGE_BATCH; s++) Mb = fmaxf(Mb, mv[s]);
-        const float r = __builtin_amdgcn_exp2f(M - Mb);      // M = -inf: 0; Mb is finite (split 0 is active)
-        o *= r;
-        L *= r;
-        #pragma unroll
-        for (int s = 0; s < MERGE_BATCH; s++) {
-            const float e = __builtin_amdgcn_exp2f(mv[s] - Mb);
-            L += e * lv[s];
-            o += e != 0.0f ? e * ov[s] : 0.0f;
-        }
+        o = (acc[0] + acc[1]) + (acc[2] + acc[3]);
         M = Mb;
     }
     const float r = o / L;
