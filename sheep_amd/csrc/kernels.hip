@@ -731,9 +731,11 @@ extern "C" __global__ void sml_embed(const sml_kembed a) {
 // Decode attention in one launch (sml/sml-run.c:180-287 per head: scores
 // q.k/sqrt(hd), softmax with the running max subtracted, weighted sum of V).
 // Workgroup (split, kv head, sequence) covers ATTN_CHUNK positions for the REP
-// query heads sharing that KV head. Lane (grp = tid/16, l16 = tid%16) owns
-// dims 8*l16..+7 of positions t0 + grp + 16i: 16 lanes read 256 contiguous
-// bytes of a position's K (then V) row, so the cache streams coalesced.
+// query heads sharing that KV head with NW waves (8 by default: two per SIMD
+// hide the compute phases' latency better than one). Lane (grp = tid/16,
+// l16 = tid%16) owns dims 8*l16..+7 of positions t0 + grp + 4*NW*i: 16 lanes
+// read 256 contiguous bytes of a position's K (then V) row, so the cache
+// streams coalesced.
 //
 // Latency, not bandwidth, bounds the kernel below a few thousand positions,
 // so every global load is issued before the first wait: q, k and v of the
@@ -741,12 +743,11 @@ extern "C" __global__ void sml_embed(const sml_kembed a) {
 // the whole K/V chunk and the RoPE table row. RoPE is applied in registers
 // (the (d, d+64) partner of lane l16 is lane l16^8 of the same DPP row), the
 // scores reduce over 16 lanes with DPP, and each wave keeps its own softmax
-// max, so the only LDS round trip is the final combine of the 4 waves. The
+// max, so the only LDS round trip is the final combine of the waves. The
 // workgroup holding position *pos rounds the rotated k and v to fp16, writes
 // them to the cache and uses them in place of the row it loaded. A split past
 // the position writes an empty partial (max -inf, sum 0), so sml_attn_merge
 // needs no position.
-#define ATTN_THREADS 256
 #define ATTN_CHUNK 128
 #define ATTN_MAXREP 8
 #define HD 128
@@ -810,10 +811,11 @@ __device__ __forceinline__ void wave_heads(const float (&x)[REP], float (&out)[R
     }
 }
 
-template <int REP>
+template <int REP, int NW>
 __device__ __forceinline__ void attn_body(const sml_kattn & a) {
-    __shared__ float red[4][REP][HD];
-    __shared__ float wm[4][REP], wl[4][REP];
+    constexpr int NT = 64 * NW, PS = NT / 16, PPL = ATTN_CHUNK / PS;   // threads, position stride, positions per lane
+    __shared__ float red[NW][REP][HD];
+    __shared__ float wm[NW][REP], wl[NW][REP];
     const int kh = blockIdx.y, split = blockIdx.x, b = blockIdx.z, tid = threadIdx.x;
     const int wave = tid >> 6, grp = tid >> 4, l16 = tid & 15, kvd = a.n_kv * HD;
     const float * aq = a.q + (size_t) b * a.qkv_stride + (size_t) kh * REP * HD + l16 * 8;
@@ -838,16 +840,16 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     uint16_t * vcache = a.vc_slots ? a.vc_slots[a.slot[b]] + a.layer_off : a.vcache;
     // all of K, then all of V: loads return in order, so the scores and the
     // softmax run while V is still arriving
-    v4u kw[ATTN_CHUNK / 16], vw[ATTN_CHUNK / 16];
+    v4u kw[PPL], vw[PPL];
     #pragma unroll
-    for (int i = 0; i < ATTN_CHUNK / 16; i++) {
-        int t = t0 + grp + 16 * i;
+    for (int i = 0; i < PPL; i++) {
+        int t = t0 + grp + PS * i;
         t = t < t1 ? t : t0;                          // in range; masked below
         kw[i] = __builtin_nontemporal_load((const v4u *) (kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
     }
     #pragma unroll
-    for (int i = 0; i < ATTN_CHUNK / 16; i++) {
-        int t = t0 + grp + 16 * i;
+    for (int i = 0; i < PPL; i++) {
+        int t = t0 + grp + PS * i;
         t = t < t1 ? t : t0;
         vw[i] = __builtin_nontemporal_load((const v4u *) (vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
     }
@@ -872,10 +874,10 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         *(v4u *) (vcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = vnew;
     }
     // scores: 8 FMAs per lane, summed over the 16 lanes of the row
-    float sc[ATTN_CHUNK / 16][REP];
+    float sc[PPL][REP];
     #pragma unroll
-    for (int i = 0; i < ATTN_CHUNK / 16; i++) {
-        const int t = t0 + grp + 16 * i;
+    for (int i = 0; i < PPL; i++) {
+        const int t = t0 + grp + PS * i;
         float kf[8];
         unpack_h8(t == pos ? knew : kw[i], kf);
         #pragma unroll
@@ -887,7 +889,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             sc[i][j] = t < t1 ? p * sl : -INFINITY;
         }
     }
-    // the wave's softmax over its 32 positions, in base 2 (scores were scaled
+    // the wave's softmax over its positions, in base 2 (scores were scaled
     // by log2 e): every lane of a row holds the row's scores, so the row
     // swaps cover the wave
     float m[REP], l[REP], xs[REP];
@@ -895,7 +897,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     for (int j = 0; j < REP; j++) {
         float x = sc[0][j];
         #pragma unroll
-        for (int i = 1; i < ATTN_CHUNK / 16; i++) x = fmaxf(x, sc[i][j]);
+        for (int i = 1; i < PPL; i++) x = fmaxf(x, sc[i][j]);
         xs[j] = x;
     }
     wave_heads<REP>(xs, m, true);
@@ -904,7 +906,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         const float mj = m[j] == -INFINITY ? 0.0f : m[j];   // a wave with no position left
         float ls = 0.0f;
         #pragma unroll
-        for (int i = 0; i < ATTN_CHUNK / 16; i++) {
+        for (int i = 0; i < PPL; i++) {
             const float p = __builtin_amdgcn_exp2f(sc[i][j] - mj);
             sc[i][j] = p;
             ls += p;
@@ -919,8 +921,8 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         #pragma unroll
         for (int e = 0; e < 8; e++) acc[j][e] = 0.0f;
     #pragma unroll
-    for (int i = 0; i < ATTN_CHUNK / 16; i++) {
-        const int t = t0 + grp + 16 * i;
+    for (int i = 0; i < PPL; i++) {
+        const int t = t0 + grp + PS * i;
         float vf[8];
         unpack_h8(t == pos ? vnew : vw[i], vf);
         #pragma unroll
@@ -941,13 +943,15 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         for (int j = 0; j < REP; j++) { wm[wave][j] = m[j]; wl[wave][j] = l[j]; }
     }
     __syncthreads();
-    // combine the 4 waves: rescale each by 2^(m_w - M)
-    for (int idx = tid; idx < REP * HD; idx += ATTN_THREADS) {
+    // combine the waves: rescale each by 2^(m_w - M)
+    for (int idx = tid; idx < REP * HD; idx += NT) {
         const int j = idx / HD, d = idx % HD;
-        float M = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+        float M = wm[0][j];
+        #pragma unroll
+        for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w][j]);
         float o = 0.0f, L = 0.0f;
         #pragma unroll
-        for (int w = 0; w < 4; w++) {
+        for (int w = 0; w < NW; w++) {
             const float e = __builtin_amdgcn_exp2f(wm[w][j] - M);     // M is finite: wave 0 holds t0
             o += e * red[w][j][d];
             L += e * wl[w][j];
@@ -958,7 +962,8 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
 }
 
 #define ATTN_KERNEL(R) \
-    extern "C" __global__ __launch_bounds__(ATTN_THREADS) void sml_attn_r##R(const sml_kattn a) { attn_body<R>(a); }
+    extern "C" __global__ __launch_bounds__(256) void sml_attn_r##R(const sml_kattn a) { attn_body<R, 4>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attn8_r##R(const sml_kattn a) { attn_body<R, 8>(a); }
 ATTN_KERNEL(1) ATTN_KERNEL(2) ATTN_KERNEL(3) ATTN_KERNEL(4) ATTN_KERNEL(5) ATTN_KERNEL(6) ATTN_KERNEL(7) ATTN_KERNEL(8)
 
 // Merge of the splits of one query head (grid: n_head workgroups of HD

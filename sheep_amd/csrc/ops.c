@@ -493,8 +493,10 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
     char name[32];
-    snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
-    hx_launch(name, (unsigned) ns, (unsigned) n_kv, 256, 0, st, &a);
+    const int aw = env_int("SML_ATTN_WAVES", 8) == 4 ? 4 : 8;
+    if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
+    else snprintf(name, sizeof name, "sml_attn%d_r%d", aw, n_head / n_kv);
+    hx_launch(name, (unsigned) ns, (unsigned) n_kv, (unsigned) (64 * aw), 0, st, &a);
     hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
 }
 
@@ -515,8 +517,10 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
     char name[32];
-    snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
-    hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) nseq, 256, 0, st, &a);
+    const int aw = env_int("SML_ATTN_WAVES", 8) == 4 ? 4 : 8;
+    if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
+    else snprintf(name, sizeof name, "sml_attn%d_r%d", aw, n_head / n_kv);
+    hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) nseq, (unsigned) (64 * aw), 0, st, &a);
     hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
 }
 
