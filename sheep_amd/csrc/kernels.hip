@@ -1520,61 +1520,65 @@ GEMM_WIDTH(2) GEMM_WIDTH(3) GEMM_WIDTH(4) GEMM_WIDTH(5) GEMM_WIDTH(6) GEMM_WIDTH
 // ---------------------------------------------------------------- small-M GEMM on MFMA (Q4)
 //
 // The same product as gemm_body for up to 16 activation rows, with the
-// per-group integer dots on v_mfma_i32_16x16x32_i8: A = 16 weight rows x 32
-// codes of one group, B = 32 activation codes x 16 activation rows. Lane l
-// holds A row l%16 / B column l%16 for codes 8*(l/16)..+7, and receives the
-// dots of weight rows 4*(l/16)..+3 for activation row l%16 -- where the
-// per-group epilogue step*s*dot + min*s*sum runs in fp32. In the Q4 plane an
-// 8-byte word at quad q, half h, offset 8*(l/16) holds those codes of groups
-// 4q+2h (low nibbles) and 4q+2h+1 (high nibbles), so one load feeds two
-// MFMAs. Activations are read from L2 (each lane's 8-byte B words), not
-// staged. A workgroup owns RB blocks of 16 rows (SwiGLU: the gate and up
-// blocks of the same rows); its 4 waves split the groups and their partial
-// sums meet in LDS, added in wave order. The float order differs from the
-// GEMV's, so rows agree with it to rounding, not bit for bit.
-#define MG_U 4            // group pairs whose loads are issued together
+// per-group integer dots on v_mfma_i32_16x16x32_i8: A = 32 activation codes
+// x 16 activation rows, B = 32 codes x 16 weight rows (lane layout, checked
+// on the device: lane l holds A row / B column l%16, codes 8*(l/16)..+7, and
+// receives D rows 4*(l/16)..+3 of column l%16). So lane l owns weight row
+// l%16 -- its group fields loaded once per group -- and activation rows
+// 4*(l/16)..+3, whose per-group (s, s*sum) the workgroup stages in LDS as
+// [group][row] float pairs; the per-group epilogue step*s*dot + min*s*sum runs
+// in fp32 on the 16x16 result. In the Q4 plane an 8-byte word at quad q, half
+// h, offset 8*(l/16) holds codes of groups 4q+2h (low nibbles) and 4q+2h+1
+// (high nibbles), so one load feeds two MFMAs. Loads are batched per 8 groups
+// (4 pairs): one 16-byte load brings a weight row's 8 (sq, mq) field pairs and
+// one 4-byte load its superblock's (sd, md). A workgroup owns RB blocks of 16
+// rows (SwiGLU: the gate and up blocks of the same rows); its 4 waves split the
+// groups in whole batches (input widths are multiples of 256 columns) and
+// their partial sums meet in LDS, added in wave order. The float order differs
+// from the GEMV's, so rows agree with it to rounding, not bit for bit.
 template <bool SW, int RB>
 __device__ void mgemm_q4_body(const sml_kgemm & a) {
     typedef long v1l;
     constexpr int NM = SW ? 2 : 1, NACC = NM * RB * 4;
+    extern __shared__ __align__(16) uint8_t lds[];
+    float2 * lsc = (float2 *) lds;                                 // [ng][16] (s, s*sum)
     __shared__ float red[4][NACC][64];
     const int e = blockIdx.y;
     const int m = a.count ? a.count[e] : a.m_all;
     if (m <= 0) return;
-    const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8, np = ng / 2;
+    const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8, nb = ng / 8;
     const int tid = threadIdx.x, lane = tid & 63, c = lane >> 4, i16 = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rb0 = blockIdx.x * (16 * RB);                       // first row of this workgroup
-    const int p0 = wave * np / 4, p1 = (wave + 1) * np / 4;      // this wave's group pairs
+    const int rb0 = blockIdx.x * (16 * RB);
+    const int b0 = wave * nb / 4, b1 = (wave + 1) * nb / 4;       // this wave's batches of 8 groups
     const sml_kmat * mt = a.mats + (size_t) e * (SW ? 2 : 1);
     const size_t abase = (size_t) e * a.mmax;
+    // activation scales of rows 0..15 (zero past m), transposed to [group][row]
+    #pragma unroll 8
+    for (int idx = tid; idx < ng * 16; idx += 256) {
+        const int r = idx / ng, g = idx - r * ng;
+        const size_t fi = (abase + (size_t) (r < m ? r : 0)) * ng + g;
+        const float sv = a.scale[fi];
+        const float su = (float) a.sums[fi];
+        lsc[g * 16 + r] = r < m ? make_float2(sv, sv * su) : make_float2(0.0f, 0.0f);
+    }
     const uint8_t * plane[NM];
     const uint8_t * fqb[NM];
     const uint8_t * fdb[NM];
     #pragma unroll
     for (int k = 0; k < NM; k++) { plane[k] = mt[k].plane[0]; fqb[k] = mt[k].sqmq; fdb[k] = (const uint8_t *) mt[k].sdmd; }
-    const uint32_t rowb = (uint32_t) n / 2;                       // nibble-plane bytes per row
-    // A rows of this lane (clamped in range; rows past the end are never stored)
-    uint32_t aoff[RB];
-    uint32_t fqo[RB][4], fdo[RB][4];                              // field offsets of the lane's 4 result rows
+    const uint32_t rowb = (uint32_t) n / 2;
+    uint32_t boff0[RB], fqo[RB], fdo[RB];
     #pragma unroll
     for (int bk = 0; bk < RB; bk++) {
         const int ra = rb0 + bk * 16 + i16;
-        aoff[bk] = (uint32_t) (ra < a.rows ? ra : a.rows - 1) * rowb + 8u * (uint32_t) c;
-        #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int rd = rb0 + bk * 16 + 4 * c + r;
-            const uint32_t rc = (uint32_t) (rd < a.rows ? rd : a.rows - 1);
-            fqo[bk][r] = rc * (uint32_t) ng * 2u;
-            fdo[bk][r] = rc * (uint32_t) ns * 4u;
-        }
+        const uint32_t rc = (uint32_t) (ra < a.rows ? ra : a.rows - 1);
+        boff0[bk] = rc * rowb + 8u * (uint32_t) c;
+        fqo[bk] = rc * (uint32_t) ng * 2u;
+        fdo[bk] = rc * (uint32_t) ns * 4u;
     }
-    // B: activation row i16 (zero past m)
     const bool tv = i16 < m;
-    const size_t ar = abase + (size_t) (tv ? i16 : 0);
-    const int8_t * qrow = a.q + ar * n + 8 * c;
-    const float * srow = a.scale + ar * ng;
-    const int32_t * urow = a.sums + ar * ng;
+    const int8_t * qrow = a.q + (abase + (size_t) (tv ? i16 : 0)) * n + 8 * c;
     float acc[NM][RB][4];
     #pragma unroll
     for (int k = 0; k < NM; k++)
@@ -1582,67 +1586,53 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
         for (int bk = 0; bk < RB; bk++)
             #pragma unroll
             for (int r = 0; r < 4; r++) acc[k][bk][r] = 0.0f;
-    for (int pb = p0; pb < p1; pb += MG_U) {
-        // loads of MG_U group pairs: A words, B words, activation scales, fields
-        v2u aw[MG_U][NM][RB];
-        v1l bw[MG_U][2];
-        float sv[MG_U][2];
-        int32_t uv[MG_U][2];
-        uint32_t fq[MG_U][NM][RB][4], fd[MG_U][NM][RB][4];
+    __syncthreads();
+    for (int bt = b0; bt < b1; bt++) {
+        const int g0 = 8 * bt;
+        // weights: the 4 pairs' 8-byte words; fields: 8 (sq, mq) pairs and one (sd, md)
+        v2u bwt[4][NM][RB];
+        v4u fq[NM][RB];
+        uint32_t fd[NM][RB];
+        v1l aq[8];
         #pragma unroll
-        for (int p = 0; p < MG_U; p++) {
-            const int pc = pb + p < p1 ? pb + p : p1 - 1;
-            const int gc = 2 * pc;
-            const uint32_t boff = (uint32_t) (gc >> 2) * 64u + (uint32_t) ((gc >> 1) & 1) * 32u;
+        for (int k = 0; k < NM; k++)
+            #pragma unroll
+            for (int bk = 0; bk < RB; bk++) {
+                #pragma unroll
+                for (int p = 0; p < 4; p++)
+                    bwt[p][k][bk] = *(const v2u *) (plane[k] + (boff0[bk] + (uint32_t) (g0 / 4 + (p >> 1)) * 64u + (uint32_t) (p & 1) * 32u));
+                fq[k][bk] = *(const v4u *) (fqb[k] + (fqo[bk] + (uint32_t) g0 * 2u));
+                fd[k][bk] = *(const uint32_t *) (fdb[k] + (fdo[bk] + (uint32_t) bt * 4u));
+            }
+        #pragma unroll
+        for (int j = 0; j < 8; j++) aq[j] = *(const v1l *) (qrow + (size_t) (g0 + j) * 32);
+        #pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int g = g0 + j, p = j >> 1, h = j & 1;
+            const v1l av = tv ? aq[j] : 0;
+            const float4 s01 = *(const float4 *) &lsc[g * 16 + 4 * c];
+            const float4 s23 = *(const float4 *) &lsc[g * 16 + 4 * c + 2];
+            const float sv[4] = {s01.x, s01.z, s23.x, s23.z}, ssv[4] = {s01.y, s01.w, s23.y, s23.w};
             #pragma unroll
             for (int k = 0; k < NM; k++)
                 #pragma unroll
                 for (int bk = 0; bk < RB; bk++) {
-                    aw[p][k][bk] = __builtin_nontemporal_load((const v2u *) (plane[k] + (aoff[bk] + boff)));
+                    const v2u w = bwt[p][k][bk];
+                    const v2u cd = h ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
+                    const v1l bv = (v1l) (((unsigned long) cd.y << 32) | cd.x);
+                    v4i d = { 0, 0, 0, 0 };
+                    d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, d, 0, 0, 0);
+                    const uint32_t f = fq[k][bk][j >> 1] >> (16 * (j & 1)), d2 = fd[k][bk];
+                    const float wsc = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
+                    const float wmn = h2f((uint16_t) (d2 >> 16)) * ((float) ((f >> 8) & 0xFFu) - 127.0f);
                     #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        fq[p][k][bk][r] = *(const uint32_t *) (fqb[k] + (fqo[bk][r] + (uint32_t) gc * 2u));
-                        fd[p][k][bk][r] = *(const uint32_t *) (fdb[k] + (fdo[bk][r] + (uint32_t) (gc >> 3) * 4u));
+                        acc[k][bk][r] += (wsc * sv[r]) * (float) d[r];
+                        acc[k][bk][r] += wmn * ssv[r];
                     }
                 }
-            #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                bw[p][h] = *(const v1l *) (qrow + (size_t) (gc + h) * 32);
-                sv[p][h] = srow[gc + h];
-                uv[p][h] = urow[gc + h];
-            }
-        }
-        #pragma unroll
-        for (int p = 0; p < MG_U; p++) {
-            if (pb + p < p1) {
-                #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const v1l b = tv ? bw[p][h] : 0;
-                    const float s = tv ? sv[p][h] : 0.0f;
-                    const float ss = s * (float) uv[p][h];
-                    #pragma unroll
-                    for (int k = 0; k < NM; k++)
-                        #pragma unroll
-                        for (int bk = 0; bk < RB; bk++) {
-                            const v2u w = aw[p][k][bk];
-                            const v2u cd = h ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
-                            const v1l av = (v1l) (((unsigned long) cd.y << 32) | cd.x);
-                            v4i d = { 0, 0, 0, 0 };
-                            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, d, 0, 0, 0);
-                            #pragma unroll
-                            for (int r = 0; r < 4; r++) {
-                                const uint32_t f = fq[p][k][bk][r] >> (16 * h), d2 = fd[p][k][bk][r];
-                                const float wsc = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
-                                const float wmn = h2f((uint16_t) (d2 >> 16)) * ((float) ((f >> 8) & 0xFFu) - 127.0f);
-                                acc[k][bk][r] += wsc * (s * (float) d[r]);
-                                acc[k][bk][r] += wmn * ss;
-                            }
-                        }
-                }
-            }
         }
     }
-    // the 4 waves' partial sums, added in wave order
     #pragma unroll
     for (int k = 0; k < NM; k++)
         #pragma unroll
@@ -1650,33 +1640,36 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             #pragma unroll
             for (int r = 0; r < 4; r++) red[wave][(k * RB + bk) * 4 + r][lane] = acc[k][bk][r];
     __syncthreads();
-    if (wave != 0 || !tv) return;
-    float * y = a.y + (abase + i16) * a.rows;
-    const float * res = a.resid ? a.resid + (abase + i16) * a.rows : nullptr;
+    if (wave != 0) return;
     #pragma unroll
-    for (int bk = 0; bk < RB; bk++)
+    for (int bk = 0; bk < RB; bk++) {
+        const int row = rb0 + bk * 16 + i16;
+        if (row >= a.rows) continue;
         #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int row = rb0 + bk * 16 + 4 * c + r;
-            if (row >= a.rows) continue;
+            const int mr = 4 * c + r;
+            if (mr >= m) continue;
             float t[NM];
             #pragma unroll
             for (int k = 0; k < NM; k++) {
                 const int j = (k * RB + bk) * 4 + r;
                 t[k] = ((red[0][j][lane] + red[1][j][lane]) + red[2][j][lane]) + red[3][j][lane];
             }
+            float * y = a.y + (abase + mr) * a.rows;
             if constexpr (SW) {
                 y[row] = (t[0] / (1.0f + expf(-t[0]))) * t[1];           // sml/sml-run.c:451-454
             } else {
                 float v = t[0];
                 if (a.bias) v += a.bias[row];
-                if (res) v = res[row] + v;
+                if (a.resid) v = a.resid[(abase + mr) * a.rows + row] + v;
                 y[row] = v;
             }
         }
+    }
 }
 
 extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_r1(const sml_kgemm a) { mgemm_q4_body<false, 1>(a); }
 extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_r2(const sml_kgemm a) { mgemm_q4_body<false, 2>(a); }
 extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_s_r1(const sml_kgemm a) { mgemm_q4_body<true, 1>(a); }
 extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_s_r2(const sml_kgemm a) { mgemm_q4_body<true, 2>(a); }
+

@@ -731,10 +731,14 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
     // (count != NULL) hold few rows each and stay on VALU.
     const char * mode = getenv("SML_MULTI");
     const int exact = mode && !strcmp(mode, "exact");
-    if (nbits == 4 && !count && m_all > 8 && !exact) {
-        const int rb = !swiglu && rows >= 32768 ? 2 : 1;
+    if (nbits == 4 && !count && m_all > 8 && !exact && cols % 256 == 0 && cols <= 14336) {
+        int rb = !swiglu && rows >= 32768 ? 2 : 1;
+        const int fr = env_int("SML_MGEMM_RB", 0);
+        if (fr == 1 || fr == 2) rb = fr;
         snprintf(name, sizeof name, "sml_mgemm_q4%s_r%d", swiglu ? "_s" : "", rb);
-        hx_launch(name, (unsigned) ((rows + 16 * rb - 1) / (16 * rb)), (unsigned) ngroups, 256, 0, st, &a);
+        // LDS: the activation rows' (s, s*sum) per group, [group][16] (56 KB at 14336 columns)
+        hx_launch(name, (unsigned) ((rows + 16 * rb - 1) / (16 * rb)), (unsigned) ngroups, 256,
+                  (size_t) (cols / 32) * 16 * 8, st, &a);
         return;
     }
     snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d", nbits, swiglu ? "_s" : "", mt);
