@@ -212,6 +212,37 @@ def moe_layer(tmp, T=16, iters=50):
             "bytes_per_step": b, "GB/s": round(b / us / 1e3, 1)}
 
 
+QWEN = dict(n_layer=28, n_embd=1536, n_head=12, n_head_kv=2, n_ff=8960, n_vocab=151936, rope_theta=1e6,
+            rms_eps=1e-6, qkv_bias=True, tied=True, random_perm=False, nbits=4, seed=1002)
+
+
+def qwen_decode(tmp, prompt_len=2048, steps=64):
+    """The Qwen2.5-1.5B-shaped decoder (28 layers, hidden 1536, FFN 8960,
+    12/2 heads, tied 151936-token head, q/k/v bias, identity permutations):
+    a 2048-id prompt read a token at a time, then 64 greedy tokens timed as
+    one generate call."""
+    path = os.path.join(tmp, "qwen25_1p5b_q4.ssf")
+    sa.synth_model(path, n_ctx_train=4096, **QWEN)
+    dec = sa.Decoder(path, n_ctx=prompt_len + steps + 8)
+    try:
+        ids = np.random.default_rng(1002).integers(0, QWEN["n_vocab"], prompt_len).astype(np.int32)
+        tok = int(np.argmax(dec.prefill(ids, 0, QWEN["n_vocab"])))
+        dec.generate(tok, prompt_len, 4)                     # warm-up (graph capture)
+        sa.sync()
+        t0 = time.perf_counter()
+        dec.generate(tok, prompt_len, steps)
+        sa.sync()
+        dt = time.perf_counter() - t0
+        wbytes = dec.weight_bytes()
+    finally:
+        dec.close()
+        os.remove(path)
+    return {"tokens": steps, "positions": f"{prompt_len}..{prompt_len + steps - 1}",
+            "tokens_per_s": round(steps / dt, 1), "weight_bytes_per_token": wbytes,
+            "roofline_tokens_per_s_weights_only": round(HBM_PEAK_GBS * 1e9 / wbytes, 1),
+            "frac_of_weights_roofline": round(steps / dt / (HBM_PEAK_GBS * 1e9 / wbytes), 4)}
+
+
 def batched_decode(dec, n_vocab, ns=16, steps=20, pos0=1024):
     """Aggregate tokens/s of ns sequences stepped together (sml_gpu_step_multi)
     at positions pos0.. of their own KV slots."""
@@ -342,6 +373,9 @@ def run(a, work):
         log(f"batched: {extra['batched_decode']} ({time.perf_counter() - t1:.1f}s)")
     dec.close()
     if not a.no_extra:
+        t1 = time.perf_counter()
+        extra["qwen25_1p5b_decode"] = qwen_decode(work)
+        log(f"qwen2.5-1.5b decode: {extra['qwen25_1p5b_decode']} ({time.perf_counter() - t1:.1f}s)")
         t1 = time.perf_counter()
         extra["moe_layer"] = moe_layer(work)
         log(f"moe: {extra['moe_layer']} ({time.perf_counter() - t1:.1f}s)")
