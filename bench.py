@@ -243,6 +243,43 @@ def qwen_decode(tmp, prompt_len=2048, steps=64):
             "frac_of_weights_roofline": round(steps / dt / (HBM_PEAK_GBS * 1e9 / wbytes), 4)}
 
 
+def small_gemm(tmp, M=16, iters=60):
+    """The 16-row small-M GEMMs of the batched step over rotating copies:
+    SwiGLU gate+up 2 x 14336 x 4096, 4096 x 4096 and 4096 x 14336, with
+    seeded int8 activation rows. Returns µs per launch (best of 3)."""
+    rng = np.random.default_rng(1005)
+    out = {}
+    for rows, cols, sw, n in [(14336, 4096, True, 8), (4096, 4096, False, 24), (4096, 14336, False, 16)]:
+        p = os.path.join(tmp, f"gemm_{rows}x{cols}.ssf")
+        sa.synth_matrix(p, rows, cols, nbits=4, seed=1005)
+        mats = [sa.Mat.from_file(p, "w") for _ in range(n * (2 if sw else 1))]
+        q = sa.DevBuf.of(rng.integers(-127, 128, M * cols).astype(np.int8))
+        s = sa.DevBuf.of((np.abs(rng.standard_normal(M * cols // 32)) * 0.01).astype(np.float32))
+        u = sa.DevBuf.of(rng.integers(-2000, 2000, M * cols // 32).astype(np.int32))
+        y = sa.DevBuf(M * rows * 4)
+        if sw:
+            fn = lambda i: sa.gemm_swiglu(mats[2 * (i % n)], mats[2 * (i % n) + 1], q, s, u, M, y)
+        else:
+            fn = lambda i: sa.gemm(mats[i % n], q, s, u, M, y)
+        for i in range(4):
+            fn(i)
+        sa.sync()
+        best = 1e9
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for i in range(iters):
+                fn(i)
+            sa.sync()
+            best = min(best, (time.perf_counter() - t0) / iters * 1e6)
+        nbytes = mats[0].bytes * (2 if sw else 1)
+        out[f"{'swiglu_2x' if sw else ''}{rows}x{cols}"] = {"rows_m": M, "us": round(best, 2),
+                                                              "GB/s": round(nbytes / best / 1e3, 1)}
+        for m in mats:
+            m.free()
+        os.remove(p)
+    return out
+
+
 def batched_decode(dec, n_vocab, ns=16, steps=20, pos0=1024):
     """Aggregate tokens/s of ns sequences stepped together (sml_gpu_step_multi)
     at positions pos0.. of their own KV slots."""
@@ -294,6 +331,7 @@ def main():
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
     ap.add_argument("--no-extra", action="store_true", help="skip the batched, MoE and width-sweep lines")
     ap.add_argument("--pmc-probe", metavar="SSF", help=argparse.SUPPRESS)
+    ap.add_argument("--small-gemm", action="store_true", help="only time the 16-row small-M GEMMs")
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: fill the 4096 context)")
     a = ap.parse_args()
@@ -308,7 +346,7 @@ def main():
     tmp = scratch_dir()
     work = tempfile.mkdtemp(prefix="smlbench_", dir=tmp)
     try:
-        res = run(a, work)
+        res = {"small_m_gemm": small_gemm(work)} if a.small_gemm else run(a, work)
     finally:
         if not a.keep:
             shutil.rmtree(work, ignore_errors=True)
@@ -376,6 +414,9 @@ def run(a, work):
         t1 = time.perf_counter()
         extra["qwen25_1p5b_decode"] = qwen_decode(work)
         log(f"qwen2.5-1.5b decode: {extra['qwen25_1p5b_decode']} ({time.perf_counter() - t1:.1f}s)")
+        t1 = time.perf_counter()
+        extra["small_m_gemm"] = small_gemm(work)
+        log(f"small-M GEMM (16 rows): {extra['small_m_gemm']} ({time.perf_counter() - t1:.1f}s)")
         t1 = time.perf_counter()
         extra["moe_layer"] = moe_layer(work)
         log(f"moe: {extra['moe_layer']} ({time.perf_counter() - t1:.1f}s)")
