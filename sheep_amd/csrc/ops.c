@@ -58,7 +58,7 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
     for (int i = 0; i < 3; i++) sz[i] = i < np ? R * ssf_plane_row_bytes(pb[i], cols) : 0;
     sz[3] = R * ng * 2;          // (sq, mq) per group
     sz[4] = R * ns * 4;          // (sd, md) per superblock
-    sz[5] = sizeof(sml_kmat);    // the descriptor, for small-M GEMM tables
+    sz[5] = 3 * sizeof(sml_kmat);   // the descriptor, then a (gate, up) pair table (small-M GEMM tables)
     for (int i = 0; i < 6; i++) { off[i] = tot; tot += al256(sz[i]); }
     // the fields interleaved on the host: 8-bit (or widened 6-bit) values, min bias 127
     uint8_t * fq = malloc(sz[3]);
@@ -762,17 +762,15 @@ int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const 
     if (!gate || !up || nrow < 1 || nrow > 16) hx_failf("gemm of %d rows (1..16)", nrow);
     if (up->nbits != gate->nbits || up->cols != gate->cols || up->k.rows != gate->k.rows)
         hx_failf("SwiGLU needs gate and up of one shape and width");
-    sml_kmat tab[2] = { gate->k, up->k };
-    sml_kmat * dt = hx_malloc(sizeof tab);
-    jmp_buf * outer = hx.jb;
-    jmp_buf jb;
-    if (setjmp(jb)) { hx.jb = outer; hipFree(dt); longjmp(*outer, 1); }
-    hx.jb = &jb;
-    HX(hipMemcpy(dt, tab, sizeof tab, hipMemcpyHostToDevice));
-    op_gemm(0, dt, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h, NULL, NULL);
-    HX(hipStreamSynchronize(0));
-    hx.jb = outer;
-    HX(hipFree(dt));
+    // the (gate, up) table lives in the gate matrix's allocation, rewritten
+    // only when the gate is paired with another up than last time
+    sml_kmat * pair = gate->kdev + 1;
+    if (gate->up_pair != up) {
+        sml_kmat tab[2] = { gate->k, up->k };
+        HX(hipMemcpy(pair, tab, sizeof tab, hipMemcpyHostToDevice));
+        ((sml_hip_mat *) gate)->up_pair = up;
+    }
+    op_gemm(0, pair, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h, NULL, NULL);
     HX_LEAVE();
     return 0;
 }
