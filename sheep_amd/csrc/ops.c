@@ -763,12 +763,14 @@ int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const 
     if (up->nbits != gate->nbits || up->cols != gate->cols || up->k.rows != gate->k.rows)
         hx_failf("SwiGLU needs gate and up of one shape and width");
     // the (gate, up) table lives in the gate matrix's allocation, rewritten
-    // only when the gate is paired with another up than last time
+    // only when the gate is paired with another up than last time (compared
+    // by descriptor, so a new matrix at a freed one's address is caught)
     sml_kmat * pair = gate->kdev + 1;
-    if (gate->up_pair != up) {
+    if (!gate->pair_set || memcmp(&gate->up_k, &up->k, sizeof up->k)) {
         sml_kmat tab[2] = { gate->k, up->k };
         HX(hipMemcpy(pair, tab, sizeof tab, hipMemcpyHostToDevice));
-        ((sml_hip_mat *) gate)->up_pair = up;
+        ((sml_hip_mat *) gate)->up_k = up->k;
+        ((sml_hip_mat *) gate)->pair_set = 1;
     }
     op_gemm(0, pair, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h, NULL, NULL);
     HX_LEAVE();

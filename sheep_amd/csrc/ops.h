@@ -9,7 +9,8 @@
 struct sml_hip_mat {
     sml_kmat k;          // device pointers; k.rows is the row count
     sml_kmat * kdev;     // the same descriptor in device memory, then room for a (gate, up) pair (small-M GEMM tables)
-    const struct sml_hip_mat * up_pair;   // the up matrix kdev[1..2] was last written for
+    sml_kmat up_k;       // the up descriptor kdev[1..2] was last written for
+    int pair_set;
     int nbits, cols;
     void * mem;          // the single allocation holding planes and fields
     size_t bytes;        // planes + fields bytes (what one GEMV streams)
