@@ -194,22 +194,28 @@ def width_sweep(tmp, target_bytes=6e8, iters=200):
 def moe_layer(tmp, T=16, iters=50):
     """A Mixtral-shaped MoE FFN layer (hidden 4096, 8 experts of 14336 SwiGLU
     Q4, top-2 softmax over the chosen, f32 router) on T tokens of N(0,1)
-    input: time per step and the bytes of the experts the step touches."""
+    input: time per step and the bytes of the experts the step touches, with
+    the expert inputs quantized per 32 (the stepped moe_ffn's regime) and per
+    256 (moe_ffn_batch's in the batched regimes)."""
     p = os.path.join(tmp, "mixtral_layer.ssf")
     sa.synth_model(p, n_layer=1, n_embd=4096, n_head=32, n_head_kv=8, n_ff=14336, n_vocab=1024, n_expert=8,
                    n_expert_used=2, moe_flags=1, rope_theta=1e6, seed=1005)
     moe = sa.MoE(p, 0, 16)
     x = sa.DevBuf.of(np.random.default_rng(1005).standard_normal((T, 4096)).astype(np.float32))
     out = sa.DevBuf(T * 4096 * 4)
-    moe.time(x, T, out, 3)
-    ms, cnt = moe.time(x, T, out, iters)
-    us = ms * 1000.0 / iters
-    touched = int((cnt > 0).sum())
-    b = touched * moe.expert_bytes + moe.nexp * 4096 * 4
+    res = {"tokens": T}
+    for name, sb in (("per32", False), ("per256", True)):
+        moe.regime(sb)
+        moe.time(x, T, out, 3)
+        ms, cnt = moe.time(x, T, out, iters)
+        us = ms * 1000.0 / iters
+        touched = int((cnt > 0).sum())
+        b = touched * moe.expert_bytes + moe.nexp * 4096 * 4
+        res.update({"experts_touched": touched, "tokens_per_expert": cnt.tolist(), "bytes_per_step": b})
+        res[name] = {"us_per_step": round(us, 2), "GB/s": round(b / us / 1e3, 1)}
     moe.free()
     os.remove(p)
-    return {"tokens": T, "us_per_step": round(us, 2), "experts_touched": touched, "tokens_per_expert": cnt.tolist(),
-            "bytes_per_step": b, "GB/s": round(b / us / 1e3, 1)}
+    return res
 
 
 QWEN = dict(n_layer=28, n_embd=1536, n_head=12, n_head_kv=2, n_ff=8960, n_vocab=151936, rope_theta=1e6,
@@ -246,7 +252,9 @@ def qwen_decode(tmp, prompt_len=2048, steps=64):
 def small_gemm(tmp, M=16, iters=60):
     """The 16-row small-M GEMMs of the batched step over rotating copies:
     SwiGLU gate+up 2 x 14336 x 4096, 4096 x 4096 and 4096 x 14336, with
-    seeded int8 activation rows. Returns µs per launch (best of 3)."""
+    seeded int8 activation rows, for per-32 and per-256 activations (the
+    per-256 scale repeats over each superblock's 8 groups). Returns µs per
+    launch (best of 3) and the weight bytes' rate."""
     rng = np.random.default_rng(1005)
     out = {}
     for rows, cols, sw, n in [(14336, 4096, True, 8), (4096, 4096, False, 24), (4096, 14336, False, 16)]:
@@ -254,26 +262,30 @@ def small_gemm(tmp, M=16, iters=60):
         sa.synth_matrix(p, rows, cols, nbits=4, seed=1005)
         mats = [sa.Mat.from_file(p, "w") for _ in range(n * (2 if sw else 1))]
         q = sa.DevBuf.of(rng.integers(-127, 128, M * cols).astype(np.int8))
-        s = sa.DevBuf.of((np.abs(rng.standard_normal(M * cols // 32)) * 0.01).astype(np.float32))
+        s32 = (np.abs(rng.standard_normal(M * cols // 32)) * 0.01).astype(np.float32)
+        s = sa.DevBuf.of(s32)
+        s256 = sa.DevBuf.of(np.repeat(s32.reshape(-1, 8)[:, :1], 8, axis=1).reshape(-1))
         u = sa.DevBuf.of(rng.integers(-2000, 2000, M * cols // 32).astype(np.int32))
         y = sa.DevBuf(M * rows * 4)
-        if sw:
-            fn = lambda i: sa.gemm_swiglu(mats[2 * (i % n)], mats[2 * (i % n) + 1], q, s, u, M, y)
-        else:
-            fn = lambda i: sa.gemm(mats[i % n], q, s, u, M, y)
-        for i in range(4):
-            fn(i)
-        sa.sync()
-        best = 1e9
-        for _ in range(3):
-            t0 = time.perf_counter()
-            for i in range(iters):
+        nbytes = mats[0].bytes * (2 if sw else 1)
+        res = {"rows_m": M}
+        for name, sb, sc in (("per32", False, s), ("per256", True, s256)):
+            if sw:
+                fn = lambda i: sa.gemm_swiglu(mats[2 * (i % n)], mats[2 * (i % n) + 1], q, sc, u, M, y, per256=sb)
+            else:
+                fn = lambda i: sa.gemm(mats[i % n], q, sc, u, M, y, per256=sb)
+            for i in range(4):
                 fn(i)
             sa.sync()
-            best = min(best, (time.perf_counter() - t0) / iters * 1e6)
-        nbytes = mats[0].bytes * (2 if sw else 1)
-        out[f"{'swiglu_2x' if sw else ''}{rows}x{cols}"] = {"rows_m": M, "us": round(best, 2),
-                                                              "GB/s": round(nbytes / best / 1e3, 1)}
+            best = 1e9
+            for _ in range(3):
+                t0 = time.perf_counter()
+                for i in range(iters):
+                    fn(i)
+                sa.sync()
+                best = min(best, (time.perf_counter() - t0) / iters * 1e6)
+            res[name] = {"us": round(best, 2), "GB/s": round(nbytes / best / 1e3, 1)}
+        out[f"{'swiglu_2x' if sw else ''}{rows}x{cols}"] = res
         for m in mats:
             m.free()
         os.remove(p)
@@ -282,19 +294,28 @@ def small_gemm(tmp, M=16, iters=60):
 
 def batched_decode(dec, n_vocab, ns=16, steps=20, pos0=1024):
     """Aggregate tokens/s of ns sequences stepped together (sml_gpu_step_multi)
-    at positions pos0.. of their own KV slots."""
+    at positions pos0.. of their own KV slots, in the default regime (per-256
+    activations above two sequences) and the per-32 one."""
     dec.slots(ns)
-    for b in range(ns):
-        dec.prefill_slot(b, (np.arange(8, dtype=np.int32) * 7 + b) % n_vocab, pos0 - 8, n_vocab)
-    toks = list(range(1, ns + 1))
-    dec.step_multi(toks, [pos0] * ns, list(range(ns)), n_vocab)
-    sa.sync()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        dec.step_multi(toks, [pos0 + 1 + i] * ns, list(range(ns)), n_vocab)
-    dt = time.perf_counter() - t0
-    return {"sequences": ns, "ms_per_step": round(dt / steps * 1e3, 3), "tokens_per_s": round(ns * steps / dt, 1),
-            "positions": f"{pos0 + 1}..{pos0 + steps}"}
+    res = {"sequences": ns}
+    for name, env in (("per256", None), ("per32", "16")):
+        if env:
+            os.environ["SML_MULTI_EXACT_MAX"] = env
+        try:
+            for b in range(ns):
+                dec.prefill_slot(b, (np.arange(8, dtype=np.int32) * 7 + b) % n_vocab, pos0 - 8, n_vocab)
+            toks = list(range(1, ns + 1))
+            dec.step_multi(toks, [pos0] * ns, list(range(ns)), n_vocab)
+            sa.sync()
+            t0 = time.perf_counter()
+            for i in range(steps):
+                dec.step_multi(toks, [pos0 + 1 + i] * ns, list(range(ns)), n_vocab)
+            dt = time.perf_counter() - t0
+        finally:
+            os.environ.pop("SML_MULTI_EXACT_MAX", None)
+        res[name] = {"ms_per_step": round(dt / steps * 1e3, 3), "tokens_per_s": round(ns * steps / dt, 1),
+                     "positions": f"{pos0 + 1}..{pos0 + steps}"}
+    return res
 
 
 def cpu_baseline(path, threads, budget_s=12.0, max_tokens=1200):

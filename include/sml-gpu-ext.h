@@ -31,9 +31,12 @@ const char * sml_gpu_last_error(void);
 
 // ---------------------------------------------------------------- several sequences
 // The multi-sequence step sml-batched drives on the CPU through
-// sml_forward_multi (sml/sml-run.h:290-294, sml/sml-batched.c:82-130), in its
-// exact activation regime (SML_MULTI=exact: per-32 int8 activations, so every
-// sequence's logits equal decoding it alone, bit for bit).
+// sml_forward_multi (sml/sml-run.h:290-294, sml/sml-batched.c:82-130), with
+// its activation regime (sml/sml-run.c:2579-2596): SML_MULTI=exact, or at
+// most SML_MULTI_EXACT_MAX (default 2) sequences, quantizes per 32 values, so
+// every sequence's logits equal decoding it alone, bit for bit; otherwise
+// every product's input is quantized per 256 values (sml_quantize_act_sb) and
+// Q4 products sum each superblock in integers, as sml_rlp_matvec does.
 //
 // Give the open model ns (1..16) KV cache slots; slot 0 is the cache
 // sml_gpu_step / sml_gpu_prefill use. Every layer's q, k and v must share one

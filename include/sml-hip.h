@@ -106,6 +106,19 @@ int sml_hip_gemm(const sml_hip_mat * m, const int8_t * q, const float * scale, c
 // (the batched gate/up of moe_expert_batch, sml/sml-run.c:3166-3185)
 int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q, const float * scale,
                         const int32_t * sums, int nrow, float * h);
+// The same two products for activations quantized per 256 values
+// (sml_hip_normq with per256 = 1, the batched regime's sml_quantize_act_sb).
+// Q4 with input widths a multiple of 256 sums each superblock's
+// sq_g*dot_g and (mq_g-127)*sum_g in integers and applies the fp32 scales
+// once per 256 columns; other widths run the per-group kernels, which are
+// exact on such activations (the scale repeats in every group).
+// replaces sml_matvec_batch_flat4_sb and sml_rlp_matvec
+// (sml/sml-kernel.c:1414-1435,1820-1840) as batch_group dispatches them in
+// the prompt and default multi-sequence regimes (sml/sml-run.c:2090-2150)
+int sml_hip_gemm_sb(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
+                    float * y);
+int sml_hip_gemm_swiglu_sb(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q, const float * scale,
+                           const int32_t * sums, int nrow, float * h);
 
 // ------------------------------------------------------------ MoE expert FFN
 // One MoE FFN layer resident in HBM: the f32 router (and bias) and every
@@ -118,6 +131,11 @@ typedef struct sml_hip_moe sml_hip_moe;
 sml_hip_moe * sml_hip_moe_from_file(const char * path, int layer, int max_tokens);
 void          sml_hip_moe_free(sml_hip_moe * m);
 int           sml_hip_moe_info(const sml_hip_moe * m, int * nexp, int * k, int * n_ff, size_t * expert_bytes);
+// Activation regime of the expert products: per256 = 0 (default) quantizes
+// per 32 values, as the stepped moe_ffn does (sml/sml-run.c:3071-3124);
+// 1 per 256, as moe_ffn_batch does in the batched regimes
+// (sml/sml-run.c:3153-3241 through batch_group, sml/sml-run.c:2103-2127).
+int           sml_hip_moe_regime(sml_hip_moe * m, int per256);
 // out[t] = sum over the chosen experts j of w[t][j] * FFN_e(x[t]) for T tokens
 // of normed input x [T][n_embd]: the router in double (sml/sml-run.c:3075-3080),
 // sml_moe_route's choice (sml/sml-run.c:2925-3037), each chosen expert's

@@ -63,6 +63,7 @@ def oracle():
             "orc_model_close": (None, [c_void_p]),
             "orc_forward": (P(c_float), [c_void_p, c_int, c_int]),
             "orc_n_vocab": (c_int, [c_void_p]),
+            "orc_model_per256": (None, [c_void_p, c_int]),
         }
         for k, (r, a) in sig.items():
             f = getattr(l, k)
@@ -102,6 +103,16 @@ def ref():
             "sml_dequant_row_flat6": (None, [c_void_p] * 7 + [c_int, c_int]),
             "sml_dequant_row_flat8": (None, [c_void_p] * 7 + [c_int, c_int]),
             "sml_dequant_bits1_add": (None, [c_void_p] * 4 + [c_int, c_int, c_int]),
+            "sml_matvec_batch_flat4": (None, [c_void_p] * 6 + [c_void_p, c_int, c_int, c_int, c_int, c_int]),
+            "sml_matvec_batch_flat4_sb": (None, [c_void_p] * 6 + [c_void_p, c_int, c_int, c_int, c_int, c_int]),
+            "sml_rlp_ok": (c_int, [c_int, c_int, c_int, c_int]),
+            "sml_rlp_bytes": (ctypes.c_size_t, [c_int, c_int, c_int]),
+            "sml_rlp_pack": (None, [c_void_p] * 7 + [c_int, c_int, c_int, c_int]),
+            "sml_rlp_matvec": (None, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int]),
+            "ref_multi_open": (c_void_p, [c_char_p, c_int, c_int, c_int]),
+            "ref_multi_forward": (P(c_float), [c_void_p, c_int, c_int, c_int]),
+            "ref_multi_step": (None, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+            "ref_multi_close": (None, [c_void_p]),
             "sml_kernel_init": (None, []),
             "sml_kernel_scale6": (None, [c_int]),
             "sml_kernel_minneg": (None, [c_int]),
@@ -210,6 +221,52 @@ def ref_matvec(t, q, s, u):
     return y
 
 
+def _acts(q, s, u):
+    """An array of the reference's sml_act over rows of q [nb][n], s/u [nb][n/32]."""
+    nb, n = q.shape
+    arr = (SmlAct * nb)()
+    for i in range(nb):
+        arr[i] = SmlAct(q[i].ctypes.data, s[i].ctypes.data, u[i].ctypes.data, n)
+    return arr
+
+
+def ref_matvec_batch(t, q, s, u, sb=True):
+    """y [nb][rows] through the reference's batched flat 4-bit kernel:
+    sml_matvec_batch_flat4_sb on per-256 activations (sb) or
+    sml_matvec_batch_flat4 on per-32 ones (sml/sml-kernel.c:1008-1021,1414-1435)."""
+    q, s, u = (np.ascontiguousarray(v) for v in (q, s, u))
+    nb = q.shape[0]
+    y = np.zeros((nb, t.rows), np.float32)
+    pl = t.planes()
+    md = t.md.ctypes.data if t.md is not None else None
+    mq = t.mq.ctypes.data if t.mq is not None else None
+    arr = _acts(q, s, u)
+    f = ref().sml_matvec_batch_flat4_sb if sb else ref().sml_matvec_batch_flat4
+    f(y.ctypes.data, pl[0].ctypes.data, t.sd.ctypes.data, t.sq.ctypes.data, md, mq, ctypes.addressof(arr), nb,
+      t.rows, 0, t.rows, t.cols)
+    return y
+
+
+def ref_rlp_matvec(t, q, s, u):
+    """y [nb][rows] through the reference's once-packed rows-in-lanes kernel
+    (sml_rlp_pack + sml_rlp_matvec, sml/sml-kernel.c:1646-1840), the default
+    multi-sequence path; per-256 activations. None when the tensor does not
+    qualify (sml_rlp_ok)."""
+    r = ref()
+    if not r.sml_rlp_ok(t.rows, t.cols, t.nbits, int(t.mq is not None)):
+        return None
+    q, s, u = (np.ascontiguousarray(v) for v in (q, s, u))
+    nb = q.shape[0]
+    pk = np.zeros(r.sml_rlp_bytes(t.rows, t.cols, t.nbits), np.uint8)
+    pl = t.planes()
+    r.sml_rlp_pack(pk.ctypes.data, pl[0].ctypes.data, None, t.sd.ctypes.data, t.sq.ctypes.data, t.md.ctypes.data,
+                   t.mq.ctypes.data, t.nbits, 0, t.rows // 8, t.cols)
+    y = np.zeros((nb, t.rows), np.float32)
+    arr = _acts(q, s, u)
+    r.sml_rlp_matvec(y.ctypes.data, t.rows, pk.ctypes.data, t.nbits, ctypes.addressof(arr), nb, 0, t.rows, t.cols)
+    return y
+
+
 def ref_dequant_row(t, row):
     """One row through the reference's own dequantizers (sml/sml-run.c:586-603,3300-3335)."""
     r = ref()
@@ -240,11 +297,16 @@ def ref_dequant_row(t, row):
 class OracleModel:
     """orc_forward over an SSF file."""
 
-    def __init__(self, path, n_ctx):
+    def __init__(self, path, n_ctx, per256=False):
         self.h = oracle().orc_model_open(str(path).encode(), n_ctx)
         if not self.h:
             raise RuntimeError(f"oracle cannot open {path}")
         self.n_vocab = oracle().orc_n_vocab(self.h)
+        self.per256(per256)
+
+    def per256(self, on):
+        """Quantize every product's input per 256 values (True) or per 32."""
+        oracle().orc_model_per256(self.h, 1 if on else 0)
 
     def forward(self, tok, pos):
         p = oracle().orc_forward(self.h, tok, pos)
@@ -277,6 +339,37 @@ class RefModel:
     def close(self):
         if self.h:
             ref().ref_close(self.h)
+            self.h = None
+
+
+class RefMulti:
+    """ns contexts of the reference engine over one SSF file: slots stepped
+    one at a time (sml_forward) and together (sml_forward_multi)."""
+
+    def __init__(self, path, n_ctx, ns, threads=8):
+        self.h = ref().ref_multi_open(str(path).encode(), n_ctx, threads, ns)
+        if not self.h:
+            raise RuntimeError(f"the reference cannot open {path}")
+        self.ns = ns
+        hh = ref().ref_open(str(path).encode(), 0, 1, 0)
+        self.n_vocab = ref().ref_n_vocab(hh)
+        ref().ref_close(hh)
+
+    def forward(self, slot, tok, pos):
+        p = ref().ref_multi_forward(self.h, slot, tok, pos)
+        return np.ctypeslib.as_array(p, shape=(self.n_vocab,)).copy()
+
+    def step(self, toks, pos):
+        ns = len(toks)
+        t = np.ascontiguousarray(toks, dtype=np.int32)
+        p = np.ascontiguousarray(pos, dtype=np.int32)
+        out = np.zeros((ns, self.n_vocab), np.float32)
+        ref().ref_multi_step(self.h, t.ctypes.data, p.ctypes.data, ns, out.ctypes.data)
+        return out
+
+    def close(self):
+        if self.h:
+            ref().ref_multi_close(self.h)
             self.h = None
 
 

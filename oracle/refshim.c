@@ -75,3 +75,47 @@ int ref_moe_route(const float * lg, int ne, int k, unsigned moe_flags, int * sel
     float sc[64], ch[64];
     return sml_moe_route(&hd, &ly, lg, sc, ch, sel, w);
 }
+
+// Several contexts of one model, set up as sml-batched does
+// (sml/sml-batched.c:70-76), for sml_forward_multi.
+typedef struct { sml_model m; int ns; sml_ctx * cs; sml_ctx ** cp; } ref_mh;
+
+void * ref_multi_open(const char * path, int n_ctx, int threads, int ns) {
+    ref_mh * h = calloc(1, sizeof *h);
+    if (!h) return NULL;
+    if (!sml_model_open(&h->m, path)) { free(h); return NULL; }
+    h->cs = calloc((size_t) ns, sizeof(sml_ctx));
+    h->cp = calloc((size_t) ns, sizeof(sml_ctx *));
+    for (int s = 0; s < ns; s++) {
+        if (!sml_ctx_init(&h->cs[s], &h->m, n_ctx, threads)) {
+            for (int t = 0; t < s; t++) sml_ctx_free(&h->cs[t]);
+            free(h->cs); free(h->cp); sml_model_close(&h->m); free(h);
+            return NULL;
+        }
+        h->cp[s] = &h->cs[s];
+    }
+    h->ns = ns;
+    return h;
+}
+
+// sml_forward on slot `slot`'s context (the stepped, per-32 path)
+const float * ref_multi_forward(void * p, int slot, int tok, int pos) {
+    ref_mh * h = (ref_mh *) p;
+    return sml_forward(h->cp[slot], tok, pos, 0);
+}
+
+// One token for each of the first ns slots: sml_forward_multi, whose regime
+// the SML_MULTI / SML_MULTI_EXACT_MAX environment picks (read once).
+void ref_multi_step(void * p, const int32_t * tok, const int * pos, int ns, float * logits) {
+    ref_mh * h = (ref_mh *) p;
+    sml_forward_multi(h->cp, tok, pos, ns, 0, logits);
+}
+
+void ref_multi_close(void * p) {
+    ref_mh * h = (ref_mh *) p;
+    if (!h) return;
+    for (int s = h->ns - 1; s >= 0; s--) sml_ctx_free(&h->cs[s]);
+    free(h->cs); free(h->cp);
+    sml_model_close(&h->m);
+    free(h);
+}

@@ -416,6 +416,7 @@ typedef struct {
 } olayer;
 
 struct orc_model {
+    int per256;
     const uint8_t * base;
     size_t size;
     uint32_t n_layer, n_embd, n_head, n_kv, n_ff, n_vocab;
@@ -574,6 +575,12 @@ void orc_model_close(orc_model * m) {
 
 int orc_n_vocab(const orc_model * m) { return (int) m->n_vocab; }
 
+// Activation regime of every product: per 32 values (0, stepped decode) or per
+// 256 (1, the batched regime: sml_quantize_act_sb before each product, whose
+// per-group kernels are exact on it, sml/sml-kernel.h:314-318,
+// sml/sml-run.c:2103-2127).
+void orc_model_per256(orc_model * m, int on) { m->per256 = on; }
+
 // ORC_DUMP=<file> appends the residual after the embedding and after every
 // layer, in the reference's SML_DUMP format (sml/sml-run.c:2696-2703)
 static void dump_x(const float * x, int n) {
@@ -590,7 +597,8 @@ static void mv(orc_model * m, const orec * r, const float * x, float * y) {
     const int n = (int) r->cols;
     const int32_t * perm = (const int32_t *) (m->base + r->perm_off);
     for (int i = 0; i < n; i++) m->xg[i] = x[perm[i]];
-    orc_quantize_act(m->xg, n, m->aq, m->as, m->asum);
+    if (m->per256) orc_quantize_act_sb(m->xg, n, m->aq, m->as, m->asum);
+    else           orc_quantize_act(m->xg, n, m->aq, m->as, m->asum);
     orc_tensor t = view(m, r);
     orc_matvec(&t, m->aq, m->as, m->asum, y, 0, (int) r->rows);
 }

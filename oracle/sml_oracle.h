@@ -112,6 +112,7 @@ void        orc_model_close(orc_model * m);
 // logits of token at position pos (positions must be fed in order from 0)
 const float * orc_forward(orc_model * m, int token, int pos);
 int orc_n_vocab(const orc_model * m);
+void orc_model_per256(orc_model * m, int on);
 // Tensor view by name, for single-matrix checks.
 int orc_model_tensor(const orc_model * m, const char * name, orc_tensor * out, const int32_t ** perm);
 

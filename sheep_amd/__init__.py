@@ -73,6 +73,9 @@ _SIGS = [
     ("sml_hip_copy", c_int, [c_void_p, c_void_p, c_size_t]),
     ("sml_hip_gemm", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     ("sml_hip_gemm_swiglu", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    ("sml_hip_gemm_sb", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    ("sml_hip_gemm_swiglu_sb", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    ("sml_hip_moe_regime", c_int, [c_void_p, c_int]),
     ("sml_hip_moe_from_file", c_void_p, [c_char_p, c_int, c_int]),
     ("sml_hip_moe_free", None, [c_void_p]),
     ("sml_hip_moe_info", c_int, [c_void_p, P(c_int), P(c_int), P(c_int), P(c_size_t)]),
@@ -343,6 +346,10 @@ class MoE:
         lib().sml_hip_moe_info(h, ctypes.byref(ne), ctypes.byref(k), ctypes.byref(nf), ctypes.byref(eb))
         self.nexp, self.k, self.n_ff, self.expert_bytes = ne.value, k.value, nf.value, eb.value
 
+    def regime(self, per256):
+        """Quantize the expert inputs per 256 values (True) or per 32 (False)."""
+        _chk(lib().sml_hip_moe_regime(self.h, 1 if per256 else 0), "moe_regime")
+
     def ffn(self, x, T, out, sel=None, w=None, logits=None):
         _chk(lib().sml_hip_moe_ffn(self.h, x.ptr, T, out.ptr, sel.ptr if sel else None, w.ptr if w else None,
                                    logits.ptr if logits else None), "moe_ffn")
@@ -365,10 +372,13 @@ class MoE:
             pass
 
 
-def gemm(m, act_q, act_s, act_u, nrow, y):
-    """y [nrow][rows] = W . a[r] for nrow activation rows (device buffers)."""
-    _chk(lib().sml_hip_gemm(m.h, act_q.ptr, act_s.ptr, act_u.ptr, nrow, y.ptr), "gemm")
+def gemm(m, act_q, act_s, act_u, nrow, y, per256=False):
+    """y [nrow][rows] = W . a[r] for nrow activation rows (device buffers),
+    quantized per 32 values (per256 False) or per 256 (True)."""
+    f = lib().sml_hip_gemm_sb if per256 else lib().sml_hip_gemm
+    _chk(f(m.h, act_q.ptr, act_s.ptr, act_u.ptr, nrow, y.ptr), "gemm")
 
 
-def gemm_swiglu(gate, up, act_q, act_s, act_u, nrow, h):
-    _chk(lib().sml_hip_gemm_swiglu(gate.h, up.h, act_q.ptr, act_s.ptr, act_u.ptr, nrow, h.ptr), "gemm_swiglu")
+def gemm_swiglu(gate, up, act_q, act_s, act_u, nrow, h, per256=False):
+    f = lib().sml_hip_gemm_swiglu_sb if per256 else lib().sml_hip_gemm_swiglu
+    _chk(f(gate.h, up.h, act_q.ptr, act_s.ptr, act_u.ptr, nrow, h.ptr), "gemm_swiglu")

@@ -204,6 +204,7 @@ static void launch_layer(int L) {
         // ffn_norm into fp32 for the router, then the routed experts; the
         // combine adds the residual (sml/sml-run.c:3470-3480)
         op_normq(G.st, G.x, NULL, y->fn, G.eps, G.E, 0, NULL, NULL, NULL, NULL, G.xn, 0);
+        y->moe->per256 = 0;
         op_moe(G.st, y->moe, G.xn, 1, G.x, G.x);
         return;
     }
@@ -575,11 +576,22 @@ void sml_gpu_set_middle(int layers, int (*fn)(float * rows, int pos0, int n)) {
 
 // ---------------------------------------------------------------- several sequences
 //
-// The GPU twin of sml_forward_multi (sml/sml-run.c:2559-2599) in its exact
-// regime (SML_MULTI=exact: per-32 activations, every sequence bit for bit as
-// decoded alone): each weight matrix streams once per step for all
-// sequences through the small-M GEMM, whose per-row arithmetic is the GEMV's;
-// attention runs per sequence over that sequence's KV cache slot.
+// The GPU twin of sml_forward_multi (sml/sml-run.c:2559-2599): each weight
+// matrix streams once per step for all sequences through the small-M GEMM;
+// attention runs per sequence over that sequence's KV cache slot. The
+// activation regime is the reference's choice (sml/sml-run.c:2579-2596):
+// SML_MULTI=exact, or at most SML_MULTI_EXACT_MAX (default 2) sequences,
+// quantizes per 32 values and gives each row the GEMV's arithmetic, so every
+// sequence is bit for bit as decoded alone; otherwise activations are
+// quantized per 256 values (sml_quantize_act_sb) and Q4 products sum each
+// superblock in integers, the arithmetic of sml_rlp_matvec.
+
+static int multi_per256(int ns) {
+    const char * x = getenv("SML_MULTI");
+    if (x && !strcmp(x, "exact")) return 0;
+    const char * e = getenv("SML_MULTI_EXACT_MAX");
+    return ns > (e ? atoi(e) : 2);
+}
 
 int sml_gpu_slots(int ns) {
     if (!G.open || ns < 1 || ns > MAX_SLOTS) return 0;
@@ -661,7 +673,7 @@ const float * sml_gpu_prefill_slot(int slot, const int * ids, int pos0, int n) {
 
 static void launch_multi(int ns) {
     const size_t kvd = (size_t) G.KV * G.hd, qkv = (size_t) (G.H + 2 * G.KV) * G.hd, hq = (size_t) G.H * G.hd;
-    const int mt = gemm_mt(ns);
+    const int mt = gemm_mt(ns), sb = multi_per256(ns);
     op_embed_rows(G.st, G.emb, G.mtok, NULL, ns, pdev(G.perm_emb), G.mx);
     for (int L = 0; L < G.n_layer; L++) {
         eng_layer * y = &G.L[L];
@@ -670,40 +682,42 @@ static void launch_multi(int ns) {
         float * ss[1] = { G.mas };
         int32_t * uu[1] = { G.masum };
         pp[0] = pdev(y->perm_qkv[0]);
-        op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, 0);
+        op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
         op_gemm(G.st, y->qkv->kdev, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
-                G.mqkv, y->bias_qkv, NULL);
-        const int fuse_q = y->perm_o < 0;
+                G.mqkv, y->bias_qkv, NULL, sb);
+        const int fuse_q = y->perm_o < 0 && !sb;         // the merge quantizes per 32
         op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, G.mslot, (size_t) L * G.n_ctx * kvd,
                            G.rc, G.rs, G.mpos, ns, G.H, G.KV, G.hd, G.n_ctx, G.mpart, G.matt,
                            fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL);
         if (!fuse_q) {
             pp[0] = pdev(y->perm_o);
-            op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, 0);
+            op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, sb);
         }
         op_gemm(G.st, y->o->kdev, 1, 0, y->o->nbits, G.E, (int) hq, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
-                G.mx, NULL, G.mx);
+                G.mx, NULL, G.mx, sb);
         if (y->moe) {
-            op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 0, NULL, NULL, NULL, NULL, G.mxn, 0);
+            op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 0, NULL, NULL, NULL, NULL, G.mxn, sb);
+            y->moe->per256 = sb;
             op_moe(G.st, y->moe, G.mxn, ns, G.mx, G.mx);
+            y->moe->per256 = 0;
             continue;
         }
         pp[0] = pdev(y->perm_gu[0]);
-        op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, 0);
+        op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
         op_gemm(G.st, y->gu_tab, 1, 1, y->gate->nbits, G.F, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mh,
-                NULL, NULL);
+                NULL, NULL, sb);
         pp[0] = pdev(y->perm_down);
-        op_normq_rows(G.st, G.mh, NULL, NULL, G.eps, G.F, ns, 1, pp, qq, ss, uu, NULL, 0);
+        op_normq_rows(G.st, G.mh, NULL, NULL, G.eps, G.F, ns, 1, pp, qq, ss, uu, NULL, sb);
         op_gemm(G.st, y->down->kdev, 1, 0, y->down->nbits, G.E, G.F, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
-                G.mx, NULL, G.mx);
+                G.mx, NULL, G.mx, sb);
     }
     const int32_t * pp[1] = { pdev(G.perm_head) };
     int8_t * qq[1] = { G.maq };
     float * ss[1] = { G.mas };
     int32_t * uu[1] = { G.masum };
-    op_normq_rows(G.st, G.mx, NULL, G.out_norm, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, 0);
+    op_normq_rows(G.st, G.mx, NULL, G.out_norm, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
     op_gemm(G.st, G.head->kdev, 1, 0, G.head->nbits, G.V, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mlog,
-            NULL, NULL);
+            NULL, NULL, sb);
 }
 
 int sml_gpu_step_multi(const int * tok, const int * pos, const int * slot, int ns, float * logits_out) {

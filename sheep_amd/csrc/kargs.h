@@ -49,10 +49,9 @@ typedef struct {
     int32_t       * hsums;
 } sml_kgemv;
 
-// Gather + optional residual add + optional RMSNorm + per-group int8 quantize.
 // Multi-workgroup RMSNorm + gather + quantize: every workgroup reduces the
 // whole vector's sum of squares itself (in double) and quantizes its own 8
-// groups of each output.
+// groups (one superblock) of each output.
 typedef struct {
     const float   * x;
     const float   * norm_w;       // NULL: no norm
@@ -63,7 +62,10 @@ typedef struct {
     int8_t        * q[3];
     float         * scale[3];
     int32_t       * sums[3];
+    int             per256;       // 1: one scale per 256 values (sml_quantize_act_sb)
 } sml_knormq2;
+
+// Gather + optional residual add + optional RMSNorm + per-group int8 quantize.
 
 typedef struct {
     float         * x;            // n floats; updated in place when resid != NULL
@@ -207,7 +209,7 @@ typedef struct {
     int32_t * list;               // [nexp][mmax] entries t*k + j, by token then choice
 } sml_kmoe_route;
 
-// Per-32 int8 quantization of activation rows into per-expert slots:
+// Per-32 (or per-256) int8 quantization of activation rows into per-expert slots:
 // mode 0 gathers row list[e][r] / k of x [T][n]; mode 1 takes row (e, r) of
 // src [nexp][mmax][n]. perms: device table of nexp permutations (NULL entries
 // or a NULL table: identity).
@@ -221,6 +223,7 @@ typedef struct {
     int8_t * q;                   // [nexp][mmax][n]
     float * scale;                // [nexp][mmax][n/32]
     int32_t * sums;
+    int per256;                   // 1: one scale per 256 values (sml_quantize_act_sb)
 } sml_kmquant;
 
 // Small-M GEMM over groups of matrices (one per expert, or a single one):

@@ -618,10 +618,13 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
     }
 }
 
-// Multi-workgroup form (the decode path's): workgroup b quantizes groups
-// 8b..8b+7 of each output; each reduces the full sum of squares first.
+// Multi-workgroup form (the decode path's): workgroup b quantizes elements
+// 256b..256b+255 (one superblock) of each output; each reduces the full sum of
+// squares first. per256: the superblock's amax meets across the 4 waves in LDS
+// (sml/sml-kernel.c:165-172).
 extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a) {
     __shared__ double red[4];
+    __shared__ float wmax[2][4];
     const int n = a.n, tid = threadIdx.x;
     // row blockIdx.y of a batch (every pointer strided by its row)
     const size_t bo = (size_t) blockIdx.y * n, bg = (size_t) blockIdx.y * (n / 32);
@@ -641,18 +644,27 @@ extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a
         sc = 1.0f / sqrtf((float) (tot / (double) n) + a.eps);
     }
     const int j = blockIdx.x * 256 + tid;           // element (group j/32) of every output
-    if (j >= n) return;
+    const bool ok = j < n;                          // whole groups of 32 (n % 32 == 0)
     const int l32 = tid & 31, g = j >> 5;
     for (int o = 0; o < a.nout; o++) {
-        const int src = a.perm[o] ? a.perm[o][j] : j;
-        const float v = a.norm_w ? x[src] * sc * a.norm_w[src] : x[src];
-        const float amax = max32(fabsf(v));
+        const int src = ok ? (a.perm[o] ? a.perm[o][j] : j) : 0;
+        const float v = ok ? (a.norm_w ? x[src] * sc * a.norm_w[src] : x[src]) : 0.0f;
+        float amax;
+        if (a.per256) {
+            // double-buffered by output: the next write to this slot follows
+            // the next output's barrier, which every reader of it has passed
+            const float wm = wave_max(fabsf(v));
+            if ((tid & 63) == 0) wmax[o & 1][tid >> 6] = wm;
+            __syncthreads();
+            amax = fmaxf(fmaxf(wmax[o & 1][0], wmax[o & 1][1]), fmaxf(wmax[o & 1][2], wmax[o & 1][3]));
+        } else {
+            amax = max32(fabsf(v));
+        }
         const float s = amax / 127.0f;
         const float is = s > 0.0f ? 1.0f / s : 0.0f;
-        const float r = __builtin_rintf(v * is);
-        int t = (r >= -2147483648.0f && r < 2147483648.0f) ? (int) r : (int) 0x80000000u;
-        t = t > 127 ? 127 : t < -127 ? -127 : t;
+        const int t = quant1(v, is);
         const int sum = isum32(t);
+        if (!ok) continue;
         a.q[o][bo + j] = (int8_t) t;
         if (l32 == 0) { a.scale[o][bg + g] = s; a.sums[o][bg + g] = sum; }
     }
@@ -1315,7 +1327,9 @@ extern "C" __global__ __launch_bounds__(64) void sml_moe_plan(const sml_kmoe_rou
 
 // Per-32 quantization of one activation row per workgroup (grid mmax x nexp),
 // the normq arithmetic (bit-exact with sml_quantize_act): a thread takes 4
-// consecutive values, 8 threads a group.
+// consecutive values, 8 threads a group, a wave a superblock of 256 (per256:
+// one amax over the wave, bit-exact with sml_quantize_act_sb). Every thread
+// of the workgroup runs every pass, so the wave-wide max sees all 64 lanes.
 #define MOE_QUANT_THREADS 1024
 extern "C" __global__ __launch_bounds__(MOE_QUANT_THREADS) void sml_moe_quant(const sml_kmquant a) {
     const int r = blockIdx.x, e = blockIdx.y;
@@ -1325,20 +1339,26 @@ extern "C" __global__ __launch_bounds__(MOE_QUANT_THREADS) void sml_moe_quant(co
                                     : a.src + ((size_t) e * a.mmax + r) * n;
     const int32_t * perm = a.perms ? a.perms[e] : nullptr;
     const size_t slot = (size_t) e * a.mmax + r;
-    for (int f = threadIdx.x; f < n / 4; f += MOE_QUANT_THREADS) {   // whole 8-thread groups stay together
-        float v[4];
-        if (perm) {
-            const int4 p = ((const int4 *) perm)[f];
-            v[0] = src[p.x]; v[1] = src[p.y]; v[2] = src[p.z]; v[3] = src[p.w];
-        } else {
-            const float4 q = ((const float4 *) src)[f];
-            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    for (int f0 = 0; f0 < n / 4; f0 += MOE_QUANT_THREADS) {
+        const int f = f0 + threadIdx.x;
+        const bool ok = f < n / 4;                  // whole 8-thread groups (n % 32 == 0)
+        float v[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+        if (ok) {
+            if (perm) {
+                const int4 p = ((const int4 *) perm)[f];
+                v[0] = src[p.x]; v[1] = src[p.y]; v[2] = src[p.z]; v[3] = src[p.w];
+            } else {
+                const float4 q = ((const float4 *) src)[f];
+                v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+            }
         }
-        const float am = max8(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        const float m4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        const float am = a.per256 ? wave_max(m4) : max8(m4);
         const float s = am / 127.0f;
         const float is = s > 0.0f ? 1.0f / s : 0.0f;
         const int t0 = quant1(v[0], is), t1 = quant1(v[1], is), t2 = quant1(v[2], is), t3 = quant1(v[3], is);
         const int sum = isum8(t0 + t1 + t2 + t3);
+        if (!ok) continue;
         ((int *) (a.q + slot * n))[f] = (t0 & 0xFF) | (t1 & 0xFF) << 8 | (t2 & 0xFF) << 16 | (int) ((unsigned) t3 << 24);
         if ((threadIdx.x & 7) == 0) { a.scale[slot * ng + f / 8] = s; a.sums[slot * ng + f / 8] = sum; }
     }
@@ -1524,44 +1544,55 @@ GEMM_WIDTH(2) GEMM_WIDTH(3) GEMM_WIDTH(4) GEMM_WIDTH(5) GEMM_WIDTH(6) GEMM_WIDTH
 // x 16 activation rows, B = 32 codes x 16 weight rows (lane layout, checked
 // on the device: lane l holds A row / B column l%16, codes 8*(l/16)..+7, and
 // receives D rows 4*(l/16)..+3 of column l%16). So lane l owns weight row
-// l%16 -- its group fields loaded once per group -- and activation rows
-// 4*(l/16)..+3, whose per-group (s, s*sum) the workgroup stages in LDS as
-// [group][row] float pairs; the per-group epilogue step*s*dot + min*s*sum runs
-// in fp32 on the 16x16 result. In the Q4 plane an 8-byte word at quad q, half
-// h, offset 8*(l/16) holds codes of groups 4q+2h (low nibbles) and 4q+2h+1
-// (high nibbles), so one load feeds two MFMAs. Loads are batched per 8 groups
-// (4 pairs): one 16-byte load brings a weight row's 8 (sq, mq) field pairs and
-// one 4-byte load its superblock's (sd, md). A workgroup owns RB blocks of 16
-// rows (SwiGLU: the gate and up blocks of the same rows); its 4 waves split the
-// groups in whole batches (input widths are multiples of 256 columns) and
-// their partial sums meet in LDS, added in wave order. The float order differs
-// from the GEMV's, so rows agree with it to rounding, not bit for bit.
-template <bool SW, int RB>
+// l%16 of each of its RB blocks of 16 rows (SwiGLU: the gate and up blocks of
+// the same rows) and activation rows 4*(l/16)..+3. In the Q4 plane an 8-byte
+// word at quad q, half h, offset 8*(l/16) holds codes of groups 4q+2h (low
+// nibbles) and 4q+2h+1 (high nibbles), so one load feeds two MFMAs.
+//
+// Work goes by superblock (8 groups = 256 columns; input widths are
+// multiples of 256): one 16-byte load brings a weight row's 8 (sq, mq) field
+// pairs and one 4-byte load its (sd, md). The NW waves of a workgroup split
+// the superblocks; each wave stages its share of the activation rows' group
+// data in its own LDS region (written and read by that wave only, so no
+// barrier) and keeps two superblocks' loads in flight: the first two go out
+// before the staging, and each computed superblock's registers are refilled
+// with the one two ahead.
+//
+// Two epilogues:
+//  - exact (per-32 activations, sml_matvec_batch_flat4): per group
+//    step*s*dot + min*s*sum in fp32, the activation's (s, s*sum) staged as
+//    [group][row] float pairs;
+//  - SB (per-256 activations, sml_matvec_batch_flat4_sb and sml_rlp_matvec,
+//    sml/sml-kernel.c:1142-1200,1746-1840): the superblock's sums
+//    sum_g sq_g*dot_g and sum_g (mq_g-127)*sum_g add in integers (24-bit
+//    multiplies: |dot| <= 32*15*127 < 2^16, sq < 2^8, |sum| <= 32*127), then
+//    one fp32 step per superblock: y += isum*(sd*s) + imin*(md*s), with the
+//    activation's group sums staged as [group][row] ints and its superblock
+//    scale as [superblock][row].
+// The waves' partial sums meet in LDS, added in wave order. The float order
+// differs from the GEMV's, so rows agree with it to rounding, not bit for bit.
+template <bool SW, bool SB, int RB, int NW>
 __device__ void mgemm_q4_body(const sml_kgemm & a) {
     typedef long v1l;
     constexpr int NM = SW ? 2 : 1, NACC = NM * RB * 4;
     extern __shared__ __align__(16) uint8_t lds[];
-    float2 * lsc = (float2 *) lds;                                 // [ng][16] (s, s*sum)
-    __shared__ float red[4][NACC][64];
     const int e = blockIdx.y;
     const int m = a.count ? a.count[e] : a.m_all;
     if (m <= 0) return;
-    const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8, nb = ng / 8;
+    const int n = a.cols, ng = n / 32, nsb = ng / 8;
     const int tid = threadIdx.x, lane = tid & 63, c = lane >> 4, i16 = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rb0 = blockIdx.x * (16 * RB);
-    const int b0 = wave * nb / 4, b1 = (wave + 1) * nb / 4;       // this wave's batches of 8 groups
-    const sml_kmat * mt = a.mats + (size_t) e * (SW ? 2 : 1);
+    const int s0 = wave * nsb / NW, s1 = (wave + 1) * nsb / NW;   // this wave's superblocks
+    const int spw = (nsb + NW - 1) / NW;                           // region size, in superblocks
+    const int gw = (s1 - s0) * 8, gb = s0 * 8;
+    const sml_kmat * mt = a.mats + (size_t) e * NM;
     const size_t abase = (size_t) e * a.mmax;
-    // activation scales of rows 0..15 (zero past m), transposed to [group][row]
-    #pragma unroll 8
-    for (int idx = tid; idx < ng * 16; idx += 256) {
-        const int r = idx / ng, g = idx - r * ng;
-        const size_t fi = (abase + (size_t) (r < m ? r : 0)) * ng + g;
-        const float sv = a.scale[fi];
-        const float su = (float) a.sums[fi];
-        lsc[g * 16 + r] = r < m ? make_float2(sv, sv * su) : make_float2(0.0f, 0.0f);
-    }
+    // this wave's LDS region: its share of the activation rows' group data
+    uint8_t * reg = lds + (size_t) wave * spw * (SB ? 576 : 1024);
+    int * lsum = (int *) reg;                                      // SB: [spw*8][16]
+    float * lscl = (float *) (reg + (size_t) spw * 512);           // SB: [spw][16]
+    float2 * lsc = (float2 *) reg;                                 // exact: [spw*8][16]
     const uint8_t * plane[NM];
     const uint8_t * fqb[NM];
     const uint8_t * fdb[NM];
@@ -1575,10 +1606,32 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
         const uint32_t rc = (uint32_t) (ra < a.rows ? ra : a.rows - 1);
         boff0[bk] = rc * rowb + 8u * (uint32_t) c;
         fqo[bk] = rc * (uint32_t) ng * 2u;
-        fdo[bk] = rc * (uint32_t) ns * 4u;
+        fdo[bk] = rc * (uint32_t) nsb * 4u;
     }
-    const bool tv = i16 < m;
-    const int8_t * qrow = a.q + (abase + (size_t) (tv ? i16 : 0)) * n + 8 * c;
+    const int8_t * qrow = a.q + (abase + (size_t) (i16 < m ? i16 : 0)) * n + 8 * c;
+    struct Batch {
+        v2u w[4][NM][RB];         // the 4 group pairs' code words
+        v4u fq[NM][RB];           // 8 (sq, mq) pairs
+        uint32_t fd[NM][RB];      // (sd, md)
+        v1l aq[8];                // activation codes, 8 per group
+    };
+    // one base address per stream and superblock, the rest immediate offsets
+    auto load = [&](Batch & b, int bt) {
+        const int g0 = 8 * bt;
+        #pragma unroll
+        for (int k = 0; k < NM; k++)
+            #pragma unroll
+            for (int bk = 0; bk < RB; bk++) {
+                const uint8_t * wp = plane[k] + (boff0[bk] + (uint32_t) g0 * 16u);
+                #pragma unroll
+                for (int p = 0; p < 4; p++) b.w[p][k][bk] = *(const v2u *) (wp + (p >> 1) * 64 + (p & 1) * 32);
+                b.fq[k][bk] = *(const v4u *) (fqb[k] + (fqo[bk] + (uint32_t) g0 * 2u));
+                b.fd[k][bk] = *(const uint32_t *) (fdb[k] + (fdo[bk] + (uint32_t) bt * 4u));
+            }
+        const int8_t * qp = qrow + (size_t) g0 * 32;
+        #pragma unroll
+        for (int j = 0; j < 8; j++) b.aq[j] = *(const v1l *) (qp + j * 32);
+    };
     float acc[NM][RB][4];
     #pragma unroll
     for (int k = 0; k < NM; k++)
@@ -1586,90 +1639,164 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
         for (int bk = 0; bk < RB; bk++)
             #pragma unroll
             for (int r = 0; r < 4; r++) acc[k][bk][r] = 0.0f;
-    __syncthreads();
-    for (int bt = b0; bt < b1; bt++) {
-        const int g0 = 8 * bt;
-        // weights: the 4 pairs' 8-byte words; fields: 8 (sq, mq) pairs and one (sd, md)
-        v2u bwt[4][NM][RB];
-        v4u fq[NM][RB];
-        uint32_t fd[NM][RB];
-        v1l aq[8];
-        #pragma unroll
-        for (int k = 0; k < NM; k++)
+    auto compute = [&](const Batch & b, int bt) {
+        const int gl0 = (bt - s0) * 8;
+        if constexpr (SB) {
+            int is[NM][RB][4], im[NM][RB][4];
             #pragma unroll
-            for (int bk = 0; bk < RB; bk++) {
+            for (int k = 0; k < NM; k++)
                 #pragma unroll
-                for (int p = 0; p < 4; p++)
-                    bwt[p][k][bk] = *(const v2u *) (plane[k] + (boff0[bk] + (uint32_t) (g0 / 4 + (p >> 1)) * 64u + (uint32_t) (p & 1) * 32u));
-                fq[k][bk] = *(const v4u *) (fqb[k] + (fqo[bk] + (uint32_t) g0 * 2u));
-                fd[k][bk] = *(const uint32_t *) (fdb[k] + (fdo[bk] + (uint32_t) bt * 4u));
+                for (int bk = 0; bk < RB; bk++)
+                    #pragma unroll
+                    for (int r = 0; r < 4; r++) { is[k][bk][r] = 0; im[k][bk][r] = 0; }
+            #pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int4 sm = *(const int4 *) &lsum[(gl0 + j) * 16 + 4 * c];
+                const int smv[4] = {sm.x, sm.y, sm.z, sm.w};
+                #pragma unroll
+                for (int k = 0; k < NM; k++)
+                    #pragma unroll
+                    for (int bk = 0; bk < RB; bk++) {
+                        const v2u w = b.w[j >> 1][k][bk];
+                        const v2u cd = (j & 1) ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
+                        const v1l bv = (v1l) (((unsigned long) cd.y << 32) | cd.x);
+                        v4i d = { 0, 0, 0, 0 };
+                        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(b.aq[j], bv, d, 0, 0, 0);
+                        const uint32_t f = b.fq[k][bk][j >> 1] >> (16 * (j & 1));
+                        const int sq = (int) (f & 0xFFu), mn = (int) ((f >> 8) & 0xFFu) - 127;
+                        #pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            is[k][bk][r] = __mul24(sq, d[r]) + is[k][bk][r];
+                            im[k][bk][r] = __mul24(mn, smv[r]) + im[k][bk][r];
+                        }
+                    }
             }
-        #pragma unroll
-        for (int j = 0; j < 8; j++) aq[j] = *(const v1l *) (qrow + (size_t) (g0 + j) * 32);
-        #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int g = g0 + j, p = j >> 1, h = j & 1;
-            const v1l av = tv ? aq[j] : 0;
-            const float4 s01 = *(const float4 *) &lsc[g * 16 + 4 * c];
-            const float4 s23 = *(const float4 *) &lsc[g * 16 + 4 * c + 2];
-            const float sv[4] = {s01.x, s01.z, s23.x, s23.z}, ssv[4] = {s01.y, s01.w, s23.y, s23.w};
+            const float4 as = *(const float4 *) &lscl[(bt - s0) * 16 + 4 * c];
+            const float asv[4] = {as.x, as.y, as.z, as.w};
             #pragma unroll
             for (int k = 0; k < NM; k++)
                 #pragma unroll
                 for (int bk = 0; bk < RB; bk++) {
-                    const v2u w = bwt[p][k][bk];
-                    const v2u cd = h ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
-                    const v1l bv = (v1l) (((unsigned long) cd.y << 32) | cd.x);
-                    v4i d = { 0, 0, 0, 0 };
-                    d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, d, 0, 0, 0);
-                    const uint32_t f = fq[k][bk][j >> 1] >> (16 * (j & 1)), d2 = fd[k][bk];
-                    const float wsc = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
-                    const float wmn = h2f((uint16_t) (d2 >> 16)) * ((float) ((f >> 8) & 0xFFu) - 127.0f);
+                    const float dsc = h2f((uint16_t) (b.fd[k][bk] & 0xFFFFu)), mdsc = h2f((uint16_t) (b.fd[k][bk] >> 16));
                     #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        acc[k][bk][r] += (wsc * sv[r]) * (float) d[r];
-                        acc[k][bk][r] += wmn * ssv[r];
+                        acc[k][bk][r] += (float) is[k][bk][r] * (dsc * asv[r]);
+                        acc[k][bk][r] += (float) im[k][bk][r] * (mdsc * asv[r]);
                     }
                 }
+        } else {
+            #pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float4 s01 = *(const float4 *) &lsc[(gl0 + j) * 16 + 4 * c];
+                const float4 s23 = *(const float4 *) &lsc[(gl0 + j) * 16 + 4 * c + 2];
+                const float sv[4] = {s01.x, s01.z, s23.x, s23.z}, ssv[4] = {s01.y, s01.w, s23.y, s23.w};
+                #pragma unroll
+                for (int k = 0; k < NM; k++)
+                    #pragma unroll
+                    for (int bk = 0; bk < RB; bk++) {
+                        const v2u w = b.w[j >> 1][k][bk];
+                        const v2u cd = (j & 1) ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
+                        const v1l bv = (v1l) (((unsigned long) cd.y << 32) | cd.x);
+                        v4i d = { 0, 0, 0, 0 };
+                        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(b.aq[j], bv, d, 0, 0, 0);
+                        const uint32_t f = b.fq[k][bk][j >> 1] >> (16 * (j & 1)), d2 = b.fd[k][bk];
+                        const float wsc = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
+                        const float wmn = h2f((uint16_t) (d2 >> 16)) * ((float) ((f >> 8) & 0xFFu) - 127.0f);
+                        #pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            acc[k][bk][r] += (wsc * sv[r]) * (float) d[r];
+                            acc[k][bk][r] += wmn * ssv[r];
+                        }
+                    }
+            }
+        }
+    };
+    // two superblocks in flight from the start: their loads go out before the
+    // activation data is staged, so the two latencies overlap
+    Batch A, B;
+    if (s0 < s1) load(A, s0);
+    if (s0 + 1 < s1) load(B, s0 + 1);
+    // stage this wave's share, [group][row]; rows past m read row 0 (their
+    // outputs are never stored, and no output row reads another's data)
+    // four entries per lane per pass, all loads issued before any is used
+    for (int base = lane; base < gw * 16; base += 256) {
+        float sv[4];
+        int su[4];
+        #pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int idx = base + 64 * u;
+            if (idx < gw * 16) {
+                const int r = idx / gw, gl = idx - r * gw;
+                const size_t fi = (abase + (size_t) (r < m ? r : 0)) * ng + gb + gl;
+                sv[u] = a.scale[fi];
+                su[u] = a.sums[fi];
+            }
+        }
+        #pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int idx = base + 64 * u;
+            if (idx < gw * 16) {
+                const int r = idx / gw, gl = idx - r * gw;
+                if constexpr (SB) {
+                    lsum[gl * 16 + r] = su[u];
+                    if ((gl & 7) == 0) lscl[(gl >> 3) * 16 + r] = sv[u];
+                } else {
+                    lsc[gl * 16 + r] = make_float2(sv[u], sv[u] * (float) su[u]);
+                }
+            }
         }
     }
+    for (int bt = s0; bt < s1; bt += 2) {
+        compute(A, bt);
+        if (bt + 2 < s1) load(A, bt + 2);
+        if (bt + 1 >= s1) break;
+        compute(B, bt + 1);
+        if (bt + 3 < s1) load(B, bt + 3);
+    }
+    __syncthreads();                                  // every wave is past its staging region
+    float * red = (float *) lds;                      // [NW][NACC][64]
     #pragma unroll
     for (int k = 0; k < NM; k++)
         #pragma unroll
         for (int bk = 0; bk < RB; bk++)
             #pragma unroll
-            for (int r = 0; r < 4; r++) red[wave][(k * RB + bk) * 4 + r][lane] = acc[k][bk][r];
+            for (int r = 0; r < 4; r++) red[(wave * NACC + (k * RB + bk) * 4 + r) * 64 + lane] = acc[k][bk][r];
     __syncthreads();
-    if (wave != 0) return;
-    #pragma unroll
-    for (int bk = 0; bk < RB; bk++) {
-        const int row = rb0 + bk * 16 + i16;
-        if (row >= a.rows) continue;
+    for (int o = tid; o < RB * 256; o += 64 * NW) {
+        const int bk = o >> 8, r = (o >> 6) & 3, l = o & 63;
+        const int row = rb0 + bk * 16 + (l & 15), mr = 4 * (l >> 4) + r;
+        if (row >= a.rows || mr >= m) continue;
+        float t[NM];
         #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int mr = 4 * c + r;
-            if (mr >= m) continue;
-            float t[NM];
+        for (int k = 0; k < NM; k++) {
+            float sum = 0.0f;
             #pragma unroll
-            for (int k = 0; k < NM; k++) {
-                const int j = (k * RB + bk) * 4 + r;
-                t[k] = ((red[0][j][lane] + red[1][j][lane]) + red[2][j][lane]) + red[3][j][lane];
-            }
-            float * y = a.y + (abase + mr) * a.rows;
-            if constexpr (SW) {
-                y[row] = (t[0] / (1.0f + expf(-t[0]))) * t[1];           // sml/sml-run.c:451-454
-            } else {
-                float v = t[0];
-                if (a.bias) v += a.bias[row];
-                if (a.resid) v = a.resid[(abase + mr) * a.rows + row] + v;
-                y[row] = v;
-            }
+            for (int w = 0; w < NW; w++) sum += red[(w * NACC + (k * RB + bk) * 4 + r) * 64 + l];
+            t[k] = sum;
+        }
+        float * y = a.y + (abase + mr) * a.rows;
+        if constexpr (SW) {
+            y[row] = (t[0] / (1.0f + expf(-t[0]))) * t[1];               // sml/sml-run.c:451-454
+        } else {
+            float v = t[0];
+            if (a.bias) v += a.bias[row];
+            if (a.resid) v = a.resid[(abase + mr) * a.rows + row] + v;
+            y[row] = v;
         }
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_r1(const sml_kgemm a) { mgemm_q4_body<false, 1>(a); }
-extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_r2(const sml_kgemm a) { mgemm_q4_body<false, 2>(a); }
-extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_s_r1(const sml_kgemm a) { mgemm_q4_body<true, 1>(a); }
-extern "C" __global__ __launch_bounds__(256) void sml_mgemm_q4_s_r2(const sml_kgemm a) { mgemm_q4_body<true, 2>(a); }
+#define MGEMM_KERNEL(RB, NW)                                                                                   \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_r##RB##_w##NW(const sml_kgemm a) {       \
+        mgemm_q4_body<false, false, RB, NW>(a); }                                                              \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_r##RB##_w##NW(const sml_kgemm a) {     \
+        mgemm_q4_body<true, false, RB, NW>(a); }                                                               \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_sb_r##RB##_w##NW(const sml_kgemm a) {    \
+        mgemm_q4_body<false, true, RB, NW>(a); }                                                               \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_sb_r##RB##_w##NW(const sml_kgemm a) {  \
+        mgemm_q4_body<true, true, RB, NW>(a); }
+MGEMM_KERNEL(1, 4)
+MGEMM_KERNEL(2, 4)
+MGEMM_KERNEL(1, 8)
+MGEMM_KERNEL(2, 8)
 

@@ -262,10 +262,10 @@ void op_normq_rows(hipStream_t st, float * x, const float * resid, const float *
     a.x = x; a.resid = resid; a.norm_w = w; a.eps = eps; a.n = n; a.nout = nout;
     for (int i = 0; i < nout; i++) { a.perm[i] = perm[i]; a.q[i] = q[i]; a.scale[i] = scale[i]; a.sums[i] = sums[i]; }
     a.normed = normed; a.per256 = per256;
-    if (!resid && !normed && !per256) {
+    if (!resid && !normed) {
         sml_knormq2 b;
         memset(&b, 0, sizeof b);
-        b.x = x; b.norm_w = w; b.eps = eps; b.n = n; b.nout = nout;
+        b.x = x; b.norm_w = w; b.eps = eps; b.n = n; b.nout = nout; b.per256 = per256;
         for (int i = 0; i < nout; i++) { b.perm[i] = perm[i]; b.q[i] = q[i]; b.scale[i] = scale[i]; b.sums[i] = sums[i]; }
         hx_launch("sml_normq2", (unsigned) ((n + 255) / 256), (unsigned) rows, 256, 0, st, &b);
         return;
@@ -714,7 +714,7 @@ int gemm_mt(int m) { return m <= 1 ? 1 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
 
 void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
-             const int32_t * sums, float * y, const float * bias, const float * resid) {
+             const int32_t * sums, float * y, const float * bias, const float * resid, int per256) {
     if (swiglu && (bias || resid)) hx_failf("SwiGLU GEMM takes no bias or residual");
     if (mt != 1 && mt != 4 && mt != 8 && mt != 16) hx_failf("small-M GEMM takes at most 16 rows");
     if (!count && (m_all < 1 || m_all > mt)) hx_failf("small-M GEMM of %d rows", m_all);
@@ -724,22 +724,32 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
     a.mats = tab; a.nmat = swiglu ? 2 : 1; a.cols = cols; a.rows = rows;
     a.count = count; a.m_all = m_all; a.mmax = mmax;
     a.q = q; a.scale = scale; a.sums = sums; a.y = y; a.bias = bias; a.resid = resid;
-    char name[40];
-    // Q4 with more than 8 activation rows runs on MFMA (measured faster there;
-    // below, the VALU dot4 kernel wins) unless the exact regime is asked for
-    // (SML_MULTI=exact: every row bit for bit the GEMV's). Expert groups
-    // (count != NULL) hold few rows each and stay on VALU.
+    char name[48];
+    // Q4 runs on MFMA: with per-256 activations always (the integer
+    // superblock epilogue); with per-32 ones for more than 8 activation rows
+    // (measured faster there; below, the VALU dot4 kernel wins) unless the
+    // exact regime is asked for (SML_MULTI=exact: every row bit for bit the
+    // GEMV's). Per-32 expert groups (count != NULL) hold few rows each and
+    // stay on VALU. SML_MGEMM=0 keeps every product on the VALU kernels.
     const char * mode = getenv("SML_MULTI");
     const int exact = mode && !strcmp(mode, "exact");
-    if (nbits == 4 && !count && m_all > 8 && !exact && cols % 256 == 0 && cols <= 14336) {
+    if (nbits == 4 && cols % 256 == 0 && (per256 || (!count && m_all > 8 && !exact)) && env_int("SML_MGEMM", 1)) {
         int rb = !swiglu && rows >= 32768 ? 2 : 1;
         const int fr = env_int("SML_MGEMM_RB", 0);
         if (fr == 1 || fr == 2) rb = fr;
-        snprintf(name, sizeof name, "sml_mgemm_q4%s_r%d", swiglu ? "_s" : "", rb);
-        // LDS: the activation rows' (s, s*sum) per group, [group][16] (56 KB at 14336 columns)
-        hx_launch(name, (unsigned) ((rows + 16 * rb - 1) / (16 * rb)), (unsigned) ngroups, 256,
-                  (size_t) (cols / 32) * 16 * 8, st, &a);
-        return;
+        const int nw = env_int("SML_MGEMM_NW", 8) == 4 ? 4 : 8;
+        // LDS: each wave's share of the activation group data, then the
+        // waves' partial sums (the same memory, after a barrier)
+        const int nsb = cols / 256, spw = (nsb + nw - 1) / nw;
+        const size_t stage = (size_t) nw * spw * (per256 ? 576 : 1024);
+        const size_t red = (size_t) nw * (swiglu ? 2 : 1) * rb * 4 * 64 * 4;
+        const size_t lds = stage > red ? stage : red;
+        if (lds <= 65536) {
+            snprintf(name, sizeof name, "sml_mgemm_q4%s%s_r%d_w%d", swiglu ? "_s" : "", per256 ? "_sb" : "", rb, nw);
+            hx_launch(name, (unsigned) ((rows + 16 * rb - 1) / (16 * rb)), (unsigned) ngroups, (unsigned) (64 * nw),
+                      lds, st, &a);
+            return;
+        }
     }
     snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d", nbits, swiglu ? "_s" : "", mt);
     const size_t lds = (size_t) mt * GEMM_TILE * (32 + 8);
@@ -747,18 +757,15 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
     hx_launch(name, (unsigned) ((rows + 7) / 8), (unsigned) ngroups, 256, lds, st, &a);
 }
 
-int sml_hip_gemm(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
-                 float * y) {
-    OP_BEGIN(-1);
+static void gemm_one(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
+                     float * y, int per256) {
     if (!m || nrow < 1 || nrow > 16) hx_failf("gemm of %d rows (1..16)", nrow);
-    op_gemm(0, m->kdev, 1, 0, m->nbits, m->k.rows, m->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, y, NULL, NULL);
-    HX_LEAVE();
-    return 0;
+    op_gemm(0, m->kdev, 1, 0, m->nbits, m->k.rows, m->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, y, NULL, NULL,
+            per256);
 }
 
-int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q, const float * scale,
-                        const int32_t * sums, int nrow, float * h) {
-    OP_BEGIN(-1);
+static void gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q, const float * scale,
+                        const int32_t * sums, int nrow, float * h, int per256) {
     if (!gate || !up || nrow < 1 || nrow > 16) hx_failf("gemm of %d rows (1..16)", nrow);
     if (up->nbits != gate->nbits || up->cols != gate->cols || up->k.rows != gate->k.rows)
         hx_failf("SwiGLU needs gate and up of one shape and width");
@@ -772,7 +779,38 @@ int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const 
         ((sml_hip_mat *) gate)->up_k = up->k;
         ((sml_hip_mat *) gate)->pair_set = 1;
     }
-    op_gemm(0, pair, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h, NULL, NULL);
+    op_gemm(0, pair, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h, NULL,
+            NULL, per256);
+}
+
+int sml_hip_gemm(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
+                 float * y) {
+    OP_BEGIN(-1);
+    gemm_one(m, q, scale, sums, nrow, y, 0);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_gemm_sb(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
+                    float * y) {
+    OP_BEGIN(-1);
+    gemm_one(m, q, scale, sums, nrow, y, 1);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q, const float * scale,
+                        const int32_t * sums, int nrow, float * h) {
+    OP_BEGIN(-1);
+    gemm_swiglu(gate, up, q, scale, sums, nrow, h, 0);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_gemm_swiglu_sb(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q, const float * scale,
+                           const int32_t * sums, int nrow, float * h) {
+    OP_BEGIN(-1);
+    gemm_swiglu(gate, up, q, scale, sums, nrow, h, 1);
     HX_LEAVE();
     return 0;
 }
@@ -949,6 +987,12 @@ void sml_hip_moe_free(sml_hip_moe * m) {
     HX_LEAVE();
 }
 
+int sml_hip_moe_regime(sml_hip_moe * m, int per256) {
+    if (!m) return -1;
+    m->per256 = per256 ? 1 : 0;
+    return 0;
+}
+
 int sml_hip_moe_info(const sml_hip_moe * m, int * nexp, int * k, int * n_ff, size_t * expert_bytes) {
     if (!m) return -1;
     if (nexp) *nexp = m->nexp;
@@ -983,16 +1027,16 @@ void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out
     sml_kmquant qa;
     memset(&qa, 0, sizeof qa);
     qa.src = x; qa.mode = 0; qa.perms = m->ptab_gu; qa.n = m->n_embd; qa.mmax = m->tmax; qa.k = m->k;
-    qa.count = m->count; qa.list = m->list; qa.q = m->qx; qa.scale = m->sx; qa.sums = m->ux;
+    qa.count = m->count; qa.list = m->list; qa.q = m->qx; qa.scale = m->sx; qa.sums = m->ux; qa.per256 = m->per256;
     hx_launch("sml_moe_quant", (unsigned) T, (unsigned) m->nexp, 1024, 0, st, &qa);
     const int mt = gemm_mt(T);
     op_gemm(st, m->tab_gu, m->nexp, 1, m->nbits, m->n_ff, m->n_embd, m->count, 0, mt, m->tmax,
-            m->qx, m->sx, m->ux, m->h, NULL, NULL);
+            m->qx, m->sx, m->ux, m->h, NULL, NULL, m->per256);
     sml_kmquant qb = qa;
     qb.src = m->h; qb.mode = 1; qb.perms = m->ptab_d; qb.n = m->n_ff; qb.q = m->qh; qb.scale = m->sh; qb.sums = m->uh;
     hx_launch("sml_moe_quant", (unsigned) T, (unsigned) m->nexp, 1024, 0, st, &qb);
     op_gemm(st, m->tab_d, m->nexp, 0, m->nbits, m->n_embd, m->n_ff, m->count, 0, mt, m->tmax,
-            m->qh, m->sh, m->uh, m->yd, NULL, NULL);
+            m->qh, m->sh, m->uh, m->yd, NULL, NULL, m->per256);
     sml_kmoe_comb c;
     memset(&c, 0, sizeof c);
     c.y = m->yd; c.sel = m->sel; c.slot = m->slot; c.w = m->w; c.T = T; c.n = m->n_embd; c.k = m->k;

@@ -49,10 +49,11 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
              const float * resid, const gemv_fuse * fu);
 // Small-M GEMM over ngroups matrix groups (device table tab: one matrix per
 // group, or gate/up pairs for SwiGLU); m_all rows (count == NULL) or count[e]
-// rows per group, at most mt (1, 4, 8 or 16).
+// rows per group, at most mt (1, 4, 8 or 16). per256: the activation is
+// quantized per 256 values (Q4 then takes the integer superblock epilogue).
 void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
-             const int32_t * sums, float * y, const float * bias, const float * resid);
+             const int32_t * sums, float * y, const float * bias, const float * resid, int per256);
 int gemm_mt(int m);
 // One matrix holding the rows of several FLAT records of one width and input
 // width, stacked in order (the q, k and v projections as one GEMV).
@@ -100,6 +101,7 @@ struct sml_hip_moe {
     void * owned[160];            // every device allocation: up to 2 permutations per expert + buffers
     int nowned;
     size_t expert_bytes;
+    int per256;                   // activations quantized per 256 values (the batched regime)
 };
 // Experts of layer `layer` for up to tmax tokens per call; scratch shared with
 // `share` (a loaded layer of the same shape) when not NULL.

@@ -85,6 +85,82 @@ def test_mfma_gemm_q4(tmpdir_s, cols, rows):
             close(got[r], ob.matvec(t, *ob.quantize_act(xs[r])), f"mfma gemm row {r} of {nrow}")
 
 
+def quant_rows_sb(xs):
+    """Per-256 quantization of each row (sml_quantize_act_sb), as host arrays."""
+    q, s, u = zip(*(ob.quantize_act(np.ascontiguousarray(x, np.float32), per256=True) for x in xs))
+    return np.stack(q), np.stack(s), np.stack(u)
+
+
+@pytest.mark.skipif(not ob.have_ref(), reason="oracle/_ref (the reference's CPU engine) is not built")
+@pytest.mark.parametrize("cols,rows", [(1536, 1000), (5120, 2048), (14336, 4096)])
+def test_gemm_q4_per256_matches_reference(tmpdir_s, cols, rows):
+    """Per-256 activations (the batched regime) on MFMA with integer
+    superblock sums: every row within 1e-3 of the reference's
+    sml_matvec_batch_flat4_sb and of its once-packed rows-in-lanes
+    sml_rlp_matvec, for 1 to 16 rows."""
+    p = tmpdir_s / f"mgsb_{cols}_{rows}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, rows, cols, nbits=4, random_perm=False, seed=500 + cols)
+    t = SSF(p)["w"]
+    m = sa.Mat.from_file(p, "w")
+    rng = np.random.default_rng(cols + 1)
+    for nrow in (1, 3, 4, 9, 16):
+        xs = [rng.standard_normal(cols).astype(np.float32) * (1 + r) for r in range(nrow)]
+        Q, S, U = quant_rows_sb(xs)
+        y = sa.DevBuf(nrow * rows * 4)
+        sa.gemm(m, sa.DevBuf.of(Q), sa.DevBuf.of(S), sa.DevBuf.of(U), nrow, y, per256=True)
+        got = y.read(np.float32).reshape(nrow, rows)
+        want = ob.ref_matvec_batch(t, Q, S, U, sb=True)
+        rlp = ob.ref_rlp_matvec(t, Q, S, U)
+        assert rlp is not None
+        for r in range(nrow):
+            close(got[r], want[r], f"per-256 gemm row {r} of {nrow} vs flat4_sb")
+            close(got[r], rlp[r], f"per-256 gemm row {r} of {nrow} vs rlp")
+
+
+@pytest.mark.parametrize("nb", [2, 3, 5, 6, 8])
+def test_gemm_per256_other_widths(tmpdir_s, nb):
+    """Widths other than Q4 take per-256 activations through the per-group
+    kernels, on which the reference's own kernels are exact (the scale
+    repeats in every group, sml/sml-kernel.h:314-318): each row within 1e-3
+    of the reference's decode kernel on the same activation."""
+    if not ob.have_ref():
+        pytest.skip("oracle/_ref (the reference's CPU engine) is not built")
+    cols, rows = 2048, 1000
+    p = tmpdir_s / f"gsb{nb}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, rows, cols, nbits=nb, random_perm=False, seed=600 + nb)
+    t = SSF(p)["w"]
+    m = sa.Mat.from_file(p, "w")
+    rng = np.random.default_rng(nb)
+    xs = [rng.standard_normal(cols).astype(np.float32) for _ in range(5)]
+    Q, S, U = quant_rows_sb(xs)
+    y = sa.DevBuf(5 * rows * 4)
+    sa.gemm(m, sa.DevBuf.of(Q), sa.DevBuf.of(S), sa.DevBuf.of(U), 5, y, per256=True)
+    got = y.read(np.float32).reshape(5, rows)
+    for r in range(5):
+        close(got[r], ob.ref_matvec(t, Q[r], S[r], U[r]), f"q{nb} per-256 row {r}")
+
+
+@pytest.mark.skipif(not ob.have_ref(), reason="oracle/_ref (the reference's CPU engine) is not built")
+def test_gemm_swiglu_per256(tmpdir_s):
+    p = tmpdir_s / "gemm_ffn_sb.ssf"
+    sa.synth_model(p, n_layer=1, n_embd=1536, n_head=12, n_head_kv=2, n_ff=2048, n_vocab=256, seed=42)
+    f = SSF(p)
+    g, u = f["blk.0.ffn_gate.weight"], f["blk.0.ffn_up.weight"]
+    mg, mu = sa.Mat.from_file(p, g.name), sa.Mat.from_file(p, u.name)
+    rng = np.random.default_rng(6)
+    xs = [rng.standard_normal(1536).astype(np.float32)[g.perm] for _ in range(12)]
+    Q, S, U = quant_rows_sb(xs)
+    h = sa.DevBuf(12 * 2048 * 4)
+    sa.gemm_swiglu(mg, mu, sa.DevBuf.of(Q), sa.DevBuf.of(S), sa.DevBuf.of(U), 12, h, per256=True)
+    got = h.read(np.float32).reshape(12, 2048)
+    yg, yu = ob.ref_matvec_batch(g, Q, S, U, sb=True), ob.ref_matvec_batch(u, Q, S, U, sb=True)
+    for r in range(12):
+        ob.oracle().orc_silu_mul(yg[r].ctypes.data, yu[r].ctypes.data, 2048)
+        close(got[r], yg[r], f"per-256 gemm swiglu row {r}")
+
+
 def test_gemm_swiglu_rows(tmpdir_s):
     p = tmpdir_s / "gemm_ffn.ssf"
     sa.synth_model(p, n_layer=1, n_embd=1536, n_head=12, n_head_kv=2, n_ff=2048, n_vocab=256, seed=41)
@@ -112,8 +188,10 @@ def moe_model(tmpdir_s, name, n_embd, n_ff, nexp, k, perm, seed):
     return p
 
 
-def oracle_moe(f, x, nexp, k, n_embd, flags=1):
-    """Per token, as moe_ffn (sml/sml-run.c:3071-3124) with the oracle's kernels."""
+def oracle_moe(f, x, nexp, k, n_embd, flags=1, per256=False):
+    """Per token, as moe_ffn (sml/sml-run.c:3071-3124) with the oracle's
+    kernels; per256 quantizes the expert inputs as moe_ffn_batch does in the
+    batched regimes."""
     router = np.ascontiguousarray(f["blk.0.ffn_gate_inp.weight"].f32)
     lg = np.zeros(nexp, np.float32)
     ob.oracle().orc_router(router.ctypes.data, x.ctypes.data, nexp, n_embd, lg.ctypes.data)
@@ -124,10 +202,10 @@ def oracle_moe(f, x, nexp, k, n_embd, flags=1):
     for j in range(k):
         e = int(sel[j])
         g, u, d = (f[f"blk.0.ffn_{kind}.{e}.weight"] for kind in ("gate", "up", "down"))
-        qa = ob.quantize_act(np.ascontiguousarray(x[g.perm]))
+        qa = ob.quantize_act(np.ascontiguousarray(x[g.perm]), per256)
         yg, yu = ob.matvec(g, *qa), ob.matvec(u, *qa)
         ob.oracle().orc_silu_mul(yg.ctypes.data, yu.ctypes.data, len(yg))
-        yd = ob.matvec(d, *ob.quantize_act(np.ascontiguousarray(yg[d.perm])))
+        yd = ob.matvec(d, *ob.quantize_act(np.ascontiguousarray(yg[d.perm]), per256))
         acc += w[j] * yd
     return lg, sel, w, acc
 
@@ -153,6 +231,28 @@ def test_moe_ffn(tmpdir_s, T, perm):
         np.testing.assert_array_equal(got_sel[t], rs, err_msg=f"token {t} routing")
         np.testing.assert_allclose(got_w[t], rw, rtol=1e-6, atol=1e-7)
         close(got_out[t], ro, f"moe token {t}")
+
+
+@pytest.mark.parametrize("T", [4, 16])
+def test_moe_ffn_per256(tmpdir_s, T):
+    """The batched regime's expert products: inputs quantized per 256
+    (bit-exact routing still), each token's output within 1e-3 of the
+    oracle's per-token composition on per-256 activations."""
+    n_embd, n_ff, nexp, k = 1024, 1536, 8, 2
+    p = moe_model(tmpdir_s, "moe_1.ssf", n_embd, n_ff, nexp, k, True, seed=1006)
+    f = SSF(p)
+    moe = sa.MoE(p, 0, 16)
+    moe.regime(True)
+    rng = np.random.default_rng(T * 11)
+    x = rng.standard_normal((T, n_embd)).astype(np.float32)
+    out, sel = sa.DevBuf(T * n_embd * 4), sa.DevBuf(T * k * 4)
+    moe.ffn(sa.DevBuf.of(x), T, out, sel)
+    got_out = out.read(np.float32).reshape(T, n_embd)
+    got_sel = sel.read(np.int32).reshape(T, k)
+    for t in range(T):
+        _, rs, _, ro = oracle_moe(f, x[t], nexp, k, n_embd, per256=True)
+        np.testing.assert_array_equal(got_sel[t], rs, err_msg=f"token {t} routing")
+        close(got_out[t], ro, f"per-256 moe token {t}")
 
 
 def test_moe_refuses_dense_layer(tmpdir_s):

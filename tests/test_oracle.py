@@ -315,6 +315,53 @@ def test_moe_decoder_matches_reference(tmpdir_s, perm):
         rm.close()
 
 
+@needs_ref
+def test_per256_regime_matches_reference_multi(tmpdir_s, monkeypatch):
+    """The oracle's per-256 regime (every product's input quantized by
+    sml_quantize_act_sb, then the per-group kernels) against the reference's
+    sml_forward_multi in its default regime for four sequences
+    (sml/sml-run.c:2559-2599), teacher-forced on the reference's tokens.
+    Float orders differ, so an int8 code flips now and then (one flip at the
+    head moves the logits ~1e-3): the mean distance must stay under a third
+    of the reference's own per-32 stepping's distance to the same logits."""
+    monkeypatch.delenv("SML_MULTI", raising=False)
+    monkeypatch.delenv("SML_MULTI_EXACT_MAX", raising=False)
+    p = tmpdir_s / "per256.ssf"
+    sa.synth_model(p, n_layer=1, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, qkv_bias=True,
+                   random_perm=True, seed=74)
+    prompts = [[5, 17, 300], [1], [42, 42, 7, 1999, 3], [250, 11]]
+    m, alone = ob.RefMulti(p, 64, 4, threads=2), ob.RefMulti(p, 64, 4, threads=2)
+    oms = [ob.OracleModel(p, 64) for _ in prompts]
+    rd = lambda a, b: np.sqrt(((a - b) ** 2).mean() / (b ** 2).mean())
+    d_orc, d_regime = [], []
+    try:
+        toks, pos = [], []
+        for b, pr in enumerate(prompts):
+            for i, t in enumerate(pr):
+                lr = m.forward(b, t, i)
+                alone.forward(b, t, i)
+                oms[b].forward(t, i)
+            toks.append(int(np.argmax(lr)))
+            pos.append(len(pr))
+        for o in oms:
+            o.per256(True)
+        for _ in range(6):
+            ref = m.step(toks, pos).astype(np.float64)
+            orc = np.stack([oms[b].forward(toks[b], pos[b]) for b in range(4)]).astype(np.float64)
+            ex = np.stack([alone.forward(b, toks[b], pos[b]) for b in range(4)]).astype(np.float64)
+            d_orc.append(rd(orc, ref))
+            d_regime.append(rd(ex, ref))
+            toks = [int(np.argmax(r)) for r in ref]
+            pos = [q + 1 for q in pos]
+    finally:
+        m.close()
+        alone.close()
+        for o in oms:
+            o.close()
+    assert np.mean(d_regime) > 1e-3                   # the regimes are told apart at all
+    assert np.mean(d_orc) < np.mean(d_regime) / 3, (np.mean(d_orc), np.mean(d_regime))
+
+
 # ------------------------------------------------------------ GPTQ-style 4-bit
 
 def test_gptq_packing_bit_order():
