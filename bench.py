@@ -232,7 +232,9 @@ def qwen_decode(tmp, prompt_len=2048, steps=64):
     dec = sa.Decoder(path, n_ctx=prompt_len + steps + 8)
     try:
         ids = np.random.default_rng(1002).integers(0, QWEN["n_vocab"], prompt_len).astype(np.int32)
+        t0 = time.perf_counter()
         tok = int(np.argmax(dec.prefill(ids, 0, QWEN["n_vocab"])))
+        t_prompt = time.perf_counter() - t0
         dec.generate(tok, prompt_len, 4)                     # warm-up (graph capture)
         sa.sync()
         t0 = time.perf_counter()
@@ -244,6 +246,7 @@ def qwen_decode(tmp, prompt_len=2048, steps=64):
         dec.close()
         os.remove(path)
     return {"tokens": steps, "positions": f"{prompt_len}..{prompt_len + steps - 1}",
+            "prompt_tokens_per_s": round(prompt_len / t_prompt, 1),
             "tokens_per_s": round(steps / dt, 1), "weight_bytes_per_token": wbytes,
             "roofline_tokens_per_s_weights_only": round(HBM_PEAK_GBS * 1e9 / wbytes, 1),
             "frac_of_weights_roofline": round(steps / dt / (HBM_PEAK_GBS * 1e9 / wbytes), 4)}
@@ -412,9 +415,24 @@ def run(a, work):
     log(f"loaded on the GPU in {time.perf_counter() - t1:.1f}s; {wbytes / 1e9:.4f} GB of weights per token")
     rng = np.random.default_rng(1003)
     ids = rng.integers(0, LLAMA["n_vocab"], prompt_len).astype(np.int32)
+    prompt = {"tokens": prompt_len}
+    if not a.no_extra:
+        # the other prompt levels first (each rewrites the same cache
+        # positions); the default level last, so decode starts from its cache
+        for lvl, n in ((2, prompt_len), (0, min(prompt_len, 256))):
+            dec.prompt_mode(lvl)
+            sa.sync()
+            t1 = time.perf_counter()
+            dec.prefill(ids[:n], 0, LLAMA["n_vocab"])
+            dt = time.perf_counter() - t1
+            prompt[f"level{lvl}"] = {"tokens": n, "s": round(dt, 3), "tokens_per_s": round(n / dt, 1)}
+        dec.prompt_mode(1)
+    sa.sync()
     t1 = time.perf_counter()
     lg = dec.prefill(ids, 0, LLAMA["n_vocab"])
-    log(f"prompt of {prompt_len} ids read a token at a time in {time.perf_counter() - t1:.1f}s")
+    dt = time.perf_counter() - t1
+    prompt["level1"] = {"tokens": prompt_len, "s": round(dt, 3), "tokens_per_s": round(prompt_len / dt, 1)}
+    log(f"prompt of {prompt_len} ids: {prompt}")
     tok = int(np.argmax(lg))
     pos = prompt_len
     warm = dec.generate(tok, pos, W)            # untimed warm-up steps
@@ -425,7 +443,7 @@ def run(a, work):
     sa.sync()
     dt = time.perf_counter() - t1
     ev_ms = dec.last_ms()
-    extra = {}
+    extra = {"prompt_reading": prompt}
     if not a.gemv_only and not a.no_extra:
         t1 = time.perf_counter()
         extra["batched_decode"] = batched_decode(dec, LLAMA["n_vocab"])

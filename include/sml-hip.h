@@ -108,10 +108,11 @@ int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const 
                         const int32_t * sums, int nrow, float * h);
 // The same two products for activations quantized per 256 values
 // (sml_hip_normq with per256 = 1, the batched regime's sml_quantize_act_sb).
-// Q4 with input widths a multiple of 256 sums each superblock's
-// sq_g*dot_g and (mq_g-127)*sum_g in integers and applies the fp32 scales
-// once per 256 columns; other widths run the per-group kernels, which are
-// exact on such activations (the scale repeats in every group).
+// Q4 with more than 8 rows and input widths a multiple of 256 runs on MFMA,
+// summing each superblock's sq_g*dot_g and (mq_g-127)*sum_g in integers and
+// applying the fp32 scales once per 256 columns; the rest runs the per-group
+// kernels, which are exact on such activations (the scale repeats in every
+// group).
 // replaces sml_matvec_batch_flat4_sb and sml_rlp_matvec
 // (sml/sml-kernel.c:1414-1435,1820-1840) as batch_group dispatches them in
 // the prompt and default multi-sequence regimes (sml/sml-run.c:2090-2150)

@@ -284,6 +284,12 @@ class Decoder:
         self.n_layer = lib().sml_gpu_layers(ctypes.byref(of))
         self.n_ctx = n_ctx
 
+    def prompt_mode(self, level):
+        """How prefill reads a prompt: 0 a token at a time, 1 batched with
+        every product the GEMV's arithmetic (the default), 2 batched with Q4
+        products on MFMA."""
+        lib().sml_gpu_prompt_mode(level)
+
     def step(self, tok, pos, n_vocab):
         p = lib().sml_gpu_step(tok, pos)
         if not p:

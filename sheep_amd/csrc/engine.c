@@ -84,6 +84,9 @@ static struct {
     int32_t * mpin;            // pinned: tokens, positions, slots of a batched step
     uint16_t ** kc_tab, ** vc_tab;   // device tables of every slot's cache base
     float * mpart;             // attention partials of every sequence of a batch
+    int32_t * iota;            // device [n_ctx]: 0, 1, 2, ... (prompt chunk positions)
+    int32_t * slotid;          // device [MAX_SLOTS][MAX_SLOTS]: row s filled with s
+    int rows_ok;               // 1: the batched body can run this model (-1: not checked yet)
 } G;
 
 static int (*g_mid_fn)(float *, int, int);
@@ -468,6 +471,10 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     HX(hipHostMalloc((void **) &G.lg_host, (size_t) G.V * 4, 0));
     HX(hipHostMalloc((void **) &G.pin, (size_t) (n_ctx + 8) * 4, 0));
     HX(hipDeviceSynchronize());
+    // prompt reading: batched (exact) unless SML_GPU_PP=0, as the reference's
+    // open does (sml/sml-gpu-fwd.c:2371-2375)
+    G.prompt_level = env_int("SML_GPU_PP", 1) == 0 ? 0 : 1;
+    G.rows_ok = -1;
     G.use_graph = env_int("SML_GRAPH", 1) != 0;
     if (G.use_graph) {
         G.g_body = capture(launch_body);
@@ -520,17 +527,28 @@ const float * sml_gpu_step(int tok, int pos) {
     return G.lg_host;
 }
 
+static void prefill_rows(int slot, int pos0, int n);
+static int rows_check(void);
+
+// A prompt, batched (prompt level 1 or 2, the reference's default) or a token
+// at a time through the decode graph (level 0, SML_GPU_PP=0).
 const float * sml_gpu_prefill(const int * ids, int pos0, int n) {
     if (!G.open || n <= 0 || pos0 < 0 || pos0 + n > G.n_ctx) return NULL;
     for (int i = 0; i < n; i++) if (ids[i] < 0 || ids[i] >= G.V) return NULL;
     HX_ENTRY(NULL);
-    G.pin[1] = pos0;
     memcpy(G.pin + 2, ids, (size_t) n * 4);
     HX(hipMemcpyAsync(G.hist + pos0, G.pin + 2, (size_t) n * 4, hipMemcpyHostToDevice, G.st));
-    HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
-    for (int i = 0; i < n; i++) {
-        run_body();
-        if (i + 1 < n) run_adv();
+    if (G.prompt_level >= 1 && n > 1 && rows_check()) {
+        prefill_rows(0, pos0, n);
+        G.pin[1] = pos0 + n - 1;
+        HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
+    } else {
+        G.pin[1] = pos0;
+        HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
+        for (int i = 0; i < n; i++) {
+            run_body();
+            if (i + 1 < n) run_adv();
+        }
     }
     run_tail();
     fetch_logits();
@@ -565,7 +583,11 @@ int sml_gpu_layers(int * of) {
     return G.open ? G.n_layer : 0;
 }
 
-void sml_gpu_prompt_mode(int level) { G.prompt_level = level > 0 ? 0 : level; }
+// 0: prompts a token at a time through the decode graph; 1: batched, exact
+// (the default); 2: batched with the Q4 products on MFMA. As the reference's
+// (sml/sml-gpu-fwd.c:2420-2423): 2 = every batched kernel, 1 = without the
+// matrix-core one, 0 = token at a time.
+void sml_gpu_prompt_mode(int level) { G.prompt_level = level <= 0 ? 0 : level >= 2 ? 2 : 1; }
 
 int sml_gpu_decode_cpu(int on) { (void) on; return 0; }
 
@@ -593,19 +615,81 @@ static int multi_per256(int ns) {
     return ns > (e ? atoi(e) : 2);
 }
 
-int sml_gpu_slots(int ns) {
-    if (!G.open || ns < 1 || ns > MAX_SLOTS) return 0;
-    HX_ENTRY(0);
+// Whether the batched body can run this model: q, k and v stacked as one
+// matrix, and gate/up sharing a permutation and width (the MoE layers batch
+// by themselves). Builds the (gate, up) tables on first use.
+static int rows_check(void) {
+    if (G.rows_ok >= 0) return G.rows_ok;
+    G.rows_ok = 0;
     for (int L = 0; L < G.n_layer; L++) {
         eng_layer * y = &G.L[L];
-        if (!y->qkv) hx_failf("layer %d: q, k and v are not one matrix; the batched step needs them stacked", L);
-        if (!y->moe && (y->perm_gu[0] != y->perm_gu[1] || y->gate->nbits != y->up->nbits))
-            hx_failf("layer %d: gate and up differ in permutation or width", L);
+        if (!y->qkv) return 0;
+        if (!y->moe && (y->perm_gu[0] != y->perm_gu[1] || y->gate->nbits != y->up->nbits)) return 0;
+    }
+    for (int L = 0; L < G.n_layer; L++) {
+        eng_layer * y = &G.L[L];
         if (!y->moe && !y->gu_tab) {
             const sml_kmat t[2] = { y->gate->k, y->up->k };
             y->gu_tab = dupload(t, sizeof t);
         }
     }
+    G.rows_ok = 1;
+    return 1;
+}
+
+static void rows_tables(void) {
+    G.kcs[0] = G.kc;
+    G.vcs[0] = G.vc;
+    HX(hipMemcpy(G.kc_tab, G.kcs, MAX_SLOTS * sizeof(void *), hipMemcpyHostToDevice));
+    HX(hipMemcpy(G.vc_tab, G.vcs, MAX_SLOTS * sizeof(void *), hipMemcpyHostToDevice));
+}
+
+// The batched body's buffers, for up to MAX_SLOTS rows (sequences, or
+// positions of one prompt chunk).
+static void rows_alloc(void) {
+    if (G.mx) return;
+    const size_t R = MAX_SLOTS;
+    size_t wide = (size_t) (G.F > G.E ? G.F : G.E);
+    if ((size_t) G.H * G.hd > wide) wide = (size_t) G.H * G.hd;
+    G.mx = dalloc(R * G.E * 4);
+    G.mxn = dalloc(R * G.E * 4);
+    G.mqkv = dalloc(R * (size_t) (G.H + 2 * G.KV) * G.hd * 4);
+    G.matt = dalloc(R * (size_t) G.H * G.hd * 4);
+    G.mh = dalloc(R * (size_t) G.F * 4);
+    G.mlog = dalloc(R * (size_t) G.V * 4);
+    G.maq = dalloc(R * wide);
+    G.mas = dalloc(R * wide / 32 * 4);
+    G.masum = dalloc(R * wide / 32 * 4);
+    G.mtok = dalloc(R * 4);
+    G.mpos = dalloc(R * 4);
+    G.mslot = dalloc(R * 4);
+    G.mpart = dalloc(R * sml_hip_attn_part_floats(G.H, G.hd, G.n_ctx) * 4);
+    G.kc_tab = dalloc(R * sizeof(void *));
+    G.vc_tab = dalloc(R * sizeof(void *));
+    HX(hipHostMalloc((void **) &G.mpin, 3 * R * 4, 0));
+    int32_t * h = malloc((size_t) (G.n_ctx > (int) (R * R) ? G.n_ctx : (int) (R * R)) * 4);
+    if (!h) hx_failf("out of host memory");
+    for (int i = 0; i < G.n_ctx; i++) h[i] = i;
+    G.iota = dalloc((size_t) G.n_ctx * 4);
+    HX(hipMemcpy(G.iota, h, (size_t) G.n_ctx * 4, hipMemcpyHostToDevice));
+    for (int i = 0; i < (int) (R * R); i++) h[i] = i / (int) R;
+    G.slotid = dalloc(R * R * 4);
+    HX(hipMemcpy(G.slotid, h, R * R * 4, hipMemcpyHostToDevice));
+    free(h);
+    rows_tables();
+}
+
+int sml_gpu_slots(int ns) {
+    if (!G.open || ns < 1 || ns > MAX_SLOTS) return 0;
+    HX_ENTRY(0);
+    if (!rows_check()) {
+        for (int L = 0; L < G.n_layer; L++) {
+            eng_layer * y = &G.L[L];
+            if (!y->qkv) hx_failf("layer %d: q, k and v are not one matrix; the batched step needs them stacked", L);
+        }
+        hx_failf("gate and up differ in permutation or width");
+    }
+    rows_alloc();
     const size_t kvn = (size_t) G.n_layer * G.n_ctx * G.KV * G.hd;
     for (int s = G.nslot > 1 ? G.nslot : 1; s < ns; s++) {
         G.kcs[s] = dalloc(kvn * 2);
@@ -613,68 +697,23 @@ int sml_gpu_slots(int ns) {
         HX(hipMemset(G.kcs[s], 0, kvn * 2));
         HX(hipMemset(G.vcs[s], 0, kvn * 2));
     }
-    if (!G.mx) {
-        const size_t R = MAX_SLOTS;
-        size_t wide = (size_t) (G.F > G.E ? G.F : G.E);
-        if ((size_t) G.H * G.hd > wide) wide = (size_t) G.H * G.hd;
-        G.mx = dalloc(R * G.E * 4);
-        G.mxn = dalloc(R * G.E * 4);
-        G.mqkv = dalloc(R * (size_t) (G.H + 2 * G.KV) * G.hd * 4);
-        G.matt = dalloc(R * (size_t) G.H * G.hd * 4);
-        G.mh = dalloc(R * (size_t) G.F * 4);
-        G.mlog = dalloc(R * (size_t) G.V * 4);
-        G.maq = dalloc(R * wide);
-        G.mas = dalloc(R * wide / 32 * 4);
-        G.masum = dalloc(R * wide / 32 * 4);
-        G.mtok = dalloc(R * 4);
-        G.mpos = dalloc(R * 4);
-        G.mslot = dalloc(R * 4);
-        G.mpart = dalloc(R * sml_hip_attn_part_floats(G.H, G.hd, G.n_ctx) * 4);
-        G.kc_tab = dalloc(R * sizeof(void *));
-        G.vc_tab = dalloc(R * sizeof(void *));
-        HX(hipHostMalloc((void **) &G.mpin, 3 * R * 4, 0));
-    }
     if (ns > G.nslot) G.nslot = ns;
-    G.kcs[0] = G.kc;
-    G.vcs[0] = G.vc;
-    HX(hipMemcpy(G.kc_tab, G.kcs, MAX_SLOTS * sizeof(void *), hipMemcpyHostToDevice));
-    HX(hipMemcpy(G.vc_tab, G.vcs, MAX_SLOTS * sizeof(void *), hipMemcpyHostToDevice));
+    rows_tables();
     HX(hipDeviceSynchronize());
     HX_LEAVE();
     return ns;
 }
 
-const float * sml_gpu_prefill_slot(int slot, const int * ids, int pos0, int n) {
-    if (slot == 0) return sml_gpu_prefill(ids, pos0, n);
-    if (!G.open || slot < 0 || slot >= G.nslot || n <= 0 || pos0 < 0 || pos0 + n > G.n_ctx) return NULL;
-    for (int i = 0; i < n; i++) if (ids[i] < 0 || ids[i] >= G.V) return NULL;
-    HX_ENTRY(NULL);
-    G.pin[1] = pos0;
-    memcpy(G.pin + 2, ids, (size_t) n * 4);
-    HX(hipMemcpyAsync(G.hist + pos0, G.pin + 2, (size_t) n * 4, hipMemcpyHostToDevice, G.st));
-    HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
-    // the captured graphs hold slot 0's cache: other slots launch directly
-    G.cur_slot = slot;
-    jmp_buf * outer = hx.jb;
-    jmp_buf jb;
-    if (setjmp(jb)) { G.cur_slot = 0; hx.jb = outer; longjmp(*outer, 1); }
-    hx.jb = &jb;
-    for (int i = 0; i < n; i++) {
-        launch_body();
-        if (i + 1 < n) launch_adv();
-    }
-    launch_tail();
-    hx.jb = outer;
-    G.cur_slot = 0;
-    fetch_logits();
-    HX_LEAVE();
-    return G.lg_host;
-}
-
-static void launch_multi(int ns) {
+// The batched body for ns rows: row b is token tok[b] at position pos[b] of
+// slot slot[b]'s cache (device arrays). Every weight matrix streams once for
+// all rows. causal: rows may be positions of one sequence (a prompt chunk),
+// so K/V are written for every row before any row attends. head: logits of
+// every row into G.mlog; otherwise the residuals stay in G.mx.
+static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const int32_t * slot, int regime,
+                        int causal, int head) {
     const size_t kvd = (size_t) G.KV * G.hd, qkv = (size_t) (G.H + 2 * G.KV) * G.hd, hq = (size_t) G.H * G.hd;
-    const int mt = gemm_mt(ns), sb = multi_per256(ns);
-    op_embed_rows(G.st, G.emb, G.mtok, NULL, ns, pdev(G.perm_emb), G.mx);
+    const int mt = gemm_mt(ns), sb = regime == GEMM_PER256;
+    op_embed_rows(G.st, G.emb, tok, NULL, ns, pdev(G.perm_emb), G.mx);
     for (int L = 0; L < G.n_layer; L++) {
         eng_layer * y = &G.L[L];
         const int32_t * pp[1];
@@ -684,17 +723,17 @@ static void launch_multi(int ns) {
         pp[0] = pdev(y->perm_qkv[0]);
         op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
         op_gemm(G.st, y->qkv->kdev, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
-                G.mqkv, y->bias_qkv, NULL, sb);
+                G.mqkv, y->bias_qkv, NULL, regime);
         const int fuse_q = y->perm_o < 0 && !sb;         // the merge quantizes per 32
-        op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, G.mslot, (size_t) L * G.n_ctx * kvd,
-                           G.rc, G.rs, G.mpos, ns, G.H, G.KV, G.hd, G.n_ctx, G.mpart, G.matt,
-                           fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL);
+        op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
+                           G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.mpart, G.matt,
+                           fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL, causal);
         if (!fuse_q) {
             pp[0] = pdev(y->perm_o);
             op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, sb);
         }
         op_gemm(G.st, y->o->kdev, 1, 0, y->o->nbits, G.E, (int) hq, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
-                G.mx, NULL, G.mx, sb);
+                G.mx, NULL, G.mx, regime);
         if (y->moe) {
             op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 0, NULL, NULL, NULL, NULL, G.mxn, sb);
             y->moe->per256 = sb;
@@ -705,19 +744,77 @@ static void launch_multi(int ns) {
         pp[0] = pdev(y->perm_gu[0]);
         op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
         op_gemm(G.st, y->gu_tab, 1, 1, y->gate->nbits, G.F, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mh,
-                NULL, NULL, sb);
+                NULL, NULL, regime);
         pp[0] = pdev(y->perm_down);
         op_normq_rows(G.st, G.mh, NULL, NULL, G.eps, G.F, ns, 1, pp, qq, ss, uu, NULL, sb);
         op_gemm(G.st, y->down->kdev, 1, 0, y->down->nbits, G.E, G.F, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
-                G.mx, NULL, G.mx, sb);
+                G.mx, NULL, G.mx, regime);
     }
+    if (!head) return;
     const int32_t * pp[1] = { pdev(G.perm_head) };
     int8_t * qq[1] = { G.maq };
     float * ss[1] = { G.mas };
     int32_t * uu[1] = { G.masum };
     op_normq_rows(G.st, G.mx, NULL, G.out_norm, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
     op_gemm(G.st, G.head->kdev, 1, 0, G.head->nbits, G.V, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mlog,
-            NULL, NULL, sb);
+            NULL, NULL, regime);
+}
+
+// Batched prompt reading, the reference's gpu_prefill (sml/sml-gpu-fwd.c:
+// 1418-1603): chunks of up to MAX_SLOTS positions through the batched body,
+// each weight matrix streamed once per chunk; the last position's residual
+// then goes through the decode tail (final norm, head, greedy pick). At
+// level 1 every product is the GEMV's arithmetic and the attention the
+// decode kernel's, so the cache, the residuals and the logits equal reading
+// the prompt a token at a time, bit for bit. The ids are already in G.hist.
+static void prefill_rows(int slot, int pos0, int n) {
+    rows_alloc();
+    const int regime = G.prompt_level >= 2 ? GEMM_PER32 : GEMM_EXACT;
+    int last = 0;
+    for (int p0 = 0; p0 < n; p0 += MAX_SLOTS) {
+        const int nb = n - p0 < MAX_SLOTS ? n - p0 : MAX_SLOTS;
+        launch_rows(nb, G.hist + pos0 + p0, G.iota + pos0 + p0, G.slotid + slot * MAX_SLOTS, regime, 1, 0);
+        last = nb - 1;
+    }
+    HX(hipMemcpyAsync(G.x, G.mx + (size_t) last * G.E, (size_t) G.E * 4, hipMemcpyDeviceToDevice, G.st));
+}
+
+const float * sml_gpu_prefill_slot(int slot, const int * ids, int pos0, int n) {
+    if (slot == 0) return sml_gpu_prefill(ids, pos0, n);
+    if (!G.open || slot < 0 || slot >= G.nslot || n <= 0 || pos0 < 0 || pos0 + n > G.n_ctx) return NULL;
+    for (int i = 0; i < n; i++) if (ids[i] < 0 || ids[i] >= G.V) return NULL;
+    HX_ENTRY(NULL);
+    G.pin[1] = pos0 + n - 1;
+    memcpy(G.pin + 2, ids, (size_t) n * 4);
+    HX(hipMemcpyAsync(G.hist + pos0, G.pin + 2, (size_t) n * 4, hipMemcpyHostToDevice, G.st));
+    if (G.prompt_level >= 1 && rows_check()) {
+        prefill_rows(slot, pos0, n);
+        HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
+        run_tail();
+    } else {
+        // the captured graphs hold slot 0's cache: other slots launch directly
+        G.pin[0] = pos0;
+        HX(hipMemcpyAsync(G.pos, &G.pin[0], 4, hipMemcpyHostToDevice, G.st));
+        G.cur_slot = slot;
+        jmp_buf * outer = hx.jb;
+        jmp_buf jb;
+        if (setjmp(jb)) { G.cur_slot = 0; hx.jb = outer; longjmp(*outer, 1); }
+        hx.jb = &jb;
+        for (int i = 0; i < n; i++) {
+            launch_body();
+            if (i + 1 < n) launch_adv();
+        }
+        launch_tail();
+        hx.jb = outer;
+        G.cur_slot = 0;
+    }
+    fetch_logits();
+    HX_LEAVE();
+    return G.lg_host;
+}
+
+static void launch_multi(int ns) {
+    launch_rows(ns, G.mtok, G.mpos, G.mslot, multi_per256(ns) ? GEMM_PER256 : GEMM_PER32, 0, 1);
 }
 
 int sml_gpu_step_multi(const int * tok, const int * pos, const int * slot, int ns, float * logits_out) {

@@ -127,6 +127,10 @@ typedef struct {
     uint16_t * const * vc_slots;
     const int32_t * slot;
     size_t layer_off;
+    // 1: sml_ropekv already rotated and wrote every sequence's k and v (several
+    // positions of one sequence in one launch attend to each other), so the
+    // attention kernel writes nothing
+    int kv_written;
 } sml_kattn;
 
 

@@ -881,7 +881,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         knew[e] = (unsigned) f2h(kn[2 * e]) | ((unsigned) f2h(kn[2 * e + 1]) << 16);
         vnew[e] = (unsigned) f2h(vn[2 * e]) | ((unsigned) f2h(vn[2 * e + 1]) << 16);
     }
-    if (t0 <= pos && pos < t1 && tid < 16) {
+    if (!a.kv_written && t0 <= pos && pos < t1 && tid < 16) {
         *(v4u *) (kcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = knew;
         *(v4u *) (vcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = vnew;
     }
@@ -971,6 +971,36 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         po[((size_t) j * a.nsplit + split) * HD + d] = o;
         if (d == 0) pml[(size_t) j * a.nsplit + split] = make_float2(M, L);
     }
+}
+
+// RoPE of k at each sequence's position and the fp16 write of k and v into
+// its slot's cache: the attention kernel's rotation and rounding, lane for
+// lane, so the cache holds what that kernel would have written. Runs ahead of
+// an attention launch with kv_written set, in which positions of one sequence
+// read each other's k and v (prompt reading). Grid: one workgroup per
+// sequence; block: one 16-lane row per kv head.
+extern "C" __global__ __launch_bounds__(128) void sml_ropekv(const sml_kattn a) {
+    const int b = blockIdx.x, tid = threadIdx.x, kh = tid >> 4, l16 = tid & 15, kvd = a.n_kv * HD;
+    const float * ak = a.k + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
+    const float * av = a.v + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
+    float kn[8], vn[8];
+    load_f8(ak, kn);
+    load_f8(av, vn);
+    const int pos = a.pos[b], half = HD / 2;
+    float cs[8], sn[8];
+    load_f8(a.cos_t + (size_t) pos * half + (l16 & 7) * 8, cs);
+    load_f8(a.sin_t + (size_t) pos * half + (l16 & 7) * 8, sn);
+    rope8(kn, cs, sn, l16 < 8);
+    v4u knew, vnew;
+    #pragma unroll
+    for (int e = 0; e < 4; e++) {
+        knew[e] = (unsigned) f2h(kn[2 * e]) | ((unsigned) f2h(kn[2 * e + 1]) << 16);
+        vnew[e] = (unsigned) f2h(vn[2 * e]) | ((unsigned) f2h(vn[2 * e + 1]) << 16);
+    }
+    uint16_t * kcache = a.kc_slots ? a.kc_slots[a.slot[b]] + a.layer_off : a.kcache;
+    uint16_t * vcache = a.vc_slots ? a.vc_slots[a.slot[b]] + a.layer_off : a.vcache;
+    *(v4u *) (kcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = knew;
+    *(v4u *) (vcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = vnew;
 }
 
 #define ATTN_KERNEL(R) \

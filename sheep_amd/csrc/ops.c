@@ -503,7 +503,7 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
-                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out) {
+                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal) {
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
     if (nseq < 1 || nseq > 65535) hx_failf("attention batch of %d", nseq);
@@ -516,6 +516,11 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     a.part = part; a.out = out; a.q_out = q_out; a.s_out = s_out; a.u_out = u_out;
     a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
+    a.kv_written = causal;
+    if (causal) {
+        if (n_kv > 8) hx_failf("causal attention takes at most 8 kv heads");
+        hx_launch("sml_ropekv", (unsigned) nseq, 1, (unsigned) (16 * n_kv), 0, st, &a);
+    }
     char name[32];
     const int aw = env_int("SML_ATTN_WAVES", 8) == 4 ? 4 : 8;
     if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
@@ -714,7 +719,8 @@ int gemm_mt(int m) { return m <= 1 ? 1 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
 
 void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
-             const int32_t * sums, float * y, const float * bias, const float * resid, int per256) {
+             const int32_t * sums, float * y, const float * bias, const float * resid, int regime) {
+    const int per256 = regime == GEMM_PER256;
     if (swiglu && (bias || resid)) hx_failf("SwiGLU GEMM takes no bias or residual");
     if (mt != 1 && mt != 4 && mt != 8 && mt != 16) hx_failf("small-M GEMM takes at most 16 rows");
     if (!count && (m_all < 1 || m_all > mt)) hx_failf("small-M GEMM of %d rows", m_all);
@@ -725,15 +731,16 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
     a.count = count; a.m_all = m_all; a.mmax = mmax;
     a.q = q; a.scale = scale; a.sums = sums; a.y = y; a.bias = bias; a.resid = resid;
     char name[48];
-    // Q4 runs on MFMA: with per-256 activations always (the integer
-    // superblock epilogue); with per-32 ones for more than 8 activation rows
-    // (measured faster there; below, the VALU dot4 kernel wins) unless the
-    // exact regime is asked for (SML_MULTI=exact: every row bit for bit the
-    // GEMV's). Per-32 expert groups (count != NULL) hold few rows each and
-    // stay on VALU. SML_MGEMM=0 keeps every product on the VALU kernels.
+    // Q4 with more than 8 activation rows runs on MFMA (measured faster
+    // there; below, the VALU dot4 kernel wins), with the integer superblock
+    // epilogue on per-256 activations, unless the exact regime is asked for
+    // (SML_MULTI=exact or GEMM_EXACT: every row bit for bit the GEMV's).
+    // Expert groups (count != NULL) hold few rows each (16 tokens top-2 over
+    // 8 experts: 2 to 7) and stay on VALU, whose per-group epilogue is exact
+    // on per-256 activations too. SML_MGEMM=0 keeps every product on VALU.
     const char * mode = getenv("SML_MULTI");
-    const int exact = mode && !strcmp(mode, "exact");
-    if (nbits == 4 && cols % 256 == 0 && (per256 || (!count && m_all > 8 && !exact)) && env_int("SML_MGEMM", 1)) {
+    const int exact = regime == GEMM_EXACT || (mode && !strcmp(mode, "exact"));
+    if (nbits == 4 && cols % 256 == 0 && !count && m_all > 8 && !exact && env_int("SML_MGEMM", 1)) {
         int rb = !swiglu && rows >= 32768 ? 2 : 1;
         const int fr = env_int("SML_MGEMM_RB", 0);
         if (fr == 1 || fr == 2) rb = fr;

@@ -49,11 +49,15 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
              const float * resid, const gemv_fuse * fu);
 // Small-M GEMM over ngroups matrix groups (device table tab: one matrix per
 // group, or gate/up pairs for SwiGLU); m_all rows (count == NULL) or count[e]
-// rows per group, at most mt (1, 4, 8 or 16). per256: the activation is
-// quantized per 256 values (Q4 then takes the integer superblock epilogue).
+// rows per group, at most mt (1, 4, 8 or 16). The activation regime:
+enum {
+    GEMM_PER32 = 0,     // per-32 activations; Q4 above 8 rows on MFMA (fp32 order differs from the GEMV's)
+    GEMM_PER256 = 1,    // per-256 activations; Q4 on MFMA with the integer superblock epilogue
+    GEMM_EXACT = 2,     // per-32 activations, every row the GEMV's arithmetic bit for bit
+};
 void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
-             const int32_t * sums, float * y, const float * bias, const float * resid, int per256);
+             const int32_t * sums, float * y, const float * bias, const float * resid, int regime);
 int gemm_mt(int m);
 // One matrix holding the rows of several FLAT records of one width and input
 // width, stacked in order (the q, k and v projections as one GEMV).
@@ -74,11 +78,13 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
 // Attention for nseq sequences in one launch: sequence b's q, k, v at
 // qkv + b * qkv_stride (q, then k, then v), its cache kc_slots[slot[b]] +
 // layer_off, its position pos[b]; part, out and the quantized out hold one
-// sequence's worth per b.
+// sequence's worth per b. causal: entries may be positions of one sequence
+// (prompt reading), so every k and v is rotated and written by one launch
+// before any entry attends.
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
-                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out);
+                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal);
 void op_argmax(hipStream_t st, const float * logits, int n, int32_t * tok, int32_t * pos, int32_t * hist,
                int hist_n);
 void op_advance(hipStream_t st, int32_t * pos);

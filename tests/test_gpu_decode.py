@@ -140,6 +140,46 @@ def test_generate_equals_stepping_and_prefill(tiny):
         d.close()
 
 
+@pytest.fixture(scope="module")
+def moe_model(tmp_path_factory):
+    p = tmp_path_factory.mktemp("dec") / "moe_pf.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, n_expert=8,
+                   n_expert_used=2, moe_flags=1, random_perm=True, seed=62)
+    return p
+
+
+@pytest.mark.parametrize("model", ["tiny", "tiny_inorder", "qwenish", "moe_model"])
+def test_batched_prompt_equals_stepping(model, request):
+    """Batched prompt reading (level 1, the default): chunks of 16 positions
+    through the small-M GEMM and the causal attention read a prompt exactly
+    as stepping it does -- the logits of the last id bit for bit, for a first
+    part and for a continuation of that prefix (37 ids: ragged chunks), and
+    the same greedy continuation. Level 2 (Q4 on MFMA) agrees to float
+    rounding."""
+    p = request.getfixturevalue(model)
+    V = 32000 if model == "qwenish" else 2000
+    ids = np.random.default_rng(17).integers(0, V, 37).astype(np.int32)
+    outs = {}
+    for level in (0, 1, 2):
+        d = sa.Decoder(p, n_ctx=96)
+        try:
+            d.prompt_mode(level)
+            a = d.prefill(ids[:20], 0, V)
+            b = d.prefill(ids[20:], 20, V)
+            gen = list(d.generate(int(np.argmax(b)), 37, 8))
+            outs[level] = (a, b, gen)
+        finally:
+            d.close()
+    for i in range(2):
+        np.testing.assert_array_equal(outs[1][i], outs[0][i], err_msg=f"level 1, part {i}")
+    assert outs[1][2] == outs[0][2]
+    for i in range(2):
+        ref = outs[0][i]
+        assert np.corrcoef(outs[2][i], ref)[0, 1] > 0.9999, f"level 2, part {i}"
+        if tie_margin(ref) > 0.01:
+            assert int(np.argmax(outs[2][i])) == int(np.argmax(ref)), f"level 2, part {i}"
+
+
 def test_greedy_tokens_qwen_layers(qwenish):
     n = 24
     toks, logits = greedy_oracle(qwenish, 100, n, 128)
