@@ -358,6 +358,8 @@ def main():
     ap.add_argument("--small-gemm", action="store_true", help="only time the 16-row small-M GEMMs")
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: fill the 4096 context)")
+    ap.add_argument("--prompt-only", type=int, metavar="LEVEL", default=-1,
+                    help="only read the Llama-3-8B-shaped prompt at this prompt level (0, 1 or 2)")
     a = ap.parse_args()
     if a.pmc_probe:
         pmc_probe(a.pmc_probe)
@@ -370,11 +372,33 @@ def main():
     tmp = scratch_dir()
     work = tempfile.mkdtemp(prefix="smlbench_", dir=tmp)
     try:
-        res = {"small_m_gemm": small_gemm(work)} if a.small_gemm else run(a, work)
+        if a.small_gemm:
+            res = {"small_m_gemm": small_gemm(work)}
+        elif a.prompt_only >= 0:
+            res = {"prompt_reading": prompt_only(work, a.prompt_only, a.prompt if a.prompt > 0 else 3960)}
+        else:
+            res = run(a, work)
     finally:
         if not a.keep:
             shutil.rmtree(work, ignore_errors=True)
     print(json.dumps(res), flush=True)
+
+
+def prompt_only(work, level, n):
+    """The Llama-3-8B-shaped file's prompt of n ids read once at one prompt level."""
+    path = os.path.join(work, "llama3_8b_q4.ssf")
+    sa.synth_model(path, n_ctx_train=N_CTX, **LLAMA)
+    dec = sa.Decoder(path, n_ctx=N_CTX)
+    try:
+        ids = np.random.default_rng(1003).integers(0, LLAMA["n_vocab"], n).astype(np.int32)
+        dec.prompt_mode(level)
+        sa.sync()
+        t0 = time.perf_counter()
+        dec.prefill(ids, 0, LLAMA["n_vocab"])
+        dt = time.perf_counter() - t0
+    finally:
+        dec.close()
+    return {"level": level, "tokens": n, "s": round(dt, 3), "tokens_per_s": round(n / dt, 1)}
 
 
 def run(a, work):

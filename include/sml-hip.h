@@ -162,6 +162,15 @@ typedef struct sml_hip_gptq sml_hip_gptq;
 sml_hip_gptq * sml_hip_gptq_upload(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
                                    int rows, int cols, int group, int zero_add);
 void           sml_hip_gptq_free(sml_hip_gptq * m);
+// An AWQ 4-bit matrix (AutoAWQ GEMM layout, what tooling/sml_unpack.py:78,
+// 100-118 dequant_awq reads): qweight int32 [cols][rows/8] with 8 outputs per
+// word, output 8j+k in nibble (0, 4, 1, 5, 2, 6, 3, 7)[k]; qzeros int32
+// [cols/128][rows/8] packed the same way, or NULL for the default zero 8;
+// scales fp16 [cols/128][rows]; weight = (code - zero) * scale. Repacked on
+// the host into the GPTQ device layout, so every sml_hip_gptq_* call takes
+// it. The reference converts AWQ copies offline and has no kernel for it.
+sml_hip_gptq * sml_hip_awq_upload(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                                  int rows, int cols, int group);
 // Bytes the matrix occupies in HBM (qweight + qzeros + scales).
 size_t         sml_hip_gptq_bytes(const sml_hip_gptq * m);
 // y = W.x with fp32 x (no activation quantization).

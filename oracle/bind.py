@@ -59,6 +59,8 @@ def oracle():
             "orc_gptq_unpack_row": (None, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
             "orc_gptq_dequant_row": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
             "orc_gptq_matvec": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+            "orc_awq_unpack_row": (None, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+            "orc_awq_dequant_row": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
             "orc_model_open": (c_void_p, [c_char_p, c_int]),
             "orc_model_close": (None, [c_void_p]),
             "orc_forward": (P(c_float), [c_void_p, c_int, c_int]),
@@ -393,3 +395,18 @@ def gptq_matvec(qweight, qzeros, scales, rows, cols, x, group=128, zero_add=1):
     x = np.ascontiguousarray(x, np.float32)
     oracle().orc_gptq_matvec(ptr(qweight), ptr(qzeros), ptr(scales), rows, cols, group, zero_add, ptr(x), ptr(y))
     return y
+
+
+# ------------------------------------------------------------ AWQ 4-bit
+
+def awq_unpack_row(qweight, qzeros, rows, cols, row, group=128):
+    c = np.zeros(cols, np.uint8)
+    z = np.zeros(cols // group, np.uint8)
+    oracle().orc_awq_unpack_row(ptr(qweight), ptr(qzeros), rows, cols, group, row, ptr(c), ptr(z))
+    return c, z
+
+
+def awq_dequant_row(qweight, qzeros, scales, rows, cols, row, group=128):
+    out = np.zeros(cols, np.float32)
+    oracle().orc_awq_dequant_row(ptr(qweight), ptr(qzeros), ptr(scales), rows, cols, group, row, ptr(out))
+    return out

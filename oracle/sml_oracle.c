@@ -391,6 +391,36 @@ void orc_gptq_matvec(const int32_t * qweight, const int32_t * qzeros, const uint
     }
 }
 
+// ------------------------------------------------------------ AWQ 4-bit
+
+// tooling/sml_unpack.py:78,100-118 (dequant_awq): qweight int32 [cols][rows/8]
+// packs 8 OUTPUTS per word, output 8j+k of word j in nibble AWQ_REVERSE[k]
+// with AWQ_REVERSE = (0, 4, 1, 5, 2, 6, 3, 7); qzeros [cols/group][rows/8]
+// the same way, or, absent, zero 2^(bits-1) = 8; no +1 on the zeros.
+static const int awq_nibble[8] = { 0, 4, 1, 5, 2, 6, 3, 7 };
+
+void orc_awq_unpack_row(const int32_t * qweight, const int32_t * qzeros, int rows, int cols, int group, int row,
+                        uint8_t * codes, uint8_t * zeros) {
+    const int sh = 4 * awq_nibble[row % 8];
+    for (int k = 0; k < cols; k++)
+        codes[k] = (uint8_t) (((uint32_t) qweight[(size_t) k * (rows / 8) + row / 8] >> sh) & 15u);
+    for (int g = 0; g < cols / group; g++)
+        zeros[g] = qzeros ? (uint8_t) (((uint32_t) qzeros[(size_t) g * (rows / 8) + row / 8] >> sh) & 15u) : 8;
+}
+
+// (w - z[g]).float() * scales[g], scales fp16 [cols/group][rows]
+void orc_awq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows,
+                         int cols, int group, int row, float * out) {
+    uint8_t * c = malloc((size_t) cols), * z = malloc((size_t) (cols / group));
+    orc_awq_unpack_row(qweight, qzeros, rows, cols, group, row, c, z);
+    for (int k = 0; k < cols; k++) {
+        const int g = k / group;
+        out[k] = (float) ((int) c[k] - (int) z[g]) * orc_f16_to_f32(scales[(size_t) g * rows + row]);
+    }
+    free(c);
+    free(z);
+}
+
 // ------------------------------------------------------------ decoder
 
 // The oracle reads the file with its own parser: offsets of the packed

@@ -101,6 +101,10 @@ void orc_gptq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const
 // y = W.x with the dequantized weights, summed in double.
 void orc_gptq_matvec(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows, int cols,
                      int group, int zero_add, const float * x, float * y);
+void orc_awq_unpack_row(const int32_t * qweight, const int32_t * qzeros, int rows, int cols, int group, int row,
+                        uint8_t * codes, uint8_t * zeros);
+void orc_awq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows,
+                         int cols, int group, int row, float * out);
 
 // ---------------------------------------------------------------- decoder
 // A whole decode step over an SSF file (Llama / Qwen2 / Mixtral family: RMSNorm,

@@ -649,6 +649,48 @@ sml_hip_gptq * sml_hip_gptq_upload(const int32_t * qweight, const int32_t * qzer
     return m;
 }
 
+// AWQ (tooling/sml_unpack.py:78,100-118): qweight int32 [cols][rows/8] packs
+// 8 outputs per word, output 8j+k in nibble awq_nibble[k]; qzeros the same
+// way over [cols/group][rows/8], or absent (zero 8); zeros stored as they
+// are. Repacked on the host into the GPTQ device layout (codes along the
+// input, zeros in natural nibble order, zero_add 0), whose kernels then run
+// it unchanged: codes and zeros are moved, never recomputed.
+static const int awq_nibble[8] = { 0, 4, 1, 5, 2, 6, 3, 7 };
+
+sml_hip_gptq * sml_hip_awq_upload(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                                  int rows, int cols, int group) {
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 128 || group != 128 || !qweight || !scales) {
+        snprintf(hx.err, sizeof hx.err, "AWQ matrix %dx%d group %d: rows must be a multiple of 8, cols of 128, "
+                 "group 128", rows, cols, group);
+        return NULL;
+    }
+    const size_t R = (size_t) rows, C = (size_t) cols, ng = C / 128;
+    uint32_t * gw = calloc(C / 8 * R, 4);
+    uint32_t * gz = calloc(ng * (R / 8), 4);
+    if (!gw || !gz) {
+        free(gw); free(gz);
+        snprintf(hx.err, sizeof hx.err, "out of host memory");
+        return NULL;
+    }
+    for (size_t k = 0; k < C; k++)
+        for (size_t j = 0; j < R / 8; j++) {
+            const uint32_t w = (uint32_t) qweight[k * (R / 8) + j];
+            for (int i = 0; i < 8; i++)
+                gw[(k / 8) * R + 8 * j + i] |= ((w >> (4 * awq_nibble[i])) & 15u) << (4 * (k % 8));
+        }
+    for (size_t g = 0; g < ng; g++)
+        for (size_t j = 0; j < R / 8; j++) {
+            const uint32_t z = qzeros ? (uint32_t) qzeros[g * (R / 8) + j] : 0x88888888u;
+            uint32_t o = 0;
+            for (int i = 0; i < 8; i++) o |= ((z >> (4 * awq_nibble[i])) & 15u) << (4 * i);
+            gz[g * (R / 8) + j] = o;
+        }
+    sml_hip_gptq * m = sml_hip_gptq_upload((const int32_t *) gw, (const int32_t *) gz, scales, rows, cols, group, 0);
+    free(gw);
+    free(gz);
+    return m;
+}
+
 void sml_hip_gptq_free(sml_hip_gptq * m) {
     HX_ENTRY();
     if (m) {

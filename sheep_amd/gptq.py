@@ -1,5 +1,6 @@
-"""GPTQ-style 4-bit matrices on the device: packing, a seeded synthetic
-generator and the ctypes wrapper of sml_hip_gptq_*.
+"""GPTQ-style and AWQ 4-bit matrices on the device: packing, a seeded
+synthetic generator and the ctypes wrapper of sml_hip_gptq_* /
+sml_hip_awq_upload.
 
 The layout is AutoGPTQ's (what tooling/sml_unpack.py:66-95 dequantizes):
 rows are outputs, cols inputs; qweight int32 [cols/8, rows] with the codes of
@@ -33,6 +34,30 @@ def pack(codes, zeros, scales, zero_add=1):
             np.ascontiguousarray(np.asarray(scales, np.float16).T))
 
 
+AWQ_NIBBLE = (0, 4, 1, 5, 2, 6, 3, 7)     # nibble of output 8j+k in word j (tooling/sml_unpack.py:78)
+
+
+def pack_awq(codes, zeros, scales):
+    """codes uint8 [rows, cols] in 0..15, zeros [rows, cols/group] (None: the
+    default 8, no qzeros), scales [rows, cols/group] -> (qweight, qzeros or
+    None, scales fp16) in the AWQ GEMM layout: qweight [cols, rows/8] with
+    output 8j+k in nibble AWQ_NIBBLE[k] of word (input, j)."""
+    codes = np.asarray(codes, np.uint32)
+    rows, cols = codes.shape
+    c = codes.T.reshape(cols, rows // 8, 8)                    # [k, j, i]
+    qweight = np.zeros((cols, rows // 8), np.uint32)
+    for i in range(8):
+        qweight |= c[:, :, i] << np.uint32(4 * AWQ_NIBBLE[i])
+    qzeros = None
+    if zeros is not None:
+        z = np.asarray(zeros, np.uint32).T.reshape(-1, rows // 8, 8)
+        qzeros = np.zeros(z.shape[:2], np.uint32)
+        for i in range(8):
+            qzeros |= (z[:, :, i] & np.uint32(15)) << np.uint32(4 * AWQ_NIBBLE[i])
+        qzeros = qzeros.view(np.int32)
+    return qweight.view(np.int32), qzeros, np.ascontiguousarray(np.asarray(scales, np.float16).T)
+
+
 def synth(rows, cols, seed, group=128):
     """Codes uniform over 0..15, zero point 8 (stored as 7), per-group scales
     |N(0, 0.02)| / 7 in fp16: the GPTQ-4 recipe of the width sweep."""
@@ -45,14 +70,20 @@ def synth(rows, cols, seed, group=128):
 
 
 class GptqMat:
-    """A GPTQ-style matrix resident in HBM."""
+    """A GPTQ-style matrix resident in HBM (awq=True: the arrays are in the
+    AWQ layout, qzeros may be None, zero_add is ignored)."""
 
-    def __init__(self, qweight, qzeros, scales, rows, cols, group=128, zero_add=1):
-        self.rows, self.cols, self.group, self.zero_add = rows, cols, group, zero_add
+    def __init__(self, qweight, qzeros, scales, rows, cols, group=128, zero_add=1, awq=False):
+        self.rows, self.cols, self.group, self.zero_add = rows, cols, group, 0 if awq else zero_add
         qw = np.ascontiguousarray(qweight, np.int32)
-        qz = np.ascontiguousarray(qzeros, np.int32)
+        qz = None if qzeros is None else np.ascontiguousarray(qzeros, np.int32)
         sc = np.ascontiguousarray(scales, np.float16)
-        h = lib().sml_hip_gptq_upload(qw.ctypes.data, qz.ctypes.data, sc.ctypes.data, rows, cols, group, zero_add)
+        if awq:
+            h = lib().sml_hip_awq_upload(qw.ctypes.data, None if qz is None else qz.ctypes.data, sc.ctypes.data,
+                                         rows, cols, group)
+        else:
+            h = lib().sml_hip_gptq_upload(qw.ctypes.data, qz.ctypes.data, sc.ctypes.data, rows, cols, group,
+                                          zero_add)
         if not h:
             raise HipError(f"gptq upload: {lib().sml_hip_last_error().decode(errors='replace')}")
         self.h = h

@@ -337,3 +337,30 @@ def test_gptq_unpack_bitexact(rows, cols, zero_add):
             wc, wz = ob.gptq_unpack_row(qw, qz, rows, cols, r0 + i, zero_add=zero_add)
             np.testing.assert_array_equal(c[i], wc)
             np.testing.assert_array_equal(z[i], wz)
+
+
+@pytest.mark.parametrize("rows,cols,with_zeros", [(4096, 14336, True), (1000, 1152, False)])
+def test_awq_unpack_and_gemv(rows, cols, with_zeros):
+    """The AWQ layout (output-packed words, nibble order 0,4,1,5,2,6,3,7;
+    default zero 8 without qzeros), repacked at upload into the GPTQ device
+    layout: codes and zeros bit-exact with the oracle's AWQ reading, the
+    GEMV within 1e-3 of the oracle's dequantize-then-dot."""
+    from sheep_amd import gptq as gq
+    rng = np.random.default_rng(rows + cols)
+    ngr = cols // 128
+    qw = rng.integers(0, 1 << 32, (cols, rows // 8), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    qz = rng.integers(0, 1 << 32, (ngr, rows // 8), dtype=np.uint64).astype(np.uint32).view(np.int32) \
+        if with_zeros else None
+    sc = (np.abs(rng.standard_normal((ngr, rows))) * 0.02 / 7).astype(np.float16)
+    m = gq.GptqMat(qw, qz, sc, rows, cols, awq=True)
+    for r0, n in ((0, 8), (rows - 5, 5), (rows // 2, 3)):
+        c, z = m.unpack(r0, n)
+        for i in range(n):
+            wc, wz = ob.awq_unpack_row(qw, qz, rows, cols, r0 + i)
+            np.testing.assert_array_equal(c[i], wc)
+            np.testing.assert_array_equal(z[i], wz)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = sa.DevBuf(rows * 4)
+    m.matvec(sa.DevBuf.of(x), y)
+    W = np.stack([ob.awq_dequant_row(qw, qz, sc, rows, cols, r) for r in range(rows)]).astype(np.float64)
+    close(y.read(np.float32), (W @ x.astype(np.float64)).astype(np.float32), f"awq {rows}x{cols}")

@@ -402,3 +402,39 @@ def test_gptq_known_answer(zero_add):
     x = rng.standard_normal(IN).astype(np.float32)
     y = ob.gptq_matvec(qw, qz, sc, OUT, IN, x, group=GS, zero_add=zero_add)
     np.testing.assert_allclose(y, (want.astype(np.float64) @ x.astype(np.float64)).astype(np.float32), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("with_zeros", [True, False])
+def test_awq_known_answer(with_zeros):
+    """The AWQ half of mlmi/tests/test_unpack.py:74-103 restated: 64 inputs x
+    32 outputs, group 16, words packed along the output with the test's own
+    order (nibble i holds output (0, 2, 4, 6, 1, 3, 5, 7)[i] of its 8), zeros
+    stored as they are (without qzeros: 8). Reading them back gives
+    (q - z) * s exactly, and the repo's packer writes the same words."""
+    from sheep_amd import gptq as gq
+    rng = np.random.default_rng(1)
+    IN, OUT, GS = 64, 32, 16
+    q = rng.integers(0, 16, (IN, OUT)).astype(np.uint32)
+    z = rng.integers(1, 16, (IN // GS, OUT)).astype(np.uint32) if with_zeros else np.full((IN // GS, OUT), 8, np.uint32)
+    s = (rng.random((IN // GS, OUT)) + 0.1).astype(np.float16)
+    order = (0, 2, 4, 6, 1, 3, 5, 7)
+
+    def pack(x):                               # [r, OUT] -> [r, OUT/8]
+        x = x.reshape(x.shape[0], -1, 8)[:, :, list(order)]
+        return sum(x[:, :, i] << np.uint32(4 * i) for i in range(8)).astype(np.uint32).view(np.int32)
+
+    qw, qz = pack(q), (pack(z) if with_zeros else None)
+    sc = np.ascontiguousarray(s)
+    want = (q.astype(np.int64) - np.repeat(z, GS, axis=0)).astype(np.float32).T * \
+        np.repeat(s.astype(np.float32), GS, axis=0).T
+    for o in range(OUT):
+        c, zz = ob.awq_unpack_row(qw, qz, OUT, IN, o, group=GS)
+        np.testing.assert_array_equal(c, q[:, o])
+        np.testing.assert_array_equal(zz, z[:, o])
+        w = ob.awq_dequant_row(qw, qz, sc, OUT, IN, o, group=GS)
+        assert np.abs(w - want[o]).max() == 0.0
+    pw, pz, ps = gq.pack_awq(q.T, z.T if with_zeros else None, s.T)
+    np.testing.assert_array_equal(pw, qw)
+    if with_zeros:
+        np.testing.assert_array_equal(pz, qz)
+    np.testing.assert_array_equal(ps, sc)
