@@ -247,6 +247,7 @@ typedef struct {
     float * y;                    // [ngroups][mmax][rows]
     const float * bias;           // [rows] added to each row (plain GEMM only), or NULL
     const float * resid;          // [ngroups][mmax][rows]: y = resid + (W.a + bias), may alias y; or NULL
+    int mlo;                      // VALU kernel: groups of mlo rows or fewer are another launch's
 } sml_kgemm;
 
 // out[t] = sum over j of w[t][j] * y[sel[t][j]][slot[t][j]], in choice order.

@@ -1424,7 +1424,7 @@ __device__ void gemm_body(const sml_kgemm & a) {
     float2 * lsc = (float2 *) (lds + MT * TILE * 32);   // [MT][TILE]
     const int e = blockIdx.y;
     const int m = a.count ? a.count[e] : a.m_all;
-    if (m <= 0) return;
+    if (m <= a.mlo || m > MT) return;                   // another launch's groups (expert counts by size)
     const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8;
     const int tid = threadIdx.x, lane = tid & (WAVE - 1);
     constexpr int RPW = SW ? RB / 2 : RB;
