@@ -1575,9 +1575,16 @@ GEMM_WIDTH(2) GEMM_WIDTH(3) GEMM_WIDTH(4) GEMM_WIDTH(5) GEMM_WIDTH(6) GEMM_WIDTH
 // on the device: lane l holds A row / B column l%16, codes 8*(l/16)..+7, and
 // receives D rows 4*(l/16)..+3 of column l%16). So lane l owns weight row
 // l%16 of each of its RB blocks of 16 rows (SwiGLU: the gate and up blocks of
-// the same rows) and activation rows 4*(l/16)..+3. In the Q4 plane an 8-byte
-// word at quad q, half h, offset 8*(l/16) holds codes of groups 4q+2h (low
-// nibbles) and 4q+2h+1 (high nibbles), so one load feeds two MFMAs.
+// the same rows) and activation rows 4*(l/16)..+3.
+//
+// Operand loads are 16 bytes per lane, the four lanes of a row contiguous:
+// lane c (= l/16) reads bytes 16c..16c+15 of a 64-byte Q4 quad (columns
+// 16(c&1)..+15 of groups 4q, 4q+1 if c < 2, else of 4q+2, 4q+3) and bytes
+// 16c..16c+15 of an activation row's 64 bytes of 2 groups. One swap between
+// lanes l and l+32 (xslice) leaves each lane an 8-byte slice of every group
+// of the quad (pair): lane c holds columns 8*(0, 2, 1, 3)[c]..+7, the same
+// permutation of k for A and B, so each MFMA's dot is the group's dot. A quad
+// load feeds four MFMAs, an activation load two.
 //
 // Work goes by superblock (8 groups = 256 columns; input widths are
 // multiples of 256): one 16-byte load brings a weight row's 8 (sq, mq) field
@@ -1601,6 +1608,19 @@ GEMM_WIDTH(2) GEMM_WIDTH(3) GEMM_WIDTH(4) GEMM_WIDTH(5) GEMM_WIDTH(6) GEMM_WIDTH
 //    scale as [superblock][row].
 // The waves' partial sums meet in LDS, added in wave order. The float order
 // differs from the GEMV's, so rows agree with it to rounding, not bit for bit.
+// Two 16-byte loads' worth of k-slices, exchanged between lanes l and l+32
+// (v_permlane32_swap): a lane of the first half keeps its dwords 0-1 and
+// takes its partner's 0-1, a lane of the second half takes its partner's
+// dwords 2-3 and keeps its own 2-3. x and y are then the lane's 8-byte slice
+// of two different groups (see mgemm_q4_body). The two operands of each swap
+// are distinct registers.
+__device__ __forceinline__ void xslice(const v4u v, v2u & x, v2u & y) {
+    const auto p = __builtin_amdgcn_permlane32_swap((int) v[0], (int) v[2], false, false);
+    const auto q = __builtin_amdgcn_permlane32_swap((int) v[1], (int) v[3], false, false);
+    x = v2u{(unsigned) p[0], (unsigned) q[0]};
+    y = v2u{(unsigned) p[1], (unsigned) q[1]};
+}
+
 template <bool SW, bool SB, int RB, int NW>
 __device__ void mgemm_q4_body(const sml_kgemm & a) {
     typedef long v1l;
@@ -1634,16 +1654,16 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
     for (int bk = 0; bk < RB; bk++) {
         const int ra = rb0 + bk * 16 + i16;
         const uint32_t rc = (uint32_t) (ra < a.rows ? ra : a.rows - 1);
-        boff0[bk] = rc * rowb + 8u * (uint32_t) c;
+        boff0[bk] = rc * rowb + 16u * (uint32_t) c;
         fqo[bk] = rc * (uint32_t) ng * 2u;
         fdo[bk] = rc * (uint32_t) nsb * 4u;
     }
-    const int8_t * qrow = a.q + (abase + (size_t) (i16 < m ? i16 : 0)) * n + 8 * c;
+    const int8_t * qrow = a.q + (abase + (size_t) (i16 < m ? i16 : 0)) * n + 16 * c;
     struct Batch {
-        v2u w[4][NM][RB];         // the 4 group pairs' code words
+        v4u w[2][NM][RB];         // the superblock's 2 quads, 16 bytes per lane
         v4u fq[NM][RB];           // 8 (sq, mq) pairs
         uint32_t fd[NM][RB];      // (sd, md)
-        v1l aq[8];                // activation codes, 8 per group
+        v4u aq[4];                // activation codes, 16 bytes per lane per 2 groups
     };
     // one base address per stream and superblock, the rest immediate offsets
     auto load = [&](Batch & b, int bt) {
@@ -1654,13 +1674,36 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             for (int bk = 0; bk < RB; bk++) {
                 const uint8_t * wp = plane[k] + (boff0[bk] + (uint32_t) g0 * 16u);
                 #pragma unroll
-                for (int p = 0; p < 4; p++) b.w[p][k][bk] = *(const v2u *) (wp + (p >> 1) * 64 + (p & 1) * 32);
+                for (int p = 0; p < 2; p++) b.w[p][k][bk] = *(const v4u *) (wp + p * 64);
                 b.fq[k][bk] = *(const v4u *) (fqb[k] + (fqo[bk] + (uint32_t) g0 * 2u));
                 b.fd[k][bk] = *(const uint32_t *) (fdb[k] + (fdo[bk] + (uint32_t) bt * 4u));
             }
         const int8_t * qp = qrow + (size_t) g0 * 32;
         #pragma unroll
-        for (int j = 0; j < 8; j++) b.aq[j] = *(const v1l *) (qp + j * 32);
+        for (int u = 0; u < 4; u++) b.aq[u] = *(const v4u *) (qp + u * 64);
+    };
+    // the MFMA operands of one superblock: B of group j from quad j/4 (low
+    // nibbles of x, high of x, low of y, high of y), A of group j from the
+    // activation load j/2 (x, y)
+    auto operands = [&](const Batch & b, v2u (&wx)[2][NM][RB], v2u (&wy)[2][NM][RB], v1l (&av)[8]) {
+        #pragma unroll
+        for (int p = 0; p < 2; p++)
+            #pragma unroll
+            for (int k = 0; k < NM; k++)
+                #pragma unroll
+                for (int bk = 0; bk < RB; bk++) xslice(b.w[p][k][bk], wx[p][k][bk], wy[p][k][bk]);
+        #pragma unroll
+        for (int u = 0; u < 4; u++) {
+            v2u x, y;
+            xslice(b.aq[u], x, y);
+            av[2 * u] = (v1l) (((unsigned long) x.y << 32) | x.x);
+            av[2 * u + 1] = (v1l) (((unsigned long) y.y << 32) | y.x);
+        }
+    };
+    auto bcodes = [&](const v2u (&wx)[2][NM][RB], const v2u (&wy)[2][NM][RB], int j, int k, int bk) -> v1l {
+        const v2u w = (j & 2) ? wy[j >> 2][k][bk] : wx[j >> 2][k][bk];
+        const v2u cd = (j & 1) ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
+        return (v1l) (((unsigned long) cd.y << 32) | cd.x);
     };
     float acc[NM][RB][4];
     #pragma unroll
@@ -1679,6 +1722,9 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
                 for (int bk = 0; bk < RB; bk++)
                     #pragma unroll
                     for (int r = 0; r < 4; r++) { is[k][bk][r] = 0; im[k][bk][r] = 0; }
+            v2u wx[2][NM][RB], wy[2][NM][RB];
+            v1l av[8];
+            operands(b, wx, wy, av);
             #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int4 sm = *(const int4 *) &lsum[(gl0 + j) * 16 + 4 * c];
@@ -1687,11 +1733,9 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
                 for (int k = 0; k < NM; k++)
                     #pragma unroll
                     for (int bk = 0; bk < RB; bk++) {
-                        const v2u w = b.w[j >> 1][k][bk];
-                        const v2u cd = (j & 1) ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
-                        const v1l bv = (v1l) (((unsigned long) cd.y << 32) | cd.x);
+                        const v1l bv = bcodes(wx, wy, j, k, bk);
                         v4i d = { 0, 0, 0, 0 };
-                        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(b.aq[j], bv, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], bv, d, 0, 0, 0);
                         const uint32_t f = b.fq[k][bk][j >> 1] >> (16 * (j & 1));
                         const int sq = (int) (f & 0xFFu), mn = (int) ((f >> 8) & 0xFFu) - 127;
                         #pragma unroll
@@ -1715,6 +1759,9 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
                     }
                 }
         } else {
+            v2u wx[2][NM][RB], wy[2][NM][RB];
+            v1l av[8];
+            operands(b, wx, wy, av);
             #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const float4 s01 = *(const float4 *) &lsc[(gl0 + j) * 16 + 4 * c];
@@ -1724,11 +1771,9 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
                 for (int k = 0; k < NM; k++)
                     #pragma unroll
                     for (int bk = 0; bk < RB; bk++) {
-                        const v2u w = b.w[j >> 1][k][bk];
-                        const v2u cd = (j & 1) ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
-                        const v1l bv = (v1l) (((unsigned long) cd.y << 32) | cd.x);
+                        const v1l bv = bcodes(wx, wy, j, k, bk);
                         v4i d = { 0, 0, 0, 0 };
-                        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(b.aq[j], bv, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], bv, d, 0, 0, 0);
                         const uint32_t f = b.fq[k][bk][j >> 1] >> (16 * (j & 1)), d2 = b.fd[k][bk];
                         const float wsc = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
                         const float wmn = h2f((uint16_t) (d2 >> 16)) * ((float) ((f >> 8) & 0xFFu) - 127.0f);
