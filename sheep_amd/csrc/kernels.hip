@@ -1675,8 +1675,12 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
                 const uint8_t * wp = plane[k] + (boff0[bk] + (uint32_t) g0 * 16u);
                 #pragma unroll
                 for (int p = 0; p < 2; p++) b.w[p][k][bk] = *(const v4u *) (wp + p * 64);
-                b.fq[k][bk] = *(const v4u *) (fqb[k] + (fqo[bk] + (uint32_t) g0 * 2u));
-                b.fd[k][bk] = *(const uint32_t *) (fdb[k] + (fdo[bk] + (uint32_t) bt * 4u));
+                // a row's fields are the same for its 4 lanes: the first lane
+                // of each row loads them, the others take them by ds_bpermute
+                if (c == 0) {
+                    b.fq[k][bk] = *(const v4u *) (fqb[k] + (fqo[bk] + (uint32_t) g0 * 2u));
+                    b.fd[k][bk] = *(const uint32_t *) (fdb[k] + (fdo[bk] + (uint32_t) bt * 4u));
+                }
             }
         const int8_t * qp = qrow + (size_t) g0 * 32;
         #pragma unroll
@@ -1685,7 +1689,16 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
     // the MFMA operands of one superblock: B of group j from quad j/4 (low
     // nibbles of x, high of x, low of y, high of y), A of group j from the
     // activation load j/2 (x, y)
-    auto operands = [&](const Batch & b, v2u (&wx)[2][NM][RB], v2u (&wy)[2][NM][RB], v1l (&av)[8]) {
+    auto operands = [&](Batch & b, v2u (&wx)[2][NM][RB], v2u (&wy)[2][NM][RB], v1l (&av)[8]) {
+        #pragma unroll
+        for (int k = 0; k < NM; k++)
+            #pragma unroll
+            for (int bk = 0; bk < RB; bk++) {
+                #pragma unroll
+                for (int e = 0; e < 4; e++)
+                    b.fq[k][bk][e] = (unsigned) __builtin_amdgcn_ds_bpermute(i16 << 2, (int) b.fq[k][bk][e]);
+                b.fd[k][bk] = (unsigned) __builtin_amdgcn_ds_bpermute(i16 << 2, (int) b.fd[k][bk]);
+            }
         #pragma unroll
         for (int p = 0; p < 2; p++)
             #pragma unroll
@@ -1712,7 +1725,7 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
         for (int bk = 0; bk < RB; bk++)
             #pragma unroll
             for (int r = 0; r < 4; r++) acc[k][bk][r] = 0.0f;
-    auto compute = [&](const Batch & b, int bt) {
+    auto compute = [&](Batch & b, int bt) {
         const int gl0 = (bt - s0) * 8;
         if constexpr (SB) {
             int is[NM][RB][4], im[NM][RB][4];
