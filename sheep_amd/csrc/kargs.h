@@ -131,6 +131,10 @@ typedef struct {
     // positions of one sequence in one launch attend to each other), so the
     // attention kernel writes nothing
     int kv_written;
+    // entries per workgroup (grid z = nseq / tpw, rounded up): above 1 the
+    // entries are consecutive positions of one sequence (one slot, positions
+    // increasing) and share each split's K/V tile
+    int tpw, nseq;
 } sml_kattn;
 
 

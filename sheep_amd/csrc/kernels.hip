@@ -823,52 +823,82 @@ __device__ __forceinline__ void wave_heads(const float (&x)[REP], float (&out)[R
     }
 }
 
-template <int REP, int NW>
+template <int REP, int NW, bool CHUNK>
 __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     constexpr int NT = 64 * NW, PS = NT / 16, PPL = ATTN_CHUNK / PS;   // threads, position stride, positions per lane
     __shared__ float red[NW][REP][HD];
     __shared__ float wm[NW][REP], wl[NW][REP];
-    const int kh = blockIdx.y, split = blockIdx.x, b = blockIdx.z, tid = threadIdx.x;
+    const int kh = blockIdx.y, split = blockIdx.x, tid = threadIdx.x;
     const int wave = tid >> 6, grp = tid >> 4, l16 = tid & 15, kvd = a.n_kv * HD;
-    const float * aq = a.q + (size_t) b * a.qkv_stride + (size_t) kh * REP * HD + l16 * 8;
-    const float * ak = a.k + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
-    const float * av = a.v + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
-    float q[REP][8], kn[8], vn[8];
+    // the workgroup's entries b0..b1-1: one, or (tpw > 1) consecutive
+    // positions of one sequence, which share this split's K/V tile
+    const int tpw = CHUNK ? a.tpw : 1;
+    const int b0 = blockIdx.z * tpw, b1 = CHUNK ? min(b0 + tpw, a.nseq) : b0 + 1;
+    const int t0 = split * ATTN_CHUNK, tlast = a.pos[b1 - 1] + 1;
+    uint16_t * kcache = a.kc_slots ? a.kc_slots[a.slot[b0]] + a.layer_off : a.kcache;
+    uint16_t * vcache = a.vc_slots ? a.vc_slots[a.slot[b0]] + a.layer_off : a.vcache;
+    // the first entry's q, k and v load first: loads return in order
+    const int half = HD / 2;
+    float nq[REP][8], nk[8], nv[8], ncs[8], nsn[8];
+    auto fetch_qkv = [&](int b) {
+        const float * aq = a.q + (size_t) b * a.qkv_stride + (size_t) kh * REP * HD + l16 * 8;
+        const float * ak = a.k + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
+        const float * av = a.v + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
+        #pragma unroll
+        for (int j = 0; j < REP; j++) load_f8(aq + j * HD, nq[j]);
+        load_f8(ak, nk);
+        load_f8(av, nv);
+    };
+    auto fetch_rope = [&](int b) {
+        const int p = a.pos[b];
+        load_f8(a.cos_t + (size_t) p * half + (l16 & 7) * 8, ncs);
+        load_f8(a.sin_t + (size_t) p * half + (l16 & 7) * 8, nsn);
+    };
+    auto fetch = [&](int b) { fetch_qkv(b); fetch_rope(b); };
+    fetch_qkv(b0);
+    if (CHUNK) fetch_rope(b0);
+    // all of K, then all of V: loads return in order, so the scores and the
+    // softmax run while V is still arriving
+    v4u kw[PPL], vw[PPL];
+    if (t0 < tlast) {
+        const int tl = min(tlast, t0 + ATTN_CHUNK);
+        #pragma unroll
+        for (int i = 0; i < PPL; i++) {
+            int t = t0 + grp + PS * i;
+            t = t < tl ? t : t0;                      // in range; masked below
+            kw[i] = __builtin_nontemporal_load((const v4u *) (kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
+        }
+        #pragma unroll
+        for (int i = 0; i < PPL; i++) {
+            int t = t0 + grp + PS * i;
+            t = t < tl ? t : t0;
+            vw[i] = __builtin_nontemporal_load((const v4u *) (vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
+        }
+    }
+    if (!CHUNK) fetch_rope(b0);                       // one entry: its RoPE rows after the tile
+    // each entry's arithmetic is the one-entry kernel's, position for position;
+    // with few heads the next entry's inputs load while this one computes
+    constexpr bool PF = CHUNK && REP <= 4;
+    for (int b = b0; b < b1; b++) {
+    if (!PF && b > b0) fetch(b);
+    float q[REP][8], kn[8], vn[8], cs[8], sn[8];
     #pragma unroll
-    for (int j = 0; j < REP; j++) load_f8(aq + j * HD, q[j]);
-    load_f8(ak, kn);
-    load_f8(av, vn);
-    const int pos = a.pos[b], T = pos + 1, t0 = split * ATTN_CHUNK;
-    // partials of sequence b: V sums [head][split][HD], then (max, sum) [head][split]
+    for (int e = 0; e < 8; e++) {
+        #pragma unroll
+        for (int j = 0; j < REP; j++) q[j][e] = nq[j][e];
+        kn[e] = nk[e]; vn[e] = nv[e]; cs[e] = ncs[e]; sn[e] = nsn[e];
+    }
+    if (PF && b + 1 < b1) fetch(b + 1);
+    const int pos = a.pos[b], T = pos + 1;
+    // partials of entry b: V sums [head][split][HD], then (max, sum) [head][split]
     float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
     float * po = blk + (size_t) kh * REP * a.nsplit * HD;
     float2 * pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) kh * REP * a.nsplit;
     if (t0 >= T) {
         if (tid < REP) pml[(size_t) tid * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
-        return;
+        continue;
     }
     const int t1 = min(T, t0 + ATTN_CHUNK);
-    uint16_t * kcache = a.kc_slots ? a.kc_slots[a.slot[b]] + a.layer_off : a.kcache;
-    uint16_t * vcache = a.vc_slots ? a.vc_slots[a.slot[b]] + a.layer_off : a.vcache;
-    // all of K, then all of V: loads return in order, so the scores and the
-    // softmax run while V is still arriving
-    v4u kw[PPL], vw[PPL];
-    #pragma unroll
-    for (int i = 0; i < PPL; i++) {
-        int t = t0 + grp + PS * i;
-        t = t < t1 ? t : t0;                          // in range; masked below
-        kw[i] = __builtin_nontemporal_load((const v4u *) (kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
-    }
-    #pragma unroll
-    for (int i = 0; i < PPL; i++) {
-        int t = t0 + grp + PS * i;
-        t = t < t1 ? t : t0;
-        vw[i] = __builtin_nontemporal_load((const v4u *) (vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
-    }
-    const int half = HD / 2;
-    float cs[8], sn[8];
-    load_f8(a.cos_t + (size_t) pos * half + (l16 & 7) * 8, cs);
-    load_f8(a.sin_t + (size_t) pos * half + (l16 & 7) * 8, sn);
     const bool lo = l16 < 8;
     const float sl = a.inv * 1.44269504088896341f;
     #pragma unroll
@@ -971,6 +1001,8 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         po[((size_t) j * a.nsplit + split) * HD + d] = o;
         if (d == 0) pml[(size_t) j * a.nsplit + split] = make_float2(M, L);
     }
+    if (b + 1 < b1) __syncthreads();                  // red, wm and wl are the next entry's
+    }
 }
 
 // RoPE of k at each sequence's position and the fp16 write of k and v into
@@ -1004,8 +1036,9 @@ extern "C" __global__ __launch_bounds__(128) void sml_ropekv(const sml_kattn a) 
 }
 
 #define ATTN_KERNEL(R) \
-    extern "C" __global__ __launch_bounds__(256) void sml_attn_r##R(const sml_kattn a) { attn_body<R, 4>(a); } \
-    extern "C" __global__ __launch_bounds__(512) void sml_attn8_r##R(const sml_kattn a) { attn_body<R, 8>(a); }
+    extern "C" __global__ __launch_bounds__(256) void sml_attn_r##R(const sml_kattn a) { attn_body<R, 4, false>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attn8_r##R(const sml_kattn a) { attn_body<R, 8, false>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attnc8_r##R(const sml_kattn a) { attn_body<R, 8, true>(a); }
 ATTN_KERNEL(1) ATTN_KERNEL(2) ATTN_KERNEL(3) ATTN_KERNEL(4) ATTN_KERNEL(5) ATTN_KERNEL(6) ATTN_KERNEL(7) ATTN_KERNEL(8)
 
 // Merge of the splits of one query head (grid: n_head workgroups of HD

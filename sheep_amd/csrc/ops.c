@@ -523,9 +523,17 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     }
     char name[32];
     const int aw = env_int("SML_ATTN_WAVES", 8) == 4 ? 4 : 8;
-    if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
+    // causal entries (positions of one sequence) share each split's K/V tile
+    // in groups of tpw per workgroup (sml_attnc8); the arithmetic per entry is
+    // the one-entry kernel's
+    a.nseq = nseq;
+    a.tpw = causal ? env_int("SML_ATTN_TPW", 16) : 1;
+    if (a.tpw < 1 || a.tpw > 16) a.tpw = 1;
+    if (a.tpw > 1) snprintf(name, sizeof name, "sml_attnc8_r%d", n_head / n_kv);
+    else if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
     else snprintf(name, sizeof name, "sml_attn%d_r%d", aw, n_head / n_kv);
-    hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) nseq, (unsigned) (64 * aw), 0, st, &a);
+    hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) ((nseq + a.tpw - 1) / a.tpw), (unsigned) (64 * aw), 0,
+               st, &a);
     hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
 }
 
