@@ -727,7 +727,8 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
         const int fuse_q = y->perm_o < 0 && !sb;         // the merge quantizes per 32
         op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
                            G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.mpart, G.matt,
-                           fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL, causal);
+                           fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL,
+                           causal ? (regime == GEMM_EXACT ? 1 : 2) : 0);
         if (!fuse_q) {
             pp[0] = pdev(y->perm_o);
             op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, sb);

@@ -1041,6 +1041,144 @@ extern "C" __global__ __launch_bounds__(128) void sml_ropekv(const sml_kattn a) 
     extern "C" __global__ __launch_bounds__(512) void sml_attnc8_r##R(const sml_kattn a) { attn_body<R, 8, true>(a); }
 ATTN_KERNEL(1) ATTN_KERNEL(2) ATTN_KERNEL(3) ATTN_KERNEL(4) ATTN_KERNEL(5) ATTN_KERNEL(6) ATTN_KERNEL(7) ATTN_KERNEL(8)
 
+// ---------------------------------------------------------------- prompt attention, a wave per position
+//
+// For prompt reading with the matrix-core products (level 2): a workgroup
+// (split, kv head, up to 16 consecutive positions of one sequence) stages the
+// split's K and V tile in LDS once; each of its 8 waves then takes whole
+// positions (w, w + 8): the position's rotated q heads into LDS (the decode
+// kernel's rope8, so the same rotated q), scores with a lane per tile
+// position (two per lane), the base-2 softmax over the wave, and P.V with a
+// lane per head dimension (two per lane). Past the staging no barrier is
+// needed. It writes sml_attn's partials, so sml_attn_merge finishes the
+// job; fp32 throughout, in its own summation order.
+#define ATTNW_WAVES 8
+#define ATTNW_ENTRIES 16
+#define KROW (HD + 8)       // halves per K row in LDS: 16 bytes of padding, no bank conflicts
+
+template <int REP>
+__device__ __forceinline__ void attnw_body(const sml_kattn & a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint16_t * lk = (uint16_t *) lds;                                   // [ATTN_CHUNK][KROW]
+    uint16_t * lv = lk + ATTN_CHUNK * KROW;                              // [ATTN_CHUNK][HD]
+    float * lq = (float *) (lv + ATTN_CHUNK * HD);                       // [waves][REP][HD]
+    float * lp = lq + ATTNW_WAVES * REP * HD;                            // [waves][ATTN_CHUNK][REP]
+    const int kh = blockIdx.y, split = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvd = a.n_kv * HD, half = HD / 2;
+    const int b0 = blockIdx.z * ATTNW_ENTRIES, b1 = min(b0 + ATTNW_ENTRIES, a.nseq);
+    const int t0 = split * ATTN_CHUNK, tlast = a.pos[b1 - 1] + 1;
+    auto partials = [&](int b, float * & po, float2 * & pml) {
+        float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
+        po = blk + (size_t) kh * REP * a.nsplit * HD;
+        pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) kh * REP * a.nsplit;
+    };
+    if (t0 >= tlast) {                                // no entry reaches this split
+        for (int idx = tid; idx < (b1 - b0) * REP; idx += ATTNW_WAVES * 64) {
+            float * po;
+            float2 * pml;
+            partials(b0 + idx / REP, po, pml);
+            pml[(size_t) (idx % REP) * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
+        }
+        return;
+    }
+    const int tl = min(tlast, t0 + ATTN_CHUNK);
+    const uint16_t * kcache = a.kc_slots ? a.kc_slots[a.slot[b0]] + a.layer_off : a.kcache;
+    const uint16_t * vcache = a.vc_slots ? a.vc_slots[a.slot[b0]] + a.layer_off : a.vcache;
+    // the tile: 16 16-byte words per row; rows past the last entry's position
+    // repeat row t0 (finite, never weighted)
+    for (int i = tid; i < ATTN_CHUNK * 16; i += ATTNW_WAVES * 64) {
+        const int r = i >> 4, c = i & 15;
+        const int t = t0 + r < tl ? t0 + r : t0;
+        const size_t off = (size_t) t * kvd + (size_t) kh * HD + c * 8;
+        *(v4u *) (lk + r * KROW + c * 8) = __builtin_nontemporal_load((const v4u *) (kcache + off));
+        *(v4u *) (lv + r * HD + c * 8) = __builtin_nontemporal_load((const v4u *) (vcache + off));
+    }
+    __syncthreads();
+    float * qw = lq + wave * REP * HD;
+    float * pw = lp + wave * ATTN_CHUNK * REP;
+    const int l16 = lane & 15, row = lane >> 4;
+    const float sl = a.inv * 1.44269504088896341f;
+    for (int b = b0 + wave; b < b1; b += ATTNW_WAVES) {
+        const int pos = a.pos[b], T = pos + 1;
+        float * po;
+        float2 * pml;
+        partials(b, po, pml);
+        if (t0 >= T) {
+            if (lane < REP) pml[(size_t) lane * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
+            continue;
+        }
+        const int n = min(T, t0 + ATTN_CHUNK) - t0;   // this entry's positions in the tile
+        // rotated q: a 16-lane row per head, 8 dims per lane, as sml_attn does
+        float cs[8], sn[8];
+        load_f8(a.cos_t + (size_t) pos * half + (l16 & 7) * 8, cs);
+        load_f8(a.sin_t + (size_t) pos * half + (l16 & 7) * 8, sn);
+        #pragma unroll
+        for (int j0 = 0; j0 < REP; j0 += 4) {
+            const int j = j0 + row;
+            float q[8];
+            load_f8(a.q + (size_t) b * a.qkv_stride + (size_t) (kh * REP + (j < REP ? j : 0)) * HD + l16 * 8, q);
+            rope8(q, cs, sn, l16 < 8);
+            if (j < REP) {
+                *(float4 *) (qw + j * HD + l16 * 8) = make_float4(q[0], q[1], q[2], q[3]);
+                *(float4 *) (qw + j * HD + l16 * 8 + 4) = make_float4(q[4], q[5], q[6], q[7]);
+            }
+        }
+        // scores of tile positions lane and lane + 64
+        float s0[REP], s1[REP];
+        #pragma unroll
+        for (int j = 0; j < REP; j++) { s0[j] = 0.0f; s1[j] = 0.0f; }
+        #pragma unroll 4
+        for (int c = 0; c < HD / 8; c++) {
+            float k0[8], k1[8];
+            unpack_h8(*(const v4u *) (lk + lane * KROW + c * 8), k0);
+            unpack_h8(*(const v4u *) (lk + (lane + 64) * KROW + c * 8), k1);
+            #pragma unroll
+            for (int j = 0; j < REP; j++) {
+                float qv[8];
+                load_f8(qw + j * HD + c * 8, qv);
+                #pragma unroll
+                for (int e = 0; e < 8; e++) { s0[j] += qv[e] * k0[e]; s1[j] += qv[e] * k1[e]; }
+            }
+        }
+        // base-2 softmax per head over the wave (position t0 is valid: lane 0)
+        float mj[REP], lj[REP];
+        #pragma unroll
+        for (int j = 0; j < REP; j++) {
+            const float x0 = lane < n ? s0[j] * sl : -INFINITY;
+            const float x1 = lane + 64 < n ? s1[j] * sl : -INFINITY;
+            const float m = wave_max(fmaxf(x0, x1));
+            const float p0 = __builtin_amdgcn_exp2f(x0 - m), p1 = __builtin_amdgcn_exp2f(x1 - m);
+            mj[j] = m;
+            lj[j] = wave_sum(p0 + p1);
+            pw[lane * REP + j] = p0;
+            pw[(lane + 64) * REP + j] = p1;
+        }
+        // P.V for dims 2 lane, 2 lane + 1
+        float o0[REP], o1[REP];
+        #pragma unroll
+        for (int j = 0; j < REP; j++) { o0[j] = 0.0f; o1[j] = 0.0f; }
+        for (int t = 0; t < n; t++) {
+            const uint32_t vv = *(const uint32_t *) (lv + t * HD + 2 * lane);
+            const float v0 = h2f((uint16_t) (vv & 0xFFFFu)), v1 = h2f((uint16_t) (vv >> 16));
+            #pragma unroll
+            for (int j = 0; j < REP; j++) {
+                const float pj = pw[t * REP + j];
+                o0[j] += pj * v0;
+                o1[j] += pj * v1;
+            }
+        }
+        #pragma unroll
+        for (int j = 0; j < REP; j++) {
+            *(float2 *) (po + ((size_t) j * a.nsplit + split) * HD + 2 * lane) = make_float2(o0[j], o1[j]);
+            if (lane == 0) pml[(size_t) j * a.nsplit + split] = make_float2(mj[j], lj[j]);
+        }
+    }
+}
+
+#define ATTNW_KERNEL(R) \
+    extern "C" __global__ __launch_bounds__(64 * ATTNW_WAVES) void sml_attnw_r##R(const sml_kattn a) { attnw_body<R>(a); }
+ATTNW_KERNEL(1) ATTNW_KERNEL(2) ATTNW_KERNEL(3) ATTNW_KERNEL(4) ATTNW_KERNEL(5) ATTNW_KERNEL(6) ATTNW_KERNEL(7) ATTNW_KERNEL(8)
+
 // Merge of the splits of one query head (grid: n_head workgroups of HD
 // threads): out = sum_s e_s o_s / sum_s e_s l_s with e_s = 2^(m_s - max m)
 // (the split maxima are in base 2). Every split has a partial (max -inf for

@@ -516,7 +516,7 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     a.part = part; a.out = out; a.q_out = q_out; a.s_out = s_out; a.u_out = u_out;
     a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
-    a.kv_written = causal;
+    a.kv_written = causal != 0;
     if (causal) {
         if (n_kv > 8) hx_failf("causal attention takes at most 8 kv heads");
         hx_launch("sml_ropekv", (unsigned) nseq, 1, (unsigned) (16 * n_kv), 0, st, &a);
@@ -529,6 +529,16 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     a.nseq = nseq;
     a.tpw = causal ? env_int("SML_ATTN_TPW", 16) : 1;
     if (a.tpw < 1 || a.tpw > 16) a.tpw = 1;
+    if (causal == 2) {
+        // a wave per position over an LDS tile (16 positions per workgroup)
+        const int rep = n_head / n_kv;
+        const size_t lds = (size_t) ATTN_CHUNK * (128 + 8) * 2 + (size_t) ATTN_CHUNK * 128 * 2 +
+                           2 * (size_t) 8 * rep * 128 * 4;
+        snprintf(name, sizeof name, "sml_attnw_r%d", rep);
+        hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) ((nseq + 15) / 16), 512, lds, st, &a);
+        hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
+        return;
+    }
     if (a.tpw > 1) snprintf(name, sizeof name, "sml_attnc8_r%d", n_head / n_kv);
     else if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
     else snprintf(name, sizeof name, "sml_attn%d_r%d", aw, n_head / n_kv);

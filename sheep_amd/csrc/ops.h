@@ -80,7 +80,9 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
 // layer_off, its position pos[b]; part, out and the quantized out hold one
 // sequence's worth per b. causal: entries may be positions of one sequence
 // (prompt reading), so every k and v is rotated and written by one launch
-// before any entry attends.
+// before any entry attends; 1 keeps the decode kernel's arithmetic per entry
+// (bit-exact with stepping), 2 runs the wave-per-position kernel (faster,
+// its own fp32 order).
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
