@@ -180,6 +180,50 @@ def test_batched_prompt_equals_stepping(model, request):
             assert int(np.argmax(outs[2][i])) == int(np.argmax(ref)), f"level 2, part {i}"
 
 
+@pytest.mark.parametrize("n", [16, 17, 33, 64])
+def test_batched_prompt_fills_context(tiny, n):
+    """Prompts that end exactly at n_ctx (the last position's K/V row is the
+    cache's last), with whole and ragged chunks: level 1 equals stepping bit
+    for bit, level 2 within float rounding; a prompt past n_ctx is refused."""
+    ids = np.random.default_rng(n).integers(0, 2000, n).astype(np.int32)
+    outs = {}
+    for level in (0, 1, 2):
+        d = sa.Decoder(tiny, n_ctx=n)
+        try:
+            d.prompt_mode(level)
+            outs[level] = d.prefill(ids, 0, 2000)
+            assert not sa.lib().sml_gpu_prefill(ids.ctypes.data_as(sa.P(sa.c_int)), 1, n)
+        finally:
+            d.close()
+    np.testing.assert_array_equal(outs[1], outs[0])
+    assert np.corrcoef(outs[2], outs[0])[0, 1] > 0.9999
+
+
+def test_batched_prompt_into_other_slots(tiny):
+    """sml_gpu_prefill_slot batched into slots 1 and 2 (levels 1 and 2) leaves
+    each slot's cache as reading the prompt a token at a time does: the
+    following multi-sequence step equals the one after stepped prompts, bit
+    for bit."""
+    prompts = [np.random.default_rng(s).integers(0, 2000, 21 + s).astype(np.int32) for s in range(3)]
+    res = {}
+    for level in (0, 1, 2):
+        d = sa.Decoder(tiny, n_ctx=64)
+        try:
+            d.prompt_mode(level)
+            d.slots(3)
+            last = [d.prefill_slot(b, p, 0, 2000) for b, p in enumerate(prompts)]
+            toks = [int(np.argmax(l)) for l in last]
+            pos = [len(p) for p in prompts]
+            steps = [d.step_multi(toks, pos, [0, 1, 2], 2000)]
+            res[level] = (last, steps)
+        finally:
+            d.close()
+    for b in range(3):
+        np.testing.assert_array_equal(res[1][0][b], res[0][0][b], err_msg=f"slot {b} prompt logits")
+        np.testing.assert_array_equal(res[1][1][0][b], res[0][1][0][b], err_msg=f"slot {b} step")
+        assert np.corrcoef(res[2][0][b], res[0][0][b])[0, 1] > 0.9999
+
+
 def test_greedy_tokens_qwen_layers(qwenish):
     n = 24
     toks, logits = greedy_oracle(qwenish, 100, n, 128)
