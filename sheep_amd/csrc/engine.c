@@ -64,6 +64,7 @@ static struct {
     int32_t * pin;             // pinned: [0] tok, [1] pos, [2..] prompt ids
     hipStream_t st;
     hipGraphExec_t g_body, g_tail, g_adv;
+    hipGraphExec_t g_multi[17][2];   // the batched step per sequence count and regime (per-256)
     int use_graph;
     hipEvent_t e0, e1;
     float last_ms;
@@ -278,6 +279,8 @@ static void release(void) {
         if (G.g_body) hipGraphExecDestroy(G.g_body);
         if (G.g_tail) hipGraphExecDestroy(G.g_tail);
         if (G.g_adv) hipGraphExecDestroy(G.g_adv);
+        for (int i = 0; i < 17; i++)
+            for (int j = 0; j < 2; j++) if (G.g_multi[i][j]) hipGraphExecDestroy(G.g_multi[i][j]);
         for (int i = 0; i < G.nmats; i++) { if (G.mats[i]->mem) hipFree(G.mats[i]->mem); free(G.mats[i]); }
         if (G.L) for (int L = 0; L < G.n_layer; L++) if (G.L[L].moe) { moe_free(G.L[L].moe); G.L[L].moe = NULL; }
         for (int i = 0; i < G.ndev; i++) hipFree(G.dev[i]);
@@ -728,7 +731,7 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
         op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
                            G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.mpart, G.matt,
                            fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL,
-                           causal ? (regime == GEMM_EXACT ? 1 : 2) : 0);
+                           causal ? (regime == GEMM_EXACT ? 1 : 2) : 0, gemm_exact(regime, ns));
         if (!fuse_q) {
             pp[0] = pdev(y->perm_o);
             op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, sb);
@@ -814,8 +817,23 @@ const float * sml_gpu_prefill_slot(int slot, const int * ids, int pos0, int n) {
     return G.lg_host;
 }
 
+static int g_multi_ns, g_multi_sb;
+
+static void launch_multi_cur(void) {
+    launch_rows(g_multi_ns, G.mtok, G.mpos, G.mslot, g_multi_sb ? GEMM_PER256 : GEMM_PER32, 0, 1);
+}
+
+// The batched step reads its tokens, positions and slots from device arrays,
+// so one captured graph per (sequence count, regime) serves every step: the
+// ~300 launches of a step are replayed, not issued from the host. The
+// regime and the environment switches are read when a graph is captured.
 static void launch_multi(int ns) {
-    launch_rows(ns, G.mtok, G.mpos, G.mslot, multi_per256(ns) ? GEMM_PER256 : GEMM_PER32, 0, 1);
+    g_multi_ns = ns;
+    g_multi_sb = multi_per256(ns);
+    if (!G.use_graph) { launch_multi_cur(); return; }
+    hipGraphExec_t * g = &G.g_multi[ns][g_multi_sb];
+    if (!*g) *g = capture(launch_multi_cur);
+    HX(hipGraphLaunch(*g, G.st));
 }
 
 int sml_gpu_step_multi(const int * tok, const int * pos, const int * slot, int ns, float * logits_out) {

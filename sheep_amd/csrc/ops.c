@@ -503,7 +503,8 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
-                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal) {
+                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal,
+                        int exact) {
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
     if (nseq < 1 || nseq > 65535) hx_failf("attention batch of %d", nseq);
@@ -522,7 +523,11 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
         hx_launch("sml_ropekv", (unsigned) nseq, 1, (unsigned) (16 * n_kv), 0, st, &a);
     }
     char name[32];
-    const int aw = env_int("SML_ATTN_WAVES", 8) == 4 ? 4 : 8;
+    // many sequences give many workgroups: 4-wave ones, two per CU, then
+    // measured faster (16 sequences at ~1k positions: 5.6 against 6.8 ms per
+    // step); one sequence, and any step that must equal decoding alone bit
+    // for bit (exact), keeps the decode kernel's 8 waves per split
+    const int aw = env_int("SML_ATTN_WAVES", nseq >= 4 && !exact ? 4 : 8) == 4 ? 4 : 8;
     // causal entries (positions of one sequence) share each split's K/V tile
     // in groups of tpw per workgroup (sml_attnc8); the arithmetic per entry is
     // the one-entry kernel's
@@ -774,6 +779,13 @@ int sml_hip_gptq_time(const sml_hip_gptq * const * mats, int ncopy, const float 
 // ------------------------------------------------------------ small-M GEMM
 
 int gemm_mt(int m) { return m <= 1 ? 1 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
+
+int gemm_exact(int regime, int m_all) {
+    if (regime == GEMM_EXACT) return 1;
+    if (regime == GEMM_PER256) return 0;
+    const char * mode = getenv("SML_MULTI");
+    return m_all <= 8 || (mode && !strcmp(mode, "exact")) || !env_int("SML_MGEMM", 1);
+}
 
 #define GEMM_TILE 128            // chunks (groups) per pass: 64 lanes x GEMM_NI
 

@@ -86,7 +86,11 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
-                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal);
+                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal,
+                        int exact);
+// Whether op_gemm computes every row with the GEMV's arithmetic in this regime
+// for m_all rows (the exact regime, or per-32 rows the VALU kernel takes).
+int gemm_exact(int regime, int m_all);
 void op_argmax(hipStream_t st, const float * logits, int n, int32_t * tok, int32_t * pos, int32_t * hist,
                int hist_n);
 void op_advance(hipStream_t st, int32_t * pos);

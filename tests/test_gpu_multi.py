@@ -180,6 +180,40 @@ def test_step_multi_greedy_tokens_match_oracle(tmp_path, monkeypatch):
             om.close()
 
 
+@pytest.mark.parametrize("ns", [2, 4])
+def test_step_multi_graph_replays_equal_direct(tmp_path, ns, monkeypatch):
+    """The batched step replays one captured HIP graph per (sequence count,
+    regime). Six steps in a row, with host work and a synchronization
+    between the replays, give every step's logits bit for bit as launching
+    each kernel directly (SML_GRAPH=0)."""
+    monkeypatch.delenv("SML_MULTI", raising=False)
+    monkeypatch.delenv("SML_MULTI_EXACT_MAX", raising=False)
+    p = tmp_path / "graph.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, qkv_bias=True,
+                   random_perm=True, seed=75, n_expert=8, n_expert_used=2, moe_flags=1)
+    outs = {}
+    for graph in ("0", "1"):
+        monkeypatch.setenv("SML_GRAPH", graph)
+        d = sa.Decoder(p, n_ctx=64)
+        try:
+            d.slots(ns)
+            last = [d.prefill_slot(b, PROMPTS[b], 0, 2000) for b in range(ns)]
+            toks = [int(np.argmax(l)) for l in last]
+            pos = [len(PROMPTS[b]) for b in range(ns)]
+            res = []
+            for _ in range(6):
+                lg = d.step_multi(toks, pos, list(range(ns)), 2000)
+                res.append(lg)
+                sa.sync()
+                toks = [int(np.argmax(l)) for l in lg]
+                pos = [q + 1 for q in pos]
+            outs[graph] = res
+        finally:
+            d.close()
+    for i in range(6):
+        np.testing.assert_array_equal(outs["1"][i], outs["0"][i], err_msg=f"step {i}")
+
+
 def test_step_multi_rejects_bad_arguments(tmp_path):
     p = tmp_path / "multi_bad.ssf"
     sa.synth_model(p, n_layer=1, n_embd=256, n_head=2, n_head_kv=1, n_ff=512, n_vocab=300, seed=72)
