@@ -71,6 +71,27 @@ def gemv_roofline(rows, cols, iters=400, target_bytes=1.2e9, tmp=None):
     return float(np.median(trials)), first.bytes
 
 
+def read_ceiling(nbytes, iters=360, target_bytes=1.2e9, grid=2048):
+    """What one streaming-read launch of nbytes takes from HBM: 16-byte
+    nontemporal loads, grid-stride over `grid` 256-thread workgroups, over
+    rotating buffers (> the 256 MB MALL), HIP events on the launch stream.
+    The ceiling a single GEMV launch of that many bytes can approach."""
+    nb = nbytes // 16 * 16
+    nbuf = max(2, int(target_bytes // nb) + 1)
+    bufs = [sa.DevBuf(nb) for _ in range(nbuf)]
+    arr = (sa.c_void_p * nbuf)(*[b.ptr for b in bufs])
+    ms = sa.c_float()
+    lib = sa.lib()
+    assert lib.sml_hip_time_read(arr, nbuf, nb, grid, 2 * nbuf, sa.ctypes.byref(ms)) == 0
+    trials = []
+    for _ in range(5):
+        assert lib.sml_hip_time_read(arr, nbuf, nb, grid, iters, sa.ctypes.byref(ms)) == 0
+        trials.append(ms.value * 1000.0 / iters)
+    for b in bufs:
+        b.free()
+    return float(np.median(trials))
+
+
 COPY_BYTES = 256 << 20
 PROBE_LAUNCHES = 12
 
@@ -413,6 +434,11 @@ def run(a, work):
     roof = {"bound": "hbm", "kernel": "sml_gemv_q4 (4096 rows x 14336 cols, Q4)",
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None, "avg_us": round(g_us, 3), "bytes_per_launch": g_bytes}
+    r_us = read_ceiling(g_bytes)
+    roof["read_ceiling"] = {"us": round(r_us, 3), "GB/s": round(g_bytes / r_us / 1e3, 1),
+                            "frac": round(g_bytes / r_us / 1e3 / HBM_PEAK_GBS, 4),
+                            "gemv_over_read": round(r_us / g_us, 4)}
+    log(f"streaming read of the same {g_bytes} bytes: {r_us:.2f} us; the GEMV runs at {r_us / g_us:.1%} of it")
     if not a.no_traffic:
         t1 = time.perf_counter()
         tb, detail = traffic(os.path.join(work, "gemv_4096x14336.ssf"), work)

@@ -60,6 +60,7 @@ static struct {
     int fuse;                  // SML_FUSE bits: 1 activation prologues, 2 h quantization (default 3)
     uint16_t * kc, * vc;
     int32_t * hist, * pos, * tok;
+    int2 * amax_part;          // pairs of the two-stage greedy pick
     float * lg_host;
     int32_t * pin;             // pinned: [0] tok, [1] pos, [2..] prompt ids
     hipStream_t st;
@@ -247,7 +248,7 @@ static void launch_tail(void) {
     int slot[1];
     prep(G.x, G.out_norm, NULL, G.E, &G.perm_head, 1, slot);
     gemv1(G.head, slot[0], SML_EPI_STORE, G.logits, NULL, NULL);
-    op_argmax(G.st, G.logits, G.V, G.tok, G.pos, G.hist, G.n_ctx + 1);
+    op_argmax(G.st, G.logits, G.V, G.tok, G.pos, G.hist, G.n_ctx + 1, G.amax_part);
 }
 
 static void launch_adv(void) { op_advance(G.st, G.pos); }
@@ -469,6 +470,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     G.hist = dalloc((size_t) (n_ctx + 1) * 4);
     HX(hipMemset(G.hist, 0, (size_t) (n_ctx + 1) * 4));
     G.pos = dalloc(64);
+    G.amax_part = dalloc((size_t) ARGMAX_MAX_PARTS * sizeof(int2));
     G.tok = dalloc(64);
     HX(hipMemset(G.pos, 0, 64));
     HX(hipHostMalloc((void **) &G.lg_host, (size_t) G.V * 4, 0));

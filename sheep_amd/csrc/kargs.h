@@ -145,6 +145,11 @@ typedef struct {
     int32_t * pos;                // when non-NULL: hist[*pos + 1] = argmax (if inside), then *pos += 1
     int32_t * hist;
     int hist_n;
+    // two-stage pick: sml_argmax_part writes one (max, index) pair per
+    // workgroup into part; sml_argmax then reduces nparts pairs (part NULL:
+    // sml_argmax scans the logits itself)
+    int2 * part;
+    int nparts;
 } sml_kargmax;
 
 typedef struct {

@@ -1237,14 +1237,53 @@ extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn 
 __device__ __forceinline__ void amax_take(float v, int i, float & bv, int & bi) {
     if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
 }
+// First stage of the two-stage pick: grid-stride over float4 words, one
+// (max, lowest index) pair per workgroup. The first-max rule is kept by
+// amax_take when the pairs are combined.
+#define ARGMAX_PART_THREADS 256
+extern "C" __global__ __launch_bounds__(ARGMAX_PART_THREADS) void sml_argmax_part(const sml_kargmax a) {
+    __shared__ float bv_s[ARGMAX_PART_THREADS / 64];
+    __shared__ int bi_s[ARGMAX_PART_THREADS / 64];
+    const int tid = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    const bool al = ((uintptr_t) a.logits & 15) == 0;
+    const int n4 = al ? a.n / 4 : 0;
+    const int stride = gridDim.x * ARGMAX_PART_THREADS;
+    const float4 * l4 = (const float4 *) a.logits;
+    for (int f = blockIdx.x * ARGMAX_PART_THREADS + tid; f < n4; f += stride) {
+        const float4 v = l4[f];
+        amax_take(v.x, 4 * f, bv, bi); amax_take(v.y, 4 * f + 1, bv, bi);
+        amax_take(v.z, 4 * f + 2, bv, bi); amax_take(v.w, 4 * f + 3, bv, bi);
+    }
+    for (int i = 4 * n4 + blockIdx.x * ARGMAX_PART_THREADS + tid; i < a.n; i += stride) amax_take(a.logits[i], i, bv, bi);
+    #pragma unroll
+    for (int o = 32; o; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        amax_take(ov, oi, bv, bi);
+    }
+    if ((tid & 63) == 0) { bv_s[tid >> 6] = bv; bi_s[tid >> 6] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < ARGMAX_PART_THREADS / 64; w++) amax_take(bv_s[w], bi_s[w], bv_s[0], bi_s[0]);
+        a.part[blockIdx.x] = make_int2(__float_as_int(bv_s[0]), bi_s[0]);
+    }
+}
+
 extern "C" __global__ __launch_bounds__(ARGMAX_THREADS) void sml_argmax(const sml_kargmax a) {
     __shared__ float bv_s[ARGMAX_THREADS / 64];
     __shared__ int bi_s[ARGMAX_THREADS / 64];
     const int tid = threadIdx.x;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
+    if (a.part)
+        for (int i = tid; i < a.nparts; i += ARGMAX_THREADS) {
+            const int2 p = a.part[i];
+            amax_take(__int_as_float(p.x), p.y, bv, bi);
+        }
     const bool al = ((uintptr_t) a.logits & 15) == 0;
-    const int n4 = al ? a.n / 4 : 0;
+    const int n4 = a.part ? 0 : al ? a.n / 4 : 0;
     const float4 * l4 = (const float4 *) a.logits;
     for (int base = 0; base < n4; base += ARGMAX_THREADS * ARGMAX_UNROLL) {
         float4 v[ARGMAX_UNROLL];
@@ -1263,7 +1302,8 @@ extern "C" __global__ __launch_bounds__(ARGMAX_THREADS) void sml_argmax(const sm
             }
         }
     }
-    for (int i = 4 * n4 + tid; i < a.n; i += ARGMAX_THREADS) amax_take(a.logits[i], i, bv, bi);
+    if (!a.part)
+        for (int i = 4 * n4 + tid; i < a.n; i += ARGMAX_THREADS) amax_take(a.logits[i], i, bv, bi);
     #pragma unroll
     for (int o = 32; o; o >>= 1) {
         const float ov = __shfl_xor(bv, o);

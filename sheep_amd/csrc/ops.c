@@ -563,10 +563,20 @@ int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kc
 }
 
 void op_argmax(hipStream_t st, const float * logits, int n, int32_t * tok, int32_t * pos, int32_t * hist,
-               int hist_n) {
+               int hist_n, int2 * part) {
     sml_kargmax a;
     memset(&a, 0, sizeof a);
     a.logits = logits; a.n = n; a.tok = tok; a.pos = pos; a.hist = hist; a.hist_n = hist_n;
+    if (part && n >= ARGMAX_TWO_STAGE_MIN) {
+        // a vocabulary's worth: one float4 per thread over many workgroups,
+        // then one workgroup over their pairs (one workgroup alone spends
+        // ~15 us on 128k logits)
+        const int words = n / 4 + 1;
+        int np = (words + 255) / 256;
+        if (np > ARGMAX_MAX_PARTS) np = ARGMAX_MAX_PARTS;
+        a.part = part; a.nparts = np;
+        hx_launch("sml_argmax_part", (unsigned) np, 1, 256, 0, st, &a);
+    }
     hx_launch("sml_argmax", 1, 1, 1024, 0, st, &a);
 }
 
@@ -582,7 +592,12 @@ void op_silu_mul(hipStream_t st, float * g, const float * u, int n) {
 
 int sml_hip_argmax(const float * logits, int n, int32_t * tok) {
     OP_BEGIN(-1);
-    op_argmax(0, logits, n, tok, NULL, NULL, 0);
+    int2 * part = n >= ARGMAX_TWO_STAGE_MIN ? hx_malloc((size_t) ARGMAX_MAX_PARTS * sizeof(int2)) : NULL;
+    op_argmax(0, logits, n, tok, NULL, NULL, 0, part);
+    if (part) {
+        HX(hipStreamSynchronize(0));
+        HX(hipFree(part));
+    }
     HX_LEAVE();
     return 0;
 }

@@ -91,8 +91,13 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
 // Whether op_gemm computes every row with the GEMV's arithmetic in this regime
 // for m_all rows (the exact regime, or per-32 rows the VALU kernel takes).
 int gemm_exact(int regime, int m_all);
+// Greedy pick over n logits (the first maximum; NaN never wins). part:
+// scratch of ARGMAX_MAX_PARTS pairs for the two-stage pick of n >=
+// ARGMAX_TWO_STAGE_MIN, or NULL for one workgroup.
+#define ARGMAX_TWO_STAGE_MIN 8192
+#define ARGMAX_MAX_PARTS 1024
 void op_argmax(hipStream_t st, const float * logits, int n, int32_t * tok, int32_t * pos, int32_t * hist,
-               int hist_n);
+               int hist_n, int2 * part);
 void op_advance(hipStream_t st, int32_t * pos);
 void op_silu_mul(hipStream_t st, float * g, const float * u, int n);
 

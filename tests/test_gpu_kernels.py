@@ -288,15 +288,28 @@ def test_attention(heads):
 
 
 def test_argmax_first_max():
+    """One workgroup below 8192 logits, two stages (per-workgroup pairs, then
+    one workgroup) from there: ties across workgroups, ragged tails, NaN and
+    all -inf keep the reference loop's answer."""
     rng = np.random.default_rng(0)
-    for n, tie in [(151936, True), (128256, False), (1000, True), (5, False)]:
+    cases = [(151936, "tie"), (128256, None), (1000, "tie"), (5, None), (8191, "tie"), (8192, "tie"),
+             (8193, "tie"), (151937, "tie"), (128256, "nan"), (128256, "nan0"), (9000, "-inf"),
+             (5_000_003, "tie")]
+    for n, kind in cases:
         lg = rng.standard_normal(n).astype(np.float32)
-        if tie:
+        if kind == "tie":
             lg[n // 3] = lg[n - 1] = lg.max() + 1.0
+        elif kind == "nan":
+            lg[n // 2] = np.nan
+            lg[n // 5] = lg[n - 2] = np.nanmax(lg) + 1.0
+        elif kind == "nan0":
+            lg[0] = np.nan
+        elif kind == "-inf":
+            lg[:] = -np.inf
         d = sa.DevBuf.of(lg)
         t = sa.DevBuf(4)
         assert sa.lib().sml_hip_argmax(d.ptr, n, t.ptr) == 0
-        assert int(t.read(np.int32)[0]) == ob.oracle().orc_argmax(lg.ctypes.data, n)
+        assert int(t.read(np.int32)[0]) == ob.oracle().orc_argmax(lg.ctypes.data, n), (n, kind)
 
 
 def test_copy_calibration_kernel():
