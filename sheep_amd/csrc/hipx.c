@@ -41,6 +41,7 @@ void hx_init(int device) {
     if (hx.inited) HX(hipModuleUnload(hx.mod));
     HX(hipModuleLoadData(&hx.mod, sml_code_object));
     fn_n = 0;
+    hx.ncu = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
     hx.device = device;
     hx.inited = 1;
 }

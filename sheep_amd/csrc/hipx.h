@@ -19,6 +19,7 @@ typedef struct {
     int       inited;
     int       device;
     hipModule_t mod;
+    int       ncu;                // compute units of the device
     long      fail_after;         // test hook: fail the Nth HIP call from now (< 0: off)
 } hx_state;
 

@@ -1346,6 +1346,19 @@ extern "C" __global__ __launch_bounds__(256) void sml_read_stream(const sml_krea
     if (a.pattern == 0) {
         for (uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x; i < nw; i += (uint64_t) gridDim.x * 256)
             acc ^= __builtin_nontemporal_load(p + i);
+    } else if (a.pattern == 3 || a.pattern == 4) {
+        // tiles of a row-major matrix with 2048-byte rows, one tile per wave
+        // step: 3 = 16 rows x 64 bytes (4 lanes per row, the small-M GEMM's
+        // operand loads), 4 = 4 rows x 256 bytes (16 lanes per row)
+        const uint64_t nrows = a.bytes / 2048;
+        const int l = threadIdx.x & 63;
+        const uint64_t ntiles = a.pattern == 3 ? (nrows / 16) * 32 : (nrows / 4) * 8;
+        for (uint64_t t = (uint64_t) blockIdx.x * 4 + (threadIdx.x >> 6); t < ntiles; t += (uint64_t) gridDim.x * 4) {
+            uint64_t row, byte;
+            if (a.pattern == 3) { row = (t / 32) * 16 + (l & 15); byte = (t % 32) * 64 + 16 * (l >> 4); }
+            else { row = (t / 8) * 4 + (l >> 4); byte = (t % 8) * 256 + 16 * (l & 15); }
+            acc ^= __builtin_nontemporal_load(p + (row * 2048 + byte) / 16);
+        }
     } else if (a.pattern == 2) {
         // one shot: each thread issues its 4 coalesced words before using any
         const uint64_t base = (uint64_t) blockIdx.x * 1024 + threadIdx.x;
@@ -1832,7 +1845,7 @@ __device__ __forceinline__ void xslice(const v4u v, v2u & x, v2u & y) {
     y = v2u{(unsigned) p[1], (unsigned) q[1]};
 }
 
-template <bool SW, bool SB, int RB, int NW>
+template <bool SW, bool SB, int RB, int NW, bool PS = false>
 __device__ void mgemm_q4_body(const sml_kgemm & a) {
     typedef long v1l;
     constexpr int NM = SW ? 2 : 1, NACC = NM * RB * 4;
@@ -1843,7 +1856,12 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
     const int n = a.cols, ng = n / 32, nsb = ng / 8;
     const int tid = threadIdx.x, lane = tid & 63, c = lane >> 4, i16 = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rb0 = blockIdx.x * (16 * RB);
+    // PS (persistent): the workgroup walks row tiles blockIdx.x, +gridDim.x,
+    // ... and keeps the activation operands of its superblocks in registers
+    // across them (at most 2 superblocks per wave); otherwise one tile
+    const int ntile = (a.rows + 16 * RB - 1) / (16 * RB);
+    int tile = blockIdx.x;
+    int rb0 = tile * (16 * RB);
     const int s0 = wave * nsb / NW, s1 = (wave + 1) * nsb / NW;   // this wave's superblocks
     const int spw = (nsb + NW - 1) / NW;                           // region size, in superblocks
     const int gw = (s1 - s0) * 8, gb = s0 * 8;
@@ -1861,14 +1879,17 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
     for (int k = 0; k < NM; k++) { plane[k] = mt[k].plane[0]; fqb[k] = mt[k].sqmq; fdb[k] = (const uint8_t *) mt[k].sdmd; }
     const uint32_t rowb = (uint32_t) n / 2;
     uint32_t boff0[RB], fqo[RB], fdo[RB];
-    #pragma unroll
-    for (int bk = 0; bk < RB; bk++) {
-        const int ra = rb0 + bk * 16 + i16;
-        const uint32_t rc = (uint32_t) (ra < a.rows ? ra : a.rows - 1);
-        boff0[bk] = rc * rowb + 16u * (uint32_t) c;
-        fqo[bk] = rc * (uint32_t) ng * 2u;
-        fdo[bk] = rc * (uint32_t) nsb * 4u;
-    }
+    auto set_tile = [&](int r0) {
+        #pragma unroll
+        for (int bk = 0; bk < RB; bk++) {
+            const int ra = r0 + bk * 16 + i16;
+            const uint32_t rc = (uint32_t) (ra < a.rows ? ra : a.rows - 1);
+            boff0[bk] = rc * rowb + 16u * (uint32_t) c;
+            fqo[bk] = rc * (uint32_t) ng * 2u;
+            fdo[bk] = rc * (uint32_t) nsb * 4u;
+        }
+    };
+    set_tile(rb0);
     const int8_t * qrow = a.q + (abase + (size_t) (i16 < m ? i16 : 0)) * n + 16 * c;
     struct Batch {
         v4u w[2][NM][RB];         // the superblock's 2 quads, 16 bytes per lane
@@ -1893,9 +1914,22 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
                     b.fd[k][bk] = *(const uint32_t *) (fdb[k] + (fdo[bk] + (uint32_t) bt * 4u));
                 }
             }
-        const int8_t * qp = qrow + (size_t) g0 * 32;
+        if constexpr (!PS) {
+            const int8_t * qp = qrow + (size_t) g0 * 32;
+            #pragma unroll
+            for (int u = 0; u < 4; u++) b.aq[u] = *(const v4u *) (qp + u * 64);
+        }
+    };
+    // the activation operands of one superblock (A of group j from the
+    // activation load j/2: x, y)
+    auto act_operands = [&](const v4u (&aq)[4], v1l (&av)[8]) {
         #pragma unroll
-        for (int u = 0; u < 4; u++) b.aq[u] = *(const v4u *) (qp + u * 64);
+        for (int u = 0; u < 4; u++) {
+            v2u x, y;
+            xslice(aq[u], x, y);
+            av[2 * u] = (v1l) (((unsigned long) x.y << 32) | x.x);
+            av[2 * u + 1] = (v1l) (((unsigned long) y.y << 32) | y.x);
+        }
     };
     // the MFMA operands of one superblock: B of group j from quad j/4 (low
     // nibbles of x, high of x, low of y, high of y), A of group j from the
@@ -1916,14 +1950,22 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             for (int k = 0; k < NM; k++)
                 #pragma unroll
                 for (int bk = 0; bk < RB; bk++) xslice(b.w[p][k][bk], wx[p][k][bk], wy[p][k][bk]);
-        #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            v2u x, y;
-            xslice(b.aq[u], x, y);
-            av[2 * u] = (v1l) (((unsigned long) x.y << 32) | x.x);
-            av[2 * u + 1] = (v1l) (((unsigned long) y.y << 32) | y.x);
-        }
+        if constexpr (!PS) act_operands(b.aq, av);
     };
+    // persistent: the wave's (at most 2) superblocks of activation operands,
+    // loaded once for every tile
+    v1l pav[PS ? 2 : 1][8];
+    if constexpr (PS) {
+        #pragma unroll
+        for (int k = 0; k < 2; k++) {
+            v4u aq[4];
+            const int bt = s0 + k < s1 ? s0 + k : s0;
+            const int8_t * qp = qrow + (size_t) (8 * bt) * 32;
+            #pragma unroll
+            for (int u = 0; u < 4; u++) aq[u] = *(const v4u *) (qp + u * 64);
+            act_operands(aq, pav[k]);
+        }
+    }
     auto bcodes = [&](const v2u (&wx)[2][NM][RB], const v2u (&wy)[2][NM][RB], int j, int k, int bk) -> v1l {
         const v2u w = (j & 2) ? wy[j >> 2][k][bk] : wx[j >> 2][k][bk];
         const v2u cd = (j & 1) ? ((w >> 4u) & 0x0F0F0F0Fu) : (w & 0x0F0F0F0Fu);
@@ -1949,6 +1991,10 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             v2u wx[2][NM][RB], wy[2][NM][RB];
             v1l av[8];
             operands(b, wx, wy, av);
+            if constexpr (PS) {
+                #pragma unroll
+                for (int j = 0; j < 8; j++) av[j] = bt == s0 ? pav[0][j] : pav[PS ? 1 : 0][j];
+            }
             #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int4 sm = *(const int4 *) &lsum[(gl0 + j) * 16 + 4 * c];
@@ -1986,6 +2032,10 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             v2u wx[2][NM][RB], wy[2][NM][RB];
             v1l av[8];
             operands(b, wx, wy, av);
+            if constexpr (PS) {
+                #pragma unroll
+                for (int j = 0; j < 8; j++) av[j] = bt == s0 ? pav[0][j] : pav[PS ? 1 : 0][j];
+            }
             #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const float4 s01 = *(const float4 *) &lsc[(gl0 + j) * 16 + 4 * c];
@@ -2045,6 +2095,7 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             }
         }
     }
+    for (;;) {
     for (int bt = s0; bt < s1; bt += 2) {
         compute(A, bt);
         if (bt + 2 < s1) load(A, bt + 2);
@@ -2052,14 +2103,27 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
         compute(B, bt + 1);
         if (bt + 3 < s1) load(B, bt + 3);
     }
-    __syncthreads();                                  // every wave is past its staging region
-    float * red = (float *) lds;                      // [NW][NACC][64]
+    const int next = tile + (PS ? (int) gridDim.x : ntile);
+    if constexpr (PS) {
+        // the next tile's weights load while this one's sums meet
+        if (next < ntile) {
+            set_tile(next * 16 * RB);
+            if (s0 < s1) load(A, s0);
+            if (s0 + 1 < s1) load(B, s0 + 1);
+        }
+    }
+    __syncthreads();                                  // every wave is past its staging region / the last tile's sums
+    // [NW][NACC][64]: over the staging regions, or (PS) after them
+    float * red = (float *) (lds + (PS ? (size_t) NW * spw * (SB ? 576 : 1024) : 0));
     #pragma unroll
     for (int k = 0; k < NM; k++)
         #pragma unroll
         for (int bk = 0; bk < RB; bk++)
             #pragma unroll
-            for (int r = 0; r < 4; r++) red[(wave * NACC + (k * RB + bk) * 4 + r) * 64 + lane] = acc[k][bk][r];
+            for (int r = 0; r < 4; r++) {
+                red[(wave * NACC + (k * RB + bk) * 4 + r) * 64 + lane] = acc[k][bk][r];
+                acc[k][bk][r] = 0.0f;
+            }
     __syncthreads();
     for (int o = tid; o < RB * 256; o += 64 * NW) {
         const int bk = o >> 8, r = (o >> 6) & 3, l = o & 63;
@@ -2083,6 +2147,10 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             y[row] = v;
         }
     }
+    if (!PS || next >= ntile) break;
+    tile = next;
+    rb0 = tile * (16 * RB);
+    }
 }
 
 #define MGEMM_KERNEL(RB, NW)                                                                                   \
@@ -2098,4 +2166,18 @@ MGEMM_KERNEL(1, 4)
 MGEMM_KERNEL(2, 4)
 MGEMM_KERNEL(1, 8)
 MGEMM_KERNEL(2, 8)
+// Persistent forms (_p): a grid smaller than the tile count, each workgroup
+// keeping its activation operands for every tile it takes (input widths of
+// at most 2 superblocks per wave)
+#define MGEMM_KERNEL_P(RB, NW)                                                                                 \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_r##RB##_w##NW##_p(const sml_kgemm a) {  \
+        mgemm_q4_body<false, false, RB, NW, true>(a); }                                                        \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_r##RB##_w##NW##_p(const sml_kgemm a) { \
+        mgemm_q4_body<true, false, RB, NW, true>(a); }                                                         \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_sb_r##RB##_w##NW##_p(const sml_kgemm a) { \
+        mgemm_q4_body<false, true, RB, NW, true>(a); }                                                         \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_sb_r##RB##_w##NW##_p(const sml_kgemm a) { \
+        mgemm_q4_body<true, true, RB, NW, true>(a); }
+MGEMM_KERNEL_P(1, 8)
+
 

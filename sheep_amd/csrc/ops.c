@@ -837,11 +837,28 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
         const int nsb = cols / 256, spw = (nsb + nw - 1) / nw;
         const size_t stage = (size_t) nw * spw * (per256 ? 576 : 1024);
         const size_t red = (size_t) nw * (swiglu ? 2 : 1) * rb * 4 * 64 * 4;
-        const size_t lds = stage > red ? stage : red;
+        const int ntile = (rows + 16 * rb - 1) / (16 * rb);
+        // persistent form where a wave's activation operands fit in registers
+        // (at most 2 superblocks per wave: inputs up to 4096 wide): each
+        // workgroup reads the activation rows once for several row tiles
+        // instead of once per tile. At most one workgroup per CU, each
+        // taking the same number of tiles: 2 x 14336 x 4096 SwiGLU at 16
+        // rows, 896 tiles on 224 workgroups, 37.3 -> 28.1 us (per-256:
+        // 33.5 -> 25.0); a grid above the CU count runs some CUs twice as
+        // long (299 workgroups: 39.9 us). SML_MGEMM_PWG sets the cap.
+        const int ps = nw == 8 && rb == 1 && spw <= 2 && env_int("SML_MGEMM_PS", 1);
+        const size_t lds = ps ? stage + red : stage > red ? stage : red;
         if (lds <= 65536) {
-            snprintf(name, sizeof name, "sml_mgemm_q4%s%s_r%d_w%d", swiglu ? "_s" : "", per256 ? "_sb" : "", rb, nw);
-            hx_launch(name, (unsigned) ((rows + 16 * rb - 1) / (16 * rb)), (unsigned) ngroups, (unsigned) (64 * nw),
-                      lds, st, &a);
+            unsigned grid = (unsigned) ntile;
+            if (ps) {
+                int cap = env_int("SML_MGEMM_PWG", hx.ncu);
+                if (cap < 1) cap = 1;
+                const int per = (ntile + cap - 1) / cap;
+                grid = (unsigned) ((ntile + per - 1) / per);
+            }
+            snprintf(name, sizeof name, "sml_mgemm_q4%s%s_r%d_w%d%s", swiglu ? "_s" : "", per256 ? "_sb" : "", rb, nw,
+                     ps ? "_p" : "");
+            hx_launch(name, grid, (unsigned) ngroups, (unsigned) (64 * nw), lds, st, &a);
             return;
         }
     }

@@ -85,6 +85,44 @@ def test_mfma_gemm_q4(tmpdir_s, cols, rows):
             close(got[r], ob.matvec(t, *ob.quantize_act(xs[r])), f"mfma gemm row {r} of {nrow}")
 
 
+@pytest.mark.parametrize("cols", [1536, 4096])
+def test_mfma_gemm_persistent_equals_one_tile(tmpdir_s, monkeypatch, cols):
+    """The persistent MFMA GEMM (a workgroup walks several 16-row tiles with
+    its activation operands kept in registers) computes each tile with the
+    one-tile kernel's arithmetic: outputs equal bit for bit, whatever the grid
+    (the default cap, 5 workgroups for 563 tiles, one tile each), for plain
+    and SwiGLU products, per-32 and per-256 activations; the last tile is
+    ragged (9000 rows)."""
+    rows = 9000
+    p = tmpdir_s / f"mgp_{cols}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, rows, cols, nbits=4, random_perm=False, seed=700 + cols)
+    m = sa.Mat.from_file(p, "w")
+    up = sa.Mat.from_file(p, "w")
+    rng = np.random.default_rng(cols + 7)
+    nrow = 13
+    xs = [rng.standard_normal(cols).astype(np.float32) * (1 + r) for r in range(nrow)]
+    for per256 in (False, True):
+        q, s, u = quant_rows_sb(xs) if per256 else (None, None, None)
+        acts = (sa.DevBuf.of(q), sa.DevBuf.of(s), sa.DevBuf.of(u)) if per256 else quant_rows(xs)
+        outs = {}
+        for mode, env in (("one tile", {"SML_MGEMM_PS": "0"}), ("default", {}), ("5 workgroups", {"SML_MGEMM_PWG": "5"})):
+            monkeypatch.delenv("SML_MGEMM_PS", raising=False)
+            monkeypatch.delenv("SML_MGEMM_PWG", raising=False)
+            for k, v in env.items():
+                monkeypatch.setenv(k, v)
+            y = sa.DevBuf(nrow * rows * 4)
+            sa.gemm(m, *acts, nrow, y, per256=per256)
+            h = sa.DevBuf(nrow * rows * 4)
+            sa.gemm_swiglu(m, up, *acts, nrow, h, per256=per256)
+            outs[mode] = (y.read(np.float32), h.read(np.float32))
+        for mode in ("default", "5 workgroups"):
+            for i, what in enumerate(("plain", "swiglu")):
+                np.testing.assert_array_equal(outs[mode][i], outs["one tile"][i],
+                                              err_msg=f"{what} per256={per256} {mode}")
+        assert np.isfinite(outs["one tile"][0]).all()
+
+
 def quant_rows_sb(xs):
     """Per-256 quantization of each row (sml_quantize_act_sb), as host arrays."""
     q, s, u = zip(*(ob.quantize_act(np.ascontiguousarray(x, np.float32), per256=True) for x in xs))
