@@ -370,14 +370,16 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
     }
     int rb, ni;
     pick_shape(a.total_rows, cols, swiglu, am, &rb, &ni);
+    int wg = 256;
+    if (!swiglu && am && env_int("SML_GEMV_WG", 512) != 256) {
+        wg = env_int("SML_GEMV_WG", 512) == 1024 ? 1024 : 512;
+        if (wg == 1024 && rb > 2) rb = 2;               // the 1024-thread forms hold 1 or 2 rows per wave
+    }
     const int rows_per_wave = swiglu ? rb / 2 : rb;
     const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
-    int wg = 256;
     if (swiglu) snprintf(name, sizeof name, "sml_gemv_q%d_s%s_r%d_i%d", nb, am ? "n" : "", rb, ni);
-    else if (am && env_int("SML_GEMV_WG", 512) != 256) {
-        wg = env_int("SML_GEMV_WG", 512) == 1024 ? 1024 : 512;
-        snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_n%d", nb, rb, ni, wg);
-    } else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d%s", nb, rb, ni, am ? "_n" : "");
+    else if (wg != 256) snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_n%d", nb, rb, ni, wg);
+    else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d%s", nb, rb, ni, am ? "_n" : "");
     hx_launch(name, (unsigned) ((waves + wg / 64 - 1) / (wg / 64)), 1, (unsigned) wg, lds, st, &a);
 }
 
