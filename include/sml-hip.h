@@ -203,7 +203,10 @@ int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kc
                       int n_head, int n_kv, int hd, int n_ctx, float * part, float * out);
 
 // ------------------------------------------------------------ argmax
-// First-max greedy pick into *tok (sml_sample_greedy, sml/sml-run.c:3539-3544)
+// First-max greedy pick into *tok (sml_sample_greedy, sml/sml-run.c:3539-3544).
+// From 8192 logits it runs in two stages over a scratch buffer of 8 KB that
+// this call allocates and frees (the decode step keeps its own); it returns
+// once the pick is done.
 int sml_hip_argmax(const float * logits, int n, int32_t * tok);
 
 #ifdef __cplusplus
