@@ -281,7 +281,8 @@ def small_gemm(tmp, M=16, iters=60):
     launch (best of 3) and the weight bytes' rate."""
     rng = np.random.default_rng(1005)
     out = {}
-    for rows, cols, sw, n in [(14336, 4096, True, 8), (4096, 4096, False, 24), (4096, 14336, False, 16)]:
+    for rows, cols, sw, n in [(14336, 4096, True, 8), (4096, 4096, False, 24), (6144, 4096, False, 24),
+                              (4096, 14336, False, 16)]:
         p = os.path.join(tmp, f"gemm_{rows}x{cols}.ssf")
         sa.synth_matrix(p, rows, cols, nbits=4, seed=1005)
         mats = [sa.Mat.from_file(p, "w") for _ in range(n * (2 if sw else 1))]
