@@ -1402,26 +1402,32 @@ extern "C" __global__ __launch_bounds__(256) void sml_copy_stream(const sml_kcop
 // consecutive groups, summed in LDS into one partial per output;
 // sml_gptq_reduce adds the partials in a fixed order.
 #define GPTQ_WAVES 8
-extern "C" __global__ __launch_bounds__(64 * GPTQ_WAVES) void sml_gptq_gemv(const sml_kgptq a) {
+// OPL outputs per lane (4: 256 outputs per wave, 16-byte weight loads; 2:
+// 128 per wave, 8-byte loads and twice the waves for the same matrix)
+template <int OPL>
+__device__ void gptq_body(const sml_kgptq & a) {
+    typedef uint32_t vw __attribute__((ext_vector_type(OPL)));
     __shared__ float xs[GPTQ_WAVES][128];
-    __shared__ float red[GPTQ_WAVES][256];
+    __shared__ float red[GPTQ_WAVES][64 * OPL];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ngr = a.cols / 128;
     const int g = blockIdx.y * GPTQ_WAVES + w;
     const bool gv = g < ngr;
-    const int o = blockIdx.x * 256 + lane * 4;
+    const int o = blockIdx.x * (64 * OPL) + lane * OPL;
     const bool ov = o < a.rows;
     const int gc = gv ? g : 0, oc = ov ? o : 0;
     const float * xg = a.x + (size_t) gc * 128;
     // 1. this group's inputs (two per lane, for their sum), every weight word,
     // then the group fields
     const float2 xv = ((const float2 *) xg)[lane];
-    v4u q[16];
+    vw q[16];
     #pragma unroll
     for (int kk = 0; kk < 16; kk++)
-        q[kk] = __builtin_nontemporal_load((const v4u *) (a.qweight + ((size_t) gc * 16 + kk) * a.rows + oc));
-    const v2u sc = *(const v2u *) (a.scales + (size_t) gc * a.rows + oc);
+        q[kk] = __builtin_nontemporal_load((const vw *) (a.qweight + ((size_t) gc * 16 + kk) * a.rows + oc));
+    uint16_t scv[OPL];
+    #pragma unroll
+    for (int j = 0; j < OPL; j++) scv[j] = a.scales[(size_t) gc * a.rows + oc + j];
     const uint32_t zw = a.qzeros[(size_t) gc * (a.rows / 8) + oc / 8];
     xs[w][2 * lane] = xv.x;
     xs[w][2 * lane + 1] = xv.y;
@@ -1429,12 +1435,14 @@ extern "C" __global__ __launch_bounds__(64 * GPTQ_WAVES) void sml_gptq_gemv(cons
     __syncthreads();
     // 2. sum q*x per output: the low and high nibbles of each byte are
     // inputs 2i and 2i+1 of the word's 8
-    float acc[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+    float acc[OPL];
+    #pragma unroll
+    for (int j = 0; j < OPL; j++) acc[j] = 0.0f;
     #pragma unroll
     for (int kk = 0; kk < 16; kk++) {
         const float4 x0 = *(const float4 *) &xs[w][kk * 8], x1 = *(const float4 *) &xs[w][kk * 8 + 4];
         #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < OPL; j++) {
             const uint32_t wd = q[kk][j], lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
             float t = acc[j];
             t = fmaf((float) (lo & 0xFFu), x0.x, t);
@@ -1450,22 +1458,24 @@ extern "C" __global__ __launch_bounds__(64 * GPTQ_WAVES) void sml_gptq_gemv(cons
     }
     // 3. the group epilogue and the workgroup's sum over its groups
     #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float s = h2f((uint16_t) ((j < 2 ? sc.x : sc.y) >> (16 * (j & 1))));
+    for (int j = 0; j < OPL; j++) {
+        const float s = h2f(scv[j]);
         const float z = (float) (((zw >> (4 * ((oc & 7) + j))) & 15u) + (uint32_t) a.zero_add);
-        red[w][lane * 4 + j] = gv ? s * (acc[j] - z * sx) : 0.0f;
+        red[w][lane * OPL + j] = gv ? s * (acc[j] - z * sx) : 0.0f;
     }
     __syncthreads();
     if (tid < 64 && ov) {
         #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float v = red[0][lane * 4 + j];
+        for (int j = 0; j < OPL; j++) {
+            float v = red[0][lane * OPL + j];
             #pragma unroll
-            for (int k = 1; k < GPTQ_WAVES; k++) v += red[k][lane * 4 + j];
+            for (int k = 1; k < GPTQ_WAVES; k++) v += red[k][lane * OPL + j];
             a.part[(size_t) blockIdx.y * a.rows + o + j] = v;
         }
     }
 }
+extern "C" __global__ __launch_bounds__(64 * GPTQ_WAVES) void sml_gptq_gemv(const sml_kgptq a) { gptq_body<4>(a); }
+extern "C" __global__ __launch_bounds__(64 * GPTQ_WAVES) void sml_gptq_gemv2(const sml_kgptq a) { gptq_body<2>(a); }
 
 extern "C" __global__ __launch_bounds__(256) void sml_gptq_reduce(const sml_kgptq a) {
     const int o = blockIdx.x * 256 + threadIdx.x;
