@@ -298,7 +298,7 @@ static int env_int(const char * name, int dflt) {
 // kernels run 512-thread workgroups with 4 rows per wave and one chunk per
 // pass, so that the fewest workgroups (each repeating the prologue) still
 // cover the chip.
-static void pick_shape(int rows, int cols, int swiglu, int fused, int * rb, int * ni) {
+static void pick_shape(int rows, int cols, int nbits, int swiglu, int fused, int * rb, int * ni) {
     const int ng = cols / 32;
     const int imax = fused ? 1 : 4;
     int i = 1;
@@ -309,6 +309,10 @@ static void pick_shape(int rows, int cols, int swiglu, int fused, int * rb, int 
         while (r > 1 && rows / (8 * r) < 192) r /= 2;
     } else {
         while (r < 4 && rows / (2 * r) >= 2048 && 2 * r * i <= 16) r *= 2;
+        // the two-plane widths' heavier unpack runs better at one row per
+        // wave with 4 chunks per pass (4096 x 14336: Q3 9.2 -> 8.5 us, Q5
+        // 10.3 -> 9.8, Q8 13.0 -> 12.7; Q4 and Q6 stay at 2 rows)
+        if ((nbits == 3 || nbits == 5 || nbits == 8) && r == 2 && i == 4 && !swiglu) r = 1;
     }
     const int fr = env_int("SML_GEMV_RB", 0), fi = env_int("SML_GEMV_NI", 0);
     if (fr == 1 || fr == 2 || fr == 4) r = fr;
@@ -369,7 +373,7 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
         return;
     }
     int rb, ni;
-    pick_shape(a.total_rows, cols, swiglu, am, &rb, &ni);
+    pick_shape(a.total_rows, cols, nb, swiglu, am, &rb, &ni);
     int wg = 256;
     if (!swiglu && am && env_int("SML_GEMV_WG", 512) != 256) {
         wg = env_int("SML_GEMV_WG", 512) == 1024 ? 1024 : 512;
