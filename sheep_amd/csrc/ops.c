@@ -839,7 +839,11 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
     const char * mode = getenv("SML_MULTI");
     const int exact = regime == GEMM_EXACT || (mode && !strcmp(mode, "exact"));
     if (nbits == 4 && cols % 256 == 0 && !count && m_all > 8 && !exact && env_int("SML_MGEMM", 1)) {
-        int rb = !swiglu && rows >= 32768 ? 2 : 1;
+        const int nsb0 = cols / 256;
+        // very tall products take 2 blocks of 16 rows per workgroup, unless
+        // the persistent form applies (it reads the activation rows once per
+        // workgroup whatever the height)
+        int rb = !swiglu && rows >= 32768 && !(nsb0 <= 16 && env_int("SML_MGEMM_PS", 1)) ? 2 : 1;
         const int fr = env_int("SML_MGEMM_RB", 0);
         if (fr == 1 || fr == 2) rb = fr;
         const int nw = env_int("SML_MGEMM_NW", 8) == 4 ? 4 : 8;
