@@ -823,9 +823,12 @@ __device__ __forceinline__ void wave_heads(const float (&x)[REP], float (&out)[R
     }
 }
 
-template <int REP, int NW, bool CHUNK>
+// CH: positions per split (128; the one-sequence decode launch also takes 32
+// or 64, so that models with few KV heads still fill the chip)
+template <int REP, int NW, bool CHUNK, int CH = ATTN_CHUNK>
 __device__ __forceinline__ void attn_body(const sml_kattn & a) {
-    constexpr int NT = 64 * NW, PS = NT / 16, PPL = ATTN_CHUNK / PS;   // threads, position stride, positions per lane
+    constexpr int NT = 64 * NW, PS = NT / 16, PPL = CH / PS;   // threads, position stride, positions per lane
+    static_assert(PPL >= 1 && PPL * PS == CH, "a split covers whole rounds of positions");
     __shared__ float red[NW][REP][HD];
     __shared__ float wm[NW][REP], wl[NW][REP];
     const int kh = blockIdx.y, split = blockIdx.x, tid = threadIdx.x;
@@ -834,7 +837,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     // positions of one sequence, which share this split's K/V tile
     const int tpw = CHUNK ? a.tpw : 1;
     const int b0 = blockIdx.z * tpw, b1 = CHUNK ? min(b0 + tpw, a.nseq) : b0 + 1;
-    const int t0 = split * ATTN_CHUNK, tlast = a.pos[b1 - 1] + 1;
+    const int t0 = split * CH, tlast = a.pos[b1 - 1] + 1;
     uint16_t * kcache = a.kc_slots ? a.kc_slots[a.slot[b0]] + a.layer_off : a.kcache;
     uint16_t * vcache = a.vc_slots ? a.vc_slots[a.slot[b0]] + a.layer_off : a.vcache;
     // the first entry's q, k and v load first: loads return in order
@@ -861,7 +864,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     // softmax run while V is still arriving
     v4u kw[PPL], vw[PPL];
     if (t0 < tlast) {
-        const int tl = min(tlast, t0 + ATTN_CHUNK);
+        const int tl = min(tlast, t0 + CH);
         #pragma unroll
         for (int i = 0; i < PPL; i++) {
             int t = t0 + grp + PS * i;
@@ -898,7 +901,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         if (tid < REP) pml[(size_t) tid * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
         continue;
     }
-    const int t1 = min(T, t0 + ATTN_CHUNK);
+    const int t1 = min(T, t0 + CH);
     const bool lo = l16 < 8;
     const float sl = a.inv * 1.44269504088896341f;
     #pragma unroll
@@ -1038,7 +1041,11 @@ extern "C" __global__ __launch_bounds__(128) void sml_ropekv(const sml_kattn a) 
 #define ATTN_KERNEL(R) \
     extern "C" __global__ __launch_bounds__(256) void sml_attn_r##R(const sml_kattn a) { attn_body<R, 4, false>(a); } \
     extern "C" __global__ __launch_bounds__(512) void sml_attn8_r##R(const sml_kattn a) { attn_body<R, 8, false>(a); } \
-    extern "C" __global__ __launch_bounds__(512) void sml_attnc8_r##R(const sml_kattn a) { attn_body<R, 8, true>(a); }
+    extern "C" __global__ __launch_bounds__(512) void sml_attnc8_r##R(const sml_kattn a) { attn_body<R, 8, true>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attn8_s32_r##R(const sml_kattn a) { attn_body<R, 8, false, 32>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attn8_s64_r##R(const sml_kattn a) { attn_body<R, 8, false, 64>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attnc8_s32_r##R(const sml_kattn a) { attn_body<R, 8, true, 32>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attnc8_s64_r##R(const sml_kattn a) { attn_body<R, 8, true, 64>(a); }
 ATTN_KERNEL(1) ATTN_KERNEL(2) ATTN_KERNEL(3) ATTN_KERNEL(4) ATTN_KERNEL(5) ATTN_KERNEL(6) ATTN_KERNEL(7) ATTN_KERNEL(8)
 
 // ---------------------------------------------------------------- prompt attention, a wave per position

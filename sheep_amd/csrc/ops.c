@@ -480,9 +480,24 @@ int sml_hip_embed(const sml_hip_mat * m, const int32_t * tok, const int32_t * pe
 
 #define ATTN_CHUNK 128
 
+#define ATTN_MIN_CHUNK 32         // the shortest split a decode launch takes
 size_t sml_hip_attn_part_floats(int n_head, int hd, int n_ctx) {
-    const int ns = (n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    const int ns = (n_ctx + ATTN_MIN_CHUNK - 1) / ATTN_MIN_CHUNK;
     return (size_t) n_head * ns * (size_t) (hd + 2);
+}
+
+// Positions per split of the 8-wave decode kernels (and the exact prompt
+// kernel, which must split as decoding does): 128, or 64 where KV heads x
+// splits of 128 leave most CUs idle. Qwen2.5-1.5B shape (2 KV heads, 4096
+// positions), 128 / 64 / 32: decode 1097 / 1112 / 1068 tokens/s, a 2048-id
+// prompt at level 1 2405 / 2598 / 2665. SML_ATTN_CHUNK overrides (32, 64 or
+// 128).
+static int attn_split(int n_kv, int n_ctx) {
+    int ch = ATTN_CHUNK;
+    while (ch > 64 && (long) n_kv * ((n_ctx + ch - 1) / ch) < 256) ch /= 2;
+    const int ce = env_int("SML_ATTN_CHUNK", 0);
+    if (ce == 32 || ce == 64 || ce == 128) ch = ce;
+    return ch;
 }
 
 void op_attention(hipStream_t st, const float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
@@ -491,7 +506,9 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
                   int32_t * u_out) {
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
-    const int ns = (n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    const int aw = env_int("SML_ATTN_WAVES", 8) == 4 ? 4 : 8;
+    const int ch = aw == 4 ? ATTN_CHUNK : attn_split(n_kv, n_ctx);   // the 4-wave form runs splits of 128 only
+    const int ns = (n_ctx + ch - 1) / ch;
     sml_kattn a;
     memset(&a, 0, sizeof a);
     a.q = q; a.k = k; a.v = v; a.kcache = kc; a.vcache = vc; a.cos_t = cos_t; a.sin_t = sin_t; a.pos = pos;
@@ -499,8 +516,8 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
     char name[32];
-    const int aw = env_int("SML_ATTN_WAVES", 8) == 4 ? 4 : 8;
     if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
+    else if (ch != ATTN_CHUNK) snprintf(name, sizeof name, "sml_attn8_s%d_r%d", ch, n_head / n_kv);
     else snprintf(name, sizeof name, "sml_attn%d_r%d", aw, n_head / n_kv);
     hx_launch(name, (unsigned) ns, (unsigned) n_kv, (unsigned) (64 * aw), 0, st, &a);
     hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
@@ -514,7 +531,11 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
     if (nseq < 1 || nseq > 65535) hx_failf("attention batch of %d", nseq);
-    const int ns = (n_ctx + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    const int aw = env_int("SML_ATTN_WAVES", nseq >= 4 && !exact ? 4 : 8) == 4 ? 4 : 8;
+    // the 8-wave kernels split as decoding does (attn_split); the 4-wave and
+    // wave-per-position kernels run splits of 128
+    const int ch = causal == 2 || (causal == 0 && aw == 4) ? ATTN_CHUNK : attn_split(n_kv, n_ctx);
+    const int ns = (n_ctx + ch - 1) / ch;
     sml_kattn a;
     memset(&a, 0, sizeof a);
     a.q = qkv; a.k = qkv + (size_t) n_head * hd; a.v = a.k + (size_t) n_kv * hd;
@@ -533,7 +554,6 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     // measured faster (16 sequences at ~1k positions: 5.6 against 6.8 ms per
     // step); one sequence, and any step that must equal decoding alone bit
     // for bit (exact), keeps the decode kernel's 8 waves per split
-    const int aw = env_int("SML_ATTN_WAVES", nseq >= 4 && !exact ? 4 : 8) == 4 ? 4 : 8;
     // causal entries (positions of one sequence) share each split's K/V tile
     // in groups of tpw per workgroup (sml_attnc8); the arithmetic per entry is
     // the one-entry kernel's
@@ -550,10 +570,14 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
         hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
         return;
     }
-    if (a.tpw > 1) snprintf(name, sizeof name, "sml_attnc8_r%d", n_head / n_kv);
-    else if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
-    else snprintf(name, sizeof name, "sml_attn%d_r%d", aw, n_head / n_kv);
-    hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) ((nseq + a.tpw - 1) / a.tpw), (unsigned) (64 * aw), 0,
+    const int nt = causal ? 512 : 64 * aw;
+    if (a.tpw > 1 || causal) {
+        if (ch == ATTN_CHUNK) snprintf(name, sizeof name, "sml_attnc8_r%d", n_head / n_kv);
+        else snprintf(name, sizeof name, "sml_attnc8_s%d_r%d", ch, n_head / n_kv);
+    } else if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
+    else if (ch == ATTN_CHUNK) snprintf(name, sizeof name, "sml_attn8_r%d", n_head / n_kv);
+    else snprintf(name, sizeof name, "sml_attn8_s%d_r%d", ch, n_head / n_kv);
+    hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) ((nseq + a.tpw - 1) / a.tpw), (unsigned) nt, 0,
                st, &a);
     hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
 }
