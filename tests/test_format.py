@@ -121,3 +121,28 @@ def test_loader_rejections_match_reference(tmpdir_s, case):
     assert ok_mine == ok_ref, f"{name}: mine {ok_mine}, reference {ok_ref} ({why.value.decode()})"
     assert not ok_ref, name
     assert why.value, "a refusal carries a reason"
+
+
+def test_server_vocab_section(tmp_path):
+    """The byte-fallback vocabulary the server test appends lands where the
+    header's tok_off / tok_n say, in the reference's layout
+    (sml/sml-vocab.c:64-78: n_tokens, n_merges, bos, eos, offsets, bytes),
+    and the tensors still read the same."""
+    from test_gpu_server import SPECIALS, add_vocab
+    p = tmp_path / "v.ssf"
+    sa.synth_model(p, n_layer=1, n_embd=256, n_head=2, n_head_kv=1, n_ff=512, n_vocab=600, seed=3)
+    before = np.array(SSF(p)["token_embd.weight"].plane(0)[:4096])
+    add_vocab(str(p), 600)
+    f = SSF(p)
+    off, n = f.hdr["tok_off"], f.hdr["tok_n"]
+    assert off % 256 == 0 and off + n == os.path.getsize(p)
+    blob = bytes(f.mm[off:off + n])
+    nt, nm, bos, eos = struct.unpack_from("<4I", blob, 0)
+    assert (nt, nm, bos, eos) == (600, 0, 256, 258)
+    offs = struct.unpack_from(f"<{nt + 1}I", blob, 16)
+    data = blob[16 + 4 * (nt + 1):]
+    tok = lambda i: data[offs[i]:offs[i + 1]]
+    assert tok(0) == b"<0x00>" and tok(255) == b"<0xFF>"
+    assert [tok(256 + i).decode() for i in range(3)] == SPECIALS
+    assert tok(599) == "▁w599".encode() and offs[-1] == len(data)
+    np.testing.assert_array_equal(np.array(f["token_embd.weight"].plane(0)[:4096]), before)
