@@ -226,24 +226,66 @@ void orc_dequant_row(const orc_tensor * t, int row, float * out) {
     free(c);
 }
 
-// sml/sml-kernel.c:2027-2066 per group: sum += ws * s_g * dot; sum += mn * s_g * sum_g
+// Integer dot of group g of one row against the activation codes.
+static int32_t group_dot(const uint8_t * c, const int8_t * q, int g) {
+    int32_t d = 0;
+    for (int j = 0; j < 32; j++) d += (int32_t) c[g * 32 + j] * (int32_t) q[g * 32 + j];
+    return d;
+}
+
+// Q4 and Q8 in the float order of the reference's x86 build, which is the
+// arm its own -march=native build selects on AVX2 hosts:
+// matvec_flat4_l8 / sml_matvec_rows_il4 (sml/sml-kernel.c:572-727,836-866).
+// Eight lanes, lane j taking group j of every 256-weight superblock in turn:
+//   v_j = fma(wsc_j, s_g*dot_g, v_j); v_j = fma(wmin_j, s_g*sum_g, v_j)
+// (the reference's mul+add pairs, which its compiler contracts to FMAs),
+// wsc = f16(sd)*sq, wmin = f16(md)*(mq - bias); then the lanes fold as
+// ((v0+v4)+(v1+v5)) + ((v2+v6)+(v3+v7)). A trailing half superblock (4
+// groups) runs four lanes of its own, folded (t0+t1)+(t2+t3) and added last.
+static float row_avx2_order(const orc_tensor * t, int r, const uint8_t * c, const int8_t * q,
+                            const float * scale, const int32_t * sums) {
+    const int ng = t->cols / 32, nblk = ng / 8, tail = ng - nblk * 8;
+    float v[8] = { 0 }, vt[4] = { 0 };
+    for (int k = 0; k <= nblk; k++) {
+        const int nl = k < nblk ? 8 : tail;
+        float * acc = k < nblk ? v : vt;
+        for (int j = 0; j < nl; j++) {
+            const int g = 8 * k + j;
+            const float af = scale[g];
+            acc[j] = fmaf(orc_step(t, r, g), af * (float) group_dot(c, q, g), acc[j]);
+            if (t->mq) acc[j] = fmaf(orc_min(t, r, g), af * (float) sums[g], acc[j]);
+        }
+    }
+    float tot = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
+    if (tail) tot += (vt[0] + vt[1]) + (vt[2] + vt[3]);
+    return tot;
+}
+
+// Other widths: per group step*s*dot + min*s*sum in group order, the scalar
+// arm's arithmetic (sml/sml-kernel.c:2027-2066 flat4, :1934-1971 2-bit planes),
+// with the plane dispatch of sml/sml-run.c:612-680 folded into one integer dot
+// over the unpacked code (the code is linear in its planes).
+static float row_group_order(const orc_tensor * t, int r, const uint8_t * c, const int8_t * q,
+                             const float * scale, const int32_t * sums) {
+    float sum = 0.0f;
+    for (int g = 0; g < t->cols / 32; g++) {
+        sum += orc_step(t, r, g) * scale[g] * (float) group_dot(c, q, g);
+        if (t->mq) sum += orc_min(t, r, g) * scale[g] * (float) sums[g];
+    }
+    return sum;
+}
+
 void orc_matvec(const orc_tensor * t, const int8_t * q, const float * scale, const int32_t * sums,
                 float * y, int row0, int row1) {
-    const int n = t->cols, ng = n / 32;
+    const int n = t->cols;
+    const int lanes8 = (t->nbits == 4 || t->nbits == 8) && !t->scale6;
     #pragma omp parallel
     {
         uint8_t * c = malloc((size_t) n);
         #pragma omp for schedule(static)
         for (int r = row0; r < row1; r++) {
             orc_unpack_row(t, r, c);
-            float sum = 0.0f;
-            for (int g = 0; g < ng; g++) {
-                int32_t d = 0;
-                for (int j = 0; j < 32; j++) d += (int32_t) c[g * 32 + j] * (int32_t) q[g * 32 + j];
-                sum += orc_step(t, r, g) * scale[g] * (float) d;
-                if (t->mq) sum += orc_min(t, r, g) * scale[g] * (float) sums[g];
-            }
-            y[r] = sum;
+            y[r] = lanes8 ? row_avx2_order(t, r, c, q, scale, sums) : row_group_order(t, r, c, q, scale, sums);
         }
         free(c);
     }
@@ -251,11 +293,13 @@ void orc_matvec(const orc_tensor * t, const int8_t * q, const float * scale, con
 
 // ------------------------------------------------------------ small ops
 
+// sml/sml-run.c:147-152; the sum of squares is the reference build's chain of
+// double FMAs, the scaling two float products
 void orc_rms_norm(float * out, const float * x, const float * w, int n, float eps) {
     double ss = 0.0;
-    for (int i = 0; i < n; i++) ss += (double) x[i] * x[i];
+    for (int i = 0; i < n; i++) ss = fma((double) x[i], (double) x[i], ss);
     const float s = 1.0f / sqrtf((float) (ss / n) + eps);
-    for (int i = 0; i < n; i++) out[i] = x[i] * s * w[i];
+    for (int i = 0; i < n; i++) out[i] = (x[i] * s) * w[i];
 }
 
 void orc_rope_table(float theta, int half, int n_ctx, float * cos_t, float * sin_t) {
@@ -268,25 +312,38 @@ void orc_rope_table(float theta, int half, int n_ctx, float * cos_t, float * sin
         }
 }
 
+// sml/sml-run.c:363-368 as the reference build contracts it:
+// x0*cs - x1*sn = fma(x0, cs, -(x1*sn)), x0*sn + x1*cs = fma(x0, sn, x1*cs)
 void orc_rope(float * x, int n_head, int head_dim, int half, const float * cs, const float * sn) {
     for (int h = 0; h < n_head; h++) {
         float * v = x + (size_t) h * head_dim;
         for (int i = 0; i < half; i++) {
             const float x0 = v[i], x1 = v[i + half];
-            v[i] = x0 * cs[i] - x1 * sn[i];
-            v[i + half] = x0 * sn[i] + x1 * cs[i];
+            v[i] = fmaf(x0, cs[i], -(x1 * sn[i]));
+            v[i + half] = fmaf(x0, sn[i], x1 * cs[i]);
         }
     }
 }
 
-// sml/sml-run.c:242-266 scalar arm + softmax :280-287
+// sml/sml-run.c:126-133 (sml_hsum256): eight lanes folded
+// ((l0+l4)+(l1+l5)) + ((l2+l6)+(l3+l7))
+static float hsum8(const float * l) {
+    return ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]));
+}
+
+// sml/sml-run.c:180-240 (AVX2 arm, head_dim a multiple of 64) + softmax :280-287.
+// Score of position t: eight FMA lanes over the head's dims (lane l takes dims
+// l, l+8, ...), folded by hsum8, times inv. Softmax: serial max, expf, a serial
+// float sum, one reciprocal, products. Output dim d: one FMA chain over the
+// positions in order, a[u]*v[u][d] + o.
 void orc_attn_head(const float * qh, const uint16_t * kc, const uint16_t * vc, size_t stride,
                    int pos, int hd, float inv, float * a, float * out) {
     for (int t = 0; t <= pos; t++) {
         const uint16_t * kh = kc + (size_t) t * stride;
-        float s = 0.0f;
-        for (int i = 0; i < hd; i++) s += qh[i] * orc_f16_to_f32(kh[i]);
-        a[t] = s * inv;
+        float l[8] = { 0 };
+        for (int i = 0; i < hd; i += 8)
+            for (int j = 0; j < 8; j++) l[j] = fmaf(qh[i + j], orc_f16_to_f32(kh[i + j]), l[j]);
+        a[t] = hsum8(l) * inv;
     }
     float mx = a[0];
     for (int i = 1; i <= pos; i++) if (a[i] > mx) mx = a[i];
@@ -294,15 +351,43 @@ void orc_attn_head(const float * qh, const uint16_t * kc, const uint16_t * vc, s
     for (int i = 0; i <= pos; i++) { a[i] = expf(a[i] - mx); sum += a[i]; }
     const float iv = 1.0f / sum;
     for (int i = 0; i <= pos; i++) a[i] *= iv;
-    for (int i = 0; i < hd; i++) out[i] = 0.0f;
-    for (int u = 0; u <= pos; u++) {
-        const uint16_t * vh = vc + (size_t) u * stride;
-        for (int i = 0; i < hd; i++) out[i] += a[u] * orc_f16_to_f32(vh[i]);
+    for (int i = 0; i < hd; i++) {
+        float o = 0.0f;
+        for (int u = 0; u <= pos; u++) o = fmaf(a[u], orc_f16_to_f32(vc[(size_t) u * stride + i]), o);
+        out[i] = o;
     }
 }
 
+// sml/sml-run.c:393-414 (sml_exp_ps) as the reference build runs it: clamp to
+// [-88, 88], f = x*log2(e), r = f rounded half-even, g = f - r, 2^g by a
+// degree-5 Horner chain of FMAs; the result is p * 2^r.
+static float exp_poly(float x, float * p_out, float * scale_out) {
+    x = x < -88.0f ? -88.0f : x > 88.0f ? 88.0f : x;
+    const float f = x * 1.44269504088896341f;
+    const float r = nearbyintf(f);
+    const float g = f - r;
+    float p = fmaf(1.3697664e-3f, g, 8.3013611e-3f);
+    p = fmaf(p, g, 5.5826318e-2f);
+    p = fmaf(p, g, 2.4022652e-1f);
+    p = fmaf(p, g, 6.9314718e-1f);
+    p = fmaf(p, g, 1.0f);
+    uint32_t eb = (uint32_t) ((int32_t) r + 127) << 23;
+    float sc;
+    memcpy(&sc, &eb, 4);
+    *p_out = p;
+    *scale_out = sc;
+    return p * sc;
+}
+
+// sml/sml-run.c:416-426 (silu_mul, AVX2 arm; n_ff is a multiple of 8): the
+// reference build folds 1 + p*2^r into one FMA, then (g / d) * u.
 void orc_silu_mul(float * g, const float * u, int n) {
-    for (int i = 0; i < n; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+    for (int i = 0; i < n; i++) {
+        float p, sc;
+        exp_poly(0.0f - g[i], &p, &sc);
+        const float d = fmaf(p, sc, 1.0f);
+        g[i] = (g[i] / d) * u[i];
+    }
 }
 
 int orc_moe_route(const float * lg, int ne, int k, unsigned moe_flags, int * sel, float * w) {
@@ -333,7 +418,7 @@ int orc_moe_route(const float * lg, int ne, int k, unsigned moe_flags, int * sel
 void orc_router(const float * router, const float * x, int ne, int n_embd, float * lg) {
     for (int e = 0; e < ne; e++) {
         double s = 0.0;
-        for (int i = 0; i < n_embd; i++) s += (double) router[(size_t) e * n_embd + i] * x[i];
+        for (int i = 0; i < n_embd; i++) s = fma((double) router[(size_t) e * n_embd + i], (double) x[i], s);
         lg[e] = (float) s;
     }
 }
@@ -684,7 +769,7 @@ const float * orc_forward(orc_model * m, int token, int pos) {
                 mv(m, y->eu[e], m->xb, m->hb2);
                 orc_silu_mul(m->hb, m->hb2, fe);
                 mv(m, y->ed[e], m->hb, m->tmp);
-                for (int i = 0; i < E; i++) m->acc[i] += w[j] * m->tmp[i];
+                for (int i = 0; i < E; i++) m->acc[i] = fmaf(w[j], m->tmp[i], m->acc[i]);
             }
             for (int i = 0; i < E; i++) m->x[i] += m->acc[i];
             dump_x(m->x, E);

@@ -27,7 +27,7 @@ class SynthSpec(ctypes.Structure):
                 ("n_ctx_train", ctypes.c_uint32), ("rope_theta", c_float), ("rms_eps", c_float),
                 ("nbits", c_int), ("tied", c_int), ("qkv_bias", c_int), ("random_perm", c_int),
                 ("n_expert", c_int), ("n_expert_used", c_int), ("moe_flags", ctypes.c_uint32),
-                ("step_sigma", c_float), ("router_sigma", c_float), ("seed", c_uint64)]
+                ("step_sigma", c_float), ("router_sigma", c_float), ("seed", c_uint64), ("zero_mean", c_int)]
 
 
 # (name, restype, argtypes) of every export
@@ -255,11 +255,15 @@ def sync():
 
 def synth_model(path, n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx_train=4096,
                 rope_theta=1e6, rms_eps=1e-6, nbits=4, tied=False, qkv_bias=False, random_perm=False,
-                n_expert=0, n_expert_used=0, moe_flags=0, step_sigma=0.02, router_sigma=1.0 / 64, seed=1):
-    """Write a seeded synthetic SSF decoder (sheep_amd/csrc/ssf.c)."""
+                n_expert=0, n_expert_used=0, moe_flags=0, step_sigma=0.02, router_sigma=1.0 / 64, seed=1,
+                zero_mean=True):
+    """Write a seeded synthetic SSF decoder (sheep_amd/csrc/ssf.c). zero_mean
+    puts every group's min at -(2^b - 1)/2 steps, so the uniform codes give
+    weights of mean zero and the logits depend on the input; False keeps the
+    single-GEMV recipe (min at -2^(b-1) steps)."""
     sp = SynthSpec(n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx_train, rope_theta, rms_eps,
                    nbits, int(tied), int(qkv_bias), int(random_perm), n_expert, n_expert_used, moe_flags,
-                   step_sigma, router_sigma, seed)
+                   step_sigma, router_sigma, seed, int(zero_mean))
     why = ctypes.create_string_buffer(512)
     if not lib().ssf_synth_model(str(path).encode(), ctypes.byref(sp), why, 512):
         raise RuntimeError(why.value.decode())

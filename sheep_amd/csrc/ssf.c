@@ -201,6 +201,7 @@ typedef struct {
     int kind;                 // SSF_KIND_*
     int rows, cols, nbits;
     int perm_key;             // tensors with equal perm_key share one permutation array
+    int zero_mean;            // QUANT: mins at -(2^b - 1)/2 steps
     int fill;                 // F32: 0 = 1+N(0,s), 1 = N(0,s)
     float sigma;
     ssf_record rec;
@@ -228,10 +229,10 @@ static char * sdup(const char * fmt, ...) {
     return strdup(buf);
 }
 
-static void add_quant(plan_list * l, const char * name, int rows, int cols, int nbits, int perm_key) {
+static void add_quant(plan_list * l, const char * name, int rows, int cols, int nbits, int perm_key, int zero_mean) {
     plan_t * p = plan_add(l);
     p->name = name; p->kind = SSF_KIND_QUANT; p->rows = rows; p->cols = cols; p->nbits = nbits;
-    p->perm_key = perm_key;
+    p->perm_key = perm_key; p->zero_mean = zero_mean;
 }
 
 static void add_f32(plan_list * l, const char * name, int count, int fill, float sigma) {
@@ -302,8 +303,10 @@ static void make_perm(int32_t * perm, int cols, int random, uint64_t seed, int p
 
 // Fill one quantized matrix: fields by the two-level encoding of random group
 // steps (sd = f16(max step / 255), sq = clip(rint(step / sd), 1, 255); mins at
-// -2^(b-1) steps: md = f16(max |min| / 127), mq = clip(rint(min / md) + 127, 0, 254)),
-// codes uniform over [0, 2^b - 1]. Rows are independent streams, so the fill
+// -zp steps: md = f16(max |min| / 127), mq = clip(rint(min / md) + 127, 0, 254)),
+// codes uniform over [0, 2^b - 1]. zp is 2^(b-1), or (2^b - 1)/2 for a
+// zero-mean matrix: a uniform code then averages the min back to zero, so no
+// common term runs through every row of a decoder. Rows are independent streams, so the fill
 // runs in parallel and stays deterministic.
 static void fill_quant(const plan_t * p, uint64_t seed, int tidx, uint8_t * const planes[SSF_MAX_PLANES],
                        uint16_t * sd, uint8_t * sq, uint16_t * md, uint8_t * mq, float sigma) {
@@ -312,7 +315,7 @@ static void fill_quant(const plan_t * p, uint64_t seed, int tidx, uint8_t * cons
     int pb[SSF_MAX_PLANES];
     const int np = ssf_flat_planes(nb, pb);
     const float qmax = (float) ((1 << (nb - 1)) - 1);
-    const float zp = (float) (1 << (nb - 1));
+    const float zp = p->zero_mean ? 0.5f * (float) ((1 << nb) - 1) : (float) (1 << (nb - 1));
     #pragma omp parallel
     {
         uint8_t * code = malloc((size_t) cols);
@@ -489,35 +492,35 @@ int ssf_synth_model(const char * path, const ssf_synth_spec * sp, char * why, in
     const int E = (int) sp->n_embd, F = (int) sp->n_ff, b = sp->nbits;
     plan_list l = { 0 };
     int pk = 0;   // permutation keys: members of one shared-activation group share one
-    add_quant(&l, "token_embd.weight", (int) sp->n_vocab, E, b, pk++);
-    if (!sp->tied) add_quant(&l, "output.weight", (int) sp->n_vocab, E, b, pk++);
+    add_quant(&l, "token_embd.weight", (int) sp->n_vocab, E, b, pk++, sp->zero_mean);
+    if (!sp->tied) add_quant(&l, "output.weight", (int) sp->n_vocab, E, b, pk++, sp->zero_mean);
     add_f32(&l, "output_norm.weight", E, 0, 0.02f);
     for (int L = 0; L < (int) sp->n_layer; L++) {
         add_f32(&l, sdup("blk.%d.attn_norm.weight", L), E, 0, 0.02f);
         const int kqkv = pk++;
-        add_quant(&l, sdup("blk.%d.attn_q.weight", L), nq, E, b, kqkv);
-        add_quant(&l, sdup("blk.%d.attn_k.weight", L), nkv, E, b, kqkv);
-        add_quant(&l, sdup("blk.%d.attn_v.weight", L), nkv, E, b, kqkv);
+        add_quant(&l, sdup("blk.%d.attn_q.weight", L), nq, E, b, kqkv, sp->zero_mean);
+        add_quant(&l, sdup("blk.%d.attn_k.weight", L), nkv, E, b, kqkv, sp->zero_mean);
+        add_quant(&l, sdup("blk.%d.attn_v.weight", L), nkv, E, b, kqkv, sp->zero_mean);
         if (sp->qkv_bias) {
             add_f32(&l, sdup("blk.%d.attn_q.bias", L), nq, 1, 0.02f);
             add_f32(&l, sdup("blk.%d.attn_k.bias", L), nkv, 1, 0.02f);
             add_f32(&l, sdup("blk.%d.attn_v.bias", L), nkv, 1, 0.02f);
         }
-        add_quant(&l, sdup("blk.%d.attn_output.weight", L), E, nq, b, pk++);
+        add_quant(&l, sdup("blk.%d.attn_output.weight", L), E, nq, b, pk++, sp->zero_mean);
         add_f32(&l, sdup("blk.%d.ffn_norm.weight", L), E, 0, 0.02f);
         if (sp->n_expert) {
             add_f32(&l, sdup("blk.%d.ffn_gate_inp.weight", L), sp->n_expert * E, 1, sp->router_sigma);
             for (int e = 0; e < sp->n_expert; e++) {
                 const int kgu = pk++;
-                add_quant(&l, sdup("blk.%d.ffn_gate.%d.weight", L, e), F, E, b, kgu);
-                add_quant(&l, sdup("blk.%d.ffn_up.%d.weight", L, e), F, E, b, kgu);
-                add_quant(&l, sdup("blk.%d.ffn_down.%d.weight", L, e), E, F, b, pk++);
+                add_quant(&l, sdup("blk.%d.ffn_gate.%d.weight", L, e), F, E, b, kgu, sp->zero_mean);
+                add_quant(&l, sdup("blk.%d.ffn_up.%d.weight", L, e), F, E, b, kgu, sp->zero_mean);
+                add_quant(&l, sdup("blk.%d.ffn_down.%d.weight", L, e), E, F, b, pk++, sp->zero_mean);
             }
         } else {
             const int kgu = pk++;
-            add_quant(&l, sdup("blk.%d.ffn_gate.weight", L), F, E, b, kgu);
-            add_quant(&l, sdup("blk.%d.ffn_up.weight", L), F, E, b, kgu);
-            add_quant(&l, sdup("blk.%d.ffn_down.weight", L), E, F, b, pk++);
+            add_quant(&l, sdup("blk.%d.ffn_gate.weight", L), F, E, b, kgu, sp->zero_mean);
+            add_quant(&l, sdup("blk.%d.ffn_up.weight", L), F, E, b, kgu, sp->zero_mean);
+            add_quant(&l, sdup("blk.%d.ffn_down.weight", L), E, F, b, pk++, sp->zero_mean);
         }
     }
     const int ok = write_plan(path, &h, &l, sp->seed, sp->random_perm, sp->step_sigma, why, nwhy);
@@ -537,7 +540,7 @@ int ssf_synth_matrix(const char * path, int rows, int cols, int nbits, int rando
     base_header(&h);
     h.n_layer = 0; h.n_embd = (uint32_t) cols; h.n_head = 1; h.n_head_kv = 1;
     plan_list l = { 0 };
-    add_quant(&l, "w", rows, cols, nbits, 0);
+    add_quant(&l, "w", rows, cols, nbits, 0, 0);
     const int ok = write_plan(path, &h, &l, seed, random_perm, step_sigma, why, nwhy);
     free(l.v);
     return ok;

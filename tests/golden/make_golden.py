@@ -68,7 +68,7 @@ def decoder_vectors(tmp):
                    qkv_bias=True, random_perm=True, seed=7)
     m = ob.RefModel(p, 32, threads=1)
     toks, logits = [5], []
-    for pos in range(6):
+    for pos in range(16):
         lg = m.forward(toks[-1], pos)
         logits.append(lg)
         toks.append(int(np.argmax(lg)))
