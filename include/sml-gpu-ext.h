@@ -29,6 +29,17 @@ uint64_t sml_gpu_weight_bytes(void);
 // Last failure message.
 const char * sml_gpu_last_error(void);
 
+// Exact mode: with SML_EXACT=1 in the environment at sml_gpu_open, every
+// kernel of the step follows the float order of the reference's x86 build
+// (sml_forward, sml/sml-run.c:3243-3523): Q4/Q8 GEMV lanes and FMAs,
+// serial sums of squares, attention scores, softmax sum and P.V as serial
+// chains, the C library's expf, the SiLU polynomial. Logits then equal the
+// reference's CPU path bit for bit, so greedy ids are identical for any
+// number of steps. It is slower (the serial chains are latency-bound), reads
+// prompts a token at a time and serves one sequence. Returns 1 when the open
+// model runs exact, else 0.
+int sml_gpu_exact(void);
+
 // ---------------------------------------------------------------- several sequences
 // The multi-sequence step sml-batched drives on the CPU through
 // sml_forward_multi (sml/sml-run.h:290-294, sml/sml-batched.c:82-130), with

@@ -26,6 +26,13 @@ int          sml_hip_memset(void * p, int value, size_t n);
 int          sml_hip_sync(void);
 // Test hook: make the n-th HIP call from now fail (n < 0 disables).
 void         sml_hip_fail_after(long n);
+// Exact mode on (1) or off (0) for the launches below: Q4/Q8 GEMVs, norms,
+// attention and the MoE router then follow the float order of the reference's
+// x86 build (sml/sml-kernel.c:572-727,836-866; sml/sml-run.c:147-152,180-287,
+// 339-372,393-426,3075-3080), so their outputs equal its CPU path bit for bit.
+// No counterpart in the reference's GPU ABI, whose kernels it grades against
+// the CPU with a tolerance (sml/sml-gpu-fwd.c:2565-2601).
+void         sml_hip_set_exact(int on);
 
 // ------------------------------------------------------------ matrices
 // A quantized FLAT matrix resident in HBM (the file's planes and fields;

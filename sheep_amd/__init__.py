@@ -47,6 +47,7 @@ _SIGS = [
     ("sml_gpu_slots", c_int, [c_int]),
     ("sml_gpu_prefill_slot", P(c_float), [c_int, P(c_int), c_int, c_int]),
     ("sml_gpu_step_multi", c_int, [P(c_int), P(c_int), P(c_int), c_int, c_void_p]),
+    ("sml_gpu_exact", c_int, []),
     ("sml_hip_init", c_int, [c_int, c_char_p, c_int]),
     ("sml_hip_last_error", c_char_p, []),
     ("sml_hip_malloc", c_void_p, [c_size_t]),
@@ -56,6 +57,7 @@ _SIGS = [
     ("sml_hip_memset", c_int, [c_void_p, c_int, c_size_t]),
     ("sml_hip_sync", c_int, []),
     ("sml_hip_fail_after", None, [c_long]),
+    ("sml_hip_set_exact", None, [c_int]),
     ("sml_hip_mat_upload", c_void_p, [P(c_void_p), c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int]),
     ("sml_hip_mat_from_file", c_void_p, [c_char_p, c_char_p]),
     ("sml_hip_mat_free", None, [c_void_p]),
@@ -281,13 +283,26 @@ def synth_matrix(path, rows, cols, nbits=4, random_perm=False, step_sigma=0.02, 
 class Decoder:
     """The sml-gpu.h forward pass: one model per process."""
 
-    def __init__(self, path, n_ctx=4096, gpu_layers=0):
+    def __init__(self, path, n_ctx=4096, gpu_layers=0, exact=False):
+        """exact: open in exact mode (SML_EXACT=1 for the open), where every
+        kernel follows the reference CPU path's float order and the logits
+        equal it bit for bit."""
         why = ctypes.create_string_buffer(1024)
-        if not lib().sml_gpu_open(str(path).encode(), n_ctx, 1, gpu_layers, why, 1024):
+        old = os.environ.get("SML_EXACT")
+        os.environ["SML_EXACT"] = "1" if exact else "0"
+        try:
+            ok = lib().sml_gpu_open(str(path).encode(), n_ctx, 1, gpu_layers, why, 1024)
+        finally:
+            if old is None:
+                del os.environ["SML_EXACT"]
+            else:
+                os.environ["SML_EXACT"] = old
+        if not ok:
             raise HipError(f"sml_gpu_open: {why.value.decode(errors='replace')}")
         of = c_int()
         self.n_layer = lib().sml_gpu_layers(ctypes.byref(of))
         self.n_ctx = n_ctx
+        self.exact = bool(lib().sml_gpu_exact())
 
     def prompt_mode(self, level):
         """How prefill reads a prompt: 0 a token at a time, 1 batched with

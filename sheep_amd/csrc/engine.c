@@ -71,6 +71,7 @@ static struct {
     float last_ms;
     uint64_t weight_bytes;
     int prompt_level;
+    int exact;                 // SML_EXACT=1 at open: every kernel in the reference's float order
     void * dev[4096];          // every device allocation, freed at close
     int ndev;
     sml_hip_mat * mats[8192];
@@ -197,7 +198,7 @@ static void launch_layer(int L) {
     }
     // with an identity o-proj permutation the attention kernel quantizes its
     // own output for the o GEMV; otherwise a gather + quantize follows it
-    const int fuse_q = y->perm_o < 0;
+    const int fuse_q = y->perm_o < 0 && !G.exact;
     uint16_t * kc = G.cur_slot ? G.kcs[G.cur_slot] : G.kc, * vc = G.cur_slot ? G.vcs[G.cur_slot] : G.vc;
     op_attention(G.st, G.q, G.k, G.v, kc + (size_t) L * G.n_ctx * kvd, vc + (size_t) L * G.n_ctx * kvd,
                  G.rc, G.rs, G.pos, G.H, G.KV, G.hd, G.n_ctx, G.part, G.att,
@@ -295,6 +296,7 @@ static void release(void) {
     hx.jb = outer;
     free(G.L);
     memset(&G, 0, sizeof G);
+    ops_set_exact(0);
 }
 
 void sml_gpu_close(void) { release(); }
@@ -462,6 +464,15 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     G.hs = dalloc((size_t) G.F / 32 * 4);
     G.hsum = dalloc((size_t) G.F / 32 * 4);
     G.fuse = env_int("SML_FUSE", 3);
+    // exact mode: the reference's float order throughout (sml_forward,
+    // sml/sml-run.c:3243-3523), so logits equal its CPU path bit for bit.
+    // Norms run as their own launches (serial sums), prompts a token at a time.
+    G.exact = env_int("SML_EXACT", 0) != 0;
+    ops_set_exact(G.exact);
+    if (G.exact) {
+        G.fuse = 0;
+        if (n_ctx > 16384) hx_failf("exact mode holds at most 16384 positions");
+    }
     const size_t kvn = (size_t) G.n_layer * n_ctx * G.KV * G.hd;
     G.kc = dalloc(kvn * 2);
     G.vc = dalloc(kvn * 2);
@@ -478,7 +489,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     HX(hipDeviceSynchronize());
     // prompt reading: batched (exact) unless SML_GPU_PP=0, as the reference's
     // open does (sml/sml-gpu-fwd.c:2371-2375)
-    G.prompt_level = env_int("SML_GPU_PP", 1) == 0 ? 0 : 1;
+    G.prompt_level = env_int("SML_GPU_PP", 1) == 0 || G.exact ? 0 : 1;
     G.rows_ok = -1;
     G.use_graph = env_int("SML_GRAPH", 1) != 0;
     if (G.use_graph) {
@@ -582,6 +593,7 @@ int sml_gpu_generate(int tok, int pos, int n, int * out) {
 float sml_gpu_last_ms(void) { return G.open ? G.last_ms : -1.0f; }
 uint64_t sml_gpu_weight_bytes(void) { return G.open ? G.weight_bytes : 0; }
 const char * sml_gpu_last_error(void) { return hx.err; }
+int sml_gpu_exact(void) { return G.open && G.exact; }
 
 int sml_gpu_layers(int * of) {
     if (of) *of = G.open ? G.n_layer : 0;
@@ -592,7 +604,7 @@ int sml_gpu_layers(int * of) {
 // (the default); 2: batched with the Q4 products on MFMA. As the reference's
 // (sml/sml-gpu-fwd.c:2420-2423): 2 = every batched kernel, 1 = without the
 // matrix-core one, 0 = token at a time.
-void sml_gpu_prompt_mode(int level) { G.prompt_level = level <= 0 ? 0 : level >= 2 ? 2 : 1; }
+void sml_gpu_prompt_mode(int level) { G.prompt_level = level <= 0 || G.exact ? 0 : level >= 2 ? 2 : 1; }
 
 int sml_gpu_decode_cpu(int on) { (void) on; return 0; }
 
@@ -687,6 +699,7 @@ static void rows_alloc(void) {
 int sml_gpu_slots(int ns) {
     if (!G.open || ns < 1 || ns > MAX_SLOTS) return 0;
     HX_ENTRY(0);
+    if (G.exact) hx_failf("exact mode decodes one sequence");
     if (!rows_check()) {
         for (int L = 0; L < G.n_layer; L++) {
             eng_layer * y = &G.L[L];

@@ -63,6 +63,7 @@ typedef struct {
     float         * scale[3];
     int32_t       * sums[3];
     int             per256;       // 1: one scale per 256 values (sml_quantize_act_sb)
+    int             exact;        // 1: the sum of squares as the reference's serial chain of double FMAs
 } sml_knormq2;
 
 // Gather + optional residual add + optional RMSNorm + per-group int8 quantize.
@@ -80,6 +81,7 @@ typedef struct {
     int32_t       * sums[3];
     float         * normed;       // optional copy of the normalised vector (pre-gather), or NULL
     int             per256;       // 1: one scale per 256 values (reference prompt regime)
+    int             exact;        // 1: the sum of squares as the reference's serial chain of double FMAs
 } sml_knormq;
 
 // Integer codes of rows [row0, row0+nrows) of one matrix, one byte per weight.
@@ -136,6 +138,21 @@ typedef struct {
     // increasing) and share each split's K/V tile
     int tpw, nseq;
 } sml_kattn;
+
+// Decode attention in the reference's float order (exact mode): RoPE of q and
+// k in place and the fp16 KV write (sml_rope_exact), then one workgroup per
+// query head (sml_attn_exact).
+typedef struct {
+    float * q;                    // n_head * hd after bias; rotated in place
+    float * k;                    // n_kv * hd after bias; rotated in place
+    const float * v;              // n_kv * hd after bias
+    uint16_t * kc, * vc;          // this layer's cache, [n_ctx][n_kv * hd]
+    const float * cos_t, * sin_t; // [n_ctx][hd / 2]
+    const int32_t * pos;
+    float * out;                  // n_head * hd
+    int n_head, n_kv, n_ctx;
+    float inv;                    // 1 / sqrtf(hd)
+} sml_kattnx;
 
 
 typedef struct {
@@ -220,6 +237,7 @@ typedef struct {
     int32_t * slot;               // [T][k] position of (t, j) in its expert's list
     int32_t * count;              // [nexp] tokens per expert
     int32_t * list;               // [nexp][mmax] entries t*k + j, by token then choice
+    int exact;                    // 1: each router dot as the reference's serial chain of double FMAs
 } sml_kmoe_route;
 
 // Per-32 (or per-256) int8 quantization of activation rows into per-expert slots:

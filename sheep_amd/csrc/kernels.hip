@@ -194,6 +194,71 @@ __device__ __forceinline__ int quant1(float v, float is) {
     return t > 127 ? 127 : t < -127 ? -127 : t;
 }
 
+// SiLU as the reference's x86 build computes it (sml_exp_ps + silu_mul,
+// sml/sml-run.c:393-426): the argument clamped to [-88, 88], f = x*log2(e),
+// r = f rounded half-even, 2^(f-r) by a degree-5 Horner chain of FMAs, and
+// 1 + p*2^r folded into one FMA (how that build's compiler contracts it);
+// then g / d. Contraction is off so f and f - r round as written.
+__device__ __forceinline__ float silu_ref(float g) {
+    #pragma clang fp contract(off)
+    float x = 0.0f - g;
+    x = fminf(fmaxf(x, -88.0f), 88.0f);
+    const float f = x * 1.44269504088896341f;
+    const float r = __builtin_rintf(f);
+    const float t = f - r;
+    float p = __builtin_fmaf(1.3697664e-3f, t, 8.3013611e-3f);
+    p = __builtin_fmaf(p, t, 5.5826318e-2f);
+    p = __builtin_fmaf(p, t, 2.4022652e-1f);
+    p = __builtin_fmaf(p, t, 6.9314718e-1f);
+    p = __builtin_fmaf(p, t, 1.0f);
+    const float sc = __builtin_bit_cast(float, ((int) r + 127) << 23);
+    return g / __builtin_fmaf(p, sc, 1.0f);
+}
+
+// expf of the C library the reference runs on (glibc 2.35 on x86-64 with FMA),
+// restated from its published algorithm (ARM optimized-routines expf, in
+// glibc since 2.27): x*32/ln2 = k + r in double (k rounded half-even through
+// the 1.5*2^52 shift, both products fused), 2^(k/32) from a 32-entry table of
+// 2^(i/32) with the exponent folded in, 2^(r/32) by a cubic, then one
+// rounding to float. Compared on the CPU over every float <= 0 against the
+// library, it gives the same bits on all of them; only x <= 0 is used here
+// (softmax and routing weights), where anything below -103.97 is 0.
+// 2^(i/32) as double bits, less i << 47 (the exponent step of the index)
+__constant__ unsigned long long EXPF_TAB[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull };
+
+__device__ __forceinline__ float expf_ref(float x) {
+    #pragma clang fp contract(off)
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 C2 = 0x1.62e42ff0c52d6p-1 / 32, InvLn2N = 0x1.71547652b82fep+0 * 32, Shift = 0x1.8p+52;
+    const double xd = (double) x;
+    double kd = __builtin_fma(InvLn2N, xd, Shift);
+    const unsigned long long ki = __builtin_bit_cast(unsigned long long, kd);
+    kd -= Shift;
+    const double r = __builtin_fma(InvLn2N, xd, -kd);
+    const double s = __builtin_bit_cast(double, EXPF_TAB[ki % 32] + (ki << 47));
+    const double z = __builtin_fma(C0, r, C1), r2 = r * r;
+    double y = __builtin_fma(C2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    return (float) (y * s);
+}
+
+// Order LDS traffic among the lanes of one wave (its LDS operations execute
+// in order; this keeps the compiler from moving them across the point).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Fused activation prologue: RMSNorm (double sum of squares, out = x*sc*w,
 // sml/sml-run.c:147-152), gather through perm, and the per-32 quantization
 // (sml/sml-kernel.c:86-106) of the whole input vector, into the workgroup's
@@ -285,7 +350,7 @@ __device__ __forceinline__ float seg_sum(float v) {
     return v;
 }
 
-template <int NB, int RB, int NI, int WG, bool NT, int AM, bool SW, bool HQ, int LPR = 64>
+template <int NB, int RB, int NI, int WG, bool NT, int AM, bool SW, bool HQ, int LPR = 64, bool EX = false>
 __device__ void gemv_body(const sml_kgemv & a) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8;
@@ -364,6 +429,22 @@ __device__ void gemv_body(const sml_kgemv & a) {
     float acc[RB];
     #pragma unroll
     for (int s = 0; s < RB; s++) acc[s] = 0.0f;
+    // EX: the reference's float order (sml/sml-kernel.c:572-727,836-866).
+    // Every group's two products go through LDS to the lane that owns the
+    // group's position in a superblock: lane 8*rw + j of the wave runs row
+    // rw's chain j, v_j = fma(wsc, s*dot, v_j); v_j = fma(wmin, s*sum, v_j)
+    // over the superblocks in order (cm; ct for a trailing half superblock,
+    // whose four lanes the reference keeps apart and adds last).
+    static_assert(!EX || AM == 0, "the exact form reads a quantized activation");
+    const int nblk8 = (ng / 8) * 8;
+    float4 * exb = nullptr;
+    float * ext = nullptr;
+    float cm = 0.0f, ct = 0.0f;
+    if constexpr (EX) {
+        const size_t base = ((size_t) n + 8u * (size_t) ng + 15u) & ~(size_t) 15u;
+        exb = (float4 *) (lds + base) + (size_t) wave * (NI * RB * 64);
+        ext = (float *) (lds + base + (size_t) (WG / 64) * NI * RB * 64 * 16) + wave * (RB * SUB);
+    }
     bool staged = false;
     for (int c0 = 0; c0 < ng; c0 += LPR * NI) {
         // 3. every weight load of this lane for NI chunks of RB rows, with no branches
@@ -420,13 +501,56 @@ __device__ void gemv_body(const sml_kgemv & a) {
                 const uint32_t f = fqv[i][s], d2 = fdv[i][s];
                 const float wsc = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
                 const float wmn = h2f((uint16_t) (d2 >> 16)) * ((float) (f >> 8) - 127.0f);
-                acc[s] += wsc * (sc.x * (float) dot);
-                acc[s] += wmn * sc.y;
+                if constexpr (EX) {
+                    exb[(i * RB + s) * 64 + u * LPR + l] = make_float4(wsc, sc.x * (float) dot, wmn, sc.y);
+                } else {
+                    acc[s] += wsc * (sc.x * (float) dot);
+                    acc[s] += wmn * sc.y;
+                }
             }
         }
+        if constexpr (EX) {
+            wave_lds_sync();
+            const int rw = lane >> 3, j = lane & 7;
+            if (rw < RB * SUB) {
+                const int s = rw / SUB, uu = rw % SUB;
+                #pragma unroll
+                for (int i = 0; i < NI; i++) {
+                    #pragma unroll
+                    for (int t = 0; t < LPR / 8; t++) {
+                        const int g = c0 + i * LPR + 8 * t + j;
+                        if (g < ng) {
+                            const float4 w4 = exb[(i * RB + s) * 64 + uu * LPR + 8 * t + j];
+                            if (g < nblk8) { cm = __builtin_fmaf(w4.x, w4.y, cm); cm = __builtin_fmaf(w4.z, w4.w, cm); }
+                            else { ct = __builtin_fmaf(w4.x, w4.y, ct); ct = __builtin_fmaf(w4.z, w4.w, ct); }
+                        }
+                    }
+                }
+            }
+            wave_lds_sync();
+        }
     }
-    #pragma unroll
-    for (int s = 0; s < RB; s++) acc[s] = seg_sum<LPR>(acc[s]);
+    if constexpr (EX) {
+        // fold each row's 8 lanes as the reference does: ((v0+v4)+(v1+v5)) +
+        // ((v2+v6)+(v3+v7)), then the trailing four (t0+t1)+(t2+t3), added last
+        float v = cm + dpp_f<0x104>(cm);              // lanes j < 4: v_j + v_(j+4)
+        v = v + dpp_f<0xB1>(v);                        // lanes 0, 2: s0+s1, s2+s3
+        v = v + dpp_f<0x4E>(v);                        // lane 0: (s0+s1)+(s2+s3)
+        if (ng != nblk8) {
+            float w = ct + dpp_f<0xB1>(ct);
+            w = w + dpp_f<0x4E>(w);
+            v = v + w;
+        }
+        const int rw = lane >> 3;
+        if ((lane & 7) == 0 && rw < RB * SUB) ext[rw] = v;
+        wave_lds_sync();
+        #pragma unroll
+        for (int s = 0; s < RB; s++) acc[s] = ext[s * SUB + u];
+    }
+    if constexpr (!EX) {
+        #pragma unroll
+        for (int s = 0; s < RB; s++) acc[s] = seg_sum<LPR>(acc[s]);
+    }
     if constexpr (HQ) {
         // WG/16 consecutive outputs per workgroup (RB/2 gate/up pairs per
         // wave, whole groups of 32): h = silu(g)*u, then its per-32
@@ -442,7 +566,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
                     float g = acc[s], u = acc[s + 1];
                     if (a.m[0].bias) g += a.m[0].bias[row];
                     if (a.m[1].bias) u += a.m[1].bias[row];
-                    h = (g / (1.0f + expf(-g))) * u;             // sml/sml-run.c:451-454
+                    h = silu_ref(g) * u;                          // sml/sml-run.c:416-426
                     a.m[0].y[row] = h;
                 }
                 hb[wave * RPW + (s >> 1) * SUB + u] = h;
@@ -472,7 +596,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
             float g = acc[s], u = acc[s + 1];
             if (a.m[0].bias) g += a.m[0].bias[row];
             if (a.m[1].bias) u += a.m[1].bias[row];
-            a.m[0].y[row] = (g / (1.0f + expf(-g))) * u;   // sml/sml-run.c:451-454
+            a.m[0].y[row] = silu_ref(g) * u;               // sml/sml-run.c:416-426
         }
     } else {
         #pragma unroll
@@ -539,6 +663,23 @@ __device__ void gemv_body(const sml_kgemv & a) {
     GEMV_KERNEL_H(NB, 2) GEMV_KERNEL_H(NB, 4) GEMV_WIDE(NB)
 GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH(7) GEMV_WIDTH(8)
 
+// The exact forms (suffix _x, Q4 and Q8): the reference's float order per row
+// (gemv_body EX), for every shape pick_shape gives an unfused launch.
+#define GEMV_KERNEL_X(NB, RB, NI)                                                                           \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_r##RB##_i##NI##_x(const sml_kgemv a) { \
+        gemv_body<NB, RB, NI, 256, true, 0, false, false, 64, true>(a);                                     \
+    }
+#define GEMV_KERNEL_SX(NB, RB, NI)                                                                          \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_s_r##RB##_i##NI##_x(const sml_kgemv a) { \
+        gemv_body<NB, RB, NI, 256, true, 0, true, false, 64, true>(a);                                      \
+    }
+#define GEMV_EXACT(NB)                                                                                      \
+    GEMV_KERNEL_X(NB, 1, 2) GEMV_KERNEL_X(NB, 1, 4) GEMV_KERNEL_X(NB, 2, 1) GEMV_KERNEL_X(NB, 2, 2)         \
+    GEMV_KERNEL_X(NB, 2, 4) GEMV_KERNEL_X(NB, 4, 1) GEMV_KERNEL_X(NB, 4, 2) GEMV_KERNEL_X(NB, 4, 4)         \
+    GEMV_KERNEL_SX(NB, 2, 1) GEMV_KERNEL_SX(NB, 2, 2) GEMV_KERNEL_SX(NB, 2, 4)                              \
+    GEMV_KERNEL_SX(NB, 4, 1) GEMV_KERNEL_SX(NB, 4, 2) GEMV_KERNEL_SX(NB, 4, 4)
+GEMV_EXACT(4) GEMV_EXACT(8)
+
 // ---------------------------------------------------------------- norm + quantize
 //
 // Residual add, RMSNorm with a double sum of squares (sml/sml-run.c:147-152),
@@ -547,6 +688,23 @@ GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH
 // and square root and round-half-even conversion, so the int8 codes, scales
 // and sums equal the reference's bit for bit on the same input.
 #define NORMQ_THREADS 1024
+
+// The sum of squares as the reference build computes it (sml/sml-run.c:
+// 147-152, a serial loop its compiler turns into double FMAs): one lane, in
+// order. Loads run ahead of the dependent chain in blocks of 16.
+__device__ __noinline__ double serial_ss(const float * x, int n) {
+    double ss = 0.0;
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+        float v[16];
+        #pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = x[i + j];
+        #pragma unroll
+        for (int j = 0; j < 16; j++) ss = __builtin_fma((double) v[j], (double) v[j], ss);
+    }
+    for (; i < n; i++) ss = __builtin_fma((double) x[i], (double) x[i], ss);
+    return ss;
+}
 
 extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_knormq a) {
     extern __shared__ __align__(16) float sx[];
@@ -569,7 +727,14 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
         double tot = 0.0;
-        for (int w = 0; w < NORMQ_THREADS / WAVE; w++) tot += red[w];
+        if (a.exact) {
+            // the reference build's loop: ss = fma(x_i, x_i, ss) in order
+            if (tid == 0) red[0] = serial_ss(sx, n);
+            __syncthreads();
+            tot = red[0];
+        } else {
+            for (int w = 0; w < NORMQ_THREADS / WAVE; w++) tot += red[w];
+        }
         // IEEE division and square root: hipcc's default for HIP is the correctly
         // rounded fp32 divide/sqrt, which the bit-exact parity tests rely on
         const float sc = 1.0f / sqrtf((float) (tot / (double) n) + a.eps);
@@ -640,7 +805,13 @@ extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a
         for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
-        const double tot = red[0] + red[1] + red[2] + red[3];
+        double tot = red[0] + red[1] + red[2] + red[3];
+        if (a.exact) {
+            __syncthreads();
+            if (tid == 0) red[0] = serial_ss(x, n);
+            __syncthreads();
+            tot = red[0];
+        }
         sc = 1.0f / sqrtf((float) (tot / (double) n) + a.eps);
     }
     const int j = blockIdx.x * 256 + tid;           // element (group j/32) of every output
@@ -774,13 +945,16 @@ __device__ __forceinline__ void load_f8(const float * p, float (&f)[8]) {
 }
 // Rotate the lane's 8 dims by the (d, d+64) pair rule of sml/sml-run.c:363-368:
 // lanes 0-7 of a row hold the first halves, lanes 8-15 the second, and
-// row_ror:8 brings each lane its partner.
+// row_ror:8 brings each lane its partner. The products fuse as the
+// reference's x86 build fuses them: x0*c - x1*s = fma(x0, c, -(x1*s)),
+// x0*s + x1*c = fma(x0, s, x1*c).
 __device__ __forceinline__ void rope8(float (&x)[8], const float (&c)[8], const float (&s)[8], bool lo) {
     float p[8];
     #pragma unroll
     for (int e = 0; e < 8; e++) p[e] = dpp_f<0x128>(x[e]);
     #pragma unroll
-    for (int e = 0; e < 8; e++) x[e] = lo ? x[e] * c[e] - p[e] * s[e] : p[e] * s[e] + x[e] * c[e];
+    for (int e = 0; e < 8; e++)
+        x[e] = lo ? __builtin_fmaf(x[e], c[e], -(p[e] * s[e])) : __builtin_fmaf(p[e], s[e], x[e] * c[e]);
 }
 // Reduce-scatter of four values over the 4 rows of a wave with the gfx950
 // row swaps (v_permlane16_swap: rows 1 and 3 of the first operand trade
@@ -1235,6 +1409,110 @@ extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn 
     if ((d & 31) == 0) { a.s_out[ob / 32 + g] = s; a.u_out[ob / 32 + g] = sum; }
 }
 
+// ---------------------------------------------------------------- attention in the reference's order
+//
+// The exact mode's decode attention: the float operations of the
+// reference's x86 build, in its order (sml/sml-run.c:180-287,339-372),
+// so the output equals its bit for bit. First sml_rope_exact rotates q and
+// k in place with the fused products of that build and writes the position's
+// fp16 K and V rows. Then sml_attn_exact, one workgroup per query head:
+// - score of position t: eight FMA lanes over the head's dims (lane j takes
+//   dims j, j+8, ...), folded ((l0+l4)+(l1+l5)) + ((l2+l6)+(l3+l7)), times
+//   1/sqrt(hd); positions in parallel;
+// - the maximum, then expf of each score less it (expf_ref: the C library's
+//   bits), then their sum as one serial float chain, one reciprocal and the
+//   products;
+// - output dim d: one FMA chain over the positions in order, p_t*v_t[d] + o.
+// The two serial chains make this latency-bound (about 8 cycles per position
+// each), which is why it is a mode and not the decode path.
+extern "C" __global__ __launch_bounds__(256) void sml_rope_exact(const sml_kattnx a) {
+    const int pos = *a.pos, kvd = a.n_kv * HD;
+    const float * cs = a.cos_t + (size_t) pos * (HD / 2), * sn = a.sin_t + (size_t) pos * (HD / 2);
+    uint16_t * kr = a.kc + (size_t) pos * kvd, * vr = a.vc + (size_t) pos * kvd;
+    for (int idx = threadIdx.x; idx < (a.n_head + a.n_kv) * (HD / 2); idx += 256) {
+        #pragma clang fp contract(off)
+        const int hh = idx / (HD / 2), i = idx % (HD / 2);
+        const bool isk = hh >= a.n_head;
+        float * v = isk ? a.k + (size_t) (hh - a.n_head) * HD : a.q + (size_t) hh * HD;
+        const float x0 = v[i], x1 = v[i + HD / 2];
+        const float y0 = __builtin_fmaf(x0, cs[i], -(x1 * sn[i]));
+        const float y1 = __builtin_fmaf(x0, sn[i], x1 * cs[i]);
+        v[i] = y0;
+        v[i + HD / 2] = y1;
+        if (isk) {
+            const int o = (hh - a.n_head) * HD + i;
+            kr[o] = f2h(y0);
+            kr[o + HD / 2] = f2h(y1);
+        }
+    }
+    for (int i = threadIdx.x; i < kvd; i += 256) vr[i] = f2h(a.v[i]);
+}
+
+extern "C" __global__ __launch_bounds__(256) void sml_attn_exact(const sml_kattnx a) {
+    #pragma clang fp contract(off)
+    extern __shared__ float pr[];                  // [n_ctx] scores, then weights
+    __shared__ float qs[HD];
+    __shared__ float red[4];
+    __shared__ float tot;
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int kh = h / (a.n_head / a.n_kv), pos = *a.pos, n = pos + 1;
+    const size_t stride = (size_t) a.n_kv * HD;
+    if (tid < HD) qs[tid] = a.q[(size_t) h * HD + tid];
+    __syncthreads();
+    const uint16_t * kb = a.kc + (size_t) kh * HD;
+    for (int t = tid; t < n; t += 256) {
+        const v4u * kr = (const v4u *) (kb + (size_t) t * stride);
+        float l[8] = { 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f };
+        #pragma unroll
+        for (int i = 0; i < HD / 8; i++) {
+            float kf[8];
+            unpack_h8(kr[i], kf);
+            #pragma unroll
+            for (int j = 0; j < 8; j++) l[j] = __builtin_fmaf(qs[8 * i + j], kf[j], l[j]);
+        }
+        pr[t] = (((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]))) * a.inv;
+    }
+    __syncthreads();
+    float m = -__builtin_inff();
+    for (int t = tid; t < n; t += 256) m = fmaxf(m, pr[t]);
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int t = tid; t < n; t += 256) pr[t] = expf_ref(pr[t] - m);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        int t = 0;
+        for (; t + 16 <= n; t += 16) {
+            float e[16];
+            #pragma unroll
+            for (int j = 0; j < 16; j++) e[j] = pr[t + j];
+            #pragma unroll
+            for (int j = 0; j < 16; j++) sum = sum + e[j];
+        }
+        for (; t < n; t++) sum = sum + pr[t];
+        tot = sum;
+    }
+    __syncthreads();
+    const float iv = 1.0f / tot;
+    for (int t = tid; t < n; t += 256) pr[t] = pr[t] * iv;
+    __syncthreads();
+    if (tid >= HD) return;
+    const uint16_t * vb = a.vc + (size_t) kh * HD + tid;
+    float o = 0.0f;
+    int t = 0;
+    for (; t + 16 <= n; t += 16) {
+        float vv[16];
+        #pragma unroll
+        for (int j = 0; j < 16; j++) vv[j] = h2f(vb[(size_t) (t + j) * stride]);
+        #pragma unroll
+        for (int j = 0; j < 16; j++) o = __builtin_fmaf(pr[t + j], vv[j], o);
+    }
+    for (; t < n; t++) o = __builtin_fmaf(pr[t], h2f(vb[(size_t) t * stride]), o);
+    a.out[(size_t) h * HD + tid] = o;
+}
+
 // ---------------------------------------------------------------- argmax
 // First maximum wins (sml/sml-run.c:3539-3544). One workgroup: every thread
 // issues all of its float4 loads (16 per round) before comparing, so the
@@ -1340,7 +1618,7 @@ extern "C" __global__ void sml_advance(const sml_kadvance a) {
 // g = g/(1+exp(-g)) * u  (sml/sml-run.c:451-454)
 extern "C" __global__ void sml_silu_mul(const sml_ksilu a) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < a.n) { const float g = a.g[i]; a.g[i] = (g / (1.0f + expf(-g))) * a.u[i]; }
+    if (i < a.n) a.g[i] = silu_ref(a.g[i]) * a.u[i];
 }
 
 // ---------------------------------------------------------------- calibration
@@ -1543,6 +1821,11 @@ extern "C" __global__ __launch_bounds__(MOE_ROUTE_THREADS) void sml_moe_route(co
         double s = (s0 + s1) + (s2 + s3);
         #pragma unroll
         for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
+        if (a.exact && lane == 0) {
+            // the reference's loop, s = fma(r_i, x_i, s) in order (sml/sml-run.c:3075-3080)
+            s = 0.0;
+            for (int i2 = 0; i2 < a.n; i2++) s = __builtin_fma((double) r[i2], (double) x[i2], s);
+        }
         if (lane == 0) {
             const float v = (float) s + (a.router_b ? a.router_b[e] : 0.0f);
             lg[e] = v;
@@ -1567,14 +1850,14 @@ extern "C" __global__ __launch_bounds__(MOE_ROUTE_THREADS) void sml_moe_route(co
     if (a.moe_flags & 1u) {
         float wj[16];
         double sum = 0.0;
-        for (int j = 0; j < a.k; j++) { wj[j] = expf(lg[sl[j]] - lg[sl[0]]); sum += wj[j]; }
+        for (int j = 0; j < a.k; j++) { wj[j] = expf_ref(lg[sl[j]] - lg[sl[0]]); sum += wj[j]; }
         for (int j = 0; j < a.k; j++) w[j] = (float) (wj[j] / sum);
     } else {
         float mx = lg[0];
         for (int e = 1; e < a.nexp; e++) mx = lg[e] > mx ? lg[e] : mx;
         double sum = 0.0;
-        for (int e = 0; e < a.nexp; e++) sum += expf(lg[e] - mx);
-        for (int j = 0; j < a.k; j++) w[j] = (float) (expf(lg[sl[j]] - mx) / sum);
+        for (int e = 0; e < a.nexp; e++) sum += expf_ref(lg[e] - mx);
+        for (int j = 0; j < a.k; j++) w[j] = (float) (expf_ref(lg[sl[j]] - mx) / sum);
     }
 }
 
@@ -1642,7 +1925,7 @@ extern "C" __global__ __launch_bounds__(256) void sml_moe_combine(const sml_kmoe
     float acc = 0.0f;
     for (int j = 0; j < a.k; j++) {
         const int e = a.sel[t * a.k + j], r = a.slot[t * a.k + j];
-        acc += a.w[t * a.k + j] * a.y[((size_t) e * a.mmax + r) * a.n + i];
+        acc = __builtin_fmaf(a.w[t * a.k + j], a.y[((size_t) e * a.mmax + r) * a.n + i], acc);
     }
     const size_t o = (size_t) t * a.n + i;
     a.out[o] = a.resid ? a.resid[o] + acc : acc;    // the residual add after moe_ffn, sml/sml-run.c:3475-3480
@@ -1782,7 +2065,7 @@ __device__ void gemm_body(const sml_kgemm & a) {
             for (int s = 0; s < RB; s += 2) {
                 if (!valid[s]) continue;
                 const float g = acc[s][t], u = acc[s + 1][t];
-                y[orow[s]] = (g / (1.0f + expf(-g))) * u;     // sml/sml-run.c:451-454
+                y[orow[s]] = silu_ref(g) * u;                  // sml/sml-run.c:416-426
             }
         } else {
             const float * res = a.resid ? a.resid + (abase + t) * a.rows : nullptr;
@@ -2156,7 +2439,7 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
         }
         float * y = a.y + (abase + mr) * a.rows;
         if constexpr (SW) {
-            y[row] = (t[0] / (1.0f + expf(-t[0]))) * t[1];               // sml/sml-run.c:451-454
+            y[row] = silu_ref(t[0]) * t[1];                              // sml/sml-run.c:416-426
         } else {
             float v = t[0];
             if (a.bias) v += a.bias[row];

@@ -23,6 +23,14 @@ int sml_hip_init(int device, char * why, int nwhy) {
 #define OP_BEGIN(fail) HX_ENTRY(fail); if (!hx.inited) hx_init(0)
 
 const char * sml_hip_last_error(void) { return hx.err; }
+
+// Exact mode: launches take the forms that follow the reference's float
+// order (Q4/Q8 GEMVs, norms, attention, router), so decoding equals its CPU
+// path bit for bit.
+static int g_exact;
+void ops_set_exact(int on) { g_exact = on != 0; }
+int ops_exact(void) { return g_exact; }
+void sml_hip_set_exact(int on) { ops_set_exact(on); }
 void sml_hip_fail_after(long n) { hx.fail_after = n; }
 
 void * sml_hip_malloc(size_t n) { OP_BEGIN(NULL); void * p = hx_malloc(n); HX_LEAVE(); return p; }
@@ -261,11 +269,11 @@ void op_normq_rows(hipStream_t st, float * x, const float * resid, const float *
     memset(&a, 0, sizeof a);
     a.x = x; a.resid = resid; a.norm_w = w; a.eps = eps; a.n = n; a.nout = nout;
     for (int i = 0; i < nout; i++) { a.perm[i] = perm[i]; a.q[i] = q[i]; a.scale[i] = scale[i]; a.sums[i] = sums[i]; }
-    a.normed = normed; a.per256 = per256;
+    a.normed = normed; a.per256 = per256; a.exact = g_exact;
     if (!resid && !normed) {
         sml_knormq2 b;
         memset(&b, 0, sizeof b);
-        b.x = x; b.norm_w = w; b.eps = eps; b.n = n; b.nout = nout; b.per256 = per256;
+        b.x = x; b.norm_w = w; b.eps = eps; b.n = n; b.nout = nout; b.per256 = per256; b.exact = g_exact;
         for (int i = 0; i < nout; i++) { b.perm[i] = perm[i]; b.q[i] = q[i]; b.scale[i] = scale[i]; b.sums[i] = sums[i]; }
         hx_launch("sml_normq2", (unsigned) ((n + 255) / 256), (unsigned) rows, 256, 0, st, &b);
         return;
@@ -374,6 +382,19 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
     }
     int rb, ni;
     pick_shape(a.total_rows, cols, nb, swiglu, am, &rb, &ni);
+    if (g_exact && (nb == 4 || nb == 8) && !am) {
+        // the reference's float order: each group's products pass through LDS
+        // (RB*NI KB per wave) to the lanes that run its superblock chains
+        size_t xl = lds + (size_t) 4 * ni * rb * 64 * 16 + (size_t) 4 * rb * 4;
+        while (xl > 65536 && ni > 1) { ni /= 2; xl = lds + (size_t) 4 * ni * rb * 64 * 16 + (size_t) 4 * rb * 4; }
+        if (xl > 65536) hx_failf("exact GEMV of %d columns needs %zu bytes of LDS", cols, xl);
+        const int rows_per_wave = swiglu ? rb / 2 : rb;
+        const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
+        if (swiglu) snprintf(name, sizeof name, "sml_gemv_q%d_s_r%d_i%d_x", nb, rb, ni);
+        else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_x", nb, rb, ni);
+        hx_launch(name, (unsigned) ((waves + 3) / 4), 1, 256, xl, st, &a);
+        return;
+    }
     int wg = 256;
     if (!swiglu && am && env_int("SML_GEMV_WG", 512) != 256) {
         wg = env_int("SML_GEMV_WG", 512) == 1024 ? 1024 : 512;
@@ -506,6 +527,21 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
                   int32_t * u_out) {
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
+    if (g_exact) {
+        // the reference's order: RoPE and the KV write, then a workgroup per
+        // query head with the scores of every position in LDS; the output
+        // stays float (the caller quantizes it for o)
+        if (n_ctx > 16384) hx_failf("exact attention holds at most 16384 positions");
+        if (q_out) hx_failf("exact attention does not quantize its output");
+        sml_kattnx x;
+        memset(&x, 0, sizeof x);
+        x.q = (float *) q; x.k = (float *) k; x.v = v; x.kc = kc; x.vc = vc; x.cos_t = cos_t; x.sin_t = sin_t;
+        x.pos = pos; x.out = out; x.n_head = n_head; x.n_kv = n_kv; x.n_ctx = n_ctx;
+        x.inv = 1.0f / __builtin_sqrtf((float) hd);
+        hx_launch("sml_rope_exact", 1, 1, 256, 0, st, &x);
+        hx_launch("sml_attn_exact", (unsigned) n_head, 1, 256, (size_t) n_ctx * 4, st, &x);
+        return;
+    }
     const int aw = env_int("SML_ATTN_WAVES", 8) == 4 ? 4 : 8;
     const int ch = aw == 4 ? ATTN_CHUNK : attn_split(n_kv, n_ctx);   // the 4-wave form runs splits of 128 only
     const int ns = (n_ctx + ch - 1) / ch;
@@ -1187,6 +1223,7 @@ void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out
     r.x = x; r.router = m->router; r.router_b = m->router_b;
     r.T = T; r.n = m->n_embd; r.nexp = m->nexp; r.k = m->k; r.mmax = m->tmax; r.moe_flags = m->flags;
     r.logits = m->logits; r.sel = m->sel; r.w = m->w; r.slot = m->slot; r.count = m->count; r.list = m->list;
+    r.exact = g_exact;
     hx_launch("sml_moe_route", (unsigned) T, 1, 512, 0, st, &r);
     hx_launch("sml_moe_plan", 1, 1, 64, 0, st, &r);
     sml_kmquant qa;

@@ -23,6 +23,10 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
 sml_hip_mat * mat_from_record(const ssf_file * f, const ssf_record * r);
 void mat_free(sml_hip_mat * m);
 
+// Exact mode (the reference's float order in GEMVs, norms, attention, router)
+void ops_set_exact(int on);
+int ops_exact(void);
+
 void op_normq(hipStream_t st, float * x, const float * resid, const float * w, float eps, int n,
               int nout, const int32_t * const * perm, int8_t * const * q, float * const * scale,
               int32_t * const * sums, float * normed, int per256);

@@ -154,6 +154,22 @@ def test_widths_match_reference(tmpdir_s, nb):
     assert np.abs(y - yr).max() <= 1e-5 * np.abs(yr).max()
 
 
+@needs_ref
+@pytest.mark.parametrize("nb", [4, 8])
+@pytest.mark.parametrize("cols", [128, 384, 1536, 4224])
+def test_q4_q8_gemv_bit_exact_with_reference(tmpdir_s, nb, cols):
+    """Q4 and Q8 rows in the reference build's lane order equal its
+    sml_matvec_rows_flat4 / _flat8 bit for bit, with whole superblocks and
+    with a trailing half superblock (128, 384 and 4224 columns)."""
+    p = tmpdir_s / f"bx{nb}_{cols}.ssf"
+    sa.synth_matrix(p, 96, cols, nbits=nb, random_perm=True, seed=cols + nb)
+    t = SSF(p)["w"]
+    x = (np.random.default_rng(cols).standard_normal(cols) * 3).astype(np.float32)
+    q, s, u = ob.quantize_act(x[t.perm])
+    y, yr = ob.matvec(t, q, s, u), ob.ref_matvec(t, q, s, u)
+    np.testing.assert_array_equal(y.view(np.uint32), yr.view(np.uint32))
+
+
 # ------------------------------------------------------------ small ops
 
 def test_rms_norm_closed_form():
