@@ -32,9 +32,12 @@ const float * sml_gpu_step(int tok, int pos);
 // Layers on the card, and (in *of) of how many. replaces sml/sml-gpu.h:20
 int sml_gpu_layers(int * of);
 
-// How a prompt is read: 2 and 1 ask for batched prompt kernels, 0 a token at
-// a time. Clamped to what the open model supports (here: 0, token at a
-// time). replaces sml/sml-gpu.h:26 (sml/sml-gpu-fwd.c:2420-2423)
+// How a prompt is read: 0 a token at a time through the decode graph; 1 (the
+// default) batched in chunks of 16 positions with every product in the
+// GEMV's arithmetic, equal to stepping bit for bit; 2 batched with the Q4
+// products on the matrix cores (MFMA), equal to float rounding. Exact mode
+// (SML_EXACT=1) reads prompts a token at a time whatever the level.
+// replaces sml/sml-gpu.h:26 (sml/sml-gpu-fwd.c:2420-2423)
 void sml_gpu_prompt_mode(int level);
 
 // A split model decoding on the CPU: 1 if on. Every layer is on the card

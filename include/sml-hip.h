@@ -24,8 +24,12 @@ int          sml_hip_h2d(void * dst, const void * src, size_t n);
 int          sml_hip_d2h(void * dst, const void * src, size_t n);
 int          sml_hip_memset(void * p, int value, size_t n);
 int          sml_hip_sync(void);
-// Test hook: make the n-th HIP call from now fail (n < 0 disables).
+// Test hook: make the n-th HIP call from now fail (n < 0 disables). Every
+// call the library makes counts, in sml_gpu_* entry points too; the entry
+// point that meets the failure returns its failure value.
 void         sml_hip_fail_after(long n);
+// HIP calls the library has made so far (to place sml_hip_fail_after).
+long         sml_hip_call_count(void);
 // Exact mode on (1) or off (0) for the launches below: Q4/Q8 GEMVs, norms,
 // attention and the MoE router then follow the float order of the reference's
 // x86 build (sml/sml-kernel.c:572-727,836-866; sml/sml-run.c:147-152,180-287,

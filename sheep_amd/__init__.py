@@ -58,6 +58,7 @@ _SIGS = [
     ("sml_hip_sync", c_int, []),
     ("sml_hip_fail_after", None, [c_long]),
     ("sml_hip_set_exact", None, [c_int]),
+    ("sml_hip_call_count", c_long, []),
     ("sml_hip_mat_upload", c_void_p, [P(c_void_p), c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int]),
     ("sml_hip_mat_from_file", c_void_p, [c_char_p, c_char_p]),
     ("sml_hip_mat_free", None, [c_void_p]),

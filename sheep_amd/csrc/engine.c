@@ -90,10 +90,31 @@ static struct {
     int32_t * iota;            // device [n_ctx]: 0, 1, 2, ... (prompt chunk positions)
     int32_t * slotid;          // device [MAX_SLOTS][MAX_SLOTS]: row s filled with s
     int rows_ok;               // 1: the batched body can run this model (-1: not checked yet)
+    int rows_ready;            // the batched body's buffers are allocated
 } G;
 
 static int (*g_mid_fn)(float *, int, int);
 static int g_mid_layers;
+
+// Test hook for callers that cannot reach sml_hip_fail_after (a server
+// process): SML_GPU_FAIL=open:N fails the N-th HIP call of sml_gpu_open;
+// prefill:N / step:N make the N-th call of that entry point fail at its
+// first HIP call. Each entry point then returns its failure value, as after a
+// real device error, and the caller's fallback runs.
+static struct { char what[16]; long n, seen_prefill, seen_step; } g_fail;
+
+static void fail_hook_read(void) {
+    memset(&g_fail, 0, sizeof g_fail);
+    const char * e = getenv("SML_GPU_FAIL");
+    const char * c = e ? strchr(e, ':') : NULL;
+    if (!c || c - e >= (long) sizeof g_fail.what) return;
+    memcpy(g_fail.what, e, (size_t) (c - e));
+    g_fail.n = atol(c + 1);
+}
+
+static void fail_hook(const char * entry, long * seen) {
+    if (g_fail.n > 0 && !strcmp(g_fail.what, entry) && ++*seen == g_fail.n) hx.fail_after = 0;
+}
 
 static void * dalloc(size_t n) {
     if (G.ndev >= (int) (sizeof G.dev / sizeof G.dev[0])) hx_failf("too many device buffers");
@@ -120,6 +141,8 @@ static sml_hip_mat * upmat(const ssf_file * f, const ssf_record * r) {
 static int perm_of(const ssf_file * f, const ssf_record * r) {
     const int n = (int) r->cols;
     if (!r->perm_bytes) return -1;
+    if (!r->perm_off || r->perm_bytes < (uint64_t) n * 4)
+        hx_failf("%.64s: permutation shorter than its %d columns", r->name, n);
     const int32_t * p = (const int32_t *) ssf_at(f, r->perm_off);
     int ident = 1;
     for (int i = 0; i < n && ident; i++) ident = p[i] == i;
@@ -258,7 +281,19 @@ static hipGraphExec_t capture(void (*fn)(void)) {
     hipGraph_t g;
     hipGraphExec_t e;
     HX(hipStreamBeginCapture(G.st, hipStreamCaptureModeThreadLocal));
+    // a failure while capturing ends the capture before it propagates, so the
+    // stream is usable (and can be destroyed) afterwards
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) {
+        hipGraph_t dead = NULL;
+        if (hipStreamEndCapture(G.st, &dead) == hipSuccess && dead) hipGraphDestroy(dead);
+        hx.jb = outer;
+        longjmp(*outer, 1);
+    }
+    hx.jb = &jb;
     fn();
+    hx.jb = outer;
     HX(hipStreamEndCapture(G.st, &g));
     HX(hipGraphInstantiate(&e, g, NULL, NULL, 0));
     HX(hipGraphDestroy(g));
@@ -504,6 +539,8 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
 int sml_gpu_open(const char * path, int n_ctx, int threads, int gpu_layers, char * why, int nwhy) {
     (void) threads;
     if (G.open) release();
+    fail_hook_read();
+    if (g_fail.n > 0 && !strcmp(g_fail.what, "open")) hx.fail_after = g_fail.n - 1;
     HX_ENTRY(0);
     jmp_buf * outer = hx.jb;
     jmp_buf jb;
@@ -517,6 +554,7 @@ int sml_gpu_open(const char * path, int n_ctx, int threads, int gpu_layers, char
     hx.jb = &jb;
     setup(path, n_ctx, gpu_layers);
     hx.jb = outer;
+    if (g_fail.n > 0 && !strcmp(g_fail.what, "open")) hx.fail_after = -1;   // the open made fewer calls
     G.open = 1;
     HX_LEAVE();
     return 1;
@@ -531,6 +569,7 @@ static void fetch_logits(void) {
 
 const float * sml_gpu_step(int tok, int pos) {
     if (!G.open || pos < 0 || pos >= G.n_ctx || tok < 0 || tok >= G.V) return NULL;
+    fail_hook("step", &g_fail.seen_step);
     HX_ENTRY(NULL);
     G.pin[0] = tok;
     G.pin[1] = pos;
@@ -551,6 +590,7 @@ static int rows_check(void);
 const float * sml_gpu_prefill(const int * ids, int pos0, int n) {
     if (!G.open || n <= 0 || pos0 < 0 || pos0 + n > G.n_ctx) return NULL;
     for (int i = 0; i < n; i++) if (ids[i] < 0 || ids[i] >= G.V) return NULL;
+    fail_hook("prefill", &g_fail.seen_prefill);
     HX_ENTRY(NULL);
     memcpy(G.pin + 2, ids, (size_t) n * 4);
     HX(hipMemcpyAsync(G.hist + pos0, G.pin + 2, (size_t) n * 4, hipMemcpyHostToDevice, G.st));
@@ -637,12 +677,14 @@ static int multi_per256(int ns) {
 // by themselves). Builds the (gate, up) tables on first use.
 static int rows_check(void) {
     if (G.rows_ok >= 0) return G.rows_ok;
-    G.rows_ok = 0;
     for (int L = 0; L < G.n_layer; L++) {
         eng_layer * y = &G.L[L];
-        if (!y->qkv) return 0;
-        if (!y->moe && (y->perm_gu[0] != y->perm_gu[1] || y->gate->nbits != y->up->nbits)) return 0;
+        if (!y->qkv || (!y->moe && (y->perm_gu[0] != y->perm_gu[1] || y->gate->nbits != y->up->nbits))) {
+            G.rows_ok = 0;
+            return 0;
+        }
     }
+    // a failure part way leaves rows_ok unset, so the next call finishes the tables
     for (int L = 0; L < G.n_layer; L++) {
         eng_layer * y = &G.L[L];
         if (!y->moe && !y->gu_tab) {
@@ -664,7 +706,7 @@ static void rows_tables(void) {
 // The batched body's buffers, for up to MAX_SLOTS rows (sequences, or
 // positions of one prompt chunk).
 static void rows_alloc(void) {
-    if (G.mx) return;
+    if (G.rows_ready) return;     // set last: a failed attempt allocates afresh next time
     const size_t R = MAX_SLOTS;
     size_t wide = (size_t) (G.F > G.E ? G.F : G.E);
     if ((size_t) G.H * G.hd > wide) wide = (size_t) G.H * G.hd;
@@ -694,6 +736,7 @@ static void rows_alloc(void) {
     HX(hipMemcpy(G.slotid, h, R * R * 4, hipMemcpyHostToDevice));
     free(h);
     rows_tables();
+    G.rows_ready = 1;
 }
 
 int sml_gpu_slots(int ns) {

@@ -6,7 +6,7 @@
 
 hx_state hx = { .fail_after = -1, .device = -1 };
 
-#define FN_CACHE 64
+#define FN_CACHE 256
 static struct { char name[64]; hipFunction_t f; } fn_cache[FN_CACHE];
 static int fn_n;
 
@@ -38,7 +38,11 @@ void hx_init(int device) {
     HX(hipGetDeviceProperties(&p, device));
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
         hx_failf("device %d is %s; this library carries gfx950 code only", device, p.gcnArchName);
-    if (hx.inited) HX(hipModuleUnload(hx.mod));
+    if (hx.inited) {
+        hx.inited = 0;            // a failure from here on leaves no stale module in use
+        fn_n = 0;
+        HX(hipModuleUnload(hx.mod));
+    }
     HX(hipModuleLoadData(&hx.mod, sml_code_object));
     fn_n = 0;
     hx.ncu = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;

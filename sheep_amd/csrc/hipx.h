@@ -21,6 +21,7 @@ typedef struct {
     hipModule_t mod;
     int       ncu;                // compute units of the device
     long      fail_after;         // test hook: fail the Nth HIP call from now (< 0: off)
+    long      calls;              // HIP calls made through HX() so far
 } hx_state;
 
 extern hx_state hx;
@@ -29,6 +30,7 @@ void hx_fail(const char * what, hipError_t e);
 void hx_failf(const char * fmt, ...);
 
 static inline void hx_check(hipError_t e, const char * what) {
+    hx.calls++;
     if (hx.fail_after >= 0 && hx.fail_after-- == 0) e = hipErrorUnknown;
     if (e != hipSuccess) hx_fail(what, e);
 }

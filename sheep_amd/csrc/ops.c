@@ -32,6 +32,7 @@ void ops_set_exact(int on) { g_exact = on != 0; }
 int ops_exact(void) { return g_exact; }
 void sml_hip_set_exact(int on) { ops_set_exact(on); }
 void sml_hip_fail_after(long n) { hx.fail_after = n; }
+long sml_hip_call_count(void) { return hx.calls; }
 
 void * sml_hip_malloc(size_t n) { OP_BEGIN(NULL); void * p = hx_malloc(n); HX_LEAVE(); return p; }
 int sml_hip_free(void * p) { OP_BEGIN(-1); if (p) HX(hipFree(p)); HX_LEAVE(); return 0; }
@@ -130,9 +131,29 @@ sml_hip_mat * sml_hip_mat_upload(const uint8_t * const planes[4], const uint16_t
     return m;
 }
 
+// A FLAT record's declared arrays must hold what its shape reads: every plane
+// of its width, the step fields (sd, sq) and, when it has a min, md and mq.
+// ssf_open has already checked each (offset, bytes) against the file.
+static void check_record(const ssf_file * f, const ssf_record * r) {
+    const int six = (f->hdr->flags & SSF_FLAG_SCALE6) != 0;
+    const uint64_t rows = r->rows, cols = r->cols, ng = cols / 32, ns = (uint64_t) SSF_NSUPER(cols);
+    const uint64_t grow = six ? ng / 4 * 3 : ng;
+    if (cols % 128) hx_failf("tensor %.64s: %llu columns is not a multiple of 128", r->name, (unsigned long long) cols);
+    int pb[SSF_MAX_PLANES];
+    const int np = ssf_flat_planes((int) r->nbits, pb);
+    for (int p = 0; p < np; p++)
+        if (!r->plane_off[p] || r->plane_bytes[p] < rows * ssf_plane_row_bytes(pb[p], (int) cols))
+            hx_failf("tensor %.64s: code plane %d is missing or shorter than its shape", r->name, p);
+    if (!r->sd_off || !r->sq_off || r->sd_bytes < rows * ns * 2 || r->sq_bytes < rows * grow)
+        hx_failf("tensor %.64s: step fields missing or shorter than its shape", r->name);
+    if (r->mq_bytes && (!r->md_off || !r->mq_off || r->md_bytes < rows * ns * 2 || r->mq_bytes < rows * grow))
+        hx_failf("tensor %.64s: min fields shorter than its shape", r->name);
+}
+
 sml_hip_mat * mat_from_record(const ssf_file * f, const ssf_record * r) {
     if (r->kind != SSF_KIND_QUANT || r->layout != SSF_LAYOUT_FLAT)
         hx_failf("tensor %.64s is not a FLAT quantized record", r->name);
+    check_record(f, r);
     const uint8_t * planes[4] = { 0 };
     for (int i = 0; i < 4; i++) planes[i] = r->plane_off[i] ? (const uint8_t *) ssf_at(f, r->plane_off[i]) : NULL;
     const int six = (f->hdr->flags & SSF_FLAG_SCALE6) != 0, neg = (f->hdr->flags & SSF_FLAG_MINNEG) != 0;
@@ -179,6 +200,7 @@ sml_hip_mat * mat_stack(const ssf_file * f, const ssf_record * const * recs, int
     const int nb = (int) r0->nbits, cols = (int) r0->cols, has_min = r0->mq_bytes != 0;
     const size_t rows = stack_rows(recs, n);
     if (!rows) return NULL;
+    for (int i = 0; i < n; i++) check_record(f, recs[i]);
     int pb[SSF_MAX_PLANES];
     const int np = ssf_flat_planes(nb, pb);
     const int six = (f->hdr->flags & SSF_FLAG_SCALE6) != 0, neg = (f->hdr->flags & SSF_FLAG_MINNEG) != 0;
@@ -542,8 +564,11 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
         hx_launch("sml_attn_exact", (unsigned) n_head, 1, 256, (size_t) n_ctx * 4, st, &x);
         return;
     }
-    const int aw = env_int("SML_ATTN_WAVES", 8) == 4 ? 4 : 8;
-    const int ch = aw == 4 ? ATTN_CHUNK : attn_split(n_kv, n_ctx);   // the 4-wave form runs splits of 128 only
+    // one sequence: the 8-wave kernel over attn_split positions, the split the
+    // exact prompt kernel (sml_attnc8) takes, so prompts read at level 1 equal
+    // stepping bit for bit (SML_ATTN_WAVES applies to the batched step only)
+    const int aw = 8;
+    const int ch = attn_split(n_kv, n_ctx);
     const int ns = (n_ctx + ch - 1) / ch;
     sml_kattn a;
     memset(&a, 0, sizeof a);
@@ -552,8 +577,7 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
     char name[32];
-    if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
-    else if (ch != ATTN_CHUNK) snprintf(name, sizeof name, "sml_attn8_s%d_r%d", ch, n_head / n_kv);
+    if (ch != ATTN_CHUNK) snprintf(name, sizeof name, "sml_attn8_s%d_r%d", ch, n_head / n_kv);
     else snprintf(name, sizeof name, "sml_attn%d_r%d", aw, n_head / n_kv);
     hx_launch(name, (unsigned) ns, (unsigned) n_kv, (unsigned) (64 * aw), 0, st, &a);
     hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);

@@ -5,7 +5,8 @@ The reference ships no data fixtures, so these are produced here: seeded
 inputs (the synthetic SSF files are regenerated from their seeds and checked
 by sha256) and the reference's outputs on them. Run from the repository root:
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py          # small vectors
+    python tests/golden/make_golden.py full     # the full-size decode runs (minutes)
 """
 import hashlib
 import os
@@ -87,7 +88,74 @@ def decoder_vectors(tmp):
                         route_sel=sel, route_w=w)
 
 
+# The full-size decode workloads (configs of the Qwen2.5-1.5B- and
+# Llama-3-8B-shaped decoders): the reference reads the prompt with
+# sml_prefill under SML_PROMPT_SB=0 (per-32 activations, equal to stepping bit
+# for bit), then greedy-decodes with sml_forward. Per step the fixture keeps
+# the token, a digest of the logits' bytes, the top 8 and the logits' spread
+# -- small enough to commit, exact enough to compare bit for bit.
+FULL = {
+    "qwen": dict(model=dict(n_layer=28, n_embd=1536, n_head=12, n_head_kv=2, n_ff=8960, n_vocab=151936,
+                            rope_theta=1e6, rms_eps=1e-6, qkv_bias=True, tied=True, random_perm=True, nbits=4,
+                            seed=1002, n_ctx_train=4096),
+                 prompt=2048, steps=64, seed=1002),
+    "llama": dict(model=dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, n_ff=14336, n_vocab=128256,
+                             rope_theta=500000.0, rms_eps=1e-5, qkv_bias=False, tied=False, random_perm=False,
+                             nbits=4, seed=1003, n_ctx_train=4096),
+                  prompt=3968, steps=128, seed=1003),
+}
+
+
+def logits_digest(lg):
+    return np.frombuffer(hashlib.sha256(np.ascontiguousarray(lg, np.float32).tobytes()).digest()[:16], np.uint8)
+
+
+def full_prompt(name):
+    c = FULL[name]
+    return np.random.default_rng(c["seed"]).integers(0, c["model"]["n_vocab"], c["prompt"]).astype(np.int32)
+
+
+def full_decode_vectors(tmp, names=("qwen", "llama")):
+    os.environ["SML_PROMPT_SB"] = "0"
+    out = {}
+    for name in names:
+        c = FULL[name]
+        p = os.path.join(tmp, f"{name}.ssf")
+        sa.synth_model(p, **c["model"])
+        out[f"{name}_sha"] = np.frombuffer(bytes.fromhex(sha(p)), np.uint8)
+        prompt = full_prompt(name)
+        n_ctx = c["prompt"] + c["steps"]
+        m = ob.RefModel(p, n_ctx, threads=os.cpu_count() or 1)
+        lg = m.prefill(prompt, 0)
+        toks, dig, top, topv, sd = [], [], [], [], []
+        for i in range(c["steps"]):
+            order = np.argsort(-lg, kind="stable")[:8]
+            toks.append(int(np.argmax(lg)))
+            dig.append(logits_digest(lg))
+            top.append(order.astype(np.int32))
+            topv.append(lg[order].astype(np.float32))
+            sd.append(np.float32(lg.std()))
+            if i + 1 < c["steps"]:
+                lg = m.forward(toks[-1], c["prompt"] + i)
+        m.close()
+        os.unlink(p)
+        out[f"{name}_tokens"] = np.array(toks, np.int32)
+        out[f"{name}_digest"] = np.stack(dig)
+        out[f"{name}_top"] = np.stack(top)
+        out[f"{name}_topv"] = np.stack(topv)
+        out[f"{name}_std"] = np.array(sd, np.float32)
+        print(name, "distinct greedy ids:", len(set(toks)), flush=True)
+    np.savez_compressed(os.path.join(OUT, "full_decode.npz"), **out)
+
+
 if __name__ == "__main__":
+    if len(sys.argv) > 1 and sys.argv[1] == "full":
+        if not ob.have_ref():
+            sys.exit("oracle/_ref/libsmlref.so is not built")
+        with tempfile.TemporaryDirectory(dir=os.environ.get("SML_BENCH_DIR")) as tmp:
+            full_decode_vectors(tmp)
+        print("full-size decode vectors written to", OUT)
+        sys.exit(0)
     if not ob.have_ref():
         sys.exit("oracle/_ref/libsmlref.so is not built: run make -C oracle where the reference is present")
     with tempfile.TemporaryDirectory() as tmp:

@@ -1,10 +1,14 @@
-"""The sml-gpu.h forward pass on the GPU against the oracle's decoder.
+"""The sml-gpu.h forward pass on the GPU (default, fast mode) against the oracle's decoder.
 
-Logits agree to the size an int8 activation-code flip makes (the quantized
-activations turn last-bit float differences into one-code steps; see the
-reference's own per-position correlation grading, sml/sml-gpu-fwd.c:2565-2601).
-Greedy token ids must be identical; a mismatch reports the oracle's top-2
-margin against the reference's 1%-of-s.d. tie rule as the diagnostic.
+The oracle equals the reference's sml_forward bit for bit (tests/test_oracle.py),
+and exact mode equals both (tests/test_gpu_exact.py). The fast mode sums in
+its own orders (split attention, 64-lane GEMV reductions), so an int8
+activation code flips now and then and the logits move by the size of one
+flip. It is graded as the reference grades its own GPU path against its CPU
+engine (sml/sml-gpu-fwd.c:2565-2601): teacher-forced on the CPU engine's
+tokens, per-position logit correlation, and top-1 agreement where a
+different top-1 counts as agreement only when the CPU's two logits are
+within 1% of its logits' standard deviation (a tie).
 """
 import numpy as np
 import pytest
@@ -67,6 +71,38 @@ def check_tokens(gpu_toks, orc_toks, orc_logits):
                         f"({'inside' if m <= 0.01 else 'outside'} the reference's 1% tie rule)")
 
 
+def grade_teacher_forced(path, start, n, n_ctx, V, min_corr=0.999):
+    """The reference grader's loop: the GPU reads the oracle's greedy tokens;
+    per step the logit correlation and the top-1 (a different top-1 is a tie
+    when the oracle's logits for the two ids are within 1% of a logit s.d.).
+    Returns (agree, ties, worst corr, distinct oracle ids)."""
+    toks, logits = greedy_oracle(path, start, n, n_ctx)
+    d = sa.Decoder(path, n_ctx=n_ctx)
+    agree = ties = 0
+    worst = 1.0
+    try:
+        for pos in range(n):
+            lg = d.step(toks[pos], pos, V)
+            ref = logits[pos]
+            c = float(np.corrcoef(lg, ref)[0, 1])
+            worst = min(worst, c)
+            a, g = int(np.argmax(ref)), int(np.argmax(lg))
+            if a == g:
+                agree += 1
+            elif float(ref[a]) - float(ref[g]) <= 0.01 * float(ref.std()):
+                agree += 1
+                ties += 1
+            else:
+                pytest.fail(f"step {pos}: gpu top-1 {g} oracle {a}, oracle gap "
+                            f"{(float(ref[a]) - float(ref[g])) / float(ref.std()):.4f} s.d. (outside the tie rule), "
+                            f"logit corr {c:.6f}")
+    finally:
+        d.close()
+    assert worst >= min_corr, f"worst logit correlation {worst:.6f}"
+    assert len(set(toks[1:])) >= 8, f"the oracle's greedy ids are not diverse: {toks[1:]}"
+    return agree, ties, worst
+
+
 @pytest.mark.parametrize("graph", ["1", "0"])
 def test_teacher_forced_logits(tiny, graph, monkeypatch):
     monkeypatch.setenv("SML_GRAPH", graph)
@@ -82,26 +118,12 @@ def test_teacher_forced_logits(tiny, graph, monkeypatch):
         d.close()
 
 
-def test_greedy_tokens_tiny(tiny):
-    n = 40
-    toks, logits = greedy_oracle(tiny, 11, n, 64)
-    d = sa.Decoder(tiny, n_ctx=64)
-    try:
-        out = d.generate(11, 0, n)
-    finally:
-        d.close()
-    check_tokens(list(out), toks[1:], logits)
-
-
-def test_greedy_tokens_inorder(tiny_inorder):
-    n = 40
-    toks, logits = greedy_oracle(tiny_inorder, 7, n, 64)
-    d = sa.Decoder(tiny_inorder, n_ctx=64)
-    try:
-        out = d.generate(7, 0, n)
-    finally:
-        d.close()
-    check_tokens(list(out), toks[1:], logits)
+@pytest.mark.parametrize("model,start", [("tiny", 11), ("tiny_inorder", 7)])
+def test_fast_graded_like_the_reference(model, start, request):
+    """40 teacher-forced steps on the oracle's greedy ids: every top-1 agrees
+    or is a tie, every logit correlation >= 0.999."""
+    agree, ties, worst = grade_teacher_forced(request.getfixturevalue(model), start, 40, 64, 2000)
+    print(f"{model}: top-1 agree 40/40 ({ties} ties), worst corr {worst:.6f}")
 
 
 @pytest.mark.parametrize("model", ["tiny", "tiny_inorder"])
@@ -224,35 +246,21 @@ def test_batched_prompt_into_other_slots(tiny):
         assert np.corrcoef(res[2][0][b], res[0][0][b])[0, 1] > 0.9999
 
 
-def test_greedy_tokens_qwen_layers(qwenish):
-    n = 24
-    toks, logits = greedy_oracle(qwenish, 100, n, 128)
-    d = sa.Decoder(qwenish, n_ctx=128)
-    try:
-        out = d.generate(100, 0, n)
-    finally:
-        d.close()
-    check_tokens(list(out), toks[1:], logits)
+def test_fast_graded_like_the_reference_qwen_layers(qwenish):
+    agree, ties, worst = grade_teacher_forced(qwenish, 100, 64, 128, 32000)
+    print(f"qwenish: top-1 agree 64/64 ({ties} ties), worst corr {worst:.6f}")
 
 
-@pytest.mark.parametrize("perm", [False, True])
-def test_greedy_tokens_moe(tmp_path, perm):
+@pytest.mark.parametrize("perm,seed", [(False, 60), (True, 61)])
+def test_moe_graded_like_the_reference(tmp_path, perm, seed):
     """A Mixtral-shaped decoder (8 experts, top-2, softmax over the chosen):
-    routed experts on the GPU, tokens identical to the oracle."""
+    routed experts on the GPU, graded against the oracle like the dense
+    decoders."""
     p = tmp_path / "moe.ssf"
     sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, n_expert=8,
-                   n_expert_used=2, moe_flags=1, random_perm=perm, seed=60 + int(perm))
-    n = 24
-    toks, logits = greedy_oracle(p, 9, n, 64)
-    d = sa.Decoder(p, n_ctx=64)
-    try:
-        for pos in range(4):
-            lg = d.step(toks[pos], pos, 2000)
-            assert np.corrcoef(lg, logits[pos])[0, 1] > 0.999, pos
-        out = d.generate(9, 0, n)
-    finally:
-        d.close()
-    check_tokens(list(out), toks[1:], logits)
+                   n_expert_used=2, moe_flags=1, random_perm=perm, seed=seed)
+    agree, ties, worst = grade_teacher_forced(p, 9, 40, 64, 2000)
+    print(f"moe: top-1 agree 40/40 ({ties} ties), worst corr {worst:.6f}")
 
 
 def test_bounds_and_reopen(tiny):

@@ -377,3 +377,40 @@ def test_awq_unpack_and_gemv(rows, cols, with_zeros):
     m.matvec(sa.DevBuf.of(x), y)
     W = np.stack([ob.awq_dequant_row(qw, qz, sc, rows, cols, r) for r in range(rows)]).astype(np.float64)
     close(y.read(np.float32), (W @ x.astype(np.float64)).astype(np.float32), f"awq {rows}x{cols}")
+
+
+# ------------------------------------------------------------ loader: declared sizes against the shape
+
+@pytest.mark.parametrize("field", ["n0", "sd_bytes", "sq_bytes", "md_bytes", "mq_bytes", "p0"])
+def test_short_record_is_refused(tmp_path, field):
+    """A record whose declared array sizes pass the file-range checks but are
+    shorter than its shape reads (or whose plane offset is 0) is refused at
+    upload with a reason, and sml_gpu_open returns 0 instead of reading past
+    the mapping."""
+    import re
+    import shutil
+    import struct
+    from sheep_amd.ssf import REC_FIELDS, REC_FMT, REC_SIZE
+    codes = []
+    for n, c in re.findall(r"(\d*)([a-zA-Z])", REC_FMT[1:]):
+        codes += [n + c] if c == "s" else [c] * (int(n) if n else 1)
+    off = struct.calcsize("<" + "".join(codes[:REC_FIELDS.index(field)]))
+    src = tmp_path / "base.ssf"
+    sa.synth_model(src, n_layer=1, n_embd=256, n_head=2, n_head_kv=1, n_ff=512, n_vocab=300, seed=3)
+    f = SSF(src)
+    name = "blk.0.ffn_down.weight"
+    i = list(f.tensors).index(name)
+    p = tmp_path / f"short_{field}.ssf"
+    shutil.copy(src, p)
+    with open(p, "r+b") as fh:
+        fh.seek(f.hdr["table_off"] + i * REC_SIZE + off)
+        fh.write(struct.pack("<Q", 0 if field == "p0" else f[name].rec[field] // 2))
+        if field == "p0":       # no plane at all: offset and size 0 pass the file-range checks
+            fh.seek(f.hdr["table_off"] + i * REC_SIZE + struct.calcsize("<" + "".join(codes[:REC_FIELDS.index("n0")])))
+            fh.write(struct.pack("<Q", 0))
+    assert not sa.lib().sml_hip_mat_from_file(str(p).encode(), name.encode())
+    err = sa.lib().sml_hip_last_error()
+    assert b"shorter" in err or b"missing" in err, err
+    why = sa.ctypes.create_string_buffer(512)
+    assert sa.lib().sml_gpu_open(str(p).encode(), 64, 1, 0, why, 512) == 0
+    assert why.value
