@@ -219,6 +219,13 @@ int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kc
 // this call allocates and frees (the decode step keeps its own); it returns
 // once the pick is done.
 int sml_hip_argmax(const float * logits, int n, int32_t * tok);
+// The same pick, allocating nothing: its two-stage scratch (1024 pairs, 8 KB)
+// is a device array the library holds per GPU for the life of the process.
+// No counterpart in the reference; it is for callers that cannot allocate
+// device memory (code under HIP graph capture, tight serving loops). Takes
+// 1..2^30 logits; enqueues on the null stream without waiting. Calls that
+// overlap on one GPU (other streams or threads) share the scratch and race.
+int sml_hip_argmax_noalloc(const float * logits, int n, int32_t * tok);
 
 #ifdef __cplusplus
 }
