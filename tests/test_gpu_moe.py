@@ -293,6 +293,47 @@ def test_moe_ffn_per256(tmpdir_s, T):
         close(got_out[t], ro, f"per-256 moe token {t}")
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("per256", [False, True])
+def test_moe_mixtral_layer_shape(tmp_path, per256):
+    """The Mixtral-shaped layer of the MoE workload at its shape: hidden
+    4096, 8 experts of 14336 SwiGLU Q4, router 4096 x 8 ~ N(0, 1/64) (seed
+    1005), top-2 with softmax over the chosen, 16 tokens of N(0, 1). Router
+    logits, choices and weights equal the oracle's bit for bit (a double sum
+    rounded once; the library's restated expf); each token's output within
+    1e-3 of the oracle's per-token composition, with the expert inputs
+    quantized per 32 (the stepped moe_ffn) or per 256 (moe_ffn_batch): max
+    |d| <= 1e-3 max |ref| and rel-RMS <= 1e-3. The expert output is a
+    composite -- h is re-quantized to int8 between the products -- and one
+    flipped code of h's 14336 moves it by ~1e-4 rel-RMS, so the bound is the
+    composite's 1e-3, not a single product's 1e-4."""
+    n_embd, n_ff, nexp, k, T = 4096, 14336, 8, 2, 16
+    p = tmp_path / "mixtral_layer.ssf"
+    sa.synth_model(p, n_layer=1, n_embd=n_embd, n_head=32, n_head_kv=8, n_ff=n_ff, n_vocab=1024, n_expert=nexp,
+                   n_expert_used=k, moe_flags=1, rope_theta=1e6, seed=1005)
+    f = SSF(p)
+    moe = sa.MoE(p, 0, 16)
+    moe.regime(per256)
+    x = np.random.default_rng(1005).standard_normal((T, n_embd)).astype(np.float32)
+    out, sel, w, lg = sa.DevBuf(T * n_embd * 4), sa.DevBuf(T * k * 4), sa.DevBuf(T * k * 4), sa.DevBuf(T * nexp * 4)
+    moe.ffn(sa.DevBuf.of(x), T, out, sel, w, lg)
+    got_out = out.read(np.float32).reshape(T, n_embd)
+    got_sel, got_w = sel.read(np.int32).reshape(T, k), w.read(np.float32).reshape(T, k)
+    got_lg = lg.read(np.float32).reshape(T, nexp)
+    used = set()
+    for t in range(T):
+        rl, rs, rw, ro = oracle_moe(f, x[t], nexp, k, n_embd, per256=per256)
+        np.testing.assert_array_equal(got_lg[t], rl, err_msg=f"token {t} router logits")
+        np.testing.assert_array_equal(got_sel[t], rs, err_msg=f"token {t} routing")
+        np.testing.assert_array_equal(got_w[t], rw, err_msg=f"token {t} weights")
+        err = np.abs(got_out[t].astype(np.float64) - ro)
+        assert err.max() <= 1e-3 * np.abs(ro).max(), (t, err.max())
+        assert np.sqrt((err ** 2).mean() / (ro.astype(np.float64) ** 2).mean()) <= 1e-3, t
+        used |= set(rs.tolist())
+    assert len(used) >= 6, used
+    moe.free()
+
+
 def test_moe_refuses_dense_layer(tmpdir_s):
     p = tmpdir_s / "dense_for_moe.ssf"
     sa.synth_model(p, n_layer=1, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=256, seed=3)
