@@ -92,6 +92,29 @@ def read_ceiling(nbytes, iters=360, target_bytes=1.2e9, grid=2048):
     return float(np.median(trials))
 
 
+def gemv_size_sweep(tmp, cols=14336, rows_list=(4096, 8192, 16384, 32768, 65536)):
+    """The Q4 GEMV and the streaming read at 34 .. 544 MB (rows x 14336),
+    each over rotating copies: a line t = a + bytes / B through the points
+    separates the fixed cost of a launch (a) from the steady-state rate (B)."""
+    pts = []
+    for rows in rows_list:
+        us, nb = gemv_roofline(rows, cols, iters=max(40, 400 * 4096 // rows), tmp=tmp)
+        rus = read_ceiling(nb, iters=max(40, 360 * 4096 // rows))
+        pts.append({"rows": rows, "bytes": nb, "gemv_us": round(us, 3), "gemv_GB/s": round(nb / us / 1e3, 1),
+                    "read_us": round(rus, 3), "read_GB/s": round(nb / rus / 1e3, 1)})
+        log(f"sweep {rows}x{cols}: {pts[-1]}")
+        os.remove(os.path.join(tmp, f"gemv_{rows}x{cols}.ssf"))
+    x = np.array([p["bytes"] for p in pts], np.float64)
+    out = {"points": pts}
+    for key in ("gemv", "read"):
+        y = np.array([p[f"{key}_us"] for p in pts], np.float64)
+        slope, icpt = np.polyfit(x, y, 1)
+        out[f"{key}_fixed_us"] = round(float(icpt), 3)
+        out[f"{key}_steady_GB/s"] = round(1e-3 / float(slope), 1)
+        out[f"{key}_steady_frac"] = round(1e-3 / float(slope) / HBM_PEAK_GBS, 4)
+    return out
+
+
 COPY_BYTES = 256 << 20
 PROBE_LAUNCHES = 12
 
@@ -378,6 +401,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the batched, MoE and width-sweep lines")
     ap.add_argument("--pmc-probe", metavar="SSF", help=argparse.SUPPRESS)
     ap.add_argument("--small-gemm", action="store_true", help="only time the 16-row small-M GEMMs")
+    ap.add_argument("--gemv-sweep", action="store_true",
+                    help="only the Q4 GEMV and streaming read at 34..544 MB (fixed cost vs steady rate)")
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: fill the 4096 context)")
     ap.add_argument("--prompt-only", type=int, metavar="LEVEL", default=-1,
@@ -396,6 +421,8 @@ def main():
     try:
         if a.small_gemm:
             res = {"small_m_gemm": small_gemm(work)}
+        elif a.gemv_sweep:
+            res = {"gemv_size_sweep": gemv_size_sweep(work)}
         elif a.prompt_only >= 0:
             res = {"prompt_reading": prompt_only(work, a.prompt_only, a.prompt if a.prompt > 0 else 3960)}
         else:

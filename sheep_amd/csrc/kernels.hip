@@ -662,6 +662,8 @@ __device__ void gemv_body(const sml_kgemv & a) {
     GEMV_KERNEL_S(NB, 4, 1) GEMV_KERNEL_S(NB, 4, 2) GEMV_KERNEL_S(NB, 4, 4)               \
     GEMV_KERNEL_H(NB, 2) GEMV_KERNEL_H(NB, 4) GEMV_WIDE(NB)
 GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH(7) GEMV_WIDTH(8)
+// a whole 14336-wide row in one pass (tuning: SML_GEMV_NI=8)
+GEMV_KERNEL(4, 1, 8) GEMV_KERNEL(4, 2, 8)
 
 // The exact forms (suffix _x, Q4 and Q8): the reference's float order per row
 // (gemv_body EX), for every shape pick_shape gives an unfused launch.

@@ -346,10 +346,10 @@ static void pick_shape(int rows, int cols, int nbits, int swiglu, int fused, int
     }
     const int fr = env_int("SML_GEMV_RB", 0), fi = env_int("SML_GEMV_NI", 0);
     if (fr == 1 || fr == 2 || fr == 4) r = fr;
-    if ((fi == 1 || fi == 2 || fi == 4 || fi == 8) && fi <= imax) i = fi;
+    if ((fi == 1 || fi == 2 || fi == 4) && fi <= imax) i = fi;
+    if (fi == 8 && !fused && !swiglu && nbits == 4 && r <= 2) i = 8;   // Q4, one or two rows per wave
     if (swiglu && r < 2) r = 2;
     if (!swiglu && !fused && r == 1 && i == 1) i = 2;
-    if (!swiglu && r == 4 && i == 8) i = 4;
     *rb = r;
     *ni = i;
 }
