@@ -10,6 +10,7 @@ weights of the Llama-3-8B architecture. The prompt (random ids) is read first
 so the timed tokens run with ~4k positions of KV cache. Prints one JSON line.
 """
 import argparse
+import ctypes
 import json
 import os
 import shutil
@@ -258,7 +259,7 @@ def moe_layer(tmp, T=16, iters=50):
         res.update({"experts_touched": touched, "tokens_per_expert": cnt.tolist(), "bytes_per_step": b})
         res[name] = {"us_per_step": round(us, 2), "GB/s": round(b / us / 1e3, 1)}
     moe.free()
-    os.remove(p)
+    res["path"] = p               # kept for the CPU baseline's MoE leg
     return res
 
 
@@ -366,28 +367,131 @@ def batched_decode(dec, n_vocab, ns=16, steps=20, pos0=1024):
     return res
 
 
-def cpu_baseline(path, threads, budget_s=12.0, max_tokens=1200):
-    """The reference's own CPU decode (sml_forward on its pool threads,
-    compiled from its sources into oracle/_ref) on the same model file, from
-    position 0 for as many tokens as fit the time budget."""
+def host_cpu():
+    model = "unknown"
     try:
-        from oracle import bind as ob
-    except Exception as e:  # noqa: BLE001
-        return {"value": None, "error": f"oracle bindings unavailable: {e}"}
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "usable": len(os.sched_getaffinity(0)), "cpu": model}
+
+
+def cpu_leg(args):
+    """One CPU-baseline measurement in its own process, pinned to CPUs
+    0..T-1 (the reference's pool threads inherit the affinity). Prints one
+    JSON object."""
+    kind, threads = args[0], int(args[1])
+    avail = sorted(os.sched_getaffinity(0))
+    os.sched_setaffinity(0, avail[:threads])
+    from oracle import bind as ob
     if not ob.have_ref():
-        return {"value": None, "error": "oracle/_ref/libsmlref.so not built"}
-    m = ob.RefModel(path, max_tokens + 8, threads=threads)
-    tok, n = 1, 0
-    m.forward(tok, 0)            # warm-up token (position 0)
-    t0 = time.perf_counter()
-    while n < max_tokens and time.perf_counter() - t0 < budget_s:
-        tok = int(np.argmax(m.forward(tok, n + 1)))
-        n += 1
-    dt = time.perf_counter() - t0
-    m.close()
-    return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"{n} greedy decode tokens at positions 2..{n + 1} of the same Llama-3-8B-shaped Q4 file "
-                      f"(short context: attention negligible), sml_forward with {threads} pool threads"}
+        print(json.dumps({"error": "oracle/_ref/libsmlref.so not built"}))
+        return
+    if kind == "decode":
+        path, pos0, budget = args[2], int(args[3]), float(args[4])
+        m = ob.RefModel(path, pos0 + 2000, threads=threads)
+        tok = 1
+        m.forward(tok, pos0)                     # warm-up token
+        n, t0 = 0, time.perf_counter()
+        while (time.perf_counter() - t0 < budget or n < 2) and n < 1990:   # stays inside the context
+            tok = int(np.argmax(m.forward(tok, pos0 + 1 + n)))
+            n += 1
+        dt = time.perf_counter() - t0
+        m.close()
+        print(json.dumps({"tokens": n, "s": round(dt, 3), "tokens_per_s": round(n / dt, 3),
+                          "positions": f"{pos0 + 1}..{pos0 + n}"}))
+    elif kind == "gemv":
+        from sheep_amd.ssf import SSF
+        path, ncopy = args[2], int(args[3])
+        t = SSF(path)["w"]
+        cols, rows = t.cols, t.rows
+        copies = []
+        for _ in range(ncopy):
+            pl = [np.array(p) for p in t.planes()] + [np.zeros(16, np.uint8)] * (3 - len(t.planes()))
+            copies.append((pl, np.array(t.sd), np.array(t.sq), np.array(t.md), np.array(t.mq)))
+        V = ctypes.c_void_p
+        planes = (V * (3 * ncopy))(*[p.ctypes.data for c in copies for p in c[0]])
+        arrs = [(V * ncopy)(*[c[i].ctypes.data for c in copies]) for i in range(1, 5)]
+        x = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
+        r = ob.ref()
+        r.ref_time_matvec.restype = ctypes.c_double
+        r.ref_time_matvec.argtypes = [V] * 5 + [ctypes.c_int] * 4 + [V, ctypes.c_int, ctypes.c_int]
+        nb = t.planes_bytes if hasattr(t, "planes_bytes") else None
+        sec = r.ref_time_matvec(planes, arrs[0], arrs[1], arrs[2], arrs[3], ncopy, rows, cols, t.nbits,
+                                x.ctypes.data, threads, 12)
+        print(json.dumps({"us": round(sec * 1e6, 1), "rows": rows, "cols": cols, "nbits": t.nbits}))
+    elif kind == "moe":
+        path, regime, steps = args[2], args[3], int(args[4])
+        if regime == "exact":
+            os.environ["SML_MULTI"] = "exact"
+        ns = 16
+        m = ob.RefMulti(path, 64, ns, threads=threads)
+        toks, pos = list(range(1, ns + 1)), [0] * ns
+        m.step(toks, pos)                        # warm-up step
+        t0 = time.perf_counter()
+        for s in range(steps):
+            m.step(toks, [s + 1] * ns)
+        dt = time.perf_counter() - t0
+        m.close()
+        print(json.dumps({"slots": ns, "steps": steps, "ms_per_step": round(dt / steps * 1e3, 2),
+                          "tokens_per_s": round(ns * steps / dt, 2), "regime": regime}))
+
+
+def run_cpu_leg(*args, timeout=300):
+    """A CPU leg in a child process (its own pinning and environment)."""
+    import subprocess
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-leg"] + [str(a) for a in args]
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=timeout,
+                       env=dict(os.environ, OMP_NUM_THREADS=str(args[1])))
+    try:
+        return json.loads(r.stdout.strip().splitlines()[-1])
+    except (ValueError, IndexError):
+        return {"error": f"exit {r.returncode}: {r.stderr[-300:]}"}
+
+
+def cpu_baseline(path, pos0, moe_path, gemv_paths, budget_s=10.0):
+    """The reference's own CPU path (sml-kernel.c kernels on sml-pool threads,
+    compiled from its sources into oracle/_ref) on the same files, on this
+    host's cores, each leg pinned to its first T CPUs:
+    - decode (sml_forward) at the GPU line's positions (pos0 + 1 ..; the cache
+      rows before them are left as allocated, which costs the same reads),
+      T = every usable CPU (the value), with the T sweep and a short-context line;
+    - the single-GEMV workloads (sml_quantize_act + the width's kernels over row
+      chunks of 32, rotating over copies larger than the LLC);
+    - the MoE layer through sml_forward_multi with 16 slots, both regimes."""
+    host = host_cpu()
+    tmax = host["usable"]
+    sweep_t = [t for t in (1, 8, 16, 32) if t < tmax] + [tmax]
+    out = {"kind": "reference", "unit": "tokens/s", "host": host}
+    sweep = {}
+    for t in sweep_t:
+        sweep[str(t)] = run_cpu_leg("decode", t, path, pos0, budget_s if t == tmax else budget_s / 2)
+        log(f"cpu decode T={t}: {sweep[str(t)]}")
+    best = max(sweep, key=lambda k: sweep[k].get("tokens_per_s", 0))
+    out["value"] = sweep[str(tmax)].get("tokens_per_s")
+    out["cores"] = tmax
+    out["threads_sweep"] = sweep
+    out["best_threads"] = int(best)
+    out["short_context"] = run_cpu_leg("decode", tmax, path, 1, budget_s / 2)
+    out["sample"] = (f"{sweep[str(tmax)].get('tokens')} greedy tokens of the same Llama-3-8B-shaped Q4 file at "
+                     f"positions {sweep[str(tmax)].get('positions')} (the GPU line's), sml_forward on {tmax} pool "
+                     f"threads pinned to CPUs 0..{tmax - 1}; T sweep {sweep_t}; {host['cpu']}, "
+                     f"{host['nproc']} CPUs ({tmax} usable, one socket)")
+    g = {}
+    for name, p in gemv_paths.items():
+        g[name] = run_cpu_leg("gemv", tmax, p, 4)
+        if "us" in g[name]:
+            g[name]["GB/s"] = round(os.path.getsize(p) / g[name]["us"] / 1e3, 1)
+        log(f"cpu gemv {name}: {g[name]}")
+    out["gemv"] = g
+    if moe_path:
+        out["moe_16_slots"] = {r: run_cpu_leg("moe", tmax, moe_path, r, 6) for r in ("default", "exact")}
+        log(f"cpu moe: {out['moe_16_slots']}")
+    return out
 
 
 def main():
@@ -400,6 +504,7 @@ def main():
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
     ap.add_argument("--no-extra", action="store_true", help="skip the batched, MoE and width-sweep lines")
     ap.add_argument("--pmc-probe", metavar="SSF", help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-leg", nargs="+", help=argparse.SUPPRESS)
     ap.add_argument("--small-gemm", action="store_true", help="only time the 16-row small-M GEMMs")
     ap.add_argument("--gemv-sweep", action="store_true",
                     help="only the Q4 GEMV and streaming read at 34..544 MB (fixed cost vs steady rate)")
@@ -408,6 +513,9 @@ def main():
     ap.add_argument("--prompt-only", type=int, metavar="LEVEL", default=-1,
                     help="only read the Llama-3-8B-shaped prompt at this prompt level (0, 1 or 2)")
     a = ap.parse_args()
+    if a.cpu_leg:
+        cpu_leg(a.cpu_leg)
+        return
     if a.pmc_probe:
         pmc_probe(a.pmc_probe)
         return
@@ -549,10 +657,20 @@ def run(a, work):
         f"roofline {roof_tps:.0f} tok/s weights-only, {roof_tps_kv:.0f} with KV")
     cpu = None
     if not a.no_cpu:
-        th = min(16, os.cpu_count() or 1)
         t1 = time.perf_counter()
-        cpu = cpu_baseline(path, th)
+        gp = {"q4_8960x1536": os.path.join(work, "cpu_q4_8960x1536.ssf")}
+        sa.synth_matrix(gp["q4_8960x1536"], 8960, 1536, nbits=4, seed=1001)
+        for nb in (2, 3, 4, 5, 6, 8):
+            for rows, cols in ((4096, 14336), (14336, 4096)):
+                p = os.path.join(work, f"cpu_q{nb}_{rows}x{cols}.ssf")
+                sa.synth_matrix(p, rows, cols, nbits=nb, seed=1004)
+                gp[f"q{nb}_{rows}x{cols}"] = p
+        cpu = cpu_baseline(path, pos, extra.get("moe_layer", {}).get("path"), gp)
+        for p in gp.values():
+            os.remove(p)
         log(f"cpu baseline: {cpu} ({time.perf_counter() - t1:.1f}s)")
+    if "moe_layer" in extra and extra["moe_layer"].get("path"):
+        os.remove(extra["moe_layer"].pop("path"))
     return {
         "metric": "Q4 GEMV HBM GB/s (% of peak); batch-1 decode tokens/s, Llama-3-8B shape",
         "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,

@@ -119,3 +119,73 @@ void ref_multi_close(void * p) {
     sml_model_close(&h->m);
     free(h);
 }
+
+// ---------------------------------------------------------------- CPU GEMV timing
+//
+// The CPU baseline of the single-GEMV workloads: sml_quantize_act, then the
+// width's kernels as issue_rows_act dispatches them (sml/sml-run.c:612-680),
+// over row chunks of 32 handed out dynamically to `threads` OpenMP threads
+// (matvec's OpenMP branch, sml/sml-run.c:786-797), rotating over `ncopy`
+// copies of the planes and fields (bigger together than the last-level cache,
+// as sml/sml-kernel-bench.c:72-90 rotates its working set). Returns seconds per
+// call (median of 5 trials of `iters` calls).
+#include <omp.h>
+#include <time.h>
+
+typedef struct { const uint8_t * pl[3]; const uint16_t * sd; const uint8_t * sq; const uint16_t * md; const uint8_t * mq; } ref_wcopy;
+
+static void rows_width(float * y, const ref_wcopy * w, const sml_act * a, int nb, int lo, int hi, int n) {
+    switch (nb) {
+    case 4: sml_matvec_rows_flat4(y, w->pl[0], w->sd, w->sq, w->md, w->mq, a, lo, hi, n); break;
+    case 2: sml_matvec_rows(y, w->pl[0], w->sd, w->sq, w->md, w->mq, a, lo, hi, n, 0, 0.0f); break;
+    case 3: sml_matvec_rows(y, w->pl[0], w->sd, w->sq, w->md, w->mq, a, lo, hi, n, 0, 0.0f);
+            sml_matvec_bits1(y, w->pl[1], w->sd, w->sq, a, 1, 0, lo, hi, n, 2); break;
+    case 5: sml_matvec_rows_flat4(y, w->pl[0], w->sd, w->sq, w->md, w->mq, a, lo, hi, n);
+            sml_matvec_bits1(y, w->pl[1], w->sd, w->sq, a, 1, 0, lo, hi, n, 4); break;
+    case 6: sml_matvec_rows_flat6(y, w->pl[1], w->pl[0], w->sd, w->sq, w->md, w->mq, a, lo, hi, n); break;
+    case 7: sml_matvec_rows_flat6(y, w->pl[0], w->pl[1], w->sd, w->sq, w->md, w->mq, a, lo, hi, n);
+            sml_matvec_bits1(y, w->pl[2], w->sd, w->sq, a, 1, 0, lo, hi, n, 6); break;
+    case 8: sml_matvec_rows_flat8(y, w->pl[0], w->pl[1], w->sd, w->sq, w->md, w->mq, a, lo, hi, n); break;
+    default: break;
+    }
+}
+
+double ref_time_matvec(const void * const * planes, const void * const * sd, const void * const * sq,
+                       const void * const * md, const void * const * mq, int ncopy, int rows, int cols, int nbits,
+                       const float * x, int threads, int iters) {
+    ref_wcopy * w = calloc((size_t) ncopy, sizeof *w);
+    for (int c = 0; c < ncopy; c++) {
+        for (int p = 0; p < 3; p++) w[c].pl[p] = (const uint8_t *) planes[3 * c + p];
+        w[c].sd = sd[c]; w[c].sq = sq[c]; w[c].md = md[c]; w[c].mq = mq[c];
+    }
+    sml_act a;
+    memset(&a, 0, sizeof a);
+    a.q = malloc((size_t) cols);
+    a.scale = malloc((size_t) cols / 32 * 4);
+    a.sums = malloc((size_t) cols / 32 * 4);
+    a.n = cols;
+    float * y = malloc((size_t) rows * 4);
+    const int nch = (rows + 31) / 32;
+    double trial[5];
+    omp_set_num_threads(threads);
+    for (int t = 0; t < 5; t++) {
+        struct timespec t0, t1;
+        clock_gettime(CLOCK_MONOTONIC, &t0);
+        for (int it = 0; it < iters; it++) {
+            const ref_wcopy * cw = &w[it % ncopy];
+            sml_quantize_act(&a, x, cols);
+            memset(y, 0, (size_t) rows * 4);
+            #pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+            for (int k = 0; k < nch; k++) {
+                const int lo = k * 32, hi = lo + 32 < rows ? lo + 32 : rows;
+                rows_width(y, cw, &a, nbits, lo, hi, cols);
+            }
+        }
+        clock_gettime(CLOCK_MONOTONIC, &t1);
+        trial[t] = ((double) (t1.tv_sec - t0.tv_sec) + 1e-9 * (double) (t1.tv_nsec - t0.tv_nsec)) / iters;
+    }
+    for (int i = 1; i < 5; i++)
+        for (int j = i; j > 0 && trial[j] < trial[j - 1]; j--) { const double s = trial[j]; trial[j] = trial[j - 1]; trial[j - 1] = s; }
+    free(a.q); free(a.scale); free(a.sums); free(y); free(w);
+    return trial[2];
+}
