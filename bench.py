@@ -505,6 +505,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the batched, MoE and width-sweep lines")
     ap.add_argument("--pmc-probe", metavar="SSF", help=argparse.SUPPRESS)
     ap.add_argument("--cpu-leg", nargs="+", help=argparse.SUPPRESS)
+    ap.add_argument("--decode-trace", metavar="MODEL", choices=("llama", "qwen"),
+                    help="only decode the last --steps positions with direct launches (run under rocprofv3)")
+    ap.add_argument("--trace-summary", metavar="DIR", help="per-kernel table of a --decode-trace kernel trace")
     ap.add_argument("--small-gemm", action="store_true", help="only time the 16-row small-M GEMMs")
     ap.add_argument("--gemv-sweep", action="store_true",
                     help="only the Q4 GEMV and streaming read at 34..544 MB (fixed cost vs steady rate)")
@@ -515,6 +518,9 @@ def main():
     a = ap.parse_args()
     if a.cpu_leg:
         cpu_leg(a.cpu_leg)
+        return
+    if a.trace_summary:
+        print(trace_summary(a.trace_summary, a.steps))
         return
     if a.pmc_probe:
         pmc_probe(a.pmc_probe)
@@ -531,6 +537,8 @@ def main():
             res = {"small_m_gemm": small_gemm(work)}
         elif a.gemv_sweep:
             res = {"gemv_size_sweep": gemv_size_sweep(work)}
+        elif a.decode_trace:
+            res = {"decode_trace": decode_trace(work, a.decode_trace, a.steps)}
         elif a.prompt_only >= 0:
             res = {"prompt_reading": prompt_only(work, a.prompt_only, a.prompt if a.prompt > 0 else 3960)}
         else:
@@ -539,6 +547,60 @@ def main():
         if not a.keep:
             shutil.rmtree(work, ignore_errors=True)
     print(json.dumps(res), flush=True)
+
+
+def decode_trace(work, model="llama", steps=32):
+    """For a kernel trace of the timed decode region only: the Llama-3-8B-
+    (or Qwen2.5-1.5B-) shaped file opened with direct launches (SML_GRAPH=0:
+    the tracer sees each kernel), its prompt read at level 1 so the cache
+    holds N_CTX - steps positions, then a 16-byte copy (sml_copy_stream, the
+    marker) and `steps` greedy tokens at the last positions of the context."""
+    os.environ["SML_GRAPH"] = "0"
+    spec = LLAMA if model == "llama" else QWEN
+    path = os.path.join(work, f"{model}_trace.ssf")
+    sa.synth_model(path, n_ctx_train=N_CTX, **spec)
+    dec = sa.Decoder(path, n_ctx=N_CTX)
+    try:
+        n = N_CTX - steps
+        ids = np.random.default_rng(1003).integers(0, spec["n_vocab"], n).astype(np.int32)
+        lg = dec.prefill(ids, 0, spec["n_vocab"])
+        a, b = sa.DevBuf(64), sa.DevBuf(64)
+        assert sa.lib().sml_hip_copy(b.ptr, a.ptr, 16) == 0
+        sa.sync()
+        dec.generate(int(np.argmax(lg)), n, steps)
+    finally:
+        dec.close()
+    return {"model": model, "decode_positions": f"{N_CTX - steps}..{N_CTX - 1}", "steps": steps}
+
+
+def trace_summary(out_dir, steps):
+    """Per-kernel statistics of the dispatches after the last marker copy in
+    a rocprofv3 --kernel-trace CSV, as a markdown table (per decode token)."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(out_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_trace.csv under {out_dir}")
+    rows = []
+    with open(files[0], newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    last = max(i for i, r in enumerate(rows) if r[2].startswith("sml_copy_stream"))
+    dec = rows[last + 1:]
+    stats = {}
+    for s, e, name in dec:
+        stats.setdefault(name, []).append((e - s) / 1e3)
+    span = (dec[-1][1] - dec[0][0]) / 1e3
+    busy = sum(v for vs in stats.values() for v in vs)
+    lines = [f"Dispatches after the marker: {len(dec)} over {steps} tokens; span {span:.1f} us "
+             f"({span / steps:.1f} us per token), kernels busy {busy / steps:.1f} us per token.", "",
+             "| kernel | per token | mean us | min us | max us | us per token | share |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    for name, v in sorted(stats.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{name}` | {len(v) / steps:g} | {np.mean(v):.2f} | {np.min(v):.2f} | {np.max(v):.2f} | "
+                     f"{sum(v) / steps:.1f} | {sum(v) / busy:.1%} |")
+    return "\n".join(lines)
 
 
 def prompt_only(work, level, n):

@@ -1035,7 +1035,9 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     };
     auto fetch = [&](int b) { fetch_qkv(b); fetch_rope(b); };
     fetch_qkv(b0);
-    if (CHUNK) fetch_rope(b0);
+    // the RoPE rows ahead of the tile: loads return in order, and q's rotation
+    // comes before the first score
+    fetch_rope(b0);
     // all of K, then all of V: loads return in order, so the scores and the
     // softmax run while V is still arriving
     v4u kw[PPL], vw[PPL];
@@ -1054,7 +1056,6 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             vw[i] = __builtin_nontemporal_load((const v4u *) (vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
         }
     }
-    if (!CHUNK) fetch_rope(b0);                       // one entry: its RoPE rows after the tile
     // each entry's arithmetic is the one-entry kernel's, position for position;
     // with few heads the next entry's inputs load while this one computes
     constexpr bool PF = CHUNK && REP <= 4;
