@@ -107,10 +107,11 @@ int sml_hip_time_read(const void * const * bufs, int nbuf, size_t bytes, int gri
 int sml_hip_copy(void * dst, const void * src, size_t bytes);
 
 // ------------------------------------------------------------ small-M GEMM
-// y[r] = W.a[r] for nrow (1..16) activation rows a[r] (q [nrow][cols], scale
-// and sums [nrow][cols/32]) into y [nrow][rows]: each weight streams once for
-// all rows. replaces sml_matvec_batch_flat4 / batch_group for the exact
-// per-32 regime (sml/sml-kernel.c:1008-1021, sml/sml-run.c:2058-2183)
+// y[r] = W.a[r] for nrow (1..65536) activation rows a[r] (q [nrow][cols],
+// scale and sums [nrow][cols/32]) into y [nrow][rows]: each weight streams
+// once for up to 16 rows (more rows run in slices of 16). replaces
+// sml_matvec_batch_flat4 / batch_group for the exact per-32 regime
+// (sml/sml-kernel.c:1008-1021, sml/sml-run.c:2058-2183)
 int sml_hip_gemm(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
                  float * y);
 // h[r] = silu(gate.a[r]) * (up.a[r]) for nrow rows, h [nrow][gate rows]
@@ -123,7 +124,10 @@ int sml_hip_gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const 
 // summing each superblock's sq_g*dot_g and (mq_g-127)*sum_g in integers and
 // applying the fp32 scales once per 256 columns; the rest runs the per-group
 // kernels, which are exact on such activations (the scale repeats in every
-// group).
+// group). Above 16 rows (prompt reading) Q4 runs on the prompt GEMM: tiles of
+// 128 weight rows (SwiGLU: 64) x 64 positions, the weight and activation
+// tiles staged in LDS, the same integer superblock sums; other widths run in
+// slices of 16 rows.
 // replaces sml_matvec_batch_flat4_sb and sml_rlp_matvec
 // (sml/sml-kernel.c:1414-1435,1820-1840) as batch_group dispatches them in
 // the prompt and default multi-sequence regimes (sml/sml-run.c:2090-2150)

@@ -61,6 +61,7 @@ static struct {
     uint16_t * kc, * vc;
     int32_t * hist, * pos, * tok;
     int2 * amax_part;          // pairs of the two-stage greedy pick
+    int * acnt;                // merge counters of the decode attention launch (one per kv head)
     float * lg_host;
     int32_t * pin;             // pinned: [0] tok, [1] pos, [2..] prompt ids
     hipStream_t st;
@@ -88,7 +89,9 @@ static struct {
     uint16_t ** kc_tab, ** vc_tab;   // device tables of every slot's cache base
     float * mpart;             // attention partials of every sequence of a batch
     int32_t * iota;            // device [n_ctx]: 0, 1, 2, ... (prompt chunk positions)
-    int32_t * slotid;          // device [MAX_SLOTS][MAX_SLOTS]: row s filled with s
+    int32_t * slotid;          // device [MAX_SLOTS][rrows]: row s filled with s
+    int rrows;                 // rows of the batched body's buffers: max(MAX_SLOTS, pb)
+    int pb;                    // positions per chunk of a level-2 prompt
     int rows_ok;               // 1: the batched body can run this model (-1: not checked yet)
     int rows_ready;            // the batched body's buffers are allocated
 } G;
@@ -225,7 +228,7 @@ static void launch_layer(int L) {
     uint16_t * kc = G.cur_slot ? G.kcs[G.cur_slot] : G.kc, * vc = G.cur_slot ? G.vcs[G.cur_slot] : G.vc;
     op_attention(G.st, G.q, G.k, G.v, kc + (size_t) L * G.n_ctx * kvd, vc + (size_t) L * G.n_ctx * kvd,
                  G.rc, G.rs, G.pos, G.H, G.KV, G.hd, G.n_ctx, G.part, G.att,
-                 fuse_q ? G.aq[0] : NULL, fuse_q ? G.as[0] : NULL, fuse_q ? G.asum[0] : NULL);
+                 fuse_q ? G.aq[0] : NULL, fuse_q ? G.as[0] : NULL, fuse_q ? G.asum[0] : NULL, G.acnt);
     if (fuse_q) slot[0] = 0;
     else prep(G.att, NULL, NULL, G.H * G.hd, &y->perm_o, 1, slot);
     gemv1(y->o, slot[0], SML_EPI_RESIDUAL, G.x, NULL, G.x);
@@ -489,6 +492,17 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     G.hb2 = dalloc((size_t) G.F * 4);
     G.logits = dalloc((size_t) G.V * 4);
     G.part = dalloc(sml_hip_attn_part_floats(G.H, G.hd, n_ctx) * 4);
+    // SML_ATTN_FOLD=1: the merge runs in the attention launch's last split of
+    // each kv head (counters, one per kv head, zero between launches). Off by
+    // default: measured slower at 4096 positions (Llama-3-8B shape 12.8 us
+    // per layer against 8.1 + 3.2 for the two launches; Qwen2.5-1.5B shape
+    // 14.8 against 7.8 + 3.9): the last split's device-scope store, count and
+    // re-read of every partial from memory sit on the launch's critical path.
+    G.acnt = NULL;
+    if (env_int("SML_ATTN_FOLD", 0)) {
+        G.acnt = dalloc((size_t) G.KV * 4);
+        HX(hipMemset(G.acnt, 0, (size_t) G.KV * 4));
+    }
     for (int i = 0; i < MAXACT; i++) {
         G.aq[i] = dalloc((size_t) wide);
         G.as[i] = dalloc((size_t) wide / 32 * 4);
@@ -525,6 +539,14 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     // prompt reading: batched (exact) unless SML_GPU_PP=0, as the reference's
     // open does (sml/sml-gpu-fwd.c:2371-2375)
     G.prompt_level = env_int("SML_GPU_PP", 1) == 0 || G.exact ? 0 : 1;
+    // level-2 chunk: SML_PB positions (16..4096, default 512); MoE layers
+    // take at most MAX_SLOTS rows per call
+    G.pb = env_int("SML_PB", 512);
+    if (G.pb < MAX_SLOTS) G.pb = MAX_SLOTS;
+    if (G.pb > 4096) G.pb = 4096;
+    if (G.pb > n_ctx) G.pb = n_ctx > MAX_SLOTS ? n_ctx : MAX_SLOTS;
+    if (G.moe_first) G.pb = MAX_SLOTS;
+    G.rrows = G.pb;
     G.rows_ok = -1;
     G.use_graph = env_int("SML_GRAPH", 1) != 0;
     if (G.use_graph) {
@@ -707,7 +729,7 @@ static void rows_tables(void) {
 // positions of one prompt chunk).
 static void rows_alloc(void) {
     if (G.rows_ready) return;     // set last: a failed attempt allocates afresh next time
-    const size_t R = MAX_SLOTS;
+    const size_t R = (size_t) G.rrows, S = MAX_SLOTS;
     size_t wide = (size_t) (G.F > G.E ? G.F : G.E);
     if ((size_t) G.H * G.hd > wide) wide = (size_t) G.H * G.hd;
     G.mx = dalloc(R * G.E * 4);
@@ -715,25 +737,30 @@ static void rows_alloc(void) {
     G.mqkv = dalloc(R * (size_t) (G.H + 2 * G.KV) * G.hd * 4);
     G.matt = dalloc(R * (size_t) G.H * G.hd * 4);
     G.mh = dalloc(R * (size_t) G.F * 4);
-    G.mlog = dalloc(R * (size_t) G.V * 4);
+    G.mlog = dalloc(S * (size_t) G.V * 4);          // the multi-sequence step's heads
     G.maq = dalloc(R * wide);
     G.mas = dalloc(R * wide / 32 * 4);
     G.masum = dalloc(R * wide / 32 * 4);
-    G.mtok = dalloc(R * 4);
-    G.mpos = dalloc(R * 4);
-    G.mslot = dalloc(R * 4);
-    G.mpart = dalloc(R * sml_hip_attn_part_floats(G.H, G.hd, G.n_ctx) * 4);
-    G.kc_tab = dalloc(R * sizeof(void *));
-    G.vc_tab = dalloc(R * sizeof(void *));
-    HX(hipHostMalloc((void **) &G.mpin, 3 * R * 4, 0));
-    int32_t * h = malloc((size_t) (G.n_ctx > (int) (R * R) ? G.n_ctx : (int) (R * R)) * 4);
+    G.mtok = dalloc(S * 4);
+    G.mpos = dalloc(S * 4);
+    G.mslot = dalloc(S * 4);
+    // partials: MAX_SLOTS entries at the decode kernels' finest split, or
+    // (level-2 prompts, the wave-per-position kernel) rrows at splits of 128
+    size_t part = S * sml_hip_attn_part_floats(G.H, G.hd, G.n_ctx);
+    const size_t part_pb = R * (size_t) G.H * (size_t) ((G.n_ctx + 127) / 128) * (size_t) (G.hd + 2);
+    if (part_pb > part) part = part_pb;
+    G.mpart = dalloc(part * 4);
+    G.kc_tab = dalloc(S * sizeof(void *));
+    G.vc_tab = dalloc(S * sizeof(void *));
+    HX(hipHostMalloc((void **) &G.mpin, 3 * S * 4, 0));
+    int32_t * h = malloc((size_t) (G.n_ctx > (int) (S * R) ? G.n_ctx : (int) (S * R)) * 4);
     if (!h) hx_failf("out of host memory");
     for (int i = 0; i < G.n_ctx; i++) h[i] = i;
     G.iota = dalloc((size_t) G.n_ctx * 4);
     HX(hipMemcpy(G.iota, h, (size_t) G.n_ctx * 4, hipMemcpyHostToDevice));
-    for (int i = 0; i < (int) (R * R); i++) h[i] = i / (int) R;
-    G.slotid = dalloc(R * R * 4);
-    HX(hipMemcpy(G.slotid, h, R * R * 4, hipMemcpyHostToDevice));
+    for (int i = 0; i < (int) (S * R); i++) h[i] = i / (int) R;
+    G.slotid = dalloc(S * R * 4);
+    HX(hipMemcpy(G.slotid, h, S * R * 4, hipMemcpyHostToDevice));
     free(h);
     rows_tables();
     G.rows_ready = 1;
@@ -823,19 +850,25 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
 }
 
 // Batched prompt reading, the reference's gpu_prefill (sml/sml-gpu-fwd.c:
-// 1418-1603): chunks of up to MAX_SLOTS positions through the batched body,
-// each weight matrix streamed once per chunk; the last position's residual
-// then goes through the decode tail (final norm, head, greedy pick). At
-// level 1 every product is the GEMV's arithmetic and the attention the
-// decode kernel's, so the cache, the residuals and the logits equal reading
-// the prompt a token at a time, bit for bit. The ids are already in G.hist.
+// 1418-1603): chunks of positions through the batched body, each weight
+// matrix streamed once per chunk; the last position's residual then goes
+// through the decode tail (final norm, head, greedy pick). The ids are
+// already in G.hist.
+//  - level 1: chunks of MAX_SLOTS; every product is the GEMV's arithmetic and
+//    the attention the decode kernel's, so the cache, the residuals and the
+//    logits equal reading the prompt a token at a time, bit for bit.
+//  - level 2: chunks of pb (512) positions in the reference's prompt regime
+//    (activations per 256 values, integer superblock sums: the CPU engine's
+//    default prompt arithmetic, sml/sml-run.c:1929-1945), Q4 products on the
+//    prompt MFMA GEMM, attention a wave per position.
 static void prefill_rows(int slot, int pos0, int n) {
     rows_alloc();
-    const int regime = G.prompt_level >= 2 ? GEMM_PER32 : GEMM_EXACT;
+    const int regime = G.prompt_level >= 2 ? GEMM_PER256 : GEMM_EXACT;
+    const int chunk = G.prompt_level >= 2 ? G.pb : MAX_SLOTS;
     int last = 0;
-    for (int p0 = 0; p0 < n; p0 += MAX_SLOTS) {
-        const int nb = n - p0 < MAX_SLOTS ? n - p0 : MAX_SLOTS;
-        launch_rows(nb, G.hist + pos0 + p0, G.iota + pos0 + p0, G.slotid + slot * MAX_SLOTS, regime, 1, 0);
+    for (int p0 = 0; p0 < n; p0 += chunk) {
+        const int nb = n - p0 < chunk ? n - p0 : chunk;
+        launch_rows(nb, G.hist + pos0 + p0, G.iota + pos0 + p0, G.slotid + (size_t) slot * G.rrows, regime, 1, 0);
         last = nb - 1;
     }
     HX(hipMemcpyAsync(G.x, G.mx + (size_t) last * G.E, (size_t) G.E * 4, hipMemcpyDeviceToDevice, G.st));

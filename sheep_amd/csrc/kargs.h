@@ -137,6 +137,12 @@ typedef struct {
     // entries are consecutive positions of one sequence (one slot, positions
     // increasing) and share each split's K/V tile
     int tpw, nseq;
+    // one-entry launches (tpw 1): when not NULL, counters [nseq][n_kv], zero
+    // between launches. Each workgroup writes its partials coherently at
+    // device scope and counts itself in; the last of a kv head's splits
+    // merges that head's query heads as sml_attn_merge does and resets the
+    // counter, so no merge launch follows. One launch at a time per array.
+    int * cnt;
 } sml_kattn;
 
 // Decode attention in the reference's float order (exact mode): RoPE of q and

@@ -999,6 +999,77 @@ __device__ __forceinline__ void wave_heads(const float (&x)[REP], float (&out)[R
     }
 }
 
+// Merge of the splits of one query head: out = sum_s e_s o_s / sum_s e_s l_s
+// with e_s = 2^(m_s - max m) (the split maxima are in base 2). Every split
+// has a partial (max -inf for splits past the position), so a batch of 32
+// splits is loaded at once with no position read first: lane s of the wave
+// takes split s's (max, sum) and its weight e_s, which the dims then read back
+// as a scalar. The calling wave holds 64 consecutive dims d of head h (lane =
+// d & 63). With q_out set, the head's 128 outputs (4 groups of 32, identity
+// permutation) are also quantized for the next GEMV (sml/sml-kernel.c:86-106).
+// DEV: the partials were written by other workgroups of the running launch,
+// so they are read at device scope.
+#define MERGE_BATCH 32
+template <bool DEV> __device__ __forceinline__ float ld_part(const float * p) {
+    if constexpr (DEV) return __hip_atomic_load((float *) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+}
+template <bool DEV> __device__ __forceinline__ float2 ld_part2(const float2 * p) {
+    if constexpr (DEV)
+        return __builtin_bit_cast(float2, __hip_atomic_load((unsigned long long *) p, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT));
+    else return *p;
+}
+// stores of partials that another workgroup of the same launch reads:
+// coherent at device scope once the storing wave's vmcnt reaches zero
+__device__ __forceinline__ void st_dev(float * p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev2(float2 * p, float2 v) {
+    __hip_atomic_store((unsigned long long *) p, __builtin_bit_cast(unsigned long long, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool DEV>
+__device__ __forceinline__ void merge_head(const sml_kattn & a, int b, int h, int d) {
+    const int lane = d & 63;
+    const float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
+    const float * po = blk + (size_t) h * a.nsplit * HD;
+    const float2 * pml = (const float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) h * a.nsplit;
+    const size_t ob = (size_t) b * a.n_head * HD;
+    float M = -INFINITY, L = 0.0f, o = 0.0f;
+    for (int s0 = 0; s0 < a.nsplit; s0 += MERGE_BATCH) {
+        const int n = min(MERGE_BATCH, a.nsplit - s0);
+        float ov[MERGE_BATCH];
+        #pragma unroll
+        for (int s = 0; s < MERGE_BATCH; s++) ov[s] = ld_part<DEV>(po + (size_t) (s0 + (s < n ? s : 0)) * HD + d);   // masked below
+        const float2 ml = ld_part2<DEV>(pml + s0 + (lane < n ? lane : 0));
+        const float mj = lane < n ? ml.x : -INFINITY;
+        const float Mb = fmaxf(M, rl(max32(mj), 0));         // finite: split 0 is active
+        const float r = __builtin_amdgcn_exp2f(M - Mb);      // M = -inf: 0
+        const float e = __builtin_amdgcn_exp2f(mj - Mb);     // 0 for splits past the position
+        L = L * r + rl(sum32(lane < n ? e * ml.y : 0.0f), 0);
+        float acc[4] = {o * r, 0.0f, 0.0f, 0.0f};
+        #pragma unroll
+        for (int s = 0; s < MERGE_BATCH; s++) {
+            const float es = rl(e, s);
+            acc[s & 3] += es != 0.0f ? es * ov[s] : 0.0f;     // an empty split's V sums are not read
+        }
+        o = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        M = Mb;
+    }
+    const float r = o / L;
+    a.out[ob + (size_t) h * HD + d] = r;
+    if (!a.q_out) return;
+    const float amax = max32(fabsf(r));
+    const float s = amax / 127.0f;
+    const float is = s > 0.0f ? 1.0f / s : 0.0f;
+    const int t = quant1(r, is);
+    const int sum = isum32(t);
+    const int g = h * 4 + (d >> 5);
+    a.q_out[ob + (size_t) h * HD + d] = (int8_t) t;
+    if ((d & 31) == 0) { a.s_out[ob / 32 + g] = s; a.u_out[ob / 32 + g] = sum; }
+}
+
 // CH: positions per split (128; the one-sequence decode launch also takes 32
 // or 64, so that models with few KV heads still fill the chip)
 template <int REP, int NW, bool CHUNK, int CH = ATTN_CHUNK>
@@ -1056,6 +1127,23 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             vw[i] = __builtin_nontemporal_load((const v4u *) (vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
         }
     }
+    // merge folded in (one-entry launches with counters): once every wave's
+    // partial stores have completed at device scope, the workgroup counts
+    // itself in; the last of the kv head's splits merges its query heads
+    // (two waves' worth of dims each) and clears the counter for the next launch
+    const bool fold = !CHUNK && a.cnt != nullptr;
+    auto fold_merge = [&](int b) {
+        __shared__ int last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        int * cnt = a.cnt + (size_t) b * a.n_kv + kh;
+        if (tid == 0)
+            last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int) gridDim.x - 1;
+        __syncthreads();
+        if (!last) return;
+        for (int t = wave; t < 2 * REP; t += NW) merge_head<true>(a, b, kh * REP + t / 2, (t & 1) * 64 + (tid & 63));
+        if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
     // each entry's arithmetic is the one-entry kernel's, position for position;
     // with few heads the next entry's inputs load while this one computes
     constexpr bool PF = CHUNK && REP <= 4;
@@ -1075,7 +1163,11 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     float * po = blk + (size_t) kh * REP * a.nsplit * HD;
     float2 * pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) kh * REP * a.nsplit;
     if (t0 >= T) {
-        if (tid < REP) pml[(size_t) tid * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
+        if (tid < REP) {
+            if (fold) st_dev2(pml + (size_t) tid * a.nsplit + split, make_float2(-INFINITY, 0.0f));
+            else pml[(size_t) tid * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
+        }
+        if (fold) fold_merge(b);
         continue;
     }
     const int t1 = min(T, t0 + CH);
@@ -1178,9 +1270,15 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             o += e * red[w][j][d];
             L += e * wl[w][j];
         }
-        po[((size_t) j * a.nsplit + split) * HD + d] = o;
-        if (d == 0) pml[(size_t) j * a.nsplit + split] = make_float2(M, L);
+        if (fold) {
+            st_dev(po + ((size_t) j * a.nsplit + split) * HD + d, o);
+            if (d == 0) st_dev2(pml + (size_t) j * a.nsplit + split, make_float2(M, L));
+        } else {
+            po[((size_t) j * a.nsplit + split) * HD + d] = o;
+            if (d == 0) pml[(size_t) j * a.nsplit + split] = make_float2(M, L);
+        }
     }
+    if (fold) fold_merge(b);
     if (b + 1 < b1) __syncthreads();                  // red, wm and wl are the next entry's
     }
 }
@@ -1363,53 +1461,10 @@ __device__ __forceinline__ void attnw_body(const sml_kattn & a) {
     extern "C" __global__ __launch_bounds__(64 * ATTNW_WAVES) void sml_attnw_r##R(const sml_kattn a) { attnw_body<R>(a); }
 ATTNW_KERNEL(1) ATTNW_KERNEL(2) ATTNW_KERNEL(3) ATTNW_KERNEL(4) ATTNW_KERNEL(5) ATTNW_KERNEL(6) ATTNW_KERNEL(7) ATTNW_KERNEL(8)
 
-// Merge of the splits of one query head (grid: n_head workgroups of HD
-// threads): out = sum_s e_s o_s / sum_s e_s l_s with e_s = 2^(m_s - max m)
-// (the split maxima are in base 2). Every split has a partial (max -inf for
-// splits past the position), so a batch of 32 splits is loaded at once with
-// no position read first: lane s of each wave takes split s's (max, sum) and
-// its weight e_s, which the dims then read back as a scalar.
-// With q_out set, the head's 128 outputs (4 groups of 32, identity
-// permutation) are also quantized for the next GEMV (sml/sml-kernel.c:86-106).
-#define MERGE_BATCH 32
+// The merge as its own launch (grid: n_head workgroups of HD threads, z:
+// the sequence).
 extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn a) {
-    const int h = blockIdx.x, d = threadIdx.x, b = blockIdx.z, lane = d & 63;     // head, dim, sequence
-    const float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
-    const float * po = blk + (size_t) h * a.nsplit * HD;
-    const float2 * pml = (const float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) h * a.nsplit;
-    const size_t ob = (size_t) b * a.n_head * HD;
-    float M = -INFINITY, L = 0.0f, o = 0.0f;
-    for (int s0 = 0; s0 < a.nsplit; s0 += MERGE_BATCH) {
-        const int n = min(MERGE_BATCH, a.nsplit - s0);
-        float ov[MERGE_BATCH];
-        #pragma unroll
-        for (int s = 0; s < MERGE_BATCH; s++) ov[s] = po[(size_t) (s0 + (s < n ? s : 0)) * HD + d];   // masked below
-        const float2 ml = pml[s0 + (lane < n ? lane : 0)];
-        const float mj = lane < n ? ml.x : -INFINITY;
-        const float Mb = fmaxf(M, rl(max32(mj), 0));         // finite: split 0 is active
-        const float r = __builtin_amdgcn_exp2f(M - Mb);      // M = -inf: 0
-        const float e = __builtin_amdgcn_exp2f(mj - Mb);     // 0 for splits past the position
-        L = L * r + rl(sum32(lane < n ? e * ml.y : 0.0f), 0);
-        float acc[4] = {o * r, 0.0f, 0.0f, 0.0f};
-        #pragma unroll
-        for (int s = 0; s < MERGE_BATCH; s++) {
-            const float es = rl(e, s);
-            acc[s & 3] += es != 0.0f ? es * ov[s] : 0.0f;     // an empty split's V sums are not read
-        }
-        o = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        M = Mb;
-    }
-    const float r = o / L;
-    a.out[ob + (size_t) h * HD + d] = r;
-    if (!a.q_out) return;
-    const float amax = max32(fabsf(r));
-    const float s = amax / 127.0f;
-    const float is = s > 0.0f ? 1.0f / s : 0.0f;
-    const int t = quant1(r, is);
-    const int sum = isum32(t);
-    const int g = h * 4 + (d >> 5);
-    a.q_out[ob + (size_t) h * HD + d] = (int8_t) t;
-    if ((d & 31) == 0) { a.s_out[ob / 32 + g] = s; a.u_out[ob / 32 + g] = sum; }
+    merge_head<false>(a, blockIdx.z, blockIdx.x, threadIdx.x);
 }
 
 // ---------------------------------------------------------------- attention in the reference's order
@@ -2484,3 +2539,272 @@ MGEMM_KERNEL(2, 8)
 MGEMM_KERNEL_P(1, 8)
 
 
+
+// ---------------------------------------------------------------- prompt GEMM on MFMA (Q4, per-256 activations)
+//
+// Y[p][r] = W.a[p] for a chunk of prompt positions p (hundreds) and every row
+// r of a Q4 matrix, in the reference's prompt regime (sml_quantize_act_sb and
+// flat4_sb_body, sml/sml-kernel.c:115-185,1142-1190): per superblock b of 256
+// columns the integer sums
+//     isum = sum_g sq_g * dot_g,    imin = sum_g (mq_g - 127) * sum(q_g),
+// then y += isum * (sd_b * s_b) + imin * (md_b * s_b) in fp32 (s_b: the
+// position's activation scale of superblock b).
+//
+// Workgroup tile: 128 weight rows x 32 positions (SwiGLU: 64 rows of gate
+// and the same 64 rows of up), 4 waves of 32 rows (SwiGLU: 16 gate + 16 up)
+// x 32 positions, i.e. 2 x 2 tiles of v_mfma_i32_16x16x32_i8 per group (lane
+// layout as in mgemm_q4_body: lane l holds A row / B column l%16 and k =
+// 8(l/16)..+7, and receives D rows 4(l/16)..+3 of column l%16, so it owns one
+// weight row of each tile and four positions).
+//  - dot_g: one MFMA per (tile, group); A = the positions' int8 codes, B =
+//    the group's 4-bit codes as bytes; sq_g * dot_g adds up on the VALU in
+//    24-bit multiply-adds (|dot_g| < 2^16, sq_g < 2^8).
+//  - imin: one MFMA per (tile, group) with B = (mq_g - 128) in every byte
+//    (an int8 for every mq_g), so the product is (mq_g - 128) * sum(q_g),
+//    accumulated over the superblock's 8 groups in the MFMA's own
+//    accumulator; the superblock's sum of q (from the activation's group
+//    sums, staged with its scale) then makes it sum_g (mq_g - 127) * sum(q_g).
+// Each superblock's weight tile (128 rows x 128 bytes) and activation tile
+// (32 positions x 256 bytes) are staged in LDS, double-buffered: the next
+// superblock's global loads are in flight while this one computes. In LDS a
+// weight row keeps, per k-slice kq, its four 8-byte chunks (quad, half) side
+// by side; an activation row keeps, per kq, its 8 groups' 8-byte slices side
+// by side (16 bytes of padding per row: no bank conflicts across the 16 rows
+// a wave reads at once). The fields (sq, mq per group; sd, md per superblock)
+// go straight to registers, one lane per row.
+//
+// Tiles are numbered so that consecutive ones share their weight rows and
+// sit on one XCD (workgroup i runs on XCD i mod 8): the positions' tiles of a
+// weight tile find it in that XCD's L2.
+#define PG_BN 128
+#define PG_BM 32
+#define PG_BROW 144
+#define PG_AROW 272
+#define PG_STAGE (PG_BN * PG_BROW + PG_BM * PG_AROW + PG_BM * 8)
+
+template <bool SW>
+__device__ void pgemm_q4_body(const sml_kgemm & a) {
+    typedef long v1l;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int n = a.cols, ng = n / 32, nsb = n / 256, m_all = a.m_all, rows = a.rows;
+    const int tid = threadIdx.x, lane = tid & 63, kq = lane >> 4, i16 = lane & 15;
+    constexpr int MT = PG_BM / 16, AWN = PG_BM / 16;          // m-tiles per wave, activation words per thread
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    constexpr int RT = SW ? PG_BN / 2 : PG_BN;                 // output rows per tile
+    const int nrt = (rows + RT - 1) / RT, npt = (m_all + PG_BM - 1) / PG_BM, total = nrt * npt;
+    const int id = blockIdx.x, xcd = id & 7, slot = id >> 3, q8 = total >> 3, rem = total & 7;
+    const int lid = (xcd < rem ? xcd * (q8 + 1) : rem * (q8 + 1) + (xcd - rem) * q8) + slot;
+    const int rt = lid / npt, pt = lid - rt * npt;
+    const int r0 = rt * RT, p0 = pt * PG_BM;
+    const uint32_t rowb = (uint32_t) n / 2;
+
+    // staging: thread t copies 16-byte words t + 256i of the weight tile
+    // (row w/8 = t/8 + 32i, bytes 16(t%8)..; SwiGLU: i < 2 gate, i >= 2 up)
+    // and of the activation tile (position t/16 + 16i, bytes 16(t%16)..);
+    // rows and positions past the end read the last one. 32-bit offsets:
+    // the host keeps rows x cols / 2 and positions x cols below 2^32.
+    const uint8_t * bplane[2] = {a.mats[0].plane[0], a.mats[SW ? 1 : 0].plane[0]};
+    uint32_t boff[4], aoff[AWN];
+    #pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int lr = (tid >> 3) + 32 * i, rr = SW ? (lr & 63) : lr;
+        boff[i] = (uint32_t) min(r0 + rr, rows - 1) * rowb + 16u * (uint32_t) (tid & 7);
+    }
+    #pragma unroll
+    for (int i = 0; i < AWN; i++)
+        aoff[i] = (uint32_t) min(p0 + (tid >> 4) + 16 * i, m_all - 1) * (uint32_t) n + 16u * (uint32_t) (tid & 15);
+    const int jb = tid & 7, ja = tid & 15;
+    const uint32_t bdst0 = (uint32_t) ((tid >> 3) * PG_BROW + (2 * (jb & 1)) * 32 + (2 * (jb >> 2) + ((jb >> 1) & 1)) * 8);
+    const uint32_t adst0 = (uint32_t) (PG_BN * PG_BROW + (tid >> 4) * PG_AROW + (2 * (ja & 1)) * 64 + (ja >> 1) * 8);
+    const float * ssrc = a.scale + (size_t) min(p0 + (tid & (PG_BM - 1)), m_all - 1) * ng;
+    const int32_t * usrc = a.sums + (size_t) min(p0 + (tid & (PG_BM - 1)), m_all - 1) * ng;
+    // this wave's two 16-row blocks (LDS row of the block's first row, and
+    // the lane's global row)
+    int lrow[2], grow[2];
+    #pragma unroll
+    for (int t = 0; t < 2; t++) {
+        lrow[t] = SW ? t * 64 + 16 * wave : 32 * wave + 16 * t;
+        grow[t] = r0 + (SW ? 16 * wave : 32 * wave + 16 * t) + i16;
+    }
+    const uint8_t * fqb[2];
+    const uint8_t * fdb[2];
+    #pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const sml_kmat & m = a.mats[SW ? t : 0];
+        const size_t gr = (size_t) min(grow[t], rows - 1);
+        fqb[t] = m.sqmq + gr * (size_t) ng * 2;
+        fdb[t] = (const uint8_t *) m.sdmd + gr * (size_t) nsb * 4;
+    }
+
+    v4u bw[4], aw[AWN];
+    float sw_ = 0.0f;
+    int4 su0 = make_int4(0, 0, 0, 0), su1 = su0;
+    v4u fq[2], fqn[2];
+    uint32_t fd[2], fdn[2];
+    auto fetch = [&](int b, v4u (&q)[2], uint32_t (&d)[2]) {
+        #pragma unroll
+        for (int i = 0; i < 4; i++)
+            bw[i] = __builtin_nontemporal_load((const v4u *) (bplane[SW && i >= 2] + (boff[i] + 128u * (uint32_t) b)));
+        #pragma unroll
+        for (int i = 0; i < AWN; i++) aw[i] = *(const v4u *) (a.q + (aoff[i] + 256u * (uint32_t) b));
+        if (tid < PG_BM) {
+            sw_ = ssrc[8 * b];
+            su0 = *(const int4 *) (usrc + 8 * b);
+            su1 = *(const int4 *) (usrc + 8 * b + 4);
+        }
+        #pragma unroll
+        for (int t = 0; t < 2; t++) {
+            q[t] = *(const v4u *) (fqb[t] + (size_t) b * 16);
+            d[t] = *(const uint32_t *) (fdb[t] + (size_t) b * 4);
+        }
+    };
+    auto stage = [&](int buf) {
+        uint8_t * base = lds + (size_t) buf * PG_STAGE;
+        #pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint8_t * bd = base + bdst0 + i * 32 * PG_BROW;
+            *(v2u *) bd = v2u{bw[i][0], bw[i][1]};
+            *(v2u *) (bd + 32) = v2u{bw[i][2], bw[i][3]};
+        }
+        #pragma unroll
+        for (int i = 0; i < AWN; i++) {
+            uint8_t * ad = base + adst0 + i * 16 * PG_AROW;
+            *(v2u *) ad = v2u{aw[i][0], aw[i][1]};
+            *(v2u *) (ad + 64) = v2u{aw[i][2], aw[i][3]};
+        }
+        if (tid < PG_BM) {
+            float * sd_ = (float *) (base + PG_BN * PG_BROW + PG_BM * PG_AROW);
+            sd_[tid] = sw_;
+            ((int *) (sd_ + PG_BM))[tid] = (su0.x + su0.y) + (su0.z + su0.w) + ((su1.x + su1.y) + (su1.z + su1.w));
+        }
+    };
+
+    float acc[2][MT][4];
+    #pragma unroll
+    for (int t = 0; t < 2; t++)
+        #pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            #pragma unroll
+            for (int r = 0; r < 4; r++) acc[t][mt][r] = 0.0f;
+
+    auto compute = [&](int buf) {
+        const uint8_t * base = lds + (size_t) buf * PG_STAGE;
+        const uint8_t * abase = base + PG_BN * PG_BROW;
+        const float * sbase = (const float *) (abase + PG_BM * PG_AROW);
+        const int * ubase = (const int *) (sbase + PG_BM);
+        // the lane's weight row: its 4 chunks of k-slice kq (quad, half)
+        v4u pk[2][2];
+        #pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const uint8_t * p = base + (lrow[t] + i16) * PG_BROW + kq * 32;
+            pk[t][0] = *(const v4u *) p;
+            pk[t][1] = *(const v4u *) (p + 16);
+        }
+        int is[2][MT][4];
+        v4i im[2][MT];
+        #pragma unroll
+        for (int t = 0; t < 2; t++)
+            #pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                im[t][mt] = v4i{0, 0, 0, 0};
+                #pragma unroll
+                for (int r = 0; r < 4; r++) is[t][mt][r] = 0;
+            }
+        #pragma unroll
+        for (int g = 0; g < 8; g++) {
+            // order the groups: the sums so far pass through an (empty)
+            // volatile statement, so this group's MFMAs cannot be issued
+            // before the last group's multiply-adds have consumed its results
+            // (pure arithmetic is otherwise free to move, and all eight
+            // groups' products would be held in registers at once)
+            #pragma unroll
+            for (int t = 0; t < 2; t++)
+                #pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    asm volatile("" : "+v"(is[t][mt][0]), "+v"(is[t][mt][1]), "+v"(is[t][mt][2]), "+v"(is[t][mt][3]));
+            const int c = 2 * (g >> 2) + ((g >> 1) & 1), sh = 4 * (g & 1);
+            v1l bc[2], bm[2];
+            int sq[2];
+            #pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const unsigned lo = (pk[t][c >> 1][2 * (c & 1)] >> sh) & 0x0F0F0F0Fu;
+                const unsigned hi = (pk[t][c >> 1][2 * (c & 1) + 1] >> sh) & 0x0F0F0F0Fu;
+                bc[t] = (v1l) (((unsigned long) hi << 32) | lo);
+                const uint32_t f = fq[t][g >> 1] >> (16 * (g & 1));
+                sq[t] = (int) (f & 0xFFu);
+                const unsigned m4 = (((f >> 8) & 0xFFu) ^ 0x80u) * 0x01010101u;     // mq - 128 as int8
+                bm[t] = (v1l) (((unsigned long) m4 << 32) | m4);
+            }
+            #pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const v1l av = *(const v1l *) (abase + (16 * mt + i16) * PG_AROW + kq * 64 + g * 8);
+                #pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    v4i d = {0, 0, 0, 0};
+                    d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bc[t], d, 0, 0, 0);
+                    im[t][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bm[t], im[t][mt], 0, 0, 0);
+                    #pragma unroll
+                    for (int r = 0; r < 4; r++) is[t][mt][r] = __mul24(sq[t], d[r]) + is[t][mt][r];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        #pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const float4 s4 = *(const float4 *) (sbase + 16 * mt + 4 * kq);
+            const int4 u4 = *(const int4 *) (ubase + 16 * mt + 4 * kq);
+            const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+            const int uv[4] = {u4.x, u4.y, u4.z, u4.w};
+            #pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const float dsc = h2f((uint16_t) (fd[t] & 0xFFFFu)), mdsc = h2f((uint16_t) (fd[t] >> 16));
+                #pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    acc[t][mt][r] += (float) is[t][mt][r] * (dsc * sv[r]);
+                    acc[t][mt][r] += (float) (im[t][mt][r] + uv[r]) * (mdsc * sv[r]);
+                }
+            }
+        }
+    };
+
+    fetch(0, fq, fd);
+    stage(0);
+    __syncthreads();
+    for (int b = 0; b < nsb; b++) {
+        const bool more = b + 1 < nsb;
+        if (more) fetch(b + 1, fqn, fdn);
+        compute(b & 1);
+        if (more) {
+            stage((b + 1) & 1);
+            #pragma unroll
+            for (int t = 0; t < 2; t++) { fq[t] = fqn[t]; fd[t] = fdn[t]; }
+        }
+        __syncthreads();
+    }
+
+    #pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+        #pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int pos = p0 + 16 * mt + 4 * kq + r;
+            if (pos >= m_all) continue;
+            float * y = a.y + (size_t) pos * rows;
+            if constexpr (SW) {
+                const int row = grow[0];
+                if (row < rows) y[row] = silu_ref(acc[0][mt][r]) * acc[1][mt][r];        // sml/sml-run.c:416-426
+            } else {
+                #pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const int row = grow[t];
+                    if (row >= rows) continue;
+                    float v = acc[t][mt][r];
+                    if (a.bias) v += a.bias[row];
+                    if (a.resid) v = a.resid[(size_t) pos * rows + row] + v;
+                    y[row] = v;
+                }
+            }
+        }
+}
+
+extern "C" __global__ __launch_bounds__(256, 2) void sml_pgemm_q4(const sml_kgemm a) { pgemm_q4_body<false>(a); }
+extern "C" __global__ __launch_bounds__(256, 2) void sml_pgemm_q4_s(const sml_kgemm a) { pgemm_q4_body<true>(a); }

@@ -546,7 +546,7 @@ static int attn_split(int n_kv, int n_ctx) {
 void op_attention(hipStream_t st, const float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
                   const float * cos_t, const float * sin_t, const int32_t * pos, int n_head, int n_kv,
                   int hd, int n_ctx, float * part, float * out, int8_t * q_out, float * s_out,
-                  int32_t * u_out) {
+                  int32_t * u_out, int * cnt) {
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
     if (g_exact) {
@@ -576,11 +576,12 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     a.part = part; a.out = out; a.q_out = q_out; a.s_out = s_out; a.u_out = u_out;
     a.n_head = n_head; a.n_kv = n_kv; a.nsplit = ns;
     a.inv = 1.0f / __builtin_sqrtf((float) hd);
+    a.cnt = cnt;                                      // the merge runs in the last split of each kv head
     char name[32];
     if (ch != ATTN_CHUNK) snprintf(name, sizeof name, "sml_attn8_s%d_r%d", ch, n_head / n_kv);
     else snprintf(name, sizeof name, "sml_attn%d_r%d", aw, n_head / n_kv);
     hx_launch(name, (unsigned) ns, (unsigned) n_kv, (unsigned) (64 * aw), 0, st, &a);
-    hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
+    if (!cnt) hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
 }
 
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
@@ -647,7 +648,7 @@ int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kc
                       int n_head, int n_kv, int hd, int n_ctx, float * part, float * out) {
     OP_BEGIN(-1);
     op_attention(0, q, k, v, kcache, vcache, cos_t, sin_t, pos, n_head, n_kv, hd, n_ctx, part, out,
-                 NULL, NULL, NULL);
+                 NULL, NULL, NULL, NULL);
     HX_LEAVE();
     return 0;
 }
@@ -898,15 +899,47 @@ int gemm_exact(int regime, int m_all) {
 }
 
 #define GEMM_TILE 128            // chunks (groups) per pass: 64 lanes x GEMM_NI
+// The prompt GEMM (sml_pgemm_q4): positions per tile, and its LDS: two
+// stages of a 128-row weight tile (144 bytes a row), a PGEMM_BM-position
+// activation tile (272 bytes a row) and the positions' scales and sums
+#define PGEMM_BM 32
+#define PGEMM_LDS (2 * (128 * 144 + PGEMM_BM * 272 + PGEMM_BM * 8))
+#define GEMM_MAX_ROWS 65536
 
 void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
              const int32_t * sums, float * y, const float * bias, const float * resid, int regime) {
     const int per256 = regime == GEMM_PER256;
     if (swiglu && (bias || resid)) hx_failf("SwiGLU GEMM takes no bias or residual");
+    if ((uint64_t) rows * (uint64_t) cols >= (1ull << 32)) hx_failf("matrix too large for one GEMM launch");
+    if (!count && m_all > 16) {
+        // prompt-sized: Q4 with per-256 activations on the prompt MFMA GEMM
+        // (tiles of 128 rows, SwiGLU 64, x PGEMM_BM positions); anything else in
+        // slices of 16 rows through the small-M kernels
+        if (per256 && nbits == 4 && cols % 256 == 0 && env_int("SML_PGEMM", 1)) {
+            const int rt = swiglu ? 64 : 128;
+            const uint64_t tiles = (uint64_t) ((rows + rt - 1) / rt) * (uint64_t) ((m_all + PGEMM_BM - 1) / PGEMM_BM);
+            if (tiles > 0x7FFFFFFFull || (uint64_t) m_all * (uint64_t) cols >= (1ull << 32))
+                hx_failf("prompt GEMM of %d rows x %d positions", rows, m_all);
+            sml_kgemm a;
+            memset(&a, 0, sizeof a);
+            a.mats = tab; a.nmat = swiglu ? 2 : 1; a.cols = cols; a.rows = rows;
+            a.m_all = m_all; a.mmax = mmax;
+            a.q = q; a.scale = scale; a.sums = sums; a.y = y; a.bias = bias; a.resid = resid;
+            hx_launch(swiglu ? "sml_pgemm_q4_s" : "sml_pgemm_q4", (unsigned) tiles, 1, 256, PGEMM_LDS, st, &a);
+            return;
+        }
+        const int ng = cols / 32;
+        for (int s = 0; s < m_all; s += 16) {
+            const int k = m_all - s < 16 ? m_all - s : 16;
+            op_gemm(st, tab, 1, swiglu, nbits, rows, cols, NULL, k, gemm_mt(k), k, q + (size_t) s * cols,
+                    scale + (size_t) s * ng, sums + (size_t) s * ng, y + (size_t) s * rows, bias,
+                    resid ? resid + (size_t) s * rows : NULL, regime);
+        }
+        return;
+    }
     if (mt != 1 && mt != 4 && mt != 8 && mt != 16) hx_failf("small-M GEMM takes at most 16 rows");
     if (!count && (m_all < 1 || m_all > mt)) hx_failf("small-M GEMM of %d rows", m_all);
-    if ((uint64_t) rows * (uint64_t) cols >= (1ull << 32)) hx_failf("matrix too large for one GEMM launch");
     sml_kgemm a;
     memset(&a, 0, sizeof a);
     a.mats = tab; a.nmat = swiglu ? 2 : 1; a.cols = cols; a.rows = rows;
@@ -984,14 +1017,14 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
 
 static void gemm_one(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
                      float * y, int per256) {
-    if (!m || nrow < 1 || nrow > 16) hx_failf("gemm of %d rows (1..16)", nrow);
+    if (!m || nrow < 1 || nrow > GEMM_MAX_ROWS) hx_failf("gemm of %d rows (1..%d)", nrow, GEMM_MAX_ROWS);
     op_gemm(0, m->kdev, 1, 0, m->nbits, m->k.rows, m->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, y, NULL, NULL,
             per256);
 }
 
 static void gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const int8_t * q, const float * scale,
                         const int32_t * sums, int nrow, float * h, int per256) {
-    if (!gate || !up || nrow < 1 || nrow > 16) hx_failf("gemm of %d rows (1..16)", nrow);
+    if (!gate || !up || nrow < 1 || nrow > GEMM_MAX_ROWS) hx_failf("gemm of %d rows (1..%d)", nrow, GEMM_MAX_ROWS);
     if (up->nbits != gate->nbits || up->cols != gate->cols || up->k.rows != gate->k.rows)
         hx_failf("SwiGLU needs gate and up of one shape and width");
     // the (gate, up) table lives in the gate matrix's allocation, rewritten

@@ -75,10 +75,13 @@ void op_embed_rows(hipStream_t st, const sml_hip_mat * m, const int32_t * tok, c
 void op_normq_rows(hipStream_t st, float * x, const float * resid, const float * w, float eps, int n, int rows,
                    int nout, const int32_t * const * perm, int8_t * const * q, float * const * scale,
                    int32_t * const * sums, float * normed, int per256);
+// Decode attention for one sequence. cnt: n_kv zeroed counters (the merge then
+// runs in the attention launch itself, see sml_kattn.cnt), or NULL for a
+// separate merge launch.
 void op_attention(hipStream_t st, const float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
                   const float * cos_t, const float * sin_t, const int32_t * pos, int n_head, int n_kv,
                   int hd, int n_ctx, float * part, float * out, int8_t * q_out, float * s_out,
-                  int32_t * u_out);
+                  int32_t * u_out, int * cnt);
 // Attention for nseq sequences in one launch: sequence b's q, k, v at
 // qkv + b * qkv_stride (q, then k, then v), its cache kc_slots[slot[b]] +
 // layer_off, its position pos[b]; part, out and the quantized out hold one

@@ -147,6 +147,29 @@ def test_fusions_do_not_change_logits(model, request, monkeypatch):
         assert int(np.argmax(a)) == int(np.argmax(b))
 
 
+@pytest.mark.parametrize("model", ["tiny", "qwenish"])
+def test_folded_merge_equals_merge_launch(model, request, monkeypatch):
+    """SML_ATTN_FOLD=1 merges the attention splits in the attention launch
+    (the last split of each kv head, after a device-scope count); the merge
+    arithmetic is the merge launch's, so every step's logits are the same
+    bits, also past the first split (positions 0..150, splits of 64/128)."""
+    path = request.getfixturevalue(model)
+    V = 2000 if model == "tiny" else 32000
+    ids = np.random.default_rng(5).integers(0, V, 150).astype(np.int32)
+    outs = []
+    for fold in ("0", "1"):
+        monkeypatch.setenv("SML_ATTN_FOLD", fold)
+        d = sa.Decoder(path, n_ctx=256)
+        try:
+            got = [d.step(int(t), i, V).copy() for i, t in enumerate(ids)]
+            got.append(np.array(d.generate(int(ids[-1]), len(ids), 8), np.float32))
+            outs.append(got)
+        finally:
+            d.close()
+    for i, (a, b) in enumerate(zip(*outs)):
+        np.testing.assert_array_equal(a, b, err_msg=f"step {i}")
+
+
 def test_generate_equals_stepping_and_prefill(tiny):
     d = sa.Decoder(tiny, n_ctx=64)
     try:
@@ -176,8 +199,11 @@ def test_batched_prompt_equals_stepping(model, request):
     through the small-M GEMM and the causal attention read a prompt exactly
     as stepping it does -- the logits of the last id bit for bit, for a first
     part and for a continuation of that prefix (37 ids: ragged chunks), and
-    the same greedy continuation. Level 2 (Q4 on MFMA) agrees to float
-    rounding."""
+    the same greedy continuation. Level 2 reads in the reference's per-256
+    prompt regime (graded against the reference's own prefill in
+    test_gpu_prompt.py), so against per-32 stepping it agrees to that
+    regime's quantization: correlation above 0.999 and the same top-1
+    unless the stepped logits are tied."""
     p = request.getfixturevalue(model)
     V = 32000 if model == "qwenish" else 2000
     ids = np.random.default_rng(17).integers(0, V, 37).astype(np.int32)
@@ -197,7 +223,7 @@ def test_batched_prompt_equals_stepping(model, request):
     assert outs[1][2] == outs[0][2]
     for i in range(2):
         ref = outs[0][i]
-        assert np.corrcoef(outs[2][i], ref)[0, 1] > 0.9999, f"level 2, part {i}"
+        assert np.corrcoef(outs[2][i], ref)[0, 1] > 0.999, f"level 2, part {i}"
         if tie_margin(ref) > 0.01:
             assert int(np.argmax(outs[2][i])) == int(np.argmax(ref)), f"level 2, part {i}"
 
@@ -206,7 +232,8 @@ def test_batched_prompt_equals_stepping(model, request):
 def test_batched_prompt_fills_context(tiny, n):
     """Prompts that end exactly at n_ctx (the last position's K/V row is the
     cache's last), with whole and ragged chunks: level 1 equals stepping bit
-    for bit, level 2 within float rounding; a prompt past n_ctx is refused."""
+    for bit, level 2 within its per-256 regime's quantization; a prompt past
+    n_ctx is refused."""
     ids = np.random.default_rng(n).integers(0, 2000, n).astype(np.int32)
     outs = {}
     for level in (0, 1, 2):
@@ -218,7 +245,7 @@ def test_batched_prompt_fills_context(tiny, n):
         finally:
             d.close()
     np.testing.assert_array_equal(outs[1], outs[0])
-    assert np.corrcoef(outs[2], outs[0])[0, 1] > 0.9999
+    assert np.corrcoef(outs[2], outs[0])[0, 1] > 0.999
 
 
 def test_batched_prompt_into_other_slots(tiny):
@@ -243,7 +270,7 @@ def test_batched_prompt_into_other_slots(tiny):
     for b in range(3):
         np.testing.assert_array_equal(res[1][0][b], res[0][0][b], err_msg=f"slot {b} prompt logits")
         np.testing.assert_array_equal(res[1][1][0][b], res[0][1][0][b], err_msg=f"slot {b} step")
-        assert np.corrcoef(res[2][0][b], res[0][0][b])[0, 1] > 0.9999
+        assert np.corrcoef(res[2][0][b], res[0][0][b])[0, 1] > 0.999
 
 
 def test_fast_graded_like_the_reference_qwen_layers(qwenish):
