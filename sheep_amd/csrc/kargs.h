@@ -143,6 +143,9 @@ typedef struct {
     // merges that head's query heads as sml_attn_merge does and resets the
     // counter, so no merge launch follows. One launch at a time per array.
     int * cnt;
+    // sml_attnf (prompt flash form): KV positions per split (grid z), a
+    // multiple of 64
+    int fchunk;
 } sml_kattn;
 
 // Decode attention in the reference's float order (exact mode): RoPE of q and

@@ -1461,6 +1461,234 @@ __device__ __forceinline__ void attnw_body(const sml_kattn & a) {
     extern "C" __global__ __launch_bounds__(64 * ATTNW_WAVES) void sml_attnw_r##R(const sml_kattn a) { attnw_body<R>(a); }
 ATTNW_KERNEL(1) ATTNW_KERNEL(2) ATTNW_KERNEL(3) ATTNW_KERNEL(4) ATTNW_KERNEL(5) ATTNW_KERNEL(6) ATTNW_KERNEL(7) ATTNW_KERNEL(8)
 
+// ---------------------------------------------------------------- prompt attention on MFMA (flash form)
+//
+// For prompt reading at level 2: the entries of a launch are consecutive
+// positions of one sequence whose K and V rows sml_ropekv has already
+// rotated and written to the cache (fp16). A workgroup takes 16 entries
+// (query rows) and one kv head, one wave per query head of the group, and
+// walks the KV positions of its split in blocks of 64 with an online
+// softmax, on v_mfma_f32_16x16x32_f16 (lane l: A row / B column l%16, k =
+// 8(l/16)..+7; D rows 4(l/16)..+3 of column l%16):
+//  - S^T = K Q^T: A = the block's K rows (fp16 from the cache), B = the
+//    wave's rotated q (rotated as rope8 does) as two fp16 parts, q_hi =
+//    fp16(q) and q_lo = fp16(q - q_hi), so the scores carry q to ~2^-22
+//    (one fp16 q moved them enough to flip a routed expert); a lane then
+//    holds query l%16 at KV positions 4(l/16)..+3 of each 16-row tile;
+//  - the scores times 1/sqrt(hd) log2(e) in fp32, masked past each entry's
+//    position; the running max and sum per query in base 2;
+//  - O += P V: A = P straight from the S^T layout (the MFMA's k slots
+//    8(l/16)..+7 hold KV rows 4(l/16)..+3 of two 16-row tiles), as fp16
+//    high and low parts like q, B = V from an LDS copy transposed to
+//    [dim][position] at staging, the same slot order.
+// One split: the output is written directly; several (few query blocks or
+// kv heads, so the grid still fills the chip): sml_attn's partials, merged
+// by sml_attn_merge. fp32 accumulation in its own order: graded as level-2
+// prompt reading is.
+#define FA_KB 64                      // KV positions per block
+#define FA_KROW 272                   // LDS bytes per K row (256 + 16)
+#define FA_VROW 144                   // LDS bytes per transposed V row (one dim, 64 positions + 16)
+#define FA_STAGE (FA_KB * FA_KROW + HD * FA_VROW)
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int REP>
+__device__ void attnf_body(const sml_kattn & a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int NT = 64 * REP;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, i16 = lane & 15;
+    const int kh = blockIdx.y, h = kh * REP + wave;
+    const int b0 = blockIdx.x * 16, nb = min(16, a.nseq - b0);
+    const int kvd = a.n_kv * HD, half = HD / 2;
+    const uint16_t * kcache = a.kc_slots ? a.kc_slots[a.slot[b0]] + a.layer_off : a.kcache;
+    const uint16_t * vcache = a.vc_slots ? a.vc_slots[a.slot[b0]] + a.layer_off : a.vcache;
+    // this split's KV range, cut at the block's last position
+    const int chk = a.fchunk;
+    const int t_lo = blockIdx.z * chk, t_end = min(t_lo + chk, a.pos[b0 + nb - 1] + 1);
+    // the lane's query (entry b0 + i16, clamped) and its position
+    const int bq = b0 + min(i16, nb - 1), posq = a.pos[bq];
+    // rotated q of head h, dims 32c + 8g + e, as fp16 B operands (hi, lo)
+    v8h qb[4], ql[4];
+    {
+        float x[4][8];
+        const float * qp = a.q + (size_t) bq * a.qkv_stride + (size_t) h * HD;
+        #pragma unroll
+        for (int c = 0; c < 4; c++) load_f8(qp + 32 * c + 8 * g, x[c]);
+        #pragma unroll
+        for (int c = 0; c < 2; c++) {
+            float cs[8], sn[8];
+            load_f8(a.cos_t + (size_t) posq * half + 32 * c + 8 * g, cs);
+            load_f8(a.sin_t + (size_t) posq * half + 32 * c + 8 * g, sn);
+            #pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float lo = x[c][e], hi = x[c + 2][e];
+                x[c][e] = __builtin_fmaf(lo, cs[e], -(hi * sn[e]));        // rope8's fused forms
+                x[c + 2][e] = __builtin_fmaf(lo, sn[e], hi * cs[e]);
+            }
+        }
+        #pragma unroll
+        for (int c = 0; c < 4; c++)
+            #pragma unroll
+            for (int e = 0; e < 8; e++) {
+                qb[c][e] = (_Float16) x[c][e];
+                ql[c][e] = (_Float16) (x[c][e] - (float) qb[c][e]);
+            }
+    }
+    const float sl = a.inv * 1.44269504088896341f;
+    float m_run = -INFINITY, l_run = 0.0f;                    // for query i16 (the same in its 4 lanes)
+    v4f o[8];
+    #pragma unroll
+    for (int dt = 0; dt < 8; dt++) o[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // staging: K rows as they are ([pos][dim], 16-byte words), V transposed
+    // to [dim][pos]; words of positions past the range repeat its first row
+    v4u kw[(FA_KB * 16 + NT - 1) / NT], vw[(FA_KB * 16 + NT - 1) / NT];
+    constexpr int NW = (FA_KB * 16 + NT - 1) / NT;
+    auto fetch = [&](int t0) {
+        #pragma unroll
+        for (int i = 0; i < NW; i++) {
+            const int w = tid + i * NT;
+            if (w < FA_KB * 16) {
+                const int r = w >> 4, c = w & 15;
+                const int t = t0 + r < t_end ? t0 + r : t0;
+                const size_t off = (size_t) t * kvd + (size_t) kh * HD + c * 8;
+                kw[i] = *(const v4u *) (kcache + off);
+                vw[i] = *(const v4u *) (vcache + off);
+            }
+        }
+    };
+    auto stage = [&](int buf) {
+        uint8_t * kb = lds + (size_t) buf * FA_STAGE;
+        uint8_t * vb = kb + FA_KB * FA_KROW;
+        #pragma unroll
+        for (int i = 0; i < NW; i++) {
+            const int w = tid + i * NT;
+            if (w < FA_KB * 16) {
+                const int r = w >> 4, c = w & 15;
+                *(v4u *) (kb + r * FA_KROW + c * 16) = kw[i];
+                #pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    *(uint16_t *) (vb + (c * 8 + 2 * e) * FA_VROW + r * 2) = (uint16_t) (vw[i][e] & 0xFFFFu);
+                    *(uint16_t *) (vb + (c * 8 + 2 * e + 1) * FA_VROW + r * 2) = (uint16_t) (vw[i][e] >> 16);
+                }
+            }
+        }
+    };
+    auto compute = [&](int buf, int t0) {
+        const uint8_t * kb = lds + (size_t) buf * FA_STAGE;
+        const uint8_t * vb = kb + FA_KB * FA_KROW;
+        // S^T: 4 tiles of 16 positions x 16 queries
+        v4f s[4];
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+            s[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            #pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const v8h ka = *(const v8h *) (kb + (16 * j + i16) * FA_KROW + (32 * c + 8 * g) * 2);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[c], s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[c], s[j], 0, 0, 0);
+            }
+        }
+        // scale, mask and the block's max for the lane's query
+        float mx = -INFINITY;
+        #pragma unroll
+        for (int j = 0; j < 4; j++)
+            #pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = t0 + 16 * j + 4 * g + r;
+                const float v = t < t_end && t <= posq ? s[j][r] * sl : -INFINITY;
+                s[j][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float mu = m_new == -INFINITY ? 0.0f : m_new;   // no position yet: keep zeros
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mu);
+        float ls = 0.0f;
+        v8h pa[2], pl[2];
+        #pragma unroll
+        for (int j = 0; j < 4; j++)
+            #pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float p = __builtin_amdgcn_exp2f(s[j][r] - mu);
+                ls += p;
+                const _Float16 ph = (_Float16) p;
+                pa[j >> 1][4 * (j & 1) + r] = ph;
+                pl[j >> 1][4 * (j & 1) + r] = (_Float16) (p - (float) ph);
+            }
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        l_run = l_run * alpha + ls;
+        m_run = m_new;
+        // rescale O: the lane's rows are queries 4g..4g+3
+        float al[4];
+        #pragma unroll
+        for (int r = 0; r < 4; r++) al[r] = __shfl(alpha, 4 * g + r);
+        #pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+            #pragma unroll
+            for (int r = 0; r < 4; r++) o[dt][r] *= al[r];
+        // O += P V: per 32 positions u, k slots 8g..8g+3 are rows 4g..4g+3
+        // of tile 2u, 8g+4..8g+7 those of tile 2u+1
+        #pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            const uint8_t * vr = vb + (16 * dt + i16) * FA_VROW;
+            #pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const v2u lo = *(const v2u *) (vr + (32 * u + 4 * g) * 2);
+                const v2u hi = *(const v2u *) (vr + (32 * u + 16 + 4 * g) * 2);
+                const v4u w4 = {lo.x, lo.y, hi.x, hi.y};
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[u], __builtin_bit_cast(v8h, w4), o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[u], __builtin_bit_cast(v8h, w4), o[dt], 0, 0, 0);
+            }
+        }
+    };
+
+    int buf = 0;
+    if (t_lo < t_end) {
+        fetch(t_lo);
+        stage(0);
+        __syncthreads();
+        for (int t0 = t_lo; t0 < t_end; t0 += FA_KB) {
+            const bool more = t0 + FA_KB < t_end;
+            if (more) fetch(t0 + FA_KB);
+            compute(buf, t0);
+            if (more) stage(buf ^ 1);
+            __syncthreads();
+            buf ^= 1;
+        }
+    }
+
+    // the lane's rows: queries 4g..4g+3, dims 16dt + i16
+    const bool one = gridDim.z == 1;
+    float lq[4], mq[4];
+    #pragma unroll
+    for (int r = 0; r < 4; r++) { lq[r] = __shfl(l_run, 4 * g + r); mq[r] = __shfl(m_run, 4 * g + r); }
+    #pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int q = 4 * g + r;
+        if (q >= nb) continue;
+        const int b = b0 + q;
+        if (one) {
+            float * out = a.out + (size_t) b * a.n_head * HD + (size_t) h * HD;
+            #pragma unroll
+            for (int dt = 0; dt < 8; dt++) out[16 * dt + i16] = o[dt][r] / lq[r];
+        } else {
+            float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
+            float * po = blk + ((size_t) h * a.nsplit + blockIdx.z) * HD;
+            float2 * pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) h * a.nsplit + blockIdx.z;
+            #pragma unroll
+            for (int dt = 0; dt < 8; dt++) po[16 * dt + i16] = o[dt][r];
+            if (i16 == 0) *pml = make_float2(mq[r], lq[r]);
+        }
+    }
+}
+
+#define ATTNF_KERNEL(R) \
+    extern "C" __global__ __launch_bounds__(64 * R) void sml_attnf_r##R(const sml_kattn a) { attnf_body<R>(a); }
+ATTNF_KERNEL(1) ATTNF_KERNEL(2) ATTNF_KERNEL(3) ATTNF_KERNEL(4) ATTNF_KERNEL(5) ATTNF_KERNEL(6) ATTNF_KERNEL(7) ATTNF_KERNEL(8)
+
 // The merge as its own launch (grid: n_head workgroups of HD threads, z:
 // the sequence).
 extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn a) {

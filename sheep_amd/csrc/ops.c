@@ -584,6 +584,9 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     if (!cnt) hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
 }
 
+// LDS of the prompt flash attention (sml_attnf): two stages of a 64-position
+// K tile (272 bytes a row) and its V transposed (128 dims x 144 bytes)
+#define ATTNF_LDS (2 * (64 * 272 + 128 * 144))
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
@@ -621,6 +624,23 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     a.nseq = nseq;
     a.tpw = causal ? env_int("SML_ATTN_TPW", 16) : 1;
     if (a.tpw < 1 || a.tpw > 16) a.tpw = 1;
+    if (causal == 2 && env_int("SML_ATTN_FLASH", 1)) {
+        // MFMA flash form: 16 entries x one kv head per workgroup (a wave per
+        // query head), the KV range cut into splits only as far as the grid
+        // needs workgroups (then merged); splits of a multiple of 64
+        // positions, at most the partial buffer's ceil(n_ctx / 128)
+        if (q_out) hx_failf("flash prompt attention does not quantize its output");
+        const int rep = n_head / n_kv, nqb = (nseq + 15) / 16;
+        const int maxs = (n_ctx + 127) / 128;
+        int ns = 1;
+        while (ns * 2 <= maxs && ns < 64 && (long) nqb * n_kv * ns < 2L * hx.ncu) ns *= 2;
+        a.nsplit = ns;
+        a.fchunk = ((n_ctx + ns - 1) / ns + 63) / 64 * 64;
+        snprintf(name, sizeof name, "sml_attnf_r%d", rep);
+        hx_launch3(name, (unsigned) nqb, (unsigned) n_kv, (unsigned) ns, (unsigned) (64 * rep), ATTNF_LDS, st, &a);
+        if (ns > 1) hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
+        return;
+    }
     if (causal == 2) {
         // a wave per position over an LDS tile (16 positions per workgroup)
         const int rep = n_head / n_kv;
