@@ -56,6 +56,8 @@ def oracle():
             "orc_moe_route": (c_int, [c_void_p, c_int, c_int, c_uint, c_void_p, c_void_p]),
             "orc_router": (None, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
             "orc_argmax": (c_int, [c_void_p, c_int]),
+            "orc_expf_published": (c_float, [c_float]),
+            "orc_expf_mismatches": (ctypes.c_long, [ctypes.c_uint]),
             "orc_gptq_unpack_row": (None, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
             "orc_gptq_dequant_row": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
             "orc_gptq_matvec": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),

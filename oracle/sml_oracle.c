@@ -786,3 +786,53 @@ const float * orc_forward(orc_model * m, int token, int pos) {
     mv(m, m->head, m->xb, m->logits);
     return m->logits;
 }
+
+// ---------------------------------------------------------------- expf restated
+// follows the published algorithm of glibc's expf (sysdeps/ieee754/flt-32/e_expf.c
+// in glibc >= 2.27, from ARM's optimized-routines), which the reference's
+// softmax and routing call (sml/sml-run.c:180-287,2925-3037)
+static const uint64_t ORC_EXPF_TAB[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull };
+
+float orc_expf_published(float x) {
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 C2 = 0x1.62e42ff0c52d6p-1 / 32, InvLn2N = 0x1.71547652b82fep+0 * 32, Shift = 0x1.8p+52;
+    const double xd = (double) x;
+    double kd = fma(InvLn2N, xd, Shift);
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= Shift;
+    const double r = fma(InvLn2N, xd, -kd);
+    const uint64_t sb = ORC_EXPF_TAB[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &sb, 8);
+    const double z = fma(C0, r, C1), r2 = r * r;
+    double y = fma(C2, r, 1.0);
+    y = fma(z, r2, y);
+    return (float) (y * s);
+}
+
+long orc_expf_mismatches(unsigned stride) {
+    long bad = 0;
+    if (stride == 0) stride = 1;
+    #pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (long long u = 0x80000000ll; u <= 0xff800000ll; u += stride) {
+        const uint32_t b = (uint32_t) u;
+        float x;
+        memcpy(&x, &b, 4);
+        const float g = orc_expf_published(x), w = expf(x);
+        uint32_t gb, wb;
+        memcpy(&gb, &g, 4);
+        memcpy(&wb, &w, 4);
+        bad += gb != wb;
+    }
+    return bad;
+}

@@ -106,6 +106,17 @@ void orc_awq_unpack_row(const int32_t * qweight, const int32_t * qzeros, int row
 void orc_awq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows,
                          int cols, int group, int row, float * out);
 
+// ---------------------------------------------------------------- expf restated
+// The C library's expf (glibc 2.35, x86-64 with FMA) from its published
+// algorithm, as the GPU's exact attention and routing restate it: x*32/ln2 =
+// k + r in double (k rounded through the 1.5*2^52 shift, both products
+// fused), 2^(k/32) from a 32-entry table of 2^(i/32), 2^(r/32) by a cubic,
+// one rounding to float. Used for x <= 0.
+float orc_expf_published(float x);
+// Count of floats x <= 0 (every stride-th bit pattern from -0.0 down to
+// -inf) where orc_expf_published(x) and the library's expf(x) differ in bits.
+long orc_expf_mismatches(unsigned stride);
+
 // ---------------------------------------------------------------- decoder
 // A whole decode step over an SSF file (Llama / Qwen2 / Mixtral family: RMSNorm,
 // halved RoPE, GQA, SwiGLU, optional q/k/v bias, tied or untied head, top-k MoE).

@@ -1472,15 +1472,17 @@ ATTNW_KERNEL(1) ATTNW_KERNEL(2) ATTNW_KERNEL(3) ATTNW_KERNEL(4) ATTNW_KERNEL(5) 
 // 8(l/16)..+7; D rows 4(l/16)..+3 of column l%16):
 //  - S^T = K Q^T: A = the block's K rows (fp16 from the cache), B = the
 //    wave's rotated q (rotated as rope8 does) as two fp16 parts, q_hi =
-//    fp16(q) and q_lo = fp16(q - q_hi), so the scores carry q to ~2^-22
-//    (one fp16 q moved them enough to flip a routed expert); a lane then
-//    holds query l%16 at KV positions 4(l/16)..+3 of each 16-row tile;
+//    fp16(q) and q_lo = fp16(q - q_hi), so the scores carry q to ~2^-22; a
+//    lane then holds query l%16 at KV positions 4(l/16)..+3 of each 16-row
+//    tile;
 //  - the scores times 1/sqrt(hd) log2(e) in fp32, masked past each entry's
 //    position; the running max and sum per query in base 2;
 //  - O += P V: A = P straight from the S^T layout (the MFMA's k slots
 //    8(l/16)..+7 hold KV rows 4(l/16)..+3 of two 16-row tiles), as fp16
-//    high and low parts like q, B = V from an LDS copy transposed to
-//    [dim][position] at staging, the same slot order.
+//    high and low parts like q (P rounded once to fp16, against a sum of
+//    the unrounded P, moved a MoE prompt enough to flip a routed expert),
+//    B = V from an LDS copy transposed to [dim][position] at staging, the
+//    same slot order.
 // One split: the output is written directly; several (few query blocks or
 // kv heads, so the grid still fills the chip): sml_attn's partials, merged
 // by sml_attn_merge. fp32 accumulation in its own order: graded as level-2

@@ -306,6 +306,19 @@ def test_zero_mean_decoder_is_informative(tmpdir_s):
             assert frac < 0.03 and distinct <= 2, (frac, distinct)
 
 
+def test_expf_restatement_equals_the_library():
+    """The restated expf (the GPU's exact softmax and routing weights use the
+    same algorithm and table) equals the C library's expf bit for bit on
+    every 7th float from -0.0 down to -inf (306 M inputs: normals, denormals,
+    the underflow edge at -103.97, -inf), and on the closed forms."""
+    o = ob.oracle()
+    assert o.orc_expf_mismatches(7) == 0
+    assert o.orc_expf_published(0.0) == 1.0
+    assert o.orc_expf_published(-200.0) == 0.0
+    for x in (-1.0, -0.5, -10.0, -50.3):        # correctly rounded from double here
+        assert o.orc_expf_published(x) == float(np.float32(np.exp(np.float64(np.float32(x))))), x
+
+
 def test_silu_polynomial_closed_form():
     """The SwiGLU activation with the reference build's 2^x polynomial
     (sml/sml-run.c:393-426): within 2.5e-4 relative of g/(1+e^-g)*u in float64
