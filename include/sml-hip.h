@@ -48,6 +48,20 @@ sml_hip_mat * sml_hip_mat_upload(const uint8_t * const planes[4], const uint16_t
                                  int rows, int cols, int nbits, int scale6, int minneg);
 // The same, for record `name` of an SSF file.
 sml_hip_mat * sml_hip_mat_from_file(const char * path, const char * name);
+// A matrix given as GGUF Q4_K blocks (ggml's block_q4_K: per 256 weights of a
+// row fp16 d, fp16 dmin, 12 bytes of 6-bit sub-block scales and mins, 128
+// bytes of 4-bit codes; rows x cols/256 blocks of 144 bytes, row-major),
+// repacked on the host into the FLAT Q4 layout: sd = d, md = dmin, sq = the
+// sub-block scale, mq = 127 - the sub-block min, code bytes as they are. The
+// arithmetic is ggml's weight d*sc*q - dmin*m exactly, so every GEMV and GEMM
+// above runs it. No counterpart in the reference, which reads GGUF only
+// through transformers into fp16 and re-quantizes (tooling/sml_gguf.py:1-35).
+sml_hip_mat * sml_hip_mat_from_q4k(const void * blocks, int rows, int cols);
+// The host repack alone (no GPU): FLAT Q4 plane [rows][cols/2], sd and md
+// [rows][cols/256], sq and mq [rows][cols/32]. Returns 0, or -1 on a shape
+// that is not whole blocks.
+int           sml_hip_q4k_repack(const void * blocks, int rows, int cols, uint8_t * plane, uint16_t * sd,
+                                 uint8_t * sq, uint16_t * md, uint8_t * mq);
 void          sml_hip_mat_free(sml_hip_mat * m);
 int           sml_hip_mat_info(const sml_hip_mat * m, int * rows, int * cols, int * nbits);
 // Bytes the matrix occupies in HBM (codes + fields): what one GEMV streams.

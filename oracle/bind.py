@@ -57,6 +57,7 @@ def oracle():
             "orc_router": (None, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
             "orc_argmax": (c_int, [c_void_p, c_int]),
             "orc_expf_published": (c_float, [c_float]),
+            "orc_q4k_dequant_row": (None, [c_void_p, c_int, c_void_p]),
             "orc_expf_mismatches": (ctypes.c_long, [ctypes.c_uint]),
             "orc_gptq_unpack_row": (None, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
             "orc_gptq_dequant_row": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
@@ -412,3 +413,77 @@ def awq_dequant_row(qweight, qzeros, scales, rows, cols, row, group=128):
     out = np.zeros(cols, np.float32)
     oracle().orc_awq_dequant_row(ptr(qweight), ptr(qzeros), ptr(scales), rows, cols, group, row, ptr(out))
     return out
+
+
+def q4k_dequant(blocks, rows, cols):
+    """GGUF Q4_K blocks [rows][cols/256][144] to float32 weights [rows][cols]
+    by the published formula (orc_q4k_dequant_row)."""
+    bl = np.ascontiguousarray(blocks, np.uint8).reshape(rows, -1)
+    out = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        oracle().orc_q4k_dequant_row(bl[r].ctypes.data, cols, out[r].ctypes.data)
+    return out
+
+
+def q4k_pack_scales(sc, m):
+    """The 12 scale bytes of a Q4_K block from eight 6-bit scales and mins, as
+    ggml's quantizer packs them: sub-blocks 0-3 in the low six bits of bytes
+    j (scale) and j+4 (min); 4-7 in the nibbles of byte j+4, their high two
+    bits in the top bits of bytes j-4 (scale) and j (min)."""
+    out = [0] * 12
+    for j in range(8):
+        s, n = int(sc[j]), int(m[j])
+        if j < 4:
+            out[j] |= s
+            out[j + 4] |= n
+        else:
+            out[j + 4] = (s & 15) | ((n & 15) << 4)
+            out[j - 4] |= (s >> 4) << 6
+            out[j] |= (n >> 4) << 6
+    return np.array(out, np.uint8)
+
+
+def q4k_random_blocks(rows, cols, seed):
+    """Random Q4_K blocks: d, dmin small positive fp16, 6-bit scales and mins,
+    uniform codes."""
+    rng = np.random.default_rng(seed)
+    nb = rows * (cols // 256)
+    blk = np.zeros((nb, 144), np.uint8)
+    d = (np.abs(rng.standard_normal(nb)) * 0.002 + 1e-4).astype(np.float16)
+    dm = (np.abs(rng.standard_normal(nb)) * 0.002 + 1e-4).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blk[:, 2:4] = dm.view(np.uint8).reshape(nb, 2)
+    for i in range(nb):
+        blk[i, 4:16] = q4k_pack_scales(rng.integers(0, 64, 8), rng.integers(0, 64, 8))
+    blk[:, 16:] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
+    return blk.reshape(rows, cols // 256, 144)
+
+
+class FlatView:
+    """An OrcTensor over raw FLAT Q4 arrays (plane, sd, md, sq, mq as numpy
+    arrays, kept alive here), e.g. a repacked Q4_K matrix."""
+
+    def __init__(self, plane, sd, md, sq, mq, rows, cols):
+        self.arrays = [np.ascontiguousarray(a) for a in (plane, sd, md, sq, mq)]
+        self.rows, self.cols = rows, cols
+        self.ot = OrcTensor()
+        self.ot.plane[0] = self.arrays[0].ctypes.data
+        self.ot.sd, self.ot.md = self.arrays[1].ctypes.data, self.arrays[2].ctypes.data
+        self.ot.sq, self.ot.mq = self.arrays[3].ctypes.data, self.arrays[4].ctypes.data
+        self.ot.rows, self.ot.cols, self.ot.nbits, self.ot.scale6, self.ot.minneg = rows, cols, 4, 0, 0
+
+    def dequant(self, row):
+        out = np.zeros(self.cols, np.float32)
+        oracle().orc_dequant_row(ctypes.byref(self.ot), row, out.ctypes.data)
+        return out
+
+    def codes(self, row):
+        out = np.zeros(self.cols, np.uint8)
+        oracle().orc_unpack_row(ctypes.byref(self.ot), row, out.ctypes.data)
+        return out
+
+    def matvec(self, q, s, u):
+        y = np.zeros(self.rows, np.float32)
+        oracle().orc_matvec(ctypes.byref(self.ot), q.ctypes.data, s.ctypes.data, u.ctypes.data, y.ctypes.data,
+                            0, self.rows)
+        return y

@@ -836,3 +836,42 @@ long orc_expf_mismatches(unsigned stride) {
     }
     return bad;
 }
+
+// ---------------------------------------------------------------- GGUF Q4_K
+// follows ggml's published block_q4_K format and dequantize_row_q4_K (the
+// K-quant layout of llama.cpp's ggml-quants.c); the reference itself reads GGUF
+// only through transformers (tooling/sml_gguf.py:1-35)
+static void q4k_unpack_scale(const uint8_t * q, int j, float * sc, float * m) {
+    unsigned a, b;
+    if (j < 4) {
+        a = q[j] & 63u;
+        b = q[j + 4] & 63u;
+    } else {
+        a = (q[j + 4] & 15u) | ((unsigned) (q[j - 4] >> 6) << 4);
+        b = (q[j + 4] >> 4) | ((unsigned) (q[j] >> 6) << 4);
+    }
+    *sc = (float) a;
+    *m = (float) b;
+}
+
+void orc_q4k_dequant_row(const uint8_t * blocks, int cols, float * out) {
+    for (int b = 0; b < cols / 256; b++) {
+        const uint8_t * blk = blocks + (size_t) b * 144;
+        uint16_t dh, mh;
+        memcpy(&dh, blk, 2);
+        memcpy(&mh, blk + 2, 2);
+        const float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
+        const uint8_t * q = blk + 16;
+        float * y = out + (size_t) b * 256;
+        for (int c = 0; c < 4; c++) {
+            float s1, m1, s2, m2;
+            q4k_unpack_scale(blk + 4, 2 * c, &s1, &m1);
+            q4k_unpack_scale(blk + 4, 2 * c + 1, &s2, &m2);
+            const float d1 = d * s1, n1 = dmin * m1, d2 = d * s2, n2 = dmin * m2;
+            for (int l = 0; l < 32; l++) y[l] = d1 * (float) (q[l] & 15) - n1;
+            for (int l = 0; l < 32; l++) y[32 + l] = d2 * (float) (q[l] >> 4) - n2;
+            q += 32;
+            y += 64;
+        }
+    }
+}

@@ -106,6 +106,14 @@ void orc_awq_unpack_row(const int32_t * qweight, const int32_t * qzeros, int row
 void orc_awq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows,
                          int cols, int group, int row, float * out);
 
+// ---------------------------------------------------------------- GGUF Q4_K
+// One row of ggml's block_q4_K blocks (cols/256 blocks of 144 bytes: fp16 d,
+// fp16 dmin, 12 bytes of packed 6-bit sub-block scales and mins, 128 bytes of
+// codes) dequantized by the published formula (ggml's dequantize_row_q4_K):
+// per 64 weights, sub-blocks 2c and 2c+1 take the low and high nibbles of the
+// same 32 code bytes, y = (d*sc)*q - dmin*m.
+void orc_q4k_dequant_row(const uint8_t * blocks, int cols, float * out);
+
 // ---------------------------------------------------------------- expf restated
 // The C library's expf (glibc 2.35, x86-64 with FMA) from its published
 // algorithm, as the GPU's exact attention and routing restate it: x*32/ln2 =

@@ -61,6 +61,8 @@ _SIGS = [
     ("sml_hip_call_count", c_long, []),
     ("sml_hip_mat_upload", c_void_p, [P(c_void_p), c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int]),
     ("sml_hip_mat_from_file", c_void_p, [c_char_p, c_char_p]),
+    ("sml_hip_mat_from_q4k", c_void_p, [c_void_p, c_int, c_int]),
+    ("sml_hip_q4k_repack", c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("sml_hip_mat_free", None, [c_void_p]),
     ("sml_hip_mat_info", c_int, [c_void_p, P(c_int), P(c_int), P(c_int)]),
     ("sml_hip_mat_bytes", c_size_t, [c_void_p]),
@@ -191,6 +193,15 @@ class Mat:
     @classmethod
     def from_file(cls, path, name):
         return cls(lib().sml_hip_mat_from_file(str(path).encode(), name.encode()))
+
+    @classmethod
+    def from_q4k(cls, blocks, rows, cols):
+        """GGUF Q4_K blocks (uint8, rows x cols/256 x 144 bytes) repacked into
+        the FLAT Q4 layout and uploaded."""
+        b = np.ascontiguousarray(blocks, np.uint8)
+        if b.size != rows * (cols // 256) * 144:
+            raise ValueError("Q4_K blocks do not match the shape")
+        return cls(lib().sml_hip_mat_from_q4k(b.ctypes.data, rows, cols))
 
     def free(self):
         if self.h:
@@ -410,3 +421,19 @@ def gemm(m, act_q, act_s, act_u, nrow, y, per256=False):
 def gemm_swiglu(gate, up, act_q, act_s, act_u, nrow, h, per256=False):
     f = lib().sml_hip_gemm_swiglu_sb if per256 else lib().sml_hip_gemm_swiglu
     _chk(f(gate.h, up.h, act_q.ptr, act_s.ptr, act_u.ptr, nrow, h.ptr), "gemm_swiglu")
+
+
+def q4k_repack(blocks, rows, cols):
+    """The host repack of GGUF Q4_K blocks into FLAT Q4 arrays (no GPU):
+    (plane [rows][cols/2], sd, md [rows][cols/256] fp16 bits, sq, mq [rows][cols/32])."""
+    b = np.ascontiguousarray(blocks, np.uint8)
+    nb = cols // 256
+    plane = np.zeros((rows, cols // 2), np.uint8)
+    sd = np.zeros((rows, nb), np.uint16)
+    md = np.zeros((rows, nb), np.uint16)
+    sq = np.zeros((rows, cols // 32), np.uint8)
+    mq = np.zeros((rows, cols // 32), np.uint8)
+    if lib().sml_hip_q4k_repack(b.ctypes.data, rows, cols, plane.ctypes.data, sd.ctypes.data, sq.ctypes.data,
+                                md.ctypes.data, mq.ctypes.data) != 0:
+        raise ValueError("Q4_K blocks do not match the shape")
+    return plane, sd, md, sq, mq

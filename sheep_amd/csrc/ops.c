@@ -131,6 +131,79 @@ sml_hip_mat * sml_hip_mat_upload(const uint8_t * const planes[4], const uint16_t
     return m;
 }
 
+// ------------------------------------------------------------ GGUF Q4_K blocks
+//
+// ggml's block_q4_K (the Q4_K_M files' main type): per 256 weights of a row,
+// fp16 d and dmin, 12 bytes packing eight 6-bit scales sc_j and mins m_j (one
+// per 32 weights), and 128 bytes of 4-bit codes q; a weight is
+// d*sc_j*q - dmin*m_j. That is the two-level FLAT Q4 record exactly: per
+// superblock sd = d and md = dmin, per group sq = sc_j and mq = 127 - m_j
+// (min = md*(mq-127)), and the 128 code bytes are already the FLAT Q4 quads
+// (bytes 32c..32c+31 of a block hold sub-blocks 2c (low nibbles) and 2c+1
+// (high), as a quad's halves hold groups 4q+2h and 4q+2h+1). So the repack
+// moves bytes and fields; nothing is re-quantized or recomputed.
+#define Q4K_BLOCK 144
+
+// scale and min of sub-block j from the 12 packed bytes: j < 4 in the low six
+// bits of bytes j and j+4; j >= 4 in the nibbles of byte j+4 with the high
+// two bits in the top bits of bytes j-4 and j
+static void q4k_scale_min(const uint8_t * s, int j, uint8_t * sc, uint8_t * mn) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *mn = s[j + 4] & 63;
+    } else {
+        *sc = (uint8_t) ((s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4));
+        *mn = (uint8_t) ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+int sml_hip_q4k_repack(const void * blocks, int rows, int cols, uint8_t * plane, uint16_t * sd, uint8_t * sq,
+                       uint16_t * md, uint8_t * mq) {
+    if (!blocks || rows <= 0 || cols <= 0 || cols % 256 || !plane || !sd || !sq || !md || !mq) return -1;
+    const size_t nb = (size_t) cols / 256;
+    for (size_t r = 0; r < (size_t) rows; r++)
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t * blk = (const uint8_t *) blocks + (r * nb + b) * Q4K_BLOCK;
+            memcpy(&sd[r * nb + b], blk, 2);
+            memcpy(&md[r * nb + b], blk + 2, 2);
+            for (int j = 0; j < 8; j++) {
+                uint8_t sc, mn;
+                q4k_scale_min(blk + 4, j, &sc, &mn);
+                sq[(r * nb + b) * 8 + j] = sc;
+                mq[(r * nb + b) * 8 + j] = (uint8_t) (127 - mn);
+            }
+            memcpy(plane + (r * nb + b) * 128, blk + 16, 128);
+        }
+    return 0;
+}
+
+sml_hip_mat * sml_hip_mat_from_q4k(const void * blocks, int rows, int cols) {
+    OP_BEGIN(NULL);
+    if (!blocks || rows <= 0 || cols <= 0 || cols % 256) hx_failf("Q4_K matrix %dx%d: not a whole number of blocks", rows, cols);
+    const size_t R = (size_t) rows, nb = (size_t) cols / 256;
+    uint8_t * plane = malloc(R * nb * 128), * sq = malloc(R * nb * 8), * mq = malloc(R * nb * 8);
+    uint16_t * sd = malloc(R * nb * 2), * md = malloc(R * nb * 2);
+    if (!plane || !sq || !mq || !sd || !md) {
+        free(plane); free(sq); free(mq); free(sd); free(md);
+        hx_failf("out of host memory");
+    }
+    sml_hip_q4k_repack(blocks, rows, cols, plane, sd, sq, md, mq);
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) {
+        hx.jb = outer;
+        free(plane); free(sq); free(mq); free(sd); free(md);
+        longjmp(*outer, 1);
+    }
+    hx.jb = &jb;
+    const uint8_t * planes[4] = { plane, NULL, NULL, NULL };
+    sml_hip_mat * m = mat_upload(planes, sd, sq, md, mq, rows, cols, 4, 0, 0);
+    hx.jb = outer;
+    free(plane); free(sq); free(mq); free(sd); free(md);
+    HX_LEAVE();
+    return m;
+}
+
 // A FLAT record's declared arrays must hold what its shape reads: every plane
 // of its width, the step fields (sd, sq) and, when it has a min, md and mq.
 // ssf_open has already checked each (offset, bytes) against the file.

@@ -1,0 +1,115 @@
+"""GGUF Q4_K blocks (ggml's block_q4_K) repacked into the FLAT Q4 layout.
+
+The reference reads GGUF only through transformers into fp16, then
+re-quantizes (tooling/sml_gguf.py:1-35), and `gguf` is not importable here;
+the blocks are pinned instead by ggml's published format: hand-built blocks
+with known answers, the quantizer's scale packing as a round trip, and the
+oracle's restatement of dequantize_row_q4_K (orc_q4k_dequant_row). A Q4_K
+weight d*sc*q - dmin*m is the FLAT record's step*q + min with sd = d, sq = sc,
+md = dmin, mq = 127 - m, and the 128 code bytes are already FLAT quads, so the
+repack (sml_hip_q4k_repack) moves bytes and fields only: after it the SSF
+dequantization equals the published formula bit for bit, and the GPU's codes
+are the block's nibbles.
+"""
+import numpy as np
+import pytest
+
+import sheep_amd as sa
+from oracle import bind as ob
+
+
+def known_block():
+    """d = 1, dmin = 0.5, sub-block j: scale j+1, min j; weight i has code i % 16."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([1.0], np.float16).view(np.uint8)
+    blk[2:4] = np.array([0.5], np.float16).view(np.uint8)
+    blk[4:16] = ob.q4k_pack_scales([1, 2, 3, 4, 5, 6, 7, 8], [0, 1, 2, 3, 4, 5, 6, 7])
+    l = np.arange(32) % 16
+    for c in range(4):
+        blk[16 + 32 * c:16 + 32 * (c + 1)] = l | (l << 4)
+    return blk
+
+
+def test_q4k_known_answers():
+    """Values worked out by hand from the format's definition."""
+    w = ob.q4k_dequant(known_block(), 1, 256)[0]
+    # (index, sub-block j = i // 32, code i % 16): (j+1)*code - 0.5*j
+    for i, want in ((0, 0.0), (17, 1.0), (31, 15.0), (40, 15.5), (63, 29.5), (64, -1.0),
+                    (127, 58.5), (200, 53.0), (255, 116.5)):
+        assert w[i] == want, (i, w[i], want)
+
+
+def test_q4k_scale_packing_round_trip():
+    """Every (scale, min) pair of every sub-block position survives ggml's
+    packing and the repack's unpacking."""
+    rng = np.random.default_rng(0)
+    for trial in range(64):
+        sc, mn = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+        if trial == 0:
+            sc, mn = np.full(8, 63), np.full(8, 63)
+        blk = known_block()
+        blk[4:16] = ob.q4k_pack_scales(sc, mn)
+        plane, sd, md, sq, mq = sa.q4k_repack(blk, 1, 256)
+        assert (sq[0] == sc).all() and (mq[0] == 127 - mn).all(), (sc, mn, sq, mq)
+        assert sd[0, 0] == blk[0:2].view(np.uint16)[0] and md[0, 0] == blk[2:4].view(np.uint16)[0]
+        assert (plane[0] == blk[16:]).all()
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(3, 256, 1), (17, 2048, 2), (64, 4096, 3)])
+def test_q4k_repack_equals_published_formula(rows, cols, seed):
+    """Random blocks: the repacked FLAT record's dequantization (the SSF
+    formula) equals dequantize_row_q4_K bit for bit, row by row."""
+    blocks = ob.q4k_random_blocks(rows, cols, seed)
+    v = ob.FlatView(*sa.q4k_repack(blocks, rows, cols), rows, cols)
+    want = ob.q4k_dequant(blocks, rows, cols)
+    for r in range(rows):
+        np.testing.assert_array_equal(v.dequant(r), want[r], err_msg=f"row {r}")
+
+
+def test_q4k_repack_refuses_partial_blocks():
+    with pytest.raises(ValueError):
+        sa.q4k_repack(np.zeros(144, np.uint8), 1, 128)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols,seed", [(4096, 4096, 11), (1000, 14336, 12)])
+def test_q4k_on_the_gpu(rows, cols, seed):
+    """Uploaded as Q4_K: the unpacked codes are the blocks' nibbles (bit for
+    bit); the GEMV and the SwiGLU GEMV on an int8 activation agree with the
+    oracle's GEMV on the repacked record and with a double-precision product
+    of the published dequantization (1e-3 of the largest output, rel-RMS
+    1e-4)."""
+    sa.init(0)
+    blocks = ob.q4k_random_blocks(rows, cols, seed)
+    m = sa.Mat.from_q4k(blocks, rows, cols)
+    v = ob.FlatView(*sa.q4k_repack(blocks, rows, cols), rows, cols)
+    for r0 in (0, rows // 2, rows - 3):
+        got = sa.unpack(m, r0, 3)
+        for i in range(3):
+            np.testing.assert_array_equal(got[i], v.codes(r0 + i), err_msg=f"codes row {r0 + i}")
+    x = np.random.default_rng(seed).standard_normal(cols).astype(np.float32)
+    q, s, u = ob.quantize_act(x)
+    act = sa.Act(cols)
+    xd = sa.DevBuf.of(x)
+    sa.normq(xd, act)
+    np.testing.assert_array_equal(act.read()[0], q)
+    y = sa.DevBuf(rows * 4)
+    sa.matvec(m, act, y)
+    got = y.read(np.float32)
+    want = v.matvec(q, s, u)
+    xq = (q.astype(np.float64).reshape(-1, 32) * s.astype(np.float64)[:, None]).reshape(-1)
+    brute = ob.q4k_dequant(blocks, rows, cols).astype(np.float64) @ xq
+    for ref, what in ((want, "oracle GEMV"), (brute, "published dequant x activation")):
+        err = np.abs(got - ref)
+        assert err.max() <= 1e-3 * np.abs(ref).max(), what
+        assert np.sqrt((err ** 2).mean() / (ref ** 2).mean()) <= 1e-4, what
+    up = sa.Mat.from_q4k(ob.q4k_random_blocks(rows, cols, seed + 100), rows, cols)
+    h = sa.DevBuf(rows * 4)
+    sa.matvec_swiglu(m, up, act, h)
+    vu = ob.FlatView(*sa.q4k_repack(ob.q4k_random_blocks(rows, cols, seed + 100), rows, cols), rows, cols)
+    g, uu = want.copy(), vu.matvec(q, s, u)
+    ob.oracle().orc_silu_mul(g.ctypes.data, uu.ctypes.data, rows)
+    hg = h.read(np.float32)
+    assert np.abs(hg - g).max() <= 1e-3 * np.abs(g).max()
+    m.free()
+    up.free()
