@@ -183,13 +183,22 @@ int sml_hip_moe_time(sml_hip_moe * m, const float * x, int T, float * out, int i
 // arrays, rows = outputs, cols = inputs: qweight int32 [cols/8][rows] (8 codes
 // along the input, lowest nibble first), qzeros int32 [cols/128][rows/8] (8
 // zero codes along the output), scales fp16 [cols/128][rows]; group 128,
-// identity g_idx; zero_add 1 for the v1 files (stored zero = zero - 1), 0 for
+// identity g_idx (desc_act: sml_hip_gptq_upload_gidx); zero_add 1 for the v1 files (stored zero = zero - 1), 0 for
 // v2. Weight = (code - zero) * scale, the layout tooling/sml_unpack.py:66-95
 // (dequant_gptq) converts offline; the reference engine has no GPU kernel for
 // it. rows % 8 == 0, cols % 128 == 0.
 typedef struct sml_hip_gptq sml_hip_gptq;
 sml_hip_gptq * sml_hip_gptq_upload(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
                                    int rows, int cols, int group, int zero_add);
+// The same with GPTQ's desc_act: g_idx int32 [cols], input k's group, every
+// group holding exactly `group` inputs (the activation-order layout GPTQ
+// writes); NULL or an identity g_idx is the upload above. The input columns
+// are reordered stably by g_idx so each group's codes are contiguous, and the
+// GEMV gathers x through that order; sml_hip_gptq_unpack then returns codes
+// in it (device column i is input column i of the stable sort by g_idx).
+// Follows dequant_gptq's g_idx branch (tooling/sml_unpack.py:90-96).
+sml_hip_gptq * sml_hip_gptq_upload_gidx(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                                        const int32_t * g_idx, int rows, int cols, int group, int zero_add);
 void           sml_hip_gptq_free(sml_hip_gptq * m);
 // An AWQ 4-bit matrix (AutoAWQ GEMM layout, what tooling/sml_unpack.py:78,
 // 100-118 dequant_awq reads): qweight int32 [cols][rows/8] with 8 outputs per

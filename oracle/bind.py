@@ -58,6 +58,8 @@ def oracle():
             "orc_argmax": (c_int, [c_void_p, c_int]),
             "orc_expf_published": (c_float, [c_float]),
             "orc_q4k_dequant_row": (None, [c_void_p, c_int, c_void_p]),
+            "orc_gptq_dequant_row_gidx": (None, [c_void_p] * 4 + [c_int] * 5 + [c_void_p]),
+            "orc_gptq_matvec_gidx": (None, [c_void_p] * 4 + [c_int] * 4 + [c_void_p, c_void_p]),
             "orc_expf_mismatches": (ctypes.c_long, [ctypes.c_uint]),
             "orc_gptq_unpack_row": (None, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
             "orc_gptq_dequant_row": (None, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
@@ -397,6 +399,21 @@ def gptq_matvec(qweight, qzeros, scales, rows, cols, x, group=128, zero_add=1):
     y = np.zeros(rows, np.float32)
     x = np.ascontiguousarray(x, np.float32)
     oracle().orc_gptq_matvec(ptr(qweight), ptr(qzeros), ptr(scales), rows, cols, group, zero_add, ptr(x), ptr(y))
+    return y
+
+
+def gptq_dequant_row_gidx(qweight, qzeros, scales, g_idx, rows, cols, row, group=128, zero_add=1):
+    out = np.zeros(cols, np.float32)
+    oracle().orc_gptq_dequant_row_gidx(ptr(qweight), ptr(qzeros), ptr(scales), ptr(g_idx), rows, cols, group,
+                                       zero_add, row, ptr(out))
+    return out
+
+
+def gptq_matvec_gidx(qweight, qzeros, scales, g_idx, rows, cols, x, group=128, zero_add=1):
+    y = np.zeros(rows, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    oracle().orc_gptq_matvec_gidx(ptr(qweight), ptr(qzeros), ptr(scales), ptr(g_idx), rows, cols, group, zero_add,
+                                  ptr(x), ptr(y))
     return y
 
 

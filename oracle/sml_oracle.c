@@ -460,6 +460,38 @@ void orc_gptq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const
     free(z);
 }
 
+// the g_idx branch of dequant_gptq (tooling/sml_unpack.py:90-96): input k
+// takes the zero and scale of group g_idx[k] (desc_act files)
+void orc_gptq_dequant_row_gidx(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                               const int32_t * g_idx, int rows, int cols, int group, int zero_add, int row,
+                               float * out) {
+    uint8_t * c = malloc((size_t) cols), * z = malloc((size_t) (cols / group));
+    orc_gptq_unpack_row(qweight, qzeros, rows, cols, group, zero_add, row, c, z);
+    for (int k = 0; k < cols; k++) {
+        const int g = g_idx[k];
+        out[k] = (float) ((int) c[k] - (int) z[g]) * orc_f16_to_f32(scales[(size_t) g * rows + row]);
+    }
+    free(c);
+    free(z);
+}
+
+void orc_gptq_matvec_gidx(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                          const int32_t * g_idx, int rows, int cols, int group, int zero_add, const float * x,
+                          float * y) {
+    #pragma omp parallel
+    {
+        float * w = malloc((size_t) cols * 4);
+        #pragma omp for schedule(static)
+        for (int r = 0; r < rows; r++) {
+            orc_gptq_dequant_row_gidx(qweight, qzeros, scales, g_idx, rows, cols, group, zero_add, r, w);
+            double acc = 0.0;
+            for (int k = 0; k < cols; k++) acc += (double) w[k] * (double) x[k];
+            y[r] = (float) acc;
+        }
+        free(w);
+    }
+}
+
 void orc_gptq_matvec(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows, int cols,
                      int group, int zero_add, const float * x, float * y) {
     #pragma omp parallel

@@ -101,6 +101,13 @@ void orc_gptq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const
 // y = W.x with the dequantized weights, summed in double.
 void orc_gptq_matvec(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows, int cols,
                      int group, int zero_add, const float * x, float * y);
+// desc_act: input k takes group g_idx[k]'s zero and scale.
+void orc_gptq_dequant_row_gidx(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                               const int32_t * g_idx, int rows, int cols, int group, int zero_add, int row,
+                               float * out);
+void orc_gptq_matvec_gidx(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                          const int32_t * g_idx, int rows, int cols, int group, int zero_add, const float * x,
+                          float * y);
 void orc_awq_unpack_row(const int32_t * qweight, const int32_t * qzeros, int rows, int cols, int group, int row,
                         uint8_t * codes, uint8_t * zeros);
 void orc_awq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales, int rows,

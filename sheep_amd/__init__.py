@@ -87,6 +87,7 @@ _SIGS = [
     ("sml_hip_moe_ffn", c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("sml_hip_moe_time", c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, P(c_float), c_void_p]),
     ("sml_hip_gptq_upload", c_void_p, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int]),
+    ("sml_hip_gptq_upload_gidx", c_void_p, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int]),
     ("sml_hip_awq_upload", c_void_p, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int]),
     ("sml_hip_gptq_free", None, [c_void_p]),
     ("sml_hip_gptq_bytes", c_size_t, [c_void_p]),

@@ -219,6 +219,9 @@ typedef struct {
     int rows, cols;
     int zero_add;                 // added to the stored zero: 1 for the v1 files, 0 for v2
     int nslice;                   // cols / 1024 rounded up
+    // desc_act files: the input columns were reordered at upload so each
+    // group's are contiguous; device input i is input perm[i] (NULL: identity)
+    const int32_t * perm;
 } sml_kgptq;
 
 typedef struct {

@@ -1991,9 +1991,16 @@ __device__ void gptq_body(const sml_kgptq & a) {
     const bool ov = o < a.rows;
     const int gc = gv ? g : 0, oc = ov ? o : 0;
     const float * xg = a.x + (size_t) gc * 128;
-    // 1. this group's inputs (two per lane, for their sum), every weight word,
-    // then the group fields
-    const float2 xv = ((const float2 *) xg)[lane];
+    // 1. this group's inputs (two per lane, for their sum; through the
+    // column order of a desc_act file), every weight word, then the group
+    // fields
+    float2 xv;
+    if (a.perm) {
+        const int2 p = ((const int2 *) (a.perm + (size_t) gc * 128))[lane];
+        xv = make_float2(a.x[p.x], a.x[p.y]);
+    } else {
+        xv = ((const float2 *) xg)[lane];
+    }
     vw q[16];
     #pragma unroll
     for (int kk = 0; kk < 16; kk++)

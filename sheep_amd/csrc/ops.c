@@ -835,6 +835,7 @@ struct sml_hip_gptq {
     uint32_t * qweight, * qzeros;
     uint16_t * scales;
     float * part;
+    int32_t * perm;              // desc_act: device input i is input perm[i], or NULL
     int rows, cols, zero_add;
     size_t bytes;
 };
@@ -913,10 +914,75 @@ sml_hip_gptq * sml_hip_awq_upload(const int32_t * qweight, const int32_t * qzero
     return m;
 }
 
+// The column order of a desc_act matrix into HBM (0, or -1 with a reason).
+static int gptq_perm_upload(sml_hip_gptq * m, const int32_t * perm, size_t n) {
+    OP_BEGIN(-1);
+    m->perm = hx_malloc(n * 4);
+    HX(hipMemcpy(m->perm, perm, n * 4, hipMemcpyHostToDevice));
+    HX_LEAVE();
+    return 0;
+}
+
+// desc_act (tooling/sml_unpack.py:90-93): g_idx[k] is input k's group,
+// groups of `group` inputs in activation order. The input columns are
+// reordered on the host, stably by g_idx, so each group's codes are the
+// contiguous 128 the GEMV reads (moved, never recomputed), and the GEMV
+// gathers x through the same order; scales and zeros stay per group. Every
+// group must hold exactly `group` inputs (as GPTQ's desc_act writes them).
+sml_hip_gptq * sml_hip_gptq_upload_gidx(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                                        const int32_t * g_idx, int rows, int cols, int group, int zero_add) {
+    if (!g_idx) return sml_hip_gptq_upload(qweight, qzeros, scales, rows, cols, group, zero_add);
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 128 || group != 128 || !qweight) {
+        snprintf(hx.err, sizeof hx.err, "GPTQ matrix %dx%d group %d: rows must be a multiple of 8, cols of 128, "
+                 "group 128", rows, cols, group);
+        return NULL;
+    }
+    const size_t R = (size_t) rows, C = (size_t) cols, ng = C / 128;
+    int32_t * perm = malloc(C * 4);
+    size_t * fill = calloc(ng, sizeof(size_t));
+    uint32_t * qw = calloc(C / 8 * R, 4);
+    if (!perm || !fill || !qw) {
+        free(perm); free(fill); free(qw);
+        snprintf(hx.err, sizeof hx.err, "out of host memory");
+        return NULL;
+    }
+    int ident = 1, bad = 0;
+    for (size_t k = 0; k < C && !bad; k++) {
+        const int32_t g = g_idx[k];
+        if (g < 0 || (size_t) g >= ng || fill[g] >= 128) bad = 1;
+        else {
+            perm[(size_t) g * 128 + fill[g]++] = (int32_t) k;
+            ident &= (size_t) g == k / 128;
+        }
+    }
+    if (bad) {
+        free(perm); free(fill); free(qw);
+        snprintf(hx.err, sizeof hx.err, "g_idx: every group must hold exactly %d of the %d inputs", group, cols);
+        return NULL;
+    }
+    free(fill);
+    for (size_t i = 0; i < C; i++) {
+        const size_t k = (size_t) perm[i];
+        const uint32_t * src = (const uint32_t *) qweight + (k / 8) * R;
+        uint32_t * dst = qw + (i / 8) * R;
+        const unsigned ss = 4u * (unsigned) (k % 8), ds = 4u * (unsigned) (i % 8);
+        for (size_t n = 0; n < R; n++) dst[n] |= ((src[n] >> ss) & 15u) << ds;
+    }
+    sml_hip_gptq * m = sml_hip_gptq_upload((const int32_t *) qw, qzeros, scales, rows, cols, group, zero_add);
+    free(qw);
+    if (m && !ident && gptq_perm_upload(m, perm, C) != 0) {
+        sml_hip_gptq_free(m);
+        m = NULL;
+    }
+    free(perm);
+    return m;
+}
+
 void sml_hip_gptq_free(sml_hip_gptq * m) {
     HX_ENTRY();
     if (m) {
         HX(hipFree(m->qweight)); HX(hipFree(m->qzeros)); HX(hipFree(m->scales)); HX(hipFree(m->part));
+        if (m->perm) HX(hipFree(m->perm));
         free(m);
     }
     HX_LEAVE();
@@ -928,7 +994,7 @@ static void op_gptq(hipStream_t st, const sml_hip_gptq * m, const float * x, flo
     sml_kgptq a;
     memset(&a, 0, sizeof a);
     a.qweight = m->qweight; a.qzeros = m->qzeros; a.scales = m->scales;
-    a.x = x; a.part = m->part; a.y = y;
+    a.x = x; a.part = m->part; a.y = y; a.perm = m->perm;
     a.rows = m->rows; a.cols = m->cols; a.zero_add = m->zero_add;
     a.nslice = (m->cols / 128 + GPTQ_GROUPS_PER_WG - 1) / GPTQ_GROUPS_PER_WG;
     // 2 outputs per lane (128 per wave): twice the waves of 4 per lane, so

@@ -73,7 +73,7 @@ class GptqMat:
     """A GPTQ-style matrix resident in HBM (awq=True: the arrays are in the
     AWQ layout, qzeros may be None, zero_add is ignored)."""
 
-    def __init__(self, qweight, qzeros, scales, rows, cols, group=128, zero_add=1, awq=False):
+    def __init__(self, qweight, qzeros, scales, rows, cols, group=128, zero_add=1, awq=False, g_idx=None):
         self.rows, self.cols, self.group, self.zero_add = rows, cols, group, 0 if awq else zero_add
         qw = np.ascontiguousarray(qweight, np.int32)
         qz = None if qzeros is None else np.ascontiguousarray(qzeros, np.int32)
@@ -81,6 +81,10 @@ class GptqMat:
         if awq:
             h = lib().sml_hip_awq_upload(qw.ctypes.data, None if qz is None else qz.ctypes.data, sc.ctypes.data,
                                          rows, cols, group)
+        elif g_idx is not None:
+            gi = np.ascontiguousarray(g_idx, np.int32)
+            h = lib().sml_hip_gptq_upload_gidx(qw.ctypes.data, qz.ctypes.data, sc.ctypes.data, gi.ctypes.data,
+                                               rows, cols, group, zero_add)
         else:
             h = lib().sml_hip_gptq_upload(qw.ctypes.data, qz.ctypes.data, sc.ctypes.data, rows, cols, group,
                                           zero_add)
@@ -119,3 +123,12 @@ def time_matvec(mats, x, y, iters):
     if lib().sml_hip_gptq_time(arr, len(mats), x.ptr, y.ptr, iters, ctypes.byref(ms)) != 0:
         raise HipError(f"gptq time: {lib().sml_hip_last_error().decode(errors='replace')}")
     return ms.value
+
+
+def desc_act_gidx(cols, seed, group=128):
+    """A desc_act g_idx: inputs taken in a random activation order, the
+    order's positions grouped by `group` (g_idx[order[j]] = j // group)."""
+    order = np.random.default_rng(seed).permutation(cols)
+    g = np.empty(cols, np.int32)
+    g[order] = np.arange(cols) // group
+    return g

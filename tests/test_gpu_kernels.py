@@ -352,6 +352,44 @@ def test_gptq_unpack_bitexact(rows, cols, zero_add):
             np.testing.assert_array_equal(z[i], wz)
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 14336), (1000, 1152)])
+def test_gptq_desc_act(rows, cols):
+    """A desc_act matrix (g_idx scattering each group's 128 inputs over the
+    row): the upload reorders the input columns stably by g_idx and the GEMV
+    gathers x the same way. Codes and zeros come back in that order, bit for
+    bit the file's codes of inputs argsort(g_idx, stable); the GEMV within 1e-3
+    of the oracle's g_idx dequantize-then-dot; an identity g_idx gives the
+    plain upload's output bit for bit."""
+    from sheep_amd import gptq as gq
+    qw, qz, sc = gq.synth(rows, cols, seed=rows + 3)
+    rng = np.random.default_rng(cols + 5)
+    qz = rng.integers(0, 1 << 32, qz.shape, dtype=np.uint64).astype(np.uint32).view(np.int32)
+    g_idx = gq.desc_act_gidx(cols, rows)
+    order = np.argsort(g_idx, kind="stable")
+    m = gq.GptqMat(qw, qz, sc, rows, cols, g_idx=g_idx)
+    for r0, n in ((0, 8), (rows - 5, 5)):
+        c, z = m.unpack(r0, n)
+        for i in range(n):
+            wc, wz = ob.gptq_unpack_row(qw, qz, rows, cols, r0 + i)
+            np.testing.assert_array_equal(c[i], wc[order])
+            np.testing.assert_array_equal(z[i], wz)
+    x = rng.standard_normal(cols).astype(np.float32)
+    xd = sa.DevBuf.of(x)
+    y = sa.DevBuf(rows * 4)
+    m.matvec(xd, y)
+    close(y.read(np.float32), ob.gptq_matvec_gidx(qw, qz, sc, g_idx, rows, cols, x), f"gptq desc_act {rows}x{cols}")
+    ident = gq.GptqMat(qw, qz, sc, rows, cols, g_idx=(np.arange(cols) // 128).astype(np.int32))
+    plain = gq.GptqMat(qw, qz, sc, rows, cols)
+    ya, yb = sa.DevBuf(rows * 4), sa.DevBuf(rows * 4)
+    ident.matvec(xd, ya)
+    plain.matvec(xd, yb)
+    np.testing.assert_array_equal(ya.read(np.float32), yb.read(np.float32))
+    bad = np.array(g_idx)
+    bad[0] = bad[1] if bad[0] != bad[1] else (bad[1] + 1) % (cols // 128)
+    with pytest.raises(sa.HipError):
+        gq.GptqMat(qw, qz, sc, rows, cols, g_idx=bad)
+
+
 @pytest.mark.parametrize("rows,cols,with_zeros", [(4096, 14336, True), (1000, 1152, False)])
 def test_awq_unpack_and_gemv(rows, cols, with_zeros):
     """The AWQ layout (output-packed words, nibble order 0,4,1,5,2,6,3,7;

@@ -475,6 +475,28 @@ def test_gptq_known_answer(zero_add):
     np.testing.assert_allclose(y, (want.astype(np.float64) @ x.astype(np.float64)).astype(np.float32), rtol=1e-6, atol=1e-6)
 
 
+def test_gptq_desc_act_closed_form():
+    """desc_act (dequant_gptq's g_idx branch, tooling/sml_unpack.py:90-96):
+    input k takes the zero and scale of group g_idx[k]. On the known answer's
+    shapes with a scattered g_idx: every weight is (q - z[g_idx[k]]) * s[g_idx[k]]
+    exactly, and an identity g_idx equals the plain reading bit for bit."""
+    from sheep_amd import gptq as gq
+    rng = np.random.default_rng(1)
+    IN, OUT, GS = 64, 32, 16
+    q = rng.integers(0, 16, (OUT, IN))
+    zg = rng.integers(1, 16, (OUT, IN // GS))
+    s = (rng.random((OUT, IN // GS)) + 0.1).astype(np.float16)
+    g_idx = gq.desc_act_gidx(IN, 3, group=GS)
+    assert sorted(np.bincount(g_idx).tolist()) == [GS] * (IN // GS) and (g_idx != np.arange(IN) // GS).any()
+    qw, qz, sc = gq.pack(q, zg, s, zero_add=1)
+    for o in range(OUT):
+        w = ob.gptq_dequant_row_gidx(qw, qz, sc, g_idx, OUT, IN, o, group=GS)
+        want = (q[o] - zg[o][g_idx]).astype(np.float32) * s[o][g_idx].astype(np.float32)
+        assert np.abs(w - want).max() == 0.0
+        ident = ob.gptq_dequant_row_gidx(qw, qz, sc, (np.arange(IN) // GS).astype(np.int32), OUT, IN, o, group=GS)
+        np.testing.assert_array_equal(ident, ob.gptq_dequant_row(qw, qz, sc, OUT, IN, o, group=GS))
+
+
 @pytest.mark.parametrize("with_zeros", [True, False])
 def test_awq_known_answer(with_zeros):
     """The AWQ half of mlmi/tests/test_unpack.py:74-103 restated: 64 inputs x
