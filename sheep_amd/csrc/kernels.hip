@@ -350,8 +350,10 @@ __device__ __forceinline__ float seg_sum(float v) {
     return v;
 }
 
+// blk: the workgroup's row block (blockIdx.x, or each block a persistent
+// workgroup takes in turn); first: the activation is not yet in LDS.
 template <int NB, int RB, int NI, int WG, bool NT, int AM, bool SW, bool HQ, int LPR = 64, bool EX = false>
-__device__ void gemv_body(const sml_kgemv & a) {
+__device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first = true) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8;
     int8_t * lq = (int8_t *) lds;
@@ -362,7 +364,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
     const int l = lane % LPR, u = lane / LPR;
     constexpr int RPW = (SW ? RB / 2 : RB) * SUB;  // output rows per wave
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int row0 = (blockIdx.x * (WG / WAVE) + wave) * RPW;
+    const int row0 = (blk * (WG / WAVE) + wave) * RPW;
 
     // 1. activation loads (L2-resident, issued first)
     constexpr int SQ = AM == 0 ? 4 : 1, SG = AM == 0 ? 2 : 1;   // staged words per thread per round
@@ -377,19 +379,19 @@ __device__ void gemv_body(const sml_kgemv & a) {
     int4 fp[FK];
     if constexpr (AM == 0) {
         #pragma unroll
-        for (int k = 0; k < SQ; k++) { const int i = tid + k * WG; if (i < nq16) sq_[k] = ((const v4i *) a.q)[i]; }
+        for (int k = 0; k < SQ; k++) { const int i = tid + k * WG; if (first && i < nq16) sq_[k] = ((const v4i *) a.q)[i]; }
         #pragma unroll
         for (int k = 0; k < SG; k++) {
             const int i = tid + k * WG;
             sg_i[k] = i;
-            if (i < ng) { sg_s[k] = a.scale[i]; sg_u[k] = a.sums[i]; }
+            if (first && i < ng) { sg_s[k] = a.scale[i]; sg_u[k] = a.sums[i]; }
         }
     } else {
         #pragma unroll
         for (int k = 0; k < FK; k++) {
             const int f = tid + k * WG;
             fx[k] = make_float4(0.f, 0.f, 0.f, 0.f); fw[k] = fx[k]; fp[k] = make_int4(0, 0, 0, 0);
-            if (f < n / 4) {
+            if (first && f < n / 4) {
                 fx[k] = ((const float4 *) a.x)[f];
                 if (a.norm_w) fw[k] = ((const float4 *) a.norm_w)[f];
                 if (a.perm) fp[k] = ((const int4 *) a.perm)[f];
@@ -445,7 +447,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
         exb = (float4 *) (lds + base) + (size_t) wave * (NI * RB * 64);
         ext = (float *) (lds + base + (size_t) (WG / 64) * NI * RB * 64 * 16) + wave * (RB * SUB);
     }
-    bool staged = false;
+    bool staged = !first;
     for (int c0 = 0; c0 < ng; c0 += LPR * NI) {
         // 3. every weight load of this lane for NI chunks of RB rows, with no branches
         ChunkW<NB> w[NI][RB];
@@ -579,7 +581,7 @@ __device__ void gemv_body(const sml_kgemv & a) {
             const float is = s > 0.0f ? 1.0f / s : 0.0f;
             const int t = quant1(v, is);
             const int sum = isum32(t);
-            const int row = blockIdx.x * HO + tid;
+            const int row = blk * HO + tid;
             if (row < a.total_rows) {
                 a.hq[row] = (int8_t) t;
                 if ((tid & 31) == 0) { a.hscale[row >> 5] = s; a.hsums[row >> 5] = sum; }
@@ -664,6 +666,36 @@ __device__ void gemv_body(const sml_kgemv & a) {
 GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH(7) GEMV_WIDTH(8)
 // a whole 14336-wide row in one pass (tuning: SML_GEMV_NI=8)
 GEMV_KERNEL(4, 1, 8) GEMV_KERNEL(4, 2, 8)
+
+// Persistent forms (suffix _p, Q4): a grid of at most a few workgroups per CU,
+// each taking row blocks blockIdx.x, +gridDim.x, ...; the activation (or the
+// fused prologue's) is staged in LDS once per workgroup.
+template <int NB, int RB, int NI, int WG, int AM, bool SW, bool HQ, int LPR = 64>
+__device__ void gemv_persistent(const sml_kgemv & a) {
+    constexpr int RPWG = (WG / 64) * (SW ? RB / 2 : RB) * (64 / LPR);     // rows (outputs) per block
+    const int nblk = (a.total_rows + RPWG - 1) / RPWG;
+    for (int b = blockIdx.x; b < nblk; b += gridDim.x) {
+        gemv_body<NB, RB, NI, WG, true, AM, SW, HQ, LPR>(a, b, b == (int) blockIdx.x);
+        __syncthreads();
+    }
+}
+#define GEMV_KERNEL_P(RB, NI)                                                                               \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q4_r##RB##_i##NI##_p(const sml_kgemv a) {     \
+        gemv_persistent<4, RB, NI, 256, 0, false, false>(a);                                                \
+    }
+#define GEMV_KERNEL_NWP(RB)                                                                                 \
+    extern "C" __global__ __launch_bounds__(512) void sml_gemv_q4_r##RB##_i1_n512_p(const sml_kgemv a) {     \
+        gemv_persistent<4, RB, 1, 512, 1, false, false>(a);                                                 \
+    }
+GEMV_KERNEL_P(1, 2) GEMV_KERNEL_P(1, 4) GEMV_KERNEL_P(2, 1) GEMV_KERNEL_P(2, 2) GEMV_KERNEL_P(2, 4)
+GEMV_KERNEL_P(4, 1) GEMV_KERNEL_P(4, 2) GEMV_KERNEL_P(4, 4)
+GEMV_KERNEL_NWP(1) GEMV_KERNEL_NWP(2) GEMV_KERNEL_NWP(4)
+extern "C" __global__ __launch_bounds__(512) void sml_gemv_q4_hn_i2_p(const sml_kgemv a) {
+    gemv_persistent<4, 2, 2, 512, 1, true, true, 16>(a);
+}
+extern "C" __global__ __launch_bounds__(512) void sml_gemv_q4_h_i2_p(const sml_kgemv a) {
+    gemv_persistent<4, 2, 2, 512, 0, true, true, 16>(a);
+}
 
 // The exact forms (suffix _x, Q4 and Q8): the reference's float order per row
 // (gemv_body EX), for every shape pick_shape gives an unfused launch.

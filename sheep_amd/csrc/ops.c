@@ -470,9 +470,14 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
         if (fi == 2 || fi == 4) ni = fi;
         const int wg = am && env_int("SML_GEMV_HWG", 512) == 1024 && ni <= 4 ? 1024 : 512;
         if (a.total_rows % (wg / 16)) hx_failf("h quantization needs rows in whole workgroups");
-        if (wg == 1024) snprintf(name, sizeof name, "sml_gemv_q%d_hn1024_i%d", nb, ni);
+        unsigned grid = (unsigned) (a.total_rows / (wg / 16));
+        const int pw = env_int("SML_GEMV_PERSIST", 0);
+        if (pw > 0 && nb == 4 && ni == 2 && wg == 512 && grid > (unsigned) (pw * hx.ncu)) {
+            snprintf(name, sizeof name, "sml_gemv_q4_h%s_i2_p", am ? "n" : "");
+            grid = (unsigned) (pw * hx.ncu);
+        } else if (wg == 1024) snprintf(name, sizeof name, "sml_gemv_q%d_hn1024_i%d", nb, ni);
         else snprintf(name, sizeof name, "sml_gemv_q%d_h%s_i%d", nb, am ? "n" : "", ni);
-        hx_launch(name, (unsigned) (a.total_rows / (wg / 16)), 1, (unsigned) wg, lds, st, &a);
+        hx_launch(name, grid, 1, (unsigned) wg, lds, st, &a);
         return;
     }
     int rb, ni;
@@ -497,10 +502,17 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
     }
     const int rows_per_wave = swiglu ? rb / 2 : rb;
     const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
+    unsigned grid = (unsigned) ((waves + wg / 64 - 1) / (wg / 64));
+    // persistent forms (SML_GEMV_PERSIST = workgroups per CU): Q4, plain or
+    // with the 512-thread prologue
+    const int pw = env_int("SML_GEMV_PERSIST", 0);
+    const int pok = pw > 0 && nb == 4 && !swiglu && ni <= 4 && (wg == 256 ? !am : wg == 512 && ni == 1) &&
+                    grid > (unsigned) (pw * hx.ncu);
     if (swiglu) snprintf(name, sizeof name, "sml_gemv_q%d_s%s_r%d_i%d", nb, am ? "n" : "", rb, ni);
-    else if (wg != 256) snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_n%d", nb, rb, ni, wg);
-    else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d%s", nb, rb, ni, am ? "_n" : "");
-    hx_launch(name, (unsigned) ((waves + wg / 64 - 1) / (wg / 64)), 1, (unsigned) wg, lds, st, &a);
+    else if (wg != 256) snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_n%d%s", nb, rb, ni, wg, pok ? "_p" : "");
+    else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d%s%s", nb, rb, ni, am ? "_n" : "", pok ? "_p" : "");
+    if (pok) grid = (unsigned) (pw * hx.ncu);
+    hx_launch(name, grid, 1, (unsigned) wg, lds, st, &a);
 }
 
 int sml_hip_matvec(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, float * y) {

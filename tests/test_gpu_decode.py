@@ -147,6 +147,23 @@ def test_fusions_do_not_change_logits(model, request, monkeypatch):
         assert int(np.argmax(a)) == int(np.argmax(b))
 
 
+def test_persistent_gemv_grid_equals_default(qwenish, monkeypatch):
+    """SML_GEMV_PERSIST=1: the Q4 GEMVs with more row blocks than CUs (the
+    32000-row head, the 8960-row h-quantizing SwiGLU) run one workgroup per
+    CU walking the row blocks; each block's arithmetic is the default
+    launch's, so every step's logits are the same bits."""
+    outs = []
+    for pw in ("0", "1"):
+        monkeypatch.setenv("SML_GEMV_PERSIST", pw)
+        d = sa.Decoder(qwenish, n_ctx=64)
+        try:
+            outs.append([d.step(t, i, 32000).copy() for i, t in enumerate([3, 17, 250, 9, 31999])])
+        finally:
+            d.close()
+    for i, (a, b) in enumerate(zip(*outs)):
+        np.testing.assert_array_equal(a, b, err_msg=f"step {i}")
+
+
 @pytest.mark.parametrize("model", ["tiny", "qwenish"])
 def test_folded_merge_equals_merge_launch(model, request, monkeypatch):
     """SML_ATTN_FOLD=1 merges the attention splits in the attention launch
