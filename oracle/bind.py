@@ -71,12 +71,140 @@ def oracle():
             "orc_forward": (P(c_float), [c_void_p, c_int, c_int]),
             "orc_n_vocab": (c_int, [c_void_p]),
             "orc_model_per256": (None, [c_void_p, c_int]),
+            "orc_asym_grid": (None, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int, c_int,
+                                     c_int, c_void_p, c_void_p]),
+            "orc_field_search": (None, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                        c_int, c_int, c_int, c_void_p, c_int]),
+            "orc_grid_facs": (c_int, [c_int, c_void_p]),
+            "orc_two_level": (None, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+            "orc_requant_codes": (None, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p]),
+            "orc_perm_maxabs": (None, [c_void_p, c_int, c_int, c_void_p]),
+            "orc_unpack_dequant_f16": (None, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
+                                              c_int, c_int, c_void_p]),
+            "orc_requant": (None, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                                   c_void_p, c_void_p, c_void_p, c_void_p]),
         }
         for k, (r, a) in sig.items():
             f = getattr(l, k)
             f.restype, f.argtypes = r, a
         _orc = l
     return _orc
+
+
+REFQ_PATH = os.path.join(HERE, "_ref", "libsmlquant.so")
+_refq = None
+
+
+def have_refq():
+    return os.path.exists(REFQ_PATH)
+
+
+def refq():
+    """The reference quantizer's fused C searches (sml/sml-quant.c), compiled from its source."""
+    global _refq
+    if _refq is None:
+        if not have_refq():
+            raise RuntimeError(f"{REFQ_PATH} is not built (its sources are only present where the reference is)")
+        l = ctypes.CDLL(REFQ_PATH)
+        l.sml_asym_grid.restype = None
+        l.sml_asym_grid.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int, c_int,
+                                    c_int, c_void_p, c_void_p]
+        l.sml_field_search.restype = None
+        l.sml_field_search.argtypes = [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                       c_int, c_int, c_int, c_void_p, c_int]
+        _refq = l
+    return _refq
+
+
+def _pp(a):
+    return None if a is None else a.ctypes.data
+
+
+def grid_facs(ncand=20):
+    f = np.zeros(max(64, ncand + 4), np.float32)
+    n = oracle().orc_grid_facs(ncand, f.ctypes.data)
+    return f[:n].copy()
+
+
+def asym_grid(wp, group, nbits, wt=None, rem=0, ncand=20, iters=3, refit=1, lib=None):
+    """(mins, steps) [rows][cols/group] from the oracle, or from the
+    reference's own library when lib is refq()."""
+    wp = np.ascontiguousarray(wp, np.float32)
+    rows, cols = wp.shape
+    facs = grid_facs(ncand)
+    ol = np.zeros((rows, cols // group), np.float32)
+    os_ = np.zeros_like(ol)
+    wt = None if wt is None else np.ascontiguousarray(wt, np.float32)
+    if lib is None:
+        oracle().orc_asym_grid(wp.ctypes.data, rows, cols, group, nbits, rem, _pp(wt), facs.ctypes.data, len(facs),
+                               iters, refit, ol.ctypes.data, os_.ctypes.data)
+    else:
+        lib.sml_asym_grid(wp.ctypes.data, rows, cols, group, nbits, rem, _pp(wt), facs.ctypes.data, len(facs),
+                          iters, refit, ol.ctypes.data, os_.ctypes.data)
+    return ol, os_
+
+
+def field_search(w, dv, dm, q8, mq8, group, nmax, hi=255, moff=127, mmax=254, wt=None, radius=2, lib=None):
+    """(q8, mq8) int32 after the field search, from the oracle or the reference's library."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    a = np.ascontiguousarray(q8, np.int32).copy()
+    b = np.ascontiguousarray(mq8, np.int32).copy()
+    dv = np.ascontiguousarray(dv, np.float32)
+    dm = np.ascontiguousarray(dm, np.float32)
+    wt = None if wt is None else np.ascontiguousarray(wt, np.float32)
+    f = oracle().orc_field_search if lib is None else lib.sml_field_search
+    f(w.ctypes.data, rows, cols, group, dv.ctypes.data, dm.ctypes.data, a.ctypes.data, b.ctypes.data, nmax, hi,
+      moff, mmax, _pp(wt), radius)
+    return a, b
+
+
+def two_level(v, gps=8, signed=False):
+    """(d16 uint16 [rows][nsb], q8 uint8 [rows][ng], eff float32 [rows][ng])."""
+    v = np.ascontiguousarray(v, np.float32)
+    rows, ng = v.shape
+    nsb = (ng + gps - 1) // gps
+    d16 = np.zeros((rows, nsb), np.uint16)
+    q8 = np.zeros((rows, ng), np.uint8)
+    eff = np.zeros((rows, ng), np.float32)
+    oracle().orc_two_level(v.ctypes.data, rows, ng, gps, int(signed), d16.ctypes.data, q8.ctypes.data, eff.ctypes.data)
+    return d16, q8, eff
+
+
+def perm_maxabs(w):
+    w = np.ascontiguousarray(w, np.float32)
+    p = np.zeros(w.shape[1], np.int32)
+    oracle().orc_perm_maxabs(w.ctypes.data, w.shape[0], w.shape[1], p.ctypes.data)
+    return p
+
+
+def unpack_dequant_f16(qweight, qzeros, scales, g_idx, rows, cols, bits, group, zero_add=1, awq=False):
+    """[rows][cols] float32 holding the fp16 values of the unpacked copy."""
+    out = np.zeros((rows, cols), np.float32)
+    qw = np.ascontiguousarray(qweight, np.int32)
+    qz = None if qzeros is None else np.ascontiguousarray(qzeros, np.int32)
+    sc = np.ascontiguousarray(scales, np.float16).view(np.uint16)
+    gi = None if g_idx is None else np.ascontiguousarray(g_idx, np.int32)
+    oracle().orc_unpack_dequant_f16(qw.ctypes.data, _pp(qz), sc.ctypes.data, _pp(gi), rows, cols, bits, group,
+                                    zero_add, int(awq), out.ctypes.data)
+    return out
+
+
+def requant(w, nbits=4, perm=None, wt=None, radius=2):
+    """The oracle's whole re-quantization: dict of codes [rows][cols] (permuted
+    order), sd, sq, md, mq, perm."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    ng, ns = cols // 32, cols // 256
+    out = {"codes": np.zeros((rows, cols), np.uint8), "sd": np.zeros((rows, ns), np.uint16),
+           "sq": np.zeros((rows, ng), np.uint8), "md": np.zeros((rows, ns), np.uint16),
+           "mq": np.zeros((rows, ng), np.uint8), "perm": np.zeros(cols, np.int32)}
+    pin = None if perm is None else np.ascontiguousarray(perm, np.int32)
+    wt = None if wt is None else np.ascontiguousarray(wt, np.float32)
+    oracle().orc_requant(w.ctypes.data, rows, cols, nbits, _pp(pin), _pp(wt), radius, out["codes"].ctypes.data,
+                         out["sd"].ctypes.data, out["sq"].ctypes.data, out["md"].ctypes.data, out["mq"].ctypes.data,
+                         out["perm"].ctypes.data)
+    return out
 
 
 def have_ref():
@@ -477,17 +605,21 @@ def q4k_random_blocks(rows, cols, seed):
 
 
 class FlatView:
-    """An OrcTensor over raw FLAT Q4 arrays (plane, sd, md, sq, mq as numpy
-    arrays, kept alive here), e.g. a repacked Q4_K matrix."""
+    """An OrcTensor over raw FLAT arrays (the plane, or the list of planes of
+    width nbits, sd, md, sq, mq as numpy arrays, kept alive here), e.g. a
+    repacked Q4_K matrix or a re-quantized tensor."""
 
-    def __init__(self, plane, sd, md, sq, mq, rows, cols):
-        self.arrays = [np.ascontiguousarray(a) for a in (plane, sd, md, sq, mq)]
+    def __init__(self, plane, sd, md, sq, mq, rows, cols, nbits=4):
+        planes = list(plane) if isinstance(plane, (list, tuple)) else [plane]
+        self.arrays = [np.ascontiguousarray(a) for a in (sd, md, sq, mq)]
+        self.planes = [np.ascontiguousarray(a) for a in planes]
         self.rows, self.cols = rows, cols
         self.ot = OrcTensor()
-        self.ot.plane[0] = self.arrays[0].ctypes.data
-        self.ot.sd, self.ot.md = self.arrays[1].ctypes.data, self.arrays[2].ctypes.data
-        self.ot.sq, self.ot.mq = self.arrays[3].ctypes.data, self.arrays[4].ctypes.data
-        self.ot.rows, self.ot.cols, self.ot.nbits, self.ot.scale6, self.ot.minneg = rows, cols, 4, 0, 0
+        for i, a in enumerate(self.planes):
+            self.ot.plane[i] = a.ctypes.data
+        self.ot.sd, self.ot.md = self.arrays[0].ctypes.data, self.arrays[1].ctypes.data
+        self.ot.sq, self.ot.mq = self.arrays[2].ctypes.data, self.arrays[3].ctypes.data
+        self.ot.rows, self.ot.cols, self.ot.nbits, self.ot.scale6, self.ot.minneg = rows, cols, nbits, 0, 0
 
     def dequant(self, row):
         out = np.zeros(self.cols, np.float32)

@@ -216,12 +216,27 @@ void orc_unpack_row(const orc_tensor * t, int row, uint8_t * codes) {
     free(a); free(b);
 }
 
+// The reference build (-O3 with FMA) contracts code*step + min into one fused
+// multiply-add; Q3, Q5 and Q7 then add their 1-bit plane's share,
+// step*2^shift, to that sum where the bit is set (sml_dequant_bits1_add).
+// follows sml/sml-kernel.c:231-263 (2-bit), :2134-2157 (flat4), :2160-2170
+// (the 1-bit add), :2174-2198 (flat8), :2235-2260 (flat6), composed per width
+// as sml/sml-run.c:3300-3335 does
 void orc_dequant_row(const orc_tensor * t, int row, float * out) {
     uint8_t * c = malloc((size_t) t->cols);
     orc_unpack_row(t, row, c);
+    const int nb = t->nbits;
+    const int shift = nb == 3 ? 2 : nb == 5 ? 4 : nb == 7 ? 6 : 0;     // the 1-bit plane's place
+    const int low = shift ? (1 << shift) - 1 : 255;
     for (int g = 0; g < t->cols / 32; g++) {
         const float st = orc_step(t, row, g), mn = orc_min(t, row, g);
-        for (int j = 0; j < 32; j++) out[g * 32 + j] = (float) c[g * 32 + j] * st + mn;
+        const float add = st * (float) (1 << shift);
+        for (int j = 0; j < 32; j++) {
+            const int code = c[g * 32 + j];
+            float v = fmaf((float) (code & low), st, mn);
+            if (shift && (code >> shift) & 1) v = v + add;
+            out[g * 32 + j] = v;
+        }
     }
     free(c);
 }

@@ -146,6 +146,33 @@ void orc_model_per256(orc_model * m, int on);
 // Tensor view by name, for single-matrix checks.
 int orc_model_tensor(const orc_model * m, const char * name, orc_tensor * out, const int32_t ** perm);
 
+
+// ---------------------------------------------------------------- re-quantization (sml_oracle_quant.c)
+// The reference quantizer's searches and encoder for a tensor without
+// calibration feedback, the step a GPTQ/AWQ copy takes after the unpacker.
+// follows sml/sml-quant.c:20-95 (sml_asym_grid), in its build's FMA order
+void orc_asym_grid(const float * wp, int rows, int cols, int group, int nbits, int rem, const float * wt,
+                   const float * facs, int ncand, int iters, int refit, float * out_l, float * out_s);
+// follows sml/sml-quant.c:101-137 (sml_field_search)
+void orc_field_search(const float * w, int rows, int cols, int group, const float * dv, const float * dm,
+                      int32_t * q8, int32_t * mq8, int nmax, int hi, int moff, int mmax, const float * wt, int radius);
+// the range factors of tooling/sml_grid_c.py:41-42; returns their count
+int orc_grid_facs(int ncand, float * facs);
+// follows tooling/sml_quantize.py:320-363 (two_level, 8-bit fields)
+void orc_two_level(const float * v, int rows, int ng, int gps, int is_signed, uint16_t * d16, uint8_t * q8, float * eff);
+// follows tooling/sml_quantize.py:565-572 (the codes of encode)
+void orc_requant_codes(const float * wp, int rows, int cols, const float * eff_s, const float * eff_m, int nmax,
+                       uint8_t * codes);
+// follows tooling/sml_quantize.py:479 (ascending max |w|; ties by column index)
+void orc_perm_maxabs(const float * w, int rows, int cols, int32_t * perm);
+// follows tooling/sml_unpack.py:66-118 (GPTQ 2/4/8-bit, AWQ 4-bit; fp16 result)
+void orc_unpack_dequant_f16(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
+                            const int32_t * g_idx, int rows, int cols, int bits, int group, int zero_add, int awq,
+                            float * out);
+// follows tooling/sml_quantize.py:426-581 (run + encode with no activations)
+void orc_requant(const float * w, int rows, int cols, int nbits, const int32_t * perm_in, const float * wt, int radius,
+                 uint8_t * codes, uint16_t * sd, uint8_t * sq, uint16_t * md, uint8_t * mq, int32_t * perm);
+
 #ifdef __cplusplus
 }
 #endif

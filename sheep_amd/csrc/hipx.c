@@ -10,8 +10,10 @@ hx_state hx = { .fail_after = -1, .device = -1 };
 static struct { char name[64]; hipFunction_t f; } fn_cache[FN_CACHE];
 static int fn_n;
 
-// the gfx950 code object, linked in from kernels.hsaco (code_object.S)
+// the gfx950 code objects, linked in from kernels.hsaco and ingest.hsaco
+// (code_object.S)
 extern const unsigned char sml_code_object[];
+extern const unsigned char sml_ingest_object[];
 
 void hx_fail(const char * what, hipError_t e) {
     snprintf(hx.err, sizeof hx.err, "%s: %s", what, hipGetErrorString(e));
@@ -42,8 +44,10 @@ void hx_init(int device) {
         hx.inited = 0;            // a failure from here on leaves no stale module in use
         fn_n = 0;
         HX(hipModuleUnload(hx.mod));
+        HX(hipModuleUnload(hx.mod_ingest));
     }
     HX(hipModuleLoadData(&hx.mod, sml_code_object));
+    HX(hipModuleLoadData(&hx.mod_ingest, sml_ingest_object));
     fn_n = 0;
     hx.ncu = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
     hx.device = device;
@@ -55,7 +59,7 @@ hipFunction_t hx_fn(const char * name) {
     for (int i = 0; i < fn_n; i++)
         if (strcmp(fn_cache[i].name, name) == 0) return fn_cache[i].f;
     hipFunction_t f;
-    HX(hipModuleGetFunction(&f, hx.mod, name));
+    HX(hipModuleGetFunction(&f, strncmp(name, "sml_ing_", 8) == 0 ? hx.mod_ingest : hx.mod, name));
     if (fn_n < FN_CACHE) {
         snprintf(fn_cache[fn_n].name, sizeof fn_cache[fn_n].name, "%s", name);
         fn_cache[fn_n].f = f;

@@ -19,6 +19,7 @@ typedef struct {
     int       inited;
     int       device;
     hipModule_t mod;
+    hipModule_t mod_ingest;       // the ingest kernels (built without contraction)
     int       ncu;                // compute units of the device
     long      fail_after;         // test hook: fail the Nth HIP call from now (< 0: off)
     long      calls;              // HIP calls made through HX() so far

@@ -298,3 +298,71 @@ typedef struct {
     const float * resid;          // [T][n] added first (may alias out), or NULL
     float * out;                  // [T][n]
 } sml_kmoe_comb;
+
+// ---------------------------------------------------------------- ingest
+// Re-quantization of a dequantized GPTQ/AWQ tensor (or any float tensor) into
+// SSF FLAT codes and two-level fields, on the GPU (ingest.hip).
+
+// GPTQ (bits 2/4/8) or AWQ (4 bits) integers to fp16-rounded floats
+// out [rows][cols], rows = outputs.
+typedef struct {
+    const uint32_t * qweight;
+    const uint32_t * qzeros;      // NULL (AWQ only): zero 2^(bits-1)
+    const uint16_t * scales;      // [groups][rows] fp16
+    const int32_t  * g_idx;       // [cols] or NULL: input k's group is k / group
+    float * out;
+    int rows, cols, bits, group, zero_add, awq;
+} sml_king_dequant;
+
+// key[c] = max over rows of |w[r][c]| (NaN wins)
+typedef struct { const float * w; float * key; int rows, cols; } sml_king_colmax;
+
+// perm[rank of key[c]] = c: ascending key, NaN last, ties by column
+typedef struct { const float * key; int32_t * perm; int cols; } sml_king_rank;
+
+// wp[r][i] = w[r][perm[i]]
+typedef struct { const float * w; const int32_t * perm; float * wp; int rows, cols; } sml_king_gather;
+
+// Per-group (min, step) of the asymmetric grid (one lane per group).
+typedef struct {
+    const float * wp;             // [rows][cols], columns already permuted
+    const float * wt;             // [cols] normalised weights, or NULL for ones
+    const float * facs;           // [ncand] range factors
+    float * out_l, * out_s;       // [rows][cols/group]
+    int rows, cols, group, nbits, rem, ncand, iters, refit;
+} sml_king_grid;
+
+// Two-level fields of a [rows][ng] float array, 8-bit: fp16 per superblock of
+// gps groups, uint8 per group; is_signed: biased by 127 (mins).
+typedef struct {
+    const float * v;
+    uint16_t * d16;               // [rows][nsb]
+    uint8_t * q8;                 // [rows][ng]
+    float * eff;                  // [rows][ng], or NULL
+    int rows, ng, gps, is_signed;
+} sml_king_two;
+
+// The field search: each group's step field q8 and min field mq8 moved to the
+// best neighbour within +-radius. Scales per group (dv/dm [rows][ng]) or per
+// superblock (d16/md16 fp16 [rows][nsb] with gps groups each).
+typedef struct {
+    const float * w;              // [rows][cols] (permuted)
+    const float * dv, * dm;       // per group, or NULL
+    const uint16_t * d16, * md16; // per superblock (when dv is NULL)
+    int gps;
+    int32_t * q8, * mq8;          // in/out (int32), or NULL
+    uint8_t * sq, * mq;           // in/out (uint8, when q8 is NULL)
+    float * eff_s, * eff_m;       // out: q8*dv and (mq8 - moff)*dm, or NULL
+    const float * wt;             // [cols] or NULL
+    int rows, cols, group, nmax, hi, moff, mmax, radius;
+} sml_king_field;
+
+// Codes clip(rint((w - M) / max(S, 1e-12)), 0, nmax) of every weight, packed
+// into the FLAT planes of width nbits (one thread per 128 weights of a row).
+typedef struct {
+    const float * wp;             // [rows][cols] (permuted)
+    const float * eff_s, * eff_m; // [rows][cols/32]
+    uint8_t * plane[3];           // the width's planes, row-major
+    uint8_t * codes;              // [rows][cols] codes too, or NULL
+    int rows, cols, nbits;
+} sml_king_pack;

@@ -937,9 +937,16 @@ extern "C" __global__ void sml_embed(const sml_kembed a) {
     const uint16_t * d = a.m.sdmd + (row * ns + g / 8) * 2;
     const float step = h2f(d[0]) * (float) f[0];
     const float mn = h2f(d[1]) * ((float) f[1] - 127.0f);
+    // the reference's order: fma(code, step, min), then Q3/Q5/Q7 add their
+    // 1-bit plane's step*2^shift where the bit is set (sml/sml-kernel.c:2134-2260)
+    const int shift = a.nbits == 3 ? 2 : a.nbits == 5 ? 4 : a.nbits == 7 ? 6 : 0;
+    const int low = shift ? (1 << shift) - 1 : 255;
+    const float add = step * (float) (1 << shift);
     for (int j = 0; j < 32; j++) {
         const int col = g * 32 + j;
-        x[a.perm ? a.perm[col] : col] = (float) c[j] * step + mn;
+        float v = __builtin_fmaf((float) (c[j] & low), step, mn);
+        if (shift && (c[j] >> shift) & 1) v = v + add;
+        x[a.perm ? a.perm[col] : col] = v;
     }
 }
 

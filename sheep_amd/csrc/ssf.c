@@ -204,6 +204,11 @@ typedef struct {
     int zero_mean;            // QUANT: mins at -(2^b - 1)/2 steps
     int fill;                 // F32: 0 = 1+N(0,s), 1 = N(0,s)
     float sigma;
+    // QUANT given by the caller instead of generated: planes, fields, perm
+    const uint8_t * g_planes[SSF_MAX_PLANES];
+    const uint16_t * g_sd, * g_md;
+    const uint8_t * g_sq, * g_mq;
+    const int32_t * g_perm;
     ssf_record rec;
 } plan_t;
 
@@ -372,6 +377,7 @@ static int write_plan(const char * path, ssf_header * h, plan_list * l, uint64_t
     uint64_t off = align256(h->table_off + (uint64_t) l->n * sizeof(ssf_record));
     // permutation arrays, one per distinct key
     int nkeys = 0;
+    const int32_t ** kperm = calloc((size_t) l->n, sizeof(int32_t *));
     int * keys = calloc((size_t) l->n, sizeof(int));
     uint64_t * koff = calloc((size_t) l->n, sizeof(uint64_t));
     int * kcols = calloc((size_t) l->n, sizeof(int));
@@ -392,7 +398,7 @@ static int write_plan(const char * path, ssf_header * h, plan_list * l, uint64_t
         for (int j = 0; j < nkeys; j++) if (keys[j] == p->perm_key && kcols[j] == p->cols) k = j;
         if (k < 0) {
             k = nkeys++;
-            keys[k] = p->perm_key; kcols[k] = p->cols; koff[k] = off;
+            keys[k] = p->perm_key; kcols[k] = p->cols; koff[k] = off; kperm[k] = p->g_perm;
             off = align256(off + (uint64_t) p->cols * 4u);
         }
         r->perm_off = koff[k]; r->perm_bytes = (uint64_t) p->cols * 4u;
@@ -422,6 +428,7 @@ static int write_plan(const char * path, ssf_header * h, plan_list * l, uint64_t
     for (int i = 0; ok && i < l->n; i++)
         ok = write_at(fd, &l->v[i].rec, sizeof(ssf_record), h->table_off + (uint64_t) i * sizeof(ssf_record));
     for (int k = 0; ok && k < nkeys; k++) {
+        if (kperm[k]) { ok = write_at(fd, kperm[k], (size_t) kcols[k] * 4u, koff[k]); continue; }
         int32_t * perm = malloc((size_t) kcols[k] * 4u);
         make_perm(perm, kcols[k], random_perm, seed, keys[k]);
         ok = write_at(fd, perm, (size_t) kcols[k] * 4u, koff[k]);
@@ -442,9 +449,16 @@ static int write_plan(const char * path, ssf_header * h, plan_list * l, uint64_t
             free(v);
             continue;
         }
-        uint8_t * planes[SSF_MAX_PLANES] = { 0 };
         int pb[SSF_MAX_PLANES];
         const int np = ssf_flat_planes(p->nbits, pb);
+        if (p->g_sd) {
+            ok = write_at(fd, p->g_sd, r->sd_bytes, r->sd_off) && write_at(fd, p->g_sq, r->sq_bytes, r->sq_off) &&
+                 write_at(fd, p->g_md, r->md_bytes, r->md_off) && write_at(fd, p->g_mq, r->mq_bytes, r->mq_off);
+            for (int j = 0; ok && j < np; j++) ok = write_at(fd, p->g_planes[j], r->plane_bytes[j], r->plane_off[j]);
+            if (!ok) say(why, nwhy, "write failed on %s", p->name);
+            continue;
+        }
+        uint8_t * planes[SSF_MAX_PLANES] = { 0 };
         for (int j = 0; j < np; j++) planes[j] = malloc(r->plane_bytes[j]);
         uint16_t * sd = malloc(r->sd_bytes), * md = malloc(r->md_bytes);
         uint8_t * sq = malloc(r->sq_bytes), * mq = malloc(r->mq_bytes);
@@ -459,7 +473,7 @@ static int write_plan(const char * path, ssf_header * h, plan_list * l, uint64_t
         if (!ok) say(why, nwhy, "write failed on %s", p->name);
     }
     if (fd >= 0) close(fd);
-    free(keys); free(koff); free(kcols);
+    free(keys); free(koff); free(kcols); free(kperm);
     if (ok && rename(tmp, path) != 0) { ok = 0; say(why, nwhy, "cannot rename %s", tmp); }
     if (!ok) unlink(tmp);
     return ok;
@@ -542,6 +556,31 @@ int ssf_synth_matrix(const char * path, int rows, int cols, int nbits, int rando
     plan_list l = { 0 };
     add_quant(&l, "w", rows, cols, nbits, 0, 0);
     const int ok = write_plan(path, &h, &l, seed, random_perm, step_sigma, why, nwhy);
+    free(l.v);
+    return ok;
+}
+
+int ssf_write_quant(const char * path, const char * name, int rows, int cols, int nbits,
+                    const uint8_t * const planes[SSF_MAX_PLANES], const uint16_t * sd, const uint8_t * sq,
+                    const uint16_t * md, const uint8_t * mq, const int32_t * perm, char * why, int nwhy) {
+    int pb[SSF_MAX_PLANES];
+    if (rows <= 0 || cols <= 0 || cols % 128 || nbits < 2 || nbits > 8 || !name || strlen(name) >= SSF_NAME_LEN ||
+        !sd || !sq || !md || !mq || !perm) {
+        say(why, nwhy, "quantized record arguments out of range");
+        return 0;
+    }
+    const int np = ssf_flat_planes(nbits, pb);
+    for (int i = 0; i < np; i++)
+        if (!planes[i]) { say(why, nwhy, "plane %d of width %d missing", i, nbits); return 0; }
+    ssf_header h;
+    base_header(&h);
+    h.n_layer = 0; h.n_embd = (uint32_t) cols; h.n_head = 1; h.n_head_kv = 1;
+    plan_list l = { 0 };
+    add_quant(&l, name, rows, cols, nbits, 0, 0);
+    plan_t * p = &l.v[0];
+    for (int i = 0; i < np; i++) p->g_planes[i] = planes[i];
+    p->g_sd = sd; p->g_sq = sq; p->g_md = md; p->g_mq = mq; p->g_perm = perm;
+    const int ok = write_plan(path, &h, &l, 0, 0, 0.0f, why, nwhy);
     free(l.v);
     return ok;
 }
