@@ -367,6 +367,29 @@ def batched_decode(dec, n_vocab, ns=16, steps=20, pos0=1024):
     return res
 
 
+def ingest_leg(rows=4096, cols=14336, trials=3):
+    """The GPTQ-4 tensor of the width sweep (group 128, seed 1004)
+    re-quantized into SSF Q4 on the device: unpack to fp16, column order,
+    grid search, two-level fields, field search, codes and planes. GPU time
+    from HIP events around the kernels, best of `trials`."""
+    from sheep_amd import gptq as gq, ingest
+    qw, qz, sc = gq.synth(rows, cols, seed=1004)
+    t = {"qweight": qw, "qzeros": qz, "scales": sc}
+    qc = {"bits": 4, "group_size": 128}
+    ingest.ingest_gptq(t, qc)                    # warm-up
+    best, wall = 1e9, 1e9
+    for _ in range(trials):
+        sa.sync()
+        t0 = time.perf_counter()
+        r = ingest.ingest_gptq(t, qc)
+        sa.sync()
+        wall = min(wall, time.perf_counter() - t0)
+        best = min(best, r.ms)
+    n = rows * cols
+    return {"tensor": f"GPTQ-4 {rows}x{cols} group 128 -> SSF Q4", "weights": n, "gpu_ms": round(best, 3),
+            "weights_per_s": round(n / (best * 1e-3), 1), "wall_ms_with_uploads": round(wall * 1e3, 2)}
+
+
 def host_cpu():
     model = "unknown"
     try:
@@ -424,6 +447,29 @@ def cpu_leg(args):
         sec = r.ref_time_matvec(planes, arrs[0], arrs[1], arrs[2], arrs[3], ncopy, rows, cols, t.nbits,
                                 x.ctypes.data, threads, 12)
         print(json.dumps({"us": round(sec * 1e6, 1), "rows": rows, "cols": cols, "nbits": t.nbits}))
+    elif kind == "ingest":
+        # the reference quantizer's fused C searches (sml-quant.c, OpenMP over
+        # rows) on a row slice of the same float16 copy: the grid, then the
+        # field search on its two-level fields
+        from sheep_amd import gptq as gq
+        rows, cols, sample = int(args[2]), int(args[3]), int(args[4])
+        qw, qz, sc = gq.synth(rows, cols, seed=1004)
+        w = ob.unpack_dequant_f16(qw, qz, sc, None, rows, cols, 4, 128, 1)[:sample]
+        rq = ob.refq()
+        t0 = time.perf_counter()
+        mins, steps = ob.asym_grid(w, 32, 4, lib=rq)
+        t1 = time.perf_counter()
+        d16, q8, _ = ob.two_level(steps, 8, signed=False)
+        md16, mq8, _ = ob.two_level(mins, 8, signed=True)
+        dv = np.repeat(d16.view(np.float16).astype(np.float32), 8, axis=1)
+        dm = np.repeat(md16.view(np.float16).astype(np.float32), 8, axis=1)
+        t2 = time.perf_counter()
+        ob.field_search(w, dv, dm, q8, mq8, 32, 15, lib=rq)
+        t3 = time.perf_counter()
+        n = sample * cols
+        print(json.dumps({"rows_sampled": sample, "weights": n, "grid_s": round(t1 - t0, 3),
+                          "field_s": round(t3 - t2, 3),
+                          "weights_per_s": round(n / ((t1 - t0) + (t3 - t2)), 1)}))
     elif kind == "moe":
         path, regime, steps = args[2], args[3], int(args[4])
         if regime == "exact":
@@ -491,6 +537,10 @@ def cpu_baseline(path, pos0, moe_path, gemv_paths, budget_s=10.0):
     if moe_path:
         out["moe_16_slots"] = {r: run_cpu_leg("moe", tmax, moe_path, r, 6) for r in ("default", "exact")}
         log(f"cpu moe: {out['moe_16_slots']}")
+    from oracle import bind as ob
+    if ob.have_refq():
+        out["ingest"] = run_cpu_leg("ingest", tmax, 4096, 14336, 512)
+        log(f"cpu ingest searches: {out['ingest']}")
     return out
 
 
@@ -511,6 +561,7 @@ def main():
     ap.add_argument("--small-gemm", action="store_true", help="only time the 16-row small-M GEMMs")
     ap.add_argument("--gemv-sweep", action="store_true",
                     help="only the Q4 GEMV and streaming read at 34..544 MB (fixed cost vs steady rate)")
+    ap.add_argument("--ingest", action="store_true", help="only re-quantize the GPTQ-4 4096 x 14336 tensor")
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: fill the 4096 context)")
     ap.add_argument("--prompt-only", type=int, metavar="LEVEL", default=-1,
@@ -537,6 +588,8 @@ def main():
             res = {"small_m_gemm": small_gemm(work)}
         elif a.gemv_sweep:
             res = {"gemv_size_sweep": gemv_size_sweep(work)}
+        elif a.ingest:
+            res = {"ingest": ingest_leg()}
         elif a.decode_trace:
             res = {"decode_trace": decode_trace(work, a.decode_trace, a.steps)}
         elif a.prompt_only >= 0:
@@ -715,6 +768,9 @@ def run(a, work):
         extra["width_sweep"] = width_sweep(work)
         log(f"width sweep ({time.perf_counter() - t1:.1f}s): " +
             ", ".join(f"{k} {v['GB/s']}" for k, v in extra["width_sweep"].items()))
+        t1 = time.perf_counter()
+        extra["ingest"] = ingest_leg()
+        log(f"ingest: {extra['ingest']} ({time.perf_counter() - t1:.1f}s)")
     tps = K / dt
     kv_bytes = 2 * LLAMA["n_layer"] * LLAMA["n_head_kv"] * 128 * 2 * (pos + K / 2)
     roof_tps = HBM_PEAK_GBS * 1e9 / wbytes

@@ -27,7 +27,8 @@ static void ing_grid(hipStream_t st, const float * wp, int rows, int cols, int g
     a.wp = wp; a.wt = wt; a.facs = facs; a.out_l = out_l; a.out_s = out_s;
     a.rows = rows; a.cols = cols; a.group = group; a.nbits = nbits; a.rem = rem;
     a.ncand = ncand; a.iters = iters; a.refit = refit;
-    hx_launch(group == 32 ? "sml_ing_grid32" : "sml_ing_grid", blocks((int64_t) rows * (cols / group)), 1, 256, 0, st, &a);
+    const char * k = group != 32 ? "sml_ing_grid" : wt ? "sml_ing_grid32w" : "sml_ing_grid32";
+    hx_launch(k, blocks((int64_t) rows * (cols / group)), 1, 256, 0, st, &a);
 }
 
 static void ing_field(hipStream_t st, sml_king_field * a) {
@@ -209,11 +210,12 @@ int sml_hip_requant(const float * w, int rows, int cols, int nbits, const int32_
         longjmp(*outer, 1);
     }
     hx.jb = &jb;
-    // scratch: wp, mins, steps, eff_s, eff_m, keys, factors
-    const size_t bytes = nw * 4 + 4 * ng * 4 + (size_t) cols * 4 + 64 * 4;
+    // scratch: wp, mins, steps, eff_s, eff_m, keys, factors, column-max partials, rank counts
+    const size_t bytes = nw * 4 + 4 * ng * 4 + (size_t) cols * 4 + 64 * 4 + (size_t) cols * 128 * 4 + (size_t) cols * 4;
     d = hx_malloc(bytes);
     float * wp = d, * mins = wp + nw, * steps = mins + ng, * es = steps + ng, * em = es + ng, * key = em + ng,
-          * dfacs = key + cols;
+          * dfacs = key + cols, * part = dfacs + 64;
+    int32_t * cnt = (int32_t *) (part + (size_t) cols * 128);
     HX(hipEventCreate(&e0));
     HX(hipEventCreate(&e1));
     HX(hipMemcpy(dfacs, facs, (size_t) nf * 4, hipMemcpyHostToDevice));
@@ -223,10 +225,16 @@ int sml_hip_requant(const float * w, int rows, int cols, int nbits, const int32_
         HX(hipMemcpyAsync(perm, perm_in, (size_t) cols * 4, hipMemcpyDeviceToDevice, 0));
     }
     else {
-        sml_king_colmax c = { w, key, rows, cols };
-        hx_launch("sml_ing_colmax", blocks(cols), 1, 256, 0, 0, &c);
-        sml_king_rank k = { key, perm, cols };
-        hx_launch("sml_ing_rank", blocks(cols), 1, 256, 0, 0, &k);
+        const int chunk = rows > 64 * 128 ? (rows + 127) / 128 : 64, nchunk = (rows + chunk - 1) / chunk;
+        sml_king_colmax c = { w, part, rows, cols, chunk };
+        hx_launch("sml_ing_colmax", blocks(cols), (unsigned) nchunk, 256, 0, 0, &c);
+        sml_king_colfold cf = { part, key, cols, nchunk };
+        hx_launch("sml_ing_colfold", blocks(cols), 1, 256, 0, 0, &cf);
+        const int slice = 1024, nslice = (cols + slice - 1) / slice;
+        HX(hipMemsetAsync(cnt, 0, (size_t) cols * 4, 0));
+        sml_king_rank k = { key, cnt, perm, cols, slice };
+        hx_launch("sml_ing_rank", blocks(cols), (unsigned) nslice, 256, 0, 0, &k);
+        hx_launch("sml_ing_scatter", blocks(cols), 1, 256, 0, 0, &k);
     }
     sml_king_gather gth = { w, perm, wp, rows, cols };
     hx_launch("sml_ing_gather", blocks((int64_t) nw), 1, 256, 0, 0, &gth);

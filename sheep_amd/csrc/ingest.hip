@@ -54,36 +54,56 @@ __device__ __forceinline__ float np_max(float m, float x, bool first) {
     return x > m ? x : m;
 }
 
+// Column maxima in two passes: workgroups over (256 columns, a chunk of rows)
+// write partial maxima, then one thread per column folds them (max with NaN
+// winning does not depend on the order).
 extern "C" __global__ __launch_bounds__(256) void sml_ing_colmax(const sml_king_colmax a) {
     const int c = blockIdx.x * 256 + threadIdx.x;
     if (c >= a.cols) return;
+    const int r0 = blockIdx.y * a.chunk, r1 = min(a.rows, r0 + a.chunk);
     float m = 0.0f;
-    for (int r = 0; r < a.rows; r++) m = np_max(m, fabsf(a.w[(size_t) r * a.cols + c]), r == 0);
+    for (int r = r0; r < r1; r++) m = np_max(m, fabsf(a.w[(size_t) r * a.cols + c]), r == r0);
+    a.part[(size_t) blockIdx.y * a.cols + c] = m;
+}
+
+extern "C" __global__ __launch_bounds__(256) void sml_ing_colfold(const sml_king_colfold a) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= a.cols) return;
+    float m = 0.0f;
+    for (int y = 0; y < a.nchunk; y++) m = np_max(m, a.part[(size_t) y * a.cols + c], y == 0);
     a.key[c] = m;
 }
 
-// Rank of each key in the ascending order (NaN last, ties by column), so
-// perm[rank] = column: a stable argsort. The keys pass through LDS in tiles.
+// A stable argsort by counting: the rank of key[c] is the number of columns
+// before it in (NaN, key, column) order, counted over column slices by
+// workgroups (blockIdx.y) through LDS and added with integer atomics (the
+// total does not depend on their order); then perm[rank] = c.
 extern "C" __global__ __launch_bounds__(256) void sml_ing_rank(const sml_king_rank a) {
     __shared__ float tile[1024];
     const int c = blockIdx.x * 256 + threadIdx.x;
     const float kc = c < a.cols ? a.key[c] : 0.0f;
     const bool nc = isnan(kc);
+    const int j0 = blockIdx.y * a.slice, j1 = min(a.cols, j0 + a.slice);
     int rank = 0;
-    for (int t0 = 0; t0 < a.cols; t0 += 1024) {
+    for (int t0 = j0; t0 < j1; t0 += 1024) {
         __syncthreads();
-        for (int j = threadIdx.x; j < 1024; j += 256) tile[j] = t0 + j < a.cols ? a.key[t0 + j] : 0.0f;
+        for (int j = threadIdx.x; j < 1024; j += 256) tile[j] = t0 + j < j1 ? a.key[t0 + j] : 0.0f;
         __syncthreads();
-        const int tn = a.cols - t0 < 1024 ? a.cols - t0 : 1024;
+        const int tn = j1 - t0 < 1024 ? j1 - t0 : 1024;
         for (int j = 0; j < tn; j++) {
             const float kj = tile[j];
             const bool nj = isnan(kj);
-            // (NaN, key, column) in lexicographic order, NaN keys after every number
+            // NaN keys after every number
             const bool before = nc ? (!nj || t0 + j < c) : (!nj && (kj < kc || (kj == kc && t0 + j < c)));
             rank += before;
         }
     }
-    if (c < a.cols) a.perm[rank] = c;
+    if (c < a.cols && rank) atomicAdd(a.cnt + c, rank);
+}
+
+extern "C" __global__ __launch_bounds__(256) void sml_ing_scatter(const sml_king_rank a) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c < a.cols) a.perm[a.cnt[c]] = c;
 }
 
 extern "C" __global__ __launch_bounds__(256) void sml_ing_gather(const sml_king_gather a) {
@@ -94,11 +114,12 @@ extern "C" __global__ __launch_bounds__(256) void sml_ing_gather(const sml_king_
 }
 
 // ---------------------------------------------------------------- the asymmetric grid
-// Weighted error of one candidate (l, step) over the group: codes into q.
-// follows sml/sml-quant.c:20-33 as the grid's vectorized loop computes it:
-// d = fma(qv, step, l) - g, then e = e + (d*d)*w in order.
-template <int G>
-__device__ __forceinline__ float err32(const float (&g)[G], const float (&w)[G], float l, float step, float n, int rem,
+// Weighted error of one candidate (l, step) over the group, and (STORE) its
+// codes into q. follows sml/sml-quant.c:20-33 as the grid's vectorized loop
+// computes it: d = fma(qv, step, l) - g, then e = e + (d*d)*w in order. WT
+// false: every weight is 1 (the product by 1 is exact, so it is left out).
+template <int G, bool WT, bool STORE>
+__device__ __forceinline__ float err32(const float (&g)[G], const float * w, float l, float step, float n, int rem,
                                        float (&q)[G]) {
     float e = 0.0f;
     #pragma unroll
@@ -106,35 +127,37 @@ __device__ __forceinline__ float err32(const float (&g)[G], const float (&w)[G],
         float c = __builtin_rintf((g[i] - l) / step);
         if (c < 0.0f) c = 0.0f;
         if (c > n) c = n;
-        q[i] = c;
+        if constexpr (STORE) q[i] = c;
         const float qv = rem ? (float) ((((int) c >> rem) << rem) + (1 << (rem - 1))) : c;
         const float d = __builtin_fmaf(qv, step, l) - g[i];
-        e = e + (d * d) * w[i];
+        e = WT ? e + (d * d) * w[i] : e + d * d;
     }
     return e;
 }
 
-// One lane per group of 32, the weights and codes in registers.
+// One lane per group of 32, the weights and the current codes in registers.
+// A refit's candidate codes are not kept: when it wins they are derived again
+// from its (min, step) -- the same function, so the same codes -- which
+// keeps the lane under 128 registers.
 // follows sml/sml-quant.c:38-95 (sml_asym_grid)
-extern "C" __global__ __launch_bounds__(256) void sml_ing_grid32(const sml_king_grid a) {
+template <bool WT>
+__device__ __forceinline__ void grid32_body(const sml_king_grid & a) {
     constexpr int G = 32;
     const int ng = a.cols / G;
     const int64_t t = (int64_t) blockIdx.x * 256 + threadIdx.x;
     if (t >= (int64_t) a.rows * ng) return;
     const int j = (int) (t % ng);
     const float * gp = a.wp + (size_t) t * G;        // row r, group j: (r*ng + j)*32
-    float g[G], w[G], q[G], q2[G];
+    float g[G], q[G];
+    float w[WT ? G : 1];
     #pragma unroll
     for (int i = 0; i < G; i += 4) {
         const float4 v = *(const float4 *) (gp + i);
         g[i] = v.x; g[i + 1] = v.y; g[i + 2] = v.z; g[i + 3] = v.w;
     }
-    if (a.wt) {
+    if constexpr (WT) {
         #pragma unroll
         for (int i = 0; i < G; i++) w[i] = a.wt[(size_t) j * G + i];
-    } else {
-        #pragma unroll
-        for (int i = 0; i < G; i++) w[i] = 1.0f;
     }
     const float n = (float) ((1 << a.nbits) - 1);
     float lo = g[0], hi = g[0], ws = 0.0f;
@@ -142,7 +165,7 @@ extern "C" __global__ __launch_bounds__(256) void sml_ing_grid32(const sml_king_
     for (int i = 0; i < G; i++) {
         if (g[i] < lo) lo = g[i];
         if (g[i] > hi) hi = g[i];
-        ws = ws + w[i];
+        ws = ws + (WT ? w[i] : 1.0f);
     }
     const float c = (lo + hi) * 0.5f;
     float bl = 0.0f, bs = 0.0f, be = 0.0f;
@@ -150,29 +173,32 @@ extern "C" __global__ __launch_bounds__(256) void sml_ing_grid32(const sml_king_
         const float half = (hi - lo) * 0.5f * a.facs[k];
         float l = c - half;
         float step = fmaxf(2.0f * half, 1e-12f) / n;
-        float e = err32<G>(g, w, l, step, n, a.rem, q);
+        float e = err32<G, WT, true>(g, w, l, step, n, a.rem, q);
         if (a.refit) {
             for (int it = 0; it < a.iters; it++) {
                 float qm = 0.0f, gm = 0.0f;
                 #pragma unroll
-                for (int i = 0; i < G; i++) { qm = qm + w[i] * q[i]; gm = gm + w[i] * g[i]; }
+                for (int i = 0; i < G; i++) {
+                    qm = qm + (WT ? w[i] * q[i] : q[i]);
+                    gm = gm + (WT ? w[i] * g[i] : g[i]);
+                }
                 qm = qm / ws;
                 gm = gm / ws;
                 float var = 0.0f, cov = 0.0f;
                 #pragma unroll
                 for (int i = 0; i < G; i++) {
                     const float dq = q[i] - qm;
-                    var = var + (w[i] * dq) * dq;
-                    cov = cov + (w[i] * dq) * (g[i] - gm);
+                    const float wdq = WT ? w[i] * dq : dq;
+                    var = var + wdq * dq;
+                    cov = cov + wdq * (g[i] - gm);
                 }
                 float s2 = var > 1e-12f ? cov / fmaxf(var, 1e-12f) : step;
                 s2 = fmaxf(s2, 1e-12f);
                 const float l2 = __builtin_fmaf(-s2, qm, gm);
-                const float e2 = err32<G>(g, w, l2, s2, n, a.rem, q2);
+                const float e2 = err32<G, WT, false>(g, w, l2, s2, n, a.rem, q);
                 if (e2 < e) {
                     l = l2; step = s2; e = e2;
-                    #pragma unroll
-                    for (int i = 0; i < G; i++) q[i] = q2[i];
+                    err32<G, WT, true>(g, w, l, step, n, a.rem, q);
                 }
             }
         }
@@ -181,6 +207,9 @@ extern "C" __global__ __launch_bounds__(256) void sml_ing_grid32(const sml_king_
     a.out_l[t] = bl;
     a.out_s[t] = bs;
 }
+
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) void sml_ing_grid32(const sml_king_grid a) { grid32_body<false>(a); }
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void sml_ing_grid32w(const sml_king_grid a) { grid32_body<true>(a); }
 
 // Any group that is a multiple of 8 up to 256 (gcc's 8-wide loop covers the
 // whole group, so the order is the one above), read from memory; the codes

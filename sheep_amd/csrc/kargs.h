@@ -314,11 +314,14 @@ typedef struct {
     int rows, cols, bits, group, zero_add, awq;
 } sml_king_dequant;
 
-// key[c] = max over rows of |w[r][c]| (NaN wins)
-typedef struct { const float * w; float * key; int rows, cols; } sml_king_colmax;
+// part[y][c] = max over rows [y*chunk, (y+1)*chunk) of |w[r][c]| (NaN wins);
+// then key[c] = the max over y of part[y][c]
+typedef struct { const float * w; float * part; int rows, cols, chunk; } sml_king_colmax;
+typedef struct { const float * part; float * key; int cols, nchunk; } sml_king_colfold;
 
-// perm[rank of key[c]] = c: ascending key, NaN last, ties by column
-typedef struct { const float * key; int32_t * perm; int cols; } sml_king_rank;
+// cnt[c] += the keys before key[c] among columns [y*slice, (y+1)*slice)
+// (ascending key, NaN last, ties by column); then perm[cnt[c]] = c
+typedef struct { const float * key; int32_t * cnt; int32_t * perm; int cols, slice; } sml_king_rank;
 
 // wp[r][i] = w[r][perm[i]]
 typedef struct { const float * w; const int32_t * perm; float * wp; int rows, cols; } sml_king_gather;
