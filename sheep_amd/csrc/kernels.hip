@@ -2274,7 +2274,7 @@ extern "C" __global__ __launch_bounds__(256) void sml_moe_combine(const sml_kmoe
 // (s, s*sum) pairs in LDS. Group e of the grid's y dimension uses matrix
 // table entry e (an expert) and its own activation slots.
 #define GEMM_NI 2
-template <int NB, int RB, int MT, bool SW>
+template <int NB, int RB, int MT, bool SW, int WG = 256>
 __device__ void gemm_body(const sml_kgemm & a) {
     constexpr int NI = GEMM_NI, TILE = WAVE * NI;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -2287,7 +2287,7 @@ __device__ void gemm_body(const sml_kgemm & a) {
     const int tid = threadIdx.x, lane = tid & (WAVE - 1);
     constexpr int RPW = SW ? RB / 2 : RB;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int row0 = (blockIdx.x * 4 + wave) * RPW;
+    const int row0 = (blockIdx.x * (WG / 64) + wave) * RPW;
     const sml_kmat * mt = a.mats + (size_t) e * (SW ? 2 : 1);
     const size_t abase = (size_t) e * a.mmax;
     using P = Planes<NB>;
@@ -2338,11 +2338,11 @@ __device__ void gemm_body(const sml_kgemm & a) {
         // this pass's slice of every activation row into LDS
         const int tg = ng - c0 < TILE ? ng - c0 : TILE;  // groups in the slice
         __syncthreads();                                 // the previous pass's reads are done
-        for (int idx = tid; idx < m * tg * 2; idx += 256) {
+        for (int idx = tid; idx < m * tg * 2; idx += WG) {
             const int t = idx / (tg * 2), wd = idx % (tg * 2);
             ((v4i *) (lq + t * TILE * 32))[wd] = ((const v4i *) (a.q + (abase + t) * n + (size_t) c0 * 32))[wd];
         }
-        for (int idx = tid; idx < m * tg; idx += 256) {
+        for (int idx = tid; idx < m * tg; idx += WG) {
             const int t = idx / tg, g = idx % tg;
             const size_t fi = (abase + t) * ng + c0 + g;
             const float sv = a.scale[fi];
@@ -2424,6 +2424,17 @@ __device__ void gemm_body(const sml_kgemm & a) {
     }
 #define GEMM_WIDTH(NB) GEMM_KERNEL(NB, 1) GEMM_KERNEL(NB, 4) GEMM_KERNEL(NB, 8) GEMM_KERNEL(NB, 16)
 GEMM_WIDTH(2) GEMM_WIDTH(3) GEMM_WIDTH(4) GEMM_WIDTH(5) GEMM_WIDTH(6) GEMM_WIDTH(7) GEMM_WIDTH(8)
+// Wider workgroups (suffix _w<threads>): the same rows per wave, more waves
+// sharing one staging of the activation rows per pass
+#define GEMM_KERNEL_W(NB, MT, W)                                                                         \
+    extern "C" __global__ __launch_bounds__(W) void sml_gemm_q##NB##_m##MT##_w##W(const sml_kgemm a) {    \
+        gemm_body<NB, 2, MT, false, W>(a);                                                               \
+    }                                                                                                    \
+    extern "C" __global__ __launch_bounds__(W) void sml_gemm_q##NB##_s_m##MT##_w##W(const sml_kgemm a) {  \
+        gemm_body<NB, 4, MT, true, W>(a);                                                                \
+    }
+GEMM_KERNEL_W(4, 4, 512) GEMM_KERNEL_W(4, 8, 512) GEMM_KERNEL_W(4, 16, 512)
+GEMM_KERNEL_W(4, 4, 1024) GEMM_KERNEL_W(4, 8, 1024) GEMM_KERNEL_W(4, 16, 1024)
 
 // ---------------------------------------------------------------- small-M GEMM on MFMA (Q4)
 //

@@ -1174,13 +1174,22 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
     // for three classes (SML_GEMM_SPLIT = 1, 0, 2), the smaller launches
     // running one after another.
     const int split = count && mt > 4 ? env_int("SML_GEMM_SPLIT", 1) : 0;
+    // expert groups (a few rows each) on 512-thread workgroups: twice the
+    // rows share each staging of the activation rows (16-token Mixtral-shaped
+    // layer 275.6 -> 266.0 us per-256, 301.0 -> 290.6 per-32; 1024 threads:
+    // 316.5 / 333.3). SML_GEMM_WG = 256, 512 or 1024 overrides (Q4).
+    int wg = env_int("SML_GEMM_WG", count ? 512 : 256);
+    if ((wg != 512 && wg != 1024) || nbits != 4) wg = 256;
     int lo = 0;
     for (int m_t = split >= 2 ? 4 : split == 1 ? 8 : mt; ; m_t *= 2) {
         if (m_t > mt) m_t = mt;
         a.mlo = lo;
-        snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d", nbits, swiglu ? "_s" : "", m_t);
+        const int w = m_t == 1 ? 256 : wg;
+        if (w == 256) snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d", nbits, swiglu ? "_s" : "", m_t);
+        else snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d_w%d", nbits, swiglu ? "_s" : "", m_t, w);
         const size_t lds = (size_t) m_t * GEMM_TILE * (32 + 8);
-        hx_launch(name, (unsigned) ((rows + 7) / 8), (unsigned) ngroups, 256, lds, st, &a);
+        const int rpw = 8 * w / 256;                    // rows (SwiGLU: outputs) per workgroup
+        hx_launch(name, (unsigned) ((rows + rpw - 1) / rpw), (unsigned) ngroups, (unsigned) w, lds, st, &a);
         if (m_t >= mt) break;
         lo = m_t;
     }
