@@ -18,7 +18,22 @@ typedef struct {
     float          * y;
     int rows;
     int pad_;
+    // Q4: the small-M MFMA GEMM's copy of the codes and fields, one
+    // SML_TILE_Q4-byte tile per (16-row block, superblock) holding what the
+    // kernel's 64 lanes load for it in lane order (sml_tile_q4), or NULL
+    const uint8_t  * tiled;
 } sml_kmat;
+
+#define SML_TILE_Q4 2368          // 2048 code bytes, 16 x 16 (sq, mq) bytes, 16 x 4 (sd, md) bytes
+
+// Build the tiled copy of a Q4 matrix: one workgroup per tile.
+typedef struct {
+    const uint8_t  * plane;
+    const uint8_t  * sqmq;
+    const uint16_t * sdmd;
+    uint8_t * out;
+    int rows, cols;
+} sml_ktile;
 
 enum { SML_EPI_STORE = 0, SML_EPI_RESIDUAL = 1, SML_EPI_SWIGLU = 2 };
 

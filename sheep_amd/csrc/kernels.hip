@@ -2483,6 +2483,36 @@ GEMM_KERNEL_W(4, 4, 1024) GEMM_KERNEL_W(4, 8, 1024) GEMM_KERNEL_W(4, 16, 1024)
 // dwords 2-3 and keeps its own 2-3. x and y are then the lane's 8-byte slice
 // of two different groups (see mgemm_q4_body). The two operands of each swap
 // are distinct registers.
+// The tiled copy of a Q4 matrix (sml_kmat.tiled): per 16-row block R and
+// superblock b, SML_TILE_Q4 bytes holding exactly what mgemm_q4_body's 64
+// lanes load for that block and superblock, in lane order: the codes of its
+// two quads as [half p][lane][16 bytes] (lane l = 16c + i: row 16R + i,
+// bytes 16c..16c+15 of quad p of the superblock), then each row's 8 (sq, mq)
+// pairs, then each row's (sd, md). A wave's code load is then 1 KB of
+// contiguous bytes, as the GEMV's is, instead of 16 rows x 64 bytes. Rows
+// past the end are zero (their outputs are never stored).
+extern "C" __global__ __launch_bounds__(256) void sml_tile_q4(const sml_ktile a) {
+    const int nsb = a.cols / 256, ng = a.cols / 32;
+    const int t = blockIdx.x, R = t / nsb, b = t % nsb, u = threadIdx.x;
+    uint8_t * dst = a.out + (size_t) t * SML_TILE_Q4;
+    if (u < 128) {
+        const int p = u >> 6, lane = u & 63, c = lane >> 4, row = R * 16 + (lane & 15);
+        v4u v = {0u, 0u, 0u, 0u};
+        if (row < a.rows) v = *(const v4u *) (a.plane + (size_t) row * (a.cols / 2) + (size_t) b * 128 + 16 * c + 64 * p);
+        *(v4u *) (dst + p * 1024 + lane * 16) = v;
+    } else if (u < 144) {
+        const int i = u - 128, row = R * 16 + i;
+        v4u v = {0u, 0u, 0u, 0u};
+        if (row < a.rows) v = *(const v4u *) (a.sqmq + ((size_t) row * ng + (size_t) b * 8) * 2);
+        *(v4u *) (dst + 2048 + i * 16) = v;
+    } else if (u < 160) {
+        const int i = u - 144, row = R * 16 + i;
+        uint32_t v = 0u;
+        if (row < a.rows) v = *(const uint32_t *) (a.sdmd + ((size_t) row * nsb + b) * 2);
+        *(uint32_t *) (dst + 2304 + i * 4) = v;
+    }
+}
+
 __device__ __forceinline__ void xslice(const v4u v, v2u & x, v2u & y) {
     const auto p = __builtin_amdgcn_permlane32_swap((int) v[0], (int) v[2], false, false);
     const auto q = __builtin_amdgcn_permlane32_swap((int) v[1], (int) v[3], false, false);
@@ -2490,7 +2520,7 @@ __device__ __forceinline__ void xslice(const v4u v, v2u & x, v2u & y) {
     y = v2u{(unsigned) p[1], (unsigned) q[1]};
 }
 
-template <bool SW, bool SB, int RB, int NW, bool PS = false>
+template <bool SW, bool SB, int RB, int NW, bool PS = false, bool TL = false>
 __device__ void mgemm_q4_body(const sml_kgemm & a) {
     typedef long v1l;
     constexpr int NM = SW ? 2 : 1, NACC = NM * RB * 4;
@@ -2524,6 +2554,10 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
     for (int k = 0; k < NM; k++) { plane[k] = mt[k].plane[0]; fqb[k] = mt[k].sqmq; fdb[k] = (const uint8_t *) mt[k].sdmd; }
     const uint32_t rowb = (uint32_t) n / 2;
     uint32_t boff0[RB], fqo[RB], fdo[RB];
+    // TL: the matrices' tiled copies (sml_tile_q4): the block's tile row; the
+    // loads then read each tile's bytes in lane order
+    const int nbl = (a.rows + 15) / 16;
+    const uint8_t * tb[NM][RB];
     auto set_tile = [&](int r0) {
         #pragma unroll
         for (int bk = 0; bk < RB; bk++) {
@@ -2532,6 +2566,11 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             boff0[bk] = rc * rowb + 16u * (uint32_t) c;
             fqo[bk] = rc * (uint32_t) ng * 2u;
             fdo[bk] = rc * (uint32_t) nsb * 4u;
+            if constexpr (TL) {
+                const int blk = min(r0 / 16 + bk, nbl - 1);
+                #pragma unroll
+                for (int k = 0; k < NM; k++) tb[k][bk] = mt[k].tiled + (size_t) blk * nsb * SML_TILE_Q4;
+            }
         }
     };
     set_tile(rb0);
@@ -2549,6 +2588,16 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
         for (int k = 0; k < NM; k++)
             #pragma unroll
             for (int bk = 0; bk < RB; bk++) {
+                if constexpr (TL) {
+                    const uint8_t * tp = tb[k][bk] + (size_t) bt * SML_TILE_Q4;
+                    #pragma unroll
+                    for (int p = 0; p < 2; p++) b.w[p][k][bk] = *(const v4u *) (tp + p * 1024 + lane * 16);
+                    if (c == 0) {
+                        b.fq[k][bk] = *(const v4u *) (tp + 2048 + i16 * 16);
+                        b.fd[k][bk] = *(const uint32_t *) (tp + 2304 + i16 * 4);
+                    }
+                    continue;
+                }
                 const uint8_t * wp = plane[k] + (boff0[bk] + (uint32_t) g0 * 16u);
                 #pragma unroll
                 for (int p = 0; p < 2; p++) b.w[p][k][bk] = *(const v4u *) (wp + p * 64);
@@ -2798,32 +2847,31 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
     }
 }
 
-#define MGEMM_KERNEL(RB, NW)                                                                                   \
-    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_r##RB##_w##NW(const sml_kgemm a) {       \
-        mgemm_q4_body<false, false, RB, NW>(a); }                                                              \
-    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_r##RB##_w##NW(const sml_kgemm a) {     \
-        mgemm_q4_body<true, false, RB, NW>(a); }                                                               \
-    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_sb_r##RB##_w##NW(const sml_kgemm a) {    \
-        mgemm_q4_body<false, true, RB, NW>(a); }                                                               \
-    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_sb_r##RB##_w##NW(const sml_kgemm a) {  \
-        mgemm_q4_body<true, true, RB, NW>(a); }
-MGEMM_KERNEL(1, 4)
-MGEMM_KERNEL(2, 4)
-MGEMM_KERNEL(1, 8)
-MGEMM_KERNEL(2, 8)
+#define MGEMM_KERNEL(RB, NW, TL, SUF)                                                                          \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_r##RB##_w##NW##SUF(const sml_kgemm a) {  \
+        mgemm_q4_body<false, false, RB, NW, false, TL>(a); }                                                   \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_r##RB##_w##NW##SUF(const sml_kgemm a) { \
+        mgemm_q4_body<true, false, RB, NW, false, TL>(a); }                                                    \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_sb_r##RB##_w##NW##SUF(const sml_kgemm a) { \
+        mgemm_q4_body<false, true, RB, NW, false, TL>(a); }                                                    \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_sb_r##RB##_w##NW##SUF(const sml_kgemm a) { \
+        mgemm_q4_body<true, true, RB, NW, false, TL>(a); }
+// suffix _t: the matrices' tiled copies (sml_kmat.tiled)
+MGEMM_KERNEL(1, 4, false, ) MGEMM_KERNEL(2, 4, false, ) MGEMM_KERNEL(1, 8, false, ) MGEMM_KERNEL(2, 8, false, )
+MGEMM_KERNEL(1, 4, true, _t) MGEMM_KERNEL(2, 4, true, _t) MGEMM_KERNEL(1, 8, true, _t) MGEMM_KERNEL(2, 8, true, _t)
 // Persistent forms (_p): a grid smaller than the tile count, each workgroup
 // keeping its activation operands for every tile it takes (input widths of
 // at most 2 superblocks per wave)
-#define MGEMM_KERNEL_P(RB, NW)                                                                                 \
-    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_r##RB##_w##NW##_p(const sml_kgemm a) {  \
-        mgemm_q4_body<false, false, RB, NW, true>(a); }                                                        \
-    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_r##RB##_w##NW##_p(const sml_kgemm a) { \
-        mgemm_q4_body<true, false, RB, NW, true>(a); }                                                         \
-    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_sb_r##RB##_w##NW##_p(const sml_kgemm a) { \
-        mgemm_q4_body<false, true, RB, NW, true>(a); }                                                         \
-    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_sb_r##RB##_w##NW##_p(const sml_kgemm a) { \
-        mgemm_q4_body<true, true, RB, NW, true>(a); }
-MGEMM_KERNEL_P(1, 8)
+#define MGEMM_KERNEL_P(RB, NW, TL, SUF)                                                                        \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_r##RB##_w##NW##_p##SUF(const sml_kgemm a) {  \
+        mgemm_q4_body<false, false, RB, NW, true, TL>(a); }                                                    \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_r##RB##_w##NW##_p##SUF(const sml_kgemm a) { \
+        mgemm_q4_body<true, false, RB, NW, true, TL>(a); }                                                     \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_sb_r##RB##_w##NW##_p##SUF(const sml_kgemm a) { \
+        mgemm_q4_body<false, true, RB, NW, true, TL>(a); }                                                     \
+    extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_sb_r##RB##_w##NW##_p##SUF(const sml_kgemm a) { \
+        mgemm_q4_body<true, true, RB, NW, true, TL>(a); }
+MGEMM_KERNEL_P(1, 8, false, ) MGEMM_KERNEL_P(1, 8, true, _t)
 
 
 

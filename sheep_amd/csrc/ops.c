@@ -55,6 +55,17 @@ static uint32_t field6(const uint8_t * row, size_t g) {
     }
 }
 
+// Whether Q4 uploads carry the small-M MFMA GEMM's tiled copy (SML_TILED=1;
+// off by default): read once per process, so every matrix of a run agrees.
+// It doubles the codes and fields a Q4 matrix holds in HBM for 7-11% on the
+// 16-row products at 4096 and 14336 columns (per-256 SwiGLU 26.6 -> 24.8 us,
+// 4096 x 14336 19.4 -> 17.3; per-32 SwiGLU 29.1 -> 29.7).
+static int tiled_on(void) {
+    static int on = -1;
+    if (on < 0) { const char * e = getenv("SML_TILED"); on = e ? atoi(e) != 0 : 0; }
+    return on;
+}
+
 sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, const uint8_t * sq,
                          const uint16_t * md, const uint8_t * mq, int rows, int cols, int nbits,
                          int scale6, int minneg) {
@@ -95,6 +106,7 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
         hx.jb = outer;
         free(fq); free(fd);
         if (m->mem) hipFree(m->mem);
+        if (m->tiled_mem) hipFree(m->tiled_mem);
         free(m);
         longjmp(*outer, 1);
     }
@@ -116,6 +128,17 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
     m->nbits = nbits;
     m->cols = cols;
     m->kdev = (sml_kmat *) (base + off[5]);
+    // Q4 with SML_TILED=1: the tiled copy the small-M MFMA GEMM streams (one
+    // more copy of the codes and fields; without it the GEMM reads the rows
+    // as they are)
+    if (nbits == 4 && cols % 256 == 0 && tiled_on()) {
+        const size_t nt = (size_t) ((rows + 15) / 16) * (size_t) (cols / 256);
+        m->tiled_mem = hx_malloc(nt * SML_TILE_Q4);
+        sml_ktile t = { m->k.plane[0], m->k.sqmq, m->k.sdmd, (uint8_t *) m->tiled_mem, rows, cols };
+        hx_launch("sml_tile_q4", (unsigned) nt, 1, 256, 0, 0, &t);
+        HX(hipDeviceSynchronize());
+        m->k.tiled = (const uint8_t *) m->tiled_mem;
+    }
     HX(hipMemcpy(m->kdev, &m->k, sizeof m->k, hipMemcpyHostToDevice));
     // the bytes a GEMV streams: the file's planes and fields at 8 bits
     m->bytes = sz[0] + sz[1] + sz[2] + R * ng * (mq ? 2 : 1) + R * ns * (md ? 4 : 2);
@@ -328,6 +351,7 @@ sml_hip_mat * sml_hip_mat_from_file(const char * path, const char * name) {
 void mat_free(sml_hip_mat * m) {
     if (!m) return;
     if (m->mem) HX(hipFree(m->mem));
+    if (m->tiled_mem) HX(hipFree(m->tiled_mem));
     free(m);
 }
 
@@ -1159,8 +1183,8 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
                 const int per = (ntile + cap - 1) / cap;
                 grid = (unsigned) ((ntile + per - 1) / per);
             }
-            snprintf(name, sizeof name, "sml_mgemm_q4%s%s_r%d_w%d%s", swiglu ? "_s" : "", per256 ? "_sb" : "", rb, nw,
-                     ps ? "_p" : "");
+            snprintf(name, sizeof name, "sml_mgemm_q4%s%s_r%d_w%d%s%s", swiglu ? "_s" : "", per256 ? "_sb" : "", rb, nw,
+                     ps ? "_p" : "", tiled_on() ? "_t" : "");
             hx_launch(name, grid, (unsigned) ngroups, (unsigned) (64 * nw), lds, st, &a);
             return;
         }

@@ -13,6 +13,7 @@ struct sml_hip_mat {
     int pair_set;
     int nbits, cols;
     void * mem;          // the single allocation holding planes and fields
+    void * tiled_mem;    // Q4: the MFMA GEMM's tiled copy (k.tiled), or NULL
     size_t bytes;        // planes + fields bytes (what one GEMV streams)
 };
 

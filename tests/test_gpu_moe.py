@@ -339,3 +339,47 @@ def test_moe_refuses_dense_layer(tmpdir_s):
     sa.synth_model(p, n_layer=1, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=256, seed=3)
     with pytest.raises(sa.HipError, match="no experts"):
         sa.MoE(p, 0, 4)
+
+
+def test_tiled_copy_gives_the_same_bits(tmpdir_s):
+    # SML_TILED=1 (read once per process): the MFMA GEMM reads each Q4
+    # matrix's tiled copy, byte for byte what it loads from the rows, so its
+    # outputs equal the untiled run's bit for bit (per-32 and per-256, plain
+    # and SwiGLU, persistent and not)
+    import subprocess
+    import sys as _sys
+    code = r'''
+import sys, numpy as np
+sys.path.insert(0, sys.argv[1])
+import sheep_amd as sa
+p = sys.argv[2]
+rng = np.random.default_rng(77)
+out = {}
+for rows, cols in ((4096, 4096), (8192, 14336)):
+    sa.synth_matrix(p, rows, cols, nbits=4, seed=rows + cols)
+    g, u = sa.Mat.from_file(p, "w"), sa.Mat.from_file(p, "w")
+    M = 13
+    q = sa.DevBuf.of(rng.integers(-127, 128, M * cols).astype(np.int8))
+    s32 = (np.abs(rng.standard_normal(M * cols // 32)) * 0.01).astype(np.float32)
+    s = sa.DevBuf.of(s32)
+    s256 = sa.DevBuf.of(np.repeat(s32.reshape(-1, 8)[:, :1], 8, axis=1).reshape(-1))
+    uu = sa.DevBuf.of(rng.integers(-2000, 2000, M * cols // 32).astype(np.int32))
+    y = sa.DevBuf(M * rows * 4)
+    for sb, sc in ((False, s), (True, s256)):
+        sa.gemm(g, q, sc, uu, M, y, per256=sb)
+        out[f"{rows}_{sb}_plain"] = y.read(np.float32)
+        sa.gemm_swiglu(g, u, q, sc, uu, M, y, per256=sb)
+        out[f"{rows}_{sb}_swiglu"] = y.read(np.float32)
+np.savez(sys.argv[3], **out)
+'''
+    import os
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = {}
+    for t in ("0", "1"):
+        f = str(tmpdir_s / f"tiled_{t}.npz")
+        r = subprocess.run([_sys.executable, "-c", code, root, str(tmpdir_s / f"tm_{t}.ssf"), f],
+                           env=dict(os.environ, SML_TILED=t), capture_output=True, text=True, timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        res[t] = np.load(f)
+    for k in res["0"].files:
+        assert np.array_equal(res["0"][k], res["1"][k]), k
