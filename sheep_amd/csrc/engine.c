@@ -812,11 +812,14 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
         op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
         op_gemm(G.st, y->qkv->kdev, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
                 G.mqkv, y->bias_qkv, NULL, regime);
-        const int fuse_q = y->perm_o < 0 && !sb;         // the merge quantizes per 32
+        // the merge quantizes its output for the o product: per 32, or per
+        // 256 in decode steps of an even head count (SML_MERGE_Q256=0 leaves
+        // that to its own launch)
+        const int fuse_q = y->perm_o < 0 && (!sb || (!causal && G.H % 2 == 0 && env_int("SML_MERGE_Q256", 1)));
         op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
                            G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.mpart, G.matt,
                            fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL,
-                           causal ? (regime == GEMM_EXACT ? 1 : 2) : 0, gemm_exact(regime, ns));
+                           causal ? (regime == GEMM_EXACT ? 1 : 2) : 0, gemm_exact(regime, ns), sb);
         if (!fuse_q) {
             pp[0] = pdev(y->perm_o);
             op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, sb);

@@ -1068,8 +1068,9 @@ __device__ __forceinline__ void st_dev2(float2 * p, float2 v) {
     __hip_atomic_store((unsigned long long *) p, __builtin_bit_cast(unsigned long long, v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
+// The merged output of dim d of head h of entry b, also stored to a.out.
 template <bool DEV>
-__device__ __forceinline__ void merge_head(const sml_kattn & a, int b, int h, int d) {
+__device__ __forceinline__ float merge_value(const sml_kattn & a, int b, int h, int d) {
     const int lane = d & 63;
     const float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
     const float * po = blk + (size_t) h * a.nsplit * HD;
@@ -1098,7 +1099,13 @@ __device__ __forceinline__ void merge_head(const sml_kattn & a, int b, int h, in
     }
     const float r = o / L;
     a.out[ob + (size_t) h * HD + d] = r;
+    return r;
+}
+template <bool DEV>
+__device__ __forceinline__ void merge_head(const sml_kattn & a, int b, int h, int d) {
+    const float r = merge_value<DEV>(a, b, h, d);
     if (!a.q_out) return;
+    const size_t ob = (size_t) b * a.n_head * HD;
     const float amax = max32(fabsf(r));
     const float s = amax / 127.0f;
     const float is = s > 0.0f ? 1.0f / s : 0.0f;
@@ -1734,6 +1741,30 @@ ATTNF_KERNEL(1) ATTNF_KERNEL(2) ATTNF_KERNEL(3) ATTNF_KERNEL(4) ATTNF_KERNEL(5) 
 // the sequence).
 extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn a) {
     merge_head<false>(a, blockIdx.z, blockIdx.x, threadIdx.x);
+}
+
+// The merge with its output quantized per 256 values (the rule of
+// sml_normq2's per256 form, sml/sml-kernel.c:165-172): two heads of HD = 128
+// make one superblock, a workgroup of 256 threads per head pair (grid:
+// n_head / 2, z: the sequence); wave w holds dims (w & 1) * 64.. of head
+// 2 * blockIdx.x + (w >> 1), as sml_normq2's wave w holds values 64 w.. of
+// its superblock, so the maxima, codes and sums are that kernel's bit for bit.
+extern "C" __global__ __launch_bounds__(256) void sml_attn_merge_sb(const sml_kattn a) {
+    __shared__ float wm[4];
+    const int tid = threadIdx.x, wave = tid >> 6, b = blockIdx.z;
+    const int h = blockIdx.x * 2 + (wave >> 1), d = (wave & 1) * 64 + (tid & 63);
+    const float r = merge_value<false>(a, b, h, d);
+    const float m = wave_max(fabsf(r));
+    if ((tid & 63) == 0) wm[wave] = m;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    const float s = amax / 127.0f;
+    const float is = s > 0.0f ? 1.0f / s : 0.0f;
+    const int t = quant1(r, is);
+    const int sum = isum32(t);
+    const size_t ob = (size_t) b * a.n_head * HD, j = (size_t) blockIdx.x * 256 + tid;
+    a.q_out[ob + j] = (int8_t) t;
+    if ((tid & 31) == 0) { a.s_out[(ob + j) / 32] = s; a.u_out[(ob + j) / 32] = sum; }
 }
 
 // ---------------------------------------------------------------- attention in the reference's order

@@ -700,9 +700,11 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
                         float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal,
-                        int exact) {
+                        int exact, int q256) {
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
+    if (q_out && q256 && (causal || n_head % 2))
+        hx_failf("the merge quantizes per 256 only decode steps of an even head count (%d heads)", n_head);
     if (nseq < 1 || nseq > 65535) hx_failf("attention batch of %d", nseq);
     const int aw = env_int("SML_ATTN_WAVES", nseq >= 4 && !exact ? 4 : 8) == 4 ? 4 : 8;
     // the 8-wave kernels split as decoding does (attn_split); the 4-wave and
@@ -769,7 +771,8 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     else snprintf(name, sizeof name, "sml_attn8_s%d_r%d", ch, n_head / n_kv);
     hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) ((nseq + a.tpw - 1) / a.tpw), (unsigned) nt, 0,
                st, &a);
-    hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
+    if (q_out && q256) hx_launch3("sml_attn_merge_sb", (unsigned) n_head / 2, 1, (unsigned) nseq, 256, 0, st, &a);
+    else hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
 }
 
 int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,

@@ -90,12 +90,13 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
 // (prompt reading), so every k and v is rotated and written by one launch
 // before any entry attends; 1 keeps the decode kernel's arithmetic per entry
 // (bit-exact with stepping), 2 runs the wave-per-position kernel (faster,
-// its own fp32 order).
+// its own fp32 order). The quantized out is per 32 values, or per 256 when
+// q256 (decode steps, causal 0, of an even head count only).
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
                         float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal,
-                        int exact);
+                        int exact, int q256);
 // Whether op_gemm computes every row with the GEMV's arithmetic in this regime
 // for m_all rows (the exact regime, or per-32 rows the VALU kernel takes).
 int gemm_exact(int regime, int m_all);

@@ -231,3 +231,24 @@ def test_step_multi_rejects_bad_arguments(tmp_path):
         assert f(I(1, 2), I(0, 0), I(0, 1), 2, out.ctypes.data) == 2
     finally:
         d.close()
+
+
+@pytest.mark.parametrize("kind", ["dense", "moe"])
+def test_step_multi_per256_merge_quantizes_as_its_own_launch(tmp_path, kind, monkeypatch):
+    """In the per-256 regime the attention merge quantizes its output per 256
+    values (two heads a superblock) for the o product; with
+    SML_MERGE_Q256=0 the same quantization runs as its own launch over the
+    merged output. Every step's logits are equal bit for bit."""
+    monkeypatch.delenv("SML_MULTI", raising=False)
+    monkeypatch.delenv("SML_MULTI_EXACT_MAX", raising=False)
+    p = tmp_path / f"merge_{kind}.ssf"
+    extra = dict(n_expert=8, n_expert_used=2, moe_flags=1) if kind == "moe" else {}
+    sa.synth_model(p, n_layer=2, n_embd=1024, n_head=8, n_head_kv=2, n_ff=2048, n_vocab=2000, qkv_bias=True,
+                   seed=76, **extra)
+    outs = {}
+    for fused in ("0", "1"):
+        monkeypatch.setenv("SML_MERGE_Q256", fused)
+        print(f"per-256 merge {kind} fused {fused}", flush=True)
+        _, outs[fused] = run_multi(p, 2000, 6)
+    for i in range(6):
+        np.testing.assert_array_equal(outs["1"][i], outs["0"][i], err_msg=f"step {i}")
