@@ -31,6 +31,12 @@ typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 #define GLOBAL __attribute__((address_space(1)))
 template <typename T> __device__ __forceinline__ T gld(const void * p) { return *(const GLOBAL T *) p; }
 
+// Marks a loaded value as used here. Arithmetic on a loop-invariant load is
+// otherwise free to move ahead of the loop, and its wait for the load then
+// comes before loads the source issues earlier (the GEMV's weights).
+__device__ __forceinline__ void pin(float & v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(int & v) { asm volatile("" : "+v"(v)); }
+
 __device__ __forceinline__ float h2f(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
 
@@ -480,9 +486,17 @@ __device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first 
                 // 4'. the activation computed from x into LDS (the gather
                 // buffer starts 16-byte aligned after the codes and fields)
                 __shared__ double red[WG / 64];
+                #pragma unroll
+                for (int k = 0; k < FK; k++) {
+                    pin(fx[k].x); pin(fx[k].y); pin(fx[k].z); pin(fx[k].w);
+                    pin(fw[k].x); pin(fw[k].y); pin(fw[k].z); pin(fw[k].w);
+                    pin(fp[k].x); pin(fp[k].y); pin(fp[k].z); pin(fp[k].w);
+                }
                 fused_act<WG, FK>(a, fx, fw, fp, lq, lsc, (float *) (lds + ((n + 8 * ng + 15) & ~15)), red);
             } else {
                 // 4. activation into LDS (waits only for the activation loads)
+                #pragma unroll
+                for (int k = 0; k < SG; k++) { pin(sg_s[k]); pin(sg_u[k]); }
                 #pragma unroll
                 for (int k = 0; k < SQ; k++) { const int idx = tid + k * WG; if (idx < nq16) ((v4i *) lq)[idx] = sq_[k]; }
                 #pragma unroll
