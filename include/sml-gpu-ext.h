@@ -18,8 +18,9 @@ void sml_gpu_close(void);
 // (sml/sml-gpu-fwd.c:2626-2661). Returns n, or -1 on failure.
 int sml_gpu_generate(int tok, int pos, int n, int * out);
 
-// Elapsed GPU milliseconds of the last sml_gpu_generate call (HIP events on
-// the decode stream), or -1.
+// Elapsed GPU milliseconds of the last sml_gpu_generate call, or of the
+// kernels of the last sml_gpu_step_multi call without its logits copy (HIP
+// events on the decode stream), or -1.
 float sml_gpu_last_ms(void);
 
 // Weight bytes one decode step streams (every quantized matrix the step reads,

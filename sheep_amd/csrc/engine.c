@@ -36,6 +36,7 @@ typedef struct {
 } eng_layer;
 
 #define MAX_SLOTS 16
+#define NBKT 8                 // position buckets of the captured steps
 
 static struct {
     int open;
@@ -65,9 +66,14 @@ static struct {
     float * lg_host;
     int32_t * pin;             // pinned: [0] tok, [1] pos, [2..] prompt ids
     hipStream_t st;
-    hipGraphExec_t g_body, g_tail, g_adv;
-    hipGraphExec_t g_multi[17][2];   // the batched step per sequence count and regime (per-256)
+    // Attention launches cover the positions below pos_cap only. A step's
+    // graph is captured per position bucket: bucket k covers positions below
+    // min(n_ctx, (k + 1) * bkt_len), so a step at a short position launches
+    // no workgroups for the splits of the context it cannot reach yet.
+    hipGraphExec_t g_body[NBKT], g_tail, g_adv;
+    hipGraphExec_t g_multi[17][2][NBKT];   // the batched step per sequence count, regime (per-256), bucket
     int use_graph;
+    int pos_cap, bkt_len, nbkt;
     hipEvent_t e0, e1;
     float last_ms;
     uint64_t weight_bytes;
@@ -227,7 +233,7 @@ static void launch_layer(int L) {
     const int fuse_q = y->perm_o < 0 && !G.exact;
     uint16_t * kc = G.cur_slot ? G.kcs[G.cur_slot] : G.kc, * vc = G.cur_slot ? G.vcs[G.cur_slot] : G.vc;
     op_attention(G.st, G.q, G.k, G.v, kc + (size_t) L * G.n_ctx * kvd, vc + (size_t) L * G.n_ctx * kvd,
-                 G.rc, G.rs, G.pos, G.H, G.KV, G.hd, G.n_ctx, G.part, G.att,
+                 G.rc, G.rs, G.pos, G.H, G.KV, G.hd, G.n_ctx, G.pos_cap, G.part, G.att,
                  fuse_q ? G.aq[0] : NULL, fuse_q ? G.as[0] : NULL, fuse_q ? G.asum[0] : NULL, G.acnt);
     if (fuse_q) slot[0] = 0;
     else prep(G.att, NULL, NULL, G.H * G.hd, &y->perm_o, 1, slot);
@@ -303,7 +309,16 @@ static hipGraphExec_t capture(void (*fn)(void)) {
     return e;
 }
 
-static void run_body(void) { if (G.use_graph) HX(hipGraphLaunch(G.g_body, G.st)); else launch_body(); }
+static int bucket_of(int pos) { const int k = pos / G.bkt_len; return k < G.nbkt ? k : G.nbkt - 1; }
+static int bucket_cap(int k) { const int c = (k + 1) * G.bkt_len; return c < G.n_ctx ? c : G.n_ctx; }
+
+// one decode step's body at position pos (the device copy of pos holds it)
+static void run_body(int pos) {
+    const int k = bucket_of(pos);
+    G.pos_cap = bucket_cap(k);
+    if (G.use_graph) HX(hipGraphLaunch(G.g_body[k], G.st));
+    else launch_body();
+}
 static void run_tail(void) { if (G.use_graph) HX(hipGraphLaunch(G.g_tail, G.st)); else launch_tail(); }
 static void run_adv(void) { if (G.use_graph) HX(hipGraphLaunch(G.g_adv, G.st)); else launch_adv(); }
 
@@ -316,11 +331,12 @@ static void release(void) {
     hx.jb = &jb;
     if (!setjmp(jb)) {
         if (G.st) hipStreamSynchronize(G.st);
-        if (G.g_body) hipGraphExecDestroy(G.g_body);
+        for (int k = 0; k < NBKT; k++) if (G.g_body[k]) hipGraphExecDestroy(G.g_body[k]);
         if (G.g_tail) hipGraphExecDestroy(G.g_tail);
         if (G.g_adv) hipGraphExecDestroy(G.g_adv);
         for (int i = 0; i < 17; i++)
-            for (int j = 0; j < 2; j++) if (G.g_multi[i][j]) hipGraphExecDestroy(G.g_multi[i][j]);
+            for (int j = 0; j < 2; j++)
+                for (int k = 0; k < NBKT; k++) if (G.g_multi[i][j][k]) hipGraphExecDestroy(G.g_multi[i][j][k]);
         for (int i = 0; i < G.nmats; i++) { if (G.mats[i]->mem) hipFree(G.mats[i]->mem); free(G.mats[i]); }
         if (G.L) for (int L = 0; L < G.n_layer; L++) if (G.L[L].moe) { moe_free(G.L[L].moe); G.L[L].moe = NULL; }
         for (int i = 0; i < G.ndev; i++) hipFree(G.dev[i]);
@@ -549,8 +565,20 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     G.rrows = G.pb;
     G.rows_ok = -1;
     G.use_graph = env_int("SML_GRAPH", 1) != 0;
+    // position buckets: at most NBKT, none shorter than 512 positions
+    // (SML_POS_BUCKETS=0: one, every launch covering the whole context)
+    G.bkt_len = (G.n_ctx + NBKT - 1) / NBKT;
+    G.bkt_len = (G.bkt_len + 127) / 128 * 128;
+    if (G.bkt_len < 512) G.bkt_len = 512;
+    if (!env_int("SML_POS_BUCKETS", 1)) G.bkt_len = G.n_ctx;
+    G.nbkt = (G.n_ctx + G.bkt_len - 1) / G.bkt_len;
+    G.pos_cap = G.n_ctx;
     if (G.use_graph) {
-        G.g_body = capture(launch_body);
+        for (int k = 0; k < G.nbkt; k++) {
+            G.pos_cap = bucket_cap(k);
+            G.g_body[k] = capture(launch_body);
+        }
+        G.pos_cap = G.n_ctx;
         G.g_tail = capture(launch_tail);
         G.g_adv = capture(launch_adv);
     }
@@ -597,7 +625,7 @@ const float * sml_gpu_step(int tok, int pos) {
     G.pin[1] = pos;
     HX(hipMemcpyAsync(G.hist + pos, &G.pin[0], 4, hipMemcpyHostToDevice, G.st));
     HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
-    run_body();
+    run_body(pos);
     run_tail();
     fetch_logits();
     HX_LEAVE();
@@ -624,7 +652,7 @@ const float * sml_gpu_prefill(const int * ids, int pos0, int n) {
         G.pin[1] = pos0;
         HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
         for (int i = 0; i < n; i++) {
-            run_body();
+            run_body(pos0 + i);
             if (i + 1 < n) run_adv();
         }
     }
@@ -642,7 +670,7 @@ int sml_gpu_generate(int tok, int pos, int n, int * out) {
     HX(hipMemcpyAsync(G.hist + pos, &G.pin[0], 4, hipMemcpyHostToDevice, G.st));
     HX(hipMemcpyAsync(G.pos, &G.pin[1], 4, hipMemcpyHostToDevice, G.st));
     HX(hipEventRecord(G.e0, G.st));
-    for (int i = 0; i < n; i++) { run_body(); run_tail(); }
+    for (int i = 0; i < n; i++) { run_body(pos + i); run_tail(); }
     HX(hipEventRecord(G.e1, G.st));
     HX(hipMemcpyAsync(G.pin + 2, G.hist + pos + 1, (size_t) n * 4, hipMemcpyDeviceToHost, G.st));
     HX(hipStreamSynchronize(G.st));
@@ -817,7 +845,7 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
         // that to its own launch)
         const int fuse_q = y->perm_o < 0 && (!sb || (!causal && G.H % 2 == 0 && env_int("SML_MERGE_Q256", 1)));
         op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
-                           G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.mpart, G.matt,
+                           G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.pos_cap, G.mpart, G.matt,
                            fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL,
                            causal ? (regime == GEMM_EXACT ? 1 : 2) : 0, gemm_exact(regime, ns), sb);
         if (!fuse_q) {
@@ -871,9 +899,11 @@ static void prefill_rows(int slot, int pos0, int n) {
     int last = 0;
     for (int p0 = 0; p0 < n; p0 += chunk) {
         const int nb = n - p0 < chunk ? n - p0 : chunk;
+        G.pos_cap = pos0 + p0 + nb;
         launch_rows(nb, G.hist + pos0 + p0, G.iota + pos0 + p0, G.slotid + (size_t) slot * G.rrows, regime, 1, 0);
         last = nb - 1;
     }
+    G.pos_cap = G.n_ctx;
     HX(hipMemcpyAsync(G.x, G.mx + (size_t) last * G.E, (size_t) G.E * 4, hipMemcpyDeviceToDevice, G.st));
 }
 
@@ -899,9 +929,11 @@ const float * sml_gpu_prefill_slot(int slot, const int * ids, int pos0, int n) {
         if (setjmp(jb)) { G.cur_slot = 0; hx.jb = outer; longjmp(*outer, 1); }
         hx.jb = &jb;
         for (int i = 0; i < n; i++) {
+            G.pos_cap = pos0 + i + 1;
             launch_body();
             if (i + 1 < n) launch_adv();
         }
+        G.pos_cap = G.n_ctx;
         launch_tail();
         hx.jb = outer;
         G.cur_slot = 0;
@@ -918,16 +950,23 @@ static void launch_multi_cur(void) {
 }
 
 // The batched step reads its tokens, positions and slots from device arrays,
-// so one captured graph per (sequence count, regime) serves every step: the
-// ~300 launches of a step are replayed, not issued from the host. The
-// regime and the environment switches are read when a graph is captured.
-static void launch_multi(int ns) {
+// so one captured graph per (sequence count, regime, position bucket of the
+// furthest sequence) serves every step: the ~300 launches of a step are
+// replayed, not issued from the host. The regime and the environment
+// switches are read when a graph is captured.
+static void launch_multi(int ns, int maxpos) {
     g_multi_ns = ns;
     g_multi_sb = multi_per256(ns);
-    if (!G.use_graph) { launch_multi_cur(); return; }
-    hipGraphExec_t * g = &G.g_multi[ns][g_multi_sb];
-    if (!*g) *g = capture(launch_multi_cur);
-    HX(hipGraphLaunch(*g, G.st));
+    const int k = bucket_of(maxpos);
+    G.pos_cap = bucket_cap(k);
+    if (G.use_graph) {
+        hipGraphExec_t * g = &G.g_multi[ns][g_multi_sb][k];
+        if (!*g) *g = capture(launch_multi_cur);
+        HX(hipGraphLaunch(*g, G.st));
+    } else {
+        launch_multi_cur();
+    }
+    G.pos_cap = G.n_ctx;
 }
 
 int sml_gpu_step_multi(const int * tok, const int * pos, const int * slot, int ns, float * logits_out) {
@@ -943,9 +982,14 @@ int sml_gpu_step_multi(const int * tok, const int * pos, const int * slot, int n
     HX(hipMemcpyAsync(G.mtok, G.mpin, (size_t) ns * 4, hipMemcpyHostToDevice, G.st));
     HX(hipMemcpyAsync(G.mpos, G.mpin + MAX_SLOTS, (size_t) ns * 4, hipMemcpyHostToDevice, G.st));
     HX(hipMemcpyAsync(G.mslot, G.mpin + 2 * MAX_SLOTS, (size_t) ns * 4, hipMemcpyHostToDevice, G.st));
-    launch_multi(ns);
+    int maxpos = 0;
+    for (int b = 0; b < ns; b++) if (pos[b] > maxpos) maxpos = pos[b];
+    HX(hipEventRecord(G.e0, G.st));
+    launch_multi(ns, maxpos);
+    HX(hipEventRecord(G.e1, G.st));
     HX(hipMemcpyAsync(logits_out, G.mlog, (size_t) ns * G.V * 4, hipMemcpyDeviceToHost, G.st));
     HX(hipStreamSynchronize(G.st));
+    HX(hipEventElapsedTime(&G.last_ms, G.e0, G.e1));
     HX_LEAVE();
     return ns;
 }

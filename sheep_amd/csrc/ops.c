@@ -654,10 +654,11 @@ static int attn_split(int n_kv, int n_ctx) {
 
 void op_attention(hipStream_t st, const float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
                   const float * cos_t, const float * sin_t, const int32_t * pos, int n_head, int n_kv,
-                  int hd, int n_ctx, float * part, float * out, int8_t * q_out, float * s_out,
+                  int hd, int n_ctx, int n_pos, float * part, float * out, int8_t * q_out, float * s_out,
                   int32_t * u_out, int * cnt) {
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
+    if (n_pos < 1 || n_pos > n_ctx) hx_failf("attention over %d of %d positions", n_pos, n_ctx);
     if (g_exact) {
         // the reference's order: RoPE and the KV write, then a workgroup per
         // query head with the scores of every position in LDS; the output
@@ -676,9 +677,11 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     // one sequence: the 8-wave kernel over attn_split positions, the split the
     // exact prompt kernel (sml_attnc8) takes, so prompts read at level 1 equal
     // stepping bit for bit (SML_ATTN_WAVES applies to the batched step only)
+    // splits past n_pos are not launched: the merge of the ones that are
+    // equals the merge of all (empty splits add exact zeros)
     const int aw = 8;
     const int ch = attn_split(n_kv, n_ctx);
-    const int ns = (n_ctx + ch - 1) / ch;
+    const int ns = (n_pos + ch - 1) / ch;
     sml_kattn a;
     memset(&a, 0, sizeof a);
     a.q = q; a.k = k; a.v = v; a.kcache = kc; a.vcache = vc; a.cos_t = cos_t; a.sin_t = sin_t; a.pos = pos;
@@ -699,10 +702,11 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
-                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal,
-                        int exact, int q256) {
+                        int n_pos, float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out,
+                        int causal, int exact, int q256) {
     if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
+    if (n_pos < 1 || n_pos > n_ctx) hx_failf("attention over %d of %d positions", n_pos, n_ctx);
     if (q_out && q256 && (causal || n_head % 2))
         hx_failf("the merge quantizes per 256 only decode steps of an even head count (%d heads)", n_head);
     if (nseq < 1 || nseq > 65535) hx_failf("attention batch of %d", nseq);
@@ -710,7 +714,7 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     // the 8-wave kernels split as decoding does (attn_split); the 4-wave and
     // wave-per-position kernels run splits of 128
     const int ch = causal == 2 || (causal == 0 && aw == 4) ? ATTN_CHUNK : attn_split(n_kv, n_ctx);
-    const int ns = (n_ctx + ch - 1) / ch;
+    const int ns = (n_pos + ch - 1) / ch;             // splits past n_pos: not launched
     sml_kattn a;
     memset(&a, 0, sizeof a);
     a.q = qkv; a.k = qkv + (size_t) n_head * hd; a.v = a.k + (size_t) n_kv * hd;
@@ -779,7 +783,7 @@ int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kc
                       const float * cos_t, const float * sin_t, const int32_t * pos,
                       int n_head, int n_kv, int hd, int n_ctx, float * part, float * out) {
     OP_BEGIN(-1);
-    op_attention(0, q, k, v, kcache, vcache, cos_t, sin_t, pos, n_head, n_kv, hd, n_ctx, part, out,
+    op_attention(0, q, k, v, kcache, vcache, cos_t, sin_t, pos, n_head, n_kv, hd, n_ctx, n_ctx, part, out,
                  NULL, NULL, NULL, NULL);
     HX_LEAVE();
     return 0;

@@ -78,10 +78,12 @@ void op_normq_rows(hipStream_t st, float * x, const float * resid, const float *
                    int32_t * const * sums, float * normed, int per256);
 // Decode attention for one sequence. cnt: n_kv zeroed counters (the merge then
 // runs in the attention launch itself, see sml_kattn.cnt), or NULL for a
-// separate merge launch.
+// separate merge launch. n_pos (<= n_ctx) bounds the positions the launch
+// may attend: the split size follows n_ctx, and only the splits below n_pos
+// are launched (the results equal launching all of them).
 void op_attention(hipStream_t st, const float * q, const float * k, const float * v, uint16_t * kc, uint16_t * vc,
                   const float * cos_t, const float * sin_t, const int32_t * pos, int n_head, int n_kv,
-                  int hd, int n_ctx, float * part, float * out, int8_t * q_out, float * s_out,
+                  int hd, int n_ctx, int n_pos, float * part, float * out, int8_t * q_out, float * s_out,
                   int32_t * u_out, int * cnt);
 // Attention for nseq sequences in one launch: sequence b's q, k, v at
 // qkv + b * qkv_stride (q, then k, then v), its cache kc_slots[slot[b]] +
@@ -91,12 +93,14 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
 // before any entry attends; 1 keeps the decode kernel's arithmetic per entry
 // (bit-exact with stepping), 2 runs the wave-per-position kernel (faster,
 // its own fp32 order). The quantized out is per 32 values, or per 256 when
-// q256 (decode steps, causal 0, of an even head count only).
+// q256 (decode steps, causal 0, of an even head count only). n_pos bounds
+// every entry's position as in op_attention (the flash prompt form splits
+// the whole n_ctx range).
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
-                        float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out, int causal,
-                        int exact, int q256);
+                        int n_pos, float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out,
+                        int causal, int exact, int q256);
 // Whether op_gemm computes every row with the GEMV's arithmetic in this regime
 // for m_all rows (the exact regime, or per-32 rows the VALU kernel takes).
 int gemm_exact(int regime, int m_all);

@@ -317,3 +317,35 @@ def test_bounds_and_reopen(tiny):
         d.close()
     d = sa.Decoder(tiny, n_ctx=32)
     d.close()
+
+
+@pytest.mark.parametrize("model", ["tiny", "qwenish"])
+def test_position_buckets_equal_whole_context_launches(model, request, monkeypatch):
+    """Steps are captured per position bucket (512 positions here), and their
+    attention launches no workgroups past the bucket's end. The merge of the
+    launched splits equals the merge of every split of the context, so with
+    SML_POS_BUCKETS=0 (every launch over all 2048 positions) a prompt, steps
+    across a bucket boundary (positions 500..530), generated tokens and a
+    three-sequence batched step give the same bits."""
+    path = request.getfixturevalue(model)
+    V = 2000 if model == "tiny" else 32000
+    rng = np.random.default_rng(8)
+    ids = rng.integers(0, V, 531).astype(np.int32)
+    outs = {}
+    for buckets in ("1", "0"):
+        monkeypatch.setenv("SML_POS_BUCKETS", buckets)
+        print(f"position buckets {buckets}", flush=True)
+        d = sa.Decoder(path, n_ctx=2048)
+        try:
+            got = [d.prefill(ids[:500], 0, V)]
+            got += [d.step(int(ids[i]), i, V).copy() for i in range(500, 531)]
+            got.append(np.array(d.generate(int(ids[-1]), 531, 4), np.float32))
+            d.slots(3)
+            for b in range(1, 3):
+                got.append(d.prefill_slot(b, ids[:400 + 60 * b], 0, V))
+            got.append(d.step_multi([int(ids[530]), 7, 9], [535, 460, 520], [0, 1, 2], V))
+            outs[buckets] = got
+        finally:
+            d.close()
+    for i, (a, b) in enumerate(zip(outs["1"], outs["0"])):
+        np.testing.assert_array_equal(a, b, err_msg=f"output {i}")
