@@ -2447,6 +2447,21 @@ __device__ void gemm_body(const sml_kgemm & a) {
                 wsc[s] = h2f((uint16_t) (d2 & 0xFFFFu)) * (float) (f & 0xFFu);
                 wmn[s] = h2f((uint16_t) (d2 >> 16)) * ((float) (f >> 8) - 127.0f);
             }
+            // Q4: the chunk's codes unpacked once for every row (held in
+            // registers: left to itself the compiler redoes the masks per row)
+            v4u ua[RB], ub[RB];
+            if constexpr (NB == 4) {
+                #pragma unroll
+                for (int s = 0; s < RB; s++) {
+                    #pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        unsigned lo = w[i][s].n4[e] & 0x0F0F0F0Fu, hi = (w[i][s].n4[e] >> 4u) & 0x0F0F0F0Fu;
+                        asm volatile("" : "+v"(lo), "+v"(hi));
+                        ua[s][e] = lo;
+                        ub[s][e] = hi;
+                    }
+                }
+            }
             #pragma unroll
             for (int t = 0; t < MT; t++) {
                 if (t < m) {
@@ -2456,8 +2471,13 @@ __device__ void gemm_body(const sml_kgemm & a) {
                 if (!live) sc = make_float2(0.0f, 0.0f);
                 #pragma unroll
                 for (int s = 0; s < RB; s++) {
-                    int da, db;
-                    chunk_dots<NB>(w[i][s], c, xa, xb, da, db);
+                    int da = 0, db = 0;
+                    if constexpr (NB == 4) {
+                        #pragma unroll
+                        for (int e = 0; e < 4; e++) { da = dot4(ua[s][e], xa[e], da); db = dot4(ub[s][e], xb[e], db); }
+                    } else {
+                        chunk_dots<NB>(w[i][s], c, xa, xb, da, db);
+                    }
                     const int keep = odd ? db : da, send = odd ? da : db;
                     const int dot = keep + pair_swap(send);
                     acc[s][t] += wsc[s] * (sc.x * (float) dot);
