@@ -2448,38 +2448,56 @@ __device__ void gemm_body(const sml_kgemm & a) {
                 wmn[s] = h2f((uint16_t) (d2 >> 16)) * ((float) (f >> 8) - 127.0f);
             }
             // Q4: the chunk's codes unpacked once for every row (held in
-            // registers: left to itself the compiler redoes the masks per row)
+            // registers: left to itself the compiler redoes the masks per row),
+            // in the order this lane keeps and sends them: an odd lane keeps
+            // the high nibbles (group c|1, against the second 16 codes of the
+            // pair) and sends the low ones, so no per-row select is needed
             v4u ua[RB], ub[RB];
+            const unsigned shk = odd ? 4u : 0u, shs = 4u - shk;
+            const int offk = off + (odd ? 32 : 0), offs = off + (odd ? 0 : 32);
             if constexpr (NB == 4) {
                 #pragma unroll
                 for (int s = 0; s < RB; s++) {
                     #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        unsigned lo = w[i][s].n4[e] & 0x0F0F0F0Fu, hi = (w[i][s].n4[e] >> 4u) & 0x0F0F0F0Fu;
-                        asm volatile("" : "+v"(lo), "+v"(hi));
-                        ua[s][e] = lo;
-                        ub[s][e] = hi;
+                        unsigned kp = (w[i][s].n4[e] >> shk) & 0x0F0F0F0Fu, sd = (w[i][s].n4[e] >> shs) & 0x0F0F0F0Fu;
+                        asm volatile("" : "+v"(kp), "+v"(sd));
+                        ua[s][e] = kp;
+                        ub[s][e] = sd;
                     }
                 }
             }
             #pragma unroll
             for (int t = 0; t < MT; t++) {
                 if (t < m) {
-                const v4i xa = *(const v4i *) (lq + t * TILE * 32 + off);
-                const v4i xb = *(const v4i *) (lq + t * TILE * 32 + off + 32);
                 float2 sc = lsc[t * TILE + cl];
                 if (!live) sc = make_float2(0.0f, 0.0f);
+                int keep[RB], send[RB];
+                if constexpr (NB == 4) {
+                    const v4i xk = *(const v4i *) (lq + t * TILE * 32 + offk);
+                    const v4i xs = *(const v4i *) (lq + t * TILE * 32 + offs);
+                    #pragma unroll
+                    for (int s = 0; s < RB; s++) {
+                        int k = 0, d = 0;
+                        #pragma unroll
+                        for (int e = 0; e < 4; e++) { k = dot4(ua[s][e], xk[e], k); d = dot4(ub[s][e], xs[e], d); }
+                        keep[s] = k;
+                        send[s] = d;
+                    }
+                } else {
+                    const v4i xa = *(const v4i *) (lq + t * TILE * 32 + off);
+                    const v4i xb = *(const v4i *) (lq + t * TILE * 32 + off + 32);
+                    #pragma unroll
+                    for (int s = 0; s < RB; s++) {
+                        int da, db;
+                        chunk_dots<NB>(w[i][s], c, xa, xb, da, db);
+                        keep[s] = odd ? db : da;
+                        send[s] = odd ? da : db;
+                    }
+                }
                 #pragma unroll
                 for (int s = 0; s < RB; s++) {
-                    int da = 0, db = 0;
-                    if constexpr (NB == 4) {
-                        #pragma unroll
-                        for (int e = 0; e < 4; e++) { da = dot4(ua[s][e], xa[e], da); db = dot4(ub[s][e], xb[e], db); }
-                    } else {
-                        chunk_dots<NB>(w[i][s], c, xa, xb, da, db);
-                    }
-                    const int keep = odd ? db : da, send = odd ? da : db;
-                    const int dot = keep + pair_swap(send);
+                    const int dot = keep[s] + pair_swap(send[s]);
                     acc[s][t] += wsc[s] * (sc.x * (float) dot);
                     acc[s][t] += wmn[s] * sc.y;
                 }
