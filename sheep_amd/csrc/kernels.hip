@@ -1117,12 +1117,19 @@ __device__ __forceinline__ float merge_value(const sml_kattn & a, int b, int h, 
     const float2 * pml = (const float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) h * a.nsplit;
     const size_t ob = (size_t) b * a.n_head * HD;
     float M = -INFINITY, L = 0.0f, o = 0.0f;
-    for (int s0 = 0; s0 < a.nsplit; s0 += MERGE_BATCH) {
-        const int n = min(MERGE_BATCH, a.nsplit - s0);
-        float ov[MERGE_BATCH];
+    // a batch of MERGE_BATCH splits; indices past the last split read split
+    // 0 (their weights are zero below)
+    auto fetch = [&](int s0, float (&ov)[MERGE_BATCH], float2 & ml) {
         #pragma unroll
-        for (int s = 0; s < MERGE_BATCH; s++) ov[s] = ld_part<DEV>(po + (size_t) (s0 + (s < n ? s : 0)) * HD + d);   // masked below
-        const float2 ml = ld_part2<DEV>(pml + s0 + (lane < n ? lane : 0));
+        for (int s = 0; s < MERGE_BATCH; s++) {
+            const int i = s0 + s < a.nsplit ? s0 + s : 0;
+            ov[s] = ld_part<DEV>(po + (size_t) i * HD + d);
+        }
+        const int j = s0 + lane < a.nsplit ? s0 + lane : 0;
+        ml = ld_part2<DEV>(pml + j);
+    };
+    auto fold = [&](int s0, const float (&ov)[MERGE_BATCH], const float2 ml) {
+        const int n = min(MERGE_BATCH, a.nsplit - s0);
         const float mj = lane < n ? ml.x : -INFINITY;
         const float Mb = fmaxf(M, rl(max32(mj), 0));         // finite: split 0 is active
         const float r = __builtin_amdgcn_exp2f(M - Mb);      // M = -inf: 0
@@ -1136,7 +1143,24 @@ __device__ __forceinline__ float merge_value(const sml_kattn & a, int b, int h, 
         }
         o = (acc[0] + acc[1]) + (acc[2] + acc[3]);
         M = Mb;
+    };
+    float ov[MERGE_BATCH];
+    float2 ml;
+    fetch(0, ov, ml);
+    int s0 = 0;
+    // more than one batch: the next batch's loads go out before this one is
+    // folded (issued only where a next batch exists, so a one-batch merge
+    // waits for nothing extra)
+    for (; s0 + MERGE_BATCH < a.nsplit; s0 += MERGE_BATCH) {
+        float ovn[MERGE_BATCH];
+        float2 mln;
+        fetch(s0 + MERGE_BATCH, ovn, mln);
+        fold(s0, ov, ml);
+        #pragma unroll
+        for (int s = 0; s < MERGE_BATCH; s++) ov[s] = ovn[s];
+        ml = mln;
     }
+    fold(s0, ov, ml);
     const float r = o / L;
     a.out[ob + (size_t) h * HD + d] = r;
     return r;
