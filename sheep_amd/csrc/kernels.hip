@@ -2808,13 +2808,14 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
     auto compute = [&](Batch & b, int bt) {
         const int gl0 = (bt - s0) * 8;
         if constexpr (SB) {
-            int is[NM][RB][4], im[NM][RB][4];
+            int is[NM][RB][4];
+            float imf[NM][RB][4];
             #pragma unroll
             for (int k = 0; k < NM; k++)
                 #pragma unroll
                 for (int bk = 0; bk < RB; bk++)
                     #pragma unroll
-                    for (int r = 0; r < 4; r++) { is[k][bk][r] = 0; im[k][bk][r] = 0; }
+                    for (int r = 0; r < 4; r++) is[k][bk][r] = 0;
             v2u wx[2][NM][RB], wy[2][NM][RB];
             v1l av[8];
             operands(b, wx, wy, av);
@@ -2824,8 +2825,6 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             }
             #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const int4 sm = *(const int4 *) &lsum[(gl0 + j) * 16 + 4 * c];
-                const int smv[4] = {sm.x, sm.y, sm.z, sm.w};
                 #pragma unroll
                 for (int k = 0; k < NM; k++)
                     #pragma unroll
@@ -2834,14 +2833,36 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
                         v4i d = { 0, 0, 0, 0 };
                         d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], bv, d, 0, 0, 0);
                         const uint32_t f = b.fq[k][bk][j >> 1] >> (16 * (j & 1));
-                        const int sq = (int) (f & 0xFFu), mn = (int) ((f >> 8) & 0xFFu) - 127;
+                        const int sq = (int) (f & 0xFFu);
                         #pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            is[k][bk][r] = __mul24(sq, d[r]) + is[k][bk][r];
-                            im[k][bk][r] = __mul24(mn, smv[r]) + im[k][bk][r];
-                        }
+                        for (int r = 0; r < 4; r++) is[k][bk][r] = __mul24(sq, d[r]) + is[k][bk][r];
                     }
             }
+            // the min term sum_g sums[r][g] * (mq[w][g] - 127) on the fp32
+            // matrix cores, two K=4 steps over the superblock's 8 groups:
+            // A = the activation rows' group sums (lane: row i16, group
+            // 4kk + c), B = the weight rows' mq - 127 (lane: group 4kk + c,
+            // row i16), D in the integer product's layout. Every product
+            // (|sum| <= 32*127, |mq - 127| <= 128) and partial sum stays below
+            // 2^24, so the fp32 sums are the integers, exactly
+            float amin[2];
+            #pragma unroll
+            for (int kk = 0; kk < 2; kk++) amin[kk] = (float) lsum[(gl0 + 4 * kk + c) * 16 + i16];
+            const uint32_t msh = 16u * (uint32_t) (c & 1) + 8u;
+            #pragma unroll
+            for (int k = 0; k < NM; k++)
+                #pragma unroll
+                for (int bk = 0; bk < RB; bk++) {
+                    v4f mf = { 0.0f, 0.0f, 0.0f, 0.0f };
+                    #pragma unroll
+                    for (int kk = 0; kk < 2; kk++) {
+                        const uint32_t wd = (c >> 1) ? b.fq[k][bk][2 * kk + 1] : b.fq[k][bk][2 * kk];
+                        const float bm = (float) ((int) ((wd >> msh) & 0xFFu) - 127);
+                        mf = __builtin_amdgcn_mfma_f32_16x16x4f32(amin[kk], bm, mf, 0, 0, 0);
+                    }
+                    #pragma unroll
+                    for (int r = 0; r < 4; r++) imf[k][bk][r] = mf[r];
+                }
             const float4 as = *(const float4 *) &lscl[(bt - s0) * 16 + 4 * c];
             const float asv[4] = {as.x, as.y, as.z, as.w};
             #pragma unroll
@@ -2852,7 +2873,7 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
                     #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         acc[k][bk][r] += (float) is[k][bk][r] * (dsc * asv[r]);
-                        acc[k][bk][r] += (float) im[k][bk][r] * (mdsc * asv[r]);
+                        acc[k][bk][r] += imf[k][bk][r] * (mdsc * asv[r]);
                     }
                 }
         } else {
