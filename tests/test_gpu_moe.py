@@ -293,6 +293,37 @@ def test_moe_ffn_per256(tmpdir_s, T):
         close(got_out[t], ro, f"per-256 moe token {t}")
 
 
+@pytest.mark.parametrize("per256", [False, True])
+def test_moe_expert_with_many_tokens(tmpdir_s, per256, monkeypatch):
+    """An expert chosen by more than 8 of 16 tokens goes to the second size
+    class's launch (up to 16 rows): 12 identical tokens send 12 rows to the
+    same two experts. Routing is bit-exact and every token's output close
+    to the oracle's; with SML_GEMM_SPLIT=0 (one launch of the 16-row class
+    for every group) the outputs are the same bits."""
+    n_embd, n_ff, nexp, k, T = 1024, 1536, 8, 2, 16
+    p = moe_model(tmpdir_s, "moe_0.ssf", n_embd, n_ff, nexp, k, False, seed=1005)
+    f = SSF(p)
+    rng = np.random.default_rng(91)
+    x = rng.standard_normal((T, n_embd)).astype(np.float32)
+    x[1:12] = x[0]
+    outs = {}
+    for split in ("1", "0"):
+        monkeypatch.setenv("SML_GEMM_SPLIT", split)
+        moe = sa.MoE(p, 0, 16)
+        moe.regime(per256)
+        out, sel = sa.DevBuf(T * n_embd * 4), sa.DevBuf(T * k * 4)
+        moe.ffn(sa.DevBuf.of(x), T, out, sel)
+        outs[split] = (out.read(np.float32).reshape(T, n_embd), sel.read(np.int32).reshape(T, k))
+        moe.free()
+    got_out, got_sel = outs["1"]
+    assert (got_sel[:12] == got_sel[0]).all()
+    np.testing.assert_array_equal(outs["0"][0], got_out)
+    for t in range(T):
+        _, rs, _, ro = oracle_moe(f, x[t], nexp, k, n_embd, per256=per256)
+        np.testing.assert_array_equal(got_sel[t], rs, err_msg=f"token {t} routing")
+        close(got_out[t], ro, f"moe token {t}")
+
+
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("per256", [False, True])
 def test_moe_mixtral_layer_shape(tmp_path, per256):
