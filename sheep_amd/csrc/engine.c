@@ -62,6 +62,7 @@ static struct {
     uint16_t * kc, * vc;
     int32_t * hist, * pos, * tok;
     int2 * amax_part;          // pairs of the two-stage greedy pick
+    int2 * head_pairs;         // the head GEMV's row blocks' pairs (at most one per row)
     int * acnt;                // merge counters of the decode attention launch (one per kv head)
     float * lg_host;
     int32_t * pin;             // pinned: [0] tok, [1] pos, [2..] prompt ids
@@ -280,6 +281,17 @@ static void launch_body(void) {
 static void launch_tail(void) {
     int slot[1];
     prep(G.x, G.out_norm, NULL, G.E, &G.perm_head, 1, slot);
+    if (!G.exact && G.V >= ARGMAX_TWO_STAGE_MIN) {
+        // the head GEMV's row blocks write the greedy pick's first stage
+        // (one (max, lowest index) pair each), so one workgroup finishes it
+        gemv_fuse fu;
+        memset(&fu, 0, sizeof fu);
+        fu.amax = G.head_pairs;
+        const int np = op_gemv(G.st, G.head, NULL, SML_EPI_STORE, G.aq[slot[0]], G.as[slot[0]], G.asum[slot[0]],
+                               G.logits, NULL, NULL, NULL, &fu);
+        op_argmax_pairs(G.st, G.head_pairs, np, G.logits, G.tok, G.pos, G.hist, G.n_ctx + 1);
+        return;
+    }
     gemv1(G.head, slot[0], SML_EPI_STORE, G.logits, NULL, NULL);
     op_argmax(G.st, G.logits, G.V, G.tok, G.pos, G.hist, G.n_ctx + 1, G.amax_part);
 }
@@ -547,6 +559,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     HX(hipMemset(G.hist, 0, (size_t) (n_ctx + 1) * 4));
     G.pos = dalloc(64);
     G.amax_part = dalloc((size_t) ARGMAX_MAX_PARTS * sizeof(int2));
+    G.head_pairs = dalloc((size_t) G.V * sizeof(int2));
     G.tok = dalloc(64);
     HX(hipMemset(G.pos, 0, 64));
     HX(hipHostMalloc((void **) &G.lg_host, (size_t) G.V * 4, 0));

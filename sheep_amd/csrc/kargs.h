@@ -62,6 +62,11 @@ typedef struct {
     int8_t        * hq;
     float         * hscale;
     int32_t       * hsums;
+    // the greedy pick's first stage (one-matrix GEMVs, not the exact
+    // form): when not NULL, each row block also writes the (max, lowest
+    // index) pair of its rows' outputs to amax[block], as sml_argmax_part
+    // would for those rows.
+    int2          * amax;
 } sml_kgemv;
 
 // Multi-workgroup RMSNorm + gather + quantize: every workgroup reduces the

@@ -31,6 +31,12 @@ typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 #define GLOBAL __attribute__((address_space(1)))
 template <typename T> __device__ __forceinline__ T gld(const void * p) { return *(const GLOBAL T *) p; }
 
+// The greedy pick's order: the larger value, the lower index on a tie; NaN is
+// never taken (the reference's loop, sml/sml-run.c:3539-3544).
+__device__ __forceinline__ void amax_take(float v, int i, float & bv, int & bi) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
 // Marks a loaded value as used here. Arithmetic on a loop-invariant load is
 // otherwise free to move ahead of the loop, and its wait for the load then
 // comes before loads the source issues earlier (the GEMV's weights).
@@ -628,6 +634,38 @@ __device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first 
             }
         }
         return;
+    }
+    if constexpr (!SW && !EX) {
+        if (a.amax) {
+            // the block's (max, lowest index) pair over its rows' outputs,
+            // the values the store below writes
+            constexpr int NS = (WG / WAVE) * SUB;
+            __shared__ float am_v[NS];
+            __shared__ int am_i[NS];
+            if (l == LPR - 1) {
+                float bv = -INFINITY;
+                int bi = 0x7fffffff;
+                #pragma unroll
+                for (int s = 0; s < RB; s++) {
+                    if (!valid[s]) continue;
+                    const int row = orow[s];
+                    float v = acc[s];
+                    if (a.m[0].bias) v += a.m[0].bias[row];
+                    if (a.epi == SML_EPI_RESIDUAL) v = a.resid[row] + v;
+                    amax_take(v, row, bv, bi);
+                }
+                am_v[wave * SUB + u] = bv;
+                am_i[wave * SUB + u] = bi;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                float bv = am_v[0];
+                int bi = am_i[0];
+                #pragma unroll
+                for (int k = 1; k < NS; k++) amax_take(am_v[k], am_i[k], bv, bi);
+                a.amax[blk] = make_int2(__float_as_int(bv), bi);
+            }
+        }
     }
     if (l != LPR - 1) return;
     if constexpr (SW) {
@@ -1954,9 +1992,6 @@ extern "C" __global__ __launch_bounds__(256) void sml_attn_exact(const sml_kattn
 // 513 KB of a 128k vocabulary arrive in a few round trips.
 #define ARGMAX_THREADS 1024
 #define ARGMAX_UNROLL 16
-__device__ __forceinline__ void amax_take(float v, int i, float & bv, int & bi) {
-    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-}
 // First stage of the two-stage pick: grid-stride over float4 words, one
 // (max, lowest index) pair per workgroup. The first-max rule is kept by
 // amax_take when the pairs are combined.

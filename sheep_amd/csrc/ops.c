@@ -453,9 +453,9 @@ static void pick_shape(int rows, int cols, int nbits, int swiglu, int fused, int
 
 int gemv_fuse_max_cols(int hq) { (void) hq; return 4096; }
 
-void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int epi, const int8_t * q,
-             const float * scale, const int32_t * sums, float * y, const float * bias, const float * up_bias,
-             const float * resid, const gemv_fuse * fu) {
+int op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int epi, const int8_t * q,
+            const float * scale, const int32_t * sums, float * y, const float * bias, const float * up_bias,
+            const float * resid, const gemv_fuse * fu) {
     const int swiglu = epi == SML_EPI_SWIGLU;
     if (swiglu != (up != NULL)) hx_failf("SwiGLU takes gate and up; other GEMVs one matrix");
     if (up && (up->nbits != m->nbits || up->cols != m->cols || up->k.rows != m->k.rows))
@@ -483,6 +483,10 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
         if (!swiglu || a.total_rows % 32) hx_failf("h quantization needs SwiGLU rows in whole groups");
         a.hq = fu->hq; a.hscale = fu->hscale; a.hsums = fu->hsums;
     }
+    if (fu && fu->amax) {
+        if (swiglu || g_exact) hx_failf("the pick's first stage runs in one-matrix GEMVs outside exact mode");
+        a.amax = fu->amax;
+    }
     // LDS: int8 codes, per-group (s, s*sum), and the fused prologue's gather buffer
     const size_t lds = ((size_t) cols + 8u * (size_t) (cols / 32) + 15u) / 16u * 16u + (am && fu->perm ? 4u * (size_t) cols : 0u);
     char name[48];
@@ -502,7 +506,7 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
         } else if (wg == 1024) snprintf(name, sizeof name, "sml_gemv_q%d_hn1024_i%d", nb, ni);
         else snprintf(name, sizeof name, "sml_gemv_q%d_h%s_i%d", nb, am ? "n" : "", ni);
         hx_launch(name, grid, 1, (unsigned) wg, lds, st, &a);
-        return;
+        return 0;
     }
     int rb, ni;
     pick_shape(a.total_rows, cols, nb, swiglu, am, &rb, &ni);
@@ -517,7 +521,7 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
         if (swiglu) snprintf(name, sizeof name, "sml_gemv_q%d_s_r%d_i%d_x", nb, rb, ni);
         else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_x", nb, rb, ni);
         hx_launch(name, (unsigned) ((waves + 3) / 4), 1, 256, xl, st, &a);
-        return;
+        return 0;
     }
     int wg = 256;
     if (!swiglu && am && env_int("SML_GEMV_WG", 512) != 256) {
@@ -527,6 +531,7 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
     const int rows_per_wave = swiglu ? rb / 2 : rb;
     const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
     unsigned grid = (unsigned) ((waves + wg / 64 - 1) / (wg / 64));
+    const int blocks = (int) grid;                      // row blocks (amax pairs), persistent or not
     // persistent forms (SML_GEMV_PERSIST = workgroups per CU): Q4, plain or
     // with the 512-thread prologue
     const int pw = env_int("SML_GEMV_PERSIST", 0);
@@ -537,6 +542,7 @@ void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int 
     else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d%s%s", nb, rb, ni, am ? "_n" : "", pok ? "_p" : "");
     if (pok) grid = (unsigned) (pw * hx.ncu);
     hx_launch(name, grid, 1, (unsigned) wg, lds, st, &a);
+    return blocks;
 }
 
 int sml_hip_matvec(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, float * y) {
@@ -804,6 +810,16 @@ void op_argmax(hipStream_t st, const float * logits, int n, int32_t * tok, int32
         a.part = part; a.nparts = np;
         hx_launch("sml_argmax_part", (unsigned) np, 1, 256, 0, st, &a);
     }
+    hx_launch("sml_argmax", 1, 1, 1024, 0, st, &a);
+}
+
+void op_argmax_pairs(hipStream_t st, const int2 * pairs, int nparts, const float * logits, int32_t * tok,
+                     int32_t * pos, int32_t * hist, int hist_n) {
+    if (nparts < 1) hx_failf("greedy pick over %d pairs", nparts);
+    sml_kargmax a;
+    memset(&a, 0, sizeof a);
+    a.logits = logits; a.tok = tok; a.pos = pos; a.hist = hist; a.hist_n = hist_n;
+    a.part = (int2 *) pairs; a.nparts = nparts;
     hx_launch("sml_argmax", 1, 1, 1024, 0, st, &a);
 }
 

@@ -44,14 +44,17 @@ typedef struct {
     int8_t * hq;
     float * hscale;
     int32_t * hsums;
+    int2 * amax;                  // one-matrix GEMVs: each row block's (max, lowest index) pair
 } gemv_fuse;
 // Widest input the fused prologue takes (hq: the 1024-thread SwiGLU kernels).
 int gemv_fuse_max_cols(int hq);
 // y = W.x (+ bias, + resid for SML_EPI_RESIDUAL) for one matrix m; SwiGLU
-// (up != NULL): y = silu(gate.x + bias) * (up.x + up_bias).
-void op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int epi, const int8_t * q,
-             const float * scale, const int32_t * sums, float * y, const float * bias, const float * up_bias,
-             const float * resid, const gemv_fuse * fu);
+// (up != NULL): y = silu(gate.x + bias) * (up.x + up_bias). Returns the
+// number of row blocks of the plain GEMV forms (fu->amax's pair count), 0
+// for the others.
+int op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int epi, const int8_t * q,
+            const float * scale, const int32_t * sums, float * y, const float * bias, const float * up_bias,
+            const float * resid, const gemv_fuse * fu);
 // Small-M GEMM over ngroups matrix groups (device table tab: one matrix per
 // group, or gate/up pairs for SwiGLU); m_all rows (count == NULL) or count[e]
 // rows per group, at most mt (1, 4, 8 or 16). The activation regime:
@@ -111,6 +114,10 @@ int gemm_exact(int regime, int m_all);
 #define ARGMAX_MAX_PARTS 1024
 void op_argmax(hipStream_t st, const float * logits, int n, int32_t * tok, int32_t * pos, int32_t * hist,
                int hist_n, int2 * part);
+// The greedy pick's second stage over nparts (max, lowest index) pairs (a
+// GEMV's amax row blocks); logits[0] keeps the reference's NaN rule.
+void op_argmax_pairs(hipStream_t st, const int2 * pairs, int nparts, const float * logits, int32_t * tok,
+                     int32_t * pos, int32_t * hist, int hist_n);
 void op_advance(hipStream_t st, int32_t * pos);
 void op_silu_mul(hipStream_t st, float * g, const float * u, int n);
 
