@@ -1009,10 +1009,30 @@ extern "C" __global__ void sml_embed(const sml_kembed a) {
     const int b = a.pos ? 0 : (int) blockIdx.y;
     const size_t row = (size_t) (a.pos ? a.tok[*a.pos] : a.tok[b]);
     float * x = a.x + (size_t) b * a.cols;
-    uint8_t c[32];
-    group_codes(a.m, a.nbits, a.cols, row, g, c);
     const uint8_t * f = a.m.sqmq + (row * ng + g) * 2;
     const uint16_t * d = a.m.sdmd + (row * ns + g / 8) * 2;
+    if (a.nbits == 4 && !a.perm) {
+        // Q4 in order: the group's 32 bytes as two 16-byte loads (its
+        // nibbles, the low or high half of each byte), 8 float4 stores
+        const uint8_t * blk = a.m.plane[0] + row * (size_t) (a.cols / 2) + (size_t) (g >> 2) * 64 + ((g & 2) ? 32 : 0);
+        const v4u lo = gld<v4u>(blk), hi = gld<v4u>(blk + 16);
+        const float step = h2f(d[0]) * (float) f[0];
+        const float mn = h2f(d[1]) * ((float) f[1] - 127.0f);
+        const unsigned sh = (g & 1) ? 4u : 0u;
+        #pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const unsigned w = k < 4 ? lo[k] : hi[k - 4];
+            float4 o;
+            o.x = __builtin_fmaf((float) ((w >> sh) & 15u), step, mn);
+            o.y = __builtin_fmaf((float) ((w >> (sh + 8)) & 15u), step, mn);
+            o.z = __builtin_fmaf((float) ((w >> (sh + 16)) & 15u), step, mn);
+            o.w = __builtin_fmaf((float) ((w >> (sh + 24)) & 15u), step, mn);
+            *(float4 *) (x + g * 32 + 4 * k) = o;
+        }
+        return;
+    }
+    uint8_t c[32];
+    group_codes(a.m, a.nbits, a.cols, row, g, c);
     const float step = h2f(d[0]) * (float) f[0];
     const float mn = h2f(d[1]) * ((float) f[1] - 127.0f);
     // the reference's order: fma(code, step, min), then Q3/Q5/Q7 add their

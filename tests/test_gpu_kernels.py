@@ -227,7 +227,7 @@ def test_swiglu_h_quantization(tmpdir_s, n_embd, nb, xin, perm):
 
 # ------------------------------------------------------------ embed, attention, argmax
 
-@pytest.mark.parametrize("nb", [4, 6, 8])
+@pytest.mark.parametrize("nb", [2, 3, 4, 5, 6, 7, 8])
 def test_embed(tmpdir_s, nb):
     p = tmpdir_s / f"emb{nb}.ssf"
     sa.synth_matrix(p, 1000, 1536, nbits=nb, random_perm=True, seed=500 + nb)
@@ -241,6 +241,9 @@ def test_embed(tmpdir_s, nb):
         want = np.zeros(1536, np.float32)
         want[t.perm] = ob.dequant_row(t, tok)
         np.testing.assert_array_equal(x.read(np.float32), want)
+        # in storage order (no permutation: Q4 takes the vector path)
+        assert sa.lib().sml_hip_embed(m.h, td.ptr, None, x.ptr) == 0
+        np.testing.assert_array_equal(x.read(np.float32), ob.dequant_row(t, tok))
 
 
 @pytest.mark.parametrize("heads", [(12, 2), (32, 8)])
