@@ -345,7 +345,7 @@ class Decoder:
         t = np.ascontiguousarray(toks, np.int32)
         p = np.ascontiguousarray(poss, np.int32)
         s = np.ascontiguousarray(slots, np.int32)
-        out = np.zeros((len(t), n_vocab), np.float32)
+        out = np.empty((len(t), n_vocab), np.float32)     # every entry is written
         if lib().sml_gpu_step_multi(t.ctypes.data_as(P(c_int)), p.ctypes.data_as(P(c_int)), s.ctypes.data_as(P(c_int)),
                                     len(t), out.ctypes.data) != len(t):
             raise HipError(f"sml_gpu_step_multi: {lib().sml_gpu_last_error().decode(errors='replace')}")
