@@ -62,6 +62,18 @@ sml_hip_mat * sml_hip_mat_from_q4k(const void * blocks, int rows, int cols);
 // that is not whole blocks.
 int           sml_hip_q4k_repack(const void * blocks, int rows, int cols, uint8_t * plane, uint16_t * sd,
                                  uint8_t * sq, uint16_t * md, uint8_t * mq);
+// A matrix given as GGUF Q5_K blocks (ggml's block_q5_K: 176 bytes per 256
+// weights, rows of cols/256 blocks), repacked on the host into a FLAT Q5
+// record: Q4_K's fields, the low nibbles as the 4-bit plane and the fifth
+// bits as the 1-bit plane. The arithmetic is ggml's weight
+// d*sc*(q + 16*h) - dmin*m exactly. No counterpart in the reference (GGUF
+// goes through transformers there, tooling/sml_gguf.py:1-35).
+sml_hip_mat * sml_hip_mat_from_q5k(const void * blocks, int rows, int cols);
+// The host repack alone (no GPU): 4-bit plane [rows][cols/2], 1-bit plane
+// [rows][cols/8], sd and md [rows][cols/256], sq and mq [rows][cols/32].
+// Returns 0, or -1 on a shape that is not whole blocks.
+int           sml_hip_q5k_repack(const void * blocks, int rows, int cols, uint8_t * plane4, uint8_t * plane1,
+                                 uint16_t * sd, uint8_t * sq, uint16_t * md, uint8_t * mq);
 void          sml_hip_mat_free(sml_hip_mat * m);
 int           sml_hip_mat_info(const sml_hip_mat * m, int * rows, int * cols, int * nbits);
 // Bytes the matrix occupies in HBM (codes + fields): what one GEMV streams.

@@ -58,6 +58,7 @@ def oracle():
             "orc_argmax": (c_int, [c_void_p, c_int]),
             "orc_expf_published": (c_float, [c_float]),
             "orc_q4k_dequant_row": (None, [c_void_p, c_int, c_void_p]),
+            "orc_q5k_dequant_row": (None, [c_void_p, c_int, c_void_p]),
             "orc_gptq_dequant_row_gidx": (None, [c_void_p] * 4 + [c_int] * 5 + [c_void_p]),
             "orc_gptq_matvec_gidx": (None, [c_void_p] * 4 + [c_int] * 4 + [c_void_p, c_void_p]),
             "orc_expf_mismatches": (ctypes.c_long, [ctypes.c_uint]),
@@ -602,6 +603,29 @@ def q4k_random_blocks(rows, cols, seed):
         blk[i, 4:16] = q4k_pack_scales(rng.integers(0, 64, 8), rng.integers(0, 64, 8))
     blk[:, 16:] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
     return blk.reshape(rows, cols // 256, 144)
+
+
+def q5k_dequant(blocks, rows, cols):
+    """GGUF Q5_K blocks [rows][cols/256][176] to float32 weights [rows][cols]
+    by the published formula (orc_q5k_dequant_row)."""
+    bl = np.ascontiguousarray(blocks, np.uint8).reshape(rows, -1)
+    out = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        oracle().orc_q5k_dequant_row(bl[r].ctypes.data, cols, out[r].ctypes.data)
+    return out
+
+
+def q5k_random_blocks(rows, cols, seed):
+    """Random Q5_K blocks: Q4_K's fields drawn as in q4k_random_blocks, then
+    random fifth bits (qh) and low nibbles."""
+    rng = np.random.default_rng(seed)
+    k4 = q4k_random_blocks(rows, cols, seed).reshape(-1, 144)
+    nb = k4.shape[0]
+    blk = np.zeros((nb, 176), np.uint8)
+    blk[:, 0:16] = k4[:, 0:16]
+    blk[:, 16:48] = rng.integers(0, 256, (nb, 32), dtype=np.uint8)
+    blk[:, 48:] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
+    return blk.reshape(rows, cols // 256, 176)
 
 
 class FlatView:

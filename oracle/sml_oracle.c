@@ -922,3 +922,28 @@ void orc_q4k_dequant_row(const uint8_t * blocks, int cols, float * out) {
         }
     }
 }
+
+// ggml's block_q5_K and dequantize_row_q5_K: Q4_K's d, dmin and scale bytes,
+// then qh[32] (bit j of byte l: the fifth bit of weight l of sub-block j) and
+// the low nibbles qs[128] in Q4_K's order; weight d*sc*(q + 16*h) - dmin*m
+void orc_q5k_dequant_row(const uint8_t * blocks, int cols, float * out) {
+    for (int b = 0; b < cols / 256; b++) {
+        const uint8_t * blk = blocks + (size_t) b * 176;
+        uint16_t dh, mh;
+        memcpy(&dh, blk, 2);
+        memcpy(&mh, blk + 2, 2);
+        const float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
+        const uint8_t * qh = blk + 16, * q = blk + 48;
+        float * y = out + (size_t) b * 256;
+        for (int c = 0; c < 4; c++) {
+            float s1, m1, s2, m2;
+            q4k_unpack_scale(blk + 4, 2 * c, &s1, &m1);
+            q4k_unpack_scale(blk + 4, 2 * c + 1, &s2, &m2);
+            const float d1 = d * s1, n1 = dmin * m1, d2 = d * s2, n2 = dmin * m2;
+            for (int l = 0; l < 32; l++) y[l] = d1 * (float) ((q[l] & 15) + ((qh[l] >> (2 * c)) & 1 ? 16 : 0)) - n1;
+            for (int l = 0; l < 32; l++) y[32 + l] = d2 * (float) ((q[l] >> 4) + ((qh[l] >> (2 * c + 1)) & 1 ? 16 : 0)) - n2;
+            q += 32;
+            y += 64;
+        }
+    }
+}

@@ -120,6 +120,7 @@ void orc_awq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const 
 // per 64 weights, sub-blocks 2c and 2c+1 take the low and high nibbles of the
 // same 32 code bytes, y = (d*sc)*q - dmin*m.
 void orc_q4k_dequant_row(const uint8_t * blocks, int cols, float * out);
+void orc_q5k_dequant_row(const uint8_t * blocks, int cols, float * out);
 
 // ---------------------------------------------------------------- expf restated
 // The C library's expf (glibc 2.35, x86-64 with FMA) from its published

@@ -63,6 +63,9 @@ _SIGS = [
     ("sml_hip_mat_from_file", c_void_p, [c_char_p, c_char_p]),
     ("sml_hip_mat_from_q4k", c_void_p, [c_void_p, c_int, c_int]),
     ("sml_hip_q4k_repack", c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("sml_hip_mat_from_q5k", c_void_p, [c_void_p, c_int, c_int]),
+    ("sml_hip_q5k_repack", c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                   c_void_p]),
     ("sml_hip_mat_free", None, [c_void_p]),
     ("sml_hip_mat_info", c_int, [c_void_p, P(c_int), P(c_int), P(c_int)]),
     ("sml_hip_mat_bytes", c_size_t, [c_void_p]),
@@ -203,6 +206,15 @@ class Mat:
         if b.size != rows * (cols // 256) * 144:
             raise ValueError("Q4_K blocks do not match the shape")
         return cls(lib().sml_hip_mat_from_q4k(b.ctypes.data, rows, cols))
+
+    @classmethod
+    def from_q5k(cls, blocks, rows, cols):
+        """GGUF Q5_K blocks (uint8, rows x cols/256 x 176 bytes) repacked into
+        the FLAT Q5 layout and uploaded."""
+        b = np.ascontiguousarray(blocks, np.uint8)
+        if b.size != rows * (cols // 256) * 176:
+            raise ValueError("Q5_K blocks do not match the shape")
+        return cls(lib().sml_hip_mat_from_q5k(b.ctypes.data, rows, cols))
 
     def free(self):
         if self.h:
@@ -438,3 +450,22 @@ def q4k_repack(blocks, rows, cols):
                                 md.ctypes.data, mq.ctypes.data) != 0:
         raise ValueError("Q4_K blocks do not match the shape")
     return plane, sd, md, sq, mq
+
+
+def q5k_repack(blocks, rows, cols):
+    """The host repack of GGUF Q5_K blocks into FLAT Q5 arrays (no GPU):
+    ([4-bit plane [rows][cols/2], 1-bit plane [rows][cols/8]], sd, md
+    [rows][cols/256] fp16 bits, sq, mq [rows][cols/32])."""
+    b = np.ascontiguousarray(blocks, np.uint8)
+    nb = cols // 256
+    p4 = np.zeros((rows, cols // 2), np.uint8)
+    p1 = np.zeros((rows, cols // 8), np.uint8)
+    sd = np.zeros((rows, nb), np.uint16)
+    md = np.zeros((rows, nb), np.uint16)
+    sq = np.zeros((rows, cols // 32), np.uint8)
+    mq = np.zeros((rows, cols // 32), np.uint8)
+    if b.size != rows * nb * 176 or lib().sml_hip_q5k_repack(b.ctypes.data, rows, cols, p4.ctypes.data,
+                                                              p1.ctypes.data, sd.ctypes.data, sq.ctypes.data,
+                                                              md.ctypes.data, mq.ctypes.data) != 0:
+        raise ValueError("Q5_K blocks do not match the shape")
+    return [p4, p1], sd, md, sq, mq

@@ -180,6 +180,19 @@ static void q4k_scale_min(const uint8_t * s, int j, uint8_t * sc, uint8_t * mn) 
     }
 }
 
+// d, dmin and the eight (scale, min) pairs of one K-quant block (Q4_K and
+// Q5_K share them) into superblock idx's FLAT fields
+static void kq_fields(const uint8_t * blk, size_t idx, uint16_t * sd, uint8_t * sq, uint16_t * md, uint8_t * mq) {
+    memcpy(&sd[idx], blk, 2);
+    memcpy(&md[idx], blk + 2, 2);
+    for (int j = 0; j < 8; j++) {
+        uint8_t sc, mn;
+        q4k_scale_min(blk + 4, j, &sc, &mn);
+        sq[idx * 8 + j] = sc;
+        mq[idx * 8 + j] = (uint8_t) (127 - mn);
+    }
+}
+
 int sml_hip_q4k_repack(const void * blocks, int rows, int cols, uint8_t * plane, uint16_t * sd, uint8_t * sq,
                        uint16_t * md, uint8_t * mq) {
     if (!blocks || rows <= 0 || cols <= 0 || cols % 256 || !plane || !sd || !sq || !md || !mq) return -1;
@@ -187,15 +200,37 @@ int sml_hip_q4k_repack(const void * blocks, int rows, int cols, uint8_t * plane,
     for (size_t r = 0; r < (size_t) rows; r++)
         for (size_t b = 0; b < nb; b++) {
             const uint8_t * blk = (const uint8_t *) blocks + (r * nb + b) * Q4K_BLOCK;
-            memcpy(&sd[r * nb + b], blk, 2);
-            memcpy(&md[r * nb + b], blk + 2, 2);
-            for (int j = 0; j < 8; j++) {
-                uint8_t sc, mn;
-                q4k_scale_min(blk + 4, j, &sc, &mn);
-                sq[(r * nb + b) * 8 + j] = sc;
-                mq[(r * nb + b) * 8 + j] = (uint8_t) (127 - mn);
-            }
+            kq_fields(blk, r * nb + b, sd, sq, md, mq);
             memcpy(plane + (r * nb + b) * 128, blk + 16, 128);
+        }
+    return 0;
+}
+
+// GGUF Q5_K (ggml's block_q5_K, 176 bytes per 256 weights): d, dmin and the
+// twelve scale bytes as in Q4_K, then qh (32 bytes; bit j of byte l is the
+// fifth code bit of weight l of sub-block j) and the 128 bytes of low nibbles
+// in Q4_K's order. A weight is d*sc_j*(q + 16*h) - dmin*m_j, the two-level
+// FLAT Q5 record with Q4_K's fields: its 4-bit plane is the nibbles (already
+// FLAT quads) and its 1-bit plane the fifth bits, four bytes per group with
+// weight l of the group in bit l%8 of byte l/8.
+#define Q5K_BLOCK 176
+int sml_hip_q5k_repack(const void * blocks, int rows, int cols, uint8_t * plane4, uint8_t * plane1, uint16_t * sd,
+                       uint8_t * sq, uint16_t * md, uint8_t * mq) {
+    if (!blocks || rows <= 0 || cols <= 0 || cols % 256 || !plane4 || !plane1 || !sd || !sq || !md || !mq) return -1;
+    const size_t nb = (size_t) cols / 256;
+    for (size_t r = 0; r < (size_t) rows; r++)
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t * blk = (const uint8_t *) blocks + (r * nb + b) * Q5K_BLOCK;
+            const uint8_t * qh = blk + 16;
+            kq_fields(blk, r * nb + b, sd, sq, md, mq);
+            memcpy(plane4 + (r * nb + b) * 128, blk + 48, 128);
+            uint8_t * p1 = plane1 + (r * nb + b) * 32;
+            for (int j = 0; j < 8; j++)
+                for (int by = 0; by < 4; by++) {
+                    uint8_t v = 0;
+                    for (int k = 0; k < 8; k++) v |= (uint8_t) (((qh[8 * by + k] >> j) & 1) << k);
+                    p1[4 * j + by] = v;
+                }
         }
     return 0;
 }
@@ -223,6 +258,33 @@ sml_hip_mat * sml_hip_mat_from_q4k(const void * blocks, int rows, int cols) {
     sml_hip_mat * m = mat_upload(planes, sd, sq, md, mq, rows, cols, 4, 0, 0);
     hx.jb = outer;
     free(plane); free(sq); free(mq); free(sd); free(md);
+    HX_LEAVE();
+    return m;
+}
+
+sml_hip_mat * sml_hip_mat_from_q5k(const void * blocks, int rows, int cols) {
+    OP_BEGIN(NULL);
+    if (!blocks || rows <= 0 || cols <= 0 || cols % 256) hx_failf("Q5_K matrix %dx%d: not a whole number of blocks", rows, cols);
+    const size_t R = (size_t) rows, nb = (size_t) cols / 256;
+    uint8_t * p4 = malloc(R * nb * 128), * p1 = malloc(R * nb * 32), * sq = malloc(R * nb * 8), * mq = malloc(R * nb * 8);
+    uint16_t * sd = malloc(R * nb * 2), * md = malloc(R * nb * 2);
+    if (!p4 || !p1 || !sq || !mq || !sd || !md) {
+        free(p4); free(p1); free(sq); free(mq); free(sd); free(md);
+        hx_failf("out of host memory");
+    }
+    sml_hip_q5k_repack(blocks, rows, cols, p4, p1, sd, sq, md, mq);
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) {
+        hx.jb = outer;
+        free(p4); free(p1); free(sq); free(mq); free(sd); free(md);
+        longjmp(*outer, 1);
+    }
+    hx.jb = &jb;
+    const uint8_t * planes[4] = { p4, p1, NULL, NULL };
+    sml_hip_mat * m = mat_upload(planes, sd, sq, md, mq, rows, cols, 5, 0, 0);
+    hx.jb = outer;
+    free(p4); free(p1); free(sq); free(mq); free(sd); free(md);
     HX_LEAVE();
     return m;
 }

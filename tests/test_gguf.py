@@ -1,4 +1,5 @@
-"""GGUF Q4_K blocks (ggml's block_q4_K) repacked into the FLAT Q4 layout.
+"""GGUF Q4_K and Q5_K blocks (ggml's block_q4_K, block_q5_K) repacked into
+the FLAT Q4 and Q5 layouts.
 
 The reference reads GGUF only through transformers into fp16, then
 re-quantizes (tooling/sml_gguf.py:1-35), and `gguf` is not importable here;
@@ -9,7 +10,10 @@ weight d*sc*q - dmin*m is the FLAT record's step*q + min with sd = d, sq = sc,
 md = dmin, mq = 127 - m, and the 128 code bytes are already FLAT quads, so the
 repack (sml_hip_q4k_repack) moves bytes and fields only: after it the SSF
 dequantization equals the published formula bit for bit, and the GPU's codes
-are the block's nibbles.
+are the block's nibbles. Q5_K adds a fifth code bit per weight (qh: bit j of
+byte l for weight l of sub-block j) to the same fields and nibbles; it
+becomes the FLAT Q5 record's 1-bit plane, pinned the same way against
+dequantize_row_q5_K (orc_q5k_dequant_row).
 """
 import numpy as np
 import pytest
@@ -71,18 +75,89 @@ def test_q4k_repack_refuses_partial_blocks():
         sa.q4k_repack(np.zeros(144, np.uint8), 1, 128)
 
 
+def known_q5_block(qh):
+    """known_block's fields and nibbles with the given 32 qh bytes."""
+    blk = np.zeros(176, np.uint8)
+    k4 = known_block()
+    blk[0:16] = k4[0:16]
+    blk[16:48] = qh
+    blk[48:] = k4[16:]
+    return blk
+
+
+def test_q5k_known_answers():
+    """Values worked out by hand: code (i % 32) % 16 plus 16 where the fifth
+    bit is set, weight (j+1)*code - 0.5*j for sub-block j = i // 32."""
+    # every odd weight of every sub-block has its fifth bit
+    w = ob.q5k_dequant(known_q5_block(np.where(np.arange(32) % 2 == 1, 0xFF, 0).astype(np.uint8)), 1, 256)[0]
+    for i, want in ((0, 0.0), (17, 17.0), (31, 31.0), (40, 15.5), (63, 61.5), (64, -1.0),
+                    (127, 122.5), (200, 53.0), (255, 244.5)):
+        assert w[i] == want, (i, w[i], want)
+    # qh[l] = 1 << (l % 8): weight l of sub-block j has it only where j == l % 8
+    w = ob.q5k_dequant(known_q5_block((1 << (np.arange(32) % 8)).astype(np.uint8)), 1, 256)[0]
+    for i, want in ((0, 16.0), (1, 1.0), (33, 33.5), (34, 3.5), (231, 180.5), (232, 60.5), (255, 244.5)):
+        assert w[i] == want, (i, w[i], want)
+    # no fifth bits, high nibbles 15 - (l % 16): odd sub-blocks read the high nibble
+    blk = known_q5_block(np.zeros(32, np.uint8))
+    l = np.arange(32) % 16
+    blk[48:] = np.tile(l | ((15 - l) << 4), 4)
+    w = ob.q5k_dequant(blk, 1, 256)[0]
+    for i, want in ((0, 0.0), (32, 29.5), (47, -0.5), (64, -1.0), (96, 58.5), (255, -3.5)):
+        assert w[i] == want, (i, w[i], want)
+
+
+def test_q5k_repack_fields_and_bits():
+    """Q4_K's fields and nibbles carry over unchanged; the 1-bit plane holds
+    bit j of qh[l] as weight l of group j."""
+    rng = np.random.default_rng(5)
+    blk = known_q5_block(rng.integers(0, 256, 32, dtype=np.uint8))
+    sc, mn = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+    blk[4:16] = ob.q4k_pack_scales(sc, mn)
+    (p4, p1), sd, md, sq, mq = sa.q5k_repack(blk, 1, 256)
+    assert (sq[0] == sc).all() and (mq[0] == 127 - mn).all()
+    assert sd[0, 0] == blk[0:2].view(np.uint16)[0] and md[0, 0] == blk[2:4].view(np.uint16)[0]
+    assert (p4[0] == blk[48:]).all()
+    bits = np.unpackbits(p1[0], bitorder="little").reshape(8, 32)
+    want = (blk[16:48][None, :] >> np.arange(8)[:, None]) & 1
+    assert (bits == want).all()
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(3, 256, 1), (17, 2048, 2), (64, 4096, 3)])
+def test_q5k_repack_equals_published_formula(rows, cols, seed):
+    """Random blocks: the repacked FLAT Q5 record's dequantization equals
+    dequantize_row_q5_K bit for bit, row by row."""
+    blocks = ob.q5k_random_blocks(rows, cols, seed)
+    v = ob.FlatView(*sa.q5k_repack(blocks, rows, cols), rows, cols, nbits=5)
+    want = ob.q5k_dequant(blocks, rows, cols)
+    for r in range(rows):
+        np.testing.assert_array_equal(v.dequant(r), want[r], err_msg=f"row {r}")
+
+
+def test_q5k_repack_refuses_partial_blocks():
+    with pytest.raises(ValueError):
+        sa.q5k_repack(np.zeros(176, np.uint8), 1, 128)
+
+
+KINDS = {
+    "q4k": (ob.q4k_random_blocks, sa.q4k_repack, sa.Mat.from_q4k, ob.q4k_dequant, 4),
+    "q5k": (ob.q5k_random_blocks, sa.q5k_repack, sa.Mat.from_q5k, ob.q5k_dequant, 5),
+}
+
+
 @pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["q4k", "q5k"])
 @pytest.mark.parametrize("rows,cols,seed", [(4096, 4096, 11), (1000, 14336, 12)])
-def test_q4k_on_the_gpu(rows, cols, seed):
-    """Uploaded as Q4_K: the unpacked codes are the blocks' nibbles (bit for
-    bit); the GEMV and the SwiGLU GEMV on an int8 activation agree with the
-    oracle's GEMV on the repacked record and with a double-precision product
-    of the published dequantization (1e-3 of the largest output, rel-RMS
-    1e-4)."""
+def test_kquant_on_the_gpu(kind, rows, cols, seed):
+    """Uploaded as Q4_K or Q5_K: the unpacked codes are the blocks' codes
+    (bit for bit); the GEMV and the SwiGLU GEMV on an int8 activation agree
+    with the oracle's GEMV on the repacked record and with a
+    double-precision product of the published dequantization (1e-3 of the
+    largest output, rel-RMS 1e-4)."""
+    gen, repack, upload, dequant, nbits = KINDS[kind]
     sa.init(0)
-    blocks = ob.q4k_random_blocks(rows, cols, seed)
-    m = sa.Mat.from_q4k(blocks, rows, cols)
-    v = ob.FlatView(*sa.q4k_repack(blocks, rows, cols), rows, cols)
+    blocks = gen(rows, cols, seed)
+    m = upload(blocks, rows, cols)
+    v = ob.FlatView(*repack(blocks, rows, cols), rows, cols, nbits=nbits)
     for r0 in (0, rows // 2, rows - 3):
         got = sa.unpack(m, r0, 3)
         for i in range(3):
@@ -98,15 +173,15 @@ def test_q4k_on_the_gpu(rows, cols, seed):
     got = y.read(np.float32)
     want = v.matvec(q, s, u)
     xq = (q.astype(np.float64).reshape(-1, 32) * s.astype(np.float64)[:, None]).reshape(-1)
-    brute = ob.q4k_dequant(blocks, rows, cols).astype(np.float64) @ xq
+    brute = dequant(blocks, rows, cols).astype(np.float64) @ xq
     for ref, what in ((want, "oracle GEMV"), (brute, "published dequant x activation")):
         err = np.abs(got - ref)
         assert err.max() <= 1e-3 * np.abs(ref).max(), what
         assert np.sqrt((err ** 2).mean() / (ref ** 2).mean()) <= 1e-4, what
-    up = sa.Mat.from_q4k(ob.q4k_random_blocks(rows, cols, seed + 100), rows, cols)
+    up = upload(gen(rows, cols, seed + 100), rows, cols)
     h = sa.DevBuf(rows * 4)
     sa.matvec_swiglu(m, up, act, h)
-    vu = ob.FlatView(*sa.q4k_repack(ob.q4k_random_blocks(rows, cols, seed + 100), rows, cols), rows, cols)
+    vu = ob.FlatView(*repack(gen(rows, cols, seed + 100), rows, cols), rows, cols, nbits=nbits)
     g, uu = want.copy(), vu.matvec(q, s, u)
     ob.oracle().orc_silu_mul(g.ctypes.data, uu.ctypes.data, rows)
     hg = h.read(np.float32)
