@@ -166,6 +166,10 @@ typedef struct {
     // sml_attnf (prompt flash form): KV positions per split (grid z), a
     // multiple of 64
     int fchunk;
+    // query-head subsets per kv head (the 8-wave kernels; 0 or 1: none):
+    // grid y = n_kv * nsub, workgroup y takes kv head y / nsub and its query
+    // heads (y % nsub) * REP .. +REP-1 (REP = n_head / n_kv / nsub)
+    int nsub;
 } sml_kattn;
 
 // Decode attention in the reference's float order (exact mode): RoPE of q and

@@ -1246,7 +1246,12 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     static_assert(PPL >= 1 && PPL * PS == CH, "a split covers whole rounds of positions");
     __shared__ float red[NW][REP][HD];
     __shared__ float wm[NW][REP], wl[NW][REP];
-    const int kh = blockIdx.y, split = blockIdx.x, tid = threadIdx.x;
+    // kv head kh; query heads qh0 .. qh0+REP-1 (a subset of the kv head's
+    // when nsub > 1: each head's arithmetic is the same whichever workgroup
+    // holds it, so the split into subsets changes no bit)
+    const int nsub = CHUNK || a.nsub < 1 ? 1 : a.nsub;
+    const int kh = (int) blockIdx.y / nsub, qh0 = kh * REP * nsub + ((int) blockIdx.y % nsub) * REP;
+    const int split = blockIdx.x, tid = threadIdx.x;
     const int wave = tid >> 6, grp = tid >> 4, l16 = tid & 15, kvd = a.n_kv * HD;
     // the workgroup's entries b0..b1-1: one, or (tpw > 1) consecutive
     // positions of one sequence, which share this split's K/V tile
@@ -1259,7 +1264,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     const int half = HD / 2;
     float nq[REP][8], nk[8], nv[8], ncs[8], nsn[8];
     auto fetch_qkv = [&](int b) {
-        const float * aq = a.q + (size_t) b * a.qkv_stride + (size_t) kh * REP * HD + l16 * 8;
+        const float * aq = a.q + (size_t) b * a.qkv_stride + (size_t) qh0 * HD + l16 * 8;
         const float * ak = a.k + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
         const float * av = a.v + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
         #pragma unroll
@@ -1287,7 +1292,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int) gridDim.x - 1;
         __syncthreads();
         if (!last) return;
-        for (int t = wave; t < 2 * REP; t += NW) merge_head<true>(a, b, kh * REP + t / 2, (t & 1) * 64 + (tid & 63));
+        for (int t = wave; t < 2 * REP; t += NW) merge_head<true>(a, b, qh0 + t / 2, (t & 1) * 64 + (tid & 63));
         if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     // a split past every entry's position (they increase) writes empty
@@ -1295,7 +1300,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     // unconditional below, so the compiler's waits stay partial.
     auto empty = [&](int b) {
         float2 * pml = (float2 *) (a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2) +
-                                   (size_t) a.n_head * a.nsplit * HD) + (size_t) kh * REP * a.nsplit;
+                                   (size_t) a.n_head * a.nsplit * HD) + (size_t) qh0 * a.nsplit;
         if (tid < REP) {
             if (fold) st_dev2(pml + (size_t) tid * a.nsplit + split, make_float2(-INFINITY, 0.0f));
             else pml[(size_t) tid * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
@@ -1345,8 +1350,8 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     const int pos = a.pos[b], T = pos + 1;
     // partials of entry b: V sums [head][split][HD], then (max, sum) [head][split]
     float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
-    float * po = blk + (size_t) kh * REP * a.nsplit * HD;
-    float2 * pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) kh * REP * a.nsplit;
+    float * po = blk + (size_t) qh0 * a.nsplit * HD;
+    float2 * pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) qh0 * a.nsplit;
     if (t0 >= T) {
         empty(b);
         continue;
@@ -1364,7 +1369,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         knew[e] = (unsigned) f2h(kn[2 * e]) | ((unsigned) f2h(kn[2 * e + 1]) << 16);
         vnew[e] = (unsigned) f2h(vn[2 * e]) | ((unsigned) f2h(vn[2 * e + 1]) << 16);
     }
-    if (!a.kv_written && t0 <= pos && pos < t1 && tid < 16) {
+    if (!a.kv_written && t0 <= pos && pos < t1 && tid < 16 && qh0 == kh * REP * nsub) {
         *(GLOBAL v4u *) (kcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = knew;
         *(GLOBAL v4u *) (vcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = vnew;
     }

@@ -349,3 +349,34 @@ def test_position_buckets_equal_whole_context_launches(model, request, monkeypat
             d.close()
     for i, (a, b) in enumerate(zip(outs["1"], outs["0"])):
         np.testing.assert_array_equal(a, b, err_msg=f"output {i}")
+
+
+@pytest.mark.parametrize("model", ["tiny", "qwenish"])
+def test_query_head_subsets_give_the_same_bits(model, request, monkeypatch):
+    """Decode attention shares a kv head's query heads out over several
+    workgroups when the model has few kv heads (automatic: up to 256
+    workgroups; SML_ATTN_SUB sets the count). Each head's arithmetic does not
+    depend on the workgroup that holds it, so steps at short and long
+    positions and generated tokens equal the one-workgroup-per-kv-head launch
+    bit for bit, for every subset count that divides the group."""
+    path = request.getfixturevalue(model)
+    V, rep = (2000, 2) if model == "tiny" else (32000, 6)
+    rng = np.random.default_rng(9)
+    ids = rng.integers(0, V, 1100).astype(np.int32)
+    outs = {}
+    for sub in ["1", ""] + [str(d) for d in range(2, rep + 1) if rep % d == 0]:
+        monkeypatch.setenv("SML_ATTN_SUB", sub)
+        print(f"query-head subsets {sub or 'automatic'}", flush=True)
+        d = sa.Decoder(path, n_ctx=2048)
+        try:
+            got = [d.prefill(ids[:40], 0, V)]
+            got += [d.step(int(ids[i]), i, V).copy() for i in range(40, 48)]
+            got.append(d.prefill(ids[48:1090], 48, V))
+            got += [d.step(int(ids[i]), i, V).copy() for i in range(1090, 1100)]
+            got.append(np.array(d.generate(int(ids[-1]), 1100, 4), np.float32))
+            outs[sub] = got
+        finally:
+            d.close()
+    for sub, got in outs.items():
+        for i, (a, b) in enumerate(zip(got, outs["1"])):
+            np.testing.assert_array_equal(a, b, err_msg=f"subsets {sub or 'automatic'}, output {i}")
