@@ -246,6 +246,12 @@ typedef struct {
     // desc_act files: the input columns were reordered at upload so each
     // group's are contiguous; device input i is input perm[i] (NULL: identity)
     const int32_t * perm;
+    // when not NULL, one counter per output block (grid x), zero between
+    // launches: each workgroup stores its partials at device scope and counts
+    // itself in, and the block's last one adds the slices into y in slice
+    // order, as sml_gptq_reduce does, then clears the counter. One launch at
+    // a time per matrix (the partials are the matrix's too).
+    int * cnt;
 } sml_kgptq;
 
 typedef struct {

@@ -2179,8 +2179,9 @@ extern "C" __global__ __launch_bounds__(256) void sml_copy_stream(const sml_kcop
 // a wave streams 256 outputs of one group of 128 inputs (16 loads per lane,
 // all issued before any use). The activation stays fp32, staged per wave
 // in LDS and read as broadcasts: per group, s * (sum q*x - z * sum x). The GPTQ_WAVES waves of a workgroup cover
-// consecutive groups, summed in LDS into one partial per output;
-// sml_gptq_reduce adds the partials in a fixed order.
+// consecutive groups, summed in LDS into one partial per output; the last
+// workgroup of each output block (or, without counters, sml_gptq_reduce)
+// adds the partials in slice order.
 #define GPTQ_WAVES 8
 // OPL outputs per lane (4: 256 outputs per wave, 16-byte weight loads; 2:
 // 128 per wave, 8-byte loads and twice the waves for the same matrix)
@@ -2251,15 +2252,43 @@ __device__ void gptq_body(const sml_kgptq & a) {
         red[w][lane * OPL + j] = gv ? s * (acc[j] - z * sx) : 0.0f;
     }
     __syncthreads();
+    const bool fold = a.cnt != nullptr;
     if (tid < 64 && ov) {
         #pragma unroll
         for (int j = 0; j < OPL; j++) {
             float v = red[0][lane * OPL + j];
             #pragma unroll
             for (int k = 1; k < GPTQ_WAVES; k++) v += red[k][lane * OPL + j];
-            a.part[(size_t) blockIdx.y * a.rows + o + j] = v;
+            float * pp = a.part + (size_t) blockIdx.y * a.rows + o + j;
+            if (fold) st_dev(pp, v);
+            else *pp = v;
         }
     }
+    if (!fold) return;
+    // 4. the output block's last workgroup (every slice's partials stored
+    // at device scope before it counts itself in) adds the slices in slice
+    // order, the reduce kernel's arithmetic, and clears the counter
+    __shared__ int last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(a.cnt + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int) gridDim.y - 1;
+    __syncthreads();
+    if (!last) return;
+    for (int i = tid; i < 64 * OPL; i += 64 * GPTQ_WAVES) {
+        const int oo = blockIdx.x * (64 * OPL) + i;
+        if (oo >= a.rows) continue;
+        float v = 0.0f;
+        for (int s0 = 0; s0 < a.nslice; s0 += 8) {
+            float p[8];
+            #pragma unroll
+            for (int k = 0; k < 8; k++) p[k] = s0 + k < a.nslice ? ld_part<true>(a.part + (size_t) (s0 + k) * a.rows + oo) : 0.0f;
+            #pragma unroll
+            for (int k = 0; k < 8; k++) v += p[k];
+        }
+        a.y[oo] = v;
+    }
+    if (tid == 0) __hip_atomic_store(a.cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 extern "C" __global__ __launch_bounds__(64 * GPTQ_WAVES) void sml_gptq_gemv(const sml_kgptq a) { gptq_body<4>(a); }
 extern "C" __global__ __launch_bounds__(64 * GPTQ_WAVES) void sml_gptq_gemv2(const sml_kgptq a) { gptq_body<2>(a); }

@@ -971,6 +971,7 @@ struct sml_hip_gptq {
     uint32_t * qweight, * qzeros;
     uint16_t * scales;
     float * part;
+    int * cnt;                   // output blocks' counters (after the partials), zero between launches
     int32_t * perm;              // desc_act: device input i is input perm[i], or NULL
     int rows, cols, zero_add;
     size_t bytes;
@@ -997,7 +998,12 @@ sml_hip_gptq * sml_hip_gptq_upload(const int32_t * qweight, const int32_t * qzer
     m->qweight = hx_malloc(bw);
     m->qzeros = hx_malloc(bz);
     m->scales = hx_malloc(bs);
-    m->part = hx_malloc(nslice * R * 4);
+    // the partials, then one counter per output block of 128 (the
+    // 2-per-lane launch's; the 4-per-lane one uses the first half)
+    const size_t nblk = (R + 127) / 128;
+    m->part = hx_malloc(nslice * R * 4 + nblk * 4);
+    m->cnt = (int *) (m->part + nslice * R);
+    HX(hipMemset(m->cnt, 0, nblk * 4));
     HX(hipMemcpy(m->qweight, qweight, bw, hipMemcpyHostToDevice));
     HX(hipMemcpy(m->qzeros, qzeros, bz, hipMemcpyHostToDevice));
     HX(hipMemcpy(m->scales, scales, bs, hipMemcpyHostToDevice));
@@ -1137,9 +1143,13 @@ static void op_gptq(hipStream_t st, const sml_hip_gptq * m, const float * x, flo
     // more of the weight stream overlaps the float dot products (4096 x 14336:
     // 14.8 -> 11.4 us; 1 per lane measured the same as 2)
     const int opl = env_int("SML_GPTQ_OPL", 2) == 4 ? 4 : 2;
+    // the slices' sum runs in each output block's last workgroup
+    // (SML_GPTQ_FOLD=0: in a second launch, sml_gptq_reduce; the same bits)
+    const int fold = env_int("SML_GPTQ_FOLD", 1) != 0;
+    a.cnt = fold ? m->cnt : NULL;
     hx_launch(opl == 4 ? "sml_gptq_gemv" : "sml_gptq_gemv2", (unsigned) ((m->rows + 64 * opl - 1) / (64 * opl)),
               (unsigned) a.nslice, 64 * GPTQ_GROUPS_PER_WG, 0, st, &a);
-    hx_launch("sml_gptq_reduce", (unsigned) ((m->rows + 255) / 256), 1, 256, 0, st, &a);
+    if (!fold) hx_launch("sml_gptq_reduce", (unsigned) ((m->rows + 255) / 256), 1, 256, 0, st, &a);
 }
 
 int sml_hip_gptq_matvec(const sml_hip_gptq * m, const float * x, float * y) {

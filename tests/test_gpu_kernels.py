@@ -340,6 +340,30 @@ def test_gptq_gemv(rows, cols):
     close(y.read(np.float32), ob.gptq_matvec(qw, qz, sc, rows, cols, x), f"gptq {rows}x{cols}")
 
 
+@pytest.mark.parametrize("rows,cols", [(1000, 1152), (4096, 14336), (14336, 4096)])
+def test_gptq_folded_reduce_equals_reduce_launch(rows, cols, monkeypatch):
+    """The split-K sum done by each output block's last workgroup (counters
+    cleared by that workgroup) equals the separate sml_gptq_reduce launch bit
+    for bit, at 2 and 4 outputs per lane, over several calls in a row on
+    different inputs (so every counter was left at zero)."""
+    from sheep_amd import gptq as gq
+    qw, qz, sc = gq.synth(rows, cols, seed=rows + 2 * cols)
+    m = gq.GptqMat(qw, qz, sc, rows, cols)
+    rng = np.random.default_rng(rows)
+    xs = [sa.DevBuf.of(rng.standard_normal(cols).astype(np.float32)) for _ in range(3)]
+    y = sa.DevBuf(rows * 4)
+    for opl in ("2", "4"):
+        monkeypatch.setenv("SML_GPTQ_OPL", opl)
+        for i, x in enumerate(xs):
+            got = {}
+            for fold in ("1", "0", "1"):
+                monkeypatch.setenv("SML_GPTQ_FOLD", fold)
+                m.matvec(x, y)
+                got.setdefault(fold, []).append(y.read(np.float32))
+            np.testing.assert_array_equal(got["1"][0], got["0"][0], err_msg=f"opl {opl} call {i}")
+            np.testing.assert_array_equal(got["1"][1], got["0"][0], err_msg=f"opl {opl} call {i} again")
+
+
 @pytest.mark.parametrize("rows,cols,zero_add", [(4096, 14336, 1), (1000, 1152, 0)])
 def test_gptq_unpack_bitexact(rows, cols, zero_add):
     from sheep_amd import gptq as gq
