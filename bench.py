@@ -563,6 +563,8 @@ def main():
     ap.add_argument("--cpu-leg", nargs="+", help=argparse.SUPPRESS)
     ap.add_argument("--decode-trace", metavar="MODEL", choices=("llama", "qwen"),
                     help="only decode the last --steps positions with direct launches (run under rocprofv3)")
+    ap.add_argument("--exact", action="store_true",
+                    help="with --decode-trace: open the decoder in exact mode (the reference's float order)")
     ap.add_argument("--trace-summary", metavar="DIR", help="per-kernel table of a --decode-trace kernel trace")
     ap.add_argument("--small-gemm", action="store_true", help="only time the 16-row small-M GEMMs")
     ap.add_argument("--gemv-sweep", action="store_true",
@@ -597,7 +599,7 @@ def main():
         elif a.ingest:
             res = {"ingest": ingest_leg()}
         elif a.decode_trace:
-            res = {"decode_trace": decode_trace(work, a.decode_trace, a.steps)}
+            res = {"decode_trace": decode_trace(work, a.decode_trace, a.steps, a.exact)}
         elif a.prompt_only >= 0:
             res = {"prompt_reading": prompt_only(work, a.prompt_only, a.prompt if a.prompt > 0 else 3960)}
         else:
@@ -608,28 +610,31 @@ def main():
     print(json.dumps(res), flush=True)
 
 
-def decode_trace(work, model="llama", steps=32):
+def decode_trace(work, model="llama", steps=32, exact=False):
     """For a kernel trace of the timed decode region only: the Llama-3-8B-
     (or Qwen2.5-1.5B-) shaped file opened with direct launches (SML_GRAPH=0:
-    the tracer sees each kernel), its prompt read at level 1 so the cache
-    holds N_CTX - steps positions, then a 16-byte copy (sml_copy_stream, the
-    marker) and `steps` greedy tokens at the last positions of the context."""
+    the tracer sees each kernel), its prompt read at level 1 (exact mode: a
+    token at a time) so the cache holds N_CTX - steps positions, then a
+    16-byte copy (sml_copy_stream, the marker) and `steps` greedy tokens at
+    the last positions of the context."""
     os.environ["SML_GRAPH"] = "0"
     spec = LLAMA if model == "llama" else QWEN
     path = os.path.join(work, f"{model}_trace.ssf")
     sa.synth_model(path, n_ctx_train=N_CTX, **spec)
-    dec = sa.Decoder(path, n_ctx=N_CTX)
+    dec = sa.Decoder(path, n_ctx=N_CTX, exact=exact)
     try:
         n = N_CTX - steps
         ids = np.random.default_rng(1003).integers(0, spec["n_vocab"], n).astype(np.int32)
+        t0 = time.perf_counter()
         lg = dec.prefill(ids, 0, spec["n_vocab"])
+        log(f"prompt of {n} ids read in {time.perf_counter() - t0:.1f} s")
         a, b = sa.DevBuf(64), sa.DevBuf(64)
         assert sa.lib().sml_hip_copy(b.ptr, a.ptr, 16) == 0
         sa.sync()
         dec.generate(int(np.argmax(lg)), n, steps)
     finally:
         dec.close()
-    return {"model": model, "decode_positions": f"{N_CTX - steps}..{N_CTX - 1}", "steps": steps}
+    return {"model": model, "exact": exact, "decode_positions": f"{N_CTX - steps}..{N_CTX - 1}", "steps": steps}
 
 
 def trace_summary(out_dir, steps):

@@ -4,12 +4,12 @@ width of their own, through libsmlhip.so.
 Mirrors the reference's route for a quantized copy: tooling/sml_unpack.py
 dequantizes it to float16 (dequant_gptq, dequant_awq), then the quantizer
 encodes every tensor (tooling/sml_quantize.py Quantizer.run / encode /
-_write), calling its fused C searches through tooling/sml_grid_c.py
-(asym_grid, field_search). The names and arguments here are those, and
-asym_grid / field_search return what sml_grid_c.py returns, so the quantizer
-can take this module in its place. Calibration (the GPTQ error feedback and
-activation importance) is the reference builder's and is not part of this
-path: importance weights are taken as given.
+_write). The quantizer's two fused C searches are not wrapped here: the
+library exports them under the reference's own C prototypes (sml_asym_grid,
+sml_field_search, sml/sml-quant.c:38-137), so the reference's loader binds
+libsmlhip.so in place of its own build. Calibration (the GPTQ error feedback
+and activation importance) is the reference builder's and is not part of
+this path: importance weights are taken as given.
 """
 import ctypes
 
@@ -72,58 +72,6 @@ def available():
         return True
     except (OSError, RuntimeError):
         return False
-
-
-# ---------------------------------------------------------------- the two searches (tooling/sml_grid_c.py)
-
-def _weights(imp, ng, group):
-    """Importance to the searches' weights, as tooling/sml_grid_c.py:31-36 does."""
-    if imp is None:
-        return None
-    wt = np.asarray(imp, dtype=np.float32).reshape(ng * group)
-    return np.ascontiguousarray(wt / max(float(wt.mean()), 1e-30) + np.float32(1e-6), dtype=np.float32)
-
-
-def grid_facs(ncand=20):
-    """The candidate range factors (tooling/sml_grid_c.py:41-42)."""
-    return np.ascontiguousarray(np.concatenate([np.linspace(0.6, 0.85, max(2, ncand // 3)),
-                                                np.linspace(0.88, 1.04, max(2, ncand - ncand // 3))]), np.float32)
-
-
-def asym_grid(wp, group, nbits, target_bits=None, imp=None, ncand=20, iters=3, refit=True):
-    """Per-group (min, step), rows x cols/group each, on the GPU.
-    follows tooling/sml_grid_c.py:38-51 (its call of sml_asym_grid)"""
-    rows, cols = wp.shape
-    ng = cols // group
-    rem = 0 if target_bits is None else nbits - target_bits
-    facs = grid_facs(ncand)
-    w = np.ascontiguousarray(wp, dtype=np.float32)
-    wt = _weights(imp, ng, group)
-    out_l = np.empty((rows, ng), np.float32)
-    out_s = np.empty((rows, ng), np.float32)
-    if _lib().sml_hip_asym_grid(_p(w), rows, cols, group, nbits, rem, _p(wt), _p(facs), len(facs), iters,
-                                int(bool(refit and not rem)), _p(out_l), _p(out_s)) != 0:
-        _err("asym_grid")
-    return out_l.astype(wp.dtype), out_s.astype(wp.dtype)
-
-
-def field_search(w, d16, q8, md16, mq8, group, gps, nmax, hi, moff, mmax, imp, radius=1):
-    """Each group's fields moved to the best neighbour, on the GPU; returns
-    (q8, mq8, effective steps, effective mins).
-    follows tooling/sml_grid_c.py:54-69 (its call of sml_field_search)"""
-    rows, cols = w.shape
-    ng = cols // group
-    dv = np.ascontiguousarray(np.repeat(d16.astype(np.float32), gps, axis=1)[:, :ng])
-    dm = np.ascontiguousarray(np.repeat(md16.astype(np.float32), gps, axis=1)[:, :ng])
-    q8o = np.ascontiguousarray(q8, dtype=np.int32).copy()
-    mq8o = np.ascontiguousarray(mq8, dtype=np.int32).copy()
-    wt = _weights(imp, ng, group)
-    if _lib().sml_hip_field_search(_p(np.ascontiguousarray(w, dtype=np.float32)), rows, cols, group, _p(dv), _p(dm),
-                                   _p(q8o), _p(mq8o), int(nmax), int(hi), int(moff), int(mmax), _p(wt),
-                                   int(radius)) != 0:
-        _err("field_search")
-    return (q8o.astype(np.uint8), mq8o.astype(np.uint8),
-            q8o.astype(np.float32) * dv, (mq8o.astype(np.float32) - moff) * dm)
 
 
 # ---------------------------------------------------------------- unpacking (tooling/sml_unpack.py)

@@ -28,16 +28,17 @@ def _data(rng, rows, cols):
 @pytest.mark.parametrize("group", [32, 64])
 @pytest.mark.parametrize("weighted", [False, True])
 def test_asym_grid_dropin_equals_reference_library(group, weighted):
+    # the library's sml_asym_grid, bound with the reference loader's argument
+    # types, against the reference's own build of sml-quant.c
     rng = np.random.default_rng(100 + group + weighted)
     rows, cols = 96, 2048
-    imp = rng.random(cols).astype(np.float32) ** 2 + 0.1 if weighted else None
-    wt = ingest._weights(imp, cols // group, group)
+    wt = (rng.random(cols).astype(np.float32) ** 2 + np.float32(0.1)) if weighted else None
     for name, w in _data(rng, rows, cols).items():
         for target in (None, 3):
             print(f"asym_grid {name} group {group} weighted {weighted} target {target}", flush=True)
-            lg, sg = ingest.asym_grid(w, group, 4, target, imp)
-            lr, sr = ob.asym_grid(w, group, 4, wt, rem=0 if target is None else 1,
-                                  refit=1 if target is None else 0, lib=ob.refq())
+            kw = dict(rem=0 if target is None else 1, refit=1 if target is None else 0)
+            lg, sg = ob.asym_grid(w, group, 4, wt, lib=ingest._lib(), **kw)
+            lr, sr = ob.asym_grid(w, group, 4, wt, lib=ob.refq(), **kw)
             assert np.array_equal(lg.view(np.uint32), lr.view(np.uint32)), name
             assert np.array_equal(sg.view(np.uint32), sr.view(np.uint32)), name
 
@@ -47,21 +48,18 @@ def test_asym_grid_dropin_equals_reference_library(group, weighted):
 def test_field_search_dropin_equals_reference_library(weighted):
     rng = np.random.default_rng(7)
     rows, cols = 64, 2048
-    ng, gps = cols // 32, 8
-    imp = rng.random(cols).astype(np.float32) + 0.5 if weighted else None
-    wt = ingest._weights(imp, ng, 32)
+    gps = 8
+    wt = (rng.random(cols).astype(np.float32) + np.float32(0.5)) if weighted else None
     for name, w in _data(rng, rows, cols).items():
         lo, st = ob.asym_grid(w, 32, 4)
         d16, q8, _ = ob.two_level(st, gps, signed=False)
         md16, mq8, _ = ob.two_level(lo, gps, signed=True)
         print(f"field_search {name} weighted {weighted}", flush=True)
-        gq, gm, es, em = ingest.field_search(w, d16.view(np.float16), q8, md16.view(np.float16), mq8, 32, gps, 15,
-                                             255, 127, 254, imp, 2)
         dv = np.repeat(d16.view(np.float16).astype(np.float32), gps, axis=1)
         dm = np.repeat(md16.view(np.float16).astype(np.float32), gps, axis=1)
+        gq, gm = ob.field_search(w, dv, dm, q8, mq8, 32, 15, wt=wt, radius=2, lib=ingest._lib())
         rq, rm = ob.field_search(w, dv, dm, q8, mq8, 32, 15, wt=wt, radius=2, lib=ob.refq())
-        assert np.array_equal(gq, rq.astype(np.uint8)) and np.array_equal(gm, rm.astype(np.uint8)), name
-        assert np.array_equal(es, rq.astype(np.float32) * dv)
+        assert np.array_equal(gq, rq) and np.array_equal(gm, rm), name
 
 
 def test_the_reference_prototypes_bind_and_agree():
@@ -69,7 +67,7 @@ def test_the_reference_prototypes_bind_and_agree():
     # loader gives them (tooling/sml_grid_c.py:23-28)
     rng = np.random.default_rng(3)
     w = rng.standard_normal((16, 512)).astype(np.float32)
-    facs = ingest.grid_facs()
+    facs = ob.grid_facs()
     l = ingest._lib()
     a_l, a_s = np.zeros((16, 16), np.float32), np.zeros((16, 16), np.float32)
     l.sml_asym_grid(w.ctypes.data, 16, 512, 32, 4, 0, None, facs.ctypes.data, len(facs), 3, 1, a_l.ctypes.data,

@@ -35,7 +35,6 @@ def test_grid_factors_are_numpys_linspace():
         want = np.concatenate([np.linspace(0.6, 0.85, max(2, ncand // 3)),
                                np.linspace(0.88, 1.04, max(2, ncand - ncand // 3))]).astype(np.float32)
         assert np.array_equal(ob.grid_facs(ncand), want)
-        assert np.array_equal(ingest.grid_facs(ncand), want)
 
 
 @needs_refq
