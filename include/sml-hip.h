@@ -251,6 +251,18 @@ size_t sml_hip_attn_part_floats(int n_head, int hd, int n_ctx);
 int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,
                       const float * cos_t, const float * sin_t, const int32_t * pos,
                       int n_head, int n_kv, int hd, int n_ctx, float * part, float * out);
+// The sum of n values (0..16384, each >= 0) in the order of a serial float
+// loop, sum = sum + x[i] for i = 0, 1, ... (the softmax sum of attn_row,
+// sml/sml-run.c:280-287), as exact-mode attention computes it: bit for bit
+// that loop's result, mostly in parallel. *out is device memory.
+int sml_hip_softmax_sum(const float * x, int n, float * out);
+// The same, with out also quantized per 32 values for the o product (the
+// codes, scales and sums of sml_quantize_act, sml/sml-kernel.c:86-106), as the
+// decode step runs it when the o product reads the heads in order.
+int sml_hip_attention_q(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,
+                        const float * cos_t, const float * sin_t, const int32_t * pos,
+                        int n_head, int n_kv, int hd, int n_ctx, float * part, float * out,
+                        int8_t * q_out, float * s_out, int32_t * u_out);
 
 // ------------------------------------------------------------ argmax
 // First-max greedy pick into *tok (sml_sample_greedy, sml/sml-run.c:3539-3544).

@@ -232,7 +232,7 @@ static void launch_layer(int L) {
     }
     // with an identity o-proj permutation the attention kernel quantizes its
     // own output for the o GEMV; otherwise a gather + quantize follows it
-    const int fuse_q = y->perm_o < 0 && !G.exact;
+    const int fuse_q = y->perm_o < 0;
     uint16_t * kc = G.cur_slot ? G.kcs[G.cur_slot] : G.kc, * vc = G.cur_slot ? G.vcs[G.cur_slot] : G.vc;
     op_attention(G.st, G.q, G.k, G.v, kc + (size_t) L * G.n_ctx * kvd, vc + (size_t) L * G.n_ctx * kvd,
                  G.rc, G.rs, G.pos, G.H, G.KV, G.hd, G.n_ctx, G.pos_cap, G.part, G.att,

@@ -172,21 +172,33 @@ typedef struct {
     int nsub;
 } sml_kattn;
 
-// Decode attention in the reference's float order (exact mode): RoPE of q and
-// k in place and the fp16 KV write (sml_rope_exact), then one workgroup per
-// query head (sml_attn_exact).
+// Decode attention in the reference's float order (exact mode), two
+// launches: RoPE, the fp16 KV write and every position's score
+// (sml_attnx_scores: splits of 128 positions x kv heads), then per query head
+// the softmax and P.V chains (sml_attnx_pv).
 typedef struct {
-    float * q;                    // n_head * hd after bias; rotated in place
-    float * k;                    // n_kv * hd after bias; rotated in place
+    const float * q;              // n_head * hd after bias (rotated in registers)
+    const float * k;              // n_kv * hd after bias
     const float * v;              // n_kv * hd after bias
     uint16_t * kc, * vc;          // this layer's cache, [n_ctx][n_kv * hd]
     const float * cos_t, * sin_t; // [n_ctx][hd / 2]
     const int32_t * pos;
+    float * sc;                   // scores [n_head][n_ctx] between the launches
     float * out;                  // n_head * hd
+    int8_t * q_out;               // when non-NULL: out also quantized per 32
+    float * s_out;                //   (sml_quantize_act) for the o product
+    int32_t * u_out;
     int n_head, n_kv, n_ctx;
     float inv;                    // 1 / sqrtf(hd)
 } sml_kattnx;
 
+
+// The softmax sum of the exact attention on its own: n values, one output.
+typedef struct {
+    const float * x;
+    float * out;
+    int n;
+} sml_ksum;
 
 typedef struct {
     const float * logits;

@@ -258,7 +258,9 @@ __constant__ unsigned long long EXPF_TAB[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull };
 
-__device__ __forceinline__ float expf_ref(float x) {
+// tab: the 32-entry table above, or a copy of it (in LDS: a kernel that
+// streams global loads keeps its waits for them apart from the lookups)
+__device__ __forceinline__ float expf_tab(float x, const unsigned long long * tab) {
     #pragma clang fp contract(off)
     if (x < -0x1.9fe368p6f) return 0.0f;
     const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
@@ -268,12 +270,13 @@ __device__ __forceinline__ float expf_ref(float x) {
     const unsigned long long ki = __builtin_bit_cast(unsigned long long, kd);
     kd -= Shift;
     const double r = __builtin_fma(InvLn2N, xd, -kd);
-    const double s = __builtin_bit_cast(double, EXPF_TAB[ki % 32] + (ki << 47));
+    const double s = __builtin_bit_cast(double, tab[ki % 32] + (ki << 47));
     const double z = __builtin_fma(C0, r, C1), r2 = r * r;
     double y = __builtin_fma(C2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     return (float) (y * s);
 }
+__device__ __forceinline__ float expf_ref(float x) { return expf_tab(x, EXPF_TAB); }
 
 // Order LDS traffic among the lanes of one wave (its LDS operations execute
 // in order; this keeps the compiler from moving them across the point).
@@ -803,19 +806,37 @@ GEMV_EXACT(4) GEMV_EXACT(8)
 
 // The sum of squares as the reference build computes it (sml/sml-run.c:
 // 147-152, a serial loop its compiler turns into double FMAs): one lane, in
-// order. Loads run ahead of the dependent chain in blocks of 16.
+// order. Loads run ahead of the dependent chain in blocks of 16. x is in
+// global memory or in LDS (generic loads: this is the rare fallback of the
+// checked parallel sum below).
 __device__ __noinline__ double serial_ss(const float * x, int n) {
     double ss = 0.0;
     int i = 0;
     for (; i + 16 <= n; i += 16) {
         float v[16];
         #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = gld<float>(x + i + j);
+        for (int j = 0; j < 16; j++) v[j] = x[i + j];
         #pragma unroll
         for (int j = 0; j < 16; j++) ss = __builtin_fma((double) v[j], (double) v[j], ss);
     }
-    for (; i < n; i++) { const float v = gld<float>(x + i); ss = __builtin_fma((double) v, (double) v, ss); }
+    for (; i < n; i++) { const float v = x[i]; ss = __builtin_fma((double) v, (double) v, ss); }
     return ss;
+}
+
+// float(ss/n) of the serial chain above, from a sum of the same squares taken
+// in any order. Every square is exact in double (24-bit mantissas), all are
+// nonnegative, so each order's sum lies within (n-1)*2^-53*(1+2^-30) of the
+// exact sum, relatively: the serial and the given sum differ by less than
+// d = 4*(n+4)*2^-53*s, with a margin for the rounding of d itself. Division
+// by n and the float conversion are monotone, so when s-d and s+d give the
+// same float that float is the serial chain's; it fails for about one input
+// in 10^4 (a rounding boundary inside the window) and for inf/NaN sums, and
+// the caller then runs the chain.
+__device__ __forceinline__ bool ss_mean_alike(double s, int n, float & out) {
+    const double d = s * ((double) (4 * (n + 4)) * 0x1p-53);
+    const float lo = (float) ((s - d) / (double) n), hi = (float) ((s + d) / (double) n);
+    out = lo;
+    return lo == hi;
 }
 
 extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_knormq a) {
@@ -839,17 +860,19 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
         double tot = 0.0;
-        if (a.exact) {
+        for (int w = 0; w < NORMQ_THREADS / WAVE; w++) tot += red[w];
+        float msq = (float) (tot / (double) n);
+        if (a.exact && !ss_mean_alike(tot, n, msq)) {
             // the reference build's loop: ss = fma(x_i, x_i, ss) in order
+            // (tot is the same in every thread, so all take this branch)
+            __syncthreads();
             if (tid == 0) red[0] = serial_ss(sx, n);
             __syncthreads();
-            tot = red[0];
-        } else {
-            for (int w = 0; w < NORMQ_THREADS / WAVE; w++) tot += red[w];
+            msq = (float) (red[0] / (double) n);
         }
         // IEEE division and square root: hipcc's default for HIP is the correctly
         // rounded fp32 divide/sqrt, which the bit-exact parity tests rely on
-        const float sc = 1.0f / sqrtf((float) (tot / (double) n) + a.eps);
+        const float sc = 1.0f / sqrtf(msq + a.eps);
         for (int i = tid; i < n; i += NORMQ_THREADS) sx[i] = sx[i] * sc * a.norm_w[i];
     }
     __syncthreads();
@@ -917,14 +940,16 @@ extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a
         for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
-        double tot = red[0] + red[1] + red[2] + red[3];
-        if (a.exact) {
+        const double tot = red[0] + red[1] + red[2] + red[3];
+        float msq = (float) (tot / (double) n);
+        if (a.exact && !ss_mean_alike(tot, n, msq)) {
+            // the serial chain (the same decision in every thread)
             __syncthreads();
             if (tid == 0) red[0] = serial_ss(x, n);
             __syncthreads();
-            tot = red[0];
+            msq = (float) (red[0] / (double) n);
         }
-        sc = 1.0f / sqrtf((float) (tot / (double) n) + a.eps);
+        sc = 1.0f / sqrtf(msq + a.eps);
     }
     const int j = blockIdx.x * 256 + tid;           // element (group j/32) of every output
     const bool ok = j < n;                          // whole groups of 32 (n % 32 == 0)
@@ -1910,105 +1935,460 @@ extern "C" __global__ __launch_bounds__(256) void sml_attn_merge_sb(const sml_ka
 // ---------------------------------------------------------------- attention in the reference's order
 //
 // The exact mode's decode attention: the float operations of the
-// reference's x86 build, in its order (sml/sml-run.c:180-287,339-372),
-// so the output equals its bit for bit. First sml_rope_exact rotates q and
-// k in place with the fused products of that build and writes the position's
-// fp16 K and V rows. Then sml_attn_exact, one workgroup per query head:
-// - score of position t: eight FMA lanes over the head's dims (lane j takes
-//   dims j, j+8, ...), folded ((l0+l4)+(l1+l5)) + ((l2+l6)+(l3+l7)), times
-//   1/sqrt(hd); positions in parallel;
-// - the maximum, then expf of each score less it (expf_ref: the C library's
-//   bits), then their sum as one serial float chain, one reciprocal and the
-//   products;
-// - output dim d: one FMA chain over the positions in order, p_t*v_t[d] + o.
-// The two serial chains make this latency-bound (about 8 cycles per position
-// each), which is why it is a mode and not the decode path.
-extern "C" __global__ __launch_bounds__(256) void sml_rope_exact(const sml_kattnx a) {
-    const int pos = *a.pos, kvd = a.n_kv * HD;
-    const float * cs = a.cos_t + (size_t) pos * (HD / 2), * sn = a.sin_t + (size_t) pos * (HD / 2);
-    uint16_t * kr = a.kc + (size_t) pos * kvd, * vr = a.vc + (size_t) pos * kvd;
-    for (int idx = threadIdx.x; idx < (a.n_head + a.n_kv) * (HD / 2); idx += 256) {
-        #pragma clang fp contract(off)
-        const int hh = idx / (HD / 2), i = idx % (HD / 2);
-        const bool isk = hh >= a.n_head;
-        float * v = isk ? a.k + (size_t) (hh - a.n_head) * HD : a.q + (size_t) hh * HD;
-        const float x0 = v[i], x1 = v[i + HD / 2];
-        const float y0 = __builtin_fmaf(x0, cs[i], -(x1 * sn[i]));
-        const float y1 = __builtin_fmaf(x0, sn[i], x1 * cs[i]);
-        v[i] = y0;
-        v[i + HD / 2] = y1;
-        if (isk) {
-            const int o = (hh - a.n_head) * HD + i;
-            kr[o] = f2h(y0);
-            kr[o + HD / 2] = f2h(y1);
-        }
+// reference's x86 build, in its order (sml/sml-run.c:180-287,339-372), so
+// the output equals its bit for bit. Two launches.
+//
+// sml_attnx_scores (splits of 128 positions x kv heads, 256 threads): RoPE
+// of the kv head's query heads into LDS and, in the split holding the
+// position, of k, whose fp16 row and v's are written to the cache (the
+// fused products of that build: x0*c - x1*s = fma(x0, c, -(x1*s)),
+// x0*s + x1*c = fma(x0, s, x1*c)); then a thread per position computes its
+// score for every other query head: eight FMA lanes over the head's dims
+// (lane j takes dims j, j+8, ...), folded ((l0+l4)+(l1+l5)) +
+// ((l2+l6)+(l3+l7)), times 1/sqrt(hd) (sml/sml-run.c:186-206).
+//
+// sml_attnx_pv (a workgroup per query head, 8 waves): the scores into LDS,
+// their maximum, expf of each score less it (expf_tab: the C library's
+// bits), their sum in the order of a serial float chain, one reciprocal and
+// the products (sml/sml-run.c:280-287); then output dim d as one FMA chain
+// over the positions in order, p_t*v_t[d] + o (sml/sml-run.c:209-229).
+//
+// A dependent float operation issues every ~12 cycles on gfx950 (measured:
+// 11.8 per v_add_f32, 17.3 per v_fma_mix_f32, at 2.4 GHz), so a 4096-step
+// chain costs ~20 us. The P.V chains are run as such (two waves, one dim
+// per lane, V staged to LDS as fp32 so the chain is v_fmac_f32 alone), with
+// every wave streaming V into a two-tile ring and ATTNX_PF tiles of loads in
+// flight. The softmax sum is computed exactly but mostly in parallel
+// (serial_sum_seg below). With q_out the workgroup also quantizes its head
+// per 32 for the o product (the arithmetic of sml_normq2 without a norm, so
+// its codes are bit for bit).
+#define ATTNX_CH 128          // positions per scores workgroup
+#define ATTNX_TP 64           // positions per V tile
+#define ATTNX_PF 6            // V tiles in flight
+#define ATTNX_THREADS 512
+#define ATTNX_SEG 64          // positions per segment of the softmax sum
+#define ATTNX_MAXSEG 256      // 16384 positions
+
+// The serial float sum s = ((e0 + e1) + e2) + ... of n >= 0 values (all >= 0,
+// finite) in LDS, exactly, mostly in parallel; called by every thread of
+// the workgroup, the result is returned to all.
+//
+// While the running sum s stays in one binade [2^E, 2^(E+1)), its floats
+// are the multiples m*u of u = 2^(E-23), m in [2^23, 2^24), and one step
+// rounds s + e to the nearest multiple: m += round(e/u), unless e/u lies
+// exactly halfway (then the even neighbour of m + floor(e/u) wins, which
+// depends on m). So for a segment of 64 values that starts in binade E,
+// contains no such tie and ends with m + K < 2^24, the chain adds exactly
+// K = sum of round(e/u) to m. Each segment's K is computed in parallel for
+// the binade of its exact prefix sum and the next one up (the chain's
+// sum lies within 2^-12 of it, relatively); one lane then walks the
+// segments from s = 0, adding K where those conditions hold and running the
+// float chain over the segment's values where they do not (the first
+// segments, a binade crossing, a tie). The result is the chain's bit for
+// bit; tests/test_gpu_exact.py checks it against the oracle's chain on
+// inputs with planted ties and crossings.
+__device__ __forceinline__ float serial_sum_seg(const float * e, int n, float * fsum, int * segk, int * sege,
+                                                float * out) {
+    const int tid = threadIdx.x, nseg = (n + ATTNX_SEG - 1) / ATTNX_SEG;
+    constexpr int TPS = 8, EPT = ATTNX_SEG / TPS;            // threads per segment, values per thread
+    // each segment's sum (8 threads, 8 values each, DPP within the 8 lanes)
+    for (int j0 = 0; j0 < nseg; j0 += ATTNX_THREADS / TPS) {
+        const int j = j0 + tid / TPS, i0 = j * ATTNX_SEG + (tid % TPS) * EPT;
+        float d = 0.0f;
+        #pragma unroll
+        for (int i = 0; i < EPT; i++) d += i0 + i < n ? e[i0 + i] : 0.0f;
+        d += dpp_f<0xB1>(d);
+        d += dpp_f<0x4E>(d);
+        d += dpp_f<0x141>(d);
+        if (j < nseg && tid % TPS == 0) fsum[j] = d;
     }
-    for (int i = threadIdx.x; i < kvd; i += 256) vr[i] = f2h(a.v[i]);
+    __syncthreads();
+    // their exclusive prefix, one lane: a binade guess (a float sum is close
+    // enough: the candidates are the guess and the binade above, and every
+    // use of a candidate is checked exactly)
+    if (tid == 0) {
+        float acc = 0.0f;
+        for (int j = 0; j < nseg; j++) { const float d = fsum[j]; fsum[j] = acc; acc += d; }
+    }
+    __syncthreads();
+    // K of each segment for binades E and E+1 (segk[2j + c]; -1: not usable).
+    // e*2^(23-E) is exact in float (a power-of-two scaling; a result past the
+    // float range is inf and fails the test, one below the normal range is
+    // far under 1/2 and rounds to 0 either way)
+    for (int j0 = 0; j0 < nseg; j0 += ATTNX_THREADS / TPS) {
+        const int j = j0 + tid / TPS, i0 = j * ATTNX_SEG + (tid % TPS) * EPT;
+        const float st = j < nseg ? fsum[j] : 0.0f;
+        const int eg = st > 0.0f && st < 1e30f ? ilogbf(st) : -1000;   // not finite: never matched
+        float x[EPT];
+        #pragma unroll
+        for (int i = 0; i < EPT; i++) x[i] = i0 + i < n ? e[i0 + i] : 0.0f;
+        #pragma unroll
+        for (int c = 0; c < 2; c++) {
+            int ks = 0, bad = eg + c <= -126 ? 1 : 0;
+            #pragma unroll
+            for (int i = 0; i < EPT; i++) {
+                const float y = __builtin_amdgcn_ldexpf(x[i], 23 - (eg + c));
+                bad |= (y >= 16777216.0f) | (y - floorf(y) == 0.5f) | (y != y);
+                ks += y < 16777216.0f ? (int) __builtin_rintf(y) : 0;
+            }
+            ks += dpp_i<0xB1>(ks); ks += dpp_i<0x4E>(ks); ks += dpp_i<0x141>(ks);
+            bad |= dpp_i<0xB1>(bad); bad |= dpp_i<0x4E>(bad); bad |= dpp_i<0x141>(bad);
+            if (j < nseg && tid % TPS == 0) segk[2 * j + c] = bad || ks >= (1 << 24) ? -1 : ks;
+        }
+        if (j < nseg && tid % TPS == 0) sege[j] = eg;
+    }
+    __syncthreads();
+    if (tid < WAVE) {
+        // the walk, by wave 0 as uniform (scalar) code: lane l holds the
+        // table of segments l, l+64, ...; the fast step is integer work on
+        // the sum's bits; a segment run as floats reads its values 16 at a
+        // time, the next 16 in flight while the current 16 are added
+        int te[ATTNX_MAXSEG / WAVE], tk0[ATTNX_MAXSEG / WAVE], tk1[ATTNX_MAXSEG / WAVE];
+        #pragma unroll
+        for (int g = 0; g < ATTNX_MAXSEG / WAVE; g++) {
+            const int j = g * WAVE + tid;
+            te[g] = j < nseg ? sege[j] : -1000;
+            tk0[g] = j < nseg ? segk[2 * j] : -1;
+            tk1[g] = j < nseg ? segk[2 * j + 1] : -1;
+        }
+        unsigned sb = 0;                                  // the bits of the sum
+        #pragma unroll
+        for (int g = 0; g < ATTNX_MAXSEG / WAVE; g++) {
+            const int jn = min(nseg - g * WAVE, WAVE);
+            for (int jj = 0; jj < jn; jj++) {
+                const int ec = __builtin_amdgcn_readlane(te[g], jj);
+                const int k0 = __builtin_amdgcn_readlane(tk0[g], jj), k1 = __builtin_amdgcn_readlane(tk1[g], jj);
+                const int E = (int) (sb >> 23) - 127, c = E - ec;
+                if (sb >= 0x00800000u && (c == 0 || c == 1)) {
+                    const int k = c ? k1 : k0;
+                    const int m = (int) ((sb & 0x7FFFFFu) | 0x800000u) + k;
+                    if (k >= 0 && m < (1 << 24)) {
+                        sb = (sb & 0xFF800000u) | ((unsigned) m & 0x7FFFFFu);
+                        continue;
+                    }
+                }
+                float s = __builtin_bit_cast(float, sb);
+                const int i0 = (g * WAVE + jj) * ATTNX_SEG, i1 = min(n, i0 + ATTNX_SEG);
+                if (i1 - i0 == ATTNX_SEG) {
+                    const float4 * q = (const float4 *) (e + i0);
+                    float4 c4[2][4];
+                    #pragma unroll
+                    for (int r = 0; r < 4; r++) c4[0][r] = q[r];
+                    #pragma unroll
+                    for (int bl = 0; bl < ATTNX_SEG / 16; bl++) {
+                        if (bl + 1 < ATTNX_SEG / 16) {
+                            #pragma unroll
+                            for (int r = 0; r < 4; r++) c4[(bl + 1) & 1][r] = q[4 * (bl + 1) + r];
+                        }
+                        #pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const float4 v = c4[bl & 1][r];
+                            s = s + v.x; s = s + v.y; s = s + v.z; s = s + v.w;
+                        }
+                    }
+                } else {
+                    for (int i = i0; i < i1; i++) s = s + e[i];
+                }
+                sb = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(unsigned, s));
+            }
+        }
+        if (tid == 0) *out = __builtin_bit_cast(float, sb);
+    }
+    __syncthreads();
+    return *out;
 }
 
-extern "C" __global__ __launch_bounds__(256) void sml_attn_exact(const sml_kattnx a) {
-    #pragma clang fp contract(off)
-    extern __shared__ float pr[];                  // [n_ctx] scores, then weights
-    __shared__ float qs[HD];
-    __shared__ float red[4];
+// serial_sum_seg over n values in global memory (its test entry point)
+extern "C" __global__ __launch_bounds__(ATTNX_THREADS) void sml_sum_seg(const sml_ksum a) {
+    extern __shared__ __align__(16) float ev[];
+    __shared__ float fsum[ATTNX_MAXSEG];
+    __shared__ int segk[2 * ATTNX_MAXSEG], sege[ATTNX_MAXSEG];
     __shared__ float tot;
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int kh = h / (a.n_head / a.n_kv), pos = *a.pos, n = pos + 1;
-    const size_t stride = (size_t) a.n_kv * HD;
-    if (tid < HD) qs[tid] = a.q[(size_t) h * HD + tid];
+    for (int i = threadIdx.x; i < a.n; i += ATTNX_THREADS) ev[i] = a.x[i];
     __syncthreads();
-    const uint16_t * kb = a.kc + (size_t) kh * HD;
-    for (int t = tid; t < n; t += 256) {
-        const v4u * kr = (const v4u *) (kb + (size_t) t * stride);
+    const float s = serial_sum_seg(ev, a.n, fsum, segk, sege, &tot);
+    if (threadIdx.x == 0) *a.out = s;
+}
+
+// K tile rows in LDS: 256 bytes and 16 of padding, so the 8 lanes a
+// 16-byte read serves per cycle start on different banks
+#define ATTNX_KROW 136
+extern "C" __global__ __launch_bounds__(256) void sml_attnx_scores(const sml_kattnx a) {
+    #pragma clang fp contract(off)
+    __shared__ float qs[ATTN_MAXREP][HD];
+    __shared__ __align__(16) uint16_t kt[ATTNX_CH * ATTNX_KROW];
+    const int kh = blockIdx.y, t0 = blockIdx.x * ATTNX_CH, tid = threadIdx.x;
+    const int pos = *a.pos, n = pos + 1, rep = a.n_head / a.n_kv, kvd = a.n_kv * HD;
+    if (t0 >= n) return;
+    const bool own = pos < t0 + ATTNX_CH;
+    GLOBAL uint16_t * kc = (GLOBAL uint16_t *) a.kc, * vc = (GLOBAL uint16_t *) a.vc;
+    // RoPE inputs first, then the split's K tile, coalesced (16 lanes a row,
+    // rows past the position load row t0 and are never read): loads complete
+    // in order. Pair idx = tid + 256r is dim pair i of query head j (j = rep:
+    // k, in the owning split only); indices past the end load a pair in range
+    // and are dropped.
+    constexpr int RR = (ATTN_MAXREP + 1) * (HD / 2) / 256 + 1;
+    constexpr int KC = ATTNX_CH * HD / 8 / 256;               // 16-byte K chunks per thread
+    const int npair = (rep + (own ? 1 : 0)) * (HD / 2);
+    const float * cs = a.cos_t + (size_t) pos * (HD / 2), * sn = a.sin_t + (size_t) pos * (HD / 2);
+    float x0[RR], x1[RR], c[RR], sv[RR];
+    #pragma unroll
+    for (int r = 0; r < RR; r++) {
+        const int idx = min(tid + 256 * r, npair - 1), j = idx / (HD / 2), i = idx % (HD / 2);
+        const float * src = j < rep ? a.q + (size_t) (kh * rep + j) * HD : a.k + (size_t) kh * HD;
+        x0[r] = src[i];
+        x1[r] = src[i + HD / 2];
+        c[r] = cs[i];
+        sv[r] = sn[i];
+    }
+    const float vnew = a.v[(size_t) kh * HD + (tid & (HD - 1))];     // used by the owning split only
+    v4u kw[KC];
+    #pragma unroll
+    for (int r = 0; r < KC; r++) {
+        const int ch = tid + 256 * r, tp = t0 + ch / 16;
+        kw[r] = __builtin_nontemporal_load((const GLOBAL v4u *) (kc + (size_t) (tp < n ? tp : t0) * kvd +
+                                                                (size_t) kh * HD + (ch % 16) * 8));
+    }
+    // the K tile first, then the position's own row over its stale copy
+    #pragma unroll
+    for (int r = 0; r < KC; r++) {
+        const int ch = tid + 256 * r;
+        if (t0 + ch / 16 != pos) *(v4u *) (kt + (ch / 16) * ATTNX_KROW + (ch % 16) * 8) = kw[r];
+    }
+    #pragma unroll
+    for (int r = 0; r < RR; r++) {
+        const int idx = tid + 256 * r;
+        if (idx >= npair) break;
+        const int j = idx / (HD / 2), i = idx % (HD / 2);
+        const float y0 = __builtin_fmaf(x0[r], c[r], -(x1[r] * sv[r]));
+        const float y1 = __builtin_fmaf(x0[r], sv[r], x1[r] * c[r]);
+        if (j < rep) {
+            qs[j][i] = y0;
+            qs[j][i + HD / 2] = y1;
+        } else {
+            // the position's own row: to the cache, and the same bits into the tile
+            const uint16_t h0 = f2h(y0), h1 = f2h(y1);
+            kc[(size_t) pos * kvd + (size_t) kh * HD + i] = h0;
+            kc[(size_t) pos * kvd + (size_t) kh * HD + i + HD / 2] = h1;
+            kt[(pos - t0) * ATTNX_KROW + i] = h0;
+            kt[(pos - t0) * ATTNX_KROW + i + HD / 2] = h1;
+        }
+    }
+    if (own && tid < HD) vc[(size_t) pos * kvd + (size_t) kh * HD + tid] = f2h(vnew);
+    __syncthreads();
+    const int t = t0 + (tid & (ATTNX_CH - 1));
+    if (t >= n) return;
+    v4u kr[HD / 8];
+    #pragma unroll
+    for (int i = 0; i < HD / 8; i++) kr[i] = *(const v4u *) (kt + (tid & (ATTNX_CH - 1)) * ATTNX_KROW + 8 * i);
+    for (int j = tid / ATTNX_CH; j < rep; j += 256 / ATTNX_CH) {
         float l[8] = { 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f };
         #pragma unroll
         for (int i = 0; i < HD / 8; i++) {
             float kf[8];
             unpack_h8(kr[i], kf);
             #pragma unroll
-            for (int j = 0; j < 8; j++) l[j] = __builtin_fmaf(qs[8 * i + j], kf[j], l[j]);
+            for (int e = 0; e < 8; e++) l[e] = __builtin_fmaf(qs[j][8 * i + e], kf[e], l[e]);
         }
-        pr[t] = (((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]))) * a.inv;
+        a.sc[(size_t) (kh * rep + j) * a.n_ctx + t] =
+            (((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]))) * a.inv;
+    }
+}
+
+// A register value the compiler cannot prove equal to another (the row swaps
+// must see two distinct operands: a register swapped with itself is folded)
+__device__ __forceinline__ unsigned opaque(unsigned x) { asm volatile("" : "+v"(x)); return x; }
+
+extern "C" __global__ __launch_bounds__(ATTNX_THREADS) void sml_attnx_pv(const sml_kattnx a) {
+    #pragma clang fp contract(off)
+    extern __shared__ __align__(16) float pr[];       // [ncap] scores, then weights; then the V ring
+    __shared__ float red[ATTNX_THREADS / WAVE];
+    __shared__ float tot;
+    __shared__ unsigned long long etab[32];
+    __shared__ float fsum[ATTNX_MAXSEG];
+    __shared__ int segk[2 * ATTNX_MAXSEG], sege[ATTNX_MAXSEG];
+    constexpr int LT = ATTNX_THREADS / 2;                     // loader threads: waves 4..7
+    constexpr int CPT = ATTNX_TP * HD / 8 / LT;               // 16-byte chunks per loader per tile
+    static_assert(CPT * LT * 8 == ATTNX_TP * HD, "a tile is whole chunks per loader");
+    static_assert(LT / 16 % 2 == 0, "a loader wave's rows hold whole position pairs");
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int kh = h / (a.n_head / a.n_kv), pos = *a.pos, n = pos + 1, kvd = a.n_kv * HD;
+    const int ncap = (a.n_ctx + 3) & ~3, nt = (n + ATTNX_TP - 1) / ATTNX_TP;
+    // waves 4..7 stream V; waves 0 and 1 run the chains (a wave-uniform test)
+    const bool loader = __builtin_amdgcn_readfirstlane(tid) >= LT;
+    const int lt = tid - LT;
+    // the ring: three slots of [ATTNX_TP/2 position pairs][HD dims] words, a
+    // word holding one dim of an even position (low half) and of the next
+    unsigned * ring = (unsigned *) (pr + ncap);
+    const GLOBAL uint16_t * vb = (const GLOBAL uint16_t *) a.vc + (size_t) kh * HD;
+    // chunk c of tile k: position k*TP + c/16 (the last position for tiles
+    // past the end: a row in range, never used), dims (c%16)*8 .. +7; a
+    // loader wave's 16-lane rows hold consecutive positions
+    // (32-bit byte offsets from the head's base: a layer's cache is < 4 GB)
+    const GLOBAL char * vbase = (const GLOBAL char *) vb;
+    auto issue = [&](int k, v4u (&b)[CPT]) {
+        #pragma unroll
+        for (int r = 0; r < CPT; r++) {
+            const int c = lt + r * LT, p = min(k * ATTNX_TP + c / 16, n - 1);
+            const unsigned off = ((unsigned) p * (unsigned) kvd + (unsigned) (c % 16) * 8u) * 2u;
+            b[r] = __builtin_nontemporal_load((const GLOBAL v4u *) (vbase + off));
+        }
+    };
+    // rows 2i and 2i+1 of a wave trade their chunks (v_permlane16_swap), so
+    // each lane holds its 8 dims at an even position and the next; the even
+    // row writes the first 4 dims' pair words, the odd row the last 4
+    auto stash = [&](int k, const v4u (&b)[CPT]) {
+        const int odd = (lt >> 4) & 1;
+        #pragma unroll
+        for (int r = 0; r < CPT; r++) {
+            const int c = lt + r * LT;
+            unsigned e[4], o[4];
+            #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const auto sw = __builtin_amdgcn_permlane16_swap(b[r][i], opaque(b[r][i]), false, false);
+                e[i] = sw[0];
+                o[i] = sw[1];
+            }
+            const unsigned e0 = odd ? e[2] : e[0], e1 = odd ? e[3] : e[1];
+            const unsigned o0 = odd ? o[2] : o[0], o1 = odd ? o[3] : o[1];
+            v4u w;
+            w[0] = (e0 & 0xFFFFu) | (o0 << 16);
+            w[1] = (e0 >> 16) | (o0 & 0xFFFF0000u);
+            w[2] = (e1 & 0xFFFFu) | (o1 << 16);
+            w[3] = (e1 >> 16) | (o1 & 0xFFFF0000u);
+            *(v4u *) (ring + ((size_t) (k % 3) * (ATTNX_TP / 2) + c / 32) * HD + (c % 16) * 8 + odd * 4) = w;
+        }
+    };
+    // the scores (8 loads per thread in flight, then into LDS) and expf's table
+    if (tid < 32) etab[tid] = EXPF_TAB[tid];
+    const GLOBAL float * sc = (const GLOBAL float *) a.sc + (size_t) h * a.n_ctx;
+    for (int base = 0; base < n; base += 8 * ATTNX_THREADS) {
+        float v[8];
+        #pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = sc[min(base + tid + i * ATTNX_THREADS, n - 1)];
+        #pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int t = base + tid + i * ATTNX_THREADS;
+            if (t < n) pr[t] = v[i];
+        }
     }
     __syncthreads();
     float m = -__builtin_inff();
-    for (int t = tid; t < n; t += 256) m = fmaxf(m, pr[t]);
+    for (int t = tid; t < n; t += ATTNX_THREADS) m = fmaxf(m, pr[t]);
     m = wave_max(m);
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int t = tid; t < n; t += 256) pr[t] = expf_ref(pr[t] - m);
+    #pragma unroll
+    for (int w = 0; w < ATTNX_THREADS / WAVE; w++) m = fmaxf(m, red[w]);
+    for (int t = tid; t < n; t += ATTNX_THREADS) pr[t] = expf_tab(pr[t] - m, etab);
     __syncthreads();
-    if (tid == 0) {
-        float sum = 0.0f;
-        int t = 0;
-        for (; t + 16 <= n; t += 16) {
-            float e[16];
-            #pragma unroll
-            for (int j = 0; j < 16; j++) e[j] = pr[t + j];
-            #pragma unroll
-            for (int j = 0; j < 16; j++) sum = sum + e[j];
-        }
-        for (; t < n; t++) sum = sum + pr[t];
-        tot = sum;
+    // the first V tiles go out now, behind every other global load: loads
+    // complete in order, so a wait for an earlier one would wait for them too
+    v4u buf[ATTNX_PF][CPT];
+    if (loader) {
+        #pragma unroll
+        for (int u = 0; u < ATTNX_PF; u++) issue(u, buf[u]);
+    }
+    const float iv = 1.0f / serial_sum_seg(pr, n, fsum, segk, sege, &tot);
+    for (int t = tid; t < n; t += ATTNX_THREADS) pr[t] = pr[t] * iv;
+    // tiles 0 and 1 into the ring; their registers take tiles PF and PF+1
+    if (loader) {
+        stash(0, buf[0]);
+        issue(ATTNX_PF, buf[0]);
+        stash(1, buf[1]);
+        issue(ATTNX_PF + 1, buf[1]);
     }
     __syncthreads();
-    const float iv = 1.0f / tot;
-    for (int t = tid; t < n; t += 256) pr[t] = pr[t] * iv;
-    __syncthreads();
-    if (tid >= HD) return;
-    const uint16_t * vb = a.vc + (size_t) kh * HD + tid;
+    // P.V: threads 0..127 each run one dim's chain over tile k in ring slot
+    // k%3 while the loaders move tile k+2 from registers into slot (k+2)%3
+    // and issue tile k+2+PF. The two kinds of waves run loops of their own
+    // that meet at the same barriers, one per round of a tile, over whole
+    // groups of PF rounds (a barrier counts waves, whichever instruction they
+    // reach it at). The loaders move a tile and issue one every round, also
+    // past the last tile (rows in range, never read), so the loads in flight
+    // are the same count at every wait and the compiler's waits stay partial.
+    // A chain reads 4 positions per LDS instruction (two pair words 256 bytes
+    // apart) and 4 weights per broadcast read, 24 positions ahead (12 of the
+    // 15 reads the LDS counter can wait on partially), also into the next
+    // tile, which is in the ring a round before its own.
     float o = 0.0f;
-    int t = 0;
-    for (; t + 16 <= n; t += 16) {
-        float vv[16];
-        #pragma unroll
-        for (int j = 0; j < 16; j++) vv[j] = h2f(vb[(size_t) (t + j) * stride]);
-        #pragma unroll
-        for (int j = 0; j < 16; j++) o = __builtin_fmaf(pr[t + j], vv[j], o);
+    if (loader) {
+        for (int kk = 0; kk < nt; kk += ATTNX_PF) {
+            #pragma unroll
+            for (int u = 0; u < ATTNX_PF; u++) {
+                stash(kk + u + 2, buf[(u + 2) % ATTNX_PF]);
+                issue(kk + u + 2 + ATTNX_PF, buf[(u + 2) % ATTNX_PF]);
+                __syncthreads();
+            }
+        }
+        return;
     }
-    for (; t < n; t++) o = __builtin_fmaf(pr[t], h2f(vb[(size_t) t * stride]), o);
+    constexpr int NB = ATTNX_TP / 8, AH = 3;                  // blocks of 8 positions per tile, blocks ahead
+    static_assert(NB % (AH + 1) == 0, "a tile is whole rounds of the read registers");
+    const unsigned * vd = ring + tid;
+    unsigned vv[AH + 1][4];
+    float4 ww[AH + 1][2];
+    // block b of tile k: pair words of pairs 4b..4b+3, weights 8b..8b+7 (past
+    // the last tile: LDS in range, never used)
+    auto ld = [&](int k, int b, unsigned (&v)[4], float4 (&w)[2]) {
+        const unsigned * vs = vd + (size_t) (k % 3) * (ATTNX_TP / 2) * HD;
+        const float * ps = pr + k * ATTNX_TP;
+        #pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = vs[(4 * b + j) * HD];
+        w[0] = *(const float4 *) (ps + b * 8);
+        w[1] = *(const float4 *) (ps + b * 8 + 4);
+    };
+    if (tid < HD) {
+        #pragma unroll
+        for (int b = 0; b < AH; b++) ld(0, b, vv[b], ww[b]);
+    }
+    for (int kk = 0; kk < nt; kk += ATTNX_PF) {
+        #pragma unroll
+        for (int u = 0; u < ATTNX_PF; u++) {
+            const int k = kk + u;
+            if (tid < HD && k < nt) {
+                const int cnt = min(ATTNX_TP, n - k * ATTNX_TP);
+                if (cnt == ATTNX_TP) {
+                    #pragma unroll
+                    for (int b = 0; b < NB; b++) {
+                        const int nb = b + AH;
+                        ld(nb < NB ? k : k + 1, nb % NB, vv[nb % (AH + 1)], ww[nb % (AH + 1)]);
+                        __builtin_amdgcn_sched_barrier(0);
+                        const unsigned (&v)[4] = vv[b % (AH + 1)];
+                        const float4 (&w)[2] = ww[b % (AH + 1)];
+                        o = __builtin_fmaf(w[0].x, h2f((uint16_t) v[0]), o);
+                        o = __builtin_fmaf(w[0].y, h2f((uint16_t) (v[0] >> 16)), o);
+                        o = __builtin_fmaf(w[0].z, h2f((uint16_t) v[1]), o);
+                        o = __builtin_fmaf(w[0].w, h2f((uint16_t) (v[1] >> 16)), o);
+                        o = __builtin_fmaf(w[1].x, h2f((uint16_t) v[2]), o);
+                        o = __builtin_fmaf(w[1].y, h2f((uint16_t) (v[2] >> 16)), o);
+                        o = __builtin_fmaf(w[1].z, h2f((uint16_t) v[3]), o);
+                        o = __builtin_fmaf(w[1].w, h2f((uint16_t) (v[3] >> 16)), o);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                } else {
+                    // the last, partial tile
+                    const unsigned * vs = vd + (size_t) (k % 3) * (ATTNX_TP / 2) * HD;
+                    const float * ps = pr + k * ATTNX_TP;
+                    for (int p = 0; p < cnt; p++)
+                        o = __builtin_fmaf(ps[p], h2f((uint16_t) (vs[(p / 2) * HD] >> (16 * (p & 1)))), o);
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (tid >= HD) return;
     a.out[(size_t) h * HD + tid] = o;
+    if (a.q_out) {
+        const float amax = max32(fabsf(o));
+        const float s = amax / 127.0f;
+        const float is = s > 0.0f ? 1.0f / s : 0.0f;
+        const int q = quant1(o, is);
+        const int sum = isum32(q);
+        const size_t j = (size_t) h * HD + tid;
+        a.q_out[j] = (int8_t) q;
+        if ((tid & 31) == 0) { a.s_out[j / 32] = s; a.u_out[j / 32] = sum; }
+    }
 }
 
 // ---------------------------------------------------------------- argmax

@@ -728,18 +728,23 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
     if (n_pos < 1 || n_pos > n_ctx) hx_failf("attention over %d of %d positions", n_pos, n_ctx);
     if (g_exact) {
-        // the reference's order: RoPE and the KV write, then a workgroup per
-        // query head with the scores of every position in LDS; the output
-        // stays float (the caller quantizes it for o)
+        // the reference's order: RoPE, the KV write and the scores over
+        // splits of 128 positions, then a workgroup per query head for the
+        // softmax and P.V chains (quantizing its output when asked); the
+        // scores pass through the partials buffer ([n_head][n_ctx] floats)
         if (n_ctx > 16384) hx_failf("exact attention holds at most 16384 positions");
-        if (q_out) hx_failf("exact attention does not quantize its output");
+        if (sml_hip_attn_part_floats(n_head, hd, n_ctx) < (size_t) n_head * n_ctx)
+            hx_failf("exact attention needs %d x %d floats of scores", n_head, n_ctx);
         sml_kattnx x;
         memset(&x, 0, sizeof x);
-        x.q = (float *) q; x.k = (float *) k; x.v = v; x.kc = kc; x.vc = vc; x.cos_t = cos_t; x.sin_t = sin_t;
-        x.pos = pos; x.out = out; x.n_head = n_head; x.n_kv = n_kv; x.n_ctx = n_ctx;
+        x.q = q; x.k = k; x.v = v; x.kc = kc; x.vc = vc; x.cos_t = cos_t; x.sin_t = sin_t;
+        x.pos = pos; x.sc = part; x.out = out; x.q_out = q_out; x.s_out = s_out; x.u_out = u_out;
+        x.n_head = n_head; x.n_kv = n_kv; x.n_ctx = n_ctx;
         x.inv = 1.0f / __builtin_sqrtf((float) hd);
-        hx_launch("sml_rope_exact", 1, 1, 256, 0, st, &x);
-        hx_launch("sml_attn_exact", (unsigned) n_head, 1, 256, (size_t) n_ctx * 4, st, &x);
+        hx_launch("sml_attnx_scores", (unsigned) ((n_pos + 127) / 128), (unsigned) n_kv, 256, 0, st, &x);
+        // the weights and three 64-position fp16 V tiles
+        const size_t lds = (size_t) ((n_ctx + 3) & ~3) * 4 + (size_t) 3 * 64 * 128 * 2;
+        hx_launch("sml_attnx_pv", (unsigned) n_head, 1, 512, lds, st, &x);
         return;
     }
     // one sequence: the 8-wave kernel over attn_split positions, the split the
@@ -868,6 +873,28 @@ int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kc
     OP_BEGIN(-1);
     op_attention(0, q, k, v, kcache, vcache, cos_t, sin_t, pos, n_head, n_kv, hd, n_ctx, n_ctx, part, out,
                  NULL, NULL, NULL, NULL);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_softmax_sum(const float * x, int n, float * out) {
+    OP_BEGIN(-1);
+    if (n < 0 || n > 16384) hx_failf("softmax sum of %d values (0..16384)", n);
+    sml_ksum a;
+    a.x = x; a.out = out; a.n = n;
+    hx_launch("sml_sum_seg", 1, 1, 512, (size_t) (n > 0 ? n : 1) * 4, 0, &a);
+    HX_LEAVE();
+    return 0;
+}
+
+int sml_hip_attention_q(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,
+                        const float * cos_t, const float * sin_t, const int32_t * pos,
+                        int n_head, int n_kv, int hd, int n_ctx, float * part, float * out,
+                        int8_t * q_out, float * s_out, int32_t * u_out) {
+    OP_BEGIN(-1);
+    if (!q_out || !s_out || !u_out) hx_failf("attention_q needs its three outputs");
+    op_attention(0, q, k, v, kcache, vcache, cos_t, sin_t, pos, n_head, n_kv, hd, n_ctx, n_ctx, part, out,
+                 q_out, s_out, u_out, NULL);
     HX_LEAVE();
     return 0;
 }

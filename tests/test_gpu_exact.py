@@ -116,6 +116,73 @@ def test_exact_normq_bit_exact(n):
         np.testing.assert_array_equal(a, b, err_msg=name)
 
 
+@pytest.mark.parametrize("n", [1536, 4096, 14336])
+@pytest.mark.parametrize("with_resid", [False, True])
+def test_exact_normq_at_rounding_boundary(n, with_resid):
+    """Inputs whose serial sum of squares ends on a float midpoint of ss/n
+    while any tree order ends above it (tests/norm_cases.py): the parallel
+    sum must fall back to the serial chain, or the norm's scale is one place
+    off. Both kernels: the multi-workgroup one, and (with a residual of
+    zeros) the one-workgroup one."""
+    import norm_cases as nc
+    rng = np.random.default_rng(n + with_resid)
+    x = nc.boundary_vector(n, rng)
+    w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+    perm = rng.permutation(n).astype(np.int32)
+    act = sa.Act(n)
+    with exact_mode():
+        sa.normq(sa.DevBuf.of(x), act, perm=sa.DevBuf.of(perm), w=sa.DevBuf.of(w), eps=1e-5,
+                 resid=sa.DevBuf.of(np.zeros(n, np.float32)) if with_resid else None)
+    normed = np.zeros(n, np.float32)
+    ob.oracle().orc_rms_norm(normed.ctypes.data, x.ctypes.data, w.ctypes.data, n, np.float32(1e-5))
+    for a, b, name in zip(act.read(), ob.quantize_act(normed[perm]), ("q", "scale", "sums")):
+        np.testing.assert_array_equal(a, b, err_msg=name)
+
+
+def _serial_sum(x):
+    s = np.float32(0)
+    for v in np.asarray(x, np.float32):
+        s = np.float32(s + v)
+    return s
+
+
+def _sum_cases(rng):
+    """Softmax-like values at many lengths, and values built to hit the
+    segmented sum's slow paths: exact half-way ties against the running
+    sum's last place, zeros, tiny values, a value that crosses several
+    binades at once, and lengths that are not whole segments."""
+    for n in (1, 2, 63, 64, 65, 1000, 4096, 4097, 16384):
+        sc = rng.standard_normal(n) * rng.uniform(0.5, 6)
+        e = np.exp((sc - sc.max()).astype(np.float32)).astype(np.float32)
+        yield f"softmax {n}", e
+    e = np.exp(-rng.random(4096).astype(np.float32) * 4).astype(np.float32)
+    # the running sum ends near 1000 (last place 2^-14 there, finer before):
+    # values on grids of 2^-15 .. 2^-17 fall half-way between its floats
+    for g in (15, 16, 17):
+        yield f"ties (multiples of 2^-{g})", (np.round(e * 2 ** g) / 2 ** g).astype(np.float32)
+    z = e.copy()
+    z[rng.integers(0, 4096, 300)] = 0.0
+    z[:100] = np.float32(1e-30)
+    yield "zeros and tiny leading values", z
+    c = np.full(4096, np.float32(2.0 ** -20))
+    c[2000] = np.float32(1.0)
+    yield "one value over many binades", c
+    yield "all equal", np.full(3000, np.float32(0.3))
+
+
+def test_softmax_sum_is_the_serial_chain():
+    """The exact attention's softmax sum (a serial float chain in the
+    reference) computed in segments: bit for bit the chain's result."""
+    rng = np.random.default_rng(5)
+    out = sa.DevBuf(4)
+    for name, e in _sum_cases(rng):
+        print(f"softmax sum: {name}", flush=True)
+        assert sa.lib().sml_hip_softmax_sum(sa.DevBuf.of(e).ptr, len(e), out.ptr) == 0
+        got = out.read(np.float32)[0]
+        want = _serial_sum(e)
+        assert got.view(np.uint32) == want.view(np.uint32), f"{name}: {got!r} vs {want!r}"
+
+
 def attention_case(H, KV, n_ctx, positions, exact, seed):
     """Fill a cache with random fp16 rows, then run attention at each of
     `positions` (rotating q and k, writing the position's rows) and compare
@@ -132,6 +199,7 @@ def attention_case(H, KV, n_ctx, positions, exact, seed):
     dcos, dsin = sa.DevBuf.of(cos_t), sa.DevBuf.of(sin_t)
     part = sa.DevBuf(sa.lib().sml_hip_attn_part_floats(H, hd, n_ctx) * 4)
     out = sa.DevBuf(H * hd * 4)
+    oq = sa.Act(H * hd)
     scratch = np.zeros(n_ctx, np.float32)
     inv = np.float32(1) / np.sqrt(np.float32(hd))
     results = []
@@ -143,11 +211,21 @@ def attention_case(H, KV, n_ctx, positions, exact, seed):
         dpos = sa.DevBuf.of(np.array([pos], np.int32))
         sa.lib().sml_hip_set_exact(1 if exact else 0)
         try:
-            rc = sa.lib().sml_hip_attention(dq.ptr, dk.ptr, dv.ptr, dkc.ptr, dvc.ptr, dcos.ptr, dsin.ptr, dpos.ptr,
-                                            H, KV, hd, n_ctx, part.ptr, out.ptr)
+            if pos % 2:
+                # odd positions: the launch that also quantizes its output for o
+                rc = sa.lib().sml_hip_attention_q(dq.ptr, dk.ptr, dv.ptr, dkc.ptr, dvc.ptr, dcos.ptr, dsin.ptr,
+                                                  dpos.ptr, H, KV, hd, n_ctx, part.ptr, out.ptr, oq.q.ptr,
+                                                  oq.scale.ptr, oq.sums.ptr)
+            else:
+                rc = sa.lib().sml_hip_attention(dq.ptr, dk.ptr, dv.ptr, dkc.ptr, dvc.ptr, dcos.ptr, dsin.ptr,
+                                                dpos.ptr, H, KV, hd, n_ctx, part.ptr, out.ptr)
         finally:
             sa.lib().sml_hip_set_exact(0)
         assert rc == 0, sa.lib().sml_hip_last_error()
+        if pos % 2:
+            got_out = out.read(np.float32)
+            for a, b, name in zip(oq.read(), ob.quantize_act(got_out), ("q", "scale", "sums")):
+                np.testing.assert_array_equal(a, b, err_msg=f"quantized attention output {name}, position {pos}")
         qr, kr = q.copy(), k.copy()
         ob.oracle().orc_rope(qr.ctypes.data, H, hd, half, cos_t[pos * half:].ctypes.data, sin_t[pos * half:].ctypes.data)
         ob.oracle().orc_rope(kr.ctypes.data, KV, hd, half, cos_t[pos * half:].ctypes.data, sin_t[pos * half:].ctypes.data)
