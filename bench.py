@@ -297,6 +297,39 @@ def qwen_decode(tmp, prompt_len=2048, steps=64):
             "frac_of_weights_roofline": round(steps / dt / (HBM_PEAK_GBS * 1e9 / wbytes), 4)}
 
 
+def exact_decode(path, ids, warmup, steps):
+    """The token-identical path: the same Llama-3-8B-shaped file opened in
+    exact mode (every kernel in the reference CPU engine's float order, so
+    each step's logits equal its sml_forward bit for bit), the same prompt
+    read exactly (a token at a time), then `warmup` untimed and `steps` timed
+    greedy tokens at the fast line's positions."""
+    dec = sa.Decoder(path, n_ctx=N_CTX, exact=True)
+    try:
+        if not dec.exact:
+            raise RuntimeError("exact mode did not open")
+        t0 = time.perf_counter()
+        lg = dec.prefill(ids, 0, LLAMA["n_vocab"])
+        t_prompt = time.perf_counter() - t0
+        pos = len(ids)
+        warm = dec.generate(int(np.argmax(lg)), pos, warmup)
+        tok, pos = int(warm[-1]), pos + warmup
+        sa.sync()
+        t1 = time.perf_counter()
+        out = dec.generate(tok, pos, steps)
+        sa.sync()
+        dt = time.perf_counter() - t1
+        ev_ms = dec.last_ms()
+        wbytes = dec.weight_bytes()
+    finally:
+        dec.close()
+    tps = steps / dt
+    return {"positions": f"{pos}..{pos + steps - 1}", "tokens_per_s": round(tps, 2),
+            "ms_per_step": round(dt * 1e3 / steps, 4), "gpu_event_ms": round(ev_ms, 3),
+            "frac_of_weights_roofline": round(tps / (HBM_PEAK_GBS * 1e9 / wbytes), 4),
+            "prompt": {"tokens": len(ids), "level": 0, "s": round(t_prompt, 2)},
+            "first_tokens": [int(t) for t in out[:8]]}
+
+
 def small_gemm(tmp, M=16, iters=60):
     """The 16-row small-M GEMMs of the batched step over rotating copies:
     SwiGLU gate+up 2 x 14336 x 4096, 4096 x 4096 and 4096 x 14336, with
@@ -559,6 +592,7 @@ def main():
     ap.add_argument("--gemv-only", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes")
     ap.add_argument("--no-extra", action="store_true", help="skip the batched, MoE and width-sweep lines")
+    ap.add_argument("--no-exact", action="store_true", help="skip the exact-mode decode leg")
     ap.add_argument("--pmc-probe", metavar="SSF", help=argparse.SUPPRESS)
     ap.add_argument("--cpu-leg", nargs="+", help=argparse.SUPPRESS)
     ap.add_argument("--decode-trace", metavar="MODEL", choices=("llama", "qwen"),
@@ -765,6 +799,11 @@ def run(a, work):
         extra["batched_decode"] = batched_decode(dec, LLAMA["n_vocab"])
         log(f"batched: {extra['batched_decode']} ({time.perf_counter() - t1:.1f}s)")
     dec.close()
+    if not a.no_exact:
+        t1 = time.perf_counter()
+        extra["exact_decode"] = exact_decode(path, ids, W, K)
+        extra["exact_decode"]["vs_fast"] = round(extra["exact_decode"]["tokens_per_s"] / (K / dt), 4)
+        log(f"exact decode: {extra['exact_decode']} ({time.perf_counter() - t1:.1f}s)")
     if not a.no_extra:
         t1 = time.perf_counter()
         extra["qwen25_1p5b_decode"] = qwen_decode(work)
