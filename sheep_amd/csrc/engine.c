@@ -212,12 +212,16 @@ static void gemv1(sml_hip_mat * m, int slot, int epi, float * y, const float * b
     op_gemv(G.st, m, NULL, epi, G.aq[slot], G.as[slot], G.asum[slot], y, bias, NULL, resid, NULL);
 }
 
+// the norm prologue is fused into a GEMV of this matrix (in exact mode only
+// the Q4/Q8 GEMVs have exact prologues)
+static int fusable(const sml_hip_mat * m) { return !G.exact || m->nbits == 4 || m->nbits == 8; }
+
 static void launch_layer(int L) {
     eng_layer * y = &G.L[L];
     const size_t kvd = (size_t) G.KV * G.hd;
     int slot[3];
     // q/k/v: the stacked GEMV computes RMSNorm + quantize of x in its prologue
-    if (y->qkv && (G.fuse & 1) && G.E <= gemv_fuse_max_cols(0)) {
+    if (y->qkv && (G.fuse & 1) && G.E <= gemv_fuse_max_cols(0) && fusable(y->qkv)) {
         gemv_fuse fu;
         memset(&fu, 0, sizeof fu);
         fu.x = G.x; fu.norm_w = y->an; fu.eps = G.eps; fu.perm = pdev(y->perm_qkv[0]);
@@ -254,7 +258,7 @@ static void launch_layer(int L) {
     if (y->perm_gu[0] == y->perm_gu[1] && y->gate->nbits == y->up->nbits) {
         gemv_fuse fu;
         memset(&fu, 0, sizeof fu);
-        const int x_fused = (G.fuse & 1) && G.E <= gemv_fuse_max_cols(h_fused);
+        const int x_fused = (G.fuse & 1) && G.E <= gemv_fuse_max_cols(h_fused) && fusable(y->gate);
         if (x_fused) { fu.x = G.x; fu.norm_w = y->fn; fu.eps = G.eps; fu.perm = pdev(y->perm_gu[0]); }
         else prep(G.x, y->fn, NULL, G.E, y->perm_gu, 2, slot);
         if (h_fused) { fu.hq = G.hq; fu.hscale = G.hs; fu.hsums = G.hsum; }
@@ -545,11 +549,11 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     G.fuse = env_int("SML_FUSE", 3);
     // exact mode: the reference's float order throughout (sml_forward,
     // sml/sml-run.c:3243-3523), so logits equal its CPU path bit for bit.
-    // Norms run as their own launches (serial sums), prompts a token at a time.
+    // Prompts read a token at a time.
     G.exact = env_int("SML_EXACT", 0) != 0;
     ops_set_exact(G.exact);
     if (G.exact) {
-        G.fuse = 0;
+        G.fuse &= 1;            // the norm prologues have exact forms; h quantization stays a launch
         if (n_ctx > 16384) hx_failf("exact mode holds at most 16384 positions");
     }
     const size_t kvn = (size_t) G.n_layer * n_ctx * G.KV * G.hd;

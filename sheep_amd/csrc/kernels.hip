@@ -286,6 +286,41 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The sum of squares as the reference build computes it (sml/sml-run.c:
+// 147-152, a serial loop its compiler turns into double FMAs): one lane, in
+// order. Loads run ahead of the dependent chain in blocks of 16. x is in
+// global memory or in LDS (generic loads: this is the rare fallback of the
+// checked parallel sum below).
+__device__ __noinline__ double serial_ss(const float * x, int n) {
+    double ss = 0.0;
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+        float v[16];
+        #pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = x[i + j];
+        #pragma unroll
+        for (int j = 0; j < 16; j++) ss = __builtin_fma((double) v[j], (double) v[j], ss);
+    }
+    for (; i < n; i++) { const float v = x[i]; ss = __builtin_fma((double) v, (double) v, ss); }
+    return ss;
+}
+
+// float(ss/n) of the serial chain above, from a sum of the same squares taken
+// in any order. Every square is exact in double (24-bit mantissas), all are
+// nonnegative, so each order's sum lies within (n-1)*2^-53*(1+2^-30) of the
+// exact sum, relatively: the serial and the given sum differ by less than
+// d = 4*(n+4)*2^-53*s, with a margin for the rounding of d itself. Division
+// by n and the float conversion are monotone, so when s-d and s+d give the
+// same float that float is the serial chain's; it fails for about one input
+// in 10^4 (a rounding boundary inside the window) and for inf/NaN sums, and
+// the caller then runs the chain.
+__device__ __forceinline__ bool ss_mean_alike(double s, int n, float & out) {
+    const double d = s * ((double) (4 * (n + 4)) * 0x1p-53);
+    const float lo = (float) ((s - d) / (double) n), hi = (float) ((s + d) / (double) n);
+    out = lo;
+    return lo == hi;
+}
+
 // Fused activation prologue: RMSNorm (double sum of squares, out = x*sc*w,
 // sml/sml-run.c:147-152), gather through perm, and the per-32 quantization
 // (sml/sml-kernel.c:86-106) of the whole input vector, into the workgroup's
@@ -293,7 +328,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // float4 words t + k*WG (loaded before the weights); 8 consecutive threads
 // hold one group of 32. The arithmetic is the normq kernels', so the codes,
 // scales and sums are theirs bit for bit.
-template <int WG, int FK>
+// EXN: the norm in exact mode, the serial chain's float(ss/n) (ss_mean_alike,
+// with the chain itself over x in global memory as its rare fallback).
+template <int WG, int FK, bool EXN = false>
 __device__ __forceinline__ void fused_act(const sml_kgemv & a, const float4 (&fx)[FK], const float4 (&fw)[FK],
                                           const int4 (&fp)[FK], int8_t * lq, float2 * lsc, float * nrm, double * red) {
     const int n = a.cols, tid = threadIdx.x, n4 = n / 4;
@@ -313,7 +350,14 @@ __device__ __forceinline__ void fused_act(const sml_kgemv & a, const float4 (&fx
         double tot = 0.0;
         #pragma unroll
         for (int w = 0; w < WG / 64; w++) tot += red[w];
-        sc = 1.0f / sqrtf((float) (tot / (double) n) + a.eps);
+        float msq = (float) (tot / (double) n);
+        if (EXN && !ss_mean_alike(tot, n, msq)) {
+            __syncthreads();                    // every thread has read red (the same decision in all)
+            if (tid == 0) red[0] = serial_ss(a.x, n);
+            __syncthreads();
+            msq = (float) (red[0] / (double) n);
+        }
+        sc = 1.0f / sqrtf(msq + a.eps);
     }
     float v[FK][4];
     #pragma unroll
@@ -464,7 +508,8 @@ __device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first 
     // rw's chain j, v_j = fma(wsc, s*dot, v_j); v_j = fma(wmin, s*sum, v_j)
     // over the superblocks in order (cm; ct for a trailing half superblock,
     // whose four lanes the reference keeps apart and adds last).
-    static_assert(!EX || AM == 0, "the exact form reads a quantized activation");
+    // (with the fused prologue the exchange buffer takes the LDS of the
+    // prologue's gather buffer, which is dead once the activation is staged)
     const int nblk8 = (ng / 8) * 8;
     float4 * exb = nullptr;
     float * ext = nullptr;
@@ -503,7 +548,7 @@ __device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first 
                     pin(fw[k].x); pin(fw[k].y); pin(fw[k].z); pin(fw[k].w);
                     pin(fp[k].x); pin(fp[k].y); pin(fp[k].z); pin(fp[k].w);
                 }
-                fused_act<WG, FK>(a, fx, fw, fp, lq, lsc, (float *) (lds + ((n + 8 * ng + 15) & ~15)), red);
+                fused_act<WG, FK, EX>(a, fx, fw, fp, lq, lsc, (float *) (lds + ((n + 8 * ng + 15) & ~15)), red);
             } else {
                 // 4. activation into LDS (waits only for the activation loads)
                 #pragma unroll
@@ -788,12 +833,20 @@ extern "C" __global__ __launch_bounds__(512) void sml_gemv_q4_h_i2_p(const sml_k
     extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_s_r##RB##_i##NI##_x(const sml_kgemv a) { \
         gemv_body<NB, RB, NI, 256, true, 0, true, false, 64, true>(a);                                      \
     }
-#define GEMV_EXACT(NB)                                                                                      \
-    GEMV_KERNEL_X(NB, 1, 2) GEMV_KERNEL_X(NB, 1, 4) GEMV_KERNEL_X(NB, 2, 1) GEMV_KERNEL_X(NB, 2, 2)         \
-    GEMV_KERNEL_X(NB, 2, 4) GEMV_KERNEL_X(NB, 4, 1) GEMV_KERNEL_X(NB, 4, 2) GEMV_KERNEL_X(NB, 4, 4)         \
-    GEMV_KERNEL_SX(NB, 2, 1) GEMV_KERNEL_SX(NB, 2, 2) GEMV_KERNEL_SX(NB, 2, 4)                              \
-    GEMV_KERNEL_SX(NB, 4, 1) GEMV_KERNEL_SX(NB, 4, 2) GEMV_KERNEL_SX(NB, 4, 4)
-GEMV_EXACT(4) GEMV_EXACT(8)
+// _xn: the same with the fused RMSNorm/gather/quantize prologue (exact norm)
+#define GEMV_KERNEL_XN(NB, RB, NI)                                                                          \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_r##RB##_i##NI##_xn(const sml_kgemv a) { \
+        gemv_body<NB, RB, NI, 256, true, 1, false, false, 64, true>(a);                                     \
+    }
+#define GEMV_KERNEL_SXN(NB, RB, NI)                                                                         \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_s_r##RB##_i##NI##_xn(const sml_kgemv a) { \
+        gemv_body<NB, RB, NI, 256, true, 1, true, false, 64, true>(a);                                      \
+    }
+#define GEMV_EXACT(NB, K, KS)                                                                               \
+    K(NB, 1, 2) K(NB, 1, 4) K(NB, 2, 1) K(NB, 2, 2) K(NB, 2, 4) K(NB, 4, 1) K(NB, 4, 2) K(NB, 4, 4)         \
+    KS(NB, 2, 1) KS(NB, 2, 2) KS(NB, 2, 4) KS(NB, 4, 1) KS(NB, 4, 2) KS(NB, 4, 4)
+GEMV_EXACT(4, GEMV_KERNEL_X, GEMV_KERNEL_SX) GEMV_EXACT(8, GEMV_KERNEL_X, GEMV_KERNEL_SX)
+GEMV_EXACT(4, GEMV_KERNEL_XN, GEMV_KERNEL_SXN) GEMV_EXACT(8, GEMV_KERNEL_XN, GEMV_KERNEL_SXN)
 
 // ---------------------------------------------------------------- norm + quantize
 //
@@ -803,41 +856,6 @@ GEMV_EXACT(4) GEMV_EXACT(8)
 // and square root and round-half-even conversion, so the int8 codes, scales
 // and sums equal the reference's bit for bit on the same input.
 #define NORMQ_THREADS 1024
-
-// The sum of squares as the reference build computes it (sml/sml-run.c:
-// 147-152, a serial loop its compiler turns into double FMAs): one lane, in
-// order. Loads run ahead of the dependent chain in blocks of 16. x is in
-// global memory or in LDS (generic loads: this is the rare fallback of the
-// checked parallel sum below).
-__device__ __noinline__ double serial_ss(const float * x, int n) {
-    double ss = 0.0;
-    int i = 0;
-    for (; i + 16 <= n; i += 16) {
-        float v[16];
-        #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = x[i + j];
-        #pragma unroll
-        for (int j = 0; j < 16; j++) ss = __builtin_fma((double) v[j], (double) v[j], ss);
-    }
-    for (; i < n; i++) { const float v = x[i]; ss = __builtin_fma((double) v, (double) v, ss); }
-    return ss;
-}
-
-// float(ss/n) of the serial chain above, from a sum of the same squares taken
-// in any order. Every square is exact in double (24-bit mantissas), all are
-// nonnegative, so each order's sum lies within (n-1)*2^-53*(1+2^-30) of the
-// exact sum, relatively: the serial and the given sum differ by less than
-// d = 4*(n+4)*2^-53*s, with a margin for the rounding of d itself. Division
-// by n and the float conversion are monotone, so when s-d and s+d give the
-// same float that float is the serial chain's; it fails for about one input
-// in 10^4 (a rounding boundary inside the window) and for inf/NaN sums, and
-// the caller then runs the chain.
-__device__ __forceinline__ bool ss_mean_alike(double s, int n, float & out) {
-    const double d = s * ((double) (4 * (n + 4)) * 0x1p-53);
-    const float lo = (float) ((s - d) / (double) n), hi = (float) ((s + d) / (double) n);
-    out = lo;
-    return lo == hi;
-}
 
 extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_knormq a) {
     extern __shared__ __align__(16) float sx[];

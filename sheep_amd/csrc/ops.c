@@ -541,6 +541,9 @@ int op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int e
     } else if (!q || !scale || !sums) {
         hx_failf("gemv without an activation");
     }
+    // exact mode: the norm prologue has exact forms at Q4/Q8 only, h quantization none
+    if (g_exact && ((am && nb != 4 && nb != 8) || hq))
+        hx_failf("exact mode fuses only the norm prologue, and only into Q4/Q8 GEMVs");
     if (hq) {
         if (!swiglu || a.total_rows % 32) hx_failf("h quantization needs SwiGLU rows in whole groups");
         a.hq = fu->hq; a.hscale = fu->hscale; a.hsums = fu->hsums;
@@ -572,16 +575,20 @@ int op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int e
     }
     int rb, ni;
     pick_shape(a.total_rows, cols, nb, swiglu, am, &rb, &ni);
-    if (g_exact && (nb == 4 || nb == 8) && !am) {
+    if (g_exact && (nb == 4 || nb == 8)) {
         // the reference's float order: each group's products pass through LDS
-        // (RB*NI KB per wave) to the lanes that run its superblock chains
-        size_t xl = lds + (size_t) 4 * ni * rb * 64 * 16 + (size_t) 4 * rb * 4;
-        while (xl > 65536 && ni > 1) { ni /= 2; xl = lds + (size_t) 4 * ni * rb * 64 * 16 + (size_t) 4 * rb * 4; }
+        // (RB*NI KB per wave) to the lanes that run its superblock chains; with
+        // the fused prologue (_xn) they reuse its gather buffer's LDS
+        pick_shape(a.total_rows, cols, nb, swiglu, 0, &rb, &ni);
+        const size_t base = ((size_t) cols + 8u * (size_t) (cols / 32) + 15u) / 16u * 16u;
+        size_t xl = base + (size_t) 4 * ni * rb * 64 * 16 + (size_t) 4 * rb * 4;
+        while (xl > 65536 && ni > 1) { ni /= 2; xl = base + (size_t) 4 * ni * rb * 64 * 16 + (size_t) 4 * rb * 4; }
+        if (xl < lds) xl = lds;
         if (xl > 65536) hx_failf("exact GEMV of %d columns needs %zu bytes of LDS", cols, xl);
         const int rows_per_wave = swiglu ? rb / 2 : rb;
         const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
-        if (swiglu) snprintf(name, sizeof name, "sml_gemv_q%d_s_r%d_i%d_x", nb, rb, ni);
-        else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_x", nb, rb, ni);
+        if (swiglu) snprintf(name, sizeof name, "sml_gemv_q%d_s_r%d_i%d_x%s", nb, rb, ni, am ? "n" : "");
+        else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_x%s", nb, rb, ni, am ? "n" : "");
         hx_launch(name, (unsigned) ((waves + 3) / 4), 1, 256, xl, st, &a);
         return 0;
     }

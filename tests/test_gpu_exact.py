@@ -79,6 +79,58 @@ def test_exact_gemv_bit_exact(tmpdir_s, nb, rows, cols):
         same_bits(got, ob.ref_matvec(t, q, s, u), f"{rows}x{cols} Q{nb} vs the reference's kernel")
 
 
+@pytest.mark.parametrize("nb", [4, 8])
+@pytest.mark.parametrize("rows,cols,boundary", [(6144, 4096, False), (2048, 1536, False), (384, 4096, True),
+                                                 (300, 1536, True)])
+def test_exact_gemv_fused_norm_bit_exact(tmpdir_s, nb, rows, cols, boundary):
+    """The exact GEMV with its RMSNorm/gather/quantize prologue (the decode
+    step's q/k/v form): every row equals the oracle's norm, quantization and
+    GEMV in the reference's order, also on inputs whose sum of squares sits
+    on a float rounding boundary (the prologue's serial-chain fallback)."""
+    import norm_cases as nc
+    p = tmpdir_s / f"xn_{rows}x{cols}_q{nb}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, rows, cols, nbits=nb, random_perm=True, seed=rows + cols + nb + 7)
+    t = SSF(p)["w"]
+    m = sa.Mat.from_file(p, "w")
+    rng = np.random.default_rng(cols + boundary)
+    x = nc.boundary_vector(cols, rng) if boundary else (rng.standard_normal(cols) * 3).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
+    y = sa.DevBuf(rows * 4)
+    with exact_mode():
+        sa.matvec_normq(m, sa.DevBuf.of(x), y, w=sa.DevBuf.of(w), perm=sa.DevBuf.of(t.perm.astype(np.int32)),
+                        eps=1e-5)
+    normed = np.zeros(cols, np.float32)
+    ob.oracle().orc_rms_norm(normed.ctypes.data, x.ctypes.data, w.ctypes.data, cols, np.float32(1e-5))
+    q, s, u = ob.quantize_act(normed[t.perm])
+    same_bits(y.read(np.float32), ob.matvec(t, q, s, u), f"{rows}x{cols} Q{nb} fused norm")
+
+
+def test_exact_swiglu_fused_norm_bit_exact(tmpdir_s):
+    """The exact SwiGLU GEMV with the prologue (the decode step's gate/up
+    form): h equals the oracle's norm, gate, up and SiLU bit for bit."""
+    n_ff = 8960
+    p = tmpdir_s / f"xffn{n_ff}.ssf"
+    if not p.exists():
+        sa.synth_model(p, n_layer=1, n_embd=1536, n_head=12, n_head_kv=2, n_ff=n_ff, n_vocab=256,
+                       random_perm=True, seed=n_ff)
+    f = SSF(p)
+    g, u = f["blk.0.ffn_gate.weight"], f["blk.0.ffn_up.weight"]
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(1536) * 2).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(1536)).astype(np.float32)
+    h = sa.DevBuf(n_ff * 4)
+    with exact_mode():
+        sa.matvec_swiglu_fused(sa.Mat.from_file(p, g.name), sa.Mat.from_file(p, u.name), h, x=sa.DevBuf.of(x),
+                               w=sa.DevBuf.of(w), perm=sa.DevBuf.of(g.perm.astype(np.int32)), eps=1e-5)
+    normed = np.zeros(1536, np.float32)
+    ob.oracle().orc_rms_norm(normed.ctypes.data, x.ctypes.data, w.ctypes.data, 1536, np.float32(1e-5))
+    q, s, su = ob.quantize_act(normed[g.perm])
+    yg, yu = ob.matvec(g, q, s, su), ob.matvec(u, q, s, su)
+    ob.oracle().orc_silu_mul(yg.ctypes.data, yu.ctypes.data, n_ff)
+    same_bits(h.read(np.float32), yg, "swiglu with the fused norm")
+
+
 @pytest.mark.parametrize("n_ff", [8960, 2048 + 128])
 def test_exact_swiglu_bit_exact(tmpdir_s, n_ff):
     """gate and up in the reference's order, then its SiLU polynomial
