@@ -251,6 +251,18 @@ size_t sml_hip_attn_part_floats(int n_head, int hd, int n_ctx);
 int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,
                       const float * cos_t, const float * sin_t, const int32_t * pos,
                       int n_head, int n_kv, int hd, int n_ctx, float * part, float * out);
+// Causal attention of a prompt chunk: rows b = 0..n_rows-1 are positions
+// pos0+b of one sequence, each row of qkv its q, k and v ((n_head + 2*n_kv)*hd
+// floats); every row's k is rotated and its k and v written to the cache
+// before any row attends, then row b's heads attend over [0, pos0+b] into out
+// (n_rows x n_head*hd). The level-2 prompt's attention (the MFMA flash kernel,
+// its KV range split and merged as the grid needs; SML_ATTN_FLASH=0: a wave
+// per position), replacing the rope + f32_to_f16 + ms_attn of the reference's
+// batched prompt body (sml/sml-run.c:2192-2210,2368-2378). hd must be 128,
+// n_kv at most 8; part holds n_rows*n_head*ceil(n_ctx/128)*(hd+2) floats.
+int sml_hip_attention_prompt(const float * qkv, int n_rows, int pos0, uint16_t * kcache, uint16_t * vcache,
+                             const float * cos_t, const float * sin_t, int n_head, int n_kv, int hd, int n_ctx,
+                             float * part, float * out);
 // The sum of n values (0..16384, each >= 0) in the order of a serial float
 // loop, sum = sum + x[i] for i = 0, 1, ... (the softmax sum of attn_row,
 // sml/sml-run.c:280-287), as exact-mode attention computes it: bit for bit

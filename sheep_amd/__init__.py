@@ -101,6 +101,7 @@ _SIGS = [
     ("sml_hip_attn_part_floats", c_size_t, [c_int, c_int, c_int]),
     ("sml_hip_attention", c_int, [c_void_p] * 8 + [c_int] * 4 + [c_void_p, c_void_p]),
     ("sml_hip_attention_q", c_int, [c_void_p] * 8 + [c_int] * 4 + [c_void_p] * 5),
+    ("sml_hip_attention_prompt", c_int, [c_void_p, c_int, c_int] + [c_void_p] * 4 + [c_int] * 4 + [c_void_p] * 2),
     ("sml_hip_softmax_sum", c_int, [c_void_p, c_int, c_void_p]),
     ("sml_hip_argmax", c_int, [c_void_p, c_int, c_void_p]),
     ("sml_hip_argmax_noalloc", c_int, [c_void_p, c_int, c_void_p]),

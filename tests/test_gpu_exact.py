@@ -229,7 +229,8 @@ def test_softmax_sum_is_the_serial_chain():
     out = sa.DevBuf(4)
     for name, e in _sum_cases(rng):
         print(f"softmax sum: {name}", flush=True)
-        assert sa.lib().sml_hip_softmax_sum(sa.DevBuf.of(e).ptr, len(e), out.ptr) == 0
+        de = sa.DevBuf.of(e)
+        assert sa.lib().sml_hip_softmax_sum(de.ptr, len(e), out.ptr) == 0
         got = out.read(np.float32)[0]
         want = _serial_sum(e)
         assert got.view(np.uint32) == want.view(np.uint32), f"{name}: {got!r} vs {want!r}"

@@ -222,3 +222,59 @@ def test_flash_prompt_attention_equals_wave_form(tmp_path_factory, model, npos, 
         print(f"{model} part {i}: corr {corr:.7f}, top-1 {'equal' if gap == 0 else gap}")
         assert corr >= 0.9998, (i, corr)
         assert ok, (i, gap)
+
+
+@pytest.mark.parametrize("flash", ["1", "0"])
+@pytest.mark.parametrize("heads,n_rows", [((32, 8), 512), ((32, 8), 64), ((12, 2), 512)])
+def test_prompt_attention_4096(heads, n_rows, flash, monkeypatch):
+    """The level-2 prompt's causal attention on its own, at the end of a
+    4096-position context: a chunk of n_rows positions ending at 4095 over a
+    cache of random fp16 rows. The flash kernel splits the KV range as the
+    grid needs (32/8 heads: 2 splits at 512 rows, 16 at 64; 12/2 heads: 8)
+    and merges; the wave-per-position form splits by 128. Every chunk row's
+    rotated K and its V as stored equal the oracle's bit for bit; sampled
+    rows' outputs are within 1e-3 of the oracle's reference-order attention
+    (max |d| <= 1e-3 max |ref|, rel-RMS <= 1e-4), as the decode path's are."""
+    monkeypatch.setenv("SML_ATTN_FLASH", flash)
+    H, KV = heads
+    hd, half, n_ctx = 128, 64, 4096
+    pos0 = n_ctx - n_rows
+    rng = np.random.default_rng(H * 1000 + n_rows)
+    cos_t = np.zeros(n_ctx * half, np.float32)
+    sin_t = np.zeros(n_ctx * half, np.float32)
+    ob.oracle().orc_rope_table(5e5, half, n_ctx, cos_t.ctypes.data, sin_t.ctypes.data)
+    kvd, w = KV * hd, (H + 2 * KV) * hd
+    kc = rng.standard_normal((n_ctx, kvd)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((n_ctx, kvd)).astype(np.float16).view(np.uint16)
+    qkv = (rng.standard_normal((n_rows, w)) * 2).astype(np.float32)
+    dkc, dvc = sa.DevBuf.of(kc), sa.DevBuf.of(vc)
+    dqkv, dcos, dsin = sa.DevBuf.of(qkv), sa.DevBuf.of(cos_t), sa.DevBuf.of(sin_t)
+    part = sa.DevBuf(n_rows * H * (n_ctx // 128) * (hd + 2) * 4)
+    out = sa.DevBuf(n_rows * H * hd * 4)
+    print(f"prompt attention {heads} rows {n_rows} flash {flash}", flush=True)
+    rc = sa.lib().sml_hip_attention_prompt(dqkv.ptr, n_rows, pos0, dkc.ptr, dvc.ptr, dcos.ptr, dsin.ptr,
+                                           H, KV, hd, n_ctx, part.ptr, out.ptr)
+    assert rc == 0, sa.lib().sml_hip_last_error()
+    got = out.read(np.float32).reshape(n_rows, H * hd)
+    qr = np.ascontiguousarray(qkv[:, :H * hd])
+    kr = np.ascontiguousarray(qkv[:, H * hd:(H + KV) * hd])
+    for b in range(n_rows):
+        cs, sn = cos_t[(pos0 + b) * half:].ctypes.data, sin_t[(pos0 + b) * half:].ctypes.data
+        ob.oracle().orc_rope(qr[b].ctypes.data, H, hd, half, cs, sn)
+        ob.oracle().orc_rope(kr[b].ctypes.data, KV, hd, half, cs, sn)
+    kc[pos0:] = kr.astype(np.float16).view(np.uint16)
+    vc[pos0:] = qkv[:, (H + KV) * hd:].astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(dkc.read(np.uint16).reshape(n_ctx, kvd), kc, err_msg="K cache")
+    np.testing.assert_array_equal(dvc.read(np.uint16).reshape(n_ctx, kvd), vc, err_msg="V cache")
+    inv = np.float32(1) / np.sqrt(np.float32(hd))
+    scratch = np.zeros(n_ctx, np.float32)
+    for b in sorted({0, 1, 63, n_rows // 2, n_rows - 2, n_rows - 1} | set(rng.integers(0, n_rows, 4).tolist())):
+        want = np.zeros(H * hd, np.float32)
+        for h in range(H):
+            kh = h // (H // KV)
+            ob.oracle().orc_attn_head(qr[b, h * hd:].ctypes.data, kc[:, kh * hd:].ctypes.data,
+                                      vc[:, kh * hd:].ctypes.data, kvd, pos0 + b, hd, inv, scratch.ctypes.data,
+                                      want[h * hd:].ctypes.data)
+        err = np.abs(got[b].astype(np.float64) - want)
+        assert err.max() <= 1e-3 * np.abs(want).max(), (b, err.max())
+        assert np.sqrt((err ** 2).mean() / (want.astype(np.float64) ** 2).mean()) <= 1e-4, b
