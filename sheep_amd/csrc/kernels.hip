@@ -64,6 +64,23 @@ template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 template <int CTRL> __device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+// Inclusive prefix sums over the 64 lanes: Hillis-Steele inside each
+// 16-lane row (row_shr 1, 2, 4, 8; lanes shifted in from outside the row
+// add 0), then each row adds the totals of the rows below it.
+__device__ __forceinline__ int wave_scan_i(int v) {
+    v += dpp_i<0x111>(v); v += dpp_i<0x112>(v); v += dpp_i<0x114>(v); v += dpp_i<0x118>(v);
+    const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31);
+    const int r2 = __builtin_amdgcn_readlane(v, 47), row = (threadIdx.x & 63) >> 4;
+    return v + (row == 0 ? 0 : row == 1 ? r0 : row == 2 ? r0 + r1 : r0 + r1 + r2);
+}
+__device__ __forceinline__ float wave_scan_f(float v) {
+    v += dpp_f<0x111>(v); v += dpp_f<0x112>(v); v += dpp_f<0x114>(v); v += dpp_f<0x118>(v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 15));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 47));
+    const int row = (threadIdx.x & 63) >> 4;
+    return v + (row == 0 ? 0.0f : row == 1 ? r0 : row == 2 ? r0 + r1 : (r0 + r1) + r2);
+}
 __device__ __forceinline__ float sum16(float v) {
     v += dpp_f<0xB1>(v); v += dpp_f<0x4E>(v); v += dpp_f<0x141>(v); v += dpp_f<0x140>(v);
     return v;
@@ -1971,15 +1988,14 @@ extern "C" __global__ __launch_bounds__(256) void sml_attn_merge_sb(const sml_ka
 // the products (sml/sml-run.c:280-287); then output dim d as one FMA chain
 // over the positions in order, p_t*v_t[d] + o (sml/sml-run.c:209-229).
 //
-// A dependent float operation issues every ~12 cycles on gfx950 (measured:
-// 11.8 per v_add_f32, 17.3 per v_fma_mix_f32, at 2.4 GHz), so a 4096-step
-// chain costs ~20 us. The P.V chains are run as such (two waves, one dim
-// per lane, V staged to LDS as fp32 so the chain is v_fmac_f32 alone), with
-// every wave streaming V into a two-tile ring and ATTNX_PF tiles of loads in
-// flight. The softmax sum is computed exactly but mostly in parallel
-// (serial_sum_seg below). With q_out the workgroup also quantizes its head
-// per 32 for the o product (the arithmetic of sml_normq2 without a norm, so
-// its codes are bit for bit).
+// A dependent float operation issues every ~8.4 cycles on gfx950 (v_add_f32,
+// v_fmac_f32; ~9.5 for v_fma_mix_f32; 2.4 GHz), so a 4096-step chain costs
+// at least ~14.5 us. The P.V chains are run as such (one output dim per
+// lane), reading V from a three-tile LDS ring of fp16 position pairs that
+// loader waves fill with ATTNX_PF tiles of loads in flight. The softmax sum
+// is computed exactly but mostly in parallel (serial_sum_seg below). With
+// q_out the workgroup also quantizes its head per 32 for the o product (the
+// arithmetic of sml_normq2 without a norm, so its codes are bit for bit).
 #define ATTNX_CH 128          // positions per scores workgroup
 #define ATTNX_TP 64           // positions per V tile
 #define ATTNX_PF 6            // V tiles in flight
@@ -1999,11 +2015,12 @@ extern "C" __global__ __launch_bounds__(256) void sml_attn_merge_sb(const sml_ka
 // contains no such tie and ends with m + K < 2^24, the chain adds exactly
 // K = sum of round(e/u) to m. Each segment's K is computed in parallel for
 // the binade of its exact prefix sum and the next one up (the chain's
-// sum lies within 2^-12 of it, relatively); one lane then walks the
-// segments from s = 0, adding K where those conditions hold and running the
-// float chain over the segment's values where they do not (the first
-// segments, a binade crossing, a tie). The result is the chain's bit for
-// bit; tests/test_gpu_exact.py checks it against the oracle's chain on
+// sum lies within 2^-12 of it, relatively); one wave then walks the
+// segments from s = 0, jumping over each run of segments where those
+// conditions hold (one prefix sum of their Ks over the lanes) and running
+// the float chain over the values of a segment where they do not (the
+// first segments, a binade crossing, a tie). The result is the chain's bit
+// for bit; tests/test_gpu_exact.py checks it against the oracle's chain on
 // inputs with planted ties and crossings.
 __device__ __forceinline__ float serial_sum_seg(const float * e, int n, float * fsum, int * segk, int * sege,
                                                 float * out) {
@@ -2021,12 +2038,25 @@ __device__ __forceinline__ float serial_sum_seg(const float * e, int n, float * 
         if (j < nseg && tid % TPS == 0) fsum[j] = d;
     }
     __syncthreads();
-    // their exclusive prefix, one lane: a binade guess (a float sum is close
-    // enough: the candidates are the guess and the binade above, and every
-    // use of a candidate is checked exactly)
-    if (tid == 0) {
-        float acc = 0.0f;
-        for (int j = 0; j < nseg; j++) { const float d = fsum[j]; fsum[j] = acc; acc += d; }
+    // their exclusive prefix, by wave 0 (4 segments a lane, then a scan over
+    // the lanes): a binade guess (a float sum in any order is close enough:
+    // the candidates are the guess and the binade above, and every use of a
+    // candidate is checked exactly)
+    if (tid < WAVE) {
+        float d[ATTNX_MAXSEG / WAVE];
+        float t = 0.0f;
+        #pragma unroll
+        for (int i = 0; i < ATTNX_MAXSEG / WAVE; i++) {
+            const int j = tid * (ATTNX_MAXSEG / WAVE) + i;
+            d[i] = t;
+            t += j < nseg ? fsum[j] : 0.0f;
+        }
+        const float before = wave_scan_f(t) - t;
+        #pragma unroll
+        for (int i = 0; i < ATTNX_MAXSEG / WAVE; i++) {
+            const int j = tid * (ATTNX_MAXSEG / WAVE) + i;
+            if (j < nseg) fsum[j] = before + d[i];
+        }
     }
     __syncthreads();
     // K of each segment for binades E and E+1 (segk[2j + c]; -1: not usable).
@@ -2057,58 +2087,57 @@ __device__ __forceinline__ float serial_sum_seg(const float * e, int n, float * 
     }
     __syncthreads();
     if (tid < WAVE) {
-        // the walk, by wave 0 as uniform (scalar) code: lane l holds the
-        // table of segments l, l+64, ...; the fast step is integer work on
-        // the sum's bits; a segment run as floats reads its values 16 at a
-        // time, the next 16 in flight while the current 16 are added
-        int te[ATTNX_MAXSEG / WAVE], tk0[ATTNX_MAXSEG / WAVE], tk1[ATTNX_MAXSEG / WAVE];
-        #pragma unroll
-        for (int g = 0; g < ATTNX_MAXSEG / WAVE; g++) {
-            const int j = g * WAVE + tid;
-            te[g] = j < nseg ? sege[j] : -1000;
-            tk0[g] = j < nseg ? segk[2 * j] : -1;
-            tk1[g] = j < nseg ? segk[2 * j + 1] : -1;
-        }
+        // the walk, by wave 0. From segment j with the sum's bits sb (binade
+        // E), lane l takes segment j+l's K for E where its table has one;
+        // a prefix sum of the Ks over the lanes gives the longest run of
+        // segments that the chain crosses inside binade E with no tie, and
+        // the walk jumps over it. The segment that ends the run (a tie, a
+        // carry into the next binade, a binade the table lacks, a sum of 0)
+        // is added as the float chain, its values read 16 at a time, the
+        // next 16 in flight while the current 16 are added.
         unsigned sb = 0;                                  // the bits of the sum
-        #pragma unroll
-        for (int g = 0; g < ATTNX_MAXSEG / WAVE; g++) {
-            const int jn = min(nseg - g * WAVE, WAVE);
-            for (int jj = 0; jj < jn; jj++) {
-                const int ec = __builtin_amdgcn_readlane(te[g], jj);
-                const int k0 = __builtin_amdgcn_readlane(tk0[g], jj), k1 = __builtin_amdgcn_readlane(tk1[g], jj);
-                const int E = (int) (sb >> 23) - 127, c = E - ec;
-                if (sb >= 0x00800000u && (c == 0 || c == 1)) {
-                    const int k = c ? k1 : k0;
-                    const int m = (int) ((sb & 0x7FFFFFu) | 0x800000u) + k;
-                    if (k >= 0 && m < (1 << 24)) {
-                        sb = (sb & 0xFF800000u) | ((unsigned) m & 0x7FFFFFu);
-                        continue;
-                    }
-                }
-                float s = __builtin_bit_cast(float, sb);
-                const int i0 = (g * WAVE + jj) * ATTNX_SEG, i1 = min(n, i0 + ATTNX_SEG);
-                if (i1 - i0 == ATTNX_SEG) {
-                    const float4 * q = (const float4 *) (e + i0);
-                    float4 c4[2][4];
-                    #pragma unroll
-                    for (int r = 0; r < 4; r++) c4[0][r] = q[r];
-                    #pragma unroll
-                    for (int bl = 0; bl < ATTNX_SEG / 16; bl++) {
-                        if (bl + 1 < ATTNX_SEG / 16) {
-                            #pragma unroll
-                            for (int r = 0; r < 4; r++) c4[(bl + 1) & 1][r] = q[4 * (bl + 1) + r];
-                        }
-                        #pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const float4 v = c4[bl & 1][r];
-                            s = s + v.x; s = s + v.y; s = s + v.z; s = s + v.w;
-                        }
-                    }
-                } else {
-                    for (int i = i0; i < i1; i++) s = s + e[i];
-                }
-                sb = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(unsigned, s));
+        int j = 0;
+        while (j < nseg) {
+            const int jl = j + tid;
+            const int m0 = (int) ((sb & 0x7FFFFFu) | 0x800000u);
+            int k = -1;
+            if (sb >= 0x00800000u && jl < nseg) {
+                const int c = (int) (sb >> 23) - 127 - sege[jl];
+                k = c == 0 ? segk[2 * jl] : c == 1 ? segk[2 * jl + 1] : -1;
             }
+            const int P = wave_scan_i(max(k, 0));          // m0 + P < 2^31: each K < 2^24, 64 of them
+            const unsigned long long ok = __builtin_amdgcn_ballot_w64(k >= 0 && m0 + P < (1 << 24));
+            const int f = ~ok == 0ull ? WAVE : (int) __builtin_ctzll(~ok);
+            if (f > 0) {
+                const int pf = __builtin_amdgcn_readlane(P, f - 1);
+                sb = (sb & 0xFF800000u) | ((unsigned) (m0 + pf) & 0x7FFFFFu);
+                j += f;
+            }
+            if (f == WAVE || j >= nseg) continue;
+            float s = __builtin_bit_cast(float, sb);
+            const int i0 = j * ATTNX_SEG, i1 = min(n, i0 + ATTNX_SEG);
+            if (i1 - i0 == ATTNX_SEG) {
+                const float4 * q = (const float4 *) (e + i0);
+                float4 c4[2][4];
+                #pragma unroll
+                for (int r = 0; r < 4; r++) c4[0][r] = q[r];
+                #pragma unroll
+                for (int bl = 0; bl < ATTNX_SEG / 16; bl++) {
+                    if (bl + 1 < ATTNX_SEG / 16) {
+                        #pragma unroll
+                        for (int r = 0; r < 4; r++) c4[(bl + 1) & 1][r] = q[4 * (bl + 1) + r];
+                    }
+                    #pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float4 v = c4[bl & 1][r];
+                        s = s + v.x; s = s + v.y; s = s + v.z; s = s + v.w;
+                    }
+                }
+            } else {
+                for (int i = i0; i < i1; i++) s = s + e[i];
+            }
+            sb = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(unsigned, s));
+            j++;
         }
         if (tid == 0) *out = __builtin_bit_cast(float, sb);
     }
