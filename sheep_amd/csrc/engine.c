@@ -254,11 +254,14 @@ static void launch_layer(int L) {
     }
     // gate/up: one SwiGLU launch when they share a permutation and width; it
     // also quantizes h for down when down reads h in order
-    const int h_fused = (G.fuse & 2) && y->perm_down < 0 && G.F % 32 == 0;
+    // (in exact mode only behind the fused norm prologue)
+    const int x_fusable = (G.fuse & 1) && fusable(y->gate);
+    const int h_fused = (G.fuse & 2) && y->perm_down < 0 && G.F % 32 == 0 &&
+                        (!G.exact || (x_fusable && G.E <= gemv_fuse_max_cols(1)));
     if (y->perm_gu[0] == y->perm_gu[1] && y->gate->nbits == y->up->nbits) {
         gemv_fuse fu;
         memset(&fu, 0, sizeof fu);
-        const int x_fused = (G.fuse & 1) && G.E <= gemv_fuse_max_cols(h_fused) && fusable(y->gate);
+        const int x_fused = x_fusable && G.E <= gemv_fuse_max_cols(h_fused);
         if (x_fused) { fu.x = G.x; fu.norm_w = y->fn; fu.eps = G.eps; fu.perm = pdev(y->perm_gu[0]); }
         else prep(G.x, y->fn, NULL, G.E, y->perm_gu, 2, slot);
         if (h_fused) { fu.hq = G.hq; fu.hscale = G.hs; fu.hsums = G.hsum; }
@@ -553,7 +556,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     G.exact = env_int("SML_EXACT", 0) != 0;
     ops_set_exact(G.exact);
     if (G.exact) {
-        G.fuse &= 1;            // the norm prologues have exact forms; h quantization stays a launch
+        // the norm prologues and the h quantization have exact forms (Q4/Q8)
         if (n_ctx > 16384) hx_failf("exact mode holds at most 16384 positions");
     }
     const size_t kvn = (size_t) G.n_layer * n_ctx * G.KV * G.hd;

@@ -665,10 +665,11 @@ __device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first 
         for (int s = 0; s < RB; s++) acc[s] = seg_sum<LPR>(acc[s]);
     }
     if constexpr (HQ) {
-        // WG/16 consecutive outputs per workgroup (RB/2 gate/up pairs per
-        // wave, whole groups of 32): h = silu(g)*u, then its per-32
+        // HO consecutive outputs per workgroup (RB/2 gate/up pairs per row
+        // slot, whole groups of 32): h = silu(g)*u, then its per-32
         // quantization for the down projection
-        constexpr int HO = WG / 16;
+        constexpr int HO = (WG / WAVE) * RPW;
+        static_assert(HO % 32 == 0, "h quantization takes whole groups of 32 per workgroup");
         __shared__ float hb[HO];
         if (l == LPR - 1) {
             #pragma unroll
@@ -859,6 +860,16 @@ extern "C" __global__ __launch_bounds__(512) void sml_gemv_q4_h_i2_p(const sml_k
     extern "C" __global__ __launch_bounds__(256) void sml_gemv_q##NB##_s_r##RB##_i##NI##_xn(const sml_kgemv a) { \
         gemv_body<NB, RB, NI, 256, true, 1, true, false, 64, true>(a);                                      \
     }
+// _hxn: the exact SwiGLU with the norm prologue and h quantized per 32 in
+// its epilogue (32 outputs per workgroup: 8 waves of 4 pairs, or 16 of 2)
+#define GEMV_KERNEL_HXN(NB)                                                                                 \
+    extern "C" __global__ __launch_bounds__(512) void sml_gemv_q##NB##_hxn_r8_i1(const sml_kgemv a) {         \
+        gemv_body<NB, 8, 1, 512, true, 1, true, true, 64, true>(a);                                         \
+    }                                                                                                       \
+    extern "C" __global__ __launch_bounds__(1024) void sml_gemv_q##NB##_hxn1024_r4_i1(const sml_kgemv a) {    \
+        gemv_body<NB, 4, 1, 1024, true, 1, true, true, 64, true>(a);                                        \
+    }
+GEMV_KERNEL_HXN(4) GEMV_KERNEL_HXN(8)
 #define GEMV_EXACT(NB, K, KS)                                                                               \
     K(NB, 1, 2) K(NB, 1, 4) K(NB, 2, 1) K(NB, 2, 2) K(NB, 2, 4) K(NB, 4, 1) K(NB, 4, 2) K(NB, 4, 4)         \
     KS(NB, 2, 1) KS(NB, 2, 2) KS(NB, 2, 4) KS(NB, 4, 1) KS(NB, 4, 2) KS(NB, 4, 4)

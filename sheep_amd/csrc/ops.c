@@ -541,9 +541,10 @@ int op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int e
     } else if (!q || !scale || !sums) {
         hx_failf("gemv without an activation");
     }
-    // exact mode: the norm prologue has exact forms at Q4/Q8 only, h quantization none
-    if (g_exact && ((am && nb != 4 && nb != 8) || hq))
-        hx_failf("exact mode fuses only the norm prologue, and only into Q4/Q8 GEMVs");
+    // exact mode: the norm prologue and the h quantization have exact forms
+    // at Q4/Q8 only, h quantization only behind the norm prologue
+    if (g_exact && (((am || hq) && nb != 4 && nb != 8) || (hq && !am)))
+        hx_failf("exact mode fuses the norm prologue (and h quantization behind it) into Q4/Q8 GEMVs only");
     if (hq) {
         if (!swiglu || a.total_rows % 32) hx_failf("h quantization needs SwiGLU rows in whole groups");
         a.hq = fu->hq; a.hscale = fu->hscale; a.hsums = fu->hsums;
@@ -555,6 +556,21 @@ int op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int e
     // LDS: int8 codes, per-group (s, s*sum), and the fused prologue's gather buffer
     const size_t lds = ((size_t) cols + 8u * (size_t) (cols / 32) + 15u) / 16u * 16u + (am && fu->perm ? 4u * (size_t) cols : 0u);
     char name[48];
+    if (hq && g_exact) {
+        // the exact SwiGLU (the reference's float order per row, 64 lanes a
+        // row) with 32 outputs per workgroup: 8 waves of 4 gate/up pairs
+        // (SML_GEMV_HXWG=1024: 16 waves of 2); the products' exchange buffer
+        // (RB KB per wave) follows the codes and fields
+        const int wg = env_int("SML_GEMV_HXWG", 512) == 1024 ? 1024 : 512, rb = wg == 1024 ? 4 : 8;
+        const size_t base = ((size_t) cols + 8u * (size_t) (cols / 32) + 15u) / 16u * 16u;
+        size_t xl = base + (size_t) (wg / 64) * rb * 64 * 16 + (size_t) (wg / 64) * rb * 4;
+        if (xl < lds) xl = lds;
+        if (xl > 160 * 1024) hx_failf("exact h-quantizing GEMV of %d columns needs %zu bytes of LDS", cols, xl);
+        if (wg == 1024) snprintf(name, sizeof name, "sml_gemv_q%d_hxn1024_r4_i1", nb);
+        else snprintf(name, sizeof name, "sml_gemv_q%d_hxn_r8_i1", nb);
+        hx_launch(name, (unsigned) (a.total_rows / 32), 1, (unsigned) wg, xl, st, &a);
+        return 0;
+    }
     if (hq) {
         // 16 lanes per row: NI chunks per lane with 16*NI >= groups (a second
         // pass beyond 8)

@@ -106,9 +106,15 @@ def test_exact_gemv_fused_norm_bit_exact(tmpdir_s, nb, rows, cols, boundary):
     same_bits(y.read(np.float32), ob.matvec(t, q, s, u), f"{rows}x{cols} Q{nb} fused norm")
 
 
-def test_exact_swiglu_fused_norm_bit_exact(tmpdir_s):
+@pytest.mark.parametrize("hq", [None, "512", "1024"])
+def test_exact_swiglu_fused_norm_bit_exact(tmpdir_s, hq, monkeypatch):
     """The exact SwiGLU GEMV with the prologue (the decode step's gate/up
-    form): h equals the oracle's norm, gate, up and SiLU bit for bit."""
+    form): h equals the oracle's norm, gate, up and SiLU bit for bit; with
+    h quantized in the epilogue (32 outputs per workgroup of 512 or 1024
+    threads), its codes, scales and sums equal the oracle's quantization
+    of that h."""
+    if hq:
+        monkeypatch.setenv("SML_GEMV_HXWG", hq)
     n_ff = 8960
     p = tmpdir_s / f"xffn{n_ff}.ssf"
     if not p.exists():
@@ -120,15 +126,20 @@ def test_exact_swiglu_fused_norm_bit_exact(tmpdir_s):
     x = (rng.standard_normal(1536) * 2).astype(np.float32)
     w = (1 + 0.02 * rng.standard_normal(1536)).astype(np.float32)
     h = sa.DevBuf(n_ff * 4)
+    hact = sa.Act(n_ff) if hq else None
     with exact_mode():
         sa.matvec_swiglu_fused(sa.Mat.from_file(p, g.name), sa.Mat.from_file(p, u.name), h, x=sa.DevBuf.of(x),
-                               w=sa.DevBuf.of(w), perm=sa.DevBuf.of(g.perm.astype(np.int32)), eps=1e-5)
+                               w=sa.DevBuf.of(w), perm=sa.DevBuf.of(g.perm.astype(np.int32)), eps=1e-5,
+                               hact=hact)
     normed = np.zeros(1536, np.float32)
     ob.oracle().orc_rms_norm(normed.ctypes.data, x.ctypes.data, w.ctypes.data, 1536, np.float32(1e-5))
     q, s, su = ob.quantize_act(normed[g.perm])
     yg, yu = ob.matvec(g, q, s, su), ob.matvec(u, q, s, su)
     ob.oracle().orc_silu_mul(yg.ctypes.data, yu.ctypes.data, n_ff)
     same_bits(h.read(np.float32), yg, "swiglu with the fused norm")
+    if hq:
+        for a, b, name in zip(hact.read(), ob.quantize_act(yg), ("q", "scale", "sums")):
+            np.testing.assert_array_equal(a, b, err_msg=f"h quantized in the epilogue: {name}")
 
 
 @pytest.mark.parametrize("n_ff", [8960, 2048 + 128])
