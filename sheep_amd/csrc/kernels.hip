@@ -875,6 +875,19 @@ GEMV_KERNEL_HXN(4) GEMV_KERNEL_HXN(8)
     KS(NB, 2, 1) KS(NB, 2, 2) KS(NB, 2, 4) KS(NB, 4, 1) KS(NB, 4, 2) KS(NB, 4, 4)
 GEMV_EXACT(4, GEMV_KERNEL_X, GEMV_KERNEL_SX) GEMV_EXACT(8, GEMV_KERNEL_X, GEMV_KERNEL_SX)
 GEMV_EXACT(4, GEMV_KERNEL_XN, GEMV_KERNEL_SXN) GEMV_EXACT(8, GEMV_KERNEL_XN, GEMV_KERNEL_SXN)
+// wider exact forms: 8 rows per wave, and 512-thread workgroups (suffix _w512)
+#define GEMV_KERNEL_XW(NB, RB, NI, W, AM, SFX)                                                              \
+    extern "C" __global__ __launch_bounds__(W) void sml_gemv_q##NB##_r##RB##_i##NI##_##SFX(const sml_kgemv a) { \
+        gemv_body<NB, RB, NI, W, true, AM, false, false, 64, true>(a);                                      \
+    }
+#define GEMV_EXACT_WIDE(NB)                                                                                 \
+    GEMV_KERNEL_XW(NB, 8, 1, 256, 0, x) GEMV_KERNEL_XW(NB, 8, 2, 256, 0, x)                                 \
+    GEMV_KERNEL_XW(NB, 8, 1, 512, 0, x_w512) GEMV_KERNEL_XW(NB, 4, 2, 512, 0, x_w512)                       \
+    GEMV_KERNEL_XW(NB, 2, 4, 512, 0, x_w512) GEMV_KERNEL_XW(NB, 8, 1, 256, 1, xn)                           \
+    GEMV_KERNEL_XW(NB, 8, 1, 512, 1, xn_w512) GEMV_KERNEL_XW(NB, 4, 1, 512, 1, xn_w512)                     \
+    GEMV_KERNEL_XW(NB, 2, 2, 512, 1, xn_w512) GEMV_KERNEL_XW(NB, 2, 1, 512, 1, xn_w512)                     \
+    GEMV_KERNEL_XW(NB, 1, 1, 512, 1, xn_w512)
+GEMV_EXACT_WIDE(4) GEMV_EXACT_WIDE(8)
 
 // ---------------------------------------------------------------- norm + quantize
 //

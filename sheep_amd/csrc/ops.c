@@ -596,16 +596,37 @@ int op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int e
         // (RB*NI KB per wave) to the lanes that run its superblock chains; with
         // the fused prologue (_xn) they reuse its gather buffer's LDS
         pick_shape(a.total_rows, cols, nb, swiglu, 0, &rb, &ni);
+        // one-matrix forms with the prologue: 512 threads and the fast
+        // path's row choice, one chunk per pass (6144 x 4096: 9.3 -> 6.9 us,
+        // the prologue's share split over twice the threads)
+        int wg = 256;
+        if (am && !swiglu) {
+            pick_shape(a.total_rows, cols, nb, 0, 1, &rb, &ni);
+            wg = 512;
+        }
+        // (tuning, one-matrix forms: SML_GEMV_XRB 1/2/4/8 rows per wave,
+        // SML_GEMV_XNI 1/2/4, SML_GEMV_XWG 256/512 threads; not every
+        // combination is built)
+        if (!swiglu) {
+            const int xr = env_int("SML_GEMV_XRB", 0), xi = env_int("SML_GEMV_XNI", 0);
+            if (xr == 1 || xr == 2 || xr == 4 || xr == 8) rb = xr;
+            if (xi == 1 || xi == 2 || xi == 4) ni = xi;
+            const int xw = env_int("SML_GEMV_XWG", 0);
+            if (xw == 256 || xw == 512) wg = xw;
+        }
         const size_t base = ((size_t) cols + 8u * (size_t) (cols / 32) + 15u) / 16u * 16u;
-        size_t xl = base + (size_t) 4 * ni * rb * 64 * 16 + (size_t) 4 * rb * 4;
-        while (xl > 65536 && ni > 1) { ni /= 2; xl = base + (size_t) 4 * ni * rb * 64 * 16 + (size_t) 4 * rb * 4; }
+        size_t xl = base + (size_t) (wg / 64) * ni * rb * 64 * 16 + (size_t) (wg / 64) * rb * 4;
+        while (xl > 160 * 1024 && ni > 1) {
+            ni /= 2;
+            xl = base + (size_t) (wg / 64) * ni * rb * 64 * 16 + (size_t) (wg / 64) * rb * 4;
+        }
         if (xl < lds) xl = lds;
-        if (xl > 65536) hx_failf("exact GEMV of %d columns needs %zu bytes of LDS", cols, xl);
+        if (xl > 160 * 1024) hx_failf("exact GEMV of %d columns needs %zu bytes of LDS", cols, xl);
         const int rows_per_wave = swiglu ? rb / 2 : rb;
         const int waves = (a.total_rows + rows_per_wave - 1) / rows_per_wave;
         if (swiglu) snprintf(name, sizeof name, "sml_gemv_q%d_s_r%d_i%d_x%s", nb, rb, ni, am ? "n" : "");
-        else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_x%s", nb, rb, ni, am ? "n" : "");
-        hx_launch(name, (unsigned) ((waves + 3) / 4), 1, 256, xl, st, &a);
+        else snprintf(name, sizeof name, "sml_gemv_q%d_r%d_i%d_x%s%s", nb, rb, ni, am ? "n" : "", wg == 512 ? "_w512" : "");
+        hx_launch(name, (unsigned) ((waves + wg / 64 - 1) / (wg / 64)), 1, (unsigned) wg, xl, st, &a);
         return 0;
     }
     int wg = 256;
