@@ -56,6 +56,14 @@ int sml_hip_field_search(const float * w, int rows, int cols, int group, const f
 int sml_hip_unpack_dequant(const int32_t * qweight, const int32_t * qzeros, const uint16_t * scales,
                            const int32_t * g_idx, int rows, int cols, int bits, int group, int zero_add, int awq,
                            float * out);
+// GGUF blocks of ggml type Q8_0 (8), Q4_0 (2) or Q6_K (14), row-major with
+// each row's blocks in order (cols a multiple of 32, of 256 for Q6_K),
+// dequantized to out [rows][cols] by ggml's published formulas and rounded
+// to fp16: the float16 copy transformers writes from a GGUF before the
+// reference re-quantizes it (sml_hip_requant takes it from there).
+// replaces tooling/sml_gguf.py:19-27 (the GGUF read through transformers) for
+// one tensor of these types
+int sml_hip_gguf_dequant(int type, const uint8_t * blocks, int rows, int cols, float * out);
 // Re-quantize w [rows][cols] (cols a multiple of 256) into SSF FLAT width
 // nbits (2..8): column order perm_in (NULL: ascending max |w| over the rows,
 // ties by column), the asymmetric grid (20 candidates, 3 refits), two-level

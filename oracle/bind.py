@@ -59,6 +59,7 @@ def oracle():
             "orc_expf_published": (c_float, [c_float]),
             "orc_q4k_dequant_row": (None, [c_void_p, c_int, c_void_p]),
             "orc_q5k_dequant_row": (None, [c_void_p, c_int, c_void_p]),
+            "orc_gguf_dequant_f16_row": (c_int, [c_int, c_void_p, c_int, c_void_p]),
             "orc_gptq_dequant_row_gidx": (None, [c_void_p] * 4 + [c_int] * 5 + [c_void_p]),
             "orc_gptq_matvec_gidx": (None, [c_void_p] * 4 + [c_int] * 4 + [c_void_p, c_void_p]),
             "orc_expf_mismatches": (ctypes.c_long, [ctypes.c_uint]),
@@ -603,6 +604,20 @@ def q4k_random_blocks(rows, cols, seed):
         blk[i, 4:16] = q4k_pack_scales(rng.integers(0, 64, 8), rng.integers(0, 64, 8))
     blk[:, 16:] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
     return blk.reshape(rows, cols // 256, 144)
+
+
+GGUF_BLOCK = {8: (32, 34), 2: (32, 18), 14: (256, 210)}   # ggml type: (weights, bytes) per block
+
+
+def gguf_dequant_f16(gtype, blocks, rows, cols):
+    """GGUF Q8_0 (8), Q4_0 (2) or Q6_K (14) blocks [rows][cols/qk][bytes] to
+    float32 [rows][cols] holding the fp16 copy (orc_gguf_dequant_f16_row)."""
+    bl = np.ascontiguousarray(blocks, np.uint8).reshape(rows, -1)
+    out = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        if oracle().orc_gguf_dequant_f16_row(gtype, bl[r].ctypes.data, cols, out[r].ctypes.data) != 0:
+            raise ValueError(f"ggml type {gtype} at {cols} columns")
+    return out
 
 
 def q5k_dequant(blocks, rows, cols):

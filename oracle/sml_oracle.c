@@ -923,6 +923,52 @@ void orc_q4k_dequant_row(const uint8_t * blocks, int cols, float * out) {
     }
 }
 
+// ggml's Q8_0, Q4_0 and Q6_K blocks (see the header), each weight's float
+// value rounded to fp16
+int orc_gguf_dequant_f16_row(int type, const uint8_t * blocks, int cols, float * out) {
+    const int qk = type == 14 ? 256 : 32;
+    const size_t bs = type == 8 ? 34 : type == 2 ? 18 : type == 14 ? 210 : 0;
+    if (!bs || cols % qk) return -1;
+    for (int b = 0; b < cols / qk; b++) {
+        const uint8_t * blk = blocks + (size_t) b * bs;
+        float * y = out + (size_t) b * qk;
+        uint16_t dh;
+        if (type == 8) {
+            memcpy(&dh, blk, 2);
+            const float d = orc_f16_to_f32(dh);
+            for (int i = 0; i < 32; i++) y[i] = d * (float) (int8_t) blk[2 + i];
+        } else if (type == 2) {
+            memcpy(&dh, blk, 2);
+            const float d = orc_f16_to_f32(dh);
+            for (int j = 0; j < 16; j++) {
+                y[j] = d * (float) ((blk[2 + j] & 15) - 8);
+                y[j + 16] = d * (float) ((blk[2 + j] >> 4) - 8);
+            }
+        } else {
+            const uint8_t * ql = blk, * qh = blk + 128;
+            const int8_t * sc = (const int8_t *) (blk + 192);
+            memcpy(&dh, blk + 208, 2);
+            const float d = orc_f16_to_f32(dh);
+            for (int half = 0; half < 2; half++) {
+                for (int l = 0; l < 32; l++) {
+                    const int is = l / 16;
+                    const int q1 = ((ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                    const int q2 = ((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                    const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                    const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                    y[l] = d * (float) sc[is] * (float) q1;
+                    y[l + 32] = d * (float) sc[is + 2] * (float) q2;
+                    y[l + 64] = d * (float) sc[is + 4] * (float) q3;
+                    y[l + 96] = d * (float) sc[is + 6] * (float) q4;
+                }
+                y += 128; ql += 64; qh += 32; sc += 8;
+            }
+        }
+    }
+    for (int i = 0; i < cols; i++) out[i] = orc_f16_to_f32(orc_f32_to_f16(out[i]));
+    return 0;
+}
+
 // ggml's block_q5_K and dequantize_row_q5_K: Q4_K's d, dmin and scale bytes,
 // then qh[32] (bit j of byte l: the fifth bit of weight l of sub-block j) and
 // the low nibbles qs[128] in Q4_K's order; weight d*sc*(q + 16*h) - dmin*m

@@ -121,6 +121,17 @@ void orc_awq_dequant_row(const int32_t * qweight, const int32_t * qzeros, const 
 // same 32 code bytes, y = (d*sc)*q - dmin*m.
 void orc_q4k_dequant_row(const uint8_t * blocks, int cols, float * out);
 void orc_q5k_dequant_row(const uint8_t * blocks, int cols, float * out);
+// One row of ggml's Q8_0 (type 8: 34-byte blocks of fp16 d and 32 int8
+// codes, y = d*q), Q4_0 (type 2: 18-byte blocks of fp16 d and 16 code bytes,
+// the low nibbles weights 0..15 and the high ones 16..31, y = d*(q - 8)) or
+// Q6_K (type 14: 210-byte blocks of ql[128], qh[64], int8 scales[16] and
+// fp16 d; per 128 weights, weight l+32k takes bits 4(k/2) of ql[l + 32(k&1)]
+// and bits 2k of qh[l], y = (d*scales[i/16])*(q - 32)) blocks dequantized by
+// the published formulas (ggml's dequantize_row_q8_0 / _q4_0 / _q6_K, which
+// gguf-py's numpy restatement follows in the same float order), then rounded
+// to fp16 as the float16 copy transformers writes. Returns -1 for another
+// type or a width that is not whole blocks.
+int orc_gguf_dequant_f16_row(int type, const uint8_t * blocks, int cols, float * out);
 
 // ---------------------------------------------------------------- expf restated
 // The C library's expf (glibc 2.35, x86-64 with FMA) from its published

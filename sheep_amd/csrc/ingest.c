@@ -164,6 +164,19 @@ int sml_hip_unpack_dequant(const int32_t * qweight, const int32_t * qzeros, cons
     return 0;
 }
 
+int sml_hip_gguf_dequant(int type, const uint8_t * blocks, int rows, int cols, float * out) {
+    OP_BEGIN(-1);
+    const int qk = type == 14 ? 256 : 32;
+    if (type != 8 && type != 2 && type != 14) hx_failf("ggml type %d: only Q8_0 (8), Q4_0 (2) and Q6_K (14) dequantize here", type);
+    if (rows <= 0 || cols <= 0 || cols % qk) hx_failf("ggml type %d: %dx%d is not whole blocks of %d", type, rows, cols, qk);
+    sml_king_gguf a;
+    memset(&a, 0, sizeof a);
+    a.blocks = blocks; a.out = out; a.rows = rows; a.cols = cols; a.type = type;
+    hx_launch("sml_ing_gguf", (unsigned) (((int64_t) rows * cols + 255) / 256), 1, 256, 0, 0, &a);
+    HX_LEAVE();
+    return 0;
+}
+
 // The candidate range factors the quantizer tries (20: six over 0.6..0.85,
 // fourteen over 0.88..1.04), numpy's linspace in double rounded to float,
 // as tooling/sml_grid_c.py:41-42 builds them.

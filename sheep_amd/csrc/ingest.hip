@@ -45,6 +45,36 @@ extern "C" __global__ __launch_bounds__(256) void sml_ing_dequant(const sml_king
     a.out[i] = h2f(f2h(v));
 }
 
+// GGUF Q8_0, Q4_0 and Q6_K (ggml's published block layouts and
+// dequantize_row_* formulas, in their float order: no contraction in this
+// file): one thread per weight; the value rounded to fp16 as the float16
+// copy transformers writes.
+extern "C" __global__ __launch_bounds__(256) void sml_ing_gguf(const sml_king_gguf a) {
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t) a.rows * a.cols) return;
+    const int r = (int) (i / a.cols), k = (int) (i % a.cols);
+    float v;
+    if (a.type == 8) {
+        const uint8_t * blk = a.blocks + ((size_t) r * (a.cols / 32) + k / 32) * 34;
+        const float d = h2f((uint16_t) (blk[0] | (blk[1] << 8)));
+        v = d * (float) (int8_t) blk[2 + k % 32];
+    } else if (a.type == 2) {
+        const uint8_t * blk = a.blocks + ((size_t) r * (a.cols / 32) + k / 32) * 18;
+        const float d = h2f((uint16_t) (blk[0] | (blk[1] << 8)));
+        const int j = k % 32, b = blk[2 + (j & 15)];
+        v = d * (float) ((j < 16 ? b & 15 : b >> 4) - 8);
+    } else {
+        const uint8_t * blk = a.blocks + ((size_t) r * (a.cols / 256) + k / 256) * 210;
+        const int w = k % 256, h = w / 128, l = w % 32, kk = (w % 128) / 32;   // weight l + 32 kk of half h
+        const uint8_t ql = blk[64 * h + l + 32 * (kk & 1)], qh = blk[128 + 32 * h + l];
+        const int q = (((ql >> (4 * (kk >> 1))) & 15) | (((qh >> (2 * kk)) & 3) << 4)) - 32;
+        const float d = h2f((uint16_t) (blk[208] | (blk[209] << 8)));
+        const float sc = (float) (int8_t) blk[192 + w / 16];
+        v = d * sc * (float) q;
+    }
+    a.out[i] = h2f(f2h(v));
+}
+
 // ---------------------------------------------------------------- column order
 // numpy's max over a column: NaN wins, otherwise the largest
 __device__ __forceinline__ float np_max(float m, float x, bool first) {

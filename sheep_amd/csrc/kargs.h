@@ -356,6 +356,10 @@ typedef struct {
     int rows, cols, bits, group, zero_add, awq;
 } sml_king_dequant;
 
+// GGUF Q8_0 / Q4_0 / Q6_K blocks (ggml type 8 / 2 / 14; row-major, blocks
+// along each row) to the float16 copy in fp32: out [rows][cols]
+typedef struct { const uint8_t * blocks; float * out; int rows, cols, type; } sml_king_gguf;
+
 // part[y][c] = max over rows [y*chunk, (y+1)*chunk) of |w[r][c]| (NaN wins);
 // then key[c] = the max over y of part[y][c]
 typedef struct { const float * w; float * part; int rows, cols, chunk; } sml_king_colmax;

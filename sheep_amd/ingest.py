@@ -29,6 +29,7 @@ _SIGS = [
                                 c_int, c_int, c_void_p, c_int]),
     ("sml_hip_unpack_dequant", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                        c_int, c_void_p]),
+    ("sml_hip_gguf_dequant", c_int, [c_int, c_void_p, c_int, c_int, c_void_p]),
     ("sml_hip_requant", c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_int, ctypes.POINTER(c_void_p),
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("sml_hip_requant_last_ms", c_float, []),
@@ -207,6 +208,31 @@ def ingest_gptq(t, qc, nbits=None, radius=2, keep_codes=False):
     a = _gptq_args(t, qc)
     w = _dequant(*a)
     return requantize_dev(w, a[4], a[5], nbits or a[6], None, None, radius, keep_codes)
+
+
+GGUF_TYPES = {"Q8_0": (8, 32, 34, 8), "Q4_0": (2, 32, 18, 4), "Q6_K": (14, 256, 210, 6)}   # type, weights, bytes, bits
+
+
+def gguf_dequant(kind, blocks, rows, cols):
+    """GGUF Q8_0 / Q4_0 / Q6_K blocks (host bytes, [rows][cols/qk][bytes]) to
+    the float16 copy in fp32 on the device (sml_hip_gguf_dequant)."""
+    gtype, qk, bs, _ = GGUF_TYPES[kind]
+    raw = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    if cols % qk or raw.size != rows * (cols // qk) * bs:
+        raise ValueError(f"{kind} {rows}x{cols}: {raw.size} bytes is not whole blocks")
+    src = DevBuf.of(raw)
+    out = DevBuf(rows * cols * 4)
+    if _lib().sml_hip_gguf_dequant(gtype, src.ptr, rows, cols, out.ptr) != 0:
+        _err("gguf_dequant")
+    return out
+
+
+def ingest_gguf(kind, blocks, rows, cols, nbits=None, radius=2, keep_codes=False):
+    """A GGUF Q8_0 / Q4_0 / Q6_K tensor to SSF FLAT (nbits None: the block
+    type's own width), dequantized and re-quantized on the device, the route
+    the reference takes for a GGUF it reads through transformers."""
+    w = gguf_dequant(kind, blocks, rows, cols)
+    return requantize_dev(w, rows, cols, nbits or GGUF_TYPES[kind][3], None, None, radius, keep_codes)
 
 
 def ingest_awq(t, qc, nbits=None, radius=2, keep_codes=False):

@@ -188,3 +188,112 @@ def test_kquant_on_the_gpu(kind, rows, cols, seed):
     assert np.abs(hg - g).max() <= 1e-3 * np.abs(g).max()
     m.free()
     up.free()
+
+
+# ------------------------------------------------- Q8_0, Q4_0, Q6_K: dequantized, then re-quantized
+# These block types do not factor into the FLAT record's per-256 fp16 step
+# times a per-32 integer, so they take the reference's own route for a GGUF:
+# the float16 copy (transformers reading the file, tooling/sml_gguf.py:19-27)
+# re-quantized by the quantizer (the GPU ingest, sml_hip_requant).
+
+def f16(x):
+    return np.array([x], np.float16).view(np.uint8)
+
+
+def test_q8_0_known_answers():
+    """d = 0.5: weight i of the block is 0.5 * code i; a second block with
+    d = 3 (exact products); codes -128, -1, 0, 1, 127 included."""
+    codes = np.array([-128, -1, 0, 1, 127] + list(range(-13, 14)), np.int8)
+    b = np.concatenate([f16(0.5), codes.view(np.uint8), f16(3.0), codes[::-1].copy().view(np.uint8)])
+    w = ob.gguf_dequant_f16(8, b, 1, 64)[0]
+    assert w[0] == -64.0 and w[1] == -0.5 and w[2] == 0.0 and w[3] == 0.5 and w[4] == 63.5
+    assert np.array_equal(w[:32], 0.5 * codes.astype(np.float32))
+    assert w[32] == 3.0 * 13 and w[63] == -384.0
+
+
+def test_q4_0_known_answers():
+    """Byte j's low nibble is weight j, its high nibble weight j + 16; value
+    d * (nibble - 8)."""
+    qs = np.array([(j & 15) | ((15 - j) << 4) for j in range(16)], np.uint8)
+    b = np.concatenate([f16(0.25), qs])
+    w = ob.gguf_dequant_f16(2, b, 1, 32)[0]
+    for j in range(16):
+        assert w[j] == 0.25 * (j - 8), j
+        assert w[j + 16] == 0.25 * (15 - j - 8), j
+
+
+def q6k_block(code_at=None, d=1.0):
+    """A Q6_K block with every code 32 (weight 0) except code_at = {weight:
+    code}; scales[j] = j + 1. Bytes placed by hand from the layout: weight
+    128h + 32k + l takes ql[64h + l + 32(k & 1)] (low nibble for k < 2, high
+    for k >= 2) and bits 2k..2k+1 of qh[32h + l]."""
+    ql = np.zeros(128, np.uint8)
+    qh = np.full(64, 0xAA, np.uint8)          # code 32 = 0b10_0000: high pair 2 in every slot
+    for wgt, c in (code_at or {}).items():
+        h, i = divmod(wgt, 128)
+        k, l = divmod(i, 32)
+        bi = 64 * h + l + 32 * (k & 1)
+        sh = 4 * (k >> 1)
+        ql[bi] = (int(ql[bi]) & (0xFF ^ (15 << sh))) | ((c & 15) << sh)
+        qi = 32 * h + l
+        qh[qi] = (int(qh[qi]) & (0xFF ^ (3 << (2 * k)))) | ((c >> 4) << (2 * k))
+    sc = np.arange(1, 17, dtype=np.int8)
+    return np.concatenate([ql, qh, sc.view(np.uint8), f16(d)])
+
+
+@pytest.mark.parametrize("wgt,code", [(0, 63), (37, 63), (70, 0), (101, 17), (127, 48), (128, 5), (200, 33),
+                                      (255, 62)])
+def test_q6k_known_answers(wgt, code):
+    """One weight's code set: that weight is d * scales[w/16] * (code - 32)
+    and every other weight 0 -- which pins the ql byte, the nibble, the qh
+    bit pair and the scale each weight reads."""
+    w = ob.gguf_dequant_f16(14, q6k_block({wgt: code}, d=0.5), 1, 256)[0]
+    want = np.zeros(256, np.float32)
+    want[wgt] = np.float32(0.5 * (wgt // 16 + 1) * (code - 32))
+    assert np.array_equal(w, want), (wgt, np.flatnonzero(w), w[np.flatnonzero(w)])
+
+
+def test_q6k_negative_scales_and_fp16_rounding():
+    """Signed scales; products rounded once to fp16 (d = 0.1 is not exact:
+    (d*sc)*q in float, then fp16)."""
+    blk = q6k_block({i: (i * 7) % 64 for i in range(256)}, d=0.1)
+    blk[192:208] = np.array([-128, -3, 5, 127, -1, 0, 2, 64, -64, 9, -9, 100, -100, 1, 33, -77], np.int8).view(np.uint8)
+    w = ob.gguf_dequant_f16(14, blk, 1, 256)[0]
+    d = np.float32(np.float16(0.1))
+    sc = blk[192:208].view(np.int8).astype(np.float32)
+    for i in (0, 17, 40, 95, 130, 255):
+        v = (d * sc[i // 16]) * np.float32((i * 7) % 64 - 32)
+        assert w[i] == np.float32(np.float16(v)), i
+
+
+def _numpy_q6k(blocks):
+    """gguf-py's published numpy formulation of Q6_K (reshapes and shifts
+    over whole blocks), an independent statement of the same layout."""
+    b = blocks.reshape(-1, 210)
+    n = b.shape[0]
+    ql, qh, sc, d = b[:, :128], b[:, 128:192], b[:, 192:208], b[:, 208:210]
+    d = d.copy().view(np.float16).astype(np.float32)
+    sc = sc.copy().view(np.int8).astype(np.float32)
+    dd = (d * sc).reshape(n, 16, 1)
+    lo = (ql.reshape(n, -1, 1, 64) >> np.array([0, 4], np.uint8).reshape(1, 1, 2, 1)) & np.uint8(15)
+    lo = lo.reshape(n, -1, 32)
+    hi = (qh.reshape(n, -1, 1, 32) >> np.array([0, 2, 4, 6], np.uint8).reshape(1, 1, 4, 1)) & np.uint8(3)
+    hi = hi.reshape(n, -1, 32)
+    q = (lo | (hi << np.uint8(4))).astype(np.int8) - np.int8(32)
+    return (dd * q.reshape(n, 16, -1).astype(np.float32)).reshape(n, 256).astype(np.float16).astype(np.float32)
+
+
+def test_q6k_equals_the_numpy_formulation():
+    rng = np.random.default_rng(6)
+    rows, cols = 7, 768
+    blocks = rng.integers(0, 256, (rows, cols // 256, 210)).astype(np.uint8)
+    blocks[..., 208:210] = (rng.standard_normal((rows, cols // 256)) * 0.01).astype(np.float16)[..., None].view(np.uint8)
+    got = ob.gguf_dequant_f16(14, blocks, rows, cols)
+    assert np.array_equal(got, _numpy_q6k(blocks).reshape(rows, cols))
+
+
+def test_gguf_dequant_refuses_other_types_and_partial_blocks():
+    with pytest.raises(ValueError):
+        ob.gguf_dequant_f16(12, np.zeros(144, np.uint8), 1, 256)
+    with pytest.raises(ValueError):
+        ob.gguf_dequant_f16(14, np.zeros(210, np.uint8), 1, 128)

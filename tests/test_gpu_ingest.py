@@ -206,3 +206,54 @@ def test_ingest_awq_and_written_file(tmpdir_s):
     if ob.have_ref():
         for r in (0, 511, 1023):
             assert np.array_equal(ob.ref_dequant_row(t, r), ob.dequant_row(t, r))
+
+
+def _gguf_blocks(kind, rows, cols, rng):
+    """Random GGUF blocks of one type: random code bytes; fp16 d of assorted
+    sizes, a few zero, subnormal or negative."""
+    gtype, qk, bs, _ = ingest.GGUF_TYPES[kind]
+    b = rng.integers(0, 256, (rows, cols // qk, bs)).astype(np.uint8)
+    d = (rng.standard_normal((rows, cols // qk)) * 0.02).astype(np.float16)
+    d.flat[::97] = np.float16(0)
+    d.flat[5::89] = np.float16(3e-7)                  # subnormal in fp16
+    at = 208 if kind == "Q6_K" else 0
+    b[..., at:at + 2] = d[..., None].view(np.uint8)
+    return gtype, b
+
+
+@pytest.mark.parametrize("kind", ["Q8_0", "Q4_0", "Q6_K"])
+def test_gguf_dequant_equals_oracle(kind):
+    """Every weight of the device's float16 copy equals the oracle's
+    restatement of ggml's dequantize_row_* bit for bit."""
+    rng = np.random.default_rng(len(kind) * 31 + ord(kind[1]))
+    rows, cols = 300, 4096
+    gtype, b = _gguf_blocks(kind, rows, cols, rng)
+    got = ingest.gguf_dequant(kind, b, rows, cols).read(np.float32).reshape(rows, cols)
+    want = ob.gguf_dequant_f16(gtype, b, rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["Q8_0", "Q6_K", "Q4_0"])
+def test_ingest_gguf_equals_oracle(kind):
+    """A GGUF tensor of each type re-quantized at the type's own width (8,
+    6, 4 bits): fields, order and codes equal the oracle's re-quantization of
+    the oracle's float16 copy, and its GEMV stays within the re-quantization
+    error of that copy."""
+    rng = np.random.default_rng(90 + len(kind))
+    rows, cols = 512, 2048
+    gtype, b = _gguf_blocks(kind, rows, cols, rng)
+    nb = ingest.GGUF_TYPES[kind][3]
+    print(f"ingest_gguf {kind} {rows}x{cols} -> Q{nb}", flush=True)
+    res = ingest.ingest_gguf(kind, b, rows, cols, keep_codes=True)
+    w16 = ob.gguf_dequant_f16(gtype, b, rows, cols)
+    h = _same(res, ob.requant(w16, nb), nb)
+    x = np.random.default_rng(3).standard_normal(cols).astype(np.float32)
+    xd = sa.DevBuf.of(x[h["perm"]])
+    act, y = sa.Act(cols), sa.DevBuf(rows * 4)
+    sa.normq(xd, act)
+    sa.matvec(res.mat(), act, y)
+    got = y.read(np.float32)
+    ref = w16.astype(np.float64) @ x.astype(np.float64)
+    rel = np.sqrt(np.mean((got - ref) ** 2) / np.mean(ref ** 2))
+    print(f"{kind}: re-quantized GEMV vs the float16 copy rel-RMS {rel:.4f}", flush=True)
+    assert rel < 0.1
