@@ -54,6 +54,8 @@ def oracle():
             "orc_attn_head": (None, [c_void_p, c_void_p, c_void_p, ctypes.c_size_t, c_int, c_int, c_float, c_void_p, c_void_p]),
             "orc_silu_mul": (None, [c_void_p, c_void_p, c_int]),
             "orc_moe_route": (c_int, [c_void_p, c_int, c_int, c_uint, c_void_p, c_void_p]),
+            "orc_moe_route2": (c_int, [c_void_p, c_int, c_int, c_uint, c_float, c_int, c_int, c_void_p, c_void_p,
+                                       c_void_p]),
             "orc_router": (None, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
             "orc_argmax": (c_int, [c_void_p, c_int]),
             "orc_expf_published": (c_float, [c_float]),
@@ -228,6 +230,8 @@ def ref():
             "ref_prefill": (P(c_float), [c_void_p, c_void_p, c_int, c_int]),
             "ref_n_vocab": (c_int, [c_void_p]),
             "ref_moe_route": (c_int, [c_void_p, c_int, c_int, c_uint, c_void_p, c_void_p]),
+            "ref_moe_route2": (c_int, [c_void_p, c_int, c_int, c_uint, c_float, c_int, c_int, c_void_p, c_void_p,
+                                       c_void_p]),
             "sml_quantize_act": (None, [P(SmlAct), c_void_p, c_int]),
             "sml_quantize_act_sb": (None, [P(SmlAct), c_void_p, c_int]),
             "sml_matvec_rows_flat4": (None, [c_void_p] * 6 + [P(SmlAct), c_int, c_int, c_int]),

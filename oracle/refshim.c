@@ -76,6 +76,25 @@ int ref_moe_route(const float * lg, int ne, int k, unsigned moe_flags, int * sel
     return sml_moe_route(&hd, &ly, lg, sc, ch, sel, w);
 }
 
+// sml_moe_route with every routing field: flags, moe_scale, groups,
+// topk_group and the layer's correction bias (exp_bias, NULL for none).
+int ref_moe_route2(const float * lg, int ne, int k, unsigned moe_flags, float scale, int groups, int topk_group,
+                   const float * exp_bias, int * sel, float * w) {
+    sml_hdr hd;
+    sml_layer ly;
+    memset(&hd, 0, sizeof hd);
+    memset(&ly, 0, sizeof ly);
+    hd.n_expert_used = (uint32_t) k;
+    hd.moe_flags = moe_flags;
+    hd.moe_scale = scale;
+    hd.moe_groups = (uint32_t) groups;
+    hd.moe_topk_group = (uint32_t) topk_group;
+    ly.n_exp = ne;
+    ly.exp_bias = exp_bias;
+    float sc[64], ch[64];
+    return sml_moe_route(&hd, &ly, lg, sc, ch, sel, w);
+}
+
 // Several contexts of one model, set up as sml-batched does
 // (sml/sml-batched.c:70-76), for sml_forward_multi.
 typedef struct { sml_model m; int ns; sml_ctx * cs; sml_ctx ** cp; } ref_mh;

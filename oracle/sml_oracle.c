@@ -430,6 +430,88 @@ int orc_moe_route(const float * lg, int ne, int k, unsigned moe_flags, int * sel
     return k;
 }
 
+// the best untaken index by key, ties to the lower index
+static int orc_best_untaken(const float * key, int ne, const int * sel, int nsel) {
+    int best = -1;
+    for (int e = 0; e < ne; e++) {
+        int taken = 0;
+        for (int q = 0; q < nsel; q++) taken |= sel[q] == e;
+        if (!taken && (best < 0 || key[e] > key[best])) best = e;
+    }
+    return best;
+}
+
+int orc_moe_route2(const float * lg, int ne, int k, unsigned moe_flags, float scale, int groups, int topk_group,
+                   const float * exp_bias, int * sel, float * w) {
+    if (k <= 0 || k > ne) k = ne;
+    if (ne > 64) return -1;
+    if (moe_flags & 4u) {
+        // sparsemixer: per pick, the best untaken logit; its weight is 1 over
+        // the double sum of exp(l - best) over untaken experts whose gap to
+        // the best, relative to max(|l|, best), is within 2 x jitter
+        const float eps2 = 2.0f * scale;
+        for (int j = 0; j < k; j++) {
+            const int b = orc_best_untaken(lg, ne, sel, j);
+            const float mx = lg[b];
+            double sum = 0.0;
+            for (int e = 0; e < ne; e++) {
+                int taken = 0;
+                for (int q = 0; q < j; q++) taken |= sel[q] == e;
+                const float f = fabsf(lg[e]) > mx ? fabsf(lg[e]) : mx;
+                if (!taken && (mx - lg[e]) / f <= eps2) sum += exp((double) lg[e] - mx);
+            }
+            sel[j] = b;
+            w[j] = (float) (1.0 / sum);
+        }
+        return k;
+    }
+    if ((moe_flags & 2u) || exp_bias || groups > 1) {
+        float sc[64], ch[64];
+        if (moe_flags & 2u) {
+            for (int e = 0; e < ne; e++) sc[e] = 1.0f / (1.0f + expf(-lg[e]));
+        } else {
+            float mx = lg[0];
+            for (int e = 1; e < ne; e++) if (lg[e] > mx) mx = lg[e];
+            double sum = 0.0;
+            for (int e = 0; e < ne; e++) sum += expf(lg[e] - mx);
+            for (int e = 0; e < ne; e++) sc[e] = (float) (expf(lg[e] - mx) / sum);
+        }
+        for (int e = 0; e < ne; e++) ch[e] = sc[e] + (exp_bias ? exp_bias[e] : 0.0f);
+        if (groups > 1 && topk_group < groups && ne % groups == 0) {
+            const int per = ne / groups;
+            float gs[64];
+            int kept[64];
+            for (int g = 0; g < groups; g++) {
+                float a1 = -1e30f, a2 = -1e30f;
+                for (int i = 0; i < per; i++) {
+                    const float v = ch[g * per + i];
+                    if (v > a1) { a2 = a1; a1 = v; } else if (v > a2) a2 = v;
+                }
+                gs[g] = (moe_flags & 8u) ? a1 : a1 + (per > 1 ? a2 : 0.0f);
+            }
+            for (int t = 0; t < topk_group; t++) kept[t] = orc_best_untaken(gs, groups, kept, t);
+            for (int e = 0; e < ne; e++) {
+                int keep = 0;
+                for (int t = 0; t < topk_group; t++) keep |= kept[t] == e / per;
+                if (!keep) ch[e] = 0.0f;
+            }
+        }
+        for (int j = 0; j < k; j++) {
+            sel[j] = orc_best_untaken(ch, ne, sel, j);
+            w[j] = sc[sel[j]];
+        }
+        if (moe_flags & 1u) {
+            float sum = 0.0f;
+            for (int j = 0; j < k; j++) sum += w[j];
+            for (int j = 0; j < k; j++) w[j] /= sum + 1e-20f;
+        }
+    } else {
+        orc_moe_route(lg, ne, k, moe_flags & 1u, sel, w);
+    }
+    if (scale != 0.0f) for (int j = 0; j < k; j++) w[j] *= scale;
+    return k;
+}
+
 void orc_router(const float * router, const float * x, int ne, int n_embd, float * lg) {
     for (int e = 0; e < ne; e++) {
         double s = 0.0;
@@ -850,6 +932,7 @@ static const uint64_t ORC_EXPF_TAB[32] = {
 
 float orc_expf_published(float x) {
     if (x < -0x1.9fe368p6f) return 0.0f;
+    if (x > 0x1.62e42ep6f) return INFINITY;
     const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                  C2 = 0x1.62e42ff0c52d6p-1 / 32, InvLn2N = 0x1.71547652b82fep+0 * 32, Shift = 0x1.8p+52;
     const double xd = (double) x;
@@ -867,11 +950,13 @@ float orc_expf_published(float x) {
     return (float) (y * s);
 }
 
+// every stride-th float <= 0 (-0 to -inf), then (positive) 0 to +inf
 long orc_expf_mismatches(unsigned stride) {
     long bad = 0;
     if (stride == 0) stride = 1;
     #pragma omp parallel for reduction(+ : bad) schedule(static)
-    for (long long u = 0x80000000ll; u <= 0xff800000ll; u += stride) {
+    for (long long v = 0; v <= 0xff800000ll - 0x80000000ll + 1 + 0x7f800000ll; v += stride) {
+        const long long u = v <= 0xff800000ll - 0x80000000ll ? v + 0x80000000ll : v - (0xff800000ll - 0x80000000ll) - 1;
         const uint32_t b = (uint32_t) u;
         float x;
         memcpy(&x, &b, 4);

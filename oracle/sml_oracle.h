@@ -82,6 +82,14 @@ void orc_silu_mul(float * g, const float * u, int n);
 // Top-k routing, ties to the lower index; moe_flags bit 0 renormalises over
 // the chosen. follows sml/sml-run.c:3010-3035
 int orc_moe_route(const float * lg, int ne, int k, unsigned moe_flags, int * sel, float * w);
+// Every routing mode of sml_moe_route (sml/sml-run.c:2925-3037): moe_flags
+// bit 0 normalizes the chosen weights (softmax over the chosen in plain
+// top-k), bit 1 scores by sigmoid, bit 2 is PhiMoE's sparsemixer (scale:
+// its jitter), bit 3 scores a group by its best expert (else its best two);
+// exp_bias (NULL: none) shifts the choice, groups/topk_group keep the best
+// groups' experts; scale multiplies the weights. expf is the C library's.
+int orc_moe_route2(const float * lg, int ne, int k, unsigned moe_flags, float scale, int groups, int topk_group,
+                   const float * exp_bias, int * sel, float * w);
 // Router logits with a double accumulator. follows sml/sml-run.c:3075-3080
 void orc_router(const float * router, const float * x, int ne, int n_embd, float * lg);
 // First-max greedy pick. follows sml/sml-run.c:3539-3544

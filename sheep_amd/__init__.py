@@ -27,7 +27,9 @@ class SynthSpec(ctypes.Structure):
                 ("n_ctx_train", ctypes.c_uint32), ("rope_theta", c_float), ("rms_eps", c_float),
                 ("nbits", c_int), ("tied", c_int), ("qkv_bias", c_int), ("random_perm", c_int),
                 ("n_expert", c_int), ("n_expert_used", c_int), ("moe_flags", ctypes.c_uint32),
-                ("step_sigma", c_float), ("router_sigma", c_float), ("seed", c_uint64), ("zero_mean", c_int)]
+                ("step_sigma", c_float), ("router_sigma", c_float), ("seed", c_uint64), ("zero_mean", c_int),
+                ("moe_scale", c_float), ("moe_groups", ctypes.c_uint32), ("moe_topk_group", ctypes.c_uint32),
+                ("exp_bias", c_int), ("n_ff_shexp", c_int), ("shexp_gate", c_int)]
 
 
 # (name, restype, argtypes) of every export
@@ -287,14 +289,19 @@ def sync():
 def synth_model(path, n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx_train=4096,
                 rope_theta=1e6, rms_eps=1e-6, nbits=4, tied=False, qkv_bias=False, random_perm=False,
                 n_expert=0, n_expert_used=0, moe_flags=0, step_sigma=0.02, router_sigma=1.0 / 64, seed=1,
-                zero_mean=True):
+                zero_mean=True, moe_scale=0.0, moe_groups=0, moe_topk_group=0, exp_bias=False, n_ff_shexp=0,
+                shexp_gate=False):
     """Write a seeded synthetic SSF decoder (sheep_amd/csrc/ssf.c). zero_mean
     puts every group's min at -(2^b - 1)/2 steps, so the uniform codes give
     weights of mean zero and the logits depend on the input; False keeps the
-    single-GEMV recipe (min at -2^(b-1) steps)."""
+    single-GEMV recipe (min at -2^(b-1) steps). MoE files may carry the
+    routing fields (moe_flags bits 0-3, moe_scale, moe_groups,
+    moe_topk_group), a correction bias per layer (exp_bias) and a shared
+    expert of width n_ff_shexp (with its sigmoid gate: shexp_gate)."""
     sp = SynthSpec(n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx_train, rope_theta, rms_eps,
                    nbits, int(tied), int(qkv_bias), int(random_perm), n_expert, n_expert_used, moe_flags,
-                   step_sigma, router_sigma, seed, int(zero_mean))
+                   step_sigma, router_sigma, seed, int(zero_mean), moe_scale, moe_groups, moe_topk_group,
+                   int(exp_bias), n_ff_shexp, int(shexp_gate))
     why = ctypes.create_string_buffer(512)
     if not lib().ssf_synth_model(str(path).encode(), ctypes.byref(sp), why, 512):
         raise RuntimeError(why.value.decode())

@@ -292,6 +292,18 @@ typedef struct {
     int32_t * count;              // [nexp] tokens per expert
     int32_t * list;               // [nexp][mmax] entries t*k + j, by token then choice
     int exact;                    // 1: each router dot as the reference's serial chain of double FMAs
+    // routing modes of sml_moe_route (sml/sml-run.c:2925-3037): flags bit 1
+    // sigmoid scores, bit 2 sparsemixer (scale: its jitter), bit 3 groups
+    // scored by their best expert; exp_bias [nexp] (NULL: none) shifts the
+    // choice; groups / topk_group keep the best groups' experts; scale (0:
+    // none) multiplies the weights
+    const float * exp_bias;
+    float scale;
+    int groups, topk_group;
+    // shared expert gate (NULL: none): sg[t] = sigmoid(shgate . x[t]), its
+    // dot summed as the router's
+    const float * shgate;
+    float * sg;                   // [T] (1 when there is a shared expert without a gate)
 } sml_kmoe_route;
 
 // Per-32 (or per-256) int8 quantization of activation rows into per-expert slots:
@@ -331,7 +343,8 @@ typedef struct {
     int mlo;                      // VALU kernel: groups of mlo rows or fewer are another launch's
 } sml_kgemm;
 
-// out[t] = sum over j of w[t][j] * y[sel[t][j]][slot[t][j]], in choice order.
+// out[t] = sum over j of w[t][j] * y[sel[t][j]][slot[t][j]], in choice order,
+// then + sg[t] * ysh[t] (the shared expert) when ysh is not NULL.
 typedef struct {
     const float   * y;            // [nexp][mmax][n]
     const int32_t * sel, * slot;
@@ -339,6 +352,8 @@ typedef struct {
     int T, n, k, mmax;
     const float * resid;          // [T][n] added first (may alias out), or NULL
     float * out;                  // [T][n]
+    const float * ysh;            // [T][n] or NULL
+    const float * sg;             // [T]
 } sml_kmoe_comb;
 
 // ---------------------------------------------------------------- ingest

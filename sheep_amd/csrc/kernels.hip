@@ -2902,18 +2902,35 @@ extern "C" __global__ void sml_gptq_unpack(const sml_kgptq_unpack a) {
 //
 // sml_moe_route, one workgroup per token: the router logits
 // (sml/sml-run.c:3075-3080: a double sum per expert, then (float) + bias),
-// one wave per expert at a time; then the top-k choice with ties to the
-// lower index and the Mixtral / Granite weights (moe_flags bit 0: softmax
-// over the chosen; else softmax over all, sml/sml-run.c:3017-3034).
+// one wave per expert at a time, and the shared expert's gate the same way;
+// then one thread routes as sml_moe_route does (sml/sml-run.c:2925-3037):
+// plain top-k with ties to the lower index and the Mixtral / Granite
+// weights (moe_flags bit 0: softmax over the chosen; else softmax over
+// all); sigmoid or softmax scores with the correction bias and the best
+// groups shaping the choice only; PhiMoE's sparsemixer; then moe_scale.
 // sml_moe_plan then lists each expert's tokens in token-then-choice order,
 // the order moe_ffn_batch gathers them in (sml/sml-run.c:3211-3219).
 #define MOE_ROUTE_THREADS 512
+// expf of the C library for any float (the restated one, with its overflow)
+__device__ __forceinline__ float expf_any(float x) { return x > 0x1.62e42ep6f ? __builtin_inff() : expf_ref(x); }
+// the best index by key not among sel[0..nsel), ties to the lower index
+__device__ __forceinline__ int best_untaken(const float * key, int n, const int * sel, int nsel) {
+    int best = -1;
+    for (int e = 0; e < n; e++) {
+        bool taken = false;
+        for (int q = 0; q < nsel; q++) taken = taken || sel[q] == e;
+        if (!taken && (best < 0 || key[e] > key[best])) best = e;
+    }
+    return best;
+}
 extern "C" __global__ __launch_bounds__(MOE_ROUTE_THREADS) void sml_moe_route(const sml_kmoe_route a) {
-    __shared__ float lg[64];
+    __shared__ float lg[65], sc[64], ch[64], gs[64];
+    __shared__ int kept[64];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, t = blockIdx.x;
     const float * x = a.x + (size_t) t * a.n;
-    for (int e = wv; e < a.nexp; e += MOE_ROUTE_THREADS / 64) {
-        const float * r = a.router + (size_t) e * a.n;
+    const int nrow = a.nexp + (a.shgate ? 1 : 0);          // row nexp: the shared expert's gate
+    for (int e = wv; e < nrow; e += MOE_ROUTE_THREADS / 64) {
+        const float * r = e < a.nexp ? a.router + (size_t) e * a.n : a.shgate;
         double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
         int i = lane * 4;
         for (; i + 3 < a.n; i += 256) {
@@ -2932,38 +2949,100 @@ extern "C" __global__ __launch_bounds__(MOE_ROUTE_THREADS) void sml_moe_route(co
             for (int i2 = 0; i2 < a.n; i2++) s = __builtin_fma((double) r[i2], (double) x[i2], s);
         }
         if (lane == 0) {
-            const float v = (float) s + (a.router_b ? a.router_b[e] : 0.0f);
-            lg[e] = v;
-            a.logits[(size_t) t * a.nexp + e] = v;
+            if (e < a.nexp) {
+                const float v = (float) s + (a.router_b ? a.router_b[e] : 0.0f);
+                lg[e] = v;
+                a.logits[(size_t) t * a.nexp + e] = v;
+            } else {
+                a.sg[t] = 1.0f / (1.0f + expf_any(-(float) s));   // sml/sml-run.c:3116-3120
+            }
         }
     }
+    if (a.sg && !a.shgate && tid == 0) a.sg[t] = 1.0f;
     __syncthreads();
     if (tid != 0) return;
-    int32_t * sel = a.sel + t * a.k;
-    float * w = a.w + t * a.k;
+    const int ne = a.nexp, k = a.k;
+    int32_t * sel = a.sel + t * k;
+    float * w = a.w + t * k;
     int sl[16];
-    for (int j = 0; j < a.k; j++) {
-        int best = -1;
-        for (int e = 0; e < a.nexp; e++) {
-            bool taken = false;
-            for (int q = 0; q < j; q++) taken = taken || sl[q] == e;
-            if (!taken && (best < 0 || lg[e] > lg[best])) best = e;
+    float wj[16];
+    if (a.moe_flags & 4u) {
+        // sparsemixer: each pick the best untaken logit, weighted by its share
+        // among the untaken experts within 2 x jitter of it
+        const float eps2 = 2.0f * a.scale;
+        for (int j = 0; j < k; j++) {
+            const int b = best_untaken(lg, ne, sl, j);
+            const float mx = lg[b];
+            double sum = 0.0;
+            for (int e = 0; e < ne; e++) {
+                bool taken = false;
+                for (int q = 0; q < j; q++) taken = taken || sl[q] == e;
+                const float f = fabsf(lg[e]) > mx ? fabsf(lg[e]) : mx;
+                if (!taken && (mx - lg[e]) / f <= eps2) sum += exp((double) lg[e] - mx);
+            }
+            sl[j] = b;
+            wj[j] = (float) (1.0 / sum);
         }
-        sl[j] = best;
-        sel[j] = best;
+        for (int j = 0; j < k; j++) { sel[j] = sl[j]; w[j] = wj[j]; }
+        return;
     }
-    if (a.moe_flags & 1u) {
-        float wj[16];
-        double sum = 0.0;
-        for (int j = 0; j < a.k; j++) { wj[j] = expf_ref(lg[sl[j]] - lg[sl[0]]); sum += wj[j]; }
-        for (int j = 0; j < a.k; j++) w[j] = (float) (wj[j] / sum);
+    if ((a.moe_flags & 2u) || a.exp_bias || a.groups > 1) {
+        // scores; the choice adds the correction bias and keeps only the best
+        // groups' experts (a group scored by its best one or two); the weights
+        // are the plain scores
+        if (a.moe_flags & 2u) {
+            for (int e = 0; e < ne; e++) sc[e] = 1.0f / (1.0f + expf_any(-lg[e]));
+        } else {
+            float mx = lg[0];
+            for (int e = 1; e < ne; e++) mx = lg[e] > mx ? lg[e] : mx;
+            double sum = 0.0;
+            for (int e = 0; e < ne; e++) sum += expf_ref(lg[e] - mx);
+            for (int e = 0; e < ne; e++) sc[e] = (float) (expf_ref(lg[e] - mx) / sum);
+        }
+        for (int e = 0; e < ne; e++) ch[e] = sc[e] + (a.exp_bias ? a.exp_bias[e] : 0.0f);
+        const int ng = a.groups, tg = a.topk_group;
+        if (ng > 1 && tg < ng && ne % ng == 0) {
+            const int per = ne / ng;
+            for (int g = 0; g < ng; g++) {
+                float b1 = -1e30f, b2 = -1e30f;
+                for (int i = 0; i < per; i++) {
+                    const float v = ch[g * per + i];
+                    if (v > b1) { b2 = b1; b1 = v; } else if (v > b2) b2 = v;
+                }
+                gs[g] = (a.moe_flags & 8u) ? b1 : b1 + (per > 1 ? b2 : 0.0f);
+            }
+            for (int q = 0; q < tg; q++) kept[q] = best_untaken(gs, ng, kept, q);
+            for (int e = 0; e < ne; e++) {
+                bool keep = false;
+                for (int q = 0; q < tg; q++) keep = keep || kept[q] == e / per;
+                if (!keep) ch[e] = 0.0f;
+            }
+        }
+        for (int j = 0; j < k; j++) {
+            sl[j] = best_untaken(ch, ne, sl, j);
+            wj[j] = sc[sl[j]];
+        }
+        if (a.moe_flags & 1u) {
+            float sum = 0.0f;
+            for (int j = 0; j < k; j++) sum += wj[j];
+            for (int j = 0; j < k; j++) wj[j] /= sum + 1e-20f;
+        }
     } else {
-        float mx = lg[0];
-        for (int e = 1; e < a.nexp; e++) mx = lg[e] > mx ? lg[e] : mx;
-        double sum = 0.0;
-        for (int e = 0; e < a.nexp; e++) sum += expf_ref(lg[e] - mx);
-        for (int j = 0; j < a.k; j++) w[j] = (float) (expf_ref(lg[sl[j]] - mx) / sum);
+        for (int j = 0; j < k; j++) sl[j] = best_untaken(lg, ne, sl, j);
+        if (a.moe_flags & 1u) {
+            double sum = 0.0;
+            for (int j = 0; j < k; j++) { wj[j] = expf_ref(lg[sl[j]] - lg[sl[0]]); sum += wj[j]; }
+            for (int j = 0; j < k; j++) wj[j] = (float) (wj[j] / sum);
+        } else {
+            float mx = lg[0];
+            for (int e = 1; e < ne; e++) mx = lg[e] > mx ? lg[e] : mx;
+            double sum = 0.0;
+            for (int e = 0; e < ne; e++) sum += expf_ref(lg[e] - mx);
+            for (int j = 0; j < k; j++) wj[j] = (float) (expf_ref(lg[sl[j]] - mx) / sum);
+        }
     }
+    if (a.scale != 0.0f) for (int j = 0; j < k; j++) wj[j] *= a.scale;
+    for (int j = 0; j < k; j++) { sel[j] = sl[j]; w[j] = wj[j]; }
 }
 
 // one thread per expert scans the choices (staged in LDS) in order
@@ -3033,6 +3112,7 @@ extern "C" __global__ __launch_bounds__(256) void sml_moe_combine(const sml_kmoe
         acc = __builtin_fmaf(a.w[t * a.k + j], a.y[((size_t) e * a.mmax + r) * a.n + i], acc);
     }
     const size_t o = (size_t) t * a.n + i;
+    if (a.ysh) acc = __builtin_fmaf(a.sg[t], a.ysh[o], acc);          // sml/sml-run.c:3121
     a.out[o] = a.resid ? a.resid[o] + acc : acc;    // the residual add after moe_ffn, sml/sml-run.c:3475-3480
 }
 

@@ -1522,6 +1522,7 @@ static void moe_release(sml_hip_moe * m) {
     if (!m) return;
     if (m->mats) for (int i = 0; i < 3 * m->nexp; i++) if (m->mats[i]) { hipFree(m->mats[i]->mem); free(m->mats[i]); }
     free(m->mats);
+    for (int i = 0; i < 3; i++) if (m->shx[i]) { hipFree(m->shx[i]->mem); free(m->shx[i]); }
     for (int i = 0; i < m->nowned; i++) hipFree(m->owned[i]);
     free(m);
 }
@@ -1539,16 +1540,57 @@ static int32_t * moe_perm(sml_hip_moe * m, const ssf_file * f, const ssf_record 
     return d;
 }
 
+// The shared expert (sml/sml-run.c:1736-1745,3104-3122): gate, up and down
+// run on every token, their output added after the routed experts' times
+// sigmoid(ffn_gate_inp_shexp . x) when that gate exists (else times 1).
+static void moe_shared_setup(sml_hip_moe * m, const ssf_file * f, int L, int tmax) {
+    const ssf_record * g = ssf_findf(f, "blk.%d.ffn_gate_shexp.weight", L);
+    const ssf_record * u = ssf_findf(f, "blk.%d.ffn_up_shexp.weight", L);
+    const ssf_record * d = ssf_findf(f, "blk.%d.ffn_down_shexp.weight", L);
+    if (!u || !d) return;
+    if (!g) hx_failf("layer %d: an ungated shared expert (up, activation, down) is not built", L);
+    if ((int) g->cols != m->n_embd || u->cols != g->cols || u->rows != g->rows || (int) d->rows != m->n_embd ||
+        d->cols != g->rows || u->nbits != g->nbits)
+        hx_failf("layer %d: shared expert of unexpected shapes", L);
+    m->sh_ff = (int) g->rows;
+    m->shx[0] = mat_from_record(f, g);
+    m->shx[1] = mat_from_record(f, u);
+    m->shx[2] = mat_from_record(f, d);
+    const int32_t * pg = moe_perm(m, f, g), * pu = moe_perm(m, f, u);
+    if (!((!pg && !pu) || (pg && pu && g->perm_off == u->perm_off)))
+        hx_failf("layer %d: shared gate and up read different permutations", L);
+    m->sh_perm_gu = pg;
+    m->sh_perm_d = moe_perm(m, f, d);
+    const sml_kmat t[2] = { m->shx[0]->k, m->shx[1]->k };
+    m->sh_gu = moe_own(m, sizeof t);
+    HX(hipMemcpy(m->sh_gu, t, sizeof t, hipMemcpyHostToDevice));
+    const ssf_record * sg = ssf_findf(f, "blk.%d.ffn_gate_inp_shexp.weight", L);
+    if (sg) {
+        if (sg->kind != SSF_KIND_F32 || (uint64_t) sg->rows * sg->cols != (uint64_t) m->n_embd)
+            hx_failf("layer %d: shared expert gate is not f32 of %d", L, m->n_embd);
+        m->shgate = moe_own(m, (size_t) m->n_embd * 4);
+        HX(hipMemcpy(m->shgate, ssf_at(f, sg->f32_off), (size_t) m->n_embd * 4, hipMemcpyHostToDevice));
+    }
+    const size_t T = (size_t) tmax, ne = (size_t) m->n_embd, nf = (size_t) m->sh_ff, w = ne > nf ? ne : nf;
+    m->sg = moe_own(m, T * 4);
+    m->sh_h = moe_own(m, T * nf * 4);
+    m->sh_y = moe_own(m, T * ne * 4);
+    m->sh_q = moe_own(m, T * w + T * (w / 32) * 8);
+    m->sh_s = (float *) (m->sh_q + T * w);
+    m->sh_u = (int32_t *) (m->sh_s + T * (w / 32));
+    m->expert_bytes += m->shx[0]->bytes + m->shx[1]->bytes + m->shx[2]->bytes;
+}
+
 static void moe_setup(sml_hip_moe * m, const ssf_file * f, int L, int tmax, const sml_hip_moe * share) {
     const ssf_header * h = f->hdr;
-    if (h->moe_flags & ~1u) hx_failf("routing mode 0x%x not built (top-k with softmax over all or over the chosen only)", h->moe_flags);
-    if (h->moe_scale != 0.0f || h->moe_groups > 1) hx_failf("scaled or grouped routing not built");
+    // routing (sml/sml-run.c:2925-3037): flags bits 0-3, moe_scale, groups
+    if (h->moe_flags & ~15u) hx_failf("routing mode 0x%x not built (flags bits 0-3)", h->moe_flags);
+    if (h->moe_groups > 64) hx_failf("%u expert groups (at most 64)", h->moe_groups);
     char nm[96];
-    snprintf(nm, sizeof nm, "blk.%d.ffn_gate_shexp.weight", L);
-    if (ssf_find(f, nm)) hx_failf("shared experts not built");
-    snprintf(nm, sizeof nm, "blk.%d.exp_probs_b.weight", L);
-    if (ssf_find(f, nm)) hx_failf("expert score bias not built");
     m->n_embd = (int) h->n_embd;
+    m->scale = h->moe_scale;
+    m->groups = (int) h->moe_groups;
+    m->topk_group = (int) h->moe_topk_group;
     // the router's rows are the experts (sml/sml-run.c:1676-1680)
     const ssf_record * rt = ssf_findf(f, "blk.%d.ffn_gate_inp.weight", L);
     if (!rt) hx_failf("layer %d has no experts (no router)", L);
@@ -1560,6 +1602,13 @@ static void moe_setup(sml_hip_moe * m, const ssf_file * f, int L, int tmax, cons
     if (m->k > 16 || m->nexp > 64 || m->nexp < 1) hx_failf("%d of %d experts: at most 16 of 64", m->k, m->nexp);
     m->flags = h->moe_flags;
     m->tmax = tmax;
+    // the choice's correction bias (the reference takes it when it holds at
+    // least one value per expert, sml/sml-run.c:1743-1745)
+    const ssf_record * eb = ssf_findf(f, "blk.%d.exp_probs_b.weight", L);
+    if (eb && eb->kind == SSF_KIND_F32 && (uint64_t) eb->rows * eb->cols >= (uint64_t) m->nexp) {
+        m->exp_bias = moe_own(m, (size_t) m->nexp * 4);
+        HX(hipMemcpy(m->exp_bias, ssf_at(f, eb->f32_off), (size_t) m->nexp * 4, hipMemcpyHostToDevice));
+    }
     m->router = moe_own(m, (size_t) m->nexp * m->n_embd * 4);
     HX(hipMemcpy(m->router, ssf_at(f, rt->f32_off), (size_t) m->nexp * m->n_embd * 4, hipMemcpyHostToDevice));
     const ssf_record * rb = ssf_findf(f, "blk.%d.ffn_gate_inp.bias", L);
@@ -1624,6 +1673,7 @@ static void moe_setup(sml_hip_moe * m, const ssf_file * f, int L, int tmax, cons
     hx.jb = outer;
     free(tgu);
     free(pgu);
+    moe_shared_setup(m, f, L, tmax);
     // scratch: this layer's own, or another layer's of the same shape (layers run one after another)
     if (share) {
         if (share->nexp != m->nexp || share->k != m->k || share->n_ff != m->n_ff || share->n_embd != m->n_embd ||
@@ -1715,6 +1765,8 @@ void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out
     r.T = T; r.n = m->n_embd; r.nexp = m->nexp; r.k = m->k; r.mmax = m->tmax; r.moe_flags = m->flags;
     r.logits = m->logits; r.sel = m->sel; r.w = m->w; r.slot = m->slot; r.count = m->count; r.list = m->list;
     r.exact = g_exact;
+    r.exp_bias = m->exp_bias; r.scale = m->scale; r.groups = m->groups; r.topk_group = m->topk_group;
+    r.shgate = m->shx[0] ? m->shgate : NULL; r.sg = m->shx[0] ? m->sg : NULL;
     hx_launch("sml_moe_route", (unsigned) T, 1, 512, 0, st, &r);
     hx_launch("sml_moe_plan", 1, 1, 64, 0, st, &r);
     sml_kmquant qa;
@@ -1730,10 +1782,26 @@ void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out
     hx_launch("sml_moe_quant", (unsigned) T, (unsigned) m->nexp, 1024, 0, st, &qb);
     op_gemm(st, m->tab_d, m->nexp, 0, m->nbits, m->n_embd, m->n_ff, m->count, 0, mt, m->tmax,
             m->qh, m->sh, m->uh, m->yd, NULL, NULL, m->per256);
+    if (m->shx[0]) {
+        // the shared expert on every token: its inputs in its permutation,
+        // gate/up with SwiGLU, then down, as one dense FFN over the T rows
+        const int32_t * pp[1] = { m->sh_perm_gu };
+        int8_t * qq[1] = { m->sh_q };
+        float * ss[1] = { m->sh_s };
+        int32_t * uu[1] = { m->sh_u };
+        op_normq_rows(st, (float *) x, NULL, NULL, 0.0f, m->n_embd, T, 1, pp, qq, ss, uu, NULL, m->per256);
+        op_gemm(st, m->sh_gu, 1, 1, m->shx[0]->nbits, m->sh_ff, m->n_embd, NULL, T, mt, T, m->sh_q, m->sh_s, m->sh_u,
+                m->sh_h, NULL, NULL, m->per256);
+        pp[0] = m->sh_perm_d;
+        op_normq_rows(st, m->sh_h, NULL, NULL, 0.0f, m->sh_ff, T, 1, pp, qq, ss, uu, NULL, m->per256);
+        op_gemm(st, m->shx[2]->kdev, 1, 0, m->shx[2]->nbits, m->n_embd, m->sh_ff, NULL, T, mt, T, m->sh_q, m->sh_s,
+                m->sh_u, m->sh_y, NULL, NULL, m->per256);
+    }
     sml_kmoe_comb c;
     memset(&c, 0, sizeof c);
     c.y = m->yd; c.sel = m->sel; c.slot = m->slot; c.w = m->w; c.T = T; c.n = m->n_embd; c.k = m->k;
     c.mmax = m->tmax; c.out = out; c.resid = resid;
+    c.ysh = m->shx[0] ? m->sh_y : NULL; c.sg = m->sg;
     hx_launch("sml_moe_combine", (unsigned) ((m->n_embd + 255) / 256), (unsigned) T, 256, 0, st, &c);
 }
 

@@ -135,10 +135,25 @@ struct sml_hip_moe {
     int8_t * qx, * qh;
     float * sx, * sh;
     int32_t * ux, * uh;
-    void * owned[160];            // every device allocation: up to 2 permutations per expert + buffers
+    void * owned[192];            // every device allocation: up to 2 permutations per expert + buffers
     int nowned;
     size_t expert_bytes;
     int per256;                   // activations quantized per 256 values (the batched regime)
+    // routing modes (sml_kmoe_route): correction bias, weight scale, groups
+    float * exp_bias;
+    float scale;
+    int groups, topk_group;
+    // the shared expert (shx[0] NULL: none): gate, up, down; its gate vector
+    // (NULL: weight 1), permutations and scratch
+    sml_hip_mat * shx[3];
+    sml_kmat * sh_gu;             // device table: gate, up
+    const int32_t * sh_perm_gu, * sh_perm_d;
+    float * shgate;
+    int sh_ff;
+    float * sg, * sh_h, * sh_y;   // [tmax], [tmax][sh_ff], [tmax][n_embd]
+    int8_t * sh_q;                // [tmax][max(n_embd, sh_ff)]
+    float * sh_s;
+    int32_t * sh_u;
 };
 // Experts of layer `layer` for up to tmax tokens per call; scratch shared with
 // `share` (a loaded layer of the same shape) when not NULL.

@@ -501,6 +501,15 @@ int ssf_synth_model(const char * path, const ssf_synth_spec * sp, char * why, in
     h.rope_theta = sp->rope_theta; h.rms_eps = sp->rms_eps;
     h.n_expert_used = sp->n_expert ? (uint32_t) sp->n_expert_used : 0;
     h.moe_flags = sp->n_expert ? sp->moe_flags : 0;
+    if (sp->n_expert) {
+        h.moe_scale = sp->moe_scale;
+        h.moe_groups = sp->moe_groups;
+        h.moe_topk_group = sp->moe_topk_group;
+    }
+    if (sp->n_ff_shexp < 0 || sp->n_ff_shexp % 128) {
+        say(why, nwhy, "shared expert width %d (a multiple of 128)", sp->n_ff_shexp);
+        return 0;
+    }
     const int hd = (int) (sp->n_embd / sp->n_head);
     const int nq = (int) sp->n_head * hd, nkv = (int) sp->n_head_kv * hd;
     const int E = (int) sp->n_embd, F = (int) sp->n_ff, b = sp->nbits;
@@ -529,6 +538,14 @@ int ssf_synth_model(const char * path, const ssf_synth_spec * sp, char * why, in
                 add_quant(&l, sdup("blk.%d.ffn_gate.%d.weight", L, e), F, E, b, kgu, sp->zero_mean);
                 add_quant(&l, sdup("blk.%d.ffn_up.%d.weight", L, e), F, E, b, kgu, sp->zero_mean);
                 add_quant(&l, sdup("blk.%d.ffn_down.%d.weight", L, e), E, F, b, pk++, sp->zero_mean);
+            }
+            if (sp->exp_bias) add_f32(&l, sdup("blk.%d.exp_probs_b.weight", L), sp->n_expert, 1, 0.05f);
+            if (sp->n_ff_shexp) {
+                const int FS = sp->n_ff_shexp, kgu = pk++;
+                add_quant(&l, sdup("blk.%d.ffn_gate_shexp.weight", L), FS, E, b, kgu, sp->zero_mean);
+                add_quant(&l, sdup("blk.%d.ffn_up_shexp.weight", L), FS, E, b, kgu, sp->zero_mean);
+                add_quant(&l, sdup("blk.%d.ffn_down_shexp.weight", L), E, FS, b, pk++, sp->zero_mean);
+                if (sp->shexp_gate) add_f32(&l, sdup("blk.%d.ffn_gate_inp_shexp.weight", L), E, 1, sp->router_sigma);
             }
         } else {
             const int kgu = pk++;

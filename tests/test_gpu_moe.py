@@ -414,3 +414,80 @@ np.savez(sys.argv[3], **out)
         res[t] = np.load(f)
     for k in res["0"].files:
         assert np.array_equal(res["0"][k], res["1"][k]), k
+
+
+# (moe_flags, moe_scale, groups, topk_group, exp_bias, shared expert width, its gate)
+MOE_MODES = {
+    "v3_sigmoid_bias_groups_shared": (3, 2.5, 4, 2, True, 1024, True),
+    "sigmoid_bias": (2, 0.0, 1, 1, True, 0, False),
+    "softmax_groups_best_one": (9, 1.0, 4, 1, False, 0, False),
+    "greedy_scaled_shared_ungated": (0, 1.5, 1, 1, False, 768, False),
+    "sparsemixer": (4, 0.01, 1, 1, False, 0, False),
+    "mixtral_shared_gated": (1, 0.0, 1, 1, False, 1024, True),
+}
+
+
+@pytest.mark.parametrize("name", list(MOE_MODES))
+def test_moe_routing_modes(tmpdir_s, name):
+    """Every routing mode of sml_moe_route (sigmoid or softmax scores, the
+    correction bias, grouped choice by a group's best one or two, the weight
+    scale, PhiMoE's sparsemixer) and a shared expert with or without its
+    sigmoid gate, on one MoE layer of 16 experts (top 4) for 16 tokens: the
+    choices and weights equal the oracle's restatement (itself equal to the
+    reference's sml_moe_route bit for bit) fed the GPU's own logits, and each
+    token's output is within 1e-3 of the oracle's composition, the shared
+    expert's gated output added after the routed ones."""
+    flags, scale, groups, tg, bias, shff, shgate = MOE_MODES[name]
+    n_embd, n_ff, nexp, k, T = 1024, 512, 16, 4, 16
+    p = tmpdir_s / f"moe_mode_{name}.ssf"
+    if not p.exists():
+        sa.synth_model(p, n_layer=1, n_embd=n_embd, n_head=8, n_head_kv=2, n_ff=n_ff, n_vocab=512, n_expert=nexp,
+                       n_expert_used=k, moe_flags=flags, moe_scale=scale, moe_groups=groups, moe_topk_group=tg,
+                       exp_bias=bias, n_ff_shexp=shff, shexp_gate=shgate, random_perm=True,
+                       router_sigma=0.5, seed=2000 + flags)
+    f = SSF(p)
+    moe = sa.MoE(p, 0, 16)
+    rng = np.random.default_rng(flags + 40)
+    x = rng.standard_normal((T, n_embd)).astype(np.float32)
+    out, sel, w, lg = sa.DevBuf(T * n_embd * 4), sa.DevBuf(T * k * 4), sa.DevBuf(T * k * 4), sa.DevBuf(T * nexp * 4)
+    xd = sa.DevBuf.of(x)
+    print(f"moe mode {name}", flush=True)
+    moe.ffn(xd, T, out, sel, w, lg)
+    got_out = out.read(np.float32).reshape(T, n_embd)
+    got_sel = sel.read(np.int32).reshape(T, k)
+    got_w = w.read(np.float32).reshape(T, k)
+    got_lg = lg.read(np.float32).reshape(T, nexp)
+    eb = np.ascontiguousarray(f["blk.0.exp_probs_b.weight"].f32) if bias else None
+    router = np.ascontiguousarray(f["blk.0.ffn_gate_inp.weight"].f32)
+    distinct = set()
+    for t in range(T):
+        rl = np.zeros(nexp, np.float32)
+        ob.oracle().orc_router(router.ctypes.data, x[t].ctypes.data, nexp, n_embd, rl.ctypes.data)
+        np.testing.assert_allclose(got_lg[t], rl, rtol=1e-6, atol=1e-6)
+        rs, rw = np.zeros(k, np.int32), np.zeros(k, np.float32)
+        lt = np.ascontiguousarray(got_lg[t])
+        ob.oracle().orc_moe_route2(lt.ctypes.data, nexp, k, flags, scale, groups, tg,
+                                   eb.ctypes.data if bias else None, rs.ctypes.data, rw.ctypes.data)
+        np.testing.assert_array_equal(got_sel[t], rs, err_msg=f"{name} token {t} choices")
+        np.testing.assert_array_equal(got_w[t].view(np.uint32), rw.view(np.uint32), err_msg=f"{name} token {t} weights")
+        distinct.update(rs.tolist())
+        acc = np.zeros(n_embd, np.float32)
+        for j in range(k):
+            g, u, d = (f[f"blk.0.ffn_{kind}.{int(rs[j])}.weight"] for kind in ("gate", "up", "down"))
+            qa = ob.quantize_act(np.ascontiguousarray(x[t][g.perm]))
+            yg, yu = ob.matvec(g, *qa), ob.matvec(u, *qa)
+            ob.oracle().orc_silu_mul(yg.ctypes.data, yu.ctypes.data, len(yg))
+            acc += rw[j] * ob.matvec(d, *ob.quantize_act(np.ascontiguousarray(yg[d.perm])))
+        if shff:
+            g, u, d = (f[f"blk.0.ffn_{kind}_shexp.weight"] for kind in ("gate", "up", "down"))
+            qa = ob.quantize_act(np.ascontiguousarray(x[t][g.perm]))
+            yg, yu = ob.matvec(g, *qa), ob.matvec(u, *qa)
+            ob.oracle().orc_silu_mul(yg.ctypes.data, yu.ctypes.data, len(yg))
+            ysh = ob.matvec(d, *ob.quantize_act(np.ascontiguousarray(yg[d.perm])))
+            sg = 1.0
+            if shgate:
+                gv = f["blk.0.ffn_gate_inp_shexp.weight"].f32.astype(np.float64)
+                sg = np.float32(1.0) / (np.float32(1.0) + np.float32(np.exp(-np.float64(np.float32(gv @ x[t].astype(np.float64))))))
+            acc += np.float32(sg) * ysh
+        close(got_out[t], acc, f"{name} token {t}")
+    assert len(distinct) >= 6, (name, distinct)          # the tokens reach many experts

@@ -309,12 +309,15 @@ def test_zero_mean_decoder_is_informative(tmpdir_s):
 def test_expf_restatement_equals_the_library():
     """The restated expf (the GPU's exact softmax and routing weights use the
     same algorithm and table) equals the C library's expf bit for bit on
-    every 7th float from -0.0 down to -inf (306 M inputs: normals, denormals,
-    the underflow edge at -103.97, -inf), and on the closed forms."""
+    every 7th float from -0.0 down to -inf and from +0.0 up to +inf (613 M
+    inputs: normals, denormals, the underflow edge at -103.97, the overflow
+    edge at 88.72, the infinities), and on the closed forms."""
     o = ob.oracle()
     assert o.orc_expf_mismatches(7) == 0
     assert o.orc_expf_published(0.0) == 1.0
     assert o.orc_expf_published(-200.0) == 0.0
+    assert o.orc_expf_published(89.0) == np.inf
+    assert o.orc_expf_published(88.7) == np.float32(np.exp(np.float64(np.float32(88.7))))
     for x in (-1.0, -0.5, -10.0, -50.3):        # correctly rounded from double here
         assert o.orc_expf_published(x) == float(np.float32(np.exp(np.float64(np.float32(x))))), x
 
@@ -531,3 +534,38 @@ def test_awq_known_answer(with_zeros):
     if with_zeros:
         np.testing.assert_array_equal(pz, qz)
     np.testing.assert_array_equal(ps, sc)
+
+
+ROUTE_MODES = [   # (moe_flags, scale, groups, topk_group, bias)
+    (0, 0.0, 1, 1, False), (1, 0.0, 1, 1, False), (0, 1.5, 1, 1, False),        # plain top-k; DeepSeek V2 greedy
+    (2, 0.0, 1, 1, True), (3, 2.5, 8, 4, True), (3, 2.5, 8, 3, False),         # sigmoid + bias (V3 noaux_tc)
+    (1, 0.0, 4, 2, False), (9, 1.0, 4, 1, False), (0, 0.0, 1, 1, True),        # softmax scores, groups, bias
+    (4, 0.01, 1, 1, False), (4, 0.1, 1, 1, False),                             # PhiMoE sparsemixer
+]
+
+
+@needs_ref
+@pytest.mark.parametrize("mode", ROUTE_MODES)
+def test_moe_route_every_mode_equals_the_reference(mode):
+    """orc_moe_route2 against the reference's own sml_moe_route (through the
+    shim, on a header and layer holding the routing fields) on 400 logit
+    vectors per mode, 64 and 16 experts: the same choices and the same
+    weights bit for bit, including ties (logits rounded to a coarse grid)."""
+    flags, scale, groups, tg, bias = mode
+    rng = np.random.default_rng(flags * 100 + groups)
+    for ne, k in ((64, 8), (16, 4)):
+        g = groups if ne % groups == 0 else 1
+        for i in range(400):
+            lg = (rng.standard_normal(ne) * 2).astype(np.float32)
+            if i % 4 == 1:
+                lg = (np.round(lg * 4) / 4).astype(np.float32)      # ties
+            eb = (rng.standard_normal(ne) * 0.1).astype(np.float32) if bias else None
+            out = []
+            for fn in (ob.oracle().orc_moe_route2, ob.ref().ref_moe_route2):
+                sel, w = np.zeros(k, np.int32), np.zeros(k, np.float32)
+                assert fn(lg.ctypes.data, ne, k, flags, scale, g, tg, eb.ctypes.data if bias else None,
+                          sel.ctypes.data, w.ctypes.data) == k
+                out.append((sel, w))
+            np.testing.assert_array_equal(out[0][0], out[1][0], err_msg=f"{mode} {ne} #{i} choices")
+            np.testing.assert_array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32),
+                                          err_msg=f"{mode} {ne} #{i} weights")
