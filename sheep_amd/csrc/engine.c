@@ -424,7 +424,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     G.n_ctx = n_ctx;
     const ssf_record * q0 = need(&f, "blk.%d.attn_q.weight", 0);
     G.hd = (int) q0->rows / G.H;
-    if ((int) q0->rows % G.H || G.hd != 128 || G.KV <= 0 || G.H % G.KV || G.H / G.KV > 8)
+    if ((int) q0->rows % G.H || (G.hd != 128 && G.hd != 64) || G.KV <= 0 || G.H % G.KV || G.H / G.KV > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", G.H, G.KV, G.hd);
     hx_init(env_int("SML_DEVICE", 0));
     HX(hipStreamCreateWithFlags(&G.st, hipStreamNonBlocking));
@@ -558,6 +558,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     if (G.exact) {
         // the norm prologues and the h quantization have exact forms (Q4/Q8)
         if (n_ctx > 16384) hx_failf("exact mode holds at most 16384 positions");
+        if (G.hd != 128) hx_failf("exact mode takes head_dim 128 (this model: %d)", G.hd);
     }
     const size_t kvn = (size_t) G.n_layer * n_ctx * G.KV * G.hd;
     G.kc = dalloc(kvn * 2);
@@ -866,7 +867,8 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
         // the merge quantizes its output for the o product: per 32, or per
         // 256 in decode steps of an even head count (SML_MERGE_Q256=0 leaves
         // that to its own launch)
-        const int fuse_q = y->perm_o < 0 && (!sb || (!causal && G.H % 2 == 0 && env_int("SML_MERGE_Q256", 1)));
+        const int fuse_q = y->perm_o < 0 &&
+                           (!sb || (!causal && G.H % 2 == 0 && G.hd == 128 && env_int("SML_MERGE_Q256", 1)));
         op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
                            G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.pos_cap, G.mpart, G.matt,
                            fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL,

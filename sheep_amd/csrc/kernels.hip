@@ -1179,6 +1179,26 @@ __device__ __forceinline__ void rope8(float (&x)[8], const float (&c)[8], const 
     for (int e = 0; e < 8; e++)
         x[e] = lo ? __builtin_fmaf(x[e], c[e], -(p[e] * s[e])) : __builtin_fmaf(p[e], s[e], x[e] * c[e]);
 }
+// rope8 for a head of LP*8 dims: the (d, d + D/2) partner of a lane is lane
+// ^ LP/2 of its position's lanes (LP 16: row_ror:8; LP 8: the half-row
+// mirror, then the quad reversal, which together map lane i to i ^ 4)
+template <int LP>
+__device__ __forceinline__ void rope8p(float (&x)[8], const float (&c)[8], const float (&s)[8], bool lo) {
+    if constexpr (LP == 16) {
+        rope8(x, c, s, lo);
+    } else {
+        float p[8];
+        #pragma unroll
+        for (int e = 0; e < 8; e++) p[e] = dpp_f<0x1B>(dpp_f<0x141>(x[e]));
+        #pragma unroll
+        for (int e = 0; e < 8; e++)
+            x[e] = lo ? __builtin_fmaf(x[e], c[e], -(p[e] * s[e])) : __builtin_fmaf(p[e], s[e], x[e] * c[e]);
+    }
+}
+// the sum over each group of 8 lanes, in every lane of the group
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp_f<0xB1>(v); v += dpp_f<0x4E>(v); return v + dpp_f<0x141>(v);
+}
 // Reduce-scatter of four values over the 4 rows of a wave with the gfx950
 // row swaps (v_permlane16_swap: rows 1 and 3 of the first operand trade
 // places with rows 0 and 2 of the second; v_permlane32_swap: rows 2-3 of the
@@ -1251,13 +1271,13 @@ __device__ __forceinline__ void st_dev2(float2 * p, float2 v) {
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 // The merged output of dim d of head h of entry b, also stored to a.out.
-template <bool DEV>
+template <bool DEV, int D = HD>
 __device__ __forceinline__ float merge_value(const sml_kattn & a, int b, int h, int d) {
     const int lane = d & 63;
-    const float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
-    const float * po = blk + (size_t) h * a.nsplit * HD;
-    const float2 * pml = (const float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) h * a.nsplit;
-    const size_t ob = (size_t) b * a.n_head * HD;
+    const float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (D + 2);
+    const float * po = blk + (size_t) h * a.nsplit * D;
+    const float2 * pml = (const float2 *) (blk + (size_t) a.n_head * a.nsplit * D) + (size_t) h * a.nsplit;
+    const size_t ob = (size_t) b * a.n_head * D;
     float M = -INFINITY, L = 0.0f, o = 0.0f;
     // a batch of MERGE_BATCH splits; indices past the last split read split
     // 0 (their weights are zero below)
@@ -1265,7 +1285,7 @@ __device__ __forceinline__ float merge_value(const sml_kattn & a, int b, int h, 
         #pragma unroll
         for (int s = 0; s < MERGE_BATCH; s++) {
             const int i = s0 + s < a.nsplit ? s0 + s : 0;
-            ov[s] = ld_part<DEV>(po + (size_t) i * HD + d);
+            ov[s] = ld_part<DEV>(po + (size_t) i * D + d);
         }
         const int j = s0 + lane < a.nsplit ? s0 + lane : 0;
         ml = ld_part2<DEV>(pml + j);
@@ -1304,31 +1324,34 @@ __device__ __forceinline__ float merge_value(const sml_kattn & a, int b, int h, 
     }
     fold(s0, ov, ml);
     const float r = o / L;
-    a.out[ob + (size_t) h * HD + d] = r;
+    a.out[ob + (size_t) h * D + d] = r;
     return r;
 }
-template <bool DEV>
+template <bool DEV, int D = HD>
 __device__ __forceinline__ void merge_head(const sml_kattn & a, int b, int h, int d) {
-    const float r = merge_value<DEV>(a, b, h, d);
+    const float r = merge_value<DEV, D>(a, b, h, d);
     if (!a.q_out) return;
-    const size_t ob = (size_t) b * a.n_head * HD;
+    const size_t ob = (size_t) b * a.n_head * D;
     const float amax = max32(fabsf(r));
     const float s = amax / 127.0f;
     const float is = s > 0.0f ? 1.0f / s : 0.0f;
     const int t = quant1(r, is);
     const int sum = isum32(t);
-    const int g = h * 4 + (d >> 5);
-    a.q_out[ob + (size_t) h * HD + d] = (int8_t) t;
+    const int g = h * (D / 32) + (d >> 5);
+    a.q_out[ob + (size_t) h * D + d] = (int8_t) t;
     if ((d & 31) == 0) { a.s_out[ob / 32 + g] = s; a.u_out[ob / 32 + g] = sum; }
 }
 
 // CH: positions per split (128; the one-sequence decode launch also takes 32
-// or 64, so that models with few KV heads still fill the chip)
-template <int REP, int NW, bool CHUNK, int CH = ATTN_CHUNK>
+// or 64, so that models with few KV heads still fill the chip). D: head_dim
+// (128, or 64: a position's 64 dims on 8 lanes, two positions to a 16-lane
+// row, whose halves are combined before the cross-row reductions).
+template <int REP, int NW, bool CHUNK, int CH = ATTN_CHUNK, int D = HD>
 __device__ __forceinline__ void attn_body(const sml_kattn & a) {
-    constexpr int NT = 64 * NW, PS = NT / 16, PPL = CH / PS;   // threads, position stride, positions per lane
+    constexpr int LP = D / 8;                                   // lanes per position
+    constexpr int NT = 64 * NW, PS = NT / LP, PPL = CH / PS;   // threads, position stride, positions per lane
     static_assert(PPL >= 1 && PPL * PS == CH, "a split covers whole rounds of positions");
-    __shared__ float red[NW][REP][HD];
+    __shared__ float red[NW][REP][D];
     __shared__ float wm[NW][REP], wl[NW][REP];
     // kv head kh; query heads qh0 .. qh0+REP-1 (a subset of the kv head's
     // when nsub > 1: each head's arithmetic is the same whichever workgroup
@@ -1336,7 +1359,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     const int nsub = CHUNK || a.nsub < 1 ? 1 : a.nsub;
     const int kh = (int) blockIdx.y / nsub, qh0 = kh * REP * nsub + ((int) blockIdx.y % nsub) * REP;
     const int split = blockIdx.x, tid = threadIdx.x;
-    const int wave = tid >> 6, grp = tid >> 4, l16 = tid & 15, kvd = a.n_kv * HD;
+    const int wave = tid >> 6, grp = tid / LP, l16 = tid % LP, kvd = a.n_kv * D;
     // the workgroup's entries b0..b1-1: one, or (tpw > 1) consecutive
     // positions of one sequence, which share this split's K/V tile
     const int tpw = CHUNK ? a.tpw : 1;
@@ -1345,21 +1368,21 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     GLOBAL uint16_t * kcache = (GLOBAL uint16_t *) (a.kc_slots ? a.kc_slots[a.slot[b0]] + a.layer_off : a.kcache);
     GLOBAL uint16_t * vcache = (GLOBAL uint16_t *) (a.vc_slots ? a.vc_slots[a.slot[b0]] + a.layer_off : a.vcache);
     // the first entry's q, k and v load first: loads return in order
-    const int half = HD / 2;
+    const int half = D / 2;
     float nq[REP][8], nk[8], nv[8], ncs[8], nsn[8];
     auto fetch_qkv = [&](int b) {
-        const float * aq = a.q + (size_t) b * a.qkv_stride + (size_t) qh0 * HD + l16 * 8;
-        const float * ak = a.k + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
-        const float * av = a.v + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
+        const float * aq = a.q + (size_t) b * a.qkv_stride + (size_t) qh0 * D + l16 * 8;
+        const float * ak = a.k + (size_t) b * a.qkv_stride + (size_t) kh * D + l16 * 8;
+        const float * av = a.v + (size_t) b * a.qkv_stride + (size_t) kh * D + l16 * 8;
         #pragma unroll
-        for (int j = 0; j < REP; j++) load_f8(aq + j * HD, nq[j]);
+        for (int j = 0; j < REP; j++) load_f8(aq + j * D, nq[j]);
         load_f8(ak, nk);
         load_f8(av, nv);
     };
     auto fetch_rope = [&](int b) {
         const int p = a.pos[b];
-        load_f8(a.cos_t + (size_t) p * half + (l16 & 7) * 8, ncs);
-        load_f8(a.sin_t + (size_t) p * half + (l16 & 7) * 8, nsn);
+        load_f8(a.cos_t + (size_t) p * half + (l16 & (LP / 2 - 1)) * 8, ncs);
+        load_f8(a.sin_t + (size_t) p * half + (l16 & (LP / 2 - 1)) * 8, nsn);
     };
     auto fetch = [&](int b) { fetch_qkv(b); fetch_rope(b); };
     // merge folded in (one-entry launches with counters): once every wave's
@@ -1376,15 +1399,17 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int) gridDim.x - 1;
         __syncthreads();
         if (!last) return;
-        for (int t = wave; t < 2 * REP; t += NW) merge_head<true>(a, b, qh0 + t / 2, (t & 1) * 64 + (tid & 63));
+        constexpr int WPH = D / 64;                   // waves per head
+        for (int t = wave; t < WPH * REP; t += NW)
+            merge_head<true, D>(a, b, qh0 + t / WPH, (t % WPH) * 64 + (tid & 63));
         if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     // a split past every entry's position (they increase) writes empty
     // partials only. Leaving here, before any K/V load, keeps those loads
     // unconditional below, so the compiler's waits stay partial.
     auto empty = [&](int b) {
-        float2 * pml = (float2 *) (a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2) +
-                                   (size_t) a.n_head * a.nsplit * HD) + (size_t) qh0 * a.nsplit;
+        float2 * pml = (float2 *) (a.part + (size_t) b * a.n_head * a.nsplit * (D + 2) +
+                                   (size_t) a.n_head * a.nsplit * D) + (size_t) qh0 * a.nsplit;
         if (tid < REP) {
             if (fold) st_dev2(pml + (size_t) tid * a.nsplit + split, make_float2(-INFINITY, 0.0f));
             else pml[(size_t) tid * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
@@ -1407,13 +1432,13 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     for (int i = 0; i < PPL; i++) {
         int t = t0 + grp + PS * i;
         t = t < tl ? t : t0;                          // in range; masked below
-        kw[i] = __builtin_nontemporal_load((const GLOBAL v4u *) (kcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
+        kw[i] = __builtin_nontemporal_load((const GLOBAL v4u *) (kcache + (size_t) t * kvd + (size_t) kh * D + l16 * 8));
     }
     #pragma unroll
     for (int i = 0; i < PPL; i++) {
         int t = t0 + grp + PS * i;
         t = t < tl ? t : t0;
-        vw[i] = __builtin_nontemporal_load((const GLOBAL v4u *) (vcache + (size_t) t * kvd + (size_t) kh * HD + l16 * 8));
+        vw[i] = __builtin_nontemporal_load((const GLOBAL v4u *) (vcache + (size_t) t * kvd + (size_t) kh * D + l16 * 8));
     }
     // the tile's loads go out before any work on q, k and v: scheduled
     // after it, they would wait for those inputs' arrival first
@@ -1432,32 +1457,32 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
     }
     if (PF && b + 1 < b1) fetch(b + 1);
     const int pos = a.pos[b], T = pos + 1;
-    // partials of entry b: V sums [head][split][HD], then (max, sum) [head][split]
-    float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (HD + 2);
-    float * po = blk + (size_t) qh0 * a.nsplit * HD;
-    float2 * pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * HD) + (size_t) qh0 * a.nsplit;
+    // partials of entry b: V sums [head][split][D], then (max, sum) [head][split]
+    float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (D + 2);
+    float * po = blk + (size_t) qh0 * a.nsplit * D;
+    float2 * pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * D) + (size_t) qh0 * a.nsplit;
     if (t0 >= T) {
         empty(b);
         continue;
     }
     const int t1 = min(T, t0 + CH);
-    const bool lo = l16 < 8;
+    const bool lo = l16 < LP / 2;
     const float sl = a.inv * 1.44269504088896341f;
     #pragma unroll
-    for (int j = 0; j < REP; j++) rope8(q[j], cs, sn, lo);
+    for (int j = 0; j < REP; j++) rope8p<LP>(q[j], cs, sn, lo);
     // k rotated, then k and v rounded to fp16 as the cache stores them (sml/sml-run.c:3414-3415)
-    rope8(kn, cs, sn, lo);
+    rope8p<LP>(kn, cs, sn, lo);
     v4u knew, vnew;
     #pragma unroll
     for (int e = 0; e < 4; e++) {
         knew[e] = (unsigned) f2h(kn[2 * e]) | ((unsigned) f2h(kn[2 * e + 1]) << 16);
         vnew[e] = (unsigned) f2h(vn[2 * e]) | ((unsigned) f2h(vn[2 * e + 1]) << 16);
     }
-    if (!a.kv_written && t0 <= pos && pos < t1 && tid < 16 && qh0 == kh * REP * nsub) {
-        *(GLOBAL v4u *) (kcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = knew;
-        *(GLOBAL v4u *) (vcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = vnew;
+    if (!a.kv_written && t0 <= pos && pos < t1 && tid < LP && qh0 == kh * REP * nsub) {
+        *(GLOBAL v4u *) (kcache + (size_t) pos * kvd + (size_t) kh * D + l16 * 8) = knew;
+        *(GLOBAL v4u *) (vcache + (size_t) pos * kvd + (size_t) kh * D + l16 * 8) = vnew;
     }
-    // scores: 8 FMAs per lane, summed over the 16 lanes of the row
+    // scores: 8 FMAs per lane, summed over the position's LP lanes
     float sc[PPL][REP];
     #pragma unroll
     for (int i = 0; i < PPL; i++) {
@@ -1469,7 +1494,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             float p = 0.0f;
             #pragma unroll
             for (int e = 0; e < 8; e++) p += q[j][e] * kf[e];
-            p = sum16(p);
+            p = LP == 16 ? sum16(p) : sum8(p);
             sc[i][j] = t < t1 ? p * sl : -INFINITY;
         }
     }
@@ -1482,7 +1507,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
         float x = sc[0][j];
         #pragma unroll
         for (int i = 1; i < PPL; i++) x = fmaxf(x, sc[i][j]);
-        xs[j] = x;
+        xs[j] = LP == 16 ? x : fmaxf(x, dpp_f<0x128>(x));   // both positions of a 16-lane row
     }
     wave_heads<REP>(xs, m, true);
     #pragma unroll
@@ -1495,7 +1520,7 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             sc[i][j] = p;
             ls += p;
         }
-        xs[j] = ls;
+        xs[j] = LP == 16 ? ls : ls + dpp_f<0x128>(ls);
     }
     wave_heads<REP>(xs, l, false);
     // weighted V over the same positions (masked weights are 0)
@@ -1514,22 +1539,30 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             #pragma unroll
             for (int e = 0; e < 8; e++) acc[j][e] += sc[i][j] * vf[e];
     }
-    // sums over the wave's 4 rows, scattered: row r keeps dims l16*8 + 4h + r
+    // sums over the wave's 4 rows (at D = 64 after the two halves of each
+    // row), scattered: row r keeps dims l16*8 + 4h + r
+    if constexpr (LP == 8) {
+        #pragma unroll
+        for (int j = 0; j < REP; j++)
+            #pragma unroll
+            for (int e = 0; e < 8; e++) acc[j][e] += dpp_f<0x128>(acc[j][e]);
+    }
     const int row = (tid >> 4) & 3;
     #pragma unroll
     for (int j = 0; j < REP; j++)
         #pragma unroll
-        for (int h = 0; h < 2; h++)
-            red[wave][j][l16 * 8 + 4 * h + row] =
-                rows_sum4(acc[j][4 * h], acc[j][4 * h + 1], acc[j][4 * h + 2], acc[j][4 * h + 3]);
+        for (int h = 0; h < 2; h++) {
+            const float r4 = rows_sum4(acc[j][4 * h], acc[j][4 * h + 1], acc[j][4 * h + 2], acc[j][4 * h + 3]);
+            if (LP == 16 || (tid & 15) < 8) red[wave][j][l16 * 8 + 4 * h + row] = r4;
+        }
     if ((tid & 63) == 0) {
         #pragma unroll
         for (int j = 0; j < REP; j++) { wm[wave][j] = m[j]; wl[wave][j] = l[j]; }
     }
     __syncthreads();
     // combine the waves: rescale each by 2^(m_w - M)
-    for (int idx = tid; idx < REP * HD; idx += NT) {
-        const int j = idx / HD, d = idx % HD;
+    for (int idx = tid; idx < REP * D; idx += NT) {
+        const int j = idx / D, d = idx % D;
         float M = wm[0][j];
         #pragma unroll
         for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w][j]);
@@ -1541,10 +1574,10 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
             L += e * wl[w][j];
         }
         if (fold) {
-            st_dev(po + ((size_t) j * a.nsplit + split) * HD + d, o);
+            st_dev(po + ((size_t) j * a.nsplit + split) * D + d, o);
             if (d == 0) st_dev2(pml + (size_t) j * a.nsplit + split, make_float2(M, L));
         } else {
-            po[((size_t) j * a.nsplit + split) * HD + d] = o;
+            po[((size_t) j * a.nsplit + split) * D + d] = o;
             if (d == 0) pml[(size_t) j * a.nsplit + split] = make_float2(M, L);
         }
     }
@@ -1558,19 +1591,21 @@ __device__ __forceinline__ void attn_body(const sml_kattn & a) {
 // lane, so the cache holds what that kernel would have written. Runs ahead of
 // an attention launch with kv_written set, in which positions of one sequence
 // read each other's k and v (prompt reading). Grid: one workgroup per
-// sequence; block: one 16-lane row per kv head.
-extern "C" __global__ __launch_bounds__(128) void sml_ropekv(const sml_kattn a) {
-    const int b = blockIdx.x, tid = threadIdx.x, kh = tid >> 4, l16 = tid & 15, kvd = a.n_kv * HD;
-    const float * ak = a.k + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
-    const float * av = a.v + (size_t) b * a.qkv_stride + (size_t) kh * HD + l16 * 8;
+// sequence; block: D/8 lanes per kv head.
+template <int D>
+__device__ __forceinline__ void ropekv_body(const sml_kattn & a) {
+    constexpr int LP = D / 8;
+    const int b = blockIdx.x, tid = threadIdx.x, kh = tid / LP, l16 = tid % LP, kvd = a.n_kv * D;
+    const float * ak = a.k + (size_t) b * a.qkv_stride + (size_t) kh * D + l16 * 8;
+    const float * av = a.v + (size_t) b * a.qkv_stride + (size_t) kh * D + l16 * 8;
     float kn[8], vn[8];
     load_f8(ak, kn);
     load_f8(av, vn);
-    const int pos = a.pos[b], half = HD / 2;
+    const int pos = a.pos[b], half = D / 2;
     float cs[8], sn[8];
-    load_f8(a.cos_t + (size_t) pos * half + (l16 & 7) * 8, cs);
-    load_f8(a.sin_t + (size_t) pos * half + (l16 & 7) * 8, sn);
-    rope8(kn, cs, sn, l16 < 8);
+    load_f8(a.cos_t + (size_t) pos * half + (l16 & (LP / 2 - 1)) * 8, cs);
+    load_f8(a.sin_t + (size_t) pos * half + (l16 & (LP / 2 - 1)) * 8, sn);
+    rope8p<LP>(kn, cs, sn, l16 < LP / 2);
     v4u knew, vnew;
     #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -1579,9 +1614,11 @@ extern "C" __global__ __launch_bounds__(128) void sml_ropekv(const sml_kattn a) 
     }
     GLOBAL uint16_t * kcache = (GLOBAL uint16_t *) (a.kc_slots ? a.kc_slots[a.slot[b]] + a.layer_off : a.kcache);
     GLOBAL uint16_t * vcache = (GLOBAL uint16_t *) (a.vc_slots ? a.vc_slots[a.slot[b]] + a.layer_off : a.vcache);
-    *(GLOBAL v4u *) (kcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = knew;
-    *(GLOBAL v4u *) (vcache + (size_t) pos * kvd + (size_t) kh * HD + l16 * 8) = vnew;
+    *(GLOBAL v4u *) (kcache + (size_t) pos * kvd + (size_t) kh * D + l16 * 8) = knew;
+    *(GLOBAL v4u *) (vcache + (size_t) pos * kvd + (size_t) kh * D + l16 * 8) = vnew;
 }
+extern "C" __global__ __launch_bounds__(128) void sml_ropekv(const sml_kattn a) { ropekv_body<HD>(a); }
+extern "C" __global__ __launch_bounds__(128) void sml_ropekv_d64(const sml_kattn a) { ropekv_body<64>(a); }
 
 #define ATTN_KERNEL(R) \
     extern "C" __global__ __launch_bounds__(256) void sml_attn_r##R(const sml_kattn a) { attn_body<R, 4, false>(a); } \
@@ -1592,6 +1629,15 @@ extern "C" __global__ __launch_bounds__(128) void sml_ropekv(const sml_kattn a) 
     extern "C" __global__ __launch_bounds__(512) void sml_attnc8_s32_r##R(const sml_kattn a) { attn_body<R, 8, true, 32>(a); } \
     extern "C" __global__ __launch_bounds__(512) void sml_attnc8_s64_r##R(const sml_kattn a) { attn_body<R, 8, true, 64>(a); }
 ATTN_KERNEL(1) ATTN_KERNEL(2) ATTN_KERNEL(3) ATTN_KERNEL(4) ATTN_KERNEL(5) ATTN_KERNEL(6) ATTN_KERNEL(7) ATTN_KERNEL(8)
+// head_dim 64 (suffix _d64): 64 positions per round of 8 waves, so splits of 64 or 128
+#define ATTN_KERNEL_D64(R) \
+    extern "C" __global__ __launch_bounds__(256) void sml_attn_d64_r##R(const sml_kattn a) { attn_body<R, 4, false, ATTN_CHUNK, 64>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attn8_d64_r##R(const sml_kattn a) { attn_body<R, 8, false, ATTN_CHUNK, 64>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attnc8_d64_r##R(const sml_kattn a) { attn_body<R, 8, true, ATTN_CHUNK, 64>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attn8_s64_d64_r##R(const sml_kattn a) { attn_body<R, 8, false, 64, 64>(a); } \
+    extern "C" __global__ __launch_bounds__(512) void sml_attnc8_s64_d64_r##R(const sml_kattn a) { attn_body<R, 8, true, 64, 64>(a); }
+ATTN_KERNEL_D64(1) ATTN_KERNEL_D64(2) ATTN_KERNEL_D64(3) ATTN_KERNEL_D64(4) ATTN_KERNEL_D64(5) ATTN_KERNEL_D64(6)
+ATTN_KERNEL_D64(7) ATTN_KERNEL_D64(8)
 
 // ---------------------------------------------------------------- prompt attention, a wave per position
 //
@@ -1965,6 +2011,9 @@ ATTNF_KERNEL(1) ATTNF_KERNEL(2) ATTNF_KERNEL(3) ATTNF_KERNEL(4) ATTNF_KERNEL(5) 
 // the sequence).
 extern "C" __global__ __launch_bounds__(HD) void sml_attn_merge(const sml_kattn a) {
     merge_head<false>(a, blockIdx.z, blockIdx.x, threadIdx.x);
+}
+extern "C" __global__ __launch_bounds__(64) void sml_attn_merge_d64(const sml_kattn a) {
+    merge_head<false, 64>(a, blockIdx.z, blockIdx.x, threadIdx.x);
 }
 
 // The merge with its output quantized per 256 values (the rule of

@@ -756,11 +756,20 @@ size_t sml_hip_attn_part_floats(int n_head, int hd, int n_ctx) {
 // positions), 128 / 64 / 32: decode 1097 / 1112 / 1068 tokens/s, a 2048-id
 // prompt at level 1 2405 / 2598 / 2665. SML_ATTN_CHUNK overrides (32, 64 or
 // 128).
-static int attn_split(int n_kv, int n_ctx) {
+// a decode/prompt attention kernel's name: base, _s<ch> for splits other
+// than 128, _d64 for head_dim 64, _r<query heads per workgroup>
+static void attn_name(char * name, size_t n, const char * base, int ch, int hd, int rep) {
+    char sp[16] = "";
+    if (ch != ATTN_CHUNK) snprintf(sp, sizeof sp, "_s%d", ch);
+    snprintf(name, n, "%s%s%s_r%d", base, sp, hd == 64 ? "_d64" : "", rep);
+}
+
+static int attn_split(int n_kv, int n_ctx, int hd) {
     int ch = ATTN_CHUNK;
     while (ch > 64 && (long) n_kv * ((n_ctx + ch - 1) / ch) < 256) ch /= 2;
     const int ce = env_int("SML_ATTN_CHUNK", 0);
     if (ce == 32 || ce == 64 || ce == 128) ch = ce;
+    if (hd == 64 && ch < 64) ch = 64;               // head_dim 64: 64 positions per round of 8 waves
     return ch;
 }
 
@@ -768,8 +777,9 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
                   const float * cos_t, const float * sin_t, const int32_t * pos, int n_head, int n_kv,
                   int hd, int n_ctx, int n_pos, float * part, float * out, int8_t * q_out, float * s_out,
                   int32_t * u_out, int * cnt) {
-    if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
+    if ((hd != 128 && hd != 64) || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
+    if (hd != 128 && (g_exact || cnt)) hx_failf("head_dim %d: exact mode and the folded merge take head_dim 128", hd);
     if (n_pos < 1 || n_pos > n_ctx) hx_failf("attention over %d of %d positions", n_pos, n_ctx);
     if (g_exact) {
         // the reference's order: RoPE, the KV write and the scores over
@@ -797,7 +807,7 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     // splits past n_pos are not launched: the merge of the ones that are
     // equals the merge of all (empty splits add exact zeros)
     const int aw = 8;
-    const int ch = attn_split(n_kv, n_ctx);
+    const int ch = attn_split(n_kv, n_ctx, hd);
     const int ns = (n_pos + ch - 1) / ch;
     sml_kattn a;
     memset(&a, 0, sizeof a);
@@ -821,11 +831,10 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
     if (se >= 1 && rep % se == 0) nsub = se;
     if (cnt) nsub = 1;
     a.nsub = nsub;
-    char name[32];
-    if (ch != ATTN_CHUNK) snprintf(name, sizeof name, "sml_attn8_s%d_r%d", ch, n_head / n_kv / nsub);
-    else snprintf(name, sizeof name, "sml_attn%d_r%d", aw, n_head / n_kv / nsub);
+    char name[40];
+    attn_name(name, sizeof name, "sml_attn8", ch, hd, n_head / n_kv / nsub);
     hx_launch(name, (unsigned) ns, (unsigned) (n_kv * nsub), (unsigned) (64 * aw), 0, st, &a);
-    if (!cnt) hx_launch("sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
+    if (!cnt) hx_launch(hd == 64 ? "sml_attn_merge_d64" : "sml_attn_merge", (unsigned) n_head, 1, (unsigned) hd, 0, st, &a);
 }
 
 // LDS of the prompt flash attention (sml_attnf): two stages of a 64-position
@@ -836,16 +845,22 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,
                         int n_pos, float * part, float * out, int8_t * q_out, float * s_out, int32_t * u_out,
                         int causal, int exact, int q256) {
-    if (hd != 128 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
+    if ((hd != 128 && hd != 64) || n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
     if (n_pos < 1 || n_pos > n_ctx) hx_failf("attention over %d of %d positions", n_pos, n_ctx);
-    if (q_out && q256 && (causal || n_head % 2))
-        hx_failf("the merge quantizes per 256 only decode steps of an even head count (%d heads)", n_head);
+    if (q_out && q256 && (causal || n_head % 2 || hd != 128))
+        hx_failf("the merge quantizes per 256 only decode steps of an even head count of head_dim 128 (%d heads, %d)",
+                 n_head, hd);
+    // head_dim 64 reads level-2 prompts with the level-1 kernel (the matrix-core
+    // and wave-per-position prompt kernels are head_dim 128), at splits of
+    // 128 as the level-2 partials are sized
+    const int c2_d64 = causal == 2 && hd == 64;
+    if (c2_d64) causal = 1;
     if (nseq < 1 || nseq > 65535) hx_failf("attention batch of %d", nseq);
     const int aw = env_int("SML_ATTN_WAVES", nseq >= 4 && !exact ? 4 : 8) == 4 ? 4 : 8;
     // the 8-wave kernels split as decoding does (attn_split); the 4-wave and
     // wave-per-position kernels run splits of 128
-    const int ch = causal == 2 || (causal == 0 && aw == 4) ? ATTN_CHUNK : attn_split(n_kv, n_ctx);
+    const int ch = causal == 2 || (causal == 0 && aw == 4) || c2_d64 ? ATTN_CHUNK : attn_split(n_kv, n_ctx, hd);
     const int ns = (n_pos + ch - 1) / ch;             // splits past n_pos: not launched
     sml_kattn a;
     memset(&a, 0, sizeof a);
@@ -858,9 +873,9 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     a.kv_written = causal != 0;
     if (causal) {
         if (n_kv > 8) hx_failf("causal attention takes at most 8 kv heads");
-        hx_launch("sml_ropekv", (unsigned) nseq, 1, (unsigned) (16 * n_kv), 0, st, &a);
+        hx_launch(hd == 64 ? "sml_ropekv_d64" : "sml_ropekv", (unsigned) nseq, 1, (unsigned) (hd / 8 * n_kv), 0, st, &a);
     }
-    char name[32];
+    char name[40];
     // many sequences give many workgroups: 4-wave ones, two per CU, then
     // measured faster (16 sequences at ~1k positions: 5.6 against 6.8 ms per
     // step); one sequence, and any step that must equal decoding alone bit
@@ -899,16 +914,13 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
         return;
     }
     const int nt = causal ? 512 : 64 * aw;
-    if (a.tpw > 1 || causal) {
-        if (ch == ATTN_CHUNK) snprintf(name, sizeof name, "sml_attnc8_r%d", n_head / n_kv);
-        else snprintf(name, sizeof name, "sml_attnc8_s%d_r%d", ch, n_head / n_kv);
-    } else if (aw == 4) snprintf(name, sizeof name, "sml_attn_r%d", n_head / n_kv);
-    else if (ch == ATTN_CHUNK) snprintf(name, sizeof name, "sml_attn8_r%d", n_head / n_kv);
-    else snprintf(name, sizeof name, "sml_attn8_s%d_r%d", ch, n_head / n_kv);
+    attn_name(name, sizeof name, a.tpw > 1 || causal ? "sml_attnc8" : aw == 4 ? "sml_attn" : "sml_attn8",
+              a.tpw > 1 || causal || aw != 4 ? ch : ATTN_CHUNK, hd, n_head / n_kv);
     hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) ((nseq + a.tpw - 1) / a.tpw), (unsigned) nt, 0,
                st, &a);
     if (q_out && q256) hx_launch3("sml_attn_merge_sb", (unsigned) n_head / 2, 1, (unsigned) nseq, 256, 0, st, &a);
-    else hx_launch3("sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq, (unsigned) hd, 0, st, &a);
+    else hx_launch3(hd == 64 ? "sml_attn_merge_d64" : "sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq,
+                    (unsigned) hd, 0, st, &a);
 }
 
 int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,
@@ -925,7 +937,7 @@ int sml_hip_attention_prompt(const float * qkv, int n_rows, int pos0, uint16_t *
                              const float * cos_t, const float * sin_t, int n_head, int n_kv, int hd, int n_ctx,
                              float * part, float * out) {
     OP_BEGIN(-1);
-    if (hd != 128 || n_kv <= 0 || n_kv > 8 || n_head % n_kv || n_head / n_kv > 8)
+    if ((hd != 128 && hd != 64) || n_kv <= 0 || n_kv > 8 || n_head % n_kv || n_head / n_kv > 8)
         hx_failf("prompt attention shape (heads %d/%d, head_dim %d) not supported", n_head, n_kv, hd);
     if (n_rows < 1 || n_rows > 65535 || pos0 < 0 || pos0 + n_rows > n_ctx)
         hx_failf("prompt attention over positions %d..%d of %d", pos0, pos0 + n_rows - 1, n_ctx);

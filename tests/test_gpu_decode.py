@@ -38,6 +38,16 @@ def tiny_inorder(tmp_path_factory):
 
 
 @pytest.fixture(scope="module")
+def hd64(tmp_path_factory):
+    """head_dim 64 (Llama-3.2-1B's attention shape, 32/8 heads of 64 at
+    hidden 2048; here 16/4 heads at hidden 1024, 2 layers)."""
+    p = tmp_path_factory.mktemp("dec") / "hd64.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=1024, n_head=16, n_head_kv=4, n_ff=2048, n_vocab=2000, rope_theta=5e5,
+                   random_perm=True, seed=64)
+    return p
+
+
+@pytest.fixture(scope="module")
 def qwenish(tmp_path_factory):
     """Qwen2.5-1.5B layer shapes (hidden 1536, FFN 8960, 12/2 heads, q/k/v bias,
     tied head) with 4 layers and a 32000 vocabulary."""
@@ -118,7 +128,7 @@ def test_teacher_forced_logits(tiny, graph, monkeypatch):
         d.close()
 
 
-@pytest.mark.parametrize("model,start", [("tiny", 11), ("tiny_inorder", 7)])
+@pytest.mark.parametrize("model,start", [("tiny", 11), ("tiny_inorder", 7), ("hd64", 5)])
 def test_fast_graded_like_the_reference(model, start, request):
     """40 teacher-forced steps on the oracle's greedy ids: every top-1 agrees
     or is a tie, every logit correlation >= 0.999."""
@@ -210,7 +220,7 @@ def moe_model(tmp_path_factory):
     return p
 
 
-@pytest.mark.parametrize("model", ["tiny", "tiny_inorder", "qwenish", "moe_model"])
+@pytest.mark.parametrize("model", ["tiny", "tiny_inorder", "qwenish", "moe_model", "hd64"])
 def test_batched_prompt_equals_stepping(model, request):
     """Batched prompt reading (level 1, the default): chunks of 16 positions
     through the small-M GEMM and the causal attention read a prompt exactly
@@ -431,3 +441,12 @@ def test_moe_modes_graded_against_the_reference(tmp_path, mode):
     assert sum(c < 0.9999 for c in corrs) <= 1 and min(corrs) >= 0.98, corrs
     assert sum(x > 0.01 for x in gaps) <= 1, gaps
     assert len(set(toks[1:])) >= 8, toks
+
+
+def test_head_dim_64_refuses_exact_mode(hd64):
+    """Exact mode's attention kernels are head_dim 128; a head_dim 64 model
+    opens in fast mode and is refused in exact mode with a reason."""
+    with pytest.raises(sa.HipError, match="head_dim"):
+        sa.Decoder(hd64, n_ctx=64, exact=True)
+    d = sa.Decoder(hd64, n_ctx=64)
+    d.close()

@@ -247,11 +247,11 @@ def test_softmax_sum_is_the_serial_chain():
         assert got.view(np.uint32) == want.view(np.uint32), f"{name}: {got!r} vs {want!r}"
 
 
-def attention_case(H, KV, n_ctx, positions, exact, seed):
+def attention_case(H, KV, n_ctx, positions, exact, seed, hd=128):
     """Fill a cache with random fp16 rows, then run attention at each of
     `positions` (rotating q and k, writing the position's rows) and compare
     the output with the oracle's reference-order attention."""
-    hd, half = 128, 64
+    half = hd // 2
     rng = np.random.default_rng(seed)
     cos_t = np.zeros(n_ctx * half, np.float32)
     sin_t = np.zeros(n_ctx * half, np.float32)
@@ -326,6 +326,22 @@ def test_fast_attention_4096(heads, split, monkeypatch):
     rel-RMS <= 1e-4)."""
     monkeypatch.setenv("SML_ATTN_CHUNK", split)
     for pos, got, want in attention_case(*heads, 4096, [0, 1, 2111, 2112, 4095], False, seed=heads[0] + 1):
+        err = np.abs(got.astype(np.float64) - want)
+        assert err.max() <= 1e-3 * np.abs(want).max(), (pos, err.max())
+        assert np.sqrt((err ** 2).mean() / (want.astype(np.float64) ** 2).mean()) <= 1e-4, pos
+
+
+@pytest.mark.parametrize("split", ["", "64"])
+@pytest.mark.parametrize("heads", [(32, 8), (14, 2), (9, 3)])
+def test_fast_attention_4096_head_dim_64(heads, split, monkeypatch):
+    """head_dim 64 (the Llama-3.2-1B, Qwen2.5-0.5B and SmolLM shapes): a
+    position's dims on 8 lanes, RoPE's partner lane i ^ 4, two positions per
+    16-lane row combined before the row reductions. At positions 0, 1, 2111,
+    2112 and 4095 of a 4096-position context: K/V rows bit for bit, outputs
+    within 1e-3 of the oracle (max |d| <= 1e-3 max |ref|, rel-RMS <= 1e-4)."""
+    if split:
+        monkeypatch.setenv("SML_ATTN_CHUNK", split)
+    for pos, got, want in attention_case(*heads, 4096, [0, 1, 2111, 2112, 4095], False, seed=heads[0] + 7, hd=64):
         err = np.abs(got.astype(np.float64) - want)
         assert err.max() <= 1e-3 * np.abs(want).max(), (pos, err.max())
         assert np.sqrt((err ** 2).mean() / (want.astype(np.float64) ** 2).mean()) <= 1e-4, pos

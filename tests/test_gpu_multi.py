@@ -51,14 +51,16 @@ def run_alone(path, n_vocab, b, steps):
         d.close()
 
 
-@pytest.mark.parametrize("kind", ["dense", "dense_perm", "moe"])
+@pytest.mark.parametrize("kind", ["dense", "dense_perm", "moe", "hd64"])
 def test_step_multi_equals_decoding_alone(tmp_path, kind, monkeypatch):
+    """hd64: head_dim 64 (8 heads at hidden 512), whose batched step runs the
+    4-wave attention of that head size."""
     monkeypatch.setenv("SML_FUSE", "1")
     monkeypatch.setenv("SML_MULTI", "exact")
     p = tmp_path / f"{kind}.ssf"
     extra = dict(n_expert=8, n_expert_used=2, moe_flags=1) if kind == "moe" else {}
-    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, qkv_bias=True,
-                   random_perm=kind == "dense_perm", seed=70, **extra)
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=8 if kind == "hd64" else 4, n_head_kv=2, n_ff=1024,
+                   n_vocab=2000, qkv_bias=True, random_perm=kind == "dense_perm", seed=70, **extra)
     steps = 6
     m_last, m_out = run_multi(p, 2000, steps)
     for b in range(len(PROMPTS)):

@@ -225,8 +225,9 @@ def test_flash_prompt_attention_equals_wave_form(tmp_path_factory, model, npos, 
 
 
 @pytest.mark.parametrize("flash", ["1", "0"])
-@pytest.mark.parametrize("heads,n_rows", [((32, 8), 512), ((32, 8), 64), ((12, 2), 512)])
-def test_prompt_attention_4096(heads, n_rows, flash, monkeypatch):
+@pytest.mark.parametrize("heads,n_rows,hd", [((32, 8), 512, 128), ((32, 8), 64, 128), ((12, 2), 512, 128),
+                                             ((32, 8), 512, 64), ((14, 2), 100, 64)])
+def test_prompt_attention_4096(heads, n_rows, hd, flash, monkeypatch):
     """The level-2 prompt's causal attention on its own, at the end of a
     4096-position context: a chunk of n_rows positions ending at 4095 over a
     cache of random fp16 rows. The flash kernel splits the KV range as the
@@ -234,10 +235,12 @@ def test_prompt_attention_4096(heads, n_rows, flash, monkeypatch):
     and merges; the wave-per-position form splits by 128. Every chunk row's
     rotated K and its V as stored equal the oracle's bit for bit; sampled
     rows' outputs are within 1e-3 of the oracle's reference-order attention
-    (max |d| <= 1e-3 max |ref|, rel-RMS <= 1e-4), as the decode path's are."""
+    (max |d| <= 1e-3 max |ref|, rel-RMS <= 1e-4), as the decode path's are.
+    head_dim 64 takes the level-1 kernel (positions sharing each split's
+    tile) whichever form is asked for."""
     monkeypatch.setenv("SML_ATTN_FLASH", flash)
     H, KV = heads
-    hd, half, n_ctx = 128, 64, 4096
+    half, n_ctx = hd // 2, 4096
     pos0 = n_ctx - n_rows
     rng = np.random.default_rng(H * 1000 + n_rows)
     cos_t = np.zeros(n_ctx * half, np.float32)
@@ -251,7 +254,7 @@ def test_prompt_attention_4096(heads, n_rows, flash, monkeypatch):
     dqkv, dcos, dsin = sa.DevBuf.of(qkv), sa.DevBuf.of(cos_t), sa.DevBuf.of(sin_t)
     part = sa.DevBuf(n_rows * H * (n_ctx // 128) * (hd + 2) * 4)
     out = sa.DevBuf(n_rows * H * hd * 4)
-    print(f"prompt attention {heads} rows {n_rows} flash {flash}", flush=True)
+    print(f"prompt attention {heads} rows {n_rows} head_dim {hd} flash {flash}", flush=True)
     rc = sa.lib().sml_hip_attention_prompt(dqkv.ptr, n_rows, pos0, dkc.ptr, dvc.ptr, dcos.ptr, dsin.ptr,
                                            H, KV, hd, n_ctx, part.ptr, out.ptr)
     assert rc == 0, sa.lib().sml_hip_last_error()
