@@ -604,6 +604,8 @@ def main():
     ap.add_argument("--gemv-sweep", action="store_true",
                     help="only the Q4 GEMV and streaming read at 34..544 MB (fixed cost vs steady rate)")
     ap.add_argument("--ingest", action="store_true", help="only re-quantize the GPTQ-4 4096 x 14336 tensor")
+    ap.add_argument("--widths", action="store_true",
+                    help="only the GEMV at every SSF width and the GPTQ-4 layout (4096x14336, 14336x4096)")
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: fill the 4096 context)")
     ap.add_argument("--prompt-only", type=int, metavar="LEVEL", default=-1,
@@ -632,6 +634,8 @@ def main():
             res = {"gemv_size_sweep": gemv_size_sweep(work)}
         elif a.ingest:
             res = {"ingest": ingest_leg()}
+        elif a.widths:
+            res = {"width_sweep": width_sweep(work, iters=50)}
         elif a.decode_trace:
             res = {"decode_trace": decode_trace(work, a.decode_trace, a.steps, a.exact)}
         elif a.prompt_only >= 0:

@@ -810,6 +810,8 @@ __device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first 
 GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH(7) GEMV_WIDTH(8)
 // a whole 14336-wide row in one pass (tuning: SML_GEMV_NI=8)
 GEMV_KERNEL(4, 1, 8) GEMV_KERNEL(4, 2, 8)
+GEMV_KERNEL(2, 1, 8) GEMV_KERNEL(2, 2, 8) GEMV_KERNEL(3, 1, 8) GEMV_KERNEL(3, 2, 8)
+GEMV_KERNEL(5, 1, 8) GEMV_KERNEL(5, 2, 8)
 
 // Persistent forms (suffix _p, Q4): a grid of at most a few workgroups per CU,
 // each taking row blocks blockIdx.x, +gridDim.x, ...; the activation (or the

@@ -502,11 +502,17 @@ static void pick_shape(int rows, int cols, int nbits, int swiglu, int fused, int
         // wave with 4 chunks per pass (4096 x 14336: Q3 9.2 -> 8.5 us, Q5
         // 10.3 -> 9.8, Q8 13.0 -> 12.7; Q4 and Q6 stay at 2 rows)
         if ((nbits == 3 || nbits == 5 || nbits == 8) && r == 2 && i == 4 && !swiglu) r = 1;
+        // and tall matrices at two rows per wave rather than four (14336 x
+        // 4096: Q3 8.2 -> 7.6 us, Q5 9.2 -> 8.7)
+        if ((nbits == 3 || nbits == 5) && r == 4 && !swiglu) r = 2;
+        // Q2's long rows in one pass of 8 chunks at one row per wave (4096 x
+        // 14336: 6.45 -> 6.21 us)
+        if (nbits == 2 && !swiglu && r <= 2 && i == 4 && ng > 256) { r = 1; i = 8; }
     }
     const int fr = env_int("SML_GEMV_RB", 0), fi = env_int("SML_GEMV_NI", 0);
     if (fr == 1 || fr == 2 || fr == 4) r = fr;
     if ((fi == 1 || fi == 2 || fi == 4) && fi <= imax) i = fi;
-    if (fi == 8 && !fused && !swiglu && nbits == 4 && r <= 2) i = 8;   // Q4, one or two rows per wave
+    if (fi == 8 && !fused && !swiglu && nbits >= 2 && nbits <= 5 && r <= 2) i = 8;   // Q2-Q5, one or two rows per wave
     if (swiglu && r < 2) r = 2;
     if (!swiglu && !fused && r == 1 && i == 1) i = 2;
     *rb = r;
