@@ -191,6 +191,57 @@ def traffic(path, work):
                "copy_bytes": COPY_BYTES, "fetch_scale": round(f_fetch, 4), "write_scale": round(f_write, 4)}
 
 
+def gemv_timeline(tmp, launches=24):
+    """The roofline GEMV's timeline inside one cold launch (4096 x 14336 Q4,
+    rotating copies beyond the MALL): per row block, the GPU clock (100 MHz)
+    at entry, at its first weight word, when the first and the last pass's
+    weights are all in, and at exit (sml_hip_gemv_timeline); per launch the
+    spread over the 2048 blocks; medians over the launches, in us from the
+    launch's first entry."""
+    rows, cols = 4096, 14336
+    p = os.path.join(tmp, "timeline_q4.ssf")
+    sa.synth_matrix(p, rows, cols, nbits=4, seed=1004)
+    first = sa.Mat.from_file(p, "w")
+    mats = [first] + [sa.Mat.from_file(p, "w") for _ in range(int(6e8 // first.bytes))]
+    x = np.random.default_rng(0).standard_normal(cols).astype(np.float32)
+    act = sa.Act(cols)
+    xd = sa.DevBuf.of(x)
+    sa.normq(xd, act)
+    y = sa.DevBuf(rows * 4)
+    arr = (sa.c_void_p * len(mats))(*[m.h for m in mats])
+    nb = rows // 8
+    ts = np.zeros(nb * 5, np.uint64)
+    lib = sa.lib()
+    per = []
+    for it in range(launches + 1):
+        n = lib.sml_hip_gemv_timeline(arr, len(mats), act.q.ptr, act.scale.ptr, act.sums.ptr, y.ptr, len(mats),
+                                      ts.ctypes.data, nb)
+        if n != nb:
+            raise RuntimeError(lib.sml_hip_last_error().decode())
+        if it == 0:
+            continue                                   # first call: the copies' pages warm in the TLB
+        t = ts.reshape(nb, 5).astype(np.int64)
+        t0 = t[:, 0].min()
+        d = (t - t0) * 10 / 1000.0                     # us
+        per.append({
+            "span": float(d[:, 4].max()),
+            "entry_p50": float(np.median(d[:, 0])), "entry_max": float(d[:, 0].max()),
+            "first_word_latency_p50": float(np.median(d[:, 1] - d[:, 0])),
+            "first_word_min": float(d[:, 1].min()), "first_word_p50": float(np.median(d[:, 1])),
+            "pass1_all_in_p50": float(np.median(d[:, 2])), "last_weights_in_p50": float(np.median(d[:, 3])),
+            "last_weights_in_max": float(d[:, 3].max()),
+            "exit_p50": float(np.median(d[:, 4])), "exit_max": float(d[:, 4].max()),
+        })
+    for m in mats:
+        m.free()
+    os.remove(p)
+    keys = per[0].keys()
+    med = {k: round(float(np.median([q[k] for q in per])), 2) for k in keys}
+    # the weights' bytes over the window from the first word anywhere to the last pass's last word
+    rate = first.bytes / ((med["last_weights_in_max"] - med["first_word_min"]) * 1e-6) / 1e12
+    return {"launches": len(per), "bytes": first.bytes, "median_us": med, "streaming_TB_per_s": round(rate, 2)}
+
+
 def width_sweep(tmp, target_bytes=6e8, iters=200):
     """The fused GEMV at every SSF width and the GPTQ-style 4-bit layout, at
     4096 x 14336 and 14336 x 4096, over rotating copies (> the 256 MB MALL)."""
@@ -604,6 +655,8 @@ def main():
     ap.add_argument("--gemv-sweep", action="store_true",
                     help="only the Q4 GEMV and streaming read at 34..544 MB (fixed cost vs steady rate)")
     ap.add_argument("--ingest", action="store_true", help="only re-quantize the GPTQ-4 4096 x 14336 tensor")
+    ap.add_argument("--gemv-timeline", action="store_true",
+                    help="only the roofline GEMV's in-kernel timeline (entry, first weight word, last, exit)")
     ap.add_argument("--widths", action="store_true",
                     help="only the GEMV at every SSF width and the GPTQ-4 layout (4096x14336, 14336x4096)")
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
@@ -634,6 +687,8 @@ def main():
             res = {"gemv_size_sweep": gemv_size_sweep(work)}
         elif a.ingest:
             res = {"ingest": ingest_leg()}
+        elif a.gemv_timeline:
+            res = {"gemv_timeline": gemv_timeline(work)}
         elif a.widths:
             res = {"width_sweep": width_sweep(work, iters=50)}
         elif a.decode_trace:

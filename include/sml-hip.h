@@ -121,6 +121,15 @@ int sml_hip_matvec_swiglu_fused(const sml_hip_mat * gate, const sml_hip_mat * up
 // events on the launch stream. ms_total receives the elapsed milliseconds.
 int sml_hip_time_matvec(const sml_hip_mat * const * mats, int ncopy, const int8_t * q, const float * scale,
                         const int32_t * sums, float * y, int iters, float * ms_total);
+// The same launches of a Q4 GEMV in its 2-rows-by-4-chunks shape (the roofline
+// workload's), instrumented: for the last launch, per row block, the GPU's
+// 100 MHz real-time clock at entry, at the first weight word's arrival, when
+// the first pass's and the last pass's weights have all arrived, and at exit
+// (5 values a block into ts, host memory, at most max_blocks blocks). Returns
+// the block count, or -1. A measurement tool (no counterpart in the
+// reference); its waits for the timestamps serialize the loads slightly.
+int sml_hip_gemv_timeline(const sml_hip_mat * const * mats, int ncopy, const int8_t * q, const float * scale,
+                          const int32_t * sums, float * y, int iters, unsigned long long * ts, int max_blocks);
 
 // Calibration: time `iters` launches of a plain streaming read of `bytes`
 // from each buffer in turn (grid workgroups of 256 threads, 128-bit loads).

@@ -78,6 +78,8 @@ _SIGS = [
     ("sml_hip_matvec_swiglu_fused", c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     ("sml_hip_time_matvec", c_int, [P(c_void_p), c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, P(c_float)]),
+    ("sml_hip_gemv_timeline", c_int, [P(c_void_p), c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
+                                      c_int]),
     ("sml_hip_unpack", c_int, [c_void_p, c_int, c_int, c_void_p]),
     ("sml_hip_time_read", c_int, [P(c_void_p), c_int, c_size_t, c_int, c_int, P(c_float)]),
     ("sml_hip_copy", c_int, [c_void_p, c_void_p, c_size_t]),

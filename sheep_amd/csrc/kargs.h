@@ -67,6 +67,10 @@ typedef struct {
     // index) pair of its rows' outputs to amax[block], as sml_argmax_part
     // would for those rows.
     int2          * amax;
+    // the timeline kernel (sml_gemv_q4_r2_i4_ts): per row block, the real-time
+    // clock (100 MHz) at entry, at the first weight word's arrival, when the
+    // first pass's and the last pass's weights have all arrived, and at exit
+    unsigned long long * ts;
 } sml_kgemv;
 
 // Multi-workgroup RMSNorm + gather + quantize: every workgroup reduces the

@@ -440,10 +440,16 @@ __device__ __forceinline__ float seg_sum(float v) {
 
 // blk: the workgroup's row block (blockIdx.x, or each block a persistent
 // workgroup takes in turn); first: the activation is not yet in LDS.
-template <int NB, int RB, int NI, int WG, bool NT, int AM, bool SW, bool HQ, int LPR = 64, bool EX = false>
-__device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first = true) {
+// TS: record the row block's timeline (a.ts) into tsh[0..3] (LDS of the
+// caller), thread 0's view: entry, the first weight word of the first pass,
+// all of the first pass's weights, all of the last pass's.
+template <int NB, int RB, int NI, int WG, bool NT, int AM, bool SW, bool HQ, int LPR = 64, bool EX = false,
+          bool TS = false>
+__device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first = true,
+                          unsigned long long * tsh = nullptr) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int n = a.cols, ng = n / 32, ns = (ng + 7) / 8;
+    if constexpr (TS) { if (threadIdx.x == 0) tsh[0] = __builtin_amdgcn_s_memrealtime(); }
     int8_t * lq = (int8_t *) lds;
     float2 * lsc = (float2 *) (lds + n);
     const int tid = threadIdx.x, lane = tid & (WAVE - 1);
@@ -640,7 +646,20 @@ __device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first 
         CW w[NI][RB];
         uint32_t fqv[NI][RB], fdv[NI][RB];
         load_pass(c0, w, fqv, fdv);
+        if constexpr (TS) {
+            // loads return in order: all but the pass's other 3*NI*RB - 1
+            // weight loads (Q4: a code word and two field words per chunk
+            // and row) have returned once the first code word has
+            static_assert(NB == 4 && 3 * NI * RB - 1 < 64, "the timeline kernel counts Q4 loads");
+            constexpr int W1 = 3 * NI * RB - 1;
+            __builtin_amdgcn_s_waitcnt((W1 & 15) | ((W1 >> 4) << 14) | (7 << 4) | (15 << 8));
+            if (c0 == 0 && threadIdx.x == 0) tsh[1] = __builtin_amdgcn_s_memrealtime();
+        }
         stage();
+        if constexpr (TS) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (threadIdx.x == 0) tsh[c0 == 0 ? 2 : 3] = __builtin_amdgcn_s_memrealtime();
+        }
         compute_pass(c0, w, fqv, fdv);
     }
     if constexpr (EX) {
@@ -808,6 +827,21 @@ __device__ void gemv_body(const sml_kgemv & a, int blk = blockIdx.x, bool first 
     GEMV_KERNEL_S(NB, 4, 1) GEMV_KERNEL_S(NB, 4, 2) GEMV_KERNEL_S(NB, 4, 4)               \
     GEMV_KERNEL_H(NB, 2) GEMV_KERNEL_H(NB, 4) GEMV_WIDE(NB)
 GEMV_WIDTH(2) GEMV_WIDTH(3) GEMV_WIDTH(4) GEMV_WIDTH(5) GEMV_WIDTH(6) GEMV_WIDTH(7) GEMV_WIDTH(8)
+// the roofline GEMV's shape with its timeline (sml_kgemv.ts): thread 0's
+// clock at entry, first weight word, first pass's and last pass's weights
+// all in, and at exit after the workgroup's stores
+extern "C" __global__ __launch_bounds__(256) void sml_gemv_q4_r2_i4_ts(const sml_kgemv a) {
+    __shared__ unsigned long long tsh[4];
+    if (threadIdx.x == 0) tsh[3] = 0;
+    gemv_body<4, 2, 4, 256, true, 0, false, false, 64, false, true>(a, blockIdx.x, true, tsh);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long * o = a.ts + (size_t) blockIdx.x * 5;
+        o[0] = tsh[0]; o[1] = tsh[1]; o[2] = tsh[2]; o[3] = tsh[3] ? tsh[3] : tsh[2];
+        o[4] = __builtin_amdgcn_s_memrealtime();
+    }
+}
 // a whole 14336-wide row in one pass (tuning: SML_GEMV_NI=8)
 GEMV_KERNEL(4, 1, 8) GEMV_KERNEL(4, 2, 8)
 GEMV_KERNEL(2, 1, 8) GEMV_KERNEL(2, 2, 8) GEMV_KERNEL(3, 1, 8) GEMV_KERNEL(3, 2, 8)

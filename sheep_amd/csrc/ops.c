@@ -698,6 +698,38 @@ int sml_hip_matvec_swiglu_fused(const sml_hip_mat * gate, const sml_hip_mat * up
     return 0;
 }
 
+int sml_hip_gemv_timeline(const sml_hip_mat * const * mats, int ncopy, const int8_t * q, const float * scale,
+                          const int32_t * sums, float * y, int iters, unsigned long long * ts, int max_blocks) {
+    OP_BEGIN(-1);
+    if (!mats || ncopy < 1 || iters < 1 || !ts) hx_failf("gemv_timeline arguments");
+    const sml_hip_mat * m0 = mats[0];
+    if (m0->nbits != 4 || m0->k.rows % 8 || m0->cols % 256) hx_failf("the timeline GEMV takes Q4, rows in blocks of 8");
+    const int blocks = m0->k.rows / 8;                  // 4 waves of 2 rows
+    if (blocks > max_blocks) hx_failf("%d row blocks, room for %d", blocks, max_blocks);
+    unsigned long long * d = hx_malloc((size_t) blocks * 5 * 8);
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) { hipFree(d); longjmp(*outer, 1); }
+    hx.jb = &jb;
+    const size_t lds = ((size_t) m0->cols + 8u * (size_t) (m0->cols / 32) + 15u) / 16u * 16u;
+    for (int i = 0; i < iters; i++) {
+        const sml_hip_mat * m = mats[i % ncopy];
+        if (m->nbits != 4 || m->k.rows != m0->k.rows || m->cols != m0->cols) hx_failf("gemv_timeline: matrices differ");
+        sml_kgemv a;
+        memset(&a, 0, sizeof a);
+        a.m[0] = m->k;
+        a.m[0].y = y;
+        a.cols = m->cols; a.epi = SML_EPI_STORE; a.total_rows = m->k.rows;
+        a.q = q; a.scale = scale; a.sums = sums; a.ts = d;
+        hx_launch("sml_gemv_q4_r2_i4_ts", (unsigned) blocks, 1, 256, lds, 0, &a);
+    }
+    HX(hipMemcpy(ts, d, (size_t) blocks * 5 * 8, hipMemcpyDeviceToHost));
+    hx.jb = outer;
+    HX(hipFree(d));
+    HX_LEAVE();
+    return blocks;
+}
+
 int sml_hip_time_matvec(const sml_hip_mat * const * mats, int ncopy, const int8_t * q, const float * scale,
                         const int32_t * sums, float * y, int iters, float * ms_total) {
     OP_BEGIN(-1);
