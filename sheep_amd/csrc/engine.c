@@ -801,6 +801,7 @@ static void rows_alloc(void) {
     const size_t part_pb = R * (size_t) G.H * (size_t) ((G.n_ctx + 127) / 128) * (size_t) (G.hd + 2);
     if (part_pb > part) part = part_pb;
     G.mpart = dalloc(part * 4);
+    hx_kpart();                                     // the split-K products' buffer, before any capture
     G.kc_tab = dalloc(S * sizeof(void *));
     G.vc_tab = dalloc(S * sizeof(void *));
     HX(hipHostMalloc((void **) &G.mpin, 3 * S * 4, 0));
@@ -862,7 +863,7 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
         int32_t * uu[1] = { G.masum };
         pp[0] = pdev(y->perm_qkv[0]);
         op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
-        op_gemm(G.st, y->qkv->kdev, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
+        op_gemm(G.st, y->qkv->kdev, &y->qkv->k, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
                 G.mqkv, y->bias_qkv, NULL, regime);
         // the merge quantizes its output for the o product: per 32, or per
         // 256 in decode steps of an even head count (SML_MERGE_Q256=0 leaves
@@ -877,7 +878,7 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
             pp[0] = pdev(y->perm_o);
             op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, sb);
         }
-        op_gemm(G.st, y->o->kdev, 1, 0, y->o->nbits, G.E, (int) hq, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
+        op_gemm(G.st, y->o->kdev, &y->o->k, 1, 0, y->o->nbits, G.E, (int) hq, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
                 G.mx, NULL, G.mx, regime);
         if (y->moe) {
             op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 0, NULL, NULL, NULL, NULL, G.mxn, sb);
@@ -888,11 +889,12 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
         }
         pp[0] = pdev(y->perm_gu[0]);
         op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
-        op_gemm(G.st, y->gu_tab, 1, 1, y->gate->nbits, G.F, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mh,
+        const sml_kmat guk[2] = { y->gate->k, y->up->k };
+        op_gemm(G.st, y->gu_tab, guk, 1, 1, y->gate->nbits, G.F, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mh,
                 NULL, NULL, regime);
         pp[0] = pdev(y->perm_down);
         op_normq_rows(G.st, G.mh, NULL, NULL, G.eps, G.F, ns, 1, pp, qq, ss, uu, NULL, sb);
-        op_gemm(G.st, y->down->kdev, 1, 0, y->down->nbits, G.E, G.F, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
+        op_gemm(G.st, y->down->kdev, &y->down->k, 1, 0, y->down->nbits, G.E, G.F, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
                 G.mx, NULL, G.mx, regime);
     }
     if (!head) return;
@@ -901,7 +903,7 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
     float * ss[1] = { G.mas };
     int32_t * uu[1] = { G.masum };
     op_normq_rows(G.st, G.mx, NULL, G.out_norm, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
-    op_gemm(G.st, G.head->kdev, 1, 0, G.head->nbits, G.V, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mlog,
+    op_gemm(G.st, G.head->kdev, &G.head->k, 1, 0, G.head->nbits, G.V, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mlog,
             NULL, NULL, regime);
 }
 

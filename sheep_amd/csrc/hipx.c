@@ -50,10 +50,20 @@ void hx_init(int device) {
     HX(hipModuleLoadData(&hx.mod_ingest, sml_ingest_object));
     fn_n = 0;
     hx.ncu = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+    if (hx.kpart) {
+        void * old = hx.kpart;
+        hx.kpart = NULL;
+        HX(hipFree(old));
+    }
     hx.device = device;
     hx.inited = 1;
 }
 
+
+float * hx_kpart(void) {
+    if (!hx.kpart) HX(hipMalloc((void **) &hx.kpart, (size_t) HX_KPART * sizeof(float)));
+    return hx.kpart;
+}
 
 hipFunction_t hx_fn(const char * name) {
     for (int i = 0; i < fn_n; i++)

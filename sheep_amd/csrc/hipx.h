@@ -23,7 +23,14 @@ typedef struct {
     int       ncu;                // compute units of the device
     long      fail_after;         // test hook: fail the Nth HIP call from now (< 0: off)
     long      calls;              // HIP calls made through HX() so far
+    float   * kpart;              // split-K GEMM partial products (HX_KPART floats on the device),
+                                  // shared by every launch: one stream at a time
 } hx_state;
+
+#define HX_KPART (1 << 20)
+// the split-K partial buffer, allocated at its first use (the engine asks for
+// it at load, before any graph capture)
+float * hx_kpart(void);
 
 extern hx_state hx;
 

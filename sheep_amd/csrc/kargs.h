@@ -345,7 +345,22 @@ typedef struct {
     const float * bias;           // [rows] added to each row (plain GEMM only), or NULL
     const float * resid;          // [ngroups][mmax][rows]: y = resid + (W.a + bias), may alias y; or NULL
     int mlo;                      // VALU kernel: groups of mlo rows or fewer are another launch's
+    float * part;                 // split-K MFMA kernels: [ks][m_all][rows] partial products
+    // one group (count NULL): its matrices' descriptors by value (inl = 1), so
+    // the MFMA kernels address the weights from the kernel arguments instead
+    // of first reading mats[] from device memory
+    int inl;
+    sml_kmat m0[2];
 } sml_kgemm;
+
+// Split-K sums: y[r][c] = resid[r][c] + (((part[0][r][c] + part[1][r][c]) + ...) + bias[c])
+typedef struct {
+    const float * part;           // [ks][m][rows]
+    const float * bias;           // [rows] or NULL
+    const float * resid;          // [m][rows] or NULL (may alias y)
+    float * y;                    // [m][rows]
+    int ks, m, rows;
+} sml_kksum;
 
 // out[t] = sum over j of w[t][j] * y[sel[t][j]][slot[t][j]], in choice order,
 // then + sg[t] * ysh[t] (the shared expert) when ysh is not NULL.

@@ -1024,6 +1024,22 @@ extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a
     // row blockIdx.y of a batch (every pointer strided by its row)
     const size_t bo = (size_t) blockIdx.y * n, bg = (size_t) blockIdx.y * (n / 32);
     const float * x = a.x + bo;
+    const int j = blockIdx.x * 256 + tid;           // element (group j/32) of every output
+    const bool ok = j < n;                          // whole groups of 32 (n % 32 == 0)
+    // every output's gathered value and norm weight are asked for first: they
+    // need only the permutation, not the sum of squares, so their two
+    // dependent loads overlap the row's read and its reduction
+    float xv[3], wv[3];
+    #pragma unroll
+    for (int o = 0; o < 3; o++) {
+        xv[o] = 0.0f;
+        wv[o] = 1.0f;
+        if (o < a.nout && ok) {
+            const int src = a.perm[o] ? a.perm[o][j] : j;
+            xv[o] = x[src];
+            if (a.norm_w) wv[o] = a.norm_w[src];
+        }
+    }
     float sc = 1.0f;
     if (a.norm_w) {
         double ss = 0.0;
@@ -1046,12 +1062,11 @@ extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a
         }
         sc = 1.0f / sqrtf(msq + a.eps);
     }
-    const int j = blockIdx.x * 256 + tid;           // element (group j/32) of every output
-    const bool ok = j < n;                          // whole groups of 32 (n % 32 == 0)
     const int l32 = tid & 31, g = j >> 5;
-    for (int o = 0; o < a.nout; o++) {
-        const int src = ok ? (a.perm[o] ? a.perm[o][j] : j) : 0;
-        const float v = ok ? (a.norm_w ? x[src] * sc * a.norm_w[src] : x[src]) : 0.0f;
+    #pragma unroll
+    for (int o = 0; o < 3; o++) {
+        if (o >= a.nout) break;
+        const float v = a.norm_w ? xv[o] * sc * wv[o] : xv[o];
         float amax;
         if (a.per256) {
             // double-buffered by output: the next write to this slot follows
@@ -1658,6 +1673,7 @@ extern "C" __global__ __launch_bounds__(128) void sml_ropekv_d64(const sml_kattn
 
 #define ATTN_KERNEL(R) \
     extern "C" __global__ __launch_bounds__(256) void sml_attn_r##R(const sml_kattn a) { attn_body<R, 4, false>(a); } \
+    extern "C" __global__ __launch_bounds__(256) void sml_attn_s64_r##R(const sml_kattn a) { attn_body<R, 4, false, 64>(a); } \
     extern "C" __global__ __launch_bounds__(512) void sml_attn8_r##R(const sml_kattn a) { attn_body<R, 8, false>(a); } \
     extern "C" __global__ __launch_bounds__(512) void sml_attnc8_r##R(const sml_kattn a) { attn_body<R, 8, true>(a); } \
     extern "C" __global__ __launch_bounds__(512) void sml_attn8_s32_r##R(const sml_kattn a) { attn_body<R, 8, false, 32>(a); } \
@@ -1674,6 +1690,206 @@ ATTN_KERNEL(1) ATTN_KERNEL(2) ATTN_KERNEL(3) ATTN_KERNEL(4) ATTN_KERNEL(5) ATTN_
     extern "C" __global__ __launch_bounds__(512) void sml_attnc8_s64_d64_r##R(const sml_kattn a) { attn_body<R, 8, true, 64, 64>(a); }
 ATTN_KERNEL_D64(1) ATTN_KERNEL_D64(2) ATTN_KERNEL_D64(3) ATTN_KERNEL_D64(4) ATTN_KERNEL_D64(5) ATTN_KERNEL_D64(6)
 ATTN_KERNEL_D64(7) ATTN_KERNEL_D64(8)
+
+// Batched decode attention (sequences of one new position each, head_dim
+// 128, 4 waves, splits of 128 positions): attn_body<REP, 4>'s arithmetic
+// value for value, with its per-workgroup inputs spread over the threads.
+// The one-entry body loads the REP query heads, k, v and the RoPE rows whole
+// into every position lane (64 + 8 REP registers while the tile's 64
+// arrive); here thread t holds dims t%64 and t%64 + 64 of query head t/64
+// (and t/64 + 4), the rotation's own pair, wave 0 the pair of k and wave 1
+// that of v. The rotated heads and the new position's fp16 k and v meet in
+// LDS, then every lane takes its 8 dims of each (118 registers at REP 4
+// against 191). (Two to eight consecutive splits a workgroup, the next
+// split's K and V asked for as each set of registers frees, measured slower:
+// 203 registers, 16 sequences at ~1k positions 3.07 -> 3.28-3.45 ms a step.)
+template <int REP>
+__device__ __forceinline__ void attnb_body(const sml_kattn & a) {
+    constexpr int D = HD, LP = 16, NW = 4, PS = 64 * NW / LP, CH = ATTN_CHUNK, PPL = CH / PS;
+    constexpr int QR = (REP + NW - 1) / NW;                     // query heads per thread in the prologue
+    __shared__ float red[NW][REP][D];
+    __shared__ float wm[NW][REP], wl[NW][REP];
+    __shared__ __align__(16) float qs[REP][D];
+    __shared__ __align__(16) uint16_t kvn[2][D];
+    // grid (kv head, split, sequence): the kv heads of one split run side by
+    // side, so together they read whole cache rows (n_kv x 256 bytes a
+    // position)
+    const int kh = blockIdx.x, qh0 = kh * REP, split = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+    const int wave = tid >> 6, grp = tid / LP, l16 = tid % LP, kvd = a.n_kv * D;
+    const int pos = a.pos[b], T = pos + 1, t0 = split * CH, t1 = min(T, t0 + CH);
+    float * blk = a.part + (size_t) b * a.n_head * a.nsplit * (D + 2);
+    float * po = blk + (size_t) qh0 * a.nsplit * D;
+    float2 * pml = (float2 *) (blk + (size_t) a.n_head * a.nsplit * D) + (size_t) qh0 * a.nsplit;
+    // a split past the position writes empty partials only
+    if (t0 >= T) {
+        if (tid < REP) pml[(size_t) tid * a.nsplit + split] = make_float2(-INFINITY, 0.0f);
+        return;
+    }
+    GLOBAL uint16_t * kcache = (GLOBAL uint16_t *) (a.kc_slots ? a.kc_slots[a.slot[b]] + a.layer_off : a.kcache);
+    GLOBAL uint16_t * vcache = (GLOBAL uint16_t *) (a.vc_slots ? a.vc_slots[a.slot[b]] + a.layer_off : a.vcache);
+    // the prologue's inputs first (loads return in order: the rotation runs
+    // while the tile arrives)
+    const int d = tid & 63;
+    const float * qkv = a.q + (size_t) b * a.qkv_stride;
+    const float c = a.cos_t[(size_t) pos * (D / 2) + d], sn = a.sin_t[(size_t) pos * (D / 2) + d];
+    float x0[QR], x1[QR];
+    #pragma unroll
+    for (int r = 0; r < QR; r++) {
+        const int j = wave + NW * r < REP ? wave + NW * r : 0;
+        x0[r] = qkv[(size_t) (qh0 + j) * D + d];
+        x1[r] = qkv[(size_t) (qh0 + j) * D + d + 64];
+    }
+    const float * kv = (wave == 0 ? a.k : a.v) + (size_t) b * a.qkv_stride + (size_t) kh * D;
+    float y0 = 0.0f, y1 = 0.0f;
+    if (wave < 2) { y0 = kv[d]; y1 = kv[d + 64]; }
+    // the tile: positions t0 + grp + PS*i, clamped into the split's range
+    // (the clamped ones are masked)
+    v4u kw[PPL], vw[PPL];
+    #pragma unroll
+    for (int i = 0; i < PPL; i++) {
+        int t = t0 + grp + PS * i;
+        t = t < t1 ? t : t0;
+        kw[i] = __builtin_nontemporal_load((const GLOBAL v4u *) (kcache + (size_t) t * kvd + (size_t) kh * D + l16 * 8));
+    }
+    #pragma unroll
+    for (int i = 0; i < PPL; i++) {
+        int t = t0 + grp + PS * i;
+        t = t < t1 ? t : t0;
+        vw[i] = __builtin_nontemporal_load((const GLOBAL v4u *) (vcache + (size_t) t * kvd + (size_t) kh * D + l16 * 8));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // rope8's pair rule: x0*c - x1*s = fma(x0, c, -(x1*s)), x0*s + x1*c = fma(x0, s, x1*c)
+    #pragma unroll
+    for (int r = 0; r < QR; r++) {
+        const int j = wave + NW * r;
+        if (j < REP) {
+            qs[j][d] = __builtin_fmaf(x0[r], c, -(x1[r] * sn));
+            qs[j][d + 64] = __builtin_fmaf(x0[r], sn, x1[r] * c);
+        }
+    }
+    const bool here = t0 <= pos && pos < t1;
+    if (wave == 0) {
+        // rounded to fp32, then to fp16, as the one-entry body does: the empty
+        // asm keeps the compiler from fusing each fma with its conversion
+        // (v_fma_mixlo_f16 rounds once, to fp16, and differs at the ties)
+        float r0 = __builtin_fmaf(y0, c, -(y1 * sn)), r1 = __builtin_fmaf(y0, sn, y1 * c);
+        asm volatile("" : "+v"(r0), "+v"(r1));
+        const uint16_t k0 = f2h(r0), k1 = f2h(r1);
+        kvn[0][d] = k0;
+        kvn[0][d + 64] = k1;
+        if (here) {
+            kcache[(size_t) pos * kvd + (size_t) kh * D + d] = k0;
+            kcache[(size_t) pos * kvd + (size_t) kh * D + d + 64] = k1;
+        }
+    } else if (wave == 1) {
+        const uint16_t v0 = f2h(y0), v1 = f2h(y1);
+        kvn[1][d] = v0;
+        kvn[1][d + 64] = v1;
+        if (here) {
+            vcache[(size_t) pos * kvd + (size_t) kh * D + d] = v0;
+            vcache[(size_t) pos * kvd + (size_t) kh * D + d + 64] = v1;
+        }
+    }
+    __syncthreads();
+    float q[REP][8];
+    #pragma unroll
+    for (int j = 0; j < REP; j++) {
+        const float4 u = *(const float4 *) &qs[j][l16 * 8], w = *(const float4 *) &qs[j][l16 * 8 + 4];
+        q[j][0] = u.x; q[j][1] = u.y; q[j][2] = u.z; q[j][3] = u.w;
+        q[j][4] = w.x; q[j][5] = w.y; q[j][6] = w.z; q[j][7] = w.w;
+    }
+    const float sl = a.inv * 1.44269504088896341f;
+    // the new position's k and v in place of the (older) cache bytes the
+    // tile read there
+    if (here) {
+        const v4u knew = *(const v4u *) &kvn[0][l16 * 8], vnew = *(const v4u *) &kvn[1][l16 * 8];
+        #pragma unroll
+        for (int i = 0; i < PPL; i++)
+            if (t0 + grp + PS * i == pos) { kw[i] = knew; vw[i] = vnew; }
+    }
+    float sc[PPL][REP];
+    #pragma unroll
+    for (int i = 0; i < PPL; i++) {
+        const int t = t0 + grp + PS * i;
+        float kf[8];
+        unpack_h8(kw[i], kf);
+        #pragma unroll
+        for (int j = 0; j < REP; j++) {
+            float p = 0.0f;
+            #pragma unroll
+            for (int e = 0; e < 8; e++) p += q[j][e] * kf[e];
+            p = sum16(p);
+            sc[i][j] = t < t1 ? p * sl : -INFINITY;
+        }
+    }
+    float m[REP], l[REP], xs[REP];
+    #pragma unroll
+    for (int j = 0; j < REP; j++) {
+        float x = sc[0][j];
+        #pragma unroll
+        for (int i = 1; i < PPL; i++) x = fmaxf(x, sc[i][j]);
+        xs[j] = x;
+    }
+    wave_heads<REP>(xs, m, true);
+    #pragma unroll
+    for (int j = 0; j < REP; j++) {
+        const float mj = m[j] == -INFINITY ? 0.0f : m[j];
+        float ls = 0.0f;
+        #pragma unroll
+        for (int i = 0; i < PPL; i++) {
+            const float p = __builtin_amdgcn_exp2f(sc[i][j] - mj);
+            sc[i][j] = p;
+            ls += p;
+        }
+        xs[j] = ls;
+    }
+    wave_heads<REP>(xs, l, false);
+    float acc[REP][8];
+    #pragma unroll
+    for (int j = 0; j < REP; j++)
+        #pragma unroll
+        for (int e = 0; e < 8; e++) acc[j][e] = 0.0f;
+    #pragma unroll
+    for (int i = 0; i < PPL; i++) {
+        float vf[8];
+        unpack_h8(vw[i], vf);
+        #pragma unroll
+        for (int j = 0; j < REP; j++)
+            #pragma unroll
+            for (int e = 0; e < 8; e++) acc[j][e] += sc[i][j] * vf[e];
+    }
+    const int row = (tid >> 4) & 3;
+    #pragma unroll
+    for (int j = 0; j < REP; j++)
+        #pragma unroll
+        for (int h = 0; h < 2; h++)
+            red[wave][j][l16 * 8 + 4 * h + row] =
+                rows_sum4(acc[j][4 * h], acc[j][4 * h + 1], acc[j][4 * h + 2], acc[j][4 * h + 3]);
+    if ((tid & 63) == 0) {
+        #pragma unroll
+        for (int j = 0; j < REP; j++) { wm[wave][j] = m[j]; wl[wave][j] = l[j]; }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < REP * D; idx += 64 * NW) {
+        const int j = idx / D, dd = idx % D;
+        float M = wm[0][j];
+        #pragma unroll
+        for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w][j]);
+        float o = 0.0f, L = 0.0f;
+        #pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float e = __builtin_amdgcn_exp2f(wm[w][j] - M);
+            o += e * red[w][j][dd];
+            L += e * wl[w][j];
+        }
+        po[((size_t) j * a.nsplit + split) * D + dd] = o;
+        if (dd == 0) pml[(size_t) j * a.nsplit + split] = make_float2(M, L);
+    }
+}
+#define ATTNB_KERNEL(R) \
+    extern "C" __global__ __launch_bounds__(256) void sml_attnb_r##R(const sml_kattn a) { attnb_body<R>(a); }
+ATTNB_KERNEL(1) ATTNB_KERNEL(2) ATTNB_KERNEL(3) ATTNB_KERNEL(4) ATTNB_KERNEL(5) ATTNB_KERNEL(6) ATTNB_KERNEL(7)
+ATTNB_KERNEL(8)
 
 // ---------------------------------------------------------------- prompt attention, a wave per position
 //
@@ -3494,7 +3710,7 @@ __device__ __forceinline__ void xslice(const v4u v, v2u & x, v2u & y) {
     y = v2u{(unsigned) p[1], (unsigned) q[1]};
 }
 
-template <bool SW, bool SB, int RB, int NW, bool PS = false, bool TL = false>
+template <bool SW, bool SB, int RB, int NW, bool PS = false, bool TL = false, int KS = 1>
 __device__ void mgemm_q4_body(const sml_kgemm & a) {
     typedef long v1l;
     constexpr int NM = SW ? 2 : 1, NACC = NM * RB * 4;
@@ -3508,11 +3724,16 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
     // PS (persistent): the workgroup walks row tiles blockIdx.x, +gridDim.x,
     // ... and keeps the activation operands of its superblocks in registers
     // across them (at most 2 superblocks per wave); otherwise one tile
+    // KS > 1 (split-K, persistent): workgroup g takes the input slice g % KS
+    // (nsb / KS superblocks) of row tiles g / KS, + gridDim.x / KS, ... and
+    // writes its products to a.part[slice]; sml_gemm_ksum adds the slices
+    const int ks = KS > 1 ? (int) blockIdx.x % KS : 0;
     const int ntile = (a.rows + 16 * RB - 1) / (16 * RB);
-    int tile = blockIdx.x;
+    int tile = KS > 1 ? (int) blockIdx.x / KS : (int) blockIdx.x;
     int rb0 = tile * (16 * RB);
-    const int s0 = wave * nsb / NW, s1 = (wave + 1) * nsb / NW;   // this wave's superblocks
-    const int spw = (nsb + NW - 1) / NW;                           // region size, in superblocks
+    const int nsbs = nsb / KS, sb0 = ks * nsbs;
+    const int s0 = sb0 + wave * nsbs / NW, s1 = sb0 + (wave + 1) * nsbs / NW;   // this wave's superblocks
+    const int spw = (nsbs + NW - 1) / NW;                          // region size, in superblocks
     const int gw = (s1 - s0) * 8, gb = s0 * 8;
     const sml_kmat * mt = a.mats + (size_t) e * NM;
     const size_t abase = (size_t) e * a.mmax;
@@ -3525,7 +3746,10 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
     const uint8_t * fqb[NM];
     const uint8_t * fdb[NM];
     #pragma unroll
-    for (int k = 0; k < NM; k++) { plane[k] = mt[k].plane[0]; fqb[k] = mt[k].sqmq; fdb[k] = (const uint8_t *) mt[k].sdmd; }
+    for (int k = 0; k < NM; k++) {
+        if (a.inl) { plane[k] = a.m0[k].plane[0]; fqb[k] = a.m0[k].sqmq; fdb[k] = (const uint8_t *) a.m0[k].sdmd; }
+        else { plane[k] = mt[k].plane[0]; fqb[k] = mt[k].sqmq; fdb[k] = (const uint8_t *) mt[k].sdmd; }
+    }
     const uint32_t rowb = (uint32_t) n / 2;
     uint32_t boff0[RB], fqo[RB], fdo[RB];
     // TL: the matrices' tiled copies (sml_tile_q4): the block's tile row; the
@@ -3543,7 +3767,8 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             if constexpr (TL) {
                 const int blk = min(r0 / 16 + bk, nbl - 1);
                 #pragma unroll
-                for (int k = 0; k < NM; k++) tb[k][bk] = mt[k].tiled + (size_t) blk * nsb * SML_TILE_Q4;
+                for (int k = 0; k < NM; k++)
+                    tb[k][bk] = (a.inl ? a.m0[k].tiled : mt[k].tiled) + (size_t) blk * nsb * SML_TILE_Q4;
             }
         }
     };
@@ -3736,27 +3961,6 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             }
         }
     };
-    // persistent: the wave's (at most 2) superblocks of activation operands,
-    // loaded once for every tile, and put in place before the weights are
-    // asked for (measured faster than issuing the weights first: 16-row
-    // SwiGLU 2x14336x4096 per-256 24.8 against 25.4 us, 6144x4096 10.0
-    // against 10.7)
-    Batch A, B;
-    if constexpr (PS) {
-        #pragma unroll
-        for (int k = 0; k < 2; k++) {
-            v4u aq[4];
-            const int bt = s0 + k < s1 ? s0 + k : s0;
-            const int8_t * qp = qrow + (size_t) (8 * bt) * 32;
-            #pragma unroll
-            for (int u = 0; u < 4; u++) aq[u] = *(const v4u *) (qp + u * 64);
-            act_operands(aq, pav[k]);
-        }
-    }
-    // two superblocks in flight, then the activation rows' group data: their
-    // latencies overlap
-    if (s0 < s1) load(A, s0);
-    if (s0 + 1 < s1) load(B, s0 + 1);
     // stage this wave's share, [group][row]; rows past m read row 0 (their
     // outputs are never stored, and no output row reads another's data)
     // four entries per lane per round
@@ -3789,67 +3993,109 @@ __device__ void mgemm_q4_body(const sml_kgemm & a) {
             }
         }
     };
-    stage_ld(lane);
-    stage_st(lane);
-    for (int base = lane + 256; base < gw * 16; base += 256) {
-        stage_ld(base);
-        stage_st(base);
-    }
-    for (;;) {
-    for (int bt = s0; bt < s1; bt += 2) {
-        compute(A, bt);
-        if (bt + 2 < s1) load(A, bt + 2);
-        if (bt + 1 >= s1) break;
-        compute(B, bt + 1);
-        if (bt + 3 < s1) load(B, bt + 3);
-    }
-    const int next = tile + (PS ? (int) gridDim.x : ntile);
-    if constexpr (PS) {
-        // the next tile's weights load while this one's sums meet
-        if (next < ntile) {
-            set_tile(next * 16 * RB);
-            if (s0 < s1) load(A, s0);
-            if (s0 + 1 < s1) load(B, s0 + 1);
+    auto stage = [&]() {
+        stage_ld(lane);
+        stage_st(lane);
+        for (int base = lane + 256; base < gw * 16; base += 256) {
+            stage_ld(base);
+            stage_st(base);
         }
-    }
-    __syncthreads();                                  // every wave is past its staging region / the last tile's sums
+    };
+    // the waves' sums of the tile at rows r0.. meet in LDS, in wave order
     // [NW][NACC][64]: over the staging regions, or (PS) after them
     float * red = (float *) (lds + (PS ? (size_t) NW * spw * (SB ? 576 : 1024) : 0));
-    #pragma unroll
-    for (int k = 0; k < NM; k++)
+    auto epilogue = [&](int r0) {
+        __syncthreads();                              // every wave is past its staging region / the last tile's sums
         #pragma unroll
-        for (int bk = 0; bk < RB; bk++)
+        for (int k = 0; k < NM; k++)
             #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                red[(wave * NACC + (k * RB + bk) * 4 + r) * 64 + lane] = acc[k][bk][r];
-                acc[k][bk][r] = 0.0f;
+            for (int bk = 0; bk < RB; bk++)
+                #pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    red[(wave * NACC + (k * RB + bk) * 4 + r) * 64 + lane] = acc[k][bk][r];
+                    acc[k][bk][r] = 0.0f;
+                }
+        __syncthreads();
+        for (int o = tid; o < RB * 256; o += 64 * NW) {
+            const int bk = o >> 8, r = (o >> 6) & 3, l = o & 63;
+            const int row = r0 + bk * 16 + (l & 15), mr = 4 * (l >> 4) + r;
+            if (row >= a.rows || mr >= m) continue;
+            float t[NM];
+            #pragma unroll
+            for (int k = 0; k < NM; k++) {
+                float sum = 0.0f;
+                #pragma unroll
+                for (int w = 0; w < NW; w++) sum += red[(w * NACC + (k * RB + bk) * 4 + r) * 64 + l];
+                t[k] = sum;
             }
-    __syncthreads();
-    for (int o = tid; o < RB * 256; o += 64 * NW) {
-        const int bk = o >> 8, r = (o >> 6) & 3, l = o & 63;
-        const int row = rb0 + bk * 16 + (l & 15), mr = 4 * (l >> 4) + r;
-        if (row >= a.rows || mr >= m) continue;
-        float t[NM];
+            if constexpr (KS > 1) {
+                a.part[((size_t) ks * a.m_all + mr) * a.rows + row] = t[0];
+                continue;
+            }
+            float * y = a.y + (abase + mr) * a.rows;
+            if constexpr (SW) {
+                y[row] = silu_ref(t[0]) * t[1];                          // sml/sml-run.c:416-426
+            } else {
+                float v = t[0];
+                if (a.bias) v += a.bias[row];
+                if (a.resid) v = a.resid[(abase + mr) * a.rows + row] + v;
+                y[row] = v;
+            }
+        }
+    };
+    if constexpr (PS) {
+        // persistent: the wave's (at most 2) superblocks of activation
+        // operands, loaded once for every tile and put in place before the
+        // weights are asked for (measured faster than issuing the weights
+        // first: 16-row SwiGLU 2x14336x4096 per-256 24.8 against 25.4 us,
+        // 6144x4096 10.0 against 10.7; and than keeping two tiles of weights
+        // in flight, the next tile's asked for before this one's compute:
+        // SwiGLU 22.5 against 23.7 us, at 234 registers against 203)
+        const int stride = (int) gridDim.x / KS;
         #pragma unroll
-        for (int k = 0; k < NM; k++) {
-            float sum = 0.0f;
+        for (int k = 0; k < 2; k++) {
+            v4u aq[4];
+            const int bt = s0 + k < s1 ? s0 + k : s0;
+            const int8_t * qp = qrow + (size_t) (8 * bt) * 32;
             #pragma unroll
-            for (int w = 0; w < NW; w++) sum += red[(w * NACC + (k * RB + bk) * 4 + r) * 64 + l];
-            t[k] = sum;
+            for (int u = 0; u < 4; u++) aq[u] = *(const v4u *) (qp + u * 64);
+            act_operands(aq, pav[k]);
         }
-        float * y = a.y + (abase + mr) * a.rows;
-        if constexpr (SW) {
-            y[row] = silu_ref(t[0]) * t[1];                              // sml/sml-run.c:416-426
-        } else {
-            float v = t[0];
-            if (a.bias) v += a.bias[row];
-            if (a.resid) v = a.resid[(abase + mr) * a.rows + row] + v;
-            y[row] = v;
+        Batch A, B;
+        if (s0 < s1) load(A, s0);
+        if (s0 + 1 < s1) load(B, s0 + 1);
+        stage();
+        for (;;) {
+            if (s0 < s1) compute(A, s0);
+            if (s0 + 1 < s1) compute(B, s0 + 1);
+            // the next tile's weights load while this one's sums meet
+            const int next = tile + stride;
+            if (next < ntile) {
+                set_tile(next * 16 * RB);
+                if (s0 < s1) load(A, s0);
+                if (s0 + 1 < s1) load(B, s0 + 1);
+            }
+            epilogue(rb0);
+            if (next >= ntile) break;
+            tile = next;
+            rb0 = tile * (16 * RB);
         }
-    }
-    if (!PS || next >= ntile) break;
-    tile = next;
-    rb0 = tile * (16 * RB);
+    } else {
+        // one tile: two superblocks in flight, then the activation rows'
+        // group data (their latencies overlap), then the wave's superblocks
+        // two at a time
+        Batch A, B;
+        if (s0 < s1) load(A, s0);
+        if (s0 + 1 < s1) load(B, s0 + 1);
+        stage();
+        for (int bt = s0; bt < s1; bt += 2) {
+            compute(A, bt);
+            if (bt + 2 < s1) load(A, bt + 2);
+            if (bt + 1 >= s1) break;
+            compute(B, bt + 1);
+            if (bt + 3 < s1) load(B, bt + 3);
+        }
+        epilogue(rb0);
     }
 }
 
@@ -3878,6 +4124,27 @@ MGEMM_KERNEL(1, 4, true, _t) MGEMM_KERNEL(2, 4, true, _t) MGEMM_KERNEL(1, 8, tru
     extern "C" __global__ __launch_bounds__(64 * NW) void sml_mgemm_q4_s_sb_r##RB##_w##NW##_p##SUF(const sml_kgemm a) { \
         mgemm_q4_body<true, true, RB, NW, true, TL>(a); }
 MGEMM_KERNEL_P(1, 8, false, ) MGEMM_KERNEL_P(1, 8, true, _t)
+// Split-K persistent forms (_k4): inputs of 17 to 64 superblocks (4352 to
+// 16384 wide) in 4 slices, each wave holding at most 2 superblocks of its
+// slice; plain products only (the SwiGLU needs whole sums)
+#define MGEMM_KERNEL_K(TL, SUF)                                                                                \
+    extern "C" __global__ __launch_bounds__(512) void sml_mgemm_q4_r1_w8_p_k4##SUF(const sml_kgemm a) {       \
+        mgemm_q4_body<false, false, 1, 8, true, TL, 4>(a); }                                                   \
+    extern "C" __global__ __launch_bounds__(512) void sml_mgemm_q4_sb_r1_w8_p_k4##SUF(const sml_kgemm a) {    \
+        mgemm_q4_body<false, true, 1, 8, true, TL, 4>(a); }
+MGEMM_KERNEL_K(false, ) MGEMM_KERNEL_K(true, _t)
+
+// The split-K slices added in slice order, then the bias and the residual
+// (the one-launch epilogue's order: v = sum + bias; y = resid + v)
+extern "C" __global__ __launch_bounds__(256) void sml_gemm_ksum(const sml_kksum a) {
+    const size_t i = (size_t) blockIdx.x * 256 + threadIdx.x, n = (size_t) a.m * a.rows;
+    if (i >= n) return;
+    float v = a.part[i];
+    for (int k = 1; k < a.ks; k++) v += a.part[(size_t) k * n + i];
+    if (a.bias) v += a.bias[i % a.rows];
+    if (a.resid) v = a.resid[i] + v;
+    a.y[i] = v;
+}
 
 
 

@@ -446,6 +446,7 @@ void op_normq_rows(hipStream_t st, float * x, const float * resid, const float *
                    int32_t * const * sums, float * normed, int per256) {
     if (rows < 1 || rows > 65535) hx_failf("normq of %d rows", rows);
     if (n <= 0 || n % 32 || n > 16384) hx_failf("normq width %d not supported", n);
+    if (nout < 0 || nout > 3) hx_failf("normq of %d outputs (at most 3)", nout);
     sml_knormq a;
     memset(&a, 0, sizeof a);
     a.x = x; a.resid = resid; a.norm_w = w; a.eps = eps; a.n = n; a.nout = nout;
@@ -898,7 +899,8 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     const int aw = env_int("SML_ATTN_WAVES", nseq >= 4 && !exact ? 4 : 8) == 4 ? 4 : 8;
     // the 8-wave kernels split as decoding does (attn_split); the 4-wave and
     // wave-per-position kernels run splits of 128
-    const int ch = causal == 2 || (causal == 0 && aw == 4) || c2_d64 ? ATTN_CHUNK : attn_split(n_kv, n_ctx, hd);
+    const int bch = env_int("SML_ATTN_BCH", ATTN_CHUNK) == 64 && hd == 128 ? 64 : ATTN_CHUNK;
+    const int ch = causal == 2 || c2_d64 ? ATTN_CHUNK : causal == 0 && aw == 4 ? bch : attn_split(n_kv, n_ctx, hd);
     const int ns = (n_pos + ch - 1) / ch;             // splits past n_pos: not launched
     sml_kattn a;
     memset(&a, 0, sizeof a);
@@ -953,9 +955,17 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
     }
     const int nt = causal ? 512 : 64 * aw;
     attn_name(name, sizeof name, a.tpw > 1 || causal ? "sml_attnc8" : aw == 4 ? "sml_attn" : "sml_attn8",
-              a.tpw > 1 || causal || aw != 4 ? ch : ATTN_CHUNK, hd, n_head / n_kv);
-    hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) ((nseq + a.tpw - 1) / a.tpw), (unsigned) nt, 0,
-               st, &a);
+              ch, hd, n_head / n_kv);
+    // the 4-wave decode split with its inputs spread over the workgroup
+    // (sml_attnb: the same values, half the registers); SML_ATTNB=0 keeps
+    // the one-entry body
+    if (!causal && aw == 4 && hd == 128 && ch == ATTN_CHUNK && env_int("SML_ATTNB", 1)) {
+        snprintf(name, sizeof name, "sml_attnb_r%d", n_head / n_kv);
+        hx_launch3(name, (unsigned) n_kv, (unsigned) ns, (unsigned) nseq, (unsigned) nt, 0, st, &a);
+    } else {
+        hx_launch3(name, (unsigned) ns, (unsigned) n_kv, (unsigned) ((nseq + a.tpw - 1) / a.tpw), (unsigned) nt, 0,
+                   st, &a);
+    }
     if (q_out && q256) hx_launch3("sml_attn_merge_sb", (unsigned) n_head / 2, 1, (unsigned) nseq, 256, 0, st, &a);
     else hx_launch3(hd == 64 ? "sml_attn_merge_d64" : "sml_attn_merge", (unsigned) n_head, 1, (unsigned) nseq,
                     (unsigned) hd, 0, st, &a);
@@ -1381,7 +1391,7 @@ int gemm_exact(int regime, int m_all) {
 #define PGEMM_LDS (2 * (128 * 144 + PGEMM_BM * 272 + PGEMM_BM * 8))
 #define GEMM_MAX_ROWS 65536
 
-void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
+void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
              const int32_t * sums, float * y, const float * bias, const float * resid, int regime) {
     const int per256 = regime == GEMM_PER256;
@@ -1407,7 +1417,7 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
         const int ng = cols / 32;
         for (int s = 0; s < m_all; s += 16) {
             const int k = m_all - s < 16 ? m_all - s : 16;
-            op_gemm(st, tab, 1, swiglu, nbits, rows, cols, NULL, k, gemm_mt(k), k, q + (size_t) s * cols,
+            op_gemm(st, tab, hk, 1, swiglu, nbits, rows, cols, NULL, k, gemm_mt(k), k, q + (size_t) s * cols,
                     scale + (size_t) s * ng, sums + (size_t) s * ng, y + (size_t) s * rows, bias,
                     resid ? resid + (size_t) s * rows : NULL, regime);
         }
@@ -1420,6 +1430,11 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
     a.mats = tab; a.nmat = swiglu ? 2 : 1; a.cols = cols; a.rows = rows;
     a.count = count; a.m_all = m_all; a.mmax = mmax;
     a.q = q; a.scale = scale; a.sums = sums; a.y = y; a.bias = bias; a.resid = resid;
+    if (hk && ngroups == 1 && !count) {
+        a.inl = 1;
+        a.m0[0] = hk[0];
+        if (swiglu) a.m0[1] = hk[1];
+    }
     char name[48];
     // Q4 with more than 8 activation rows runs on MFMA (measured faster
     // there; below, the VALU dot4 kernel wins), with the integer superblock
@@ -1439,9 +1454,20 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
         const int fr = env_int("SML_MGEMM_RB", 0);
         if (fr == 1 || fr == 2) rb = fr;
         const int nw = env_int("SML_MGEMM_NW", 8) == 4 ? 4 : 8;
+        // inputs too wide for the persistent form (more than 2 superblocks a
+        // wave) split into 4 slices of at most 2 a wave: each workgroup then
+        // holds one slice's activation operands for all its row tiles instead
+        // of reading the whole rows again per tile, and sml_gemm_ksum adds
+        // the slices with the bias and the residual. SML_MGEMM_KS=1 keeps one
+        // tile per workgroup over the whole input.
+        int kslices = 1;
+        if (!swiglu && ngroups == 1 && nw == 8 && rb == 1 && nsb0 > 2 * nw && nsb0 % 4 == 0 && nsb0 / 4 <= 2 * nw &&
+            (size_t) 4 * (size_t) m_all * (size_t) rows <= HX_KPART && env_int("SML_MGEMM_KS", 4) == 4 &&
+            env_int("SML_MGEMM_PS", 1))
+            kslices = 4;
         // LDS: each wave's share of the activation group data, then the
         // waves' partial sums (the same memory, after a barrier)
-        const int nsb = cols / 256, spw = (nsb + nw - 1) / nw;
+        const int nsb = cols / 256 / kslices, spw = (nsb + nw - 1) / nw;
         const size_t stage = (size_t) nw * spw * (per256 ? 576 : 1024);
         const size_t red = (size_t) nw * (swiglu ? 2 : 1) * rb * 4 * 64 * 4;
         const int ntile = (rows + 16 * rb - 1) / (16 * rb);
@@ -1458,14 +1484,21 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
         if (lds <= 65536) {
             unsigned grid = (unsigned) ntile;
             if (ps) {
-                int cap = env_int("SML_MGEMM_PWG", hx.ncu);
+                // the cap counts workgroups of every slice
+                int cap = env_int("SML_MGEMM_PWG", hx.ncu) / kslices;
                 if (cap < 1) cap = 1;
                 const int per = (ntile + cap - 1) / cap;
-                grid = (unsigned) ((ntile + per - 1) / per);
+                grid = (unsigned) ((ntile + per - 1) / per * kslices);
             }
-            snprintf(name, sizeof name, "sml_mgemm_q4%s%s_r%d_w%d%s%s", swiglu ? "_s" : "", per256 ? "_sb" : "", rb, nw,
-                     ps ? "_p" : "", tiled_on() ? "_t" : "");
+            if (kslices > 1) a.part = hx_kpart();
+            snprintf(name, sizeof name, "sml_mgemm_q4%s%s_r%d_w%d%s%s%s", swiglu ? "_s" : "", per256 ? "_sb" : "", rb, nw,
+                     ps ? "_p" : "", kslices > 1 ? "_k4" : "", tiled_on() ? "_t" : "");
             hx_launch(name, grid, (unsigned) ngroups, (unsigned) (64 * nw), lds, st, &a);
+            if (kslices > 1) {
+                sml_kksum k;
+                k.part = a.part; k.bias = bias; k.resid = resid; k.y = y; k.ks = kslices; k.m = m_all; k.rows = rows;
+                hx_launch("sml_gemm_ksum", (unsigned) (((size_t) m_all * rows + 255) / 256), 1, 256, 0, st, &k);
+            }
             return;
         }
     }
@@ -1502,7 +1535,7 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int 
 static void gemm_one(const sml_hip_mat * m, const int8_t * q, const float * scale, const int32_t * sums, int nrow,
                      float * y, int per256) {
     if (!m || nrow < 1 || nrow > GEMM_MAX_ROWS) hx_failf("gemm of %d rows (1..%d)", nrow, GEMM_MAX_ROWS);
-    op_gemm(0, m->kdev, 1, 0, m->nbits, m->k.rows, m->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, y, NULL, NULL,
+    op_gemm(0, m->kdev, &m->k, 1, 0, m->nbits, m->k.rows, m->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, y, NULL, NULL,
             per256);
 }
 
@@ -1521,7 +1554,8 @@ static void gemm_swiglu(const sml_hip_mat * gate, const sml_hip_mat * up, const 
         ((sml_hip_mat *) gate)->up_k = up->k;
         ((sml_hip_mat *) gate)->pair_set = 1;
     }
-    op_gemm(0, pair, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h, NULL,
+    const sml_kmat hk[2] = { gate->k, up->k };
+    op_gemm(0, pair, hk, 1, 1, gate->nbits, gate->k.rows, gate->cols, NULL, nrow, gemm_mt(nrow), nrow, q, scale, sums, h, NULL,
             NULL, per256);
 }
 
@@ -1825,12 +1859,12 @@ void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out
     qa.count = m->count; qa.list = m->list; qa.q = m->qx; qa.scale = m->sx; qa.sums = m->ux; qa.per256 = m->per256;
     hx_launch("sml_moe_quant", (unsigned) T, (unsigned) m->nexp, 1024, 0, st, &qa);
     const int mt = gemm_mt(T);
-    op_gemm(st, m->tab_gu, m->nexp, 1, m->nbits, m->n_ff, m->n_embd, m->count, 0, mt, m->tmax,
+    op_gemm(st, m->tab_gu, NULL, m->nexp, 1, m->nbits, m->n_ff, m->n_embd, m->count, 0, mt, m->tmax,
             m->qx, m->sx, m->ux, m->h, NULL, NULL, m->per256);
     sml_kmquant qb = qa;
     qb.src = m->h; qb.mode = 1; qb.perms = m->ptab_d; qb.n = m->n_ff; qb.q = m->qh; qb.scale = m->sh; qb.sums = m->uh;
     hx_launch("sml_moe_quant", (unsigned) T, (unsigned) m->nexp, 1024, 0, st, &qb);
-    op_gemm(st, m->tab_d, m->nexp, 0, m->nbits, m->n_embd, m->n_ff, m->count, 0, mt, m->tmax,
+    op_gemm(st, m->tab_d, NULL, m->nexp, 0, m->nbits, m->n_embd, m->n_ff, m->count, 0, mt, m->tmax,
             m->qh, m->sh, m->uh, m->yd, NULL, NULL, m->per256);
     if (m->shx[0]) {
         // the shared expert on every token: its inputs in its permutation,
@@ -1840,11 +1874,12 @@ void op_moe(hipStream_t st, sml_hip_moe * m, const float * x, int T, float * out
         float * ss[1] = { m->sh_s };
         int32_t * uu[1] = { m->sh_u };
         op_normq_rows(st, (float *) x, NULL, NULL, 0.0f, m->n_embd, T, 1, pp, qq, ss, uu, NULL, m->per256);
-        op_gemm(st, m->sh_gu, 1, 1, m->shx[0]->nbits, m->sh_ff, m->n_embd, NULL, T, mt, T, m->sh_q, m->sh_s, m->sh_u,
+        const sml_kmat shk[2] = { m->shx[0]->k, m->shx[1]->k };
+        op_gemm(st, m->sh_gu, shk, 1, 1, m->shx[0]->nbits, m->sh_ff, m->n_embd, NULL, T, mt, T, m->sh_q, m->sh_s, m->sh_u,
                 m->sh_h, NULL, NULL, m->per256);
         pp[0] = m->sh_perm_d;
         op_normq_rows(st, m->sh_h, NULL, NULL, 0.0f, m->sh_ff, T, 1, pp, qq, ss, uu, NULL, m->per256);
-        op_gemm(st, m->shx[2]->kdev, 1, 0, m->shx[2]->nbits, m->n_embd, m->sh_ff, NULL, T, mt, T, m->sh_q, m->sh_s,
+        op_gemm(st, m->shx[2]->kdev, &m->shx[2]->k, 1, 0, m->shx[2]->nbits, m->n_embd, m->sh_ff, NULL, T, mt, T, m->sh_q, m->sh_s,
                 m->sh_u, m->sh_y, NULL, NULL, m->per256);
     }
     sml_kmoe_comb c;

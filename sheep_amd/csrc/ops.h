@@ -56,14 +56,15 @@ int op_gemv(hipStream_t st, const sml_hip_mat * m, const sml_hip_mat * up, int e
             const float * scale, const int32_t * sums, float * y, const float * bias, const float * up_bias,
             const float * resid, const gemv_fuse * fu);
 // Small-M GEMM over ngroups matrix groups (device table tab: one matrix per
-// group, or gate/up pairs for SwiGLU); m_all rows (count == NULL) or count[e]
+// group, or gate/up pairs for SwiGLU; hk: the host copies of a single group's
+// descriptors, or NULL); m_all rows (count == NULL) or count[e]
 // rows per group, at most mt (1, 4, 8 or 16). The activation regime:
 enum {
     GEMM_PER32 = 0,     // per-32 activations; Q4 above 8 rows on MFMA (fp32 order differs from the GEMV's)
     GEMM_PER256 = 1,    // per-256 activations; Q4 on MFMA with the integer superblock epilogue
     GEMM_EXACT = 2,     // per-32 activations, every row the GEMV's arithmetic bit for bit
 };
-void op_gemm(hipStream_t st, const sml_kmat * tab, int ngroups, int swiglu, int nbits, int rows, int cols,
+void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
              const int32_t * sums, float * y, const float * bias, const float * resid, int regime);
 int gemm_mt(int m);

@@ -123,6 +123,37 @@ def test_mfma_gemm_persistent_equals_one_tile(tmpdir_s, monkeypatch, cols):
         assert np.isfinite(outs["one tile"][0]).all()
 
 
+@pytest.mark.parametrize("cols,rows", [(5120, 2048), (14336, 1000)])
+def test_mfma_gemm_split_k_close_to_one_pass(tmpdir_s, monkeypatch, cols, rows):
+    """Inputs wider than 16 superblocks split into 4 slices (a persistent
+    workgroup per slice and row tiles, then sml_gemm_ksum adds the slices in
+    order): every output within float rounding of the one-pass kernel
+    (SML_MGEMM_KS=1), which sums each wave's superblocks and then the waves
+    in another order; per-32 and per-256 activations, 9 and 16 rows, a
+    ragged last tile (1000 rows)."""
+    p = tmpdir_s / f"mgk_{cols}_{rows}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, rows, cols, nbits=4, random_perm=False, seed=900 + cols)
+    m = sa.Mat.from_file(p, "w")
+    rng = np.random.default_rng(cols + 9)
+    for nrow in (9, 16):
+        xs = [rng.standard_normal(cols).astype(np.float32) * (1 + r) for r in range(nrow)]
+        for per256 in (False, True):
+            acts = tuple(sa.DevBuf.of(a) for a in quant_rows_sb(xs)) if per256 else quant_rows(xs)
+            outs = {}
+            for ks in ("1", "4"):
+                monkeypatch.setenv("SML_MGEMM_KS", ks)
+                y = sa.DevBuf(nrow * rows * 4)
+                sa.gemm(m, *acts, nrow, y, per256=per256)
+                outs[ks] = y.read(np.float32).reshape(nrow, rows)
+            a, b = outs["4"], outs["1"]
+            assert np.isfinite(a).all()
+            scale = np.abs(b).max(axis=1, keepdims=True)
+            err = float((np.abs(a - b) / scale).max())
+            assert err < 1e-5, (nrow, per256, err)
+            assert not np.array_equal(a, b), "the split form did not run"
+
+
 def quant_rows_sb(xs):
     """Per-256 quantization of each row (sml_quantize_act_sb), as host arrays."""
     q, s, u = zip(*(ob.quantize_act(np.ascontiguousarray(x, np.float32), per256=True) for x in xs))

@@ -254,3 +254,85 @@ def test_step_multi_per256_merge_quantizes_as_its_own_launch(tmp_path, kind, mon
         _, outs[fused] = run_multi(p, 2000, 6)
     for i in range(6):
         np.testing.assert_array_equal(outs["1"][i], outs["0"][i], err_msg=f"step {i}")
+
+
+@pytest.mark.parametrize("heads", [(8, 2), (12, 2), (8, 8), (16, 2)])
+def test_step_multi_spread_attention_equals_one_entry_body(tmp_path, heads, monkeypatch):
+    """The batched decode attention with its q, k, v and RoPE inputs spread
+    over the workgroup (sml_attnb) against the one-entry body's 4-wave form
+    (SML_ATTNB=0): six sequences whose positions cross split boundaries
+    (1..384 of a 512-position cache), 1, 4, 6 and 8 query heads per kv head;
+    every step's logits are equal bit for bit."""
+    monkeypatch.delenv("SML_MULTI", raising=False)
+    monkeypatch.delenv("SML_MULTI_EXACT_MAX", raising=False)
+    nh, nkv = heads
+    p = tmp_path / f"spread_{nh}_{nkv}.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=nh * 128, n_head=nh, n_head_kv=nkv, n_ff=1024, n_vocab=2000,
+                   qkv_bias=True, seed=77)
+    lens = [1, 127, 128, 129, 300, 383]
+    rng = np.random.default_rng(77)
+    prompts = [rng.integers(0, 2000, n).astype(np.int32) for n in lens]
+    outs = {}
+    for spread in ("0", "1"):
+        monkeypatch.setenv("SML_ATTNB", spread)
+        print(f"spread attention {heads} {spread}", flush=True)
+        d = sa.Decoder(p, n_ctx=512)
+        try:
+            d.slots(len(lens))
+            last = [d.prefill_slot(b, pr, 0, 2000) for b, pr in enumerate(prompts)]
+            toks, pos, out = [int(np.argmax(l)) for l in last], list(lens), []
+            for _ in range(3):
+                lg = d.step_multi(toks, pos, list(range(len(lens))), 2000)
+                out.append(lg)
+                toks = [int(np.argmax(l)) for l in lg]
+                pos = [x + 1 for x in pos]
+            outs[spread] = out
+        finally:
+            d.close()
+    for i in range(3):
+        np.testing.assert_array_equal(outs["1"][i], outs["0"][i], err_msg=f"step {i}")
+
+
+def test_step_multi_split_k_down_product(tmp_path, monkeypatch):
+    """The per-256 batched step of 12 sequences (the matrix-core products
+    take more than 8) with a 5120-wide FFN: the down product (20
+    superblocks) runs split in 4 slices, its residual added by
+    sml_gemm_ksum. Against the one-pass kernel (SML_MGEMM_KS=1) every step's
+    logits correlate to 0.99999 and keep their top-1 wherever the top two
+    are more than 1% of a logit s.d. apart."""
+    monkeypatch.delenv("SML_MULTI", raising=False)
+    monkeypatch.delenv("SML_MULTI_EXACT_MAX", raising=False)
+    p = tmp_path / "splitk.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=5120, n_vocab=2000, qkv_bias=True,
+                   seed=78)
+    prompts = [[(7 * b + 3 * j + 1) % 2000 for j in range(1 + b % 5)] for b in range(12)]
+    outs, forced = {}, None
+    for ks in ("1", "4"):
+        monkeypatch.setenv("SML_MGEMM_KS", ks)
+        print(f"split-k {ks}", flush=True)
+        d = sa.Decoder(p, n_ctx=64)
+        try:
+            d.slots(len(prompts))
+            last = [d.prefill_slot(b, pr, 0, 2000) for b, pr in enumerate(prompts)]
+            toks, pos, out, used = [int(np.argmax(l)) for l in last], [len(pr) for pr in prompts], [], []
+            for i in range(4):
+                if forced is not None:
+                    toks = forced[i]                # teacher-forced on the one-pass run's ids
+                used.append(list(toks))
+                lg = d.step_multi(toks, pos, list(range(len(prompts))), 2000)
+                out.append(lg)
+                toks = [int(np.argmax(l)) for l in lg]
+                pos = [x + 1 for x in pos]
+            outs[ks], forced = out, used
+        finally:
+            d.close()
+    differ = False
+    for i in range(4):
+        for b in range(len(prompts)):
+            a, r = outs["4"][i][b], outs["1"][i][b]
+            differ |= not np.array_equal(a, r)
+            assert corr(a, r) > 0.99999, (i, b)
+            top = np.sort(r)[-2:]
+            if top[1] - top[0] > 1e-2 * r.std():
+                assert int(np.argmax(a)) == int(np.argmax(r)), (i, b)
+    assert differ, "the split form did not run"
