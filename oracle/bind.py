@@ -246,6 +246,7 @@ def ref():
             "sml_dequant_bits1_add": (None, [c_void_p] * 4 + [c_int, c_int, c_int]),
             "sml_matvec_batch_flat4": (None, [c_void_p] * 6 + [c_void_p, c_int, c_int, c_int, c_int, c_int]),
             "sml_matvec_batch_flat4_sb": (None, [c_void_p] * 6 + [c_void_p, c_int, c_int, c_int, c_int, c_int]),
+            "sml_matvec_batch_flat6_sb": (None, [c_void_p] * 7 + [c_void_p, c_int, c_int, c_int, c_int, c_int]),
             "sml_rlp_ok": (c_int, [c_int, c_int, c_int, c_int]),
             "sml_rlp_bytes": (ctypes.c_size_t, [c_int, c_int, c_int]),
             "sml_rlp_pack": (None, [c_void_p] * 7 + [c_int, c_int, c_int, c_int]),
@@ -374,7 +375,9 @@ def _acts(q, s, u):
 def ref_matvec_batch(t, q, s, u, sb=True):
     """y [nb][rows] through the reference's batched flat 4-bit kernel:
     sml_matvec_batch_flat4_sb on per-256 activations (sb) or
-    sml_matvec_batch_flat4 on per-32 ones (sml/sml-kernel.c:1008-1021,1414-1435)."""
+    sml_matvec_batch_flat4 on per-32 ones (sml/sml-kernel.c:1008-1021,1414-1435);
+    a 6-bit tensor through sml_matvec_batch_flat6_sb (per-256 only,
+    sml/sml-kernel.c:1604-1619: the 4-bit plane's and the 2-bit plane's parts)."""
     q, s, u = (np.ascontiguousarray(v) for v in (q, s, u))
     nb = q.shape[0]
     y = np.zeros((nb, t.rows), np.float32)
@@ -382,6 +385,13 @@ def ref_matvec_batch(t, q, s, u, sb=True):
     md = t.md.ctypes.data if t.md is not None else None
     mq = t.mq.ctypes.data if t.mq is not None else None
     arr = _acts(q, s, u)
+    if t.nbits == 6:
+        if not sb:
+            raise ValueError("the reference's 6-bit batch kernel takes per-256 activations")
+        # the file's planes: [0] the 2-bit plane (code bits 4-5), [1] the 4-bit plane
+        ref().sml_matvec_batch_flat6_sb(y.ctypes.data, pl[1].ctypes.data, pl[0].ctypes.data, t.sd.ctypes.data,
+                                        t.sq.ctypes.data, md, mq, ctypes.addressof(arr), nb, t.rows, 0, t.rows, t.cols)
+        return y
     f = ref().sml_matvec_batch_flat4_sb if sb else ref().sml_matvec_batch_flat4
     f(y.ctypes.data, pl[0].ctypes.data, t.sd.ctypes.data, t.sq.ctypes.data, md, mq, ctypes.addressof(arr), nb,
       t.rows, 0, t.rows, t.cols)

@@ -4184,14 +4184,28 @@ extern "C" __global__ __launch_bounds__(256) void sml_gemm_ksum(const sml_kksum 
 // Tiles are numbered so that consecutive ones share their weight rows and
 // sit on one XCD (workgroup i runs on XCD i mod 8): the positions' tiles of a
 // weight tile find it in that XCD's L2.
+//
+// Q6 (NB = 6; the file's 4-bit plane holds code bits 0-3 in the Q4 layout,
+// its 2-bit plane bits 4-5): the 2-bit plane's tile (128 rows x 64 bytes a
+// superblock; per group quad 32 bytes, byte j holding column j of its four
+// groups at bits 2(g%4)) is staged beside the nibbles, and each group's B
+// operand is nibble | bits << 4, a code 0..63 (|dot_g| < 2^18, sq_g * dot_g
+// < 2^26: the integer sums hold). The fields are Q4's (widened to bytes at
+// upload). The reference's per-256 Q6 prompt kernel
+// (sml_matvec_batch_flat6_sb, sml/sml-kernel.c:1604-1619) sums the 2-bit
+// plane's part and the nibbles' part in two fp32 passes; the integers here
+// are its integers, the fp32 order another.
 #define PG_BN 128
 #define PG_BM 32
 #define PG_BROW 144
 #define PG_AROW 272
+#define PG_HROW 72
 #define PG_STAGE (PG_BN * PG_BROW + PG_BM * PG_AROW + PG_BM * 8)
+#define PG_STAGE6 (PG_STAGE + PG_BN * PG_HROW)
 
-template <bool SW>
+template <int NB, bool SW>
 __device__ void pgemm_q4_body(const sml_kgemm & a) {
+    constexpr int STG = NB == 6 ? PG_STAGE6 : PG_STAGE;
     typedef long v1l;
     extern __shared__ __align__(16) uint8_t lds[];
     const int n = a.cols, ng = n / 32, nsb = n / 256, m_all = a.m_all, rows = a.rows;
@@ -4211,8 +4225,17 @@ __device__ void pgemm_q4_body(const sml_kgemm & a) {
     // and of the activation tile (position t/16 + 16i, bytes 16(t%16)..);
     // rows and positions past the end read the last one. 32-bit offsets:
     // the host keeps rows x cols / 2 and positions x cols below 2^32.
-    const uint8_t * bplane[2] = {a.mats[0].plane[0], a.mats[SW ? 1 : 0].plane[0]};
+    constexpr int NIB = NB == 6 ? 1 : 0;                        // the nibble plane's index
+    const uint8_t * bplane[2] = {a.mats[0].plane[NIB], a.mats[SW ? 1 : 0].plane[NIB]};
     uint32_t boff[4], aoff[AWN];
+    // Q6: the 2-bit plane's words (row w/4 = t/4 + 64i, bytes 16(t%4)..)
+    const uint8_t * hplane[2] = {a.mats[0].plane[0], a.mats[SW ? 1 : 0].plane[0]};
+    uint32_t hoff[2];
+    #pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int lr = (tid >> 2) + 64 * i, rr = SW ? (lr & 63) : lr;
+        hoff[i] = (uint32_t) min(r0 + rr, rows - 1) * ((uint32_t) n / 4) + 16u * (uint32_t) (tid & 3);
+    }
     #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int lr = (tid >> 3) + 32 * i, rr = SW ? (lr & 63) : lr;
@@ -4244,7 +4267,7 @@ __device__ void pgemm_q4_body(const sml_kgemm & a) {
         fdb[t] = (const uint8_t *) m.sdmd + gr * (size_t) nsb * 4;
     }
 
-    v4u bw[4], aw[AWN];
+    v4u bw[4], aw[AWN], hw[2];
     float sw_ = 0.0f;
     int4 su0 = make_int4(0, 0, 0, 0), su1 = su0;
     v4u fq[2], fqn[2];
@@ -4253,6 +4276,11 @@ __device__ void pgemm_q4_body(const sml_kgemm & a) {
         #pragma unroll
         for (int i = 0; i < 4; i++)
             bw[i] = __builtin_nontemporal_load((const GLOBAL v4u *) (bplane[SW && i >= 2] + (boff[i] + 128u * (uint32_t) b)));
+        if constexpr (NB == 6) {
+            #pragma unroll
+            for (int i = 0; i < 2; i++)
+                hw[i] = __builtin_nontemporal_load((const GLOBAL v4u *) (hplane[SW && i >= 1] + (hoff[i] + 64u * (uint32_t) b)));
+        }
         #pragma unroll
         for (int i = 0; i < AWN; i++) aw[i] = *(const v4u *) (a.q + (aoff[i] + 256u * (uint32_t) b));
         if (tid < PG_BM) {
@@ -4267,7 +4295,15 @@ __device__ void pgemm_q4_body(const sml_kgemm & a) {
         }
     };
     auto stage = [&](int buf) {
-        uint8_t * base = lds + (size_t) buf * PG_STAGE;
+        uint8_t * base = lds + (size_t) buf * STG;
+        if constexpr (NB == 6) {
+            #pragma unroll
+            for (int i = 0; i < 2; i++) {
+                uint8_t * hd = base + PG_STAGE + ((tid >> 2) + 64 * i) * PG_HROW + 16 * (tid & 3);
+                *(v2u *) hd = v2u{hw[i][0], hw[i][1]};
+                *(v2u *) (hd + 8) = v2u{hw[i][2], hw[i][3]};
+            }
+        }
         #pragma unroll
         for (int i = 0; i < 4; i++) {
             uint8_t * bd = base + bdst0 + i * 32 * PG_BROW;
@@ -4296,7 +4332,7 @@ __device__ void pgemm_q4_body(const sml_kgemm & a) {
             for (int r = 0; r < 4; r++) acc[t][mt][r] = 0.0f;
 
     auto compute = [&](int buf) {
-        const uint8_t * base = lds + (size_t) buf * PG_STAGE;
+        const uint8_t * base = lds + (size_t) buf * STG;
         const uint8_t * abase = base + PG_BN * PG_BROW;
         const float * sbase = (const float *) (abase + PG_BM * PG_AROW);
         const int * ubase = (const int *) (sbase + PG_BM);
@@ -4307,6 +4343,16 @@ __device__ void pgemm_q4_body(const sml_kgemm & a) {
             const uint8_t * p = base + (lrow[t] + i16) * PG_BROW + kq * 32;
             pk[t][0] = *(const v4u *) p;
             pk[t][1] = *(const v4u *) (p + 16);
+        }
+        // Q6: the lane's 8 bytes of k-slice kq in each group quad of the 2-bit plane
+        v2u hk[2][2];
+        if constexpr (NB == 6) {
+            #pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint8_t * p = base + PG_STAGE + (lrow[t] + i16) * PG_HROW + kq * 8;
+                hk[t][0] = *(const v2u *) p;
+                hk[t][1] = *(const v2u *) (p + 32);
+            }
         }
         int is[2][MT][4];
         v4i im[2][MT];
@@ -4335,8 +4381,13 @@ __device__ void pgemm_q4_body(const sml_kgemm & a) {
             int sq[2];
             #pragma unroll
             for (int t = 0; t < 2; t++) {
-                const unsigned lo = (pk[t][c >> 1][2 * (c & 1)] >> sh) & 0x0F0F0F0Fu;
-                const unsigned hi = (pk[t][c >> 1][2 * (c & 1) + 1] >> sh) & 0x0F0F0F0Fu;
+                unsigned lo = (pk[t][c >> 1][2 * (c & 1)] >> sh) & 0x0F0F0F0Fu;
+                unsigned hi = (pk[t][c >> 1][2 * (c & 1) + 1] >> sh) & 0x0F0F0F0Fu;
+                if constexpr (NB == 6) {
+                    const v2u h = hk[t][g >> 2];
+                    lo |= ((h.x >> (2 * (g & 3))) & 0x03030303u) << 4;
+                    hi |= ((h.y >> (2 * (g & 3))) & 0x03030303u) << 4;
+                }
                 bc[t] = (v1l) (((unsigned long) hi << 32) | lo);
                 const uint32_t f = fq[t][g >> 1] >> (16 * (g & 1));
                 sq[t] = (int) (f & 0xFFu);
@@ -4414,5 +4465,7 @@ __device__ void pgemm_q4_body(const sml_kgemm & a) {
         }
 }
 
-extern "C" __global__ __launch_bounds__(256, 2) void sml_pgemm_q4(const sml_kgemm a) { pgemm_q4_body<false>(a); }
-extern "C" __global__ __launch_bounds__(256, 2) void sml_pgemm_q4_s(const sml_kgemm a) { pgemm_q4_body<true>(a); }
+extern "C" __global__ __launch_bounds__(256, 2) void sml_pgemm_q4(const sml_kgemm a) { pgemm_q4_body<4, false>(a); }
+extern "C" __global__ __launch_bounds__(256, 2) void sml_pgemm_q4_s(const sml_kgemm a) { pgemm_q4_body<4, true>(a); }
+extern "C" __global__ __launch_bounds__(256, 2) void sml_pgemm_q6(const sml_kgemm a) { pgemm_q4_body<6, false>(a); }
+extern "C" __global__ __launch_bounds__(256, 2) void sml_pgemm_q6_s(const sml_kgemm a) { pgemm_q4_body<6, true>(a); }

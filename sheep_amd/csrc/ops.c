@@ -1384,11 +1384,13 @@ int gemm_exact(int regime, int m_all) {
 }
 
 #define GEMM_TILE 128            // chunks (groups) per pass: 64 lanes x GEMM_NI
-// The prompt GEMM (sml_pgemm_q4): positions per tile, and its LDS: two
+// The prompt GEMM (sml_pgemm_q4 / _q6): positions per tile, and its LDS: two
 // stages of a 128-row weight tile (144 bytes a row), a PGEMM_BM-position
-// activation tile (272 bytes a row) and the positions' scales and sums
+// activation tile (272 bytes a row) and the positions' scales and sums; Q6
+// adds the 2-bit plane's 128-row tile (72 bytes a row)
 #define PGEMM_BM 32
 #define PGEMM_LDS (2 * (128 * 144 + PGEMM_BM * 272 + PGEMM_BM * 8))
+#define PGEMM_LDS6 (PGEMM_LDS + 2 * 128 * 72)
 #define GEMM_MAX_ROWS 65536
 
 void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngroups, int swiglu, int nbits, int rows, int cols,
@@ -1398,10 +1400,10 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngro
     if (swiglu && (bias || resid)) hx_failf("SwiGLU GEMM takes no bias or residual");
     if ((uint64_t) rows * (uint64_t) cols >= (1ull << 32)) hx_failf("matrix too large for one GEMM launch");
     if (!count && m_all > 16) {
-        // prompt-sized: Q4 with per-256 activations on the prompt MFMA GEMM
-        // (tiles of 128 rows, SwiGLU 64, x PGEMM_BM positions); anything else in
-        // slices of 16 rows through the small-M kernels
-        if (per256 && nbits == 4 && cols % 256 == 0 && env_int("SML_PGEMM", 1)) {
+        // prompt-sized: Q4 and Q6 with per-256 activations on the prompt MFMA
+        // GEMM (tiles of 128 rows, SwiGLU 64, x PGEMM_BM positions); anything
+        // else in slices of 16 rows through the small-M kernels
+        if (per256 && (nbits == 4 || nbits == 6) && cols % 256 == 0 && env_int("SML_PGEMM", 1)) {
             const int rt = swiglu ? 64 : 128;
             const uint64_t tiles = (uint64_t) ((rows + rt - 1) / rt) * (uint64_t) ((m_all + PGEMM_BM - 1) / PGEMM_BM);
             if (tiles > 0x7FFFFFFFull || (uint64_t) m_all * (uint64_t) cols >= (1ull << 32))
@@ -1411,7 +1413,9 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngro
             a.mats = tab; a.nmat = swiglu ? 2 : 1; a.cols = cols; a.rows = rows;
             a.m_all = m_all; a.mmax = mmax;
             a.q = q; a.scale = scale; a.sums = sums; a.y = y; a.bias = bias; a.resid = resid;
-            hx_launch(swiglu ? "sml_pgemm_q4_s" : "sml_pgemm_q4", (unsigned) tiles, 1, 256, PGEMM_LDS, st, &a);
+            char pname[32];
+            snprintf(pname, sizeof pname, "sml_pgemm_q%d%s", nbits, swiglu ? "_s" : "");
+            hx_launch(pname, (unsigned) tiles, 1, 256, nbits == 6 ? PGEMM_LDS6 : PGEMM_LDS, st, &a);
             return;
         }
         const int ng = cols / 32;

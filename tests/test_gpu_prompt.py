@@ -1,4 +1,4 @@
-"""Prompt reading at level 2 on the GPU: the prompt MFMA GEMM (sml_pgemm_q4,
+"""Prompt reading at level 2 on the GPU: the prompt MFMA GEMM (sml_pgemm_q4/_q6,
 hundreds of positions per weight read) against the reference's own CPU
 kernels, and whole prompts against the reference's sml_prefill.
 
@@ -99,6 +99,56 @@ def test_prompt_gemm_swiglu_matches_reference(tmpdir_s, rows, cols, npos):
 
 
 @need_ref
+@pytest.mark.parametrize("rows,cols,npos", [(1024, 4096, 200), (1000, 1536, 100), (4096, 14336, 77), (130, 256, 65)])
+def test_prompt_gemm_q6_matches_reference(tmpdir_s, rows, cols, npos):
+    """sml_pgemm_q6 (6-bit codes: the 4-bit plane's nibble | the 2-bit plane's
+    bits << 4, on the Q4 tile's integer superblock sums) against the
+    reference's sml_matvec_batch_flat6_sb on the same per-256 activations,
+    which sums the two planes' parts in separate fp32 passes: rel-RMS within
+    2e-6 per position, ragged row and position tiles."""
+    p = tmpdir_s / f"pg6_{rows}_{cols}.ssf"
+    if not p.exists():
+        sa.synth_matrix(p, rows, cols, nbits=6, random_perm=False, seed=710 + cols + rows)
+    t = SSF(p)["w"]
+    assert t.nbits == 6
+    m = sa.Mat.from_file(p, "w")
+    rng = np.random.default_rng(rows + npos + 6)
+    xs = rng.standard_normal((npos, cols)).astype(np.float32) * (1 + np.arange(npos, dtype=np.float32)[:, None] / 8)
+    Q, S, U = quant_rows_sb(xs)
+    y = sa.DevBuf(npos * rows * 4)
+    sa.gemm(m, sa.DevBuf.of(Q), sa.DevBuf.of(S), sa.DevBuf.of(U), npos, y, per256=True)
+    got = y.read(np.float32).reshape(npos, rows)
+    want = ref_batch_sb(t, Q, S, U)
+    err = rel_rms(got, want)
+    worst = max(rel_rms(got[i], want[i]) for i in range(npos))
+    print(f"q6 {rows}x{cols}, {npos} positions: rel-RMS {err:.2e}, worst position {worst:.2e}")
+    assert worst <= 2e-6, worst
+
+
+@need_ref
+def test_prompt_gemm_q6_swiglu_matches_reference(tmpdir_s):
+    """The Q6 SwiGLU form against the reference's flat6_sb products and SiLU."""
+    rows, cols, npos = 1024, 4096, 150
+    pg, pu = tmpdir_s / "pg6g.ssf", tmpdir_s / "pg6u.ssf"
+    for p, s in ((pg, 1), (pu, 2)):
+        if not p.exists():
+            sa.synth_matrix(p, rows, cols, nbits=6, random_perm=False, seed=820 + s)
+    tg, tu = SSF(pg)["w"], SSF(pu)["w"]
+    mg, mu = sa.Mat.from_file(pg, "w"), sa.Mat.from_file(pu, "w")
+    xs = np.random.default_rng(cols + 6).standard_normal((npos, cols)).astype(np.float32)
+    Q, S, U = quant_rows_sb(xs)
+    h = sa.DevBuf(npos * rows * 4)
+    sa.gemm_swiglu(mg, mu, sa.DevBuf.of(Q), sa.DevBuf.of(S), sa.DevBuf.of(U), npos, h, per256=True)
+    got = h.read(np.float32).reshape(npos, rows)
+    g, u = ref_batch_sb(tg, Q, S, U), ref_batch_sb(tu, Q, S, U)
+    want = np.ascontiguousarray(g, np.float32).copy()
+    ob.oracle().orc_silu_mul(want.ctypes.data, np.ascontiguousarray(u, np.float32).ctypes.data, want.size)
+    err = rel_rms(got, want)
+    print(f"q6 swiglu {rows}x{cols}, {npos} positions: rel-RMS {err:.2e}")
+    assert err <= 2e-6, err
+
+
+@need_ref
 def test_prompt_gemm_extreme_min_fields(tmpdir_s):
     """mq = 255 (a min code of +128, one past int8) and mq = 0 are summed
     exactly: the kernel takes B = mq - 128 and adds the superblock's sum of
@@ -135,11 +185,13 @@ def grade(got, ref):
 
 
 @need_ref
-@pytest.mark.parametrize("model,npos,pb", [("tiny", 100, 512), ("tiny", 700, 256), ("qwenish", 300, 512)])
+@pytest.mark.parametrize("model,npos,pb", [("tiny", 100, 512), ("tiny", 700, 256), ("qwenish", 300, 512),
+                                            ("tiny_q6", 300, 512)])
 def test_level2_prompt_graded_against_reference(request, tmp_path_factory, model, npos, pb, monkeypatch):
     """A prompt read at level 2 (chunks of pb positions) against the
     reference's sml_prefill in its default prompt regime: the logits after
-    the prompt, then 8 steps on the reference's greedy ids, each graded.
+    the prompt, then 8 steps on the reference's greedy ids, each graded
+    (tiny_q6: the tiny model with 6-bit matrices).
     The attention (a wave per position) and the fp32 sums run in their own
     orders, so an int8 activation code flips now and then; measured: prompt
     logits correlate at 0.99996 (tiny) and 0.99983 (Qwen-shaped layers), and
@@ -149,11 +201,12 @@ def test_level2_prompt_graded_against_reference(request, tmp_path_factory, model
     than 5% of a logit s.d."""
     assert os.environ.get("SML_PROMPT_SB", "1") != "0", "the reference must read prompts per 256 here"
     d = tmp_path_factory.mktemp("pp")
-    V = 2000 if model == "tiny" else 32000
+    V = 2000 if model.startswith("tiny") else 32000
     path = d / f"{model}.ssf"
-    if model == "tiny":
+    if model.startswith("tiny"):
+        # tiny_q6: every matrix 6-bit (the prompt products on sml_pgemm_q6)
         sa.synth_model(path, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=V,
-                       qkv_bias=True, random_perm=True, seed=31)
+                       qkv_bias=True, random_perm=True, seed=31, nbits=6 if model == "tiny_q6" else 4)
     else:
         sa.synth_model(path, n_layer=4, n_embd=1536, n_head=12, n_head_kv=2, n_ff=8960, n_vocab=V,
                        rope_theta=1e6, qkv_bias=True, tied=True, random_perm=True, seed=1002)
