@@ -352,8 +352,9 @@ def exact_decode(path, ids, warmup, steps):
     """The token-identical path: the same Llama-3-8B-shaped file opened in
     exact mode (every kernel in the reference CPU engine's float order, so
     each step's logits equal its sml_forward bit for bit), the same prompt
-    read exactly (a token at a time), then `warmup` untimed and `steps` timed
-    greedy tokens at the fast line's positions."""
+    read exactly (batched: 64-position chunks through the reference-order
+    GEMM and attention, equal to stepping it bit for bit), then `warmup`
+    untimed and `steps` timed greedy tokens at the fast line's positions."""
     dec = sa.Decoder(path, n_ctx=N_CTX, exact=True)
     try:
         if not dec.exact:
@@ -377,7 +378,8 @@ def exact_decode(path, ids, warmup, steps):
     return {"positions": f"{pos}..{pos + steps - 1}", "tokens_per_s": round(tps, 2),
             "ms_per_step": round(dt * 1e3 / steps, 4), "gpu_event_ms": round(ev_ms, 3),
             "frac_of_weights_roofline": round(tps / (HBM_PEAK_GBS * 1e9 / wbytes), 4),
-            "prompt": {"tokens": len(ids), "level": 0, "s": round(t_prompt, 2)},
+            "prompt": {"tokens": len(ids), "level": 1, "s": round(t_prompt, 3),
+                       "tokens_per_s": round(len(ids) / t_prompt, 1)},
             "first_tokens": [int(t) for t in out[:8]]}
 
 

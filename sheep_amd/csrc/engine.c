@@ -96,6 +96,8 @@ static struct {
     float * mlog_host;         // pinned: a batched step's logits, copied on to the caller's buffer
     uint16_t ** kc_tab, ** vc_tab;   // device tables of every slot's cache base
     float * mpart;             // attention partials of every sequence of a batch
+    size_t mpart_floats;
+    int xchunk;                // exact mode's prompt chunk: its rows' scores fit in mpart
     int32_t * iota;            // device [n_ctx]: 0, 1, 2, ... (prompt chunk positions)
     int32_t * slotid;          // device [MAX_SLOTS][rrows]: row s filled with s
     int rrows;                 // rows of the batched body's buffers: max(MAX_SLOTS, pb)
@@ -576,8 +578,9 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     HX(hipHostMalloc((void **) &G.pin, (size_t) (n_ctx + 8) * 4, 0));
     HX(hipDeviceSynchronize());
     // prompt reading: batched (exact) unless SML_GPU_PP=0, as the reference's
-    // open does (sml/sml-gpu-fwd.c:2371-2375)
-    G.prompt_level = env_int("SML_GPU_PP", 1) == 0 || G.exact ? 0 : 1;
+    // open does (sml/sml-gpu-fwd.c:2371-2375); in exact mode level 1 is the
+    // reference-order batched prompt where every product takes it (rows_check)
+    G.prompt_level = env_int("SML_GPU_PP", 1) == 0 ? 0 : 1;
     // level-2 chunk: SML_PB positions (16..4096, default 512); MoE layers
     // take at most MAX_SLOTS rows per call
     G.pb = env_int("SML_PB", 512);
@@ -717,7 +720,7 @@ int sml_gpu_layers(int * of) {
 // (the default); 2: batched with the Q4 products on MFMA. As the reference's
 // (sml/sml-gpu-fwd.c:2420-2423): 2 = every batched kernel, 1 = without the
 // matrix-core one, 0 = token at a time.
-void sml_gpu_prompt_mode(int level) { G.prompt_level = level <= 0 || G.exact ? 0 : level >= 2 ? 2 : 1; }
+void sml_gpu_prompt_mode(int level) { G.prompt_level = level <= 0 ? 0 : level >= 2 && !G.exact ? 2 : 1; }
 
 int sml_gpu_decode_cpu(int on) { (void) on; return 0; }
 
@@ -748,11 +751,21 @@ static int multi_per256(int ns) {
 // Whether the batched body can run this model: q, k and v stacked as one
 // matrix, and gate/up sharing a permutation and width (the MoE layers batch
 // by themselves). Builds the (gate, up) tables on first use.
+// A Q4 matrix 256-aligned: the exact batched GEMM's input
+static int xgemm_ok(const sml_hip_mat * m) { return m && m->nbits == 4 && m->cols % 256 == 0; }
+
 static int rows_check(void) {
     if (G.rows_ok >= 0) return G.rows_ok;
     for (int L = 0; L < G.n_layer; L++) {
         eng_layer * y = &G.L[L];
         if (!y->qkv || (!y->moe && (y->perm_gu[0] != y->perm_gu[1] || y->gate->nbits != y->up->nbits))) {
+            G.rows_ok = 0;
+            return 0;
+        }
+        // exact mode batches prompts of dense Q4 layers only (the
+        // reference-order GEMM); anything else reads them a token at a time
+        if (G.exact && (y->moe || !xgemm_ok(y->qkv) || !xgemm_ok(y->o) || !xgemm_ok(y->gate) || !xgemm_ok(y->up) ||
+                        !xgemm_ok(y->down))) {
             G.rows_ok = 0;
             return 0;
         }
@@ -801,6 +814,12 @@ static void rows_alloc(void) {
     const size_t part_pb = R * (size_t) G.H * (size_t) ((G.n_ctx + 127) / 128) * (size_t) (G.hd + 2);
     if (part_pb > part) part = part_pb;
     G.mpart = dalloc(part * 4);
+    G.mpart_floats = part;
+    // exact mode reads a prompt in chunks whose reference-order scores
+    // ([rows][H][n_ctx] floats) fit in the partials buffer: at most 64 rows
+    G.xchunk = (int) (part / ((size_t) G.H * (size_t) G.n_ctx));
+    if (G.xchunk > 64) G.xchunk = 64;
+    if (G.xchunk > G.rrows) G.xchunk = G.rrows;
     hx_kpart();                                     // the split-K products' buffer, before any capture
     G.kc_tab = dalloc(S * sizeof(void *));
     G.vc_tab = dalloc(S * sizeof(void *));
@@ -870,10 +889,19 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
         // that to its own launch)
         const int fuse_q = y->perm_o < 0 &&
                            (!sb || (!causal && G.H % 2 == 0 && G.hd == 128 && env_int("SML_MERGE_Q256", 1)));
-        op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
-                           G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.pos_cap, G.mpart, G.matt,
-                           fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL,
-                           causal ? (regime == GEMM_EXACT ? 1 : 2) : 0, gemm_exact(regime, ns), sb);
+        if (regime == GEMM_REF) {
+            // exact mode: one sequence (slot 0), the reference's order
+            if (!causal) hx_failf("exact mode batches prompts only");
+            op_attention_rows_exact(G.st, G.mqkv, (int) qkv, G.kc + (size_t) L * G.n_ctx * kvd,
+                                    G.vc + (size_t) L * G.n_ctx * kvd, G.rc, G.rs, pos, ns, G.H, G.KV, G.n_ctx,
+                                    G.pos_cap, G.mpart, G.matt, fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL,
+                                    fuse_q ? G.masum : NULL);
+        } else {
+            op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
+                               G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.pos_cap, G.mpart, G.matt,
+                               fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL,
+                               causal ? (regime == GEMM_EXACT ? 1 : 2) : 0, gemm_exact(regime, ns), sb);
+        }
         if (!fuse_q) {
             pp[0] = pdev(y->perm_o);
             op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, sb);
@@ -921,8 +949,11 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
 //    prompt MFMA GEMM, attention a wave per position.
 static void prefill_rows(int slot, int pos0, int n) {
     rows_alloc();
-    const int regime = G.prompt_level >= 2 ? GEMM_PER256 : GEMM_EXACT;
-    const int chunk = G.prompt_level >= 2 ? G.pb : MAX_SLOTS;
+    // exact mode: the reference-order products and attention, in chunks of
+    // xchunk positions
+    const int regime = G.exact ? GEMM_REF : G.prompt_level >= 2 ? GEMM_PER256 : GEMM_EXACT;
+    const int chunk = G.exact ? G.xchunk : G.prompt_level >= 2 ? G.pb : MAX_SLOTS;
+    if (chunk < 1) hx_failf("exact prompt chunk of %d rows", chunk);
     int last = 0;
     for (int p0 = 0; p0 < n; p0 += chunk) {
         const int nb = n - p0 < chunk ? n - p0 : chunk;

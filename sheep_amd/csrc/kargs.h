@@ -194,6 +194,12 @@ typedef struct {
     int32_t * u_out;
     int n_head, n_kv, n_ctx;
     float inv;                    // 1 / sqrtf(hd)
+    // rows (grid z of the scores, grid y of P.V): row b is position pos[b],
+    // its q/k/v at b * qkv_stride floats, its scores at b * n_head * n_ctx,
+    // its output at b * n_head * hd; kv_written: every row's k and v are
+    // in the cache already (exact batched prompts; the kernels write none)
+    int qkv_stride;
+    int kv_written;
 } sml_kattnx;
 
 

@@ -2489,10 +2489,14 @@ extern "C" __global__ __launch_bounds__(256) void sml_attnx_scores(const sml_kat
     #pragma clang fp contract(off)
     __shared__ float qs[ATTN_MAXREP][HD];
     __shared__ __align__(16) uint16_t kt[ATTNX_CH * ATTNX_KROW];
-    const int kh = blockIdx.y, t0 = blockIdx.x * ATTNX_CH, tid = threadIdx.x;
-    const int pos = *a.pos, n = pos + 1, rep = a.n_head / a.n_kv, kvd = a.n_kv * HD;
+    const int kh = blockIdx.y, t0 = blockIdx.x * ATTNX_CH, tid = threadIdx.x, b = blockIdx.z;
+    const int pos = a.pos[b], n = pos + 1, rep = a.n_head / a.n_kv, kvd = a.n_kv * HD;
     if (t0 >= n) return;
-    const bool own = pos < t0 + ATTNX_CH;
+    // own: this split holds the position and rotates and writes its k and v
+    const bool own = pos < t0 + ATTNX_CH && !a.kv_written;
+    const float * aq = a.q + (size_t) b * a.qkv_stride, * ak = a.k + (size_t) b * a.qkv_stride;
+    const float * avv = a.v + (size_t) b * a.qkv_stride;
+    float * scb = a.sc + (size_t) b * a.n_head * a.n_ctx;
     GLOBAL uint16_t * kc = (GLOBAL uint16_t *) a.kc, * vc = (GLOBAL uint16_t *) a.vc;
     // RoPE inputs first, then the split's K tile, coalesced (16 lanes a row,
     // rows past the position load row t0 and are never read): loads complete
@@ -2507,13 +2511,13 @@ extern "C" __global__ __launch_bounds__(256) void sml_attnx_scores(const sml_kat
     #pragma unroll
     for (int r = 0; r < RR; r++) {
         const int idx = min(tid + 256 * r, npair - 1), j = idx / (HD / 2), i = idx % (HD / 2);
-        const float * src = j < rep ? a.q + (size_t) (kh * rep + j) * HD : a.k + (size_t) kh * HD;
+        const float * src = j < rep ? aq + (size_t) (kh * rep + j) * HD : ak + (size_t) kh * HD;
         x0[r] = src[i];
         x1[r] = src[i + HD / 2];
         c[r] = cs[i];
         sv[r] = sn[i];
     }
-    const float vnew = a.v[(size_t) kh * HD + (tid & (HD - 1))];     // used by the owning split only
+    const float vnew = avv[(size_t) kh * HD + (tid & (HD - 1))];     // used by the owning split only
     v4u kw[KC];
     #pragma unroll
     for (int r = 0; r < KC; r++) {
@@ -2525,7 +2529,7 @@ extern "C" __global__ __launch_bounds__(256) void sml_attnx_scores(const sml_kat
     #pragma unroll
     for (int r = 0; r < KC; r++) {
         const int ch = tid + 256 * r;
-        if (t0 + ch / 16 != pos) *(v4u *) (kt + (ch / 16) * ATTNX_KROW + (ch % 16) * 8) = kw[r];
+        if (!own || t0 + ch / 16 != pos) *(v4u *) (kt + (ch / 16) * ATTNX_KROW + (ch % 16) * 8) = kw[r];
     }
     #pragma unroll
     for (int r = 0; r < RR; r++) {
@@ -2562,7 +2566,7 @@ extern "C" __global__ __launch_bounds__(256) void sml_attnx_scores(const sml_kat
             #pragma unroll
             for (int e = 0; e < 8; e++) l[e] = __builtin_fmaf(qs[j][8 * i + e], kf[e], l[e]);
         }
-        a.sc[(size_t) (kh * rep + j) * a.n_ctx + t] =
+        scb[(size_t) (kh * rep + j) * a.n_ctx + t] =
             (((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]))) * a.inv;
     }
 }
@@ -2583,8 +2587,8 @@ extern "C" __global__ __launch_bounds__(ATTNX_THREADS) void sml_attnx_pv(const s
     constexpr int CPT = ATTNX_TP * HD / 8 / LT;               // 16-byte chunks per loader per tile
     static_assert(CPT * LT * 8 == ATTNX_TP * HD, "a tile is whole chunks per loader");
     static_assert(LT / 16 % 2 == 0, "a loader wave's rows hold whole position pairs");
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int kh = h / (a.n_head / a.n_kv), pos = *a.pos, n = pos + 1, kvd = a.n_kv * HD;
+    const int h = blockIdx.x, tid = threadIdx.x, rb = blockIdx.y;
+    const int kh = h / (a.n_head / a.n_kv), pos = a.pos[rb], n = pos + 1, kvd = a.n_kv * HD;
     const int ncap = (a.n_ctx + 3) & ~3, nt = (n + ATTNX_TP - 1) / ATTNX_TP;
     // waves 4..7 stream V; waves 0 and 1 run the chains (a wave-uniform test)
     const bool loader = __builtin_amdgcn_readfirstlane(tid) >= LT;
@@ -2633,7 +2637,7 @@ extern "C" __global__ __launch_bounds__(ATTNX_THREADS) void sml_attnx_pv(const s
     };
     // the scores (8 loads per thread in flight, then into LDS) and expf's table
     if (tid < 32) etab[tid] = EXPF_TAB[tid];
-    const GLOBAL float * sc = (const GLOBAL float *) a.sc + (size_t) h * a.n_ctx;
+    const GLOBAL float * sc = (const GLOBAL float *) a.sc + ((size_t) rb * a.n_head + h) * a.n_ctx;
     for (int base = 0; base < n; base += 8 * ATTNX_THREADS) {
         float v[8];
         #pragma unroll
@@ -2750,14 +2754,15 @@ extern "C" __global__ __launch_bounds__(ATTNX_THREADS) void sml_attnx_pv(const s
         }
     }
     if (tid >= HD) return;
-    a.out[(size_t) h * HD + tid] = o;
+    const size_t ob = (size_t) rb * a.n_head * HD;
+    a.out[ob + (size_t) h * HD + tid] = o;
     if (a.q_out) {
         const float amax = max32(fabsf(o));
         const float s = amax / 127.0f;
         const float is = s > 0.0f ? 1.0f / s : 0.0f;
         const int q = quant1(o, is);
         const int sum = isum32(q);
-        const size_t j = (size_t) h * HD + tid;
+        const size_t j = ob + (size_t) h * HD + tid;
         a.q_out[j] = (int8_t) q;
         if ((tid & 31) == 0) { a.s_out[j / 32] = s; a.u_out[j / 32] = sum; }
     }
@@ -4147,6 +4152,147 @@ extern "C" __global__ __launch_bounds__(256) void sml_gemm_ksum(const sml_kksum 
 }
 
 
+
+// ---------------------------------------------------------------- batched GEMM in the reference's order (exact mode)
+//
+// Y[p][r] = W.a[p] for the positions p of an exact-mode prompt chunk, each
+// output the exact GEMV's (gemv_body EX, the reference's flat4 kernel,
+// sml/sml-kernel.c:572-727) bit for bit, the weights read once for 64
+// positions. Per-32 activations (s_g, sum_g per group). For each (row,
+// position) the reference keeps 8 float chains, chain j taking groups j,
+// j+8, ... of the row in order:
+//     v_j = fma(sd*sq_g, s_g*dot_g, v_j);  v_j = fma(md*(mq_g-127), s_g*sum_g, v_j)
+// then ((v0+v4)+(v1+v5)) + ((v2+v6)+(v3+v7)); y = resid + (v + bias).
+// The integer dot_g comes from one v_mfma_i32_16x16x32_i8 per group and
+// 16 x 16 tile (the operand layout of mgemm_q4_body: lane l holds weight row
+// l%16 and positions 4(l/16)..+3 of the wave's 16). A lane runs the chains
+// of its own (row, position) pairs over the groups in order, 8 chains x 4
+// positions in registers (x 2 for SwiGLU: gate and up), so no value crosses
+// lanes before the fold. Workgroup: 4 waves = 64 positions x 16 weight rows;
+// the waves read the same weight bytes (L1). Inputs a multiple of 256 wide
+// (no trailing half superblock: the caller checks).
+template <bool SW>
+__device__ void xgemm_q4_body(const sml_kgemm & a) {
+    #pragma clang fp contract(off)
+    typedef long v1l;
+    constexpr int NM = SW ? 2 : 1;
+    const int n = a.cols, ng = n / 32, nsb = ng / 8, rows = a.rows, m_all = a.m_all;
+    const int tid = threadIdx.x, lane = tid & 63, c = lane >> 4, i16 = lane & 15;
+    const int wave = tid >> 6;
+    const int r0 = (int) blockIdx.x * 16, p0 = (int) blockIdx.y * 64 + wave * 16;
+    const int row = min(r0 + i16, rows - 1);
+    const uint8_t * plane[NM];
+    const uint8_t * fqb[NM];
+    const uint8_t * fdb[NM];
+    #pragma unroll
+    for (int k = 0; k < NM; k++) {
+        const sml_kmat & mk = a.inl ? a.m0[k] : a.mats[k];
+        plane[k] = mk.plane[0] + (size_t) row * (n / 2) + 16 * c;
+        fqb[k] = mk.sqmq + (size_t) row * ng * 2;
+        fdb[k] = (const uint8_t *) mk.sdmd + (size_t) row * nsb * 4;
+    }
+    // the A operand's activation row (position p0 + i16) and the lane's four
+    // output positions' fields
+    const int8_t * qrow = a.q + (size_t) min(p0 + i16, m_all - 1) * n + 16 * c;
+    const float * srow[4];
+    const int32_t * urow[4];
+    #pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const size_t pr = (size_t) min(p0 + 4 * c + r, m_all - 1);
+        srow[r] = a.scale + pr * ng;
+        urow[r] = a.sums + pr * ng;
+    }
+    float ch[NM][4][8];
+    #pragma unroll
+    for (int k = 0; k < NM; k++)
+        #pragma unroll
+        for (int r = 0; r < 4; r++)
+            #pragma unroll
+            for (int j = 0; j < 8; j++) ch[k][r][j] = 0.0f;
+    for (int b = 0; b < nsb; b++) {
+        v4u w[NM][2], fq[NM];
+        uint32_t fd[NM];
+        v4u aq[4];
+        #pragma unroll
+        for (int k = 0; k < NM; k++) {
+            #pragma unroll
+            for (int p = 0; p < 2; p++) w[k][p] = gld<v4u>(plane[k] + (size_t) b * 128 + p * 64);
+            fq[k] = gld<v4u>(fqb[k] + (size_t) b * 16);
+            fd[k] = gld<uint32_t>(fdb[k] + (size_t) b * 4);
+        }
+        #pragma unroll
+        for (int u = 0; u < 4; u++) aq[u] = *(const v4u *) (qrow + (size_t) b * 256 + u * 64);
+        float sv[4][8];
+        int uv[4][8];
+        #pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float4 s0 = *(const float4 *) (srow[r] + 8 * b), s1 = *(const float4 *) (srow[r] + 8 * b + 4);
+            const int4 u0 = *(const int4 *) (urow[r] + 8 * b), u1 = *(const int4 *) (urow[r] + 8 * b + 4);
+            sv[r][0] = s0.x; sv[r][1] = s0.y; sv[r][2] = s0.z; sv[r][3] = s0.w;
+            sv[r][4] = s1.x; sv[r][5] = s1.y; sv[r][6] = s1.z; sv[r][7] = s1.w;
+            uv[r][0] = u0.x; uv[r][1] = u0.y; uv[r][2] = u0.z; uv[r][3] = u0.w;
+            uv[r][4] = u1.x; uv[r][5] = u1.y; uv[r][6] = u1.z; uv[r][7] = u1.w;
+        }
+        // the operands: an 8-byte k-slice of every group in every lane, the
+        // same permutation of k for A and B (see mgemm_q4_body)
+        v1l av[8];
+        #pragma unroll
+        for (int u = 0; u < 4; u++) {
+            v2u x, y;
+            xslice(aq[u], x, y);
+            av[2 * u] = (v1l) (((unsigned long) x.y << 32) | x.x);
+            av[2 * u + 1] = (v1l) (((unsigned long) y.y << 32) | y.x);
+        }
+        v2u wx[NM][2], wy[NM][2];
+        #pragma unroll
+        for (int k = 0; k < NM; k++)
+            #pragma unroll
+            for (int p = 0; p < 2; p++) xslice(w[k][p], wx[k][p], wy[k][p]);
+        #pragma unroll
+        for (int j = 0; j < 8; j++) {
+            #pragma unroll
+            for (int k = 0; k < NM; k++) {
+                const v2u ww = (j & 2) ? wy[k][j >> 2] : wx[k][j >> 2];
+                const v2u cd = (j & 1) ? ((ww >> 4u) & 0x0F0F0F0Fu) : (ww & 0x0F0F0F0Fu);
+                v4i d = {0, 0, 0, 0};
+                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], (v1l) (((unsigned long) cd.y << 32) | cd.x), d, 0, 0, 0);
+                const uint32_t f = fq[k][j >> 1] >> (16 * (j & 1));
+                const float wsc = h2f((uint16_t) (fd[k] & 0xFFFFu)) * (float) (f & 0xFFu);
+                const float wmn = h2f((uint16_t) (fd[k] >> 16)) * ((float) ((f >> 8) & 0xFFu) - 127.0f);
+                #pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float s = sv[r][j];
+                    ch[k][r][j] = __builtin_fmaf(wsc, s * (float) d[r], ch[k][r][j]);
+                    ch[k][r][j] = __builtin_fmaf(wmn, s * (float) uv[r][j], ch[k][r][j]);
+                }
+            }
+        }
+    }
+    if (r0 + i16 >= rows) return;
+    #pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int p = p0 + 4 * c + r;
+        if (p >= m_all) continue;
+        float v[NM];
+        #pragma unroll
+        for (int k = 0; k < NM; k++) {
+            const float (&q)[8] = ch[k][r];
+            v[k] = ((q[0] + q[4]) + (q[1] + q[5])) + ((q[2] + q[6]) + (q[3] + q[7]));
+        }
+        float * y = a.y + (size_t) p * rows;
+        const int rr = r0 + i16;
+        if constexpr (SW) {
+            y[rr] = silu_ref(v[0]) * v[1];                                       // sml/sml-run.c:416-426
+        } else {
+            float o = v[0];
+            if (a.bias) o += a.bias[rr];
+            if (a.resid) o = a.resid[(size_t) p * rows + rr] + o;
+            y[rr] = o;
+        }
+    }
+}
+extern "C" __global__ __launch_bounds__(256) void sml_xgemm_q4(const sml_kgemm a) { xgemm_q4_body<false>(a); }
+extern "C" __global__ __launch_bounds__(256) void sml_xgemm_q4_s(const sml_kgemm a) { xgemm_q4_body<true>(a); }
 
 // ---------------------------------------------------------------- prompt GEMM on MFMA (Q4, per-256 activations)
 //

@@ -971,6 +971,40 @@ void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint1
                     (unsigned) hd, 0, st, &a);
 }
 
+// Exact mode's batched prompt rows: row b = position pos[b] of one sequence,
+// its q/k/v at b * qkv_stride of qkv. RoPE and the fp16 K/V write of every
+// row first (sml_ropekv: the decode kernels' rotation and rounding), then
+// the reference-order scores and P.V of every row (sml_attnx_scores /
+// sml_attnx_pv with a row dimension), as decoding each position computes
+// them. sc: nrows * n_head * n_ctx floats of scores.
+void op_attention_rows_exact(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * kc, uint16_t * vc,
+                             const float * cos_t, const float * sin_t, const int32_t * pos, int nrows, int n_head,
+                             int n_kv, int n_ctx, int n_pos, float * sc, float * out, int8_t * q_out, float * s_out,
+                             int32_t * u_out) {
+    const int hd = 128;                               // exact mode's head size
+    if (n_kv <= 0 || n_head % n_kv || n_head / n_kv > 8 || n_kv > 8)
+        hx_failf("attention shape (heads %d/%d) not supported", n_head, n_kv);
+    if (nrows < 1 || nrows > 65535 || n_pos < 1 || n_pos > n_ctx || n_ctx > 16384)
+        hx_failf("exact attention rows: %d rows over %d of %d positions", nrows, n_pos, n_ctx);
+    sml_kattn r;
+    memset(&r, 0, sizeof r);
+    r.q = qkv; r.k = qkv + (size_t) n_head * hd; r.v = r.k + (size_t) n_kv * hd;
+    r.qkv_stride = qkv_stride; r.kcache = kc; r.vcache = vc; r.cos_t = cos_t; r.sin_t = sin_t; r.pos = pos;
+    r.n_head = n_head; r.n_kv = n_kv;
+    hx_launch("sml_ropekv", (unsigned) nrows, 1, (unsigned) (hd / 8 * n_kv), 0, st, &r);
+    sml_kattnx x;
+    memset(&x, 0, sizeof x);
+    x.q = r.q; x.k = r.k; x.v = r.v; x.kc = kc; x.vc = vc; x.cos_t = cos_t; x.sin_t = sin_t;
+    x.pos = pos; x.sc = sc; x.out = out; x.q_out = q_out; x.s_out = s_out; x.u_out = u_out;
+    x.n_head = n_head; x.n_kv = n_kv; x.n_ctx = n_ctx;
+    x.inv = 1.0f / __builtin_sqrtf((float) hd);
+    x.qkv_stride = qkv_stride;
+    x.kv_written = 1;
+    hx_launch3("sml_attnx_scores", (unsigned) ((n_pos + 127) / 128), (unsigned) n_kv, (unsigned) nrows, 256, 0, st, &x);
+    const size_t lds = (size_t) ((n_ctx + 3) & ~3) * 4 + (size_t) 3 * 64 * 128 * 2;
+    hx_launch3("sml_attnx_pv", (unsigned) n_head, (unsigned) nrows, 1, 512, lds, st, &x);
+}
+
 int sml_hip_attention(float * q, const float * k, const float * v, uint16_t * kcache, uint16_t * vcache,
                       const float * cos_t, const float * sin_t, const int32_t * pos,
                       int n_head, int n_kv, int hd, int n_ctx, float * part, float * out) {
@@ -1399,6 +1433,25 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngro
     const int per256 = regime == GEMM_PER256;
     if (swiglu && (bias || resid)) hx_failf("SwiGLU GEMM takes no bias or residual");
     if ((uint64_t) rows * (uint64_t) cols >= (1ull << 32)) hx_failf("matrix too large for one GEMM launch");
+    if (regime == GEMM_REF) {
+        // exact mode's batched prompt: Q4 inputs a multiple of 256 wide, 16
+        // weight rows x 64 positions per workgroup
+        if (nbits != 4 || cols % 256 || count || ngroups != 1 || m_all < 1 || (uint64_t) m_all * cols >= (1ull << 32))
+            hx_failf("the exact batched GEMM takes one Q4 matrix 256-aligned (%d bits, %d columns)", nbits, cols);
+        sml_kgemm a;
+        memset(&a, 0, sizeof a);
+        a.mats = tab; a.nmat = swiglu ? 2 : 1; a.cols = cols; a.rows = rows;
+        a.m_all = m_all; a.mmax = mmax;
+        a.q = q; a.scale = scale; a.sums = sums; a.y = y; a.bias = bias; a.resid = resid;
+        if (hk) {
+            a.inl = 1;
+            a.m0[0] = hk[0];
+            if (swiglu) a.m0[1] = hk[1];
+        }
+        hx_launch3(swiglu ? "sml_xgemm_q4_s" : "sml_xgemm_q4", (unsigned) ((rows + 15) / 16),
+                   (unsigned) ((m_all + 63) / 64), 1, 256, 0, st, &a);
+        return;
+    }
     if (!count && m_all > 16) {
         // prompt-sized: Q4 and Q6 with per-256 activations on the prompt MFMA
         // GEMM (tiles of 128 rows, SwiGLU 64, x PGEMM_BM positions); anything

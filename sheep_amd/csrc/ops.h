@@ -63,6 +63,7 @@ enum {
     GEMM_PER32 = 0,     // per-32 activations; Q4 above 8 rows on MFMA (fp32 order differs from the GEMV's)
     GEMM_PER256 = 1,    // per-256 activations; Q4 on MFMA with the integer superblock epilogue
     GEMM_EXACT = 2,     // per-32 activations, every row the GEMV's arithmetic bit for bit
+    GEMM_REF = 3,       // exact mode: per-32 activations, every row the exact (reference-order) GEMV's bit for bit
 };
 void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngroups, int swiglu, int nbits, int rows, int cols,
              const int32_t * count, int m_all, int mt, int mmax, const int8_t * q, const float * scale,
@@ -100,6 +101,13 @@ void op_attention(hipStream_t st, const float * q, const float * k, const float 
 // q256 (decode steps, causal 0, of an even head count only). n_pos bounds
 // every entry's position as in op_attention (the flash prompt form splits
 // the whole n_ctx range).
+// Exact mode's batched prompt rows (head_dim 128): every row's K/V written,
+// then each row's reference-order attention over positions 0..pos[b];
+// sc holds nrows * n_head * n_ctx floats of scores.
+void op_attention_rows_exact(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * kc, uint16_t * vc,
+                             const float * cos_t, const float * sin_t, const int32_t * pos, int nrows, int n_head,
+                             int n_kv, int n_ctx, int n_pos, float * sc, float * out, int8_t * q_out, float * s_out,
+                             int32_t * u_out);
 void op_attention_batch(hipStream_t st, const float * qkv, int qkv_stride, uint16_t * const * kc_slots,
                         uint16_t * const * vc_slots, const int32_t * slot, size_t layer_off, const float * cos_t,
                         const float * sin_t, const int32_t * pos, int nseq, int n_head, int n_kv, int hd, int n_ctx,

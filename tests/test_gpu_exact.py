@@ -417,3 +417,40 @@ def test_exact_greedy_64_equals_reference(decoder_file, name):
     assert len(set(ref)) >= 8, f"the reference's greedy ids are not diverse: {ref}"
     first = next((i for i, (a, b) in enumerate(zip(gpu, ref)) if a != b), None)
     assert first is None, f"step {first}: gpu {gpu[first]} reference {ref[first]}"
+
+
+@needs_ref
+@pytest.mark.parametrize("name,n", [("dense", 130), ("inorder", 64), ("qwenish", 77)])
+def test_exact_batched_prompt_equals_reference(decoder_file, name, n):
+    """Exact mode reads a prompt batched (level 1: 64-position chunks through
+    the reference-order Q4 GEMM, sml_xgemm_q4, and the row form of the
+    reference-order attention), and its logits equal the reference stepping
+    the same ids through sml_forward bit for bit; so do 4 greedy steps after
+    it. Chunk boundaries inside the prompt (130 = 64 + 64 + 2), one whole
+    chunk (64), Qwen-shaped layers (77). The same prompt read a token at a
+    time (level 0) gives the same bits."""
+    p = decoder_file(name)
+    V = DECODERS[name]["n_vocab"]
+    ids = np.random.default_rng(n).integers(0, V, n).astype(np.int32)
+    rm = ob.RefModel(p, 256, threads=min(16, os.cpu_count() or 1))
+    try:
+        for pos, tok in enumerate(ids):
+            want = rm.forward(int(tok), pos)
+        wants, toks = [want], [int(np.argmax(want))]
+        for i in range(4):
+            wants.append(rm.forward(toks[-1], n + i))
+            toks.append(int(np.argmax(wants[-1])))
+    finally:
+        rm.close()
+    for level in (1, 0):
+        d = sa.Decoder(p, n_ctx=256, exact=True)
+        try:
+            assert d.exact
+            d.prompt_mode(level)
+            got = [d.prefill(ids, 0, V)]
+            for i in range(4):
+                got.append(d.step(toks[i], n + i, V))
+        finally:
+            d.close()
+        for i, (g, w) in enumerate(zip(got, wants)):
+            same_bits(g, w, f"{name} level {level} {'prompt' if i == 0 else f'step {i}'}")

@@ -13,7 +13,8 @@ prompt with sml_prefill under SML_PROMPT_SB=0 (equal to stepping, bit for
 bit), then decodes with sml_forward; per step it keeps the greedy id, a
 digest of the logits' bytes, the top 8 and the logits' spread.
 
-- exact mode: the GPU reads the prompt and greedy-decodes on its own argmax;
+- exact mode: the GPU reads the prompt (batched, in 64-position chunks of the
+  reference-order GEMM and attention) and greedy-decodes on its own argmax;
   every step's logits have the reference's digest (equal bit for bit), so the
   ids are identical at every step.
 - fast mode (the default kernels, the throughput path): teacher-forced on the
@@ -38,6 +39,7 @@ flash attention with its KV range split and merged) and is graded per step.
 import hashlib
 import importlib.util
 import os
+import time
 
 import numpy as np
 import pytest
@@ -95,7 +97,9 @@ def test_full_decode_exact_then_fast(tmp_path, name):
         exact_logits = []
         try:
             assert d.exact
+            t0 = time.perf_counter()
             lg = d.prefill(prompt, 0, V)
+            print(f"{name} exact prompt of {P} ids (batched, reference order): {time.perf_counter() - t0:.2f} s")
             for i in range(S):
                 assert (digest(lg) == FIX[f"{name}_digest"][i]).all(), (
                     f"{name} step {i}: logits differ from the reference's; top ids {np.argsort(-lg)[:4]} "
