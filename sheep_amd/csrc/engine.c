@@ -940,9 +940,11 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
 // matrix streamed once per chunk; the last position's residual then goes
 // through the decode tail (final norm, head, greedy pick). The ids are
 // already in G.hist.
-//  - level 1: chunks of MAX_SLOTS; every product is the GEMV's arithmetic and
-//    the attention the decode kernel's, so the cache, the residuals and the
-//    logits equal reading the prompt a token at a time, bit for bit.
+//  - level 1: chunks of 32 positions (16 with MoE layers); every product is
+//    the GEMV's arithmetic and the attention the decode kernel's, so the
+//    cache, the residuals and the logits equal reading the prompt a token at
+//    a time, bit for bit.
+//  - exact mode: chunks of 64 through the reference-order GEMM and attention.
 //  - level 2: chunks of pb (512) positions in the reference's prompt regime
 //    (activations per 256 values, integer superblock sums: the CPU engine's
 //    default prompt arithmetic, sml/sml-run.c:1929-1945), Q4 products on the
@@ -952,7 +954,12 @@ static void prefill_rows(int slot, int pos0, int n) {
     // exact mode: the reference-order products and attention, in chunks of
     // xchunk positions
     const int regime = G.exact ? GEMM_REF : G.prompt_level >= 2 ? GEMM_PER256 : GEMM_EXACT;
-    const int chunk = G.exact ? G.xchunk : G.prompt_level >= 2 ? G.pb : MAX_SLOTS;
+    // level 1: 32 positions a chunk (the exact-regime GEMM's widest form),
+    // 16 where MoE layers take part (the expert kernels' row limit)
+    int moe = 0;
+    for (int L = 0; L < G.n_layer; L++) moe |= G.L[L].moe != NULL;
+    const int c1 = moe ? MAX_SLOTS : (G.rrows < 32 ? G.rrows : 32);
+    const int chunk = G.exact ? G.xchunk : G.prompt_level >= 2 ? G.pb : c1;
     if (chunk < 1) hx_failf("exact prompt chunk of %d rows", chunk);
     int last = 0;
     for (int p0 = 0; p0 < n; p0 += chunk) {

@@ -3426,14 +3426,17 @@ extern "C" __global__ __launch_bounds__(256) void sml_moe_combine(const sml_kmoe
 //
 // The GEMV's chunk-per-lane streaming with M activation rows: each weight
 // chunk is unpacked once and dotted with every row's int8 codes from LDS.
-// The input is taken in passes of 64*GEMM_NI chunks (4096 columns); each pass
+// The input is taken in passes of 64*NI chunks (4096 columns at NI 2; the
+// 32-row form takes passes of 2048, so its staging fits the LDS); each pass
 // issues its weight loads, then stages that slice of every row's codes and
-// (s, s*sum) pairs in LDS. Group e of the grid's y dimension uses matrix
-// table entry e (an expert) and its own activation slots.
+// (s, s*sum) pairs in LDS. A lane takes chunks lane, lane+64, ... in order
+// whatever NI is, so the rows' arithmetic is the GEMV's at every M. Group e
+// of the grid's y dimension uses matrix table entry e (an expert) and its
+// own activation slots.
 #define GEMM_NI 2
-template <int NB, int RB, int MT, bool SW, int WG = 256>
+template <int NB, int RB, int MT, bool SW, int WG = 256, int NI = GEMM_NI>
 __device__ void gemm_body(const sml_kgemm & a) {
-    constexpr int NI = GEMM_NI, TILE = WAVE * NI;
+    constexpr int TILE = WAVE * NI;
     extern __shared__ __align__(16) uint8_t lds[];
     int8_t * lq = (int8_t *) lds;                       // [MT][TILE * 32]
     float2 * lsc = (float2 *) (lds + MT * TILE * 32);   // [MT][TILE]
@@ -3617,7 +3620,15 @@ __device__ void gemm_body(const sml_kgemm & a) {
     extern "C" __global__ __launch_bounds__(256) void sml_gemm_q##NB##_s_m##MT(const sml_kgemm a) {       \
         gemm_body<NB, 4, MT, true>(a);                                                                   \
     }
-#define GEMM_WIDTH(NB) GEMM_KERNEL(NB, 1) GEMM_KERNEL(NB, 4) GEMM_KERNEL(NB, 8) GEMM_KERNEL(NB, 16)
+// 32 rows (prompt chunks read at level 1): passes of 2048 columns
+#define GEMM_KERNEL_32(NB)                                                                               \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemm_q##NB##_m32(const sml_kgemm a) {           \
+        gemm_body<NB, 2, 32, false, 256, 1>(a);                                                          \
+    }                                                                                                    \
+    extern "C" __global__ __launch_bounds__(256) void sml_gemm_q##NB##_s_m32(const sml_kgemm a) {         \
+        gemm_body<NB, 2, 32, true, 256, 1>(a);                                                           \
+    }
+#define GEMM_WIDTH(NB) GEMM_KERNEL(NB, 1) GEMM_KERNEL(NB, 4) GEMM_KERNEL(NB, 8) GEMM_KERNEL(NB, 16) GEMM_KERNEL_32(NB)
 GEMM_WIDTH(2) GEMM_WIDTH(3) GEMM_WIDTH(4) GEMM_WIDTH(5) GEMM_WIDTH(6) GEMM_WIDTH(7) GEMM_WIDTH(8)
 // Wider workgroups (suffix _w<threads>): the same rows per wave, more waves
 // sharing one staging of the activation rows per pass

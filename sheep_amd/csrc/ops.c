@@ -1408,7 +1408,7 @@ int sml_hip_gptq_time(const sml_hip_gptq * const * mats, int ncopy, const float 
 
 // ------------------------------------------------------------ small-M GEMM
 
-int gemm_mt(int m) { return m <= 1 ? 1 : m <= 4 ? 4 : m <= 8 ? 8 : 16; }
+int gemm_mt(int m) { return m <= 1 ? 1 : m <= 4 ? 4 : m <= 8 ? 8 : m <= 16 ? 16 : 32; }
 
 int gemm_exact(int regime, int m_all) {
     if (regime == GEMM_EXACT) return 1;
@@ -1452,10 +1452,12 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngro
                    (unsigned) ((m_all + 63) / 64), 1, 256, 0, st, &a);
         return;
     }
-    if (!count && m_all > 16) {
+    // the widest small-M launch: 32 rows in the exact regime (VALU), else 16
+    const int msmall = regime == GEMM_EXACT ? 32 : 16;
+    if (!count && m_all > msmall) {
         // prompt-sized: Q4 and Q6 with per-256 activations on the prompt MFMA
         // GEMM (tiles of 128 rows, SwiGLU 64, x PGEMM_BM positions); anything
-        // else in slices of 16 rows through the small-M kernels
+        // else in slices of msmall rows through the small-M kernels
         if (per256 && (nbits == 4 || nbits == 6) && cols % 256 == 0 && env_int("SML_PGEMM", 1)) {
             const int rt = swiglu ? 64 : 128;
             const uint64_t tiles = (uint64_t) ((rows + rt - 1) / rt) * (uint64_t) ((m_all + PGEMM_BM - 1) / PGEMM_BM);
@@ -1471,16 +1473,17 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngro
             hx_launch(pname, (unsigned) tiles, 1, 256, nbits == 6 ? PGEMM_LDS6 : PGEMM_LDS, st, &a);
             return;
         }
-        const int ng = cols / 32;
-        for (int s = 0; s < m_all; s += 16) {
-            const int k = m_all - s < 16 ? m_all - s : 16;
+        // (the exact regime's VALU kernel takes 32 rows a weight read)
+        const int ng = cols / 32, sl = msmall;
+        for (int s = 0; s < m_all; s += sl) {
+            const int k = m_all - s < sl ? m_all - s : sl;
             op_gemm(st, tab, hk, 1, swiglu, nbits, rows, cols, NULL, k, gemm_mt(k), k, q + (size_t) s * cols,
                     scale + (size_t) s * ng, sums + (size_t) s * ng, y + (size_t) s * rows, bias,
                     resid ? resid + (size_t) s * rows : NULL, regime);
         }
         return;
     }
-    if (mt != 1 && mt != 4 && mt != 8 && mt != 16) hx_failf("small-M GEMM takes at most 16 rows");
+    if (mt != 1 && mt != 4 && mt != 8 && mt != 16 && (mt != 32 || count)) hx_failf("small-M GEMM of %d rows", mt);
     if (!count && (m_all < 1 || m_all > mt)) hx_failf("small-M GEMM of %d rows", m_all);
     sml_kgemm a;
     memset(&a, 0, sizeof a);
@@ -1581,8 +1584,9 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngro
         const int w = m_t == 1 ? 256 : wg;
         if (w == 256) snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d", nbits, swiglu ? "_s" : "", m_t);
         else snprintf(name, sizeof name, "sml_gemm_q%d%s_m%d_w%d", nbits, swiglu ? "_s" : "", m_t, w);
-        const size_t lds = (size_t) m_t * GEMM_TILE * (32 + 8);
-        const int rpw = 8 * w / 256;                    // rows (SwiGLU: outputs) per workgroup
+        // 32 rows: passes of half the columns, one gate/up pair a wave
+        const size_t lds = (size_t) m_t * (m_t == 32 ? GEMM_TILE / 2 : GEMM_TILE) * (32 + 8);
+        const int rpw = (m_t == 32 && swiglu ? 4 : 8) * w / 256;   // rows (SwiGLU: outputs) per workgroup
         hx_launch(name, (unsigned) ((rows + rpw - 1) / rpw), (unsigned) ngroups, (unsigned) w, lds, st, &a);
         if (m_t >= mt) break;
         lo = m_t;

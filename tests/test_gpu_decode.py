@@ -275,6 +275,29 @@ def test_batched_prompt_fills_context(tiny, n):
     assert np.corrcoef(outs[2], outs[0])[0, 1] > 0.999
 
 
+@pytest.mark.parametrize("nbits", [3, 6, 8])
+def test_batched_prompt_level1_other_widths(tmp_path, nbits):
+    """Level 1 at other widths (the 32-row exact-regime GEMM of every width:
+    2048-column passes, one gate/up pair a wave): a 70-id prompt (two chunks
+    of 32 and a ragged 6) equals reading it a token at a time, bit for bit,
+    and so does the step after it."""
+    p = tmp_path / f"w{nbits}.ssf"
+    sa.synth_model(p, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, qkv_bias=True,
+                   random_perm=True, nbits=nbits, seed=40 + nbits)
+    ids = np.random.default_rng(nbits).integers(0, 2000, 70).astype(np.int32)
+    outs = {}
+    for level in (0, 1):
+        d = sa.Decoder(p, n_ctx=128)
+        try:
+            d.prompt_mode(level)
+            lg = d.prefill(ids, 0, 2000)
+            outs[level] = (lg, d.step(int(np.argmax(lg)), 70, 2000))
+        finally:
+            d.close()
+    np.testing.assert_array_equal(outs[1][0], outs[0][0], err_msg="prompt logits")
+    np.testing.assert_array_equal(outs[1][1], outs[0][1], err_msg="the step after")
+
+
 def test_batched_prompt_into_other_slots(tiny):
     """sml_gpu_prefill_slot batched into slots 1 and 2 (levels 1 and 2) leaves
     each slot's cache as reading the prompt a token at a time does: the
