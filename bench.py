@@ -659,6 +659,9 @@ def main():
     ap.add_argument("--ingest", action="store_true", help="only re-quantize the GPTQ-4 4096 x 14336 tensor")
     ap.add_argument("--gemv-timeline", action="store_true",
                     help="only the roofline GEMV's in-kernel timeline (entry, first weight word, last, exit)")
+    ap.add_argument("--batched-trace", action="store_true",
+                    help="only the 16-sequence batched step, --steps steps after a marker copy, direct launches "
+                         "(run under rocprofv3; summarise with --trace-summary)")
     ap.add_argument("--widths", action="store_true",
                     help="only the GEMV at every SSF width and the GPTQ-4 layout (4096x14336, 14336x4096)")
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
@@ -695,6 +698,8 @@ def main():
             res = {"width_sweep": width_sweep(work, iters=50)}
         elif a.decode_trace:
             res = {"decode_trace": decode_trace(work, a.decode_trace, a.steps, a.exact)}
+        elif a.batched_trace:
+            res = {"batched_trace": batched_trace(work, a.steps)}
         elif a.prompt_only >= 0:
             res = {"prompt_reading": prompt_only(work, a.prompt_only, a.prompt if a.prompt > 0 else 3960)}
         else:
@@ -730,6 +735,34 @@ def decode_trace(work, model="llama", steps=32, exact=False):
     finally:
         dec.close()
     return {"model": model, "exact": exact, "decode_positions": f"{N_CTX - steps}..{N_CTX - 1}", "steps": steps}
+
+
+def batched_trace(work, steps=10, ns=16, pos0=1024):
+    """For a kernel trace of the 16-sequence batched step (per-256 regime):
+    the Llama-3-8B-shaped file with direct launches (SML_GRAPH=0), ns slots
+    with 8-id prompts ending at pos0 - 1, one untimed step, a 16-byte copy
+    (sml_copy_stream, the marker), then `steps` steps at positions pos0 + 1..
+    (the bench line's batched_decode leg, launched one kernel at a time)."""
+    os.environ["SML_GRAPH"] = "0"
+    path = os.path.join(work, "llama_batched_trace.ssf")
+    sa.synth_model(path, n_ctx_train=N_CTX, **LLAMA)
+    V = LLAMA["n_vocab"]
+    dec = sa.Decoder(path, n_ctx=N_CTX)
+    try:
+        dec.slots(ns)
+        for b in range(ns):
+            dec.prefill_slot(b, (np.arange(8, dtype=np.int32) * 7 + b) % V, pos0 - 8, V)
+        toks = list(range(1, ns + 1))
+        dec.step_multi(toks, [pos0] * ns, list(range(ns)), V)
+        a, b = sa.DevBuf(64), sa.DevBuf(64)
+        assert sa.lib().sml_hip_copy(b.ptr, a.ptr, 16) == 0
+        sa.sync()
+        for i in range(steps):
+            dec.step_multi(toks, [pos0 + 1 + i] * ns, list(range(ns)), V)
+        sa.sync()
+    finally:
+        dec.close()
+    return {"sequences": ns, "positions": f"{pos0 + 1}..{pos0 + steps}", "steps": steps}
 
 
 def trace_summary(out_dir, steps):
