@@ -338,7 +338,9 @@ class Decoder:
         if not ok:
             raise HipError(f"sml_gpu_open: {why.value.decode(errors='replace')}")
         of = c_int()
-        self.n_layer = lib().sml_gpu_layers(ctypes.byref(of))
+        # layers whose matrices stay in HBM (a split streams the rest), of n_layer
+        self.gpu_layers = lib().sml_gpu_layers(ctypes.byref(of))
+        self.n_layer = of.value
         self.n_ctx = n_ctx
         self.exact = bool(lib().sml_gpu_exact())
 

@@ -104,6 +104,17 @@ static struct {
     int pb;                    // positions per chunk of a level-2 prompt
     int rows_ok;               // 1: the batched body can run this model (-1: not checked yet)
     int rows_ready;            // the batched body's buffers are allocated
+    // A layer split: layers below nres keep their matrices in HBM. The rest
+    // are streamed: their matrices were laid out in the staging region and
+    // kept as pinned host images, one copied back into the region ahead of
+    // each use of its layer. nres == n_layer: no split.
+    int nres;
+    void * stage;
+    size_t stage_cap;
+    void ** img;               // [n_layer]: a streamed layer's image, else NULL
+    size_t * img_n;
+    float * mid_host;          // pinned: the hidden rows handed to a middle stage
+    int cur_pos;               // position of the first row of the body being launched
 } G;
 
 static int (*g_mid_fn)(float *, int, int);
@@ -283,9 +294,43 @@ static void launch_layer(int L) {
     gemv1(y->down, slot[0], SML_EPI_RESIDUAL, G.x, NULL, G.x);
 }
 
+// A streamed layer's matrices into the staging region. The copy follows the
+// previous layer's kernels on the stream, so it overwrites the region only
+// once they are done with it.
+static void stage_layer(int L) {
+    if (L >= G.nres) HX(hipMemcpyAsync(G.stage, G.img[L], G.img_n[L], hipMemcpyHostToDevice, G.st));
+}
+
+// A middle stage of a split model (sml_gpu_set_middle): after the layers on
+// the card, the caller's function runs the next g_mid_layers layers on the
+// n hidden rows (positions pos0..pos0+n-1) in host memory, in place, and the
+// layers after them continue here (sml/sml-gpu-fwd.c:1582-1587,1748-1754).
+// It returns 0 on failure, which fails the call.
+static int mid_on(void) { return G.nres < G.n_layer && g_mid_fn && g_mid_layers > 0; }
+
+static void middle(float * rows, int n, int pos0) {
+    if (G.nres + g_mid_layers > G.n_layer)
+        hx_failf("a middle stage of %d layers after %d of %d", g_mid_layers, G.nres, G.n_layer);
+    if (!G.mid_host) HX(hipHostMalloc((void **) &G.mid_host, (size_t) (G.rrows > 1 ? G.rrows : 1) * G.E * 4, 0));
+    if (n > (G.rrows > 1 ? G.rrows : 1)) hx_failf("a middle stage of %d rows", n);
+    const size_t b = (size_t) n * G.E * 4;
+    HX(hipMemcpyAsync(G.mid_host, rows, b, hipMemcpyDeviceToHost, G.st));
+    HX(hipStreamSynchronize(G.st));
+    if (!g_mid_fn(G.mid_host, pos0, n)) hx_failf("the middle stage failed at position %d", pos0);
+    HX(hipMemcpyAsync(rows, G.mid_host, b, hipMemcpyHostToDevice, G.st));
+}
+
 static void launch_body(void) {
     op_embed(G.st, G.emb, G.hist, G.pos, pdev(G.perm_emb), G.x);
-    for (int L = 0; L < G.n_layer; L++) launch_layer(L);
+    for (int L = 0; L < G.n_layer; L++) {
+        if (L == G.nres && mid_on()) {
+            middle(G.x, 1, G.cur_pos);
+            L += g_mid_layers - 1;
+            continue;
+        }
+        stage_layer(L);
+        launch_layer(L);
+    }
 }
 
 static void launch_tail(void) {
@@ -336,6 +381,7 @@ static int bucket_cap(int k) { const int c = (k + 1) * G.bkt_len; return c < G.n
 
 // one decode step's body at position pos (the device copy of pos holds it)
 static void run_body(int pos) {
+    G.cur_pos = pos;
     const int k = bucket_of(pos);
     G.pos_cap = bucket_cap(k);
     if (G.use_graph) HX(hipGraphLaunch(G.g_body[k], G.st));
@@ -359,7 +405,9 @@ static void release(void) {
         for (int i = 0; i < 17; i++)
             for (int j = 0; j < 2; j++)
                 for (int k = 0; k < NBKT; k++) if (G.g_multi[i][j][k]) hipGraphExecDestroy(G.g_multi[i][j][k]);
-        for (int i = 0; i < G.nmats; i++) { if (G.mats[i]->mem) hipFree(G.mats[i]->mem); free(G.mats[i]); }
+        for (int i = 0; i < G.nmats; i++) { if (G.mats[i]->mem && !G.mats[i]->placed) hipFree(G.mats[i]->mem); free(G.mats[i]); }
+        if (G.img) for (int L = 0; L < G.n_layer; L++) if (G.img[L]) hipHostFree(G.img[L]);
+        if (G.mid_host) hipHostFree(G.mid_host);
         if (G.L) for (int L = 0; L < G.n_layer; L++) if (G.L[L].moe) { moe_free(G.L[L].moe); G.L[L].moe = NULL; }
         for (int i = 0; i < G.ndev; i++) hipFree(G.dev[i]);
         if (G.lg_host) hipHostFree(G.lg_host);
@@ -372,6 +420,8 @@ static void release(void) {
     }
     hx.jb = outer;
     free(G.L);
+    free(G.img);
+    free(G.img_n);
     memset(&G, 0, sizeof G);
     ops_set_exact(0);
 }
@@ -407,21 +457,86 @@ static const char * unsupported(const ssf_file * f) {
     return NULL;
 }
 
+// Bytes the matrices of layer L take in HBM (at most: q, k and v counted
+// apart, as when they are not stacked).
+static size_t layer_bytes(const ssf_file * f, int L) {
+    static const char * nm[] = { "blk.%d.attn_q.weight", "blk.%d.attn_k.weight", "blk.%d.attn_v.weight",
+                                 "blk.%d.attn_output.weight", "blk.%d.ffn_gate.weight", "blk.%d.ffn_up.weight",
+                                 "blk.%d.ffn_down.weight" };
+    size_t b = 0;
+    for (size_t i = 0; i < sizeof nm / sizeof nm[0]; i++) {
+        const ssf_record * r = ssf_findf(f, nm[i], L);
+        if (r && r->kind == SSF_KIND_QUANT && r->nbits >= 2 && r->nbits <= 8 && r->cols % 128 == 0)
+            b += mat_block_bytes((int) r->rows, (int) r->cols, (int) r->nbits);
+    }
+    return b;
+}
+
+// How many leading layers keep their matrices in HBM (the reference's
+// gpu_layers, sml/sml-gpu-fwd.c:2028-2097): gpu_layers > 0, else
+// SML_GPU_LAYERS, else every layer when the matrices, every layer's K/V
+// cache, the embedding and head and SML_SPLIT_RESERVE_MB (1024) of scratch
+// fit in the free HBM; otherwise the leading layers that fit beside one
+// staging region. Streamed layers still compute here: their matrices cross
+// the host link ahead of each use, so a split gives the same bits as the
+// whole model on the card.
+static void split_plan(const ssf_file * f, int n_ctx, int gpu_layers) {
+    const int nl = G.n_layer;
+    int k = nl;
+    const int forced = gpu_layers > 0 ? gpu_layers : env_int("SML_GPU_LAYERS", 0);
+    size_t stage = 0;
+    if (forced > 0) {
+        k = forced < nl ? forced : nl;
+    } else {
+        size_t fr = 0, tot = 0;
+        if (hipMemGetInfo(&fr, &tot) == hipSuccess && fr) {
+            size_t fixed = (size_t) 2 * nl * n_ctx * G.KV * G.hd * 2, all = 0;
+            const ssf_record * er = ssf_find(f, "token_embd.weight"), * hr = ssf_find(f, "output.weight");
+            if (er && er->kind == SSF_KIND_QUANT) fixed += mat_block_bytes((int) er->rows, (int) er->cols, (int) er->nbits);
+            if (hr && hr->kind == SSF_KIND_QUANT) fixed += mat_block_bytes((int) hr->rows, (int) hr->cols, (int) hr->nbits);
+            fixed += (size_t) env_int("SML_SPLIT_RESERVE_MB", 1024) << 20;
+            for (int L = 0; L < nl; L++) {
+                const size_t b = layer_bytes(f, L);
+                all += b;
+                if (b > stage) stage = b;
+            }
+            if (fixed + all > fr) {
+                size_t used = 0;
+                k = 0;
+                while (k < nl && fixed + stage + used + layer_bytes(f, k) <= fr) used += layer_bytes(f, k++);
+                if (k < 1) k = 1;
+            }
+        }
+    }
+    G.nres = k;
+    if (k == nl) return;
+    for (int L = k; L < nl; L++) {
+        if (ssf_findf(f, "blk.%d.ffn_gate_inp.weight", L))
+            hx_failf("a layer split of a mixture-of-experts model (%d of %d layers) is not built", k, nl);
+        const size_t b = layer_bytes(f, L);
+        if (b > stage) stage = b;
+    }
+    if (env_int("SML_TILED", 0)) hx_failf("a layer split streams the matrices as stored (SML_TILED=1 is not taken)");
+    G.img = calloc((size_t) nl, sizeof(void *));
+    G.img_n = calloc((size_t) nl, sizeof(size_t));
+    if (!G.img || !G.img_n) hx_failf("out of host memory");
+    G.stage_cap = stage;
+    G.stage = dalloc(stage);
+}
+
 static void setup(const char * path, int want_ctx, int gpu_layers) {
     ssf_file f;
     char why[512];
     if (!ssf_open(&f, path, why, sizeof why)) hx_failf("%s", why);
     jmp_buf * outer = hx.jb;
     jmp_buf jb;
-    if (setjmp(jb)) { ssf_close(&f); hx.jb = outer; longjmp(*outer, 1); }
+    if (setjmp(jb)) { mat_place(NULL, 0); ssf_close(&f); hx.jb = outer; longjmp(*outer, 1); }
     hx.jb = &jb;
     const ssf_header * h = f.hdr;
     const char * no = unsupported(&f);
     if (no) hx_failf("this GPU path does not compute %s", no);
     G.n_layer = (int) h->n_layer; G.E = (int) h->n_embd; G.H = (int) h->n_head; G.KV = (int) h->n_head_kv;
     G.F = (int) h->n_ff; G.V = (int) h->n_vocab; G.eps = h->rms_eps;
-    if (gpu_layers > 0 && gpu_layers < G.n_layer)
-        hx_failf("a GPU/CPU layer split (%d of %d layers) is not built; every layer runs on the card", gpu_layers, G.n_layer);
     const int n_ctx = want_ctx > 0 ? want_ctx : h->n_ctx_train ? (int) h->n_ctx_train : 4096;
     G.n_ctx = n_ctx;
     const ssf_record * q0 = need(&f, "blk.%d.attn_q.weight", 0);
@@ -429,6 +544,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     if ((int) q0->rows % G.H || (G.hd != 128 && G.hd != 64) || G.KV <= 0 || G.H % G.KV || G.H / G.KV > 8)
         hx_failf("attention shape (heads %d/%d, head_dim %d) not supported", G.H, G.KV, G.hd);
     hx_init(env_int("SML_DEVICE", 0));
+    split_plan(&f, n_ctx, gpu_layers);
     HX(hipStreamCreateWithFlags(&G.st, hipStreamNonBlocking));
     HX(hipEventCreate(&G.e0));
     HX(hipEventCreate(&G.e1));
@@ -452,6 +568,7 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     const int qkv_rows = wrows[0] + wrows[1] + wrows[2];
     for (int L = 0; L < G.n_layer; L++) {
         eng_layer * y = &G.L[L];
+        if (L >= G.nres) mat_place(G.stage, G.stage_cap);
         const ssf_record * rq[3];
         for (int i = 0; i < 3; i++) {
             rq[i] = need(&f, wn[i], L);
@@ -496,6 +613,14 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
                 y->down->k.rows != G.E || y->down->cols != G.F)
                 hx_failf("layer %d has unexpected projection shapes", L);
             G.weight_bytes += y->gate->bytes + y->up->bytes + y->down->bytes;
+        }
+        if (L >= G.nres) {
+            // the layer's matrices as laid out in the staging region, kept on the host
+            const size_t used = mat_place_used();
+            mat_place(NULL, 0);
+            HX(hipHostMalloc(&G.img[L], used, 0));
+            HX(hipMemcpy(G.img[L], G.stage, used, hipMemcpyDeviceToHost));
+            G.img_n[L] = used;
         }
         y->an = f32_tensor(&f, "blk.%d.attn_norm.weight", L, G.E);
         y->fn = f32_tensor(&f, "blk.%d.ffn_norm.weight", L, G.E);
@@ -590,7 +715,9 @@ static void setup(const char * path, int want_ctx, int gpu_layers) {
     if (G.moe_first) G.pb = MAX_SLOTS;
     G.rrows = G.pb;
     G.rows_ok = -1;
-    G.use_graph = env_int("SML_GRAPH", 1) != 0;
+    // a split model launches directly: each streamed layer's copy sits
+    // between its neighbours' kernels, and a middle stage runs on the host
+    G.use_graph = env_int("SML_GRAPH", 1) != 0 && G.nres == G.n_layer;
     // position buckets: at most NBKT, none shorter than 512 positions
     // (SML_POS_BUCKETS=0: one, every launch covering the whole context)
     G.bkt_len = (G.n_ctx + NBKT - 1) / NBKT;
@@ -711,9 +838,10 @@ uint64_t sml_gpu_weight_bytes(void) { return G.open ? G.weight_bytes : 0; }
 const char * sml_gpu_last_error(void) { return hx.err; }
 int sml_gpu_exact(void) { return G.open && G.exact; }
 
+// Layers whose matrices stay in HBM, of how many (a split streams the rest).
 int sml_gpu_layers(int * of) {
     if (of) *of = G.open ? G.n_layer : 0;
-    return G.open ? G.n_layer : 0;
+    return G.open ? G.nres : 0;
 }
 
 // 0: prompts a token at a time through the decode graph; 1: batched, exact
@@ -875,6 +1003,14 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
     const int mt = gemm_mt(ns), sb = regime == GEMM_PER256;
     op_embed_rows(G.st, G.emb, tok, NULL, ns, pdev(G.perm_emb), G.mx);
     for (int L = 0; L < G.n_layer; L++) {
+        if (L == G.nres && mid_on()) {
+            // the rows of one prompt chunk (slot 0), positions cur_pos..
+            if (!causal) hx_failf("a middle stage serves one sequence, not a batched step");
+            middle(G.mx, ns, G.cur_pos);
+            L += g_mid_layers - 1;
+            continue;
+        }
+        stage_layer(L);
         eng_layer * y = &G.L[L];
         const int32_t * pp[1];
         int8_t * qq[1] = { G.maq };
@@ -950,6 +1086,7 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
 //    default prompt arithmetic, sml/sml-run.c:1929-1945), Q4 products on the
 //    prompt MFMA GEMM, attention a wave per position.
 static void prefill_rows(int slot, int pos0, int n) {
+    if (slot != 0 && mid_on()) hx_failf("a middle stage serves slot 0 only");
     rows_alloc();
     // exact mode: the reference-order products and attention, in chunks of
     // xchunk positions
@@ -965,6 +1102,7 @@ static void prefill_rows(int slot, int pos0, int n) {
     for (int p0 = 0; p0 < n; p0 += chunk) {
         const int nb = n - p0 < chunk ? n - p0 : chunk;
         G.pos_cap = pos0 + p0 + nb;
+        G.cur_pos = pos0 + p0;
         launch_rows(nb, G.hist + pos0 + p0, G.iota + pos0 + p0, G.slotid + (size_t) slot * G.rrows, regime, 1, 0);
         last = nb - 1;
     }
@@ -993,8 +1131,10 @@ const float * sml_gpu_prefill_slot(int slot, const int * ids, int pos0, int n) {
         jmp_buf jb;
         if (setjmp(jb)) { G.cur_slot = 0; hx.jb = outer; longjmp(*outer, 1); }
         hx.jb = &jb;
+        if (mid_on()) hx_failf("a middle stage serves slot 0 only");
         for (int i = 0; i < n; i++) {
             G.pos_cap = pos0 + i + 1;
+            G.cur_pos = pos0 + i;
             launch_body();
             if (i + 1 < n) launch_adv();
         }

@@ -66,6 +66,41 @@ static int tiled_on(void) {
     return on;
 }
 
+// A matrix's single allocation: its code planes, the (sq, mq) group fields,
+// the (sd, md) superblock fields and its descriptors, each 256-byte aligned.
+// Returns the total; off/sz receive each part's offset and size.
+static size_t mat_layout(int rows, int cols, int nbits, size_t off[6], size_t sz[6]) {
+    int pb[SSF_MAX_PLANES];
+    const int np = ssf_flat_planes(nbits, pb);
+    const size_t R = (size_t) rows, ng = (size_t) cols / 32, ns = (size_t) SSF_NSUPER(cols);
+    size_t tot = 0;
+    for (int i = 0; i < 3; i++) sz[i] = i < np ? R * ssf_plane_row_bytes(pb[i], cols) : 0;
+    sz[3] = R * ng * 2;          // (sq, mq) per group
+    sz[4] = R * ns * 4;          // (sd, md) per superblock
+    sz[5] = 3 * sizeof(sml_kmat);   // the descriptor, then a (gate, up) pair table (small-M GEMM tables)
+    for (int i = 0; i < 6; i++) { off[i] = tot; tot += al256(sz[i]); }
+    return tot;
+}
+
+size_t mat_block_bytes(int rows, int cols, int nbits) {
+    size_t off[6], sz[6];
+    return mat_layout(rows, cols, nbits, off, sz);
+}
+
+// Placement (a model's streamed layers): while a region is set, each upload
+// takes the next bytes of [base, base + cap) instead of an allocation of its
+// own, and its matrix is marked so that freeing it leaves that memory alone.
+static uint8_t * g_place;
+static size_t g_place_off, g_place_cap;
+
+void mat_place(void * base, size_t cap) {
+    g_place = (uint8_t *) base;
+    g_place_off = 0;
+    g_place_cap = base ? cap : 0;
+}
+
+size_t mat_place_used(void) { return g_place_off; }
+
 sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, const uint8_t * sq,
                          const uint16_t * md, const uint8_t * mq, int rows, int cols, int nbits,
                          int scale6, int minneg) {
@@ -74,12 +109,10 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
     int pb[SSF_MAX_PLANES];
     const int np = ssf_flat_planes(nbits, pb);
     const size_t R = (size_t) rows, ng = (size_t) cols / 32, ns = (size_t) SSF_NSUPER(cols);
-    size_t off[6], sz[6], tot = 0;
-    for (int i = 0; i < 3; i++) sz[i] = i < np ? R * ssf_plane_row_bytes(pb[i], cols) : 0;
-    sz[3] = R * ng * 2;          // (sq, mq) per group
-    sz[4] = R * ns * 4;          // (sd, md) per superblock
-    sz[5] = 3 * sizeof(sml_kmat);   // the descriptor, then a (gate, up) pair table (small-M GEMM tables)
-    for (int i = 0; i < 6; i++) { off[i] = tot; tot += al256(sz[i]); }
+    size_t off[6], sz[6];
+    const size_t tot = mat_layout(rows, cols, nbits, off, sz);
+    if (g_place && g_place_off + tot > g_place_cap)
+        hx_failf("a streamed layer's matrices exceed their %zu-byte staging region", g_place_cap);
     // the fields interleaved on the host: 8-bit (or widened 6-bit) values, min bias 127
     uint8_t * fq = malloc(sz[3]);
     uint16_t * fd = malloc(sz[4]);
@@ -105,13 +138,19 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
     if (setjmp(jb)) {
         hx.jb = outer;
         free(fq); free(fd);
-        if (m->mem) hipFree(m->mem);
+        if (m->mem && !m->placed) hipFree(m->mem);
         if (m->tiled_mem) hipFree(m->tiled_mem);
         free(m);
         longjmp(*outer, 1);
     }
     hx.jb = &jb;
-    m->mem = hx_malloc(tot);
+    if (g_place) {
+        m->mem = g_place + g_place_off;
+        m->placed = 1;
+        g_place_off += tot;
+    } else {
+        m->mem = hx_malloc(tot);
+    }
     uint8_t * base = (uint8_t *) m->mem;
     for (int i = 0; i < np; i++) {
         HX(hipMemcpy(base + off[i], planes[i], sz[i], hipMemcpyHostToDevice));
@@ -131,7 +170,7 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
     // Q4 with SML_TILED=1: the tiled copy the small-M MFMA GEMM streams (one
     // more copy of the codes and fields; without it the GEMM reads the rows
     // as they are)
-    if (nbits == 4 && cols % 256 == 0 && tiled_on()) {
+    if (nbits == 4 && cols % 256 == 0 && tiled_on() && !m->placed) {
         const size_t nt = (size_t) ((rows + 15) / 16) * (size_t) (cols / 256);
         m->tiled_mem = hx_malloc(nt * SML_TILE_Q4);
         sml_ktile t = { m->k.plane[0], m->k.sqmq, m->k.sdmd, (uint8_t *) m->tiled_mem, rows, cols };
@@ -412,7 +451,7 @@ sml_hip_mat * sml_hip_mat_from_file(const char * path, const char * name) {
 
 void mat_free(sml_hip_mat * m) {
     if (!m) return;
-    if (m->mem) HX(hipFree(m->mem));
+    if (m->mem && !m->placed) HX(hipFree(m->mem));
     if (m->tiled_mem) HX(hipFree(m->tiled_mem));
     free(m);
 }

@@ -15,6 +15,7 @@ struct sml_hip_mat {
     void * mem;          // the single allocation holding planes and fields
     void * tiled_mem;    // Q4: the MFMA GEMM's tiled copy (k.tiled), or NULL
     size_t bytes;        // planes + fields bytes (what one GEMV streams)
+    int placed;          // mem lies in a region the caller owns (mat_place): not freed here
 };
 
 
@@ -23,6 +24,13 @@ sml_hip_mat * mat_upload(const uint8_t * const planes[4], const uint16_t * sd, c
                          int scale6, int minneg);
 sml_hip_mat * mat_from_record(const ssf_file * f, const ssf_record * r);
 void mat_free(sml_hip_mat * m);
+// The bytes of one matrix's allocation (planes, fields, descriptors).
+size_t mat_block_bytes(int rows, int cols, int nbits);
+// Uploads after mat_place(base, cap) take consecutive bytes of that device
+// region instead of allocations of their own (base NULL: allocate again);
+// mat_place_used() is how far they reached.
+void mat_place(void * base, size_t cap);
+size_t mat_place_used(void);
 
 // Exact mode (the reference's float order in GEMVs, norms, attention, router)
 void ops_set_exact(int on);

@@ -88,15 +88,15 @@ def http(port, path, body=None, timeout=60):
         return r.read()
 
 
-def serve_turn(model, device, workdir, messages, env=None):
+def serve_turn(model, device, workdir, messages, env=None, args=()):
     """Start the server on the model, wait for /health, run one greedy chat
     turn, read /stats, stop the server. Returns (reply text, stats, log)."""
     port = free_port()
     log_path = os.path.join(workdir, f"server_{device}.log")
     with open(log_path, "w") as log:
-        print(f"starting sml-server --device {device} on port {port}", flush=True)
+        print(f"starting sml-server --device {device} {' '.join(args)} on port {port}", flush=True)
         p = subprocess.Popen([SERVER, "-m", model, "--port", str(port), "-c", "256", "--threads", "4",
-                              "--device", device], stdout=log, stderr=subprocess.STDOUT, cwd=workdir,
+                              "--device", device, *args], stdout=log, stderr=subprocess.STDOUT, cwd=workdir,
                              env=dict(os.environ, **(env or {})))
         try:
             deadline = time.time() + 90
@@ -151,6 +151,26 @@ def test_reference_server_on_this_library(tmp_path, mode):
         assert gpu_text == cpu_text, (gpu_text, cpu_text)
     else:
         assert gpu_text.split()[:4] == cpu_text.split()[:4], (gpu_text, cpu_text)
+
+
+def test_reference_server_hybrid_split(tmp_path):
+    """--device hybrid --gpu-layers 1 on a two-layer model: the library keeps
+    one layer's matrices on the card and streams the other's, the server
+    reports the split as hybrid (sml/sml-server.c:1596-1604), and in exact
+    mode the reply equals the CPU path's token for token."""
+    model = str(tmp_path / "chat.ssf")
+    sa.synth_model(model, n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000,
+                   qkv_bias=True, random_perm=True, seed=7)
+    add_vocab(model, 2000)
+    msgs = [{"role": "user", "content": "Name three rivers in Africa, one per line."}]
+    gpu_text, gpu_stats, gpu_log = serve_turn(model, "hybrid", str(tmp_path), msgs, {"SML_EXACT": "1"},
+                                              ("--gpu-layers", "1"))
+    assert gpu_stats["device"] == "hybrid", gpu_log[-2000:]
+    assert (gpu_stats["gpu_layers"], gpu_stats["gpu_of"]) == (1, 2), gpu_stats
+    cpu_text, cpu_stats, cpu_log = serve_turn(model, "cpu", str(tmp_path), msgs, {"SML_PROMPT_SB": "0"})
+    assert len(set(cpu_text.split())) >= 4, cpu_text
+    assert gpu_stats["last_gen"] == cpu_stats["last_gen"]
+    assert gpu_text == cpu_text, (gpu_text, cpu_text)
 
 
 @pytest.mark.parametrize("fail", ["open:40", "prefill:2", "step:90"])
