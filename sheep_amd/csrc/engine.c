@@ -1001,6 +1001,11 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
                         int causal, int head) {
     const size_t kvd = (size_t) G.KV * G.hd, qkv = (size_t) (G.H + 2 * G.KV) * G.hd, hq = (size_t) G.H * G.hd;
     const int mt = gemm_mt(ns), sb = regime == GEMM_PER256;
+    // a batched step leaves the down product's split-K sums to the next
+    // norm, which adds them as it normalizes (one launch instead of two;
+    // SML_KSUM_NORMQ=0: two)
+    ops_ksum_reset();
+    const int defer = head && !mid_on() && regime != GEMM_REF && env_int("SML_KSUM_NORMQ", 1);
     op_embed_rows(G.st, G.emb, tok, NULL, ns, pdev(G.perm_emb), G.mx);
     for (int L = 0; L < G.n_layer; L++) {
         if (L == G.nres && mid_on()) {
@@ -1017,7 +1022,8 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
         float * ss[1] = { G.mas };
         int32_t * uu[1] = { G.masum };
         pp[0] = pdev(y->perm_qkv[0]);
-        op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
+        if (ops_ksum_pending()) op_ksum_normq_rows(G.st, G.mx, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, sb);
+        else op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
         op_gemm(G.st, y->qkv->kdev, &y->qkv->k, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
                 G.mqkv, y->bias_qkv, NULL, regime);
         // the merge quantizes its output for the o product: per 32, or per
@@ -1058,15 +1064,18 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
                 NULL, NULL, regime);
         pp[0] = pdev(y->perm_down);
         op_normq_rows(G.st, G.mh, NULL, NULL, G.eps, G.F, ns, 1, pp, qq, ss, uu, NULL, sb);
+        ops_defer_ksum(defer);
         op_gemm(G.st, y->down->kdev, &y->down->k, 1, 0, y->down->nbits, G.E, G.F, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
                 G.mx, NULL, G.mx, regime);
+        ops_defer_ksum(0);
     }
     if (!head) return;
     const int32_t * pp[1] = { pdev(G.perm_head) };
     int8_t * qq[1] = { G.maq };
     float * ss[1] = { G.mas };
     int32_t * uu[1] = { G.masum };
-    op_normq_rows(G.st, G.mx, NULL, G.out_norm, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
+    if (ops_ksum_pending()) op_ksum_normq_rows(G.st, G.mx, G.out_norm, G.eps, G.E, ns, 1, pp, qq, ss, uu, sb);
+    else op_normq_rows(G.st, G.mx, NULL, G.out_norm, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
     op_gemm(G.st, G.head->kdev, &G.head->k, 1, 0, G.head->nbits, G.V, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mlog,
             NULL, NULL, regime);
 }

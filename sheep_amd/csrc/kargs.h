@@ -368,6 +368,13 @@ typedef struct {
     int ks, m, rows;
 } sml_kksum;
 
+// Split-K sums and the next normq of each row in one launch (s.rows == q.n;
+// q.x is unused: the rows come from the sums)
+typedef struct {
+    sml_kksum s;
+    sml_knormq2 q;
+} sml_kksumq;
+
 // out[t] = sum over j of w[t][j] * y[sel[t][j]][slot[t][j]], in choice order,
 // then + sg[t] * ysh[t] (the shared expert) when ysh is not NULL.
 typedef struct {

@@ -1013,6 +1013,12 @@ extern "C" __global__ __launch_bounds__(NORMQ_THREADS) void sml_normq(const sml_
     }
 }
 
+// Four values' squares added to a double sum, in sml_normq2's order (its
+// callers share it so that their sums agree bit for bit).
+__device__ __forceinline__ double ss_add4(double ss, float4 v) {
+    return ss + ((double) v.x * v.x + (double) v.y * v.y + (double) v.z * v.z + (double) v.w * v.w);
+}
+
 // Multi-workgroup form (the decode path's): workgroup b quantizes elements
 // 256b..256b+255 (one superblock) of each output; each reduces the full sum of
 // squares first. per256: the superblock's amax meets across the 4 waves in LDS
@@ -1043,10 +1049,7 @@ extern "C" __global__ __launch_bounds__(256) void sml_normq2(const sml_knormq2 a
     float sc = 1.0f;
     if (a.norm_w) {
         double ss = 0.0;
-        for (int i = tid * 4; i < n; i += 1024) {
-            const float4 v = *(const float4 *) (x + i);
-            ss += (double) v.x * v.x + (double) v.y * v.y + (double) v.z * v.z + (double) v.w * v.w;
-        }
+        for (int i = tid * 4; i < n; i += 1024) ss = ss_add4(ss, *(const float4 *) (x + i));
         #pragma unroll
         for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -4149,6 +4152,128 @@ MGEMM_KERNEL_P(1, 8, false, ) MGEMM_KERNEL_P(1, 8, true, _t)
     extern "C" __global__ __launch_bounds__(512) void sml_mgemm_q4_sb_r1_w8_p_k4##SUF(const sml_kgemm a) {    \
         mgemm_q4_body<false, true, 1, 8, true, TL, 4>(a); }
 MGEMM_KERNEL_K(false, ) MGEMM_KERNEL_K(true, _t)
+
+// sml_gemm_ksum and the sml_normq2 that follows it in one launch, one
+// workgroup of 256 threads a row. Each thread adds the slices of the
+// elements sml_normq2's thread tid sums (4 tid.., + 1024, ...), writes them
+// to y and to LDS, and sums their squares in that kernel's order; the norm
+// weights and permutations of the row go to LDS beside it. Then each wave
+// quantizes whole superblocks (wave w: w, w + 4, ...), 4 consecutive values
+// a lane: a superblock's (or a group's) max is a max over the same values as
+// sml_normq2's, and its codes, scales and sums follow the same formulas, so
+// every value equals the two launches' bit for bit. Needs 4 slices, a
+// residual, no bias, a norm, no exact mode, n % 32 == 0 and n <= 1024 NI;
+// dynamic LDS (2 + nout) * n * 4 bytes with permutations, 2 n * 4 without.
+template <int NI, bool PERM>
+__device__ void ksum_normq_body(const sml_kksumq & a) {
+    extern __shared__ float xs[];                  // [n] the row, [n] the norm weights, [nout][n] permutations
+    __shared__ double red[4];
+    const int n = a.q.n, tid = threadIdx.x;
+    float * ws = xs + n;
+    int * ps = (int *) (ws + n);
+    const size_t ro = (size_t) blockIdx.x * n, nn = (size_t) a.s.m * n;
+    const float * part = a.s.part + ro;
+    // every load of the thread first, before any store to memory (a store
+    // could alias a later load and hold it back), and unconditional (indexes
+    // past the row clamped to its last float4), so they all go out
+    // together: the 4 slices, the residual, the norm weights and the first
+    // output's permutation of each of the thread's NI float4s. (No bias: the
+    // products this follows have none.)
+    // (the norm weights and the permutation go straight to LDS: stores there
+    // cannot alias the loads; a clamped index rewrites the row's last float4
+    // with its own value)
+    float4 p[4][NI], r[NI];
+    #pragma unroll
+    for (int t = 0; t < NI; t++) {
+        const int i = min(tid * 4 + t * 1024, n - 4);
+        #pragma unroll
+        for (int k = 0; k < 4; k++) p[k][t] = *(const float4 *) (part + (size_t) k * nn + i);
+        r[t] = *(const float4 *) (a.s.resid + ro + i);
+    }
+    // the scheduler otherwise interleaves these with waits for the first
+    // loads before the last ones are issued
+    __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+    for (int t = 0; t < NI; t++) {
+        const int i = min(tid * 4 + t * 1024, n - 4);
+        *(float4 *) (ws + i) = *(const float4 *) (a.q.norm_w + i);
+        if (PERM) *(int4 *) (ps + i) = *(const int4 *) (a.q.perm[0] + i);
+    }
+    // the sums are unconditional too (a float4 past the row adds 0 to the
+    // sum of squares), so that no load is sunk into the stores' branch
+    double ss = 0.0;
+    float4 v[NI];
+    #pragma unroll
+    for (int t = 0; t < NI; t++) {
+        const bool in = tid * 4 + t * 1024 < n;
+        v[t] = p[0][t];
+        #pragma unroll
+        for (int k = 1; k < 4; k++) {
+            v[t].x += p[k][t].x; v[t].y += p[k][t].y; v[t].z += p[k][t].z; v[t].w += p[k][t].w;
+        }
+        v[t].x = r[t].x + v[t].x; v[t].y = r[t].y + v[t].y; v[t].z = r[t].z + v[t].z; v[t].w = r[t].w + v[t].w;
+        ss = ss_add4(ss, in ? v[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f));
+    }
+    #pragma unroll
+    for (int t = 0; t < NI; t++) {
+        const int i = tid * 4 + t * 1024;
+        if (i < n) {
+            *(float4 *) (a.s.y + ro + i) = v[t];
+            *(float4 *) (xs + i) = v[t];
+        }
+    }
+    for (int o = 1; o < a.q.nout; o++)
+        if (a.q.perm[o])
+            for (int i = tid * 4; i < n; i += 1024) *(int4 *) (ps + (size_t) o * n + i) = *(const int4 *) (a.q.perm[o] + i);
+    #pragma unroll
+    for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const double tot = red[0] + red[1] + red[2] + red[3];
+    const float msq = (float) (tot / (double) n);
+    const float sc = 1.0f / sqrtf(msq + a.q.eps);
+    const size_t bg = (size_t) blockIdx.x * (n / 32);
+    const int lane = tid & 63;
+    for (int j0 = (tid >> 6) * 256; j0 < n; j0 += 1024) {
+        const int e = j0 + 4 * lane;                 // this lane's 4 values
+        const bool ok = e < n;                       // a last superblock may be partial (whole groups)
+        for (int o = 0; o < a.q.nout; o++) {
+            float v[4];
+            float m = 0.0f;
+            #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[i] = 0.0f;
+                if (ok) {
+                    const int src = a.q.perm[o] ? ps[(size_t) o * n + e + i] : e + i;
+                    v[i] = xs[src] * sc * ws[src];
+                }
+                m = fmaxf(m, fabsf(v[i]));
+            }
+            const float amax = a.q.per256 ? wave_max(m) : max8(m);
+            const float s = amax / 127.0f;
+            const float is = s > 0.0f ? 1.0f / s : 0.0f;
+            int w = 0, sum = 0;
+            #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = quant1(v[i], is);
+                sum += t;
+                w |= (t & 0xFF) << (8 * i);
+            }
+            sum = isum8(sum);
+            if (!ok) continue;
+            *(int *) (a.q.q[o] + ro + e) = w;
+            if ((lane & 7) == 0) { a.q.scale[o][bg + (e >> 5)] = s; a.q.sums[o][bg + (e >> 5)] = sum; }
+        }
+    }
+}
+
+// one kernel per NI (n <= 1024 NI) and first output's permutation (_p)
+#define KSUMQ_KERNEL(NI) \
+    extern "C" __global__ __launch_bounds__(256) void sml_ksum_normq_##NI(const sml_kksumq a) { ksum_normq_body<NI, false>(a); } \
+    extern "C" __global__ __launch_bounds__(256) void sml_ksum_normq_##NI##_p(const sml_kksumq a) { ksum_normq_body<NI, true>(a); }
+KSUMQ_KERNEL(1)
+KSUMQ_KERNEL(2)
+KSUMQ_KERNEL(4)
 
 // The split-K slices added in slice order, then the bias and the residual
 // (the one-launch epilogue's order: v = sum + bias; y = resid + v)

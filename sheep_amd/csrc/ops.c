@@ -11,6 +11,10 @@
 
 static size_t al256(size_t x) { return (x + 255u) & ~(size_t) 255u; }
 
+// the split-K sums op_gemm left for the next normq (ops_defer_ksum)
+static int g_defer, g_pending;
+static sml_kksum g_pend;
+
 int sml_hip_init(int device, char * why, int nwhy) {
     HX_ENTRY(0);
     hx_init(device);
@@ -478,6 +482,46 @@ void op_normq(hipStream_t st, float * x, const float * resid, const float * w, f
               int nout, const int32_t * const * perm, int8_t * const * q, float * const * scale,
               int32_t * const * sums, float * normed, int per256) {
     op_normq_rows(st, x, resid, w, eps, n, 1, nout, perm, q, scale, sums, normed, per256);
+}
+
+// Deferred split-K sums. While deferral is on, a split-K product leaves its
+// slices, and the next op_ksum_normq_rows adds them as it normalizes the
+// rows (sml_ksum_normq: one launch for sml_gemm_ksum + sml_normq2, the same
+// bits); op_ksum_flush adds them alone.
+void ops_defer_ksum(int on) { g_defer = on; }
+void ops_ksum_reset(void) { g_defer = g_pending = 0; }
+int ops_ksum_pending(void) { return g_pending; }
+
+void op_ksum_flush(hipStream_t st) {
+    if (!g_pending) return;
+    g_pending = 0;
+    hx_launch("sml_gemm_ksum", (unsigned) (((size_t) g_pend.m * g_pend.rows + 255) / 256), 1, 256, 0, st, &g_pend);
+}
+
+void op_ksum_normq_rows(hipStream_t st, float * x, const float * w, float eps, int n, int rows, int nout,
+                        const int32_t * const * perm, int8_t * const * q, float * const * scale,
+                        int32_t * const * sums, int per256) {
+    if (!g_pending) hx_failf("no split-K sums pending");
+    int np = 0;
+    for (int i = 0; i < nout && i < 3; i++) np += perm[i] != NULL;
+    const size_t lds = (size_t) (2 + (np ? nout : 0)) * n * 4;
+    if (!w || g_exact || nout < 1 || nout > 3 || n % 32 || n > 4096 || lds > 65536 || g_pend.ks != 4 || g_pend.bias || !g_pend.resid || g_pend.y != x ||
+        g_pend.rows != n ||
+        g_pend.m != rows) {
+        op_ksum_flush(st);
+        op_normq_rows(st, x, NULL, w, eps, n, rows, nout, perm, q, scale, sums, NULL, per256);
+        return;
+    }
+    sml_kksumq a;
+    memset(&a, 0, sizeof a);
+    a.s = g_pend;
+    a.q.norm_w = w; a.q.eps = eps; a.q.n = n; a.q.nout = nout; a.q.per256 = per256;
+    for (int i = 0; i < nout; i++) { a.q.perm[i] = perm[i]; a.q.q[i] = q[i]; a.q.scale[i] = scale[i]; a.q.sums[i] = sums[i]; }
+    g_pending = 0;
+    const int ni = n <= 1024 ? 1 : n <= 2048 ? 2 : 4;   // float4s a thread holds
+    char name[32];
+    snprintf(name, sizeof name, "sml_ksum_normq_%d%s", ni, perm[0] ? "_p" : "");
+    hx_launch(name, (unsigned) rows, 1, 256, lds, st, &a);
 }
 
 void op_normq_rows(hipStream_t st, float * x, const float * resid, const float * w, float eps, int n, int rows,
@@ -1596,7 +1640,8 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngro
             if (kslices > 1) {
                 sml_kksum k;
                 k.part = a.part; k.bias = bias; k.resid = resid; k.y = y; k.ks = kslices; k.m = m_all; k.rows = rows;
-                hx_launch("sml_gemm_ksum", (unsigned) (((size_t) m_all * rows + 255) / 256), 1, 256, 0, st, &k);
+                if (g_defer) { g_pend = k; g_pending = 1; }
+                else hx_launch("sml_gemm_ksum", (unsigned) (((size_t) m_all * rows + 255) / 256), 1, 256, 0, st, &k);
             }
             return;
         }

@@ -86,6 +86,16 @@ void op_embed(hipStream_t st, const sml_hip_mat * m, const int32_t * tok, const 
 void op_embed_rows(hipStream_t st, const sml_hip_mat * m, const int32_t * tok, const int32_t * pos, int rows,
                    const int32_t * perm, float * x);
 // op_normq over rows vectors: every pointer advances by n (scale, sums by n/32) per row
+// While deferral is on, a split-K product leaves its slice sums pending;
+// op_ksum_normq_rows adds them (into x, which must be the product's output)
+// while it normalizes and quantizes the rows, op_ksum_flush adds them alone.
+void ops_defer_ksum(int on);
+void ops_ksum_reset(void);      // off, and anything pending dropped (a failed call's leftovers)
+int ops_ksum_pending(void);
+void op_ksum_flush(hipStream_t st);
+void op_ksum_normq_rows(hipStream_t st, float * x, const float * w, float eps, int n, int rows, int nout,
+                        const int32_t * const * perm, int8_t * const * q, float * const * scale,
+                        int32_t * const * sums, int per256);
 void op_normq_rows(hipStream_t st, float * x, const float * resid, const float * w, float eps, int n, int rows,
                    int nout, const int32_t * const * perm, int8_t * const * q, float * const * scale,
                    int32_t * const * sums, float * normed, int per256);

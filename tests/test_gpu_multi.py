@@ -336,3 +336,42 @@ def test_step_multi_split_k_down_product(tmp_path, monkeypatch):
             if top[1] - top[0] > 1e-2 * r.std():
                 assert int(np.argmax(a)) == int(np.argmax(r)), (i, b)
     assert differ, "the split form did not run"
+
+
+def test_step_multi_split_k_sums_fused_with_the_next_norm(tmp_path, monkeypatch):
+    """The per-256 batched step leaves the split-K down product's slice sums
+    to the next layer's (and the head's) norm, which adds them as it
+    normalizes and quantizes each row (sml_ksum_normq). Every step's logits
+    equal the two launches' (SML_KSUM_NORMQ=0: sml_gemm_ksum, then
+    sml_normq2) bit for bit: 12 sequences, a 1536-wide residual (rows that
+    are no multiple of 1024 values), permuted columns and q/k/v biases. The
+    one-pass product (SML_MGEMM_KS=1) differs, so the split form ran."""
+    monkeypatch.delenv("SML_MULTI", raising=False)
+    monkeypatch.delenv("SML_MULTI_EXACT_MAX", raising=False)
+    p = tmp_path / "ksumq.ssf"
+    sa.synth_model(p, n_layer=3, n_embd=1536, n_head=12, n_head_kv=4, n_ff=5120, n_vocab=2000, qkv_bias=True,
+                   random_perm=True, seed=79)
+    prompts = [[(5 * b + 3 * j + 2) % 2000 for j in range(1 + b % 4)] for b in range(12)]
+    outs = {}
+    for name, fused, ks in (("two", "0", "4"), ("fused", "1", "4"), ("one-pass", "1", "1")):
+        monkeypatch.setenv("SML_KSUM_NORMQ", fused)
+        monkeypatch.setenv("SML_MGEMM_KS", ks)
+        print(name, flush=True)
+        d = sa.Decoder(p, n_ctx=64)
+        try:
+            d.slots(len(prompts))
+            last = [d.prefill_slot(b, pr, 0, 2000) for b, pr in enumerate(prompts)]
+            toks, pos, out = [int(np.argmax(l)) for l in last], [len(pr) for pr in prompts], []
+            for i in range(3):
+                lg = d.step_multi(toks, pos, list(range(len(prompts))), 2000)
+                out.append(lg)
+                toks = [int(np.argmax(l)) for l in lg]
+                pos = [x + 1 for x in pos]
+            outs[name] = out
+        finally:
+            d.close()
+    for i in range(3):
+        a, r = outs["fused"][i], outs["two"][i]
+        bad = np.flatnonzero(a.view(np.uint32) != r.view(np.uint32))
+        assert bad.size == 0, (i, bad.size, bad[:4])
+    assert not np.array_equal(outs["fused"][0], outs["one-pass"][0]), "the split form did not run"
