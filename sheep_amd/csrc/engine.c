@@ -1001,11 +1001,15 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
                         int causal, int head) {
     const size_t kvd = (size_t) G.KV * G.hd, qkv = (size_t) (G.H + 2 * G.KV) * G.hd, hq = (size_t) G.H * G.hd;
     const int mt = gemm_mt(ns), sb = regime == GEMM_PER256;
-    // a batched step leaves the down product's split-K sums to the next
-    // norm, which adds them as it normalizes (one launch instead of two;
-    // SML_KSUM_NORMQ=0: two)
+    // SML_KSUM_NORMQ=1: a batched step leaves the down product's split-K
+    // sums to the next norm, which adds them as it normalizes (one launch
+    // instead of two, the same bits). Off by default: replayed from a graph,
+    // the 16-sequence Llama step measured 3.061 ms against 3.047 for the two
+    // launches (directly launched, 3.15 against 3.19: the graph already hides
+    // most of a launch boundary, and the one workgroup a row of the fused
+    // kernel takes longer than the two wide launches' bodies).
     ops_ksum_reset();
-    const int defer = head && !mid_on() && regime != GEMM_REF && env_int("SML_KSUM_NORMQ", 1);
+    const int defer = head && !mid_on() && regime != GEMM_REF && env_int("SML_KSUM_NORMQ", 0);
     op_embed_rows(G.st, G.emb, tok, NULL, ns, pdev(G.perm_emb), G.mx);
     for (int L = 0; L < G.n_layer; L++) {
         if (L == G.nres && mid_on()) {
