@@ -113,7 +113,8 @@ static struct {
     size_t stage_cap;
     void ** img;               // [n_layer]: a streamed layer's image, else NULL
     size_t * img_n;
-    float * mid_host;          // pinned: the hidden rows handed to a middle stage
+    float * mid_host;          // pinned: the hidden rows handed to a middle stage (n_ctx rows)
+    float * px;                // a split model's prompt: the residual rows of every position
     int cur_pos;               // position of the first row of the body being launched
 } G;
 
@@ -311,8 +312,9 @@ static int mid_on(void) { return G.nres < G.n_layer && g_mid_fn && g_mid_layers 
 static void middle(float * rows, int n, int pos0) {
     if (G.nres + g_mid_layers > G.n_layer)
         hx_failf("a middle stage of %d layers after %d of %d", g_mid_layers, G.nres, G.n_layer);
-    if (!G.mid_host) HX(hipHostMalloc((void **) &G.mid_host, (size_t) (G.rrows > 1 ? G.rrows : 1) * G.E * 4, 0));
-    if (n > (G.rrows > 1 ? G.rrows : 1)) hx_failf("a middle stage of %d rows", n);
+    // room for a whole prompt (a split model's prompt hands over every row)
+    if (!G.mid_host) HX(hipHostMalloc((void **) &G.mid_host, (size_t) G.n_ctx * G.E * 4, 0));
+    if (n > G.n_ctx) hx_failf("a middle stage of %d rows", n);
     const size_t b = (size_t) n * G.E * 4;
     HX(hipMemcpyAsync(G.mid_host, rows, b, hipMemcpyDeviceToHost, G.st));
     HX(hipStreamSynchronize(G.st));
@@ -997,9 +999,67 @@ int sml_gpu_slots(int ns) {
 // all rows. causal: rows may be positions of one sequence (a prompt chunk),
 // so K/V are written for every row before any row attends. head: logits of
 // every row into G.mlog; otherwise the residuals stay in G.mx.
+// Layer L of the batched body for the ns rows of G.mx (defer: leave the
+// down product's split-K sums to the next norm).
+static void rows_layer(int L, int ns, const int32_t * pos, const int32_t * slot, int regime, int causal, int defer) {
+    const size_t kvd = (size_t) G.KV * G.hd, qkv = (size_t) (G.H + 2 * G.KV) * G.hd, hq = (size_t) G.H * G.hd;
+    const int mt = gemm_mt(ns), sb = regime == GEMM_PER256;
+    eng_layer * y = &G.L[L];
+    const int32_t * pp[1];
+    int8_t * qq[1] = { G.maq };
+    float * ss[1] = { G.mas };
+    int32_t * uu[1] = { G.masum };
+    pp[0] = pdev(y->perm_qkv[0]);
+    if (ops_ksum_pending()) op_ksum_normq_rows(G.st, G.mx, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, sb);
+    else op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
+    op_gemm(G.st, y->qkv->kdev, &y->qkv->k, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
+            G.mqkv, y->bias_qkv, NULL, regime);
+    // the merge quantizes its output for the o product: per 32, or per
+    // 256 in decode steps of an even head count (SML_MERGE_Q256=0 leaves
+    // that to its own launch)
+    const int fuse_q = y->perm_o < 0 &&
+                       (!sb || (!causal && G.H % 2 == 0 && G.hd == 128 && env_int("SML_MERGE_Q256", 1)));
+    if (regime == GEMM_REF) {
+        // exact mode: one sequence (slot 0), the reference's order
+        if (!causal) hx_failf("exact mode batches prompts only");
+        op_attention_rows_exact(G.st, G.mqkv, (int) qkv, G.kc + (size_t) L * G.n_ctx * kvd,
+                                G.vc + (size_t) L * G.n_ctx * kvd, G.rc, G.rs, pos, ns, G.H, G.KV, G.n_ctx,
+                                G.pos_cap, G.mpart, G.matt, fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL,
+                                fuse_q ? G.masum : NULL);
+    } else {
+        op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
+                           G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.pos_cap, G.mpart, G.matt,
+                           fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL,
+                           causal ? (regime == GEMM_EXACT ? 1 : 2) : 0, gemm_exact(regime, ns), sb);
+    }
+    if (!fuse_q) {
+        pp[0] = pdev(y->perm_o);
+        op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, sb);
+    }
+    op_gemm(G.st, y->o->kdev, &y->o->k, 1, 0, y->o->nbits, G.E, (int) hq, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
+            G.mx, NULL, G.mx, regime);
+    if (y->moe) {
+        op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 0, NULL, NULL, NULL, NULL, G.mxn, sb);
+        y->moe->per256 = sb;
+        op_moe(G.st, y->moe, G.mxn, ns, G.mx, G.mx);
+        y->moe->per256 = 0;
+        return;
+    }
+    pp[0] = pdev(y->perm_gu[0]);
+    op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
+    const sml_kmat guk[2] = { y->gate->k, y->up->k };
+    op_gemm(G.st, y->gu_tab, guk, 1, 1, y->gate->nbits, G.F, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mh,
+            NULL, NULL, regime);
+    pp[0] = pdev(y->perm_down);
+    op_normq_rows(G.st, G.mh, NULL, NULL, G.eps, G.F, ns, 1, pp, qq, ss, uu, NULL, sb);
+    ops_defer_ksum(defer);
+    op_gemm(G.st, y->down->kdev, &y->down->k, 1, 0, y->down->nbits, G.E, G.F, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
+            G.mx, NULL, G.mx, regime);
+    ops_defer_ksum(0);
+}
+
 static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const int32_t * slot, int regime,
                         int causal, int head) {
-    const size_t kvd = (size_t) G.KV * G.hd, qkv = (size_t) (G.H + 2 * G.KV) * G.hd, hq = (size_t) G.H * G.hd;
     const int mt = gemm_mt(ns), sb = regime == GEMM_PER256;
     // SML_KSUM_NORMQ=1: a batched step leaves the down product's split-K
     // sums to the next norm, which adds them as it normalizes (one launch
@@ -1020,58 +1080,7 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
             continue;
         }
         stage_layer(L);
-        eng_layer * y = &G.L[L];
-        const int32_t * pp[1];
-        int8_t * qq[1] = { G.maq };
-        float * ss[1] = { G.mas };
-        int32_t * uu[1] = { G.masum };
-        pp[0] = pdev(y->perm_qkv[0]);
-        if (ops_ksum_pending()) op_ksum_normq_rows(G.st, G.mx, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, sb);
-        else op_normq_rows(G.st, G.mx, NULL, y->an, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
-        op_gemm(G.st, y->qkv->kdev, &y->qkv->k, 1, 0, y->qkv->nbits, (int) qkv, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
-                G.mqkv, y->bias_qkv, NULL, regime);
-        // the merge quantizes its output for the o product: per 32, or per
-        // 256 in decode steps of an even head count (SML_MERGE_Q256=0 leaves
-        // that to its own launch)
-        const int fuse_q = y->perm_o < 0 &&
-                           (!sb || (!causal && G.H % 2 == 0 && G.hd == 128 && env_int("SML_MERGE_Q256", 1)));
-        if (regime == GEMM_REF) {
-            // exact mode: one sequence (slot 0), the reference's order
-            if (!causal) hx_failf("exact mode batches prompts only");
-            op_attention_rows_exact(G.st, G.mqkv, (int) qkv, G.kc + (size_t) L * G.n_ctx * kvd,
-                                    G.vc + (size_t) L * G.n_ctx * kvd, G.rc, G.rs, pos, ns, G.H, G.KV, G.n_ctx,
-                                    G.pos_cap, G.mpart, G.matt, fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL,
-                                    fuse_q ? G.masum : NULL);
-        } else {
-            op_attention_batch(G.st, G.mqkv, (int) qkv, G.kc_tab, G.vc_tab, slot, (size_t) L * G.n_ctx * kvd,
-                               G.rc, G.rs, pos, ns, G.H, G.KV, G.hd, G.n_ctx, G.pos_cap, G.mpart, G.matt,
-                               fuse_q ? G.maq : NULL, fuse_q ? G.mas : NULL, fuse_q ? G.masum : NULL,
-                               causal ? (regime == GEMM_EXACT ? 1 : 2) : 0, gemm_exact(regime, ns), sb);
-        }
-        if (!fuse_q) {
-            pp[0] = pdev(y->perm_o);
-            op_normq_rows(G.st, G.matt, NULL, NULL, G.eps, (int) hq, ns, 1, pp, qq, ss, uu, NULL, sb);
-        }
-        op_gemm(G.st, y->o->kdev, &y->o->k, 1, 0, y->o->nbits, G.E, (int) hq, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
-                G.mx, NULL, G.mx, regime);
-        if (y->moe) {
-            op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 0, NULL, NULL, NULL, NULL, G.mxn, sb);
-            y->moe->per256 = sb;
-            op_moe(G.st, y->moe, G.mxn, ns, G.mx, G.mx);
-            y->moe->per256 = 0;
-            continue;
-        }
-        pp[0] = pdev(y->perm_gu[0]);
-        op_normq_rows(G.st, G.mx, NULL, y->fn, G.eps, G.E, ns, 1, pp, qq, ss, uu, NULL, sb);
-        const sml_kmat guk[2] = { y->gate->k, y->up->k };
-        op_gemm(G.st, y->gu_tab, guk, 1, 1, y->gate->nbits, G.F, G.E, NULL, ns, mt, ns, G.maq, G.mas, G.masum, G.mh,
-                NULL, NULL, regime);
-        pp[0] = pdev(y->perm_down);
-        op_normq_rows(G.st, G.mh, NULL, NULL, G.eps, G.F, ns, 1, pp, qq, ss, uu, NULL, sb);
-        ops_defer_ksum(defer);
-        op_gemm(G.st, y->down->kdev, &y->down->k, 1, 0, y->down->nbits, G.E, G.F, NULL, ns, mt, ns, G.maq, G.mas, G.masum,
-                G.mx, NULL, G.mx, regime);
-        ops_defer_ksum(0);
+        rows_layer(L, ns, pos, slot, regime, causal, defer);
     }
     if (!head) return;
     const int32_t * pp[1] = { pdev(G.perm_head) };
@@ -1098,6 +1107,46 @@ static void launch_rows(int ns, const int32_t * tok, const int32_t * pos, const 
 //    (activations per 256 values, integer superblock sums: the CPU engine's
 //    default prompt arithmetic, sml/sml-run.c:1929-1945), Q4 products on the
 //    prompt MFMA GEMM, attention a wave per position.
+// A split model's prompt, layer by layer: each layer runs over every chunk
+// before the next starts, so a streamed layer crosses the host link once per
+// prompt instead of once per chunk. The residual rows of all n positions
+// wait in G.px; the chunks of one layer run in order, so each chunk's
+// attention finds the earlier positions' K/V of that layer written, and
+// every chunk computes what the chunk-major order does (the same bits). A
+// middle stage receives all n rows at once, as the reference's does
+// (sml/sml-gpu-fwd.c:1582-1587).
+static void prefill_layers(int slot, int pos0, int n, int chunk, int regime) {
+    if (!G.px) G.px = dalloc((size_t) G.n_ctx * G.E * 4);
+    float * const mx = G.mx;
+    jmp_buf * outer = hx.jb;
+    jmp_buf jb;
+    if (setjmp(jb)) { G.mx = mx; G.pos_cap = G.n_ctx; hx.jb = outer; longjmp(*outer, 1); }
+    hx.jb = &jb;
+    ops_ksum_reset();
+    for (int p0 = 0; p0 < n; p0 += chunk) {
+        const int nb = n - p0 < chunk ? n - p0 : chunk;
+        op_embed_rows(G.st, G.emb, G.hist + pos0 + p0, NULL, nb, pdev(G.perm_emb), G.px + (size_t) p0 * G.E);
+    }
+    for (int L = 0; L < G.n_layer; L++) {
+        if (L == G.nres && mid_on()) {
+            middle(G.px, n, pos0);
+            L += g_mid_layers - 1;
+            continue;
+        }
+        stage_layer(L);
+        for (int p0 = 0; p0 < n; p0 += chunk) {
+            const int nb = n - p0 < chunk ? n - p0 : chunk;
+            G.pos_cap = pos0 + p0 + nb;
+            G.mx = G.px + (size_t) p0 * G.E;
+            rows_layer(L, nb, G.iota + pos0 + p0, G.slotid + (size_t) slot * G.rrows, regime, 1, 0);
+        }
+    }
+    G.mx = mx;
+    G.pos_cap = G.n_ctx;
+    hx.jb = outer;
+    HX(hipMemcpyAsync(G.x, G.px + (size_t) (n - 1) * G.E, (size_t) G.E * 4, hipMemcpyDeviceToDevice, G.st));
+}
+
 static void prefill_rows(int slot, int pos0, int n) {
     if (slot != 0 && mid_on()) hx_failf("a middle stage serves slot 0 only");
     rows_alloc();
@@ -1111,6 +1160,10 @@ static void prefill_rows(int slot, int pos0, int n) {
     const int c1 = moe ? MAX_SLOTS : (G.rrows < 32 ? G.rrows : 32);
     const int chunk = G.exact ? G.xchunk : G.prompt_level >= 2 ? G.pb : c1;
     if (chunk < 1) hx_failf("exact prompt chunk of %d rows", chunk);
+    if (G.nres < G.n_layer) {
+        prefill_layers(slot, pos0, n, chunk, regime);
+        return;
+    }
     int last = 0;
     for (int p0 = 0; p0 < n; p0 += chunk) {
         const int nb = n - p0 < chunk ? n - p0 : chunk;

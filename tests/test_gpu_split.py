@@ -8,6 +8,10 @@ region in HBM ahead of each use, and the same kernels run on the same bytes.
 So every path of a split model gives the whole model's logits bit for bit:
 stepping, the three prompt levels, exact mode and the batched step.
 
+A split model reads a prompt layer by layer (each streamed layer crosses the
+host link once per prompt), every chunk computing what it computes in the
+whole model's chunk-by-chunk order.
+
 A middle stage (sml_gpu_set_middle, sml/sml-gpu.h:30-34) receives the hidden
 rows after the layers on the card and runs the next layers itself. Checked
 on a file whose middle layer adds nothing (its o and down steps are zero), so
@@ -179,9 +183,11 @@ def test_middle_stage(tmpdir_s):
         for i, (g, w) in enumerate(zip(got, whole)):
             same_bits(g, w, f"identity middle stage for the quiet layer, call {i}")
         steps = [(40, 1, True), (41, 1, True), (42, 1, True)]
-        want = ([(i, 1, True) for i in range(40)] + steps          # level 0: a token at a time
-                + [(0, 32, True), (32, 8, True)] + steps           # level 1: chunks of 32
-                + [(0, 40, True)] + steps)                         # level 2: one chunk
+        # level 0 a token at a time; levels 1 and 2 read a split model's
+        # prompt layer by layer, so the stage gets every row at once
+        want = ([(i, 1, True) for i in range(40)] + steps
+                + [(0, 40, True)] + steps
+                + [(0, 40, True)] + steps)
         assert calls == want, calls
         # a stage that fails fails the call
         dec = sa.Decoder(p, n_ctx=256, gpu_layers=3)
