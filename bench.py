@@ -662,6 +662,9 @@ def main():
     ap.add_argument("--batched-trace", action="store_true",
                     help="only the 16-sequence batched step, --steps steps after a marker copy, direct launches "
                          "(run under rocprofv3; summarise with --trace-summary)")
+    ap.add_argument("--split", type=int, nargs="*", metavar="K",
+                    help="only the layer split: a 1024-id prompt (levels 2 and 1) and 16 decode steps with K of "
+                         "the 32 Llama layers' matrices in HBM (default K: 32 24 16)")
     ap.add_argument("--widths", action="store_true",
                     help="only the GEMV at every SSF width and the GPTQ-4 layout (4096x14336, 14336x4096)")
     ap.add_argument("--keep", action="store_true", help="keep the generated model file")
@@ -698,6 +701,8 @@ def main():
             res = {"width_sweep": width_sweep(work, iters=50)}
         elif a.decode_trace:
             res = {"decode_trace": decode_trace(work, a.decode_trace, a.steps, a.exact)}
+        elif a.split is not None:
+            res = {"split": split_leg(work, a.split or [32, 24, 16])}
         elif a.batched_trace:
             res = {"batched_trace": batched_trace(work, a.steps)}
         elif a.prompt_only >= 0:
@@ -735,6 +740,45 @@ def decode_trace(work, model="llama", steps=32, exact=False):
     finally:
         dec.close()
     return {"model": model, "exact": exact, "decode_positions": f"{N_CTX - steps}..{N_CTX - 1}", "steps": steps}
+
+
+def split_leg(work, ks, n=1024, steps=16):
+    """The Llama-3-8B-shaped file opened with gpu_layers = k for each k: the
+    other layers' matrices are streamed from pinned host memory ahead of
+    each use. A prompt of n ids at levels 2 and 1 (after a 64-id warm-up
+    read), then `steps` greedy steps from position n + 3; wall time around
+    each (a split model launches directly)."""
+    path = os.path.join(work, "llama_split.ssf")
+    sa.synth_model(path, n_ctx_train=N_CTX, **LLAMA)
+    V = LLAMA["n_vocab"]
+    ids = (np.arange(n, dtype=np.int32) * 7 + 3) % V
+    out = {}
+    for k in ks:
+        dec = sa.Decoder(path, n_ctx=N_CTX, gpu_layers=k)
+        try:
+            r = {"layers_in_hbm": dec.gpu_layers, "of": dec.n_layer}
+            for lvl in (2, 1):
+                dec.prompt_mode(lvl)
+                dec.prefill(ids[:64], 0, V)
+                sa.sync()
+                t = time.perf_counter()
+                lg = dec.prefill(ids, 0, V)
+                dt = time.perf_counter() - t
+                r[f"prompt_level{lvl}"] = {"tokens": n, "ms": round(dt * 1e3, 1), "tokens_per_s": round(n / dt, 1)}
+            for i in range(3):
+                lg = dec.step(int(np.argmax(lg)), n + i, V)
+            sa.sync()
+            t = time.perf_counter()
+            for i in range(steps):
+                lg = dec.step(int(np.argmax(lg)), n + 3 + i, V)
+            dt = time.perf_counter() - t
+            r["decode"] = {"steps": steps, "ms_per_token": round(dt / steps * 1e3, 2),
+                           "tokens_per_s": round(steps / dt, 1)}
+            out[str(k)] = r
+            log(f"split {k}: {r}")
+        finally:
+            dec.close()
+    return out
 
 
 def batched_trace(work, steps=10, ns=16, pos0=1024):
