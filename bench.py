@@ -507,18 +507,23 @@ def cpu_leg(args):
         print(json.dumps({"error": "oracle/_ref/libsmlref.so not built"}))
         return
     if kind == "decode":
-        path, pos0, budget = args[2], int(args[3]), float(args[4])
-        m = ob.RefModel(path, pos0 + 2000, threads=threads)
+        # positions pos0 + 1 .. end, cycled until the budget is spent (a
+        # revisited position overwrites its cache row and attends to the
+        # rows before it, the same work as the first visit)
+        path, pos0, budget, end = args[2], int(args[3]), float(args[4]), int(args[5])
+        span = end - pos0
+        m = ob.RefModel(path, end + 1, threads=threads)
         tok = 1
         m.forward(tok, pos0)                     # warm-up token
         n, t0 = 0, time.perf_counter()
-        while (time.perf_counter() - t0 < budget or n < 2) and n < 1990:   # stays inside the context
-            tok = int(np.argmax(m.forward(tok, pos0 + 1 + n)))
+        while time.perf_counter() - t0 < budget or n < 2:
+            tok = int(np.argmax(m.forward(tok, pos0 + 1 + n % span)))
             n += 1
         dt = time.perf_counter() - t0
         m.close()
+        cycled = f", cycled {n / span:.1f} times" if n > span else ""
         print(json.dumps({"tokens": n, "s": round(dt, 3), "tokens_per_s": round(n / dt, 3),
-                          "positions": f"{pos0 + 1}..{pos0 + n}"}))
+                          "positions": f"{pos0 + 1}..{pos0 + min(n, span)}{cycled}"}))
     elif kind == "gemv":
         from sheep_amd.ssf import SSF
         path, ncopy = args[2], int(args[3])
@@ -595,8 +600,9 @@ def cpu_baseline(path, pos0, moe_path, gemv_paths, budget_s=10.0):
     """The reference's own CPU path (sml-kernel.c kernels on sml-pool threads,
     compiled from its sources into oracle/_ref) on the same files, on this
     host's cores, each leg pinned to its first T CPUs:
-    - decode (sml_forward) at the GPU line's positions (pos0 + 1 ..; the cache
-      rows before them are left as allocated, which costs the same reads),
+    - decode (sml_forward) at the GPU line's positions (pos0 + 1 .. the
+      context's last, cycled; the cache rows before them are left as
+      allocated, which costs the same reads),
       T = every usable CPU (the value), with the T sweep and a short-context line;
     - the single-GEMV workloads (sml_quantize_act + the width's kernels over row
       chunks of 32, rotating over copies larger than the LLC);
@@ -607,14 +613,14 @@ def cpu_baseline(path, pos0, moe_path, gemv_paths, budget_s=10.0):
     out = {"kind": "reference", "unit": "tokens/s", "host": host}
     sweep = {}
     for t in sweep_t:
-        sweep[str(t)] = run_cpu_leg("decode", t, path, pos0, budget_s if t == tmax else budget_s / 2)
+        sweep[str(t)] = run_cpu_leg("decode", t, path, pos0, budget_s if t == tmax else budget_s / 2, N_CTX - 1)
         log(f"cpu decode T={t}: {sweep[str(t)]}")
     best = max(sweep, key=lambda k: sweep[k].get("tokens_per_s", 0))
     out["value"] = sweep[str(tmax)].get("tokens_per_s")
     out["cores"] = tmax
     out["threads_sweep"] = sweep
     out["best_threads"] = int(best)
-    out["short_context"] = run_cpu_leg("decode", tmax, path, 1, budget_s / 2)
+    out["short_context"] = run_cpu_leg("decode", tmax, path, 1, budget_s / 2, 2001)
     out["sample"] = (f"{sweep[str(tmax)].get('tokens')} greedy tokens of the same Llama-3-8B-shaped Q4 file at "
                      f"positions {sweep[str(tmax)].get('positions')} (the GPU line's), sml_forward on {tmax} pool "
                      f"threads pinned to CPUs 0..{tmax - 1}; T sweep {sweep_t}; {host['cpu']}, "
