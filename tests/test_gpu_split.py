@@ -132,6 +132,16 @@ def test_split_layer_counts(tmpdir_s, monkeypatch):
         assert (dec.gpu_layers, dec.n_layer) == (2, 6)
     finally:
         dec.close()
+    # left to the free memory: a reserve larger than any card leaves room for
+    # no layer, so the open keeps the first one (the reference's least)
+    monkeypatch.delenv("SML_GPU_LAYERS")
+    monkeypatch.setenv("SML_SPLIT_RESERVE_MB", "10000000")
+    got, counts = run(p, 0)
+    assert counts == (1, 6), counts
+    monkeypatch.delenv("SML_SPLIT_RESERVE_MB")
+    whole, _ = run(p, 0)
+    for i, (g, w) in enumerate(zip(got, whole)):
+        same_bits(g, w, f"split chosen by the free memory, call {i}")
 
 
 def test_split_refuses_a_mixture_of_experts_model(tmpdir_s):
