@@ -37,7 +37,7 @@ const char * sml_gpu_last_error(void);
 // chains, the C library's expf, the SiLU polynomial. Logits then equal the
 // reference's CPU path bit for bit, so greedy ids are identical for any
 // number of steps. It is slower (the serial chains are latency-bound) and
-// serves one sequence. Prompts of dense Q4 models are read batched, 64
+// serves one sequence. Prompts of dense Q4/Q8 models are read batched, 64
 // positions a chunk, with the same arithmetic per position (logits equal to
 // stepping the prompt, bit for bit); others a token at a time. Returns 1 when
 // the open model runs exact, else 0.

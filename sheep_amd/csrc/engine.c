@@ -882,7 +882,7 @@ static int multi_per256(int ns) {
 // matrix, and gate/up sharing a permutation and width (the MoE layers batch
 // by themselves). Builds the (gate, up) tables on first use.
 // A Q4 matrix 256-aligned: the exact batched GEMM's input
-static int xgemm_ok(const sml_hip_mat * m) { return m && m->nbits == 4 && m->cols % 256 == 0; }
+static int xgemm_ok(const sml_hip_mat * m) { return m && (m->nbits == 4 || m->nbits == 8) && m->cols % 256 == 0; }
 
 static int rows_check(void) {
     if (G.rows_ok >= 0) return G.rows_ok;
@@ -892,7 +892,7 @@ static int rows_check(void) {
             G.rows_ok = 0;
             return 0;
         }
-        // exact mode batches prompts of dense Q4 layers only (the
+        // exact mode batches prompts of dense Q4/Q8 layers only (the
         // reference-order GEMM); anything else reads them a token at a time
         if (G.exact && (y->moe || !xgemm_ok(y->qkv) || !xgemm_ok(y->o) || !xgemm_ok(y->gate) || !xgemm_ok(y->up) ||
                         !xgemm_ok(y->down))) {

@@ -4306,10 +4306,15 @@ extern "C" __global__ __launch_bounds__(256) void sml_gemm_ksum(const sml_kksum 
 // positions in registers (x 2 for SwiGLU: gate and up), so no value crosses
 // lanes before the fold. Workgroup: 4 waves = 64 positions x 16 weight rows;
 // the waves read the same weight bytes (L1). Inputs a multiple of 256 wide
-// (no trailing half superblock: the caller checks).
-template <bool SW>
+// (no trailing half superblock: the caller checks). Q8 (NB 8: two nibble
+// planes, code = lo + 16 hi, the reference's flat8 reads the same planes
+// with the 4-bit kernel, sml/sml-kernel.c:1066-1073): dot_g = dot_lo +
+// 16 dot_hi from two MFMAs, the same integer.
+template <bool SW, int NB = 4>
 __device__ void xgemm_q4_body(const sml_kgemm & a) {
     #pragma clang fp contract(off)
+    static_assert(NB == 4 || NB == 8, "Q4 or Q8");
+    constexpr int NP = NB == 8 ? 2 : 1;                       // nibble planes
     typedef long v1l;
     constexpr int NM = SW ? 2 : 1;
     const int n = a.cols, ng = n / 32, nsb = ng / 8, rows = a.rows, m_all = a.m_all;
@@ -4317,13 +4322,14 @@ __device__ void xgemm_q4_body(const sml_kgemm & a) {
     const int wave = tid >> 6;
     const int r0 = (int) blockIdx.x * 16, p0 = (int) blockIdx.y * 64 + wave * 16;
     const int row = min(r0 + i16, rows - 1);
-    const uint8_t * plane[NM];
+    const uint8_t * plane[NM][NP];
     const uint8_t * fqb[NM];
     const uint8_t * fdb[NM];
     #pragma unroll
     for (int k = 0; k < NM; k++) {
         const sml_kmat & mk = a.inl ? a.m0[k] : a.mats[k];
-        plane[k] = mk.plane[0] + (size_t) row * (n / 2) + 16 * c;
+        #pragma unroll
+        for (int pl = 0; pl < NP; pl++) plane[k][pl] = mk.plane[pl] + (size_t) row * (n / 2) + 16 * c;
         fqb[k] = mk.sqmq + (size_t) row * ng * 2;
         fdb[k] = (const uint8_t *) mk.sdmd + (size_t) row * nsb * 4;
     }
@@ -4346,13 +4352,15 @@ __device__ void xgemm_q4_body(const sml_kgemm & a) {
             #pragma unroll
             for (int j = 0; j < 8; j++) ch[k][r][j] = 0.0f;
     for (int b = 0; b < nsb; b++) {
-        v4u w[NM][2], fq[NM];
+        v4u w[NM][NP][2], fq[NM];
         uint32_t fd[NM];
         v4u aq[4];
         #pragma unroll
         for (int k = 0; k < NM; k++) {
             #pragma unroll
-            for (int p = 0; p < 2; p++) w[k][p] = gld<v4u>(plane[k] + (size_t) b * 128 + p * 64);
+            for (int pl = 0; pl < NP; pl++)
+                #pragma unroll
+                for (int p = 0; p < 2; p++) w[k][pl][p] = gld<v4u>(plane[k][pl] + (size_t) b * 128 + p * 64);
             fq[k] = gld<v4u>(fqb[k] + (size_t) b * 16);
             fd[k] = gld<uint32_t>(fdb[k] + (size_t) b * 4);
         }
@@ -4379,19 +4387,31 @@ __device__ void xgemm_q4_body(const sml_kgemm & a) {
             av[2 * u] = (v1l) (((unsigned long) x.y << 32) | x.x);
             av[2 * u + 1] = (v1l) (((unsigned long) y.y << 32) | y.x);
         }
-        v2u wx[NM][2], wy[NM][2];
+        v2u wx[NM][NP][2], wy[NM][NP][2];
         #pragma unroll
         for (int k = 0; k < NM; k++)
             #pragma unroll
-            for (int p = 0; p < 2; p++) xslice(w[k][p], wx[k][p], wy[k][p]);
+            for (int pl = 0; pl < NP; pl++)
+                #pragma unroll
+                for (int p = 0; p < 2; p++) xslice(w[k][pl][p], wx[k][pl][p], wy[k][pl][p]);
         #pragma unroll
         for (int j = 0; j < 8; j++) {
             #pragma unroll
             for (int k = 0; k < NM; k++) {
-                const v2u ww = (j & 2) ? wy[k][j >> 2] : wx[k][j >> 2];
-                const v2u cd = (j & 1) ? ((ww >> 4u) & 0x0F0F0F0Fu) : (ww & 0x0F0F0F0Fu);
                 v4i d = {0, 0, 0, 0};
-                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], (v1l) (((unsigned long) cd.y << 32) | cd.x), d, 0, 0, 0);
+                #pragma unroll
+                for (int pl = NP - 1; pl >= 0; pl--) {
+                    const v2u ww = (j & 2) ? wy[k][pl][j >> 2] : wx[k][pl][j >> 2];
+                    const v2u cd = (j & 1) ? ((ww >> 4u) & 0x0F0F0F0Fu) : (ww & 0x0F0F0F0Fu);
+                    if (pl == 1) {
+                        // the high nibbles' dot, times 16, then the low ones added on
+                        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], (v1l) (((unsigned long) cd.y << 32) | cd.x), d, 0, 0, 0);
+                        #pragma unroll
+                        for (int r = 0; r < 4; r++) d[r] *= 16;
+                    } else {
+                        d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], (v1l) (((unsigned long) cd.y << 32) | cd.x), d, 0, 0, 0);
+                    }
+                }
                 const uint32_t f = fq[k][j >> 1] >> (16 * (j & 1));
                 const float wsc = h2f((uint16_t) (fd[k] & 0xFFFFu)) * (float) (f & 0xFFu);
                 const float wmn = h2f((uint16_t) (fd[k] >> 16)) * ((float) ((f >> 8) & 0xFFu) - 127.0f);
@@ -4429,6 +4449,8 @@ __device__ void xgemm_q4_body(const sml_kgemm & a) {
 }
 extern "C" __global__ __launch_bounds__(256) void sml_xgemm_q4(const sml_kgemm a) { xgemm_q4_body<false>(a); }
 extern "C" __global__ __launch_bounds__(256) void sml_xgemm_q4_s(const sml_kgemm a) { xgemm_q4_body<true>(a); }
+extern "C" __global__ __launch_bounds__(256) void sml_xgemm_q8(const sml_kgemm a) { xgemm_q4_body<false, 8>(a); }
+extern "C" __global__ __launch_bounds__(256) void sml_xgemm_q8_s(const sml_kgemm a) { xgemm_q4_body<true, 8>(a); }
 
 // ---------------------------------------------------------------- prompt GEMM on MFMA (Q4, per-256 activations)
 //

@@ -1517,10 +1517,11 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngro
     if (swiglu && (bias || resid)) hx_failf("SwiGLU GEMM takes no bias or residual");
     if ((uint64_t) rows * (uint64_t) cols >= (1ull << 32)) hx_failf("matrix too large for one GEMM launch");
     if (regime == GEMM_REF) {
-        // exact mode's batched prompt: Q4 inputs a multiple of 256 wide, 16
-        // weight rows x 64 positions per workgroup
-        if (nbits != 4 || cols % 256 || count || ngroups != 1 || m_all < 1 || (uint64_t) m_all * cols >= (1ull << 32))
-            hx_failf("the exact batched GEMM takes one Q4 matrix 256-aligned (%d bits, %d columns)", nbits, cols);
+        // exact mode's batched prompt: Q4 or Q8 inputs a multiple of 256
+        // wide, 16 weight rows x 64 positions per workgroup
+        if ((nbits != 4 && nbits != 8) || cols % 256 || count || ngroups != 1 || m_all < 1 ||
+            (uint64_t) m_all * cols >= (1ull << 32))
+            hx_failf("the exact batched GEMM takes one Q4 or Q8 matrix 256-aligned (%d bits, %d columns)", nbits, cols);
         sml_kgemm a;
         memset(&a, 0, sizeof a);
         a.mats = tab; a.nmat = swiglu ? 2 : 1; a.cols = cols; a.rows = rows;
@@ -1531,7 +1532,9 @@ void op_gemm(hipStream_t st, const sml_kmat * tab, const sml_kmat * hk, int ngro
             a.m0[0] = hk[0];
             if (swiglu) a.m0[1] = hk[1];
         }
-        hx_launch3(swiglu ? "sml_xgemm_q4_s" : "sml_xgemm_q4", (unsigned) ((rows + 15) / 16),
+        char xname[24];
+        snprintf(xname, sizeof xname, "sml_xgemm_q%d%s", nbits, swiglu ? "_s" : "");
+        hx_launch3(xname, (unsigned) ((rows + 15) / 16),
                    (unsigned) ((m_all + 63) / 64), 1, 256, 0, st, &a);
         return;
     }

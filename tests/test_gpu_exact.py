@@ -356,8 +356,10 @@ DECODERS = {
                     random_perm=False, seed=32),
     "qwenish": dict(n_layer=4, n_embd=1536, n_head=12, n_head_kv=2, n_ff=8960, n_vocab=32000, rope_theta=1e6,
                     qkv_bias=True, tied=True, random_perm=True, seed=1002),
+    "dense_q8": dict(n_layer=2, n_embd=512, n_head=4, n_head_kv=2, n_ff=1024, n_vocab=2000, qkv_bias=True,
+                     random_perm=True, nbits=8, seed=33),
 }
-STARTS = {"dense": 11, "inorder": 7, "qwenish": 100}
+STARTS = {"dense": 11, "inorder": 7, "qwenish": 100, "dense_q8": 13}
 
 
 @pytest.fixture(scope="module")
@@ -420,15 +422,15 @@ def test_exact_greedy_64_equals_reference(decoder_file, name):
 
 
 @needs_ref
-@pytest.mark.parametrize("name,n", [("dense", 130), ("inorder", 64), ("qwenish", 77)])
+@pytest.mark.parametrize("name,n", [("dense", 130), ("inorder", 64), ("qwenish", 77), ("dense_q8", 100)])
 def test_exact_batched_prompt_equals_reference(decoder_file, name, n):
     """Exact mode reads a prompt batched (level 1: 64-position chunks through
-    the reference-order Q4 GEMM, sml_xgemm_q4, and the row form of the
-    reference-order attention), and its logits equal the reference stepping
-    the same ids through sml_forward bit for bit; so do 4 greedy steps after
-    it. Chunk boundaries inside the prompt (130 = 64 + 64 + 2), one whole
-    chunk (64), Qwen-shaped layers (77). The same prompt read a token at a
-    time (level 0) gives the same bits."""
+    the reference-order Q4 or Q8 GEMM, sml_xgemm_q4 / _q8, and the row form
+    of the reference-order attention), and its logits equal the reference
+    stepping the same ids through sml_forward bit for bit; so do 4 greedy
+    steps after it. Chunk boundaries inside the prompt (130 = 64 + 64 + 2),
+    one whole chunk (64), Qwen-shaped layers (77), Q8 layers (100). The same
+    prompt read a token at a time (level 0) gives the same bits."""
     p = decoder_file(name)
     V = DECODERS[name]["n_vocab"]
     ids = np.random.default_rng(n).integers(0, V, n).astype(np.int32)
