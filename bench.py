@@ -657,7 +657,8 @@ def main():
     ap.add_argument("--decode-trace", metavar="MODEL", choices=("llama", "qwen"),
                     help="only decode the last --steps positions with direct launches (run under rocprofv3)")
     ap.add_argument("--exact", action="store_true",
-                    help="with --decode-trace: open the decoder in exact mode (the reference's float order)")
+                    help="with --decode-trace or --prompt-only: open the decoder in exact mode (the reference's "
+                         "float order)")
     ap.add_argument("--trace-summary", metavar="DIR", help="per-kernel table of a --decode-trace kernel trace")
     ap.add_argument("--small-gemm", action="store_true", help="only time the 16-row small-M GEMMs")
     ap.add_argument("--gemv-sweep", action="store_true",
@@ -712,7 +713,7 @@ def main():
         elif a.batched_trace:
             res = {"batched_trace": batched_trace(work, a.steps)}
         elif a.prompt_only >= 0:
-            res = {"prompt_reading": prompt_only(work, a.prompt_only, a.prompt if a.prompt > 0 else 3960)}
+            res = {"prompt_reading": prompt_only(work, a.prompt_only, a.prompt if a.prompt > 0 else 3960, a.exact)}
         else:
             res = run(a, work)
     finally:
@@ -845,11 +846,13 @@ def trace_summary(out_dir, steps):
     return "\n".join(lines)
 
 
-def prompt_only(work, level, n):
-    """The Llama-3-8B-shaped file's prompt of n ids read once at one prompt level."""
+def prompt_only(work, level, n, exact=False):
+    """The Llama-3-8B-shaped file's prompt of n ids read once at one prompt
+    level (exact: opened in exact mode, where level 1 is the reference-order
+    batched prompt)."""
     path = os.path.join(work, "llama3_8b_q4.ssf")
     sa.synth_model(path, n_ctx_train=N_CTX, **LLAMA)
-    dec = sa.Decoder(path, n_ctx=N_CTX)
+    dec = sa.Decoder(path, n_ctx=N_CTX, exact=exact)
     try:
         ids = np.random.default_rng(1003).integers(0, LLAMA["n_vocab"], n).astype(np.int32)
         dec.prompt_mode(level)
@@ -860,7 +863,7 @@ def prompt_only(work, level, n):
         dt = time.perf_counter() - t0
     finally:
         dec.close()
-    return {"level": level, "tokens": n, "s": round(dt, 3), "tokens_per_s": round(n / dt, 1)}
+    return {"level": level, "exact": exact, "tokens": n, "s": round(dt, 3), "tokens_per_s": round(n / dt, 1)}
 
 
 def run(a, work):
